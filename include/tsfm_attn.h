@@ -1,0 +1,178 @@
+/*
+ * tsfm_attn.h -- C ABI of libtsfm_attn.so, the gfx950 (MI355X) attention path for tsfm-zig.
+ *
+ * Drop-in boundary. In the reference every attention call funnels through
+ *   core.attn.selfAttend / selfAttendRuntime        src/core/attn.zig:72-117
+ * called once per (series, head) from a fork-join job:
+ *   Chronos-Bolt encoder   par.forRange(nb*nh, SelfJob.attend)   src/chronos_bolt/model.zig:243, 317-346
+ *   Chronos-Bolt decoder   par.forRange(nb*nh, CrossJob.attend)  src/chronos_bolt/model.zig:297, 349-381
+ *   Chronos-2 time attn    RoPE loop + forRange(b*nh, TimeJob)   src/chronos2/model.zig:236-245, 260, 277-309
+ *   Timestral time attn    forRange(rows*nh, TimeJob.attend)     src/timestral/model.zig:513-515, 558-635
+ * and its arithmetic reaches a device only as two GEMMs per (series, head) through
+ *   Backend.sgemm_nt / sgemm_nn                      src/platform/backend.zig:69-72
+ *   cuda_sgemm_nt / cuda_sgemm_nn                    src/platform/cuda/gemm.c:316-330
+ * tsfm_attn_fwd() replaces one whole forRange(B*H, Job.attend) call: the caller keeps its Zig
+ * signatures and, at the forRange call site, tries one batched call first and runs its unchanged
+ * per-item CPU loop when the call returns non-zero.
+ *
+ * Conventions (the reference backend's, src/platform/cuda/gemm.c:1-16, backend.zig:33-36):
+ *   - every entry point returns 0 on success; any other value means "not run, use the CPU path"
+ *     and promises no partial output. Nothing here aborts the process;
+ *   - the caller owns every buffer it passes; the library never frees caller memory;
+ *   - the library is thread-safe: device set-up runs once (pthread_once), and each host thread
+ *     gets its own HIP stream and device staging buffers, released when the thread exits;
+ *   - results do not depend on how many host threads call in, nor on batch composition: there
+ *     are no atomics in any reduction and tile order is fixed.
+ *
+ * Layouts follow the reference: element (b, t, h, c) of Q lives at
+ *   q[b * q_batch + t * q_tok + h * head_dim + c]
+ * (`attn.Strides`, src/core/attn.zig:32, plus a batch stride). The supported head_dim is 64.
+ */
+#ifndef TSFM_ATTN_H
+#define TSFM_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSFM_ATTN_ABI_VERSION 1
+
+/* Return codes. Non-zero always means "fall back to the CPU". */
+enum {
+    TSFM_OK = 0,
+    TSFM_E_UNAVAILABLE = 1, /* no gfx950 device / HIP runtime, or TSFM_HIP_DISABLE is set */
+    TSFM_E_UNSUPPORTED = 2, /* valid request this library does not implement (shape, dtype, stride) */
+    TSFM_E_INVALID = 3,     /* malformed arguments */
+    TSFM_E_DEVICE = 4       /* a HIP call failed */
+};
+
+/* Mask variants. Values 0..4 are `attn.Mask` in declaration order (src/core/attn.zig:10-21):
+ *   FULL           every query reads every key
+ *   KEYS_ADDITIVE  invalid keys get -FLT_MAX added to their score (T5)
+ *   CAUSAL         query i reads keys 0..=i
+ *   CAUSAL_KEYS    causal over valid keys, diagonal always open (-inf elsewhere)
+ *   FULL_KEYS      bidirectional over valid keys, diagonal always open
+ * DECODER is the Timestral decoder-row mask written inline in TimeJob.attend
+ * (src/timestral/model.zig:612-632): query i reads valid keys in [0, ctx_keys) and the chain
+ * [chain_start, q_pos0 + i]; everything else gets -inf.
+ * For masks 2..5, query i sits at key index q_pos0 + i ("i" and "j == i" in attn.zig). */
+enum {
+    TSFM_MASK_FULL = 0,
+    TSFM_MASK_KEYS_ADDITIVE = 1,
+    TSFM_MASK_CAUSAL = 2,
+    TSFM_MASK_CAUSAL_KEYS = 3,
+    TSFM_MASK_FULL_KEYS = 4,
+    TSFM_MASK_DECODER = 5
+};
+
+/* Element type of q, k, v and o. Reference arithmetic is f32 (half checkpoints are widened at load,
+ * src/core/safetensors.zig:81-91); BF16/F16 are new here and accumulate in f32. */
+enum { TSFM_DTYPE_F32 = 0, TSFM_DTYPE_BF16 = 1, TSFM_DTYPE_F16 = 2 };
+
+/* flags */
+#define TSFM_ATTN_DEVICE_PTRS 1u /* every pointer is device memory; the call is asynchronous on `stream` */
+
+/* One batched attention call: o = softmax(mask(scale * q k^T + bias)) v for every (b, h).
+ * Replaces: selfAttendRuntime per item (src/core/attn.zig:99-117) inside the forRange calls listed
+ * above; the Chronos-2 serial RoPE loop (src/chronos2/model.zig:236-245) when rope_cos is set; the
+ * positionBias materialisation (src/chronos_bolt/model.zig:195-205) when rel_table is set. */
+typedef struct tsfm_attn_args {
+    int32_t dtype;       /* TSFM_DTYPE_* */
+    int32_t mask;        /* TSFM_MASK_* */
+    int32_t batch;       /* B: series (Bolt, Chronos-2) or rows (Timestral) */
+    int32_t heads;       /* H */
+    int32_t n_q;         /* queries per (b, h) */
+    int32_t n_k;         /* keys per (b, h) */
+    int32_t head_dim;    /* D; 64 */
+    int32_t q_pos0;      /* key index of query 0 (masks 2..5 and the RoPE position of queries) */
+    int32_t ctx_keys;    /* DECODER: context keys are [0, ctx_keys) */
+    int32_t chain_start; /* DECODER: first key of the decoder chain */
+    float scale;         /* score scale (attn.selfAttend `scale`) */
+    uint32_t flags;      /* TSFM_ATTN_DEVICE_PTRS or 0 (host pointers, synchronous) */
+
+    const void *q;  int64_t q_tok, q_batch; /* element strides */
+    const void *k;  int64_t k_tok, k_batch;
+    const void *v;  int64_t v_tok, v_batch;
+    void *o;        int64_t o_tok, o_batch;
+
+    /* One byte per key, non-zero = valid (Zig `[]const bool`), row b at key_valid + b * kv_batch.
+     * Read by masks KEYS_ADDITIVE, CAUSAL_KEYS, FULL_KEYS (n_k bytes per row) and DECODER
+     * (min(n_k, ctx_keys) bytes per row); may be NULL for the others. */
+    const uint8_t *key_valid; int64_t kv_batch;
+
+    /* Additive score bias, applied before the mask (src/core/attn.zig:93). At most one of:
+     *  - dense: bias[h * bias_head + i * bias_row + j], shared by every b (positionBias layout);
+     *  - T5 relative: bias = rel_table[rel_bucket[j - i + n_q - 1] * heads + h], where rel_table is
+     *    the (rel_buckets, heads) table (src/chronos_bolt/model.zig:115) and rel_bucket holds
+     *    n_q + n_k - 1 bucket ids (tsfm_t5_bucket_table). Requires q_pos0 == 0. */
+    const float *bias; int64_t bias_head, bias_row;
+    const float *rel_table; const int32_t *rel_bucket; int32_t rel_buckets;
+
+    /* Rotate-half RoPE applied to q and k before the product (nn.ropeHalf, src/core/nn.zig:448-467),
+     * NULL rope_cos = none. Tables are (positions, rope_half) f32; key j uses row j, query i row
+     * q_pos0 + i, of table number t = (rope_row0 + b) / rope_rows_per_table, which starts at
+     * t * rope_table_stride. rope_half must be head_dim / 2. rope_rows_per_table = 0 means one
+     * table shared by every b (Chronos-2); Timestral has one table per series group of
+     * rope_rows_per_table rows, and rope_row0 is the group position of batch row 0. */
+    const float *rope_cos, *rope_sin;
+    int32_t rope_half; int32_t rope_rows_per_table; int32_t rope_row0; int64_t rope_table_stride;
+
+    void *stream; /* hipStream_t for TSFM_ATTN_DEVICE_PTRS; NULL = this thread's library stream */
+} tsfm_attn_args;
+
+/* Device set-up, run once per process (cuda/gemm.c:112-166 init_cuda / ensure_cuda). Optional:
+ * every entry point calls it. Returns TSFM_OK or TSFM_E_UNAVAILABLE. */
+int tsfm_attn_init(void);
+
+/* 1 when the library can run (gfx950 device present, not disabled), else 0.
+ * Counterpart of gpu.context() returning a backend or null (src/platform/cuda/gpu.zig:95-97). */
+int tsfm_attn_available(void);
+
+/* Batched attention (see tsfm_attn_args). */
+int tsfm_attn_fwd(const tsfm_attn_args *args);
+
+/* Human-readable reason for this thread's last non-zero return ("" if none). */
+const char *tsfm_attn_last_error(void);
+
+/* T5 bidirectional relative-position bucket of rel = key - query, with the reference's float32
+ * log (src/chronos_bolt/model.zig:74-85). Host function. */
+uint32_t tsfm_t5_relative_bucket(int64_t rel, uint32_t num_buckets, uint32_t max_distance);
+
+/* Fills out[t] = tsfm_t5_relative_bucket(t - (n_q - 1), ...) for t in [0, n_q + n_k - 1): the
+ * rel_bucket array of tsfm_attn_args. Host function; the bucket half of positionBias
+ * (src/chronos_bolt/model.zig:195-205). Returns TSFM_OK or TSFM_E_INVALID. */
+int tsfm_t5_bucket_table(int32_t *out, int32_t n_q, int32_t n_k, uint32_t num_buckets, uint32_t max_distance);
+
+/* ---------------------------------------------------------------------------------------------
+ * KV cache for block-autoregressive decode. No counterpart in the reference: Timestral's
+ * blockDecode re-encodes the whole grown context every block (src/timestral/forecaster.zig:423-563),
+ * recomputing K/V of unchanged prefix tokens. With a causal encoder and a fixed prefix the cached
+ * result equals rows [P, P + n) of causal selfAttend over the concatenated sequence.
+ * The cache lives in device memory in the layout the decode kernel streams (per (b, h): K rows
+ * [pos][D]; V in 32-key chunks transposed for the matrix cores). bf16 and f16 only. */
+typedef struct tsfm_kv_cache tsfm_kv_cache;
+
+int tsfm_kv_create(tsfm_kv_cache **out, int32_t dtype, int32_t batch, int32_t heads, int32_t head_dim,
+                   int32_t capacity);
+int tsfm_kv_free(tsfm_kv_cache *cache);
+int tsfm_kv_reset(tsfm_kv_cache *cache);
+int32_t tsfm_kv_len(const tsfm_kv_cache *cache);
+
+/* Append n_new tokens to every (b, h): k/v element (b, t, h, c) at b * batch + t * tok + h * D + c.
+ * flags/stream as in tsfm_attn_args. */
+int tsfm_kv_append(tsfm_kv_cache *cache, const void *k, int64_t k_tok, int64_t k_batch, const void *v,
+                   int64_t v_tok, int64_t v_batch, int32_t n_new, uint32_t flags, void *stream);
+
+/* Causal attention of n_q queries over the cached keys [0, tsfm_kv_len): query i sits at key
+ * index q_pos0 + i and reads keys 0..=q_pos0+i; requires q_pos0 + n_q <= tsfm_kv_len. */
+int tsfm_kv_attend(tsfm_kv_cache *cache, const void *q, int64_t q_tok, int64_t q_batch, void *o,
+                   int64_t o_tok, int64_t o_batch, int32_t n_q, int32_t q_pos0, float scale, uint32_t flags,
+                   void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

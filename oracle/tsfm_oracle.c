@@ -1,0 +1,684 @@
+/*
+ * tsfm_oracle.c -- CPU oracle for the tsfm-zig attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the CPU
+ * baseline that bench.py times beside them. Product code never calls it.
+ *
+ * A C restatement of the reference's builtin CPU path (`-Dblas=builtin`, the
+ * Linux default, build.zig:11-12). Arithmetic follows the Zig source:
+ *   - Zig does not contract `a * b + c`; this file is compiled with
+ *     -ffp-contract=off and uses fmaf() exactly where Zig calls @mulAdd;
+ *   - @reduce(.Add, v) on floats keeps associativity (strict float mode), i.e.
+ *     an ordered sum over lanes 0..L-1, restated by red_add();
+ *   - @round is round-half-away-from-zero (roundf); @exp/@log/@cos/@sin of f32
+ *     are libm's expf/logf/cosf/sinf; std.math.pow(f32) is powf.
+ * The lane count L = ORC_LANES is fixed at compile time like nn.lanes
+ * (src/core/nn.zig:296).
+ */
+#include "tsfm_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifndef ORC_LANES
+#define ORC_LANES 8
+#endif
+#define L ORC_LANES
+
+int orc_lanes(void) { return L; }
+
+/* Ordered lane sum: @reduce(.Add, v) with associativity preserved. */
+static inline float red_add(const float *v) {
+    float s = v[0];
+    for (int e = 1; e < L; e++) s += v[e];
+    return s;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* nn.expVec (src/core/nn.zig:344-359): Cephes expf, clamp + range reduction + degree-6 poly. */
+
+float orc_exp_vec(float x_in) {
+    float x = x_in;
+    if (x < -87.33654f) x = -87.33654f; /* @max(x_in, -87.33654) */
+    if (x > 88.72284f) x = 88.72284f;   /* @min(.., 88.72284) */
+    const float fx = roundf(x * 1.44269504088896341f);
+    float r = x - fx * 0.693359375f;
+    r = r - fx * -2.12194440e-4f;
+    float y = 1.9875691500e-4f;
+    y = y * r + 1.3981999507e-3f;
+    y = y * r + 8.3334519073e-3f;
+    y = y * r + 4.1665795894e-2f;
+    y = y * r + 1.6666665459e-1f;
+    y = y * r + 5.0000001201e-1f;
+    y = y * r * r + r + 1.0f;
+    const int32_t n = (int32_t)fx;
+    const uint32_t bits = (uint32_t)(n + 127) << 23;
+    float pow2;
+    memcpy(&pow2, &bits, sizeof pow2);
+    return y * pow2;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* nn.gemmNTFallback builtin path (src/core/nn.zig:68-162). Register tile of row_tile rows of A
+ * against 4 rows of B; each output is an @mulAdd chain per lane, an ordered lane sum, then the
+ * k % L tail added unfused, then scaled by alpha. */
+
+#define RT ((L > 4) ? 2 : 4)
+
+void orc_gemm_nt(float *cc, size_t ldc, const float *a, size_t lda, const float *b, size_t ldb,
+                 size_t m, size_t n, size_t k, float alpha) {
+    const size_t kv = k / L * L;
+    size_t i = 0;
+    for (; i + RT <= m; i += RT) {
+        size_t j = 0;
+        for (; j + 4 <= n; j += 4) {
+            float acc[RT][4][L];
+            memset(acc, 0, sizeof acc);
+            for (size_t p = 0; p < kv; p += L)
+                for (int u = 0; u < RT; u++)
+                    for (int w = 0; w < 4; w++)
+                        for (int e = 0; e < L; e++)
+                            acc[u][w][e] = fmaf(a[(i + u) * lda + p + e], b[(j + w) * ldb + p + e], acc[u][w][e]);
+            for (int u = 0; u < RT; u++)
+                for (int w = 0; w < 4; w++) {
+                    float sum = red_add(acc[u][w]);
+                    for (size_t q = kv; q < k; q++) sum += a[(i + u) * lda + q] * b[(j + w) * ldb + q];
+                    cc[(i + u) * ldc + j + w] = alpha * sum;
+                }
+        }
+        for (; j < n; j++) { /* column remainder */
+            float acc[RT][L];
+            memset(acc, 0, sizeof acc);
+            for (size_t p = 0; p < kv; p += L)
+                for (int u = 0; u < RT; u++)
+                    for (int e = 0; e < L; e++)
+                        acc[u][e] = fmaf(a[(i + u) * lda + p + e], b[j * ldb + p + e], acc[u][e]);
+            for (int u = 0; u < RT; u++) {
+                float sum = red_add(acc[u]);
+                for (size_t q = kv; q < k; q++) sum += a[(i + u) * lda + q] * b[j * ldb + q];
+                cc[(i + u) * ldc + j] = alpha * sum;
+            }
+        }
+    }
+    for (; i < m; i++) { /* row remainder */
+        const float *ar = a + i * lda;
+        size_t j = 0;
+        for (; j + 4 <= n; j += 4) {
+            float acc[4][L];
+            memset(acc, 0, sizeof acc);
+            for (size_t p = 0; p < kv; p += L)
+                for (int u = 0; u < 4; u++)
+                    for (int e = 0; e < L; e++)
+                        acc[u][e] = fmaf(ar[p + e], b[(j + u) * ldb + p + e], acc[u][e]);
+            for (int u = 0; u < 4; u++) {
+                float sum = red_add(acc[u]);
+                for (size_t q = kv; q < k; q++) sum += ar[q] * b[(j + u) * ldb + q];
+                cc[i * ldc + j + u] = alpha * sum;
+            }
+        }
+        for (; j < n; j++) {
+            float acc[L];
+            memset(acc, 0, sizeof acc);
+            for (size_t p = 0; p < kv; p += L)
+                for (int e = 0; e < L; e++) acc[e] = fmaf(ar[p + e], b[j * ldb + p + e], acc[e]);
+            float sum = red_add(acc);
+            for (size_t q = kv; q < k; q++) sum += ar[q] * b[j * ldb + q];
+            cc[i * ldc + j] = alpha * sum;
+        }
+    }
+}
+
+/* nn.gemmNN builtin path (src/core/nn.zig:179-238): four rows of A share each row of B; a k index
+ * whose four A values are all exactly zero is skipped (`:196`), a single remainder row skips its
+ * zeros (`:227`). Accumulation is `c + a * b`, unfused, in increasing k. */
+void orc_gemm_nn(float *cc, size_t ldc, const float *a, size_t lda, const float *b, size_t ldb,
+                 size_t m, size_t n, size_t k) {
+    size_t i = 0;
+    for (; i + 4 <= m; i += 4) {
+        float *c0 = cc + (i + 0) * ldc, *c1 = cc + (i + 1) * ldc;
+        float *c2 = cc + (i + 2) * ldc, *c3 = cc + (i + 3) * ldc;
+        memset(c0, 0, n * sizeof(float));
+        memset(c1, 0, n * sizeof(float));
+        memset(c2, 0, n * sizeof(float));
+        memset(c3, 0, n * sizeof(float));
+        for (size_t p = 0; p < k; p++) {
+            const float a0 = a[(i + 0) * lda + p], a1 = a[(i + 1) * lda + p];
+            const float a2 = a[(i + 2) * lda + p], a3 = a[(i + 3) * lda + p];
+            if (a0 == 0 && a1 == 0 && a2 == 0 && a3 == 0) continue;
+            const float *brow = b + p * ldb;
+            for (size_t j = 0; j < n; j++) {
+                const float bv = brow[j];
+                c0[j] = c0[j] + a0 * bv;
+                c1[j] = c1[j] + a1 * bv;
+                c2[j] = c2[j] + a2 * bv;
+                c3[j] = c3[j] + a3 * bv;
+            }
+        }
+    }
+    for (; i < m; i++) {
+        float *crow = cc + i * ldc;
+        memset(crow, 0, n * sizeof(float));
+        for (size_t p = 0; p < k; p++) {
+            const float av = a[i * lda + p];
+            if (av == 0) continue;
+            const float *brow = b + p * ldb;
+            for (size_t j = 0; j < n; j++) crow[j] = crow[j] + av * brow[j];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* nn.softmax (src/core/nn.zig:470-505): lane-wise max, then expVec over whole vectors and @exp
+ * over the tail, -inf mapped to exactly 0, a lane-wise partial sum reduced in order, then every
+ * entry multiplied by 1/sum. */
+void orc_softmax(float *row, size_t n) {
+    const float ninf = -INFINITY;
+    float mxv[L];
+    for (int e = 0; e < L; e++) mxv[e] = ninf;
+    size_t i = 0;
+    for (; i + L <= n; i += L)
+        for (int e = 0; e < L; e++) mxv[e] = fmaxf(mxv[e], row[i + e]);
+    float mx = mxv[0];
+    for (int e = 1; e < L; e++) mx = fmaxf(mx, mxv[e]);
+    for (; i < n; i++) mx = fmaxf(mx, row[i]);
+
+    float sumv[L];
+    memset(sumv, 0, sizeof sumv);
+    i = 0;
+    for (; i + L <= n; i += L)
+        for (int e = 0; e < L; e++) {
+            const float v = row[i + e];
+            const float ev = (v == ninf) ? 0.0f : orc_exp_vec(v - mx);
+            row[i + e] = ev;
+            sumv[e] += ev;
+        }
+    float sum = red_add(sumv);
+    for (; i < n; i++) {
+        row[i] = (row[i] == ninf) ? 0.0f : expf(row[i] - mx);
+        sum += row[i];
+    }
+    const float inv = 1.0f / sum;
+    for (i = 0; i < n; i++) row[i] *= inv;
+}
+
+/* nn.dot (src/core/nn.zig:328-340): `acc += av * bv` (unfused) per lane, ordered lane sum, tail. */
+float orc_dot(const float *a, const float *b, size_t n) {
+    float acc[L];
+    memset(acc, 0, sizeof acc);
+    size_t i = 0;
+    for (; i + L <= n; i += L)
+        for (int e = 0; e < L; e++) acc[e] += a[i + e] * b[i + e];
+    float sum = red_add(acc);
+    for (; i < n; i++) sum += a[i] * b[i];
+    return sum;
+}
+
+void orc_add_in_place(float *dst, const float *src, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = dst[i] + src[i];
+}
+
+void orc_mul_add_in_place(float *dst, const float *src, size_t n, float scalar) {
+    for (size_t i = 0; i < n; i++) dst[i] = dst[i] + scalar * src[i];
+}
+
+/* nn.ropeHalf (src/core/nn.zig:448-467): pairs (i, i + half), unfused products. */
+void orc_rope_half(float *x, const float *cos_t, const float *sin_t, size_t half) {
+    float *lo = x, *hi = x + half;
+    for (size_t i = 0; i < half; i++) {
+        const float x1 = lo[i], x2 = hi[i];
+        lo[i] = x1 * cos_t[i] - x2 * sin_t[i];
+        hi[i] = x2 * cos_t[i] + x1 * sin_t[i];
+    }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* attn.zig */
+
+int orc_mask_pick(int causal, int all_keys_valid, int additive) {
+    if (all_keys_valid) return causal ? ORC_CAUSAL : ORC_FULL;
+    if (causal) return ORC_CAUSAL_KEYS;
+    return additive ? ORC_KEYS_ADDITIVE : ORC_FULL_KEYS;
+}
+
+void orc_masked_softmax(int mask, float *scores, size_t n, const uint8_t *key_valid) {
+    switch (mask) {
+    case ORC_FULL:
+        for (size_t i = 0; i < n; i++) orc_softmax(scores + i * n, n);
+        break;
+    case ORC_KEYS_ADDITIVE: {
+        const float mask_min = -FLT_MAX;
+        for (size_t i = 0; i < n; i++) {
+            float *row = scores + i * n;
+            for (size_t j = 0; j < n; j++)
+                if (!key_valid[j]) row[j] += mask_min;
+            orc_softmax(row, n);
+        }
+        break;
+    }
+    case ORC_CAUSAL:
+        for (size_t i = 0; i < n; i++) {
+            orc_softmax(scores + i * n, i + 1);
+            memset(scores + i * n + i + 1, 0, (n - i - 1) * sizeof(float));
+        }
+        break;
+    case ORC_CAUSAL_KEYS:
+    case ORC_FULL_KEYS:
+        for (size_t i = 0; i < n; i++) {
+            float *row = scores + i * n;
+            for (size_t j = 0; j < n; j++) {
+                const int allowed = j == i || (key_valid[j] && (mask == ORC_FULL_KEYS || j <= i));
+                if (!allowed) row[j] = -INFINITY;
+            }
+            orc_softmax(row, n);
+        }
+        break;
+    default:
+        break;
+    }
+}
+
+void orc_self_attend(int mask, float *scores, const float *q, const float *k, const float *v, float *o,
+                     const size_t st[4], size_t n, size_t hd, float scale, const uint8_t *key_valid,
+                     const float *bias) {
+    orc_gemm_nt(scores, n, q, st[0], k, st[1], n, n, hd, scale);
+    if (bias) orc_add_in_place(scores, bias, n * n);
+    orc_masked_softmax(mask, scores, n, key_valid);
+    orc_gemm_nn(o, st[3], scores, n, v, st[2], n, hd, n);
+}
+
+/* allowedRef (src/core/attn.zig:122-130). */
+static int allowed_ref(int mask, const uint8_t *kv, size_t i, size_t j) {
+    switch (mask) {
+    case ORC_FULL: return 1;
+    case ORC_KEYS_ADDITIVE: return kv[j] != 0;
+    case ORC_CAUSAL: return j <= i;
+    case ORC_CAUSAL_KEYS: return j == i || (kv[j] && j <= i);
+    case ORC_FULL_KEYS: return j == i || kv[j];
+    default: return 0;
+    }
+}
+
+void orc_reference_attend_f64(int mask, double *o, const float *q, const float *k, const float *v,
+                              const size_t st[4], size_t n, size_t hd, double scale,
+                              const uint8_t *key_valid, const float *bias) {
+    double *s = (double *)malloc((n ? n : 1) * sizeof(double));
+    for (size_t i = 0; i < n; i++) {
+        double mx = -INFINITY;
+        for (size_t j = 0; j < n; j++) {
+            double dot = 0;
+            for (size_t c = 0; c < hd; c++) dot += (double)q[i * st[0] + c] * (double)k[j * st[1] + c];
+            s[j] = dot * scale + (bias ? (double)bias[i * n + j] : 0.0);
+            if (allowed_ref(mask, key_valid, i, j)) mx = fmax(mx, s[j]);
+        }
+        double z = 0;
+        for (size_t j = 0; j < n; j++) {
+            s[j] = allowed_ref(mask, key_valid, i, j) ? exp(s[j] - mx) : 0.0;
+            z += s[j];
+        }
+        for (size_t c = 0; c < hd; c++) {
+            double acc = 0;
+            for (size_t j = 0; j < n; j++) acc += s[j] / z * (double)v[j * st[2] + c];
+            o[i * hd + c] = acc;
+        }
+    }
+    free(s);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Chronos-Bolt (src/chronos_bolt/model.zig) */
+
+uint32_t orc_relative_bucket(int64_t rel, uint32_t num_buckets, uint32_t max_distance) {
+    const uint32_t half = num_buckets / 2;
+    const uint32_t base = rel > 0 ? half : 0;
+    const uint32_t rp = (uint32_t)(rel < 0 ? -rel : rel);
+    const uint32_t max_exact = half / 2;
+    if (rp < max_exact) return base + rp;
+    const float ratio = (float)rp / (float)max_exact;
+    const float denom = (float)log((double)max_distance / (double)max_exact);
+    const float large_f = logf(ratio) / denom * (float)(half - max_exact);
+    const uint32_t large = max_exact + (uint32_t)large_f;
+    return base + (large < half - 1 ? large : half - 1);
+}
+
+void orc_position_bias(float *out, const float *table, size_t seq, size_t nh, uint32_t num_buckets,
+                       uint32_t max_distance) {
+    for (size_t i = 0; i < seq; i++)
+        for (size_t j = 0; j < seq; j++) {
+            const int64_t rel = (int64_t)j - (int64_t)i;
+            const uint32_t bucket = orc_relative_bucket(rel, num_buckets, max_distance);
+            for (size_t h = 0; h < nh; h++) out[h * seq * seq + i * seq + j] = table[bucket * nh + h];
+        }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* par.forRangeMin (src/core/par.zig:18-28) on pthreads: contiguous chunks, the first one on the
+ * calling thread. */
+
+typedef struct {
+    const void *ctx;
+    orc_range_fn f;
+    size_t first, last;
+} range_task;
+
+static void *range_thread(void *p) {
+    range_task *t = (range_task *)p;
+    t->f(t->ctx, t->first, t->last);
+    return NULL;
+}
+
+void orc_for_range_min(size_t threads, size_t n, size_t min_chunk, const void *ctx, orc_range_fn f) {
+    if (min_chunk == 0) min_chunk = 1;
+    size_t chunks = (n + min_chunk - 1) / min_chunk;
+    if (threads < chunks) chunks = threads;
+    if (chunks <= 1) {
+        f(ctx, 0, n);
+        return;
+    }
+    const size_t size = (n + chunks - 1) / chunks;
+    size_t ntasks = 0;
+    for (size_t start = size; start < n; start += size) ntasks++;
+    pthread_t *tid = (pthread_t *)calloc(ntasks ? ntasks : 1, sizeof(pthread_t));
+    range_task *tasks = (range_task *)calloc(ntasks ? ntasks : 1, sizeof(range_task));
+    int *started = (int *)calloc(ntasks ? ntasks : 1, sizeof(int));
+    size_t t = 0;
+    for (size_t start = size; start < n; start += size, t++) {
+        tasks[t] = (range_task){ctx, f, start, start + size < n ? start + size : n};
+        /* Io.async runs the task inline when no thread is free; do the same if creation fails. */
+        if (pthread_create(&tid[t], NULL, range_thread, &tasks[t]) == 0) started[t] = 1;
+        else range_thread(&tasks[t]);
+    }
+    f(ctx, 0, size < n ? size : n);
+    for (t = 0; t < ntasks; t++)
+        if (started[t]) pthread_join(tid[t], NULL);
+    free(started);
+    free(tasks);
+    free(tid);
+}
+
+/* SelfJob.attend (src/chronos_bolt/model.zig:331-345). */
+typedef struct {
+    const float *q, *k, *v;
+    float *o;
+    const float *bias;
+    const uint8_t *key_valid;
+    int keys_all_valid;
+    size_t seq, inner, nh, hd;
+} bolt_self_job;
+
+static void bolt_self_attend(const void *p, size_t first, size_t last) {
+    const bolt_self_job *j = (const bolt_self_job *)p;
+    const size_t seq = j->seq;
+    float *scores = (float *)malloc(seq * seq * sizeof(float));
+    const int mask = orc_mask_pick(0, j->keys_all_valid, 1);
+    const size_t st[4] = {j->inner, j->inner, j->inner, j->inner};
+    for (size_t item = first; item < last; item++) {
+        const size_t r = item / j->nh, h = item % j->nh;
+        const size_t off = r * seq * j->inner + h * j->hd;
+        orc_self_attend(mask, scores, j->q + off, j->k + off, j->v + off, j->o + off, st, seq, j->hd, 1.0f,
+                        j->key_valid + r * seq, j->bias + h * seq * seq);
+    }
+    free(scores);
+}
+
+void orc_bolt_self_attention(size_t threads, const float *q, const float *k, const float *v, float *o,
+                             const float *bias, const uint8_t *key_valid, int keys_all_valid,
+                             size_t nb, size_t seq, size_t inner, size_t nh, size_t hd) {
+    const bolt_self_job job = {q, k, v, o, bias, key_valid, keys_all_valid, seq, inner, nh, hd};
+    orc_for_range_min(threads, nb * nh, 1, &job, bolt_self_attend);
+}
+
+/* CrossJob.attend (src/chronos_bolt/model.zig:360-380). */
+typedef struct {
+    const float *q, *k, *v;
+    float *o;
+    const uint8_t *key_valid;
+    size_t seq, inner, nh, hd;
+} bolt_cross_job;
+
+static void bolt_cross_attend(const void *p, size_t first, size_t last) {
+    const bolt_cross_job *j = (const bolt_cross_job *)p;
+    const size_t seq = j->seq, hd = j->hd;
+    const float mask_min = -FLT_MAX;
+    float *scores = (float *)malloc(seq * sizeof(float));
+    for (size_t item = first; item < last; item++) {
+        const size_t r = item / j->nh, h = item % j->nh;
+        const float *qh = j->q + r * j->inner + h * hd;
+        for (size_t t = 0; t < seq; t++) {
+            const float *kh = j->k + (r * seq + t) * j->inner + h * hd;
+            scores[t] = orc_dot(qh, kh, hd);
+            if (!j->key_valid[r * seq + t]) scores[t] += mask_min;
+        }
+        orc_softmax(scores, seq);
+        float *oh = j->o + r * j->inner + h * hd;
+        memset(oh, 0, hd * sizeof(float));
+        for (size_t t = 0; t < seq; t++)
+            orc_mul_add_in_place(oh, j->v + (r * seq + t) * j->inner + h * hd, hd, scores[t]);
+    }
+    free(scores);
+}
+
+void orc_bolt_cross_attention(size_t threads, const float *q, const float *k, const float *v, float *o,
+                              const uint8_t *key_valid, size_t nb, size_t seq, size_t inner, size_t nh,
+                              size_t hd) {
+    const bolt_cross_job job = {q, k, v, o, key_valid, seq, inner, nh, hd};
+    orc_for_range_min(threads, nb * nh, 1, &job, bolt_cross_attend);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Chronos-2 (src/chronos2/model.zig) */
+
+void orc_chronos2_rope_tables(float *cos_t, float *sin_t, size_t seq, size_t hd, float theta) {
+    const size_t half = hd / 2;
+    float *inv_freq = (float *)malloc((half ? half : 1) * sizeof(float));
+    for (size_t i = 0; i < half; i++) {
+        const float idx = (float)(2 * i);
+        inv_freq[i] = 1.0f / powf(theta, idx / (float)hd);
+    }
+    for (size_t tok = 0; tok < seq; tok++) {
+        const float pos = (float)tok;
+        for (size_t i = 0; i < half; i++) {
+            const float ang = inv_freq[i] * pos;
+            cos_t[tok * half + i] = cosf(ang);
+            sin_t[tok * half + i] = sinf(ang);
+        }
+    }
+    free(inv_freq);
+}
+
+void orc_chronos2_rope(float *q, float *k, const float *cos_t, const float *sin_t, size_t rows,
+                       size_t seq, size_t d, size_t nh, size_t hd) {
+    const size_t half = hd / 2;
+    for (size_t r = 0; r < rows; r++) {
+        const size_t tok = r % seq;
+        const float *cs = cos_t + tok * half, *sn = sin_t + tok * half;
+        for (size_t hh = 0; hh < nh; hh++) {
+            const size_t off = r * d + hh * hd;
+            orc_rope_half(q + off, cs, sn, half);
+            orc_rope_half(k + off, cs, sn, half);
+        }
+    }
+}
+
+typedef struct {
+    const float *q, *k, *v;
+    float *o;
+    const uint8_t *key_valid;
+    int keys_all_valid;
+    size_t seq, d, nh, hd;
+    float scale;
+} c2_time_job;
+
+static void c2_time_attend(const void *p, size_t first, size_t last) {
+    const c2_time_job *j = (const c2_time_job *)p;
+    const size_t seq = j->seq, d = j->d, hd = j->hd;
+    float *scores = (float *)malloc(seq * seq * sizeof(float));
+    const size_t st[4] = {d, d, d, d};
+    for (size_t item = first; item < last; item++) {
+        const size_t r = item / j->nh, hh = item % j->nh;
+        const size_t off = hh * hd, base = r * seq * d;
+        const int mask = orc_mask_pick(0, j->keys_all_valid, 1);
+        orc_self_attend(mask, scores, j->q + base + off, j->k + base + off, j->v + base + off,
+                        j->o + base + off, st, seq, hd, j->scale, j->key_valid + r * seq, NULL);
+    }
+    free(scores);
+}
+
+void orc_chronos2_time_attention(size_t threads, const float *q, const float *k, const float *v, float *o,
+                                 const uint8_t *key_valid, int keys_all_valid, size_t b, size_t seq,
+                                 size_t d, size_t nh, size_t hd, float scale) {
+    const c2_time_job job = {q, k, v, o, key_valid, keys_all_valid, seq, d, nh, hd, scale};
+    orc_for_range_min(threads, b * nh, 1, &job, c2_time_attend);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Timestral (src/timestral/model.zig) */
+
+void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
+                               size_t hd, size_t rope_dim, float theta, const size_t *first_obs) {
+    const size_t half = hd / 2, sl = ne + h;
+    float *inv_freq = (float *)calloc(half ? half : 1, sizeof(float));
+    for (size_t i = 0; i < rope_dim / 2; i++) {
+        const float idx = (float)(2 * i);
+        inv_freq[i] = 1.0f / powf(theta, idx / (float)rope_dim);
+    }
+    for (size_t g = 0; g < groups; g++)
+        for (size_t tok = 0; tok < sl; tok++) {
+            const int64_t time = tok < ne ? (int64_t)tok : (int64_t)(l + tok - ne);
+            const float pos = (float)(time - (int64_t)first_obs[g]);
+            for (size_t i = 0; i < half; i++) {
+                const float ang = inv_freq[i] * pos;
+                cos_t[(g * sl + tok) * half + i] = cosf(ang);
+                sin_t[(g * sl + tok) * half + i] = sinf(ang);
+            }
+        }
+    free(inv_freq);
+}
+
+typedef struct {
+    float *qkv;
+    const float *cos_t, *sin_t;
+    size_t sl, vall, d, nh, hd;
+} ts_rope_job;
+
+static void ts_rope(const void *p, size_t t0, size_t t1) {
+    const ts_rope_job *j = (const ts_rope_job *)p;
+    const size_t half = j->hd / 2, d = j->d;
+    for (size_t idx = t0; idx < t1; idx++) {
+        const size_t r = idx / j->sl, tok = idx % j->sl, g = r / j->vall;
+        const float *cs = j->cos_t + (g * j->sl + tok) * half, *sn = j->sin_t + (g * j->sl + tok) * half;
+        const size_t base = idx * 3 * d;
+        for (size_t hh = 0; hh < j->nh; hh++) {
+            orc_rope_half(j->qkv + base + hh * j->hd, cs, sn, half);
+            orc_rope_half(j->qkv + base + d + hh * j->hd, cs, sn, half);
+        }
+    }
+}
+
+void orc_timestral_rope(size_t threads, float *qkv, const float *cos_t, const float *sin_t, size_t rows,
+                        size_t sl, size_t vall, size_t d, size_t nh, size_t hd) {
+    const ts_rope_job job = {qkv, cos_t, sin_t, sl, vall, d, nh, hd};
+    orc_for_range_min(threads, rows * sl, 16, &job, ts_rope);
+}
+
+typedef struct {
+    const float *qkv;
+    float *o;
+    const uint8_t *key_valid;
+    int keys_all_valid;
+    const uint8_t *bidir;
+    size_t ne, l, h, d, nh, hd;
+} ts_time_job;
+
+static void ts_time_attend(const void *p, size_t first, size_t last) {
+    const ts_time_job *j = (const ts_time_job *)p;
+    const size_t d = j->d, nh = j->nh, hd = j->hd, ne = j->ne, l = j->l, h = j->h, sl = ne + h;
+    const float sm_scale = 1.0f / sqrtf((float)hd);
+    const float ninf = -INFINITY;
+    const size_t cap = ne * ne > h * sl ? ne * ne : h * sl;
+    float *scores = (float *)malloc((cap ? cap : 1) * sizeof(float));
+    const size_t st[4] = {3 * d, 3 * d, 3 * d, d};
+    for (size_t item = first; item < last; item++) {
+        const size_t r = item / nh, hh = item % nh, off = hh * hd;
+        const int bidir = j->bidir ? j->bidir[r] != 0 : 0;
+        const size_t base = r * sl * 3 * d;
+        const float *q = j->qkv + base + off;
+        const float *k = j->qkv + base + d + off;
+        const float *v = j->qkv + base + 2 * d + off;
+        float *o = j->o + r * sl * d + off;
+        const uint8_t *kv = j->key_valid + r * ne;
+
+        const int mask = orc_mask_pick(!bidir, j->keys_all_valid, 0);
+        orc_self_attend(mask, scores, q, k, v, o, st, ne, hd, sm_scale, kv, NULL);
+        orc_gemm_nt(scores, sl, j->qkv + base + ne * 3 * d + off, 3 * d, k, 3 * d, h, sl, hd, sm_scale);
+        if (j->keys_all_valid) {
+            for (size_t jj = 0; jj < h; jj++) {
+                float *row = scores + jj * sl;
+                for (size_t kk = l; kk < ne; kk++) row[kk] = ninf;
+                const size_t end = ne + jj + 1;
+                orc_softmax(row, end);
+                for (size_t kk = end; kk < sl; kk++) row[kk] = 0;
+            }
+        } else {
+            for (size_t jj = 0; jj < h; jj++) {
+                float *row = scores + jj * sl;
+                for (size_t kk = 0; kk < ne; kk++)
+                    if (kk >= l || !kv[kk]) row[kk] = ninf;
+                for (size_t kk = ne + jj + 1; kk < sl; kk++) row[kk] = ninf;
+                orc_softmax(row, sl);
+            }
+        }
+        orc_gemm_nn(o + ne * d, d, scores, sl, v, 3 * d, h, hd, sl);
+    }
+    free(scores);
+}
+
+void orc_timestral_time_attention(size_t threads, const float *qkv, float *o, const uint8_t *key_valid,
+                                  int keys_all_valid, const uint8_t *bidir, size_t rows, size_t ne,
+                                  size_t l, size_t h, size_t d, size_t nh, size_t hd) {
+    const ts_time_job job = {qkv, o, key_valid, keys_all_valid, bidir, ne, l, h, d, nh, hd};
+    orc_for_range_min(threads, rows * nh, 1, &job, ts_time_attend);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Generic batched selfAttend. */
+
+typedef struct {
+    int mask;
+    const float *q, *k, *v;
+    float *o;
+    size_t q_tok, q_batch, k_tok, k_batch, v_tok, v_batch, o_tok, o_batch;
+    const uint8_t *key_valid;
+    size_t kv_batch;
+    const float *bias;
+    size_t nh, n, hd;
+    float scale;
+} batched_job;
+
+static void batched_attend(const void *p, size_t first, size_t last) {
+    const batched_job *j = (const batched_job *)p;
+    const size_t n = j->n, hd = j->hd;
+    float *scores = (float *)malloc((n > 0 ? n * n : 1) * sizeof(float));
+    const size_t st[4] = {j->q_tok, j->k_tok, j->v_tok, j->o_tok};
+    for (size_t item = first; item < last; item++) {
+        const size_t b = item / j->nh, h = item % j->nh;
+        orc_self_attend(j->mask, scores, j->q + b * j->q_batch + h * hd, j->k + b * j->k_batch + h * hd,
+                        j->v + b * j->v_batch + h * hd, j->o + b * j->o_batch + h * hd, st, n, hd, j->scale,
+                        j->key_valid ? j->key_valid + b * j->kv_batch : NULL,
+                        j->bias ? j->bias + h * n * n : NULL);
+    }
+    free(scores);
+}
+
+void orc_batched_self_attend(size_t threads, int mask, const float *q, size_t q_tok, size_t q_batch,
+                             const float *k, size_t k_tok, size_t k_batch, const float *v, size_t v_tok,
+                             size_t v_batch, float *o, size_t o_tok, size_t o_batch,
+                             const uint8_t *key_valid, size_t kv_batch, const float *bias,
+                             size_t nb, size_t nh, size_t n, size_t hd, float scale) {
+    const batched_job job = {mask,    q,       k,       v,         o,        q_tok, q_batch, k_tok,
+                             k_batch, v_tok,   v_batch, o_tok,     o_batch,  key_valid, kv_batch,
+                             bias,    nh,      n,       hd,        scale};
+    orc_for_range_min(threads, nb * nh, 1, &job, batched_attend);
+}

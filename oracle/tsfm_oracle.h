@@ -1,0 +1,124 @@
+/*
+ * tsfm_oracle.h -- CPU oracle for the tsfm-zig attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: the parity tests, the
+ * smoke check and the CPU-baseline leg of bench.py call it. Product code never
+ * links, loads or calls it, and nothing falls back to it.
+ *
+ * Every function restates one piece of the reference Zig code (path:line under
+ * the reference checkout) in C with the same arithmetic: the same operation
+ * order, fused multiply-adds exactly where Zig uses @mulAdd, and an ordered
+ * lane reduction where Zig uses @reduce(.Add). The SIMD lane count is a
+ * compile-time constant (ORC_LANES), as `nn.lanes` is in the reference
+ * (src/core/nn.zig:296, std.simd.suggestVectorLength(f32)).
+ *
+ * How each function is pinned (golden vectors, known-answer tests, closed
+ * forms) is listed in tests/test_oracle.py; a function that none of those
+ * pins is marked "parity unpinned" below. Currently every exported function
+ * has at least one pin.
+ */
+#ifndef TSFM_ORACLE_H
+#define TSFM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* attn.Mask declaration order (src/core/attn.zig:10-21). */
+enum { ORC_FULL = 0, ORC_KEYS_ADDITIVE = 1, ORC_CAUSAL = 2, ORC_CAUSAL_KEYS = 3, ORC_FULL_KEYS = 4 };
+
+int orc_lanes(void);
+
+/* nn.expVec, one lane (src/core/nn.zig:344-359). */
+float orc_exp_vec(float x);
+/* nn.gemmNT builtin path (src/core/nn.zig:49-60, 68-162). */
+void orc_gemm_nt(float *cc, size_t ldc, const float *a, size_t lda, const float *b, size_t ldb,
+                 size_t m, size_t n, size_t k, float alpha);
+/* nn.gemmNN builtin path (src/core/nn.zig:165-239). */
+void orc_gemm_nn(float *cc, size_t ldc, const float *a, size_t lda, const float *b, size_t ldb,
+                 size_t m, size_t n, size_t k);
+/* nn.softmax (src/core/nn.zig:470-505). */
+void orc_softmax(float *row, size_t n);
+/* nn.dot (src/core/nn.zig:328-340). */
+float orc_dot(const float *a, const float *b, size_t n);
+/* nn.addInPlace / nn.mulAddInPlace (src/core/nn.zig:302-324). */
+void orc_add_in_place(float *dst, const float *src, size_t n);
+void orc_mul_add_in_place(float *dst, const float *src, size_t n, float scalar);
+/* nn.ropeHalf (src/core/nn.zig:448-467). */
+void orc_rope_half(float *x, const float *cos_t, const float *sin_t, size_t half);
+
+/* attn.Mask.pick (src/core/attn.zig:24-28). */
+int orc_mask_pick(int causal, int all_keys_valid, int additive);
+/* attn.maskedSoftmax (src/core/attn.zig:35-67). key_valid: n bytes (Zig bool). */
+void orc_masked_softmax(int mask, float *scores, size_t n, const uint8_t *key_valid);
+/* attn.selfAttend (src/core/attn.zig:72-96). st = {q, k, v, o} token strides in floats. */
+void orc_self_attend(int mask, float *scores, const float *q, const float *k, const float *v, float *o,
+                     const size_t st[4], size_t n, size_t hd, float scale, const uint8_t *key_valid,
+                     const float *bias);
+/* attn.zig's float64 naive reference (src/core/attn.zig:121-154); o is n x hd, dense. */
+void orc_reference_attend_f64(int mask, double *o, const float *q, const float *k, const float *v,
+                              const size_t st[4], size_t n, size_t hd, double scale,
+                              const uint8_t *key_valid, const float *bias);
+
+/* T5 relative-position bucket (src/chronos_bolt/model.zig:74-85). */
+uint32_t orc_relative_bucket(int64_t rel, uint32_t num_buckets, uint32_t max_distance);
+/* Model.positionBias (src/chronos_bolt/model.zig:195-205): out (nh, seq, seq) from table (buckets, nh). */
+void orc_position_bias(float *out, const float *table, size_t seq, size_t nh, uint32_t num_buckets,
+                       uint32_t max_distance);
+
+/* par.forRangeMin over pthreads (src/core/par.zig:18-28). */
+typedef void (*orc_range_fn)(const void *ctx, size_t first, size_t last);
+void orc_for_range_min(size_t threads, size_t n, size_t min_chunk, const void *ctx, orc_range_fn f);
+
+/* Chronos-Bolt encoder self-attention: forRange(nb*nh, SelfJob.attend)
+ * (src/chronos_bolt/model.zig:242-243, 317-346). q/k/v/o are (nb, seq, inner). */
+void orc_bolt_self_attention(size_t threads, const float *q, const float *k, const float *v, float *o,
+                             const float *bias, const uint8_t *key_valid, int keys_all_valid,
+                             size_t nb, size_t seq, size_t inner, size_t nh, size_t hd);
+/* Chronos-Bolt decoder cross-attention: forRange(nb*nh, CrossJob.attend)
+ * (src/chronos_bolt/model.zig:296-297, 349-381). q/o (nb, inner); k/v (nb, seq, inner). */
+void orc_bolt_cross_attention(size_t threads, const float *q, const float *k, const float *v, float *o,
+                              const uint8_t *key_valid, size_t nb, size_t seq, size_t inner, size_t nh,
+                              size_t hd);
+
+/* Chronos-2 RoPE tables (src/chronos2/model.zig:107-113, 178-187): (seq, hd/2) each. */
+void orc_chronos2_rope_tables(float *cos_t, float *sin_t, size_t seq, size_t hd, float theta);
+/* Chronos-2 serial RoPE loop over q and k (src/chronos2/model.zig:236-245), in place. */
+void orc_chronos2_rope(float *q, float *k, const float *cos_t, const float *sin_t, size_t rows,
+                       size_t seq, size_t d, size_t nh, size_t hd);
+/* Chronos-2 time attention: forRange(b*nh, TimeJob.attend) (src/chronos2/model.zig:260, 277-309).
+ * The model passes scale 1.0 (:306); `scale` is a parameter so other scales can be checked. */
+void orc_chronos2_time_attention(size_t threads, const float *q, const float *k, const float *v, float *o,
+                                 const uint8_t *key_valid, int keys_all_valid, size_t b, size_t seq,
+                                 size_t d, size_t nh, size_t hd, float scale);
+
+/* Timestral RoPE tables (src/timestral/model.zig:180-188, 447-463): (groups, sl, hd/2).
+ * first_obs: per group; rope_dim = rotated dims (partial RoPE). */
+void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
+                               size_t hd, size_t rope_dim, float theta, const size_t *first_obs);
+/* Timestral TimeJob.rope (src/timestral/model.zig:558-577), in place on the fused qkv buffer. */
+void orc_timestral_rope(size_t threads, float *qkv, const float *cos_t, const float *sin_t, size_t rows,
+                        size_t sl, size_t vall, size_t d, size_t nh, size_t hd);
+/* Timestral TimeJob.attend (src/timestral/model.zig:580-635). qkv (rows, sl, 3d) in the
+ * permuted (token, qkv, head, hd) layout, o (rows, sl, d). bidir: per-row flag (known-future
+ * covariate rows), may be NULL. */
+void orc_timestral_time_attention(size_t threads, const float *qkv, float *o, const uint8_t *key_valid,
+                                  int keys_all_valid, const uint8_t *bidir, size_t rows, size_t ne,
+                                  size_t l, size_t h, size_t d, size_t nh, size_t hd);
+
+/* Batched selfAttend over (b, h) items with (token, head, dim) layouts: the generic form of
+ * the three family jobs above, used by the tests for shapes the families do not fix.
+ * q/k/v/o strides: token stride and batch stride in floats; head h at +h*hd. */
+void orc_batched_self_attend(size_t threads, int mask, const float *q, size_t q_tok, size_t q_batch,
+                             const float *k, size_t k_tok, size_t k_batch, const float *v, size_t v_tok,
+                             size_t v_batch, float *o, size_t o_tok, size_t o_batch,
+                             const uint8_t *key_valid, size_t kv_batch, const float *bias,
+                             size_t nb, size_t nh, size_t n, size_t hd, float scale);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,146 @@
+"""ctypes wrapper of the CPU oracle (oracle/liboracle_l*.so) for the tests and the CPU baseline.
+
+Test infrastructure: the checker, never the thing measured or shipped.
+"""
+import ctypes
+
+import numpy as np
+
+ORC_FULL, ORC_KEYS_ADDITIVE, ORC_CAUSAL, ORC_CAUSAL_KEYS, ORC_FULL_KEYS = range(5)
+
+_sz = ctypes.c_size_t
+_vp = ctypes.c_void_p
+_f = ctypes.c_float
+
+
+def ptr(a):
+    if a is None:
+        return None
+    assert isinstance(a, np.ndarray) and a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous numpy arrays"
+    return a.ctypes.data
+
+
+class Oracle:
+    def __init__(self, path):
+        self.path = str(path)
+        L = self.lib = ctypes.CDLL(self.path)
+        L.orc_lanes.restype = ctypes.c_int
+        L.orc_exp_vec.argtypes = [_f]
+        L.orc_exp_vec.restype = _f
+        L.orc_gemm_nt.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
+        L.orc_gemm_nn.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz]
+        L.orc_softmax.argtypes = [_vp, _sz]
+        L.orc_dot.argtypes = [_vp, _vp, _sz]
+        L.orc_dot.restype = _f
+        L.orc_rope_half.argtypes = [_vp, _vp, _vp, _sz]
+        L.orc_mask_pick.argtypes = [ctypes.c_int] * 3
+        L.orc_mask_pick.restype = ctypes.c_int
+        L.orc_masked_softmax.argtypes = [ctypes.c_int, _vp, _sz, _vp]
+        L.orc_self_attend.argtypes = [ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _vp, _vp]
+        L.orc_reference_attend_f64.argtypes = [ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _sz, _sz, ctypes.c_double, _vp, _vp]
+        L.orc_relative_bucket.argtypes = [ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint32]
+        L.orc_relative_bucket.restype = ctypes.c_uint32
+        L.orc_position_bias.argtypes = [_vp, _vp, _sz, _sz, ctypes.c_uint32, ctypes.c_uint32]
+        L.orc_bolt_self_attention.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _sz, _sz]
+        L.orc_bolt_cross_attention.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz]
+        L.orc_chronos2_rope_tables.argtypes = [_vp, _vp, _sz, _sz, _f]
+        L.orc_chronos2_rope.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz]
+        L.orc_chronos2_time_attention.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _sz, _sz, _f]
+        L.orc_timestral_rope_tables.argtypes = [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _f, _vp]
+        L.orc_timestral_rope.argtypes = [_sz, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.orc_timestral_time_attention.argtypes = [_sz, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.orc_batched_self_attend.argtypes = [_sz, ctypes.c_int, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz,
+                                              _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
+
+    @property
+    def lanes(self):
+        return self.lib.orc_lanes()
+
+    # ---- nn.zig ----
+    def exp_vec(self, x):
+        return np.float32(self.lib.orc_exp_vec(float(x)))
+
+    def gemm_nt(self, c, ldc, a, lda, b, ldb, m, n, k, alpha):
+        self.lib.orc_gemm_nt(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k, alpha)
+
+    def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
+        self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)
+
+    def softmax(self, row):
+        self.lib.orc_softmax(ptr(row), row.size)
+
+    def dot(self, a, b):
+        return np.float32(self.lib.orc_dot(ptr(a), ptr(b), min(a.size, b.size)))
+
+    def rope_half(self, x, cos_t, sin_t, half):
+        self.lib.orc_rope_half(ptr(x), ptr(cos_t), ptr(sin_t), half)
+
+    # ---- attn.zig ----
+    def mask_pick(self, causal, all_valid, additive):
+        return self.lib.orc_mask_pick(int(causal), int(all_valid), int(additive))
+
+    def masked_softmax(self, mask, scores, n, key_valid):
+        self.lib.orc_masked_softmax(mask, ptr(scores), n, ptr(key_valid))
+
+    def self_attend(self, mask, q, k, v, o, st, n, hd, scale, key_valid=None, bias=None):
+        scores = np.empty(max(n * n, 1), np.float32)
+        st_arr = (ctypes.c_size_t * 4)(*st)
+        self.lib.orc_self_attend(mask, ptr(scores), ptr(q), ptr(k), ptr(v), ptr(o), st_arr, n, hd, scale,
+                                 ptr(key_valid), ptr(bias))
+
+    def reference_attend_f64(self, mask, q, k, v, st, n, hd, scale, key_valid=None, bias=None):
+        o = np.empty(n * hd, np.float64)
+        st_arr = (ctypes.c_size_t * 4)(*st)
+        kv = key_valid if key_valid is not None else np.ones(n, np.uint8)
+        self.lib.orc_reference_attend_f64(mask, ptr(o), ptr(q), ptr(k), ptr(v), st_arr, n, hd, scale, ptr(kv), ptr(bias))
+        return o.reshape(n, hd)
+
+    # ---- families ----
+    def relative_bucket(self, rel, nb, maxd):
+        return self.lib.orc_relative_bucket(rel, nb, maxd)
+
+    def position_bias(self, table, seq, nh, nb, maxd):
+        out = np.empty(nh * seq * seq, np.float32)
+        self.lib.orc_position_bias(ptr(out), ptr(table), seq, nh, nb, maxd)
+        return out
+
+    def bolt_self_attention(self, threads, q, k, v, o, bias, key_valid, keys_all_valid, nb, seq, inner, nh, hd):
+        self.lib.orc_bolt_self_attention(threads, ptr(q), ptr(k), ptr(v), ptr(o), ptr(bias), ptr(key_valid),
+                                         int(keys_all_valid), nb, seq, inner, nh, hd)
+
+    def bolt_cross_attention(self, threads, q, k, v, o, key_valid, nb, seq, inner, nh, hd):
+        self.lib.orc_bolt_cross_attention(threads, ptr(q), ptr(k), ptr(v), ptr(o), ptr(key_valid), nb, seq, inner, nh, hd)
+
+    def chronos2_rope_tables(self, seq, hd, theta=10000.0):
+        c = np.empty(seq * (hd // 2), np.float32)
+        s = np.empty_like(c)
+        self.lib.orc_chronos2_rope_tables(ptr(c), ptr(s), seq, hd, theta)
+        return c, s
+
+    def chronos2_rope(self, q, k, cos_t, sin_t, rows, seq, d, nh, hd):
+        self.lib.orc_chronos2_rope(ptr(q), ptr(k), ptr(cos_t), ptr(sin_t), rows, seq, d, nh, hd)
+
+    def chronos2_time_attention(self, threads, q, k, v, o, key_valid, keys_all_valid, b, seq, d, nh, hd, scale):
+        self.lib.orc_chronos2_time_attention(threads, ptr(q), ptr(k), ptr(v), ptr(o), ptr(key_valid),
+                                             int(keys_all_valid), b, seq, d, nh, hd, scale)
+
+    def timestral_rope_tables(self, groups, ne, l, h, hd, rope_dim, theta, first_obs):
+        sl = ne + h
+        c = np.empty(groups * sl * (hd // 2), np.float32)
+        s = np.empty_like(c)
+        fo = np.ascontiguousarray(first_obs, dtype=np.uintp)
+        self.lib.orc_timestral_rope_tables(ptr(c), ptr(s), groups, ne, l, h, hd, rope_dim, theta, ptr(fo))
+        return c, s
+
+    def timestral_rope(self, threads, qkv, cos_t, sin_t, rows, sl, vall, d, nh, hd):
+        self.lib.orc_timestral_rope(threads, ptr(qkv), ptr(cos_t), ptr(sin_t), rows, sl, vall, d, nh, hd)
+
+    def timestral_time_attention(self, threads, qkv, o, key_valid, keys_all_valid, bidir, rows, ne, l, h, d, nh, hd):
+        self.lib.orc_timestral_time_attention(threads, ptr(qkv), ptr(o), ptr(key_valid), int(keys_all_valid),
+                                              ptr(bidir), rows, ne, l, h, d, nh, hd)
+
+    def batched_self_attend(self, threads, mask, q, q_tok, q_batch, k, k_tok, k_batch, v, v_tok, v_batch, o, o_tok,
+                            o_batch, key_valid, kv_batch, bias, nb, nh, n, hd, scale):
+        self.lib.orc_batched_self_attend(threads, mask, ptr(q), q_tok, q_batch, ptr(k), k_tok, k_batch, ptr(v), v_tok,
+                                         v_batch, ptr(o), o_tok, o_batch, ptr(key_valid), kv_batch, ptr(bias), nb, nh,
+                                         n, hd, scale)

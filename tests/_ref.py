@@ -1,0 +1,84 @@
+"""Independent float64 attention in numpy, the parity metric, and seeded input builders.
+
+`naive_attend` is written from the mathematics (softmax over an explicit allowed-key matrix),
+not from the reference code, so it can pin the oracle: a dropped scale, a wrong mask index or a
+transposed operand in the oracle shows up as a disagreement with it.
+"""
+import numpy as np
+
+FLT_MAX = np.finfo(np.float32).max
+
+
+def scaled_err(got, ref):
+    """max |got - ref| / max(|ref|, 1): tests/compare.py:15 of the reference."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1.0))) if ref.size else 0.0
+
+
+def allowed_matrix(mask, n_q, n_k, key_valid=None, q_pos0=0, ctx_keys=0, chain_start=0):
+    """Boolean (n_q, n_k): which keys each query reads under a mask (attn.Mask semantics; for
+    KEYS_ADDITIVE the invalid keys, whose weight is ~1e-38 in the reference)."""
+    i = np.arange(n_q)[:, None] + q_pos0
+    j = np.arange(n_k)[None, :]
+    kv = np.ones(n_k, bool) if key_valid is None else np.asarray(key_valid[:n_k], bool)
+    if mask == 0:
+        return np.ones((n_q, n_k), bool)
+    if mask == 1:
+        return np.broadcast_to(kv[None, :], (n_q, n_k)).copy()
+    if mask == 2:
+        return j <= i
+    if mask == 3:
+        return (j == i) | (kv[None, :] & (j <= i))
+    if mask == 4:
+        return (j == i) | kv[None, :]
+    if mask == 5:
+        kvc = np.zeros(n_k, bool)
+        kvc[: min(ctx_keys, n_k)] = kv[: min(ctx_keys, n_k)] if key_valid is not None else True
+        return (kvc[None, :] & (j < ctx_keys)) | ((j >= chain_start) & (j <= i))
+    raise ValueError(mask)
+
+
+def naive_attend(q, k, v, allowed, scale, bias=None):
+    """float64 o = softmax over allowed keys of (scale q.k + bias), times v. Rows with no allowed
+    key are uniform over every key (what the additive -FLT_MAX mask gives in that case)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    s = scale * (q @ k.T)
+    if bias is not None:
+        s = s + np.asarray(bias, np.float64)
+    allowed = np.asarray(allowed, bool).copy()
+    empty = ~allowed.any(axis=1)
+    allowed[empty, :] = True
+    s = np.where(allowed, s, -np.inf)
+    s = s - s.max(axis=1, keepdims=True)
+    p = np.where(allowed, np.exp(s), 0.0)
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ v
+
+
+def bf16_round(x):
+    """Round float32 to bfloat16 (nearest-even), returned as float32 values."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def f16_round(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def t5_bias_table(rng, buckets, heads):
+    return (rng.standard_normal((buckets, heads)) * 0.1).astype(np.float32)
+
+
+def left_pad_valid(rng, batch, n, max_pad, tail_valid=0):
+    """Per-row key validity: the first pad_b ~ U{0..max_pad} of the first n - tail_valid keys are
+    invalid (left-truncated / missing patches); the last tail_valid keys (REG, future) are valid."""
+    kv = np.ones((batch, n), np.uint8)
+    pads = rng.integers(0, max_pad + 1, size=batch)
+    for b, p in enumerate(pads):
+        kv[b, : min(p, n - tail_valid)] = 0
+    return kv

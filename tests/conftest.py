@@ -1,0 +1,61 @@
+"""pytest configuration: the `gpu` marker, import paths, and the built libraries."""
+import os
+import pathlib
+import subprocess
+import sys
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+for p in (ROOT / "tsfm-zig_amd", ROOT / "tests"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a gfx950 (MI355X) GPU")
+
+
+def _ensure_oracle():
+    """The oracle is plain C; build it here if build() has not run yet (gcc only)."""
+    lib = ROOT / "oracle" / "liboracle_l8.so"
+    if not lib.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle")], check=True, capture_output=True)
+
+
+@pytest.fixture(scope="session")
+def orc():
+    _ensure_oracle()
+    import _oracle
+
+    return _oracle.Oracle(ROOT / "oracle" / "liboracle_l8.so")
+
+
+@pytest.fixture(scope="session")
+def orc16():
+    _ensure_oracle()
+    import _oracle
+
+    return _oracle.Oracle(ROOT / "oracle" / "liboracle_l16.so")
+
+
+@pytest.fixture(scope="session")
+def ta():
+    """The product binding (tsfm-zig_amd/tsfm_attn); fails if the library is not built."""
+    import tsfm_attn
+
+    tsfm_attn.load()
+    return tsfm_attn
+
+
+@pytest.fixture(scope="session")
+def gpu_ready(ta):
+    """For gpu tests: the library must see a gfx950 device; anything else is a failure, not a skip."""
+    if os.environ.get("TSFM_HIP_DISABLE"):
+        pytest.fail("TSFM_HIP_DISABLE is set in a gpu test run")
+    if not ta.available():
+        pytest.fail(f"libtsfm_attn sees no usable gfx950 device: {ta.last_error()}")
+    import torch
+
+    assert torch.cuda.is_available()
+    return True

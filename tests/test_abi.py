@@ -1,0 +1,125 @@
+"""CPU-side checks of the C ABI (no GPU needed): exports, host functions, argument validation and
+the "return non-zero so the caller uses the CPU" contract (src/platform/backend.zig:33-36)."""
+import ctypes
+import json
+import os
+import pathlib
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tsfm_attn.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tsfm_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree(ta):
+    assert sorted(ta.EXPORTS) == declared_functions()
+
+
+def test_library_exports_every_declared_symbol(ta):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ta.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT (tsfm_\w+)", out.stdout))
+    missing = [f for f in declared_functions() if f not in exported]
+    assert not missing, missing
+
+
+def test_args_struct_layout_matches_header(ta):
+    """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
+    fields = [f[0] for f in ta.AttnArgs._fields_]
+    src = "#include <stdio.h>\n#include <stddef.h>\n#include \"tsfm_attn.h\"\nint main(void){\n"
+    src += 'printf("%zu\\n", sizeof(tsfm_attn_args));\n'
+    for f in fields:
+        src += f'printf("%zu\\n", offsetof(tsfm_attn_args, {f}));\n'
+    src += "return 0;}\n"
+    tmp = pathlib.Path(os.environ.get("TMPDIR", "/tmp")) / f"tsfm_layout_{os.getpid()}"
+    tmp.mkdir(exist_ok=True)
+    (tmp / "l.c").write_text(src)
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), "-o", str(tmp / "l"), str(tmp / "l.c")], check=True)
+    got = [int(x) for x in subprocess.run([str(tmp / "l")], capture_output=True, text=True, check=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(ta.AttnArgs)
+    assert got[1:] == [getattr(ta.AttnArgs, f).offset for f in fields]
+
+
+def test_t5_bucket_host_function_golden(ta):
+    g = json.loads((ROOT / "tests" / "golden" / "t5_buckets_32_128.json").read_text())
+    lib = ta.load()
+    got = [lib.tsfm_t5_relative_bucket(g["rel_first"] + i, 32, 128) for i in range(len(g["buckets"]))]
+    assert got == g["buckets"]
+    # The table form used by the kernel: out[t] = bucket(t - (n_q - 1)).
+    n_q, n_k = 129, 129
+    out = np.zeros(n_q + n_k - 1, np.int32)
+    assert lib.tsfm_t5_bucket_table(out.ctypes.data, n_q, n_k, 32, 128) == ta.OK
+    rel = np.arange(-(n_q - 1), n_k)
+    sel = (rel >= -140) & (rel <= 140)
+    assert out[sel].tolist() == [g["buckets"][r + 140] for r in rel[sel]]
+
+
+def test_mask_pick_mirror():
+    sys.path.insert(0, str(ROOT / "tsfm-zig_amd"))
+    import tsfm_attn
+
+    g = json.loads((ROOT / "tests" / "golden" / "mask_pick.json").read_text())
+    for c in g["cases"]:
+        assert tsfm_attn.Mask.pick(c["causal"], c["all_keys_valid"], c["additive"]).name.lower() == c["mask"]
+
+
+def _valid_host_args(ta, **over):
+    n, H = 8, 2
+    bufs = {name: np.zeros(n * H * 64, np.float32) for name in "qkvo"}
+    kw = dict(q=bufs["q"], k=bufs["k"], v=bufs["v"], o=bufs["o"], mask=ta.Mask.FULL, batch=1, heads=H, n_q=n,
+              n_k=n, q_tok=H * 64, q_batch=0, k_tok=H * 64, k_batch=0, v_tok=H * 64, v_batch=0, o_tok=H * 64,
+              o_batch=0, scale=0.125)
+    kw.update(over)
+    return ta.make_args(**kw), bufs
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(head_dim=32), 2),
+    (dict(mask=7), 3),
+    (dict(q_tok=130), 2),
+    (dict(mask=1), 3),            # keys_additive without key_valid
+    (dict(q_pos0=-1), 3),
+])
+def test_validation_codes(ta, over, code):
+    args, _ = _valid_host_args(ta, **over)
+    assert ta.fwd(args) == code
+    assert ta.last_error()
+
+
+def test_empty_batch_is_a_no_op(ta):
+    args, _ = _valid_host_args(ta, batch=0)
+    assert ta.fwd(args) == ta.OK
+
+
+def test_disabled_library_reports_unavailable():
+    """With TSFM_HIP_DISABLE set every call returns E_UNAVAILABLE (the CPU-fallback signal), in a
+    fresh process so the one-time initialisation sees the variable."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import numpy as np, tsfm_attn as ta\n"
+        "assert ta.available() is False\n"
+        "b = {c: np.zeros(8*64, np.float32) for c in 'qkvo'}\n"
+        "a = ta.make_args(q=b['q'], k=b['k'], v=b['v'], o=b['o'], mask=0, batch=1, heads=1, n_q=8, n_k=8,"
+        " q_tok=64, q_batch=0, k_tok=64, k_batch=0, v_tok=64, v_batch=0, o_tok=64, o_batch=0, scale=1.0)\n"
+        "rc = ta.fwd(a)\n"
+        "assert rc == ta.E_UNAVAILABLE, rc\n"
+        "assert 'TSFM_HIP_DISABLE' in ta.last_error()\n"
+    ) % str(ROOT / "tsfm-zig_amd")
+    env = dict(os.environ, TSFM_HIP_DISABLE="1")
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_kv_cache_rejects_f32(ta):
+    lib = ta.load()
+    h = ctypes.c_void_p()
+    assert lib.tsfm_kv_create(ctypes.byref(h), ta.DTYPE_F32, 1, 1, 64, 32) == ta.E_UNSUPPORTED
+    assert not h.value

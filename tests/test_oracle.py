@@ -1,0 +1,416 @@
+"""Pins the CPU oracle (oracle/tsfm_oracle.c) before it is trusted as the GPU checker.
+
+Each oracle function is checked against at least one of: the reference's golden vectors
+(tests/golden/*.json), the reference's own known-answer test restated (every mask, with and
+without bias, against a float64 naive reference: src/core/attn.zig:156-189), an independent
+float64 numpy formulation (tests/_ref.py), or a closed form / invariant chosen so that a plausible
+slip (dropped scale, j < i instead of j <= i, bias after mask, transposed operand, wrong RoPE pair)
+fails.
+"""
+import json
+import pathlib
+
+import numpy as np
+import pytest
+
+import _ref
+from _oracle import ORC_CAUSAL, ORC_CAUSAL_KEYS, ORC_FULL, ORC_FULL_KEYS, ORC_KEYS_ADDITIVE
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+MASKS = [ORC_FULL, ORC_KEYS_ADDITIVE, ORC_CAUSAL, ORC_CAUSAL_KEYS, ORC_FULL_KEYS]
+
+
+# ---- golden vectors ----------------------------------------------------------------------------
+
+
+def test_relative_bucket_golden(orc):
+    g = json.loads((GOLDEN / "t5_buckets_32_128.json").read_text())
+    got = [orc.relative_bucket(g["rel_first"] + i, g["num_buckets"], g["max_distance"]) for i in range(len(g["buckets"]))]
+    assert got == g["buckets"]
+
+
+def test_mask_pick_truth_table(orc):
+    g = json.loads((GOLDEN / "mask_pick.json").read_text())
+    names = {"full": ORC_FULL, "keys_additive": ORC_KEYS_ADDITIVE, "causal": ORC_CAUSAL,
+             "causal_keys": ORC_CAUSAL_KEYS, "full_keys": ORC_FULL_KEYS}
+    for c in g["cases"]:
+        assert orc.mask_pick(c["causal"], c["all_keys_valid"], c["additive"]) == names[c["mask"]]
+
+
+# ---- the reference's known-answer test (src/core/attn.zig:156-189) ------------------------------
+
+
+def _kat_inputs():
+    n, hd = 11, 8
+    ld = 3 * hd + 2  # fused-qkv-like stride with padding
+    rng = np.random.default_rng(0x7A11)
+    qkv = (rng.random(n * ld, dtype=np.float32) * 2 - 1).astype(np.float32)
+    key_valid = np.array([i % 3 != 1 for i in range(n)], np.uint8)
+    bias = (rng.random(n * n, dtype=np.float32) * 4 - 2).astype(np.float32)
+    return n, hd, ld, qkv, key_valid, bias
+
+
+@pytest.mark.parametrize("mask", MASKS)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_self_attend_matches_f64_reference(orc, mask, with_bias):
+    n, hd, ld, qkv, key_valid, bias = _kat_inputs()
+    st = (ld, ld, ld, hd)
+    q, k, v = qkv[0:], qkv[hd:], qkv[2 * hd:]
+    got = np.zeros(n * hd, np.float32)
+    orc.self_attend(mask, q, k, v, got, st, n, hd, 0.35, key_valid, bias if with_bias else None)
+    want = orc.reference_attend_f64(mask, q, k, v, st, n, hd, 0.35, key_valid, bias if with_bias else None)
+    np.testing.assert_allclose(got.reshape(n, hd), want, atol=1e-4, rtol=0)
+    # And the float64 reference itself against the independent numpy formulation.
+    Q = np.stack([qkv[i * ld: i * ld + hd] for i in range(n)])
+    K = np.stack([qkv[i * ld + hd: i * ld + 2 * hd] for i in range(n)])
+    V = np.stack([qkv[i * ld + 2 * hd: i * ld + 3 * hd] for i in range(n)])
+    np_ref = _ref.naive_attend(Q, K, V, _ref.allowed_matrix(mask, n, n, key_valid), 0.35,
+                               bias.reshape(n, n) if with_bias else None)
+    np.testing.assert_allclose(want, np_ref, atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("mask", MASKS)
+def test_self_attend_head_sized(orc, mask):
+    """Head-sized case (n = 129, hd = 64, the Chronos-Bolt shape) at the f32 tolerance."""
+    rng = np.random.default_rng(1)
+    n, hd, ld = 129, 64, 3 * 64
+    qkv = rng.standard_normal(n * ld).astype(np.float32)
+    kv = (rng.random(n) > 0.3).astype(np.uint8)
+    kv[-1] = 1
+    bias = (rng.standard_normal(n * n) * 0.5).astype(np.float32)
+    got = np.zeros(n * hd, np.float32)
+    orc.self_attend(mask, qkv[0:], qkv[hd:], qkv[2 * hd:], got, (ld, ld, ld, hd), n, hd, 0.125, kv, bias)
+    Q = qkv.reshape(n, ld)[:, :hd]
+    K = qkv.reshape(n, ld)[:, hd:2 * hd]
+    V = qkv.reshape(n, ld)[:, 2 * hd:]
+    want = _ref.naive_attend(Q, K, V, _ref.allowed_matrix(mask, n, n, kv), 0.125, bias.reshape(n, n))
+    assert _ref.scaled_err(got.reshape(n, hd), want) < 2e-6
+
+
+# ---- closed forms and invariants ---------------------------------------------------------------
+
+
+def _qkv(rng, n, hd):
+    return [rng.standard_normal(n * hd).astype(np.float32) for _ in range(3)]
+
+
+@pytest.mark.parametrize("mask", MASKS)
+def test_single_key_returns_v(orc, mask):
+    """Softmax over one key is exactly 1, so o == v bit for bit (src/chronos2/model.zig:264-269)."""
+    rng = np.random.default_rng(2)
+    q, k, v = _qkv(rng, 1, 64)
+    o = np.zeros(64, np.float32)
+    orc.self_attend(mask, q, k, v, o, (64, 64, 64, 64), 1, 64, 0.7, np.ones(1, np.uint8), None)
+    assert np.array_equal(o, v)
+
+
+def test_zero_query_gives_mean_of_allowed_values(orc):
+    rng = np.random.default_rng(3)
+    n, hd = 37, 64
+    _, k, v = _qkv(rng, n, hd)
+    q = np.zeros(n * hd, np.float32)
+    kv = (rng.random(n) > 0.5).astype(np.uint8)
+    kv[0] = 1
+    for mask in (ORC_FULL, ORC_FULL_KEYS):
+        o = np.zeros(n * hd, np.float32)
+        orc.self_attend(mask, q, k, v, o, (hd,) * 4, n, hd, 1.0, kv, None)
+        V = v.reshape(n, hd)
+        for i in (0, 5, n - 1):
+            sel = np.ones(n, bool) if mask == ORC_FULL else (kv.astype(bool) | (np.arange(n) == i))
+            np.testing.assert_allclose(o.reshape(n, hd)[i], V[sel].mean(axis=0), atol=2e-6)
+
+
+def test_constant_values_pass_through(orc):
+    rng = np.random.default_rng(4)
+    n, hd = 50, 64
+    q, k, _ = _qkv(rng, n, hd)
+    row = rng.standard_normal(hd).astype(np.float32)
+    v = np.tile(row, n)
+    for mask in MASKS:
+        o = np.zeros(n * hd, np.float32)
+        orc.self_attend(mask, q, k, v, o, (hd,) * 4, n, hd, 0.125, np.ones(n, np.uint8), None)
+        np.testing.assert_allclose(o.reshape(n, hd), np.tile(row, (n, 1)), rtol=2e-6, atol=2e-6)
+
+
+def test_causal_first_row_is_v0(orc):
+    rng = np.random.default_rng(5)
+    n, hd = 20, 64
+    q, k, v = _qkv(rng, n, hd)
+    o = np.zeros(n * hd, np.float32)
+    orc.self_attend(ORC_CAUSAL, q, k, v, o, (hd,) * 4, n, hd, 0.3, None, None)
+    assert np.array_equal(o[:hd], v[:hd])
+
+
+@pytest.mark.parametrize("mask", [ORC_CAUSAL_KEYS, ORC_FULL_KEYS, ORC_KEYS_ADDITIVE])
+def test_masked_keys_carry_no_weight(orc, mask):
+    """-inf keys get exactly zero weight, -FLT_MAX keys ~1e-38: perturbing their k and v leaves o
+    unchanged bit for bit."""
+    rng = np.random.default_rng(6)
+    n, hd = 33, 64
+    q, k, v = _qkv(rng, n, hd)
+    kv = (rng.random(n) > 0.4).astype(np.uint8)
+    kv[-1] = 1
+    o1 = np.zeros(n * hd, np.float32)
+    orc.self_attend(mask, q, k, v, o1, (hd,) * 4, n, hd, 0.125, kv, None)
+    k2, v2 = k.copy().reshape(n, hd), v.copy().reshape(n, hd)
+    bad = np.where(kv == 0)[0]
+    k2[bad] += 3.0
+    v2[bad] *= -7.0
+    o2 = np.zeros(n * hd, np.float32)
+    orc.self_attend(mask, q, k2.ravel(), v2.ravel(), o2, (hd,) * 4, n, hd, 0.125, kv, None)
+    rows = [i for i in range(n) if mask == ORC_KEYS_ADDITIVE or kv[i]]  # diagonal rows read themselves
+    assert np.array_equal(o1.reshape(n, hd)[rows], o2.reshape(n, hd)[rows])
+
+
+def test_keys_additive_all_invalid_is_uniform(orc):
+    """With every key invalid each score becomes -FLT_MAX and softmax is uniform over all keys."""
+    rng = np.random.default_rng(7)
+    n, hd = 9, 64
+    q, k, v = _qkv(rng, n, hd)
+    o = np.zeros(n * hd, np.float32)
+    orc.self_attend(ORC_KEYS_ADDITIVE, q, k, v, o, (hd,) * 4, n, hd, 1.0, np.zeros(n, np.uint8), None)
+    np.testing.assert_allclose(o.reshape(n, hd), np.tile(v.reshape(n, hd).mean(axis=0), (n, 1)), atol=2e-6)
+
+
+def test_key_permutation_invariance(orc):
+    rng = np.random.default_rng(8)
+    n, hd = 40, 64
+    q, k, v = _qkv(rng, n, hd)
+    perm = rng.permutation(n)
+    o1 = np.zeros(n * hd, np.float32)
+    o2 = np.zeros(n * hd, np.float32)
+    orc.self_attend(ORC_FULL, q, k, v, o1, (hd,) * 4, n, hd, 0.125, None, None)
+    orc.self_attend(ORC_FULL, q, k.reshape(n, hd)[perm].ravel(), v.reshape(n, hd)[perm].ravel(), o2, (hd,) * 4, n,
+                    hd, 0.125, None, None)
+    np.testing.assert_allclose(o1, o2, atol=2e-6)
+
+
+def test_bias_shifts_scores_before_softmax(orc):
+    """A bias that is constant along each row leaves softmax unchanged; a bias of +50 on one key
+    makes that key dominate (a bias applied after the softmax would fail both)."""
+    rng = np.random.default_rng(9)
+    n, hd = 16, 64
+    q, k, v = _qkv(rng, n, hd)
+    base = np.zeros(n * hd, np.float32)
+    orc.self_attend(ORC_FULL, q, k, v, base, (hd,) * 4, n, hd, 0.125, None, None)
+    rowconst = np.repeat(rng.standard_normal(n).astype(np.float32), n)
+    o = np.zeros(n * hd, np.float32)
+    orc.self_attend(ORC_FULL, q, k, v, o, (hd,) * 4, n, hd, 0.125, None, rowconst)
+    np.testing.assert_allclose(o, base, atol=2e-6)
+    spike = np.zeros((n, n), np.float32)
+    spike[:, 3] = 50.0
+    orc.self_attend(ORC_FULL, q, k, v, o, (hd,) * 4, n, hd, 0.125, None, spike.ravel())
+    np.testing.assert_allclose(o.reshape(n, hd), np.tile(v.reshape(n, hd)[3], (n, 1)), atol=1e-5)
+
+
+# ---- nn.zig primitives -------------------------------------------------------------------------
+
+
+def test_exp_vec_accuracy_and_clamp(orc):
+    xs = np.concatenate([np.linspace(-87.0, 0.0, 4001), np.linspace(0, 80, 801)]).astype(np.float32)
+    got = np.array([orc.exp_vec(x) for x in xs], np.float64)
+    want = np.exp(xs.astype(np.float64))
+    assert np.max(np.abs(got - want) / want) < 3e-7  # about 2 ulp
+    assert orc.exp_vec(0.0) == np.float32(1.0)
+    assert orc.exp_vec(-1e9) == orc.exp_vec(-87.33654)  # clamped to the smallest normal range
+    assert 1.0e-38 < float(orc.exp_vec(-1e9)) < 1.3e-38
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 16, 17, 129, 577])
+def test_softmax(orc, n):
+    rng = np.random.default_rng(10 + n)
+    row = (rng.standard_normal(n) * 4).astype(np.float32)
+    if n > 3:
+        row[[1, n - 2]] = -np.inf
+    x = row.copy()
+    orc.softmax(x)
+    r64 = row.astype(np.float64)
+    e = np.where(np.isinf(r64), 0.0, np.exp(r64 - r64.max()))
+    np.testing.assert_allclose(x, e / e.sum(), atol=1e-7, rtol=3e-6)
+    assert np.all(x[np.isinf(row)] == 0.0)
+
+
+def test_gemm_nt_and_tiling_independence(orc):
+    rng = np.random.default_rng(11)
+    m, n, k, lda, ldb, ldc = 37, 29, 71, 75, 80, 33
+    a = rng.standard_normal(m * lda).astype(np.float32)
+    b = rng.standard_normal(n * ldb).astype(np.float32)
+    c = np.full(m * ldc, -12345.0, np.float32)
+    orc.gemm_nt(c, ldc, a, lda, b, ldb, m, n, k, 0.7)
+    A = a.reshape(m, lda)[:, :k].astype(np.float64)
+    B = b.reshape(n, ldb)[:, :k].astype(np.float64)
+    np.testing.assert_allclose(c.reshape(m, ldc)[:, :n], 0.7 * A @ B.T, atol=1e-4, rtol=1e-5)
+    assert np.all(c.reshape(m, ldc)[:, n:] == -12345.0)  # padding untouched (gpu_test.zig:30-34)
+    # Each output depends only on its own row and column: row-by-row calls are bit-identical.
+    c1 = np.zeros(ldc, np.float32)
+    for i in (0, 1, m - 1):
+        orc.gemm_nt(c1, ldc, a[i * lda:], lda, b, ldb, 1, n, k, 0.7)
+        assert np.array_equal(c1[:n], c.reshape(m, ldc)[i, :n])
+
+
+def test_gemm_nn_skips_zero_probabilities(orc):
+    rng = np.random.default_rng(12)
+    m, n, k = 13, 64, 41
+    a = rng.random((m, k)).astype(np.float32)
+    a[:, ::3] = 0.0
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    c = np.zeros((m, n), np.float32)
+    orc.gemm_nn(c, n, a, k, b, n, m, n, k)
+    np.testing.assert_allclose(c, a.astype(np.float64) @ b.astype(np.float64), atol=1e-5, rtol=1e-5)
+    b2 = b.copy()
+    b2[::3] = np.nan  # rows of B with an all-zero A column are never read
+    c2 = np.zeros((m, n), np.float32)
+    orc.gemm_nn(c2, n, a, k, b2, n, m, n, k)
+    assert np.array_equal(c, c2)
+
+
+def test_dot_matches_f64(orc):
+    rng = np.random.default_rng(13)
+    a = rng.standard_normal(67).astype(np.float32)
+    b = rng.standard_normal(67).astype(np.float32)
+    assert abs(float(orc.dot(a, b)) - float(a.astype(np.float64) @ b.astype(np.float64))) < 1e-5
+
+
+def test_rope_invariants(orc):
+    """RoPE preserves each pair's norm and makes q.k depend only on the position difference."""
+    hd, seq = 64, 40
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, hd, 10000.0)
+    np.testing.assert_allclose(cos_t.astype(np.float64) ** 2 + sin_t.astype(np.float64) ** 2, 1.0, atol=1e-6)
+    inv = 1.0 / 10000.0 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)
+    np.testing.assert_allclose(cos_t.reshape(seq, hd // 2), np.cos(np.outer(np.arange(seq), inv)), atol=3e-6)
+    rng = np.random.default_rng(14)
+    q0 = rng.standard_normal(hd).astype(np.float32)
+    k0 = rng.standard_normal(hd).astype(np.float32)
+
+    def rot(x, pos):
+        y = x.copy()
+        orc.rope_half(y, cos_t[pos * 32:], sin_t[pos * 32:], 32)
+        return y
+
+    for p in (0, 3, 17):
+        y = rot(q0, p)
+        np.testing.assert_allclose(y[:32] ** 2 + y[32:] ** 2, q0[:32] ** 2 + q0[32:] ** 2, rtol=1e-5, atol=1e-6)
+    d1 = float(rot(q0, 10) @ rot(k0, 4))
+    d2 = float(rot(q0, 20) @ rot(k0, 14))
+    d3 = float(rot(q0, 6) @ rot(k0, 0))
+    assert abs(d1 - d2) < 1e-4 and abs(d1 - d3) < 1e-4
+    assert abs(d1 - float(q0 @ k0)) > 1e-3  # rotation is not the identity
+
+
+def test_position_bias_layout(orc):
+    rng = np.random.default_rng(15)
+    table = _ref.t5_bias_table(rng, 32, 12)
+    seq = 21
+    bias = orc.position_bias(table, seq, 12, 32, 128).reshape(12, seq, seq)
+    for h in (0, 7):
+        for i, j in ((0, 0), (3, 15), (20, 1)):
+            assert bias[h, i, j] == table[orc.relative_bucket(j - i, 32, 128), h]
+
+
+# ---- family jobs -------------------------------------------------------------------------------
+
+
+def test_bolt_cross_attention(orc):
+    rng = np.random.default_rng(16)
+    nb, seq, nh, hd = 3, 33, 8, 64
+    inner = nh * hd
+    q = rng.standard_normal(nb * inner).astype(np.float32)
+    k = rng.standard_normal(nb * seq * inner).astype(np.float32)
+    v = rng.standard_normal(nb * seq * inner).astype(np.float32)
+    kv = _ref.left_pad_valid(rng, nb, seq, 10, tail_valid=1)
+    o = np.zeros(nb * inner, np.float32)
+    orc.bolt_cross_attention(2, q, k, v, o, kv.ravel(), nb, seq, inner, nh, hd)
+    for r in range(nb):
+        for h in range(nh):
+            Q = q.reshape(nb, nh, hd)[r, h][None]
+            K = k.reshape(nb, seq, nh, hd)[r, :, h]
+            V = v.reshape(nb, seq, nh, hd)[r, :, h]
+            want = _ref.naive_attend(Q, K, V, kv[r][None].astype(bool), 1.0)
+            assert _ref.scaled_err(o.reshape(nb, nh, hd)[r, h], want[0]) < 2e-6
+
+
+def test_bolt_self_attention(orc):
+    rng = np.random.default_rng(17)
+    nb, seq, nh, hd = 2, 33, 4, 64
+    inner = nh * hd
+    q, k, v = (rng.standard_normal(nb * seq * inner).astype(np.float32) for _ in range(3))
+    table = _ref.t5_bias_table(rng, 32, nh)
+    bias = orc.position_bias(table, seq, nh, 32, 128)
+    kv = _ref.left_pad_valid(rng, nb, seq, 8, tail_valid=1)
+    o = np.zeros(nb * seq * inner, np.float32)
+    orc.bolt_self_attention(2, q, k, v, o, bias, kv.ravel(), False, nb, seq, inner, nh, hd)
+    B3 = bias.reshape(nh, seq, seq)
+    for r in range(nb):
+        for h in range(nh):
+            sl = lambda x: x.reshape(nb, seq, nh, hd)[r, :, h]  # noqa: E731
+            want = _ref.naive_attend(sl(q), sl(k), sl(v), _ref.allowed_matrix(1, seq, seq, kv[r]), 1.0, B3[h])
+            # Unscaled T5 scores reach |s| ~ 30: f32 rounding of s alone gives ~2e-6 here.
+            assert _ref.scaled_err(sl(o), want) < 5e-6
+
+
+def test_chronos2_time_attention_and_threads(orc):
+    rng = np.random.default_rng(18)
+    b, seq, nh, hd = 2, 45, 3, 64
+    d = nh * hd
+    q, k, v = (rng.standard_normal(b * seq * d).astype(np.float32) for _ in range(3))
+    kv = _ref.left_pad_valid(rng, b, seq, 10, tail_valid=5)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, hd)
+    qr, kr = q.copy(), k.copy()
+    orc.chronos2_rope(qr, kr, cos_t, sin_t, b * seq, seq, d, nh, hd)
+    o1 = np.zeros_like(q)
+    o4 = np.zeros_like(q)
+    orc.chronos2_time_attention(1, qr, kr, v, o1, kv.ravel(), False, b, seq, d, nh, hd, 0.125)
+    orc.chronos2_time_attention(4, qr, kr, v, o4, kv.ravel(), False, b, seq, d, nh, hd, 0.125)
+    assert np.array_equal(o1, o4)  # thread count is bit-identical (README.md:282)
+    # RoPE applied with numpy from the same tables, then the float64 reference.
+    C = cos_t.reshape(seq, hd // 2).astype(np.float64)
+    S = sin_t.reshape(seq, hd // 2).astype(np.float64)
+
+    def rope64(x):
+        lo, hi = x[:, :32], x[:, 32:]
+        return np.concatenate([lo * C - hi * S, hi * C + lo * S], axis=1)
+
+    for r in range(b):
+        for h in range(nh):
+            sl = lambda x: x.reshape(b, seq, nh, hd)[r, :, h].astype(np.float64)  # noqa: E731
+            want = _ref.naive_attend(rope64(sl(q)), rope64(sl(k)), sl(v), _ref.allowed_matrix(1, seq, seq, kv[r]), 0.125)
+            assert _ref.scaled_err(sl(o1), want) < 2e-6
+
+
+@pytest.mark.parametrize("all_valid", [True, False])
+def test_timestral_time_attention(orc, all_valid):
+    rng = np.random.default_rng(19 + all_valid)
+    rows, vall, ne, l, h, nh, hd = 4, 2, 24, 24, 6, 2, 64
+    d = nh * hd
+    sl = ne + h
+    qkv = rng.standard_normal(rows * sl * 3 * d).astype(np.float32)
+    kv = np.ones((rows, ne), np.uint8) if all_valid else _ref.left_pad_valid(rng, rows, ne, 6)
+    bidir = np.array([0, 1, 0, 0], np.uint8)
+    o = np.zeros(rows * sl * d, np.float32)
+    orc.timestral_time_attention(2, qkv, o, kv.ravel(), all_valid, bidir, rows, ne, l, h, d, nh, hd)
+    X = qkv.reshape(rows, sl, 3, nh, hd).astype(np.float64)
+    O = o.reshape(rows, sl, nh, hd)
+    for r in range(rows):
+        for hh in range(nh):
+            Q, K, V = X[r, :, 0, hh], X[r, :, 1, hh], X[r, :, 2, hh]
+            enc_mask = (4 if bidir[r] else 3) if not all_valid else (0 if bidir[r] else 2)
+            want = _ref.naive_attend(Q[:ne], K[:ne], V[:ne], _ref.allowed_matrix(enc_mask, ne, ne, kv[r]), 0.125)
+            assert _ref.scaled_err(O[r, :ne, hh], want) < 2e-6
+            dec = _ref.allowed_matrix(5, h, sl, np.concatenate([kv[r], np.ones(h, np.uint8)]), q_pos0=ne, ctx_keys=l,
+                                      chain_start=ne)
+            want = _ref.naive_attend(Q[ne:], K, V, dec, 0.125)
+            assert _ref.scaled_err(O[r, ne:, hh], want) < 2e-6
+
+
+def test_lane_counts_agree(orc, orc16):
+    assert (orc.lanes, orc16.lanes) == (8, 16)
+    rng = np.random.default_rng(21)
+    n, hd = 70, 64
+    q, k, v = _qkv(rng, n, hd)
+    kv = (rng.random(n) > 0.2).astype(np.uint8)
+    for mask in MASKS:
+        o8 = np.zeros(n * hd, np.float32)
+        o16 = np.zeros(n * hd, np.float32)
+        orc.self_attend(mask, q, k, v, o8, (hd,) * 4, n, hd, 0.125, kv, None)
+        orc16.self_attend(mask, q, k, v, o16, (hd,) * 4, n, hd, 0.125, kv, None)
+        assert _ref.scaled_err(o16, o8) < 1e-6

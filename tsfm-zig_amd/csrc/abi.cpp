@@ -1,0 +1,481 @@
+// extern "C" ABI of libtsfm_attn.so (declared in include/tsfm_attn.h).
+//
+// Mirrors the reference backend's conventions (src/platform/cuda/gemm.c): one-time device set-up
+// under pthread_once (:112-166), one stream and growable device staging buffer per host thread
+// kept in a pthread key with a destructor (:171-227), synchronous host round trip for host
+// pointers (:252-314), int return with 0 = success and anything else = "use the CPU" (:1-15).
+// Unlike the reference, a call covers a whole batch of (series, head) items and the device work
+// is one fused kernel instead of two cuBLAS GEMMs per item.
+#include <hip/hip_runtime.h>
+#include <pthread.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "../../include/tsfm_attn.h"
+#include "launch.hpp"
+
+namespace {
+
+pthread_once_t g_once = PTHREAD_ONCE_INIT;
+int g_ready = 0;
+int g_device = 0;
+char g_init_err[256] = "not initialised";
+thread_local char t_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof t_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void init_once() {
+    const char* dis = getenv("TSFM_HIP_DISABLE");
+    if (dis != nullptr && dis[0] != '\0' && strcmp(dis, "0") != 0) {
+        snprintf(g_init_err, sizeof g_init_err, "disabled by TSFM_HIP_DISABLE");
+        return;
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        snprintf(g_init_err, sizeof g_init_err, "no HIP device");
+        fprintf(stderr, "tsfm_attn unavailable: %s\n", g_init_err);
+        return;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        snprintf(g_init_err, sizeof g_init_err, "cannot query device %d", dev);
+        fprintf(stderr, "tsfm_attn unavailable: %s\n", g_init_err);
+        return;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        snprintf(g_init_err, sizeof g_init_err, "device %d is %s, the kernels are built for gfx950", dev,
+                 prop.gcnArchName);
+        fprintf(stderr, "tsfm_attn unavailable: %s\n", g_init_err);
+        return;
+    }
+    g_device = dev;
+    g_ready = 1;
+}
+
+int ensure_ready() {
+    pthread_once(&g_once, init_once);
+    if (!g_ready) return fail(TSFM_E_UNAVAILABLE, "%s", g_init_err);
+    return TSFM_OK;
+}
+
+// ---- per-thread stream and staging buffer -------------------------------------------------------
+
+struct ThreadCtx {
+    hipStream_t stream = nullptr;
+    void* buf = nullptr;
+    size_t cap = 0;
+};
+
+pthread_key_t g_ctx_key;
+pthread_once_t g_ctx_once = PTHREAD_ONCE_INIT;
+
+void destroy_ctx(void* ptr) {
+    ThreadCtx* c = static_cast<ThreadCtx*>(ptr);
+    if (c == nullptr) return;
+    if (c->stream != nullptr) (void)hipStreamDestroy(c->stream);
+    if (c->buf != nullptr) (void)hipFree(c->buf);
+    delete c;
+}
+
+void create_ctx_key() { pthread_key_create(&g_ctx_key, destroy_ctx); }
+
+ThreadCtx* thread_ctx() {
+    pthread_once(&g_ctx_once, create_ctx_key);
+    ThreadCtx* c = static_cast<ThreadCtx*>(pthread_getspecific(g_ctx_key));
+    if (c != nullptr) return c;
+    c = new ThreadCtx();
+    if (hipSetDevice(g_device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        destroy_ctx(c);
+        return nullptr;
+    }
+    pthread_setspecific(g_ctx_key, c);
+    return c;
+}
+
+int ensure_buf(ThreadCtx* c, size_t bytes) {
+    if (c->cap >= bytes) return TSFM_OK;
+    void* next = nullptr;
+    if (hipMalloc(&next, bytes) != hipSuccess || next == nullptr)
+        return fail(TSFM_E_DEVICE, "device staging allocation of %zu bytes failed", bytes);
+    if (c->buf != nullptr) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->buf);
+    }
+    c->buf = next;
+    c->cap = bytes;
+    return TSFM_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorNotSupported) return fail(TSFM_E_UNSUPPORTED, "%s: not supported", what);
+    return fail(TSFM_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Sub-allocation plan over the staging buffer (256-byte aligned pieces).
+struct Plan {
+    size_t off = 0;
+    size_t take(size_t bytes) {
+        const size_t at = off;
+        off = (off + bytes + 255) & ~size_t(255);
+        return at;
+    }
+};
+
+size_t elem_size(int dtype) { return dtype == TSFM_DTYPE_F32 ? 4 : 2; }
+
+// Elements spanned by a (B, n, H*D) view with the given strides.
+int64_t span(int64_t B, int64_t n, int64_t tok, int64_t batch, int64_t row) {
+    return (B - 1) * batch + (n - 1) * tok + row;
+}
+
+// Copy `rows` rows of `width` bytes, pitch `pitch` bytes, per batch, from device to host. Only the
+// row contents move: padding between rows (other heads, fused-projection gaps) is left alone.
+hipError_t copy_rows_d2h(void* dst, const void* src, int64_t B, int64_t rows, int64_t batch_bytes, int64_t pitch,
+                         int64_t width, hipStream_t s) {
+    if (batch_bytes == rows * pitch)
+        return hipMemcpy2DAsync(dst, pitch, src, pitch, width, B * rows, hipMemcpyDeviceToHost, s);
+    for (int64_t b = 0; b < B; b++) {
+        hipError_t e = hipMemcpy2DAsync(static_cast<char*>(dst) + b * batch_bytes, pitch,
+                                        static_cast<const char*>(src) + b * batch_bytes, pitch, width, rows,
+                                        hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int validate(const tsfm_attn_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (a->dtype < TSFM_DTYPE_F32 || a->dtype > TSFM_DTYPE_F16) return fail(TSFM_E_INVALID, "bad dtype %d", a->dtype);
+    if (a->mask < TSFM_MASK_FULL || a->mask > TSFM_MASK_DECODER) return fail(TSFM_E_INVALID, "bad mask %d", a->mask);
+    if (a->batch < 0 || a->heads < 0 || a->n_q < 0 || a->n_k < 0) return fail(TSFM_E_INVALID, "negative size");
+    if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
+    if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr)
+        return fail(TSFM_E_INVALID, "q, k, v and o are required");
+    if (a->q_tok < 0 || a->q_batch < 0 || a->k_tok < 0 || a->k_batch < 0 || a->v_tok < 0 || a->v_batch < 0 ||
+        a->o_tok < 0 || a->o_batch < 0)
+        return fail(TSFM_E_INVALID, "negative stride");
+    const int64_t vec = a->dtype == TSFM_DTYPE_F32 ? 4 : 8;  // elements per 16-byte load
+    if (a->q_tok % vec || a->q_batch % vec || a->k_tok % vec || a->k_batch % vec || a->v_tok % vec ||
+        a->v_batch % vec || a->o_tok % vec || a->o_batch % vec)
+        return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    const int64_t row = (int64_t)a->heads * a->head_dim;
+    if (a->o_tok < row && a->n_q > 1) return fail(TSFM_E_INVALID, "o token stride smaller than heads * head_dim");
+    const bool reads_valid = a->mask == TSFM_MASK_KEYS_ADDITIVE || a->mask == TSFM_MASK_CAUSAL_KEYS ||
+                             a->mask == TSFM_MASK_FULL_KEYS || a->mask == TSFM_MASK_DECODER;
+    if (reads_valid && a->key_valid == nullptr) return fail(TSFM_E_INVALID, "mask %d needs key_valid", a->mask);
+    if (a->kv_batch < 0) return fail(TSFM_E_INVALID, "negative kv_batch");
+    if (a->q_pos0 < 0) return fail(TSFM_E_INVALID, "negative q_pos0");
+    if (a->mask == TSFM_MASK_DECODER && (a->ctx_keys < 0 || a->chain_start < 0))
+        return fail(TSFM_E_INVALID, "negative decoder bounds");
+    if (a->bias != nullptr && a->rel_table != nullptr) return fail(TSFM_E_INVALID, "both dense and T5 bias given");
+    if (a->bias != nullptr && (a->bias_head < 0 || a->bias_row < 0)) return fail(TSFM_E_INVALID, "negative bias stride");
+    if (a->rel_table != nullptr) {
+        if (a->rel_bucket == nullptr || a->rel_buckets <= 0) return fail(TSFM_E_INVALID, "T5 bias needs rel_bucket");
+        if (a->q_pos0 != 0) return fail(TSFM_E_UNSUPPORTED, "T5 bias needs q_pos0 == 0");
+        if ((int64_t)a->n_q + a->n_k - 1 > tsfm::kRelMax)
+            return fail(TSFM_E_UNSUPPORTED, "T5 bias supports n_q + n_k - 1 <= %d", tsfm::kRelMax);
+    }
+    if (a->rope_cos != nullptr) {
+        if (a->rope_sin == nullptr) return fail(TSFM_E_INVALID, "rope_sin is NULL");
+        if (a->rope_half != a->head_dim / 2) return fail(TSFM_E_UNSUPPORTED, "rope_half must be head_dim / 2");
+        if (a->rope_rows_per_table < 0 || a->rope_row0 < 0 || a->rope_table_stride < 0)
+            return fail(TSFM_E_INVALID, "bad rope table layout");
+        if (a->rope_table_stride % 4) return fail(TSFM_E_UNSUPPORTED, "rope_table_stride must be a multiple of 4");
+    }
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
+        if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 16))
+            return fail(TSFM_E_UNSUPPORTED, "device q/k/v/o must be 16-byte aligned");
+        if (a->rope_cos != nullptr && (!aligned(a->rope_cos, 16) || !aligned(a->rope_sin, 16)))
+            return fail(TSFM_E_UNSUPPORTED, "device RoPE tables must be 16-byte aligned");
+    }
+    return TSFM_OK;
+}
+
+int launch(const tsfm_attn_args* a, const tsfm::Params& p, hipStream_t s) {
+    const int bias = a->rel_table != nullptr ? tsfm::BIAS_REL : (a->bias != nullptr ? tsfm::BIAS_DENSE : tsfm::BIAS_NONE);
+    const bool rope = a->rope_cos != nullptr;
+    hipError_t e;
+    if (a->dtype == TSFM_DTYPE_F32) e = tsfm::launch_attn_f32(p, a->mask, bias, rope, s);
+    else e = tsfm::launch_attn_half(p, a->dtype == TSFM_DTYPE_BF16, a->mask, bias, rope, s);
+    if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
+    return TSFM_OK;
+}
+
+tsfm::Params params_from(const tsfm_attn_args* a) {
+    tsfm::Params p{};
+    p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
+    p.q_tok = a->q_tok; p.q_batch = a->q_batch; p.k_tok = a->k_tok; p.k_batch = a->k_batch;
+    p.v_tok = a->v_tok; p.v_batch = a->v_batch; p.o_tok = a->o_tok; p.o_batch = a->o_batch;
+    p.key_valid = a->key_valid; p.kv_batch = a->kv_batch;
+    p.bias = a->bias; p.bias_head = a->bias_head; p.bias_row = a->bias_row;
+    p.rel_table = a->rel_table; p.rel_bucket = a->rel_bucket; p.rel_buckets = a->rel_buckets;
+    p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
+    p.rope_table_stride = a->rope_table_stride; p.rope_rows_per_table = a->rope_rows_per_table;
+    p.rope_row0 = a->rope_row0;
+    p.B = a->batch; p.H = a->heads; p.n_q = a->n_q; p.n_k = a->n_k; p.q_pos0 = a->q_pos0;
+    p.ctx_keys = a->ctx_keys; p.chain_start = a->chain_start; p.scale = a->scale;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsfm_attn_init(void) { return ensure_ready(); }
+
+int tsfm_attn_available(void) { return ensure_ready() == TSFM_OK ? 1 : 0; }
+
+const char* tsfm_attn_last_error(void) { return t_err; }
+
+uint32_t tsfm_t5_relative_bucket(int64_t rel, uint32_t num_buckets, uint32_t max_distance) {
+    // T5 bidirectional bucket with a float32 log (src/chronos_bolt/model.zig:74-85).
+    const uint32_t half = num_buckets / 2;
+    const uint32_t base = rel > 0 ? half : 0;
+    const uint32_t rp = (uint32_t)(rel < 0 ? -rel : rel);
+    const uint32_t max_exact = half / 2;
+    if (rp < max_exact) return base + rp;
+    const float ratio = (float)rp / (float)max_exact;
+    const float denom = (float)std::log((double)max_distance / (double)max_exact);
+    const float large_f = std::log(ratio) / denom * (float)(half - max_exact);
+    const uint32_t large = max_exact + (uint32_t)large_f;
+    return base + (large < half - 1 ? large : half - 1);
+}
+
+int tsfm_t5_bucket_table(int32_t* out, int32_t n_q, int32_t n_k, uint32_t num_buckets, uint32_t max_distance) {
+    if (out == nullptr || n_q <= 0 || n_k <= 0 || num_buckets < 4)
+        return fail(TSFM_E_INVALID, "bad bucket table request");
+    const int64_t n = (int64_t)n_q + n_k - 1;
+    for (int64_t t = 0; t < n; t++)
+        out[t] = (int32_t)tsfm_t5_relative_bucket(t - (n_q - 1), num_buckets, max_distance);
+    return TSFM_OK;
+}
+
+int tsfm_attn_fwd(const tsfm_attn_args* a) {
+    int rc = validate(a);
+    if (rc != TSFM_OK) return rc;
+    if (a->batch == 0 || a->heads == 0 || a->n_q == 0) return TSFM_OK;  // nothing to compute
+    if (a->n_k == 0) return fail(TSFM_E_INVALID, "n_k is 0 with queries present");
+    rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+
+    tsfm::Params p = params_from(a);
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
+        hipStream_t s = a->stream != nullptr ? static_cast<hipStream_t>(a->stream) : ctx->stream;
+        return launch(a, p, s);
+    }
+
+    // Host pointers: stage every input, run, copy the output rows back, synchronise.
+    const int64_t B = a->batch, H = a->heads, D = a->head_dim, row = H * D;
+    const size_t es = elem_size(a->dtype);
+    const bool reads_valid = a->mask == TSFM_MASK_KEYS_ADDITIVE || a->mask == TSFM_MASK_CAUSAL_KEYS ||
+                             a->mask == TSFM_MASK_FULL_KEYS || a->mask == TSFM_MASK_DECODER;
+    const size_t q_n = span(B, a->n_q, a->q_tok, a->q_batch, row) * es;
+    const size_t k_n = span(B, a->n_k, a->k_tok, a->k_batch, row) * es;
+    const size_t v_n = span(B, a->n_k, a->v_tok, a->v_batch, row) * es;
+    const size_t o_n = span(B, a->n_q, a->o_tok, a->o_batch, row) * es;
+    const int64_t kv_len = a->mask == TSFM_MASK_DECODER ? (a->ctx_keys < a->n_k ? a->ctx_keys : a->n_k) : a->n_k;
+    const size_t kv_n = reads_valid && kv_len > 0 ? (size_t)span(B, 1, 0, a->kv_batch, kv_len) : 0;
+    const size_t bias_n = a->bias ? (size_t)((H - 1) * a->bias_head + (a->n_q - 1) * a->bias_row + a->n_k) * 4 : 0;
+    const size_t relt_n = a->rel_table ? (size_t)a->rel_buckets * H * 4 : 0;
+    const size_t relb_n = a->rel_table ? (size_t)(a->n_q + a->n_k - 1) * 4 : 0;
+    int64_t ntab = 1;
+    if (a->rope_cos != nullptr && a->rope_rows_per_table > 0)
+        ntab = (a->rope_row0 + B - 1) / a->rope_rows_per_table + 1;
+    const int64_t npos = a->n_k > a->q_pos0 + a->n_q ? a->n_k : a->q_pos0 + a->n_q;
+    const size_t rope_n = a->rope_cos ? (size_t)((ntab - 1) * a->rope_table_stride + npos * a->rope_half) * 4 : 0;
+
+    Plan plan;
+    const size_t q_at = plan.take(q_n), k_at = plan.take(k_n), v_at = plan.take(v_n), o_at = plan.take(o_n);
+    const size_t kv_at = plan.take(kv_n), bias_at = plan.take(bias_n), relt_at = plan.take(relt_n);
+    const size_t relb_at = plan.take(relb_n), rc_at = plan.take(rope_n), rs_at = plan.take(rope_n);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+
+    // Bucket ids index the bias table on the device: check them here, where they are readable.
+    if (a->rel_table != nullptr)
+        for (int64_t t = 0; t < a->n_q + a->n_k - 1; t++)
+            if (a->rel_bucket[t] < 0 || a->rel_bucket[t] >= a->rel_buckets)
+                return fail(TSFM_E_INVALID, "rel_bucket[%lld] = %d outside [0, %d)", (long long)t, a->rel_bucket[t],
+                            a->rel_buckets);
+
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    struct Up { const void* src; size_t at, n; } ups[] = {
+        {a->q, q_at, q_n}, {a->k, k_at, k_n}, {a->v, v_at, v_n}, {a->key_valid, kv_at, kv_n},
+        {a->bias, bias_at, bias_n}, {a->rel_table, relt_at, relt_n}, {a->rel_bucket, relb_at, relb_n},
+        {a->rope_cos, rc_at, rope_n}, {a->rope_sin, rs_at, rope_n}};
+    for (const Up& u : ups) {
+        if (u.n == 0 || u.src == nullptr) continue;
+        hipError_t e = hipMemcpyAsync(base + u.at, u.src, u.n, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail(e, "host-to-device copy");
+    }
+    p.q = base + q_at; p.k = base + k_at; p.v = base + v_at; p.o = base + o_at;
+    p.key_valid = kv_n > 0 ? reinterpret_cast<const uint8_t*>(base + kv_at) : nullptr;
+    if (a->bias) p.bias = reinterpret_cast<const float*>(base + bias_at);
+    if (a->rel_table) {
+        p.rel_table = reinterpret_cast<const float*>(base + relt_at);
+        p.rel_bucket = reinterpret_cast<const int32_t*>(base + relb_at);
+    }
+    if (a->rope_cos) {
+        p.rope_cos = reinterpret_cast<const float*>(base + rc_at);
+        p.rope_sin = reinterpret_cast<const float*>(base + rs_at);
+    }
+    rc = launch(a, p, s);
+    if (rc != TSFM_OK) {
+        (void)hipStreamSynchronize(s);
+        return rc;
+    }
+    hipError_t e = copy_rows_d2h(a->o, base + o_at, B, a->n_q, a->o_batch * es, a->o_tok * es, row * es, s);
+    if (e != hipSuccess) return hip_fail(e, "device-to-host copy");
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
+// ---- KV cache ------------------------------------------------------------------------------------
+
+struct tsfm_kv_cache {
+    int32_t dtype, B, H, D, cap, len;
+    void* k;
+    void* v;
+};
+
+int tsfm_kv_create(tsfm_kv_cache** out, int32_t dtype, int32_t batch, int32_t heads, int32_t head_dim,
+                   int32_t capacity) {
+    if (out == nullptr) return fail(TSFM_E_INVALID, "out is NULL");
+    *out = nullptr;
+    if (dtype != TSFM_DTYPE_BF16 && dtype != TSFM_DTYPE_F16) return fail(TSFM_E_UNSUPPORTED, "KV cache is bf16/f16 only");
+    if (head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", head_dim);
+    if (batch <= 0 || heads <= 0 || capacity <= 0) return fail(TSFM_E_INVALID, "bad cache shape");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    const int32_t cap = (capacity + 31) / 32 * 32;
+    const size_t bytes = (size_t)batch * heads * cap * head_dim * 2;
+    tsfm_kv_cache* c = new tsfm_kv_cache{dtype, batch, heads, head_dim, cap, 0, nullptr, nullptr};
+    if (hipSetDevice(g_device) != hipSuccess || hipMalloc(&c->k, bytes) != hipSuccess ||
+        hipMalloc(&c->v, bytes) != hipSuccess) {
+        if (c->k) (void)hipFree(c->k);
+        delete c;
+        return fail(TSFM_E_DEVICE, "KV cache allocation of 2 x %zu bytes failed", bytes);
+    }
+    *out = c;
+    return TSFM_OK;
+}
+
+int tsfm_kv_free(tsfm_kv_cache* c) {
+    if (c == nullptr) return TSFM_OK;
+    (void)hipDeviceSynchronize();
+    if (c->k) (void)hipFree(c->k);
+    if (c->v) (void)hipFree(c->v);
+    delete c;
+    return TSFM_OK;
+}
+
+int tsfm_kv_reset(tsfm_kv_cache* c) {
+    if (c == nullptr) return fail(TSFM_E_INVALID, "cache is NULL");
+    c->len = 0;
+    return TSFM_OK;
+}
+
+int32_t tsfm_kv_len(const tsfm_kv_cache* c) { return c == nullptr ? 0 : c->len; }
+
+int tsfm_kv_append(tsfm_kv_cache* c, const void* k, int64_t k_tok, int64_t k_batch, const void* v, int64_t v_tok,
+                   int64_t v_batch, int32_t n_new, uint32_t flags, void* stream) {
+    if (c == nullptr || k == nullptr || v == nullptr) return fail(TSFM_E_INVALID, "NULL argument");
+    if (n_new < 0 || k_tok < 0 || k_batch < 0 || v_tok < 0 || v_batch < 0) return fail(TSFM_E_INVALID, "negative size");
+    if (n_new == 0) return TSFM_OK;
+    if (c->len + n_new > c->cap) return fail(TSFM_E_INVALID, "append of %d exceeds capacity %d (len %d)", n_new, c->cap, c->len);
+    if (k_tok % 8 || k_batch % 8 || v_tok % 8 || v_batch % 8) return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    tsfm::KvLayout L{c->k, c->v, c->B, c->H, c->cap};
+    const bool bf16 = c->dtype == TSFM_DTYPE_BF16;
+    hipError_t e;
+    if (flags & TSFM_ATTN_DEVICE_PTRS) {
+        if (!aligned(k, 16) || !aligned(v, 16)) return fail(TSFM_E_UNSUPPORTED, "device k/v must be 16-byte aligned");
+        hipStream_t s = stream != nullptr ? static_cast<hipStream_t>(stream) : ctx->stream;
+        e = tsfm::launch_kv_append(L, bf16, k, k_tok, k_batch, v, v_tok, v_batch, c->len, n_new, s);
+        if (e != hipSuccess) return hip_fail(e, "KV append launch");
+    } else {
+        const int64_t row = (int64_t)c->H * c->D;
+        const size_t k_n = span(c->B, n_new, k_tok, k_batch, row) * 2, v_n = span(c->B, n_new, v_tok, v_batch, row) * 2;
+        Plan plan;
+        const size_t k_at = plan.take(k_n), v_at = plan.take(v_n);
+        rc = ensure_buf(ctx, plan.off);
+        if (rc != TSFM_OK) return rc;
+        char* base = static_cast<char*>(ctx->buf);
+        hipStream_t s = ctx->stream;
+        if ((e = hipMemcpyAsync(base + k_at, k, k_n, hipMemcpyHostToDevice, s)) != hipSuccess ||
+            (e = hipMemcpyAsync(base + v_at, v, v_n, hipMemcpyHostToDevice, s)) != hipSuccess)
+            return hip_fail(e, "host-to-device copy");
+        e = tsfm::launch_kv_append(L, bf16, base + k_at, k_tok, k_batch, base + v_at, v_tok, v_batch, c->len, n_new, s);
+        if (e != hipSuccess) return hip_fail(e, "KV append launch");
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    }
+    c->len += n_new;
+    return TSFM_OK;
+}
+
+int tsfm_kv_attend(tsfm_kv_cache* c, const void* q, int64_t q_tok, int64_t q_batch, void* o, int64_t o_tok,
+                   int64_t o_batch, int32_t n_q, int32_t q_pos0, float scale, uint32_t flags, void* stream) {
+    if (c == nullptr || q == nullptr || o == nullptr) return fail(TSFM_E_INVALID, "NULL argument");
+    if (n_q < 0 || q_pos0 < 0 || q_tok < 0 || q_batch < 0 || o_tok < 0 || o_batch < 0)
+        return fail(TSFM_E_INVALID, "negative size");
+    if (n_q == 0) return TSFM_OK;
+    if (q_pos0 + n_q > c->len) return fail(TSFM_E_INVALID, "queries [%d, %d) beyond cache length %d", q_pos0, q_pos0 + n_q, c->len);
+    if (q_tok % 8 || q_batch % 8 || o_tok % 8 || o_batch % 8) return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    const int64_t row = (int64_t)c->H * c->D;
+    if (o_tok < row && n_q > 1) return fail(TSFM_E_INVALID, "o token stride smaller than heads * head_dim");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    tsfm::KvLayout L{c->k, c->v, c->B, c->H, c->cap};
+    const bool bf16 = c->dtype == TSFM_DTYPE_BF16;
+    const int32_t n_k = q_pos0 + n_q;
+    hipError_t e;
+    if (flags & TSFM_ATTN_DEVICE_PTRS) {
+        if (!aligned(q, 16) || !aligned(o, 16)) return fail(TSFM_E_UNSUPPORTED, "device q/o must be 16-byte aligned");
+        hipStream_t s = stream != nullptr ? static_cast<hipStream_t>(stream) : ctx->stream;
+        e = tsfm::launch_kv_attend(L, bf16, q, q_tok, q_batch, o, o_tok, o_batch, n_q, q_pos0, n_k, scale, s);
+        if (e != hipSuccess) return hip_fail(e, "KV attend launch");
+        return TSFM_OK;
+    }
+    const size_t q_n = span(c->B, n_q, q_tok, q_batch, row) * 2, o_n = span(c->B, n_q, o_tok, o_batch, row) * 2;
+    Plan plan;
+    const size_t q_at = plan.take(q_n), o_at = plan.take(o_n);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    if ((e = hipMemcpyAsync(base + q_at, q, q_n, hipMemcpyHostToDevice, s)) != hipSuccess) return hip_fail(e, "host-to-device copy");
+    e = tsfm::launch_kv_attend(L, bf16, base + q_at, q_tok, q_batch, base + o_at, o_tok, o_batch, n_q, q_pos0, n_k, scale, s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "KV attend launch");
+    }
+    if ((e = copy_rows_d2h(o, base + o_at, c->B, n_q, o_batch * 2, o_tok * 2, row * 2, s)) != hipSuccess)
+        return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Shared device-side definitions for the tsfm attention kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tsfm {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHeadDim = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kFltMax = 3.40282347e+38f;
+
+// Mask values: attn.Mask declaration order (src/core/attn.zig:10-21) plus the Timestral decoder
+// rows (src/timestral/model.zig:612-632). Same numbering as TSFM_MASK_* in tsfm_attn.h.
+enum Mask : int { FULL = 0, KEYS_ADDITIVE = 1, CAUSAL = 2, CAUSAL_KEYS = 3, FULL_KEYS = 4, DECODER = 5 };
+enum BiasKind : int { BIAS_NONE = 0, BIAS_DENSE = 1, BIAS_REL = 2 };
+
+// Longest T5 relative-offset table kept in LDS (n_q + n_k - 1 entries).
+constexpr int kRelMax = 2048;
+
+// Kernel arguments, by value. Strides are in elements.
+struct Params {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    int64_t q_tok, q_batch, k_tok, k_batch, v_tok, v_batch, o_tok, o_batch;
+    const uint8_t* key_valid;
+    int64_t kv_batch;
+    const float* bias;
+    int64_t bias_head, bias_row;
+    const float* rel_table;
+    const int32_t* rel_bucket;
+    int32_t rel_buckets;
+    const float* rope_cos;
+    const float* rope_sin;
+    int64_t rope_table_stride;
+    int32_t rope_rows_per_table, rope_row0;
+    int32_t B, H, n_q, n_k, q_pos0, ctx_keys, chain_start;
+    float scale;
+};
+
+// Workgroup ids are dealt round-robin over the 8 XCDs (id % 8). Re-map them so that consecutive
+// logical ids -- the query tiles of one (series, head), which read the same K/V -- run on the
+// same XCD and share its L2. A bijection on [0, n) for any n.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+    const int xcd = bid & 7, idx = bid >> 3, full = n >> 3, rem = n & 7;
+    return xcd < rem ? xcd * (full + 1) + idx : rem * (full + 1) + (xcd - rem) * full + idx;
+}
+
+// Key index range a query at position qpos may read under each mask, and the exclusive end of
+// keys any query of [qpos_lo, qpos_hi] may read (used to skip whole tiles).
+template <int MASK>
+__device__ __forceinline__ int key_end_for(int qpos_hi, int n_k, int ctx_keys) {
+    if (MASK == CAUSAL || MASK == CAUSAL_KEYS) return min(n_k, qpos_hi + 1);
+    if (MASK == DECODER) return min(n_k, max(ctx_keys, qpos_hi + 1));
+    return n_k;
+}
+
+// One score after scale and bias: the reference's mask rule (src/core/attn.zig:35-67,
+// src/timestral/model.zig:612-632). Keys past n_k are tile padding and always excluded.
+template <int MASK>
+__device__ __forceinline__ float apply_mask(float x, int key, int qpos, int n_k, bool valid, int ctx_keys,
+                                            int chain_start) {
+    if (key >= n_k) return kNegInf;
+    if (MASK == KEYS_ADDITIVE) return valid ? x : x + (-kFltMax);
+    if (MASK == CAUSAL) return key <= qpos ? x : kNegInf;
+    if (MASK == CAUSAL_KEYS) return (key == qpos || (valid && key <= qpos)) ? x : kNegInf;
+    if (MASK == FULL_KEYS) return (key == qpos || valid) ? x : kNegInf;
+    if (MASK == DECODER) return ((key < ctx_keys && valid) || (key >= chain_start && key <= qpos)) ? x : kNegInf;
+    return x;
+}
+
+// Bytes of key_valid per row the mask reads: DECODER only tests keys below ctx_keys.
+template <int MASK>
+__device__ __forceinline__ int valid_len(int n_k, int ctx_keys) {
+    return MASK == DECODER ? min(n_k, ctx_keys) : n_k;
+}
+
+template <int MASK>
+constexpr bool mask_reads_valid() {
+    return MASK == KEYS_ADDITIVE || MASK == CAUSAL_KEYS || MASK == FULL_KEYS || MASK == DECODER;
+}
+
+// Rotate-half RoPE of four pairs (nn.ropeHalf, src/core/nn.zig:453-460): lo holds dims i..i+3,
+// hi dims i+half..i+half+3. Unfused products, like the Zig code.
+__device__ __forceinline__ void rope4(f32x4& lo, f32x4& hi, f32x4 c, f32x4 s) {
+#pragma clang fp contract(off)
+    const f32x4 x1 = lo, x2 = hi;
+    lo = x1 * c - x2 * s;
+    hi = x2 * c + x1 * s;
+}
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+
+// Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float rows4_max(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+
+}  // namespace tsfm

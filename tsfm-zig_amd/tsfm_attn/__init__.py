@@ -1,0 +1,406 @@
+"""Python binding of libtsfm_attn.so, the gfx950 attention path of tsfm-zig.
+
+The shared object exports the C ABI of ``include/tsfm_attn.h``; this module loads it with ctypes
+and mirrors, on top of it, the reference's attention interface:
+
+* ``Mask`` / ``Mask.pick``                 -- ``attn.Mask`` (src/core/attn.zig:10-29)
+* ``Strides``                              -- ``attn.Strides`` (src/core/attn.zig:32)
+* ``self_attend``                          -- ``attn.selfAttendRuntime`` for one (series, head)
+                                              (src/core/attn.zig:99-117)
+* ``bolt_self_attention``                  -- forRange(nb*nh, SelfJob.attend)
+                                              (src/chronos_bolt/model.zig:242-243, 317-346)
+* ``bolt_cross_attention``                 -- forRange(nb*nh, CrossJob.attend)
+                                              (src/chronos_bolt/model.zig:296-297, 349-381)
+* ``chronos2_time_attention``              -- RoPE loop + forRange(b*nh, TimeJob.attend)
+                                              (src/chronos2/model.zig:236-260, 277-309)
+* ``timestral_time_attention``             -- TimeJob.rope + TimeJob.attend
+                                              (src/timestral/model.zig:513-515, 558-635)
+
+Every call returns the ABI's int code: 0 = done, anything else = "not run, use the CPU path", with
+``last_error()`` giving the reason -- the reference backend's contract (src/platform/backend.zig:33-36).
+The ``*_checked`` helpers raise ``TsfmError`` instead. Arrays may be numpy arrays (host pointers:
+the call copies in, runs and copies out synchronously) or torch device tensors (device pointers:
+the call is asynchronous on the given stream). No computation happens in Python: without the
+shared object or without a gfx950 device every call fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import math
+import os
+import pathlib
+from dataclasses import dataclass
+from typing import Any, Optional, Sequence
+
+LIB_PATH = pathlib.Path(__file__).with_name("libtsfm_attn.so")
+
+OK = 0
+E_UNAVAILABLE = 1
+E_UNSUPPORTED = 2
+E_INVALID = 3
+E_DEVICE = 4
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+
+DEVICE_PTRS = 1
+
+# Every symbol include/tsfm_attn.h declares.
+EXPORTS = (
+    "tsfm_attn_init",
+    "tsfm_attn_available",
+    "tsfm_attn_fwd",
+    "tsfm_attn_last_error",
+    "tsfm_t5_relative_bucket",
+    "tsfm_t5_bucket_table",
+    "tsfm_kv_create",
+    "tsfm_kv_free",
+    "tsfm_kv_reset",
+    "tsfm_kv_len",
+    "tsfm_kv_append",
+    "tsfm_kv_attend",
+)
+
+
+class Mask(enum.IntEnum):
+    """``attn.Mask`` in declaration order, plus the Timestral decoder-row mask."""
+
+    FULL = 0
+    KEYS_ADDITIVE = 1
+    CAUSAL = 2
+    CAUSAL_KEYS = 3
+    FULL_KEYS = 4
+    DECODER = 5
+
+    @staticmethod
+    def pick(causal: bool, all_keys_valid: bool, additive: bool) -> "Mask":
+        """``Mask.pick`` (src/core/attn.zig:24-28)."""
+        if all_keys_valid:
+            return Mask.CAUSAL if causal else Mask.FULL
+        if causal:
+            return Mask.CAUSAL_KEYS
+        return Mask.KEYS_ADDITIVE if additive else Mask.FULL_KEYS
+
+
+@dataclass(frozen=True)
+class Strides:
+    """Token strides (elements) of q, k, v and o -- ``attn.Strides``."""
+
+    q: int
+    k: int
+    v: int
+    o: int
+
+
+class TsfmError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"tsfm_attn error {code}: {message}")
+        self.code = code
+
+
+class AttnArgs(ctypes.Structure):
+    """``tsfm_attn_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("mask", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("n_q", ctypes.c_int32),
+        ("n_k", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("q_pos0", ctypes.c_int32),
+        ("ctx_keys", ctypes.c_int32),
+        ("chain_start", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("flags", ctypes.c_uint32),
+        ("q", ctypes.c_void_p),
+        ("q_tok", ctypes.c_int64),
+        ("q_batch", ctypes.c_int64),
+        ("k", ctypes.c_void_p),
+        ("k_tok", ctypes.c_int64),
+        ("k_batch", ctypes.c_int64),
+        ("v", ctypes.c_void_p),
+        ("v_tok", ctypes.c_int64),
+        ("v_batch", ctypes.c_int64),
+        ("o", ctypes.c_void_p),
+        ("o_tok", ctypes.c_int64),
+        ("o_batch", ctypes.c_int64),
+        ("key_valid", ctypes.c_void_p),
+        ("kv_batch", ctypes.c_int64),
+        ("bias", ctypes.c_void_p),
+        ("bias_head", ctypes.c_int64),
+        ("bias_row", ctypes.c_int64),
+        ("rel_table", ctypes.c_void_p),
+        ("rel_bucket", ctypes.c_void_p),
+        ("rel_buckets", ctypes.c_int32),
+        ("rope_cos", ctypes.c_void_p),
+        ("rope_sin", ctypes.c_void_p),
+        ("rope_half", ctypes.c_int32),
+        ("rope_rows_per_table", ctypes.c_int32),
+        ("rope_row0", ctypes.c_int32),
+        ("rope_table_stride", ctypes.c_int64),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    """Load libtsfm_attn.so (built in-tree by ``make -C tsfm-zig_amd``). Raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = pathlib.Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built: run `make -C tsfm-zig_amd` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(p))
+    vp, i32, i64, u32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
+    lib.tsfm_attn_init.restype = ctypes.c_int
+    lib.tsfm_attn_available.restype = ctypes.c_int
+    lib.tsfm_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs)]
+    lib.tsfm_attn_fwd.restype = ctypes.c_int
+    lib.tsfm_attn_last_error.restype = ctypes.c_char_p
+    lib.tsfm_t5_relative_bucket.argtypes = [i64, u32, u32]
+    lib.tsfm_t5_relative_bucket.restype = u32
+    lib.tsfm_t5_bucket_table.argtypes = [vp, i32, i32, u32, u32]
+    lib.tsfm_t5_bucket_table.restype = ctypes.c_int
+    lib.tsfm_kv_create.argtypes = [ctypes.POINTER(vp), i32, i32, i32, i32, i32]
+    lib.tsfm_kv_create.restype = ctypes.c_int
+    lib.tsfm_kv_free.argtypes = [vp]
+    lib.tsfm_kv_free.restype = ctypes.c_int
+    lib.tsfm_kv_reset.argtypes = [vp]
+    lib.tsfm_kv_reset.restype = ctypes.c_int
+    lib.tsfm_kv_len.argtypes = [vp]
+    lib.tsfm_kv_len.restype = i32
+    lib.tsfm_kv_append.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, u32, vp]
+    lib.tsfm_kv_append.restype = ctypes.c_int
+    lib.tsfm_kv_attend.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, ctypes.c_float, u32, vp]
+    lib.tsfm_kv_attend.restype = ctypes.c_int
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().tsfm_attn_last_error().decode()
+
+
+def available() -> bool:
+    return bool(load().tsfm_attn_available())
+
+
+def _ptr(x: Any) -> Optional[int]:
+    """Address of a numpy array, a torch tensor, or an int; None stays None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if hasattr(x, "ctypes"):
+        if not x.flags["C_CONTIGUOUS"]:
+            raise ValueError("numpy arrays passed to tsfm_attn must be C-contiguous")
+        return x.ctypes.data
+    raise TypeError(f"cannot take the address of {type(x)}")
+
+
+def _is_device(x: Any) -> bool:
+    return hasattr(x, "is_cuda") and bool(x.is_cuda)
+
+
+def _dtype_code(x: Any) -> int:
+    name = str(getattr(x, "dtype", "float32"))
+    if "bfloat16" in name:
+        return DTYPE_BF16
+    if "float16" in name:
+        return DTYPE_F16
+    if "float32" in name:
+        return DTYPE_F32
+    raise TypeError(f"unsupported element type {name}")
+
+
+def _stream_of(x: Any, stream: Any) -> Optional[int]:
+    if stream is not None:
+        return int(getattr(stream, "cuda_stream", stream))
+    if _is_device(x):
+        import torch  # device-pointer calls run on torch's current stream by default
+
+        return int(torch.cuda.current_stream(x.device).cuda_stream)
+    return None
+
+
+def fwd(args: AttnArgs) -> int:
+    """``tsfm_attn_fwd``: returns the ABI code."""
+    return int(load().tsfm_attn_fwd(ctypes.byref(args)))
+
+
+def fwd_checked(args: AttnArgs) -> None:
+    rc = fwd(args)
+    if rc != OK:
+        raise TsfmError(rc, last_error())
+
+
+def make_args(
+    *,
+    q: Any,
+    k: Any,
+    v: Any,
+    o: Any,
+    mask: int,
+    batch: int,
+    heads: int,
+    n_q: int,
+    n_k: int,
+    q_tok: int,
+    q_batch: int,
+    k_tok: int,
+    k_batch: int,
+    v_tok: int,
+    v_batch: int,
+    o_tok: int,
+    o_batch: int,
+    scale: float,
+    head_dim: int = 64,
+    q_pos0: int = 0,
+    ctx_keys: int = 0,
+    chain_start: int = 0,
+    key_valid: Any = None,
+    kv_batch: int = 0,
+    bias: Any = None,
+    bias_head: int = 0,
+    bias_row: int = 0,
+    rel_table: Any = None,
+    rel_bucket: Any = None,
+    rel_buckets: int = 0,
+    rope_cos: Any = None,
+    rope_sin: Any = None,
+    rope_rows_per_table: int = 0,
+    rope_row0: int = 0,
+    rope_table_stride: int = 0,
+    stream: Any = None,
+    dtype: Optional[int] = None,
+) -> AttnArgs:
+    """Build ``tsfm_attn_args``; device mode is chosen when q is a device tensor."""
+    device = _is_device(q)
+    a = AttnArgs()
+    a.dtype = _dtype_code(q) if dtype is None else dtype
+    a.mask = int(mask)
+    a.batch, a.heads, a.n_q, a.n_k, a.head_dim = batch, heads, n_q, n_k, head_dim
+    a.q_pos0, a.ctx_keys, a.chain_start = q_pos0, ctx_keys, chain_start
+    a.scale = float(scale)
+    a.flags = DEVICE_PTRS if device else 0
+    a.q, a.q_tok, a.q_batch = _ptr(q), q_tok, q_batch
+    a.k, a.k_tok, a.k_batch = _ptr(k), k_tok, k_batch
+    a.v, a.v_tok, a.v_batch = _ptr(v), v_tok, v_batch
+    a.o, a.o_tok, a.o_batch = _ptr(o), o_tok, o_batch
+    a.key_valid, a.kv_batch = _ptr(key_valid), kv_batch
+    a.bias, a.bias_head, a.bias_row = _ptr(bias), bias_head, bias_row
+    a.rel_table, a.rel_bucket, a.rel_buckets = _ptr(rel_table), _ptr(rel_bucket), rel_buckets
+    a.rope_cos, a.rope_sin = _ptr(rope_cos), _ptr(rope_sin)
+    a.rope_half = head_dim // 2 if rope_cos is not None else 0
+    a.rope_rows_per_table, a.rope_row0, a.rope_table_stride = rope_rows_per_table, rope_row0, rope_table_stride
+    a.stream = _stream_of(q, stream) if device else None
+    return a
+
+
+def _flat_view(x: Any, offset: int) -> Any:
+    """x shifted by `offset` elements (numpy view or torch view)."""
+    if offset == 0:
+        return x
+    return x.reshape(-1)[offset:]
+
+
+# ---------------------------------------------------------------------------------------------
+# Mirrors of the reference call sites.
+
+
+def self_attend(mask: Mask, q, k, v, o, st: Strides, n: int, hd: int, scale: float, key_valid=None, bias=None) -> int:
+    """``attn.selfAttendRuntime`` for one (series, head): q/k/v/o start at the head's first element,
+    ``st`` gives token strides, ``bias`` is an optional (n, n) additive bias."""
+    return fwd(
+        make_args(
+            q=q, k=k, v=v, o=o, mask=mask, batch=1, heads=1, n_q=n, n_k=n, head_dim=hd,
+            q_tok=st.q, q_batch=0, k_tok=st.k, k_batch=0, v_tok=st.v, v_batch=0, o_tok=st.o, o_batch=0,
+            scale=scale, key_valid=key_valid, kv_batch=0, bias=bias, bias_head=0, bias_row=n,
+        )
+    )
+
+
+def bolt_self_attention(q, k, v, o, rel_table, rel_bucket, key_valid, keys_all_valid: bool, nb: int, seq: int,
+                        inner: int, nh: int, hd: int, num_buckets: int, stream=None) -> int:
+    """Chronos-Bolt encoder self-attention over all (series, head): no scale, T5 bias from the
+    (buckets, heads) table, additive key mask unless every key of the chunk is valid."""
+    mask = Mask.pick(False, keys_all_valid, True)
+    return fwd(
+        make_args(
+            q=q, k=k, v=v, o=o, mask=mask, batch=nb, heads=nh, n_q=seq, n_k=seq, head_dim=hd,
+            q_tok=inner, q_batch=seq * inner, k_tok=inner, k_batch=seq * inner, v_tok=inner, v_batch=seq * inner,
+            o_tok=inner, o_batch=seq * inner, scale=1.0, key_valid=key_valid, kv_batch=seq,
+            rel_table=rel_table, rel_bucket=rel_bucket, rel_buckets=num_buckets, stream=stream,
+        )
+    )
+
+
+def bolt_cross_attention(q, k, v, o, key_valid, nb: int, seq: int, inner: int, nh: int, hd: int, stream=None) -> int:
+    """Chronos-Bolt decoder cross-attention: one query per (series, head), additive key mask."""
+    return fwd(
+        make_args(
+            q=q, k=k, v=v, o=o, mask=Mask.KEYS_ADDITIVE, batch=nb, heads=nh, n_q=1, n_k=seq, head_dim=hd,
+            q_tok=inner, q_batch=inner, k_tok=inner, k_batch=seq * inner, v_tok=inner, v_batch=seq * inner,
+            o_tok=inner, o_batch=inner, scale=1.0, key_valid=key_valid, kv_batch=seq, stream=stream,
+        )
+    )
+
+
+def chronos2_time_attention(q, k, v, o, cos_t, sin_t, key_valid, keys_all_valid: bool, b: int, seq: int, d: int,
+                            nh: int, hd: int, scale: float = 1.0, stream=None) -> int:
+    """Chronos-2 time attention: RoPE on q and k (tables (seq, hd/2)), then non-causal attention with
+    the additive key mask. The model uses scale 1.0 (src/chronos2/model.zig:306)."""
+    mask = Mask.pick(False, keys_all_valid, True)
+    return fwd(
+        make_args(
+            q=q, k=k, v=v, o=o, mask=mask, batch=b, heads=nh, n_q=seq, n_k=seq, head_dim=hd,
+            q_tok=d, q_batch=seq * d, k_tok=d, k_batch=seq * d, v_tok=d, v_batch=seq * d, o_tok=d, o_batch=seq * d,
+            scale=scale, key_valid=key_valid, kv_batch=seq, rope_cos=cos_t, rope_sin=sin_t, stream=stream,
+        )
+    )
+
+
+def timestral_time_attention(qkv, o, cos_t, sin_t, key_valid, keys_all_valid: bool, bidir: Optional[Sequence[bool]],
+                             rows: int, vall: int, ne: int, l: int, h: int, d: int, nh: int, hd: int,
+                             stream=None) -> int:
+    """Timestral time attention over [Enc ; Dec] tokens of every row: RoPE (per-group tables
+    (groups, sl, hd/2)), encoder rows causal (or bidirectional for known-future rows), decoder rows
+    over valid context keys plus their own causal chain. qkv is (rows, sl, 3d), o is (rows, sl, d)."""
+    sl = ne + h
+    scale = 1.0 / math.sqrt(hd)
+    flags = [bool(x) for x in bidir] if bidir is not None else [False] * rows
+    common = dict(heads=nh, head_dim=hd, scale=scale, rope_cos=cos_t, rope_sin=sin_t, rope_rows_per_table=vall,
+                  rope_table_stride=sl * (hd // 2), stream=stream, q_tok=3 * d, k_tok=3 * d, v_tok=3 * d, o_tok=d,
+                  q_batch=sl * 3 * d, k_batch=sl * 3 * d, v_batch=sl * 3 * d, o_batch=sl * d,
+                  key_valid=key_valid, kv_batch=ne)
+    # Encoder rows, grouped into runs of rows with the same causality (rows of one run share a call).
+    r = 0
+    while r < rows:
+        r1 = r
+        while r1 < rows and flags[r1] == flags[r]:
+            r1 += 1
+        mask = Mask.pick(not flags[r], keys_all_valid, False)
+        rc = fwd(make_args(
+            q=_flat_view(qkv, r * sl * 3 * d), k=_flat_view(qkv, r * sl * 3 * d + d),
+            v=_flat_view(qkv, r * sl * 3 * d + 2 * d), o=_flat_view(o, r * sl * d), mask=mask, batch=r1 - r,
+            n_q=ne, n_k=ne, rope_row0=r, **{**common, "key_valid": _flat_view(key_valid, r * ne)}))
+        if rc != OK:
+            return rc
+        r = r1
+    if h == 0:
+        return OK
+    # Decoder rows: queries at [ne, sl), keys [0, sl).
+    return fwd(make_args(
+        q=_flat_view(qkv, ne * 3 * d), k=_flat_view(qkv, d), v=_flat_view(qkv, 2 * d), o=_flat_view(o, ne * d),
+        mask=Mask.DECODER, batch=rows, n_q=h, n_k=sl, q_pos0=ne, ctx_keys=l, chain_start=ne,
+        **{**common, "key_valid": key_valid}))

@@ -1,0 +1,143 @@
+"""Synthetic attention workloads at the shapes of tsfm-zig's model families, with their
+algorithmic FLOP and byte counts. Used by the benchmark and the parity tests; numpy only.
+
+Counting rules (per call):
+  FLOPs = 4 * D * (scored query-key pairs): non-causal pairs are n_q * n_k per (b, h) with padding
+          not subtracted; causal pairs are n(n+1)/2; decode pairs are each query's visible prefix.
+  bytes = q + k + v + o read/written once at the element size (plus, for decode, the cache re-read
+          of every block).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict
+
+import numpy as np
+
+MI355X_PEAK = {  # dense, per GPU
+    "f32_mfma_tflops": 157.3,
+    "f16_mfma_tflops": 2516.6,
+    "bf16_mfma_tflops": 2516.6,
+    "hbm_gbps": 8000.0,
+}
+
+
+def left_pad_valid(rng: np.random.Generator, batch: int, n: int, max_pad: int, lead: int) -> np.ndarray:
+    """(batch, n) uint8 key validity: the first pad_b ~ U{0..max_pad} of the first `lead` keys are
+    invalid (left-padded / missing leading patches); everything else is valid."""
+    kv = np.ones((batch, n), np.uint8)
+    pads = rng.integers(0, max_pad + 1, size=batch)
+    for b, p in enumerate(pads):
+        kv[b, : min(int(p), lead)] = 0
+    return kv
+
+
+@dataclass
+class Workload:
+    name: str
+    dtype: str
+    B: int
+    H: int
+    n_q: int
+    n_k: int
+    D: int = 64
+    scale: float = 1.0
+    arrays: Dict[str, np.ndarray] = field(default_factory=dict)
+    meta: Dict[str, object] = field(default_factory=dict)
+
+    @property
+    def pairs(self) -> int:
+        return int(self.meta.get("pairs", self.B * self.H * self.n_q * self.n_k))
+
+    @property
+    def flops(self) -> float:
+        return 4.0 * self.D * self.pairs
+
+    @property
+    def bytes(self) -> float:
+        return float(self.meta["bytes"])
+
+
+def chronos2(B: int = 64, H: int = 12, n_ctx: int = 512, n_fut: int = 64, seed: int = 0, scale: float = 0.125,
+             theta: float = 10000.0) -> Workload:
+    """Chronos-2 encoder time attention: sequence [512 context patches; REG; 64 future patches]
+    (src/chronos2/forecaster.zig:162-174), RoPE on q and k, additive key mask with 0-25% of the
+    context patches of each series left-padded invalid. Inputs (B, L, H*D) f32 ~ N(0, 1)."""
+    L = n_ctx + 1 + n_fut
+    D = 64
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    k = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    v = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    kv = left_pad_valid(rng, B, L, n_ctx // 4, n_ctx)
+    half = D // 2
+    inv = (1.0 / np.power(np.float32(theta), np.arange(0, D, 2, dtype=np.float32) / np.float32(D))).astype(np.float32)
+    ang = (np.arange(L, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    cos_t = np.cos(ang).astype(np.float32).reshape(L * half)
+    sin_t = np.sin(ang).astype(np.float32).reshape(L * half)
+    w = Workload("chronos2_time_attention", "f32", B, H, L, L, D, scale,
+                 dict(q=q, k=k, v=v, key_valid=kv, rope_cos=cos_t, rope_sin=sin_t),
+                 dict(n_ctx=n_ctx, n_fut=n_fut, theta=theta, seed=seed, num_layers=12))
+    w.meta["bytes"] = 4.0 * 4 * B * L * H * D
+    return w
+
+
+def bolt(B: int = 256, H: int = 12, n_patch: int = 128, seed: int = 0, buckets: int = 32, max_distance: int = 128
+         ) -> Workload:
+    """Chronos-Bolt-base encoder self-attention: [128 patches; REG], no score scale, T5 relative
+    bias from a (buckets, H) table ~ N(0, 0.1), additive mask over left-truncated NaN patches."""
+    L = n_patch + 1
+    D = 64
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    k = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    v = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    kv = left_pad_valid(rng, B, L, n_patch // 4, n_patch)
+    table = (rng.standard_normal((buckets, H)) * 0.1).astype(np.float32)
+    w = Workload("bolt_self_attention", "f32", B, H, L, L, D, 1.0, dict(q=q, k=k, v=v, key_valid=kv, rel_table=table),
+                 dict(buckets=buckets, max_distance=max_distance, seed=seed, num_layers=12))
+    w.meta["bytes"] = 4.0 * 4 * B * L * H * D
+    return w
+
+
+def timestral_prefill(B: int = 32, H: int = 16, L: int = 2048, seed: int = 0, dtype: str = "f16",
+                      pad_rows: float = 0.1, pad_keys: int = 512) -> Workload:
+    """Timestral-shaped causal prefill over L patches: rows (series x variates) folded into B; a
+    fraction of the rows get causal_keys with their oldest `pad_keys` patches invalid."""
+    D = 64
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    k = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    v = rng.standard_normal((B, L, H * D), dtype=np.float32)
+    padded = rng.random(B) < pad_rows
+    kv = np.ones((B, L), np.uint8)
+    kv[padded, :pad_keys] = 0
+    w = Workload("timestral_causal_prefill", dtype, B, H, L, L, D, 1.0 / np.sqrt(D),
+                 dict(q=q, k=k, v=v, key_valid=kv, padded_rows=padded.astype(np.uint8)),
+                 dict(seed=seed, pairs=B * H * L * (L + 1) // 2))
+    w.meta["bytes"] = 2.0 * 4 * B * L * H * D
+    return w
+
+
+def timestral_decode(B: int = 128, H: int = 16, prefix: int = 256, blocks: int = 8, block: int = 32, seed: int = 0,
+                     dtype: str = "bf16") -> Workload:
+    """Block-autoregressive decode against a KV cache: a prefix of `prefix` tokens, then `blocks`
+    blocks of `block` queries; each block is causal over the cache and earlier rows of the block,
+    and appends its K/V before the next block."""
+    D = 64
+    rng = np.random.default_rng(seed)
+    T = prefix + blocks * block
+    q = rng.standard_normal((B, T, H * D), dtype=np.float32)
+    k = rng.standard_normal((B, T, H * D), dtype=np.float32)
+    v = rng.standard_normal((B, T, H * D), dtype=np.float32)
+    pairs = 0
+    reread = 0
+    for i in range(blocks):
+        p0 = prefix + i * block
+        pairs += sum(p0 + t + 1 for t in range(block))
+        reread += (p0 + block) * D * 2 * 2  # K and V of the whole cache, per (b, h)
+    w = Workload("timestral_kv_decode", dtype, B, H, blocks * block, T, D, 1.0 / np.sqrt(D),
+                 dict(q=q, k=k, v=v), dict(prefix=prefix, blocks=blocks, block=block, seed=seed, pairs=B * H * pairs))
+    # q + o of the decoded blocks, the new K/V written once, and every block's cache read.
+    w.meta["bytes"] = float(B * H * (2 * blocks * block * D * 2 + 2 * blocks * block * D * 2) + B * H * reread)
+    return w
