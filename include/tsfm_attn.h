@@ -120,7 +120,8 @@ typedef struct tsfm_attn_args {
     const float *rope_cos, *rope_sin;
     int32_t rope_half; int32_t rope_rows_per_table; int32_t rope_row0; int64_t rope_table_stride;
 
-    void *stream; /* hipStream_t for TSFM_ATTN_DEVICE_PTRS; NULL = this thread's library stream */
+    void *stream; /* hipStream_t the call is queued on with TSFM_ATTN_DEVICE_PTRS (NULL = the null
+                   * stream, as in every HIP call); host-pointer calls use the thread's own stream */
 } tsfm_attn_args;
 
 /* Device set-up, run once per process (cuda/gemm.c:112-166 init_cuda / ensure_cuda). Optional:

@@ -82,3 +82,24 @@ def left_pad_valid(rng, batch, n, max_pad, tail_valid=0):
     for b, p in enumerate(pads):
         kv[b, : min(p, n - tail_valid)] = 0
     return kv
+
+
+def f64_errors(outs, q, k, v, key_valid, n_series, heads, n, scale, bias=None, mask=1, threads=16):
+    """Max scaled error of each array in `outs` (all (B, n, heads*64)) against float64 attention
+    over the first n_series series: how far each f32 evaluation is from exact arithmetic."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def one(b):
+        allowed = allowed_matrix(mask, n, n, None if key_valid is None else key_valid[b])
+        errs = [0.0] * len(outs)
+        for h in range(heads):
+            sel = slice(h * 64, h * 64 + 64)
+            ref = naive_attend(q[b, :, sel], k[b, :, sel], v[b, :, sel], allowed, scale,
+                               None if bias is None else bias[h])
+            for i, o in enumerate(outs):
+                errs[i] = max(errs[i], scaled_err(o[b, :, sel], ref))
+        return errs
+
+    with ThreadPoolExecutor(threads) as ex:
+        per = list(ex.map(one, range(n_series)))
+    return [max(e[i] for e in per) for i in range(len(outs))]

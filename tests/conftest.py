@@ -39,6 +39,21 @@ def orc16():
     return _oracle.Oracle(ROOT / "oracle" / "liboracle_l16.so")
 
 
+def host_has_avx512() -> bool:
+    info = pathlib.Path("/proc/cpuinfo")
+    return info.exists() and " avx512f" in info.read_text()
+
+
+@pytest.fixture(scope="session")
+def orc_host():
+    """The oracle with the f32 lane count the reference would use on this host (nn.lanes =
+    suggestVectorLength(f32), src/core/nn.zig:296): 16 on AVX-512, else 8."""
+    _ensure_oracle()
+    import _oracle
+
+    return _oracle.Oracle(ROOT / "oracle" / ("liboracle_l16.so" if host_has_avx512() else "liboracle_l8.so"))
+
+
 @pytest.fixture(scope="session")
 def ta():
     """The product binding (tsfm-zig_amd/tsfm_attn); fails if the library is not built."""

@@ -133,6 +133,7 @@ def test_keys_additive_all_invalid_row_is_uniform(ta, orc, gpu_ready):
 
 
 def _c2_oracle(orc, w, B):
+    """Oracle output plus the RoPE'd q and k it attended over (for the float64 reference)."""
     q = np.ascontiguousarray(w.arrays["q"][:B]).ravel().copy()
     k = np.ascontiguousarray(w.arrays["k"][:B]).ravel().copy()
     v = np.ascontiguousarray(w.arrays["v"][:B]).ravel()
@@ -141,11 +142,23 @@ def _c2_oracle(orc, w, B):
     orc.chronos2_rope(q, k, w.arrays["rope_cos"], w.arrays["rope_sin"], B * w.n_q, w.n_q, d, w.H, 64)
     o = np.zeros(B * w.n_q * d, np.float32)
     orc.chronos2_time_attention(THREADS, q, k, v, o, kv.ravel(), bool(kv.all()), B, w.n_q, d, w.H, 64, w.scale)
-    return o.reshape(B, w.n_q, d)
+    shape = (B, w.n_q, d)
+    return o.reshape(shape), q.reshape(shape), k.reshape(shape)
+
+
+# Scale-1.0 parity. With q, k ~ N(0, 1) and D = 64 unscaled, logits have standard deviation 8 and
+# the softmax amplifies last-bit differences of the 64-term dot products: the oracle (the
+# reference's f32 arithmetic) is itself 1.25e-5 (Chronos-2, 64 series) and 1.16e-5 (Bolt, 256
+# series) from float64 attention on these inputs, so two correct f32 evaluations can differ by up
+# to the sum of their errors. The bar there is accuracy against exact arithmetic: the GPU must be
+# no further from float64 than the reference's own arithmetic (measured on the same series), and
+# within 2.5e-5 of the oracle. At scale 1/8 (the benchmarked shape) the reference is 8e-7 from
+# float64 and the 1e-5 bar applies directly against the oracle.
+TOL_UNSCALED = 2.5e-5
 
 
 @pytest.mark.parametrize("scale", [0.125, 1.0])
-def test_chronos2_time_attention_full_shape(ta, orc, gpu_ready, scale):
+def test_chronos2_time_attention_full_shape(ta, orc_host, gpu_ready, scale):
     """Chronos-2 time attention at B=64, H=12, L=577 (RoPE, left-padding mask), scale 1/sqrt(64)
     as benchmarked and 1.0 as the model calls it (src/chronos2/model.zig:306)."""
     from tsfm_attn import workloads
@@ -156,13 +169,20 @@ def test_chronos2_time_attention_full_shape(ta, orc, gpu_ready, scale):
     rc = ta.chronos2_time_attention(a["q"], a["k"], a["v"], o, a["rope_cos"], a["rope_sin"], a["key_valid"],
                                     bool(a["key_valid"].all()), w.B, w.n_q, w.H * 64, w.H, 64, scale=scale)
     assert rc == ta.OK, ta.last_error()
-    want = _c2_oracle(orc, w, w.B)
-    assert _ref.scaled_err(o, want) <= TOL
+    want, q_rot, k_rot = _c2_oracle(orc_host, w, w.B)
+    err = _ref.scaled_err(o, want)
+    if scale != 1.0:
+        assert err <= TOL
+        return
+    assert err <= TOL_UNSCALED
+    gpu_f64, orc_f64 = _ref.f64_errors([o, want], q_rot, k_rot, a["v"], a["key_valid"], 16, w.H, w.n_q, scale)
+    assert gpu_f64 <= orc_f64, (gpu_f64, orc_f64)
 
 
-def test_bolt_self_attention_full_shape(ta, orc, gpu_ready):
+def test_bolt_self_attention_full_shape(ta, orc_host, gpu_ready):
     """Chronos-Bolt-base encoder self-attention at B=256, H=12, L=129 with the T5 bias built on the
-    device from the (32, 12) table, against the oracle's positionBias + SelfJob."""
+    device from the (32, 12) table, against the oracle's positionBias + SelfJob (scale 1.0: the
+    accuracy bar above)."""
     from tsfm_attn import workloads
 
     w = workloads.bolt()
@@ -174,11 +194,14 @@ def test_bolt_self_attention_full_shape(ta, orc, gpu_ready):
     rc = ta.bolt_self_attention(a["q"], a["k"], a["v"], o, a["rel_table"], buckets, a["key_valid"],
                                 bool(a["key_valid"].all()), w.B, L, d, H, 64, 32)
     assert rc == ta.OK, ta.last_error()
-    bias = orc.position_bias(a["rel_table"], L, H, 32, 128)
+    bias = orc_host.position_bias(a["rel_table"], L, H, 32, 128)
     want = np.zeros_like(a["q"])
-    orc.bolt_self_attention(THREADS, a["q"], a["k"], a["v"], want, bias, a["key_valid"], bool(a["key_valid"].all()),
-                            w.B, L, d, H, 64)
-    assert _ref.scaled_err(o, want) <= TOL
+    orc_host.bolt_self_attention(THREADS, a["q"], a["k"], a["v"], want, bias, a["key_valid"],
+                                 bool(a["key_valid"].all()), w.B, L, d, H, 64)
+    assert _ref.scaled_err(o, want) <= TOL_UNSCALED
+    gpu_f64, orc_f64 = _ref.f64_errors([o, want], a["q"], a["k"], a["v"], a["key_valid"], w.B, H, L, 1.0,
+                                       bias.reshape(H, L, L))
+    assert gpu_f64 <= orc_f64, (gpu_f64, orc_f64)
     # The dense-bias path (positionBias materialised by the caller) gives the same result.
     o2 = np.zeros_like(a["q"])
     ta.fwd_checked(ta.make_args(q=a["q"], k=a["k"], v=a["v"], o=o2, mask=ta.Mask.KEYS_ADDITIVE, batch=w.B, heads=H,

@@ -275,10 +275,7 @@ int tsfm_attn_fwd(const tsfm_attn_args* a) {
     if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
 
     tsfm::Params p = params_from(a);
-    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
-        hipStream_t s = a->stream != nullptr ? static_cast<hipStream_t>(a->stream) : ctx->stream;
-        return launch(a, p, s);
-    }
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) return launch(a, p, static_cast<hipStream_t>(a->stream));
 
     // Host pointers: stage every input, run, copy the output rows back, synchronise.
     const int64_t B = a->batch, H = a->heads, D = a->head_dim, row = H * D;
@@ -411,8 +408,8 @@ int tsfm_kv_append(tsfm_kv_cache* c, const void* k, int64_t k_tok, int64_t k_bat
     hipError_t e;
     if (flags & TSFM_ATTN_DEVICE_PTRS) {
         if (!aligned(k, 16) || !aligned(v, 16)) return fail(TSFM_E_UNSUPPORTED, "device k/v must be 16-byte aligned");
-        hipStream_t s = stream != nullptr ? static_cast<hipStream_t>(stream) : ctx->stream;
-        e = tsfm::launch_kv_append(L, bf16, k, k_tok, k_batch, v, v_tok, v_batch, c->len, n_new, s);
+        e = tsfm::launch_kv_append(L, bf16, k, k_tok, k_batch, v, v_tok, v_batch, c->len, n_new,
+                                   static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return hip_fail(e, "KV append launch");
     } else {
         const int64_t row = (int64_t)c->H * c->D;
@@ -454,8 +451,8 @@ int tsfm_kv_attend(tsfm_kv_cache* c, const void* q, int64_t q_tok, int64_t q_bat
     hipError_t e;
     if (flags & TSFM_ATTN_DEVICE_PTRS) {
         if (!aligned(q, 16) || !aligned(o, 16)) return fail(TSFM_E_UNSUPPORTED, "device q/o must be 16-byte aligned");
-        hipStream_t s = stream != nullptr ? static_cast<hipStream_t>(stream) : ctx->stream;
-        e = tsfm::launch_kv_attend(L, bf16, q, q_tok, q_batch, o, o_tok, o_batch, n_q, q_pos0, n_k, scale, s);
+        e = tsfm::launch_kv_attend(L, bf16, q, q_tok, q_batch, o, o_tok, o_batch, n_q, q_pos0, n_k, scale,
+                                   static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return hip_fail(e, "KV attend launch");
         return TSFM_OK;
     }

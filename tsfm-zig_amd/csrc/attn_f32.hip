@@ -5,8 +5,8 @@
 // launch and no score matrix exists: K/V tiles of 64 keys are staged in LDS and both products run
 // on the f32 matrix cores (v_mfma_f32_16x16x4_f32) with an online softmax in registers.
 //
-// Wave layout (4 waves x 32 queries):
-//   S^T = K . Q^T   A = K tile rows (16 keys) from LDS, B = Q^T (16 queries) held in VGPRs.
+// Wave layout (4 waves x 32 queries, two 16-query blocks qb per wave):
+//   S^T = K . Q^T   A = K rows (16 keys) from LDS, B = Q^T (16 queries) held in VGPRs.
 //                   Accumulator lane l holds query l%16 and keys 4*(l/16)+r, r=0..3.
 //   O^T += V^T . P^T  A = V^T (16 dims x 4 keys) from LDS, B = P^T straight from the S^T
 //                   accumulator: register r of lane l is key 4*(l/16)+r, exactly the k-slot the
@@ -16,25 +16,65 @@
 // The contraction order over head dims is permuted (lane group g holds dims 8g..8g+7 and
 // 32+8g..32+8g+7) so that every RoPE pair (i, i+32) sits in one lane and K reads are 128-bit.
 //
-// LDS: K tile [64 keys][68] (padded: conflict-free 128-bit reads), V tile [16 key quads][64][4]
-// (transposed so one 128-bit read gives the four keys of one MFMA group), key mask, T5 bias LUT.
+// Accuracy: the f32 matrix instruction rounds after every product, so one 16-step accumulation
+// chain over the 64 head dims carries ~2.5x the rounding error of the reference's lane-parallel
+// dot product (a few sequential products per SIMD lane, then a tree over lanes). S is therefore
+// accumulated in four independent chains of four instructions, summed as a tree, which brings the
+// scores to the reference's accuracy and gives the matrix pipe four independent dependency chains.
+//
+// Pipeline: two LDS stages. While the waves compute on stage t&1, tile t+1 is fetched from HBM and
+// written to the other stage in two 32-key halves (one over the S product, one over softmax and
+// the PV product), so the staging costs 25 registers; one barrier per tile.
+// LDS per stage: K [64 keys][68] (padded: conflict-free 128-bit reads and writes), V [16 key
+// quads][64 dims, XOR-swizzled][4 keys] (conflict-free transposing writes and operand reads), and
+// one additive mask term per key. Two stages + the T5 table fit two workgroups per CU.
 #include "common.hpp"
 #include "launch.hpp"
 
 namespace tsfm {
 namespace {
 
-constexpr int NK = 64;       // keys per LDS tile
-constexpr int QW = 32;       // queries per wave (2 blocks of 16)
+constexpr int NK = 64;          // keys per LDS tile
+constexpr int QW = 32;          // queries per wave (2 blocks of 16)
 constexpr int NWAVE = 4;
+constexpr int NT = 64 * NWAVE;  // threads per workgroup
 constexpr int QT = QW * NWAVE;  // queries per workgroup
-constexpr int KPAD = 68;     // K row pitch in LDS (floats)
+constexpr int KPAD = 68;        // K row pitch in LDS (floats)
+
+struct Stage {
+    float k[NK * KPAD];      // [key][KPAD], RoPE applied
+    float v[NK * kHeadDim];  // [key quad][swizzled dim][4 keys]
+    float kadd[NK];          // additive mask term of each key (0, -FLT_MAX or -inf)
+};
+
+// Swizzled V slot of a head dim: XOR of bits 3..4 into bits 0..1 spreads both the transposing
+// writes (stride 4 dims) and the operand reads (16 consecutive dims) over all LDS banks.
+__device__ __forceinline__ int vslot(int dim) { return dim ^ ((dim >> 3) & 3); }
+
+// Additive mask term of one key: the part of the reference's mask rule (src/core/attn.zig:35-67,
+// src/timestral/model.zig:612-632) that depends on the key alone. Keys past n_k are tile padding.
+template <int MASK>
+__device__ __forceinline__ float key_term(int key, int n_k, bool valid, int ctx_keys) {
+    if (key >= n_k) return kNegInf;
+    if (MASK == KEYS_ADDITIVE) return valid ? 0.f : -kFltMax;
+    if (MASK == CAUSAL_KEYS || MASK == FULL_KEYS) return valid ? 0.f : kNegInf;
+    if (MASK == DECODER) return (key < ctx_keys && valid) ? 0.f : kNegInf;
+    return 0.f;  // FULL, CAUSAL
+}
+
+// The whole mask rule for one scaled, biased score x, given its key term ka.
+template <int MASK>
+__device__ __forceinline__ float masked(float x, float ka, int key, int qpos, int n_k, int chain_start) {
+    if (MASK == CAUSAL) return key <= qpos ? x + ka : kNegInf;
+    if (MASK == CAUSAL_KEYS) return (key == qpos && key < n_k) ? x : (key <= qpos ? x + ka : kNegInf);
+    if (MASK == FULL_KEYS) return (key == qpos && key < n_k) ? x : x + ka;
+    if (MASK == DECODER) return (key >= chain_start && key <= qpos && key < n_k) ? x : x + ka;
+    return x + ka;  // FULL, KEYS_ADDITIVE: x + 0, x + (-FLT_MAX), or -inf for padding
+}
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(256) void attn_fwd_f32(Params p) {
-    __shared__ __attribute__((aligned(16))) float Ks[NK * KPAD];
-    __shared__ __attribute__((aligned(16))) float Vs[NK * kHeadDim];
-    __shared__ __attribute__((aligned(16))) uint8_t kvs[NK];
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_f32(Params p) {
+    __shared__ __attribute__((aligned(16))) Stage stage[2];
     __shared__ float lut[BIAS == BIAS_REL ? kRelMax : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -60,7 +100,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32(Params p) {
     // T5 relative-position bias LUT for this head: lut[j - i + n_q - 1].
     if (BIAS == BIAS_REL) {
         const int n_rel = p.n_q + p.n_k - 1;
-        for (int t = tid; t < n_rel; t += 256)
+        for (int t = tid; t < n_rel; t += NT)
             lut[t] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
     }
 
@@ -109,114 +149,142 @@ __global__ __launch_bounds__(256) void attn_fwd_f32(Params p) {
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) oacc[db][qb] = f32x4{0, 0, 0, 0};
 
-    // Tile loader. K: thread -> (row tid/8 [+32], float4 c4 = tid%8 at dims 4c4 and 32+4c4).
-    // V: thread -> (key quad tid/16, dims 4c..4c+3 with c = tid%16), transposed on the way to LDS.
-    const int k_row = tid >> 3, k_c4 = tid & 7;
-    const int v_kq = tid >> 4, v_c = tid & 15;
-    f32x4 kreg[2][2], creg[2], sreg[2], vreg[4];
-    uint8_t kvreg = 0;
+    // ---- tile staging: HBM -> registers -> LDS, one 32-key half at a time ----
+    // K: thread -> key row tid/8 of the half, dims 4c..4c+3 and 32+4c..32+4c+3 with c = tid%8
+    //    (RoPE pairs). V: thread -> key quad tid/32 of the half, dims 2vc, 2vc+1 with vc = tid%32,
+    //    transposed on the way to LDS. Each half is fetched and stored within one tile's compute,
+    //    so only one half (25 registers) is ever in flight.
+    const int krow = tid >> 3, kc = tid & 7;
+    const int vq = tid >> 5, vc = tid & 31;
+    f32x4 klo, khi, kcos, ksin;
+    float2 v0, v1, v2, v3;
+    float kar = 0.f;
 
-    auto load_tile = [&](int kbase) {
-#pragma unroll
-        for (int ps = 0; ps < 2; ps++) {
-            const int key = kbase + ps * 32 + k_row;
-            if (key < p.n_k) {
-                const float* src = K + (int64_t)key * p.k_tok;
-                kreg[ps][0] = ld4(src + 4 * k_c4);
-                kreg[ps][1] = ld4(src + 32 + 4 * k_c4);
-                if (ROPE) {
-                    creg[ps] = ld4(RC + (int64_t)key * 32 + 4 * k_c4);
-                    sreg[ps] = ld4(RS + (int64_t)key * 32 + 4 * k_c4);
-                }
-            } else {
-                kreg[ps][0] = kreg[ps][1] = f32x4{0, 0, 0, 0};
-                if (ROPE) creg[ps] = sreg[ps] = f32x4{0, 0, 0, 0};
-            }
+    auto fetch = [&](int hbase) {  // keys [hbase, hbase + 32)
+        const bool full = hbase + NK / 2 <= p.n_k;  // uniform
+        const int key = hbase + krow;
+        const int keyc = full ? key : min(key, p.n_k - 1);
+        const float* ks = K + (int64_t)keyc * p.k_tok + 4 * kc;
+        klo = ld4(ks);
+        khi = ld4(ks + 32);
+        if (ROPE) {
+            kcos = ld4(RC + (int64_t)keyc * 32 + 4 * kc);
+            ksin = ld4(RS + (int64_t)keyc * 32 + 4 * kc);
         }
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const int key = kbase + 4 * v_kq + m;
-            vreg[m] = key < p.n_k ? ld4(V + (int64_t)key * p.v_tok + 4 * v_c) : f32x4{0, 0, 0, 0};
+        const int vkey = hbase + 4 * vq;
+        const float* vs = V + 2 * vc;
+        if (full) {
+            v0 = ld2(vs + (int64_t)vkey * p.v_tok);
+            v1 = ld2(vs + (int64_t)(vkey + 1) * p.v_tok);
+            v2 = ld2(vs + (int64_t)(vkey + 2) * p.v_tok);
+            v3 = ld2(vs + (int64_t)(vkey + 3) * p.v_tok);
+        } else {
+            const float2 z = {0.f, 0.f};
+            const int last = p.n_k - 1;
+            v0 = ld2(vs + (int64_t)min(vkey, last) * p.v_tok);
+            v1 = ld2(vs + (int64_t)min(vkey + 1, last) * p.v_tok);
+            v2 = ld2(vs + (int64_t)min(vkey + 2, last) * p.v_tok);
+            v3 = ld2(vs + (int64_t)min(vkey + 3, last) * p.v_tok);
+            if (vkey >= p.n_k) v0 = z;
+            if (vkey + 1 >= p.n_k) v1 = z;
+            if (vkey + 2 >= p.n_k) v2 = z;
+            if (vkey + 3 >= p.n_k) v3 = z;
+            if (key >= p.n_k) klo = khi = f32x4{0, 0, 0, 0};
         }
-        if (mask_reads_valid<MASK>() && tid < NK) kvreg = (kbase + tid < kv_len) ? KV[kbase + tid] : 0;
+        if (tid < NK / 2) {
+            const int kk = hbase + tid;
+            bool valid = true;
+            if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
+            kar = key_term<MASK>(kk, p.n_k, valid, p.ctx_keys);
+        }
     };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int ps = 0; ps < 2; ps++) {
-            f32x4 lo = kreg[ps][0], hi = kreg[ps][1];
-            if (ROPE) rope4(lo, hi, creg[ps], sreg[ps]);
-            float* dst = Ks + (ps * 32 + k_row) * KPAD;
-            st4(dst + 4 * k_c4, lo);
-            st4(dst + 32 + 4 * k_c4, hi);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            st4(Vs + ((v_kq * kHeadDim) + 4 * v_c + j) * 4, f32x4{vreg[0][j], vreg[1][j], vreg[2][j], vreg[3][j]});
-        if (mask_reads_valid<MASK>() && tid < NK) kvs[tid] = kvreg;
+    auto store = [&](Stage& st, int half) {
+        if (ROPE) rope4(klo, khi, kcos, ksin);
+        float* kd = st.k + (half * (NK / 2) + krow) * KPAD + 4 * kc;
+        st4(kd, klo);
+        st4(kd + 32, khi);
+        float* vd = st.v + (half * 8 + vq) * (kHeadDim * 4);
+        st4(vd + vslot(2 * vc) * 4, f32x4{v0.x, v1.x, v2.x, v3.x});
+        st4(vd + vslot(2 * vc + 1) * 4, f32x4{v0.y, v1.y, v2.y, v3.y});
+        if (tid < NK / 2) st.kadd[half * (NK / 2) + tid] = kar;
     };
 
-    if (ntiles > 0) load_tile(0);
-    for (int t = 0; t < ntiles; t++) {
-        const int kbase = t * NK;
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (t + 1 < ntiles) load_tile(kbase + NK);
-        if (kbase >= wave_kend) continue;  // nothing left for this wave (uniform)
+    // V operand offsets of this lane (floats, within a key quad): dim db*16 + ql, swizzled.
+    const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // db even / odd
 
-        // ---- S^T = K . Q^T ----
+    // One 64-key tile on stage `st`. FULLT: every key of the tile is below n_k and every query of
+    // the wave below n_q, so the body has no bounds tests; otherwise only the first nkb key blocks
+    // and nqb query blocks are computed (both uniform) and keys/queries are tested.
+    auto tile = [&](const Stage& st, int kbase, int nkb, int nqb, auto full_tag, int t) {
+        constexpr bool FULLT = decltype(full_tag)::value;
+        const bool more = t + 1 < ntiles;
+        Stage& nxt = stage[(t + 1) & 1];
+        if (more) fetch(kbase + NK);
+
+        // ---- S^T = K . Q^T, four accumulation chains per block ----
         f32x4 sacc[4][2];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-            const bool kb_on = kbase + kb * 16 < wave_kend;
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) sacc[kb][qb] = f32x4{0, 0, 0, 0};
-            if (!kb_on) continue;
-            const float* kr = Ks + (kb * 16 + ql) * KPAD;
+            if (!FULLT && kb >= nkb) continue;
+            const float* kr = st.k + (kb * 16 + ql) * KPAD;
             const f32x4 k0 = ld4(kr + 8 * g), k1 = ld4(kr + 8 * g + 4);
             const f32x4 k2 = ld4(kr + 32 + 8 * g), k3 = ld4(kr + 32 + 8 * g + 4);
             const float kv16[16] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3],
                                     k2[0], k2[1], k2[2], k2[3], k3[0], k3[1], k3[2], k3[3]};
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) {
-                if (16 * qb >= wave_nq) continue;
-                f32x4 acc = {0, 0, 0, 0};
+                if (!FULLT && qb >= nqb) continue;
+                f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
 #pragma unroll
-                for (int s = 0; s < 16; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s], qreg[qb][s], acc, 0, 0, 0);
-                sacc[kb][qb] = acc;
+                for (int s = 0; s < 16; s += 4) {
+                    c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s], qreg[qb][s], c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 1], qreg[qb][s + 1], c1, 0, 0, 0);
+                    c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 2], qreg[qb][s + 2], c2, 0, 0, 0);
+                    c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 3], qreg[qb][s + 3], c3, 0, 0, 0);
+                }
+                sacc[kb][qb] = (c0 + c1) + (c2 + c3);
+                // Materialise the sum here: left alone, the optimiser sinks it to the softmax and
+                // keeps all 32 chain accumulators of the tile live (~130 more registers).
+                asm volatile("" : "+v"(sacc[kb][qb]));
             }
+        }
+
+        // First half of the next tile to LDS while the matrix cores work; fetch its second half.
+        if (more) {
+            store(nxt, 0);
+            fetch(kbase + NK + NK / 2);
         }
 
         // ---- scale, bias, mask, online softmax ----
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
-            if (16 * qb >= wave_nq) continue;
+            if (!FULLT && qb >= nqb) continue;
             const int qi = wq0 + 16 * qb + ql;
             const int qpos = p.q_pos0 + qi;
             float mloc = kNegInf;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
-                const bool kb_on = kbase + kb * 16 < wave_kend;
-                uint32_t vw = 0;
-                if (mask_reads_valid<MASK>()) vw = *reinterpret_cast<const uint32_t*>(kvs + kb * 16 + 4 * g);
+                const bool on = FULLT || kb < nkb;
+                const f32x4 ka = ld4(st.kadd + kb * 16 + 4 * g);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int key = kbase + kb * 16 + 4 * g + r;
                     float x = kNegInf;
-                    if (kb_on) {
+                    if (on) {
 #pragma clang fp contract(off)
                         x = sacc[kb][qb][r] * p.scale;
                         if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), kRelMax - 1)];
-                        if (BIAS == BIAS_DENSE && key < p.n_k && qi < p.n_q)
+                        if (BIAS == BIAS_DENSE && (FULLT || (key < p.n_k && qi < p.n_q)))
                             x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
-                        x = apply_mask<MASK>(x, key, qpos, p.n_k, ((vw >> (8 * r)) & 0xff) != 0, p.ctx_keys,
-                                             p.chain_start);
+                        x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
                     }
                     sacc[kb][qb][r] = x;
                     mloc = fmaxf(mloc, x);
                 }
             }
-            const float m_new = fmaxf(m_run[qb], rows4_max(mloc));
+            const float m_new = fmaxf(m_run[qb], max4(mloc));
             const float m_use = m_new == kNegInf ? 0.f : m_new;
             const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * kLog2e);
             float lsum = 0.f;
@@ -237,26 +305,55 @@ __global__ __launch_bounds__(256) void attn_fwd_f32(Params p) {
         // ---- O^T += V^T . P^T ----
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-            if (kbase + kb * 16 >= wave_kend) continue;
+            if (!FULLT && kb >= nkb) continue;
+            const float* vq4 = st.v + (kb * 4 + g) * (kHeadDim * 4);
+            f32x4 va[4];
 #pragma unroll
-            for (int db = 0; db < 4; db++) {
-                const f32x4 va = ld4(Vs + ((kb * 4 + g) * kHeadDim + db * 16 + ql) * 4);
+            for (int db = 0; db < 4; db++) va[db] = ld4(vq4 + db * 64 + ((db & 1) ? voff_odd - 64 : voff_even));
 #pragma unroll
-                for (int qb = 0; qb < 2; qb++) {
-                    if (16 * qb >= wave_nq) continue;
+            for (int r = 0; r < 4; r++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        oacc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[r], sacc[kb][qb][r], oacc[db][qb], 0, 0, 0);
-                }
-            }
+                for (int db = 0; db < 4; db++)
+#pragma unroll
+                    for (int qb = 0; qb < 2; qb++) {
+                        if (!FULLT && qb >= nqb) continue;
+                        oacc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db][r], sacc[kb][qb][r], oacc[db][qb], 0, 0, 0);
+                    }
         }
+        if (more) store(nxt, 1);
+    };
+
+    if (ntiles > 0) {
+        fetch(0);
+        store(stage[0], 0);
+        fetch(NK / 2);
+        store(stage[0], 1);
+    }
+    __syncthreads();
+    const int nqb = (wave_nq + 15) >> 4;
+    for (int t = 0; t < ntiles; t++) {
+        const int kbase = t * NK;
+        const Stage& st = stage[t & 1];
+        const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
+        // Full tile: all 64 keys below wave_kend (<= n_k) and all 32 queries below n_q.
+        if (kbase + NK <= wave_kend && wave_nq == QW) {
+            tile(st, kbase, 4, 2, std::integral_constant<bool, true>{}, t);
+        } else if (nkb > 0 && nqb > 0) {
+            tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
+        } else if (t + 1 < ntiles) {
+            fetch(kbase + NK);
+            store(stage[(t + 1) & 1], 0);
+            fetch(kbase + NK + NK / 2);
+            store(stage[(t + 1) & 1], 1);
+        }
+        __syncthreads();
     }
 
     // ---- normalise and store: lane holds query ql, dims 16db + 4g + r ----
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
         const int qi = wq0 + 16 * qb + ql;
-        const float l = rows4_sum(l_run[qb]);
+        const float l = sum4(l_run[qb]);
         if (qi >= p.n_q) continue;
         const float inv = 1.0f / l;
         float* dst = O + (int64_t)qi * p.o_tok;
@@ -270,7 +367,7 @@ hipError_t launch_one(const Params& p, hipStream_t stream) {
     const int q_tiles = (p.n_q + QT - 1) / QT;
     const int64_t blocks = (int64_t)p.B * p.H * q_tiles;
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_f32<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((attn_fwd_f32<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(NT), 0, stream, p);
     return hipGetLastError();
 }
 

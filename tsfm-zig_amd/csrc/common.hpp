@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace tsfm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -95,16 +97,24 @@ __device__ __forceinline__ void rope4(f32x4& lo, f32x4& hi, f32x4 c, f32x4 s) {
 }
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ float2 ld2(const float* p) { return *reinterpret_cast<const float2*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
-// Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
-__device__ __forceinline__ float rows4_max(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16));
-    return fmaxf(x, __shfl_xor(x, 32));
+// Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48), on the VALU with
+// gfx950's lane swaps: permlane32_swap(x, x) returns (x of lanes 0-31 in both halves, x of lanes
+// 32-63 in both halves), permlane16_swap likewise for even/odd 16-lane rows. Every lane ends with
+// the same value, combined in the same order.
+__device__ __forceinline__ float max4(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-__device__ __forceinline__ float rows4_sum(float x) {
-    x += __shfl_xor(x, 16);
-    return x + __shfl_xor(x, 32);
+__device__ __forceinline__ float sum4(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 }  // namespace tsfm

@@ -157,6 +157,15 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     p = pathlib.Path(path) if path is not None else LIB_PATH
     if not p.exists():
         raise FileNotFoundError(f"{p} is not built: run `make -C tsfm-zig_amd` (or __graft_entry__.build())")
+    # A process must hold exactly one HIP runtime. torch wheels bundle their own libamdhip64
+    # (soname libamdhip64.so.7) and their HIP libraries ask for it by the unversioned name, so a
+    # system runtime loaded first (by this library) would not satisfy them and torch would load a
+    # second one, under which it sees no device and its streams mean nothing to this library.
+    # Loading torch first lets this library's libamdhip64.so.7 dependency bind to torch's copy.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(p))
     vp, i32, i64, u32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
     lib.tsfm_attn_init.restype = ctypes.c_int
