@@ -8,7 +8,8 @@ algorithmic TFLOP/s over the kernel's event-timed average duration vs the f32 ma
 series-forecasts/sec of one call, and the CPU baseline: the C restatement of the reference's CPU
 attention (oracle/, `kind: port`) timed on this host's cores over the same inputs.
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode]
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt]
+    python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
 import json
@@ -135,6 +136,8 @@ def main() -> int:
     ap.add_argument("--workload", default="chronos2", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-series", type=int, default=None, help="series in the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB, 3 times (counter calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -150,6 +153,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
+    if args.copy_mib:
+        n = args.copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": n * 4, "launches": 3}), flush=True)
+        return 0
     if not ta.available():
         print(f"bench.py: libtsfm_attn unavailable: {ta.last_error()}", file=sys.stderr)
         return 1
@@ -160,15 +172,18 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # One event pair per launch, recorded on the stream the kernel runs on (the same per-dispatch
+    # duration rocprofv3 --kernel-trace reports); wall time around the whole loop gives `value`.
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        starts[i].record(stream)
         step()
-    end.record(stream)
+        ends[i].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = start.elapsed_time(end) / args.steps
+    kernel_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / args.steps
     ms_per_step = wall * 1e3 / args.steps
 
     achieved = w.flops / (kernel_ms * 1e-3) / 1e12
