@@ -1,14 +1,21 @@
 #!/usr/bin/env python3
-"""Benchmark of the gfx950 attention path at the Chronos-2 time-attention shape.
+"""Benchmark of the gfx950 attention path.
 
-A step is one batched attention call over the whole synthetic batch (B=64 series x 12 heads,
-L=577 tokens, D=64, f32, RoPE, left-padding key mask, scale 1/8) with every input already resident
-in HBM. Prints one JSON line with whole-job TFLOP/s, the roofline of the kernel (achieved
-algorithmic TFLOP/s over the kernel's event-timed average duration vs the f32 matrix peak), the
-series-forecasts/sec of one call, and the CPU baseline: the C restatement of the reference's CPU
-attention (oracle/, `kind: port`) timed on this host's cores over the same inputs.
+Default workload (the metric's): Chronos-2 time attention, B=64 series x 12 heads, L=577 tokens,
+D=64, f32, RoPE, left-padding key mask, scale 1/8. A step is one batched attention call over the
+whole synthetic batch with every input already resident in HBM. Prints one JSON line with
+whole-job TFLOP/s, the roofline of the dominant kernel (algorithmic work over its HIP-event-timed
+mean launch duration, against the MI355X peak that bounds it), series-forecasts/sec, and the CPU
+baseline: the C restatement of the reference's CPU attention (oracle/, `kind: port`) timed on this
+host's cores over a sample of the same inputs.
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt]
+Other workloads (parity-test shapes, measured the same way):
+  bolt     Chronos-Bolt-base encoder self-attention, B=256 H=12 L=129, f32, T5 bias, no scale
+  prefill  Timestral-shaped causal prefill, f16, B=32 rows H=16 L=2048, 10 % rows key-padded
+  decode   Timestral-shaped KV-cached block decode, bf16, B=128 H=16, prefix 256 + 8 x 32;
+           a step rewinds the cache to the prefix and runs 8 x (append 32, attend 32)
+
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
@@ -17,6 +24,8 @@ import os
 import pathlib
 import sys
 import time
+from dataclasses import dataclass
+from typing import Callable, Optional
 
 import numpy as np
 
@@ -33,99 +42,206 @@ def cpu_threads() -> int:
 
 
 def oracle_path() -> pathlib.Path:
-    flags = pathlib.Path("/proc/cpuinfo").read_text() if pathlib.Path("/proc/cpuinfo").exists() else ""
+    """The oracle build with the f32 lane count the reference picks on this host (nn.lanes)."""
+    info = pathlib.Path("/proc/cpuinfo")
+    flags = info.read_text() if info.exists() else ""
     lib16 = ROOT / "oracle" / "liboracle_l16.so"
     return lib16 if (" avx512f" in flags and lib16.exists()) else ROOT / "oracle" / "liboracle_l8.so"
 
 
 def traffic_for(workload: str):
+    """Measured HBM bytes per launch of the dominant kernel (rocprofv3 FETCH_SIZE/WRITE_SIZE,
+    calibrated against a plain copy), or None when not measured for this workload."""
     p = ROOT / "profiles" / "traffic.json"
     if p.exists():
         return json.loads(p.read_text()).get(workload)
     return None
 
 
-def run_chronos2(args, torch, ta, workloads):
+@dataclass
+class Bench:
+    w: object                          # tsfm_attn.workloads.Workload
+    step: Callable[[], None]
+    output: Callable[[], np.ndarray]   # f32 numpy of the step's result, for the parity check
+    cpu_leg: Callable[[int], tuple]    # n_series -> (seconds, expected output, lanes)
+    config: dict
+    dtype: str
+    bound: str                         # "mfma" or "hbm"
+    peak: float
+    unit: str
+    cpu_default: int                   # series in the default CPU sample
+    # For a step of several launches: the mean duration (ms) of the dominant kernel over the
+    # timed steps, from events the step recorded around it; None = the step is one launch.
+    kernel_ms: Optional[Callable[[], float]] = None
+    kernel_work: Optional[float] = None  # algorithmic work per dominant launch (bound's unit)
+
+
+def _check(ta, rc):
+    if rc != ta.OK:
+        raise RuntimeError(f"tsfm_attn returned {rc}: {ta.last_error()}")
+
+
+def _orc():
+    import _oracle
+
+    return _oracle.Oracle(oracle_path())
+
+
+def run_chronos2(torch, ta, workloads, peak):
     w = workloads.chronos2()
     a = w.arrays
     dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).cuda() for n in ("q", "k", "v", "key_valid", "rope_cos", "rope_sin")}
     o = torch.empty_like(dev["q"])
-    stream = torch.cuda.current_stream()
     all_valid = bool(a["key_valid"].all())
+    d = w.H * 64
 
     def step():
-        rc = ta.chronos2_time_attention(dev["q"], dev["k"], dev["v"], o, dev["rope_cos"], dev["rope_sin"],
-                                        dev["key_valid"], all_valid, w.B, w.n_q, w.H * 64, w.H, 64, scale=w.scale,
-                                        stream=stream)
-        if rc != ta.OK:
-            raise RuntimeError(f"tsfm_attn_fwd returned {rc}: {ta.last_error()}")
+        _check(ta, ta.chronos2_time_attention(dev["q"], dev["k"], dev["v"], o, dev["rope_cos"], dev["rope_sin"],
+                                              dev["key_valid"], all_valid, w.B, w.n_q, d, w.H, 64, scale=w.scale))
 
-    config = {"workload": w.name, "B": w.B, "H": w.H, "L": w.n_q, "D": 64, "mask": "keys_additive", "rope": True,
-              "scale": w.scale, "layout": "(B, L, H*D) f32"}
-
-    def cpu_leg(n_series):
-        import _oracle
-
-        orc = _oracle.Oracle(oracle_path())
-        B = n_series
+    def cpu_leg(B):
+        orc = _orc()
         q = np.ascontiguousarray(a["q"][:B]).ravel().copy()
         k = np.ascontiguousarray(a["k"][:B]).ravel().copy()
         v = np.ascontiguousarray(a["v"][:B]).ravel()
         kv = np.ascontiguousarray(a["key_valid"][:B]).ravel()
-        d = w.H * 64
         out = np.zeros(B * w.n_q * d, np.float32)
         t0 = time.perf_counter()
         # The reference path this call replaces: serial RoPE loop, then forRange(b*nh, TimeJob.attend).
         orc.chronos2_rope(q, k, a["rope_cos"], a["rope_sin"], B * w.n_q, w.n_q, d, w.H, 64)
         orc.chronos2_time_attention(cpu_threads(), q, k, v, out, kv, bool(kv.all()), B, w.n_q, d, w.H, 64, w.scale)
-        dt = time.perf_counter() - t0
-        return dt, out.reshape(B, w.n_q, d), orc.lanes
+        return time.perf_counter() - t0, out.reshape(B, w.n_q, d), orc.lanes
 
-    return w, step, o, config, cpu_leg
+    config = {"workload": w.name, "B": w.B, "H": w.H, "L": w.n_q, "D": 64, "mask": "keys_additive", "rope": True,
+              "scale": w.scale, "layout": "(B, L, H*D) f32"}
+    return Bench(w, step, lambda: o.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
+                 "TFLOP/s", w.B)
 
 
-def run_bolt(args, torch, ta, workloads):
+def run_bolt(torch, ta, workloads, peak):
     w = workloads.bolt()
     a = w.arrays
-    L = w.n_q
+    L, d = w.n_q, w.H * 64
     buckets = np.zeros(2 * L - 1, np.int32)
-    ta.load().tsfm_t5_bucket_table(buckets.ctypes.data, L, L, 32, 128)
+    _check(ta, ta.load().tsfm_t5_bucket_table(buckets.ctypes.data, L, L, 32, 128))
     dev = {n: torch.from_numpy(np.ascontiguousarray(x)).cuda() for n, x in
            dict(q=a["q"], k=a["k"], v=a["v"], key_valid=a["key_valid"], rel_table=a["rel_table"], buckets=buckets).items()}
     o = torch.empty_like(dev["q"])
-    stream = torch.cuda.current_stream()
     all_valid = bool(a["key_valid"].all())
 
     def step():
-        rc = ta.bolt_self_attention(dev["q"], dev["k"], dev["v"], o, dev["rel_table"], dev["buckets"], dev["key_valid"],
-                                    all_valid, w.B, L, w.H * 64, w.H, 64, 32, stream=stream)
-        if rc != ta.OK:
-            raise RuntimeError(f"tsfm_attn_fwd returned {rc}: {ta.last_error()}")
+        _check(ta, ta.bolt_self_attention(dev["q"], dev["k"], dev["v"], o, dev["rel_table"], dev["buckets"],
+                                          dev["key_valid"], all_valid, w.B, L, d, w.H, 64, 32))
 
-    config = {"workload": w.name, "B": w.B, "H": w.H, "L": L, "D": 64, "mask": "keys_additive", "bias": "t5 32/128",
-              "scale": 1.0, "layout": "(B, L, H*D) f32"}
-
-    def cpu_leg(n_series):
-        import _oracle
-
-        orc = _oracle.Oracle(oracle_path())
-        B = n_series
+    def cpu_leg(B):
+        orc = _orc()
         q = np.ascontiguousarray(a["q"][:B]).ravel()
         k = np.ascontiguousarray(a["k"][:B]).ravel()
         v = np.ascontiguousarray(a["v"][:B]).ravel()
         kv = np.ascontiguousarray(a["key_valid"][:B]).ravel()
-        d = w.H * 64
         out = np.zeros(B * L * d, np.float32)
         t0 = time.perf_counter()
         bias = orc.position_bias(a["rel_table"], L, w.H, 32, 128)
         orc.bolt_self_attention(cpu_threads(), q, k, v, out, bias, kv, bool(kv.all()), B, L, d, w.H, 64)
-        dt = time.perf_counter() - t0
-        return dt, out.reshape(B, L, d), orc.lanes
+        return time.perf_counter() - t0, out.reshape(B, L, d), orc.lanes
 
-    return w, step, o, config, cpu_leg
+    config = {"workload": w.name, "B": w.B, "H": w.H, "L": L, "D": 64, "mask": "keys_additive", "bias": "t5 32/128",
+              "scale": 1.0, "layout": "(B, L, H*D) f32"}
+    return Bench(w, step, lambda: o.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
+                 "TFLOP/s", w.B)
 
 
-WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt}
+def run_prefill(torch, ta, workloads, peak):
+    w = workloads.timestral_prefill()
+    a = w.arrays
+    row = w.H * 64
+    dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).to(torch.float16).cuda() for n in ("q", "k", "v")}
+    kvd = torch.from_numpy(np.ascontiguousarray(a["key_valid"])).cuda()
+    o = torch.empty_like(dev["q"])
+    mask = ta.Mask.pick(True, bool(a["key_valid"].all()), False)  # per chunk, as the reference decides
+    args = ta.make_args(q=dev["q"], k=dev["k"], v=dev["v"], o=o, mask=mask, batch=w.B, heads=w.H, n_q=w.n_q,
+                        n_k=w.n_k, q_tok=row, q_batch=w.n_q * row, k_tok=row, k_batch=w.n_k * row, v_tok=row,
+                        v_batch=w.n_k * row, o_tok=row, o_batch=w.n_q * row, scale=w.scale, key_valid=kvd,
+                        kv_batch=w.n_k)
+
+    def step():
+        _check(ta, ta.fwd(args))
+
+    def cpu_leg(B):
+        orc = _orc()
+        r = lambda x: np.ascontiguousarray(x[:B]).astype(np.float16).astype(np.float32)
+        q, k, v = r(a["q"]), r(a["k"]), r(a["v"])
+        kv = np.ascontiguousarray(a["key_valid"][:B])
+        out = np.zeros((B, w.n_q, row), np.float32)
+        t0 = time.perf_counter()
+        orc.batched_self_attend(cpu_threads(), int(mask), q, row, w.n_q * row, k, row, w.n_k * row, v, row,
+                                w.n_k * row, out, row, w.n_q * row, kv, w.n_k, None, B, w.H, w.n_q, 64, w.scale)
+        return time.perf_counter() - t0, out, orc.lanes
+
+    config = {"workload": w.name, "B": w.B, "H": w.H, "L": w.n_q, "D": 64, "mask": mask.name.lower(),
+              "padded_rows": int(a["padded_rows"].sum()), "scale": w.scale, "layout": "(B, L, H*D) f16"}
+    return Bench(w, step, lambda: o.float().cpu().numpy(), cpu_leg, config, "f16", "mfma", peak["f16_mfma_tflops"],
+                 "TFLOP/s", 8)
+
+
+def run_decode(torch, ta, workloads, peak):
+    w = workloads.timestral_decode()
+    a = w.arrays
+    P, nb, blk = w.meta["prefix"], w.meta["blocks"], w.meta["block"]
+    row, T = w.H * 64, P + nb * blk
+    dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).to(torch.bfloat16).cuda() for n in ("q", "k", "v")}
+    out = torch.zeros((w.B, nb * blk, row), dtype=torch.bfloat16, device="cuda")
+    cache = ta.KvCache(ta.DTYPE_BF16, w.B, w.H, T)
+    cache.append(dev["k"], dev["v"], P, row, T * row, row, T * row)
+    stream = torch.cuda.current_stream()
+    events = []  # (start, end) around every attend launch of the timed steps
+
+    def step(record=True):
+        cache.truncate(P)
+        for i in range(nb):
+            p0 = P + i * blk
+            cache.append(dev["k"][:, p0:], dev["v"][:, p0:], blk, row, T * row, row, T * row)
+            if record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+            cache.attend(dev["q"][:, p0:], out[:, i * blk:], blk, p0, w.scale, row, T * row, row, nb * blk * row)
+            if record:
+                e1.record(stream)
+                events.append((e0, e1))
+
+    def kernel_ms():
+        return sum(a0.elapsed_time(a1) for a0, a1 in events) / len(events)
+
+    def cpu_leg(B):
+        orc = _orc()
+        r = lambda x: np.ascontiguousarray(x[:B]).astype(np.float32)
+        bf = lambda x: torch.from_numpy(r(x)).to(torch.bfloat16).float().numpy()
+        q, k, v = bf(a["q"]), bf(a["k"]), bf(a["v"])
+        want = np.zeros((B, nb * blk, row), np.float32)
+        full = np.zeros((B, T, row), np.float32)
+        t0 = time.perf_counter()
+        # The reference's way (src/timestral/forecaster.zig:466-561): every block re-encodes the whole
+        # grown context, i.e. causal selfAttend over P + 32(i+1) tokens; block i's rows are its output.
+        for i in range(nb):
+            n = P + (i + 1) * blk
+            orc.batched_self_attend(cpu_threads(), 2, q, row, T * row, k, row, T * row, v, row, T * row, full, row,
+                                    T * row, None, 0, None, B, w.H, n, 64, w.scale)
+            want[:, i * blk:(i + 1) * blk] = full[:, n - blk:n]
+        return time.perf_counter() - t0, want, orc.lanes
+
+    # Work of the dominant kernel (kv_attend), per launch, averaged over the 8 blocks: cache K/V
+    # read + q read + o written, in bytes.
+    bytes_per_attend = w.B * w.H * sum((P + i * blk + blk) * 64 * 2 * 2 + 2 * blk * 64 * 2 for i in range(nb)) / nb
+    config = {"workload": w.name, "B": w.B, "H": w.H, "D": 64, "prefix": P, "blocks": nb, "block": blk,
+              "mask": "causal", "scale": w.scale, "layout": "(B, T, H*D) bf16; cache K [B][H][cap][64], V chunked"}
+    b = Bench(w, lambda: step(True), lambda: out.float().cpu().numpy(), cpu_leg, config, "bf16", "hbm",
+              peak["hbm_gbps"], "GB/s", 8, kernel_ms, bytes_per_attend / 1e9)
+    b.warm = lambda: step(False)
+    b.reset_events = events.clear
+    return b
+
+
+WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode}
 
 
 def main() -> int:
@@ -134,7 +250,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="chronos2", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-series", type=int, default=None, help="series in the CPU-baseline sample")
+    ap.add_argument("--cpu-series", type=int, default=None, help="series (rows) in the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, 3 times (counter calibration)")
@@ -166,29 +282,39 @@ def main() -> int:
         print(f"bench.py: libtsfm_attn unavailable: {ta.last_error()}", file=sys.stderr)
         return 1
 
-    w, step, o, config, cpu_leg = WORKLOADS[args.workload](args, torch, ta, workloads)
+    bench = WORKLOADS[args.workload](torch, ta, workloads, workloads.MI355X_PEAK)
+    w = bench.w
     stream = torch.cuda.current_stream()
 
+    warm = getattr(bench, "warm", bench.step)
     for _ in range(args.warmup):
-        step()
+        warm()
     torch.cuda.synchronize()
-    # One event pair per launch, recorded on the stream the kernel runs on (the same per-dispatch
-    # duration rocprofv3 --kernel-trace reports); wall time around the whole loop gives `value`.
+    # Timed region: the steps between two full synchronisations. A single-launch step gets one
+    # event pair per launch on the stream the kernel runs on (the per-dispatch duration rocprofv3
+    # --kernel-trace reports); a multi-launch step records its dominant kernel itself.
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     t0 = time.perf_counter()
     for i in range(args.steps):
         starts[i].record(stream)
-        step()
+        bench.step()
         ends[i].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / args.steps
     ms_per_step = wall * 1e3 / args.steps
+    step_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / args.steps
+    if bench.kernel_ms is not None:
+        kernel_ms = bench.kernel_ms()
+        work = bench.kernel_work
+    else:
+        kernel_ms = step_ms
+        work = w.flops / 1e12 if bench.bound == "mfma" else w.bytes / 1e9
 
-    achieved = w.flops / (kernel_ms * 1e-3) / 1e12
-    peak = workloads.MI355X_PEAK["f32_mfma_tflops"]
+    achieved = work / (kernel_ms * 1e-3)
     value = w.flops / (ms_per_step * 1e-3) / 1e12
+    flop_peak = workloads.MI355X_PEAK["f32_mfma_tflops" if bench.dtype == "f32" else "f16_mfma_tflops"]
+    n_layers = w.meta.get("num_layers")
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -200,19 +326,17 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": bench.dtype,
         "data": "synthetic",
-        "config": config,
-        "mfma_peak_frac": round(value / peak, 4),
+        "config": bench.config,
+        "mfma_peak_frac": round(value / flop_peak, 4),
         "series_forecasts_per_s": round(w.B / (ms_per_step * 1e-3), 1),
-        "series_forecasts_per_s_all_layers": round(w.B / (ms_per_step * 1e-3 * w.meta["num_layers"]), 1),
-        "num_layers": w.meta["num_layers"],
         "roofline": {
-            "bound": "mfma",
+            "bound": bench.bound,
             "achieved": round(achieved, 3),
-            "peak": peak,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4),
+            "peak": bench.peak,
+            "unit": bench.unit,
+            "frac": round(achieved / bench.peak, 4),
             "traffic": traffic_for(w.name),
             "algorithmic_flops": w.flops,
             "algorithmic_bytes": w.bytes,
@@ -220,11 +344,14 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if n_layers:
+        line["series_forecasts_per_s_all_layers"] = round(w.B / (ms_per_step * 1e-3 * n_layers), 1)
+        line["num_layers"] = n_layers
 
     if not args.no_cpu:
-        n_series = args.cpu_series or w.B
-        dt, want, lanes = cpu_leg(n_series)
-        got = o.cpu().numpy()[:n_series]
+        n_series = min(w.B, args.cpu_series or bench.cpu_default)
+        dt, want, lanes = bench.cpu_leg(n_series)
+        got = bench.output()[:n_series]
         import _ref
 
         sample_flops = w.flops * n_series / w.B
@@ -234,7 +361,7 @@ def main() -> int:
             "cores": cpu_threads(),
             "kind": "port",
             "sample": f"{n_series} of {w.B} series x {w.H} heads, same inputs; C restatement of the reference CPU "
-                      f"path ({lanes} f32 lanes), {dt:.2f} s",
+                      f"path ({lanes} f32 lanes, {cpu_threads()} threads), {dt:.2f} s",
             "series_forecasts_per_s": round(n_series / dt, 2),
             "gpu_speedup": round((dt / n_series) / (ms_per_step * 1e-3 / w.B), 1),
         }

@@ -156,10 +156,14 @@ int tsfm_t5_bucket_table(int32_t *out, int32_t n_q, int32_t n_k, uint32_t num_bu
  * [pos][D]; V in 32-key chunks transposed for the matrix cores). bf16 and f16 only. */
 typedef struct tsfm_kv_cache tsfm_kv_cache;
 
+/* Capacity is rounded up to a multiple of 64 tokens; the cache memory is zero-filled. */
 int tsfm_kv_create(tsfm_kv_cache **out, int32_t dtype, int32_t batch, int32_t heads, int32_t head_dim,
                    int32_t capacity);
 int tsfm_kv_free(tsfm_kv_cache *cache);
 int tsfm_kv_reset(tsfm_kv_cache *cache);
+/* Rewind the cache to its first `len` tokens (len <= tsfm_kv_len): a forecast that restarts from
+ * the same prefix keeps the prefix's K/V. */
+int tsfm_kv_truncate(tsfm_kv_cache *cache, int32_t len);
 int32_t tsfm_kv_len(const tsfm_kv_cache *cache);
 
 /* Append n_new tokens to every (b, h): k/v element (b, t, h, c) at b * batch + t * tok + h * D + c.

@@ -362,7 +362,8 @@ int tsfm_kv_create(tsfm_kv_cache** out, int32_t dtype, int32_t batch, int32_t he
     if (batch <= 0 || heads <= 0 || capacity <= 0) return fail(TSFM_E_INVALID, "bad cache shape");
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
-    const int32_t cap = (capacity + 31) / 32 * 32;
+    // Whole 64-key tiles: the decode kernel reads every row of the tiles it touches.
+    const int32_t cap = (capacity + 63) / 64 * 64;
     const size_t bytes = (size_t)batch * heads * cap * head_dim * 2;
     tsfm_kv_cache* c = new tsfm_kv_cache{dtype, batch, heads, head_dim, cap, 0, nullptr, nullptr};
     if (hipSetDevice(g_device) != hipSuccess || hipMalloc(&c->k, bytes) != hipSuccess ||
@@ -370,6 +371,14 @@ int tsfm_kv_create(tsfm_kv_cache** out, int32_t dtype, int32_t batch, int32_t he
         if (c->k) (void)hipFree(c->k);
         delete c;
         return fail(TSFM_E_DEVICE, "KV cache allocation of 2 x %zu bytes failed", bytes);
+    }
+    // Rows past the length are read (and masked) by the decode kernel: keep them finite.
+    if (hipMemset(c->k, 0, bytes) != hipSuccess || hipMemset(c->v, 0, bytes) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(c->k);
+        (void)hipFree(c->v);
+        delete c;
+        return fail(TSFM_E_DEVICE, "KV cache initialisation failed");
     }
     *out = c;
     return TSFM_OK;
@@ -387,6 +396,13 @@ int tsfm_kv_free(tsfm_kv_cache* c) {
 int tsfm_kv_reset(tsfm_kv_cache* c) {
     if (c == nullptr) return fail(TSFM_E_INVALID, "cache is NULL");
     c->len = 0;
+    return TSFM_OK;
+}
+
+int tsfm_kv_truncate(tsfm_kv_cache* c, int32_t len) {
+    if (c == nullptr) return fail(TSFM_E_INVALID, "cache is NULL");
+    if (len < 0 || len > c->len) return fail(TSFM_E_INVALID, "truncate to %d outside [0, %d]", len, c->len);
+    c->len = len;
     return TSFM_OK;
 }
 

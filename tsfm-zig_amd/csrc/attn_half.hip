@@ -1,4 +1,416 @@
+// Fused bf16 / f16 attention with f32 accumulation for gfx950: one workgroup = one (series, head)
+// x 128 queries, 4 waves x 32 queries, 64-key tiles.
+//
+// Same algorithm as attn_f32.hip (the reference's gemmNT -> bias -> masked softmax -> gemmNN,
+// src/core/attn.zig:72-96, fused into one pass with an online softmax), on the half-precision
+// matrix cores: v_mfma_f32_16x16x32_{f16,bf16}.
+//
+//   S^T = K . Q^T   A = 16 K rows x 32 dims (lane: key l%16, dims 8*(l/16)..+7) from LDS,
+//                   B = Q^T from registers; two instructions cover the 64 head dims. Accumulator
+//                   lane l holds query l%16 and keys 4*(l/16)+r.
+//   O^T += V^T . P^T  per 32-key chunk: B = P^T packed from the two S^T accumulators of the chunk
+//                   (k-slot 8g+j = key 4g+j for j<4, key 16+4g+(j-4) for j>=4), A = V^T from LDS
+//                   stored in exactly that key order: [key octet (chunk, g)][dim][8 keys].
+// Softmax in f32 registers; P is rounded to the input type for the second product (round to
+// nearest even); the row sum uses the unrounded f32 probabilities.
+//
+// The score scale is folded into the exponent: e = exp2(s * scale*log2(e) - m * scale*log2(e)) is
+// one FMA and one v_exp_f32 per score. Tiles below every query's diagonal with all keys valid and
+// in range take a body with no mask arithmetic at all: at half precision the matrix cores are 16x
+// faster than for f32 and the softmax, not the products, bounds the kernel.
+//
+// LDS per stage (two stages, one barrier per tile): K [64 keys][72 halves] (padded: conflict-free
+// 128-bit operand reads), V [8 octets][64 dims][8 keys] (each staging thread writes whole 16-byte
+// slots: conflict-free), the additive mask term of each key, and a per-tile "every key valid" flag.
+#include "common.hpp"
 #include "launch.hpp"
+
 namespace tsfm {
-hipError_t launch_attn_half(const Params&, bool, int, int, bool, hipStream_t) { return hipErrorNotSupported; }
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int NK = 64;          // keys per tile
+constexpr int QW = 32;          // queries per wave
+constexpr int NWAVE = 4;
+constexpr int NT = 64 * NWAVE;
+constexpr int QT = QW * NWAVE;
+constexpr int KROW = 36;        // K row pitch in LDS, dwords (64 halves + 8 pad)
+
+struct StageH {
+    uint32_t k[NK * KROW];           // [key][36 dwords]
+    uint32_t v[8 * kHeadDim * 4];    // [octet][dim][4 dwords = 8 keys]
+    float kadd[NK];
+    int all_valid;
+};
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (BF16) {
+        const bf16x2 v = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        const f16x2 v = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    }
 }
+
+template <bool BF16>
+__device__ __forceinline__ float lo_f(uint32_t w) {
+    if constexpr (BF16) return __uint_as_float(w << 16);
+    else return (float)__builtin_bit_cast(f16x2, w)[0];
+}
+template <bool BF16>
+__device__ __forceinline__ float hi_f(uint32_t w) {
+    if constexpr (BF16) return __uint_as_float(w & 0xffff0000u);
+    else return (float)__builtin_bit_cast(f16x2, w)[1];
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                       0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
+}
+
+__device__ __forceinline__ u32x4 ldu4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void stu4(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Rotate-half RoPE on 8 dims held as halves: lo = dims i..i+7, hi = dims i+32..i+39, rotated in
+// f32 (nn.ropeHalf, src/core/nn.zig:453-460, unfused products) and rounded back.
+template <bool BF16>
+__device__ __forceinline__ void rope8(u32x4& lo, u32x4& hi, const float* c, const float* s) {
+#pragma clang fp contract(off)
+    const f32x4 c0 = ld4(c), c1 = ld4(c + 4), s0 = ld4(s), s1 = ld4(s + 4);
+    const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+    u32x4 nlo, nhi;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float x1a = lo_f<BF16>(lo[w]), x1b = hi_f<BF16>(lo[w]);
+        const float x2a = lo_f<BF16>(hi[w]), x2b = hi_f<BF16>(hi[w]);
+        const int i = 2 * w;
+        nlo[w] = pack2<BF16>(x1a * cs[i] - x2a * sn[i], x1b * cs[i + 1] - x2b * sn[i + 1]);
+        nhi[w] = pack2<BF16>(x2a * cs[i] + x1a * sn[i], x2b * cs[i + 1] + x1b * sn[i + 1]);
+    }
+    lo = nlo;
+    hi = nhi;
+}
+
+template <int MASK>
+__device__ __forceinline__ float key_term_h(int key, int n_k, bool valid, int ctx_keys) {
+    if (key >= n_k) return kNegInf;
+    if (MASK == KEYS_ADDITIVE) return valid ? 0.f : -kFltMax;
+    if (MASK == CAUSAL_KEYS || MASK == FULL_KEYS) return valid ? 0.f : kNegInf;
+    if (MASK == DECODER) return (key < ctx_keys && valid) ? 0.f : kNegInf;
+    return 0.f;
+}
+
+template <int MASK>
+__device__ __forceinline__ float masked_h(float x, float ka, int key, int qpos, int n_k, int chain_start) {
+    if (MASK == CAUSAL) return key <= qpos ? x + ka : kNegInf;
+    if (MASK == CAUSAL_KEYS) return (key == qpos && key < n_k) ? x : (key <= qpos ? x + ka : kNegInf);
+    if (MASK == FULL_KEYS) return (key == qpos && key < n_k) ? x : x + ka;
+    if (MASK == DECODER) return (key >= chain_start && key <= qpos && key < n_k) ? x : x + ka;
+    return x + ka;
+}
+
+template <bool BF16, int MASK, bool ROPE>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_half(Params p) {
+    __shared__ __attribute__((aligned(16))) StageH stage[2];
+
+    typedef uint16_t E;  // element storage
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, g = lane >> 4;
+    const int q_tiles = (p.n_q + QT - 1) / QT;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = logical / q_tiles;
+    int qt = logical % q_tiles;
+    if (MASK == CAUSAL || MASK == CAUSAL_KEYS) qt = q_tiles - 1 - qt;  // longest rows first
+    const int b = bh / p.H, h = bh % p.H;
+    const int q0 = qt * QT;
+    const int wq0 = q0 + wave * QW;
+
+    const E* __restrict__ Q = static_cast<const E*>(p.q) + b * p.q_batch + h * kHeadDim;
+    const E* __restrict__ K = static_cast<const E*>(p.k) + b * p.k_batch + h * kHeadDim;
+    const E* __restrict__ V = static_cast<const E*>(p.v) + b * p.v_batch + h * kHeadDim;
+    E* __restrict__ O = static_cast<E*>(p.o) + b * p.o_batch + h * kHeadDim;
+    const uint8_t* __restrict__ KV = mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : nullptr;
+    const int rope_tab = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
+    const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
+    const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
+
+    const int wg_qhi = p.q_pos0 + min(p.n_q, q0 + QT) - 1;
+    const int kend = key_end_for<MASK>(wg_qhi, p.n_k, p.ctx_keys);
+    const int wave_nq = max(0, min(QW, p.n_q - wq0));
+    const int wave_qlo = p.q_pos0 + wq0;  // lowest query position of the wave
+    const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys) : 0;
+    const int ntiles = (kend + NK - 1) / NK;
+    const int kv_len = valid_len<MASK>(p.n_k, p.ctx_keys);
+    // exp2 argument factor; KEYS_ADDITIVE keeps the subtract-then-scale form so that the
+    // -FLT_MAX terms of an all-invalid row cancel exactly (the reference's uniform row).
+    const float c2 = p.scale * kLog2e;
+
+    // Q^T operand: qf[qb][c] = 8 halves, dims 32c + 8g .. 32c + 8g + 7 of query wq0 + 16qb + ql.
+    u32x4 qf[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const int qi = wq0 + 16 * qb + ql;
+        u32x4 lo = {0, 0, 0, 0}, hi = lo;
+        if (qi < p.n_q) {
+            const E* src = Q + (int64_t)qi * p.q_tok + 8 * g;
+            lo = ldu4(src);
+            hi = ldu4(src + 32);
+            if (ROPE) {
+                const int64_t row = (int64_t)(p.q_pos0 + qi) * 32 + 8 * g;
+                rope8<BF16>(lo, hi, RC + row, RS + row);
+            }
+        }
+        qf[qb][0] = lo;
+        qf[qb][1] = hi;
+    }
+
+    float mc_run[2] = {kNegInf, kNegInf};  // running max, in exp2 units (max * scale * log2 e)
+    float l_run[2] = {0.f, 0.f};
+    f32x4 oacc[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) oacc[db][qb] = f32x4{0, 0, 0, 0};
+
+    // ---- staging: K thread -> key tid/4, dims 8c..8c+7 and 32+8c..32+8c+7 (c = tid%4);
+    //      V thread -> dims 2dp, 2dp+1 (dp = tid%32) of the 8 keys of octet tid/32 ----
+    const int krow = tid >> 2, kc = tid & 3;
+    const int dp = tid & 31, oct = tid >> 5;
+    const int vkey0 = 32 * (oct >> 2) + 4 * (oct & 3);  // keys vkey0 + {0..3} and vkey0 + 16 + {0..3}
+    u32x4 klo, khi;
+    uint32_t vw[8];
+    float kar = 0.f;
+
+    auto fetch = [&](int kbase) {
+        const bool full = kbase + NK <= p.n_k;  // uniform
+        const int key = kbase + krow;
+        const int keyc = full ? key : min(key, p.n_k - 1);
+        const E* ks = K + (int64_t)keyc * p.k_tok + 8 * kc;
+        klo = ldu4(ks);
+        khi = ldu4(ks + 32);
+        if (ROPE) rope8<BF16>(klo, khi, RC + (int64_t)keyc * 32 + 8 * kc, RS + (int64_t)keyc * 32 + 8 * kc);
+        if (!full && key >= p.n_k) klo = khi = u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int vk = kbase + vkey0 + (j < 4 ? j : 12 + j);
+            const int vkc = full ? vk : min(vk, p.n_k - 1);
+            vw[j] = *reinterpret_cast<const uint32_t*>(V + (int64_t)vkc * p.v_tok + 2 * dp);
+            if (!full && vk >= p.n_k) vw[j] = 0;
+        }
+        if (tid < NK) {
+            const int kk = kbase + tid;
+            bool valid = true;
+            if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
+            kar = key_term_h<MASK>(kk, p.n_k, valid, p.ctx_keys);
+        }
+    };
+    auto store = [&](StageH& st) {
+        stu4(st.k + krow * KROW + 4 * kc, klo);
+        stu4(st.k + krow * KROW + 16 + 4 * kc, khi);
+        u32x4 even, odd;  // dims 2dp and 2dp+1, keys in octet order
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t a = vw[2 * w], c = vw[2 * w + 1];
+            even[w] = (a & 0xffffu) | (c << 16);
+            odd[w] = (a >> 16) | (c & 0xffff0000u);
+        }
+        stu4(st.v + (oct * kHeadDim + 2 * dp) * 4, even);
+        stu4(st.v + (oct * kHeadDim + 2 * dp + 1) * 4, odd);
+        if (tid < NK) {
+            st.kadd[tid] = kar;
+            const uint64_t bad = __ballot(kar != 0.f);  // wave 0 holds all 64 keys
+            if (tid == 0) st.all_valid = bad == 0;
+        }
+    };
+
+    // One 64-key tile on stage st. PLAIN: no mask arithmetic (every key valid and in range, every
+    // query of the wave past the tile, all 32 queries in range). Otherwise nkb key blocks and nqb
+    // query blocks are computed and each score goes through the mask rule.
+    auto tile = [&](const StageH& st, int kbase, int nkb, int nqb, auto plain_tag, int t) {
+        constexpr bool PLAIN = decltype(plain_tag)::value;
+        const bool more = t + 1 < ntiles;
+        if (more) fetch(kbase + NK);
+
+        f32x4 sacc[4][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) sacc[kb][qb] = f32x4{0, 0, 0, 0};
+            if (!PLAIN && kb >= nkb) continue;
+            const uint32_t* kr = st.k + (kb * 16 + ql) * KROW + 4 * g;
+            const u32x4 k0 = ldu4(kr), k1 = ldu4(kr + 16);
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                if (!PLAIN && qb >= nqb) continue;
+                sacc[kb][qb] = mfma<BF16>(k1, qf[qb][1], mfma<BF16>(k0, qf[qb][0], sacc[kb][qb]));
+            }
+        }
+
+        // ---- online softmax in exp2 units ----
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            if (!PLAIN && qb >= nqb) continue;
+            const int qpos = p.q_pos0 + wq0 + 16 * qb + ql;
+            float mloc = kNegInf;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const bool on = PLAIN || kb < nkb;
+                f32x4 ka = {0, 0, 0, 0};
+                if (!PLAIN) ka = ld4(st.kadd + kb * 16 + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float x = sacc[kb][qb][r];
+                    if (!PLAIN) {
+                        const int key = kbase + kb * 16 + 4 * g + r;
+                        x = on ? masked_h<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start) : kNegInf;
+                    }
+                    sacc[kb][qb][r] = x;
+                    mloc = fmaxf(mloc, x);
+                }
+            }
+            float mc_use, alpha;
+            if (MASK == KEYS_ADDITIVE) {
+                // mc_run holds the raw-score max here: e = exp2((x - m) * c2) keeps x - m exact.
+                const float mr = fmaxf(max4(mloc), mc_run[qb]);
+                mc_use = mr == kNegInf ? 0.f : mr;
+                alpha = __builtin_amdgcn_exp2f((mc_run[qb] - mc_use) * c2);
+                mc_run[qb] = mr;
+            } else {
+                // exp2 units: e = exp2(x * c2 - max * c2), one FMA per score.
+                const float mt = mloc == kNegInf ? kNegInf : mloc * c2;
+                const float mn = fmaxf(max4(mt), mc_run[qb]);
+                mc_use = mn == kNegInf ? 0.f : mn;
+                alpha = __builtin_amdgcn_exp2f(mc_run[qb] - mc_use);
+                mc_run[qb] = mn;
+            }
+            float lsum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float x = sacc[kb][qb][r];
+                    const float e = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((x - mc_use) * c2)
+                                                          : __builtin_amdgcn_exp2f(__builtin_fmaf(x, c2, -mc_use));
+                    sacc[kb][qb][r] = e;
+                    lsum += e;
+                }
+            l_run[qb] = l_run[qb] * alpha + lsum;
+#pragma unroll
+            for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+        }
+
+        if (more) store(stage[(t + 1) & 1]);
+
+        // ---- O^T += V^T . P^T, two 32-key chunks ----
+#pragma unroll
+        for (int ch = 0; ch < 2; ch++) {
+            if (!PLAIN && 2 * ch >= nkb) continue;
+            u32x4 pf[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                const f32x4 a = sacc[2 * ch][qb], c = sacc[2 * ch + 1][qb];
+                pf[qb] = u32x4{pack2<BF16>(a[0], a[1]), pack2<BF16>(a[2], a[3]), pack2<BF16>(c[0], c[1]),
+                               pack2<BF16>(c[2], c[3])};
+            }
+            const uint32_t* vr = st.v + ((ch * 4 + g) * kHeadDim + ql) * 4;
+#pragma unroll
+            for (int db = 0; db < 4; db++) {
+                const u32x4 vf = ldu4(vr + db * 64);
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++) {
+                    if (!PLAIN && qb >= nqb) continue;
+                    oacc[db][qb] = mfma<BF16>(vf, pf[qb], oacc[db][qb]);
+                }
+            }
+        }
+    };
+
+    if (ntiles > 0) {
+        fetch(0);
+        store(stage[0]);
+    }
+    __syncthreads();
+    const int nqb = (wave_nq + 15) >> 4;
+    for (int t = 0; t < ntiles; t++) {
+        const int kbase = t * NK;
+        const StageH& st = stage[t & 1];
+        const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
+        bool plain = kbase + NK <= wave_kend && wave_nq == QW && MASK != DECODER;
+        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= wave_qlo;
+        if (mask_reads_valid<MASK>()) plain = plain && st.all_valid;
+        if (plain) {
+            tile(st, kbase, 4, 2, std::integral_constant<bool, true>{}, t);
+        } else if (nkb > 0 && nqb > 0) {
+            tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
+        } else if (t + 1 < ntiles) {
+            fetch(kbase + NK);
+            store(stage[(t + 1) & 1]);
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise and store: lane holds query ql, dims 16db + 4g + r ----
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const int qi = wq0 + 16 * qb + ql;
+        const float l = sum4(l_run[qb]);
+        if (qi >= p.n_q) continue;
+        const float inv = 1.0f / l;
+        E* dst = O + (int64_t)qi * p.o_tok + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            const f32x4 o = oacc[db][qb] * inv;
+            *reinterpret_cast<u32x2*>(dst + 16 * db) = u32x2{pack2<BF16>(o[0], o[1]), pack2<BF16>(o[2], o[3])};
+        }
+    }
+}
+
+template <bool BF16, int MASK, bool ROPE>
+hipError_t launch_one(const Params& p, hipStream_t stream) {
+    const int q_tiles = (p.n_q + QT - 1) / QT;
+    const int64_t blocks = (int64_t)p.B * p.H * q_tiles;
+    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_fwd_half<BF16, MASK, ROPE>), dim3((unsigned)blocks), dim3(NT), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <bool BF16, int MASK>
+hipError_t launch_rope(const Params& p, bool rope, hipStream_t s) {
+    return rope ? launch_one<BF16, MASK, true>(p, s) : launch_one<BF16, MASK, false>(p, s);
+}
+
+template <bool BF16>
+hipError_t launch_mask(const Params& p, int mask, bool rope, hipStream_t s) {
+    switch (mask) {
+    case FULL: return launch_rope<BF16, FULL>(p, rope, s);
+    case KEYS_ADDITIVE: return launch_rope<BF16, KEYS_ADDITIVE>(p, rope, s);
+    case CAUSAL: return launch_rope<BF16, CAUSAL>(p, rope, s);
+    case CAUSAL_KEYS: return launch_rope<BF16, CAUSAL_KEYS>(p, rope, s);
+    case FULL_KEYS: return launch_rope<BF16, FULL_KEYS>(p, rope, s);
+    case DECODER: return launch_rope<BF16, DECODER>(p, rope, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_attn_half(const Params& p, bool is_bf16, int mask, int bias, bool rope, hipStream_t s) {
+    if (bias != BIAS_NONE) return hipErrorNotSupported;  // the bias-carrying families are f32
+    return is_bf16 ? launch_mask<true>(p, mask, rope, s) : launch_mask<false>(p, mask, rope, s);
+}
+
+}  // namespace tsfm

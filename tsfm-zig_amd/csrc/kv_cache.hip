@@ -1,5 +1,286 @@
+// KV cache for block-autoregressive decode (bf16 / f16, f32 accumulation) on gfx950.
+//
+// The reference has no cache: Timestral's blockDecode re-encodes the whole grown context every
+// block (src/timestral/forecaster.zig:423-563), so the K/V of every unchanged prefix token is
+// recomputed. With a causal encoder and a fixed prefix, rows [P, P + n) of causal selfAttend over
+// the concatenated sequence equal n queries at positions P.. attending over cached keys, which is
+// what tsfm_kv_attend computes.
+//
+// Layout (per (series, head), `cap` rounded up to 32 keys):
+//   K: [cap][64] halves, one 128-byte row per key.
+//   V: [cap/32][4][64][8] halves: 32-key chunks in the operand order of
+//      v_mfma_f32_16x16x32_{bf16,f16} (see attn_half.hip): octet g of a chunk holds keys
+//      {4g..4g+3, 16+4g..16+4g+3} of every dim, so a lane's A operand is one 16-byte load and a
+//      16-lane group reads 256 contiguous bytes.
+// Decode reads both straight from HBM with no LDS staging: one workgroup per
+// (series, head, 32 queries); its four waves take key tiles t = w, w+4, ... and merge their
+// (max, sum, O) partials through LDS at the end (split-key flash decoding).
+#include "common.hpp"
 #include "launch.hpp"
+
 namespace tsfm {
-hipError_t launch_kv_append(const KvLayout&, bool, const void*, int64_t, int64_t, const void*, int64_t, int64_t, int32_t, int32_t, hipStream_t) { return hipErrorNotSupported; }
-hipError_t launch_kv_attend(const KvLayout&, bool, const void*, int64_t, int64_t, void*, int64_t, int64_t, int32_t, int32_t, int32_t, float, hipStream_t) { return hipErrorNotSupported; }
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int NK = 64;
+constexpr int NWAVE = 4;
+constexpr int NT = 64 * NWAVE;
+constexpr int QB = 32;  // queries per workgroup
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (BF16) {
+        const bf16x2 v = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        const f16x2 v = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    }
 }
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                       0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
+}
+
+__device__ __forceinline__ u32x4 ldu4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// ---- append: one thread per (series, head, new token, 8-dim chunk) ----
+__global__ __launch_bounds__(256) void kv_append(KvLayout c, const uint16_t* __restrict__ k, int64_t k_tok,
+                                                 int64_t k_batch, const uint16_t* __restrict__ v, int64_t v_tok,
+                                                 int64_t v_batch, int32_t pos0, int32_t n_new) {
+    const int64_t total = (int64_t)c.B * c.H * n_new * 8;
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= total) return;
+    const int chunk = (int)(id & 7);
+    int64_t rest = id >> 3;
+    const int t = (int)(rest % n_new);
+    rest /= n_new;
+    const int h = (int)(rest % c.H);
+    const int b = (int)(rest / c.H);
+    const int pos = pos0 + t;
+    const int64_t bh = (int64_t)b * c.H + h;
+    const int64_t src_off = h * kHeadDim + 8 * chunk;
+    const u32x4 kv = ldu4(k + b * k_batch + t * k_tok + src_off);
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(c.k) + (bh * c.cap + pos) * kHeadDim + 8 * chunk) = kv;
+    const u32x4 vv = ldu4(v + b * v_batch + t * v_tok + src_off);
+    const int p = pos >> 5, kk = pos & 31;
+    const int g = (kk & 15) >> 2, j = (kk & 3) + 4 * (kk >> 4);
+    uint16_t* vd = static_cast<uint16_t*>(c.v) + (((bh * (c.cap / 32) + p) * 4 + g) * kHeadDim + 8 * chunk) * 8 + j;
+#pragma unroll
+    for (int e = 0; e < 8; e++) vd[e * 8] = (uint16_t)((e & 1) ? (vv[e >> 1] >> 16) : (vv[e >> 1] & 0xffffu));
+}
+
+// ---- attend ----
+template <bool BF16>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void kv_attend(
+    KvLayout c, const uint16_t* __restrict__ q, int64_t q_tok, int64_t q_batch, uint16_t* __restrict__ o, int64_t o_tok,
+    int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k, float scale) {
+    __shared__ float part_m[NWAVE][QB], part_l[NWAVE][QB];
+    __shared__ __attribute__((aligned(16))) float part_o[NWAVE][QB][kHeadDim + 4];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, g = lane >> 4;
+    const int qblocks = (n_q + QB - 1) / QB;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = logical / qblocks, qbk = logical % qblocks;
+    const int b = bh / c.H, h = bh % c.H;
+    const int qi0 = qbk * QB;
+    const int nqv = min(QB, n_q - qi0);           // valid queries of this workgroup
+    const int qlo = q_pos0 + qi0;                  // position of its first query
+    const int kend = min(n_k, qlo + nqv);          // keys any of its queries reads
+    const int ntiles = (kend + NK - 1) / NK;
+    const float c2 = scale * kLog2e;
+
+    const uint16_t* __restrict__ Kc = static_cast<const uint16_t*>(c.k) + (int64_t)bh * c.cap * kHeadDim;
+    const uint16_t* __restrict__ Vc = static_cast<const uint16_t*>(c.v) + (int64_t)bh * c.cap * kHeadDim;
+
+    u32x4 qf[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const int qi = qi0 + 16 * qb + ql;
+        u32x4 lo = {0, 0, 0, 0}, hi = lo;
+        if (qi < n_q) {
+            const uint16_t* src = q + b * q_batch + (int64_t)qi * q_tok + h * kHeadDim + 8 * g;
+            lo = ldu4(src);
+            hi = ldu4(src + 32);
+        }
+        qf[qb][0] = lo;
+        qf[qb][1] = hi;
+    }
+
+    float mc_run[2] = {kNegInf, kNegInf};
+    float l_run[2] = {0.f, 0.f};
+    f32x4 oacc[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) oacc[db][qb] = f32x4{0, 0, 0, 0};
+
+    // Operand fragments of one tile, loaded straight from the cache. Rows past n_k (up to the
+    // capacity) are read but always masked: the cache is zero-filled at creation, so they hold
+    // finite values and contribute exactly 0.
+    u32x4 kf[4][2], vf[2][4];
+    auto load_k = [&](int kbase) {
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            const uint16_t* kr = Kc + (int64_t)(kbase + kb * 16 + ql) * kHeadDim + 8 * g;
+            kf[kb][0] = ldu4(kr);
+            kf[kb][1] = ldu4(kr + 32);
+        }
+    };
+    auto load_v = [&](int kbase) {
+#pragma unroll
+        for (int ch = 0; ch < 2; ch++) {
+            const uint16_t* vr = Vc + ((((int64_t)(kbase >> 5) + ch) * 4 + g) * kHeadDim + ql) * 8;
+#pragma unroll
+            for (int db = 0; db < 4; db++) vf[ch][db] = ldu4(vr + db * 16 * 8);
+        }
+    };
+
+    int t = wave;
+    if (t < ntiles) {
+        load_k(t * NK);
+        load_v(t * NK);
+    }
+    for (; t < ntiles; t += NWAVE) {
+        const int kbase = t * NK;
+        const int tn = t + NWAVE;
+        f32x4 sacc[4][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++)
+                sacc[kb][qb] = mfma<BF16>(kf[kb][1], qf[qb][1], mfma<BF16>(kf[kb][0], qf[qb][0], f32x4{0, 0, 0, 0}));
+        if (tn < ntiles) load_k(tn * NK);
+
+        const bool plain = kbase + NK - 1 <= qlo;  // every key of the tile is visible to every query
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            const int qpos = qlo + 16 * qb + ql;
+            float mloc = kNegInf;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float x = sacc[kb][qb][r];
+                    if (!plain && kbase + kb * 16 + 4 * g + r > qpos) x = kNegInf;
+                    sacc[kb][qb][r] = x;
+                    mloc = fmaxf(mloc, x);
+                }
+            const float mt = mloc == kNegInf ? kNegInf : mloc * c2;
+            const float mn = fmaxf(max4(mt), mc_run[qb]);
+            const float mc_use = mn == kNegInf ? 0.f : mn;
+            const float alpha = __builtin_amdgcn_exp2f(mc_run[qb] - mc_use);
+            mc_run[qb] = mn;
+            float lsum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], c2, -mc_use));
+                    sacc[kb][qb][r] = e;
+                    lsum += e;
+                }
+            l_run[qb] = l_run[qb] * alpha + lsum;
+#pragma unroll
+            for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+        }
+
+#pragma unroll
+        for (int ch = 0; ch < 2; ch++) {
+            u32x4 pf[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                const f32x4 a = sacc[2 * ch][qb], d = sacc[2 * ch + 1][qb];
+                pf[qb] = u32x4{pack2<BF16>(a[0], a[1]), pack2<BF16>(a[2], a[3]), pack2<BF16>(d[0], d[1]),
+                               pack2<BF16>(d[2], d[3])};
+            }
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++) oacc[db][qb] = mfma<BF16>(vf[ch][db], pf[qb], oacc[db][qb]);
+        }
+        if (tn < ntiles) load_v(tn * NK);
+    }
+
+    // ---- merge the four waves' partial results ----
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const float l = sum4(l_run[qb]);
+        const int qq = 16 * qb + ql;
+        if (g == 0) {
+            part_m[wave][qq] = mc_run[qb];
+            part_l[wave][qq] = l;
+        }
+#pragma unroll
+        for (int db = 0; db < 4; db++) st4(&part_o[wave][qq][16 * db + 4 * g], oacc[db][qb]);
+    }
+    __syncthreads();
+    {
+        const int qq = tid >> 3, d0 = 8 * (tid & 7);  // 32 queries x 8 dim groups
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) M = fmaxf(M, part_m[w][qq]);
+        float L = 0.f;
+        f32x4 a0 = {0, 0, 0, 0}, a1 = a0;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) {
+            const float f = part_m[w][qq] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(part_m[w][qq] - M);
+            L += f * part_l[w][qq];
+            a0 += f * ld4(&part_o[w][qq][d0]);
+            a1 += f * ld4(&part_o[w][qq][d0 + 4]);
+        }
+        if (qq < nqv) {
+            const float inv = 1.0f / L;
+            a0 *= inv;
+            a1 *= inv;
+            uint16_t* dst = o + b * o_batch + (int64_t)(qi0 + qq) * o_tok + h * kHeadDim + d0;
+            *reinterpret_cast<u32x4*>(dst) = u32x4{pack2<BF16>(a0[0], a0[1]), pack2<BF16>(a0[2], a0[3]),
+                                                   pack2<BF16>(a1[0], a1[1]), pack2<BF16>(a1[2], a1[3])};
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_kv_append(const KvLayout& c, bool /*is_bf16*/, const void* k, int64_t k_tok, int64_t k_batch,
+                            const void* v, int64_t v_tok, int64_t v_batch, int32_t pos0, int32_t n_new,
+                            hipStream_t stream) {
+    const int64_t total = (int64_t)c.B * c.H * n_new * 8;
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(kv_append, dim3((unsigned)blocks), dim3(256), 0, stream, c,
+                       static_cast<const uint16_t*>(k), k_tok, k_batch, static_cast<const uint16_t*>(v), v_tok,
+                       v_batch, pos0, n_new);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_attend(const KvLayout& c, bool is_bf16, const void* q, int64_t q_tok, int64_t q_batch, void* o,
+                            int64_t o_tok, int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k, float scale,
+                            hipStream_t stream) {
+    const int64_t blocks = (int64_t)c.B * c.H * ((n_q + QB - 1) / QB);
+    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (is_bf16)
+        hipLaunchKernelGGL(kv_attend<true>, dim3((unsigned)blocks), dim3(NT), 0, stream, c,
+                           static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
+                           n_q, q_pos0, n_k, scale);
+    else
+        hipLaunchKernelGGL(kv_attend<false>, dim3((unsigned)blocks), dim3(NT), 0, stream, c,
+                           static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
+                           n_q, q_pos0, n_k, scale);
+    return hipGetLastError();
+}
+
+}  // namespace tsfm

@@ -17,7 +17,7 @@ hipError_t launch_attn_half(const Params& p, bool is_bf16, int mask, int bias, b
 struct KvLayout {
     void* k;          // [B][H][cap][64]
     void* v;          // [B][H][cap/32][4][64][8]  (32-key chunks, matrix-core operand order)
-    int32_t B, H, cap;
+    int32_t B, H, cap;  // cap: a multiple of 64
 };
 hipError_t launch_kv_append(const KvLayout& c, bool is_bf16, const void* k, int64_t k_tok, int64_t k_batch,
                             const void* v, int64_t v_tok, int64_t v_batch, int32_t pos0, int32_t n_new,

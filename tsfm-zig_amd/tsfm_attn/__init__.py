@@ -58,6 +58,7 @@ EXPORTS = (
     "tsfm_kv_create",
     "tsfm_kv_free",
     "tsfm_kv_reset",
+    "tsfm_kv_truncate",
     "tsfm_kv_len",
     "tsfm_kv_append",
     "tsfm_kv_attend",
@@ -183,6 +184,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_kv_free.restype = ctypes.c_int
     lib.tsfm_kv_reset.argtypes = [vp]
     lib.tsfm_kv_reset.restype = ctypes.c_int
+    lib.tsfm_kv_truncate.argtypes = [vp, i32]
+    lib.tsfm_kv_truncate.restype = ctypes.c_int
     lib.tsfm_kv_len.argtypes = [vp]
     lib.tsfm_kv_len.restype = i32
     lib.tsfm_kv_append.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, u32, vp]
@@ -413,3 +416,70 @@ def timestral_time_attention(qkv, o, cos_t, sin_t, key_valid, keys_all_valid: bo
         q=_flat_view(qkv, ne * 3 * d), k=_flat_view(qkv, d), v=_flat_view(qkv, 2 * d), o=_flat_view(o, ne * d),
         mask=Mask.DECODER, batch=rows, n_q=h, n_k=sl, q_pos0=ne, ctx_keys=l, chain_start=ne,
         **{**common, "key_valid": key_valid}))
+
+
+# ---------------------------------------------------------------------------------------------
+# KV cache (no counterpart in the reference: Timestral's blockDecode re-encodes the whole context
+# every block, src/timestral/forecaster.zig:423-563).
+
+
+class KvCache:
+    """``tsfm_kv_*``: a device K/V cache of ``capacity`` tokens for every (series, head), bf16 or
+    f16. ``append`` adds the K/V of new tokens; ``attend`` runs causal attention of queries at
+    positions ``q_pos0..`` over the cached keys. Arrays follow the (B, tokens, H*D) layout with
+    token/batch strides in elements; device tensors make the calls asynchronous on the given (or
+    current) stream, numpy arrays make them synchronous."""
+
+    def __init__(self, dtype: int, batch: int, heads: int, capacity: int, head_dim: int = 64):
+        self.dtype, self.batch, self.heads, self.head_dim = dtype, batch, heads, head_dim
+        h = ctypes.c_void_p()
+        rc = load().tsfm_kv_create(ctypes.byref(h), dtype, batch, heads, head_dim, capacity)
+        if rc != OK:
+            raise TsfmError(rc, last_error())
+        self._h = h
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise TsfmError(rc, last_error())
+
+    @property
+    def handle(self) -> int:
+        return int(self._h.value or 0)
+
+    def __len__(self) -> int:
+        return int(load().tsfm_kv_len(self._h))
+
+    def append(self, k, v, n_new: int, k_tok: int, k_batch: int, v_tok: int, v_batch: int, stream=None) -> None:
+        device = _is_device(k)
+        self._check(load().tsfm_kv_append(self._h, _ptr(k), k_tok, k_batch, _ptr(v), v_tok, v_batch, n_new,
+                                          DEVICE_PTRS if device else 0, _stream_of(k, stream) if device else None))
+
+    def attend(self, q, o, n_q: int, q_pos0: int, scale: float, q_tok: int, q_batch: int, o_tok: int, o_batch: int,
+               stream=None) -> None:
+        device = _is_device(q)
+        self._check(load().tsfm_kv_attend(self._h, _ptr(q), q_tok, q_batch, _ptr(o), o_tok, o_batch, n_q, q_pos0,
+                                          float(scale), DEVICE_PTRS if device else 0,
+                                          _stream_of(q, stream) if device else None))
+
+    def truncate(self, length: int) -> None:
+        self._check(load().tsfm_kv_truncate(self._h, length))
+
+    def reset(self) -> None:
+        self._check(load().tsfm_kv_reset(self._h))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            load().tsfm_kv_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self) -> "KvCache":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
