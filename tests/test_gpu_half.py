@@ -84,6 +84,22 @@ def test_half_masks_match_oracle(ta, orc, gpu_ready, name, mask, n):
 
 
 @pytest.mark.parametrize("name", DTYPES)
+@pytest.mark.parametrize("mask", [3, 4])
+def test_half_long_left_padding(ta, orc, gpu_ready, name, mask):
+    """Rows whose first 200 of 300 keys are invalid: whole 64-key tiles with no valid key are
+    skipped, except where a query's own (always open) diagonal falls in them."""
+    B, H, n = 3, 2, 300
+    q, k, v, _ = _inputs(41 + mask, B, H, n, n)
+    kv = np.ones((B, n), np.uint8)
+    kv[0, :200] = 0
+    kv[1, :64] = 0
+    kv[2, 100:164] = 0
+    got, qr, kr, vr = _run_half(ta, name, mask, q, k, v, kv, B, H, n, n, 0.125)
+    want = _oracle(orc, mask, qr, kr, vr, kv, B, H, n, 0.125)
+    assert _ref.scaled_err(got, want) <= TOL_HALF
+
+
+@pytest.mark.parametrize("name", DTYPES)
 def test_half_decoder_mask_matches_float64(ta, gpu_ready, name):
     B, H, ne, h, l = 3, 2, 80, 9, 70
     sl = ne + h

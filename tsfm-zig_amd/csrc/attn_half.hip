@@ -46,7 +46,6 @@ struct StageH {
     uint32_t k[NK * KROW];           // [key][36 dwords]
     uint32_t v[8 * kHeadDim * 4];    // [octet][dim][4 dwords = 8 keys]
     float kadd[NK];
-    int all_valid;
 };
 
 template <bool BF16>
@@ -82,14 +81,18 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 }
 
 __device__ __forceinline__ u32x4 ldu4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// V dim slot within an octet: bit 3 of the dim XORed into bit 0. The staging writes (dims 2dp, then
+// 2dp+1, for 8 consecutive dp) and the operand reads (16 consecutive dims, whose slot offset
+// vslot_h(db*16 + ql) = db*16 + vslot_h(ql)) then both hit 8 distinct 16-byte bank groups.
+__device__ __forceinline__ int vslot_h(int dim) { return dim ^ ((dim >> 3) & 1); }
 __device__ __forceinline__ void stu4(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // Rotate-half RoPE on 8 dims held as halves: lo = dims i..i+7, hi = dims i+32..i+39, rotated in
 // f32 (nn.ropeHalf, src/core/nn.zig:453-460, unfused products) and rounded back.
 template <bool BF16>
-__device__ __forceinline__ void rope8(u32x4& lo, u32x4& hi, const float* c, const float* s) {
+__device__ __forceinline__ void rope8(u32x4& lo, u32x4& hi, f32x4 c0, f32x4 c1, f32x4 s0, f32x4 s1) {
 #pragma clang fp contract(off)
-    const f32x4 c0 = ld4(c), c1 = ld4(c + 4), s0 = ld4(s), s1 = ld4(s + 4);
     const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
     const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
     u32x4 nlo, nhi;
@@ -123,8 +126,15 @@ __device__ __forceinline__ float masked_h(float x, float ka, int key, int qpos, 
     return x + ka;
 }
 
+// Waves per SIMD the register budget targets: three (168 VGPRs) where the body fits without
+// spills, two where RoPE staging or the decoder mask needs more.
+template <int MASK, bool ROPE>
+constexpr int waves_per_simd() { return (ROPE || MASK == DECODER) ? 2 : 3; }
+
 template <bool BF16, int MASK, bool ROPE>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_half(Params p) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(waves_per_simd<MASK, ROPE>(),
+                                                                   waves_per_simd<MASK, ROPE>()))) void
+attn_fwd_half(Params p) {
     __shared__ __attribute__((aligned(16))) StageH stage[2];
 
     typedef uint16_t E;  // element storage
@@ -171,7 +181,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             hi = ldu4(src + 32);
             if (ROPE) {
                 const int64_t row = (int64_t)(p.q_pos0 + qi) * 32 + 8 * g;
-                rope8<BF16>(lo, hi, RC + row, RS + row);
+                rope8<BF16>(lo, hi, ld4(RC + row), ld4(RC + row + 4), ld4(RS + row), ld4(RS + row + 4));
             }
         }
         qf[qb][0] = lo;
@@ -188,37 +198,76 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
     // ---- staging: K thread -> key tid/4, dims 8c..8c+7 and 32+8c..32+8c+7 (c = tid%4);
     //      V thread -> dims 2dp, 2dp+1 (dp = tid%32) of the 8 keys of octet tid/32 ----
-    const int krow = tid >> 2, kc = tid & 3;
+    // K rows: 16 consecutive lanes take 16 consecutive rows, so each 128-bit LDS write phase of 8
+    // lanes covers all banks (row pitch 36 dwords).
+    const int krow = (tid & 15) + 16 * (tid >> 6), kc = (tid >> 4) & 3;
     const int dp = tid & 31, oct = tid >> 5;
     const int vkey0 = 32 * (oct >> 2) + 4 * (oct & 3);  // keys vkey0 + {0..3} and vkey0 + 16 + {0..3}
     u32x4 klo, khi;
+    f32x4 kc0, kc1, ks0, ks1;  // RoPE cos/sin of the thread's K row, applied at the LDS store
     uint32_t vw[8];
     float kar = 0.f;
+    bool next_all_valid = true;    // uniform: every key term of the fetched tile is 0
+    bool next_none_valid = false;  // uniform: no key term of the fetched tile is 0
+
+    // Per-thread base pointers; a tile adds the uniform kbase * stride, a V row the uniform
+    // j * v_tok, so full tiles issue ten straight-line loads with no per-lane address arithmetic.
+    const E* const kbase_p = K + (int64_t)krow * p.k_tok + 8 * kc;
+    const E* const vbase_p = V + (int64_t)vkey0 * p.v_tok + 2 * dp;
+    const int64_t vt = p.v_tok;
+    auto ld32 = [](const E* q) { return *reinterpret_cast<const uint32_t*>(q); };
 
     auto fetch = [&](int kbase) {
-        const bool full = kbase + NK <= p.n_k;  // uniform
         const int key = kbase + krow;
-        const int keyc = full ? key : min(key, p.n_k - 1);
-        const E* ks = K + (int64_t)keyc * p.k_tok + 8 * kc;
-        klo = ldu4(ks);
-        khi = ldu4(ks + 32);
-        if (ROPE) rope8<BF16>(klo, khi, RC + (int64_t)keyc * 32 + 8 * kc, RS + (int64_t)keyc * 32 + 8 * kc);
-        if (!full && key >= p.n_k) klo = khi = u32x4{0, 0, 0, 0};
+        int keyc = key;
+        if (kbase + NK <= p.n_k) {  // uniform: the whole tile is in range
+            const E* ks = kbase_p + (int64_t)kbase * p.k_tok;
+            klo = ldu4(ks);
+            khi = ldu4(ks + 32);
+            const E* vs = vbase_p + (int64_t)kbase * vt;
+            vw[0] = ld32(vs);
+            vw[1] = ld32(vs + vt);
+            vw[2] = ld32(vs + 2 * vt);
+            vw[3] = ld32(vs + 3 * vt);
+            vw[4] = ld32(vs + 16 * vt);
+            vw[5] = ld32(vs + 17 * vt);
+            vw[6] = ld32(vs + 18 * vt);
+            vw[7] = ld32(vs + 19 * vt);
+        } else {  // the last tile: clamp every row into range, then zero the padding rows
+            const int last = p.n_k - 1;
+            keyc = min(key, last);
+            const E* ks = K + (int64_t)keyc * p.k_tok + 8 * kc;
+            klo = ldu4(ks);
+            khi = ldu4(ks + 32);
+            const E* vs = V + 2 * dp;
+            const int v0 = kbase + vkey0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int vk = kbase + vkey0 + (j < 4 ? j : 12 + j);
-            const int vkc = full ? vk : min(vk, p.n_k - 1);
-            vw[j] = *reinterpret_cast<const uint32_t*>(V + (int64_t)vkc * p.v_tok + 2 * dp);
-            if (!full && vk >= p.n_k) vw[j] = 0;
+            for (int j = 0; j < 8; j++) vw[j] = ld32(vs + (int64_t)min(v0 + (j < 4 ? j : 12 + j), last) * vt);
+#pragma unroll
+            for (int j = 0; j < 8; j++) vw[j] = v0 + (j < 4 ? j : 12 + j) <= last ? vw[j] : 0u;
+            const bool kin = key <= last;
+            klo = kin ? klo : u32x4{0, 0, 0, 0};
+            khi = kin ? khi : u32x4{0, 0, 0, 0};
         }
-        if (tid < NK) {
-            const int kk = kbase + tid;
+        if (ROPE) {
+            const float* cs = RC + (int64_t)keyc * 32 + 8 * kc;
+            const float* sn = RS + (int64_t)keyc * 32 + 8 * kc;
+            kc0 = ld4(cs);
+            kc1 = ld4(cs + 4);
+            ks0 = ld4(sn);
+            ks1 = ld4(sn + 4);
+        }
+        {  // every wave evaluates the 64 key terms itself: the tile flag needs no LDS round trip
+            const int kk = kbase + lane;
             bool valid = true;
             if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
             kar = key_term_h<MASK>(kk, p.n_k, valid, p.ctx_keys);
+            next_all_valid = __ballot(kar != 0.f) == 0;
+            next_none_valid = __ballot(kar == 0.f) == 0;
         }
     };
     auto store = [&](StageH& st) {
+        if (ROPE) rope8<BF16>(klo, khi, kc0, kc1, ks0, ks1);
         stu4(st.k + krow * KROW + 4 * kc, klo);
         stu4(st.k + krow * KROW + 16 + 4 * kc, khi);
         u32x4 even, odd;  // dims 2dp and 2dp+1, keys in octet order
@@ -228,13 +277,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             even[w] = (a & 0xffffu) | (c << 16);
             odd[w] = (a >> 16) | (c & 0xffff0000u);
         }
-        stu4(st.v + (oct * kHeadDim + 2 * dp) * 4, even);
-        stu4(st.v + (oct * kHeadDim + 2 * dp + 1) * 4, odd);
-        if (tid < NK) {
-            st.kadd[tid] = kar;
-            const uint64_t bad = __ballot(kar != 0.f);  // wave 0 holds all 64 keys
-            if (tid == 0) st.all_valid = bad == 0;
-        }
+        stu4(st.v + (oct * kHeadDim + vslot_h(2 * dp)) * 4, even);
+        stu4(st.v + (oct * kHeadDim + vslot_h(2 * dp + 1)) * 4, odd);
+        if (tid < NK) st.kadd[tid] = kar;
     };
 
     // One 64-key tile on stage st. PLAIN: no mask arithmetic (every key valid and in range, every
@@ -309,11 +354,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                     lsum += e;
                 }
             l_run[qb] = l_run[qb] * alpha + lsum;
+            // Rescale O only when some lane's running max moved (alpha == 1 exactly otherwise):
+            // later in a long row the max rarely changes.
+            if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
-            for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+            }
         }
-
-        if (more) store(stage[(t + 1) & 1]);
 
         // ---- O^T += V^T . P^T, two 32-key chunks ----
 #pragma unroll
@@ -326,7 +373,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                 pf[qb] = u32x4{pack2<BF16>(a[0], a[1]), pack2<BF16>(a[2], a[3]), pack2<BF16>(c[0], c[1]),
                                pack2<BF16>(c[2], c[3])};
             }
-            const uint32_t* vr = st.v + ((ch * 4 + g) * kHeadDim + ql) * 4;
+            const uint32_t* vr = st.v + ((ch * 4 + g) * kHeadDim + vslot_h(ql)) * 4;
 #pragma unroll
             for (int db = 0; db < 4; db++) {
                 const u32x4 vf = ldu4(vr + db * 64);
@@ -337,6 +384,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                 }
             }
         }
+        // The next tile goes to the other stage last: its loads had the whole tile to land.
+        if (more) store(stage[(t + 1) & 1]);
     };
 
     if (ntiles > 0) {
@@ -351,10 +400,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
         bool plain = kbase + NK <= wave_kend && wave_nq == QW && MASK != DECODER;
         if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= wave_qlo;
-        if (mask_reads_valid<MASK>()) plain = plain && st.all_valid;
+        if (mask_reads_valid<MASK>()) plain = plain && next_all_valid;  // fetched with tile t
+        // -inf-masked keys contribute nothing: a tile with no valid key and no query's own (always
+        // open) diagonal in it is skipped outright (left-padded rows, src/core/attn.zig:46-62).
+        const bool empty = (MASK == CAUSAL_KEYS || MASK == FULL_KEYS) && next_none_valid &&
+                           (kbase + NK <= wave_qlo || kbase >= wave_qlo + wave_nq);
         if (plain) {
             tile(st, kbase, 4, 2, std::integral_constant<bool, true>{}, t);
-        } else if (nkb > 0 && nqb > 0) {
+        } else if (nkb > 0 && nqb > 0 && !empty) {
             tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
         } else if (t + 1 < ntiles) {
             fetch(kbase + NK);
