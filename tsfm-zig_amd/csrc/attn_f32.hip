@@ -131,6 +131,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                 rope4(a0, a2, c0, s0);
                 rope4(a1, a3, c1, s1);
             }
+            // The score scale goes into q: scores = (scale q) . k. For the power-of-two scales every
+            // family uses (1, 1/8) this equals the reference's alpha * (q . k) bit for bit (scaling
+            // by 2^n commutes with every rounding of the dot product).
+            a0 *= p.scale;
+            a1 *= p.scale;
+            a2 *= p.scale;
+            a3 *= p.scale;
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -141,7 +148,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
     }
 
-    float m_run[2] = {kNegInf, kNegInf};
+    float m_run[2] = {kNegInf, kNegInf};   // running max of the scores
+    float ml_run[2] = {kNegInf, kNegInf};  // the same in exp2 units, as used by the weights
     float l_run[2] = {0.f, 0.f};
     f32x4 oacc[4][2];
 #pragma unroll
@@ -159,43 +167,58 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     f32x4 klo, khi, kcos, ksin;
     float2 v0, v1, v2, v3;
     float kar = 0.f;
+    bool next_all_valid = true;  // uniform: every key term of the tile being fetched is 0
+
+    // Per-thread base pointers: a half tile adds the uniform hbase * stride.
+    const float* const kp = K + (int64_t)krow * p.k_tok + 4 * kc;
+    const float* const vp = V + (int64_t)(4 * vq) * p.v_tok + 2 * vc;
+    const int64_t vt = p.v_tok;
 
     auto fetch = [&](int hbase) {  // keys [hbase, hbase + 32)
-        const bool full = hbase + NK / 2 <= p.n_k;  // uniform
         const int key = hbase + krow;
-        const int keyc = full ? key : min(key, p.n_k - 1);
-        const float* ks = K + (int64_t)keyc * p.k_tok + 4 * kc;
-        klo = ld4(ks);
-        khi = ld4(ks + 32);
+        int keyc = key;
+        if (hbase + NK / 2 <= p.n_k) {  // uniform: the whole half is in range
+            const float* ks = kp + (int64_t)hbase * p.k_tok;
+            klo = ld4(ks);
+            khi = ld4(ks + 32);
+            const float* vs = vp + (int64_t)hbase * vt;
+            v0 = ld2(vs);
+            v1 = ld2(vs + vt);
+            v2 = ld2(vs + 2 * vt);
+            v3 = ld2(vs + 3 * vt);
+        } else {  // clamp every row into range, then zero the padding rows
+            const int last = p.n_k - 1;
+            keyc = min(key, last);
+            const float* ks = K + (int64_t)keyc * p.k_tok + 4 * kc;
+            klo = ld4(ks);
+            khi = ld4(ks + 32);
+            const int vkey = hbase + 4 * vq;
+            const float* vs = V + 2 * vc;
+            v0 = ld2(vs + (int64_t)min(vkey, last) * vt);
+            v1 = ld2(vs + (int64_t)min(vkey + 1, last) * vt);
+            v2 = ld2(vs + (int64_t)min(vkey + 2, last) * vt);
+            v3 = ld2(vs + (int64_t)min(vkey + 3, last) * vt);
+            const float2 z = {0.f, 0.f};
+            v0 = vkey <= last ? v0 : z;
+            v1 = vkey + 1 <= last ? v1 : z;
+            v2 = vkey + 2 <= last ? v2 : z;
+            v3 = vkey + 3 <= last ? v3 : z;
+            const bool kin = key <= last;
+            klo = kin ? klo : f32x4{0, 0, 0, 0};
+            khi = kin ? khi : f32x4{0, 0, 0, 0};
+        }
         if (ROPE) {
             kcos = ld4(RC + (int64_t)keyc * 32 + 4 * kc);
             ksin = ld4(RS + (int64_t)keyc * 32 + 4 * kc);
         }
-        const int vkey = hbase + 4 * vq;
-        const float* vs = V + 2 * vc;
-        if (full) {
-            v0 = ld2(vs + (int64_t)vkey * p.v_tok);
-            v1 = ld2(vs + (int64_t)(vkey + 1) * p.v_tok);
-            v2 = ld2(vs + (int64_t)(vkey + 2) * p.v_tok);
-            v3 = ld2(vs + (int64_t)(vkey + 3) * p.v_tok);
-        } else {
-            const float2 z = {0.f, 0.f};
-            const int last = p.n_k - 1;
-            v0 = ld2(vs + (int64_t)min(vkey, last) * p.v_tok);
-            v1 = ld2(vs + (int64_t)min(vkey + 1, last) * p.v_tok);
-            v2 = ld2(vs + (int64_t)min(vkey + 2, last) * p.v_tok);
-            v3 = ld2(vs + (int64_t)min(vkey + 3, last) * p.v_tok);
-            if (vkey >= p.n_k) v0 = z;
-            if (vkey + 1 >= p.n_k) v1 = z;
-            if (vkey + 2 >= p.n_k) v2 = z;
-            if (vkey + 3 >= p.n_k) v3 = z;
-            if (key >= p.n_k) klo = khi = f32x4{0, 0, 0, 0};
-        }
-        if (tid < NK / 2) {
-            const int kk = hbase + tid;
+        if ((hbase & (NK - 1)) == 0) {
+            // First half of a tile: every wave evaluates the 64 key terms of the tile (lane = key),
+            // so its mask-free decision needs no LDS round trip; wave 0 also stores them.
+            const int kk = hbase + lane;
             bool valid = true;
             if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
             kar = key_term<MASK>(kk, p.n_k, valid, p.ctx_keys);
+            next_all_valid = __ballot(kar != 0.f) == 0;
         }
     };
     auto store = [&](Stage& st, int half) {
@@ -206,15 +229,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         float* vd = st.v + (half * 8 + vq) * (kHeadDim * 4);
         st4(vd + vslot(2 * vc) * 4, f32x4{v0.x, v1.x, v2.x, v3.x});
         st4(vd + vslot(2 * vc + 1) * 4, f32x4{v0.y, v1.y, v2.y, v3.y});
-        if (tid < NK / 2) st.kadd[half * (NK / 2) + tid] = kar;
+        if (half == 0 && tid < NK) st.kadd[tid] = kar;
     };
 
     // V operand offsets of this lane (floats, within a key quad): dim db*16 + ql, swizzled.
     const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // db even / odd
 
-    // One 64-key tile on stage `st`. FULLT: every key of the tile is below n_k and every query of
-    // the wave below n_q, so the body has no bounds tests; otherwise only the first nkb key blocks
-    // and nqb query blocks are computed (both uniform) and keys/queries are tested.
+    // One 64-key tile on stage `st`. PLAIN (FULLT): every key of the tile is below n_k and valid,
+    // every query of the wave below n_q and past the tile (causal masks), so the body has no bounds
+    // tests and no mask arithmetic; otherwise only the first nkb key blocks and nqb query blocks are
+    // computed (both uniform) and every score goes through the mask rule.
     auto tile = [&](const Stage& st, int kbase, int nkb, int nqb, auto full_tag, int t) {
         constexpr bool FULLT = decltype(full_tag)::value;
         const bool more = t + 1 < ntiles;
@@ -257,9 +281,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             fetch(kbase + NK + NK / 2);
         }
 
-        // ---- scale, bias, mask, online softmax ----
+        // ---- bias, mask, online softmax (the scale is already in q) ----
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
+            // No contraction in this block: ml below must be rounded once and the same value used in
+            // the weights and in the rescale (a fused ml_run - m * log2e would mix a rounded and an
+            // unrounded maximum: ~1e-6 relative error per rescale, visible at unscaled logits).
+#pragma clang fp contract(off)
             if (!FULLT && qb >= nqb) continue;
             const int qi = wq0 + 16 * qb + ql;
             const int qpos = p.q_pos0 + qi;
@@ -267,18 +295,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
                 const bool on = FULLT || kb < nkb;
-                const f32x4 ka = ld4(st.kadd + kb * 16 + 4 * g);
+                f32x4 ka = {0, 0, 0, 0};
+                if (!FULLT) ka = ld4(st.kadd + kb * 16 + 4 * g);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int key = kbase + kb * 16 + 4 * g + r;
                     float x = kNegInf;
                     if (on) {
 #pragma clang fp contract(off)
-                        x = sacc[kb][qb][r] * p.scale;
+                        x = sacc[kb][qb][r];
                         if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), kRelMax - 1)];
                         if (BIAS == BIAS_DENSE && (FULLT || (key < p.n_k && qi < p.n_q)))
                             x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
-                        x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
+                        if (!FULLT) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
                     }
                     sacc[kb][qb][r] = x;
                     mloc = fmaxf(mloc, x);
@@ -286,20 +315,43 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             }
             const float m_new = fmaxf(m_run[qb], max4(mloc));
             const float m_use = m_new == kNegInf ? 0.f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * kLog2e);
-            float lsum = 0.f;
+            float alpha, lsum = 0.f;
+            if (__ballot(m_use < -1e30f) == 0) {
+                // e = exp2(x log2e - m log2e): one FMA per score. The running max is kept in exp2
+                // units (ml_run), so the rescale uses the same rounded values as the weights.
+                const float ml = m_use * kLog2e;
+                alpha = __builtin_amdgcn_exp2f(ml_run[qb] - ml);
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+                for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float e = __builtin_amdgcn_exp2f((sacc[kb][qb][r] - m_use) * kLog2e);
-                    sacc[kb][qb][r] = e;
-                    lsum += e;
-                }
+                    for (int r = 0; r < 4; r++) {
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], kLog2e, -ml));
+                        sacc[kb][qb][r] = e;
+                        lsum += e;
+                    }
+                ml_run[qb] = m_new == kNegInf ? kNegInf : ml;
+            } else {
+                // Some row has seen only additively masked keys (scores near -FLT_MAX): subtract
+                // first so x - m stays exact and an all-invalid row stays uniform, as in the
+                // reference (src/core/nn.zig:470-505 on scores + (-floatMax)).
+                alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * kLog2e);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float e = __builtin_amdgcn_exp2f((sacc[kb][qb][r] - m_use) * kLog2e);
+                        sacc[kb][qb][r] = e;
+                        lsum += e;
+                    }
+                ml_run[qb] = m_new == kNegInf ? kNegInf : m_use * kLog2e;
+            }
             l_run[qb] = l_run[qb] * alpha + lsum;
             m_run[qb] = m_new;
+            // Rescale O only when some lane's running max moved (alpha == 1 exactly otherwise).
+            if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
-            for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+            }
         }
 
         // ---- O^T += V^T . P^T ----
@@ -335,8 +387,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const int kbase = t * NK;
         const Stage& st = stage[t & 1];
         const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
-        // Full tile: all 64 keys below wave_kend (<= n_k) and all 32 queries below n_q.
-        if (kbase + NK <= wave_kend && wave_nq == QW) {
+        // Mask-free tile: all 64 keys below wave_kend (<= n_k) and valid, all 32 queries below n_q
+        // and, for the causal masks, at or past the tile's last key.
+        bool plain = kbase + NK <= wave_kend && wave_nq == QW && MASK != DECODER && next_all_valid;
+        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
+        if (plain) {
             tile(st, kbase, 4, 2, std::integral_constant<bool, true>{}, t);
         } else if (nkb > 0 && nqb > 0) {
             tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
