@@ -97,13 +97,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
     const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
 
-    // T5 relative-position bias LUT for this head: lut[j - i + n_q - 1].
-    if (BIAS == BIAS_REL) {
-        const int n_rel = p.n_q + p.n_k - 1;
-        for (int t = tid; t < n_rel; t += NT)
-            lut[t] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
-    }
-
     // Key range of the workgroup and of this wave (tiles past it are skipped).
     const int wg_qhi = p.q_pos0 + min(p.n_q, q0 + QT) - 1;
     const int kend = key_end_for<MASK>(wg_qhi, p.n_k, p.ctx_keys);
@@ -112,41 +105,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const int ntiles = (kend + NK - 1) / NK;
     const int kv_len = valid_len<MASK>(p.n_k, p.ctx_keys);  // key_valid bytes of this row
 
-    // Q^T operand: qreg[qb][s], step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8). Rotated here.
+    // Q^T operand: qreg[qb][s], step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8). Filled by
+    // load_q() in the prologue (rotated and scaled there).
     float qreg[2][16];
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int qi = wq0 + 16 * qb + ql;
-        f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
-        if (qi < p.n_q) {
-            const float* src = Q + (int64_t)qi * p.q_tok;
-            a0 = ld4(src + 8 * g);
-            a1 = ld4(src + 8 * g + 4);
-            a2 = ld4(src + 32 + 8 * g);
-            a3 = ld4(src + 32 + 8 * g + 4);
-            if (ROPE) {
-                const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
-                const f32x4 c0 = ld4(RC + row + 8 * g), c1 = ld4(RC + row + 8 * g + 4);
-                const f32x4 s0 = ld4(RS + row + 8 * g), s1 = ld4(RS + row + 8 * g + 4);
-                rope4(a0, a2, c0, s0);
-                rope4(a1, a3, c1, s1);
-            }
-            // The score scale goes into q: scores = (scale q) . k. For the power-of-two scales every
-            // family uses (1, 1/8) this equals the reference's alpha * (q . k) bit for bit (scaling
-            // by 2^n commutes with every rounding of the dot product).
-            a0 *= p.scale;
-            a1 *= p.scale;
-            a2 *= p.scale;
-            a3 *= p.scale;
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            qreg[qb][t] = a0[t];
-            qreg[qb][4 + t] = a1[t];
-            qreg[qb][8 + t] = a2[t];
-            qreg[qb][12 + t] = a3[t];
-        }
-    }
 
     float m_run[2] = {kNegInf, kNegInf};   // running max of the scores
     float ml_run[2] = {kNegInf, kNegInf};  // the same in exp2 units, as used by the weights
@@ -164,9 +125,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     //    so only one half (25 registers) is ever in flight.
     const int krow = tid >> 3, kc = tid & 7;
     const int vq = tid >> 5, vc = tid & 31;
-    f32x4 klo, khi, kcos, ksin;
-    float2 v0, v1, v2, v3;
-    float kar = 0.f;
+    struct Half {  // one thread's share of a 32-key half tile, in flight from HBM to LDS
+        f32x4 klo, khi, kcos, ksin;
+        f32x4 v01, v23;  // V rows 4vq+0,1 and 4vq+2,3 (two dims each)
+        float kar;
+    };
+    Half ha, hb;  // the loop stages through ha; the prologue fetches both halves of tile 0 at once
     bool next_all_valid = true;  // uniform: every key term of the tile being fetched is 0
 
     // Per-thread base pointers: a half tile adds the uniform hbase * stride.
@@ -174,7 +138,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const float* const vp = V + (int64_t)(4 * vq) * p.v_tok + 2 * vc;
     const int64_t vt = p.v_tok;
 
-    auto fetch = [&](int hbase) {  // keys [hbase, hbase + 32)
+    auto fetch = [&](int hbase, Half& hs) {  // keys [hbase, hbase + 32)
+        f32x4 klo, khi;
+        f32x2 v0, v1, v2, v3;
         const int key = hbase + krow;
         int keyc = key;
         if (hbase + NK / 2 <= p.n_k) {  // uniform: the whole half is in range
@@ -198,7 +164,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             v1 = ld2(vs + (int64_t)min(vkey + 1, last) * vt);
             v2 = ld2(vs + (int64_t)min(vkey + 2, last) * vt);
             v3 = ld2(vs + (int64_t)min(vkey + 3, last) * vt);
-            const float2 z = {0.f, 0.f};
+            const f32x2 z = {0.f, 0.f};
             v0 = vkey <= last ? v0 : z;
             v1 = vkey + 1 <= last ? v1 : z;
             v2 = vkey + 2 <= last ? v2 : z;
@@ -207,9 +173,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             klo = kin ? klo : f32x4{0, 0, 0, 0};
             khi = kin ? khi : f32x4{0, 0, 0, 0};
         }
+        hs.klo = klo;
+        hs.khi = khi;
+        hs.v01 = f32x4{v0[0], v0[1], v1[0], v1[1]};
+        hs.v23 = f32x4{v2[0], v2[1], v3[0], v3[1]};
         if (ROPE) {
-            kcos = ld4(RC + (int64_t)keyc * 32 + 4 * kc);
-            ksin = ld4(RS + (int64_t)keyc * 32 + 4 * kc);
+            hs.kcos = ld4(RC + (int64_t)keyc * 32 + 4 * kc);
+            hs.ksin = ld4(RS + (int64_t)keyc * 32 + 4 * kc);
         }
         if ((hbase & (NK - 1)) == 0) {
             // First half of a tile: every wave evaluates the 64 key terms of the tile (lane = key),
@@ -217,19 +187,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             const int kk = hbase + lane;
             bool valid = true;
             if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
-            kar = key_term<MASK>(kk, p.n_k, valid, p.ctx_keys);
-            next_all_valid = __ballot(kar != 0.f) == 0;
+            hs.kar = key_term<MASK>(kk, p.n_k, valid, p.ctx_keys);
+            next_all_valid = __ballot(hs.kar != 0.f) == 0;
         }
     };
-    auto store = [&](Stage& st, int half) {
-        if (ROPE) rope4(klo, khi, kcos, ksin);
+    auto store = [&](Stage& st, int half, Half& hs) {
+        if (ROPE) rope4(hs.klo, hs.khi, hs.kcos, hs.ksin);
         float* kd = st.k + (half * (NK / 2) + krow) * KPAD + 4 * kc;
-        st4(kd, klo);
-        st4(kd + 32, khi);
+        st4(kd, hs.klo);
+        st4(kd + 32, hs.khi);
         float* vd = st.v + (half * 8 + vq) * (kHeadDim * 4);
-        st4(vd + vslot(2 * vc) * 4, f32x4{v0.x, v1.x, v2.x, v3.x});
-        st4(vd + vslot(2 * vc + 1) * 4, f32x4{v0.y, v1.y, v2.y, v3.y});
-        if (half == 0 && tid < NK) st.kadd[tid] = kar;
+        st4(vd + vslot(2 * vc) * 4, f32x4{hs.v01[0], hs.v01[2], hs.v23[0], hs.v23[2]});
+        st4(vd + vslot(2 * vc + 1) * 4, f32x4{hs.v01[1], hs.v01[3], hs.v23[1], hs.v23[3]});
+        if (half == 0 && tid < NK) st.kadd[tid] = hs.kar;
     };
 
     // V operand offsets of this lane (floats, within a key quad): dim db*16 + ql, swizzled.
@@ -243,7 +213,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         constexpr bool FULLT = decltype(full_tag)::value;
         const bool more = t + 1 < ntiles;
         Stage& nxt = stage[(t + 1) & 1];
-        if (more) fetch(kbase + NK);
+        if (more) fetch(kbase + NK, ha);
 
         // ---- S^T = K . Q^T, four accumulation chains per block ----
         f32x4 sacc[4][2];
@@ -277,8 +247,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
         // First half of the next tile to LDS while the matrix cores work; fetch its second half.
         if (more) {
-            store(nxt, 0);
-            fetch(kbase + NK + NK / 2);
+            store(nxt, 0, ha);
+            fetch(kbase + NK + NK / 2, ha);
         }
 
         // ---- bias, mask, online softmax (the scale is already in q) ----
@@ -372,15 +342,67 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                         oacc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db][r], sacc[kb][qb][r], oacc[db][qb], 0, 0, 0);
                     }
         }
-        if (more) store(nxt, 1);
+        if (more) store(nxt, 1, ha);
     };
 
-    if (ntiles > 0) {
-        fetch(0);
-        store(stage[0], 0);
-        fetch(NK / 2);
-        store(stage[0], 1);
+    // Prologue: tile 0's two halves, q and the T5 table are all requested before anything waits,
+    // so a short row (three tiles at L = 129) pays about one memory latency here, not six.
+    fetch(0, ha);
+    fetch(NK / 2, hb);
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const int qi = wq0 + 16 * qb + ql;
+        f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
+        if (qi < p.n_q) {
+            const float* src = Q + (int64_t)qi * p.q_tok;
+            a0 = ld4(src + 8 * g);
+            a1 = ld4(src + 8 * g + 4);
+            a2 = ld4(src + 32 + 8 * g);
+            a3 = ld4(src + 32 + 8 * g + 4);
+            if (ROPE) {
+                const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
+                const f32x4 c0 = ld4(RC + row + 8 * g), c1 = ld4(RC + row + 8 * g + 4);
+                const f32x4 s0 = ld4(RS + row + 8 * g), s1 = ld4(RS + row + 8 * g + 4);
+                rope4(a0, a2, c0, s0);
+                rope4(a1, a3, c1, s1);
+            }
+            // The score scale goes into q: scores = (scale q) . k. For the power-of-two scales every
+            // family uses (1, 1/8) this equals the reference's alpha * (q . k) bit for bit (scaling
+            // by 2^n commutes with every rounding of the dot product).
+            a0 *= p.scale;
+            a1 *= p.scale;
+            a2 *= p.scale;
+            a3 *= p.scale;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            qreg[qb][t] = a0[t];
+            qreg[qb][4 + t] = a1[t];
+            qreg[qb][8 + t] = a2[t];
+            qreg[qb][12 + t] = a3[t];
+        }
     }
+    if (BIAS == BIAS_REL) {  // lut[j - i + n_q - 1] for this head, four entries per thread per round
+        const int n_rel = p.n_q + p.n_k - 1;
+        for (int t0 = 0; t0 < n_rel; t0 += 4 * NT) {
+            int bk[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = t0 + u * NT + tid;
+                bk[u] = t < n_rel ? min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) : 0;
+            }
+            float val[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) val[u] = p.rel_table[bk[u] * p.H + h];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = t0 + u * NT + tid;
+                if (t < n_rel) lut[t] = val[u];
+            }
+        }
+    }
+    store(stage[0], 0, ha);
+    store(stage[0], 1, hb);
     __syncthreads();
     const int nqb = (wave_nq + 15) >> 4;
     for (int t = 0; t < ntiles; t++) {
@@ -396,10 +418,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         } else if (nkb > 0 && nqb > 0) {
             tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
         } else if (t + 1 < ntiles) {
-            fetch(kbase + NK);
-            store(stage[(t + 1) & 1], 0);
-            fetch(kbase + NK + NK / 2);
-            store(stage[(t + 1) & 1], 1);
+            fetch(kbase + NK, ha);
+            store(stage[(t + 1) & 1], 0, ha);
+            fetch(kbase + NK + NK / 2, ha);
+            store(stage[(t + 1) & 1], 1, ha);
         }
         __syncthreads();
     }

@@ -9,6 +9,9 @@
 namespace tsfm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));  // not HIP's float2: a union-based struct
+                                                          // that the optimiser cannot keep in registers
+                                                          // once it sits inside another struct
 
 constexpr int kHeadDim = 64;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -97,7 +100,7 @@ __device__ __forceinline__ void rope4(f32x4& lo, f32x4& hi, f32x4 c, f32x4 s) {
 }
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
-__device__ __forceinline__ float2 ld2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+__device__ __forceinline__ f32x2 ld2(const float* p) { return *reinterpret_cast<const f32x2*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
 // Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48), on the VALU with
