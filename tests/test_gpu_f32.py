@@ -64,7 +64,7 @@ def _inputs(seed, B, H, n_q, n_k):
 
 
 @pytest.mark.parametrize("mask", [0, 1, 2, 3, 4])
-@pytest.mark.parametrize("n", [1, 15, 16, 17, 65, 129, 200])
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 65, 129, 144, 145, 200, 400])
 def test_masks_match_oracle(ta, orc, gpu_ready, mask, n):
     B, H = 2, 3
     q, k, v, kv = _inputs(100 + n + 7 * mask, B, H, n, n)
@@ -117,6 +117,21 @@ def test_causal_with_query_offset_matches_concatenated_rows(ta, orc, gpu_ready):
     full = oracle_generic(orc, 2, q, k, v, None, B, H, P + n, 0.125)
     got = run_generic(ta, 2, np.ascontiguousarray(q[:, P:]), k, v, None, B, H, n, P + n, 0.125, q_pos0=P)
     assert _ref.scaled_err(got, full[:, P:]) <= TOL
+
+
+@pytest.mark.parametrize("n_q,n_k", [(300, 100), (145, 144), (20, 144), (1, 577)])
+def test_rectangular_full_mask_matches_float64(ta, gpu_ready, n_q, n_k):
+    """n_q != n_k (several query tiles over one short key row; one query over a long one),
+    against float64, so both the LDS-resident (n_k <= 144) and the streaming kernel are covered."""
+    B, H = 2, 2
+    q, k, v, _ = _inputs(17 + n_q, B, H, n_q, n_k)
+    got = run_generic(ta, 0, q, k, v, None, B, H, n_q, n_k, 0.125)
+    for b in range(B):
+        allowed = np.ones((n_q, n_k), bool)
+        for hh in range(H):
+            sel = slice(hh * 64, hh * 64 + 64)
+            want = _ref.naive_attend(q[b, :, sel], k[b, :, sel], v[b, :, sel], allowed, 0.125)
+            assert _ref.scaled_err(got[b, :, sel], want) <= TOL
 
 
 def test_keys_additive_all_invalid_row_is_uniform(ta, orc, gpu_ready):

@@ -439,8 +439,315 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
 }
 
+// ---- short rows: every key resident in LDS ------------------------------------------------------
+//
+// Chronos-Bolt rows are short (at most 128 patches + REG = 129 tokens). Streamed through the
+// two-stage pipeline above they pay a staging round and a barrier for each of three tiles, and
+// 128-query workgroups leave a one-query tail workgroup (129 = 128 + 1) that stages all of K/V
+// again. Here one workgroup of 3 waves x 3 query blocks (144 queries) loads the whole K, V, key
+// terms and T5 table of its (series, head) into LDS once, then runs the same per-tile arithmetic
+// (four-chain scores, online softmax, P kept in registers) without any further barrier.
+
+constexpr int RQB = 3;                  // query blocks of 16 per wave
+constexpr int RNW = 3;                  // waves per workgroup
+constexpr int RNT = 64 * RNW;           // threads
+constexpr int RQT = 16 * RQB * RNW;     // queries per workgroup (144)
+constexpr int kResidentKeys = 144;      // longest row the resident kernel takes
+constexpr int RKIT = (kResidentKeys * 8 + RNT - 1) / RNT;  // K staging items per thread
+constexpr int RVIT = (kResidentKeys * 8 + RNT - 1) / RNT;  // V staging items per thread
+
+// Dynamic LDS layout, in floats: K [nkp][KPAD] | V [nkp/4 quads][64 swizzled][4] | key terms [nkp] |
+// T5 table [n_q + n_k - 1], with nkp = n_k rounded up to 16 keys.
+struct ResidentLayout {
+    int nkp, v_off, a_off, l_off, total;
+};
+__host__ __device__ inline ResidentLayout resident_layout(int n_q, int n_k, bool rel_lut) {
+    ResidentLayout L;
+    L.nkp = (n_k + 15) & ~15;
+    L.v_off = L.nkp * KPAD;
+    L.a_off = L.v_off + L.nkp * kHeadDim;
+    L.l_off = L.a_off + L.nkp;
+    L.total = L.l_off + (rel_lut ? n_q + n_k - 1 : 0);
+    return L;
+}
+
+template <int MASK, int BIAS, bool ROPE>
+__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_f32_resident(Params p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    const ResidentLayout lay = resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL);
+    float* const Ks = smem;
+    float* const Vs = smem + lay.v_off;
+    float* const kadd = smem + lay.a_off;
+    float* const lut = smem + lay.l_off;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, g = lane >> 4;
+    const int q_tiles = (p.n_q + RQT - 1) / RQT;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = logical / q_tiles, qt = logical % q_tiles;
+    const int b = bh / p.H, h = bh % p.H;
+    const int wq0 = qt * RQT + wave * 16 * RQB;  // first query of this wave
+
+    const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.q_batch + h * kHeadDim;
+    const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.k_batch + h * kHeadDim;
+    const float* __restrict__ V = static_cast<const float*>(p.v) + b * p.v_batch + h * kHeadDim;
+    float* __restrict__ O = static_cast<float*>(p.o) + b * p.o_batch + h * kHeadDim;
+    const uint8_t* __restrict__ KV = mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : nullptr;
+    const int rope_tab = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
+    const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
+    const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
+    const int kv_len = valid_len<MASK>(p.n_k, p.ctx_keys);
+    const int last = p.n_k - 1;
+
+    // ---- stage K, V, key terms, T5 table and q: every load is issued before the first wait ----
+    f32x4 klo[RKIT], khi[RKIT], kcs[RKIT], ksn[RKIT];
+#pragma unroll
+    for (int u = 0; u < RKIT; u++) {  // K item = (row, c): dims 4c..4c+3 and 32+4c..32+4c+3
+        const int it = tid + u * RNT, row = it >> 3, c = it & 7, rc = min(row, last);
+        const float* src = K + (int64_t)rc * p.k_tok + 4 * c;
+        klo[u] = ld4(src);
+        khi[u] = ld4(src + 32);
+        if (ROPE) {
+            kcs[u] = ld4(RC + (int64_t)rc * 32 + 4 * c);
+            ksn[u] = ld4(RS + (int64_t)rc * 32 + 4 * c);
+        }
+    }
+    f32x4 v01[RVIT], v23[RVIT];
+#pragma unroll
+    for (int u = 0; u < RVIT; u++) {  // V item = (quad of 4 rows, dims 2vc, 2vc+1)
+        const int it = tid + u * RNT, quad = it >> 5, vc = it & 31, r0 = 4 * quad;
+        const float* src = V + 2 * vc;
+        const f32x2 a = ld2(src + (int64_t)min(r0, last) * p.v_tok);
+        const f32x2 bb = ld2(src + (int64_t)min(r0 + 1, last) * p.v_tok);
+        const f32x2 c = ld2(src + (int64_t)min(r0 + 2, last) * p.v_tok);
+        const f32x2 d = ld2(src + (int64_t)min(r0 + 3, last) * p.v_tok);
+        v01[u] = f32x4{r0 <= last ? a[0] : 0.f, r0 <= last ? a[1] : 0.f, r0 + 1 <= last ? bb[0] : 0.f,
+                       r0 + 1 <= last ? bb[1] : 0.f};
+        v23[u] = f32x4{r0 + 2 <= last ? c[0] : 0.f, r0 + 2 <= last ? c[1] : 0.f, r0 + 3 <= last ? d[0] : 0.f,
+                       r0 + 3 <= last ? d[1] : 0.f};
+    }
+    float kterm = 0.f;
+    if (tid < lay.nkp) {
+        bool valid = true;
+        if (mask_reads_valid<MASK>()) valid = tid < kv_len && KV[tid] != 0;
+        kterm = key_term<MASK>(tid, p.n_k, valid, p.ctx_keys);
+    }
+    float qreg[RQB][16];
+#pragma unroll
+    for (int qb = 0; qb < RQB; qb++) {
+        const int qi = wq0 + 16 * qb + ql;
+        f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
+        if (qi < p.n_q) {
+            const float* src = Q + (int64_t)qi * p.q_tok;
+            a0 = ld4(src + 8 * g);
+            a1 = ld4(src + 8 * g + 4);
+            a2 = ld4(src + 32 + 8 * g);
+            a3 = ld4(src + 32 + 8 * g + 4);
+            if (ROPE) {
+                const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
+                rope4(a0, a2, ld4(RC + row + 8 * g), ld4(RS + row + 8 * g));
+                rope4(a1, a3, ld4(RC + row + 8 * g + 4), ld4(RS + row + 8 * g + 4));
+            }
+            a0 *= p.scale;  // power-of-two scales: exact, as in the streaming kernel
+            a1 *= p.scale;
+            a2 *= p.scale;
+            a3 *= p.scale;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            qreg[qb][t] = a0[t];
+            qreg[qb][4 + t] = a1[t];
+            qreg[qb][8 + t] = a2[t];
+            qreg[qb][12 + t] = a3[t];
+        }
+    }
+    if (BIAS == BIAS_REL) {
+        const int n_rel = p.n_q + p.n_k - 1;
+        for (int t0 = 0; t0 < n_rel; t0 += 2 * RNT) {
+            const int t1 = t0 + tid, t2 = t1 + RNT;
+            const int b1 = t1 < n_rel ? min(max(p.rel_bucket[t1], 0), p.rel_buckets - 1) : 0;
+            const int b2 = t2 < n_rel ? min(max(p.rel_bucket[t2], 0), p.rel_buckets - 1) : 0;
+            const float x1 = p.rel_table[b1 * p.H + h], x2 = p.rel_table[b2 * p.H + h];
+            if (t1 < n_rel) lut[t1] = x1;
+            if (t2 < n_rel) lut[t2] = x2;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < RKIT; u++) {
+        const int it = tid + u * RNT, row = it >> 3, c = it & 7;
+        if (row >= lay.nkp) continue;
+        f32x4 lo = row <= last ? klo[u] : f32x4{0, 0, 0, 0}, hi = row <= last ? khi[u] : f32x4{0, 0, 0, 0};
+        if (ROPE) rope4(lo, hi, kcs[u], ksn[u]);
+        st4(Ks + row * KPAD + 4 * c, lo);
+        st4(Ks + row * KPAD + 32 + 4 * c, hi);
+    }
+#pragma unroll
+    for (int u = 0; u < RVIT; u++) {
+        const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
+        if (4 * quad >= lay.nkp) continue;
+        float* vd = Vs + quad * (kHeadDim * 4);
+        st4(vd + vslot(2 * vc) * 4, f32x4{v01[u][0], v01[u][2], v23[u][0], v23[u][2]});
+        st4(vd + vslot(2 * vc + 1) * 4, f32x4{v01[u][1], v01[u][3], v23[u][1], v23[u][3]});
+    }
+    if (tid < lay.nkp) kadd[tid] = kterm;
+    __syncthreads();  // the only barrier: everything below reads LDS that no one writes again
+
+    const int wave_nq = max(0, min(16 * RQB, p.n_q - wq0));
+    if (wave_nq == 0) return;
+    const int nqb = (wave_nq + 15) >> 4;
+    const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
+    const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;
+
+    float m_run[RQB], ml_run[RQB], l_run[RQB];
+    f32x4 oacc[4][RQB];
+#pragma unroll
+    for (int qb = 0; qb < RQB; qb++) {
+        m_run[qb] = ml_run[qb] = kNegInf;
+        l_run[qb] = 0.f;
+#pragma unroll
+        for (int db = 0; db < 4; db++) oacc[db][qb] = f32x4{0, 0, 0, 0};
+    }
+
+    auto tile = [&](int kbase, int nkb, auto plain_tag) {
+        constexpr bool PLAIN = decltype(plain_tag)::value;
+        f32x4 sacc[4][RQB];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+#pragma unroll
+            for (int qb = 0; qb < RQB; qb++) sacc[kb][qb] = f32x4{0, 0, 0, 0};
+            if (!PLAIN && kb >= nkb) continue;
+            const float* kr = Ks + (kbase + kb * 16 + ql) * KPAD;
+            const f32x4 k0 = ld4(kr + 8 * g), k1 = ld4(kr + 8 * g + 4);
+            const f32x4 k2 = ld4(kr + 32 + 8 * g), k3 = ld4(kr + 32 + 8 * g + 4);
+            const float kv16[16] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3],
+                                    k2[0], k2[1], k2[2], k2[3], k3[0], k3[1], k3[2], k3[3]};
+#pragma unroll
+            for (int qb = 0; qb < RQB; qb++) {
+                if (!PLAIN && qb >= nqb) continue;
+                f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+#pragma unroll
+                for (int s = 0; s < 16; s += 4) {
+                    c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s], qreg[qb][s], c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 1], qreg[qb][s + 1], c1, 0, 0, 0);
+                    c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 2], qreg[qb][s + 2], c2, 0, 0, 0);
+                    c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 3], qreg[qb][s + 3], c3, 0, 0, 0);
+                }
+                sacc[kb][qb] = (c0 + c1) + (c2 + c3);
+                asm volatile("" : "+v"(sacc[kb][qb]));  // keep the tree sum here (see above)
+            }
+        }
+#pragma unroll
+        for (int qb = 0; qb < RQB; qb++) {
+#pragma clang fp contract(off)
+            if (!PLAIN && qb >= nqb) continue;
+            const int qi = wq0 + 16 * qb + ql;
+            const int qpos = p.q_pos0 + qi;
+            float mloc = kNegInf;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const bool on = PLAIN || kb < nkb;
+                f32x4 ka = {0, 0, 0, 0};
+                if (!PLAIN && on) ka = ld4(kadd + kbase + kb * 16 + 4 * g);  // blocks past nkb: past nkp
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = kbase + kb * 16 + 4 * g + r;
+                    float x = kNegInf;
+                    if (on) {
+                        x = sacc[kb][qb][r];
+                        if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), p.n_q + p.n_k - 2)];
+                        if (BIAS == BIAS_DENSE && (PLAIN || (key < p.n_k && qi < p.n_q)))
+                            x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
+                        if (!PLAIN) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
+                    }
+                    sacc[kb][qb][r] = x;
+                    mloc = fmaxf(mloc, x);
+                }
+            }
+            const float m_new = fmaxf(m_run[qb], max4(mloc));
+            const float m_use = m_new == kNegInf ? 0.f : m_new;
+            float alpha, lsum = 0.f;
+            if (__ballot(m_use < -1e30f) == 0) {
+                const float ml = m_use * kLog2e;
+                alpha = __builtin_amdgcn_exp2f(ml_run[qb] - ml);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], kLog2e, -ml));
+                        sacc[kb][qb][r] = e;
+                        lsum += e;
+                    }
+                ml_run[qb] = m_new == kNegInf ? kNegInf : ml;
+            } else {
+                alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * kLog2e);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float e = __builtin_amdgcn_exp2f((sacc[kb][qb][r] - m_use) * kLog2e);
+                        sacc[kb][qb][r] = e;
+                        lsum += e;
+                    }
+                ml_run[qb] = m_new == kNegInf ? kNegInf : m_use * kLog2e;
+            }
+            l_run[qb] = l_run[qb] * alpha + lsum;
+            m_run[qb] = m_new;
+            if (__ballot(alpha != 1.f) != 0) {
+#pragma unroll
+                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            if (!PLAIN && kb >= nkb) continue;
+            const float* vq4 = Vs + ((kbase >> 2) + kb * 4 + g) * (kHeadDim * 4);
+            f32x4 va[4];
+#pragma unroll
+            for (int db = 0; db < 4; db++) va[db] = ld4(vq4 + db * 64 + ((db & 1) ? voff_odd - 64 : voff_even));
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+#pragma unroll
+                    for (int qb = 0; qb < RQB; qb++) {
+                        if (!PLAIN && qb >= nqb) continue;
+                        oacc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db][r], sacc[kb][qb][r], oacc[db][qb], 0, 0, 0);
+                    }
+        }
+    };
+
+    for (int kbase = 0; kbase < wave_kend; kbase += NK) {
+        const int nkb = min(4, (wave_kend - kbase + 15) >> 4);
+        bool plain = kbase + NK <= wave_kend && wave_nq == 16 * RQB && MASK != DECODER;
+        if (plain && mask_reads_valid<MASK>()) plain = __ballot(kadd[kbase + lane] != 0.f) == 0;
+        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
+        if (plain) tile(kbase, 4, std::integral_constant<bool, true>{});
+        else tile(kbase, nkb, std::integral_constant<bool, false>{});
+    }
+
+#pragma unroll
+    for (int qb = 0; qb < RQB; qb++) {
+        const int qi = wq0 + 16 * qb + ql;
+        const float l = sum4(l_run[qb]);
+        if (qi >= p.n_q) continue;
+        const float inv = 1.0f / l;
+        float* dst = O + (int64_t)qi * p.o_tok;
+#pragma unroll
+        for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, oacc[db][qb] * inv);
+    }
+}
+
 template <int MASK, int BIAS, bool ROPE>
 hipError_t launch_one(const Params& p, hipStream_t stream) {
+    if (p.n_k <= kResidentKeys) {  // short rows: the whole K/V of a (series, head) in LDS
+        const int q_tiles = (p.n_q + RQT - 1) / RQT;
+        const int64_t blocks = (int64_t)p.B * p.H * q_tiles;
+        if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+        const size_t lds = (size_t)resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL).total * sizeof(float);
+        hipLaunchKernelGGL((attn_fwd_f32_resident<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(RNT), lds, stream,
+                           p);
+        return hipGetLastError();
+    }
     const int q_tiles = (p.n_q + QT - 1) / QT;
     const int64_t blocks = (int64_t)p.B * p.H * q_tiles;
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
