@@ -242,6 +242,7 @@ def run_decode(torch, ta, workloads, peak):
 
 
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode}
+SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 
 
 def main() -> int:
@@ -290,6 +291,13 @@ def main() -> int:
     for _ in range(args.warmup):
         warm()
     torch.cuda.synchronize()
+    # The engine clock ramps up over the first milliseconds of load: keep warming (untimed) until
+    # the GPU has been busy for SPINUP_S, so the timed steps do not start on a cold clock.
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < SPINUP_S:
+        for _ in range(8):
+            warm()
+        torch.cuda.synchronize()
     # Timed region: the steps between two full synchronisations. A single-launch step gets one
     # event pair per launch on the stream the kernel runs on (the per-dispatch duration rocprofv3
     # --kernel-trace reports); a multi-launch step records its dominant kernel itself.

@@ -5,7 +5,7 @@
 // launch and no score matrix exists: K/V tiles of 64 keys are staged in LDS and both products run
 // on the f32 matrix cores (v_mfma_f32_16x16x4_f32) with an online softmax in registers.
 //
-// Wave layout (4 waves x 32 queries, two 16-query blocks qb per wave):
+// Wave layout (8 waves x 16 queries; four waves per SIMD hide each other's latencies):
 //   S^T = K . Q^T   A = K rows (16 keys) from LDS, B = Q^T (16 queries) held in VGPRs.
 //                   Accumulator lane l holds query l%16 and keys 4*(l/16)+r, r=0..3.
 //   O^T += V^T . P^T  A = V^T (16 dims x 4 keys) from LDS, B = P^T straight from the S^T
@@ -24,10 +24,11 @@
 //
 // Pipeline: two LDS stages. While the waves compute on stage t&1, tile t+1 is fetched from HBM and
 // written to the other stage in two 32-key halves (one over the S product, one over softmax and
-// the PV product), so the staging costs 25 registers; one barrier per tile.
-// LDS per stage: K [64 keys][68] (padded: conflict-free 128-bit reads and writes), V [16 key
-// quads][64 dims, XOR-swizzled][4 keys] (conflict-free transposing writes and operand reads), and
-// one additive mask term per key. Two stages + the T5 table fit two workgroups per CU.
+// the PV product), 13 registers per thread; one barrier per tile. The whole wave state (q, O,
+// scores, operands, staging) fits 128 registers, which gives four waves per SIMD.
+// LDS per stage: K [64 keys][68] (padded: conflict-free 128-bit reads), V [16 key quads][64 dims,
+// XOR-swizzled][4 keys] (conflict-free transposing writes and operand reads), and one additive mask
+// term per key. Two stages + the T5 table fit two workgroups per CU.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -35,8 +36,8 @@ namespace tsfm {
 namespace {
 
 constexpr int NK = 64;          // keys per LDS tile
-constexpr int QW = 32;          // queries per wave (2 blocks of 16)
-constexpr int NWAVE = 4;
+constexpr int QW = 16;          // queries per wave (one 16-query block)
+constexpr int NWAVE = 8;
 constexpr int NT = 64 * NWAVE;  // threads per workgroup
 constexpr int QT = QW * NWAVE;  // queries per workgroup
 constexpr int KPAD = 68;        // K row pitch in LDS (floats)
@@ -73,7 +74,7 @@ __device__ __forceinline__ float masked(float x, float ka, int key, int qpos, in
 }
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_f32(Params p) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_fwd_f32(Params p) {
     __shared__ __attribute__((aligned(16))) Stage stage[2];
     __shared__ float lut[BIAS == BIAS_REL ? kRelMax : 1];
 
@@ -92,7 +93,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.k_batch + h * kHeadDim;
     const float* __restrict__ V = static_cast<const float*>(p.v) + b * p.v_batch + h * kHeadDim;
     float* __restrict__ O = static_cast<float*>(p.o) + b * p.o_batch + h * kHeadDim;
-    const uint8_t* __restrict__ KV = mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : nullptr;
     const int rope_tab = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
     const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
     const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
@@ -103,255 +103,214 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const int wave_nq = max(0, min(QW, p.n_q - wq0));
     const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys) : 0;
     const int ntiles = (kend + NK - 1) / NK;
-    const int kv_len = valid_len<MASK>(p.n_k, p.ctx_keys);  // key_valid bytes of this row
 
-    // Q^T operand: qreg[qb][s], step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8). Filled by
-    // load_q() in the prologue (rotated and scaled there).
-    float qreg[2][16];
+    // key_valid of this row through a buffer descriptor sized to the bytes the mask reads: a read
+    // past them returns 0 (= invalid), so the load needs neither a bounds test nor a branch.
+    const __amdgpu_buffer_rsrc_t kv_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid), (short)0,
+        mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0, kBufferConfig);
 
-    float m_run[2] = {kNegInf, kNegInf};   // running max of the scores
-    float ml_run[2] = {kNegInf, kNegInf};  // the same in exp2 units, as used by the weights
-    float l_run[2] = {0.f, 0.f};
-    f32x4 oacc[4][2];
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-        for (int qb = 0; qb < 2; qb++) oacc[db][qb] = f32x4{0, 0, 0, 0};
+    // Q^T operand: qreg[s], step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8) of query wq0 + ql,
+    // rotated and scaled in the prologue.
+    float qreg[16];
+    float m_run = kNegInf;   // running max of the scores
+    float ml_run = kNegInf;  // the same in exp2 units, as used by the weights
+    float l_run = 0.f;
+    f32x4 oacc[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 
-    // ---- tile staging: HBM -> registers -> LDS, one 32-key half at a time ----
-    // K: thread -> key row tid/8 of the half, dims 4c..4c+3 and 32+4c..32+4c+3 with c = tid%8
-    //    (RoPE pairs). V: thread -> key quad tid/32 of the half, dims 2vc, 2vc+1 with vc = tid%32,
-    //    transposed on the way to LDS. Each half is fetched and stored within one tile's compute,
-    //    so only one half (25 registers) is ever in flight.
-    const int krow = tid >> 3, kc = tid & 7;
-    const int vq = tid >> 5, vc = tid & 31;
-    struct Half {  // one thread's share of a 32-key half tile, in flight from HBM to LDS
-        f32x4 klo, khi, kcos, ksin;
-        f32x4 v01, v23;  // V rows 4vq+0,1 and 4vq+2,3 (two dims each)
-        float kar;
+    // ---- tile staging: HBM -> registers -> LDS, one 16-key quarter at a time (6 registers) ----
+    // K: thread -> key row tid/32 of the quarter, dims c and c+32 with c = tid%32 (a RoPE pair).
+    // V: wave w -> half w%2 of key quad w/2 of the quarter, lane -> dim: two keys of one dim, half
+    //    of a 16-byte slot of the transposed layout. Key valid bytes: lane = key of the tile, in every
+    //    wave, with the tile's first quarter.
+    // All through buffer descriptors that end after key n_k - 1: rows past it (tile padding) read
+    // as zeros, so a partial tile needs no clamping and no branch.
+    const int krow = tid >> 5, kc = tid & 31;
+    struct Quarter {  // one thread's share of a 16-key quarter tile, in flight from HBM to LDS
+        float klo, khi, kcs, ksn;
+        f32x2 v;  // V rows 4*(wave/2) + 2*(wave%2) + 0..1 of the quarter, dim `lane`
     };
-    Half ha, hb;  // the loop stages through ha; the prologue fetches both halves of tile 0 at once
-    bool next_all_valid = true;  // uniform: every key term of the tile being fetched is 0
+    const __amdgpu_buffer_rsrc_t k_buf = make_buf(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 4));
+    const __amdgpu_buffer_rsrc_t v_buf = make_buf(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 4));
+    const __amdgpu_buffer_rsrc_t c_buf = make_buf(RC, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+    const __amdgpu_buffer_rsrc_t s_buf = make_buf(RS, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+    const uint32_t koff = (uint32_t)(krow * p.k_tok + kc) * 4u;
+    const uint32_t voff = (uint32_t)((4 * (wave >> 1) + 2 * (wave & 1)) * p.v_tok + lane) * 4u;
+    const uint32_t coff = (uint32_t)(krow * 32 + kc) * 4u;
 
-    // Per-thread base pointers: a half tile adds the uniform hbase * stride.
-    const float* const kp = K + (int64_t)krow * p.k_tok + 4 * kc;
-    const float* const vp = V + (int64_t)(4 * vq) * p.v_tok + 2 * vc;
-    const int64_t vt = p.v_tok;
-
-    auto fetch = [&](int hbase, Half& hs) {  // keys [hbase, hbase + 32)
-        f32x4 klo, khi;
-        f32x2 v0, v1, v2, v3;
-        const int key = hbase + krow;
-        int keyc = key;
-        if (hbase + NK / 2 <= p.n_k) {  // uniform: the whole half is in range
-            const float* ks = kp + (int64_t)hbase * p.k_tok;
-            klo = ld4(ks);
-            khi = ld4(ks + 32);
-            const float* vs = vp + (int64_t)hbase * vt;
-            v0 = ld2(vs);
-            v1 = ld2(vs + vt);
-            v2 = ld2(vs + 2 * vt);
-            v3 = ld2(vs + 3 * vt);
-        } else {  // clamp every row into range, then zero the padding rows
-            const int last = p.n_k - 1;
-            keyc = min(key, last);
-            const float* ks = K + (int64_t)keyc * p.k_tok + 4 * kc;
-            klo = ld4(ks);
-            khi = ld4(ks + 32);
-            const int vkey = hbase + 4 * vq;
-            const float* vs = V + 2 * vc;
-            v0 = ld2(vs + (int64_t)min(vkey, last) * vt);
-            v1 = ld2(vs + (int64_t)min(vkey + 1, last) * vt);
-            v2 = ld2(vs + (int64_t)min(vkey + 2, last) * vt);
-            v3 = ld2(vs + (int64_t)min(vkey + 3, last) * vt);
-            const f32x2 z = {0.f, 0.f};
-            v0 = vkey <= last ? v0 : z;
-            v1 = vkey + 1 <= last ? v1 : z;
-            v2 = vkey + 2 <= last ? v2 : z;
-            v3 = vkey + 3 <= last ? v3 : z;
-            const bool kin = key <= last;
-            klo = kin ? klo : f32x4{0, 0, 0, 0};
-            khi = kin ? khi : f32x4{0, 0, 0, 0};
-        }
-        hs.klo = klo;
-        hs.khi = khi;
-        hs.v01 = f32x4{v0[0], v0[1], v1[0], v1[1]};
-        hs.v23 = f32x4{v2[0], v2[1], v3[0], v3[1]};
+    auto fetch = [&](int qbase, Quarter& hs) {  // keys [qbase, qbase + 16)
+        const uint32_t kq = koff + (uint32_t)(qbase * p.k_tok) * 4u;
+        hs.klo = bld1(k_buf, kq);
+        hs.khi = bld1(k_buf, kq + 128u);
+        const uint32_t vq = voff + (uint32_t)(qbase * p.v_tok) * 4u;
+        hs.v = f32x2{bld1(v_buf, vq), bld1(v_buf, vq + (uint32_t)p.v_tok * 4u)};
         if (ROPE) {
-            hs.kcos = ld4(RC + (int64_t)keyc * 32 + 4 * kc);
-            hs.ksin = ld4(RS + (int64_t)keyc * 32 + 4 * kc);
-        }
-        if ((hbase & (NK - 1)) == 0) {
-            // First half of a tile: every wave evaluates the 64 key terms of the tile (lane = key),
-            // so its mask-free decision needs no LDS round trip; wave 0 also stores them.
-            const int kk = hbase + lane;
-            bool valid = true;
-            if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
-            hs.kar = key_term<MASK>(kk, p.n_k, valid, p.ctx_keys);
-            next_all_valid = __ballot(hs.kar != 0.f) == 0;
+            hs.kcs = bld1(c_buf, coff + (uint32_t)qbase * 128u);
+            hs.ksn = bld1(s_buf, coff + (uint32_t)qbase * 128u);
         }
     };
-    auto store = [&](Stage& st, int half, Half& hs) {
-        if (ROPE) rope4(hs.klo, hs.khi, hs.kcos, hs.ksin);
-        float* kd = st.k + (half * (NK / 2) + krow) * KPAD + 4 * kc;
-        st4(kd, hs.klo);
-        st4(kd + 32, hs.khi);
-        float* vd = st.v + (half * 8 + vq) * (kHeadDim * 4);
-        st4(vd + vslot(2 * vc) * 4, f32x4{hs.v01[0], hs.v01[2], hs.v23[0], hs.v23[2]});
-        st4(vd + vslot(2 * vc + 1) * 4, f32x4{hs.v01[1], hs.v01[3], hs.v23[1], hs.v23[3]});
-        if (half == 0 && tid < NK) st.kadd[tid] = hs.kar;
+    auto store = [&](Stage& st, int quarter, Quarter& hs) {
+        if (ROPE) {
+#pragma clang fp contract(off)
+            const float x1 = hs.klo, x2 = hs.khi;  // nn.ropeHalf, src/core/nn.zig:453-460
+            hs.klo = x1 * hs.kcs - x2 * hs.ksn;
+            hs.khi = x2 * hs.kcs + x1 * hs.ksn;
+        }
+        float* kd = st.k + (quarter * 16 + krow) * KPAD + kc;
+        kd[0] = hs.klo;
+        kd[32] = hs.khi;
+        st2(st.v + (quarter * 4 + (wave >> 1)) * (kHeadDim * 4) + vslot(lane) * 4 + 2 * (wave & 1), hs.v);
     };
+    // key_valid byte of key tbase + lane (returned as loaded; 1 for masks that do not read it).
+    auto fetch_valid = [&](int tbase) -> uint32_t {
+        return mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, tbase + lane, 0, 0) : 1u;
+    };
+    // Additive mask term of key tbase + lane, and the tile's mask-free test (every term 0).
+    auto kterm = [&](int tbase, uint32_t kvb) { return key_term<MASK>(tbase + lane, p.n_k, kvb != 0, p.ctx_keys); };
+    auto all_valid = [&](int tbase, uint32_t kvb) { return __ballot(kterm(tbase, kvb) != 0.f) == 0; };
+    uint32_t kvb_next;  // key_valid bytes of the tile being staged
 
     // V operand offsets of this lane (floats, within a key quad): dim db*16 + ql, swizzled.
     const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // db even / odd
 
-    // One 64-key tile on stage `st`. PLAIN (FULLT): every key of the tile is below n_k and valid,
-    // every query of the wave below n_q and past the tile (causal masks), so the body has no bounds
-    // tests and no mask arithmetic; otherwise only the first nkb key blocks and nqb query blocks are
-    // computed (both uniform) and every score goes through the mask rule.
-    auto tile = [&](const Stage& st, int kbase, int nkb, int nqb, auto full_tag, int t) {
-        constexpr bool FULLT = decltype(full_tag)::value;
+    // One 64-key tile on stage `st`. PLAIN: every key of the tile is below n_k and valid, every
+    // query of the wave below n_q and, for the causal masks, past the tile, so the body has no
+    // bounds tests and no mask arithmetic; otherwise only the first nkb key blocks are computed
+    // (uniform) and every score goes through the mask rule.
+    auto tile = [&](const Stage& st, int kbase, int nkb, auto plain_tag, int t) {
+        constexpr bool PLAIN = decltype(plain_tag)::value;
         const bool more = t + 1 < ntiles;
         Stage& nxt = stage[(t + 1) & 1];
-        if (more) fetch(kbase + NK, ha);
+        const int nbase = kbase + NK;
+        Quarter sq;  // the next tile's quarters pass through here, one per quarter of this tile's work
+        if (more) {
+            fetch(nbase, sq);
+            kvb_next = fetch_valid(nbase);
+        }
 
-        // ---- S^T = K . Q^T, four accumulation chains per block ----
-        f32x4 sacc[4][2];
+        // ---- S^T = K . Q^T, four accumulation chains per 16-key block ----
+        f32x4 sacc[4];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-#pragma unroll
-            for (int qb = 0; qb < 2; qb++) sacc[kb][qb] = f32x4{0, 0, 0, 0};
-            if (!FULLT && kb >= nkb) continue;
-            const float* kr = st.k + (kb * 16 + ql) * KPAD;
-            const f32x4 k0 = ld4(kr + 8 * g), k1 = ld4(kr + 8 * g + 4);
-            const f32x4 k2 = ld4(kr + 32 + 8 * g), k3 = ld4(kr + 32 + 8 * g + 4);
-            const float kv16[16] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3],
-                                    k2[0], k2[1], k2[2], k2[3], k3[0], k3[1], k3[2], k3[3]};
-#pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                if (!FULLT && qb >= nqb) continue;
-                f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
-#pragma unroll
-                for (int s = 0; s < 16; s += 4) {
-                    c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s], qreg[qb][s], c0, 0, 0, 0);
-                    c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 1], qreg[qb][s + 1], c1, 0, 0, 0);
-                    c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 2], qreg[qb][s + 2], c2, 0, 0, 0);
-                    c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 3], qreg[qb][s + 3], c3, 0, 0, 0);
-                }
-                sacc[kb][qb] = (c0 + c1) + (c2 + c3);
-                // Materialise the sum here: left alone, the optimiser sinks it to the softmax and
-                // keeps all 32 chain accumulators of the tile live (~130 more registers).
-                asm volatile("" : "+v"(sacc[kb][qb]));
+            sacc[kb] = f32x4{0, 0, 0, 0};
+            if (more && (kb == 1 || kb == 3)) {  // next tile: quarter kb/2 to LDS, fetch the next one
+                store(nxt, kb >> 1, sq);
+                fetch(nbase + 16 * (kb / 2 + 1), sq);
             }
+            if (!PLAIN && kb >= nkb) continue;
+            const float* kr = st.k + (kb * 16 + ql) * KPAD;
+            f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {  // dims 8g.. then 32+8g..: eight K values live at a time
+                const f32x4 ka = ld4(kr + 32 * hh + 8 * g), kb4 = ld4(kr + 32 * hh + 8 * g + 4);
+                const float* qh = qreg + 8 * hh;
+                c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[0], qh[0], c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[1], qh[1], c1, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[2], qh[2], c2, 0, 0, 0);
+                c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[3], qh[3], c3, 0, 0, 0);
+                c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[0], qh[4], c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[1], qh[5], c1, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[2], qh[6], c2, 0, 0, 0);
+                c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[3], qh[7], c3, 0, 0, 0);
+            }
+            sacc[kb] = (c0 + c1) + (c2 + c3);
+            // Materialise the sum here: left alone, the optimiser sinks it to the softmax and keeps
+            // the chain accumulators of the whole tile live.
+            asm volatile("" : "+v"(sacc[kb]));
         }
-
-        // First half of the next tile to LDS while the matrix cores work; fetch its second half.
-        if (more) {
-            store(nxt, 0, ha);
-            fetch(kbase + NK + NK / 2, ha);
-        }
+        if (more) nxt.kadd[lane] = kterm(nbase, kvb_next);  // every wave writes the same 64 terms
 
         // ---- bias, mask, online softmax (the scale is already in q) ----
-#pragma unroll
-        for (int qb = 0; qb < 2; qb++) {
+        {
             // No contraction in this block: ml below must be rounded once and the same value used in
             // the weights and in the rescale (a fused ml_run - m * log2e would mix a rounded and an
             // unrounded maximum: ~1e-6 relative error per rescale, visible at unscaled logits).
 #pragma clang fp contract(off)
-            if (!FULLT && qb >= nqb) continue;
-            const int qi = wq0 + 16 * qb + ql;
+            const int qi = wq0 + ql;
             const int qpos = p.q_pos0 + qi;
             float mloc = kNegInf;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
-                const bool on = FULLT || kb < nkb;
+                const bool on = PLAIN || kb < nkb;
                 f32x4 ka = {0, 0, 0, 0};
-                if (!FULLT) ka = ld4(st.kadd + kb * 16 + 4 * g);
+                if (!PLAIN && on) ka = ld4(st.kadd + kb * 16 + 4 * g);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int key = kbase + kb * 16 + 4 * g + r;
                     float x = kNegInf;
                     if (on) {
-#pragma clang fp contract(off)
-                        x = sacc[kb][qb][r];
+                        x = sacc[kb][r];
                         if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), kRelMax - 1)];
-                        if (BIAS == BIAS_DENSE && (FULLT || (key < p.n_k && qi < p.n_q)))
+                        if (BIAS == BIAS_DENSE && (PLAIN || (key < p.n_k && qi < p.n_q)))
                             x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
-                        if (!FULLT) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
+                        if (!PLAIN) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
                     }
-                    sacc[kb][qb][r] = x;
+                    sacc[kb][r] = x;
                     mloc = fmaxf(mloc, x);
                 }
             }
-            const float m_new = fmaxf(m_run[qb], max4(mloc));
+            const float m_new = fmaxf(m_run, max4(mloc));
             const float m_use = m_new == kNegInf ? 0.f : m_new;
-            float alpha, lsum = 0.f;
-            if (__ballot(m_use < -1e30f) == 0) {
-                // e = exp2(x log2e - m log2e): one FMA per score. The running max is kept in exp2
-                // units (ml_run), so the rescale uses the same rounded values as the weights.
-                const float ml = m_use * kLog2e;
-                alpha = __builtin_amdgcn_exp2f(ml_run[qb] - ml);
+            // e = exp2(x log2e - m log2e): one FMA per score. The running max is kept in exp2 units
+            // (ml_run), so the rescale uses the same rounded values as the weights. A row whose max
+            // is still an additively masked score (about -FLT_MAX: only invalid keys so far) takes
+            // exp2((x - m) log2e) instead, which keeps x - m exact and gives such a row the
+            // reference's uniform weights (src/core/nn.zig:470-505 on scores + (-floatMax)).
+            const bool big = m_use < -1e30f;
+            const float shift = big ? m_use : 0.f;
+            const float ml = big ? 0.f : m_use * kLog2e;
+            const float alpha = __builtin_amdgcn_exp2f(big ? (m_run - m_use) * kLog2e : ml_run - ml);
+            float lsum = 0.f;
 #pragma unroll
-                for (int kb = 0; kb < 4; kb++)
+            for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], kLog2e, -ml));
-                        sacc[kb][qb][r] = e;
-                        lsum += e;
-                    }
-                ml_run[qb] = m_new == kNegInf ? kNegInf : ml;
-            } else {
-                // Some row has seen only additively masked keys (scores near -FLT_MAX): subtract
-                // first so x - m stays exact and an all-invalid row stays uniform, as in the
-                // reference (src/core/nn.zig:470-505 on scores + (-floatMax)).
-                alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * kLog2e);
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float e = __builtin_amdgcn_exp2f((sacc[kb][qb][r] - m_use) * kLog2e);
-                        sacc[kb][qb][r] = e;
-                        lsum += e;
-                    }
-                ml_run[qb] = m_new == kNegInf ? kNegInf : m_use * kLog2e;
-            }
-            l_run[qb] = l_run[qb] * alpha + lsum;
-            m_run[qb] = m_new;
+                for (int r = 0; r < 4; r++) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r] - shift, kLog2e, -ml));
+                    sacc[kb][r] = e;
+                    lsum += e;
+                }
+            ml_run = (big || m_new == kNegInf) ? kNegInf : ml;
+            l_run = l_run * alpha + lsum;
+            m_run = m_new;
             // Rescale O only when some lane's running max moved (alpha == 1 exactly otherwise).
             if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
-                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+                for (int db = 0; db < 4; db++) oacc[db] *= alpha;
             }
         }
 
         // ---- O^T += V^T . P^T ----
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-            if (!FULLT && kb >= nkb) continue;
+            if (more && kb == 2) {
+                store(nxt, 2, sq);
+                fetch(nbase + 48, sq);
+            }
+            if (!PLAIN && kb >= nkb) continue;
             const float* vq4 = st.v + (kb * 4 + g) * (kHeadDim * 4);
-            f32x4 va[4];
 #pragma unroll
-            for (int db = 0; db < 4; db++) va[db] = ld4(vq4 + db * 64 + ((db & 1) ? voff_odd - 64 : voff_even));
+            for (int dp = 0; dp < 4; dp += 2) {  // two dim blocks at a time: eight V values live
+                const f32x4 va0 = ld4(vq4 + dp * 64 + voff_even), va1 = ld4(vq4 + dp * 64 + voff_odd);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int db = 0; db < 4; db++)
-#pragma unroll
-                    for (int qb = 0; qb < 2; qb++) {
-                        if (!FULLT && qb >= nqb) continue;
-                        oacc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db][r], sacc[kb][qb][r], oacc[db][qb], 0, 0, 0);
-                    }
+                for (int r = 0; r < 4; r++) {
+                    oacc[dp] = __builtin_amdgcn_mfma_f32_16x16x4f32(va0[r], sacc[kb][r], oacc[dp], 0, 0, 0);
+                    oacc[dp + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va1[r], sacc[kb][r], oacc[dp + 1], 0, 0, 0);
+                }
+            }
         }
-        if (more) store(nxt, 1, ha);
+        if (more) store(nxt, 3, sq);
     };
 
     // Prologue: tile 0's two halves, q and the T5 table are all requested before anything waits,
-    // so a short row (three tiles at L = 129) pays about one memory latency here, not six.
-    fetch(0, ha);
-    fetch(NK / 2, hb);
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int qi = wq0 + 16 * qb + ql;
+    // so a short row pays about one memory latency here, not several.
+    kvb_next = fetch_valid(0);
+    Quarter s0, s1, s2, s3;
+    fetch(0, s0);
+    fetch(16, s1);
+    fetch(32, s2);
+    fetch(48, s3);
+    {
+        const int qi = wq0 + ql;
         f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
         if (qi < p.n_q) {
             const float* src = Q + (int64_t)qi * p.q_tok;
@@ -361,10 +320,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             a3 = ld4(src + 32 + 8 * g + 4);
             if (ROPE) {
                 const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
-                const f32x4 c0 = ld4(RC + row + 8 * g), c1 = ld4(RC + row + 8 * g + 4);
-                const f32x4 s0 = ld4(RS + row + 8 * g), s1 = ld4(RS + row + 8 * g + 4);
-                rope4(a0, a2, c0, s0);
-                rope4(a1, a3, c1, s1);
+                rope4(a0, a2, ld4(RC + row + 8 * g), ld4(RS + row + 8 * g));
+                rope4(a1, a3, ld4(RC + row + 8 * g + 4), ld4(RS + row + 8 * g + 4));
             }
             // The score scale goes into q: scores = (scale q) . k. For the power-of-two scales every
             // family uses (1, 1/8) this equals the reference's alpha * (q . k) bit for bit (scaling
@@ -376,66 +333,74 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            qreg[qb][t] = a0[t];
-            qreg[qb][4 + t] = a1[t];
-            qreg[qb][8 + t] = a2[t];
-            qreg[qb][12 + t] = a3[t];
+            qreg[t] = a0[t];
+            qreg[4 + t] = a1[t];
+            qreg[8 + t] = a2[t];
+            qreg[12 + t] = a3[t];
         }
     }
-    if (BIAS == BIAS_REL) {  // lut[j - i + n_q - 1] for this head, four entries per thread per round
+    if (BIAS == BIAS_REL) {  // lut[j - i + n_q - 1] for this head, two entries per thread per round
         const int n_rel = p.n_q + p.n_k - 1;
-        for (int t0 = 0; t0 < n_rel; t0 += 4 * NT) {
-            int bk[4];
+        for (int t0 = 0; t0 < n_rel; t0 += 2 * NT) {
+            int bk[2];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 2; u++) {
                 const int t = t0 + u * NT + tid;
                 bk[u] = t < n_rel ? min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) : 0;
             }
-            float val[4];
+            float val[2];
 #pragma unroll
-            for (int u = 0; u < 4; u++) val[u] = p.rel_table[bk[u] * p.H + h];
+            for (int u = 0; u < 2; u++) val[u] = p.rel_table[bk[u] * p.H + h];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 2; u++) {
                 const int t = t0 + u * NT + tid;
                 if (t < n_rel) lut[t] = val[u];
             }
         }
     }
-    store(stage[0], 0, ha);
-    store(stage[0], 1, hb);
+    store(stage[0], 0, s0);
+    store(stage[0], 1, s1);
+    store(stage[0], 2, s2);
+    store(stage[0], 3, s3);
+    stage[0].kadd[lane] = kterm(0, kvb_next);
+    bool next_all_valid = all_valid(0, kvb_next);  // of the tile about to be computed
     __syncthreads();
-    const int nqb = (wave_nq + 15) >> 4;
     for (int t = 0; t < ntiles; t++) {
         const int kbase = t * NK;
         const Stage& st = stage[t & 1];
         const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
-        // Mask-free tile: all 64 keys below wave_kend (<= n_k) and valid, all 32 queries below n_q
+        // Mask-free tile: all 64 keys below wave_kend (<= n_k) and valid, all 16 queries below n_q
         // and, for the causal masks, at or past the tile's last key.
         bool plain = kbase + NK <= wave_kend && wave_nq == QW && MASK != DECODER && next_all_valid;
         if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
         if (plain) {
-            tile(st, kbase, 4, 2, std::integral_constant<bool, true>{}, t);
-        } else if (nkb > 0 && nqb > 0) {
-            tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
+            tile(st, kbase, 4, std::integral_constant<bool, true>{}, t);
+        } else if (nkb > 0) {
+            tile(st, kbase, nkb, std::integral_constant<bool, false>{}, t);
         } else if (t + 1 < ntiles) {
-            fetch(kbase + NK, ha);
-            store(stage[(t + 1) & 1], 0, ha);
-            fetch(kbase + NK + NK / 2, ha);
-            store(stage[(t + 1) & 1], 1, ha);
+            Stage& nxt = stage[(t + 1) & 1];
+            kvb_next = fetch_valid(kbase + NK);
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                Quarter sq;
+                fetch(kbase + NK + 16 * qq, sq);
+                store(nxt, qq, sq);
+            }
+            nxt.kadd[lane] = kterm(kbase + NK, kvb_next);
         }
+        // The next tile's flag, from its key_valid bytes fetched at the start of this one.
+        if (t + 1 < ntiles) next_all_valid = all_valid(kbase + NK, kvb_next);
         __syncthreads();
     }
 
     // ---- normalise and store: lane holds query ql, dims 16db + 4g + r ----
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int qi = wq0 + 16 * qb + ql;
-        const float l = sum4(l_run[qb]);
-        if (qi >= p.n_q) continue;
+    const int qi = wq0 + ql;
+    const float l = sum4(l_run);
+    if (qi < p.n_q) {
         const float inv = 1.0f / l;
         float* dst = O + (int64_t)qi * p.o_tok;
 #pragma unroll
-        for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, oacc[db][qb] * inv);
+        for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, oacc[db] * inv);
     }
 }
 

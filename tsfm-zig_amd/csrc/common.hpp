@@ -102,6 +102,31 @@ __device__ __forceinline__ void rope4(f32x4& lo, f32x4& hi, f32x4 c, f32x4 s) {
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ f32x2 ld2(const float* p) { return *reinterpret_cast<const f32x2*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ void st2(float* p, f32x2 v) { *reinterpret_cast<f32x2*>(p) = v; }
+
+// Rotate-half RoPE of two pairs, as rope4.
+__device__ __forceinline__ void rope2(f32x2& lo, f32x2& hi, f32x2 c, f32x2 s) {
+#pragma clang fp contract(off)
+    const f32x2 x1 = lo, x2 = hi;
+    lo = x1 * c - x2 * s;
+    hi = x2 * c + x1 * s;
+}
+
+// Word 3 of a raw buffer descriptor on gfx9 parts: 32-bit data format, no swizzle. Loads past the
+// descriptor's byte count return 0.
+constexpr int kBufferConfig = 0x00020000;
+
+// Raw buffer over `bytes` bytes at base, and loads at a per-lane byte offset: a 32-bit offset in
+// one VGPR instead of a 64-bit pointer in two, and zeros instead of a fault past the end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferConfig);
+}
+__device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ f32x2 bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
 
 // Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48), on the VALU with
 // gfx950's lane swaps: permlane32_swap(x, x) returns (x of lanes 0-31 in both halves, x of lanes
