@@ -73,6 +73,186 @@ __device__ __forceinline__ float masked(float x, float ka, int key, int qpos, in
     return x + ka;  // FULL, KEYS_ADDITIVE: x + 0, x + (-FLT_MAX), or -inf for padding
 }
 
+// ---- one wave's 16-query block: state and the per-tile arithmetic shared by both kernels ----
+
+// Q^T operand q[s] (step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8) of query ql), the O^T
+// accumulator (lane: query ql, dims 16db + 4g + r) and the online-softmax state of the lane's query.
+struct QBlock {
+    float q[16];
+    f32x4 o[4];
+    float m;   // running max of the scores
+    float ml;  // the same in exp2 units, as used by the weights
+    float l;   // running sum of the weights
+};
+
+// Load, rotate and scale query qi (zeros past n_q). The score scale goes into q: scores =
+// (scale q) . k. For the power-of-two scales every family uses (1, 1/8) this equals the reference's
+// alpha * (q . k) bit for bit (scaling by 2^n commutes with every rounding of the dot product).
+template <bool ROPE>
+__device__ __forceinline__ void load_q(QBlock& w, const float* Q, const float* RC, const float* RS, const Params& p,
+                                       int qi, int g) {
+    f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
+    if (qi < p.n_q) {
+        const float* src = Q + (int64_t)qi * p.q_tok;
+        a0 = ld4(src + 8 * g);
+        a1 = ld4(src + 8 * g + 4);
+        a2 = ld4(src + 32 + 8 * g);
+        a3 = ld4(src + 32 + 8 * g + 4);
+        if (ROPE) {
+            const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
+            rope4(a0, a2, ld4(RC + row + 8 * g), ld4(RS + row + 8 * g));
+            rope4(a1, a3, ld4(RC + row + 8 * g + 4), ld4(RS + row + 8 * g + 4));
+        }
+        a0 *= p.scale;
+        a1 *= p.scale;
+        a2 *= p.scale;
+        a3 *= p.scale;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        w.q[t] = a0[t];
+        w.q[4 + t] = a1[t];
+        w.q[8 + t] = a2[t];
+        w.q[12 + t] = a3[t];
+    }
+#pragma unroll
+    for (int db = 0; db < 4; db++) w.o[db] = f32x4{0, 0, 0, 0};
+    w.m = w.ml = kNegInf;
+    w.l = 0.f;
+}
+
+// One tile of NKB 16-key blocks for one 16-query block. kt: K rows [key][KPAD] of the tile, vt: its
+// V key quads, kat: its key terms, lut: the T5 table (j - i + n_q - 1). PLAIN: every key of the tile
+// is below n_k and valid, every query past it for the causal masks, so the body has no bounds tests
+// and no mask arithmetic; otherwise only the first nkb key blocks are computed and every score goes
+// through the mask rule. hook(phase, kb) runs at fixed points (S block kb, after S, PV block kb)
+// whether or not the block is computed: the streaming kernel stages the next tile there.
+template <int MASK, int BIAS, bool PLAIN, int NKB, class Hook>
+__device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const float* kt, const float* vt,
+                                            const float* kat, const float* lut, int kbase, int nkb, int qi, int h,
+                                            int ql, int g, int voff_even, int voff_odd, Hook&& hook) {
+    // Lane indices pass through an opaque copy: with both tile variants in one loop the optimiser
+    // otherwise hoists every address and key index either variant derives from them out of the
+    // loop, and the union of those live ranges spills.
+    asm volatile("" : "+v"(g), "+v"(ql), "+v"(qi), "+v"(voff_even), "+v"(voff_odd));
+
+    // ---- S^T = K . Q^T: four accumulation chains per 16-key block, summed as a tree ----
+    f32x4 sacc[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        sacc[kb] = f32x4{0, 0, 0, 0};
+        hook(0, kb);
+        if (!PLAIN && kb >= nkb) continue;
+        const float* kr = kt + (kb * 16 + ql) * KPAD;
+        f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {  // dims 8g.. then 32+8g..: eight K values live at a time
+            const f32x4 ka = ld4(kr + 32 * hh + 8 * g), kb4 = ld4(kr + 32 * hh + 8 * g + 4);
+            const float* qh = w.q + 8 * hh;
+            c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[0], qh[0], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[1], qh[1], c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[2], qh[2], c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[3], qh[3], c3, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[0], qh[4], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[1], qh[5], c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[2], qh[6], c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[3], qh[7], c3, 0, 0, 0);
+        }
+        sacc[kb] = (c0 + c1) + (c2 + c3);
+        // Materialise the sum here: left alone, the optimiser sinks it to the softmax and keeps the
+        // chain accumulators of the whole tile live.
+        asm volatile("" : "+v"(sacc[kb]));
+    }
+    hook(1, 0);
+
+    // ---- bias, mask, online softmax (the scale is already in q) ----
+    {
+        // No contraction in this block: ml below must be rounded once and the same value used in the
+        // weights and in the rescale (a fused ml_run - m * log2e would mix a rounded and an unrounded
+        // maximum: ~1e-6 relative error per rescale, visible at unscaled logits).
+#pragma clang fp contract(off)
+        const int qpos = p.q_pos0 + qi;
+        float mloc = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const bool on = PLAIN || kb < nkb;
+            f32x4 ka = {0, 0, 0, 0};
+            if (!PLAIN && on) ka = ld4(kat + kb * 16 + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = kbase + kb * 16 + 4 * g + r;
+                float x = kNegInf;
+                if (on) {
+                    x = sacc[kb][r];
+                    if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), p.n_q + p.n_k - 2)];
+                    if (BIAS == BIAS_DENSE && (PLAIN || (key < p.n_k && qi < p.n_q)))
+                        x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
+                    if (!PLAIN) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
+                }
+                sacc[kb][r] = x;
+                mloc = fmaxf(mloc, x);
+            }
+        }
+        const float m_new = fmaxf(w.m, max4(mloc));
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        // e = exp2(x log2e - m log2e): one FMA per score, with ml = m log2e rounded once and used
+        // again by the rescale exp2(ml_old - ml). A row whose max is still an additively masked
+        // score (about -FLT_MAX: only invalid keys so far) takes exp2((x - m) log2e) instead, which
+        // keeps x - m exact and gives such a row the reference's uniform weights
+        // (src/core/nn.zig:470-505 on scores + (-floatMax)).
+        const bool big = m_use < -1e30f;
+        const float shift = big ? m_use : 0.f;
+        const float ml = big ? 0.f : m_use * kLog2e;
+        const float alpha = __builtin_amdgcn_exp2f(big ? (w.m - m_use) * kLog2e : w.ml - ml);
+        float lsum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r] - shift, kLog2e, -ml));
+                sacc[kb][r] = e;
+                lsum += e;
+            }
+        w.ml = (big || m_new == kNegInf) ? kNegInf : ml;
+        w.l = w.l * alpha + lsum;
+        w.m = m_new;
+        // Rescale O only when some lane's running max moved (alpha == 1 exactly otherwise).
+        if (__ballot(alpha != 1.f) != 0) {
+#pragma unroll
+            for (int db = 0; db < 4; db++) w.o[db] *= alpha;
+        }
+    }
+
+    // ---- O^T += V^T . P^T, P straight from the S^T accumulator ----
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        hook(2, kb);
+        if (!PLAIN && kb >= nkb) continue;
+        const float* vq4 = vt + (kb * 4 + g) * (kHeadDim * 4);
+#pragma unroll
+        for (int dp = 0; dp < 4; dp += 2) {  // two dim blocks at a time: eight V values live
+            const f32x4 va0 = ld4(vq4 + dp * 64 + voff_even), va1 = ld4(vq4 + dp * 64 + voff_odd);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                w.o[dp] = __builtin_amdgcn_mfma_f32_16x16x4f32(va0[r], sacc[kb][r], w.o[dp], 0, 0, 0);
+                w.o[dp + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va1[r], sacc[kb][r], w.o[dp + 1], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// Normalise and store query qi: lane holds dims 16db + 4g + r.
+__device__ __forceinline__ void store_o(const QBlock& w, float* O, const Params& p, int qi, int g) {
+    const float l = sum4(w.l);
+    if (qi >= p.n_q) return;
+    const float inv = 1.0f / l;
+    float* dst = O + (int64_t)qi * p.o_tok;
+#pragma unroll
+    for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, w.o[db] * inv);
+}
+
+// ---- streaming kernel: K/V tiles through two LDS stages ----------------------------------------
+
 template <int MASK, int BIAS, bool ROPE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_fwd_f32(Params p) {
     __shared__ __attribute__((aligned(16))) Stage stage[2];
@@ -88,6 +268,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * QT;
     const int wq0 = q0 + wave * QW;
+    const int qi = wq0 + ql;
 
     const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.q_batch + h * kHeadDim;
     const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.k_batch + h * kHeadDim;
@@ -106,17 +287,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
 
     // key_valid of this row through a buffer descriptor sized to the bytes the mask reads: a read
     // past them returns 0 (= invalid), so the load needs neither a bounds test nor a branch.
-    const __amdgpu_buffer_rsrc_t kv_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid), (short)0,
-        mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0, kBufferConfig);
-
-    // Q^T operand: qreg[s], step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8) of query wq0 + ql,
-    // rotated and scaled in the prologue.
-    float qreg[16];
-    float m_run = kNegInf;   // running max of the scores
-    float ml_run = kNegInf;  // the same in exp2 units, as used by the weights
-    float l_run = 0.f;
-    f32x4 oacc[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+    const __amdgpu_buffer_rsrc_t kv_rsrc = make_buf(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid,
+                                                    mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0);
 
     // ---- tile staging: HBM -> registers -> LDS, one 16-key quarter at a time (6 registers) ----
     // K: thread -> key row tid/32 of the quarter, dims c and c+32 with c = tid%32 (a RoPE pair).
@@ -168,239 +340,99 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
     // Additive mask term of key tbase + lane, and the tile's mask-free test (every term 0).
     auto kterm = [&](int tbase, uint32_t kvb) { return key_term<MASK>(tbase + lane, p.n_k, kvb != 0, p.ctx_keys); };
     auto all_valid = [&](int tbase, uint32_t kvb) { return __ballot(kterm(tbase, kvb) != 0.f) == 0; };
-    uint32_t kvb_next;  // key_valid bytes of the tile being staged
 
-    // V operand offsets of this lane (floats, within a key quad): dim db*16 + ql, swizzled.
-    const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // db even / odd
-
-    // One 64-key tile on stage `st`. PLAIN: every key of the tile is below n_k and valid, every
-    // query of the wave below n_q and, for the causal masks, past the tile, so the body has no
-    // bounds tests and no mask arithmetic; otherwise only the first nkb key blocks are computed
-    // (uniform) and every score goes through the mask rule.
-    auto tile = [&](const Stage& st, int kbase, int nkb, auto plain_tag, int t) {
-        constexpr bool PLAIN = decltype(plain_tag)::value;
-        const bool more = t + 1 < ntiles;
-        Stage& nxt = stage[(t + 1) & 1];
-        const int nbase = kbase + NK;
-        Quarter sq;  // the next tile's quarters pass through here, one per quarter of this tile's work
-        if (more) {
-            fetch(nbase, sq);
-            kvb_next = fetch_valid(nbase);
-        }
-
-        // ---- S^T = K . Q^T, four accumulation chains per 16-key block ----
-        f32x4 sacc[4];
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            sacc[kb] = f32x4{0, 0, 0, 0};
-            if (more && (kb == 1 || kb == 3)) {  // next tile: quarter kb/2 to LDS, fetch the next one
-                store(nxt, kb >> 1, sq);
-                fetch(nbase + 16 * (kb / 2 + 1), sq);
-            }
-            if (!PLAIN && kb >= nkb) continue;
-            const float* kr = st.k + (kb * 16 + ql) * KPAD;
-            f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {  // dims 8g.. then 32+8g..: eight K values live at a time
-                const f32x4 ka = ld4(kr + 32 * hh + 8 * g), kb4 = ld4(kr + 32 * hh + 8 * g + 4);
-                const float* qh = qreg + 8 * hh;
-                c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[0], qh[0], c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[1], qh[1], c1, 0, 0, 0);
-                c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[2], qh[2], c2, 0, 0, 0);
-                c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[3], qh[3], c3, 0, 0, 0);
-                c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[0], qh[4], c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[1], qh[5], c1, 0, 0, 0);
-                c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[2], qh[6], c2, 0, 0, 0);
-                c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[3], qh[7], c3, 0, 0, 0);
-            }
-            sacc[kb] = (c0 + c1) + (c2 + c3);
-            // Materialise the sum here: left alone, the optimiser sinks it to the softmax and keeps
-            // the chain accumulators of the whole tile live.
-            asm volatile("" : "+v"(sacc[kb]));
-        }
-        if (more) nxt.kadd[lane] = kterm(nbase, kvb_next);  // every wave writes the same 64 terms
-
-        // ---- bias, mask, online softmax (the scale is already in q) ----
-        {
-            // No contraction in this block: ml below must be rounded once and the same value used in
-            // the weights and in the rescale (a fused ml_run - m * log2e would mix a rounded and an
-            // unrounded maximum: ~1e-6 relative error per rescale, visible at unscaled logits).
-#pragma clang fp contract(off)
-            const int qi = wq0 + ql;
-            const int qpos = p.q_pos0 + qi;
-            float mloc = kNegInf;
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                const bool on = PLAIN || kb < nkb;
-                f32x4 ka = {0, 0, 0, 0};
-                if (!PLAIN && on) ka = ld4(st.kadd + kb * 16 + 4 * g);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = kbase + kb * 16 + 4 * g + r;
-                    float x = kNegInf;
-                    if (on) {
-                        x = sacc[kb][r];
-                        if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), kRelMax - 1)];
-                        if (BIAS == BIAS_DENSE && (PLAIN || (key < p.n_k && qi < p.n_q)))
-                            x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
-                        if (!PLAIN) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
-                    }
-                    sacc[kb][r] = x;
-                    mloc = fmaxf(mloc, x);
-                }
-            }
-            const float m_new = fmaxf(m_run, max4(mloc));
-            const float m_use = m_new == kNegInf ? 0.f : m_new;
-            // e = exp2(x log2e - m log2e): one FMA per score. The running max is kept in exp2 units
-            // (ml_run), so the rescale uses the same rounded values as the weights. A row whose max
-            // is still an additively masked score (about -FLT_MAX: only invalid keys so far) takes
-            // exp2((x - m) log2e) instead, which keeps x - m exact and gives such a row the
-            // reference's uniform weights (src/core/nn.zig:470-505 on scores + (-floatMax)).
-            const bool big = m_use < -1e30f;
-            const float shift = big ? m_use : 0.f;
-            const float ml = big ? 0.f : m_use * kLog2e;
-            const float alpha = __builtin_amdgcn_exp2f(big ? (m_run - m_use) * kLog2e : ml_run - ml);
-            float lsum = 0.f;
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r] - shift, kLog2e, -ml));
-                    sacc[kb][r] = e;
-                    lsum += e;
-                }
-            ml_run = (big || m_new == kNegInf) ? kNegInf : ml;
-            l_run = l_run * alpha + lsum;
-            m_run = m_new;
-            // Rescale O only when some lane's running max moved (alpha == 1 exactly otherwise).
-            if (__ballot(alpha != 1.f) != 0) {
-#pragma unroll
-                for (int db = 0; db < 4; db++) oacc[db] *= alpha;
-            }
-        }
-
-        // ---- O^T += V^T . P^T ----
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            if (more && kb == 2) {
-                store(nxt, 2, sq);
-                fetch(nbase + 48, sq);
-            }
-            if (!PLAIN && kb >= nkb) continue;
-            const float* vq4 = st.v + (kb * 4 + g) * (kHeadDim * 4);
-#pragma unroll
-            for (int dp = 0; dp < 4; dp += 2) {  // two dim blocks at a time: eight V values live
-                const f32x4 va0 = ld4(vq4 + dp * 64 + voff_even), va1 = ld4(vq4 + dp * 64 + voff_odd);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    oacc[dp] = __builtin_amdgcn_mfma_f32_16x16x4f32(va0[r], sacc[kb][r], oacc[dp], 0, 0, 0);
-                    oacc[dp + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va1[r], sacc[kb][r], oacc[dp + 1], 0, 0, 0);
-                }
-            }
-        }
-        if (more) store(nxt, 3, sq);
-    };
-
-    // Prologue: tile 0's two halves, q and the T5 table are all requested before anything waits,
-    // so a short row pays about one memory latency here, not several.
-    kvb_next = fetch_valid(0);
-    Quarter s0, s1, s2, s3;
-    fetch(0, s0);
-    fetch(16, s1);
-    fetch(32, s2);
-    fetch(48, s3);
+    // Prologue: tile 0's four quarters, q and the T5 table are all requested before anything waits.
+    uint32_t kvb_next = fetch_valid(0);  // key_valid bytes of the tile being staged
     {
-        const int qi = wq0 + ql;
-        f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
-        if (qi < p.n_q) {
-            const float* src = Q + (int64_t)qi * p.q_tok;
-            a0 = ld4(src + 8 * g);
-            a1 = ld4(src + 8 * g + 4);
-            a2 = ld4(src + 32 + 8 * g);
-            a3 = ld4(src + 32 + 8 * g + 4);
-            if (ROPE) {
-                const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
-                rope4(a0, a2, ld4(RC + row + 8 * g), ld4(RS + row + 8 * g));
-                rope4(a1, a3, ld4(RC + row + 8 * g + 4), ld4(RS + row + 8 * g + 4));
-            }
-            // The score scale goes into q: scores = (scale q) . k. For the power-of-two scales every
-            // family uses (1, 1/8) this equals the reference's alpha * (q . k) bit for bit (scaling
-            // by 2^n commutes with every rounding of the dot product).
-            a0 *= p.scale;
-            a1 *= p.scale;
-            a2 *= p.scale;
-            a3 *= p.scale;
-        }
+        Quarter s0, s1, s2, s3;
+        fetch(0, s0);
+        fetch(16, s1);
+        fetch(32, s2);
+        fetch(48, s3);
+        QBlock w;
+        load_q<ROPE>(w, Q, RC, RS, p, qi, g);
+        if (BIAS == BIAS_REL) {  // lut[j - i + n_q - 1] for this head, two entries per thread per round
+            const int n_rel = p.n_q + p.n_k - 1;
+            for (int t0 = 0; t0 < n_rel; t0 += 2 * NT) {
+                int bk[2];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            qreg[t] = a0[t];
-            qreg[4 + t] = a1[t];
-            qreg[8 + t] = a2[t];
-            qreg[12 + t] = a3[t];
-        }
-    }
-    if (BIAS == BIAS_REL) {  // lut[j - i + n_q - 1] for this head, two entries per thread per round
-        const int n_rel = p.n_q + p.n_k - 1;
-        for (int t0 = 0; t0 < n_rel; t0 += 2 * NT) {
-            int bk[2];
+                for (int u = 0; u < 2; u++) {
+                    const int t = t0 + u * NT + tid;
+                    bk[u] = t < n_rel ? min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) : 0;
+                }
+                float val[2];
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int t = t0 + u * NT + tid;
-                bk[u] = t < n_rel ? min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) : 0;
-            }
-            float val[2];
+                for (int u = 0; u < 2; u++) val[u] = p.rel_table[bk[u] * p.H + h];
 #pragma unroll
-            for (int u = 0; u < 2; u++) val[u] = p.rel_table[bk[u] * p.H + h];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int t = t0 + u * NT + tid;
-                if (t < n_rel) lut[t] = val[u];
+                for (int u = 0; u < 2; u++) {
+                    const int t = t0 + u * NT + tid;
+                    if (t < n_rel) lut[t] = val[u];
+                }
             }
         }
-    }
-    store(stage[0], 0, s0);
-    store(stage[0], 1, s1);
-    store(stage[0], 2, s2);
-    store(stage[0], 3, s3);
-    stage[0].kadd[lane] = kterm(0, kvb_next);
-    bool next_all_valid = all_valid(0, kvb_next);  // of the tile about to be computed
-    __syncthreads();
-    for (int t = 0; t < ntiles; t++) {
-        const int kbase = t * NK;
-        const Stage& st = stage[t & 1];
-        const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
-        // Mask-free tile: all 64 keys below wave_kend (<= n_k) and valid, all 16 queries below n_q
-        // and, for the causal masks, at or past the tile's last key.
-        bool plain = kbase + NK <= wave_kend && wave_nq == QW && MASK != DECODER && next_all_valid;
-        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
-        if (plain) {
-            tile(st, kbase, 4, std::integral_constant<bool, true>{}, t);
-        } else if (nkb > 0) {
-            tile(st, kbase, nkb, std::integral_constant<bool, false>{}, t);
-        } else if (t + 1 < ntiles) {
-            Stage& nxt = stage[(t + 1) & 1];
-            kvb_next = fetch_valid(kbase + NK);
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                Quarter sq;
-                fetch(kbase + NK + 16 * qq, sq);
-                store(nxt, qq, sq);
-            }
-            nxt.kadd[lane] = kterm(kbase + NK, kvb_next);
-        }
-        // The next tile's flag, from its key_valid bytes fetched at the start of this one.
-        if (t + 1 < ntiles) next_all_valid = all_valid(kbase + NK, kvb_next);
+        store(stage[0], 0, s0);
+        store(stage[0], 1, s1);
+        store(stage[0], 2, s2);
+        store(stage[0], 3, s3);
+        stage[0].kadd[lane] = kterm(0, kvb_next);  // every wave writes the same 64 terms
+        bool next_all_valid = all_valid(0, kvb_next);  // of the tile about to be computed
         __syncthreads();
-    }
 
-    // ---- normalise and store: lane holds query ql, dims 16db + 4g + r ----
-    const int qi = wq0 + ql;
-    const float l = sum4(l_run);
-    if (qi < p.n_q) {
-        const float inv = 1.0f / l;
-        float* dst = O + (int64_t)qi * p.o_tok;
+        const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // V operands, db even / odd
+        for (int t = 0; t < ntiles; t++) {
+            const int kbase = t * NK;
+            const Stage& st = stage[t & 1];
+            Stage& nxt = stage[(t + 1) & 1];
+            const int nbase = kbase + NK;
+            const bool more = t + 1 < ntiles;
+            // The next tile passes through one quarter register set, a quarter per quarter of this
+            // tile's work: fetched at S blocks 0, 1, 3 and PV block 2, stored one step later.
+            Quarter sq;
+            auto stage_next = [&](int phase, int kb) {
+                if (!more) return;
+                if (phase == 0 && kb == 0) {
+                    fetch(nbase, sq);
+                    kvb_next = fetch_valid(nbase);
+                }
+                if (phase == 0 && (kb == 1 || kb == 3)) {
+                    store(nxt, kb >> 1, sq);
+                    fetch(nbase + 16 * (kb / 2 + 1), sq);
+                }
+                if (phase == 1) nxt.kadd[lane] = kterm(nbase, kvb_next);
+                if (phase == 2 && kb == 2) {
+                    store(nxt, 2, sq);
+                    fetch(nbase + 48, sq);
+                }
+            };
+            const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
+            // Mask-free tile: all 64 keys below wave_kend (<= n_k) and valid and, for the causal
+            // masks, every query at or past the tile's last key. Query slots past n_q hold q = 0 and
+            // are never stored, so they may run mask-free too, except with a dense bias (no bias
+            // row to read).
+            bool plain = kbase + NK <= wave_kend && (wave_nq == QW || BIAS != BIAS_DENSE) && MASK != DECODER &&
+                         next_all_valid;
+            if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
+            if (plain) {
+                attend_tile<MASK, BIAS, true, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g, voff_even,
+                                                 voff_odd, stage_next);
+            } else if (nkb > 0) {
+                attend_tile<MASK, BIAS, false, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g, voff_even,
+                                                  voff_odd, stage_next);
+            } else if (more) {
+                kvb_next = fetch_valid(nbase);
 #pragma unroll
-        for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, oacc[db] * inv);
+                for (int qq = 0; qq < 4; qq++) {
+                    fetch(nbase + 16 * qq, sq);
+                    store(nxt, qq, sq);
+                }
+                nxt.kadd[lane] = kterm(nbase, kvb_next);
+            }
+            if (more && (plain || nkb > 0)) store(nxt, 3, sq);
+            // The next tile's flag, from its key_valid bytes fetched at the start of this one.
+            if (more) next_all_valid = all_valid(nbase, kvb_next);
+            __syncthreads();
+        }
+        store_o(w, O, p, qi, g);
     }
 }
 
@@ -409,17 +441,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
 // Chronos-Bolt rows are short (at most 128 patches + REG = 129 tokens). Streamed through the
 // two-stage pipeline above they pay a staging round and a barrier for each of three tiles, and
 // 128-query workgroups leave a one-query tail workgroup (129 = 128 + 1) that stages all of K/V
-// again. Here one workgroup of 3 waves x 3 query blocks (144 queries) loads the whole K, V, key
-// terms and T5 table of its (series, head) into LDS once, then runs the same per-tile arithmetic
-// (four-chain scores, online softmax, P kept in registers) without any further barrier.
+// again. Here one workgroup of 9 waves (one 16-query block each, 144 queries) loads the whole K, V,
+// key terms and T5 table of its (series, head) into LDS once; then every wave runs the per-tile
+// arithmetic above over the resident keys with no further barrier. At 96 VGPRs two workgroups
+// (18 waves) share a CU.
 
-constexpr int RQB = 3;                  // query blocks of 16 per wave
-constexpr int RNW = 3;                  // waves per workgroup
+constexpr int RNW = 9;                  // waves per workgroup
 constexpr int RNT = 64 * RNW;           // threads
-constexpr int RQT = 16 * RQB * RNW;     // queries per workgroup (144)
+constexpr int RQT = 16 * RNW;           // queries per workgroup (144)
 constexpr int kResidentKeys = 144;      // longest row the resident kernel takes
-constexpr int RKIT = (kResidentKeys * 8 + RNT - 1) / RNT;  // K staging items per thread
-constexpr int RVIT = (kResidentKeys * 8 + RNT - 1) / RNT;  // V staging items per thread
+constexpr int RNK = 32;                 // keys per tile of the resident loop
+constexpr int RKIT = (kResidentKeys * 8 + RNT - 1) / RNT;   // K staging items per thread
+constexpr int RVIT = (kResidentKeys * 8 + RNT - 1) / RNT;   // V staging items per thread
 
 // Dynamic LDS layout, in floats: K [nkp][KPAD] | V [nkp/4 quads][64 swizzled][4] | key terms [nkp] |
 // T5 table [n_q + n_k - 1], with nkp = n_k rounded up to 16 keys.
@@ -437,7 +470,7 @@ __host__ __device__ inline ResidentLayout resident_layout(int n_q, int n_k, bool
 }
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_f32_resident(Params p) {
+__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(5, 5))) void attn_fwd_f32_resident(Params p) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     const ResidentLayout lay = resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL);
     float* const Ks = smem;
@@ -451,101 +484,79 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = logical / q_tiles, qt = logical % q_tiles;
     const int b = bh / p.H, h = bh % p.H;
-    const int wq0 = qt * RQT + wave * 16 * RQB;  // first query of this wave
+    const int wq0 = qt * RQT + wave * 16;  // first query of this wave
+    const int qi = wq0 + ql;
 
     const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.q_batch + h * kHeadDim;
     const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.k_batch + h * kHeadDim;
     const float* __restrict__ V = static_cast<const float*>(p.v) + b * p.v_batch + h * kHeadDim;
     float* __restrict__ O = static_cast<float*>(p.o) + b * p.o_batch + h * kHeadDim;
-    const uint8_t* __restrict__ KV = mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : nullptr;
     const int rope_tab = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
     const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
     const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
-    const int kv_len = valid_len<MASK>(p.n_k, p.ctx_keys);
-    const int last = p.n_k - 1;
+    // Buffer descriptors ending after key n_k - 1: padding rows up to nkp read as zeros.
+    const __amdgpu_buffer_rsrc_t k_buf = make_buf(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 4));
+    const __amdgpu_buffer_rsrc_t v_buf = make_buf(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 4));
+    const __amdgpu_buffer_rsrc_t c_buf = make_buf(RC, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+    const __amdgpu_buffer_rsrc_t s_buf = make_buf(RS, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+    const __amdgpu_buffer_rsrc_t kv_rsrc = make_buf(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid,
+                                                    mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0);
 
-    // ---- stage K, V, key terms, T5 table and q: every load is issued before the first wait ----
-    f32x4 klo[RKIT], khi[RKIT], kcs[RKIT], ksn[RKIT];
+    // ---- stage K (rotated), V, key terms, T5 table and q: every load issued before the first wait
+    //      (with RoPE, K and its tables go first and are stored before V is requested: holding all
+    //      of them at once would not fit 96 registers) ----
+    f32x4 klo[RKIT], khi[RKIT];
+    auto store_k = [&]() {
+#pragma unroll
+        for (int u = 0; u < RKIT; u++) {
+            const int it = tid + u * RNT, row = it >> 3, c = it & 7;
+            if (row >= lay.nkp) continue;
+            st4(Ks + row * KPAD + 4 * c, klo[u]);
+            st4(Ks + row * KPAD + 32 + 4 * c, khi[u]);
+        }
+    };
 #pragma unroll
     for (int u = 0; u < RKIT; u++) {  // K item = (row, c): dims 4c..4c+3 and 32+4c..32+4c+3
-        const int it = tid + u * RNT, row = it >> 3, c = it & 7, rc = min(row, last);
-        const float* src = K + (int64_t)rc * p.k_tok + 4 * c;
-        klo[u] = ld4(src);
-        khi[u] = ld4(src + 32);
-        if (ROPE) {
-            kcs[u] = ld4(RC + (int64_t)rc * 32 + 4 * c);
-            ksn[u] = ld4(RS + (int64_t)rc * 32 + 4 * c);
+        const int it = tid + u * RNT, row = it >> 3, c = it & 7;
+        const uint32_t off = (uint32_t)(row * p.k_tok + 4 * c) * 4u;
+        klo[u] = bld4(k_buf, off);
+        khi[u] = bld4(k_buf, off + 128u);
+    }
+    if (ROPE) {
+        f32x4 kcs[RKIT], ksn[RKIT];
+#pragma unroll
+        for (int u = 0; u < RKIT; u++) {
+            const int it = tid + u * RNT, row = it >> 3, c = it & 7;
+            const uint32_t coff = (uint32_t)(row * 32 + 4 * c) * 4u;
+            kcs[u] = bld4(c_buf, coff);
+            ksn[u] = bld4(s_buf, coff);
         }
+#pragma unroll
+        for (int u = 0; u < RKIT; u++) rope4(klo[u], khi[u], kcs[u], ksn[u]);
+        store_k();
     }
     f32x4 v01[RVIT], v23[RVIT];
 #pragma unroll
     for (int u = 0; u < RVIT; u++) {  // V item = (quad of 4 rows, dims 2vc, 2vc+1)
-        const int it = tid + u * RNT, quad = it >> 5, vc = it & 31, r0 = 4 * quad;
-        const float* src = V + 2 * vc;
-        const f32x2 a = ld2(src + (int64_t)min(r0, last) * p.v_tok);
-        const f32x2 bb = ld2(src + (int64_t)min(r0 + 1, last) * p.v_tok);
-        const f32x2 c = ld2(src + (int64_t)min(r0 + 2, last) * p.v_tok);
-        const f32x2 d = ld2(src + (int64_t)min(r0 + 3, last) * p.v_tok);
-        v01[u] = f32x4{r0 <= last ? a[0] : 0.f, r0 <= last ? a[1] : 0.f, r0 + 1 <= last ? bb[0] : 0.f,
-                       r0 + 1 <= last ? bb[1] : 0.f};
-        v23[u] = f32x4{r0 + 2 <= last ? c[0] : 0.f, r0 + 2 <= last ? c[1] : 0.f, r0 + 3 <= last ? d[0] : 0.f,
-                       r0 + 3 <= last ? d[1] : 0.f};
+        const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
+        const uint32_t off = (uint32_t)(4 * quad * p.v_tok + 2 * vc) * 4u, step = (uint32_t)p.v_tok * 4u;
+        const f32x2 a = bld2(v_buf, off), bb = bld2(v_buf, off + step);
+        const f32x2 c = bld2(v_buf, off + 2 * step), d = bld2(v_buf, off + 3 * step);
+        v01[u] = f32x4{a[0], a[1], bb[0], bb[1]};
+        v23[u] = f32x4{c[0], c[1], d[0], d[1]};
     }
     float kterm = 0.f;
     if (tid < lay.nkp) {
-        bool valid = true;
-        if (mask_reads_valid<MASK>()) valid = tid < kv_len && KV[tid] != 0;
-        kterm = key_term<MASK>(tid, p.n_k, valid, p.ctx_keys);
+        const uint32_t kvb = mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, tid, 0, 0) : 1u;
+        kterm = key_term<MASK>(tid, p.n_k, kvb != 0, p.ctx_keys);
     }
-    float qreg[RQB][16];
-#pragma unroll
-    for (int qb = 0; qb < RQB; qb++) {
-        const int qi = wq0 + 16 * qb + ql;
-        f32x4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
-        if (qi < p.n_q) {
-            const float* src = Q + (int64_t)qi * p.q_tok;
-            a0 = ld4(src + 8 * g);
-            a1 = ld4(src + 8 * g + 4);
-            a2 = ld4(src + 32 + 8 * g);
-            a3 = ld4(src + 32 + 8 * g + 4);
-            if (ROPE) {
-                const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
-                rope4(a0, a2, ld4(RC + row + 8 * g), ld4(RS + row + 8 * g));
-                rope4(a1, a3, ld4(RC + row + 8 * g + 4), ld4(RS + row + 8 * g + 4));
-            }
-            a0 *= p.scale;  // power-of-two scales: exact, as in the streaming kernel
-            a1 *= p.scale;
-            a2 *= p.scale;
-            a3 *= p.scale;
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            qreg[qb][t] = a0[t];
-            qreg[qb][4 + t] = a1[t];
-            qreg[qb][8 + t] = a2[t];
-            qreg[qb][12 + t] = a3[t];
-        }
-    }
+    QBlock w;
+    load_q<ROPE>(w, Q, RC, RS, p, qi, g);
     if (BIAS == BIAS_REL) {
         const int n_rel = p.n_q + p.n_k - 1;
-        for (int t0 = 0; t0 < n_rel; t0 += 2 * RNT) {
-            const int t1 = t0 + tid, t2 = t1 + RNT;
-            const int b1 = t1 < n_rel ? min(max(p.rel_bucket[t1], 0), p.rel_buckets - 1) : 0;
-            const int b2 = t2 < n_rel ? min(max(p.rel_bucket[t2], 0), p.rel_buckets - 1) : 0;
-            const float x1 = p.rel_table[b1 * p.H + h], x2 = p.rel_table[b2 * p.H + h];
-            if (t1 < n_rel) lut[t1] = x1;
-            if (t2 < n_rel) lut[t2] = x2;
-        }
+        for (int t = tid; t < n_rel; t += RNT) lut[t] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
     }
-#pragma unroll
-    for (int u = 0; u < RKIT; u++) {
-        const int it = tid + u * RNT, row = it >> 3, c = it & 7;
-        if (row >= lay.nkp) continue;
-        f32x4 lo = row <= last ? klo[u] : f32x4{0, 0, 0, 0}, hi = row <= last ? khi[u] : f32x4{0, 0, 0, 0};
-        if (ROPE) rope4(lo, hi, kcs[u], ksn[u]);
-        st4(Ks + row * KPAD + 4 * c, lo);
-        st4(Ks + row * KPAD + 32 + 4 * c, hi);
-    }
+    if (!ROPE) store_k();
 #pragma unroll
     for (int u = 0; u < RVIT; u++) {
         const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
@@ -557,149 +568,29 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (tid < lay.nkp) kadd[tid] = kterm;
     __syncthreads();  // the only barrier: everything below reads LDS that no one writes again
 
-    const int wave_nq = max(0, min(16 * RQB, p.n_q - wq0));
+    const int wave_nq = max(0, min(16, p.n_q - wq0));
     if (wave_nq == 0) return;
-    const int nqb = (wave_nq + 15) >> 4;
     const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
     const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;
-
-    float m_run[RQB], ml_run[RQB], l_run[RQB];
-    f32x4 oacc[4][RQB];
-#pragma unroll
-    for (int qb = 0; qb < RQB; qb++) {
-        m_run[qb] = ml_run[qb] = kNegInf;
-        l_run[qb] = 0.f;
-#pragma unroll
-        for (int db = 0; db < 4; db++) oacc[db][qb] = f32x4{0, 0, 0, 0};
+    auto no_hook = [](int, int) {};
+    // 32-key tiles (two key blocks): half the score registers of a 64-key tile, which keeps the
+    // wave within 96 VGPRs (five waves per SIMD) at the price of one more max/rescale per 64 keys.
+    for (int kbase = 0; kbase < wave_kend; kbase += RNK) {
+        const int nkb = min(2, (wave_kend - kbase + 15) >> 4);
+        // Query slots past n_q (q = 0, never stored) may run mask-free, except with a dense bias.
+        bool plain = kbase + RNK <= wave_kend && (wave_nq == 16 || BIAS != BIAS_DENSE) && MASK != DECODER;
+        if (plain && mask_reads_valid<MASK>()) plain = __ballot(lane < RNK && kadd[kbase + (lane & (RNK - 1))] != 0.f) == 0;
+        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + RNK - 1 <= p.q_pos0 + wq0;
+        const float* kt = Ks + kbase * KPAD;
+        const float* vt = Vs + (kbase >> 2) * (kHeadDim * 4);
+        if (plain)
+            attend_tile<MASK, BIAS, true, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g, voff_even,
+                                             voff_odd, no_hook);
+        else
+            attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g, voff_even,
+                                              voff_odd, no_hook);
     }
-
-    auto tile = [&](int kbase, int nkb, auto plain_tag) {
-        constexpr bool PLAIN = decltype(plain_tag)::value;
-        f32x4 sacc[4][RQB];
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-#pragma unroll
-            for (int qb = 0; qb < RQB; qb++) sacc[kb][qb] = f32x4{0, 0, 0, 0};
-            if (!PLAIN && kb >= nkb) continue;
-            const float* kr = Ks + (kbase + kb * 16 + ql) * KPAD;
-            const f32x4 k0 = ld4(kr + 8 * g), k1 = ld4(kr + 8 * g + 4);
-            const f32x4 k2 = ld4(kr + 32 + 8 * g), k3 = ld4(kr + 32 + 8 * g + 4);
-            const float kv16[16] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3],
-                                    k2[0], k2[1], k2[2], k2[3], k3[0], k3[1], k3[2], k3[3]};
-#pragma unroll
-            for (int qb = 0; qb < RQB; qb++) {
-                if (!PLAIN && qb >= nqb) continue;
-                f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
-#pragma unroll
-                for (int s = 0; s < 16; s += 4) {
-                    c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s], qreg[qb][s], c0, 0, 0, 0);
-                    c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 1], qreg[qb][s + 1], c1, 0, 0, 0);
-                    c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 2], qreg[qb][s + 2], c2, 0, 0, 0);
-                    c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv16[s + 3], qreg[qb][s + 3], c3, 0, 0, 0);
-                }
-                sacc[kb][qb] = (c0 + c1) + (c2 + c3);
-                asm volatile("" : "+v"(sacc[kb][qb]));  // keep the tree sum here (see above)
-            }
-        }
-#pragma unroll
-        for (int qb = 0; qb < RQB; qb++) {
-#pragma clang fp contract(off)
-            if (!PLAIN && qb >= nqb) continue;
-            const int qi = wq0 + 16 * qb + ql;
-            const int qpos = p.q_pos0 + qi;
-            float mloc = kNegInf;
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                const bool on = PLAIN || kb < nkb;
-                f32x4 ka = {0, 0, 0, 0};
-                if (!PLAIN && on) ka = ld4(kadd + kbase + kb * 16 + 4 * g);  // blocks past nkb: past nkp
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = kbase + kb * 16 + 4 * g + r;
-                    float x = kNegInf;
-                    if (on) {
-                        x = sacc[kb][qb][r];
-                        if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), p.n_q + p.n_k - 2)];
-                        if (BIAS == BIAS_DENSE && (PLAIN || (key < p.n_k && qi < p.n_q)))
-                            x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
-                        if (!PLAIN) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
-                    }
-                    sacc[kb][qb][r] = x;
-                    mloc = fmaxf(mloc, x);
-                }
-            }
-            const float m_new = fmaxf(m_run[qb], max4(mloc));
-            const float m_use = m_new == kNegInf ? 0.f : m_new;
-            float alpha, lsum = 0.f;
-            if (__ballot(m_use < -1e30f) == 0) {
-                const float ml = m_use * kLog2e;
-                alpha = __builtin_amdgcn_exp2f(ml_run[qb] - ml);
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], kLog2e, -ml));
-                        sacc[kb][qb][r] = e;
-                        lsum += e;
-                    }
-                ml_run[qb] = m_new == kNegInf ? kNegInf : ml;
-            } else {
-                alpha = __builtin_amdgcn_exp2f((m_run[qb] - m_use) * kLog2e);
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float e = __builtin_amdgcn_exp2f((sacc[kb][qb][r] - m_use) * kLog2e);
-                        sacc[kb][qb][r] = e;
-                        lsum += e;
-                    }
-                ml_run[qb] = m_new == kNegInf ? kNegInf : m_use * kLog2e;
-            }
-            l_run[qb] = l_run[qb] * alpha + lsum;
-            m_run[qb] = m_new;
-            if (__ballot(alpha != 1.f) != 0) {
-#pragma unroll
-                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
-            }
-        }
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            if (!PLAIN && kb >= nkb) continue;
-            const float* vq4 = Vs + ((kbase >> 2) + kb * 4 + g) * (kHeadDim * 4);
-            f32x4 va[4];
-#pragma unroll
-            for (int db = 0; db < 4; db++) va[db] = ld4(vq4 + db * 64 + ((db & 1) ? voff_odd - 64 : voff_even));
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int db = 0; db < 4; db++)
-#pragma unroll
-                    for (int qb = 0; qb < RQB; qb++) {
-                        if (!PLAIN && qb >= nqb) continue;
-                        oacc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db][r], sacc[kb][qb][r], oacc[db][qb], 0, 0, 0);
-                    }
-        }
-    };
-
-    for (int kbase = 0; kbase < wave_kend; kbase += NK) {
-        const int nkb = min(4, (wave_kend - kbase + 15) >> 4);
-        bool plain = kbase + NK <= wave_kend && wave_nq == 16 * RQB && MASK != DECODER;
-        if (plain && mask_reads_valid<MASK>()) plain = __ballot(kadd[kbase + lane] != 0.f) == 0;
-        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
-        if (plain) tile(kbase, 4, std::integral_constant<bool, true>{});
-        else tile(kbase, nkb, std::integral_constant<bool, false>{});
-    }
-
-#pragma unroll
-    for (int qb = 0; qb < RQB; qb++) {
-        const int qi = wq0 + 16 * qb + ql;
-        const float l = sum4(l_run[qb]);
-        if (qi >= p.n_q) continue;
-        const float inv = 1.0f / l;
-        float* dst = O + (int64_t)qi * p.o_tok;
-#pragma unroll
-        for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, oacc[db][qb] * inv);
-    }
+    store_o(w, O, p, qi, g);
 }
 
 template <int MASK, int BIAS, bool ROPE>

@@ -127,6 +127,9 @@ __device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 __device__ __forceinline__ f32x2 bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
+__device__ __forceinline__ f32x4 bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
 // Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48), on the VALU with
 // gfx950's lane swaps: permlane32_swap(x, x) returns (x of lanes 0-31 in both halves, x of lanes
