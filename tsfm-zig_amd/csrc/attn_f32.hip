@@ -41,6 +41,7 @@ constexpr int NWAVE = 8;
 constexpr int NT = 64 * NWAVE;  // threads per workgroup
 constexpr int QT = QW * NWAVE;  // queries per workgroup
 constexpr int KPAD = 68;        // K row pitch in LDS (floats)
+constexpr int kLutPad = 16;     // T5 table margin on each side (entries)
 
 struct Stage {
     float k[NK * KPAD];      // [key][KPAD], RoPE applied
@@ -122,7 +123,8 @@ __device__ __forceinline__ void load_q(QBlock& w, const float* Q, const float* R
 }
 
 // One tile of NKB 16-key blocks for one 16-query block. kt: K rows [key][KPAD] of the tile, vt: its
-// V key quads, kat: its key terms, lut: the T5 table (j - i + n_q - 1). PLAIN: every key of the tile
+// V key quads, kat: its key terms, lut: the T5 table (j - i + n_q - 1, readable from -kLutPad to
+// n_q + n_k - 1 + kLutPad, so that no index needs a clamp). PLAIN: every key of the tile
 // is below n_k and valid, every query past it for the causal masks, so the body has no bounds tests
 // and no mask arithmetic; otherwise only the first nkb key blocks are computed and every score goes
 // through the mask rule. hook(phase, kb) runs at fixed points (S block kb, after S, PV block kb)
@@ -184,7 +186,7 @@ __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const fl
                 float x = kNegInf;
                 if (on) {
                     x = sacc[kb][r];
-                    if (BIAS == BIAS_REL) x = x + lut[min(max(key - qi + p.n_q - 1, 0), p.n_q + p.n_k - 2)];
+                    if (BIAS == BIAS_REL) x = x + lut[key - qi + p.n_q - 1];  // margins: no clamp
                     if (BIAS == BIAS_DENSE && (PLAIN || (key < p.n_k && qi < p.n_q)))
                         x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
                     if (!PLAIN) x = masked<MASK>(x, ka[r], key, qpos, p.n_k, p.chain_start);
@@ -251,12 +253,24 @@ __device__ __forceinline__ void store_o(const QBlock& w, float* O, const Params&
     for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, w.o[db] * inv);
 }
 
+// T5 bias of head h by relative index t = j - i + n_q - 1, stored at lut_raw[kLutPad + t] for t in
+// [-kLutPad, n_q + n_k - 1 + kLutPad): the margins repeat the end values (the bucket of the nearest
+// real index), so padded keys and query slots index it without a clamp.
+__device__ __forceinline__ void fill_rel_lut(float* lut_raw, const Params& p, int h, int tid, int nthreads) {
+    const int n_rel = p.n_q + p.n_k - 1;
+    for (int u = tid; u < n_rel + 2 * kLutPad; u += nthreads) {
+        const int t = min(max(u - kLutPad, 0), n_rel - 1);
+        lut_raw[u] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
+    }
+}
+
 // ---- streaming kernel: K/V tiles through two LDS stages ----------------------------------------
 
 template <int MASK, int BIAS, bool ROPE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_fwd_f32(Params p) {
     __shared__ __attribute__((aligned(16))) Stage stage[2];
-    __shared__ float lut[BIAS == BIAS_REL ? kRelMax : 1];
+    __shared__ float lut_raw[BIAS == BIAS_REL ? kRelMax + 2 * kLutPad : 1];
+    float* const lut = lut_raw + (BIAS == BIAS_REL ? kLutPad : 0);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
@@ -351,25 +365,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
         fetch(48, s3);
         QBlock w;
         load_q<ROPE>(w, Q, RC, RS, p, qi, g);
-        if (BIAS == BIAS_REL) {  // lut[j - i + n_q - 1] for this head, two entries per thread per round
-            const int n_rel = p.n_q + p.n_k - 1;
-            for (int t0 = 0; t0 < n_rel; t0 += 2 * NT) {
-                int bk[2];
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int t = t0 + u * NT + tid;
-                    bk[u] = t < n_rel ? min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) : 0;
-                }
-                float val[2];
-#pragma unroll
-                for (int u = 0; u < 2; u++) val[u] = p.rel_table[bk[u] * p.H + h];
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int t = t0 + u * NT + tid;
-                    if (t < n_rel) lut[t] = val[u];
-                }
-            }
-        }
+        if (BIAS == BIAS_REL) fill_rel_lut(lut_raw, p, h, tid, NT);
         store(stage[0], 0, s0);
         store(stage[0], 1, s1);
         store(stage[0], 2, s2);
@@ -443,8 +439,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
 // 128-query workgroups leave a one-query tail workgroup (129 = 128 + 1) that stages all of K/V
 // again. Here one workgroup of 9 waves (one 16-query block each, 144 queries) loads the whole K, V,
 // key terms and T5 table of its (series, head) into LDS once; then every wave runs the per-tile
-// arithmetic above over the resident keys with no further barrier. At 96 VGPRs two workgroups
-// (18 waves) share a CU.
+// arithmetic above over the resident keys with no further barrier. The waves of a workgroup land
+// two or three to a SIMD, so two workgroups per CU need room for six waves per SIMD: the kernel is
+// built for 80 VGPRs (a few spill to scratch; no global load is in flight there).
 
 constexpr int RNW = 9;                  // waves per workgroup
 constexpr int RNT = 64 * RNW;           // threads
@@ -465,18 +462,18 @@ __host__ __device__ inline ResidentLayout resident_layout(int n_q, int n_k, bool
     L.v_off = L.nkp * KPAD;
     L.a_off = L.v_off + L.nkp * kHeadDim;
     L.l_off = L.a_off + L.nkp;
-    L.total = L.l_off + (rel_lut ? n_q + n_k - 1 : 0);
+    L.total = L.l_off + (rel_lut ? n_q + n_k - 1 + 2 * kLutPad : 0);
     return L;
 }
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(5, 5))) void attn_fwd_f32_resident(Params p) {
+__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) void attn_fwd_f32_resident(Params p) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     const ResidentLayout lay = resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL);
     float* const Ks = smem;
     float* const Vs = smem + lay.v_off;
     float* const kadd = smem + lay.a_off;
-    float* const lut = smem + lay.l_off;
+    float* const lut = smem + lay.l_off + kLutPad;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
@@ -504,7 +501,7 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(5, 5))) voi
 
     // ---- stage K (rotated), V, key terms, T5 table and q: every load issued before the first wait
     //      (with RoPE, K and its tables go first and are stored before V is requested: holding all
-    //      of them at once would not fit 96 registers) ----
+    //      of them at once would not fit the register budget) ----
     f32x4 klo[RKIT], khi[RKIT];
     auto store_k = [&]() {
 #pragma unroll
@@ -552,10 +549,7 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(5, 5))) voi
     }
     QBlock w;
     load_q<ROPE>(w, Q, RC, RS, p, qi, g);
-    if (BIAS == BIAS_REL) {
-        const int n_rel = p.n_q + p.n_k - 1;
-        for (int t = tid; t < n_rel; t += RNT) lut[t] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
-    }
+    if (BIAS == BIAS_REL) fill_rel_lut(lut - kLutPad, p, h, tid, RNT);
     if (!ROPE) store_k();
 #pragma unroll
     for (int u = 0; u < RVIT; u++) {
@@ -573,8 +567,8 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(5, 5))) voi
     const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
     const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;
     auto no_hook = [](int, int) {};
-    // 32-key tiles (two key blocks): half the score registers of a 64-key tile, which keeps the
-    // wave within 96 VGPRs (five waves per SIMD) at the price of one more max/rescale per 64 keys.
+    // 32-key tiles (two key blocks): half the score registers of a 64-key tile, for the 80-VGPR
+    // budget, at the price of one more max/rescale per 64 keys.
     for (int kbase = 0; kbase < wave_kend; kbase += RNK) {
         const int nkb = min(2, (wave_kend - kbase + 15) >> 4);
         // Query slots past n_q (q = 0, never stored) may run mask-free, except with a dense bias.
