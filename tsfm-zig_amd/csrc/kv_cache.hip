@@ -6,7 +6,7 @@
 // the concatenated sequence equal n queries at positions P.. attending over cached keys, which is
 // what tsfm_kv_attend computes.
 //
-// Layout (per (series, head), `cap` rounded up to 32 keys):
+// Layout (per (series, head), `cap` a multiple of 64 keys, set by tsfm_kv_create):
 //   K: [cap][64] halves, one 128-byte row per key.
 //   V: [cap/32][4][64][8] halves: 32-key chunks in the operand order of
 //      v_mfma_f32_16x16x32_{bf16,f16} (see attn_half.hip): octet g of a chunk holds keys
