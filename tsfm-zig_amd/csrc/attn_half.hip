@@ -41,6 +41,7 @@ constexpr int NWAVE = 4;
 constexpr int NT = 64 * NWAVE;
 constexpr int QT = QW * NWAVE;
 constexpr int KROW = 36;        // K row pitch in LDS, dwords (64 halves + 8 pad)
+constexpr float kStale = 8.f;   // a stale running max may trail the true one by this (exp2 units)
 
 struct StageH {
     uint32_t k[NK * KROW];           // [key][36 dwords]
@@ -189,7 +190,12 @@ attn_fwd_half(Params p) {
     }
 
     float mc_run[2] = {kNegInf, kNegInf};  // running max, in exp2 units (max * scale * log2 e)
-    float l_run[2] = {0.f, 0.f};
+    // Row sums on the matrix cores: V^T replaced by ones gives, in every register of the lane,
+    // the sum over the chunk's keys of the rounded weights of query ql (the same weights the O
+    // product uses). 16 VALU adds per tile and block become one instruction per 32-key chunk.
+    f32x4 lacc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    const u32x4 ones = BF16 ? u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u}
+                            : u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
     f32x4 oacc[4][2];
 #pragma unroll
     for (int db = 0; db < 4; db++)
@@ -327,38 +333,40 @@ attn_fwd_half(Params p) {
                     mloc = fmaxf(mloc, x);
                 }
             }
+            // A stale running max is kept until the true one exceeds it by more than kStale (exp2
+            // units): weights then stay below 2^kStale, and O and the row sum are rescaled only when
+            // some lane of the wave moves past that, rarely after the first tiles of a row.
             float mc_use, alpha;
             if (MASK == KEYS_ADDITIVE) {
                 // mc_run holds the raw-score max here: e = exp2((x - m) * c2) keeps x - m exact.
                 const float mr = fmaxf(max4(mloc), mc_run[qb]);
-                mc_use = mr == kNegInf ? 0.f : mr;
-                alpha = __builtin_amdgcn_exp2f((mc_run[qb] - mc_use) * c2);
-                mc_run[qb] = mr;
+                const bool upd = __ballot(mr > mc_run[qb] + kStale / c2) != 0;
+                const float mk = upd ? mr : mc_run[qb];
+                mc_use = mk == kNegInf ? 0.f : mk;
+                alpha = upd ? __builtin_amdgcn_exp2f((mc_run[qb] - mc_use) * c2) : 1.f;
+                mc_run[qb] = mk;
             } else {
                 // exp2 units: e = exp2(x * c2 - max * c2), one FMA per score.
                 const float mt = mloc == kNegInf ? kNegInf : mloc * c2;
                 const float mn = fmaxf(max4(mt), mc_run[qb]);
-                mc_use = mn == kNegInf ? 0.f : mn;
-                alpha = __builtin_amdgcn_exp2f(mc_run[qb] - mc_use);
-                mc_run[qb] = mn;
+                const bool upd = __ballot(mn > mc_run[qb] + kStale) != 0;
+                const float mk = upd ? mn : mc_run[qb];
+                mc_use = mk == kNegInf ? 0.f : mk;
+                alpha = upd ? __builtin_amdgcn_exp2f(mc_run[qb] - mc_use) : 1.f;
+                mc_run[qb] = mk;
             }
-            float lsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float x = sacc[kb][qb][r];
-                    const float e = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((x - mc_use) * c2)
-                                                          : __builtin_amdgcn_exp2f(__builtin_fmaf(x, c2, -mc_use));
-                    sacc[kb][qb][r] = e;
-                    lsum += e;
+                    sacc[kb][qb][r] = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((x - mc_use) * c2)
+                                                            : __builtin_amdgcn_exp2f(__builtin_fmaf(x, c2, -mc_use));
                 }
-            l_run[qb] = l_run[qb] * alpha + lsum;
-            // Rescale O only when some lane's running max moved (alpha == 1 exactly otherwise):
-            // later in a long row the max rarely changes.
             if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
                 for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+                lacc[qb] *= alpha;
             }
         }
 
@@ -382,6 +390,11 @@ attn_fwd_half(Params p) {
                     if (!PLAIN && qb >= nqb) continue;
                     oacc[db][qb] = mfma<BF16>(vf, pf[qb], oacc[db][qb]);
                 }
+            }
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                if (!PLAIN && qb >= nqb) continue;
+                lacc[qb] = mfma<BF16>(ones, pf[qb], lacc[qb]);
             }
         }
         // The next tile goes to the other stage last: its loads had the whole tile to land.
@@ -420,7 +433,7 @@ attn_fwd_half(Params p) {
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
         const int qi = wq0 + 16 * qb + ql;
-        const float l = sum4(l_run[qb]);
+        const float l = lacc[qb][0];
         if (qi >= p.n_q) continue;
         const float inv = 1.0f / l;
         E* dst = O + (int64_t)qi * p.o_tok + 4 * g;
