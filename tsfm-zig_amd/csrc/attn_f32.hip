@@ -243,6 +243,54 @@ __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const fl
     }
 }
 
+// The last few keys of a row (at most kValuKeys) on the VALU instead of a whole key block of
+// matrix instructions: per key, the lane's 16-dim partial dot product (four FMA chains and a tree),
+// summed over the query's four lanes, then the same bias, mask and online-softmax update as the
+// tile body with one score, and O += e v. Same tile operands in LDS as attend_tile.
+constexpr int kValuKeys = 4;
+template <int MASK, int BIAS, bool VROW>
+__device__ __forceinline__ void attend_keys_valu(QBlock& w, const Params& p, const float* kt, const float* vt,
+                                                 const float* kat, const float* lut, int kbase, int nkeys, int qi,
+                                                 int h, int g) {
+#pragma clang fp contract(off)
+    asm volatile("" : "+v"(g), "+v"(qi));  // as in attend_tile: no hoisting out of this variant
+    const int qpos = p.q_pos0 + qi;
+    for (int j = 0; j < nkeys; j++) {
+        const float* kr = kt + j * KPAD;
+        const f32x4 k4[4] = {ld4(kr + 8 * g), ld4(kr + 8 * g + 4), ld4(kr + 32 + 8 * g), ld4(kr + 32 + 8 * g + 4)};
+        float part[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            part[c] = w.q[4 * c] * k4[c][0];
+#pragma unroll
+            for (int i = 1; i < 4; i++) part[c] = __builtin_fmaf(w.q[4 * c + i], k4[c][i], part[c]);
+        }
+        float x = sum4((part[0] + part[1]) + (part[2] + part[3]));
+        const int key = kbase + j;
+        if (BIAS == BIAS_REL) x = x + lut[key - qi + p.n_q - 1];
+        if (BIAS == BIAS_DENSE && key < p.n_k && qi < p.n_q) x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
+        x = masked<MASK>(x, kat[j], key, qpos, p.n_k, p.chain_start);
+        const float m_new = fmaxf(w.m, x);
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        const bool big = m_use < -1e30f;
+        const float shift = big ? m_use : 0.f;
+        const float ml = big ? 0.f : m_use * kLog2e;
+        const float alpha = __builtin_amdgcn_exp2f(big ? (w.m - m_use) * kLog2e : w.ml - ml);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x - shift, kLog2e, -ml));
+        w.ml = (big || m_new == kNegInf) ? kNegInf : ml;
+        w.m = m_new;
+        w.l = w.l * alpha + (g == 0 ? e : 0.f);  // the query's four lanes share one sum
+#pragma unroll
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int dim = 16 * db + 4 * g + r;
+                const float vv = VROW ? vt[j * KPAD + dim] : vt[(j >> 2) * (kHeadDim * 4) + vslot(dim) * 4 + (j & 3)];
+                w.o[db][r] = __builtin_fmaf(e, vv, w.o[db][r] * alpha);
+            }
+    }
+}
+
 // Normalise and store query qi: lane holds dims 16db + 4g + r.
 __device__ __forceinline__ void store_o(const QBlock& w, float* O, const Params& p, int qi, int g) {
     const float l = sum4(w.l);
@@ -408,10 +456,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
             bool plain = kbase + NK <= wave_kend && (wave_nq == QW || BIAS != BIAS_DENSE) && MASK != DECODER &&
                          next_all_valid;
             if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
+            // A wave with only a few keys left in this tile takes them on the VALU (and stages the
+            // next tile, if the workgroup has one, in one go).
+            const bool few = !plain && nkb > 0 && wave_kend - kbase <= kValuKeys;
             if (plain) {
                 attend_tile<MASK, BIAS, true, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g, voff_even,
                                                  voff_odd, stage_next);
-            } else if (nkb > 0) {
+            } else if (nkb > 0 && !few) {
                 attend_tile<MASK, BIAS, false, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g, voff_even,
                                                   voff_odd, stage_next);
             } else if (more) {
@@ -423,7 +474,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
                 }
                 nxt.kadd[lane] = kterm(nbase, kvb_next);
             }
-            if (more && (plain || nkb > 0)) store(nxt, 3, sq);
+            if (few) attend_keys_valu<MASK, BIAS, false>(w, p, st.k, st.v, st.kadd, lut, kbase, wave_kend - kbase, qi, h, g);
+            if (more && (plain || (nkb > 0 && !few))) store(nxt, 3, sq);
             // The next tile's flag, from its key_valid bytes fetched at the start of this one.
             if (more) next_all_valid = all_valid(nbase, kvb_next);
             __syncthreads();
@@ -569,7 +621,10 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
     auto no_hook = [](int, int) {};
     // 32-key tiles (two key blocks): half the score registers of a 64-key tile, for the 80-VGPR
     // budget, at the price of one more max/rescale per 64 keys.
-    for (int kbase = 0; kbase < wave_kend; kbase += RNK) {
+    // The last few keys of the row (a tile of at most kValuKeys) go to the VALU after the loop.
+    const int klast = wave_kend > 0 ? (wave_kend - 1) / RNK * RNK : 0;
+    const int kloop = wave_kend - klast <= kValuKeys ? klast : wave_kend;
+    for (int kbase = 0; kbase < kloop; kbase += RNK) {
         const int nkb = min(2, (wave_kend - kbase + 15) >> 4);
         // Query slots past n_q (q = 0, never stored) may run mask-free, except with a dense bias.
         bool plain = kbase + RNK <= wave_kend && (wave_nq == 16 || BIAS != BIAS_DENSE) && MASK != DECODER;
@@ -584,6 +639,9 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
             attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g, voff_even,
                                               voff_odd, no_hook);
     }
+    if (kloop < wave_kend)
+        attend_keys_valu<MASK, BIAS, false>(w, p, Ks + kloop * KPAD, Vs + (kloop >> 2) * (kHeadDim * 4), kadd + kloop,
+                                            lut, kloop, wave_kend - kloop, qi, h, g);
     store_o(w, O, p, qi, g);
 }
 
