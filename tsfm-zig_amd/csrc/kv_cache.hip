@@ -56,30 +56,53 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ u32x4 ldu4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// ---- append: one thread per (series, head, new token, 8-dim chunk) ----
+// ---- append ----
+// K: one thread per (series, head, new token, 8-dim chunk): 16-byte load, 16-byte store.
+// V: one thread per (series, head, touched 32-key chunk, octet, dim) builds the whole 16-byte slot
+//    (8 keys of one dim) in registers and stores it once; consecutive threads take consecutive dims,
+//    so the eight 2-byte loads (one per key, from eight token rows) and the store are all contiguous
+//    across the wave. A slot the append covers only in part is read first and its other keys kept.
 __global__ __launch_bounds__(256) void kv_append(KvLayout c, const uint16_t* __restrict__ k, int64_t k_tok,
                                                  int64_t k_batch, const uint16_t* __restrict__ v, int64_t v_tok,
-                                                 int64_t v_batch, int32_t pos0, int32_t n_new) {
-    const int64_t total = (int64_t)c.B * c.H * n_new * 8;
+                                                 int64_t v_batch, int32_t pos0, int32_t n_new, int64_t k_items,
+                                                 int32_t ch0, int32_t nch) {
     const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (id >= total) return;
-    const int chunk = (int)(id & 7);
-    int64_t rest = id >> 3;
-    const int t = (int)(rest % n_new);
-    rest /= n_new;
+    if (id < k_items) {
+        const int chunk = (int)(id & 7);
+        int64_t rest = id >> 3;
+        const int t = (int)(rest % n_new);
+        rest /= n_new;
+        const int h = (int)(rest % c.H);
+        const int b = (int)(rest / c.H);
+        const int64_t bh = (int64_t)b * c.H + h;
+        const u32x4 kv = ldu4(k + b * k_batch + t * k_tok + h * kHeadDim + 8 * chunk);
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(c.k) + (bh * c.cap + pos0 + t) * kHeadDim + 8 * chunk) = kv;
+        return;
+    }
+    const int64_t vid = id - k_items;
+    if (vid >= (int64_t)c.B * c.H * nch * 4 * kHeadDim) return;
+    const int d = (int)(vid & 63);
+    const int o = (int)((vid >> 6) & 3);
+    int64_t rest = vid >> 8;
+    const int ch = ch0 + (int)(rest % nch);
+    rest /= nch;
     const int h = (int)(rest % c.H);
     const int b = (int)(rest / c.H);
-    const int pos = pos0 + t;
     const int64_t bh = (int64_t)b * c.H + h;
-    const int64_t src_off = h * kHeadDim + 8 * chunk;
-    const u32x4 kv = ldu4(k + b * k_batch + t * k_tok + src_off);
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(c.k) + (bh * c.cap + pos) * kHeadDim + 8 * chunk) = kv;
-    const u32x4 vv = ldu4(v + b * v_batch + t * v_tok + src_off);
-    const int p = pos >> 5, kk = pos & 31;
-    const int g = (kk & 15) >> 2, j = (kk & 3) + 4 * (kk >> 4);
-    uint16_t* vd = static_cast<uint16_t*>(c.v) + (((bh * (c.cap / 32) + p) * 4 + g) * kHeadDim + 8 * chunk) * 8 + j;
+    u32x4* slot = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(c.v) +
+                                           (((bh * (c.cap / 32) + ch) * 4 + o) * kHeadDim + d) * 8);
+    const int key0 = 32 * ch + 4 * o;  // slot j holds key key0 + j (j < 4) or key0 + 16 + (j - 4)
+    const bool whole = key0 >= pos0 && key0 + 19 < pos0 + n_new;  // uniform over the 64 dims
+    u32x4 w = whole ? u32x4{0, 0, 0, 0} : *slot;
+    const uint16_t* src = v + b * v_batch + h * kHeadDim + d;
 #pragma unroll
-    for (int e = 0; e < 8; e++) vd[e * 8] = (uint16_t)((e & 1) ? (vv[e >> 1] >> 16) : (vv[e >> 1] & 0xffffu));
+    for (int j = 0; j < 8; j++) {
+        const int t = key0 + (j < 4 ? j : 12 + j) - pos0;
+        if (t < 0 || t >= n_new) continue;
+        const uint32_t x = src[t * v_tok];
+        w[j >> 1] = (j & 1) ? (w[j >> 1] & 0xffffu) | (x << 16) : (w[j >> 1] & 0xffff0000u) | x;
+    }
+    *slot = w;
 }
 
 // ---- attend ----
@@ -258,12 +281,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 hipError_t launch_kv_append(const KvLayout& c, bool /*is_bf16*/, const void* k, int64_t k_tok, int64_t k_batch,
                             const void* v, int64_t v_tok, int64_t v_batch, int32_t pos0, int32_t n_new,
                             hipStream_t stream) {
-    const int64_t total = (int64_t)c.B * c.H * n_new * 8;
-    const int64_t blocks = (total + 255) / 256;
-    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const int64_t k_items = (int64_t)c.B * c.H * n_new * 8;
+    const int32_t ch0 = pos0 / 32, nch = (pos0 + n_new - 1) / 32 - ch0 + 1;
+    const int64_t v_items = (int64_t)c.B * c.H * nch * 4 * kHeadDim;
+    const int64_t blocks = (k_items + v_items + 255) / 256;
+    if (n_new <= 0 || blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(kv_append, dim3((unsigned)blocks), dim3(256), 0, stream, c,
                        static_cast<const uint16_t*>(k), k_tok, k_batch, static_cast<const uint16_t*>(v), v_tok,
-                       v_batch, pos0, n_new);
+                       v_batch, pos0, n_new, k_items, ch0, nch);
     return hipGetLastError();
 }
 
