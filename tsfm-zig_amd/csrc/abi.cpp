@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -174,6 +175,11 @@ int validate(const tsfm_attn_args* a) {
         return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
     const int64_t row = (int64_t)a->heads * a->head_dim;
     if (a->o_tok < row && a->n_q > 1) return fail(TSFM_E_INVALID, "o token stride smaller than heads * head_dim");
+    // The kernels address the K and V rows of one (series, head), and the rows of a tile past the
+    // last key, through 32-bit byte offsets.
+    const int64_t esz = a->dtype == TSFM_DTYPE_F32 ? 4 : 2;
+    if (((int64_t)a->n_k + 64) * std::max(a->k_tok, a->v_tok) * esz + 256 > 0xffffffffLL)
+        return fail(TSFM_E_UNSUPPORTED, "the K/V rows of one series must span less than 4 GiB");
     const bool reads_valid = a->mask == TSFM_MASK_KEYS_ADDITIVE || a->mask == TSFM_MASK_CAUSAL_KEYS ||
                              a->mask == TSFM_MASK_FULL_KEYS || a->mask == TSFM_MASK_DECODER;
     if (reads_valid && a->key_valid == nullptr) return fail(TSFM_E_INVALID, "mask %d needs key_valid", a->mask);

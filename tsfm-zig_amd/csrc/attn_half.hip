@@ -212,67 +212,51 @@ attn_fwd_half(Params p) {
     u32x4 klo, khi;
     f32x4 kc0, kc1, ks0, ks1;  // RoPE cos/sin of the thread's K row, applied at the LDS store
     uint32_t vw[8];
+    uint32_t kvb = 1;              // key_valid byte of key kbase + lane of the fetched tile
     float kar = 0.f;
     bool next_all_valid = true;    // uniform: every key term of the fetched tile is 0
     bool next_none_valid = false;  // uniform: no key term of the fetched tile is 0
 
-    // Per-thread base pointers; a tile adds the uniform kbase * stride, a V row the uniform
-    // j * v_tok, so full tiles issue ten straight-line loads with no per-lane address arithmetic.
-    const E* const kbase_p = K + (int64_t)krow * p.k_tok + 8 * kc;
-    const E* const vbase_p = V + (int64_t)vkey0 * p.v_tok + 2 * dp;
-    const int64_t vt = p.v_tok;
-    auto ld32 = [](const E* q) { return *reinterpret_cast<const uint32_t*>(q); };
+    // All tile loads go through buffer descriptors that end after key n_k - 1 (key_valid: after
+    // the bytes the mask reads): rows of the last tile past the end read as zeros, so no load needs
+    // a clamp or a branch, and an offset is one 32-bit VGPR (the host keeps a (series, head) span
+    // of K or V below 4 GiB).
+    const __amdgpu_buffer_rsrc_t k_buf = make_buf(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 2));
+    const __amdgpu_buffer_rsrc_t v_buf = make_buf(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 2));
+    const __amdgpu_buffer_rsrc_t c_buf = make_buf(RC, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+    const __amdgpu_buffer_rsrc_t s_buf = make_buf(RS, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+    const __amdgpu_buffer_rsrc_t kv_rsrc = make_buf(mask_reads_valid<MASK>() ? KV : p.key_valid,
+                                                    mask_reads_valid<MASK>() ? (uint32_t)kv_len : 0u);
+    const uint32_t koff = (uint32_t)(krow * p.k_tok + 8 * kc) * 2u;
+    const uint32_t voff = (uint32_t)(vkey0 * p.v_tok + 2 * dp) * 2u;
+    const uint32_t coff = (uint32_t)(krow * 32 + 8 * kc) * 4u;
+    const uint32_t vrow = (uint32_t)p.v_tok * 2u;
 
+    // Loads only: the key terms and the tile flags are derived from kvb in `store`, after the tile
+    // being computed, so no wait for this tile's loads sits in front of the products.
     auto fetch = [&](int kbase) {
-        const int key = kbase + krow;
-        int keyc = key;
-        if (kbase + NK <= p.n_k) {  // uniform: the whole tile is in range
-            const E* ks = kbase_p + (int64_t)kbase * p.k_tok;
-            klo = ldu4(ks);
-            khi = ldu4(ks + 32);
-            const E* vs = vbase_p + (int64_t)kbase * vt;
-            vw[0] = ld32(vs);
-            vw[1] = ld32(vs + vt);
-            vw[2] = ld32(vs + 2 * vt);
-            vw[3] = ld32(vs + 3 * vt);
-            vw[4] = ld32(vs + 16 * vt);
-            vw[5] = ld32(vs + 17 * vt);
-            vw[6] = ld32(vs + 18 * vt);
-            vw[7] = ld32(vs + 19 * vt);
-        } else {  // the last tile: clamp every row into range, then zero the padding rows
-            const int last = p.n_k - 1;
-            keyc = min(key, last);
-            const E* ks = K + (int64_t)keyc * p.k_tok + 8 * kc;
-            klo = ldu4(ks);
-            khi = ldu4(ks + 32);
-            const E* vs = V + 2 * dp;
-            const int v0 = kbase + vkey0;
+        const uint32_t kq = koff + (uint32_t)kbase * (uint32_t)p.k_tok * 2u;
+        klo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(k_buf, kq, 0, 0));
+        khi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(k_buf, kq + 64u, 0, 0));
+        const uint32_t vq = voff + (uint32_t)kbase * vrow;
 #pragma unroll
-            for (int j = 0; j < 8; j++) vw[j] = ld32(vs + (int64_t)min(v0 + (j < 4 ? j : 12 + j), last) * vt);
-#pragma unroll
-            for (int j = 0; j < 8; j++) vw[j] = v0 + (j < 4 ? j : 12 + j) <= last ? vw[j] : 0u;
-            const bool kin = key <= last;
-            klo = kin ? klo : u32x4{0, 0, 0, 0};
-            khi = kin ? khi : u32x4{0, 0, 0, 0};
-        }
+        for (int j = 0; j < 8; j++)
+            vw[j] = __builtin_amdgcn_raw_buffer_load_b32(v_buf, vq + (uint32_t)(j < 4 ? j : 12 + j) * vrow, 0, 0);
         if (ROPE) {
-            const float* cs = RC + (int64_t)keyc * 32 + 8 * kc;
-            const float* sn = RS + (int64_t)keyc * 32 + 8 * kc;
-            kc0 = ld4(cs);
-            kc1 = ld4(cs + 4);
-            ks0 = ld4(sn);
-            ks1 = ld4(sn + 4);
+            const uint32_t cq = coff + (uint32_t)kbase * 128u;
+            kc0 = bld4(c_buf, cq);
+            kc1 = bld4(c_buf, cq + 16u);
+            ks0 = bld4(s_buf, cq);
+            ks1 = bld4(s_buf, cq + 16u);
         }
-        {  // every wave evaluates the 64 key terms itself: the tile flag needs no LDS round trip
-            const int kk = kbase + lane;
-            bool valid = true;
-            if (mask_reads_valid<MASK>()) valid = kk < kv_len && KV[kk] != 0;
-            kar = key_term_h<MASK>(kk, p.n_k, valid, p.ctx_keys);
+        if (mask_reads_valid<MASK>()) kvb = __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, (uint32_t)(kbase + lane), 0, 0);
+    };
+    auto store = [&](StageH& st, int kbase) {
+        {  // every wave evaluates the 64 key terms itself: the tile flags need no LDS round trip
+            kar = key_term_h<MASK>(kbase + lane, p.n_k, kvb != 0, p.ctx_keys);
             next_all_valid = __ballot(kar != 0.f) == 0;
             next_none_valid = __ballot(kar == 0.f) == 0;
         }
-    };
-    auto store = [&](StageH& st) {
         if (ROPE) rope8<BF16>(klo, khi, kc0, kc1, ks0, ks1);
         stu4(st.k + krow * KROW + 4 * kc, klo);
         stu4(st.k + krow * KROW + 16 + 4 * kc, khi);
@@ -398,13 +382,16 @@ attn_fwd_half(Params p) {
             }
         }
         // The next tile goes to the other stage last: its loads had the whole tile to land.
-        if (more) store(stage[(t + 1) & 1]);
+        if (more) store(stage[(t + 1) & 1], kbase + NK);
     };
 
     if (ntiles > 0) {
         fetch(0);
-        store(stage[0]);
+        store(stage[0], 0);
     }
+    // Q has landed here on every path (an empty use makes the compiler wait for it now), so no
+    // wait for Q is merged into the loop: there, the only loads in flight are the next tile's.
+    asm volatile("" : "+v"(qf[0][0]), "+v"(qf[0][1]), "+v"(qf[1][0]), "+v"(qf[1][1]));
     __syncthreads();
     const int nqb = (wave_nq + 15) >> 4;
     for (int t = 0; t < ntiles; t++) {
@@ -424,7 +411,7 @@ attn_fwd_half(Params p) {
             tile(st, kbase, nkb, nqb, std::integral_constant<bool, false>{}, t);
         } else if (t + 1 < ntiles) {
             fetch(kbase + NK);
-            store(stage[(t + 1) & 1]);
+            store(stage[(t + 1) & 1], kbase + NK);
         }
         __syncthreads();
     }
