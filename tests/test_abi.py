@@ -87,6 +87,8 @@ def _valid_host_args(ta, **over):
     (dict(q_tok=130), 2),
     (dict(mask=1), 3),            # keys_additive without key_valid
     (dict(q_pos0=-1), 3),
+    (dict(dtype=2, scale=-0.5), 2),  # half precision takes the row max before scaling
+    (dict(k_tok=1 << 26), 2),        # K rows of one series past 32-bit byte offsets
 ])
 def test_validation_codes(ta, over, code):
     args, _ = _valid_host_args(ta, **over)

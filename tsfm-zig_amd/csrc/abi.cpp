@@ -177,6 +177,8 @@ int validate(const tsfm_attn_args* a) {
     if (a->o_tok < row && a->n_q > 1) return fail(TSFM_E_INVALID, "o token stride smaller than heads * head_dim");
     // The kernels address the K and V rows of one (series, head), and the rows of a tile past the
     // last key, through 32-bit byte offsets.
+    if (a->dtype != TSFM_DTYPE_F32 && !(a->scale >= 0.f))
+        return fail(TSFM_E_UNSUPPORTED, "half-precision attention needs a non-negative scale");
     const int64_t esz = a->dtype == TSFM_DTYPE_F32 ? 4 : 2;
     if (((int64_t)a->n_k + 64) * std::max(a->k_tok, a->v_tok) * esz + 256 > 0xffffffffLL)
         return fail(TSFM_E_UNSUPPORTED, "the K/V rows of one series must span less than 4 GiB");

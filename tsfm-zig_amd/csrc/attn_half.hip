@@ -264,8 +264,8 @@ attn_fwd_half(Params p) {
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const uint32_t a = vw[2 * w], c = vw[2 * w + 1];
-            even[w] = (a & 0xffffu) | (c << 16);
-            odd[w] = (a >> 16) | (c & 0xffff0000u);
+            even[w] = __builtin_amdgcn_perm(c, a, 0x05040100u);  // low halves of a and c
+            odd[w] = __builtin_amdgcn_perm(c, a, 0x07060302u);   // high halves
         }
         stu4(st.v + (oct * kHeadDim + vslot_h(2 * dp)) * 4, even);
         stu4(st.v + (oct * kHeadDim + vslot_h(2 * dp + 1)) * 4, odd);
@@ -296,6 +296,10 @@ attn_fwd_half(Params p) {
         }
 
         // ---- online softmax in exp2 units ----
+        // Row maxima of the tile per query block, in the units of mc_run (exp2 units; raw scores
+        // for KEYS_ADDITIVE). The scale is non-negative (checked on the host), so the max of the
+        // raw scores times c2 is the max of the scaled ones.
+        float mn[2] = {kNegInf, kNegInf};
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
             if (!PLAIN && qb >= nqb) continue;
@@ -317,28 +321,35 @@ attn_fwd_half(Params p) {
                     mloc = fmaxf(mloc, x);
                 }
             }
-            // A stale running max is kept until the true one exceeds it by more than kStale (exp2
-            // units): weights then stay below 2^kStale, and O and the row sum are rescaled only when
-            // some lane of the wave moves past that, rarely after the first tiles of a row.
-            float mc_use, alpha;
-            if (MASK == KEYS_ADDITIVE) {
-                // mc_run holds the raw-score max here: e = exp2((x - m) * c2) keeps x - m exact.
-                const float mr = fmaxf(max4(mloc), mc_run[qb]);
-                const bool upd = __ballot(mr > mc_run[qb] + kStale / c2) != 0;
-                const float mk = upd ? mr : mc_run[qb];
-                mc_use = mk == kNegInf ? 0.f : mk;
-                alpha = upd ? __builtin_amdgcn_exp2f((mc_run[qb] - mc_use) * c2) : 1.f;
-                mc_run[qb] = mk;
-            } else {
-                // exp2 units: e = exp2(x * c2 - max * c2), one FMA per score.
-                const float mt = mloc == kNegInf ? kNegInf : mloc * c2;
-                const float mn = fmaxf(max4(mt), mc_run[qb]);
-                const bool upd = __ballot(mn > mc_run[qb] + kStale) != 0;
-                const float mk = upd ? mn : mc_run[qb];
-                mc_use = mk == kNegInf ? 0.f : mk;
-                alpha = upd ? __builtin_amdgcn_exp2f(mc_run[qb] - mc_use) : 1.f;
+            if (MASK == KEYS_ADDITIVE) mn[qb] = max4(mloc);
+            else if (PLAIN) mn[qb] = max4(mloc) * c2;  // every score of a mask-free tile is finite
+            else mn[qb] = max4(mloc == kNegInf ? kNegInf : mloc * c2);
+        }
+        // A stale running max is kept until the true one exceeds it by more than kStale (exp2
+        // units): weights then stay below 2^kStale, and O and the row sum are rescaled only when
+        // some lane of the wave moves past that, rarely after the first tiles of a row. The test
+        // is wave-uniform, so the common case is one compare and one branch per query block.
+        const float slack = MASK == KEYS_ADDITIVE ? kStale / c2 : kStale;
+        bool upd[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) upd[qb] = (PLAIN || qb < nqb) && __ballot(mn[qb] > mc_run[qb] + slack) != 0;
+        if (upd[0] || upd[1]) {
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                if (!upd[qb]) continue;
+                const float mk = fmaxf(mn[qb], mc_run[qb]);  // finite: mn exceeded mc_run
+                const float alpha = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((mc_run[qb] - mk) * c2)
+                                                          : __builtin_amdgcn_exp2f(mc_run[qb] - mk);
+#pragma unroll
+                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
+                lacc[qb] *= alpha;
                 mc_run[qb] = mk;
             }
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            if (!PLAIN && qb >= nqb) continue;
+            const float mc_use = mc_run[qb] == kNegInf ? 0.f : mc_run[qb];  // no valid key yet: e = 0
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
@@ -347,11 +358,6 @@ attn_fwd_half(Params p) {
                     sacc[kb][qb][r] = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((x - mc_use) * c2)
                                                             : __builtin_amdgcn_exp2f(__builtin_fmaf(x, c2, -mc_use));
                 }
-            if (__ballot(alpha != 1.f) != 0) {
-#pragma unroll
-                for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
-                lacc[qb] *= alpha;
-            }
         }
 
         // ---- O^T += V^T . P^T, two 32-key chunks ----
@@ -463,6 +469,7 @@ hipError_t launch_mask(const Params& p, int mask, bool rope, hipStream_t s) {
 
 hipError_t launch_attn_half(const Params& p, bool is_bf16, int mask, int bias, bool rope, hipStream_t s) {
     if (bias != BIAS_NONE) return hipErrorNotSupported;  // the bias-carrying families are f32
+    if (!(p.scale >= 0.f)) return hipErrorNotSupported;  // the row max is taken before scaling
     return is_bf16 ? launch_mask<true>(p, mask, rope, s) : launch_mask<false>(p, mask, rope, s);
 }
 

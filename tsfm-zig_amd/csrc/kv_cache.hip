@@ -297,6 +297,7 @@ hipError_t launch_kv_attend(const KvLayout& c, bool is_bf16, const void* q, int6
                             hipStream_t stream) {
     const int64_t blocks = (int64_t)c.B * c.H * ((n_q + QB - 1) / QB);
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (!(scale >= 0.f)) return hipErrorNotSupported;  // the row max is taken before scaling
     if (is_bf16)
         hipLaunchKernelGGL(kv_attend<true>, dim3((unsigned)blocks), dim3(NT), 0, stream, c,
                            static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
