@@ -190,6 +190,10 @@ attn_fwd_half(Params p) {
     }
 
     float mc_run[2] = {kNegInf, kNegInf};  // running max, in exp2 units (max * scale * log2 e)
+    // Per query block: the score (same units) past which the running max must move, and the max
+    // the exponentials subtract (0 while no key is valid, so that masked scores give e = 0).
+    const float slack = MASK == KEYS_ADDITIVE ? kStale / c2 : kStale;
+    float thr[2] = {kNegInf, kNegInf}, mc_use[2] = {0.f, 0.f};
     // Row sums on the matrix cores: V^T replaced by ones gives, in every register of the lane,
     // the sum over the chunk's keys of the rounded weights of query ql (the same weights the O
     // product uses). 16 VALU adds per tile and block become one instruction per 32-key chunk.
@@ -296,10 +300,10 @@ attn_fwd_half(Params p) {
         }
 
         // ---- online softmax in exp2 units ----
-        // Row maxima of the tile per query block, in the units of mc_run (exp2 units; raw scores
-        // for KEYS_ADDITIVE). The scale is non-negative (checked on the host), so the max of the
-        // raw scores times c2 is the max of the scaled ones.
-        float mn[2] = {kNegInf, kNegInf};
+        // Per lane and query block, the max of the lane's scores in the units of mc_run (exp2
+        // units; raw scores for KEYS_ADDITIVE). The scale is non-negative (checked on the host), so
+        // the max of the raw scores times c2 is the max of the scaled ones.
+        float mt[2] = {kNegInf, kNegInf};
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
             if (!PLAIN && qb >= nqb) continue;
@@ -321,42 +325,43 @@ attn_fwd_half(Params p) {
                     mloc = fmaxf(mloc, x);
                 }
             }
-            if (MASK == KEYS_ADDITIVE) mn[qb] = max4(mloc);
-            else if (PLAIN) mn[qb] = max4(mloc) * c2;  // every score of a mask-free tile is finite
-            else mn[qb] = max4(mloc == kNegInf ? kNegInf : mloc * c2);
+            if (MASK == KEYS_ADDITIVE) mt[qb] = mloc;
+            else if (PLAIN) mt[qb] = mloc * c2;  // every score of a mask-free tile is finite
+            else mt[qb] = mloc == kNegInf ? kNegInf : mloc * c2;
         }
-        // A stale running max is kept until the true one exceeds it by more than kStale (exp2
-        // units): weights then stay below 2^kStale, and O and the row sum are rescaled only when
-        // some lane of the wave moves past that, rarely after the first tiles of a row. The test
-        // is wave-uniform, so the common case is one compare and one branch per query block.
-        const float slack = MASK == KEYS_ADDITIVE ? kStale / c2 : kStale;
+        // A stale running max is kept until a score exceeds it by more than kStale (exp2 units):
+        // weights then stay below 2^kStale, and O and the row sum are rescaled only when some lane
+        // of the wave moves past that, rarely after the first tiles of a row. The common case is
+        // one compare and a wave-uniform branch per query block; the cross-lane row max is only
+        // formed when the running max moves.
         bool upd[2];
 #pragma unroll
-        for (int qb = 0; qb < 2; qb++) upd[qb] = (PLAIN || qb < nqb) && __ballot(mn[qb] > mc_run[qb] + slack) != 0;
+        for (int qb = 0; qb < 2; qb++) upd[qb] = (PLAIN || qb < nqb) && __ballot(mt[qb] > thr[qb]) != 0;
         if (upd[0] || upd[1]) {
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) {
                 if (!upd[qb]) continue;
-                const float mk = fmaxf(mn[qb], mc_run[qb]);  // finite: mn exceeded mc_run
+                const float mk = fmaxf(max4(mt[qb]), mc_run[qb]);  // finite: some score exceeded thr
                 const float alpha = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((mc_run[qb] - mk) * c2)
                                                           : __builtin_amdgcn_exp2f(mc_run[qb] - mk);
 #pragma unroll
                 for (int db = 0; db < 4; db++) oacc[db][qb] *= alpha;
                 lacc[qb] *= alpha;
                 mc_run[qb] = mk;
+                thr[qb] = mk + slack;
+                mc_use[qb] = mk;
             }
         }
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
             if (!PLAIN && qb >= nqb) continue;
-            const float mc_use = mc_run[qb] == kNegInf ? 0.f : mc_run[qb];  // no valid key yet: e = 0
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float x = sacc[kb][qb][r];
-                    sacc[kb][qb][r] = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((x - mc_use) * c2)
-                                                            : __builtin_amdgcn_exp2f(__builtin_fmaf(x, c2, -mc_use));
+                    sacc[kb][qb][r] = MASK == KEYS_ADDITIVE ? __builtin_amdgcn_exp2f((x - mc_use[qb]) * c2)
+                                                            : __builtin_amdgcn_exp2f(__builtin_fmaf(x, c2, -mc_use[qb]));
                 }
         }
 
