@@ -73,6 +73,23 @@ def test_masks_match_oracle(ta, orc, gpu_ready, mask, n):
     assert _ref.scaled_err(got, want) <= TOL
 
 
+@pytest.mark.parametrize("mask", [1, 3])
+@pytest.mark.parametrize("n", [17, 145, 577])
+def test_dense_bias_matches_oracle(ta, orc, gpu_ready, mask, n):
+    """A dense additive bias [H, n, n] (the reference's bias argument of selfAttend). n = 16k + 1
+    leaves one query in the last 16-query block of a workgroup: the single-query VALU path, in the
+    LDS-resident kernel (17) and in the streaming one (145, 577)."""
+    B, H = 2, 2
+    q, k, v, kv = _inputs(40 + n + mask, B, H, n, n)
+    bias = np.random.default_rng(41 + n).standard_normal((H, n, n)).astype(np.float32)
+    got = run_generic(ta, mask, q, k, v, kv, B, H, n, n, 0.125, bias=bias, bias_head=n * n, bias_row=n)
+    row = H * 64
+    want = np.zeros((B, n, row), np.float32)
+    orc.batched_self_attend(THREADS, mask, q, row, n * row, k, row, n * row, v, row, n * row, want, row, n * row, kv,
+                            n, bias, B, H, n, 64, 0.125)
+    assert _ref.scaled_err(got, want) <= TOL
+
+
 @pytest.mark.parametrize("mask", [0, 1, 3])
 def test_device_pointers_match_host_pointers(ta, gpu_ready, mask):
     B, H, n = 3, 2, 97

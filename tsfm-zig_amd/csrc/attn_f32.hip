@@ -291,6 +291,103 @@ __device__ __forceinline__ void attend_keys_valu(QBlock& w, const Params& p, con
     }
 }
 
+// ---- a single query on the VALU ----
+//
+// A 16-query block that holds one query (n_q = 16k + 1: 577-token Chronos-2 rows, 129-token Bolt
+// rows) would spend 15/16 of every matrix instruction on empty query slots. Such a wave takes its
+// keys 64 at a time on the VALU instead: lane = key for the score (a 64-term dot product against q,
+// read from LDS as a broadcast), one online-softmax step over the chunk with the same update as
+// attend_tile, then lane = dim for O += sum_j e_j v_j with the weights broadcast from LDS. The
+// running state lives in the QBlock's registers: o[0][0] = O[query, dim lane], m / ml as in
+// attend_tile, l = the share of the row sum of the keys this lane has taken.
+
+// DPP lane moves within rows of 16 (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror): combined with max4 / sum4 they reduce over the 64 lanes, every lane getting the
+// same value (each step adds two values that are equal up to operand order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp_mov<0xb1>(x));
+    x = fmaxf(x, dpp_mov<0x4e>(x));
+    x = fmaxf(x, dpp_mov<0x141>(x));
+    x = fmaxf(x, dpp_mov<0x140>(x));
+    return max4(x);
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x = x + dpp_mov<0xb1>(x);
+    x = x + dpp_mov<0x4e>(x);
+    x = x + dpp_mov<0x141>(x);
+    x = x + dpp_mov<0x140>(x);
+    return sum4(x);
+}
+
+// The wave's query (already rotated and scaled in w.q, lanes with ql == 0) to LDS as 64 floats.
+__device__ __forceinline__ void thin_store_q(const QBlock& w, float* qs, int ql, int g) {
+    if (ql != 0) return;
+    st4(qs + 8 * g, f32x4{w.q[0], w.q[1], w.q[2], w.q[3]});
+    st4(qs + 8 * g + 4, f32x4{w.q[4], w.q[5], w.q[6], w.q[7]});
+    st4(qs + 32 + 8 * g, f32x4{w.q[8], w.q[9], w.q[10], w.q[11]});
+    st4(qs + 36 + 8 * g, f32x4{w.q[12], w.q[13], w.q[14], w.q[15]});
+}
+
+// Keys kbase .. kbase + nkeys - 1 (1 <= nkeys <= 64) of query qi. kt / vt / kat: the keys' K rows,
+// V key quads and key terms; qs: the query (thin_store_q); ps: 64 floats of LDS for the weights.
+template <int MASK, int BIAS>
+__device__ __forceinline__ void attend_thin(QBlock& w, const Params& p, const float* kt, const float* vt,
+                                            const float* kat, const float* lut, const float* qs, float* ps, int kbase,
+                                            int nkeys, int qi, int h, int lane) {
+#pragma clang fp contract(off)
+    asm volatile("" : "+v"(lane));  // as in attend_tile: no hoisting out of this variant
+    const int j = min(lane, nkeys - 1);  // lanes past the chunk read a real row; their score is dropped
+    const float* kr = kt + j * KPAD;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        const f32x4 k4 = ld4(kr + 4 * c), q4 = ld4(qs + 4 * c);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(q4[i], k4[i], acc[i]);
+    }
+    float x = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const int key = kbase + j;
+    if (BIAS == BIAS_REL) x = x + lut[key - qi + p.n_q - 1];
+    if (BIAS == BIAS_DENSE) x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
+    x = masked<MASK>(x, kat[j], key, p.q_pos0 + qi, p.n_k, p.chain_start);
+    x = lane < nkeys ? x : kNegInf;
+
+    const float m_new = fmaxf(w.m, wave_max(x));
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const bool big = m_use < -1e30f;  // as in attend_tile
+    const float shift = big ? m_use : 0.f;
+    const float ml = big ? 0.f : m_use * kLog2e;
+    const float alpha = __builtin_amdgcn_exp2f(big ? (w.m - m_use) * kLog2e : w.ml - ml);
+    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x - shift, kLog2e, -ml));
+    w.ml = (big || m_new == kNegInf) ? kNegInf : ml;
+    w.m = m_new;
+    w.l = w.l * alpha + e;
+
+    ps[lane] = e;  // read back below by the same wave: LDS keeps a wave's accesses in order
+    float o = w.o[0][0] * alpha;
+    const float* vd = vt + vslot(lane) * 4;
+    const int nq4 = (nkeys + 3) >> 2;
+    for (int kq = 0; kq < nq4; kq++) {
+        const f32x4 p4 = ld4(ps + 4 * kq), v4 = ld4(vd + kq * (kHeadDim * 4));
+        o = __builtin_fmaf(p4[0], v4[0], o);
+        o = __builtin_fmaf(p4[1], v4[1], o);
+        o = __builtin_fmaf(p4[2], v4[2], o);
+        o = __builtin_fmaf(p4[3], v4[3], o);
+    }
+    w.o[0][0] = o;
+}
+
+// Normalise and store the single query qi of a thin wave: lane = dim.
+__device__ __forceinline__ void store_thin(const QBlock& w, float* O, const Params& p, int qi, int lane) {
+    const float l = wave_sum(w.l);
+    const float inv = 1.0f / l;
+    O[(int64_t)qi * p.o_tok + lane] = w.o[0][0] * inv;
+}
+
 // Normalise and store query qi: lane holds dims 16db + 4g + r.
 __device__ __forceinline__ void store_o(const QBlock& w, float* O, const Params& p, int qi, int g) {
     const float l = sum4(w.l);
@@ -318,6 +415,7 @@ template <int MASK, int BIAS, bool ROPE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_fwd_f32(Params p) {
     __shared__ __attribute__((aligned(16))) Stage stage[2];
     __shared__ float lut_raw[BIAS == BIAS_REL ? kRelMax + 2 * kLutPad : 1];
+    __shared__ __attribute__((aligned(16))) float thin_qp[2 * kHeadDim];  // a thin wave's q and weights
     float* const lut = lut_raw + (BIAS == BIAS_REL ? kLutPad : 0);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -346,6 +444,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
     const int wave_nq = max(0, min(QW, p.n_q - wq0));
     const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys) : 0;
     const int ntiles = (kend + NK - 1) / NK;
+    const bool thin = wave_nq == 1;  // one query: the VALU path (attend_thin)
 
     // key_valid of this row through a buffer descriptor sized to the bytes the mask reads: a read
     // past them returns 0 (= invalid), so the load needs neither a bounds test nor a branch.
@@ -402,6 +501,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
     // Additive mask term of key tbase + lane, and the tile's mask-free test (every term 0).
     auto kterm = [&](int tbase, uint32_t kvb) { return key_term<MASK>(tbase + lane, p.n_k, kvb != 0, p.ctx_keys); };
     auto all_valid = [&](int tbase, uint32_t kvb) { return __ballot(kterm(tbase, kvb) != 0.f) == 0; };
+    // A whole tile in one go, quarter by quarter (for waves with no products to hide it behind);
+    // returns the tile's key_valid bytes.
+    auto stage_all = [&](Stage& st, int tbase) {
+        Quarter hs;
+        const uint32_t kvb = fetch_valid(tbase);
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            fetch(tbase + 16 * qq, hs);
+            store(st, qq, hs);
+        }
+        st.kadd[lane] = kterm(tbase, kvb);
+        return kvb;
+    };
 
     // Prologue: tile 0's four quarters, q and the T5 table are all requested before anything waits.
     uint32_t kvb_next = fetch_valid(0);  // key_valid bytes of the tile being staged
@@ -413,6 +525,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
         fetch(48, s3);
         QBlock w;
         load_q<ROPE>(w, Q, RC, RS, p, qi, g);
+        if (thin) thin_store_q(w, thin_qp, ql, g);
         if (BIAS == BIAS_REL) fill_rel_lut(lut_raw, p, h, tid, NT);
         store(stage[0], 0, s0);
         store(stage[0], 1, s1);
@@ -422,6 +535,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
         bool next_all_valid = all_valid(0, kvb_next);  // of the tile about to be computed
         __syncthreads();
 
+        if (thin) {
+            // Same staging and barriers as the loop below, one whole tile at a time.
+            for (int t = 0; t < ntiles; t++) {
+                const int kbase = t * NK;
+                const Stage& st = stage[t & 1];
+                if (kbase < wave_kend)
+                    attend_thin<MASK, BIAS>(w, p, st.k, st.v, st.kadd, lut, thin_qp, thin_qp + kHeadDim, kbase,
+                                            min(NK, wave_kend - kbase), wq0, h, lane);
+                if (t + 1 < ntiles) stage_all(stage[(t + 1) & 1], kbase + NK);
+                __syncthreads();
+            }
+            store_thin(w, O, p, wq0, lane);
+            return;
+        }
         const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // V operands, db even / odd
         for (int t = 0; t < ntiles; t++) {
             const int kbase = t * NK;
@@ -466,13 +593,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
                 attend_tile<MASK, BIAS, false, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g, voff_even,
                                                   voff_odd, stage_next);
             } else if (more) {
-                kvb_next = fetch_valid(nbase);
-#pragma unroll
-                for (int qq = 0; qq < 4; qq++) {
-                    fetch(nbase + 16 * qq, sq);
-                    store(nxt, qq, sq);
-                }
-                nxt.kadd[lane] = kterm(nbase, kvb_next);
+                kvb_next = stage_all(nxt, nbase);
             }
             if (few) attend_keys_valu<MASK, BIAS, false>(w, p, st.k, st.v, st.kadd, lut, kbase, wave_kend - kbase, qi, h, g);
             if (more && (plain || (nkb > 0 && !few))) store(nxt, 3, sq);
@@ -504,9 +625,10 @@ constexpr int RKIT = (kResidentKeys * 8 + RNT - 1) / RNT;   // K staging items p
 constexpr int RVIT = (kResidentKeys * 8 + RNT - 1) / RNT;   // V staging items per thread
 
 // Dynamic LDS layout, in floats: K [nkp][KPAD] | V [nkp/4 quads][64 swizzled][4] | key terms [nkp] |
-// T5 table [n_q + n_k - 1], with nkp = n_k rounded up to 16 keys.
+// T5 table [n_q + n_k - 1 + margins] | a thin wave's q and weights [2][64], with nkp = n_k rounded
+// up to 16 keys.
 struct ResidentLayout {
-    int nkp, v_off, a_off, l_off, total;
+    int nkp, v_off, a_off, l_off, t_off, total;
 };
 __host__ __device__ inline ResidentLayout resident_layout(int n_q, int n_k, bool rel_lut) {
     ResidentLayout L;
@@ -514,7 +636,8 @@ __host__ __device__ inline ResidentLayout resident_layout(int n_q, int n_k, bool
     L.v_off = L.nkp * KPAD;
     L.a_off = L.v_off + L.nkp * kHeadDim;
     L.l_off = L.a_off + L.nkp;
-    L.total = L.l_off + (rel_lut ? n_q + n_k - 1 + 2 * kLutPad : 0);
+    L.t_off = (L.l_off + (rel_lut ? n_q + n_k - 1 + 2 * kLutPad : 0) + 3) & ~3;
+    L.total = L.t_off + 2 * kHeadDim;
     return L;
 }
 
@@ -526,6 +649,7 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
     float* const Vs = smem + lay.v_off;
     float* const kadd = smem + lay.a_off;
     float* const lut = smem + lay.l_off + kLutPad;
+    float* const thin_qp = smem + lay.t_off;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
@@ -601,6 +725,8 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
     }
     QBlock w;
     load_q<ROPE>(w, Q, RC, RS, p, qi, g);
+    const int wave_nq = max(0, min(16, p.n_q - wq0));
+    if (wave_nq == 1) thin_store_q(w, thin_qp, ql, g);
     if (BIAS == BIAS_REL) fill_rel_lut(lut - kLutPad, p, h, tid, RNT);
     if (!ROPE) store_k();
 #pragma unroll
@@ -614,9 +740,15 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
     if (tid < lay.nkp) kadd[tid] = kterm;
     __syncthreads();  // the only barrier: everything below reads LDS that no one writes again
 
-    const int wave_nq = max(0, min(16, p.n_q - wq0));
     if (wave_nq == 0) return;
     const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
+    if (wave_nq == 1) {  // one query: the VALU path, 64 resident keys at a time
+        for (int kb0 = 0; kb0 < wave_kend; kb0 += 64)
+            attend_thin<MASK, BIAS>(w, p, Ks + kb0 * KPAD, Vs + (kb0 >> 2) * (kHeadDim * 4), kadd + kb0, lut, thin_qp,
+                                    thin_qp + kHeadDim, kb0, min(64, wave_kend - kb0), wq0, h, lane);
+        store_thin(w, O, p, wq0, lane);
+        return;
+    }
     const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;
     auto no_hook = [](int, int) {};
     // 32-key tiles (two key blocks): half the score registers of a 64-key tile, for the 80-VGPR
