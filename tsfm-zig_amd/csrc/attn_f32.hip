@@ -132,11 +132,12 @@ __device__ __forceinline__ void load_q(QBlock& w, const float* Q, const float* R
 template <int MASK, int BIAS, bool PLAIN, int NKB, class Hook>
 __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const float* kt, const float* vt,
                                             const float* kat, const float* lut, int kbase, int nkb, int qi, int h,
-                                            int ql, int g, int voff_even, int voff_odd, Hook&& hook) {
+                                            int ql, int g, Hook&& hook) {
     // Lane indices pass through an opaque copy: with both tile variants in one loop the optimiser
     // otherwise hoists every address and key index either variant derives from them out of the
-    // loop, and the union of those live ranges spills.
-    asm volatile("" : "+v"(g), "+v"(ql), "+v"(qi), "+v"(voff_even), "+v"(voff_odd));
+    // loop, and the union of those live ranges spills. The V operand slots are derived here too.
+    asm volatile("" : "+v"(g), "+v"(ql), "+v"(qi));
+    const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // V operands, db even / odd
 
     // ---- S^T = K . Q^T: four accumulation chains per 16-key block, summed as a tree ----
     f32x4 sacc[NKB];
@@ -549,7 +550,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
             store_thin(w, O, p, wq0, lane);
             return;
         }
-        const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;  // V operands, db even / odd
         for (int t = 0; t < ntiles; t++) {
             const int kbase = t * NK;
             const Stage& st = stage[t & 1];
@@ -587,11 +587,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
             // next tile, if the workgroup has one, in one go).
             const bool few = !plain && nkb > 0 && wave_kend - kbase <= kValuKeys;
             if (plain) {
-                attend_tile<MASK, BIAS, true, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g, voff_even,
-                                                 voff_odd, stage_next);
+                attend_tile<MASK, BIAS, true, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g,
+                                                 stage_next);
             } else if (nkb > 0 && !few) {
-                attend_tile<MASK, BIAS, false, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g, voff_even,
-                                                  voff_odd, stage_next);
+                attend_tile<MASK, BIAS, false, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g,
+                                                  stage_next);
             } else if (more) {
                 kvb_next = stage_all(nxt, nbase);
             }
@@ -749,7 +749,6 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
         store_thin(w, O, p, wq0, lane);
         return;
     }
-    const int voff_even = vslot(ql) * 4, voff_odd = vslot(16 + ql) * 4;
     auto no_hook = [](int, int) {};
     // 32-key tiles (two key blocks): half the score registers of a 64-key tile, for the 80-VGPR
     // budget, at the price of one more max/rescale per 64 keys.
@@ -765,11 +764,11 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) voi
         const float* kt = Ks + kbase * KPAD;
         const float* vt = Vs + (kbase >> 2) * (kHeadDim * 4);
         if (plain)
-            attend_tile<MASK, BIAS, true, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g, voff_even,
-                                             voff_odd, no_hook);
+            attend_tile<MASK, BIAS, true, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g,
+                                             no_hook);
         else
-            attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g, voff_even,
-                                              voff_odd, no_hook);
+            attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g,
+                                              no_hook);
     }
     if (kloop < wave_kend)
         attend_keys_valu<MASK, BIAS, false>(w, p, Ks + kloop * KPAD, Vs + (kloop >> 2) * (kHeadDim * 4), kadd + kloop,
