@@ -14,8 +14,10 @@ Other workloads (parity-test shapes, measured the same way):
   prefill  Timestral-shaped causal prefill, f16, B=32 rows H=16 L=2048, 10 % rows key-padded
   decode   Timestral-shaped KV-cached block decode, bf16, B=128 H=16, prefix 256 + 8 x 32;
            a step rewinds the cache to the prefix and runs 8 x (append 32, attend 32)
+  variate  Timestral variate attention at the prefill shape, f32: 8 series x 4 variates (target,
+           past, 2 known) over L=2048 slots, H=16, covariate firewalls, key padding, sigmoid gate
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode]
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
@@ -241,7 +243,38 @@ def run_decode(torch, ta, workloads, peak):
     return b
 
 
-WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode}
+def run_variate(torch, ta, workloads, peak):
+    w = workloads.timestral_variate()
+    a = w.arrays
+    G, V, L, H = w.meta["groups"], w.meta["vall"], w.meta["L"], w.H
+    d = H * 64
+    dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).cuda() for n in ("qkv", "gate", "key_valid")}
+    o = torch.empty((G * V, L, d), dtype=torch.float32, device="cuda")
+    roles = [int(r) for r in a["roles"]]
+
+    def step():
+        _check(ta, ta.timestral_variate_attention(dev["qkv"], o, dev["key_valid"], roles, True, G, V, L, 0, d, H, 64,
+                                                  gate=dev["gate"]))
+
+    def cpu_leg(n):
+        orc = _orc()
+        qkv = np.ascontiguousarray(a["qkv"][: n * V])
+        gate = np.ascontiguousarray(a["gate"][: n * V])
+        kv = np.ascontiguousarray(a["key_valid"][: n * V])
+        want = np.zeros((n * V, L, d), np.float32)
+        t0 = time.perf_counter()
+        orc.timestral_variate_attention(cpu_threads(), qkv, want, kv, a["roles"], True, n, V, L, 0, d, H, 64)
+        orc.mul_sigmoid(want, want, gate)
+        return time.perf_counter() - t0, want.reshape(n, V, L, d), orc.lanes
+
+    config = {"workload": w.name, "series": G, "variates": V, "H": H, "L": L, "D": 64, "roles": "target,past,known,known",
+              "covariates": True, "gate": "sigmoid", "layout": "qkv (rows, L, 3d) permuted, o and gate (rows, L, d) f32"}
+    return Bench(w, step, lambda: o.cpu().numpy().reshape(G, V, L, d), cpu_leg, config, "f32", "hbm",
+                 peak["hbm_gbps"], "GB/s", 1)
+
+
+WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
+             "variate": run_variate}
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
 

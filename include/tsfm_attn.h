@@ -148,6 +148,44 @@ uint32_t tsfm_t5_relative_bucket(int64_t rel, uint32_t num_buckets, uint32_t max
 int tsfm_t5_bucket_table(int32_t *out, int32_t n_q, int32_t n_k, uint32_t num_buckets, uint32_t max_distance);
 
 /* ---------------------------------------------------------------------------------------------
+ * Timestral variate attention. Replaces the forRangeMin(groups * sl, VariateJob.run) call of
+ * Model.variateAttention (src/timestral/model.zig:525-544, job at :648-709) and, when gate is set,
+ * the nn.mulSigmoid that follows it (:541, src/core/nn.zig:423-433).
+ *
+ * At every (series group g, token slot t) the vall rows r = g * vall + i of the group attend each
+ * other, per head: o[r, t, h] = sum_j softmax_j(scale * q[r, t, h] . k[g*vall + j, t, h]) v[...].
+ * Row i may read row j when i == j, or when (t >= n_enc or key_valid[(g*vall + j) * kv_row + t])
+ * and, with cov != 0, neither (role[i] != TARGET and role[j] == TARGET) nor (role[i] == KNOWN and
+ * role[j] != KNOWN). Roles are model.Role in declaration order (src/timestral/model.zig:89).
+ * With gate != NULL the result is multiplied by sigmoid(gate) (same layout as o) before it is stored.
+ * f32 only; vall <= 16 (more rows: TSFM_E_UNSUPPORTED, use the CPU path); head_dim 64. */
+enum { TSFM_ROLE_TARGET = 0, TSFM_ROLE_PAST = 1, TSFM_ROLE_KNOWN = 2 };
+
+typedef struct tsfm_variate_args {
+    int32_t dtype;     /* TSFM_DTYPE_F32 */
+    int32_t groups;    /* series */
+    int32_t vall;      /* rows per series, 1..16 */
+    int32_t n_tok;     /* token slots per row (sl = ne + h) */
+    int32_t n_enc;     /* encoder slots (ne): key_valid applies to slots t < n_enc */
+    int32_t heads;     /* H; d_model = heads * head_dim */
+    int32_t head_dim;  /* 64 */
+    int32_t cov;       /* non-zero: the covariate firewalls apply */
+    float scale;       /* 1/sqrt(head_dim) in the reference */
+    uint32_t flags;    /* TSFM_ATTN_DEVICE_PTRS or 0 */
+    /* Fused projection, element (r, t, part, h, c) at qkv + r*qkv_row + t*qkv_tok + part*heads*64
+     * + h*64 + c with part 0/1/2 = q/k/v (the permuted (token, qkv, head, head_dim) layout,
+     * src/timestral/model.zig:72-85). */
+    const void *qkv; int64_t qkv_row, qkv_tok;
+    void *o;         int64_t o_row, o_tok;     /* (r, t, h, c) */
+    const void *gate; int64_t gate_row, gate_tok; /* optional, as o */
+    const uint8_t *key_valid; int64_t kv_row;   /* (rows, n_enc) bytes */
+    uint8_t roles[16];                          /* role of row i of every series, i < vall */
+    void *stream;
+} tsfm_variate_args;
+
+int tsfm_variate_attend(const tsfm_variate_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * KV cache for block-autoregressive decode. No counterpart in the reference: Timestral's
  * blockDecode re-encodes the whole grown context every block (src/timestral/forecaster.zig:423-563),
  * recomputing K/V of unchanged prefix tokens. With a causal encoder and a fixed prefix the cached

@@ -643,6 +643,92 @@ void orc_timestral_time_attention(size_t threads, const float *qkv, float *o, co
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* Timestral variate attention, VariateJob.run (src/timestral/model.zig:648-709): at every
+ * (series group, token slot) the vall rows of the group attend each other, per head. The allowed
+ * matrix is built once per item: the diagonal is always open; another row is read on an encoder
+ * slot only if its patch is a valid key; with covariates, a non-target row never reads a target
+ * row and a known-future row never reads a non-known row. Scores nn.dot(q, k) * 1/sqrt(hd),
+ * nn.softmax, then o = sum of w * v over the rows with w != 0, in row order (mulAddInPlace). */
+
+typedef struct {
+    const float *qkv;
+    float *o;
+    const uint8_t *key_valid;
+    const uint8_t *roles;
+    int cov;
+    size_t vall, ne, sl, d, nh, hd;
+} ts_variate_job;
+
+enum { ORC_ROLE_TARGET = 0, ORC_ROLE_PAST = 1, ORC_ROLE_KNOWN = 2 }; /* model.zig:89 order */
+
+static void ts_variate_run(const void *p, size_t first, size_t last) {
+    const ts_variate_job *j = (const ts_variate_job *)p;
+    const size_t vall = j->vall, ne = j->ne, sl = j->sl, d = j->d, nh = j->nh, hd = j->hd;
+    const float sm_scale = 1.0f / sqrtf((float)hd);
+    const float ninf = -INFINITY;
+    float *sc = (float *)malloc(vall * sizeof(float));
+    uint8_t *allowed = (uint8_t *)malloc(vall * vall);
+    for (size_t item = first; item < last; item++) {
+        const size_t g = item / sl, tok = item % sl, r0 = g * vall;
+        for (size_t iq = 0; iq < vall; iq++)
+            for (size_t ik = 0; ik < vall; ik++) {
+                int ok = ik == iq;
+                if (!ok) {
+                    const int valid = tok >= ne || j->key_valid[(r0 + ik) * ne + tok];
+                    int forbidden = 0;
+                    if (j->cov) {
+                        const int rq = j->roles[iq], rk = j->roles[ik];
+                        forbidden = (rq != ORC_ROLE_TARGET && rk == ORC_ROLE_TARGET) ||
+                                    (rq == ORC_ROLE_KNOWN && rk != ORC_ROLE_KNOWN);
+                    }
+                    ok = valid && !forbidden;
+                }
+                allowed[iq * vall + ik] = (uint8_t)ok;
+            }
+        for (size_t hh = 0; hh < nh; hh++) {
+            const size_t qoff = hh * hd;
+            for (size_t iq = 0; iq < vall; iq++) {
+                const float *qsrc = j->qkv + (r0 + iq) * sl * 3 * d + tok * 3 * d + qoff;
+                for (size_t ik = 0; ik < vall; ik++) {
+                    if (!allowed[iq * vall + ik]) {
+                        sc[ik] = ninf;
+                        continue;
+                    }
+                    const float *ksrc = j->qkv + (r0 + ik) * sl * 3 * d + tok * 3 * d + d + qoff;
+                    sc[ik] = orc_dot(qsrc, ksrc, hd) * sm_scale;
+                }
+                orc_softmax(sc, vall);
+                float *dst = j->o + (r0 + iq) * sl * d + tok * d + qoff;
+                memset(dst, 0, hd * sizeof(float));
+                for (size_t ik = 0; ik < vall; ik++) {
+                    const float w = sc[ik];
+                    if (w == 0) continue;
+                    orc_mul_add_in_place(dst, j->qkv + (r0 + ik) * sl * 3 * d + tok * 3 * d + 2 * d + qoff, hd, w);
+                }
+            }
+        }
+    }
+    free(allowed);
+    free(sc);
+}
+
+void orc_timestral_variate_attention(size_t threads, const float *qkv, float *o, const uint8_t *key_valid,
+                                     const uint8_t *roles, int cov, size_t groups, size_t vall, size_t ne,
+                                     size_t h, size_t d, size_t nh, size_t hd) {
+    const ts_variate_job job = {qkv, o, key_valid, roles, cov, vall, ne, ne + h, d, nh, hd};
+    orc_for_range_min(threads, groups * (ne + h), 8, &job, ts_variate_run);
+}
+
+/* nn.mulSigmoid (src/core/nn.zig:423-433): dst = x / (1 + expVec(-g)) over whole vectors (unfused
+ * division), x * sigmoid(g) = x * (1 / (1 + @exp(-g))) over the tail. */
+void orc_mul_sigmoid(float *dst, const float *x, const float *g, size_t n) {
+    size_t i = 0;
+    for (; i + L <= n; i += L)
+        for (int e = 0; e < L; e++) dst[i + e] = x[i + e] / (1.0f + orc_exp_vec(-g[i + e]));
+    for (; i < n; i++) dst[i] = x[i] * (1.0f / (1.0f + expf(-g[i])));
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* Generic batched selfAttend. */
 
 typedef struct {

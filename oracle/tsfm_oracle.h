@@ -109,6 +109,16 @@ void orc_timestral_time_attention(size_t threads, const float *qkv, float *o, co
                                   int keys_all_valid, const uint8_t *bidir, size_t rows, size_t ne,
                                   size_t l, size_t h, size_t d, size_t nh, size_t hd);
 
+/* Timestral variate attention (VariateJob.run, src/timestral/model.zig:648-709). qkv (rows*sl, 3d)
+ * with rows = groups * vall, o (rows*sl, d), key_valid (rows, ne), roles (vall) in
+ * model.Role order (target, past, known); sl = ne + h. */
+void orc_timestral_variate_attention(size_t threads, const float *qkv, float *o, const uint8_t *key_valid,
+                                     const uint8_t *roles, int cov, size_t groups, size_t vall, size_t ne,
+                                     size_t h, size_t d, size_t nh, size_t hd);
+
+/* nn.mulSigmoid (src/core/nn.zig:423-433). */
+void orc_mul_sigmoid(float *dst, const float *x, const float *g, size_t n);
+
 /* Batched selfAttend over (b, h) items with (token, head, dim) layouts: the generic form of
  * the three family jobs above, used by the tests for shapes the families do not fix.
  * q/k/v/o strides: token stride and batch stride in floats; head h at +h*hd. */

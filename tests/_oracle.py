@@ -49,6 +49,9 @@ class Oracle:
         L.orc_timestral_rope_tables.argtypes = [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _f, _vp]
         L.orc_timestral_rope.argtypes = [_sz, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz]
         L.orc_timestral_time_attention.argtypes = [_sz, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.orc_timestral_variate_attention.argtypes = [_sz, _vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _sz, _sz, _sz,
+                                                      _sz]
+        L.orc_mul_sigmoid.argtypes = [_vp, _vp, _vp, _sz]
         L.orc_batched_self_attend.argtypes = [_sz, ctypes.c_int, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz,
                                               _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
 
@@ -138,6 +141,13 @@ class Oracle:
     def timestral_time_attention(self, threads, qkv, o, key_valid, keys_all_valid, bidir, rows, ne, l, h, d, nh, hd):
         self.lib.orc_timestral_time_attention(threads, ptr(qkv), ptr(o), ptr(key_valid), int(keys_all_valid),
                                               ptr(bidir), rows, ne, l, h, d, nh, hd)
+
+    def timestral_variate_attention(self, threads, qkv, o, key_valid, roles, cov, groups, vall, ne, h, d, nh, hd):
+        self.lib.orc_timestral_variate_attention(threads, ptr(qkv), ptr(o), ptr(key_valid), ptr(roles), int(cov), groups,
+                                                 vall, ne, h, d, nh, hd)
+
+    def mul_sigmoid(self, dst, x, g):
+        self.lib.orc_mul_sigmoid(ptr(dst), ptr(x), ptr(g), x.size)
 
     def batched_self_attend(self, threads, mask, q, q_tok, q_batch, k, k_tok, k_batch, v, v_tok, v_batch, o, o_tok,
                             o_batch, key_valid, kv_batch, bias, nb, nh, n, hd, scale):

@@ -103,3 +103,46 @@ def f64_errors(outs, q, k, v, key_valid, n_series, heads, n, scale, bias=None, m
     with ThreadPoolExecutor(threads) as ex:
         per = list(ex.map(one, range(n_series)))
     return [max(e[i] for e in per) for i in range(len(outs))]
+
+
+ROLE_TARGET, ROLE_PAST, ROLE_KNOWN = 0, 1, 2
+
+
+def variate_allowed(vall, tok, ne, key_valid_rows, roles, cov):
+    """(vall, vall) bool: row iq may read row ik at token slot tok (diagonal always; else the key is
+    valid on an encoder slot, and with covariates no non-target -> target and no known -> non-known
+    edge)."""
+    a = np.zeros((vall, vall), bool)
+    for iq in range(vall):
+        for ik in range(vall):
+            if iq == ik:
+                a[iq, ik] = True
+                continue
+            valid = tok >= ne or bool(key_valid_rows[ik, tok])
+            bad = cov and ((roles[iq] != ROLE_TARGET and roles[ik] == ROLE_TARGET) or
+                           (roles[iq] == ROLE_KNOWN and roles[ik] != ROLE_KNOWN))
+            a[iq, ik] = valid and not bad
+    return a
+
+
+def variate_attend_f64(qkv, key_valid, roles, cov, groups, vall, ne, h, d, nh, hd):
+    """Variate attention in float64 from its definition: per (group, token slot, head), softmax over
+    the allowed rows of q.k / sqrt(hd), then the weighted sum of v. qkv (groups*vall, sl, 3d)."""
+    sl = ne + h
+    x = qkv.reshape(groups * vall, sl, 3 * d).astype(np.float64)
+    kv = key_valid.reshape(groups * vall, ne)
+    o = np.zeros((groups * vall, sl, d))
+    for g in range(groups):
+        rows = slice(g * vall, (g + 1) * vall)
+        for tok in range(sl):
+            allowed = variate_allowed(vall, tok, ne, kv[rows], roles, cov)
+            for hh in range(nh):
+                c = slice(hh * hd, (hh + 1) * hd)
+                q = x[rows, tok, c]
+                k = x[rows, tok, d + hh * hd:d + (hh + 1) * hd]
+                v = x[rows, tok, 2 * d + hh * hd:2 * d + (hh + 1) * hd]
+                s = np.where(allowed, q @ k.T / np.sqrt(hd), -np.inf)
+                w = np.exp(s - s.max(axis=1, keepdims=True))
+                w /= w.sum(axis=1, keepdims=True)
+                o[rows, tok, c] = w @ v
+    return o

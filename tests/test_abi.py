@@ -31,21 +31,23 @@ def test_library_exports_every_declared_symbol(ta):
     assert not missing, missing
 
 
-def test_args_struct_layout_matches_header(ta):
+@pytest.mark.parametrize("struct,cname", [("AttnArgs", "tsfm_attn_args"), ("VariateArgs", "tsfm_variate_args")])
+def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
-    fields = [f[0] for f in ta.AttnArgs._fields_]
+    cls = getattr(ta, struct)
+    fields = [f[0] for f in cls._fields_]
     src = "#include <stdio.h>\n#include <stddef.h>\n#include \"tsfm_attn.h\"\nint main(void){\n"
-    src += 'printf("%zu\\n", sizeof(tsfm_attn_args));\n'
+    src += f'printf("%zu\\n", sizeof({cname}));\n'
     for f in fields:
-        src += f'printf("%zu\\n", offsetof(tsfm_attn_args, {f}));\n'
+        src += f'printf("%zu\\n", offsetof({cname}, {f}));\n'
     src += "return 0;}\n"
-    tmp = pathlib.Path(os.environ.get("TMPDIR", "/tmp")) / f"tsfm_layout_{os.getpid()}"
+    tmp = pathlib.Path(os.environ.get("TMPDIR", "/tmp")) / f"tsfm_layout_{os.getpid()}_{cname}"
     tmp.mkdir(exist_ok=True)
     (tmp / "l.c").write_text(src)
     subprocess.run(["gcc", "-I", str(ROOT / "include"), "-o", str(tmp / "l"), str(tmp / "l.c")], check=True)
     got = [int(x) for x in subprocess.run([str(tmp / "l")], capture_output=True, text=True, check=True).stdout.split()]
-    assert got[0] == ctypes.sizeof(ta.AttnArgs)
-    assert got[1:] == [getattr(ta.AttnArgs, f).offset for f in fields]
+    assert got[0] == ctypes.sizeof(cls)
+    assert got[1:] == [getattr(cls, f).offset for f in fields]
 
 
 def test_t5_bucket_host_function_golden(ta):
@@ -125,3 +127,40 @@ def test_kv_cache_rejects_f32(ta):
     h = ctypes.c_void_p()
     assert lib.tsfm_kv_create(ctypes.byref(h), ta.DTYPE_F32, 1, 1, 64, 32) == ta.E_UNSUPPORTED
     assert not h.value
+
+
+def _variate_host_args(ta, **over):
+    groups, vall, ne, h, nh = 2, 3, 5, 2, 2
+    sl, d = ne + h, nh * 64
+    qkv = np.zeros(groups * vall * sl * 3 * d, np.float32)
+    o = np.zeros(groups * vall * sl * d, np.float32)
+    kv = np.ones(groups * vall * ne, np.uint8)
+    kw = dict(dtype=ta.DTYPE_F32, groups=groups, vall=vall, n_tok=sl, n_enc=ne, heads=nh, head_dim=64, cov=1,
+              scale=0.125, qkv=qkv.ctypes.data, qkv_row=sl * 3 * d, qkv_tok=3 * d, o=o.ctypes.data, o_row=sl * d,
+              o_tok=d, key_valid=kv.ctypes.data, kv_row=ne)
+    kw.update(over)
+    roles = kw.pop("roles", [0, 1, 2])
+    a = ta.VariateArgs(**kw)
+    for i, r in enumerate(roles):
+        a.roles[i] = r
+    return a, (qkv, o, kv)
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(vall=17), 2),            # more rows than one 16-slot score block
+    (dict(dtype=2), 2),            # f32 only
+    (dict(head_dim=32), 2),
+    (dict(n_enc=9), 3),            # more encoder slots than tokens
+    (dict(roles=[0, 3, 1]), 3),    # not a model.Role
+    (dict(key_valid=None), 3),
+    (dict(o_tok=130), 2),          # strides in whole 16-byte units
+])
+def test_variate_validation_codes(ta, over, code):
+    a, _keep = _variate_host_args(ta, **over)
+    assert ta.variate_attend(a) == code
+    assert ta.last_error()
+
+
+def test_variate_empty_is_a_no_op(ta):
+    a, _keep = _variate_host_args(ta, groups=0)
+    assert ta.variate_attend(a) == ta.OK

@@ -414,3 +414,85 @@ def test_lane_counts_agree(orc, orc16):
         orc.self_attend(mask, q, k, v, o8, (hd,) * 4, n, hd, 0.125, kv, None)
         orc16.self_attend(mask, q, k, v, o16, (hd,) * 4, n, hd, 0.125, kv, None)
         assert _ref.scaled_err(o16, o8) < 1e-6
+
+
+# ---- Timestral variate attention (VariateJob.run, src/timestral/model.zig:648-709) -------------
+
+
+def _variate_inputs(seed, groups, vall, ne, h, d, p_valid=0.7):
+    rng = np.random.default_rng(seed)
+    sl = ne + h
+    qkv = rng.standard_normal((groups * vall, sl, 3 * d)).astype(np.float32)
+    kv = (rng.random((groups * vall, ne)) < p_valid).astype(np.uint8)
+    return qkv, kv
+
+
+@pytest.mark.parametrize("vall,cov", [(1, False), (3, False), (5, True), (8, True)])
+def test_variate_attention_matches_f64(orc, vall, cov):
+    groups, ne, h, nh, hd = 3, 9, 4, 2, 16
+    d = nh * hd
+    qkv, kv = _variate_inputs(vall, groups, vall, ne, h, d)
+    roles = np.array(([_ref.ROLE_TARGET, _ref.ROLE_PAST, _ref.ROLE_KNOWN] * 4)[:vall], np.uint8)
+    o = np.zeros((groups * vall, ne + h, d), np.float32)
+    orc.timestral_variate_attention(4, qkv, o, kv, roles, cov, groups, vall, ne, h, d, nh, hd)
+    want = _ref.variate_attend_f64(qkv, kv, roles, cov, groups, vall, ne, h, d, nh, hd)
+    assert _ref.scaled_err(o, want) <= 1e-5
+
+
+def test_variate_singleton_is_v(orc):
+    """vall = 1: every row reads only itself, so o = v exactly (the survey's singleton pin)."""
+    groups, ne, h, nh, hd = 4, 7, 3, 2, 16
+    d = nh * hd
+    qkv, kv = _variate_inputs(1, groups, 1, ne, h, d, p_valid=0.0)
+    o = np.zeros((groups, ne + h, d), np.float32)
+    orc.timestral_variate_attention(2, qkv, o, kv, np.zeros(1, np.uint8), False, groups, 1, ne, h, d, nh, hd)
+    assert np.array_equal(o, qkv[:, :, 2 * d:])
+
+
+def test_variate_firewalls_and_validity(orc):
+    """What a row may not read does not move its output: with covariates, past/known rows ignore
+    the target row; known rows ignore past rows; on encoder slots an invalid key row is ignored,
+    on decoder slots (tok >= ne) it is read."""
+    groups, vall, ne, h, nh, hd = 1, 4, 6, 3, 2, 16
+    d = nh * hd
+    roles = np.array([_ref.ROLE_TARGET, _ref.ROLE_PAST, _ref.ROLE_KNOWN, _ref.ROLE_KNOWN], np.uint8)
+    qkv, kv = _variate_inputs(11, groups, vall, ne, h, d, p_valid=1.0)
+    kv[3, 2] = 0  # row 3 is not a valid key at slot 2
+
+    def run(x):
+        o = np.zeros((vall, ne + h, d), np.float32)
+        orc.timestral_variate_attention(1, x, o, kv, roles, True, groups, vall, ne, h, d, nh, hd)
+        return o
+
+    base = run(qkv)
+    bumped = qkv.copy()
+    bumped[0, :, d:] += 3.0  # the target row's k and v
+    o = run(bumped)
+    assert np.array_equal(o[1:], base[1:]) and not np.array_equal(o[0], base[0])
+    bumped = qkv.copy()
+    bumped[1, :, d:] += 3.0  # the past row's k and v: the target reads it, known rows do not
+    o = run(bumped)
+    assert np.array_equal(o[2:], base[2:]) and not np.array_equal(o[0], base[0])
+    bumped = qkv.copy()
+    bumped[3, 2, d:] += 3.0  # invalid key at encoder slot 2: only row 3 itself sees it
+    o = run(bumped)
+    assert np.array_equal(o[:3, 2], base[:3, 2]) and not np.array_equal(o[3, 2], base[3, 2])
+    kv2 = kv.copy()
+    kv2[:] = 0  # decoder slots read every row whatever key_valid says
+    o2 = np.zeros((vall, ne + h, d), np.float32)
+    orc.timestral_variate_attention(1, qkv, o2, kv2, roles, True, groups, vall, ne, h, d, nh, hd)
+    assert np.array_equal(o2[:, ne:], base[:, ne:])
+
+
+def test_mul_sigmoid_closed_form(orc):
+    rng = np.random.default_rng(5)
+    n = 37  # whole vectors and a tail
+    x = rng.standard_normal(n).astype(np.float32)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    out = np.zeros(n, np.float32)
+    orc.mul_sigmoid(out, x, g)
+    want = x.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    assert np.max(np.abs(out - want)) <= 1e-6 * max(1.0, np.abs(want).max())
+    zero = np.zeros(n, np.float32)
+    orc.mul_sigmoid(out, x, zero)
+    assert np.array_equal(out, x * np.float32(0.5))  # sigmoid(0) = 1/2 exactly

@@ -353,6 +353,83 @@ int tsfm_attn_fwd(const tsfm_attn_args* a) {
     return TSFM_OK;
 }
 
+// ---- Timestral variate attention ----------------------------------------------------------------
+
+int tsfm_variate_attend(const tsfm_variate_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (a->dtype != TSFM_DTYPE_F32) return fail(TSFM_E_UNSUPPORTED, "variate attention is f32 only");
+    if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
+    if (a->groups < 0 || a->vall < 0 || a->n_tok < 0 || a->n_enc < 0 || a->heads < 0)
+        return fail(TSFM_E_INVALID, "negative size");
+    if (a->vall > 16) return fail(TSFM_E_UNSUPPORTED, "vall %d (supported: up to 16 rows per series)", a->vall);
+    if (a->n_enc > a->n_tok) return fail(TSFM_E_INVALID, "n_enc %d > n_tok %d", a->n_enc, a->n_tok);
+    if (a->qkv == nullptr || a->o == nullptr) return fail(TSFM_E_INVALID, "qkv and o are required");
+    for (int32_t i = 0; i < a->vall; i++)
+        if (a->roles[i] > TSFM_ROLE_KNOWN) return fail(TSFM_E_INVALID, "roles[%d] = %d", i, a->roles[i]);
+    if (a->n_enc > 0 && a->vall > 1 && a->key_valid == nullptr) return fail(TSFM_E_INVALID, "key_valid is required");
+    if (a->qkv_row < 0 || a->qkv_tok < 0 || a->o_row < 0 || a->o_tok < 0 || a->gate_row < 0 || a->gate_tok < 0 ||
+        a->kv_row < 0)
+        return fail(TSFM_E_INVALID, "negative stride");
+    if (a->key_valid != nullptr && a->kv_row < a->n_enc && a->groups * a->vall > 1)
+        return fail(TSFM_E_INVALID, "kv_row %lld shorter than n_enc %d", (long long)a->kv_row, a->n_enc);
+    if (a->qkv_row % 4 || a->qkv_tok % 4 || a->o_row % 4 || a->o_tok % 4 || a->gate_row % 4 || a->gate_tok % 4)
+        return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    if (a->groups == 0 || a->vall == 0 || a->n_tok == 0 || a->heads == 0) return TSFM_OK;  // nothing to compute
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+
+    tsfm::VariateParams p{};
+    p.qkv = static_cast<const float*>(a->qkv); p.qkv_row = a->qkv_row; p.qkv_tok = a->qkv_tok;
+    p.o = static_cast<float*>(a->o); p.o_row = a->o_row; p.o_tok = a->o_tok;
+    p.gate = static_cast<const float*>(a->gate); p.gate_row = a->gate_row; p.gate_tok = a->gate_tok;
+    p.key_valid = a->key_valid; p.kv_row = a->kv_row;
+    for (int i = 0; i < 16; i++) p.roles[i >> 2] |= (uint32_t)(i < a->vall ? a->roles[i] : 0) << (8 * (i & 3));
+    p.groups = a->groups; p.vall = a->vall; p.n_tok = a->n_tok; p.n_enc = a->n_enc; p.heads = a->heads;
+    p.cov = a->cov != 0; p.scale = a->scale;
+    hipError_t e;
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
+        if (!aligned(a->qkv, 16) || !aligned(a->o, 16) || (a->gate != nullptr && !aligned(a->gate, 16)))
+            return fail(TSFM_E_UNSUPPORTED, "device qkv/o/gate must be 16-byte aligned");
+        e = tsfm::launch_variate(p, static_cast<hipStream_t>(a->stream));
+        if (e != hipSuccess) return hip_fail(e, "variate attention launch");
+        return TSFM_OK;
+    }
+    // Host pointers: stage every input, run, copy the output rows back, synchronise.
+    const int64_t rows = (int64_t)a->groups * a->vall, D = (int64_t)a->heads * a->head_dim;
+    const size_t qkv_n = span(rows, a->n_tok, a->qkv_tok, a->qkv_row, 3 * D) * 4;
+    const size_t o_n = span(rows, a->n_tok, a->o_tok, a->o_row, D) * 4;
+    const size_t g_n = a->gate ? span(rows, a->n_tok, a->gate_tok, a->gate_row, D) * 4 : 0;
+    const size_t kv_n = a->key_valid && a->n_enc > 0 ? (size_t)span(rows, 1, 0, a->kv_row, a->n_enc) : 0;
+    Plan plan;
+    const size_t qkv_at = plan.take(qkv_n), o_at = plan.take(o_n), g_at = plan.take(g_n), kv_at = plan.take(kv_n);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    struct Up { const void* src; size_t at, n; } ups[] = {
+        {a->qkv, qkv_at, qkv_n}, {a->gate, g_at, g_n}, {a->key_valid, kv_at, kv_n}};
+    for (const Up& u : ups) {
+        if (u.n == 0 || u.src == nullptr) continue;
+        if ((e = hipMemcpyAsync(base + u.at, u.src, u.n, hipMemcpyHostToDevice, s)) != hipSuccess)
+            return hip_fail(e, "host-to-device copy");
+    }
+    p.qkv = reinterpret_cast<const float*>(base + qkv_at);
+    p.o = reinterpret_cast<float*>(base + o_at);
+    if (a->gate) p.gate = reinterpret_cast<const float*>(base + g_at);
+    p.key_valid = kv_n > 0 ? reinterpret_cast<const uint8_t*>(base + kv_at) : nullptr;
+    e = tsfm::launch_variate(p, s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "variate attention launch");
+    }
+    if ((e = copy_rows_d2h(a->o, base + o_at, rows, a->n_tok, a->o_row * 4, a->o_tok * 4, D * 4, s)) != hipSuccess)
+        return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
 // ---- KV cache ------------------------------------------------------------------------------------
 
 struct tsfm_kv_cache {

@@ -26,4 +26,18 @@ hipError_t launch_kv_attend(const KvLayout& c, bool is_bf16, const void* q, int6
                             void* o, int64_t o_tok, int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k,
                             float scale, hipStream_t stream);
 
+// Timestral variate attention (variate.hip). f32; vall <= 16.
+constexpr int kRoleTarget = 0, kRoleKnown = 2;  // model.Role (src/timestral/model.zig:89)
+struct VariateParams {
+    const float* qkv; int64_t qkv_row, qkv_tok;
+    float* o; int64_t o_row, o_tok;
+    const float* gate; int64_t gate_row, gate_tok;
+    const uint8_t* key_valid; int64_t kv_row;
+    uint32_t roles[4];  // 16 role bytes, row i in byte i
+    int32_t groups, vall, n_tok, n_enc, heads, cov;
+    float scale;
+    int32_t heads_per_block, nblk;  // set by launch_variate
+};
+hipError_t launch_variate(const VariateParams& p, hipStream_t stream);
+
 }  // namespace tsfm

@@ -55,6 +55,7 @@ EXPORTS = (
     "tsfm_attn_last_error",
     "tsfm_t5_relative_bucket",
     "tsfm_t5_bucket_table",
+    "tsfm_variate_attend",
     "tsfm_kv_create",
     "tsfm_kv_free",
     "tsfm_kv_reset",
@@ -150,6 +151,39 @@ class AttnArgs(ctypes.Structure):
 _lib: Optional[ctypes.CDLL] = None
 
 
+class VariateArgs(ctypes.Structure):
+    """``tsfm_variate_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("groups", ctypes.c_int32),
+        ("vall", ctypes.c_int32),
+        ("n_tok", ctypes.c_int32),
+        ("n_enc", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("cov", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("flags", ctypes.c_uint32),
+        ("qkv", ctypes.c_void_p),
+        ("qkv_row", ctypes.c_int64),
+        ("qkv_tok", ctypes.c_int64),
+        ("o", ctypes.c_void_p),
+        ("o_row", ctypes.c_int64),
+        ("o_tok", ctypes.c_int64),
+        ("gate", ctypes.c_void_p),
+        ("gate_row", ctypes.c_int64),
+        ("gate_tok", ctypes.c_int64),
+        ("key_valid", ctypes.c_void_p),
+        ("kv_row", ctypes.c_int64),
+        ("roles", ctypes.c_uint8 * 16),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+ROLE_TARGET, ROLE_PAST, ROLE_KNOWN = 0, 1, 2  # model.Role (src/timestral/model.zig:89)
+
+
 def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     """Load libtsfm_attn.so (built in-tree by ``make -C tsfm-zig_amd``). Raises if it is missing."""
     global _lib
@@ -192,6 +226,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_kv_append.restype = ctypes.c_int
     lib.tsfm_kv_attend.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, ctypes.c_float, u32, vp]
     lib.tsfm_kv_attend.restype = ctypes.c_int
+    lib.tsfm_variate_attend.argtypes = [ctypes.POINTER(VariateArgs)]
+    lib.tsfm_variate_attend.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -416,6 +452,31 @@ def timestral_time_attention(qkv, o, cos_t, sin_t, key_valid, keys_all_valid: bo
         q=_flat_view(qkv, ne * 3 * d), k=_flat_view(qkv, d), v=_flat_view(qkv, 2 * d), o=_flat_view(o, ne * d),
         mask=Mask.DECODER, batch=rows, n_q=h, n_k=sl, q_pos0=ne, ctx_keys=l, chain_start=ne,
         **{**common, "key_valid": key_valid}))
+
+
+def variate_attend(args: VariateArgs) -> int:
+    """``tsfm_variate_attend``: returns the ABI code."""
+    return int(load().tsfm_variate_attend(ctypes.byref(args)))
+
+
+def timestral_variate_attention(qkv, o, key_valid, roles: Sequence[int], cov: bool, groups: int, vall: int, ne: int,
+                                h: int, d: int, nh: int, hd: int, gate=None, stream=None) -> int:
+    """Timestral variate attention (Model.variateAttention, src/timestral/model.zig:525-544): the
+    forRangeMin(groups * sl, VariateJob.run) call and, with ``gate``, the nn.mulSigmoid after it.
+    qkv is (groups * vall, sl, 3d) in the permuted (token, qkv, head, hd) layout, o and gate are
+    (groups * vall, sl, d), key_valid (groups * vall, ne); ``roles`` holds vall model.Role values.
+    Device tensors run asynchronously on ``stream`` (default: torch's current stream); numpy arrays
+    are staged through the library and the call returns when o is written."""
+    sl = ne + h
+    device = _is_device(qkv)
+    role_bytes = (ctypes.c_uint8 * 16)(*[int(r) for r in list(roles)[:16]])
+    a = VariateArgs(dtype=_dtype_code(qkv), groups=groups, vall=vall, n_tok=sl, n_enc=ne, heads=nh, head_dim=hd,
+                    cov=int(bool(cov)), scale=1.0 / math.sqrt(hd), flags=DEVICE_PTRS if device else 0,
+                    qkv=_ptr(qkv), qkv_row=sl * 3 * d, qkv_tok=3 * d, o=_ptr(o), o_row=sl * d, o_tok=d,
+                    gate=_ptr(gate), gate_row=sl * d if gate is not None else 0, gate_tok=d if gate is not None else 0,
+                    key_valid=_ptr(key_valid), kv_row=ne, roles=role_bytes,
+                    stream=_stream_of(qkv, stream) if device else None)
+    return variate_attend(a)
 
 
 # ---------------------------------------------------------------------------------------------

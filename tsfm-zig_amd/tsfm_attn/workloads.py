@@ -141,3 +141,27 @@ def timestral_decode(B: int = 128, H: int = 16, prefix: int = 256, blocks: int =
     # q + o of the decoded blocks, the new K/V written once, and every block's cache read.
     w.meta["bytes"] = float(B * H * (2 * blocks * block * D * 2 + 2 * blocks * block * D * 2) + B * H * reread)
     return w
+
+
+def timestral_variate(groups: int = 8, vall: int = 4, H: int = 16, L: int = 2048, seed: int = 0,
+                      pad_rows: float = 0.1, pad_keys: int = 512) -> Workload:
+    """Timestral variate attention at the prefill shape: `groups` series of `vall` rows (target,
+    past covariate, two known-future covariates) over L token slots; at every slot the rows of a
+    series attend each other, per head, with the covariate firewalls and key validity; the result
+    is gated by sigmoid(gate). f32 (the reference arithmetic). FLOPs count the vall x vall pairs of
+    every (series, slot, head); bytes are the fused qkv, the gate and o, once."""
+    D = 64
+    d = H * D
+    rows = groups * vall
+    rng = np.random.default_rng(seed)
+    qkv = rng.standard_normal((rows, L, 3 * d), dtype=np.float32)
+    gate = rng.standard_normal((rows, L, d), dtype=np.float32)
+    padded = rng.random(rows) < pad_rows
+    kv = np.ones((rows, L), np.uint8)
+    kv[padded, :pad_keys] = 0
+    roles = np.array(([0, 1, 2, 2] * 4)[:vall], np.uint8)
+    w = Workload("timestral_variate_attention", "f32", groups, H, vall, vall, D, 1.0 / np.sqrt(D),
+                 dict(qkv=qkv, gate=gate, key_valid=kv, roles=roles),
+                 dict(seed=seed, groups=groups, vall=vall, L=L, pairs=groups * L * H * vall * vall))
+    w.meta["bytes"] = 4.0 * rows * L * (3 * d + d + d)
+    return w
