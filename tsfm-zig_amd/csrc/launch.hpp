@@ -37,6 +37,7 @@ struct VariateParams {
     int32_t groups, vall, n_tok, n_enc, heads, cov;
     float scale;
     int32_t heads_per_block, nblk;  // set by launch_variate
+    uint32_t qkv_span_bytes;         // set by launch_variate
 };
 hipError_t launch_variate(const VariateParams& p, hipStream_t stream);
 

@@ -3,7 +3,8 @@
 // The reference's VariateJob.run (src/timestral/model.zig:648-709): at every (series group g,
 // token slot t) the vall rows of the group attend each other, per head, through a vall x vall
 // allowed matrix (diagonal always open; key validity on encoder slots; the covariate firewalls).
-// Here one wave takes one (g, t) and a block of heads: with vall rows per head, 16 / vall heads
+// Here one wave takes one (g, t) and a block of heads (a workgroup, every head block of one (g, t)):
+// with vall rows per head, 16 / vall heads
 // share one 16 x 16 score block (slot s = head-in-block * vall + row), so one set of
 // v_mfma_f32_16x16x4_f32 serves several heads; scores between different heads are masked out.
 //
@@ -12,81 +13,86 @@
 //   softmax         per query slot over the four 16-lane groups (max4 / sum4), exp2-based.
 //   O^T += V^T P^T  4 key steps x 4 dim blocks, P straight from the S^T accumulator.
 //
-// Operands come straight from HBM (each (g, t) is read once): q and k as 16-byte loads of the
-// lane's dims, v as 4-byte loads of 16 consecutive dims. An optional gate multiplies the result by
-// sigmoid(gate) before the store (nn.mulSigmoid, src/core/nn.zig:423-433, fused).
+// Operands come straight from HBM (each (g, t) is read once), through one buffer descriptor over
+// the token's rows: q and k as 16-byte loads of the lane's dims, v as 4-byte loads of 16
+// consecutive dims. An optional gate multiplies the result by sigmoid(gate) before the store
+// (nn.mulSigmoid, src/core/nn.zig:423-433, fused; the reciprocal is v_rcp_f32, within 1 ulp of the
+// reference's division).
 #include "common.hpp"
 #include "launch.hpp"
 
 namespace tsfm {
 namespace {
 
-__global__ __launch_bounds__(64) void variate_attend(VariateParams p) {
+// One head block of one (group, token) item.
+__device__ __forceinline__ void variate_block(const VariateParams& p, int item, int blk, int lane) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x, ql = lane & 15, g = lane >> 4;
-    const int vall = p.vall, slots = p.heads_per_block * vall;
-    const int64_t bid = blockIdx.x;
-    const int blk = (int)(bid % p.nblk);
-    const int64_t item = bid / p.nblk;
-    const int grp = (int)(item / p.n_tok), tok = (int)(item % p.n_tok);
+    const int ql = lane & 15, g = lane >> 4;
+    const int vall = p.vall;
+    const int grp = item / p.n_tok, tok = item % p.n_tok;
     const int h0 = blk * p.heads_per_block;
+    const int heads_here = min(p.heads_per_block, p.heads - h0);
+    const int live = heads_here * vall;  // valid slots of this block
     const int64_t r0 = (int64_t)grp * vall;
     const int dm = p.heads * kHeadDim;  // d_model: offset of k, and 2 * dm of v, in a token's qkv
-    const float* __restrict__ tokq = p.qkv + r0 * p.qkv_row + (int64_t)tok * p.qkv_tok;
 
-    // Slot s of the block: head h0 + s / vall, row s % vall; valid while s < slots and the head
-    // exists (the last block may hold fewer heads).
-    auto slot_ok = [&](int s) { return s < slots && h0 + s / vall < p.heads; };
-    auto slot_ptr = [&](int s, int part) {
-        return tokq + (int64_t)(s % vall) * p.qkv_row + part * dm + (h0 + s / vall) * kHeadDim;
+    // Slot s < 16 of the block: head h0 + s / vall, row s % vall. s / vall by a multiply and a
+    // shift (exact for s < 16 with the rounded-up 16-bit reciprocal).
+    const uint32_t rcp = (65536u + (uint32_t)vall - 1u) / (uint32_t)vall;
+    auto sdiv = [&](int s) { return (int)(((uint32_t)s * rcp) >> 16); };
+
+    // The vall rows of this token, through one buffer descriptor: a slot's byte offset is
+    // row * qkv_row + part * dm + head * 64 (+ dims); offsets of slots past `live` are pushed out of
+    // range, where loads return 0 (no branch, no exec mask).
+    const float* tokq = p.qkv + r0 * p.qkv_row + (int64_t)tok * p.qkv_tok;
+    const __amdgpu_buffer_rsrc_t qb = make_buf(tokq, p.qkv_span_bytes);
+    auto slot_off = [&](int s, int part) -> uint32_t {
+        const int hs = sdiv(s), row = s - hs * vall;
+        const uint32_t off = (uint32_t)(row * p.qkv_row + part * dm + (h0 + hs) * kHeadDim) * 4u;
+        return s < live ? off : 0x80000000u;
     };
 
     // ---- operands of S^T: lane (ql, g) holds dims 8g..8g+7 and 32+8g..32+8g+7 of query slot ql
     //      (B operand) and of key slot ql (A operand) ----
-    const bool row_ok = slot_ok(ql);
-    f32x4 qv[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-    f32x4 kv[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-    if (row_ok) {
-        const float* qs = slot_ptr(ql, 0) + 8 * g;
-        const float* ks = slot_ptr(ql, 1) + 8 * g;
-        qv[0] = ld4(qs);
-        qv[1] = ld4(qs + 4);
-        qv[2] = ld4(qs + 32);
-        qv[3] = ld4(qs + 36);
-        kv[0] = ld4(ks);
-        kv[1] = ld4(ks + 4);
-        kv[2] = ld4(ks + 32);
-        kv[3] = ld4(ks + 36);
-    }
+    const uint32_t qo = slot_off(ql, 0) + 32u * g, ko = slot_off(ql, 1) + 32u * g;
+    f32x4 qv[4], kv[4];
+    qv[0] = bld4(qb, qo);
+    qv[1] = bld4(qb, qo + 16u);
+    qv[2] = bld4(qb, qo + 128u);
+    qv[3] = bld4(qb, qo + 144u);
+    kv[0] = bld4(qb, ko);
+    kv[1] = bld4(qb, ko + 16u);
+    kv[2] = bld4(qb, ko + 128u);
+    kv[3] = bld4(qb, ko + 144u);
     // ---- V^T operand: lane (i = ql, g) takes dim 16db + i of key slot 4g + r ----
     float vv[4][4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int s = 4 * g + r;
-        const bool ok = slot_ok(s);
-        const float* vs = slot_ptr(ok ? s : 0, 2) + ql;
+        const uint32_t vo = slot_off(4 * g + r, 2) + 4u * ql;
 #pragma unroll
-        for (int db = 0; db < 4; db++) vv[r][db] = ok ? vs[16 * db] : 0.f;
+        for (int db = 0; db < 4; db++) vv[r][db] = bld1(qb, vo + 64u * db);
     }
 
     // ---- allowed(query slot ql, key slot 4g + r) ----
-    const int hq = ql / vall, iq = ql % vall;
+    const bool row_ok = ql < live;
+    const int hq = sdiv(ql), iq = ql - hq * vall;
     auto role = [&](int i) { return (int)((p.roles[i >> 2] >> (8 * (i & 3))) & 0xffu); };
     const int role_q = role(iq);
     bool allow[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int s = 4 * g + r, ik = s % vall;
-        bool ok = row_ok && slot_ok(s) && s / vall == hq;
-        if (ok && ik != iq) {
-            const bool valid = tok >= p.n_enc || p.key_valid[(r0 + ik) * p.kv_row + tok] != 0;
+        const int s = 4 * g + r, hs = sdiv(s), ik = s - hs * vall;
+        bool ok = row_ok && s < live && hs == hq;
+        if (ik != iq) {
+            bool valid = true;
+            if (tok < p.n_enc) valid = p.key_valid[(r0 + ik) * p.kv_row + tok] != 0;
             bool forbidden = false;
             if (p.cov) {
                 const int role_k = role(ik);
                 forbidden = (role_q != kRoleTarget && role_k == kRoleTarget) ||
                             (role_q == kRoleKnown && role_k != kRoleKnown);
             }
-            ok = valid && !forbidden;
+            ok = ok && valid && !forbidden;
         }
         allow[r] = ok;
     }
@@ -102,22 +108,22 @@ __global__ __launch_bounds__(64) void variate_attend(VariateParams p) {
         c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[t][2], qv[t][2], c2, 0, 0, 0);
         c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[t][3], qv[t][3], c3, 0, 0, 0);
     }
-    f32x4 s = (c0 + c1) + (c2 + c3);
+    f32x4 sc = (c0 + c1) + (c2 + c3);
 
     // ---- softmax over the query slot's allowed key slots (the diagonal is one of them) ----
     float mloc = kNegInf;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        s[r] = allow[r] ? s[r] : kNegInf;
-        mloc = fmaxf(mloc, s[r]);
+        sc[r] = allow[r] ? sc[r] : kNegInf;
+        mloc = fmaxf(mloc, sc[r]);
     }
     const float m = max4(mloc);
     const float m_use = m == kNegInf ? 0.f : m;  // an empty query slot: every weight 0
     float lsum = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        s[r] = __builtin_amdgcn_exp2f((s[r] - m_use) * kLog2e);
-        lsum += s[r];
+        sc[r] = __builtin_amdgcn_exp2f((sc[r] - m_use) * kLog2e);
+        lsum += sc[r];
     }
     const float l = sum4(lsum);
 
@@ -126,10 +132,10 @@ __global__ __launch_bounds__(64) void variate_attend(VariateParams p) {
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int db = 0; db < 4; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r][db], s[r], o[db], 0, 0, 0);
+        for (int db = 0; db < 4; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r][db], sc[r], o[db], 0, 0, 0);
 
     // ---- normalise, gate, store: lane holds query slot ql, dims 16db + 4g + r ----
-    if (!row_ok) return;
+    if (!row_ok) return;  // a lane with no query slot is done with this block
     const float inv = 1.0f / l;
     const int head = h0 + hq;
     float* dst = p.o + (r0 + iq) * p.o_row + (int64_t)tok * p.o_tok + head * kHeadDim + 4 * g;
@@ -141,10 +147,17 @@ __global__ __launch_bounds__(64) void variate_attend(VariateParams p) {
         if (gp) {
             const f32x4 gv = ld4(gp + 16 * db);
 #pragma unroll
-            for (int r = 0; r < 4; r++) x[r] = x[r] / (1.0f + __builtin_amdgcn_exp2f(-gv[r] * kLog2e));
+            for (int r = 0; r < 4; r++) x[r] = x[r] * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv[r] * kLog2e));
         }
         st4(dst + 16 * db, x);
     }
+}
+
+// One workgroup per (group, token) item: its waves take the item's head blocks, so the rows of
+// the token are read by one CU at once.
+__global__ __launch_bounds__(256) void variate_attend(VariateParams p) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int blk = wave; blk < p.nblk; blk += 4) variate_block(p, blockIdx.x, blk, lane);
 }
 
 }  // namespace
@@ -155,9 +168,13 @@ hipError_t launch_variate(const VariateParams& p0, hipStream_t stream) {
     p.heads_per_block = 16 / p.vall;
     if (p.heads_per_block > p.heads) p.heads_per_block = p.heads;
     p.nblk = (p.heads + p.heads_per_block - 1) / p.heads_per_block;
-    const int64_t blocks = (int64_t)p.groups * p.n_tok * p.nblk;
+    const int64_t blocks = (int64_t)p.groups * p.n_tok;
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(variate_attend, dim3((unsigned)blocks), dim3(64), 0, stream, p);
+    // One token's vall rows through a 32-bit buffer range (offsets past it read as 0).
+    const int64_t span = ((int64_t)(p.vall - 1) * p.qkv_row + 3 * p.heads * kHeadDim) * 4;
+    if (span >= 0x80000000LL) return hipErrorNotSupported;
+    p.qkv_span_bytes = (uint32_t)span;
+    hipLaunchKernelGGL(variate_attend, dim3((unsigned)blocks), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
