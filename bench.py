@@ -16,8 +16,10 @@ Other workloads (parity-test shapes, measured the same way):
            a step rewinds the cache to the prefix and runs 8 x (append 32, attend 32)
   variate  Timestral variate attention at the prefill shape, f32: 8 series x 4 variates (target,
            past, 2 known) over L=2048 slots, H=16, covariate firewalls, key padding, sigmoid gate
+  proj     the Chronos-2 q/k/v projections with RoPE epilogue at the attention's shape, f32:
+           64 x 577 tokens, d_model 768, three (768, 768) weights
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate]
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
@@ -273,8 +275,38 @@ def run_variate(torch, ta, workloads, peak):
                  peak["hbm_gbps"], "GB/s", 1)
 
 
+def run_proj(torch, ta, workloads, peak):
+    w = workloads.chronos2_projection()
+    a = w.arrays
+    d, L, M = w.meta["d_model"], w.n_q, w.meta["tokens"]
+    dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).cuda() for n in ("x", "wq", "wk", "wv", "rope_cos", "rope_sin")}
+    outs = [torch.empty((M, d), dtype=torch.float32, device="cuda") for _ in range(3)]
+
+    def step():
+        _check(ta, ta.chronos2_qkv_projection(dev["x"], dev["wq"], dev["wk"], dev["wv"], *outs, dev["rope_cos"],
+                                              dev["rope_sin"], w.B, L, d, w.H, 64))
+
+    def output():
+        return torch.stack(outs).reshape(3, w.B, L, d).permute(1, 0, 2, 3).cpu().numpy()
+
+    def cpu_leg(B):
+        orc = _orc()
+        x = np.ascontiguousarray(a["x"][: B * L])
+        ys = [np.zeros((B * L, d), np.float32) for _ in range(3)]
+        t0 = time.perf_counter()
+        # The reference path this call replaces: three nn.linear calls, then the serial RoPE loop.
+        for y, wt in zip(ys, (a["wq"], a["wk"], a["wv"])):
+            orc.linear(cpu_threads(), y, x, B * L, wt, d, d)
+        orc.chronos2_rope(ys[0], ys[1], a["rope_cos"], a["rope_sin"], B * L, L, d, w.H, 64)
+        return time.perf_counter() - t0, np.stack(ys).reshape(3, B, L, d).transpose(1, 0, 2, 3), orc.lanes
+
+    config = {"workload": w.name, "B": w.B, "L": L, "d_model": d, "H": w.H, "outputs": "q,k,v", "rope": True,
+              "layout": "x (B*L, d), W (d, d) x3, q/k/v (B*L, d) f32"}
+    return Bench(w, step, output, cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"], "TFLOP/s", 16)
+
+
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
-             "variate": run_variate}
+             "variate": run_variate, "proj": run_proj}
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
 

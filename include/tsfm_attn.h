@@ -186,6 +186,45 @@ typedef struct tsfm_variate_args {
 int tsfm_variate_attend(const tsfm_variate_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * Fused projection ahead of time attention, with RoPE in its epilogue. Replaces, in one launch:
+ *  - Chronos-2: nn.linear for q, k and v and the serial RoPE loop (src/chronos2/model.zig:232-245);
+ *  - Timestral: the fused qkv nn.linear over the permuted weight, the gate nn.linear and
+ *    TimeJob.rope (src/timestral/model.zig:495,500,513,558-577): pass w_q/w_k/w_v = the three
+ *    (d, d) blocks of the permuted weight and q/k/v = qkv, qkv + d, qkv + 2d with stride 3d;
+ *  - Timestral variate attention: the same projections without RoPE (:532,535);
+ *  - Chronos-Bolt: the q, k, v nn.linear calls of the encoder self-attention, no RoPE
+ *    (src/chronos_bolt/model.zig:239-241).
+ * For every token r = b * seq + t (r < batch * seq) of x (element (r, c) at x[r * x_tok + c]):
+ *   q[r * q_tok + n] = (x[r, :] . w_q[n, :]) for n < heads * head_dim, then nn.ropeHalf on each
+ *   head of q and k when rope_cos is set (token t of series row b uses row t of table
+ *   (rope_row0 + b) / rope_rows_per_table, as in tsfm_attn_args); v and gate likewise, no RoPE.
+ * Weights are nn.Weight's (out, in) row-major f32 (src/core/nn.zig:270-293, no bias). f32 only;
+ * head_dim 64; d_in a multiple of 16; strides in elements, multiples of 4. */
+typedef struct tsfm_proj_args {
+    int32_t dtype;      /* TSFM_DTYPE_F32 */
+    int32_t batch;      /* series (rows) */
+    int32_t seq;        /* tokens per series */
+    int32_t d_in;       /* width of x (d_model); a multiple of 16 */
+    int32_t heads;      /* each output has heads * head_dim columns */
+    int32_t head_dim;   /* 64 */
+    uint32_t flags;     /* TSFM_ATTN_DEVICE_PTRS or 0 */
+    int32_t rope_half;  /* 32 when rope_cos is set */
+    int32_t rope_rows_per_table, rope_row0;
+    int64_t rope_table_stride;
+    const float *x; int64_t x_tok;
+    const float *w_q, *w_k, *w_v;
+    const float *w_gate;            /* optional; with gate */
+    float *q;    int64_t q_tok;
+    float *k;    int64_t k_tok;
+    float *v;    int64_t v_tok;
+    float *gate; int64_t gate_tok;  /* optional; with w_gate */
+    const float *rope_cos, *rope_sin;
+    void *stream;
+} tsfm_proj_args;
+
+int tsfm_qkv_project(const tsfm_proj_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * KV cache for block-autoregressive decode. No counterpart in the reference: Timestral's
  * blockDecode re-encodes the whole grown context every block (src/timestral/forecaster.zig:423-563),
  * recomputing K/V of unchanged prefix tokens. With a causal encoder and a fixed prefix the cached

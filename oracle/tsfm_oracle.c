@@ -398,6 +398,40 @@ void orc_for_range_min(size_t threads, size_t n, size_t min_chunk, const void *c
     free(tid);
 }
 
+/* nn.linear on the builtin CPU path (src/core/nn.zig:262-293): y[rows, out] = x[rows, in] w^T
+ * (+ bias). Products with rows*out*in >= 2^20 and out >= 2*col_block split their output columns
+ * into blocks of col_block = 16 over the pool (linearBlocks, :264-267); each block is linearCols
+ * (:250-256): gemmNTWeight = gemmNTFallback over the block's contiguous weight rows, then the bias. */
+typedef struct {
+    float *y;
+    const float *x;
+    size_t rows;
+    const float *w;
+    size_t out, in;
+    const float *bias;
+} linear_ctx;
+
+static void linear_cols(const linear_ctx *c, size_t j0, size_t j1) {
+    orc_gemm_nt(c->y + j0, c->out, c->x, c->in, c->w + j0 * c->in, c->in, c->rows, j1 - j0, c->in, 1.0f);
+    if (c->bias)
+        for (size_t r = 0; r < c->rows; r++) orc_add_in_place(c->y + r * c->out + j0, c->bias + j0, j1 - j0);
+}
+
+static void linear_blocks(const void *ctx, size_t b0, size_t b1) {
+    const linear_ctx *c = (const linear_ctx *)ctx;
+    const size_t col_block = 16, nblocks = (c->out + col_block - 1) / col_block;
+    linear_cols(c, b0 * col_block, b1 == nblocks ? c->out : b1 * col_block);
+}
+
+void orc_linear(size_t threads, float *y, const float *x, size_t rows, const float *w, size_t out, size_t in,
+                const float *bias) {
+    const linear_ctx c = {y, x, rows, w, out, in, bias};
+    if (rows * out * in >= ((size_t)1 << 20) && out >= 2 * 16)
+        orc_for_range_min(threads, (out + 15) / 16, 1, &c, linear_blocks);
+    else
+        linear_cols(&c, 0, out);
+}
+
 /* SelfJob.attend (src/chronos_bolt/model.zig:331-345). */
 typedef struct {
     const float *q, *k, *v;

@@ -37,6 +37,10 @@ float orc_exp_vec(float x);
 /* nn.gemmNT builtin path (src/core/nn.zig:49-60, 68-162). */
 void orc_gemm_nt(float *cc, size_t ldc, const float *a, size_t lda, const float *b, size_t ldb,
                  size_t m, size_t n, size_t k, float alpha);
+/* nn.linear builtin path (src/core/nn.zig:262-293): y = x w^T (+ bias), w (out, in) row-major,
+ * output column blocks of 16 over `threads` (par.forRange). */
+void orc_linear(size_t threads, float *y, const float *x, size_t rows, const float *w, size_t out, size_t in,
+                const float *bias);
 /* nn.gemmNN builtin path (src/core/nn.zig:165-239). */
 void orc_gemm_nn(float *cc, size_t ldc, const float *a, size_t lda, const float *b, size_t ldb,
                  size_t m, size_t n, size_t k);

@@ -29,6 +29,7 @@ class Oracle:
         L.orc_exp_vec.restype = _f
         L.orc_gemm_nt.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
         L.orc_gemm_nn.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz]
+        L.orc_linear.argtypes = [_sz, _vp, _vp, _sz, _vp, _sz, _sz, _vp]
         L.orc_softmax.argtypes = [_vp, _sz]
         L.orc_dot.argtypes = [_vp, _vp, _sz]
         L.orc_dot.restype = _f
@@ -65,6 +66,10 @@ class Oracle:
 
     def gemm_nt(self, c, ldc, a, lda, b, ldb, m, n, k, alpha):
         self.lib.orc_gemm_nt(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k, alpha)
+
+    def linear(self, threads, y, x, rows, w, out, inp, bias=None):
+        """nn.linear: y (rows, out) = x (rows, inp) w (out, inp)^T (+ bias)."""
+        self.lib.orc_linear(threads, ptr(y), ptr(x), rows, ptr(w), out, inp, ptr(bias))
 
     def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
         self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)

@@ -31,7 +31,8 @@ def test_library_exports_every_declared_symbol(ta):
     assert not missing, missing
 
 
-@pytest.mark.parametrize("struct,cname", [("AttnArgs", "tsfm_attn_args"), ("VariateArgs", "tsfm_variate_args")])
+@pytest.mark.parametrize("struct,cname", [("AttnArgs", "tsfm_attn_args"), ("VariateArgs", "tsfm_variate_args"),
+                                          ("ProjArgs", "tsfm_proj_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)
@@ -164,3 +165,43 @@ def test_variate_validation_codes(ta, over, code):
 def test_variate_empty_is_a_no_op(ta):
     a, _keep = _variate_host_args(ta, groups=0)
     assert ta.variate_attend(a) == ta.OK
+
+
+def _proj_host_args(ta, **over):
+    b, seq, d_in, nh = 2, 5, 64, 2
+    width = nh * 64
+    x = np.zeros(b * seq * d_in, np.float32)
+    w = np.zeros(width * d_in, np.float32)
+    y = np.zeros(b * seq * width, np.float32)
+    tab = np.zeros(seq * 32, np.float32)
+    kw = dict(dtype=ta.DTYPE_F32, batch=b, seq=seq, d_in=d_in, heads=nh, head_dim=64, rope_half=32,
+              x=x.ctypes.data, x_tok=d_in, w_q=w.ctypes.data, w_k=w.ctypes.data, w_v=w.ctypes.data,
+              q=y.ctypes.data, q_tok=width, k=y.ctypes.data, k_tok=width, v=y.ctypes.data, v_tok=width,
+              rope_cos=tab.ctypes.data, rope_sin=tab.ctypes.data)
+    kw.update(over)
+    return ta.ProjArgs(**kw), (x, w, y, tab)
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(dtype=1), 2),                 # f32 only
+    (dict(head_dim=32), 2),
+    (dict(d_in=40, x_tok=40), 2),       # d_in not a multiple of 16
+    (dict(x_tok=66), 2),                # stride not a multiple of 16 bytes
+    (dict(batch=-1), 3),
+    (dict(w_k=None), 3),
+    (dict(rope_sin=None), 3),           # rope_cos without rope_sin
+    (dict(rope_half=16), 3),            # tables must be head_dim / 2 wide
+    (dict(x_tok=32), 3),                # token stride shorter than d_in
+    (dict(q_tok=64), 3),                # token stride shorter than heads * 64
+    (dict(w_gate=1 << 20), 3),          # w_gate without gate
+])
+def test_proj_validation_codes(ta, over, code):
+    a, _keep = _proj_host_args(ta, **over)
+    assert ta.qkv_project(a) == code
+    assert ta.last_error()
+
+
+def test_proj_empty_is_a_no_op(ta):
+    for over in (dict(batch=0), dict(seq=0), dict(heads=0)):
+        a, _keep = _proj_host_args(ta, **over)
+        assert ta.qkv_project(a) == ta.OK

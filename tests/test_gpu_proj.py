@@ -1,0 +1,134 @@
+"""GPU parity of the fused Q/K/V(/gate) projection with RoPE epilogue (tsfm_qkv_project) against
+the oracle's nn.linear (src/core/nn.zig:262-293) followed by the family RoPE loops
+(src/chronos2/model.zig:236-245, src/timestral/model.zig:558-577), through the C ABI.
+
+Bar: scaled error max|gpu - oracle| / max(|oracle|, 1) <= 1e-5 (the f32 tolerance). Covered: the
+Chronos-2 layout (three weights, one RoPE table), the Timestral layout (the permuted fused weight,
+interleaved qkv output, per-group tables with partial RoPE and negative positions, the gate),
+Chronos-Bolt (no RoPE), token counts that leave a partial 128-token tile, head counts whose
+columns leave a partial 128-column tile, d_in != heads * 64, padded strides (padding untouched),
+host and device pointers, and the argument checks.
+"""
+import numpy as np
+import pytest
+
+import _ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+THREADS = 16
+
+
+def _weights(rng, n, d_in, count):
+    return [(rng.standard_normal((n, d_in)) / np.sqrt(d_in)).astype(np.float32) for _ in range(count)]
+
+
+def _linear(orc, x, w):
+    y = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    orc.linear(THREADS, y, np.ascontiguousarray(x), x.shape[0], np.ascontiguousarray(w), w.shape[0], x.shape[1])
+    return y
+
+
+def _chronos2_oracle(orc, x, wq, wk, wv, cos_t, sin_t, b, seq, d, nh):
+    q, k, v = (_linear(orc, x, w) for w in (wq, wk, wv))
+    orc.chronos2_rope(q, k, cos_t, sin_t, b * seq, seq, d, nh, 64)
+    return q, k, v
+
+
+@pytest.mark.parametrize("b,seq", [(2, 77), (1, 128), (3, 200)])
+def test_chronos2_projection_matches_oracle(ta, orc, gpu_ready, b, seq):
+    d, nh = 768, 12
+    rng = np.random.default_rng(b * 1000 + seq)
+    x = rng.standard_normal((b * seq, d)).astype(np.float32)
+    wq, wk, wv = _weights(rng, d, d, 3)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    q, k, v = (np.full((b * seq, d), -3.0, np.float32) for _ in range(3))
+    rc = ta.chronos2_qkv_projection(x, wq, wk, wv, q, k, v, cos_t, sin_t, b, seq, d, nh, 64)
+    assert rc == ta.OK, ta.last_error()
+    want = _chronos2_oracle(orc, x, wq, wk, wv, cos_t, sin_t, b, seq, d, nh)
+    for got, ref in zip((q, k, v), want):
+        assert _ref.scaled_err(got, ref) <= TOL
+
+
+def test_chronos2_projection_device_pointers(ta, orc, gpu_ready):
+    import torch
+
+    b, seq, d, nh = 4, 145, 768, 12
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((b * seq, d)).astype(np.float32)
+    wq, wk, wv = _weights(rng, d, d, 3)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    dev = [torch.from_numpy(a).cuda() for a in (x, wq, wk, wv, cos_t, sin_t)]
+    outs = [torch.full((b * seq, d), -3.0, device="cuda") for _ in range(3)]
+    rc = ta.chronos2_qkv_projection(dev[0], dev[1], dev[2], dev[3], *outs, dev[4], dev[5], b, seq, d, nh, 64)
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    want = _chronos2_oracle(orc, x, wq, wk, wv, cos_t, sin_t, b, seq, d, nh)
+    for got, ref in zip(outs, want):
+        assert _ref.scaled_err(got.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_timestral_projection_matches_oracle(ta, orc, gpu_ready, gated):
+    """Fused permuted weight into the interleaved (token, qkv, head, hd) buffer, per-group RoPE
+    tables (partial RoPE: rope_dim = hd / 2; positions relative to the first observed patch, so
+    negative for early tokens), and the gate projection."""
+    groups, vall, ne, l, h, nh = 2, 3, 30, 24, 8, 4
+    d, sl, rows = nh * 64, ne + h, groups * vall
+    rng = np.random.default_rng(40 + gated)
+    x = rng.standard_normal((rows * sl, d)).astype(np.float32)
+    w_qkv = (rng.standard_normal((3 * d, d)) / np.sqrt(d)).astype(np.float32)
+    w_gate = (rng.standard_normal((d, d)) / np.sqrt(d)).astype(np.float32) if gated else None
+    cos_t, sin_t = orc.timestral_rope_tables(groups, ne, l, h, 64, 32, 10000.0, [5, 0])
+    qkv = np.full((rows * sl, 3 * d), -3.0, np.float32)
+    gate = np.full((rows * sl, d), -3.0, np.float32) if gated else None
+    rc = ta.timestral_qkv_projection(x, w_qkv, qkv, cos_t, sin_t, rows, vall, sl, d, nh, 64, w_gate=w_gate,
+                                     gate=gate)
+    assert rc == ta.OK, ta.last_error()
+    want = _linear(orc, x, w_qkv)
+    orc.timestral_rope(THREADS, want, cos_t, sin_t, rows, sl, vall, d, nh, 64)
+    assert _ref.scaled_err(qkv, want) <= TOL
+    if gated:
+        assert _ref.scaled_err(gate, _linear(orc, x, w_gate)) <= TOL
+
+
+@pytest.mark.parametrize("nh,d_in,tokens", [(3, 96, 200), (1, 32, 5), (5, 160, 129), (12, 768, 1), (2, 48, 77), (1, 16, 3)])
+def test_bolt_projection_odd_shapes(ta, orc, gpu_ready, nh, d_in, tokens):
+    """No RoPE (Chronos-Bolt); d_in != heads * 64; column counts 3 * nh * 64 that end in half a
+    128-column tile; token counts that end in a partial 128-token tile."""
+    inner = nh * 64
+    rng = np.random.default_rng(nh * 7 + d_in + tokens)
+    x = rng.standard_normal((tokens, d_in)).astype(np.float32)
+    ws = _weights(rng, inner, d_in, 3)
+    outs = [np.full((tokens, inner), -3.0, np.float32) for _ in range(3)]
+    rc = ta.bolt_qkv_projection(x, *ws, *outs, 1, tokens, d_in, nh, 64)
+    assert rc == ta.OK, ta.last_error()
+    for got, w in zip(outs, ws):
+        assert _ref.scaled_err(got, _linear(orc, x, w)) <= TOL
+
+
+def test_padded_strides_leave_padding_untouched(ta, orc, gpu_ready):
+    """x_tok > d_in and q/k/v token strides > heads * 64: only each token's own columns are written
+    (src/core/gpu_test.zig:30-34 guards the same for the reference's GEMM)."""
+    b, seq, d_in, nh = 2, 50, 128, 2
+    width, x_tok, y_tok = nh * 64, 132, 200
+    rng = np.random.default_rng(9)
+    xp = rng.standard_normal((b * seq, x_tok)).astype(np.float32)
+    wq, wk, wv = _weights(rng, width, d_in, 3)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    outs = [np.full((b * seq, y_tok), -5.0, np.float32) for _ in range(3)]
+    a = ta.ProjArgs(dtype=ta.DTYPE_F32, batch=b, seq=seq, d_in=d_in, heads=nh, head_dim=64, flags=0, rope_half=32,
+                    x=xp.ctypes.data, x_tok=x_tok, w_q=wq.ctypes.data, w_k=wk.ctypes.data, w_v=wv.ctypes.data,
+                    q=outs[0].ctypes.data, q_tok=y_tok, k=outs[1].ctypes.data, k_tok=y_tok, v=outs[2].ctypes.data,
+                    v_tok=y_tok, rope_cos=cos_t.ctypes.data, rope_sin=sin_t.ctypes.data)
+    assert ta.qkv_project(a) == ta.OK, ta.last_error()
+    x = np.ascontiguousarray(xp[:, :d_in])
+    q, k, v = (_linear(orc, x, w) for w in (wq, wk, wv))
+    qf = np.zeros((b * seq, width), np.float32)
+    kf = np.zeros_like(qf)
+    qf[:], kf[:] = q, k
+    orc.chronos2_rope(qf, kf, cos_t, sin_t, b * seq, seq, width, nh, 64)
+    for got, ref in zip(outs, (qf, kf, v)):
+        assert _ref.scaled_err(got[:, :width], ref) <= TOL
+        assert np.all(got[:, width:] == -5.0)

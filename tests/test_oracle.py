@@ -496,3 +496,39 @@ def test_mul_sigmoid_closed_form(orc):
     zero = np.zeros(n, np.float32)
     orc.mul_sigmoid(out, x, zero)
     assert np.array_equal(out, x * np.float32(0.5))  # sigmoid(0) = 1/2 exactly
+
+
+def test_linear_matches_f64_and_thread_count(orc):
+    """nn.linear: y = x w^T + bias, with the column blocks split over threads above 2^20 products."""
+    rng = np.random.default_rng(21)
+    rows, inp, out = 40, 160, 200  # 1.28e6 products: the threaded column-block path
+    x = rng.standard_normal((rows, inp)).astype(np.float32)
+    w = (rng.standard_normal((out, inp)) / np.sqrt(inp)).astype(np.float32)
+    bias = rng.standard_normal(out).astype(np.float32)
+    y1 = np.zeros((rows, out), np.float32)
+    orc.linear(1, y1, x, rows, w, out, inp, bias)
+    want = x.astype(np.float64) @ w.astype(np.float64).T + bias
+    assert np.max(np.abs(y1 - want) / np.maximum(np.abs(want), 1.0)) < 5e-6
+    for threads in (3, 8):  # blocks of 16 columns: the result does not depend on the split
+        y = np.zeros_like(y1)
+        orc.linear(threads, y, x, rows, w, out, inp, bias)
+        assert np.array_equal(y, y1)
+    small = np.zeros((3, 24), np.float32)  # below the threshold: one linearCols call
+    orc.linear(4, small, x[:3], 3, w[:24], 24, inp)
+    want_small = x[:3].astype(np.float64) @ w[:24].astype(np.float64).T
+    assert np.max(np.abs(small - want_small)) < 5e-6
+
+
+def test_linear_permutation_weight_is_exact(orc):
+    """A permutation weight picks columns of x exactly: y[:, j] = x[:, perm[j]] (a transposed
+    operand would apply the inverse permutation)."""
+    rng = np.random.default_rng(22)
+    rows, n = 9, 48
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    perm = rng.permutation(n)
+    w = np.zeros((n, n), np.float32)
+    w[np.arange(n), perm] = 1.0
+    y = np.zeros((rows, n), np.float32)
+    orc.linear(2, y, x, rows, w, n, n)
+    assert np.array_equal(y, x[:, perm])
+    assert not np.array_equal(y, x[:, np.argsort(perm)])

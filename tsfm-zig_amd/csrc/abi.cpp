@@ -430,6 +430,116 @@ int tsfm_variate_attend(const tsfm_variate_args* a) {
     return TSFM_OK;
 }
 
+// ---- fused projection ---------------------------------------------------------------------------
+
+int tsfm_qkv_project(const tsfm_proj_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (a->dtype != TSFM_DTYPE_F32) return fail(TSFM_E_UNSUPPORTED, "the projection is f32 only");
+    if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
+    if (a->batch < 0 || a->seq < 0 || a->d_in < 0 || a->heads < 0) return fail(TSFM_E_INVALID, "negative size");
+    if (a->x == nullptr || a->w_q == nullptr || a->w_k == nullptr || a->w_v == nullptr || a->q == nullptr ||
+        a->k == nullptr || a->v == nullptr)
+        return fail(TSFM_E_INVALID, "x, w_q, w_k, w_v, q, k and v are required");
+    if ((a->w_gate == nullptr) != (a->gate == nullptr)) return fail(TSFM_E_INVALID, "w_gate and gate go together");
+    if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr))
+        return fail(TSFM_E_INVALID, "rope_cos and rope_sin go together");
+    const int64_t width = (int64_t)a->heads * a->head_dim;
+    const bool gated = a->gate != nullptr, rope = a->rope_cos != nullptr;
+    if (a->x_tok < a->d_in || a->q_tok < width || a->k_tok < width || a->v_tok < width ||
+        (gated && a->gate_tok < width))
+        return fail(TSFM_E_INVALID, "a token stride is shorter than its row");
+    if (rope && (a->rope_half != a->head_dim / 2 || a->rope_rows_per_table < 0 || a->rope_row0 < 0 ||
+                 a->rope_table_stride < 0))
+        return fail(TSFM_E_INVALID, "bad RoPE table description");
+    const int64_t tokens = (int64_t)a->batch * a->seq;
+    if (tokens == 0 || width == 0) return TSFM_OK;  // nothing to compute
+    if (a->d_in == 0 || a->d_in % 16) return fail(TSFM_E_UNSUPPORTED, "d_in %d (supported: multiples of 16)", a->d_in);
+    if (tokens > 0x7fffffff || 4 * width > 0x7fffffff) return fail(TSFM_E_UNSUPPORTED, "too many tokens or heads");
+    if (a->x_tok % 4 || a->q_tok % 4 || a->k_tok % 4 || a->v_tok % 4 || (gated && a->gate_tok % 4) ||
+        (rope && a->rope_table_stride % 4))
+        return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+
+    tsfm::ProjParams p{};
+    p.x = a->x; p.x_tok = a->x_tok;
+    p.w0 = a->w_q; p.w1 = a->w_k; p.w2 = a->w_v; p.w3 = a->w_gate;
+    p.y0 = a->q; p.y1 = a->k; p.y2 = a->v; p.y3 = a->gate;
+    p.y0_tok = a->q_tok; p.y1_tok = a->k_tok; p.y2_tok = a->v_tok; p.y3_tok = a->gate_tok;
+    p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
+    p.rope_table_stride = a->rope_table_stride;
+    p.rope_rows_per_table = a->rope_rows_per_table; p.rope_row0 = a->rope_row0;
+    p.tokens = (int32_t)tokens; p.seq = a->seq; p.d_in = a->d_in; p.width = (int32_t)width;
+    p.n_out = gated ? 4 : 3;
+    hipError_t e;
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
+        const void* ptrs[] = {a->x, a->w_q, a->w_k, a->w_v, a->w_gate, a->q, a->k, a->v, a->gate, a->rope_cos,
+                              a->rope_sin};
+        for (const void* q : ptrs)
+            if (q != nullptr && !aligned(q, 16)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
+        e = tsfm::launch_proj(p, static_cast<hipStream_t>(a->stream));
+        if (e != hipSuccess) return hip_fail(e, "projection launch");
+        return TSFM_OK;
+    }
+    // Host pointers: stage x, the weights and the tables, run, copy the output rows back.
+    const size_t x_n = (size_t)span(1, tokens, a->x_tok, 0, a->d_in) * 4;
+    const size_t w_n = (size_t)(width * a->d_in) * 4;
+    const size_t y_n[4] = {(size_t)span(1, tokens, a->q_tok, 0, width) * 4, (size_t)span(1, tokens, a->k_tok, 0, width) * 4,
+                           (size_t)span(1, tokens, a->v_tok, 0, width) * 4,
+                           gated ? (size_t)span(1, tokens, a->gate_tok, 0, width) * 4 : 0};
+    size_t t_n = 0;
+    if (rope) {
+        const int64_t last = a->rope_rows_per_table > 0 ? (a->rope_row0 + a->batch - 1) / a->rope_rows_per_table : 0;
+        t_n = (size_t)(last * a->rope_table_stride + (int64_t)a->seq * a->rope_half) * 4;
+    }
+    Plan plan;
+    const size_t x_at = plan.take(x_n);
+    size_t w_at[4], y_at[4];
+    for (int i = 0; i < 4; i++) w_at[i] = plan.take(i < 3 || gated ? w_n : 0);
+    for (int i = 0; i < 4; i++) y_at[i] = plan.take(y_n[i]);
+    const size_t c_at = plan.take(t_n), s_at = plan.take(t_n);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    const float* w_src[4] = {a->w_q, a->w_k, a->w_v, a->w_gate};
+    struct Up { const void* src; size_t at, n; } ups[] = {
+        {a->x, x_at, x_n}, {w_src[0], w_at[0], w_n}, {w_src[1], w_at[1], w_n}, {w_src[2], w_at[2], w_n},
+        {w_src[3], w_at[3], gated ? w_n : 0}, {a->rope_cos, c_at, t_n}, {a->rope_sin, s_at, t_n}};
+    for (const Up& u : ups) {
+        if (u.n == 0 || u.src == nullptr) continue;
+        if ((e = hipMemcpyAsync(base + u.at, u.src, u.n, hipMemcpyHostToDevice, s)) != hipSuccess)
+            return hip_fail(e, "host-to-device copy");
+    }
+    p.x = reinterpret_cast<const float*>(base + x_at);
+    p.w0 = reinterpret_cast<const float*>(base + w_at[0]);
+    p.w1 = reinterpret_cast<const float*>(base + w_at[1]);
+    p.w2 = reinterpret_cast<const float*>(base + w_at[2]);
+    p.w3 = gated ? reinterpret_cast<const float*>(base + w_at[3]) : nullptr;
+    p.y0 = reinterpret_cast<float*>(base + y_at[0]);
+    p.y1 = reinterpret_cast<float*>(base + y_at[1]);
+    p.y2 = reinterpret_cast<float*>(base + y_at[2]);
+    p.y3 = gated ? reinterpret_cast<float*>(base + y_at[3]) : nullptr;
+    if (rope) {
+        p.rope_cos = reinterpret_cast<const float*>(base + c_at);
+        p.rope_sin = reinterpret_cast<const float*>(base + s_at);
+    }
+    e = tsfm::launch_proj(p, s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "projection launch");
+    }
+    float* const dst[4] = {a->q, a->k, a->v, a->gate};
+    const int64_t tok[4] = {a->q_tok, a->k_tok, a->v_tok, a->gate_tok};
+    for (int i = 0; i < (gated ? 4 : 3); i++)
+        if ((e = copy_rows_d2h(dst[i], base + y_at[i], 1, tokens, 0, tok[i] * 4, width * 4, s)) != hipSuccess)
+            return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
 // ---- KV cache ------------------------------------------------------------------------------------
 
 struct tsfm_kv_cache {

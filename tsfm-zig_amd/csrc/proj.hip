@@ -1,0 +1,172 @@
+// Fused Q/K/V (and gate) projection with rotate-half RoPE in the epilogue, f32 on the matrix cores
+// (gfx950).
+//
+// What it replaces, for the time-attention block of each family:
+//  - Chronos-2: three nn.linear calls (q, k, v) and the serial RoPE loop over every (token, head)
+//    (src/chronos2/model.zig:232-245);
+//  - Timestral: the fused qkv nn.linear over the permuted (qkv, head, head_dim) weight, the gate
+//    nn.linear, and TimeJob.rope (src/timestral/model.zig:495,500,513,558-577); without RoPE,
+//    the projections of Model.variateAttention (:532,535);
+//  - Chronos-Bolt: the q, k, v nn.linear calls of the encoder self-attention
+//    (src/chronos_bolt/model.zig:239-241, no RoPE).
+// nn.linear (src/core/nn.zig:262-293) is y[rows, out] = x[rows, in] w[out, in]^T; these calls pass
+// no bias. RoPE is nn.ropeHalf (src/core/nn.zig:448-467) on each 64-wide head of q and k.
+//
+// One launch computes every output: the output columns are the concatenation [q | k | v | gate]
+// (each heads * 64 wide), so x is streamed through the chip once for all of them. A workgroup
+// computes a 128-token x 128-column tile with K = d_in in 16-wide steps: x and w tiles go
+// HBM/L2 -> registers -> LDS (double-buffered, one barrier per step), and each of the four waves
+// multiplies a 64 x 64 sub-tile with v_mfma_f32_16x16x4_f32, the weight rows as the A operand so
+// that each lane ends with four consecutive output columns of one token (16-byte stores, and the
+// RoPE partner column i + 32 in the same lane). Three workgroups share a CU (40 KB of LDS and at
+// most 168 registers per lane each), so a wave waiting at its step's barrier or LDS reads leaves
+// the matrix pipe to two others.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace tsfm {
+namespace {
+
+constexpr int BM = 128;          // tokens per workgroup tile
+constexpr int BN = 128;          // output columns per workgroup tile
+constexpr int BK = 16;           // reduction step
+constexpr int LDS_ROW = BK + 4;  // padded LDS row (floats): 8 consecutive rows hit distinct banks
+constexpr int NT = 256;          // four waves: 2 (tokens) x 2 (columns), 64 x 64 each
+constexpr int GM = 8;            // token tiles that sweep the column tiles together
+constexpr int LROWS = NT / (BK / 4);  // tile rows one loader pass stages (a float4 per thread)
+constexpr int LPASS = BM / LROWS;     // loader passes per tile
+constexpr size_t kProjLds = (size_t)2 * (BM + BN) * LDS_ROW * sizeof(float);
+
+// Workgroup tile of a logical id: GM token tiles at a time go through all column tiles, token tile
+// fastest, so the x rows of a group stay in L2 while the weight tiles stream past.
+__device__ __forceinline__ void tile_of(int id, int m_tiles, int n_tiles, int& tm, int& tn) {
+    const int per = GM * n_tiles;
+    const int g = id / per, r = id - g * per;
+    const int m0 = g * GM, gm = min(GM, m_tiles - m0);
+    tm = m0 + r % gm;
+    tn = r / gm;
+}
+
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void qkv_proj(ProjParams p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* const xs = smem;                          // [2][BM][LDS_ROW]
+    float* const ws = smem + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, tm, tn);
+    const int n_cols = p.width * p.n_out;
+
+    // Loader: thread t stages rows t / (BK / 4) + LROWS i, i < LPASS, columns 4 (t % (BK / 4))
+    // .. + 3 of both tiles. Rows past the end are clamped to the last row: they feed only outputs
+    // that are not stored.
+    const int lr = tid / (BK / 4), lc = (tid % (BK / 4)) * 4;
+    const float* xp[LPASS];
+    const float* wp[LPASS];
+#pragma unroll
+    for (int i = 0; i < LPASS; i++) {
+        const int m = min(tm * BM + lr + LROWS * i, p.tokens - 1);
+        xp[i] = p.x + (int64_t)m * p.x_tok + lc;
+        const int n = min(tn * BN + lr + LROWS * i, n_cols - 1);
+        const int sel = n / p.width;
+        const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
+        wp[i] = w + (int64_t)(n - sel * p.width) * p.d_in + lc;
+    }
+    f32x4 rx[LPASS], rw[LPASS];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < LPASS; i++) {
+            rx[i] = ld4(xp[i] + k0);
+            rw[i] = ld4(wp[i] + k0);
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LPASS; i++) {
+            st4(xs + (buf * BM + lr + LROWS * i) * LDS_ROW + lc, rx[i]);
+            st4(ws + (buf * BN + lr + LROWS * i) * LDS_ROW + lc, rw[i]);
+        }
+    };
+
+    // Operand reads: lane l takes row (l & 15) of a 16-row block and the four reduction indices
+    // 4 (l >> 4) .. + 3 of a 16-wide chunk; matrix instruction j of the chunk uses element j, the
+    // same reduction index on both operands.
+    const int wm = wave & 1, wn = wave >> 1;
+    const float* const xr = xs + (wm * 64 + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
+    const float* const wr = ws + (wn * 64 + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
+
+    f32x4 acc[4][4];  // [column block][token block]: lane holds columns 4 (l >> 4) + r, token l & 15
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int steps = p.d_in / BK;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int t = 0; t < steps; t++) {
+        const int buf = t & 1;
+        if (t + 1 < steps) fetch((t + 1) * BK);
+#pragma unroll
+        for (int kc = 0; kc < BK / 16; kc++) {
+            f32x4 wa[4], xb[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                wa[b] = ld4(wr + (buf * BN + 16 * b) * LDS_ROW + 16 * kc);
+                xb[b] = ld4(xr + (buf * BM + 16 * b) * LDS_ROW + 16 * kc);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                    for (int mb = 0; mb < 4; mb++)
+                        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][j], xb[mb][j], acc[nb][mb], 0, 0, 0);
+        }
+        // The other buffer was last read in step t - 1, which every wave has left (barrier below).
+        if (t + 1 < steps) stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: this wave's 64 columns are one head of one output.
+    const int n0 = tn * BN + wn * 64;
+    if (n0 >= n_cols) return;
+    const int sel = n0 / p.width, col = n0 - sel * p.width;
+    float* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
+    const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
+    const bool rope = p.rope_cos != nullptr && sel < 2;
+    const int cq = 4 * (lane >> 4);
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+        const int m = tm * BM + wm * 64 + mb * 16 + (lane & 15);
+        if (m >= p.tokens) continue;
+        if (rope) {
+            // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table.
+            const int b = m / p.seq, tok = m - b * p.seq;
+            const int table = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
+            const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq;
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++)
+                rope4(acc[nb][mb], acc[nb + 2][mb], ld4(p.rope_cos + at + 16 * nb), ld4(p.rope_sin + at + 16 * nb));
+        }
+        float* const out = y + (int64_t)m * y_tok + col + cq;
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) st4(out + 16 * nb, acc[nb][mb]);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
+    ProjParams p = p0;
+    if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
+    if (p.d_in % BK || p.d_in <= 0 || p.width % kHeadDim || p.n_out > 4 || p.seq <= 0) return hipErrorInvalidValue;
+    p.m_tiles = (p.tokens + BM - 1) / BM;
+    p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
+    const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(qkv_proj, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace tsfm

@@ -56,6 +56,7 @@ EXPORTS = (
     "tsfm_t5_relative_bucket",
     "tsfm_t5_bucket_table",
     "tsfm_variate_attend",
+    "tsfm_qkv_project",
     "tsfm_kv_create",
     "tsfm_kv_free",
     "tsfm_kv_reset",
@@ -184,6 +185,41 @@ class VariateArgs(ctypes.Structure):
 ROLE_TARGET, ROLE_PAST, ROLE_KNOWN = 0, 1, 2  # model.Role (src/timestral/model.zig:89)
 
 
+class ProjArgs(ctypes.Structure):
+    """``tsfm_proj_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("seq", ctypes.c_int32),
+        ("d_in", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("rope_half", ctypes.c_int32),
+        ("rope_rows_per_table", ctypes.c_int32),
+        ("rope_row0", ctypes.c_int32),
+        ("rope_table_stride", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("x_tok", ctypes.c_int64),
+        ("w_q", ctypes.c_void_p),
+        ("w_k", ctypes.c_void_p),
+        ("w_v", ctypes.c_void_p),
+        ("w_gate", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("q_tok", ctypes.c_int64),
+        ("k", ctypes.c_void_p),
+        ("k_tok", ctypes.c_int64),
+        ("v", ctypes.c_void_p),
+        ("v_tok", ctypes.c_int64),
+        ("gate", ctypes.c_void_p),
+        ("gate_tok", ctypes.c_int64),
+        ("rope_cos", ctypes.c_void_p),
+        ("rope_sin", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
 def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     """Load libtsfm_attn.so (built in-tree by ``make -C tsfm-zig_amd``). Raises if it is missing."""
     global _lib
@@ -228,6 +264,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_kv_attend.restype = ctypes.c_int
     lib.tsfm_variate_attend.argtypes = [ctypes.POINTER(VariateArgs)]
     lib.tsfm_variate_attend.restype = ctypes.c_int
+    lib.tsfm_qkv_project.argtypes = [ctypes.POINTER(ProjArgs)]
+    lib.tsfm_qkv_project.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -477,6 +515,53 @@ def timestral_variate_attention(qkv, o, key_valid, roles: Sequence[int], cov: bo
                     key_valid=_ptr(key_valid), kv_row=ne, roles=role_bytes,
                     stream=_stream_of(qkv, stream) if device else None)
     return variate_attend(a)
+
+
+def qkv_project(args: ProjArgs) -> int:
+    """``tsfm_qkv_project``: returns the ABI code."""
+    return int(load().tsfm_qkv_project(ctypes.byref(args)))
+
+
+def _proj(x, wq, wk, wv, q, k, v, *, batch: int, seq: int, d_in: int, nh: int, hd: int, x_tok: int, y_tok: int,
+          cos_t=None, sin_t=None, rope_rows_per_table: int = 0, rope_row0: int = 0, rope_table_stride: int = 0,
+          w_gate=None, gate=None, gate_tok: int = 0, stream=None) -> int:
+    device = _is_device(x)
+    a = ProjArgs(dtype=_dtype_code(x), batch=batch, seq=seq, d_in=d_in, heads=nh, head_dim=hd,
+                 flags=DEVICE_PTRS if device else 0, rope_half=hd // 2 if cos_t is not None else 0,
+                 rope_rows_per_table=rope_rows_per_table, rope_row0=rope_row0, rope_table_stride=rope_table_stride,
+                 x=_ptr(x), x_tok=x_tok, w_q=_ptr(wq), w_k=_ptr(wk), w_v=_ptr(wv), w_gate=_ptr(w_gate),
+                 q=_ptr(q), q_tok=y_tok, k=_ptr(k), k_tok=y_tok, v=_ptr(v), v_tok=y_tok, gate=_ptr(gate),
+                 gate_tok=gate_tok, rope_cos=_ptr(cos_t), rope_sin=_ptr(sin_t),
+                 stream=_stream_of(x, stream) if device else None)
+    return qkv_project(a)
+
+
+def chronos2_qkv_projection(xn, wq, wk, wv, q, k, v, cos_t, sin_t, b: int, seq: int, d: int, nh: int, hd: int,
+                            stream=None) -> int:
+    """Chronos-2 time-attention projections (src/chronos2/model.zig:232-245): q, k, v =
+    nn.linear(xn, W) for the three (d, d) weights, then RoPE on every head of q and k with the
+    (seq, hd/2) tables. xn, q, k, v are (b * seq, d)."""
+    return _proj(xn, wq, wk, wv, q, k, v, batch=b, seq=seq, d_in=d, nh=nh, hd=hd, x_tok=d, y_tok=d, cos_t=cos_t,
+                 sin_t=sin_t, stream=stream)
+
+
+def timestral_qkv_projection(xn, w_qkv, qkv, cos_t, sin_t, rows: int, vall: int, sl: int, d: int, nh: int, hd: int,
+                             w_gate=None, gate=None, stream=None) -> int:
+    """Timestral time-attention projections (src/timestral/model.zig:494-500,513): the fused qkv
+    nn.linear over the permuted (3d, d) weight into qkv (rows * sl, 3d), TimeJob.rope on its q and k
+    heads with the per-group (groups, sl, hd/2) tables, and with ``w_gate`` the gate nn.linear into
+    gate (rows * sl, d)."""
+    return _proj(xn, w_qkv, _flat_view(w_qkv, d * d), _flat_view(w_qkv, 2 * d * d), qkv, _flat_view(qkv, d),
+                 _flat_view(qkv, 2 * d), batch=rows, seq=sl, d_in=d, nh=nh, hd=hd, x_tok=d, y_tok=3 * d,
+                 cos_t=cos_t, sin_t=sin_t, rope_rows_per_table=vall, rope_table_stride=sl * (hd // 2),
+                 w_gate=w_gate, gate=gate, gate_tok=d if gate is not None else 0, stream=stream)
+
+
+def bolt_qkv_projection(x, wq, wk, wv, q, k, v, nb: int, seq: int, d: int, nh: int, hd: int, stream=None) -> int:
+    """Chronos-Bolt encoder self-attention projections (src/chronos_bolt/model.zig:239-241): q, k,
+    v = nn.linear(x, W) with (inner, d) weights, inner = nh * hd; no RoPE."""
+    return _proj(x, wq, wk, wv, q, k, v, batch=nb, seq=seq, d_in=d, nh=nh, hd=hd, x_tok=d, y_tok=nh * hd,
+                 stream=stream)
 
 
 # ---------------------------------------------------------------------------------------------

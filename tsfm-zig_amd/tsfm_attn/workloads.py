@@ -51,6 +51,8 @@ class Workload:
 
     @property
     def flops(self) -> float:
+        if "flops" in self.meta:  # not an attention count (the projection workload)
+            return float(self.meta["flops"])
         return 4.0 * self.D * self.pairs
 
     @property
@@ -165,3 +167,28 @@ def timestral_variate(groups: int = 8, vall: int = 4, H: int = 16, L: int = 2048
                  dict(seed=seed, groups=groups, vall=vall, L=L, pairs=groups * L * H * vall * vall))
     w.meta["bytes"] = 4.0 * rows * L * (3 * d + d + d)
     return w
+
+
+def chronos2_projection(B: int = 64, H: int = 12, n_ctx: int = 512, n_fut: int = 64, seed: int = 0,
+                        theta: float = 10000.0) -> Workload:
+    """Chronos-2 time-attention projections at the attention's shape (src/chronos2/model.zig:232-245):
+    x (B * L, d) ~ N(0, 1) standing for the rmsNorm output, W_q, W_k, W_v (d, d) ~ N(0, 1/d), RoPE
+    tables (L, 32) as the attention workload's. FLOPs = 2 * tokens * d * 3d; bytes = x and the three
+    weights read once, q, k, v written once, plus the tables."""
+    L, D = n_ctx + 1 + n_fut, 64
+    d = H * D
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((B * L, d), dtype=np.float32)
+    ws = [(rng.standard_normal((d, d), dtype=np.float32) / np.float32(np.sqrt(d))).astype(np.float32)
+          for _ in range(3)]
+    half = D // 2
+    inv = (1.0 / np.power(np.float32(theta), np.arange(0, D, 2, dtype=np.float32) / np.float32(D))).astype(np.float32)
+    ang = (np.arange(L, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    cos_t = np.cos(ang).astype(np.float32).reshape(L * half)
+    sin_t = np.sin(ang).astype(np.float32).reshape(L * half)
+    tokens = B * L
+    flops = 2.0 * tokens * d * 3 * d
+    nbytes = 4.0 * (tokens * d + 3 * d * d + 3 * tokens * d + 2 * L * half)
+    return Workload("chronos2_qkv_projection", "f32", B, H, L, L, D, 1.0,
+                    dict(x=x, wq=ws[0], wk=ws[1], wv=ws[2], rope_cos=cos_t, rope_sin=sin_t),
+                    dict(d_model=d, tokens=tokens, flops=flops, bytes=nbytes, seed=seed, num_layers=12))
