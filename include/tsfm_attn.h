@@ -210,14 +210,16 @@ typedef struct tsfm_proj_args {
     uint32_t flags;     /* TSFM_ATTN_DEVICE_PTRS or 0 */
     int32_t rope_half;  /* 32 when rope_cos is set */
     int32_t rope_rows_per_table, rope_row0;
+    int32_t out_dtype;  /* element type of q/k/v/gate: TSFM_DTYPE_F32, _BF16 or _F16 (rounded once,
+                         * to nearest even, from the f32 result; feeds the half-precision attention) */
     int64_t rope_table_stride;
     const float *x; int64_t x_tok;
     const float *w_q, *w_k, *w_v;
     const float *w_gate;            /* optional; with gate */
-    float *q;    int64_t q_tok;
-    float *k;    int64_t k_tok;
-    float *v;    int64_t v_tok;
-    float *gate; int64_t gate_tok;  /* optional; with w_gate */
+    void *q;    int64_t q_tok;      /* strides in elements of out_dtype */
+    void *k;    int64_t k_tok;
+    void *v;    int64_t v_tok;
+    void *gate; int64_t gate_tok;   /* optional; with w_gate */
     const float *rope_cos, *rope_sin;
     void *stream;
 } tsfm_proj_args;

@@ -194,6 +194,7 @@ def _proj_host_args(ta, **over):
     (dict(x_tok=32), 3),                # token stride shorter than d_in
     (dict(q_tok=64), 3),                # token stride shorter than heads * 64
     (dict(w_gate=1 << 20), 3),          # w_gate without gate
+    (dict(out_dtype=3), 3),             # not a TSFM_DTYPE_*
 ])
 def test_proj_validation_codes(ta, over, code):
     a, _keep = _proj_host_args(ta, **over)

@@ -132,3 +132,42 @@ def test_padded_strides_leave_padding_untouched(ta, orc, gpu_ready):
     for got, ref in zip(outs, (qf, kf, v)):
         assert _ref.scaled_err(got[:, :width], ref) <= TOL
         assert np.all(got[:, width:] == -5.0)
+
+
+@pytest.mark.parametrize("out", ["float16", "bfloat16"])
+@pytest.mark.parametrize("device", [False, True])
+def test_half_outputs_round_the_f32_result(ta, orc, gpu_ready, out, device):
+    """q/k/v/gate emitted in bf16 or f16 for the half-precision attention: the f32 result rounded
+    once. The bound is the rounding itself (half an ulp: 2^-11 relative for f16, 2^-8 for bf16)
+    plus the f32 product's own difference from the oracle."""
+    import torch
+
+    groups, vall, ne, l, h, nh = 2, 2, 40, 32, 8, 3
+    d, sl, rows = nh * 64, ne + h, groups * vall
+    rng = np.random.default_rng(60 + device)
+    x = rng.standard_normal((rows * sl, d)).astype(np.float32)
+    w_qkv = (rng.standard_normal((3 * d, d)) / np.sqrt(d)).astype(np.float32)
+    w_gate = (rng.standard_normal((d, d)) / np.sqrt(d)).astype(np.float32)
+    cos_t, sin_t = orc.timestral_rope_tables(groups, ne, l, h, 64, 32, 10000.0, [3, 0])
+    dt = getattr(torch, out)
+    qkv = torch.full((rows * sl, 3 * d), -3.0, dtype=dt)
+    gate = torch.full((rows * sl, d), -3.0, dtype=dt)
+    args = [x, w_qkv, qkv, cos_t, sin_t]
+    if device:
+        args = [torch.from_numpy(a).cuda() if isinstance(a, np.ndarray) else a.cuda() for a in args]
+        wg, gt = torch.from_numpy(w_gate).cuda(), gate.cuda()
+    else:
+        wg, gt = w_gate, gate
+    rc = ta.timestral_qkv_projection(*args, rows, vall, sl, d, nh, 64, w_gate=wg, gate=gt)
+    assert rc == ta.OK, ta.last_error()
+    if device:
+        torch.cuda.synchronize()
+        qkv, gate = args[2].cpu(), gt.cpu()
+    want = _linear(orc, x, w_qkv)
+    orc.timestral_rope(THREADS, want, cos_t, sin_t, rows, sl, vall, d, nh, 64)
+    rel = 2.0 ** -11 if out == "float16" else 2.0 ** -8
+    for got, ref in ((qkv, want), (gate, _linear(orc, x, w_gate))):
+        g = got.float().numpy()
+        assert np.all(np.abs(g - ref) <= rel * np.abs(ref) + 1e-5 * np.maximum(np.abs(ref), 1.0))
+        # and it is the rounding of a value within the f32 bar of the oracle
+        assert _ref.scaled_err(g, torch.from_numpy(ref).to(dt).float().numpy()) <= 2 * rel

@@ -434,7 +434,9 @@ int tsfm_variate_attend(const tsfm_variate_args* a) {
 
 int tsfm_qkv_project(const tsfm_proj_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
-    if (a->dtype != TSFM_DTYPE_F32) return fail(TSFM_E_UNSUPPORTED, "the projection is f32 only");
+    if (a->dtype != TSFM_DTYPE_F32) return fail(TSFM_E_UNSUPPORTED, "the projection computes in f32 only");
+    if (a->out_dtype < TSFM_DTYPE_F32 || a->out_dtype > TSFM_DTYPE_F16)
+        return fail(TSFM_E_INVALID, "bad out_dtype %d", a->out_dtype);
     if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
     if (a->batch < 0 || a->seq < 0 || a->d_in < 0 || a->heads < 0) return fail(TSFM_E_INVALID, "negative size");
     if (a->x == nullptr || a->w_q == nullptr || a->w_k == nullptr || a->w_v == nullptr || a->q == nullptr ||
@@ -467,6 +469,8 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     p.x = a->x; p.x_tok = a->x_tok;
     p.w0 = a->w_q; p.w1 = a->w_k; p.w2 = a->w_v; p.w3 = a->w_gate;
     p.y0 = a->q; p.y1 = a->k; p.y2 = a->v; p.y3 = a->gate;
+    p.out_dtype = a->out_dtype;
+    const int64_t oes = (int64_t)elem_size(a->out_dtype);
     p.y0_tok = a->q_tok; p.y1_tok = a->k_tok; p.y2_tok = a->v_tok; p.y3_tok = a->gate_tok;
     p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
     p.rope_table_stride = a->rope_table_stride;
@@ -486,9 +490,10 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     // Host pointers: stage x, the weights and the tables, run, copy the output rows back.
     const size_t x_n = (size_t)span(1, tokens, a->x_tok, 0, a->d_in) * 4;
     const size_t w_n = (size_t)(width * a->d_in) * 4;
-    const size_t y_n[4] = {(size_t)span(1, tokens, a->q_tok, 0, width) * 4, (size_t)span(1, tokens, a->k_tok, 0, width) * 4,
-                           (size_t)span(1, tokens, a->v_tok, 0, width) * 4,
-                           gated ? (size_t)span(1, tokens, a->gate_tok, 0, width) * 4 : 0};
+    const size_t y_n[4] = {(size_t)(span(1, tokens, a->q_tok, 0, width) * oes),
+                           (size_t)(span(1, tokens, a->k_tok, 0, width) * oes),
+                           (size_t)(span(1, tokens, a->v_tok, 0, width) * oes),
+                           gated ? (size_t)(span(1, tokens, a->gate_tok, 0, width) * oes) : 0};
     size_t t_n = 0;
     if (rope) {
         const int64_t last = a->rope_rows_per_table > 0 ? (a->rope_row0 + a->batch - 1) / a->rope_rows_per_table : 0;
@@ -518,10 +523,10 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     p.w1 = reinterpret_cast<const float*>(base + w_at[1]);
     p.w2 = reinterpret_cast<const float*>(base + w_at[2]);
     p.w3 = gated ? reinterpret_cast<const float*>(base + w_at[3]) : nullptr;
-    p.y0 = reinterpret_cast<float*>(base + y_at[0]);
-    p.y1 = reinterpret_cast<float*>(base + y_at[1]);
-    p.y2 = reinterpret_cast<float*>(base + y_at[2]);
-    p.y3 = gated ? reinterpret_cast<float*>(base + y_at[3]) : nullptr;
+    p.y0 = base + y_at[0];
+    p.y1 = base + y_at[1];
+    p.y2 = base + y_at[2];
+    p.y3 = gated ? base + y_at[3] : nullptr;
     if (rope) {
         p.rope_cos = reinterpret_cast<const float*>(base + c_at);
         p.rope_sin = reinterpret_cast<const float*>(base + s_at);
@@ -531,10 +536,10 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
         (void)hipStreamSynchronize(s);
         return hip_fail(e, "projection launch");
     }
-    float* const dst[4] = {a->q, a->k, a->v, a->gate};
+    void* const dst[4] = {a->q, a->k, a->v, a->gate};
     const int64_t tok[4] = {a->q_tok, a->k_tok, a->v_tok, a->gate_tok};
     for (int i = 0; i < (gated ? 4 : 3); i++)
-        if ((e = copy_rows_d2h(dst[i], base + y_at[i], 1, tokens, 0, tok[i] * 4, width * 4, s)) != hipSuccess)
+        if ((e = copy_rows_d2h(dst[i], base + y_at[i], 1, tokens, 0, tok[i] * oes, width * oes, s)) != hipSuccess)
             return hip_fail(e, "device-to-host copy");
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
     return TSFM_OK;

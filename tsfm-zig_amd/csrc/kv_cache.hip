@@ -23,26 +23,11 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int NK = 64;
 constexpr int NWAVE = 4;
 constexpr int NT = 64 * NWAVE;
 constexpr int QB = 32;  // queries per workgroup
-
-template <bool BF16>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    if constexpr (BF16) {
-        const bf16x2 v = {(__bf16)a, (__bf16)b};
-        return __builtin_bit_cast(uint32_t, v);
-    } else {
-        const f16x2 v = {(_Float16)a, (_Float16)b};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-}
 
 template <bool BF16>
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {

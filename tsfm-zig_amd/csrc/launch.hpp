@@ -42,17 +42,18 @@ struct VariateParams {
 hipError_t launch_variate(const VariateParams& p, hipStream_t stream);
 
 // Fused projection (proj.hip): output sel (0..n_out-1) is y_sel[token, :] = x[token, :] w_sel^T,
-// width columns each; outputs 0 and 1 (q, k) get RoPE when rope_cos is set. f32; d_in a multiple
+// width columns each; outputs 0 and 1 (q, k) get RoPE when rope_cos is set. f32 in (out_dtype:
+// 0 f32, 1 bf16, 2 f16 out); d_in a multiple
 // of 16, width a multiple of 64, x_tok, y*_tok multiples of 4 and 16-byte aligned pointers.
 struct ProjParams {
     const float* x; int64_t x_tok;
     const float *w0, *w1, *w2, *w3;  // (width, d_in) row-major each
-    float *y0, *y1, *y2, *y3;
+    void *y0, *y1, *y2, *y3;             // f32, bf16 or f16 elements (out_dtype)
     int64_t y0_tok, y1_tok, y2_tok, y3_tok;
     const float* rope_cos; const float* rope_sin;
     int64_t rope_table_stride;
     int32_t rope_rows_per_table, rope_row0;
-    int32_t tokens, seq, d_in, width, n_out;
+    int32_t tokens, seq, d_in, width, n_out, out_dtype;
     int32_t m_tiles, n_tiles;  // set by launch_proj
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);

@@ -18,7 +18,8 @@
 // HBM/L2 -> registers -> LDS (double-buffered, one barrier per step), and each of the four waves
 // multiplies a 64 x 64 sub-tile with v_mfma_f32_16x16x4_f32, the weight rows as the A operand so
 // that each lane ends with four consecutive output columns of one token (16-byte stores, and the
-// RoPE partner column i + 32 in the same lane). Three workgroups share a CU (40 KB of LDS and at
+// RoPE partner column i + 32 in the same lane); f32 outputs, or bf16/f16 for the half-precision
+// attention path. Three workgroups share a CU (40 KB of LDS and at
 // most 168 registers per lane each), so a wave waiting at its step's barrier or LDS reads leaves
 // the matrix pipe to two others.
 #include "common.hpp"
@@ -47,6 +48,9 @@ __device__ __forceinline__ void tile_of(int id, int m_tiles, int n_tiles, int& t
     tn = r / gm;
 }
 
+// OUT: element type of the outputs, TSFM_DTYPE_* (0 f32, 1 bf16, 2 f16); the products and RoPE
+// are f32 either way and the result is rounded once, to nearest even, when it is stored.
+template <int OUT>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void qkv_proj(ProjParams p) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* const xs = smem;                          // [2][BM][LDS_ROW]
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     const int n0 = tn * BN + wn * 64;
     if (n0 >= n_cols) return;
     const int sel = n0 / p.width, col = n0 - sel * p.width;
-    float* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
+    void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
     const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
     const bool rope = p.rope_cos != nullptr && sel < 2;
     const int cq = 4 * (lane >> 4);
@@ -149,9 +153,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             for (int nb = 0; nb < 2; nb++)
                 rope4(acc[nb][mb], acc[nb + 2][mb], ld4(p.rope_cos + at + 16 * nb), ld4(p.rope_sin + at + 16 * nb));
         }
-        float* const out = y + (int64_t)m * y_tok + col + cq;
+        const int64_t at = (int64_t)m * y_tok + col + cq;
+        if constexpr (OUT == 0) {
+            float* const out = static_cast<float*>(y) + at;
 #pragma unroll
-        for (int nb = 0; nb < 4; nb++) st4(out + 16 * nb, acc[nb][mb]);
+            for (int nb = 0; nb < 4; nb++) st4(out + 16 * nb, acc[nb][mb]);
+        } else {
+            uint16_t* const out = static_cast<uint16_t*>(y) + at;
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) {
+                const f32x4 v = acc[nb][mb];
+                *reinterpret_cast<u32x2*>(out + 16 * nb) = u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
+            }
+        }
     }
 }
 
@@ -160,12 +174,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
-    if (p.d_in % BK || p.d_in <= 0 || p.width % kHeadDim || p.n_out > 4 || p.seq <= 0) return hipErrorInvalidValue;
+    if (p.d_in % BK || p.d_in <= 0 || p.width % kHeadDim || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 ||
+        p.out_dtype > 2)
+        return hipErrorInvalidValue;
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
     const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(qkv_proj, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
+    if (p.out_dtype == 1)
+        hipLaunchKernelGGL(qkv_proj<1>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
+    else if (p.out_dtype == 2)
+        hipLaunchKernelGGL(qkv_proj<2>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
+    else
+        hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
     return hipGetLastError();
 }
 

@@ -199,6 +199,7 @@ class ProjArgs(ctypes.Structure):
         ("rope_half", ctypes.c_int32),
         ("rope_rows_per_table", ctypes.c_int32),
         ("rope_row0", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
         ("rope_table_stride", ctypes.c_int64),
         ("x", ctypes.c_void_p),
         ("x_tok", ctypes.c_int64),
@@ -526,7 +527,7 @@ def _proj(x, wq, wk, wv, q, k, v, *, batch: int, seq: int, d_in: int, nh: int, h
           cos_t=None, sin_t=None, rope_rows_per_table: int = 0, rope_row0: int = 0, rope_table_stride: int = 0,
           w_gate=None, gate=None, gate_tok: int = 0, stream=None) -> int:
     device = _is_device(x)
-    a = ProjArgs(dtype=_dtype_code(x), batch=batch, seq=seq, d_in=d_in, heads=nh, head_dim=hd,
+    a = ProjArgs(dtype=_dtype_code(x), out_dtype=_dtype_code(q), batch=batch, seq=seq, d_in=d_in, heads=nh, head_dim=hd,
                  flags=DEVICE_PTRS if device else 0, rope_half=hd // 2 if cos_t is not None else 0,
                  rope_rows_per_table=rope_rows_per_table, rope_row0=rope_row0, rope_table_stride=rope_table_stride,
                  x=_ptr(x), x_tok=x_tok, w_q=_ptr(wq), w_k=_ptr(wk), w_v=_ptr(wv), w_gate=_ptr(w_gate),
