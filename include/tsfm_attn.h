@@ -227,6 +227,27 @@ typedef struct tsfm_proj_args {
 int tsfm_qkv_project(const tsfm_proj_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * The reference backend's GEMM seam, with the signatures of src/platform/cuda/gemm.c so that the
+ * reference's own binding (src/platform/cuda/gpu.zig:16-44) can link this library unchanged:
+ * nn.linear's weight products (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then
+ * run on the gfx950 matrix cores (the projection kernel, one output, no RoPE).
+ *
+ * tsfm_weight_register: cuda_weight_register (gemm.c:232-242): a device copy of `len` floats,
+ *   NULL on failure. tsfm_weight_release: cuda_weight_release (gemm.c:244-247).
+ * tsfm_sgemm_nt: cuda_sgemm_nt (gemm.c:316-322): C[m, n] = alpha * A[m, k] B[n, k]^T, row-major
+ *   with leading dimensions; host pointers, synchronous; b_buf = a registered weight (B unused)
+ *   or NULL (B uploaded). 0 = done; non-zero = use the CPU. Runs when k % 16 == 0 and n, lda,
+ *   ldb, ldc are multiples of 4 (every linear layer of the three families).
+ * tsfm_sgemm_nn: cuda_sgemm_nn (gemm.c:324-330); always returns TSFM_E_UNSUPPORTED (the caller's
+ *   CPU path runs): its one user, the attention's P.V product, runs inside tsfm_attn_fwd. */
+void *tsfm_weight_register(const float *data, size_t len);
+void tsfm_weight_release(void *handle);
+int tsfm_sgemm_nt(int m, int n, int k, float alpha, const float *A, int lda, const float *B, int ldb, float *C,
+                  int ldc, void *b_buf);
+int tsfm_sgemm_nn(int m, int n, int k, const float *A, int lda, const float *B, int ldb, float *C, int ldc,
+                  void *b_buf);
+
+/* ---------------------------------------------------------------------------------------------
  * KV cache for block-autoregressive decode. No counterpart in the reference: Timestral's
  * blockDecode re-encodes the whole grown context every block (src/timestral/forecaster.zig:423-563),
  * recomputing K/V of unchanged prefix tokens. With a causal encoder and a fixed prefix the cached

@@ -206,3 +206,24 @@ def test_proj_empty_is_a_no_op(ta):
     for over in (dict(batch=0), dict(seq=0), dict(heads=0)):
         a, _keep = _proj_host_args(ta, **over)
         assert ta.qkv_project(a) == ta.OK
+
+
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc,code", [
+    (0, 8, 16, 16, 16, 8, 3),     # empty: the caller's CPU path (cuda_sgemm_nt returns -1 too)
+    (4, 8, 16, 12, 16, 8, 3),     # lda < k
+    (4, 8, 24, 24, 24, 8, 2),     # k not a multiple of 16
+    (4, 6, 16, 16, 16, 8, 2),     # n not a multiple of 4
+    (4, 8, 16, 18, 16, 8, 2),     # lda not a multiple of 4
+])
+def test_sgemm_nt_argument_codes(ta, m, n, k, lda, ldb, ldc, code):
+    a = np.zeros(max(m, 1) * lda, np.float32)
+    b = np.zeros(n * ldb, np.float32)
+    c = np.zeros(max(m, 1) * ldc, np.float32)
+    assert ta.sgemm_nt(m, n, k, 1.0, a, lda, b, ldb, c, ldc) == code
+    assert ta.last_error()
+
+
+def test_sgemm_nn_declines(ta):
+    a = np.zeros(64, np.float32)
+    lib = ta.load()
+    assert lib.tsfm_sgemm_nn(4, 4, 4, a.ctypes.data, 4, a.ctypes.data, 4, a.ctypes.data, 4, None) == ta.E_UNSUPPORTED

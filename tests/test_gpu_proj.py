@@ -171,3 +171,54 @@ def test_half_outputs_round_the_f32_result(ta, orc, gpu_ready, out, device):
         assert np.all(np.abs(g - ref) <= rel * np.abs(ref) + 1e-5 * np.maximum(np.abs(ref), 1.0))
         # and it is the rounding of a value within the f32 bar of the oracle
         assert _ref.scaled_err(g, torch.from_numpy(ref).to(dt).float().numpy()) <= 2 * rel
+
+
+# ---- the reference backend's GEMM seam: tsfm_sgemm_nt / tsfm_weight_register ---------------------
+
+
+@pytest.mark.parametrize("m,n,k,pad", [(37, 36, 48, 0), (300, 128, 160, 4), (129, 2304, 768, 0), (5, 4, 16, 8)])
+def test_sgemm_nt_matches_oracle_gemm_nt(ta, orc, gpu_ready, m, n, k, pad):
+    """cuda_sgemm_nt's contract (src/platform/cuda/gemm.c:316-322): C = alpha A B^T with leading
+    dimensions; only the n columns of each C row are written. Against the oracle's gemmNT."""
+    rng = np.random.default_rng(m + n + k)
+    lda, ldb, ldc = k + pad, k + 2 * pad, n + pad
+    a = rng.standard_normal(m * lda).astype(np.float32)
+    b = rng.standard_normal(n * ldb).astype(np.float32)
+    c = np.full(m * ldc, -9.0, np.float32)
+    assert ta.sgemm_nt(m, n, k, 0.7, a, lda, b, ldb, c, ldc) == ta.OK, ta.last_error()
+    want = np.zeros(m * ldc, np.float32)
+    orc.gemm_nt(want, ldc, a, lda, b, ldb, m, n, k, 0.7)
+    got, ref = c.reshape(m, ldc)[:, :n], want.reshape(m, ldc)[:, :n]
+    assert np.all(c.reshape(m, ldc)[:, n:] == -9.0)
+    # Unnormalised N(0, 1) operands: any f32 summation order is off the exact product by up to
+    # k * 2^-24 * sum|a_i b_i| (the textbook bound); the oracle's order and the matrix cores' differ,
+    # so both are held to that bound against float64 rather than to each other.
+    A = a.reshape(m, lda)[:, :k].astype(np.float64)
+    B = b.reshape(n, ldb)[:, :k].astype(np.float64)
+    exact = 0.7 * A @ B.T
+    bound = k * 2.0 ** -24 * 0.7 * (np.abs(A) @ np.abs(B).T) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.all(np.abs(ref - exact) <= bound)
+    # and no further from float64 than a few times the oracle (one accumulator per output against
+    # the oracle's sixteen lane sums and a tree)
+    assert np.abs(got - exact).max() <= 8 * np.abs(ref - exact).max() + 1e-7
+
+
+def test_registered_weight_linear_matches_oracle(ta, orc, gpu_ready):
+    """nn.linear with a registered weight (Weight.handle, src/core/nn.zig:276-283): the same result
+    as with the weight uploaded per call, and as the oracle's linear."""
+    rows, inp, out = 150, 768, 3072
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((rows, inp)).astype(np.float32)
+    w = (rng.standard_normal((out, inp)) / np.sqrt(inp)).astype(np.float32)
+    h = ta.weight_register(w)
+    assert h is not None, ta.last_error()
+    try:
+        y1 = np.zeros((rows, out), np.float32)
+        y2 = np.zeros((rows, out), np.float32)
+        assert ta.linear(y1, x, rows, w, out, inp, w_buf=h) == ta.OK, ta.last_error()
+        assert ta.linear(y2, x, rows, w, out, inp) == ta.OK, ta.last_error()
+    finally:
+        ta.weight_release(h)
+    assert np.array_equal(y1, y2)
+    assert _ref.scaled_err(y1, _linear(orc, x, w)) <= TOL

@@ -468,6 +468,7 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     tsfm::ProjParams p{};
     p.x = a->x; p.x_tok = a->x_tok;
     p.w0 = a->w_q; p.w1 = a->w_k; p.w2 = a->w_v; p.w3 = a->w_gate;
+    p.w_ld = a->d_in; p.alpha = 1.f; p.epi = tsfm::kEpiNone;
     p.y0 = a->q; p.y1 = a->k; p.y2 = a->v; p.y3 = a->gate;
     p.out_dtype = a->out_dtype;
     const int64_t oes = (int64_t)elem_size(a->out_dtype);
@@ -543,6 +544,73 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
             return hip_fail(e, "device-to-host copy");
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
     return TSFM_OK;
+}
+
+// ---- the reference backend's GEMM seam ------------------------------------------------------------
+
+void* tsfm_weight_register(const float* data, size_t len) {
+    if (len == 0 || data == nullptr || ensure_ready() != TSFM_OK) return nullptr;
+    void* dev = nullptr;
+    if (hipSetDevice(g_device) != hipSuccess || hipMalloc(&dev, len * sizeof(float)) != hipSuccess || dev == nullptr) {
+        fail(TSFM_E_DEVICE, "weight allocation of %zu floats failed", len);
+        return nullptr;
+    }
+    if (hipMemcpy(dev, data, len * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(dev);
+        fail(TSFM_E_DEVICE, "weight upload failed");
+        return nullptr;
+    }
+    return dev;
+}
+
+void tsfm_weight_release(void* handle) {
+    if (handle != nullptr) (void)hipFree(handle);
+}
+
+int tsfm_sgemm_nt(int m, int n, int k, float alpha, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
+                  void* b_buf) {
+    if (m <= 0 || n <= 0 || k <= 0) return fail(TSFM_E_INVALID, "empty or negative product %d x %d x %d", m, n, k);
+    if (A == nullptr || C == nullptr || (B == nullptr && b_buf == nullptr)) return fail(TSFM_E_INVALID, "NULL operand");
+    if (lda < k || ldb < k || ldc < n) return fail(TSFM_E_INVALID, "leading dimension shorter than the row");
+    if (k % 16 || n % 4 || lda % 4 || ldb % 4 || ldc % 4)
+        return fail(TSFM_E_UNSUPPORTED, "k must be a multiple of 16, n and the leading dimensions of 4");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    const size_t a_n = ((size_t)(m - 1) * lda + k) * 4, b_n = b_buf ? 0 : ((size_t)(n - 1) * ldb + k) * 4;
+    const size_t c_n = ((size_t)(m - 1) * ldc + n) * 4;
+    Plan plan;
+    const size_t a_at = plan.take(a_n), b_at = plan.take(b_n), c_at = plan.take(c_n);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(base + a_at, A, a_n, hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "host-to-device copy");
+    if (b_n && (e = hipMemcpyAsync(base + b_at, B, b_n, hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "host-to-device copy");
+    tsfm::ProjParams p{};
+    p.x = reinterpret_cast<const float*>(base + a_at); p.x_tok = lda;
+    p.w0 = b_buf ? static_cast<const float*>(b_buf) : reinterpret_cast<const float*>(base + b_at);
+    p.w_ld = ldb; p.alpha = alpha; p.epi = tsfm::kEpiNone;
+    p.y0 = base + c_at; p.y0_tok = ldc;
+    p.tokens = m; p.seq = m; p.d_in = k; p.width = n; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
+    if ((e = tsfm::launch_proj(p, s)) != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "GEMM launch");
+    }
+    if ((e = copy_rows_d2h(C, base + c_at, 1, m, 0, (int64_t)ldc * 4, (int64_t)n * 4, s)) != hipSuccess)
+        return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
+int tsfm_sgemm_nn(int m, int n, int k, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
+                  void* b_buf) {
+    (void)m; (void)n; (void)k; (void)A; (void)lda; (void)B; (void)ldb; (void)C; (void)ldc; (void)b_buf;
+    return fail(TSFM_E_UNSUPPORTED, "A x B is not run here: the attention's products run inside tsfm_attn_fwd");
 }
 
 // ---- KV cache ------------------------------------------------------------------------------------

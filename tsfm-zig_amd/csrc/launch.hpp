@@ -42,12 +42,18 @@ struct VariateParams {
 hipError_t launch_variate(const VariateParams& p, hipStream_t stream);
 
 // Fused projection (proj.hip): output sel (0..n_out-1) is y_sel[token, :] = x[token, :] w_sel^T,
-// width columns each; outputs 0 and 1 (q, k) get RoPE when rope_cos is set. f32 in (out_dtype:
+// width columns each (a multiple of 64, or of 4 with a single output); outputs 0 and 1 (q, k)
+// get RoPE when rope_cos is set. f32 in (out_dtype:
 // 0 f32, 1 bf16, 2 f16 out); d_in a multiple
 // of 16, width a multiple of 64, x_tok, y*_tok multiples of 4 and 16-byte aligned pointers.
+constexpr int kEpiNone = 0, kEpiRelu = 1, kEpiResidual = 2;
 struct ProjParams {
     const float* x; int64_t x_tok;
-    const float *w0, *w1, *w2, *w3;  // (width, d_in) row-major each
+    const float *w0, *w1, *w2, *w3;  // (width, d_in) row-major each, rows w_ld apart
+    int64_t w_ld;
+    float alpha;                     // result scale (1: none)
+    int32_t epi;                     // kEpi*: f32 outputs only
+    const float* resid; int64_t resid_tok;  // kEpiResidual: y = resid + x w^T (resid may be y)
     void *y0, *y1, *y2, *y3;             // f32, bf16 or f16 elements (out_dtype)
     int64_t y0_tok, y1_tok, y2_tok, y3_tok;
     const float* rope_cos; const float* rope_sin;

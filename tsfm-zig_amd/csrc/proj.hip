@@ -73,7 +73,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         const int n = min(tn * BN + lr + LROWS * i, n_cols - 1);
         const int sel = n / p.width;
         const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
-        wp[i] = w + (int64_t)(n - sel * p.width) * p.d_in + lc;
+        wp[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + lc;
     }
     f32x4 rx[LPASS], rw[LPASS];
     auto fetch = [&](int k0) {
@@ -132,7 +132,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         __syncthreads();
     }
 
-    // Epilogue: this wave's 64 columns are one head of one output.
+    // Epilogue: this wave's 64 columns are one head of one output (or, with one output of a width
+    // that is not a multiple of 64, the first columns of a partial block: groups of four columns
+    // past the width are not stored).
     const int n0 = tn * BN + wn * 64;
     if (n0 >= n_cols) return;
     const int sel = n0 / p.width, col = n0 - sel * p.width;
@@ -144,6 +146,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     for (int mb = 0; mb < 4; mb++) {
         const int m = tm * BM + wm * 64 + mb * 16 + (lane & 15);
         if (m >= p.tokens) continue;
+        if (p.alpha != 1.f) {  // gemmNT's alpha, applied to the finished sum (src/core/nn.zig:100)
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) acc[nb][mb] *= p.alpha;
+        }
         if (rope) {
             // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table.
             const int b = m / p.seq, tok = m - b * p.seq;
@@ -156,8 +162,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         const int64_t at = (int64_t)m * y_tok + col + cq;
         if constexpr (OUT == 0) {
             float* const out = static_cast<float*>(y) + at;
+            const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col + cq : nullptr;
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++) st4(out + 16 * nb, acc[nb][mb]);
+            for (int nb = 0; nb < 4; nb++) {
+                if (col + cq + 16 * nb >= p.width) continue;
+                f32x4 v = acc[nb][mb];
+                if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
+                else if (p.epi == kEpiResidual) v = ld4(res + 16 * nb) + v;  // x + delta, one rounding
+                st4(out + 16 * nb, v);
+            }
         } else {
             uint16_t* const out = static_cast<uint16_t*>(y) + at;
 #pragma unroll
@@ -174,8 +187,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
-    if (p.d_in % BK || p.d_in <= 0 || p.width % kHeadDim || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 ||
-        p.out_dtype > 2)
+    if (p.d_in % BK || p.d_in <= 0 || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 || p.out_dtype > 2 ||
+        p.w_ld < p.d_in || p.width % 4 || (p.n_out > 1 && p.width % kHeadDim) ||
+        (p.rope_cos != nullptr && p.width % kHeadDim) || (p.out_dtype != 0 && (p.epi != kEpiNone || p.alpha != 1.f)))
         return hipErrorInvalidValue;
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;

@@ -57,6 +57,10 @@ EXPORTS = (
     "tsfm_t5_bucket_table",
     "tsfm_variate_attend",
     "tsfm_qkv_project",
+    "tsfm_weight_register",
+    "tsfm_weight_release",
+    "tsfm_sgemm_nt",
+    "tsfm_sgemm_nn",
     "tsfm_kv_create",
     "tsfm_kv_free",
     "tsfm_kv_reset",
@@ -267,6 +271,15 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_variate_attend.restype = ctypes.c_int
     lib.tsfm_qkv_project.argtypes = [ctypes.POINTER(ProjArgs)]
     lib.tsfm_qkv_project.restype = ctypes.c_int
+    lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
+    lib.tsfm_weight_register.restype = vp
+    lib.tsfm_weight_release.argtypes = [vp]
+    lib.tsfm_weight_release.restype = None
+    ci, cf = ctypes.c_int, ctypes.c_float
+    lib.tsfm_sgemm_nt.argtypes = [ci, ci, ci, cf, vp, ci, vp, ci, vp, ci, vp]
+    lib.tsfm_sgemm_nt.restype = ci
+    lib.tsfm_sgemm_nn.argtypes = [ci, ci, ci, vp, ci, vp, ci, vp, ci, vp]
+    lib.tsfm_sgemm_nn.restype = ci
     if path is None:
         _lib = lib
     return lib
@@ -563,6 +576,30 @@ def bolt_qkv_projection(x, wq, wk, wv, q, k, v, nb: int, seq: int, d: int, nh: i
     v = nn.linear(x, W) with (inner, d) weights, inner = nh * hd; no RoPE."""
     return _proj(x, wq, wk, wv, q, k, v, batch=nb, seq=seq, d_in=d, nh=nh, hd=hd, x_tok=d, y_tok=nh * hd,
                  stream=stream)
+
+
+def weight_register(w) -> Optional[int]:
+    """``tsfm_weight_register`` (Backend.register_weight): device copy of a C-contiguous f32 array;
+    the handle, or None on failure."""
+    n = int(w.numel()) if hasattr(w, "numel") else int(w.size)
+    h = load().tsfm_weight_register(_ptr(w), n)
+    return h or None
+
+
+def weight_release(handle: Optional[int]) -> None:
+    load().tsfm_weight_release(handle)
+
+
+def sgemm_nt(m: int, n: int, k: int, alpha: float, a, lda: int, b, ldb: int, c, ldc: int, b_buf=None) -> int:
+    """``tsfm_sgemm_nt`` (Backend.sgemm_nt): c[m, n] = alpha * a[m, k] b[n, k]^T with leading
+    dimensions, host arrays; ``b_buf`` a handle from :func:`weight_register` (then ``b`` is unused)."""
+    return int(load().tsfm_sgemm_nt(m, n, k, alpha, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc, b_buf))
+
+
+def linear(y, x, rows: int, w, out: int, inp: int, w_buf=None) -> int:
+    """nn.linear without bias through the backend seam (src/core/nn.zig:270-293): y (rows, out) =
+    x (rows, inp) w (out, inp)^T."""
+    return sgemm_nt(rows, out, inp, 1.0, x, inp, w, inp, y, out, w_buf)
 
 
 # ---------------------------------------------------------------------------------------------
