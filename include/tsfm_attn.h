@@ -227,6 +227,48 @@ typedef struct tsfm_proj_args {
 int tsfm_qkv_project(const tsfm_proj_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * Chronos-2 encoder stack: Model.encode's layer loop and final norm (src/chronos2/model.zig:144-206)
+ * in one call, every product on the matrix cores. Per layer, on x (batch * seq tokens of d_model):
+ *   x += o(attn(rope(q(n1(x))), rope(k(n1(x))), v(n1(x))))   time attention (:208-262), the mask
+ *        Mask.pick(false, keys_all_valid, true), the given scale (the model passes 1.0, :306);
+ *   x += o_g(v_g(n2(x)))                                       group attention, singleton groups (:264-269);
+ *   x += wo(relu(wi(n3(x))))                                   the MLP (:198-202);
+ * with n1..n3 the layer's rmsNorms (nn.rmsNorm, src/core/nn.zig:361-396), then x = rmsNorm(x, final_norm).
+ * x is the embedded tokens in and the hidden states out. Weights are nn.Weight's (out, in)
+ * row-major f32. head_dim 64, d_model = heads * 64, d_ff a multiple of 16. With
+ * TSFM_ATTN_DEVICE_PTRS every pointer (x, key_valid, tables, weights, final_norm; not `layers`
+ * itself) is device memory and the call is asynchronous on `stream` (its scratch is allocated
+ * and freed in stream order); with host pointers it uploads everything and returns when x is
+ * written back. */
+typedef struct tsfm_chronos2_layer {
+    const float *time_norm;                          /* (d) */
+    const float *time_q, *time_k, *time_v, *time_o;  /* (d, d) */
+    const float *group_norm;                         /* (d) */
+    const float *group_v, *group_o;                  /* (d, d) */
+    const float *mlp_norm;                           /* (d) */
+    const float *mlp_wi;                             /* (d_ff, d) */
+    const float *mlp_wo;                             /* (d, d_ff) */
+} tsfm_chronos2_layer;
+
+typedef struct tsfm_chronos2_encode_args {
+    int32_t batch;           /* series b */
+    int32_t seq;             /* tokens per series (n_ctx + 1 + n_out) */
+    int32_t d_model, heads, head_dim, d_ff, n_layers;
+    int32_t keys_all_valid;  /* non-zero: every key_valid byte is set (Mask.pick -> FULL) */
+    float eps;               /* layer_norm_epsilon */
+    float scale;             /* time-attention score scale */
+    uint32_t flags;          /* TSFM_ATTN_DEVICE_PTRS or 0 */
+    float *x;                /* (b * seq, d_model), in place */
+    const uint8_t *key_valid;          /* (b, seq) */
+    const float *rope_cos, *rope_sin;  /* (seq, head_dim / 2) */
+    const tsfm_chronos2_layer *layers; /* n_layers entries, host memory */
+    const float *final_norm;           /* (d) */
+    void *stream;
+} tsfm_chronos2_encode_args;
+
+int tsfm_chronos2_encode(const tsfm_chronos2_encode_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * The reference backend's GEMM seam, with the signatures of src/platform/cuda/gemm.c so that the
  * reference's own binding (src/platform/cuda/gpu.zig:16-44) can link this library unchanged:
  * nn.linear's weight products (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then

@@ -567,6 +567,98 @@ void orc_chronos2_time_attention(size_t threads, const float *q, const float *k,
     orc_for_range_min(threads, b * nh, 1, &job, c2_time_attend);
 }
 
+/* nn.rmsNorm (src/core/nn.zig:361-396): per row, a lane-parallel sum of squares (multiply, then
+ * add: no fused multiply-add in the Zig), an ordered lane reduce, the scalar tail, then
+ * inv = 1 / sqrt(ss / dim + eps) and out = x * inv * scale, left to right. Rows split over the pool
+ * in chunks of at least 64 (par.forRangeMin), which does not change the result. */
+typedef struct {
+    float *out;
+    const float *x;
+    size_t dim;
+    const float *scale;
+    float eps;
+} norm_ctx;
+
+static void rms_norm_rows(const void *p, size_t r0, size_t r1) {
+    const norm_ctx *c = (const norm_ctx *)p;
+    const size_t dim = c->dim;
+    for (size_t r = r0; r < r1; r++) {
+        const float *xr = c->x + r * dim;
+        float acc[L];
+        for (int e = 0; e < L; e++) acc[e] = 0.f;
+        size_t i = 0;
+        for (; i + L <= dim; i += L)
+            for (int e = 0; e < L; e++) {
+                const float sq = xr[i + e] * xr[i + e];
+                acc[e] = acc[e] + sq;
+            }
+        float ss = red_add(acc);
+        for (; i < dim; i++) ss += xr[i] * xr[i];
+        const float inv = 1.0f / sqrtf(ss / (float)dim + c->eps);
+        float *o = c->out + r * dim;
+        for (i = 0; i < dim; i++) {
+            const float t = xr[i] * inv;
+            o[i] = t * c->scale[i];
+        }
+    }
+}
+
+void orc_rms_norm(size_t threads, float *out, const float *x, size_t rows, size_t dim, const float *scale,
+                  float eps) {
+    const norm_ctx c = {out, x, dim, scale, eps};
+    orc_for_range_min(threads, rows, 64, &c, rms_norm_rows);
+}
+
+/* nn.relu (src/core/nn.zig:436-444). */
+void orc_relu(float *x, size_t n) {
+    for (size_t i = 0; i < n; i++) x[i] = x[i] > 0.f ? x[i] : 0.f;
+}
+
+/* Model.encode's layer loop and final norm (src/chronos2/model.zig:144-206): per layer, time
+ * attention (timeAttention, :208-262: q/k/v linear, the serial RoPE loop, TimeJob over
+ * (series, head) with Mask.pick(false, keys_all_valid, true), the o linear), group attention with
+ * singleton groups (groupAttention, :264-269: v linear then o linear) and the ReLU MLP, each
+ * behind an rmsNorm and added back to x; then the final rmsNorm in place. The attention scale is
+ * a parameter here (the model's TimeJob passes 1.0, :306). */
+void orc_chronos2_encode(size_t threads, float *x, const uint8_t *key_valid, size_t b, size_t seq, size_t d,
+                         size_t nh, size_t hd, size_t d_ff, size_t n_layers, const orc_chronos2_layer *layers,
+                         const float *final_norm, float eps, const float *cos_t, const float *sin_t, float scale) {
+    const size_t rows = b * seq;
+    float *xn = (float *)malloc(rows * d * sizeof(float));
+    float *delta = (float *)malloc(rows * d * sizeof(float));
+    float *mlp_h = (float *)malloc(rows * d_ff * sizeof(float));
+    float *qb = (float *)malloc(rows * d * sizeof(float));
+    float *kb = (float *)malloc(rows * d * sizeof(float));
+    float *vb = (float *)malloc(rows * d * sizeof(float));
+    float *ab = (float *)malloc(rows * d * sizeof(float));
+    int all_valid = 1;
+    for (size_t i = 0; i < rows; i++) all_valid = all_valid && key_valid[i] != 0;
+    for (size_t l = 0; l < n_layers; l++) {
+        const orc_chronos2_layer *ly = &layers[l];
+        orc_rms_norm(threads, xn, x, rows, d, ly->time_norm, eps);
+        orc_linear(threads, qb, xn, rows, ly->time_q, d, d, NULL);
+        orc_linear(threads, kb, xn, rows, ly->time_k, d, d, NULL);
+        orc_linear(threads, vb, xn, rows, ly->time_v, d, d, NULL);
+        orc_chronos2_rope(qb, kb, cos_t, sin_t, rows, seq, d, nh, hd);
+        orc_chronos2_time_attention(threads, qb, kb, vb, ab, key_valid, all_valid, b, seq, d, nh, hd, scale);
+        orc_linear(threads, delta, ab, rows, ly->time_o, d, d, NULL);
+        orc_add_in_place(x, delta, rows * d);
+
+        orc_rms_norm(threads, xn, x, rows, d, ly->group_norm, eps);
+        orc_linear(threads, vb, xn, rows, ly->group_v, d, d, NULL);
+        orc_linear(threads, delta, vb, rows, ly->group_o, d, d, NULL);
+        orc_add_in_place(x, delta, rows * d);
+
+        orc_rms_norm(threads, xn, x, rows, d, ly->mlp_norm, eps);
+        orc_linear(threads, mlp_h, xn, rows, ly->mlp_wi, d_ff, d, NULL);
+        orc_relu(mlp_h, rows * d_ff);
+        orc_linear(threads, delta, mlp_h, rows, ly->mlp_wo, d, d_ff, NULL);
+        orc_add_in_place(x, delta, rows * d);
+    }
+    orc_rms_norm(threads, x, x, rows, d, final_norm, eps);
+    free(xn); free(delta); free(mlp_h); free(qb); free(kb); free(vb); free(ab);
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* Timestral (src/timestral/model.zig) */
 

@@ -101,6 +101,21 @@ void orc_chronos2_time_attention(size_t threads, const float *q, const float *k,
 
 /* Timestral RoPE tables (src/timestral/model.zig:180-188, 447-463): (groups, sl, hd/2).
  * first_obs: per group; rope_dim = rotated dims (partial RoPE). */
+/* nn.rmsNorm (src/core/nn.zig:361-396) and nn.relu (:436-444). out may equal x. */
+void orc_rms_norm(size_t threads, float *out, const float *x, size_t rows, size_t dim, const float *scale,
+                  float eps);
+void orc_relu(float *x, size_t n);
+/* One Chronos-2 encoder layer's weights (src/chronos2/model.zig Layer), nn.Weight (out, in) layout. */
+typedef struct orc_chronos2_layer {
+    const float *time_norm, *time_q, *time_k, *time_v, *time_o;
+    const float *group_norm, *group_v, *group_o;
+    const float *mlp_norm, *mlp_wi, *mlp_wo;
+} orc_chronos2_layer;
+/* Model.encode (src/chronos2/model.zig:144-206): x (b*seq, d) embedded tokens in, final-normed
+ * hidden states out. */
+void orc_chronos2_encode(size_t threads, float *x, const uint8_t *key_valid, size_t b, size_t seq, size_t d,
+                         size_t nh, size_t hd, size_t d_ff, size_t n_layers, const orc_chronos2_layer *layers,
+                         const float *final_norm, float eps, const float *cos_t, const float *sin_t, float scale);
 void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
                                size_t hd, size_t rope_dim, float theta, const size_t *first_obs);
 /* Timestral TimeJob.rope (src/timestral/model.zig:558-577), in place on the fused qkv buffer. */

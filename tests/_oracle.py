@@ -20,6 +20,16 @@ def ptr(a):
     return a.ctypes.data
 
 
+LAYER_FIELDS = ("time_norm", "time_q", "time_k", "time_v", "time_o", "group_norm", "group_v", "group_o", "mlp_norm",
+                "mlp_wi", "mlp_wo")
+
+
+class Chronos2Layer(ctypes.Structure):
+    """orc_chronos2_layer (oracle/tsfm_oracle.h)."""
+
+    _fields_ = [(f, _vp) for f in LAYER_FIELDS]
+
+
 class Oracle:
     def __init__(self, path):
         self.path = str(path)
@@ -30,6 +40,10 @@ class Oracle:
         L.orc_gemm_nt.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
         L.orc_gemm_nn.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz]
         L.orc_linear.argtypes = [_sz, _vp, _vp, _sz, _vp, _sz, _sz, _vp]
+        L.orc_rms_norm.argtypes = [_sz, _vp, _vp, _sz, _sz, _vp, _f]
+        L.orc_relu.argtypes = [_vp, _sz]
+        L.orc_chronos2_encode.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, ctypes.POINTER(Chronos2Layer),
+                                          _vp, _f, _vp, _vp, _f]
         L.orc_softmax.argtypes = [_vp, _sz]
         L.orc_dot.argtypes = [_vp, _vp, _sz]
         L.orc_dot.restype = _f
@@ -70,6 +84,22 @@ class Oracle:
     def linear(self, threads, y, x, rows, w, out, inp, bias=None):
         """nn.linear: y (rows, out) = x (rows, inp) w (out, inp)^T (+ bias)."""
         self.lib.orc_linear(threads, ptr(y), ptr(x), rows, ptr(w), out, inp, ptr(bias))
+
+    def rms_norm(self, threads, out, x, rows, dim, scale, eps):
+        self.lib.orc_rms_norm(threads, ptr(out), ptr(x), rows, dim, ptr(scale), eps)
+
+    def relu(self, x):
+        self.lib.orc_relu(ptr(x), x.size)
+
+    def chronos2_encode(self, threads, x, key_valid, b, seq, d, nh, hd, d_ff, layers, final_norm, eps, cos_t, sin_t,
+                        scale):
+        """x (b*seq, d) in place; layers: list of dicts of the LAYER_FIELDS arrays."""
+        arr = (Chronos2Layer * max(1, len(layers)))()
+        for i, ly in enumerate(layers):
+            for f in LAYER_FIELDS:
+                setattr(arr[i], f, ptr(ly[f]))
+        self.lib.orc_chronos2_encode(threads, ptr(x), ptr(key_valid), b, seq, d, nh, hd, d_ff, len(layers), arr,
+                                     ptr(final_norm), eps, ptr(cos_t), ptr(sin_t), scale)
 
     def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
         self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)

@@ -146,3 +146,66 @@ def variate_attend_f64(qkv, key_valid, roles, cov, groups, vall, ne, h, d, nh, h
                 w /= w.sum(axis=1, keepdims=True)
                 o[rows, tok, c] = w @ v
     return o
+
+
+def rms_norm_f64(x, scale, eps):
+    """nn.rmsNorm from its definition: x / sqrt(mean(x^2) + eps) * scale, per row, in float64."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps) * np.asarray(scale, np.float64)
+
+
+def rope_f64(x, cos_t, sin_t, seq, nh, hd=64):
+    """Rotate-half RoPE of every head of x (rows = b * seq tokens, token t uses row t % seq)."""
+    x = np.asarray(x, np.float64).copy()
+    half = hd // 2
+    rows = x.shape[0]
+    c = np.asarray(cos_t, np.float64).reshape(-1, half)[np.arange(rows) % seq]
+    s = np.asarray(sin_t, np.float64).reshape(-1, half)[np.arange(rows) % seq]
+    for h in range(nh):
+        lo = x[:, h * hd:h * hd + half].copy()
+        hi = x[:, h * hd + half:(h + 1) * hd].copy()
+        x[:, h * hd:h * hd + half] = lo * c - hi * s
+        x[:, h * hd + half:(h + 1) * hd] = hi * c + lo * s
+    return x
+
+
+def chronos2_encode_f64(x, key_valid, b, seq, nh, layers, final_norm, eps, cos_t, sin_t, scale, hd=64):
+    """Chronos-2 Model.encode (src/chronos2/model.zig:144-206) written from its definition in
+    float64: per layer x += o(attn(rope(q), rope(k), v)) over n1(x), x += o_g(v_g(n2(x))),
+    x += wo(relu(wi(n3(x)))), then the final rmsNorm."""
+    x = np.asarray(x, np.float64).copy()
+    d = x.shape[1]
+    kv = np.asarray(key_valid, bool).reshape(b, seq)
+    W = lambda a: np.asarray(a, np.float64)
+    for ly in layers:
+        xn = rms_norm_f64(x, ly["time_norm"], eps)
+        q = rope_f64(xn @ W(ly["time_q"]).T, cos_t, sin_t, seq, nh, hd)
+        k = rope_f64(xn @ W(ly["time_k"]).T, cos_t, sin_t, seq, nh, hd)
+        v = xn @ W(ly["time_v"]).T
+        ab = np.zeros_like(x)
+        for r in range(b):
+            sl = slice(r * seq, (r + 1) * seq)
+            allowed = allowed_matrix(1, seq, seq, kv[r])
+            for h in range(nh):
+                hs = slice(h * hd, (h + 1) * hd)
+                ab[sl, hs] = naive_attend(q[sl, hs], k[sl, hs], v[sl, hs], allowed, scale)
+        x = x + ab @ W(ly["time_o"]).T
+        xn = rms_norm_f64(x, ly["group_norm"], eps)
+        x = x + (xn @ W(ly["group_v"]).T) @ W(ly["group_o"]).T
+        xn = rms_norm_f64(x, ly["mlp_norm"], eps)
+        x = x + np.maximum(xn @ W(ly["mlp_wi"]).T, 0.0) @ W(ly["mlp_wo"]).T
+    return rms_norm_f64(x, final_norm, eps)
+
+
+def chronos2_layers(rng, n_layers, d, d_ff):
+    """Random-init Chronos-2 layer weights (the (out, in) nn.Weight layout), scaled so activations
+    stay O(1): linear weights ~ N(0, 1/in), norm scales ~ 1 + N(0, 0.1)."""
+    def lin(o, i):
+        return (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+
+    return [dict(time_norm=norm(), time_q=lin(d, d), time_k=lin(d, d), time_v=lin(d, d), time_o=lin(d, d),
+                 group_norm=norm(), group_v=lin(d, d), group_o=lin(d, d), mlp_norm=norm(), mlp_wi=lin(d_ff, d),
+                 mlp_wo=lin(d, d_ff)) for _ in range(n_layers)]

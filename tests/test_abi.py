@@ -32,7 +32,8 @@ def test_library_exports_every_declared_symbol(ta):
 
 
 @pytest.mark.parametrize("struct,cname", [("AttnArgs", "tsfm_attn_args"), ("VariateArgs", "tsfm_variate_args"),
-                                          ("ProjArgs", "tsfm_proj_args")])
+                                          ("ProjArgs", "tsfm_proj_args"), ("Chronos2Layer", "tsfm_chronos2_layer"),
+                                          ("Chronos2EncodeArgs", "tsfm_chronos2_encode_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)
@@ -227,3 +228,45 @@ def test_sgemm_nn_declines(ta):
     a = np.zeros(64, np.float32)
     lib = ta.load()
     assert lib.tsfm_sgemm_nn(4, 4, 4, a.ctypes.data, 4, a.ctypes.data, 4, a.ctypes.data, 4, None) == ta.E_UNSUPPORTED
+
+
+def _encode_args(ta, **over):
+    d, seq, b = 128, 4, 2
+    x = np.zeros(b * seq * d, np.float32)
+    kv = np.ones(b * seq, np.uint8)
+    tab = np.zeros(seq * 32, np.float32)
+    w = np.zeros(512 * 128, np.float32)
+    arr = (ta.Chronos2Layer * 1)()
+    for f in ta.CHRONOS2_LAYER_FIELDS:
+        setattr(arr[0], f, w.ctypes.data)
+    kw = dict(batch=b, seq=seq, d_model=d, heads=2, head_dim=64, d_ff=256, n_layers=1, keys_all_valid=1, eps=1e-6,
+              scale=1.0, x=x.ctypes.data, key_valid=kv.ctypes.data, rope_cos=tab.ctypes.data,
+              rope_sin=tab.ctypes.data, layers=arr, final_norm=w.ctypes.data)
+    kw.update(over)
+    return ta.Chronos2EncodeArgs(**kw), (x, kv, tab, w, arr)
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(head_dim=32, d_model=64), 2),
+    (dict(d_model=130), 3),          # not heads * head_dim
+    (dict(d_ff=100), 2),             # not a multiple of 16
+    (dict(x=None), 3),
+    (dict(key_valid=None), 3),
+    (dict(layers=None), 3),
+    (dict(batch=-1), 3),
+])
+def test_encode_validation_codes(ta, over, code):
+    a, _keep = _encode_args(ta, **over)
+    assert ta.load().tsfm_chronos2_encode(ctypes.byref(a)) == code
+    assert ta.last_error()
+
+
+def test_encode_null_layer_weight_is_invalid(ta):
+    a, keep = _encode_args(ta)
+    keep[4][0].mlp_wo = None
+    assert ta.load().tsfm_chronos2_encode(ctypes.byref(a)) == ta.E_INVALID
+
+
+def test_encode_empty_is_a_no_op(ta):
+    a, _keep = _encode_args(ta, batch=0)
+    assert ta.load().tsfm_chronos2_encode(ctypes.byref(a)) == ta.OK

@@ -1,0 +1,98 @@
+"""GPU parity of the Chronos-2 encoder stack (tsfm_chronos2_encode) against the oracle's
+restatement of Model.encode (src/chronos2/model.zig:144-206) and against the same stack in
+float64, through the C ABI.
+
+A stack of layers composes many f32 reductions: the GPU's and the oracle's summation orders
+differ, and both differ from exact arithmetic by about as much. The bar is therefore twofold:
+the GPU result is within 5e-5 scaled error of the oracle's, and no further from float64 than
+twice the oracle's own distance (plus 1e-6). Covered: scale 1/8 and the model's 1.0, padded and
+all-valid keys (FULL and KEYS_ADDITIVE masks give the same result when every key is valid), no
+layers (final norm only), host and device pointers (same bits), a Chronos-2-base shaped run
+(d 768, 12 heads, d_ff 3072, 577 tokens).
+"""
+import numpy as np
+import pytest
+
+import _ref
+
+pytestmark = pytest.mark.gpu
+
+THREADS = 16
+
+
+def _setup(seed, b, seq, nh, d_ff, n_layers, pad=True):
+    rng = np.random.default_rng(seed)
+    d = nh * 64
+    x = rng.standard_normal((b * seq, d)).astype(np.float32)
+    kv = _ref.left_pad_valid(rng, b, seq, seq // 4, tail_valid=2) if pad else np.ones((b, seq), np.uint8)
+    layers = _ref.chronos2_layers(rng, n_layers, d, d_ff)
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    return x, kv, layers, fn, d
+
+
+def _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, scale):
+    want = x.copy()
+    orc.chronos2_encode(THREADS, want, kv.ravel().copy(), b, seq, d, nh, 64, d_ff, layers, fn, eps, cos_t, sin_t,
+                        scale)
+    return want
+
+
+@pytest.mark.parametrize("scale", [0.125, 1.0])
+@pytest.mark.parametrize("pad", [True, False])
+def test_encode_matches_oracle_and_f64(ta, orc, gpu_ready, scale, pad):
+    b, seq, nh, d_ff, n_layers, eps = 3, 45, 2, 256, 3, 1e-6
+    x, kv, layers, fn, d = _setup(int(scale * 8) + 10 * pad, b, seq, nh, d_ff, n_layers, pad)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    got = x.copy()
+    rc = ta.chronos2_encode(got, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=scale)
+    assert rc == ta.OK, ta.last_error()
+    want = _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, scale)
+    exact = _ref.chronos2_encode_f64(x, kv, b, seq, nh, layers, fn, eps, cos_t, sin_t, scale)
+    assert _ref.scaled_err(got, want) <= 5e-5
+    assert _ref.scaled_err(got, exact) <= 2 * _ref.scaled_err(want, exact) + 1e-6
+    if not pad:  # every key valid: the KEYS_ADDITIVE mask (keys_all_valid=False) gives the same bits
+        again = x.copy()
+        rc = ta.chronos2_encode(again, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=scale,
+                                keys_all_valid=False)
+        assert rc == ta.OK, ta.last_error()
+        assert _ref.scaled_err(again, got) <= 1e-6
+
+
+def test_encode_without_layers_is_the_final_norm(ta, orc, gpu_ready):
+    b, seq, nh = 2, 17, 1
+    x, kv, _, fn, d = _setup(3, b, seq, nh, 64, 0)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    got = x.copy()
+    assert ta.chronos2_encode(got, kv, cos_t, sin_t, [], fn, b, seq, d, nh, 64, 1e-6) == ta.OK, ta.last_error()
+    assert _ref.scaled_err(got, _ref.rms_norm_f64(x, fn, 1e-6)) <= 2e-6
+
+
+def test_encode_device_pointers_match_host(ta, orc, gpu_ready):
+    import torch
+
+    b, seq, nh, d_ff, n_layers, eps = 2, 33, 2, 128, 2, 1e-6
+    x, kv, layers, fn, d = _setup(21, b, seq, nh, d_ff, n_layers)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    host = x.copy()
+    assert ta.chronos2_encode(host, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps) == ta.OK, ta.last_error()
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    dl = [{k: cu(v) for k, v in ly.items()} for ly in layers]
+    xd = cu(x)
+    rc = ta.chronos2_encode(xd, cu(kv), cu(cos_t), cu(sin_t), dl, cu(fn), b, seq, d, nh, d_ff, eps,
+                            keys_all_valid=bool(kv.all()))
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(xd.cpu().numpy(), host)
+
+
+def test_encode_chronos2_base_shape(ta, orc, gpu_ready):
+    """d_model 768, 12 heads, d_ff 3072 over 577 tokens (512 context patches, REG, 64 future), two
+    layers of the model's scale 1.0."""
+    b, seq, nh, d_ff, n_layers, eps = 2, 577, 12, 3072, 2, 1e-6
+    x, kv, layers, fn, d = _setup(5, b, seq, nh, d_ff, n_layers)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    got = x.copy()
+    rc = ta.chronos2_encode(got, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=1.0)
+    assert rc == ta.OK, ta.last_error()
+    want = _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, 1.0)
+    assert _ref.scaled_err(got, want) <= 5e-5

@@ -532,3 +532,50 @@ def test_linear_permutation_weight_is_exact(orc):
     orc.linear(2, y, x, rows, w, n, n)
     assert np.array_equal(y, x[:, perm])
     assert not np.array_equal(y, x[:, np.argsort(perm)])
+
+
+def test_rms_norm_matches_definition(orc):
+    rng = np.random.default_rng(31)
+    rows, dim = 70, 100  # whole lane groups and a tail
+    x = (rng.standard_normal((rows, dim)) * 3).astype(np.float32)
+    scale = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    out = np.zeros_like(x)
+    orc.rms_norm(4, out, x, rows, dim, scale, 1e-6)
+    assert _ref.scaled_err(out, _ref.rms_norm_f64(x, scale, 1e-6)) < 2e-6
+    y = x.copy()
+    orc.rms_norm(1, y, y, rows, dim, scale, 1e-6)  # in place, one thread: the same bits
+    assert np.array_equal(y, out)
+    z = np.zeros((2, dim), np.float32)  # a zero row: eps keeps it finite and it stays zero
+    orc.rms_norm(1, z, z, 2, dim, scale, 1e-6)
+    assert np.array_equal(z, np.zeros_like(z))
+
+
+def test_relu_closed_form(orc):
+    x = np.array([-2.0, -0.0, 0.0, 1e-30, 3.5, -1e30], np.float32)
+    y = x.copy()
+    orc.relu(y)
+    assert np.array_equal(y, np.maximum(x, 0))
+
+
+@pytest.mark.parametrize("scale", [0.125, 1.0])
+def test_chronos2_encode_matches_f64(orc, scale):
+    """Model.encode's layer loop against the same stack written from its definition in float64."""
+    rng = np.random.default_rng(33)
+    b, seq, nh, d_ff, n_layers, eps = 2, 21, 2, 256, 2, 1e-6
+    d = nh * 64
+    x = rng.standard_normal((b * seq, d)).astype(np.float32)
+    kv = _ref.left_pad_valid(rng, b, seq, 6, tail_valid=3)
+    kv[0, :] = 1
+    layers = _ref.chronos2_layers(rng, n_layers, d, d_ff)
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    got = x.copy()
+    orc.chronos2_encode(4, got, kv.ravel().copy(), b, seq, d, nh, 64, d_ff, layers, fn, eps, cos_t, sin_t, scale)
+    want = _ref.chronos2_encode_f64(x, kv, b, seq, nh, layers, fn, eps, cos_t, sin_t, scale)
+    assert _ref.scaled_err(got, want) < 2e-5
+    # no layers: the final norm alone
+    y = x.copy()
+    orc.chronos2_encode(1, y, kv.ravel().copy(), b, seq, d, nh, 64, d_ff, [], fn, eps, cos_t, sin_t, scale)
+    z = np.zeros_like(x)
+    orc.rms_norm(1, z, x, b * seq, d, fn, eps)
+    assert np.array_equal(y, z)

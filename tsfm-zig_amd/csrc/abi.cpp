@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <vector>
 
 #include "../../include/tsfm_attn.h"
 #include "launch.hpp"
@@ -542,6 +543,165 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     for (int i = 0; i < (gated ? 4 : 3); i++)
         if ((e = copy_rows_d2h(dst[i], base + y_at[i], 1, tokens, 0, tok[i] * oes, width * oes, s)) != hipSuccess)
             return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
+// ---- Chronos-2 encoder stack ----------------------------------------------------------------------
+
+namespace {
+
+// One nn.linear on the matrix cores: y = x w^T over rows tokens, with an optional ReLU or residual
+// (y = resid + x w^T) epilogue.
+hipError_t linear_on(const float* x, int64_t x_tok, const float* w, int out, int in, float* y, int64_t y_tok,
+                     int rows, int epi, const float* resid, hipStream_t s) {
+    tsfm::ProjParams p{};
+    p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi;
+    p.resid = resid; p.resid_tok = y_tok;
+    p.y0 = y; p.y0_tok = y_tok;
+    p.tokens = rows; p.seq = rows; p.d_in = in; p.width = out; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
+    return tsfm::launch_proj(p, s);
+}
+
+// The layer loop on device buffers. scratch: xn, q, k, v, ab (rows x d each), then h (rows x d_ff).
+hipError_t encode_on(const tsfm_chronos2_encode_args* a, float* x, const uint8_t* kv, const float* cs,
+                     const float* sn, const tsfm_chronos2_layer* layers, const float* final_norm, float* scratch,
+                     hipStream_t s) {
+    const int64_t d = a->d_model, rows = (int64_t)a->batch * a->seq;
+    float* xn = scratch;
+    float* q = xn + rows * d;
+    float* k = q + rows * d;
+    float* v = k + rows * d;
+    float* ab = v + rows * d;
+    float* h = ab + rows * d;
+    const int R = (int)rows, D = (int)d, F = a->d_ff;
+    hipError_t e = hipSuccess;
+    for (int l = 0; l < a->n_layers && e == hipSuccess; l++) {
+        const tsfm_chronos2_layer& ly = layers[l];
+        // time attention
+        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.time_norm, R, D, a->eps, s)) != hipSuccess) break;
+        tsfm::ProjParams p{};
+        p.x = xn; p.x_tok = d; p.w0 = ly.time_q; p.w1 = ly.time_k; p.w2 = ly.time_v; p.w_ld = d;
+        p.alpha = 1.f; p.epi = tsfm::kEpiNone;
+        p.y0 = q; p.y1 = k; p.y2 = v; p.y0_tok = p.y1_tok = p.y2_tok = d;
+        p.rope_cos = cs; p.rope_sin = sn;
+        p.tokens = R; p.seq = a->seq; p.d_in = D; p.width = D; p.n_out = 3; p.out_dtype = TSFM_DTYPE_F32;
+        if ((e = tsfm::launch_proj(p, s)) != hipSuccess) break;
+        tsfm::Params ap{};
+        ap.q = q; ap.k = k; ap.v = v; ap.o = ab;
+        ap.q_tok = ap.k_tok = ap.v_tok = ap.o_tok = d;
+        ap.q_batch = ap.k_batch = ap.v_batch = ap.o_batch = (int64_t)a->seq * d;
+        ap.key_valid = kv; ap.kv_batch = a->seq;
+        ap.B = a->batch; ap.H = a->heads; ap.n_q = a->seq; ap.n_k = a->seq; ap.scale = a->scale;
+        const int mask = a->keys_all_valid ? TSFM_MASK_FULL : TSFM_MASK_KEYS_ADDITIVE;  // Mask.pick(false, all, true)
+        if ((e = tsfm::launch_attn_f32(ap, mask, tsfm::BIAS_NONE, false, s)) != hipSuccess) break;
+        if ((e = linear_on(ab, d, ly.time_o, D, D, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+        // group attention with singleton groups
+        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.group_norm, R, D, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.group_v, D, D, v, d, R, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
+        if ((e = linear_on(v, d, ly.group_o, D, D, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+        // MLP
+        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.mlp_norm, R, D, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.mlp_wi, F, D, h, F, R, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
+        if ((e = linear_on(h, F, ly.mlp_wo, D, F, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+    }
+    if (e == hipSuccess) e = tsfm::launch_rms_norm(x, d, x, d, final_norm, R, D, a->eps, s);
+    return e;
+}
+
+}  // namespace
+
+int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (a->batch < 0 || a->seq < 0 || a->n_layers < 0 || a->heads < 0 || a->d_ff < 0)
+        return fail(TSFM_E_INVALID, "negative size");
+    if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
+    if (a->d_model != a->heads * a->head_dim) return fail(TSFM_E_INVALID, "d_model != heads * head_dim");
+    if ((int64_t)a->batch * a->seq == 0) return TSFM_OK;  // nothing to compute
+    if (a->d_model == 0 || a->d_ff <= 0 || a->d_ff % 16)
+        return fail(TSFM_E_UNSUPPORTED, "d_ff %d (supported: positive multiples of 16)", a->d_ff);
+    if (a->x == nullptr || a->key_valid == nullptr || a->rope_cos == nullptr || a->rope_sin == nullptr ||
+        a->final_norm == nullptr || (a->n_layers > 0 && a->layers == nullptr))
+        return fail(TSFM_E_INVALID, "x, key_valid, rope tables, final_norm and layers are required");
+    for (int l = 0; l < a->n_layers; l++) {
+        const tsfm_chronos2_layer& y = a->layers[l];
+        const float* w[] = {y.time_norm, y.time_q, y.time_k, y.time_v, y.time_o, y.group_norm,
+                            y.group_v, y.group_o, y.mlp_norm, y.mlp_wi, y.mlp_wo};
+        for (const float* p : w)
+            if (p == nullptr) return fail(TSFM_E_INVALID, "layer %d has a NULL weight", l);
+    }
+    const int64_t rows = (int64_t)a->batch * a->seq, d = a->d_model, F = a->d_ff;
+    if (rows > 0x7fffffff / 4) return fail(TSFM_E_UNSUPPORTED, "too many tokens");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    const size_t scratch_n = (size_t)(rows * (5 * d + F)) * 4;
+    hipError_t e;
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
+        bool ok = aligned(a->x, 16) && aligned(a->rope_cos, 16) && aligned(a->rope_sin, 16) && aligned(a->final_norm, 16);
+        for (int l = 0; l < a->n_layers; l++) {
+            const tsfm_chronos2_layer& y = a->layers[l];
+            const float* w[] = {y.time_norm, y.time_q, y.time_k, y.time_v, y.time_o, y.group_norm,
+                                y.group_v, y.group_o, y.mlp_norm, y.mlp_wi, y.mlp_wo};
+            for (const float* p : w) ok = ok && aligned(p, 16);
+        }
+        if (!ok) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
+        hipStream_t s = static_cast<hipStream_t>(a->stream);
+        void* scratch = nullptr;
+        if ((e = hipMallocAsync(&scratch, scratch_n, s)) != hipSuccess) return hip_fail(e, "encoder scratch allocation");
+        e = encode_on(a, a->x, a->key_valid, a->rope_cos, a->rope_sin, a->layers, a->final_norm,
+                      static_cast<float*>(scratch), s);
+        const hipError_t f = hipFreeAsync(scratch, s);
+        if (e != hipSuccess) return hip_fail(e, "encoder launch");
+        if (f != hipSuccess) return hip_fail(f, "encoder scratch release");
+        return TSFM_OK;
+    }
+    // Host pointers: upload x, the mask, the tables and every weight; run; copy x back.
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    const size_t x_n = (size_t)(rows * d) * 4, kv_n = (size_t)rows, t_n = (size_t)a->seq * 32 * 4;
+    const size_t dd = (size_t)(d * d) * 4, df = (size_t)(d * F) * 4, vn = (size_t)d * 4;
+    const size_t sizes[11] = {vn, dd, dd, dd, dd, vn, dd, dd, vn, df, df};
+    Plan plan;
+    const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), c_at = plan.take(t_n), s_at = plan.take(t_n);
+    const size_t fn_at = plan.take(vn), scr_at = plan.take(scratch_n);
+    std::vector<size_t> w_at((size_t)a->n_layers * 11);
+    for (int l = 0; l < a->n_layers; l++)
+        for (int i = 0; i < 11; i++) w_at[(size_t)l * 11 + i] = plan.take(sizes[i]);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    auto up = [&](size_t at, const void* src, size_t n) {
+        return hipMemcpyAsync(base + at, src, n, hipMemcpyHostToDevice, s);
+    };
+    if ((e = up(x_at, a->x, x_n)) != hipSuccess || (e = up(kv_at, a->key_valid, kv_n)) != hipSuccess ||
+        (e = up(c_at, a->rope_cos, t_n)) != hipSuccess || (e = up(s_at, a->rope_sin, t_n)) != hipSuccess ||
+        (e = up(fn_at, a->final_norm, vn)) != hipSuccess)
+        return hip_fail(e, "host-to-device copy");
+    std::vector<tsfm_chronos2_layer> dev_layers((size_t)a->n_layers);
+    for (int l = 0; l < a->n_layers; l++) {
+        const tsfm_chronos2_layer& y = a->layers[l];
+        const float* src[11] = {y.time_norm, y.time_q, y.time_k, y.time_v, y.time_o, y.group_norm,
+                                y.group_v, y.group_o, y.mlp_norm, y.mlp_wi, y.mlp_wo};
+        const float* dst[11];
+        for (int i = 0; i < 11; i++) {
+            const size_t at = w_at[(size_t)l * 11 + i];
+            if ((e = up(at, src[i], sizes[i])) != hipSuccess) return hip_fail(e, "host-to-device copy");
+            dst[i] = reinterpret_cast<const float*>(base + at);
+        }
+        dev_layers[(size_t)l] = tsfm_chronos2_layer{dst[0], dst[1], dst[2], dst[3], dst[4], dst[5],
+                                                    dst[6], dst[7], dst[8], dst[9], dst[10]};
+    }
+    float* x = reinterpret_cast<float*>(base + x_at);
+    e = encode_on(a, x, reinterpret_cast<const uint8_t*>(base + kv_at), reinterpret_cast<const float*>(base + c_at),
+                  reinterpret_cast<const float*>(base + s_at), dev_layers.data(),
+                  reinterpret_cast<const float*>(base + fn_at), reinterpret_cast<float*>(base + scr_at), s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "encoder launch");
+    }
+    if ((e = hipMemcpyAsync(a->x, x, x_n, hipMemcpyDeviceToHost, s)) != hipSuccess)
+        return hip_fail(e, "device-to-host copy");
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
     return TSFM_OK;
 }

@@ -64,4 +64,8 @@ struct ProjParams {
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 
+// nn.rmsNorm over rows of dim floats (encoder.hip): dim a multiple of 4, rows 16-byte aligned.
+hipError_t launch_rms_norm(const float* x, int64_t x_tok, float* out, int64_t out_tok, const float* scale, int rows,
+                           int dim, float eps, hipStream_t stream);
+
 }  // namespace tsfm

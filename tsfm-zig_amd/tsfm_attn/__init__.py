@@ -33,6 +33,8 @@ import pathlib
 from dataclasses import dataclass
 from typing import Any, Optional, Sequence
 
+import numpy as np
+
 LIB_PATH = pathlib.Path(__file__).with_name("libtsfm_attn.so")
 
 OK = 0
@@ -57,6 +59,7 @@ EXPORTS = (
     "tsfm_t5_bucket_table",
     "tsfm_variate_attend",
     "tsfm_qkv_project",
+    "tsfm_chronos2_encode",
     "tsfm_weight_register",
     "tsfm_weight_release",
     "tsfm_sgemm_nt",
@@ -188,6 +191,40 @@ class VariateArgs(ctypes.Structure):
 
 ROLE_TARGET, ROLE_PAST, ROLE_KNOWN = 0, 1, 2  # model.Role (src/timestral/model.zig:89)
 
+CHRONOS2_LAYER_FIELDS = ("time_norm", "time_q", "time_k", "time_v", "time_o", "group_norm", "group_v", "group_o",
+                         "mlp_norm", "mlp_wi", "mlp_wo")
+
+
+class Chronos2Layer(ctypes.Structure):
+    """``tsfm_chronos2_layer`` (include/tsfm_attn.h)."""
+
+    _fields_ = [(f, ctypes.c_void_p) for f in CHRONOS2_LAYER_FIELDS]
+
+
+class Chronos2EncodeArgs(ctypes.Structure):
+    """``tsfm_chronos2_encode_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("seq", ctypes.c_int32),
+        ("d_model", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("d_ff", ctypes.c_int32),
+        ("n_layers", ctypes.c_int32),
+        ("keys_all_valid", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("scale", ctypes.c_float),
+        ("flags", ctypes.c_uint32),
+        ("x", ctypes.c_void_p),
+        ("key_valid", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p),
+        ("rope_sin", ctypes.c_void_p),
+        ("layers", ctypes.POINTER(Chronos2Layer)),
+        ("final_norm", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p),
+    ]
+
 
 class ProjArgs(ctypes.Structure):
     """``tsfm_proj_args`` (include/tsfm_attn.h)."""
@@ -271,6 +308,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_variate_attend.restype = ctypes.c_int
     lib.tsfm_qkv_project.argtypes = [ctypes.POINTER(ProjArgs)]
     lib.tsfm_qkv_project.restype = ctypes.c_int
+    lib.tsfm_chronos2_encode.argtypes = [ctypes.POINTER(Chronos2EncodeArgs)]
+    lib.tsfm_chronos2_encode.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -576,6 +615,30 @@ def bolt_qkv_projection(x, wq, wk, wv, q, k, v, nb: int, seq: int, d: int, nh: i
     v = nn.linear(x, W) with (inner, d) weights, inner = nh * hd; no RoPE."""
     return _proj(x, wq, wk, wv, q, k, v, batch=nb, seq=seq, d_in=d, nh=nh, hd=hd, x_tok=d, y_tok=nh * hd,
                  stream=stream)
+
+
+def chronos2_encode(x, key_valid, cos_t, sin_t, layers: Sequence[dict], final_norm, b: int, seq: int, d: int,
+                    nh: int, d_ff: int, eps: float, keys_all_valid: Optional[bool] = None, scale: float = 1.0,
+                    hd: int = 64, stream=None) -> int:
+    """Chronos-2 ``Model.encode`` layer loop and final norm (src/chronos2/model.zig:144-206) in one
+    call: x (b * seq, d) embedded tokens in, hidden states out (in place); layers: one dict per
+    layer of the CHRONOS2_LAYER_FIELDS arrays. ``keys_all_valid`` defaults to the AND of key_valid
+    (computed here for host arrays; device callers pass it, as the reference's caller does)."""
+    device = _is_device(x)
+    if keys_all_valid is None:
+        if device:
+            raise ValueError("keys_all_valid is required with device tensors")
+        keys_all_valid = bool(np.asarray(key_valid).all())
+    arr = (Chronos2Layer * max(1, len(layers)))()
+    for i, ly in enumerate(layers):
+        for f in CHRONOS2_LAYER_FIELDS:
+            setattr(arr[i], f, _ptr(ly[f]))
+    a = Chronos2EncodeArgs(batch=b, seq=seq, d_model=d, heads=nh, head_dim=hd, d_ff=d_ff, n_layers=len(layers),
+                           keys_all_valid=int(bool(keys_all_valid)), eps=eps, scale=scale,
+                           flags=DEVICE_PTRS if device else 0, x=_ptr(x), key_valid=_ptr(key_valid),
+                           rope_cos=_ptr(cos_t), rope_sin=_ptr(sin_t), layers=arr, final_norm=_ptr(final_norm),
+                           stream=_stream_of(x, stream) if device else None)
+    return int(load().tsfm_chronos2_encode(ctypes.byref(a)))
 
 
 def weight_register(w) -> Optional[int]:
