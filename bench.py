@@ -18,8 +18,11 @@ Other workloads (parity-test shapes, measured the same way):
            past, 2 known) over L=2048 slots, H=16, covariate firewalls, key padding, sigmoid gate
   proj     the Chronos-2 q/k/v projections with RoPE epilogue at the attention's shape, f32:
            64 x 577 tokens, d_model 768, three (768, 768) weights
+  encoder  the Chronos-2 encoder stack at the Chronos-2-base size (12 layers, d_model 768, 12 heads,
+           d_ff 3072) over 64 series x 577 tokens, f32, random-init weights; the roofline is over
+           the whole stack (every launch but the row norms runs on the f32 matrix cores)
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj]
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj|encoder]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
@@ -305,8 +308,39 @@ def run_proj(torch, ta, workloads, peak):
     return Bench(w, step, output, cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"], "TFLOP/s", 16)
 
 
+def run_encoder(torch, ta, workloads, peak):
+    w = workloads.chronos2_encoder()
+    a, m = w.arrays, w.meta
+    d, L, F = m["d_model"], w.n_q, m["d_ff"]
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    dev = {n: cu(a[n]) for n in ("x", "key_valid", "rope_cos", "rope_sin", "final_norm")}
+    layers = [{k: cu(v) for k, v in ly.items()} for ly in m["layers"]]
+    x = torch.empty_like(dev["x"])
+    all_valid = bool(a["key_valid"].all())
+
+    def step():
+        x.copy_(dev["x"])  # the stack runs in place: each step starts from the same embedded tokens
+        _check(ta, ta.chronos2_encode(x, dev["key_valid"], dev["rope_cos"], dev["rope_sin"], layers, dev["final_norm"],
+                                      w.B, L, d, w.H, F, m["eps"], keys_all_valid=all_valid, scale=1.0))
+
+    def cpu_leg(B):
+        orc = _orc()
+        out = np.ascontiguousarray(a["x"][: B * L]).copy()
+        kv = np.ascontiguousarray(a["key_valid"][:B]).ravel().copy()
+        t0 = time.perf_counter()
+        orc.chronos2_encode(cpu_threads(), out, kv, B, L, d, w.H, 64, F, m["layers"], a["final_norm"], m["eps"],
+                            a["rope_cos"], a["rope_sin"], 1.0)
+        return time.perf_counter() - t0, out.reshape(B, L, d), orc.lanes
+
+    config = {"workload": w.name, "B": w.B, "L": L, "d_model": d, "H": w.H, "d_ff": F, "layers": m["n_layers"],
+              "mask": "keys_additive", "rope": True, "scale": 1.0, "weights": "random-init f32"}
+    b = Bench(w, step, lambda: x.cpu().numpy().reshape(w.B, L, d), cpu_leg, config, "f32", "mfma",
+              peak["f32_mfma_tflops"], "TFLOP/s", 1)
+    return b
+
+
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
-             "variate": run_variate, "proj": run_proj}
+             "variate": run_variate, "proj": run_proj, "encoder": run_encoder}
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
 

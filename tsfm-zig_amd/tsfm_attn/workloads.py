@@ -192,3 +192,43 @@ def chronos2_projection(B: int = 64, H: int = 12, n_ctx: int = 512, n_fut: int =
     return Workload("chronos2_qkv_projection", "f32", B, H, L, L, D, 1.0,
                     dict(x=x, wq=ws[0], wk=ws[1], wv=ws[2], rope_cos=cos_t, rope_sin=sin_t),
                     dict(d_model=d, tokens=tokens, flops=flops, bytes=nbytes, seed=seed, num_layers=12))
+
+
+def chronos2_encoder(B: int = 64, H: int = 12, n_ctx: int = 512, n_fut: int = 64, d_ff: int = 3072,
+                     n_layers: int = 12, seed: int = 0, eps: float = 1e-6, theta: float = 10000.0) -> Workload:
+    """The Chronos-2 encoder stack (src/chronos2/model.zig:144-206) at the Chronos-2-base size:
+    d_model 768, 12 heads, d_ff 3072, 12 layers, over the attention workload's 64 series x 577
+    tokens with the same left padding. Random-init weights (linear ~ N(0, 1/in), norm scales
+    ~ 1 + N(0, 0.1)); x ~ N(0, 1) stands for the embedded patches. FLOPs per call: per layer
+    2 * tokens * (6 d^2 + 2 d d_ff) for the seven linear layers plus the time attention's
+    4 * 64 * H * B * L^2, times the layers. Bytes: x in and out once, the weights once, and per layer
+    the activations each launch streams (norm in/out, q/k/v, attention in/out, the MLP hidden)."""
+    L, D = n_ctx + 1 + n_fut, 64
+    d = H * D
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((B * L, d), dtype=np.float32)
+    kv = left_pad_valid(rng, B, L, n_ctx // 4, n_ctx)
+
+    def lin(o, i):
+        return (rng.standard_normal((o, i), dtype=np.float32) / np.float32(np.sqrt(i))).astype(np.float32)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(d, dtype=np.float32)).astype(np.float32)
+
+    layers = [dict(time_norm=norm(), time_q=lin(d, d), time_k=lin(d, d), time_v=lin(d, d), time_o=lin(d, d),
+                   group_norm=norm(), group_v=lin(d, d), group_o=lin(d, d), mlp_norm=norm(), mlp_wi=lin(d_ff, d),
+                   mlp_wo=lin(d, d_ff)) for _ in range(n_layers)]
+    half = D // 2
+    inv = (1.0 / np.power(np.float32(theta), np.arange(0, D, 2, dtype=np.float32) / np.float32(D))).astype(np.float32)
+    ang = (np.arange(L, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    tokens = B * L
+    flops = n_layers * (2.0 * tokens * (6 * d * d + 2 * d * d_ff) + 4.0 * D * H * B * L * L)
+    w_bytes = 4.0 * n_layers * (6 * d * d + 2 * d * d_ff + 3 * d)
+    act = 4.0 * tokens * (2 * d + 3 * d + 4 * d + 2 * d + 2 * d + 2 * d + 2 * d_ff + 2 * d_ff + 2 * d)
+    nbytes = 4.0 * tokens * d * 2 + w_bytes + n_layers * act
+    return Workload("chronos2_encoder", "f32", B, H, L, L, D, 1.0,
+                    dict(x=x, key_valid=kv, rope_cos=np.cos(ang).astype(np.float32).reshape(L * half),
+                         rope_sin=np.sin(ang).astype(np.float32).reshape(L * half),
+                         final_norm=norm()),
+                    dict(layers=layers, d_model=d, d_ff=d_ff, n_layers=n_layers, eps=eps, tokens=tokens, flops=flops,
+                         bytes=nbytes, seed=seed, num_layers=n_layers))
