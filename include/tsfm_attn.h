@@ -269,6 +269,38 @@ typedef struct tsfm_chronos2_encode_args {
 int tsfm_chronos2_encode(const tsfm_chronos2_encode_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * Chronos-2 model forward: the model part of the forecaster's runChunk
+ * (src/chronos2/forecaster.zig:155-183) in one call:
+ *   the input embedding (ResBlock, src/core/resblock.zig:63-79) of the context and future patch
+ *   features -> the sequence [context; REG; future] with its key_valid (:162-173) -> the encoder
+ *   stack (tsfm_chronos2_encode) -> the future tokens' hidden states (:177-181) -> the output head
+ *   (ResBlock) -> raw (batch * n_out, num_quantiles * patch), before the forecaster's inverse
+ *   scaling. The instance norm, patch features and inverse scaling (:88-153, :184-201) are per-series
+ *   scalar loops and stay with the caller. */
+typedef struct tsfm_resblock {
+    const float *hidden_w, *hidden_b;      /* (hid, in), (hid) */
+    const float *output_w, *output_b;      /* (out, hid), (out) */
+    const float *residual_w, *residual_b;  /* (out, in), (out) */
+    int32_t in, hid, out;                  /* in, hid multiples of 16; out of 4 */
+    int32_t act;                           /* 0 = ReLU (ResBlock(.relu), Chronos-2); others unsupported */
+} tsfm_resblock;
+
+typedef struct tsfm_chronos2_forward_args {
+    tsfm_chronos2_encode_args enc;  /* model dims, layers, final_norm, tables, eps, scale, flags, stream,
+                                     * keys_all_valid (of the context patches); enc.seq = n_ctx + 1 + n_out;
+                                     * enc.x and enc.key_valid are not read */
+    int32_t n_ctx, n_out;           /* context and future patches per series */
+    const float *feats;             /* (batch * n_ctx, 3 * patch) [time_enc, values, mask] features */
+    const float *fut_feats;         /* (batch * n_out, 3 * patch) */
+    const uint8_t *ctx_valid;       /* (batch, n_ctx): the patch has an observation */
+    const float *reg;               /* (d_model) the [REG] token */
+    tsfm_resblock input_embed, output_embed;
+    float *raw;                     /* (batch * n_out, output_embed.out) */
+} tsfm_chronos2_forward_args;
+
+int tsfm_chronos2_forward(const tsfm_chronos2_forward_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * The reference backend's GEMM seam, with the signatures of src/platform/cuda/gemm.c so that the
  * reference's own binding (src/platform/cuda/gpu.zig:16-44) can link this library unchanged:
  * nn.linear's weight products (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then

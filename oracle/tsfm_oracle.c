@@ -659,6 +659,56 @@ void orc_chronos2_encode(size_t threads, float *x, const uint8_t *key_valid, siz
     free(xn); free(delta); free(mlp_h); free(qb); free(kb); free(vb); free(ab);
 }
 
+/* ResBlock(.relu).forward (src/core/resblock.zig:63-79): y = output(relu(hidden(x))) + residual(x),
+ * each nn.linear with its bias, the residual added last (addInPlace). */
+void orc_resblock_relu(size_t threads, float *y, const float *x, size_t rows, const orc_resblock *rb) {
+    const size_t in = rb->in, hid = rb->hid, out = rb->out;
+    float *h = (float *)malloc(rows * hid * sizeof(float));
+    float *r = (float *)malloc(rows * out * sizeof(float));
+    orc_linear(threads, h, x, rows, rb->hidden_w, hid, in, rb->hidden_b);
+    orc_relu(h, rows * hid);
+    orc_linear(threads, y, h, rows, rb->output_w, out, hid, rb->output_b);
+    orc_linear(threads, r, x, rows, rb->residual_w, out, in, rb->residual_b);
+    orc_add_in_place(y, r, rows * out);
+    free(h);
+    free(r);
+}
+
+/* The model part of the Chronos-2 forecaster's runChunk (src/chronos2/forecaster.zig:155-183):
+ * embed the context and future patch features, lay out [context; REG; future] with its key
+ * validity, encode, take the future tokens' hidden states and run the output head. raw:
+ * (b * n_out, output_embed->out). */
+void orc_chronos2_model_forward(size_t threads, float *raw, const float *feats, const float *fut_feats,
+                                const uint8_t *ctx_valid, const float *reg, size_t b, size_t n_ctx, size_t n_out,
+                                size_t d, size_t nh, size_t hd, size_t d_ff, size_t n_layers,
+                                const orc_chronos2_layer *layers, const float *final_norm, float eps,
+                                const float *cos_t, const float *sin_t, float scale, const orc_resblock *input_embed,
+                                const orc_resblock *output_embed) {
+    const size_t seq = n_ctx + 1 + n_out;
+    float *emb = (float *)malloc(b * n_ctx * d * sizeof(float) + 1);
+    float *fut_emb = (float *)malloc(b * n_out * d * sizeof(float) + 1);
+    orc_resblock_relu(threads, emb, feats, b * n_ctx, input_embed);
+    orc_resblock_relu(threads, fut_emb, fut_feats, b * n_out, input_embed);
+    float *x = (float *)malloc(b * seq * d * sizeof(float));
+    uint8_t *kv = (uint8_t *)malloc(b * seq);
+    for (size_t li = 0; li < b; li++) {
+        const size_t xb = li * seq * d;
+        memcpy(x + xb, emb + li * n_ctx * d, n_ctx * d * sizeof(float));
+        memcpy(x + xb + n_ctx * d, reg, d * sizeof(float));
+        memcpy(x + xb + (n_ctx + 1) * d, fut_emb + li * n_out * d, n_out * d * sizeof(float));
+        for (size_t t = 0; t < n_ctx; t++) kv[li * seq + t] = ctx_valid[li * n_ctx + t] != 0;
+        kv[li * seq + n_ctx] = 1;
+        for (size_t t = 0; t < n_out; t++) kv[li * seq + n_ctx + 1 + t] = 1;
+    }
+    orc_chronos2_encode(threads, x, kv, b, seq, d, nh, hd, d_ff, n_layers, layers, final_norm, eps, cos_t, sin_t,
+                        scale);
+    float *hidden = (float *)malloc(b * n_out * d * sizeof(float) + 1);
+    for (size_t li = 0; li < b; li++)
+        memcpy(hidden + li * n_out * d, x + (li * seq + n_ctx + 1) * d, n_out * d * sizeof(float));
+    orc_resblock_relu(threads, raw, hidden, b * n_out, output_embed);
+    free(emb); free(fut_emb); free(x); free(kv); free(hidden);
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* Timestral (src/timestral/model.zig) */
 

@@ -116,6 +116,20 @@ typedef struct orc_chronos2_layer {
 void orc_chronos2_encode(size_t threads, float *x, const uint8_t *key_valid, size_t b, size_t seq, size_t d,
                          size_t nh, size_t hd, size_t d_ff, size_t n_layers, const orc_chronos2_layer *layers,
                          const float *final_norm, float eps, const float *cos_t, const float *sin_t, float scale);
+/* ResBlock weights with biases (src/core/resblock.zig:36-61). */
+typedef struct orc_resblock {
+    const float *hidden_w, *hidden_b, *output_w, *output_b, *residual_w, *residual_b;
+    size_t in, hid, out;
+} orc_resblock;
+/* ResBlock(.relu).forward (src/core/resblock.zig:63-79). */
+void orc_resblock_relu(size_t threads, float *y, const float *x, size_t rows, const orc_resblock *rb);
+/* The model part of the Chronos-2 forecaster's runChunk (src/chronos2/forecaster.zig:155-183). */
+void orc_chronos2_model_forward(size_t threads, float *raw, const float *feats, const float *fut_feats,
+                                const uint8_t *ctx_valid, const float *reg, size_t b, size_t n_ctx, size_t n_out,
+                                size_t d, size_t nh, size_t hd, size_t d_ff, size_t n_layers,
+                                const orc_chronos2_layer *layers, const float *final_norm, float eps,
+                                const float *cos_t, const float *sin_t, float scale, const orc_resblock *input_embed,
+                                const orc_resblock *output_embed);
 void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
                                size_t hd, size_t rope_dim, float theta, const size_t *first_obs);
 /* Timestral TimeJob.rope (src/timestral/model.zig:558-577), in place on the fused qkv buffer. */

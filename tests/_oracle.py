@@ -30,6 +30,25 @@ class Chronos2Layer(ctypes.Structure):
     _fields_ = [(f, _vp) for f in LAYER_FIELDS]
 
 
+RESBLOCK_FIELDS = ("hidden_w", "hidden_b", "output_w", "output_b", "residual_w", "residual_b")
+
+
+class OrcResblock(ctypes.Structure):
+    """orc_resblock (oracle/tsfm_oracle.h)."""
+
+    _fields_ = [(f, _vp) for f in RESBLOCK_FIELDS] + [("in_", _sz), ("hid", _sz), ("out", _sz)]
+
+
+def resblock_struct(rb):
+    """rb: dict of the RESBLOCK_FIELDS arrays (weights (out, in) layout)."""
+    st = OrcResblock()
+    for f in RESBLOCK_FIELDS:
+        setattr(st, f, ptr(rb[f]))
+    st.hid, st.in_ = rb["hidden_w"].shape
+    st.out = rb["output_w"].shape[0]
+    return st
+
+
 class Oracle:
     def __init__(self, path):
         self.path = str(path)
@@ -42,6 +61,10 @@ class Oracle:
         L.orc_linear.argtypes = [_sz, _vp, _vp, _sz, _vp, _sz, _sz, _vp]
         L.orc_rms_norm.argtypes = [_sz, _vp, _vp, _sz, _sz, _vp, _f]
         L.orc_relu.argtypes = [_vp, _sz]
+        L.orc_resblock_relu.argtypes = [_sz, _vp, _vp, _sz, ctypes.POINTER(OrcResblock)]
+        L.orc_chronos2_model_forward.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz,
+                                                 ctypes.POINTER(Chronos2Layer), _vp, _f, _vp, _vp, _f,
+                                                 ctypes.POINTER(OrcResblock), ctypes.POINTER(OrcResblock)]
         L.orc_chronos2_encode.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, ctypes.POINTER(Chronos2Layer),
                                           _vp, _f, _vp, _vp, _f]
         L.orc_softmax.argtypes = [_vp, _sz]
@@ -100,6 +123,21 @@ class Oracle:
                 setattr(arr[i], f, ptr(ly[f]))
         self.lib.orc_chronos2_encode(threads, ptr(x), ptr(key_valid), b, seq, d, nh, hd, d_ff, len(layers), arr,
                                      ptr(final_norm), eps, ptr(cos_t), ptr(sin_t), scale)
+
+    def resblock_relu(self, threads, y, x, rows, rb):
+        st = resblock_struct(rb)
+        self.lib.orc_resblock_relu(threads, ptr(y), ptr(x), rows, ctypes.byref(st))
+
+    def chronos2_model_forward(self, threads, raw, feats, fut_feats, ctx_valid, reg, b, n_ctx, n_out, d, nh, hd, d_ff,
+                               layers, final_norm, eps, cos_t, sin_t, scale, input_embed, output_embed):
+        arr = (Chronos2Layer * max(1, len(layers)))()
+        for i, ly in enumerate(layers):
+            for f in LAYER_FIELDS:
+                setattr(arr[i], f, ptr(ly[f]))
+        ie, oe = resblock_struct(input_embed), resblock_struct(output_embed)
+        self.lib.orc_chronos2_model_forward(threads, ptr(raw), ptr(feats), ptr(fut_feats), ptr(ctx_valid), ptr(reg), b,
+                                            n_ctx, n_out, d, nh, hd, d_ff, len(layers), arr, ptr(final_norm), eps,
+                                            ptr(cos_t), ptr(sin_t), scale, ctypes.byref(ie), ctypes.byref(oe))
 
     def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
         self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)

@@ -209,3 +209,37 @@ def chronos2_layers(rng, n_layers, d, d_ff):
     return [dict(time_norm=norm(), time_q=lin(d, d), time_k=lin(d, d), time_v=lin(d, d), time_o=lin(d, d),
                  group_norm=norm(), group_v=lin(d, d), group_o=lin(d, d), mlp_norm=norm(), mlp_wi=lin(d_ff, d),
                  mlp_wo=lin(d, d_ff)) for _ in range(n_layers)]
+
+
+def resblock(rng, d_in, hid, d_out):
+    """Random-init ResBlock weights with biases ((out, in) layout)."""
+    def lin(o, i):
+        return (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+
+    def bias(o):
+        return (0.1 * rng.standard_normal(o)).astype(np.float32)
+
+    return dict(hidden_w=lin(hid, d_in), hidden_b=bias(hid), output_w=lin(d_out, hid), output_b=bias(d_out),
+                residual_w=lin(d_out, d_in), residual_b=bias(d_out))
+
+
+def resblock_f64(rb, x):
+    """ResBlock(.relu) from its definition: output(relu(hidden(x))) + residual(x), with biases."""
+    W = lambda k: np.asarray(rb[k], np.float64)
+    x = np.asarray(x, np.float64)
+    h = np.maximum(x @ W("hidden_w").T + W("hidden_b"), 0.0)
+    return h @ W("output_w").T + W("output_b") + x @ W("residual_w").T + W("residual_b")
+
+
+def chronos2_model_forward_f64(feats, fut_feats, ctx_valid, reg, b, n_ctx, n_out, nh, layers, final_norm, eps, cos_t,
+                               sin_t, scale, input_embed, output_embed):
+    """The model part of the Chronos-2 forecaster (src/chronos2/forecaster.zig:155-183) in float64:
+    embed, [context; REG; future] with key validity, encode, the future rows, the output head."""
+    emb = resblock_f64(input_embed, feats).reshape(b, n_ctx, -1)
+    fut = resblock_f64(input_embed, fut_feats).reshape(b, n_out, -1)
+    d = emb.shape[2]
+    seq = n_ctx + 1 + n_out
+    x = np.concatenate([emb, np.broadcast_to(np.asarray(reg, np.float64), (b, 1, d)), fut], axis=1).reshape(b * seq, d)
+    kv = np.concatenate([np.asarray(ctx_valid, bool).reshape(b, n_ctx), np.ones((b, 1 + n_out), bool)], axis=1)
+    x = chronos2_encode_f64(x, kv, b, seq, nh, layers, final_norm, eps, cos_t, sin_t, scale).reshape(b, seq, d)
+    return resblock_f64(output_embed, x[:, n_ctx + 1:].reshape(b * n_out, d))

@@ -33,7 +33,9 @@ def test_library_exports_every_declared_symbol(ta):
 
 @pytest.mark.parametrize("struct,cname", [("AttnArgs", "tsfm_attn_args"), ("VariateArgs", "tsfm_variate_args"),
                                           ("ProjArgs", "tsfm_proj_args"), ("Chronos2Layer", "tsfm_chronos2_layer"),
-                                          ("Chronos2EncodeArgs", "tsfm_chronos2_encode_args")])
+                                          ("Chronos2EncodeArgs", "tsfm_chronos2_encode_args"),
+                                          ("Resblock", "tsfm_resblock"),
+                                          ("Chronos2ForwardArgs", "tsfm_chronos2_forward_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)

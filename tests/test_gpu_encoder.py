@@ -1,6 +1,8 @@
-"""GPU parity of the Chronos-2 encoder stack (tsfm_chronos2_encode) against the oracle's
-restatement of Model.encode (src/chronos2/model.zig:144-206) and against the same stack in
-float64, through the C ABI.
+"""GPU parity of the Chronos-2 encoder stack (tsfm_chronos2_encode) and of the model part of the
+forecaster (tsfm_chronos2_forward: input embedding, [context; REG; future], encoder, output head)
+against the oracle's restatements of Model.encode (src/chronos2/model.zig:144-206) and of runChunk
+(src/chronos2/forecaster.zig:155-183), and against the same computations in float64, through the
+C ABI.
 
 A stack of layers composes many f32 reductions: the GPU's and the oracle's summation orders
 differ, and both differ from exact arithmetic by about as much. The bar is therefore twofold:
@@ -114,3 +116,59 @@ def test_encode_twelve_layers_drift_like_the_oracle(ta, orc, gpu_ready):
     e_orc = _ref.scaled_err(want, exact)
     assert e_orc < 5e-4  # the f32 reference path itself, for scale
     assert _ref.scaled_err(got, exact) <= 4 * e_orc + 1e-6
+
+
+# ---- the model part of the Chronos-2 forecaster: embedding, encoder, output head ------------------
+
+
+def _forward_setup(seed, b, n_ctx, n_out, nh, d_ff, n_layers, ps=16, q=3):
+    rng = np.random.default_rng(seed)
+    d = nh * 64
+    feats = rng.standard_normal((b * n_ctx, 3 * ps)).astype(np.float32)
+    fut = rng.standard_normal((b * n_out, 3 * ps)).astype(np.float32)
+    cv = (rng.random((b, n_ctx)) < 0.8).astype(np.uint8)
+    reg = rng.standard_normal(d).astype(np.float32)
+    layers = _ref.chronos2_layers(rng, n_layers, d, d_ff)
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    ie, oe = _ref.resblock(rng, 3 * ps, d_ff, d), _ref.resblock(rng, d, d_ff, q * ps)
+    return feats, fut, cv, reg, layers, fn, ie, oe, d
+
+
+@pytest.mark.parametrize("b,n_ctx,n_out", [(3, 20, 4), (2, 64, 8)])
+def test_forward_matches_oracle_and_f64(ta, orc, gpu_ready, b, n_ctx, n_out):
+    nh, d_ff, n_layers, eps, q, ps = 2, 256, 2, 1e-6, 3, 16
+    feats, fut, cv, reg, layers, fn, ie, oe, d = _forward_setup(b + n_ctx, b, n_ctx, n_out, nh, d_ff, n_layers)
+    seq = n_ctx + 1 + n_out
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    raw = np.full((b * n_out, q * ps), -9.0, np.float32)
+    rc = ta.chronos2_forward(raw, feats, fut, cv, reg, cos_t, sin_t, layers, fn, ie, oe, b, n_ctx, n_out, d, nh, d_ff,
+                             eps)
+    assert rc == ta.OK, ta.last_error()
+    want = np.zeros_like(raw)
+    orc.chronos2_model_forward(THREADS, want, feats, fut, cv, reg, b, n_ctx, n_out, d, nh, 64, d_ff, layers, fn, eps,
+                               cos_t, sin_t, 1.0, ie, oe)
+    exact = _ref.chronos2_model_forward_f64(feats, fut, cv, reg, b, n_ctx, n_out, nh, layers, fn, eps, cos_t, sin_t,
+                                            1.0, ie, oe)
+    assert _ref.scaled_err(raw, want) <= 5e-5
+    assert _ref.scaled_err(raw, exact) <= 2 * _ref.scaled_err(want, exact) + 1e-6
+
+
+def test_forward_device_pointers_match_host(ta, orc, gpu_ready):
+    import torch
+
+    b, n_ctx, n_out, nh, d_ff, eps, q, ps = 2, 30, 5, 2, 128, 1e-6, 3, 16
+    feats, fut, cv, reg, layers, fn, ie, oe, d = _forward_setup(77, b, n_ctx, n_out, nh, d_ff, 2)
+    cos_t, sin_t = orc.chronos2_rope_tables(n_ctx + 1 + n_out, 64, 10000.0)
+    host = np.zeros((b * n_out, q * ps), np.float32)
+    rc = ta.chronos2_forward(host, feats, fut, cv, reg, cos_t, sin_t, layers, fn, ie, oe, b, n_ctx, n_out, d, nh,
+                             d_ff, eps)
+    assert rc == ta.OK, ta.last_error()
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    raw = torch.zeros((b * n_out, q * ps), device="cuda")
+    rc = ta.chronos2_forward(raw, cu(feats), cu(fut), cu(cv), cu(reg), cu(cos_t), cu(sin_t),
+                             [{k: cu(v) for k, v in ly.items()} for ly in layers], cu(fn),
+                             {k: cu(v) for k, v in ie.items()}, {k: cu(v) for k, v in oe.items()}, b, n_ctx, n_out, d,
+                             nh, d_ff, eps, keys_all_valid=bool(cv.all()))
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(raw.cpu().numpy(), host)

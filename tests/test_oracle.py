@@ -579,3 +579,34 @@ def test_chronos2_encode_matches_f64(orc, scale):
     z = np.zeros_like(x)
     orc.rms_norm(1, z, x, b * seq, d, fn, eps)
     assert np.array_equal(y, z)
+
+
+def test_resblock_matches_definition(orc):
+    rng = np.random.default_rng(41)
+    rows, d_in, hid, d_out = 37, 48, 64, 40
+    rb = _ref.resblock(rng, d_in, hid, d_out)
+    x = rng.standard_normal((rows, d_in)).astype(np.float32)
+    y = np.zeros((rows, d_out), np.float32)
+    orc.resblock_relu(4, y, x, rows, rb)
+    assert _ref.scaled_err(y, _ref.resblock_f64(rb, x)) < 5e-6
+
+
+def test_chronos2_model_forward_matches_f64(orc):
+    """The model part of runChunk: embed, [context; REG; future], encode, future rows, head."""
+    rng = np.random.default_rng(43)
+    b, n_ctx, n_out, nh, d_ff, ps, q = 2, 12, 3, 2, 256, 16, 3
+    d, seq = nh * 64, n_ctx + 1 + n_out
+    feats = rng.standard_normal((b * n_ctx, 3 * ps)).astype(np.float32)
+    fut = rng.standard_normal((b * n_out, 3 * ps)).astype(np.float32)
+    cv = (rng.random((b, n_ctx)) < 0.8).astype(np.uint8)
+    reg = rng.standard_normal(d).astype(np.float32)
+    layers = _ref.chronos2_layers(rng, 2, d, d_ff)
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    ie, oe = _ref.resblock(rng, 3 * ps, d_ff, d), _ref.resblock(rng, d, d_ff, q * ps)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    raw = np.zeros((b * n_out, q * ps), np.float32)
+    orc.chronos2_model_forward(4, raw, feats, fut, cv, reg, b, n_ctx, n_out, d, nh, 64, d_ff, layers, fn, 1e-6, cos_t,
+                               sin_t, 1.0, ie, oe)
+    want = _ref.chronos2_model_forward_f64(feats, fut, cv, reg, b, n_ctx, n_out, nh, layers, fn, 1e-6, cos_t, sin_t,
+                                           1.0, ie, oe)
+    assert _ref.scaled_err(raw, want) < 3e-5

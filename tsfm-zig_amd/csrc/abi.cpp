@@ -554,9 +554,9 @@ namespace {
 // One nn.linear on the matrix cores: y = x w^T over rows tokens, with an optional ReLU or residual
 // (y = resid + x w^T) epilogue.
 hipError_t linear_on(const float* x, int64_t x_tok, const float* w, int out, int in, float* y, int64_t y_tok,
-                     int rows, int epi, const float* resid, hipStream_t s) {
+                     int rows, int epi, const float* resid, hipStream_t s, const float* bias = nullptr) {
     tsfm::ProjParams p{};
-    p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi;
+    p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi; p.bias = bias;
     p.resid = resid; p.resid_tok = y_tok;
     p.y0 = y; p.y0_tok = y_tok;
     p.tokens = rows; p.seq = rows; p.d_in = in; p.width = out; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
@@ -701,6 +701,213 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
         return hip_fail(e, "encoder launch");
     }
     if ((e = hipMemcpyAsync(a->x, x, x_n, hipMemcpyDeviceToHost, s)) != hipSuccess)
+        return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
+// ---- Chronos-2 model forward: embedding, encoder stack, output head --------------------------------
+
+namespace {
+
+// Host buffers staged into the thread's device buffer: regions are planned first (src NULL = device
+// scratch only), then the sources are uploaded in one pass.
+struct Staging {
+    struct Up { const void* src; size_t n, at; };
+    Plan plan;
+    std::vector<Up> ups;
+    size_t add(const void* src, size_t n) {
+        const size_t at = plan.take(n);
+        if (src != nullptr && n > 0) ups.push_back({src, n, at});
+        return at;
+    }
+    hipError_t upload(char* base, hipStream_t s) const {
+        for (const Up& u : ups) {
+            const hipError_t e = hipMemcpyAsync(base + u.at, u.src, u.n, hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+};
+
+// ResBlock.forward (src/core/resblock.zig:63-79) with ReLU: y = output(relu(hidden(x))) + residual(x),
+// every linear with its bias. h: rows x hid, r: rows x out scratch.
+hipError_t resblock_on(const tsfm_resblock& rb, const float* x, int rows, float* y, float* h, float* r, hipStream_t s) {
+    hipError_t e = linear_on(x, rb.in, rb.hidden_w, rb.hid, rb.in, h, rb.hid, rows, tsfm::kEpiRelu, nullptr, s, rb.hidden_b);
+    if (e == hipSuccess)
+        e = linear_on(x, rb.in, rb.residual_w, rb.out, rb.in, r, rb.out, rows, tsfm::kEpiNone, nullptr, s, rb.residual_b);
+    if (e == hipSuccess)
+        e = linear_on(h, rb.hid, rb.output_w, rb.out, rb.hid, y, rb.out, rows, tsfm::kEpiResidual, r, s, rb.output_b);
+    return e;
+}
+
+int validate_encode(const tsfm_chronos2_encode_args* a, bool needs_x) {
+    if (a->batch < 0 || a->seq < 0 || a->n_layers < 0 || a->heads < 0 || a->d_ff < 0)
+        return fail(TSFM_E_INVALID, "negative size");
+    if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
+    if (a->d_model != a->heads * a->head_dim) return fail(TSFM_E_INVALID, "d_model != heads * head_dim");
+    if ((int64_t)a->batch * a->seq == 0) return TSFM_OK;
+    if (a->d_model == 0 || a->d_ff <= 0 || a->d_ff % 16)
+        return fail(TSFM_E_UNSUPPORTED, "d_ff %d (supported: positive multiples of 16)", a->d_ff);
+    if ((needs_x && (a->x == nullptr || a->key_valid == nullptr)) || a->rope_cos == nullptr ||
+        a->rope_sin == nullptr || a->final_norm == nullptr || (a->n_layers > 0 && a->layers == nullptr))
+        return fail(TSFM_E_INVALID, "x, key_valid, rope tables, final_norm and layers are required");
+    for (int l = 0; l < a->n_layers; l++) {
+        const tsfm_chronos2_layer& y = a->layers[l];
+        const float* w[] = {y.time_norm, y.time_q, y.time_k, y.time_v, y.time_o, y.group_norm,
+                            y.group_v, y.group_o, y.mlp_norm, y.mlp_wi, y.mlp_wo};
+        for (const float* p : w)
+            if (p == nullptr) return fail(TSFM_E_INVALID, "layer %d has a NULL weight", l);
+    }
+    if ((int64_t)a->batch * a->seq > 0x7fffffff / 4) return fail(TSFM_E_UNSUPPORTED, "too many tokens");
+    return TSFM_OK;
+}
+
+int validate_resblock(const tsfm_resblock& rb, int in, int out, const char* what) {
+    if (rb.in != in || (out > 0 && rb.out != out)) return fail(TSFM_E_INVALID, "%s: in/out do not match the model", what);
+    if (rb.act != 0) return fail(TSFM_E_UNSUPPORTED, "%s: only the ReLU block (Chronos-2) runs here", what);
+    if (rb.in <= 0 || rb.hid <= 0 || rb.out <= 0 || rb.in % 16 || rb.hid % 16 || rb.out % 4)
+        return fail(TSFM_E_UNSUPPORTED, "%s: in and hid must be multiples of 16, out of 4", what);
+    if (!rb.hidden_w || !rb.hidden_b || !rb.output_w || !rb.output_b || !rb.residual_w || !rb.residual_b)
+        return fail(TSFM_E_INVALID, "%s: a weight or bias is NULL", what);
+    return TSFM_OK;
+}
+
+// The forward on device buffers. x_buf: rows x d; kv: rows bytes; emb: rows x d; h: rows x hid_max;
+// r: rows x out_max; enc: the encoder's scratch.
+hipError_t forward_on(const tsfm_chronos2_forward_args* a, const tsfm_chronos2_encode_args& enc, const float* feats,
+                      const float* fut_feats, const uint8_t* ctx_valid, const float* reg, float* raw, float* x_buf,
+                      uint8_t* kv, float* emb, float* h, float* r, float* enc_scratch, hipStream_t s) {
+    const int nb = enc.batch, d = enc.d_model, rows_ctx = nb * a->n_ctx, rows_fut = nb * a->n_out;
+    float* emb_fut = emb + (int64_t)rows_ctx * d;
+    hipError_t e = resblock_on(a->input_embed, feats, rows_ctx, emb, h, r, s);
+    if (e == hipSuccess) e = resblock_on(a->input_embed, fut_feats, rows_fut, emb_fut, h, r, s);
+    if (e == hipSuccess)
+        e = tsfm::launch_assemble_sequence(emb, emb_fut, reg, ctx_valid, x_buf, kv, nb, a->n_ctx, a->n_out, d, s);
+    if (e == hipSuccess)
+        e = encode_on(&enc, x_buf, kv, enc.rope_cos, enc.rope_sin, enc.layers, enc.final_norm, enc_scratch, s);
+    if (e == hipSuccess) e = tsfm::launch_gather_future(x_buf, emb, nb, a->n_ctx, a->n_out, d, s);
+    if (e == hipSuccess) e = resblock_on(a->output_embed, emb, rows_fut, raw, h, r, s);
+    return e;
+}
+
+}  // namespace
+
+int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (a->n_ctx < 0 || a->n_out < 0) return fail(TSFM_E_INVALID, "negative size");
+    tsfm_chronos2_encode_args enc = a->enc;
+    if (enc.seq != a->n_ctx + 1 + a->n_out) return fail(TSFM_E_INVALID, "enc.seq must be n_ctx + 1 + n_out");
+    int rc = validate_encode(&enc, false);
+    if (rc != TSFM_OK) return rc;
+    if (enc.batch == 0) return TSFM_OK;
+    if ((rc = validate_resblock(a->input_embed, a->input_embed.in, enc.d_model, "input_embed")) != TSFM_OK) return rc;
+    if ((rc = validate_resblock(a->output_embed, enc.d_model, 0, "output_embed")) != TSFM_OK) return rc;
+    if (a->feats == nullptr || a->fut_feats == nullptr || a->ctx_valid == nullptr || a->reg == nullptr || a->raw == nullptr)
+        return fail(TSFM_E_INVALID, "feats, fut_feats, ctx_valid, reg and raw are required");
+    rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    const int64_t nb = enc.batch, d = enc.d_model, rows = nb * enc.seq, F = enc.d_ff;
+    const int64_t rows_ctx = nb * a->n_ctx, rows_fut = nb * a->n_out;
+    const int64_t hid = std::max(a->input_embed.hid, a->output_embed.hid);
+    const int64_t outw = std::max<int64_t>(d, a->output_embed.out);
+    const size_t x_n = (size_t)(rows * d) * 4, kv_n = (size_t)rows, emb_n = (size_t)(rows * d) * 4;
+    const size_t h_n = (size_t)(rows * hid) * 4, r_n = (size_t)(rows * outw) * 4;
+    const size_t enc_n = (size_t)(rows * (5 * d + F)) * 4;
+    const size_t raw_n = (size_t)(rows_fut * a->output_embed.out) * 4;
+    hipError_t e;
+    if (enc.flags & TSFM_ATTN_DEVICE_PTRS) {
+        bool ok = aligned(a->feats, 16) && aligned(a->fut_feats, 16) && aligned(a->reg, 16) && aligned(a->raw, 16) &&
+                  aligned(enc.rope_cos, 16) && aligned(enc.rope_sin, 16) && aligned(enc.final_norm, 16);
+        for (const tsfm_resblock* rb : {&a->input_embed, &a->output_embed})
+            for (const float* p : {rb->hidden_w, rb->hidden_b, rb->output_w, rb->output_b, rb->residual_w, rb->residual_b})
+                ok = ok && aligned(p, 16);
+        for (int l = 0; l < enc.n_layers; l++) {
+            const tsfm_chronos2_layer& y = enc.layers[l];
+            for (const float* p : {y.time_norm, y.time_q, y.time_k, y.time_v, y.time_o, y.group_norm, y.group_v,
+                                   y.group_o, y.mlp_norm, y.mlp_wi, y.mlp_wo})
+                ok = ok && aligned(p, 16);
+        }
+        if (!ok) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
+        hipStream_t s = static_cast<hipStream_t>(enc.stream);
+        Plan plan;
+        const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), emb_at = plan.take(emb_n), h_at = plan.take(h_n),
+                     r_at = plan.take(r_n), enc_at = plan.take(enc_n);
+        char* scratch = nullptr;
+        if ((e = hipMallocAsync(reinterpret_cast<void**>(&scratch), plan.off, s)) != hipSuccess)
+            return hip_fail(e, "forward scratch allocation");
+        e = forward_on(a, enc, a->feats, a->fut_feats, a->ctx_valid, a->reg, a->raw,
+                       reinterpret_cast<float*>(scratch + x_at), reinterpret_cast<uint8_t*>(scratch + kv_at),
+                       reinterpret_cast<float*>(scratch + emb_at), reinterpret_cast<float*>(scratch + h_at),
+                       reinterpret_cast<float*>(scratch + r_at), reinterpret_cast<float*>(scratch + enc_at), s);
+        const hipError_t f = hipFreeAsync(scratch, s);
+        if (e != hipSuccess) return hip_fail(e, "forward launch");
+        if (f != hipSuccess) return hip_fail(f, "forward scratch release");
+        return TSFM_OK;
+    }
+    // Host pointers: stage every input and weight, run, copy the head's output back.
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    Staging st;
+    const int64_t pin = a->input_embed.in;
+    const size_t feats_at = st.add(a->feats, (size_t)(rows_ctx * pin) * 4);
+    const size_t fut_at = st.add(a->fut_feats, (size_t)(rows_fut * pin) * 4);
+    const size_t cv_at = st.add(a->ctx_valid, (size_t)rows_ctx);
+    const size_t reg_at = st.add(a->reg, (size_t)d * 4);
+    const size_t c_at = st.add(enc.rope_cos, (size_t)enc.seq * 32 * 4), s_at = st.add(enc.rope_sin, (size_t)enc.seq * 32 * 4);
+    const size_t fn_at = st.add(enc.final_norm, (size_t)d * 4);
+    auto stage_block = [&](const tsfm_resblock& rb, size_t at[6]) {
+        at[0] = st.add(rb.hidden_w, (size_t)rb.hid * rb.in * 4);   at[1] = st.add(rb.hidden_b, (size_t)rb.hid * 4);
+        at[2] = st.add(rb.output_w, (size_t)rb.out * rb.hid * 4);  at[3] = st.add(rb.output_b, (size_t)rb.out * 4);
+        at[4] = st.add(rb.residual_w, (size_t)rb.out * rb.in * 4); at[5] = st.add(rb.residual_b, (size_t)rb.out * 4);
+    };
+    size_t in_at[6], out_at[6];
+    stage_block(a->input_embed, in_at);
+    stage_block(a->output_embed, out_at);
+    const size_t dd = (size_t)(d * d) * 4, df = (size_t)(d * F) * 4, vn = (size_t)d * 4;
+    const size_t sizes[11] = {vn, dd, dd, dd, dd, vn, dd, dd, vn, df, df};
+    std::vector<size_t> w_at((size_t)enc.n_layers * 11);
+    for (int l = 0; l < enc.n_layers; l++) {
+        const tsfm_chronos2_layer& y = enc.layers[l];
+        const float* src[11] = {y.time_norm, y.time_q, y.time_k, y.time_v, y.time_o, y.group_norm,
+                                y.group_v, y.group_o, y.mlp_norm, y.mlp_wi, y.mlp_wo};
+        for (int i = 0; i < 11; i++) w_at[(size_t)l * 11 + i] = st.add(src[i], sizes[i]);
+    }
+    const size_t x_at = st.add(nullptr, x_n), kv_at = st.add(nullptr, kv_n), emb_at = st.add(nullptr, emb_n);
+    const size_t h_at = st.add(nullptr, h_n), r_at = st.add(nullptr, r_n), enc_at = st.add(nullptr, enc_n);
+    const size_t raw_at = st.add(nullptr, raw_n);
+    rc = ensure_buf(ctx, st.plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    if ((e = st.upload(base, s)) != hipSuccess) return hip_fail(e, "host-to-device copy");
+    auto dp = [&](size_t at) { return reinterpret_cast<const float*>(base + at); };
+    std::vector<tsfm_chronos2_layer> dev_layers((size_t)enc.n_layers);
+    for (int l = 0; l < enc.n_layers; l++) {
+        const size_t* w = &w_at[(size_t)l * 11];
+        dev_layers[(size_t)l] = tsfm_chronos2_layer{dp(w[0]), dp(w[1]), dp(w[2]), dp(w[3]), dp(w[4]), dp(w[5]),
+                                                    dp(w[6]), dp(w[7]), dp(w[8]), dp(w[9]), dp(w[10])};
+    }
+    tsfm_chronos2_forward_args da = *a;
+    auto dev_block = [&](const tsfm_resblock& rb, const size_t at[6]) {
+        tsfm_resblock o = rb;
+        o.hidden_w = dp(at[0]); o.hidden_b = dp(at[1]); o.output_w = dp(at[2]); o.output_b = dp(at[3]);
+        o.residual_w = dp(at[4]); o.residual_b = dp(at[5]);
+        return o;
+    };
+    da.input_embed = dev_block(a->input_embed, in_at);
+    da.output_embed = dev_block(a->output_embed, out_at);
+    enc.rope_cos = dp(c_at); enc.rope_sin = dp(s_at); enc.final_norm = dp(fn_at); enc.layers = dev_layers.data();
+    e = forward_on(&da, enc, dp(feats_at), dp(fut_at), reinterpret_cast<const uint8_t*>(base + cv_at), dp(reg_at),
+                   reinterpret_cast<float*>(base + raw_at), reinterpret_cast<float*>(base + x_at),
+                   reinterpret_cast<uint8_t*>(base + kv_at), reinterpret_cast<float*>(base + emb_at),
+                   reinterpret_cast<float*>(base + h_at), reinterpret_cast<float*>(base + r_at),
+                   reinterpret_cast<float*>(base + enc_at), s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "forward launch");
+    }
+    if ((e = hipMemcpyAsync(a->raw, base + raw_at, raw_n, hipMemcpyDeviceToHost, s)) != hipSuccess)
         return hip_fail(e, "device-to-host copy");
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
     return TSFM_OK;

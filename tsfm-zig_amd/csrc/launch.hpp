@@ -54,6 +54,7 @@ struct ProjParams {
     float alpha;                     // result scale (1: none)
     int32_t epi;                     // kEpi*: f32 outputs only
     const float* resid; int64_t resid_tok;  // kEpiResidual: y = resid + x w^T (resid may be y)
+    const float* bias;               // per output column, added before the epilogue (one output only)
     void *y0, *y1, *y2, *y3;             // f32, bf16 or f16 elements (out_dtype)
     int64_t y0_tok, y1_tok, y2_tok, y3_tok;
     const float* rope_cos; const float* rope_sin;
@@ -67,5 +68,12 @@ hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 // nn.rmsNorm over rows of dim floats (encoder.hip): dim a multiple of 4, rows 16-byte aligned.
 hipError_t launch_rms_norm(const float* x, int64_t x_tok, float* out, int64_t out_tok, const float* scale, int rows,
                            int dim, float eps, hipStream_t stream);
+// Chronos-2 sequence [context; REG; future] and its key_valid from the two embeddings, and the
+// future tokens' rows back out of it (encoder.hip).
+hipError_t launch_assemble_sequence(const float* ctx_emb, const float* fut_emb, const float* reg,
+                                    const uint8_t* ctx_valid, float* x, uint8_t* key_valid, int nb, int n_ctx,
+                                    int n_out, int d, hipStream_t stream);
+hipError_t launch_gather_future(const float* x, float* hidden, int nb, int n_ctx, int n_out, int d,
+                                hipStream_t stream);
 
 }  // namespace tsfm

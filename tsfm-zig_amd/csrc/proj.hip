@@ -167,6 +167,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             for (int nb = 0; nb < 4; nb++) {
                 if (col + cq + 16 * nb >= p.width) continue;
                 f32x4 v = acc[nb][mb];
+                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq + 16 * nb);  // nn.linear's bias (linearCols, nn.zig:254)
                 if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
                 else if (p.epi == kEpiResidual) v = ld4(res + 16 * nb) + v;  // x + delta, one rounding
                 st4(out + 16 * nb, v);
@@ -189,7 +190,9 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
     if (p.d_in % BK || p.d_in <= 0 || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 || p.out_dtype > 2 ||
         p.w_ld < p.d_in || p.width % 4 || (p.n_out > 1 && p.width % kHeadDim) ||
-        (p.rope_cos != nullptr && p.width % kHeadDim) || (p.out_dtype != 0 && (p.epi != kEpiNone || p.alpha != 1.f)))
+        (p.rope_cos != nullptr && p.width % kHeadDim) ||
+        (p.out_dtype != 0 && (p.epi != kEpiNone || p.alpha != 1.f || p.bias != nullptr)) ||
+        (p.bias != nullptr && p.n_out != 1))
         return hipErrorInvalidValue;
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;

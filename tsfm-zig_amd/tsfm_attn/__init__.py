@@ -60,6 +60,7 @@ EXPORTS = (
     "tsfm_variate_attend",
     "tsfm_qkv_project",
     "tsfm_chronos2_encode",
+    "tsfm_chronos2_forward",
     "tsfm_weight_register",
     "tsfm_weight_release",
     "tsfm_sgemm_nt",
@@ -201,6 +202,16 @@ class Chronos2Layer(ctypes.Structure):
     _fields_ = [(f, ctypes.c_void_p) for f in CHRONOS2_LAYER_FIELDS]
 
 
+RESBLOCK_FIELDS = ("hidden_w", "hidden_b", "output_w", "output_b", "residual_w", "residual_b")
+
+
+class Resblock(ctypes.Structure):
+    """``tsfm_resblock`` (include/tsfm_attn.h)."""
+
+    _fields_ = [(f, ctypes.c_void_p) for f in RESBLOCK_FIELDS] + [
+        ("in", ctypes.c_int32), ("hid", ctypes.c_int32), ("out", ctypes.c_int32), ("act", ctypes.c_int32)]
+
+
 class Chronos2EncodeArgs(ctypes.Structure):
     """``tsfm_chronos2_encode_args`` (include/tsfm_attn.h)."""
 
@@ -223,6 +234,23 @@ class Chronos2EncodeArgs(ctypes.Structure):
         ("layers", ctypes.POINTER(Chronos2Layer)),
         ("final_norm", ctypes.c_void_p),
         ("stream", ctypes.c_void_p),
+    ]
+
+
+class Chronos2ForwardArgs(ctypes.Structure):
+    """``tsfm_chronos2_forward_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("enc", Chronos2EncodeArgs),
+        ("n_ctx", ctypes.c_int32),
+        ("n_out", ctypes.c_int32),
+        ("feats", ctypes.c_void_p),
+        ("fut_feats", ctypes.c_void_p),
+        ("ctx_valid", ctypes.c_void_p),
+        ("reg", ctypes.c_void_p),
+        ("input_embed", Resblock),
+        ("output_embed", Resblock),
+        ("raw", ctypes.c_void_p),
     ]
 
 
@@ -310,6 +338,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_qkv_project.restype = ctypes.c_int
     lib.tsfm_chronos2_encode.argtypes = [ctypes.POINTER(Chronos2EncodeArgs)]
     lib.tsfm_chronos2_encode.restype = ctypes.c_int
+    lib.tsfm_chronos2_forward.argtypes = [ctypes.POINTER(Chronos2ForwardArgs)]
+    lib.tsfm_chronos2_forward.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -639,6 +669,47 @@ def chronos2_encode(x, key_valid, cos_t, sin_t, layers: Sequence[dict], final_no
                            rope_cos=_ptr(cos_t), rope_sin=_ptr(sin_t), layers=arr, final_norm=_ptr(final_norm),
                            stream=_stream_of(x, stream) if device else None)
     return int(load().tsfm_chronos2_encode(ctypes.byref(a)))
+
+
+def _resblock(rb: dict) -> Resblock:
+    st = Resblock(act=0)
+    for f in RESBLOCK_FIELDS:
+        setattr(st, f, _ptr(rb[f]))
+    hid, d_in = (int(x) for x in rb["hidden_w"].shape)
+    st.hid = hid
+    setattr(st, "in", d_in)
+    st.out = int(rb["output_w"].shape[0])
+    return st
+
+
+def chronos2_forward(raw, feats, fut_feats, ctx_valid, reg, cos_t, sin_t, layers: Sequence[dict], final_norm,
+                     input_embed: dict, output_embed: dict, b: int, n_ctx: int, n_out: int, d: int, nh: int,
+                     d_ff: int, eps: float, keys_all_valid: Optional[bool] = None, scale: float = 1.0, hd: int = 64,
+                     stream=None) -> int:
+    """The model part of the Chronos-2 forecaster (src/chronos2/forecaster.zig:155-183) in one
+    call: input embedding of the context and future patch features, [context; REG; future], the
+    encoder stack, the future rows, the output head into raw (b * n_out, head out). The ResBlocks are
+    dicts of RESBLOCK_FIELDS arrays; ``keys_all_valid`` (of the context patches) defaults to the
+    AND of ctx_valid for host arrays."""
+    device = _is_device(feats)
+    if keys_all_valid is None:
+        if device:
+            raise ValueError("keys_all_valid is required with device tensors")
+        keys_all_valid = bool(np.asarray(ctx_valid).all())
+    arr = (Chronos2Layer * max(1, len(layers)))()
+    for i, ly in enumerate(layers):
+        for f in CHRONOS2_LAYER_FIELDS:
+            setattr(arr[i], f, _ptr(ly[f]))
+    enc = Chronos2EncodeArgs(batch=b, seq=n_ctx + 1 + n_out, d_model=d, heads=nh, head_dim=hd, d_ff=d_ff,
+                             n_layers=len(layers), keys_all_valid=int(bool(keys_all_valid)), eps=eps, scale=scale,
+                             flags=DEVICE_PTRS if device else 0, rope_cos=_ptr(cos_t), rope_sin=_ptr(sin_t),
+                             layers=arr, final_norm=_ptr(final_norm),
+                             stream=_stream_of(feats, stream) if device else None)
+    a = Chronos2ForwardArgs(enc=enc, n_ctx=n_ctx, n_out=n_out, feats=_ptr(feats), fut_feats=_ptr(fut_feats),
+                            ctx_valid=_ptr(ctx_valid), reg=_ptr(reg), input_embed=_resblock(input_embed),
+                            output_embed=_resblock(output_embed), raw=_ptr(raw))
+    a._keep = arr  # the layer array must outlive the call
+    return int(load().tsfm_chronos2_forward(ctypes.byref(a)))
 
 
 def weight_register(w) -> Optional[int]:
