@@ -301,6 +301,52 @@ typedef struct tsfm_chronos2_forward_args {
 int tsfm_chronos2_forward(const tsfm_chronos2_forward_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * Chronos-Bolt model forward: the model part of the forecaster's chunk
+ * (src/chronos_bolt/forecaster.zig:199-213) in one call:
+ *   input embedding (ResBlock(.relu)) of the [values, mask] patch features -> [patches; REG] with
+ *   its key validity -> the T5 encoder (Model.encode, src/chronos_bolt/model.zig:210-254: rmsNorm,
+ *   q/k/v, self-attention with the T5 relative bias and the additive key mask at scale 1, o, ReLU FFN,
+ *   each added back; final norm) -> the one-token decoder (Model.decode, :258-308: self-attention
+ *   over one token = o(v(x)), cross-attention to the encoder output, ReLU FFN; final norm) -> the
+ *   output head (ResBlock) -> raw (batch, output_embed.out), before the inverse instance norm.
+ * The T5 bucket ids are computed on the host with the reference's float32 formula
+ * (tsfm_t5_bucket_table). Requires use_reg (Chronos-Bolt checkpoints set use_reg_token). */
+typedef struct tsfm_bolt_enc_layer {
+    const float *attn_norm, *q, *k, *v, *o;   /* norm (d); q/k/v (inner, d); o (d, inner) */
+    const float *ffn_norm, *wi, *wo;          /* norm (d); wi (d_ff, d); wo (d, d_ff) */
+} tsfm_bolt_enc_layer;
+
+typedef struct tsfm_bolt_dec_layer {
+    const float *self_norm, *self_v, *self_o;                           /* (d); (inner, d); (d, inner) */
+    const float *cross_norm, *cross_q, *cross_k, *cross_v, *cross_o;  /* (d); (inner, d) x3; (d, inner) */
+    const float *ffn_norm, *wi, *wo;
+} tsfm_bolt_dec_layer;
+
+typedef struct tsfm_bolt_forward_args {
+    int32_t batch, n_patch;          /* series; context patches (seq = n_patch + 1 with [REG]) */
+    int32_t d_model, heads, head_dim, d_ff;  /* head_dim = d_kv = 64; inner = heads * head_dim */
+    int32_t n_enc_layers, n_dec_layers;
+    int32_t keys_all_valid;          /* every patch observed (Mask.pick -> FULL) */
+    int32_t rel_buckets, rel_max_distance;
+    float eps;
+    uint32_t flags;                  /* TSFM_ATTN_DEVICE_PTRS or 0 */
+    const float *feats;              /* (batch * n_patch, input_embed.in) [values, mask] */
+    const uint8_t *patch_valid;      /* (batch, n_patch) */
+    const float *reg;                /* (d) the [REG] embedding */
+    const float *dec_start;          /* (d) the decoder start token embedding */
+    const float *rel_table;          /* (rel_buckets, heads), shared by every encoder layer */
+    const tsfm_bolt_enc_layer *enc_layers;  /* host memory */
+    const float *enc_final_norm;
+    const tsfm_bolt_dec_layer *dec_layers;  /* host memory */
+    const float *dec_final_norm;
+    tsfm_resblock input_embed, output_embed;
+    float *raw;                      /* (batch, output_embed.out) */
+    void *stream;
+} tsfm_bolt_forward_args;
+
+int tsfm_bolt_forward(const tsfm_bolt_forward_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * The reference backend's GEMM seam, with the signatures of src/platform/cuda/gemm.c so that the
  * reference's own binding (src/platform/cuda/gpu.zig:16-44) can link this library unchanged:
  * nn.linear's weight products (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then

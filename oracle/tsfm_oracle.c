@@ -709,6 +709,82 @@ void orc_chronos2_model_forward(size_t threads, float *raw, const float *feats, 
     free(emb); free(fut_emb); free(x); free(kv); free(hidden);
 }
 
+/* The model part of the Chronos-Bolt forecaster's chunk (src/chronos_bolt/forecaster.zig:199-213):
+ * embed the patch features, [patches; REG] with its key validity, Model.encode
+ * (src/chronos_bolt/model.zig:210-254), Model.decode (:258-308), the output head. */
+void orc_bolt_model_forward(size_t threads, float *raw, const float *feats, const uint8_t *patch_valid,
+                            const float *reg, const float *dec_start, const float *rel_table, uint32_t num_buckets,
+                            uint32_t max_distance, size_t b, size_t n_patch, size_t d, size_t nh, size_t hd,
+                            size_t d_ff, const orc_bolt_enc_layer *enc, size_t n_enc, const float *enc_final_norm,
+                            const orc_bolt_dec_layer *dec, size_t n_dec, const float *dec_final_norm, float eps,
+                            const orc_resblock *input_embed, const orc_resblock *output_embed) {
+    const size_t seq = n_patch + 1, rows = b * seq, inner = nh * hd;
+    float *emb = (float *)malloc(b * n_patch * d * sizeof(float) + 1);
+    orc_resblock_relu(threads, emb, feats, b * n_patch, input_embed);
+    float *x = (float *)malloc(rows * d * sizeof(float));
+    uint8_t *kv = (uint8_t *)malloc(rows);
+    int all_valid = 1;
+    for (size_t li = 0; li < b; li++) {
+        memcpy(x + li * seq * d, emb + li * n_patch * d, n_patch * d * sizeof(float));
+        memcpy(x + (li * seq + n_patch) * d, reg, d * sizeof(float));
+        for (size_t p = 0; p < n_patch; p++) {
+            kv[li * seq + p] = patch_valid[li * n_patch + p] != 0;
+            all_valid = all_valid && kv[li * seq + p];
+        }
+        kv[li * seq + n_patch] = 1;
+    }
+    float *xn = (float *)malloc(rows * d * sizeof(float));
+    float *delta = (float *)malloc(rows * d * sizeof(float));
+    float *h = (float *)malloc(rows * d_ff * sizeof(float));
+    float *qb = (float *)malloc(rows * inner * sizeof(float));
+    float *kb = (float *)malloc(rows * inner * sizeof(float));
+    float *vb = (float *)malloc(rows * inner * sizeof(float));
+    float *ab = (float *)malloc(rows * inner * sizeof(float));
+    float *bias = (float *)malloc(nh * seq * seq * sizeof(float));
+    orc_position_bias(bias, rel_table, seq, nh, num_buckets, max_distance);
+    for (size_t l = 0; l < n_enc; l++) {
+        const orc_bolt_enc_layer *ly = &enc[l];
+        orc_rms_norm(threads, xn, x, rows, d, ly->attn_norm, eps);
+        orc_linear(threads, qb, xn, rows, ly->q, inner, d, NULL);
+        orc_linear(threads, kb, xn, rows, ly->k, inner, d, NULL);
+        orc_linear(threads, vb, xn, rows, ly->v, inner, d, NULL);
+        orc_bolt_self_attention(threads, qb, kb, vb, ab, bias, kv, all_valid, b, seq, inner, nh, hd);
+        orc_linear(threads, delta, ab, rows, ly->o, d, inner, NULL);
+        orc_add_in_place(x, delta, rows * d);
+        orc_rms_norm(threads, xn, x, rows, d, ly->ffn_norm, eps);
+        orc_linear(threads, h, xn, rows, ly->wi, d_ff, d, NULL);
+        orc_relu(h, rows * d_ff);
+        orc_linear(threads, delta, h, rows, ly->wo, d, d_ff, NULL);
+        orc_add_in_place(x, delta, rows * d);
+    }
+    orc_rms_norm(threads, x, x, rows, d, enc_final_norm, eps);
+    float *y = (float *)malloc(b * d * sizeof(float));
+    for (size_t r = 0; r < b; r++) memcpy(y + r * d, dec_start, d * sizeof(float));
+    for (size_t l = 0; l < n_dec; l++) {
+        const orc_bolt_dec_layer *ly = &dec[l];
+        orc_rms_norm(threads, xn, y, b, d, ly->self_norm, eps);
+        orc_linear(threads, vb, xn, b, ly->self_v, inner, d, NULL);
+        orc_linear(threads, delta, vb, b, ly->self_o, d, inner, NULL);
+        orc_add_in_place(y, delta, b * d);
+        orc_rms_norm(threads, xn, y, b, d, ly->cross_norm, eps);
+        orc_linear(threads, qb, xn, b, ly->cross_q, inner, d, NULL);
+        orc_linear(threads, kb, x, rows, ly->cross_k, inner, d, NULL);
+        orc_linear(threads, vb, x, rows, ly->cross_v, inner, d, NULL);
+        orc_bolt_cross_attention(threads, qb, kb, vb, ab, kv, b, seq, inner, nh, hd);
+        orc_linear(threads, delta, ab, b, ly->cross_o, d, inner, NULL);
+        orc_add_in_place(y, delta, b * d);
+        orc_rms_norm(threads, xn, y, b, d, ly->ffn_norm, eps);
+        orc_linear(threads, h, xn, b, ly->wi, d_ff, d, NULL);
+        orc_relu(h, b * d_ff);
+        orc_linear(threads, delta, h, b, ly->wo, d, d_ff, NULL);
+        orc_add_in_place(y, delta, b * d);
+    }
+    orc_rms_norm(threads, xn, y, b, d, dec_final_norm, eps);
+    orc_resblock_relu(threads, raw, xn, b, output_embed);
+    free(emb); free(x); free(kv); free(xn); free(delta); free(h); free(qb); free(kb); free(vb); free(ab);
+    free(bias); free(y);
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* Timestral (src/timestral/model.zig) */
 

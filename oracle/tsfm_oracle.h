@@ -130,6 +130,21 @@ void orc_chronos2_model_forward(size_t threads, float *raw, const float *feats, 
                                 const orc_chronos2_layer *layers, const float *final_norm, float eps,
                                 const float *cos_t, const float *sin_t, float scale, const orc_resblock *input_embed,
                                 const orc_resblock *output_embed);
+/* Chronos-Bolt layer weights (src/chronos_bolt/model.zig:12-55), nn.Weight (out, in) layout. */
+typedef struct orc_bolt_enc_layer {
+    const float *attn_norm, *q, *k, *v, *o, *ffn_norm, *wi, *wo;
+} orc_bolt_enc_layer;
+typedef struct orc_bolt_dec_layer {
+    const float *self_norm, *self_v, *self_o, *cross_norm, *cross_q, *cross_k, *cross_v, *cross_o;
+    const float *ffn_norm, *wi, *wo;
+} orc_bolt_dec_layer;
+/* The model part of the Chronos-Bolt forecaster's chunk (src/chronos_bolt/forecaster.zig:199-213). */
+void orc_bolt_model_forward(size_t threads, float *raw, const float *feats, const uint8_t *patch_valid,
+                            const float *reg, const float *dec_start, const float *rel_table, uint32_t num_buckets,
+                            uint32_t max_distance, size_t b, size_t n_patch, size_t d, size_t nh, size_t hd,
+                            size_t d_ff, const orc_bolt_enc_layer *enc, size_t n_enc, const float *enc_final_norm,
+                            const orc_bolt_dec_layer *dec, size_t n_dec, const float *dec_final_norm, float eps,
+                            const orc_resblock *input_embed, const orc_resblock *output_embed);
 void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
                                size_t hd, size_t rope_dim, float theta, const size_t *first_obs);
 /* Timestral TimeJob.rope (src/timestral/model.zig:558-577), in place on the fused qkv buffer. */

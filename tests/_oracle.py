@@ -49,6 +49,19 @@ def resblock_struct(rb):
     return st
 
 
+BOLT_ENC_FIELDS = ("attn_norm", "q", "k", "v", "o", "ffn_norm", "wi", "wo")
+BOLT_DEC_FIELDS = ("self_norm", "self_v", "self_o", "cross_norm", "cross_q", "cross_k", "cross_v", "cross_o",
+                   "ffn_norm", "wi", "wo")
+
+
+class BoltEncLayer(ctypes.Structure):
+    _fields_ = [(f, _vp) for f in BOLT_ENC_FIELDS]
+
+
+class BoltDecLayer(ctypes.Structure):
+    _fields_ = [(f, _vp) for f in BOLT_DEC_FIELDS]
+
+
 class Oracle:
     def __init__(self, path):
         self.path = str(path)
@@ -62,6 +75,10 @@ class Oracle:
         L.orc_rms_norm.argtypes = [_sz, _vp, _vp, _sz, _sz, _vp, _f]
         L.orc_relu.argtypes = [_vp, _sz]
         L.orc_resblock_relu.argtypes = [_sz, _vp, _vp, _sz, ctypes.POINTER(OrcResblock)]
+        L.orc_bolt_model_forward.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, _sz,
+                                             _sz, _sz, _sz, _sz, _sz, ctypes.POINTER(BoltEncLayer), _sz, _vp,
+                                             ctypes.POINTER(BoltDecLayer), _sz, _vp, _f, ctypes.POINTER(OrcResblock),
+                                             ctypes.POINTER(OrcResblock)]
         L.orc_chronos2_model_forward.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz,
                                                  ctypes.POINTER(Chronos2Layer), _vp, _f, _vp, _vp, _f,
                                                  ctypes.POINTER(OrcResblock), ctypes.POINTER(OrcResblock)]
@@ -138,6 +155,23 @@ class Oracle:
         self.lib.orc_chronos2_model_forward(threads, ptr(raw), ptr(feats), ptr(fut_feats), ptr(ctx_valid), ptr(reg), b,
                                             n_ctx, n_out, d, nh, hd, d_ff, len(layers), arr, ptr(final_norm), eps,
                                             ptr(cos_t), ptr(sin_t), scale, ctypes.byref(ie), ctypes.byref(oe))
+
+    def bolt_model_forward(self, threads, raw, feats, patch_valid, reg, dec_start, rel_table, buckets, max_distance,
+                           b, n_patch, d, nh, hd, d_ff, enc, enc_final_norm, dec, dec_final_norm, eps, input_embed,
+                           output_embed):
+        ea = (BoltEncLayer * max(1, len(enc)))()
+        for i, ly in enumerate(enc):
+            for f in BOLT_ENC_FIELDS:
+                setattr(ea[i], f, ptr(ly[f]))
+        da = (BoltDecLayer * max(1, len(dec)))()
+        for i, ly in enumerate(dec):
+            for f in BOLT_DEC_FIELDS:
+                setattr(da[i], f, ptr(ly[f]))
+        ie, oe = resblock_struct(input_embed), resblock_struct(output_embed)
+        self.lib.orc_bolt_model_forward(threads, ptr(raw), ptr(feats), ptr(patch_valid), ptr(reg), ptr(dec_start),
+                                        ptr(rel_table), buckets, max_distance, b, n_patch, d, nh, hd, d_ff, ea, len(enc),
+                                        ptr(enc_final_norm), da, len(dec), ptr(dec_final_norm), eps, ctypes.byref(ie),
+                                        ctypes.byref(oe))
 
     def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
         self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)

@@ -243,3 +243,60 @@ def chronos2_model_forward_f64(feats, fut_feats, ctx_valid, reg, b, n_ctx, n_out
     kv = np.concatenate([np.asarray(ctx_valid, bool).reshape(b, n_ctx), np.ones((b, 1 + n_out), bool)], axis=1)
     x = chronos2_encode_f64(x, kv, b, seq, nh, layers, final_norm, eps, cos_t, sin_t, scale).reshape(b, seq, d)
     return resblock_f64(output_embed, x[:, n_ctx + 1:].reshape(b * n_out, d))
+
+
+def bolt_layers(rng, n_enc, n_dec, d, inner, d_ff):
+    """Random-init Chronos-Bolt encoder and decoder layer weights ((out, in) layout)."""
+    def lin(o, i):
+        return (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+
+    enc = [dict(attn_norm=norm(), q=lin(inner, d), k=lin(inner, d), v=lin(inner, d), o=lin(d, inner), ffn_norm=norm(),
+                wi=lin(d_ff, d), wo=lin(d, d_ff)) for _ in range(n_enc)]
+    dec = [dict(self_norm=norm(), self_v=lin(inner, d), self_o=lin(d, inner), cross_norm=norm(), cross_q=lin(inner, d),
+                cross_k=lin(inner, d), cross_v=lin(inner, d), cross_o=lin(d, inner), ffn_norm=norm(), wi=lin(d_ff, d),
+                wo=lin(d, d_ff)) for _ in range(n_dec)]
+    return enc, dec
+
+
+def bolt_model_forward_f64(feats, patch_valid, reg, dec_start, bias, b, n_patch, nh, enc, enc_final_norm, dec,
+                           dec_final_norm, eps, input_embed, output_embed, hd=64):
+    """The model part of the Chronos-Bolt forecaster (src/chronos_bolt/forecaster.zig:199-213) in
+    float64 from its definition: bias is the (H, seq, seq) T5 position bias."""
+    W = lambda a: np.asarray(a, np.float64)
+    emb = resblock_f64(input_embed, feats).reshape(b, n_patch, -1)
+    d = emb.shape[2]
+    seq = n_patch + 1
+    x = np.concatenate([emb, np.broadcast_to(W(reg), (b, 1, d))], axis=1).reshape(b * seq, d)
+    kv = np.concatenate([np.asarray(patch_valid, bool).reshape(b, n_patch), np.ones((b, 1), bool)], axis=1)
+    bias = W(bias).reshape(nh, seq, seq)
+    for ly in enc:
+        xn = rms_norm_f64(x, ly["attn_norm"], eps)
+        q, k, v = xn @ W(ly["q"]).T, xn @ W(ly["k"]).T, xn @ W(ly["v"]).T
+        ab = np.zeros_like(q)
+        for r in range(b):
+            sl = slice(r * seq, (r + 1) * seq)
+            allowed = allowed_matrix(1, seq, seq, kv[r])
+            for h in range(nh):
+                hs = slice(h * hd, (h + 1) * hd)
+                ab[sl, hs] = naive_attend(q[sl, hs], k[sl, hs], v[sl, hs], allowed, 1.0, bias[h])
+        x = x + ab @ W(ly["o"]).T
+        xn = rms_norm_f64(x, ly["ffn_norm"], eps)
+        x = x + np.maximum(xn @ W(ly["wi"]).T, 0.0) @ W(ly["wo"]).T
+    x = rms_norm_f64(x, enc_final_norm, eps)
+    y = np.broadcast_to(W(dec_start), (b, d)).copy()
+    for ly in dec:
+        y = y + (rms_norm_f64(y, ly["self_norm"], eps) @ W(ly["self_v"]).T) @ W(ly["self_o"]).T
+        qd = rms_norm_f64(y, ly["cross_norm"], eps) @ W(ly["cross_q"]).T
+        k, v = x @ W(ly["cross_k"]).T, x @ W(ly["cross_v"]).T
+        ad = np.zeros_like(qd)
+        for r in range(b):
+            sl = slice(r * seq, (r + 1) * seq)
+            for h in range(nh):
+                hs = slice(h * hd, (h + 1) * hd)
+                ad[r:r + 1, hs] = naive_attend(qd[r:r + 1, hs], k[sl, hs], v[sl, hs], kv[r][None, :], 1.0)
+        y = y + ad @ W(ly["cross_o"]).T
+        y = y + np.maximum(rms_norm_f64(y, ly["ffn_norm"], eps) @ W(ly["wi"]).T, 0.0) @ W(ly["wo"]).T
+    return resblock_f64(output_embed, rms_norm_f64(y, dec_final_norm, eps))

@@ -35,7 +35,9 @@ def test_library_exports_every_declared_symbol(ta):
                                           ("ProjArgs", "tsfm_proj_args"), ("Chronos2Layer", "tsfm_chronos2_layer"),
                                           ("Chronos2EncodeArgs", "tsfm_chronos2_encode_args"),
                                           ("Resblock", "tsfm_resblock"),
-                                          ("Chronos2ForwardArgs", "tsfm_chronos2_forward_args")])
+                                          ("Chronos2ForwardArgs", "tsfm_chronos2_forward_args"),
+                                          ("BoltEncLayer", "tsfm_bolt_enc_layer"), ("BoltDecLayer", "tsfm_bolt_dec_layer"),
+                                          ("BoltForwardArgs", "tsfm_bolt_forward_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)

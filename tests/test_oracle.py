@@ -610,3 +610,25 @@ def test_chronos2_model_forward_matches_f64(orc):
     want = _ref.chronos2_model_forward_f64(feats, fut, cv, reg, b, n_ctx, n_out, nh, layers, fn, 1e-6, cos_t, sin_t,
                                            1.0, ie, oe)
     assert _ref.scaled_err(raw, want) < 3e-5
+
+
+def test_bolt_model_forward_matches_f64(orc):
+    """The model part of the Chronos-Bolt chunk: embed, [patches; REG], T5 encoder with the relative
+    bias, one-token decoder with cross-attention, output head; against float64 from the definition."""
+    rng = np.random.default_rng(47)
+    b, n_patch, nh, d_ff, ps, out = 3, 10, 2, 256, 16, 36
+    d = inner = nh * 64
+    seq = n_patch + 1
+    feats = rng.standard_normal((b * n_patch, 2 * ps)).astype(np.float32)
+    pv = (rng.random((b, n_patch)) < 0.8).astype(np.uint8)
+    reg, start = (rng.standard_normal(d).astype(np.float32) for _ in range(2))
+    table = _ref.t5_bias_table(rng, 32, nh)
+    enc, dec = _ref.bolt_layers(rng, 2, 2, d, inner, d_ff)
+    ef, df = ((1 + 0.1 * rng.standard_normal(d)).astype(np.float32) for _ in range(2))
+    ie, oe = _ref.resblock(rng, 2 * ps, d_ff, d), _ref.resblock(rng, d, d_ff, out)
+    raw = np.zeros((b, out), np.float32)
+    orc.bolt_model_forward(4, raw, feats, pv, reg, start, table, 32, 128, b, n_patch, d, nh, 64, d_ff, enc, ef, dec,
+                           df, 1e-6, ie, oe)
+    bias = orc.position_bias(table, seq, nh, 32, 128)
+    want = _ref.bolt_model_forward_f64(feats, pv, reg, start, bias, b, n_patch, nh, enc, ef, dec, df, 1e-6, ie, oe)
+    assert _ref.scaled_err(raw, want) < 3e-5

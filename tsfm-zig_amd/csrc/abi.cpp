@@ -913,6 +913,235 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
     return TSFM_OK;
 }
 
+// ---- Chronos-Bolt model forward -------------------------------------------------------------------
+
+namespace {
+
+struct BoltDev {  // device-side pointers of one call
+    const float *feats, *reg, *dec_start, *rel_table, *enc_final_norm, *dec_final_norm;
+    const uint8_t* patch_valid;
+    const int32_t* rel_bucket;
+    const tsfm_bolt_enc_layer* enc;
+    const tsfm_bolt_dec_layer* dec;
+    tsfm_resblock ie, oe;
+    float* raw;
+};
+
+// Scratch: x (rows x d), kv (rows bytes), emb (rows x d), xn (rows x d), q/k/v/ab (rows x inner
+// each), hbuf (rows x max(d_ff, hid)), rbuf (rows x max(d, head out)); the decoder reuses q/k/v/ab.
+hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, char* scratch, const size_t* at,
+                           hipStream_t s) {
+    const int nb = a->batch, np = a->n_patch, seq = np + 1, d = a->d_model, inner = a->heads * a->head_dim;
+    const int F = a->d_ff, R = nb * seq;
+    float* x = reinterpret_cast<float*>(scratch + at[0]);
+    uint8_t* kv = reinterpret_cast<uint8_t*>(scratch + at[1]);
+    float* emb = reinterpret_cast<float*>(scratch + at[2]);
+    float* xn = reinterpret_cast<float*>(scratch + at[3]);
+    float* q = reinterpret_cast<float*>(scratch + at[4]);
+    float* k = reinterpret_cast<float*>(scratch + at[5]);
+    float* v = reinterpret_cast<float*>(scratch + at[6]);
+    float* ab = reinterpret_cast<float*>(scratch + at[7]);
+    float* hb = reinterpret_cast<float*>(scratch + at[8]);
+    float* rb = reinterpret_cast<float*>(scratch + at[9]);
+    hipError_t e = resblock_on(dv.ie, dv.feats, nb * np, emb, hb, rb, s);
+    if (e == hipSuccess) e = tsfm::launch_assemble_sequence(emb, nullptr, dv.reg, dv.patch_valid, x, kv, nb, np, 0, d, s);
+    // ---- encoder (Model.encode) ----
+    for (int l = 0; l < a->n_enc_layers && e == hipSuccess; l++) {
+        const tsfm_bolt_enc_layer& ly = dv.enc[l];
+        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.attn_norm, R, d, a->eps, s)) != hipSuccess) break;
+        tsfm::ProjParams p{};
+        p.x = xn; p.x_tok = d; p.w0 = ly.q; p.w1 = ly.k; p.w2 = ly.v; p.w_ld = d; p.alpha = 1.f;
+        p.y0 = q; p.y1 = k; p.y2 = v; p.y0_tok = p.y1_tok = p.y2_tok = inner;
+        p.tokens = R; p.seq = seq; p.d_in = d; p.width = inner; p.n_out = 3; p.out_dtype = TSFM_DTYPE_F32;
+        if ((e = tsfm::launch_proj(p, s)) != hipSuccess) break;
+        tsfm::Params ap{};
+        ap.q = q; ap.k = k; ap.v = v; ap.o = ab;
+        ap.q_tok = ap.k_tok = ap.v_tok = ap.o_tok = inner;
+        ap.q_batch = ap.k_batch = ap.v_batch = ap.o_batch = (int64_t)seq * inner;
+        ap.key_valid = kv; ap.kv_batch = seq;
+        ap.rel_table = dv.rel_table; ap.rel_bucket = dv.rel_bucket; ap.rel_buckets = a->rel_buckets;
+        ap.B = nb; ap.H = a->heads; ap.n_q = seq; ap.n_k = seq; ap.scale = 1.f;
+        const int mask = a->keys_all_valid ? TSFM_MASK_FULL : TSFM_MASK_KEYS_ADDITIVE;  // Mask.pick(false, all, true)
+        if ((e = tsfm::launch_attn_f32(ap, mask, tsfm::BIAS_REL, false, s)) != hipSuccess) break;
+        if ((e = linear_on(ab, inner, ly.o, d, inner, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.ffn_norm, R, d, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.wi, F, d, hb, F, R, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
+        if ((e = linear_on(hb, F, ly.wo, d, F, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+    }
+    if (e == hipSuccess) e = tsfm::launch_rms_norm(x, d, x, d, dv.enc_final_norm, R, d, a->eps, s);
+    // ---- decoder (Model.decode): one token per series; y (nb x d) in emb ----
+    float* y = emb;
+    if (e == hipSuccess) e = tsfm::launch_broadcast_rows(dv.dec_start, y, nb, d, s);
+    for (int l = 0; l < a->n_dec_layers && e == hipSuccess; l++) {
+        const tsfm_bolt_dec_layer& ly = dv.dec[l];
+        // self-attention over the single decoder token: o(v(norm(y)))
+        if ((e = tsfm::launch_rms_norm(y, d, xn, d, ly.self_norm, nb, d, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.self_v, inner, d, v, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
+        if ((e = linear_on(v, inner, ly.self_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
+        // cross-attention to the encoder output
+        if ((e = tsfm::launch_rms_norm(y, d, xn, d, ly.cross_norm, nb, d, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.cross_q, inner, d, q, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
+        tsfm::ProjParams p{};
+        p.x = x; p.x_tok = d; p.w0 = ly.cross_k; p.w1 = ly.cross_v; p.w_ld = d; p.alpha = 1.f;
+        p.y0 = k; p.y1 = v; p.y0_tok = p.y1_tok = inner;
+        p.tokens = R; p.seq = seq; p.d_in = d; p.width = inner; p.n_out = 2; p.out_dtype = TSFM_DTYPE_F32;
+        if ((e = tsfm::launch_proj(p, s)) != hipSuccess) break;
+        tsfm::Params ap{};  // CrossJob.attend (:349-381): one query per (series, head), key mask, no scale
+        ap.q = q; ap.k = k; ap.v = v; ap.o = ab;
+        ap.q_tok = inner; ap.q_batch = inner; ap.o_tok = inner; ap.o_batch = inner;
+        ap.k_tok = ap.v_tok = inner; ap.k_batch = ap.v_batch = (int64_t)seq * inner;
+        ap.key_valid = kv; ap.kv_batch = seq;
+        ap.B = nb; ap.H = a->heads; ap.n_q = 1; ap.n_k = seq; ap.scale = 1.f;
+        if ((e = tsfm::launch_attn_f32(ap, TSFM_MASK_KEYS_ADDITIVE, tsfm::BIAS_NONE, false, s)) != hipSuccess) break;
+        if ((e = linear_on(ab, inner, ly.cross_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
+        // FFN
+        if ((e = tsfm::launch_rms_norm(y, d, xn, d, ly.ffn_norm, nb, d, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.wi, F, d, hb, F, nb, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
+        if ((e = linear_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
+    }
+    if (e == hipSuccess) e = tsfm::launch_rms_norm(y, d, xn, d, dv.dec_final_norm, nb, d, a->eps, s);
+    if (e == hipSuccess) e = resblock_on(dv.oe, xn, nb, dv.raw, hb, rb, s);
+    return e;
+}
+
+}  // namespace
+
+int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (a->batch < 0 || a->n_patch < 0 || a->n_enc_layers < 0 || a->n_dec_layers < 0 || a->heads < 0 || a->d_ff < 0)
+        return fail(TSFM_E_INVALID, "negative size");
+    if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
+    if (a->batch == 0) return TSFM_OK;
+    const int64_t nb = a->batch, seq = (int64_t)a->n_patch + 1, d = a->d_model, inner = (int64_t)a->heads * 64;
+    const int64_t F = a->d_ff, R = nb * seq;
+    if (d <= 0 || d % 16 || F <= 0 || F % 16 || inner % 64 || inner == 0)
+        return fail(TSFM_E_UNSUPPORTED, "d_model and d_ff must be positive multiples of 16");
+    if (2 * seq - 1 > 2048) return fail(TSFM_E_UNSUPPORTED, "sequence too long for the T5 offset table");
+    if (R > 0x7fffffff / 4) return fail(TSFM_E_UNSUPPORTED, "too many tokens");
+    if (a->rel_buckets < 4 || a->rel_table == nullptr) return fail(TSFM_E_INVALID, "the T5 table is required");
+    if (!a->feats || !a->patch_valid || !a->reg || !a->dec_start || !a->enc_final_norm || !a->dec_final_norm ||
+        !a->raw || (a->n_enc_layers && !a->enc_layers) || (a->n_dec_layers && !a->dec_layers))
+        return fail(TSFM_E_INVALID, "a required pointer is NULL");
+    for (int l = 0; l < a->n_enc_layers; l++) {
+        const tsfm_bolt_enc_layer& y = a->enc_layers[l];
+        for (const float* p : {y.attn_norm, y.q, y.k, y.v, y.o, y.ffn_norm, y.wi, y.wo})
+            if (p == nullptr) return fail(TSFM_E_INVALID, "encoder layer %d has a NULL weight", l);
+    }
+    for (int l = 0; l < a->n_dec_layers; l++) {
+        const tsfm_bolt_dec_layer& y = a->dec_layers[l];
+        for (const float* p : {y.self_norm, y.self_v, y.self_o, y.cross_norm, y.cross_q, y.cross_k, y.cross_v,
+                               y.cross_o, y.ffn_norm, y.wi, y.wo})
+            if (p == nullptr) return fail(TSFM_E_INVALID, "decoder layer %d has a NULL weight", l);
+    }
+    int rc;
+    if ((rc = validate_resblock(a->input_embed, a->input_embed.in, (int)d, "input_embed")) != TSFM_OK) return rc;
+    if ((rc = validate_resblock(a->output_embed, (int)d, 0, "output_embed")) != TSFM_OK) return rc;
+    if ((rc = ensure_ready()) != TSFM_OK) return rc;
+    // T5 bucket ids of key - query for the (seq, seq) self-attention (host, float32 log as the reference).
+    std::vector<int32_t> buckets((size_t)(2 * seq - 1));
+    if ((rc = tsfm_t5_bucket_table(buckets.data(), (int32_t)seq, (int32_t)seq, (uint32_t)a->rel_buckets,
+                                   (uint32_t)a->rel_max_distance)) != TSFM_OK)
+        return rc;
+    const int64_t hid = std::max(std::max<int64_t>(a->input_embed.hid, a->output_embed.hid), F);
+    const int64_t rw = std::max<int64_t>(d, a->output_embed.out);
+    const size_t sz[11] = {(size_t)(R * d) * 4, (size_t)R, (size_t)(R * d) * 4, (size_t)(R * d) * 4,
+                           (size_t)(R * inner) * 4, (size_t)(R * inner) * 4, (size_t)(R * inner) * 4,
+                           (size_t)(R * inner) * 4, (size_t)(R * hid) * 4, (size_t)(R * rw) * 4,
+                           buckets.size() * 4};
+    hipError_t e;
+    if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
+        hipStream_t s = static_cast<hipStream_t>(a->stream);
+        Plan plan;
+        size_t at[11];
+        for (int i = 0; i < 11; i++) at[i] = plan.take(sz[i]);
+        char* scratch = nullptr;
+        if ((e = hipMallocAsync(reinterpret_cast<void**>(&scratch), plan.off, s)) != hipSuccess)
+            return hip_fail(e, "forward scratch allocation");
+        // Pageable source: the call returns once the ids are staged, so the vector may go.
+        e = hipMemcpyAsync(scratch + at[10], buckets.data(), sz[10], hipMemcpyHostToDevice, s);
+        BoltDev dv{a->feats, a->reg, a->dec_start, a->rel_table, a->enc_final_norm, a->dec_final_norm,
+                   a->patch_valid, reinterpret_cast<const int32_t*>(scratch + at[10]), a->enc_layers, a->dec_layers,
+                   a->input_embed, a->output_embed, a->raw};
+        if (e == hipSuccess) e = bolt_forward_on(a, dv, scratch, at, s);
+        const hipError_t f = hipFreeAsync(scratch, s);
+        if (e != hipSuccess) return hip_fail(e, "forward launch");
+        if (f != hipSuccess) return hip_fail(f, "forward scratch release");
+        return TSFM_OK;
+    }
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    Staging st;
+    size_t at[11];
+    for (int i = 0; i < 10; i++) at[i] = st.add(nullptr, sz[i]);
+    at[10] = st.add(buckets.data(), sz[10]);
+    const int64_t pin = a->input_embed.in;
+    const size_t feats_at = st.add(a->feats, (size_t)(nb * a->n_patch * pin) * 4);
+    const size_t pv_at = st.add(a->patch_valid, (size_t)(nb * a->n_patch));
+    const size_t reg_at = st.add(a->reg, (size_t)d * 4), ds_at = st.add(a->dec_start, (size_t)d * 4);
+    const size_t rt_at = st.add(a->rel_table, (size_t)a->rel_buckets * a->heads * 4);
+    const size_t ef_at = st.add(a->enc_final_norm, (size_t)d * 4), df_at = st.add(a->dec_final_norm, (size_t)d * 4);
+    const size_t raw_at = st.add(nullptr, (size_t)(nb * a->output_embed.out) * 4);
+    auto stage_block = [&](const tsfm_resblock& rb, size_t o[6]) {
+        o[0] = st.add(rb.hidden_w, (size_t)rb.hid * rb.in * 4);   o[1] = st.add(rb.hidden_b, (size_t)rb.hid * 4);
+        o[2] = st.add(rb.output_w, (size_t)rb.out * rb.hid * 4);  o[3] = st.add(rb.output_b, (size_t)rb.out * 4);
+        o[4] = st.add(rb.residual_w, (size_t)rb.out * rb.in * 4); o[5] = st.add(rb.residual_b, (size_t)rb.out * 4);
+    };
+    size_t ie_at[6], oe_at[6];
+    stage_block(a->input_embed, ie_at);
+    stage_block(a->output_embed, oe_at);
+    const size_t vd = (size_t)d * 4, di = (size_t)(d * inner) * 4, df = (size_t)(d * F) * 4;
+    const size_t enc_sz[8] = {vd, di, di, di, di, vd, df, df};
+    const size_t dec_sz[11] = {vd, di, di, vd, di, di, di, di, vd, df, df};
+    std::vector<size_t> ew((size_t)a->n_enc_layers * 8), dw((size_t)a->n_dec_layers * 11);
+    for (int l = 0; l < a->n_enc_layers; l++) {
+        const tsfm_bolt_enc_layer& y = a->enc_layers[l];
+        const float* src[8] = {y.attn_norm, y.q, y.k, y.v, y.o, y.ffn_norm, y.wi, y.wo};
+        for (int i = 0; i < 8; i++) ew[(size_t)l * 8 + i] = st.add(src[i], enc_sz[i]);
+    }
+    for (int l = 0; l < a->n_dec_layers; l++) {
+        const tsfm_bolt_dec_layer& y = a->dec_layers[l];
+        const float* src[11] = {y.self_norm, y.self_v, y.self_o, y.cross_norm, y.cross_q, y.cross_k, y.cross_v,
+                                y.cross_o, y.ffn_norm, y.wi, y.wo};
+        for (int i = 0; i < 11; i++) dw[(size_t)l * 11 + i] = st.add(src[i], dec_sz[i]);
+    }
+    if ((rc = ensure_buf(ctx, st.plan.off)) != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    if ((e = st.upload(base, s)) != hipSuccess) return hip_fail(e, "host-to-device copy");
+    auto dp = [&](size_t off) { return reinterpret_cast<const float*>(base + off); };
+    std::vector<tsfm_bolt_enc_layer> el((size_t)a->n_enc_layers);
+    std::vector<tsfm_bolt_dec_layer> dl((size_t)a->n_dec_layers);
+    for (int l = 0; l < a->n_enc_layers; l++) {
+        const size_t* w = &ew[(size_t)l * 8];
+        el[(size_t)l] = tsfm_bolt_enc_layer{dp(w[0]), dp(w[1]), dp(w[2]), dp(w[3]), dp(w[4]), dp(w[5]), dp(w[6]), dp(w[7])};
+    }
+    for (int l = 0; l < a->n_dec_layers; l++) {
+        const size_t* w = &dw[(size_t)l * 11];
+        dl[(size_t)l] = tsfm_bolt_dec_layer{dp(w[0]), dp(w[1]), dp(w[2]), dp(w[3]), dp(w[4]), dp(w[5]),
+                                            dp(w[6]), dp(w[7]), dp(w[8]), dp(w[9]), dp(w[10])};
+    }
+    auto dev_block = [&](const tsfm_resblock& rb, const size_t o[6]) {
+        tsfm_resblock r = rb;
+        r.hidden_w = dp(o[0]); r.hidden_b = dp(o[1]); r.output_w = dp(o[2]); r.output_b = dp(o[3]);
+        r.residual_w = dp(o[4]); r.residual_b = dp(o[5]);
+        return r;
+    };
+    BoltDev dv{dp(feats_at), dp(reg_at), dp(ds_at), dp(rt_at), dp(ef_at), dp(df_at),
+               reinterpret_cast<const uint8_t*>(base + pv_at), reinterpret_cast<const int32_t*>(base + at[10]),
+               el.data(), dl.data(), dev_block(a->input_embed, ie_at), dev_block(a->output_embed, oe_at),
+               reinterpret_cast<float*>(base + raw_at)};
+    e = bolt_forward_on(a, dv, base, at, s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "forward launch");
+    }
+    if ((e = hipMemcpyAsync(a->raw, base + raw_at, (size_t)(nb * a->output_embed.out) * 4, hipMemcpyDeviceToHost, s)) !=
+        hipSuccess)
+        return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
+}
+
 // ---- the reference backend's GEMM seam ------------------------------------------------------------
 
 void* tsfm_weight_register(const float* data, size_t len) {

@@ -64,7 +64,21 @@ __global__ __launch_bounds__(256) void gather_future(const float* x, float* hidd
     for (int i = 4 * lane; i < d; i += 256) st4(dst + i, ld4(src + i));
 }
 
+// Every row of y is the same vector (the decoder start token, src/chronos_bolt/model.zig:281-282).
+__global__ __launch_bounds__(256) void broadcast_rows(const float* v, float* y, int rows, int d) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    for (int i = 4 * lane; i < d; i += 256) st4(y + (int64_t)row * d + i, ld4(v + i));
+}
+
 }  // namespace
+
+hipError_t launch_broadcast_rows(const float* v, float* y, int rows, int d, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (d % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(broadcast_rows, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, v, y, rows, d);
+    return hipGetLastError();
+}
 
 hipError_t launch_assemble_sequence(const float* ctx_emb, const float* fut_emb, const float* reg,
                                     const uint8_t* ctx_valid, float* x, uint8_t* key_valid, int nb, int n_ctx,

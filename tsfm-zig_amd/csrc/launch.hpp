@@ -75,5 +75,6 @@ hipError_t launch_assemble_sequence(const float* ctx_emb, const float* fut_emb, 
                                     int n_out, int d, hipStream_t stream);
 hipError_t launch_gather_future(const float* x, float* hidden, int nb, int n_ctx, int n_out, int d,
                                 hipStream_t stream);
+hipError_t launch_broadcast_rows(const float* v, float* y, int rows, int d, hipStream_t stream);
 
 }  // namespace tsfm

@@ -61,6 +61,7 @@ EXPORTS = (
     "tsfm_qkv_project",
     "tsfm_chronos2_encode",
     "tsfm_chronos2_forward",
+    "tsfm_bolt_forward",
     "tsfm_weight_register",
     "tsfm_weight_release",
     "tsfm_sgemm_nt",
@@ -237,6 +238,23 @@ class Chronos2EncodeArgs(ctypes.Structure):
     ]
 
 
+BOLT_ENC_FIELDS = ("attn_norm", "q", "k", "v", "o", "ffn_norm", "wi", "wo")
+BOLT_DEC_FIELDS = ("self_norm", "self_v", "self_o", "cross_norm", "cross_q", "cross_k", "cross_v", "cross_o",
+                   "ffn_norm", "wi", "wo")
+
+
+class BoltEncLayer(ctypes.Structure):
+    """``tsfm_bolt_enc_layer`` (include/tsfm_attn.h)."""
+
+    _fields_ = [(f, ctypes.c_void_p) for f in BOLT_ENC_FIELDS]
+
+
+class BoltDecLayer(ctypes.Structure):
+    """``tsfm_bolt_dec_layer`` (include/tsfm_attn.h)."""
+
+    _fields_ = [(f, ctypes.c_void_p) for f in BOLT_DEC_FIELDS]
+
+
 class Chronos2ForwardArgs(ctypes.Structure):
     """``tsfm_chronos2_forward_args`` (include/tsfm_attn.h)."""
 
@@ -251,6 +269,39 @@ class Chronos2ForwardArgs(ctypes.Structure):
         ("input_embed", Resblock),
         ("output_embed", Resblock),
         ("raw", ctypes.c_void_p),
+    ]
+
+
+class BoltForwardArgs(ctypes.Structure):
+    """``tsfm_bolt_forward_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("n_patch", ctypes.c_int32),
+        ("d_model", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("d_ff", ctypes.c_int32),
+        ("n_enc_layers", ctypes.c_int32),
+        ("n_dec_layers", ctypes.c_int32),
+        ("keys_all_valid", ctypes.c_int32),
+        ("rel_buckets", ctypes.c_int32),
+        ("rel_max_distance", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("flags", ctypes.c_uint32),
+        ("feats", ctypes.c_void_p),
+        ("patch_valid", ctypes.c_void_p),
+        ("reg", ctypes.c_void_p),
+        ("dec_start", ctypes.c_void_p),
+        ("rel_table", ctypes.c_void_p),
+        ("enc_layers", ctypes.POINTER(BoltEncLayer)),
+        ("enc_final_norm", ctypes.c_void_p),
+        ("dec_layers", ctypes.POINTER(BoltDecLayer)),
+        ("dec_final_norm", ctypes.c_void_p),
+        ("input_embed", Resblock),
+        ("output_embed", Resblock),
+        ("raw", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p),
     ]
 
 
@@ -340,6 +391,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_chronos2_encode.restype = ctypes.c_int
     lib.tsfm_chronos2_forward.argtypes = [ctypes.POINTER(Chronos2ForwardArgs)]
     lib.tsfm_chronos2_forward.restype = ctypes.c_int
+    lib.tsfm_bolt_forward.argtypes = [ctypes.POINTER(BoltForwardArgs)]
+    lib.tsfm_bolt_forward.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -710,6 +763,39 @@ def chronos2_forward(raw, feats, fut_feats, ctx_valid, reg, cos_t, sin_t, layers
                             output_embed=_resblock(output_embed), raw=_ptr(raw))
     a._keep = arr  # the layer array must outlive the call
     return int(load().tsfm_chronos2_forward(ctypes.byref(a)))
+
+
+def bolt_forward(raw, feats, patch_valid, reg, dec_start, rel_table, enc_layers: Sequence[dict], enc_final_norm,
+                 dec_layers: Sequence[dict], dec_final_norm, input_embed: dict, output_embed: dict, b: int,
+                 n_patch: int, d: int, nh: int, d_ff: int, eps: float, num_buckets: int = 32, max_distance: int = 128,
+                 keys_all_valid: Optional[bool] = None, hd: int = 64, stream=None) -> int:
+    """The model part of the Chronos-Bolt forecaster (src/chronos_bolt/forecaster.zig:199-213) in one
+    call: input embedding of the [values, mask] patch features, [patches; REG], the T5 encoder with
+    the relative position bias, the one-token decoder with cross-attention, the output head into
+    raw (b, head out). Layers are dicts of BOLT_ENC_FIELDS / BOLT_DEC_FIELDS arrays."""
+    device = _is_device(feats)
+    if keys_all_valid is None:
+        if device:
+            raise ValueError("keys_all_valid is required with device tensors")
+        keys_all_valid = bool(np.asarray(patch_valid).all())
+    ea = (BoltEncLayer * max(1, len(enc_layers)))()
+    for i, ly in enumerate(enc_layers):
+        for f in BOLT_ENC_FIELDS:
+            setattr(ea[i], f, _ptr(ly[f]))
+    da = (BoltDecLayer * max(1, len(dec_layers)))()
+    for i, ly in enumerate(dec_layers):
+        for f in BOLT_DEC_FIELDS:
+            setattr(da[i], f, _ptr(ly[f]))
+    a = BoltForwardArgs(batch=b, n_patch=n_patch, d_model=d, heads=nh, head_dim=hd, d_ff=d_ff,
+                        n_enc_layers=len(enc_layers), n_dec_layers=len(dec_layers),
+                        keys_all_valid=int(bool(keys_all_valid)), rel_buckets=num_buckets,
+                        rel_max_distance=max_distance, eps=eps, flags=DEVICE_PTRS if device else 0, feats=_ptr(feats),
+                        patch_valid=_ptr(patch_valid), reg=_ptr(reg), dec_start=_ptr(dec_start),
+                        rel_table=_ptr(rel_table), enc_layers=ea, enc_final_norm=_ptr(enc_final_norm), dec_layers=da,
+                        dec_final_norm=_ptr(dec_final_norm), input_embed=_resblock(input_embed),
+                        output_embed=_resblock(output_embed), raw=_ptr(raw),
+                        stream=_stream_of(feats, stream) if device else None)
+    return int(load().tsfm_bolt_forward(ctypes.byref(a)))
 
 
 def weight_register(w) -> Optional[int]:
