@@ -232,3 +232,52 @@ def chronos2_encoder(B: int = 64, H: int = 12, n_ctx: int = 512, n_fut: int = 64
                          final_norm=norm()),
                     dict(layers=layers, d_model=d, d_ff=d_ff, n_layers=n_layers, eps=eps, tokens=tokens, flops=flops,
                          bytes=nbytes, seed=seed, num_layers=n_layers))
+
+
+def bolt_forward(B: int = 16, n_patch: int = 32, H: int = 8, d_ff: int = 2048, n_layers: int = 6, quantiles: int = 9,
+                 horizon: int = 64, patch: int = 16, buckets: int = 32, max_distance: int = 128, seed: int = 0,
+                 eps: float = 1e-6) -> Workload:
+    """The Chronos-Bolt-small model forward at the end-to-end configuration: 16 series x 512 context
+    steps = 32 patches of 16 + [REG], d_model 512, 8 heads of 64, d_ff 2048, 6 encoder + 6 decoder
+    layers, 9 quantiles x 64 steps. Random-init weights (linear ~ N(0, 1/in), biases ~ N(0, 0.01),
+    norm scales ~ 1 + N(0, 0.1)); patch features [values ~ N(0, 1), mask] with 2 % of the steps
+    missing. FLOPs: every linear layer (2 rows out in) and the attention products."""
+    rng = np.random.default_rng(seed)
+    d = inner = H * 64
+    seq = n_patch + 1
+    out = quantiles * horizon
+    vals = rng.standard_normal((B * n_patch, patch)).astype(np.float32)
+    mask = (rng.random((B * n_patch, patch)) >= 0.02).astype(np.float32)
+    feats = np.concatenate([vals * mask, mask], axis=1).astype(np.float32)
+    pv = (mask.reshape(B, n_patch, patch).max(axis=2) > 0).astype(np.uint8)
+
+    def lin(o, i):
+        return (rng.standard_normal((o, i), dtype=np.float32) / np.float32(np.sqrt(i))).astype(np.float32)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(d, dtype=np.float32)).astype(np.float32)
+
+    def block(i, h, o):
+        return dict(hidden_w=lin(h, i), hidden_b=(0.1 * rng.standard_normal(h)).astype(np.float32),
+                    output_w=lin(o, h), output_b=(0.1 * rng.standard_normal(o)).astype(np.float32),
+                    residual_w=lin(o, i), residual_b=(0.1 * rng.standard_normal(o)).astype(np.float32))
+
+    enc = [dict(attn_norm=norm(), q=lin(inner, d), k=lin(inner, d), v=lin(inner, d), o=lin(d, inner), ffn_norm=norm(),
+                wi=lin(d_ff, d), wo=lin(d, d_ff)) for _ in range(n_layers)]
+    dec = [dict(self_norm=norm(), self_v=lin(inner, d), self_o=lin(d, inner), cross_norm=norm(), cross_q=lin(inner, d),
+                cross_k=lin(inner, d), cross_v=lin(inner, d), cross_o=lin(d, inner), ffn_norm=norm(), wi=lin(d_ff, d),
+                wo=lin(d, d_ff)) for _ in range(n_layers)]
+    ie, oe = block(2 * patch, d_ff, d), block(d, d_ff, out)
+    rows = B * seq
+    f_enc = n_layers * (2.0 * rows * (4 * d * inner + 2 * d * d_ff) + 4.0 * 64 * H * B * seq * seq)
+    f_dec = n_layers * (2.0 * B * (4 * d * inner + 2 * d * d_ff) + 2.0 * rows * 2 * d * inner + 4.0 * 64 * H * B * seq)
+    f_emb = 2.0 * B * n_patch * (2 * patch * d_ff + d_ff * d + 2 * patch * d) + 2.0 * B * (d * d_ff + d_ff * out + d * out)
+    w_bytes = 4.0 * (sum(a.size for ly in enc + dec for a in ly.values()) + sum(a.size for a in ie.values()) +
+                     sum(a.size for a in oe.values()))
+    return Workload("bolt_small_forward", "f32", B, H, seq, seq, 64, 1.0,
+                    dict(feats=feats, patch_valid=pv, reg=norm(), dec_start=norm(),
+                         rel_table=(0.1 * rng.standard_normal((buckets, H))).astype(np.float32),
+                         enc_final_norm=norm(), dec_final_norm=norm()),
+                    dict(enc=enc, dec=dec, ie=ie, oe=oe, d_model=d, d_ff=d_ff, n_patch=n_patch, out=out, eps=eps,
+                         buckets=buckets, max_distance=max_distance, flops=f_enc + f_dec + f_emb,
+                         bytes=w_bytes + 4.0 * (feats.size + B * out), seed=seed, num_layers=2 * n_layers))
