@@ -62,6 +62,8 @@ struct ProjParams {
     int32_t rope_rows_per_table, rope_row0;
     int32_t tokens, seq, d_in, width, n_out, out_dtype;
     int32_t m_tiles, n_tiles;  // set by launch_proj
+    int32_t splits, split_steps;  // set by launch_proj: reduction split over workgroups (small products)
+    float* partial;               // set by launch_proj: [splits][tokens][width] partial sums
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 

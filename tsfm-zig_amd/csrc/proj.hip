@@ -22,6 +22,8 @@
 // attention path. Three workgroups share a CU (40 KB of LDS and at
 // most 168 registers per lane each), so a wave waiting at its step's barrier or LDS reads leaves
 // the matrix pipe to two others.
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -57,7 +59,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     float* const ws = smem + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int tm, tn;
-    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, tm, tn);
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int split = p.splits > 1 ? logical % p.splits : 0;  // this workgroup's share of the reduction
+    tile_of(p.splits > 1 ? logical / p.splits : logical, p.m_tiles, p.n_tiles, tm, tn);
     const int n_cols = p.width * p.n_out;
 
     // Loader: thread t stages rows t / (BK / 4) + LROWS i, i < LPASS, columns 4 (t % (BK / 4))
@@ -104,12 +108,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int steps = p.d_in / BK;
-    fetch(0);
+    const int t0 = split * p.split_steps;
+    const int steps = p.splits > 1 ? min(p.d_in / BK, t0 + p.split_steps) : p.d_in / BK;
+    fetch(t0 * BK);
     stage(0);
     __syncthreads();
-    for (int t = 0; t < steps; t++) {
-        const int buf = t & 1;
+    for (int t = t0; t < steps; t++) {
+        const int buf = (t - t0) & 1;
         if (t + 1 < steps) fetch((t + 1) * BK);
 #pragma unroll
         for (int kc = 0; kc < BK / 16; kc++) {
@@ -137,6 +142,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // past the width are not stored).
     const int n0 = tn * BN + wn * 64;
     if (n0 >= n_cols) return;
+    if (p.splits > 1) {  // partial sums only; proj_reduce adds them up in split order and finishes
+        const int cq4 = 4 * (lane >> 4);
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) {
+            const int m = tm * BM + wm * 64 + mb * 16 + (lane & 15);
+            if (m >= p.tokens) continue;
+            float* const out = p.partial + ((int64_t)split * p.tokens + m) * p.width + n0 + cq4;
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+                if (n0 + cq4 + 16 * nb < p.width) st4(out + 16 * nb, acc[nb][mb]);
+        }
+        return;
+    }
     const int sel = n0 / p.width, col = n0 - sel * p.width;
     void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
     const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
@@ -183,6 +201,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     }
 }
 
+// Sum of the split partials in split order (deterministic), then the one-output epilogue: alpha,
+// bias, ReLU or residual, f32 store. One thread per four columns of a token.
+__global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
+    const int q = p.width / 4;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)p.tokens * q) return;
+    const int m = (int)(idx / q), c = (int)(idx % q) * 4;
+    f32x4 v = ld4(p.partial + (int64_t)m * p.width + c);
+    for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + m) * p.width + c);
+    if (p.alpha != 1.f) v *= p.alpha;
+    if (p.bias != nullptr) v = v + ld4(p.bias + c);
+    if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
+    else if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + c) + v;
+    st4(static_cast<float*>(p.y0) + (int64_t)m * p.y0_tok + c, v);
+}
+
 }  // namespace
 
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
@@ -196,8 +230,39 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         return hipErrorInvalidValue;
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
-    const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
+    int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
+    // and each workgroup walks the whole reduction; split it over workgroups instead, with the
+    // partial tiles summed in a fixed order by proj_reduce. One output, f32, no RoPE.
+    const int steps = p.d_in / BK;
+    p.splits = 1;
+    p.split_steps = steps;
+    p.partial = nullptr;
+    if (p.n_out == 1 && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 128 && steps >= 16) {
+        int s = (int)std::min<int64_t>((256 + blocks - 1) / blocks, std::min(steps / 8, 16));
+        if (s >= 2) {
+            const int per = (steps + s - 1) / s;
+            s = (steps + per - 1) / per;
+            void* part = nullptr;
+            if (hipMallocAsync(&part, (size_t)s * p.tokens * p.width * sizeof(float), stream) == hipSuccess) {
+                p.splits = s;
+                p.split_steps = per;
+                p.partial = static_cast<float*>(part);
+            }
+        }
+    }
+    if (p.splits > 1) {
+        hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)(blocks * p.splits)), dim3(NT), kProjLds, stream, p);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) {
+            const int64_t n = (int64_t)p.tokens * (p.width / 4);
+            hipLaunchKernelGGL(proj_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
+            e = hipGetLastError();
+        }
+        const hipError_t f = hipFreeAsync(p.partial, stream);
+        return e != hipSuccess ? e : f;
+    }
     if (p.out_dtype == 1)
         hipLaunchKernelGGL(qkv_proj<1>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
     else if (p.out_dtype == 2)
