@@ -346,6 +346,26 @@ typedef struct tsfm_bolt_forward_args {
 
 int tsfm_bolt_forward(const tsfm_bolt_forward_args *args);
 
+/* The whole Chronos-Bolt forecast of a block of series (predictBlock/runChunk,
+ * src/chronos_bolt/forecaster.zig:115-220) on device memory: per series the instance norm over the
+ * observed values (NaN = missing) and the [values, mask] patch features left-padded to whole
+ * patches, the model forward, and the inverse norm. Row s of the context is
+ * ctx[s * stride + offset ..][0..len]; out is (batch, q * P) = (batch, output_embed.out).
+ * model.n_patch must be ceil(len / patch); model.feats, model.patch_valid, model.raw and
+ * model.keys_all_valid are not read (the additive key mask is used: the same weights as FULL when
+ * every patch is observed). Device pointers only (TSFM_ATTN_DEVICE_PTRS in model.flags); host callers keep their
+ * per-series loops around tsfm_bolt_forward. */
+typedef struct tsfm_bolt_forecast_args {
+    tsfm_bolt_forward_args model;
+    const float *ctx; int64_t stride, offset;
+    int32_t len;        /* context steps per series */
+    int32_t patch;      /* input_patch_size; input_embed.in = 2 * patch */
+    float norm_eps;     /* the scale of a series with zero spread (forecaster.zig:18: 1e-5) */
+    float *out;
+} tsfm_bolt_forecast_args;
+
+int tsfm_bolt_forecast(const tsfm_bolt_forecast_args *args);
+
 /* ---------------------------------------------------------------------------------------------
  * The reference backend's GEMM seam, with the signatures of src/platform/cuda/gemm.c so that the
  * reference's own binding (src/platform/cuda/gpu.zig:16-44) can link this library unchanged:

@@ -785,6 +785,73 @@ void orc_bolt_model_forward(size_t threads, float *raw, const float *feats, cons
     free(bias); free(y);
 }
 
+/* The Chronos-Bolt forecaster's runChunk (src/chronos_bolt/forecaster.zig:130-220) for n series:
+ * per series the instance norm over observed values (double sums; a zero scale becomes norm_eps),
+ * the [values, mask] patch features left-padded to whole patches and the patch validity, the
+ * model forward, and out = raw * scale + loc. out: (n, output_embed->out). */
+void orc_bolt_forecast(size_t threads, float *out, const float *ctx, size_t stride, size_t offset, size_t len,
+                       size_t n, size_t ps, float norm_eps, const float *reg, const float *dec_start,
+                       const float *rel_table, uint32_t num_buckets, uint32_t max_distance, size_t d, size_t nh,
+                       size_t hd, size_t d_ff, const orc_bolt_enc_layer *enc, size_t n_enc,
+                       const float *enc_final_norm, const orc_bolt_dec_layer *dec, size_t n_dec,
+                       const float *dec_final_norm, float eps, const orc_resblock *input_embed,
+                       const orc_resblock *output_embed) {
+    const size_t pad = (ps - len % ps) % ps, n_patch = (len + pad) / ps, per = output_embed->out;
+    float *loc = (float *)malloc(n * sizeof(float)), *scale = (float *)malloc(n * sizeof(float));
+    float *feats = (float *)calloc(n * n_patch * 2 * ps + 1, sizeof(float));
+    uint8_t *pv = (uint8_t *)calloc(n * n_patch + 1, 1);
+    for (size_t li = 0; li < n; li++) {
+        const float *row = ctx + li * stride + offset;
+        double count = 0, sum = 0;
+        for (size_t i = 0; i < len; i++)
+            if (!isnan(row[i])) {
+                count += 1;
+                sum += row[i];
+            }
+        float lo = 0, sc = 1;
+        if (count > 0) {
+            lo = (float)(sum / count);
+            double ss = 0;
+            for (size_t i = 0; i < len; i++)
+                if (!isnan(row[i])) {
+                    const float dv = row[i] - lo;
+                    ss += (double)dv * (double)dv;
+                }
+            sc = (float)sqrt(ss / count);
+            if (sc == 0) sc = norm_eps;
+        }
+        loc[li] = lo;
+        scale[li] = sc;
+        for (size_t p = 0; p < n_patch; p++) {
+            int any = 0;
+            float *f = feats + (li * n_patch + p) * 2 * ps;
+            for (size_t i = 0; i < ps; i++) {
+                const long src = (long)(p * ps + i) - (long)pad;
+                int obs = 0;
+                float val = 0;
+                if (src >= 0 && !isnan(row[src])) {
+                    obs = 1;
+                    val = (row[src] - lo) / sc;
+                }
+                f[i] = val;
+                f[ps + i] = obs ? 1.f : 0.f;
+                any = any || obs;
+            }
+            pv[li * n_patch + p] = (uint8_t)any;
+        }
+    }
+    float *raw = (float *)malloc(n * per * sizeof(float));
+    orc_bolt_model_forward(threads, raw, feats, pv, reg, dec_start, rel_table, num_buckets, max_distance, n, n_patch, d,
+                           nh, hd, d_ff, enc, n_enc, enc_final_norm, dec, n_dec, dec_final_norm, eps, input_embed,
+                           output_embed);
+    for (size_t li = 0; li < n; li++)
+        for (size_t j = 0; j < per; j++) {
+            const float t = raw[li * per + j] * scale[li];
+            out[li * per + j] = t + loc[li];
+        }
+    free(loc); free(scale); free(feats); free(pv); free(raw);
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* Timestral (src/timestral/model.zig) */
 

@@ -145,6 +145,14 @@ void orc_bolt_model_forward(size_t threads, float *raw, const float *feats, cons
                             size_t d_ff, const orc_bolt_enc_layer *enc, size_t n_enc, const float *enc_final_norm,
                             const orc_bolt_dec_layer *dec, size_t n_dec, const float *dec_final_norm, float eps,
                             const orc_resblock *input_embed, const orc_resblock *output_embed);
+/* The Chronos-Bolt forecaster's runChunk (src/chronos_bolt/forecaster.zig:130-220). */
+void orc_bolt_forecast(size_t threads, float *out, const float *ctx, size_t stride, size_t offset, size_t len,
+                       size_t n, size_t ps, float norm_eps, const float *reg, const float *dec_start,
+                       const float *rel_table, uint32_t num_buckets, uint32_t max_distance, size_t d, size_t nh,
+                       size_t hd, size_t d_ff, const orc_bolt_enc_layer *enc, size_t n_enc,
+                       const float *enc_final_norm, const orc_bolt_dec_layer *dec, size_t n_dec,
+                       const float *dec_final_norm, float eps, const orc_resblock *input_embed,
+                       const orc_resblock *output_embed);
 void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
                                size_t hd, size_t rope_dim, float theta, const size_t *first_obs);
 /* Timestral TimeJob.rope (src/timestral/model.zig:558-577), in place on the fused qkv buffer. */

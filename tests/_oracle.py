@@ -75,6 +75,10 @@ class Oracle:
         L.orc_rms_norm.argtypes = [_sz, _vp, _vp, _sz, _sz, _vp, _f]
         L.orc_relu.argtypes = [_vp, _sz]
         L.orc_resblock_relu.argtypes = [_sz, _vp, _vp, _sz, ctypes.POINTER(OrcResblock)]
+        L.orc_bolt_forecast.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _f, _vp, _vp, _vp, ctypes.c_uint32,
+                                        ctypes.c_uint32, _sz, _sz, _sz, _sz, ctypes.POINTER(BoltEncLayer), _sz, _vp,
+                                        ctypes.POINTER(BoltDecLayer), _sz, _vp, _f, ctypes.POINTER(OrcResblock),
+                                        ctypes.POINTER(OrcResblock)]
         L.orc_bolt_model_forward.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, _sz,
                                              _sz, _sz, _sz, _sz, _sz, ctypes.POINTER(BoltEncLayer), _sz, _vp,
                                              ctypes.POINTER(BoltDecLayer), _sz, _vp, _f, ctypes.POINTER(OrcResblock),
@@ -172,6 +176,23 @@ class Oracle:
                                         ptr(rel_table), buckets, max_distance, b, n_patch, d, nh, hd, d_ff, ea, len(enc),
                                         ptr(enc_final_norm), da, len(dec), ptr(dec_final_norm), eps, ctypes.byref(ie),
                                         ctypes.byref(oe))
+
+    def bolt_forecast(self, threads, out, ctx, stride, offset, length, n, ps, norm_eps, reg, dec_start, rel_table,
+                      buckets, max_distance, d, nh, hd, d_ff, enc, enc_final_norm, dec, dec_final_norm, eps,
+                      input_embed, output_embed):
+        ea = (BoltEncLayer * max(1, len(enc)))()
+        for i, ly in enumerate(enc):
+            for f in BOLT_ENC_FIELDS:
+                setattr(ea[i], f, ptr(ly[f]))
+        da = (BoltDecLayer * max(1, len(dec)))()
+        for i, ly in enumerate(dec):
+            for f in BOLT_DEC_FIELDS:
+                setattr(da[i], f, ptr(ly[f]))
+        ie, oe = resblock_struct(input_embed), resblock_struct(output_embed)
+        self.lib.orc_bolt_forecast(threads, ptr(out), ptr(ctx), stride, offset, length, n, ps, norm_eps, ptr(reg),
+                                   ptr(dec_start), ptr(rel_table), buckets, max_distance, d, nh, hd, d_ff, ea, len(enc),
+                                   ptr(enc_final_norm), da, len(dec), ptr(dec_final_norm), eps, ctypes.byref(ie),
+                                   ctypes.byref(oe))
 
     def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
         self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)

@@ -37,7 +37,8 @@ def test_library_exports_every_declared_symbol(ta):
                                           ("Resblock", "tsfm_resblock"),
                                           ("Chronos2ForwardArgs", "tsfm_chronos2_forward_args"),
                                           ("BoltEncLayer", "tsfm_bolt_enc_layer"), ("BoltDecLayer", "tsfm_bolt_dec_layer"),
-                                          ("BoltForwardArgs", "tsfm_bolt_forward_args")])
+                                          ("BoltForwardArgs", "tsfm_bolt_forward_args"),
+                                          ("BoltForecastArgs", "tsfm_bolt_forecast_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)
@@ -274,3 +275,17 @@ def test_encode_null_layer_weight_is_invalid(ta):
 def test_encode_empty_is_a_no_op(ta):
     a, _keep = _encode_args(ta, batch=0)
     assert ta.load().tsfm_chronos2_encode(ctypes.byref(a)) == ta.OK
+
+
+def test_bolt_forecast_is_device_only(ta):
+    """The forecast's preparation and inverse norm run on the device: host pointers are refused
+    (before any device work), and a NULL argument block is invalid."""
+    lib = ta.load()
+    assert lib.tsfm_bolt_forecast(None) == ta.E_INVALID
+    ctx = np.zeros(64, np.float32)
+    out = np.zeros(64, np.float32)
+    a = ta.BoltForecastArgs(ctx=ctx.ctypes.data, stride=64, len=64, patch=16, norm_eps=1e-5, out=out.ctypes.data)
+    a.model.batch = 1
+    a.model.n_patch = 4
+    assert lib.tsfm_bolt_forecast(ctypes.byref(a)) == ta.E_UNSUPPORTED
+    assert "device" in ta.last_error()

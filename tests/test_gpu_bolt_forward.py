@@ -10,7 +10,10 @@ output on the matrix cores against the oracle's sixteen lane sums and a tree (th
 is about 2.5 here, at errors of a few 1e-6). The twelve-layer Chronos-Bolt-small shape is held to
 the float64 bar alone. Covered: padded and
 all-valid patches, the Chronos-Bolt-small shape (d 512, 8 heads, d_ff 2048, 32 patches + REG,
-9 quantiles x 64 steps), host and device pointers (same bits).
+9 quantiles x 64 steps), host and device pointers (same bits); the whole forecast
+(src/chronos_bolt/forecaster.zig:128-220: instance norm, left-padded [values, mask] patches, the
+model, the inverse norm) on whole, padded and sub-patch contexts with missing values, strided rows,
+a constant and an all-missing series.
 """
 import numpy as np
 import pytest
@@ -97,3 +100,77 @@ def test_bolt_forward_device_pointers_match_host(ta, orc, gpu_ready):
     assert rc == ta.OK, ta.last_error()
     torch.cuda.synchronize()
     assert np.array_equal(raw.cpu().numpy(), host)
+
+
+# ---- the whole forecast: instance norm and patching on the device, the model, the inverse norm ----
+
+
+def _forecast_ctx(rng, n, length, nan_frac=0.1):
+    ctx = (3.0 + 2.0 * rng.standard_normal((n, length))).astype(np.float32)
+    ctx[rng.random((n, length)) < nan_frac] = np.nan
+    return ctx
+
+
+def _forecast(ta, s, ctx, n, length, nh, d_ff, out_w, stride=None, offset=0):
+    import torch
+
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = torch.full((n, out_w), -9.0, device="cuda")
+    rc = ta.bolt_forecast(out, cu(ctx), length, cu(s["reg"]), cu(s["start"]), cu(s["table"]),
+                          [{k: cu(v) for k, v in ly.items()} for ly in s["enc"]], cu(s["ef"]),
+                          [{k: cu(v) for k, v in ly.items()} for ly in s["dec"]], cu(s["df"]),
+                          {k: cu(v) for k, v in s["ie"].items()}, {k: cu(v) for k, v in s["oe"].items()}, n, s["d"],
+                          nh, d_ff, 1e-6, stride=stride, offset=offset)
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _forecast_oracle(orc, s, ctx, length, n, nh, d_ff, out_w, stride=None, offset=0):
+    want = np.zeros((n, out_w), np.float32)
+    orc.bolt_forecast(THREADS, want, ctx, stride or length, offset, length, n, 16, 1e-5, s["reg"], s["start"],
+                      s["table"], 32, 128, s["d"], nh, 64, d_ff, s["enc"], s["ef"], s["dec"], s["df"], 1e-6, s["ie"],
+                      s["oe"])
+    return want
+
+
+@pytest.mark.parametrize("length", [160, 150, 7])
+def test_bolt_forecast_matches_oracle(ta, orc, gpu_ready, length):
+    """Context lengths that fill whole patches (160), that need left padding (150: 10 missing steps
+    before the first patch) and that are shorter than one patch (7), with ~10 % missing values. The
+    instance norm and patching are exact restatements, so the bar is the model forward's."""
+    nh, d_ff, out_w, n = 2, 256, 48, 5
+    n_patch = (length + 15) // 16
+    s = _setup(60 + length, n, n_patch, nh, d_ff, 2, 2, out_w)
+    ctx = _forecast_ctx(np.random.default_rng(length), n, length)
+    got = _forecast(ta, s, ctx, n, length, nh, d_ff, out_w)
+    want = _forecast_oracle(orc, s, ctx, length, n, nh, d_ff, out_w)
+    assert np.isfinite(got).all()
+    assert _ref.scaled_err(got, want) <= 5e-5
+
+
+def test_bolt_forecast_strided_rows_and_degenerate_series(ta, orc, gpu_ready):
+    """Rows read at a stride and offset from a wider buffer; one series constant (zero spread: the
+    scale becomes norm_eps, so every forecast is the constant plus 1e-5 times the raw output) and one
+    entirely missing (loc 0, scale 1: the forecast is the raw output of all-zero features)."""
+    nh, d_ff, out_w, n, length, stride, offset = 2, 128, 32, 4, 40, 57, 9
+    s = _setup(71, n, 3, nh, d_ff, 1, 1, out_w)
+    rng = np.random.default_rng(3)
+    buf = (1.0 + rng.standard_normal(n * stride + offset)).astype(np.float32)
+    rows = lambda: [buf[i * stride + offset:][:length] for i in range(n)]
+    rows()[1][:] = 4.25
+    rows()[2][:] = np.nan
+    rows()[3][::3] = np.nan
+    got = _forecast(ta, s, buf, n, length, nh, d_ff, out_w, stride=stride, offset=offset)
+    want = _forecast_oracle(orc, s, buf, length, n, nh, d_ff, out_w, stride=stride, offset=offset)
+    assert _ref.scaled_err(got, want) <= 5e-5
+    assert np.abs(got[1] - 4.25).max() < 1e-3
+    # The all-missing series: features are all zero and every context patch is masked, so its
+    # forecast is the model forward of zero features with no valid patch (a batch of one here, so
+    # the products may split their sums differently: the usual bar).
+    feats = np.zeros((3, 32), np.float32)
+    raw = np.zeros((1, out_w), np.float32)
+    rc = ta.bolt_forward(raw, feats, np.zeros((1, 3), np.uint8), s["reg"], s["start"], s["table"], s["enc"], s["ef"],
+                         s["dec"], s["df"], s["ie"], s["oe"], 1, 3, s["d"], nh, d_ff, 1e-6)
+    assert rc == ta.OK, ta.last_error()
+    assert _ref.scaled_err(got[2:3], raw) <= 5e-5

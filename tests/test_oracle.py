@@ -632,3 +632,54 @@ def test_bolt_model_forward_matches_f64(orc):
     bias = orc.position_bias(table, seq, nh, 32, 128)
     want = _ref.bolt_model_forward_f64(feats, pv, reg, start, bias, b, n_patch, nh, enc, ef, dec, df, 1e-6, ie, oe)
     assert _ref.scaled_err(raw, want) < 3e-5
+
+
+def test_bolt_forecast_instance_norm_and_patching(orc):
+    """The forecaster's preparation and inverse norm around the model (src/chronos_bolt/
+    forecaster.zig:150-219), pinned by numpy's nanmean / nanstd (population) for loc and scale, a
+    left pad of (16 - len % 16) % 16 missing steps, [values, mask] features with missing steps 0,
+    and out = raw * scale + loc; plus the special cases: a constant series gets scale norm_eps, an
+    all-missing one loc 0 and scale 1. Strided rows at an offset in a wider buffer."""
+    rng = np.random.default_rng(48)
+    n, length, stride, offset, nh, d_ff, ps, out, norm_eps = 4, 37, 45, 3, 1, 64, 16, 20, 1e-5
+    d = inner = nh * 64
+    buf = (2.0 + 3.0 * rng.standard_normal(n * stride + offset)).astype(np.float32)
+    rows = [buf[i * stride + offset:][:length] for i in range(n)]
+    rows[0][rng.random(length) < 0.3] = np.nan
+    rows[1][:] = -1.5
+    rows[2][:] = np.nan
+    reg, start = (rng.standard_normal(d).astype(np.float32) for _ in range(2))
+    table = _ref.t5_bias_table(rng, 32, nh)
+    enc, dec = _ref.bolt_layers(rng, 1, 1, d, inner, d_ff)
+    ef, df = ((1 + 0.1 * rng.standard_normal(d)).astype(np.float32) for _ in range(2))
+    ie, oe = _ref.resblock(rng, 2 * ps, d_ff, d), _ref.resblock(rng, d, d_ff, out)
+    got = np.zeros((n, out), np.float32)
+    orc.bolt_forecast(2, got, buf, stride, offset, length, n, ps, norm_eps, reg, start, table, 32, 128, d, nh, 64, d_ff,
+                      enc, ef, dec, df, 1e-6, ie, oe)
+
+    pad = (ps - length % ps) % ps
+    n_patch = (length + pad) // ps
+    assert (pad, n_patch) == (11, 3)
+    loc, scale = np.zeros(n, np.float32), np.ones(n, np.float32)
+    feats = np.zeros((n, n_patch, 2 * ps), np.float32)
+    pv = np.zeros((n, n_patch), np.uint8)
+    for i, r in enumerate(rows):
+        obs = ~np.isnan(r)
+        if obs.any():
+            loc[i] = np.float32(np.nanmean(r.astype(np.float64)))
+            scale[i] = np.float32(np.sqrt(np.mean((r[obs] - loc[i]).astype(np.float64) ** 2)))
+            if scale[i] == 0:
+                scale[i] = norm_eps
+        padded = np.concatenate([np.full(pad, np.nan, np.float32), r]).reshape(n_patch, ps)
+        m = ~np.isnan(padded)
+        feats[i, :, :ps] = np.where(m, (np.nan_to_num(padded) - loc[i]) / scale[i], 0)
+        feats[i, :, ps:] = m
+        pv[i] = m.any(axis=1)
+    assert (loc[1], scale[1]) == (np.float32(-1.5), np.float32(norm_eps))
+    assert (loc[2], scale[2]) == (0, 1) and not pv[2].any() and not feats[2].any()
+    assert pv[3].all() and feats[3, 0, ps:ps + pad].sum() == 0  # 11 padded steps, then 5 observed values
+    raw = np.zeros((n, out), np.float32)
+    orc.bolt_model_forward(2, raw, feats.reshape(n * n_patch, 2 * ps), pv, reg, start, table, 32, 128, n, n_patch, d,
+                           nh, 64, d_ff, enc, ef, dec, df, 1e-6, ie, oe)
+    want = raw * scale[:, None] + loc[:, None]
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())

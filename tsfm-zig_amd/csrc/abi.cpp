@@ -1142,6 +1142,54 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
     return TSFM_OK;
 }
 
+int tsfm_bolt_forecast(const tsfm_bolt_forecast_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (!(a->model.flags & TSFM_ATTN_DEVICE_PTRS))
+        return fail(TSFM_E_UNSUPPORTED, "the forecast runs on device memory only; host callers use tsfm_bolt_forward");
+    if (a->len <= 0 || a->patch <= 0 || a->ctx == nullptr || a->out == nullptr || a->stride < 0 || a->offset < 0)
+        return fail(TSFM_E_INVALID, "bad context description");
+    const int32_t pad = (a->patch - a->len % a->patch) % a->patch, n_patch = (a->len + pad) / a->patch;
+    if (a->model.n_patch != n_patch) return fail(TSFM_E_INVALID, "model.n_patch must be ceil(len / patch)");
+    if (a->model.input_embed.in != 2 * a->patch) return fail(TSFM_E_INVALID, "input_embed.in must be 2 * patch");
+    const int64_t nb = a->model.batch;
+    if (nb < 0) return fail(TSFM_E_INVALID, "negative size");
+    if (nb == 0) return TSFM_OK;
+    if (!aligned(a->out, 16)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(a->model.stream);
+    const int64_t per = a->model.output_embed.out;
+    Plan plan;
+    const size_t f_at = plan.take((size_t)(nb * n_patch * 2 * a->patch) * 4), pv_at = plan.take((size_t)(nb * n_patch));
+    const size_t lo_at = plan.take((size_t)nb * 4), sc_at = plan.take((size_t)nb * 4), raw_at = plan.take((size_t)(nb * per) * 4);
+    char* buf = nullptr;
+    hipError_t e;
+    if ((e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off, s)) != hipSuccess)
+        return hip_fail(e, "forecast scratch allocation");
+    float* feats = reinterpret_cast<float*>(buf + f_at);
+    uint8_t* pv = reinterpret_cast<uint8_t*>(buf + pv_at);
+    float* lo = reinterpret_cast<float*>(buf + lo_at);
+    float* sc = reinterpret_cast<float*>(buf + sc_at);
+    float* raw = reinterpret_cast<float*>(buf + raw_at);
+    e = tsfm::launch_bolt_prepare(a->ctx, a->stride, a->offset, a->len, a->patch, n_patch, pad, a->norm_eps, feats, pv, lo,
+                                  sc, (int)nb, s);
+    if (e == hipSuccess) {
+        tsfm_bolt_forward_args m = a->model;
+        m.feats = feats; m.patch_valid = pv; m.raw = raw;
+        m.keys_all_valid = 0;  // validity is only known on the device: the additive mask, exact either way
+        rc = tsfm_bolt_forward(&m);
+        if (rc != TSFM_OK) {
+            (void)hipFreeAsync(buf, s);
+            return rc;
+        }
+        e = tsfm::launch_bolt_finish(raw, lo, sc, a->out, (int)nb, (int)per, s);
+    }
+    const hipError_t f = hipFreeAsync(buf, s);
+    if (e != hipSuccess) return hip_fail(e, "forecast launch");
+    if (f != hipSuccess) return hip_fail(f, "forecast scratch release");
+    return TSFM_OK;
+}
+
 // ---- the reference backend's GEMM seam ------------------------------------------------------------
 
 void* tsfm_weight_register(const float* data, size_t len) {

@@ -71,7 +71,115 @@ __global__ __launch_bounds__(256) void broadcast_rows(const float* v, float* y, 
     for (int i = 4 * lane; i < d; i += 256) st4(y + (int64_t)row * d + i, ld4(v + i));
 }
 
+// Fixed-order sum of one double per thread over a 256-thread workgroup (tree in LDS).
+__device__ double block_sum(double v, double* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+// The Chronos-Bolt forecaster's per-series preparation (src/chronos_bolt/forecaster.zig:150-196),
+// one workgroup per series: the instance norm over the observed (non-NaN) values, with the sums
+// in double as the Zig does (count, sum, then sum of (x - loc)^2 with x - loc in f32; a zero scale
+// becomes norm_eps), then the [values, mask] features of n_patch patches left-padded with pad
+// missing steps, and each patch's "has an observation" byte.
+__global__ __launch_bounds__(256) void bolt_prepare(const float* ctx, int64_t stride, int64_t offset, int len,
+                                                    int ps, int n_patch, int pad, float norm_eps, float* feats,
+                                                    uint8_t* patch_valid, float* loc, float* scale) {
+    __shared__ double red[256];
+    const int li = blockIdx.x, tid = threadIdx.x;
+    const float* row = ctx + (int64_t)li * stride + offset;
+    double cnt = 0.0, sum = 0.0;
+    for (int i = tid; i < len; i += 256) {
+        const float x = row[i];
+        if (!__builtin_isnan(x)) {
+            cnt += 1.0;
+            sum += (double)x;
+        }
+    }
+    cnt = block_sum(cnt, red);
+    sum = block_sum(sum, red);
+    float lo = 0.f, sc = 1.f;
+    if (cnt > 0.0) {
+        lo = (float)(sum / cnt);
+        double ss = 0.0;
+        for (int i = tid; i < len; i += 256) {
+            const float x = row[i];
+            if (!__builtin_isnan(x)) {
+                const float dv = x - lo;
+                ss += (double)dv * (double)dv;
+            }
+        }
+        ss = block_sum(ss, red);
+        sc = (float)__builtin_sqrt(ss / cnt);
+        if (sc == 0.f) sc = norm_eps;
+    }
+    for (int e = tid; e < n_patch * ps; e += 256) {
+        const int pp = e / ps, i = e - pp * ps;
+        const int src = pp * ps + i - pad;
+        float val = 0.f, obs = 0.f;
+        if (src >= 0) {
+            const float x = row[src];
+            if (!__builtin_isnan(x)) {
+                obs = 1.f;
+                val = (x - lo) / sc;
+            }
+        }
+        float* f = feats + ((int64_t)li * n_patch + pp) * 2 * ps;
+        f[i] = val;
+        f[ps + i] = obs;
+    }
+    for (int pp = tid; pp < n_patch; pp += 256) {
+        bool any = false;
+        for (int i = 0; i < ps; i++) {
+            const int src = pp * ps + i - pad;
+            any = any || (src >= 0 && !__builtin_isnan(row[src]));
+        }
+        patch_valid[(int64_t)li * n_patch + pp] = any ? 1 : 0;
+    }
+    if (tid == 0) {
+        loc[li] = lo;
+        scale[li] = sc;
+    }
+}
+
+// The inverse instance norm (src/chronos_bolt/forecaster.zig:215-219): out = raw * scale + loc.
+__global__ __launch_bounds__(256) void bolt_finish(const float* raw, const float* loc, const float* scale, float* out,
+                                                   int n, int per) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)n * per) return;
+    const int li = (int)(idx / per);
+    {
+#pragma clang fp contract(off)
+        out[idx] = raw[idx] * scale[li] + loc[li];  // unfused, like the Zig
+    }
+}
+
 }  // namespace
+
+hipError_t launch_bolt_prepare(const float* ctx, int64_t stride, int64_t offset, int len, int ps, int n_patch, int pad,
+                               float norm_eps, float* feats, uint8_t* patch_valid, float* loc, float* scale, int n,
+                               hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bolt_prepare, dim3((unsigned)n), dim3(256), 0, stream, ctx, stride, offset, len, ps, n_patch, pad,
+                       norm_eps, feats, patch_valid, loc, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_bolt_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int per,
+                              hipStream_t stream) {
+    const int64_t total = (int64_t)n * per;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bolt_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, raw, loc, scale, out, n,
+                       per);
+    return hipGetLastError();
+}
 
 hipError_t launch_broadcast_rows(const float* v, float* y, int rows, int d, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;

@@ -78,5 +78,11 @@ hipError_t launch_assemble_sequence(const float* ctx_emb, const float* fut_emb, 
 hipError_t launch_gather_future(const float* x, float* hidden, int nb, int n_ctx, int n_out, int d,
                                 hipStream_t stream);
 hipError_t launch_broadcast_rows(const float* v, float* y, int rows, int d, hipStream_t stream);
+// Chronos-Bolt forecaster's per-series instance norm + patch features, and the inverse norm (encoder.hip).
+hipError_t launch_bolt_prepare(const float* ctx, int64_t stride, int64_t offset, int len, int ps, int n_patch, int pad,
+                               float norm_eps, float* feats, uint8_t* patch_valid, float* loc, float* scale, int n,
+                               hipStream_t stream);
+hipError_t launch_bolt_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int per,
+                              hipStream_t stream);
 
 }  // namespace tsfm

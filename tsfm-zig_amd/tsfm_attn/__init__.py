@@ -62,6 +62,7 @@ EXPORTS = (
     "tsfm_chronos2_encode",
     "tsfm_chronos2_forward",
     "tsfm_bolt_forward",
+    "tsfm_bolt_forecast",
     "tsfm_weight_register",
     "tsfm_weight_release",
     "tsfm_sgemm_nt",
@@ -305,6 +306,21 @@ class BoltForwardArgs(ctypes.Structure):
     ]
 
 
+class BoltForecastArgs(ctypes.Structure):
+    """``tsfm_bolt_forecast_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("model", BoltForwardArgs),
+        ("ctx", ctypes.c_void_p),
+        ("stride", ctypes.c_int64),
+        ("offset", ctypes.c_int64),
+        ("len", ctypes.c_int32),
+        ("patch", ctypes.c_int32),
+        ("norm_eps", ctypes.c_float),
+        ("out", ctypes.c_void_p),
+    ]
+
+
 class ProjArgs(ctypes.Structure):
     """``tsfm_proj_args`` (include/tsfm_attn.h)."""
 
@@ -393,6 +409,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_chronos2_forward.restype = ctypes.c_int
     lib.tsfm_bolt_forward.argtypes = [ctypes.POINTER(BoltForwardArgs)]
     lib.tsfm_bolt_forward.restype = ctypes.c_int
+    lib.tsfm_bolt_forecast.argtypes = [ctypes.POINTER(BoltForecastArgs)]
+    lib.tsfm_bolt_forecast.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -778,6 +796,15 @@ def bolt_forward(raw, feats, patch_valid, reg, dec_start, rel_table, enc_layers:
         if device:
             raise ValueError("keys_all_valid is required with device tensors")
         keys_all_valid = bool(np.asarray(patch_valid).all())
+    a = _bolt_args(enc_layers, dec_layers, feats, patch_valid, reg, dec_start, rel_table, enc_final_norm, dec_final_norm, input_embed,
+                   output_embed, raw, b, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, keys_all_valid,
+                   device, stream)
+    return int(load().tsfm_bolt_forward(ctypes.byref(a)))
+
+
+def _bolt_args(enc_layers, dec_layers, feats, patch_valid, reg, dec_start, rel_table, enc_final_norm, dec_final_norm, input_embed,
+               output_embed, raw, b, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, keys_all_valid, device,
+               stream):
     ea = (BoltEncLayer * max(1, len(enc_layers)))()
     for i, ly in enumerate(enc_layers):
         for f in BOLT_ENC_FIELDS:
@@ -794,8 +821,28 @@ def bolt_forward(raw, feats, patch_valid, reg, dec_start, rel_table, enc_layers:
                         rel_table=_ptr(rel_table), enc_layers=ea, enc_final_norm=_ptr(enc_final_norm), dec_layers=da,
                         dec_final_norm=_ptr(dec_final_norm), input_embed=_resblock(input_embed),
                         output_embed=_resblock(output_embed), raw=_ptr(raw),
-                        stream=_stream_of(feats, stream) if device else None)
-    return int(load().tsfm_bolt_forward(ctypes.byref(a)))
+                        stream=_stream_of(reg, stream) if device else None)
+    a._keep = (ea, da)
+    return a
+
+
+def bolt_forecast(out, ctx, length: int, reg, dec_start, rel_table, enc_layers: Sequence[dict], enc_final_norm,
+                  dec_layers: Sequence[dict], dec_final_norm, input_embed: dict, output_embed: dict, n: int, d: int,
+                  nh: int, d_ff: int, eps: float, patch: int = 16, stride: Optional[int] = None, offset: int = 0,
+                  norm_eps: float = 1e-5, num_buckets: int = 32, max_distance: int = 128, hd: int = 64,
+                  stream=None) -> int:
+    """The whole Chronos-Bolt forecast of n series on device tensors (predictBlock/runChunk,
+    src/chronos_bolt/forecaster.zig:115-220): row s of the context is ctx[s * stride + offset:][:length]
+    (NaN = missing); out (n, q * P) receives the quantile forecasts in data units."""
+    if not _is_device(ctx):
+        raise ValueError("bolt_forecast runs on device tensors; host callers use bolt_forward")
+    n_patch = (length + patch - 1) // patch
+    m = _bolt_args(enc_layers, dec_layers, None, None, reg, dec_start, rel_table, enc_final_norm, dec_final_norm,
+                   input_embed, output_embed, None, n, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, False,
+                   True, stream)
+    a = BoltForecastArgs(model=m, ctx=_ptr(ctx), stride=length if stride is None else stride, offset=offset,
+                         len=length, patch=patch, norm_eps=norm_eps, out=_ptr(out))
+    return int(load().tsfm_bolt_forecast(ctypes.byref(a)))
 
 
 def weight_register(w) -> Optional[int]:
