@@ -300,6 +300,29 @@ typedef struct tsfm_chronos2_forward_args {
 
 int tsfm_chronos2_forward(const tsfm_chronos2_forward_args *args);
 
+/* The whole Chronos-2 forecast of a block of series (runChunk, src/chronos2/forecaster.zig:59-204)
+ * on device memory: per series the instance norm over the observed values (NaN = missing; a
+ * zero scale becomes 1e-5), the [time_enc, values, mask] features of the context patches
+ * (left-padded to whole patches, values optionally asinh'd) and of the future patches, the model
+ * forward, and the inverse scaling into out (batch, horizon, q) in the model's quantile order.
+ * Row s of the inputs is inputs[s * stride + start ..][0..len] (forecast() passes stride = t_in
+ * and start = t_in - len after truncating to context_length, :27-36). patch = input_embed.in / 3;
+ * q = output_embed.out / patch; model.n_ctx must be ceil(len / patch) and model.n_out
+ * ceil(horizon / patch). model.feats, fut_feats, ctx_valid, raw and enc.keys_all_valid are not read
+ * (the additive key mask is used). Device pointers only (TSFM_ATTN_DEVICE_PTRS in model.enc.flags);
+ * host callers keep their per-series loops around tsfm_chronos2_forward. */
+typedef struct tsfm_chronos2_forecast_args {
+    tsfm_chronos2_forward_args model;
+    const float *inputs; int64_t stride, start;
+    int32_t len;        /* context steps per series */
+    int32_t horizon;    /* forecast steps, 1 .. n_out * patch */
+    float time_scale;   /* chronos_config.time_encoding_scale */
+    int32_t arcsinh;    /* chronos_config.use_arcsinh */
+    float *out;         /* (batch, horizon, q) */
+} tsfm_chronos2_forecast_args;
+
+int tsfm_chronos2_forecast(const tsfm_chronos2_forecast_args *args);
+
 /* ---------------------------------------------------------------------------------------------
  * Chronos-Bolt model forward: the model part of the forecaster's chunk
  * (src/chronos_bolt/forecaster.zig:199-213) in one call:

@@ -852,6 +852,84 @@ void orc_bolt_forecast(size_t threads, float *out, const float *ctx, size_t stri
     free(loc); free(scale); free(feats); free(pv); free(raw);
 }
 
+/* src/chronos2/forecaster.zig:59-204 (runChunk) for the series of one chunk. */
+void orc_chronos2_forecast(size_t threads, float *out, const float *inputs, size_t stride, size_t start, size_t len,
+                           size_t n, size_t ps, size_t horizon, float time_scale, int arcsinh, const float *reg,
+                           size_t d, size_t nh, size_t hd, size_t d_ff, size_t n_layers,
+                           const orc_chronos2_layer *layers, const float *final_norm, float eps, const float *cos_t,
+                           const float *sin_t, float scale, const orc_resblock *input_embed,
+                           const orc_resblock *output_embed) {
+    const size_t pad = (ps - len % ps) % ps, n_ctx = (len + pad) / ps, n_out = (horizon + ps - 1) / ps;
+    const size_t q = output_embed->out / ps;
+    float *loc = (float *)malloc((n + 1) * sizeof(float)), *scl = (float *)malloc((n + 1) * sizeof(float));
+    float *feats = (float *)calloc(n * n_ctx * 3 * ps + 1, sizeof(float));
+    float *fut = (float *)calloc(n * n_out * 3 * ps + 1, sizeof(float));
+    uint8_t *cv = (uint8_t *)calloc(n * n_ctx + 1, 1);
+    for (size_t li = 0; li < n; li++) {
+        const float *row = inputs + li * stride + start;
+        double count = 0, sum = 0;
+        for (size_t i = 0; i < len; i++)
+            if (!isnan(row[i])) {
+                count += 1;
+                sum += row[i];
+            }
+        float lo = 0, sc = 1;
+        if (count > 0) {
+            lo = (float)(sum / count);
+            double ss = 0;
+            for (size_t i = 0; i < len; i++)
+                if (!isnan(row[i])) {
+                    const float dv = row[i] - lo;
+                    ss += (double)dv * (double)dv;
+                }
+            sc = (float)sqrt(ss / count);
+            if (sc == 0) sc = 1e-5f;
+        }
+        loc[li] = lo;
+        scl[li] = sc;
+        for (size_t p = 0; p < n_ctx; p++) {
+            int any = 0;
+            float *f = feats + (li * n_ctx + p) * 3 * ps;
+            for (size_t i = 0; i < ps; i++) {
+                const size_t j = p * ps + i;
+                const long src = (long)j - (long)pad;
+                int obs = 0;
+                float val = 0;
+                if (src >= 0 && src < (long)len && !isnan(row[src])) {
+                    obs = 1;
+                    val = (row[src] - lo) / sc;
+                    if (arcsinh) val = asinhf(val);
+                }
+                f[i] = ((float)j - (float)(n_ctx * ps)) / time_scale;
+                f[ps + i] = val;
+                f[2 * ps + i] = obs ? 1.f : 0.f;
+                any = any || obs;
+            }
+            cv[li * n_ctx + p] = (uint8_t)any;
+        }
+        for (size_t p = 0; p < n_out; p++) {
+            float *f = fut + (li * n_out + p) * 3 * ps;
+            for (size_t i = 0; i < ps; i++) f[i] = (float)(p * ps + i) / time_scale;
+        }
+    }
+    float *raw = (float *)malloc((n * n_out * q * ps + 1) * sizeof(float));
+    orc_chronos2_model_forward(threads, raw, feats, fut, cv, reg, n, n_ctx, n_out, d, nh, hd, d_ff, n_layers, layers,
+                               final_norm, eps, cos_t, sin_t, scale, input_embed, output_embed);
+    for (size_t li = 0; li < n; li++)
+        for (size_t p = 0; p < n_out; p++)
+            for (size_t i = 0; i < ps; i++) {
+                const size_t step = p * ps + i;
+                if (step >= horizon) continue;
+                for (size_t qi = 0; qi < q; qi++) {
+                    float v = raw[(li * n_out + p) * q * ps + qi * ps + i];
+                    if (arcsinh) v = sinhf(v);
+                    const float t = v * scl[li];
+                    out[(li * horizon + step) * q + qi] = t + loc[li];
+                }
+            }
+    free(loc); free(scl); free(feats); free(fut); free(cv); free(raw);
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* Timestral (src/timestral/model.zig) */
 

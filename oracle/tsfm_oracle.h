@@ -130,6 +130,15 @@ void orc_chronos2_model_forward(size_t threads, float *raw, const float *feats, 
                                 const orc_chronos2_layer *layers, const float *final_norm, float eps,
                                 const float *cos_t, const float *sin_t, float scale, const orc_resblock *input_embed,
                                 const orc_resblock *output_embed);
+/* The Chronos-2 forecaster's runChunk (src/chronos2/forecaster.zig:59-204) around
+ * orc_chronos2_model_forward: instance norm, [time_enc, values, mask] patch features, the model,
+ * inverse scaling into out (n, horizon, q). Row s is inputs[s * stride + start ..][0..len]. */
+void orc_chronos2_forecast(size_t threads, float *out, const float *inputs, size_t stride, size_t start, size_t len,
+                           size_t n, size_t ps, size_t horizon, float time_scale, int arcsinh, const float *reg,
+                           size_t d, size_t nh, size_t hd, size_t d_ff, size_t n_layers,
+                           const orc_chronos2_layer *layers, const float *final_norm, float eps, const float *cos_t,
+                           const float *sin_t, float scale, const orc_resblock *input_embed,
+                           const orc_resblock *output_embed);
 /* Chronos-Bolt layer weights (src/chronos_bolt/model.zig:12-55), nn.Weight (out, in) layout. */
 typedef struct orc_bolt_enc_layer {
     const float *attn_norm, *q, *k, *v, *o, *ffn_norm, *wi, *wo;

@@ -86,6 +86,9 @@ class Oracle:
         L.orc_chronos2_model_forward.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz,
                                                  ctypes.POINTER(Chronos2Layer), _vp, _f, _vp, _vp, _f,
                                                  ctypes.POINTER(OrcResblock), ctypes.POINTER(OrcResblock)]
+        L.orc_chronos2_forecast.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _f, ctypes.c_int, _vp, _sz,
+                                            _sz, _sz, _sz, _sz, ctypes.POINTER(Chronos2Layer), _vp, _f, _vp, _vp, _f,
+                                            ctypes.POINTER(OrcResblock), ctypes.POINTER(OrcResblock)]
         L.orc_chronos2_encode.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, ctypes.POINTER(Chronos2Layer),
                                           _vp, _f, _vp, _vp, _f]
         L.orc_softmax.argtypes = [_vp, _sz]
@@ -159,6 +162,18 @@ class Oracle:
         self.lib.orc_chronos2_model_forward(threads, ptr(raw), ptr(feats), ptr(fut_feats), ptr(ctx_valid), ptr(reg), b,
                                             n_ctx, n_out, d, nh, hd, d_ff, len(layers), arr, ptr(final_norm), eps,
                                             ptr(cos_t), ptr(sin_t), scale, ctypes.byref(ie), ctypes.byref(oe))
+
+    def chronos2_forecast(self, threads, out, inputs, stride, start, length, n, ps, horizon, time_scale, arcsinh, reg,
+                          d, nh, hd, d_ff, layers, final_norm, eps, cos_t, sin_t, scale, input_embed, output_embed):
+        arr = (Chronos2Layer * max(1, len(layers)))()
+        for i, ly in enumerate(layers):
+            for f in LAYER_FIELDS:
+                setattr(arr[i], f, ptr(ly[f]))
+        ie, oe = resblock_struct(input_embed), resblock_struct(output_embed)
+        self.lib.orc_chronos2_forecast(threads, ptr(out), ptr(inputs), stride, start, length, n, ps, horizon,
+                                       time_scale, int(bool(arcsinh)), ptr(reg), d, nh, hd, d_ff, len(layers), arr,
+                                       ptr(final_norm), eps, ptr(cos_t), ptr(sin_t), scale, ctypes.byref(ie),
+                                       ctypes.byref(oe))
 
     def bolt_model_forward(self, threads, raw, feats, patch_valid, reg, dec_start, rel_table, buckets, max_distance,
                            b, n_patch, d, nh, hd, d_ff, enc, enc_final_norm, dec, dec_final_norm, eps, input_embed,

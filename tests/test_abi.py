@@ -38,7 +38,8 @@ def test_library_exports_every_declared_symbol(ta):
                                           ("Chronos2ForwardArgs", "tsfm_chronos2_forward_args"),
                                           ("BoltEncLayer", "tsfm_bolt_enc_layer"), ("BoltDecLayer", "tsfm_bolt_dec_layer"),
                                           ("BoltForwardArgs", "tsfm_bolt_forward_args"),
-                                          ("BoltForecastArgs", "tsfm_bolt_forecast_args")])
+                                          ("BoltForecastArgs", "tsfm_bolt_forecast_args"),
+                                          ("Chronos2ForecastArgs", "tsfm_chronos2_forecast_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)
@@ -288,4 +289,15 @@ def test_bolt_forecast_is_device_only(ta):
     a.model.batch = 1
     a.model.n_patch = 4
     assert lib.tsfm_bolt_forecast(ctypes.byref(a)) == ta.E_UNSUPPORTED
+    assert "device" in ta.last_error()
+
+
+def test_chronos2_forecast_is_device_only(ta):
+    lib = ta.load()
+    assert lib.tsfm_chronos2_forecast(None) == ta.E_INVALID
+    x = np.zeros(64, np.float32)
+    a = ta.Chronos2ForecastArgs(inputs=x.ctypes.data, stride=64, len=64, horizon=16, time_scale=1.0,
+                                out=x.ctypes.data)
+    a.model.enc.batch = 1
+    assert lib.tsfm_chronos2_forecast(ctypes.byref(a)) == ta.E_UNSUPPORTED
     assert "device" in ta.last_error()

@@ -11,7 +11,10 @@ twice the oracle's own distance (plus 1e-6). Covered: scale 1/8 and the model's 
 all-valid keys (FULL and KEYS_ADDITIVE masks give the same result when every key is valid), no
 layers (final norm only), host and device pointers (same bits), a Chronos-2-base shaped run
 (d 768, 12 heads, d_ff 3072, 577 tokens), and twelve layers, where the bar against float64 is 4x
-the oracle's own drift.
+the oracle's own drift. The whole forecast (tsfm_chronos2_forecast: instance norm, time-encoded
+patch features, the model, inverse scaling) against the oracle's runChunk on whole, padded and
+sub-patch contexts, cut horizons, asinh space on and off, strided rows, a constant and an
+all-missing series.
 """
 import numpy as np
 import pytest
@@ -172,3 +175,73 @@ def test_forward_device_pointers_match_host(ta, orc, gpu_ready):
     assert rc == ta.OK, ta.last_error()
     torch.cuda.synchronize()
     assert np.array_equal(raw.cpu().numpy(), host)
+
+
+# ---- the whole Chronos-2 forecast: preparation and inverse scaling on the device around the model -
+
+
+def _forecast_case(orc, seed, length, horizon, nh=2, d_ff=256, n_layers=2, ps=16, q=3):
+    rng = np.random.default_rng(seed)
+    d = nh * 64
+    reg = rng.standard_normal(d).astype(np.float32)
+    layers = _ref.chronos2_layers(rng, n_layers, d, d_ff)
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    ie, oe = _ref.resblock(rng, 3 * ps, d_ff, d), _ref.resblock(rng, d, d_ff, q * ps)
+    n_ctx, n_out = (length + ps - 1) // ps, (horizon + ps - 1) // ps
+    cos_t, sin_t = orc.chronos2_rope_tables(n_ctx + 1 + n_out, 64, 10000.0)
+    return dict(reg=reg, layers=layers, fn=fn, ie=ie, oe=oe, d=d, cos=cos_t, sin=sin_t, q=q)
+
+
+def _c2_forecast(ta, c, inputs, n, length, horizon, nh, d_ff, arcsinh, tsc, stride=None, start=0):
+    import torch
+
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = torch.full((n, horizon, c["q"]), -9.0, device="cuda")
+    rc = ta.chronos2_forecast(out, cu(inputs), length, horizon, cu(c["reg"]), cu(c["cos"]), cu(c["sin"]),
+                              [{k: cu(v) for k, v in ly.items()} for ly in c["layers"]], cu(c["fn"]),
+                              {k: cu(v) for k, v in c["ie"].items()}, {k: cu(v) for k, v in c["oe"].items()}, n,
+                              c["d"], nh, d_ff, 1e-6, stride=stride, start=start, time_scale=tsc, arcsinh=arcsinh)
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _c2_forecast_oracle(orc, c, inputs, n, length, horizon, nh, d_ff, arcsinh, tsc, stride=None, start=0):
+    want = np.zeros((n, horizon, c["q"]), np.float32)
+    orc.chronos2_forecast(THREADS, want, inputs, stride or length, start, length, n, 16, horizon, tsc, arcsinh,
+                          c["reg"], c["d"], nh, 64, d_ff, c["layers"], c["fn"], 1e-6, c["cos"], c["sin"], 1.0, c["ie"],
+                          c["oe"])
+    return want
+
+
+@pytest.mark.parametrize("length,horizon,arcsinh", [(160, 64, True), (150, 20, True), (9, 16, False)])
+def test_chronos2_forecast_matches_oracle(ta, orc, gpu_ready, length, horizon, arcsinh):
+    """Whole patches (160), left padding (150) and less than one patch (9); horizons that fill and
+    that cut the last future patch; the model's asinh space on and off; ~10 % missing values."""
+    nh, d_ff, n, tsc = 2, 256, 4, 8192.0
+    c = _forecast_case(orc, length + horizon, length, horizon, nh, d_ff)
+    rng = np.random.default_rng(length)
+    x = (5.0 + 3.0 * rng.standard_normal((n, length))).astype(np.float32)
+    x[rng.random((n, length)) < 0.1] = np.nan
+    got = _c2_forecast(ta, c, x, n, length, horizon, nh, d_ff, arcsinh, tsc)
+    want = _c2_forecast_oracle(orc, c, x, n, length, horizon, nh, d_ff, arcsinh, tsc)
+    assert np.isfinite(got).all()
+    assert _ref.scaled_err(got, want) <= 5e-5
+
+
+def test_chronos2_forecast_strided_rows_and_degenerate_series(ta, orc, gpu_ready):
+    """Rows at a stride and start offset in a wider buffer (as forecast() reads the last
+    context_length steps of each (b, t_in) row); a constant series (scale 1e-5) and an all-missing
+    one (loc 0, scale 1, no valid context patch: only REG and the future patches are attended)."""
+    nh, d_ff, n, length, horizon, stride, start, tsc = 2, 128, 4, 48, 30, 70, 22, 8192.0
+    c = _forecast_case(orc, 5, length, horizon, nh, d_ff, n_layers=1)
+    rng = np.random.default_rng(11)
+    buf = (1.0 + rng.standard_normal(n * stride)).astype(np.float32)
+    rows = lambda: [buf[i * stride + start:][:length] for i in range(n)]
+    rows()[1][:] = -3.5
+    rows()[2][:] = np.nan
+    rows()[3][1::4] = np.nan
+    got = _c2_forecast(ta, c, buf, n, length, horizon, nh, d_ff, True, tsc, stride=stride, start=start)
+    want = _c2_forecast_oracle(orc, c, buf, n, length, horizon, nh, d_ff, True, tsc, stride=stride, start=start)
+    assert np.isfinite(got).all()
+    assert _ref.scaled_err(got, want) <= 5e-5

@@ -683,3 +683,64 @@ def test_bolt_forecast_instance_norm_and_patching(orc):
                            nh, 64, d_ff, enc, ef, dec, df, 1e-6, ie, oe)
     want = raw * scale[:, None] + loc[:, None]
     assert np.allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("arcsinh", [False, True])
+def test_chronos2_forecast_preparation_and_inverse_scaling(orc, arcsinh):
+    """runChunk around the model (src/chronos2/forecaster.zig:93-201), pinned by numpy: loc and
+    scale are nanmean and the population nanstd (zero spread -> 1e-5, nothing observed -> 0 and 1),
+    the context is left-padded by (16 - len % 16) % 16 missing steps, the time encodings are
+    (j - n_ctx * 16) / time_scale and j / time_scale, values optionally go through arcsinh, and the
+    (n * n_out, q * 16) raw head output is transposed to (n, horizon, q), through sinh, and
+    scaled back. Strided rows at a start offset; horizon not a multiple of the patch."""
+    rng = np.random.default_rng(49)
+    n, length, stride, start, nh, d_ff, ps, q, horizon, tsc = 4, 41, 50, 6, 1, 64, 16, 3, 21, 512.0
+    d = nh * 64
+    buf = (2.0 + 3.0 * rng.standard_normal(n * stride + start)).astype(np.float32)
+    rows = [buf[i * stride + start:][:length] for i in range(n)]
+    rows[0][rng.random(length) < 0.3] = np.nan
+    rows[1][:] = 7.0
+    rows[2][:] = np.nan
+    reg = rng.standard_normal(d).astype(np.float32)
+    layers = _ref.chronos2_layers(rng, 1, d, d_ff)
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    ie, oe = _ref.resblock(rng, 3 * ps, d_ff, d), _ref.resblock(rng, d, d_ff, q * ps)
+    pad = (ps - length % ps) % ps
+    n_ctx, n_out = (length + pad) // ps, (horizon + ps - 1) // ps
+    assert (pad, n_ctx, n_out) == (7, 3, 2)
+    cos_t, sin_t = orc.chronos2_rope_tables(n_ctx + 1 + n_out, 64, 10000.0)
+    got = np.zeros((n, horizon, q), np.float32)
+    orc.chronos2_forecast(2, got, buf, stride, start, length, n, ps, horizon, tsc, arcsinh, reg, d, nh, 64, d_ff,
+                          layers, fn, 1e-6, cos_t, sin_t, 1.0, ie, oe)
+
+    loc, scale = np.zeros(n, np.float32), np.ones(n, np.float32)
+    feats = np.zeros((n, n_ctx, 3 * ps), np.float32)
+    fut = np.zeros((n, n_out, 3 * ps), np.float32)
+    cv = np.zeros((n, n_ctx), np.uint8)
+    j = np.arange(n_ctx * ps, dtype=np.float32).reshape(n_ctx, ps)
+    for i, r in enumerate(rows):
+        obs = ~np.isnan(r)
+        if obs.any():
+            loc[i] = np.float32(np.nanmean(r.astype(np.float64)))
+            scale[i] = np.float32(np.sqrt(np.mean((r[obs] - loc[i]).astype(np.float64) ** 2)))
+            if scale[i] == 0:
+                scale[i] = 1e-5
+        padded = np.concatenate([np.full(pad, np.nan, np.float32), r]).reshape(n_ctx, ps)
+        m = ~np.isnan(padded)
+        val = np.where(m, (np.nan_to_num(padded) - loc[i]) / scale[i], 0).astype(np.float32)
+        feats[i, :, :ps] = (j - np.float32(n_ctx * ps)) / np.float32(tsc)
+        feats[i, :, ps:2 * ps] = np.arcsinh(val) if arcsinh else val
+        feats[i, :, 2 * ps:] = m
+        cv[i] = m.any(axis=1)
+        fut[i, :, :ps] = np.arange(n_out * ps, dtype=np.float32).reshape(n_out, ps) / np.float32(tsc)
+    assert (loc[1], scale[1]) == (7, np.float32(1e-5)) and (loc[2], scale[2]) == (0, 1) and not cv[2].any()
+    raw = np.zeros((n * n_out, q * ps), np.float32)
+    orc.chronos2_model_forward(2, raw, feats.reshape(-1, 3 * ps), fut.reshape(-1, 3 * ps), cv, reg, n, n_ctx, n_out,
+                               d, nh, 64, d_ff, layers, fn, 1e-6, cos_t, sin_t, 1.0, ie, oe)
+    r = raw.reshape(n, n_out, q, ps).transpose(0, 1, 3, 2).reshape(n, n_out * ps, q)[:, :horizon]
+    if arcsinh:
+        r = np.sinh(r.astype(np.float64))
+    want = r * scale[:, None, None] + loc[:, None, None]
+    # arcsinh / sinh: libm's single-precision functions against numpy's double ones (an ulp or two).
+    tol = 2e-6 if arcsinh else 1e-6
+    assert np.allclose(got, want, rtol=tol, atol=tol * np.abs(want).max())

@@ -1190,6 +1190,61 @@ int tsfm_bolt_forecast(const tsfm_bolt_forecast_args* a) {
     return TSFM_OK;
 }
 
+int tsfm_chronos2_forecast(const tsfm_chronos2_forecast_args* a) {
+    if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
+    if (!(a->model.enc.flags & TSFM_ATTN_DEVICE_PTRS))
+        return fail(TSFM_E_UNSUPPORTED,
+                    "the forecast runs on device memory only; host callers use tsfm_chronos2_forward");
+    const int32_t ps = a->model.input_embed.in / 3;
+    if (ps <= 0 || a->model.input_embed.in != 3 * ps) return fail(TSFM_E_INVALID, "input_embed.in must be 3 * patch");
+    if (a->len <= 0 || a->horizon <= 0 || a->inputs == nullptr || a->out == nullptr || a->stride < 0 || a->start < 0 ||
+        !(a->time_scale != 0.f))
+        return fail(TSFM_E_INVALID, "bad context description");
+    const int32_t pad = (ps - a->len % ps) % ps, n_ctx = (a->len + pad) / ps, n_out = (a->horizon + ps - 1) / ps;
+    if (a->model.n_ctx != n_ctx) return fail(TSFM_E_INVALID, "model.n_ctx must be ceil(len / patch)");
+    if (a->model.n_out != n_out) return fail(TSFM_E_INVALID, "model.n_out must be ceil(horizon / patch)");
+    const int32_t per = a->model.output_embed.out;
+    if (per <= 0 || per % ps) return fail(TSFM_E_INVALID, "output_embed.out must be q * patch");
+    const int64_t nb = a->model.enc.batch;
+    if (nb < 0) return fail(TSFM_E_INVALID, "negative size");
+    if (nb == 0) return TSFM_OK;
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(a->model.enc.stream);
+    Plan plan;
+    const size_t f_at = plan.take((size_t)(nb * n_ctx * 3 * ps) * 4), ff_at = plan.take((size_t)(nb * n_out * 3 * ps) * 4);
+    const size_t cv_at = plan.take((size_t)(nb * n_ctx)), lo_at = plan.take((size_t)nb * 4);
+    const size_t sc_at = plan.take((size_t)nb * 4), raw_at = plan.take((size_t)(nb * n_out * per) * 4);
+    char* buf = nullptr;
+    hipError_t e;
+    if ((e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off, s)) != hipSuccess)
+        return hip_fail(e, "forecast scratch allocation");
+    float* feats = reinterpret_cast<float*>(buf + f_at);
+    float* fut = reinterpret_cast<float*>(buf + ff_at);
+    uint8_t* cv = reinterpret_cast<uint8_t*>(buf + cv_at);
+    float* lo = reinterpret_cast<float*>(buf + lo_at);
+    float* sc = reinterpret_cast<float*>(buf + sc_at);
+    float* raw = reinterpret_cast<float*>(buf + raw_at);
+    e = tsfm::launch_chronos2_prepare(a->inputs, a->stride, a->start, a->len, ps, n_ctx, n_out, pad, a->time_scale,
+                                      a->arcsinh ? 1 : 0, feats, fut, cv, lo, sc, (int)nb, s);
+    if (e == hipSuccess) {
+        tsfm_chronos2_forward_args m = a->model;
+        m.feats = feats; m.fut_feats = fut; m.ctx_valid = cv; m.raw = raw;
+        m.enc.keys_all_valid = 0;  // validity is only known on the device: the additive mask, exact either way
+        rc = tsfm_chronos2_forward(&m);
+        if (rc != TSFM_OK) {
+            (void)hipFreeAsync(buf, s);
+            return rc;
+        }
+        e = tsfm::launch_chronos2_finish(raw, lo, sc, a->out, (int)nb, n_out, per / ps, ps, a->horizon,
+                                         a->arcsinh ? 1 : 0, s);
+    }
+    const hipError_t f = hipFreeAsync(buf, s);
+    if (e != hipSuccess) return hip_fail(e, "forecast launch");
+    if (f != hipSuccess) return hip_fail(f, "forecast scratch release");
+    return TSFM_OK;
+}
+
 // ---- the reference backend's GEMM seam ------------------------------------------------------------
 
 void* tsfm_weight_register(const float* data, size_t len) {

@@ -84,17 +84,13 @@ __device__ double block_sum(double v, double* red) {
     return r;
 }
 
-// The Chronos-Bolt forecaster's per-series preparation (src/chronos_bolt/forecaster.zig:150-196),
-// one workgroup per series: the instance norm over the observed (non-NaN) values, with the sums
-// in double as the Zig does (count, sum, then sum of (x - loc)^2 with x - loc in f32; a zero scale
-// becomes norm_eps), then the [values, mask] features of n_patch patches left-padded with pad
-// missing steps, and each patch's "has an observation" byte.
-__global__ __launch_bounds__(256) void bolt_prepare(const float* ctx, int64_t stride, int64_t offset, int len,
-                                                    int ps, int n_patch, int pad, float norm_eps, float* feats,
-                                                    uint8_t* patch_valid, float* loc, float* scale) {
-    __shared__ double red[256];
-    const int li = blockIdx.x, tid = threadIdx.x;
-    const float* row = ctx + (int64_t)li * stride + offset;
+// The forecasters' instance norm over one series' observed (non-NaN) values
+// (src/chronos_bolt/forecaster.zig:153-172, src/chronos2/forecaster.zig:97-116), for a whole
+// 256-thread workgroup: count, sum and then the sum of (x - loc)^2 with x - loc in f32 are kept
+// in double as the Zig does; loc = f32(sum / count), scale = f32(sqrt(ss / count)), and a zero
+// scale becomes norm_eps. No observation: loc 0, scale 1.
+__device__ void instance_norm(const float* row, int len, float norm_eps, double* red, float& lo, float& sc) {
+    const int tid = threadIdx.x;
     double cnt = 0.0, sum = 0.0;
     for (int i = tid; i < len; i += 256) {
         const float x = row[i];
@@ -105,7 +101,8 @@ __global__ __launch_bounds__(256) void bolt_prepare(const float* ctx, int64_t st
     }
     cnt = block_sum(cnt, red);
     sum = block_sum(sum, red);
-    float lo = 0.f, sc = 1.f;
+    lo = 0.f;
+    sc = 1.f;
     if (cnt > 0.0) {
         lo = (float)(sum / cnt);
         double ss = 0.0;
@@ -120,6 +117,19 @@ __global__ __launch_bounds__(256) void bolt_prepare(const float* ctx, int64_t st
         sc = (float)__builtin_sqrt(ss / cnt);
         if (sc == 0.f) sc = norm_eps;
     }
+}
+
+// The Chronos-Bolt forecaster's per-series preparation (src/chronos_bolt/forecaster.zig:150-196),
+// one workgroup per series: the instance norm, then the [values, mask] features of n_patch
+// patches left-padded with pad missing steps, and each patch's "has an observation" byte.
+__global__ __launch_bounds__(256) void bolt_prepare(const float* ctx, int64_t stride, int64_t offset, int len,
+                                                    int ps, int n_patch, int pad, float norm_eps, float* feats,
+                                                    uint8_t* patch_valid, float* loc, float* scale) {
+    __shared__ double red[256];
+    const int li = blockIdx.x, tid = threadIdx.x;
+    const float* row = ctx + (int64_t)li * stride + offset;
+    float lo, sc;
+    instance_norm(row, len, norm_eps, red, lo, sc);
     for (int e = tid; e < n_patch * ps; e += 256) {
         const int pp = e / ps, i = e - pp * ps;
         const int src = pp * ps + i - pad;
@@ -149,6 +159,79 @@ __global__ __launch_bounds__(256) void bolt_prepare(const float* ctx, int64_t st
     }
 }
 
+// The Chronos-2 forecaster's per-series preparation (src/chronos2/forecaster.zig:93-153), one
+// workgroup per series: the instance norm (zero scale -> 1e-5), then the [time_enc, values, mask]
+// features of n_ctx context patches (left-padded with pad missing steps; values optionally
+// asinh'd) with their "has an observation" byte, and of n_out future patches, which carry only
+// their time encoding. Time encodings are (j - n_ctx * ps) / tscale and j / tscale in f32.
+__global__ __launch_bounds__(256) void chronos2_prepare(const float* inputs, int64_t stride, int64_t start, int len,
+                                                        int ps, int n_ctx, int n_out, int pad, float tscale,
+                                                        int arcsinh, float* feats, float* fut_feats,
+                                                        uint8_t* ctx_valid, float* loc, float* scale) {
+    __shared__ double red[256];
+    const int li = blockIdx.x, tid = threadIdx.x;
+    const float* row = inputs + (int64_t)li * stride + start;
+    float lo, sc;
+    instance_norm(row, len, 1e-5f, red, lo, sc);
+    const float origin = (float)(n_ctx * ps);
+    for (int e = tid; e < n_ctx * ps; e += 256) {
+        const int pp = e / ps, i = e - pp * ps;
+        const int src = e - pad;
+        float val = 0.f, obs = 0.f;
+        if (src >= 0 && src < len) {
+            const float x = row[src];
+            if (!__builtin_isnan(x)) {
+                obs = 1.f;
+                val = (x - lo) / sc;
+                if (arcsinh) val = asinhf(val);
+            }
+        }
+        float* f = feats + ((int64_t)li * n_ctx + pp) * 3 * ps;
+        f[i] = ((float)e - origin) / tscale;
+        f[ps + i] = val;
+        f[2 * ps + i] = obs;
+    }
+    for (int pp = tid; pp < n_ctx; pp += 256) {
+        bool any = false;
+        for (int i = 0; i < ps; i++) {
+            const int src = pp * ps + i - pad;
+            any = any || (src >= 0 && src < len && !__builtin_isnan(row[src]));
+        }
+        ctx_valid[(int64_t)li * n_ctx + pp] = any ? 1 : 0;
+    }
+    for (int e = tid; e < n_out * ps; e += 256) {
+        const int pp = e / ps, i = e - pp * ps;
+        float* f = fut_feats + ((int64_t)li * n_out + pp) * 3 * ps;
+        f[i] = (float)e / tscale;
+        f[ps + i] = 0.f;
+        f[2 * ps + i] = 0.f;
+    }
+    if (tid == 0) {
+        loc[li] = lo;
+        scale[li] = sc;
+    }
+}
+
+// The Chronos-2 inverse scaling (src/chronos2/forecaster.zig:184-201): out (n, horizon, q) from
+// raw (n * n_out, q * ps), where step p * ps + i of quantile qi is raw[(li * n_out + p) * q * ps
+// + qi * ps + i]; sinh first when the model works in asinh space, then v * scale + loc unfused.
+__global__ __launch_bounds__(256) void chronos2_finish(const float* raw, const float* loc, const float* scale,
+                                                       float* out, int n, int n_out, int q, int ps, int horizon,
+                                                       int arcsinh) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per = (int64_t)horizon * q;
+    if (idx >= (int64_t)n * per) return;
+    const int li = (int)(idx / per);
+    const int rem = (int)(idx - li * per), step = rem / q, qi = rem - step * q;
+    const int pp = step / ps, i = step - pp * ps;
+    float v = raw[((int64_t)li * n_out + pp) * q * ps + qi * ps + i];
+    if (arcsinh) v = sinhf(v);
+    {
+#pragma clang fp contract(off)
+        out[idx] = v * scale[li] + loc[li];
+    }
+}
+
 // The inverse instance norm (src/chronos_bolt/forecaster.zig:215-219): out = raw * scale + loc.
 __global__ __launch_bounds__(256) void bolt_finish(const float* raw, const float* loc, const float* scale, float* out,
                                                    int n, int per) {
@@ -169,6 +252,25 @@ hipError_t launch_bolt_prepare(const float* ctx, int64_t stride, int64_t offset,
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(bolt_prepare, dim3((unsigned)n), dim3(256), 0, stream, ctx, stride, offset, len, ps, n_patch, pad,
                        norm_eps, feats, patch_valid, loc, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_chronos2_prepare(const float* inputs, int64_t stride, int64_t start, int len, int ps, int n_ctx,
+                                  int n_out, int pad, float tscale, int arcsinh, float* feats, float* fut_feats,
+                                  uint8_t* ctx_valid, float* loc, float* scale, int n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(chronos2_prepare, dim3((unsigned)n), dim3(256), 0, stream, inputs, stride, start, len, ps, n_ctx,
+                       n_out, pad, tscale, arcsinh, feats, fut_feats, ctx_valid, loc, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_chronos2_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int n_out,
+                                  int q, int ps, int horizon, int arcsinh, hipStream_t stream) {
+    const int64_t total = (int64_t)n * horizon * q;
+    if (total <= 0) return hipSuccess;
+    if (horizon > n_out * ps) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(chronos2_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, raw, loc, scale,
+                       out, n, n_out, q, ps, horizon, arcsinh);
     return hipGetLastError();
 }
 

@@ -82,6 +82,11 @@ hipError_t launch_broadcast_rows(const float* v, float* y, int rows, int d, hipS
 hipError_t launch_bolt_prepare(const float* ctx, int64_t stride, int64_t offset, int len, int ps, int n_patch, int pad,
                                float norm_eps, float* feats, uint8_t* patch_valid, float* loc, float* scale, int n,
                                hipStream_t stream);
+hipError_t launch_chronos2_prepare(const float* inputs, int64_t stride, int64_t start, int len, int ps, int n_ctx,
+                                  int n_out, int pad, float tscale, int arcsinh, float* feats, float* fut_feats,
+                                  uint8_t* ctx_valid, float* loc, float* scale, int n, hipStream_t stream);
+hipError_t launch_chronos2_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int n_out,
+                                  int q, int ps, int horizon, int arcsinh, hipStream_t stream);
 hipError_t launch_bolt_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int per,
                               hipStream_t stream);
 

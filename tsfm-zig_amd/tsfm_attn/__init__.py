@@ -63,6 +63,7 @@ EXPORTS = (
     "tsfm_chronos2_forward",
     "tsfm_bolt_forward",
     "tsfm_bolt_forecast",
+    "tsfm_chronos2_forecast",
     "tsfm_weight_register",
     "tsfm_weight_release",
     "tsfm_sgemm_nt",
@@ -306,6 +307,22 @@ class BoltForwardArgs(ctypes.Structure):
     ]
 
 
+class Chronos2ForecastArgs(ctypes.Structure):
+    """``tsfm_chronos2_forecast_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("model", Chronos2ForwardArgs),
+        ("inputs", ctypes.c_void_p),
+        ("stride", ctypes.c_int64),
+        ("start", ctypes.c_int64),
+        ("len", ctypes.c_int32),
+        ("horizon", ctypes.c_int32),
+        ("time_scale", ctypes.c_float),
+        ("arcsinh", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+    ]
+
+
 class BoltForecastArgs(ctypes.Structure):
     """``tsfm_bolt_forecast_args`` (include/tsfm_attn.h)."""
 
@@ -411,6 +428,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_bolt_forward.restype = ctypes.c_int
     lib.tsfm_bolt_forecast.argtypes = [ctypes.POINTER(BoltForecastArgs)]
     lib.tsfm_bolt_forecast.restype = ctypes.c_int
+    lib.tsfm_chronos2_forecast.argtypes = [ctypes.POINTER(Chronos2ForecastArgs)]
+    lib.tsfm_chronos2_forecast.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -767,6 +786,13 @@ def chronos2_forward(raw, feats, fut_feats, ctx_valid, reg, cos_t, sin_t, layers
         if device:
             raise ValueError("keys_all_valid is required with device tensors")
         keys_all_valid = bool(np.asarray(ctx_valid).all())
+    a = _chronos2_args(raw, feats, fut_feats, ctx_valid, reg, cos_t, sin_t, layers, final_norm, input_embed,
+                       output_embed, b, n_ctx, n_out, d, nh, d_ff, eps, keys_all_valid, scale, hd, device, stream)
+    return int(load().tsfm_chronos2_forward(ctypes.byref(a)))
+
+
+def _chronos2_args(raw, feats, fut_feats, ctx_valid, reg, cos_t, sin_t, layers, final_norm, input_embed, output_embed,
+                   b, n_ctx, n_out, d, nh, d_ff, eps, keys_all_valid, scale, hd, device, stream):
     arr = (Chronos2Layer * max(1, len(layers)))()
     for i, ly in enumerate(layers):
         for f in CHRONOS2_LAYER_FIELDS:
@@ -775,12 +801,31 @@ def chronos2_forward(raw, feats, fut_feats, ctx_valid, reg, cos_t, sin_t, layers
                              n_layers=len(layers), keys_all_valid=int(bool(keys_all_valid)), eps=eps, scale=scale,
                              flags=DEVICE_PTRS if device else 0, rope_cos=_ptr(cos_t), rope_sin=_ptr(sin_t),
                              layers=arr, final_norm=_ptr(final_norm),
-                             stream=_stream_of(feats, stream) if device else None)
+                             stream=_stream_of(reg, stream) if device else None)
     a = Chronos2ForwardArgs(enc=enc, n_ctx=n_ctx, n_out=n_out, feats=_ptr(feats), fut_feats=_ptr(fut_feats),
                             ctx_valid=_ptr(ctx_valid), reg=_ptr(reg), input_embed=_resblock(input_embed),
                             output_embed=_resblock(output_embed), raw=_ptr(raw))
     a._keep = arr  # the layer array must outlive the call
-    return int(load().tsfm_chronos2_forward(ctypes.byref(a)))
+    return a
+
+
+def chronos2_forecast(out, inputs, length: int, horizon: int, reg, cos_t, sin_t, layers: Sequence[dict], final_norm,
+                      input_embed: dict, output_embed: dict, n: int, d: int, nh: int, d_ff: int, eps: float,
+                      patch: int = 16, stride: Optional[int] = None, start: int = 0, time_scale: float = 1.0,
+                      arcsinh: bool = False, scale: float = 1.0, hd: int = 64, stream=None) -> int:
+    """The whole Chronos-2 forecast of n series on device tensors (runChunk,
+    src/chronos2/forecaster.zig:59-204): row s is inputs[s * stride + start:][:length] (NaN =
+    missing); out (n, horizon, q) receives the quantile forecasts in data units. cos_t / sin_t are
+    the (n_ctx + 1 + n_out, 32) RoPE tables of the sequence."""
+    if not _is_device(inputs):
+        raise ValueError("chronos2_forecast runs on device tensors; host callers use chronos2_forward")
+    n_ctx, n_out = (length + patch - 1) // patch, (horizon + patch - 1) // patch
+    m = _chronos2_args(None, None, None, None, reg, cos_t, sin_t, layers, final_norm, input_embed, output_embed, n,
+                       n_ctx, n_out, d, nh, d_ff, eps, False, scale, hd, True, stream)
+    a = Chronos2ForecastArgs(model=m, inputs=_ptr(inputs), stride=length if stride is None else stride, start=start,
+                             len=length, horizon=horizon, time_scale=time_scale, arcsinh=int(bool(arcsinh)),
+                             out=_ptr(out))
+    return int(load().tsfm_chronos2_forecast(ctypes.byref(a)))
 
 
 def bolt_forward(raw, feats, patch_valid, reg, dec_start, rel_table, enc_layers: Sequence[dict], enc_final_norm,
