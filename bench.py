@@ -20,14 +20,18 @@ Other workloads (parity-test shapes, measured the same way):
            64 x 577 tokens, d_model 768, three (768, 768) weights
   bolt_forward  the Chronos-Bolt-small model forward at the end-to-end configuration (16 series,
            32 patches + REG, d_model 512, 6 + 6 layers, 9 quantiles x 64), f32, random-init weights
+  bolt_forecast  the whole Chronos-Bolt-small forecast at the end-to-end configuration: 16 series
+           x 512 raw steps (sinusoid + trend + noise, 2 % NaN) in, 9 quantiles x 64 steps out; the
+           instance norm, patching and inverse norm run on the device around bolt_forward
   encoder  the Chronos-2 encoder stack at the Chronos-2-base size (12 layers, d_model 768, 12 heads,
            d_ff 3072) over 64 series x 577 tokens, f32, random-init weights; the roofline is over
            the whole stack (every launch but the row norms runs on the f32 matrix cores)
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward]
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward|bolt_forecast]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
+import ctypes
 import json
 import os
 import pathlib
@@ -353,11 +357,14 @@ def run_bolt_forward(torch, ta, workloads, peak):
     all_valid = bool(a["patch_valid"].all())
     d, F, npch = m["d_model"], m["d_ff"], m["n_patch"]
 
+    # The argument block is built once, as a caller holding a loaded model does.
+    args = ta.bolt_forward_args(enc, dec, dev["feats"], dev["patch_valid"], dev["reg"], dev["dec_start"],
+                         dev["rel_table"], dev["enc_final_norm"], dev["dec_final_norm"], ie, oe, raw, w.B, npch, d, w.H,
+                         64, F, m["eps"], m["buckets"], m["max_distance"], all_valid, True, None)
+    fn = ta.load().tsfm_bolt_forward
+
     def step():
-        _check(ta, ta.bolt_forward(raw, dev["feats"], dev["patch_valid"], dev["reg"], dev["dec_start"],
-                                   dev["rel_table"], enc, dev["enc_final_norm"], dec, dev["dec_final_norm"], ie, oe,
-                                   w.B, npch, d, w.H, F, m["eps"], num_buckets=m["buckets"],
-                                   max_distance=m["max_distance"], keys_all_valid=all_valid))
+        _check(ta, fn(ctypes.byref(args)))
 
     def cpu_leg(B):
         orc = _orc()
@@ -375,8 +382,48 @@ def run_bolt_forward(torch, ta, workloads, peak):
                  "TFLOP/s", w.B)
 
 
+def run_bolt_forecast(torch, ta, workloads, peak):
+    w = workloads.bolt_forward()
+    a, m = w.arrays, w.meta
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    dev = {n: cu(v) for n, v in a.items()}
+    enc = [{k: cu(v) for k, v in ly.items()} for ly in m["enc"]]
+    dec = [{k: cu(v) for k, v in ly.items()} for ly in m["dec"]]
+    ie, oe = ({k: cu(v) for k, v in b.items()} for b in (m["ie"], m["oe"]))
+    out = torch.empty((w.B, m["out"]), dtype=torch.float32, device="cuda")
+    d, F, length = m["d_model"], m["d_ff"], a["ctx"].shape[1]
+
+    # The argument block (about 130 weight pointers) is built once, as a caller holding a loaded
+    # model does; each step is one tsfm_bolt_forecast call.
+    args = ta.bolt_forecast_args(out, dev["ctx"], length, dev["reg"], dev["dec_start"], dev["rel_table"], enc,
+                                 dev["enc_final_norm"], dec, dev["dec_final_norm"], ie, oe, w.B, d, w.H, F, m["eps"],
+                                 num_buckets=m["buckets"], max_distance=m["max_distance"])
+    fn = ta.load().tsfm_bolt_forecast
+
+    def step():
+        _check(ta, fn(ctypes.byref(args)))
+
+    def cpu_leg(B):
+        orc = _orc()
+        want = np.zeros((B, m["out"]), np.float32)
+        ctx = np.ascontiguousarray(a["ctx"][:B])
+        t0 = time.perf_counter()
+        orc.bolt_forecast(cpu_threads(), want, ctx, length, 0, length, B, 16, 1e-5, a["reg"], a["dec_start"],
+                          a["rel_table"], m["buckets"], m["max_distance"], d, w.H, 64, F, m["enc"],
+                          a["enc_final_norm"], m["dec"], a["dec_final_norm"], m["eps"], m["ie"], m["oe"])
+        return time.perf_counter() - t0, want, orc.lanes
+
+    config = {"workload": "bolt_small_forecast", "series": w.B, "context": length, "horizon": 64,
+              "missing": "2 %", "d_model": d, "H": w.H, "d_ff": F, "layers": "6 enc + 6 dec",
+              "head": f"{m['out']} (9 quantiles x 64)", "weights": "random-init f32",
+              "input": "sinusoid (period 24, amplitude 10) + trend + N(0,1), seed 0"}
+    return Bench(w, step, lambda: out.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
+                 "TFLOP/s", w.B)
+
+
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
-             "variate": run_variate, "proj": run_proj, "encoder": run_encoder, "bolt_forward": run_bolt_forward}
+             "variate": run_variate, "proj": run_proj, "encoder": run_encoder, "bolt_forward": run_bolt_forward,
+             "bolt_forecast": run_bolt_forecast}
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
 

@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "../../include/tsfm_attn.h"
@@ -1006,6 +1007,39 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
 
 }  // namespace
 
+// Device copies of T5 bucket-id tables, one per (device, length, buckets, max distance), made on
+// first use with a synchronous upload and kept until the process ends (a few KB each). Read-only
+// after creation; the mutex guards the list.
+static hipError_t cached_bucket_ids(const std::vector<int32_t>& ids, int64_t seq, int32_t buckets, int32_t max_distance,
+                             const int32_t** out) {
+    struct Entry {
+        int device;
+        int64_t seq;
+        int32_t buckets, max_distance;
+        int32_t* dev;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& c : cache)
+        if (c.device == device && c.seq == seq && c.buckets == buckets && c.max_distance == max_distance) {
+            *out = c.dev;
+            return hipSuccess;
+        }
+    int32_t* dev = nullptr;
+    if ((e = hipMalloc(reinterpret_cast<void**>(&dev), ids.size() * 4)) != hipSuccess) return e;
+    if ((e = hipMemcpy(dev, ids.data(), ids.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) {
+        (void)hipFree(dev);
+        return e;
+    }
+    cache.push_back({device, seq, buckets, max_distance, dev});
+    *out = dev;
+    return hipSuccess;
+}
+
 int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (a->batch < 0 || a->n_patch < 0 || a->n_enc_layers < 0 || a->n_dec_layers < 0 || a->heads < 0 || a->d_ff < 0)
@@ -1054,15 +1088,18 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
         Plan plan;
         size_t at[11];
         for (int i = 0; i < 11; i++) at[i] = plan.take(sz[i]);
+        // The bucket ids live on the device once per (length, buckets, max distance): a per-call
+        // upload from pageable memory would make the host wait for the stream to drain before it
+        // could queue the forward's launches.
+        const int32_t* ids = nullptr;
+        if ((e = cached_bucket_ids(buckets, seq, a->rel_buckets, a->rel_max_distance, &ids)) != hipSuccess)
+            return hip_fail(e, "bucket id upload");
         char* scratch = nullptr;
         if ((e = hipMallocAsync(reinterpret_cast<void**>(&scratch), plan.off, s)) != hipSuccess)
             return hip_fail(e, "forward scratch allocation");
-        // Pageable source: the call returns once the ids are staged, so the vector may go.
-        e = hipMemcpyAsync(scratch + at[10], buckets.data(), sz[10], hipMemcpyHostToDevice, s);
         BoltDev dv{a->feats, a->reg, a->dec_start, a->rel_table, a->enc_final_norm, a->dec_final_norm,
-                   a->patch_valid, reinterpret_cast<const int32_t*>(scratch + at[10]), a->enc_layers, a->dec_layers,
-                   a->input_embed, a->output_embed, a->raw};
-        if (e == hipSuccess) e = bolt_forward_on(a, dv, scratch, at, s);
+                   a->patch_valid, ids, a->enc_layers, a->dec_layers, a->input_embed, a->output_embed, a->raw};
+        e = bolt_forward_on(a, dv, scratch, at, s);
         const hipError_t f = hipFreeAsync(scratch, s);
         if (e != hipSuccess) return hip_fail(e, "forward launch");
         if (f != hipSuccess) return hip_fail(f, "forward scratch release");

@@ -24,6 +24,9 @@
 // the matrix pipe to two others.
 #include <algorithm>
 
+#include <mutex>
+#include <vector>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -219,6 +222,37 @@ __global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
 
 }  // namespace
 
+namespace {
+
+// Split partials: one device buffer per (device, stream) for every split product queued on that
+// stream, allocated on first use and kept until the process ends. Stream order makes the reuse
+// safe: a product's reduce has read its partials before the next product on the stream writes
+// them. Calls that overlap on different streams use different buffers. A per-launch stream-ordered
+// allocation costs host time comparable to a small product's whole GPU time.
+constexpr size_t kSplitFloats = (size_t)383 * BM * BN;
+
+float* split_workspace(hipStream_t stream) {
+    struct Entry {
+        int device;
+        hipStream_t stream;
+        float* buf;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& c : cache)
+        if (c.device == device && c.stream == stream) return c.buf;
+    if (cache.size() >= 64) return nullptr;  // many streams: the product runs unsplit
+    void* buf = nullptr;
+    if (hipMalloc(&buf, kSplitFloats * sizeof(float)) != hipSuccess) return nullptr;
+    cache.push_back({device, stream, static_cast<float*>(buf)});
+    return static_cast<float*>(buf);
+}
+
+}  // namespace
+
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
@@ -244,11 +278,13 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         if (s >= 2) {
             const int per = (steps + s - 1) / s;
             s = (steps + per - 1) / per;
-            void* part = nullptr;
-            if (hipMallocAsync(&part, (size_t)s * p.tokens * p.width * sizeof(float), stream) == hipSuccess) {
+            // s * blocks <= 256 + blocks - 1 < 383 and tokens * width <= blocks * BM * BN, so the
+            // partials always fit the stream's workspace.
+            float* part = split_workspace(stream);
+            if (part != nullptr) {
                 p.splits = s;
                 p.split_steps = per;
-                p.partial = static_cast<float*>(part);
+                p.partial = part;
             }
         }
     }
@@ -260,8 +296,7 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
             hipLaunchKernelGGL(proj_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
             e = hipGetLastError();
         }
-        const hipError_t f = hipFreeAsync(p.partial, stream);
-        return e != hipSuccess ? e : f;
+        return e;
     }
     if (p.out_dtype == 1)
         hipLaunchKernelGGL(qkv_proj<1>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);

@@ -841,15 +841,17 @@ def bolt_forward(raw, feats, patch_valid, reg, dec_start, rel_table, enc_layers:
         if device:
             raise ValueError("keys_all_valid is required with device tensors")
         keys_all_valid = bool(np.asarray(patch_valid).all())
-    a = _bolt_args(enc_layers, dec_layers, feats, patch_valid, reg, dec_start, rel_table, enc_final_norm, dec_final_norm, input_embed,
+    a = bolt_forward_args(enc_layers, dec_layers, feats, patch_valid, reg, dec_start, rel_table, enc_final_norm, dec_final_norm, input_embed,
                    output_embed, raw, b, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, keys_all_valid,
                    device, stream)
     return int(load().tsfm_bolt_forward(ctypes.byref(a)))
 
 
-def _bolt_args(enc_layers, dec_layers, feats, patch_valid, reg, dec_start, rel_table, enc_final_norm, dec_final_norm, input_embed,
-               output_embed, raw, b, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, keys_all_valid, device,
-               stream):
+def bolt_forward_args(enc_layers, dec_layers, feats, patch_valid, reg, dec_start, rel_table, enc_final_norm,
+                      dec_final_norm, input_embed, output_embed, raw, b, n_patch, d, nh, hd, d_ff, eps, num_buckets,
+                      max_distance, keys_all_valid, device, stream) -> BoltForwardArgs:
+    """The argument block of bolt_forward, built once for repeated tsfm_bolt_forward calls (the
+    layer arrays it points to live as long as the returned object)."""
     ea = (BoltEncLayer * max(1, len(enc_layers)))()
     for i, ly in enumerate(enc_layers):
         for f in BOLT_ENC_FIELDS:
@@ -879,15 +881,28 @@ def bolt_forecast(out, ctx, length: int, reg, dec_start, rel_table, enc_layers: 
     """The whole Chronos-Bolt forecast of n series on device tensors (predictBlock/runChunk,
     src/chronos_bolt/forecaster.zig:115-220): row s of the context is ctx[s * stride + offset:][:length]
     (NaN = missing); out (n, q * P) receives the quantile forecasts in data units."""
+    a = bolt_forecast_args(out, ctx, length, reg, dec_start, rel_table, enc_layers, enc_final_norm, dec_layers,
+                           dec_final_norm, input_embed, output_embed, n, d, nh, d_ff, eps, patch, stride, offset,
+                           norm_eps, num_buckets, max_distance, hd, stream)
+    return int(load().tsfm_bolt_forecast(ctypes.byref(a)))
+
+
+def bolt_forecast_args(out, ctx, length, reg, dec_start, rel_table, enc_layers, enc_final_norm, dec_layers,
+                       dec_final_norm, input_embed, output_embed, n, d, nh, d_ff, eps, patch=16, stride=None, offset=0,
+                       norm_eps=1e-5, num_buckets=32, max_distance=128, hd=64, stream=None) -> BoltForecastArgs:
+    """The argument block of bolt_forecast, built once: a caller that forecasts repeatedly with the
+    same weights and buffers passes it to tsfm_bolt_forecast each time (the layer arrays it points
+    to live as long as the returned object)."""
     if not _is_device(ctx):
         raise ValueError("bolt_forecast runs on device tensors; host callers use bolt_forward")
     n_patch = (length + patch - 1) // patch
-    m = _bolt_args(enc_layers, dec_layers, None, None, reg, dec_start, rel_table, enc_final_norm, dec_final_norm,
+    m = bolt_forward_args(enc_layers, dec_layers, None, None, reg, dec_start, rel_table, enc_final_norm, dec_final_norm,
                    input_embed, output_embed, None, n, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, False,
                    True, stream)
     a = BoltForecastArgs(model=m, ctx=_ptr(ctx), stride=length if stride is None else stride, offset=offset,
                          len=length, patch=patch, norm_eps=norm_eps, out=_ptr(out))
-    return int(load().tsfm_bolt_forecast(ctypes.byref(a)))
+    a._keep = m._keep
+    return a
 
 
 def weight_register(w) -> Optional[int]:

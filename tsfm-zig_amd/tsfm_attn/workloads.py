@@ -274,8 +274,15 @@ def bolt_forward(B: int = 16, n_patch: int = 32, H: int = 8, d_ff: int = 2048, n
     f_emb = 2.0 * B * n_patch * (2 * patch * d_ff + d_ff * d + 2 * patch * d) + 2.0 * B * (d * d_ff + d_ff * out + d * out)
     w_bytes = 4.0 * (sum(a.size for ly in enc + dec for a in ly.values()) + sum(a.size for a in ie.values()) +
                      sum(a.size for a in oe.values()))
+    # The raw context of the end-to-end run: each series a period-24 sinusoid of amplitude 10 plus
+    # a linear trend plus N(0, 1) noise (its own generator from the seed), 2 % of the steps NaN.
+    crng = np.random.default_rng(seed)
+    t = np.arange(n_patch * patch, dtype=np.float64)
+    slope = crng.uniform(-0.05, 0.05, (B, 1))
+    ctx = 10.0 * np.sin(2 * np.pi * t / 24.0) + slope * t + crng.standard_normal((B, t.size))
+    ctx[crng.random(ctx.shape) < 0.02] = np.nan
     return Workload("bolt_small_forward", "f32", B, H, seq, seq, 64, 1.0,
-                    dict(feats=feats, patch_valid=pv, reg=norm(), dec_start=norm(),
+                    dict(feats=feats, patch_valid=pv, ctx=ctx.astype(np.float32), reg=norm(), dec_start=norm(),
                          rel_table=(0.1 * rng.standard_normal((buckets, H))).astype(np.float32),
                          enc_final_norm=norm(), dec_final_norm=norm()),
                     dict(enc=enc, dec=dec, ie=ie, oe=oe, d_model=d, d_ff=d_ff, n_patch=n_patch, out=out, eps=eps,
