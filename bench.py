@@ -23,11 +23,14 @@ Other workloads (parity-test shapes, measured the same way):
   bolt_forecast  the whole Chronos-Bolt-small forecast at the end-to-end configuration: 16 series
            x 512 raw steps (sinusoid + trend + noise, 2 % NaN) in, 9 quantiles x 64 steps out; the
            instance norm, patching and inverse norm run on the device around bolt_forward
+  chronos2_forecast  the whole Chronos-2-base forecast at the attention's shape: 64 series x 8192
+           raw steps in (512 patches + REG + 64 future = 577 tokens), 21 quantiles x 1024 steps out
   encoder  the Chronos-2 encoder stack at the Chronos-2-base size (12 layers, d_model 768, 12 heads,
            d_ff 3072) over 64 series x 577 tokens, f32, random-init weights; the roofline is over
            the whole stack (every launch but the row norms runs on the f32 matrix cores)
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward|bolt_forecast]
+    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward|bolt_forecast|
+                     chronos2_forecast]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
@@ -421,9 +424,46 @@ def run_bolt_forecast(torch, ta, workloads, peak):
                  "TFLOP/s", w.B)
 
 
+def run_chronos2_forecast(torch, ta, workloads, peak):
+    w = workloads.chronos2_forecast()
+    a, m = w.arrays, w.meta
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    dev = {n: cu(v) for n, v in a.items()}
+    layers = [{k: cu(v) for k, v in ly.items()} for ly in m["layers"]]
+    ie, oe = ({k: cu(v) for k, v in b.items()} for b in (m["ie"], m["oe"]))
+    d, F, T, hz, q = m["d_model"], m["d_ff"], m["context"], m["horizon"], m["quantiles"]
+    out = torch.empty((w.B, hz, q), dtype=torch.float32, device="cuda")
+    # The argument block (about 140 weight pointers) is built once, as a caller holding a loaded
+    # model does; each step is one tsfm_chronos2_forecast call.
+    args = ta.chronos2_forecast_args(out, dev["ctx"], T, hz, dev["reg"], dev["rope_cos"], dev["rope_sin"], layers,
+                                     dev["final_norm"], ie, oe, w.B, d, w.H, F, m["eps"], time_scale=m["time_scale"],
+                                     arcsinh=True)
+    fn = ta.load().tsfm_chronos2_forecast
+
+    def step():
+        _check(ta, fn(ctypes.byref(args)))
+
+    def cpu_leg(B):
+        orc = _orc()
+        want = np.zeros((B, hz, q), np.float32)
+        ctx = np.ascontiguousarray(a["ctx"][:B])
+        t0 = time.perf_counter()
+        orc.chronos2_forecast(cpu_threads(), want, ctx, T, 0, T, B, m["patch"], hz, m["time_scale"], True, a["reg"], d,
+                              w.H, 64, F, m["layers"], a["final_norm"], m["eps"], a["rope_cos"], a["rope_sin"], 1.0,
+                              m["ie"], m["oe"])
+        return time.perf_counter() - t0, want, orc.lanes
+
+    config = {"workload": "chronos2_base_forecast", "series": w.B, "context": T, "horizon": hz, "quantiles": q,
+              "tokens": w.n_q, "d_model": d, "H": w.H, "d_ff": F, "layers": m["n_layers"], "asinh": True,
+              "missing": "oldest 0-25 % + 2 %", "weights": "random-init f32",
+              "input": "sinusoid (period 24, amplitude 10) + trend + N(0,1)"}
+    return Bench(w, step, lambda: out.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
+                 "TFLOP/s", 1)
+
+
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
              "variate": run_variate, "proj": run_proj, "encoder": run_encoder, "bolt_forward": run_bolt_forward,
-             "bolt_forecast": run_bolt_forecast}
+             "bolt_forecast": run_bolt_forecast, "chronos2_forecast": run_chronos2_forecast}
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
 

@@ -817,6 +817,17 @@ def chronos2_forecast(out, inputs, length: int, horizon: int, reg, cos_t, sin_t,
     src/chronos2/forecaster.zig:59-204): row s is inputs[s * stride + start:][:length] (NaN =
     missing); out (n, horizon, q) receives the quantile forecasts in data units. cos_t / sin_t are
     the (n_ctx + 1 + n_out, 32) RoPE tables of the sequence."""
+    a = chronos2_forecast_args(out, inputs, length, horizon, reg, cos_t, sin_t, layers, final_norm, input_embed,
+                               output_embed, n, d, nh, d_ff, eps, patch, stride, start, time_scale, arcsinh, scale, hd,
+                               stream)
+    return int(load().tsfm_chronos2_forecast(ctypes.byref(a)))
+
+
+def chronos2_forecast_args(out, inputs, length, horizon, reg, cos_t, sin_t, layers, final_norm, input_embed,
+                           output_embed, n, d, nh, d_ff, eps, patch=16, stride=None, start=0, time_scale=1.0,
+                           arcsinh=False, scale=1.0, hd=64, stream=None) -> Chronos2ForecastArgs:
+    """The argument block of chronos2_forecast, built once for repeated tsfm_chronos2_forecast calls
+    (the layer array it points to lives as long as the returned object)."""
     if not _is_device(inputs):
         raise ValueError("chronos2_forecast runs on device tensors; host callers use chronos2_forward")
     n_ctx, n_out = (length + patch - 1) // patch, (horizon + patch - 1) // patch
@@ -825,7 +836,8 @@ def chronos2_forecast(out, inputs, length: int, horizon: int, reg, cos_t, sin_t,
     a = Chronos2ForecastArgs(model=m, inputs=_ptr(inputs), stride=length if stride is None else stride, start=start,
                              len=length, horizon=horizon, time_scale=time_scale, arcsinh=int(bool(arcsinh)),
                              out=_ptr(out))
-    return int(load().tsfm_chronos2_forecast(ctypes.byref(a)))
+    a._keep = m._keep
+    return a
 
 
 def bolt_forward(raw, feats, patch_valid, reg, dec_start, rel_table, enc_layers: Sequence[dict], enc_final_norm,

@@ -234,6 +234,48 @@ def chronos2_encoder(B: int = 64, H: int = 12, n_ctx: int = 512, n_fut: int = 64
                          bytes=nbytes, seed=seed, num_layers=n_layers))
 
 
+def chronos2_forecast(B: int = 64, context: int = 8192, horizon: int = 1024, quantiles: int = 21, patch: int = 16,
+                      seed: int = 0) -> Workload:
+    """The whole Chronos-2-base forecast at the attention workload's shape: 64 series of 8192 raw
+    steps (512 context patches) and a 1024-step horizon (64 future patches), so the sequence is the
+    attention's 577 tokens, through the 12-layer encoder of chronos2_encoder (same weights), the
+    input and output ResBlocks (hidden d_ff, 21 quantiles) and the forecaster's instance norm,
+    asinh space and inverse scaling (time_encoding_scale 8192). Each series is a period-24
+    sinusoid of amplitude 10 plus a trend plus N(0, 1) noise, with its oldest 0-25 % of steps
+    missing (whole patches, as the attention workload's left padding) and 2 % of the rest.
+    FLOPs: the encoder's plus both ResBlocks' products."""
+    w = chronos2_encoder(B=B, n_ctx=context // patch, n_fut=(horizon + patch - 1) // patch, seed=seed)
+    a, m = w.arrays, w.meta
+    d, F = m["d_model"], m["d_ff"]
+    n_ctx, n_out = context // patch, (horizon + patch - 1) // patch
+    rng = np.random.default_rng(seed + 1)
+
+    def block(i, h, o):
+        return dict(hidden_w=(rng.standard_normal((h, i)) / np.sqrt(i)).astype(np.float32),
+                    hidden_b=(0.1 * rng.standard_normal(h)).astype(np.float32),
+                    output_w=(rng.standard_normal((o, h)) / np.sqrt(h)).astype(np.float32),
+                    output_b=(0.1 * rng.standard_normal(o)).astype(np.float32),
+                    residual_w=(rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32),
+                    residual_b=(0.1 * rng.standard_normal(o)).astype(np.float32))
+
+    ie, oe = block(3 * patch, F, d), block(d, F, quantiles * patch)
+    t = np.arange(context, dtype=np.float64)
+    slope = rng.uniform(-0.01, 0.01, (B, 1))
+    ctx = 10.0 * np.sin(2 * np.pi * t / 24.0) + slope * t + rng.standard_normal((B, context))
+    ctx[rng.random(ctx.shape) < 0.02] = np.nan
+    pad = rng.integers(0, n_ctx // 4 + 1, B)
+    for b in range(B):
+        ctx[b, : pad[b] * patch] = np.nan
+    rows_in, rows_out = B * (n_ctx + n_out), B * n_out
+    f_res = 2.0 * rows_in * (3 * patch * F + F * d + 3 * patch * d) + \
+        2.0 * rows_out * (d * F + F * quantiles * patch + d * quantiles * patch)
+    return Workload("chronos2_forecast", "f32", B, w.H, w.n_q, w.n_k, 64, 1.0,
+                    dict(ctx=ctx.astype(np.float32), rope_cos=a["rope_cos"], rope_sin=a["rope_sin"],
+                         final_norm=a["final_norm"], reg=(rng.standard_normal(d)).astype(np.float32)),
+                    dict(m, ie=ie, oe=oe, context=context, horizon=horizon, quantiles=quantiles, patch=patch,
+                         time_scale=float(context), flops=m["flops"] + f_res))
+
+
 def bolt_forward(B: int = 16, n_patch: int = 32, H: int = 8, d_ff: int = 2048, n_layers: int = 6, quantiles: int = 9,
                  horizon: int = 64, patch: int = 16, buckets: int = 32, max_distance: int = 128, seed: int = 0,
                  eps: float = 1e-6) -> Workload:
