@@ -145,20 +145,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // past the width are not stored).
     const int n0 = tn * BN + wn * 64;
     if (n0 >= n_cols) return;
+    const int sel = n0 / p.width, col = n0 - sel * p.width;
     if (p.splits > 1) {  // partial sums only; proj_reduce adds them up in split order and finishes
+        // Partial row m of split s holds all n_cols columns (every output side by side).
         const int cq4 = 4 * (lane >> 4);
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) {
             const int m = tm * BM + wm * 64 + mb * 16 + (lane & 15);
             if (m >= p.tokens) continue;
-            float* const out = p.partial + ((int64_t)split * p.tokens + m) * p.width + n0 + cq4;
+            float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0 + cq4;
 #pragma unroll
             for (int nb = 0; nb < 4; nb++)
-                if (n0 + cq4 + 16 * nb < p.width) st4(out + 16 * nb, acc[nb][mb]);
+                if (col + cq4 + 16 * nb < p.width) st4(out + 16 * nb, acc[nb][mb]);
         }
         return;
     }
-    const int sel = n0 / p.width, col = n0 - sel * p.width;
     void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
     const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
     const bool rope = p.rope_cos != nullptr && sel < 2;
@@ -204,20 +205,24 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     }
 }
 
-// Sum of the split partials in split order (deterministic), then the one-output epilogue: alpha,
-// bias, ReLU or residual, f32 store. One thread per four columns of a token.
+// Sum of the split partials in split order (deterministic), then the epilogue: alpha, and with one
+// output bias, ReLU or residual; f32 store into the output the column belongs to. One thread per
+// four columns of a token (width is a multiple of 4, so a group never straddles two outputs).
 __global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
-    const int q = p.width / 4;
+    const int n_cols = p.width * p.n_out, q = n_cols / 4;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (int64_t)p.tokens * q) return;
     const int m = (int)(idx / q), c = (int)(idx % q) * 4;
-    f32x4 v = ld4(p.partial + (int64_t)m * p.width + c);
-    for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + m) * p.width + c);
+    f32x4 v = ld4(p.partial + (int64_t)m * n_cols + c);
+    for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + m) * n_cols + c);
     if (p.alpha != 1.f) v *= p.alpha;
-    if (p.bias != nullptr) v = v + ld4(p.bias + c);
+    const int sel = c / p.width, col = c - sel * p.width;
+    if (p.bias != nullptr) v = v + ld4(p.bias + col);
     if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
-    else if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + c) + v;
-    st4(static_cast<float*>(p.y0) + (int64_t)m * p.y0_tok + c, v);
+    else if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + col) + v;
+    float* const y = static_cast<float*>(sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3);
+    const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
+    st4(y + (int64_t)m * y_tok + col, v);
 }
 
 }  // namespace
@@ -268,12 +273,14 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
     // and each workgroup walks the whole reduction; split it over workgroups instead, with the
-    // partial tiles summed in a fixed order by proj_reduce. One output, f32, no RoPE.
+    // partial tiles summed in a fixed order by proj_reduce. f32 outputs, no RoPE; several outputs
+    // only without an epilogue.
     const int steps = p.d_in / BK;
     p.splits = 1;
     p.split_steps = steps;
     p.partial = nullptr;
-    if (p.n_out == 1 && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 128 && steps >= 16) {
+    if ((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 128 &&
+        steps >= 16) {
         int s = (int)std::min<int64_t>((256 + blocks - 1) / blocks, std::min(steps / 8, 16));
         if (s >= 2) {
             const int per = (steps + s - 1) / s;
@@ -292,7 +299,7 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)(blocks * p.splits)), dim3(NT), kProjLds, stream, p);
         hipError_t e = hipGetLastError();
         if (e == hipSuccess) {
-            const int64_t n = (int64_t)p.tokens * (p.width / 4);
+            const int64_t n = (int64_t)p.tokens * (p.width * p.n_out / 4);
             hipLaunchKernelGGL(proj_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
             e = hipGetLastError();
         }
