@@ -564,6 +564,20 @@ hipError_t linear_on(const float* x, int64_t x_tok, const float* w, int out, int
     return tsfm::launch_proj(p, s);
 }
 
+// linear_on followed by nn.rmsNorm of the finished rows into norm_out (may be y): one launch fewer
+// when the product splits its reduction (the reduce normalises the rows), the same bits either way.
+hipError_t linear_norm_on(const float* x, int64_t x_tok, const float* w, int out, int in, float* y, int64_t y_tok,
+                          int rows, int epi, const float* resid, const float* norm_scale, float* norm_out,
+                          int64_t norm_tok, float eps, hipStream_t s) {
+    tsfm::ProjParams p{};
+    p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi;
+    p.resid = resid; p.resid_tok = y_tok;
+    p.y0 = y; p.y0_tok = y_tok;
+    p.tokens = rows; p.seq = rows; p.d_in = in; p.width = out; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
+    p.norm_scale = norm_scale; p.norm_out = norm_out; p.norm_out_tok = norm_tok; p.norm_eps = eps;
+    return tsfm::launch_proj(p, s);
+}
+
 // The layer loop on device buffers. scratch: xn, q, k, v, ab (rows x d each), then h (rows x d_ff).
 hipError_t encode_on(const tsfm_chronos2_encode_args* a, float* x, const uint8_t* kv, const float* cs,
                      const float* sn, const tsfm_chronos2_layer* layers, const float* final_norm, float* scratch,
@@ -947,9 +961,14 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
     hipError_t e = resblock_on(dv.ie, dv.feats, nb * np, emb, hb, rb, s);
     if (e == hipSuccess) e = tsfm::launch_assemble_sequence(emb, nullptr, dv.reg, dv.patch_valid, x, kv, nb, np, 0, d, s);
     // ---- encoder (Model.encode) ----
+    // Each residual product also normalises its rows for what comes next (linear_norm_on): the o
+    // projection for the FFN norm, wo for the next layer's attention norm or the final norm.
+    if (e == hipSuccess)
+        e = a->n_enc_layers > 0 ? tsfm::launch_rms_norm(x, d, xn, d, dv.enc[0].attn_norm, R, d, a->eps, s)
+                                : tsfm::launch_rms_norm(x, d, x, d, dv.enc_final_norm, R, d, a->eps, s);
     for (int l = 0; l < a->n_enc_layers && e == hipSuccess; l++) {
         const tsfm_bolt_enc_layer& ly = dv.enc[l];
-        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.attn_norm, R, d, a->eps, s)) != hipSuccess) break;
+        const bool last = l + 1 == a->n_enc_layers;
         tsfm::ProjParams p{};
         p.x = xn; p.x_tok = d; p.w0 = ly.q; p.w1 = ly.k; p.w2 = ly.v; p.w_ld = d; p.alpha = 1.f;
         p.y0 = q; p.y1 = k; p.y2 = v; p.y0_tok = p.y1_tok = p.y2_tok = inner;
@@ -964,23 +983,31 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
         ap.B = nb; ap.H = a->heads; ap.n_q = seq; ap.n_k = seq; ap.scale = 1.f;
         const int mask = a->keys_all_valid ? TSFM_MASK_FULL : TSFM_MASK_KEYS_ADDITIVE;  // Mask.pick(false, all, true)
         if ((e = tsfm::launch_attn_f32(ap, mask, tsfm::BIAS_REL, false, s)) != hipSuccess) break;
-        if ((e = linear_on(ab, inner, ly.o, d, inner, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
-        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.ffn_norm, R, d, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_norm_on(ab, inner, ly.o, d, inner, x, d, R, tsfm::kEpiResidual, x, ly.ffn_norm, xn, d, a->eps,
+                                s)) != hipSuccess)
+            break;
         if ((e = linear_on(xn, d, ly.wi, F, d, hb, F, R, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_on(hb, F, ly.wo, d, F, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+        if ((e = linear_norm_on(hb, F, ly.wo, d, F, x, d, R, tsfm::kEpiResidual, x,
+                                last ? dv.enc_final_norm : dv.enc[l + 1].attn_norm, last ? x : xn, d, a->eps, s)) !=
+            hipSuccess)
+            break;
     }
-    if (e == hipSuccess) e = tsfm::launch_rms_norm(x, d, x, d, dv.enc_final_norm, R, d, a->eps, s);
     // ---- decoder (Model.decode): one token per series; y (nb x d) in emb ----
     float* y = emb;
     if (e == hipSuccess) e = tsfm::launch_broadcast_rows(dv.dec_start, y, nb, d, s);
+    if (e == hipSuccess)
+        e = tsfm::launch_rms_norm(y, d, xn, d, a->n_dec_layers > 0 ? dv.dec[0].self_norm : dv.dec_final_norm, nb, d,
+                                  a->eps, s);
     for (int l = 0; l < a->n_dec_layers && e == hipSuccess; l++) {
         const tsfm_bolt_dec_layer& ly = dv.dec[l];
-        // self-attention over the single decoder token: o(v(norm(y)))
-        if ((e = tsfm::launch_rms_norm(y, d, xn, d, ly.self_norm, nb, d, a->eps, s)) != hipSuccess) break;
+        const bool last = l + 1 == a->n_dec_layers;
+        // self-attention over the single decoder token: o(v(norm(y))); the o projection also
+        // normalises y for the cross-attention
         if ((e = linear_on(xn, d, ly.self_v, inner, d, v, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_on(v, inner, ly.self_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
+        if ((e = linear_norm_on(v, inner, ly.self_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, ly.cross_norm, xn, d,
+                                a->eps, s)) != hipSuccess)
+            break;
         // cross-attention to the encoder output
-        if ((e = tsfm::launch_rms_norm(y, d, xn, d, ly.cross_norm, nb, d, a->eps, s)) != hipSuccess) break;
         if ((e = linear_on(xn, d, ly.cross_q, inner, d, q, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
         tsfm::ProjParams p{};
         p.x = x; p.x_tok = d; p.w0 = ly.cross_k; p.w1 = ly.cross_v; p.w_ld = d; p.alpha = 1.f;
@@ -994,13 +1021,15 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
         ap.key_valid = kv; ap.kv_batch = seq;
         ap.B = nb; ap.H = a->heads; ap.n_q = 1; ap.n_k = seq; ap.scale = 1.f;
         if ((e = tsfm::launch_attn_f32(ap, TSFM_MASK_KEYS_ADDITIVE, tsfm::BIAS_NONE, false, s)) != hipSuccess) break;
-        if ((e = linear_on(ab, inner, ly.cross_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
-        // FFN
-        if ((e = tsfm::launch_rms_norm(y, d, xn, d, ly.ffn_norm, nb, d, a->eps, s)) != hipSuccess) break;
+        if ((e = linear_norm_on(ab, inner, ly.cross_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, ly.ffn_norm, xn, d,
+                                a->eps, s)) != hipSuccess)
+            break;
+        // FFN; wo also normalises y for the next layer (or the final norm)
         if ((e = linear_on(xn, d, ly.wi, F, d, hb, F, nb, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
+        if ((e = linear_norm_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y,
+                                last ? dv.dec_final_norm : dv.dec[l + 1].self_norm, xn, d, a->eps, s)) != hipSuccess)
+            break;
     }
-    if (e == hipSuccess) e = tsfm::launch_rms_norm(y, d, xn, d, dv.dec_final_norm, nb, d, a->eps, s);
     if (e == hipSuccess) e = resblock_on(dv.oe, xn, nb, dv.raw, hb, rb, s);
     return e;
 }

@@ -165,4 +165,21 @@ __device__ __forceinline__ float sum4(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// nn.rmsNorm pieces shared by every kernel that normalises a row (one wave per row, lane l
+// holding the four-column groups 4 l, 4 l + 256, ...): the lane's running sum of squares, the
+// wave-wide total, and the scaled output x * inv * scale, left to right.
+__device__ inline float sumsq4(float ss, f32x4 v) { return ss + (v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]); }
+
+__device__ inline float rms_inv(float ss, int dim, float eps) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    return 1.0f / sqrtf(ss / (float)dim + eps);
+}
+
+__device__ inline f32x4 rms_apply(f32x4 x, float inv, f32x4 scale) {
+#pragma clang fp contract(off)
+    const f32x4 t = x * inv;
+    return t * scale;
+}
+
 }  // namespace tsfm

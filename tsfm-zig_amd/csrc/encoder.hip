@@ -18,19 +18,10 @@ __global__ __launch_bounds__(256) void rms_norm_rows(const float* x, int64_t x_t
     if (row >= rows) return;
     const float* xr = x + (int64_t)row * x_tok;
     float ss = 0.f;
-    for (int i = 4 * lane; i < dim; i += 256) {
-        const f32x4 v = ld4(xr + i);
-        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = 4 * lane; i < dim; i += 256) ss = sumsq4(ss, ld4(xr + i));
+    const float inv = rms_inv(ss, dim, eps);
     float* o = out + (int64_t)row * out_tok;
-    for (int i = 4 * lane; i < dim; i += 256) {
-#pragma clang fp contract(off)
-        const f32x4 t = ld4(xr + i) * inv;  // x * inv * scale, left to right like the Zig
-        st4(o + i, t * ld4(scale + i));
-    }
+    for (int i = 4 * lane; i < dim; i += 256) st4(o + i, rms_apply(ld4(xr + i), inv, ld4(scale + i)));
 }
 
 // Chronos-2 token sequence (src/chronos2/forecaster.zig:162-173): row li * seq + t of x is context

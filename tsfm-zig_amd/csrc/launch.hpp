@@ -64,6 +64,12 @@ struct ProjParams {
     int32_t m_tiles, n_tiles;  // set by launch_proj
     int32_t splits, split_steps;  // set by launch_proj: reduction split over workgroups (small products)
     float* partial;               // set by launch_proj: [splits][tokens][width] partial sums
+    // Optional row norm of the finished product (one f32 output): norm_out = rmsNorm(y0, norm_scale,
+    // norm_eps), the same arithmetic as launch_rms_norm; may be y0 itself.
+    const float* norm_scale;
+    float* norm_out;
+    int64_t norm_out_tok;
+    float norm_eps;
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 

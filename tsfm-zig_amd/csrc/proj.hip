@@ -225,6 +225,31 @@ __global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
     st4(y + (int64_t)m * y_tok + col, v);
 }
 
+// proj_reduce for one output followed by the row norm of the finished rows: one wave per token
+// row sums the partials of its four-column groups in split order, applies the epilogue, stores
+// y0, and keeps the row's sum of squares; then norm_out = y0 * inv * norm_scale. The row norm's
+// grouping and order are rms_norm_rows', so the result has the same bits as the two launches.
+__global__ __launch_bounds__(256) void proj_reduce_norm(ProjParams p) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= p.tokens) return;
+    const int W = p.width;
+    float* const y = static_cast<float*>(p.y0) + (int64_t)row * p.y0_tok;
+    float ss = 0.f;
+    for (int c = 4 * lane; c < W; c += 256) {
+        f32x4 v = ld4(p.partial + (int64_t)row * W + c);
+        for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + row) * W + c);
+        if (p.alpha != 1.f) v *= p.alpha;
+        if (p.bias != nullptr) v = v + ld4(p.bias + c);
+        if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
+        else if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)row * p.resid_tok + c) + v;
+        st4(y + c, v);
+        ss = sumsq4(ss, v);
+    }
+    const float inv = rms_inv(ss, W, p.norm_eps);
+    float* const o = p.norm_out + (int64_t)row * p.norm_out_tok;
+    for (int c = 4 * lane; c < W; c += 256) st4(o + c, rms_apply(ld4(y + c), inv, ld4(p.norm_scale + c)));
+}
+
 }  // namespace
 
 namespace {
@@ -265,7 +290,8 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         p.w_ld < p.d_in || p.width % 4 || (p.n_out > 1 && p.width % kHeadDim) ||
         (p.rope_cos != nullptr && p.width % kHeadDim) ||
         (p.out_dtype != 0 && (p.epi != kEpiNone || p.alpha != 1.f || p.bias != nullptr)) ||
-        (p.bias != nullptr && p.n_out != 1))
+        (p.bias != nullptr && p.n_out != 1) ||
+        (p.norm_scale != nullptr && (p.n_out != 1 || p.out_dtype != 0 || p.norm_out == nullptr)))
         return hipErrorInvalidValue;
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
@@ -298,12 +324,22 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     if (p.splits > 1) {
         hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)(blocks * p.splits)), dim3(NT), kProjLds, stream, p);
         hipError_t e = hipGetLastError();
-        if (e == hipSuccess) {
+        if (e == hipSuccess && p.norm_scale != nullptr) {
+            hipLaunchKernelGGL(proj_reduce_norm, dim3((unsigned)((p.tokens + 3) / 4)), dim3(256), 0, stream, p);
+            e = hipGetLastError();
+        } else if (e == hipSuccess) {
             const int64_t n = (int64_t)p.tokens * (p.width * p.n_out / 4);
             hipLaunchKernelGGL(proj_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p);
             e = hipGetLastError();
         }
         return e;
+    }
+    if (p.norm_scale != nullptr) {
+        hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_rms_norm(static_cast<const float*>(p.y0), p.y0_tok, p.norm_out, p.norm_out_tok, p.norm_scale,
+                               p.tokens, p.width, p.norm_eps, stream);
     }
     if (p.out_dtype == 1)
         hipLaunchKernelGGL(qkv_proj<1>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
