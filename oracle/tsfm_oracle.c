@@ -933,6 +933,28 @@ void orc_chronos2_forecast(size_t threads, float *out, const float *inputs, size
 /* ------------------------------------------------------------------------------------------ */
 /* Timestral (src/timestral/model.zig) */
 
+int orc_timestral_key_valid(uint8_t *key_valid, size_t *first_obs, const uint8_t *obs, size_t rows, size_t vall,
+                            size_t ne, size_t ps, int attend_missing) {
+    const size_t w = ne * ps, groups = vall ? rows / vall : 0;
+    for (size_t g = 0; g < groups; g++) first_obs[g] = ne;
+    for (size_t r = 0; r < rows; r++) {
+        const size_t g = r / vall;
+        int started = 0;
+        for (size_t p = 0; p < ne; p++) {
+            int ob = 0;
+            for (size_t i = 0; i < ps; i++) ob = ob || obs[r * w + p * ps + i] != 0;
+            if (ob && p < first_obs[g]) first_obs[g] = p;
+            started = started || ob;
+            key_valid[r * ne + p] = (uint8_t)(attend_missing ? (ob || started) : ob);
+        }
+    }
+    for (size_t g = 0; g < groups; g++)
+        if (first_obs[g] == ne) first_obs[g] = 0;
+    int all = 1;
+    for (size_t i = 0; i < rows * ne; i++) all = all && key_valid[i];
+    return all;
+}
+
 void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
                                size_t hd, size_t rope_dim, float theta, const size_t *first_obs) {
     const size_t half = hd / 2, sl = ne + h;

@@ -99,8 +99,6 @@ void orc_chronos2_time_attention(size_t threads, const float *q, const float *k,
                                  const uint8_t *key_valid, int keys_all_valid, size_t b, size_t seq,
                                  size_t d, size_t nh, size_t hd, float scale);
 
-/* Timestral RoPE tables (src/timestral/model.zig:180-188, 447-463): (groups, sl, hd/2).
- * first_obs: per group; rope_dim = rotated dims (partial RoPE). */
 /* nn.rmsNorm (src/core/nn.zig:361-396) and nn.relu (:436-444). out may equal x. */
 void orc_rms_norm(size_t threads, float *out, const float *x, size_t rows, size_t dim, const float *scale,
                   float eps);
@@ -162,6 +160,16 @@ void orc_bolt_forecast(size_t threads, float *out, const float *ctx, size_t stri
                        const float *enc_final_norm, const orc_bolt_dec_layer *dec, size_t n_dec,
                        const float *dec_final_norm, float eps, const orc_resblock *input_embed,
                        const orc_resblock *output_embed);
+/* Timestral key validity and first observed patch (src/timestral/model.zig:343-362). obs: (rows, w)
+ * observation bytes, w = ne * ps; key_valid: (rows, ne) out; first_obs: (rows / vall) out, the first
+ * patch with an observation in any row of the group, 0 when the group has none. With
+ * attend_missing a patch is valid once any earlier patch of its row was observed. Returns
+ * keys_all_valid. */
+int orc_timestral_key_valid(uint8_t *key_valid, size_t *first_obs, const uint8_t *obs, size_t rows, size_t vall,
+                            size_t ne, size_t ps, int attend_missing);
+/* Timestral RoPE tables (src/timestral/model.zig:180-188, 447-463): (groups, sl, hd/2) with
+ * sl = ne + h. Encoder token p sits at time p, decoder token j at time l + j, both relative to
+ * first_obs[g]; inv_freq is zero past rope_dim / 2 (partial RoPE). */
 void orc_timestral_rope_tables(float *cos_t, float *sin_t, size_t groups, size_t ne, size_t l, size_t h,
                                size_t hd, size_t rope_dim, float theta, const size_t *first_obs);
 /* Timestral TimeJob.rope (src/timestral/model.zig:558-577), in place on the fused qkv buffer. */

@@ -108,6 +108,8 @@ class Oracle:
         L.orc_chronos2_rope_tables.argtypes = [_vp, _vp, _sz, _sz, _f]
         L.orc_chronos2_rope.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz]
         L.orc_chronos2_time_attention.argtypes = [_sz, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _sz, _sz, _f]
+        L.orc_timestral_key_valid.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz, ctypes.c_int]
+        L.orc_timestral_key_valid.restype = ctypes.c_int
         L.orc_timestral_rope_tables.argtypes = [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _f, _vp]
         L.orc_timestral_rope.argtypes = [_sz, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz]
         L.orc_timestral_time_attention.argtypes = [_sz, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz]
@@ -277,6 +279,16 @@ class Oracle:
         fo = np.ascontiguousarray(first_obs, dtype=np.uintp)
         self.lib.orc_timestral_rope_tables(ptr(c), ptr(s), groups, ne, l, h, hd, rope_dim, theta, ptr(fo))
         return c, s
+
+    def timestral_key_valid(self, obs, rows, vall, ne, ps, attend_missing=True):
+        """(key_valid (rows, ne) uint8, first_obs (rows // vall) int, keys_all_valid bool)."""
+        obs = np.ascontiguousarray(obs, np.uint8)
+        assert obs.size == rows * ne * ps
+        kv = np.zeros(rows * ne, np.uint8)
+        fo = np.zeros(max(rows // vall, 1), np.uintp)
+        all_valid = self.lib.orc_timestral_key_valid(ptr(kv), ptr(fo), ptr(obs), rows, vall, ne, ps,
+                                                     int(attend_missing))
+        return kv.reshape(rows, ne), fo[: rows // vall].astype(np.int64), bool(all_valid)
 
     def timestral_rope(self, threads, qkv, cos_t, sin_t, rows, sl, vall, d, nh, hd):
         self.lib.orc_timestral_rope(threads, ptr(qkv), ptr(cos_t), ptr(sin_t), rows, sl, vall, d, nh, hd)

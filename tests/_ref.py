@@ -300,3 +300,85 @@ def bolt_model_forward_f64(feats, patch_valid, reg, dec_start, bias, b, n_patch,
         y = y + ad @ W(ly["cross_o"]).T
         y = y + np.maximum(rms_norm_f64(y, ly["ffn_norm"], eps) @ W(ly["wi"]).T, 0.0) @ W(ly["wo"]).T
     return resblock_f64(output_embed, rms_norm_f64(y, dec_final_norm, eps))
+
+
+# ---- Timestral (src/timestral/model.zig) written from the definitions --------------------------
+
+
+def timestral_positions(ne, l, h, first_obs_g):
+    """Time of every token of a group relative to its first observed patch: encoder token p sits at
+    p, decoder token j (index ne + j) at l + j."""
+    tok = np.arange(ne + h)
+    time = np.where(tok < ne, tok, l + (tok - ne))
+    return time - int(first_obs_g)
+
+
+def timestral_rope_tables_f64(groups, ne, l, h, hd, rope_dim, theta, first_obs):
+    """float64 (groups, ne + h, hd/2) cos and sin: frequency theta^(-2i/rope_dim) for i < rope_dim/2,
+    zero beyond (those dims are not rotated)."""
+    half = hd // 2
+    i = np.arange(half, dtype=np.float64)
+    inv = np.where(i < rope_dim // 2, theta ** (-2.0 * i / rope_dim), 0.0)
+    ang = np.stack([timestral_positions(ne, l, h, first_obs[g]).astype(np.float64)[:, None] * inv[None, :]
+                    for g in range(groups)])
+    return np.cos(ang), np.sin(ang), ang
+
+
+def timestral_rope_tables(groups, ne, l, h, hd, rope_dim, theta, first_obs):
+    """The float64 tables rounded once to float32, flattened as the kernels take them: an input
+    builder for the GPU tests that does not go through the oracle."""
+    c, s, _ = timestral_rope_tables_f64(groups, ne, l, h, hd, rope_dim, theta, first_obs)
+    return c.astype(np.float32).ravel(), s.astype(np.float32).ravel()
+
+
+def timestral_rope_f64(qkv, cos_t, sin_t, rows, sl, vall, d, nh, hd):
+    """Rotate-half RoPE of every head of q and k (parts 0 and 1 of the (token, qkv, head, hd)
+    layout) in float64; row r uses its group's table, g = r // vall."""
+    half = hd // 2
+    x = np.asarray(qkv, np.float64).reshape(rows, sl, 3, nh, hd).copy()
+    c = np.asarray(cos_t, np.float64).reshape(-1, sl, half)
+    s = np.asarray(sin_t, np.float64).reshape(-1, sl, half)
+    for r in range(rows):
+        cg, sg = c[r // vall][:, None, :], s[r // vall][:, None, :]
+        for part in (0, 1):
+            lo, hi = x[r, :, part, :, :half].copy(), x[r, :, part, :, half:].copy()
+            x[r, :, part, :, :half] = lo * cg - hi * sg
+            x[r, :, part, :, half:] = hi * cg + lo * sg
+    return x.ravel()
+
+
+def timestral_key_valid(obs, rows, vall, ne, ps, attend_missing=True):
+    """(key_valid (rows, ne), first_obs (groups,), keys_all_valid): a patch is observed when any of
+    its steps is; with attend_missing, every patch from a row's first observed patch on is valid.
+    first_obs is the earliest observed patch over the rows of a group, 0 if it has none."""
+    patch = np.asarray(obs, bool).reshape(rows, ne, ps).any(axis=2)
+    kv = np.logical_or.accumulate(patch, axis=1) if attend_missing else patch
+    groups = rows // vall
+    gp = patch.reshape(groups, vall, ne).any(axis=1)
+    first = np.where(gp.any(axis=1), gp.argmax(axis=1), 0)
+    return kv.astype(np.uint8), first.astype(np.int64), bool(kv.all())
+
+
+# ---- the f32 parity bar, derived from the reference itself ---------------------------------------
+
+
+def reference_bar(lane8, lane16, exact=None):
+    """The f32 bar for a GPU result compared with the 16-lane oracle, and its two ingredients.
+
+    The reference computes in f32 with nn.lanes partial sums (src/core/nn.zig:296): 8 on an AVX2
+    host, 16 on an AVX-512 host, so its own output moves with the host by s = |lane8 - lane16|.
+    With a float64 evaluation `exact`, m = the larger distance of the two builds from it. An f32
+    evaluation as accurate as the reference on its worse host is within m of exact, hence within
+    2m of the 16-lane build (triangle inequality). Without `exact`, s stands in for m (s <= 2m;
+    for independent rounding s ~ 1.4 m). Bar = max(1e-5, 2 max(s, m)): never tighter than the
+    north star's 1e-5, never looser than the reference's own cross-host floor needs."""
+    s = scaled_err(lane8, lane16)
+    m = 0.0 if exact is None else max(scaled_err(lane8, exact), scaled_err(lane16, exact))
+    return max(1e-5, 2.0 * max(s, m)), s, m
+
+
+def assert_within_reference_bar(got, lane8, lane16, exact=None):
+    bar, s, m = reference_bar(lane8, lane16, exact)
+    err = scaled_err(got, lane16)
+    assert err <= bar, f"GPU vs 16-lane oracle {err:.3e} > bar {bar:.3e} (cross-host spread {s:.3e}, f64 {m:.3e})"
+    return err, bar

@@ -5,13 +5,14 @@ against the oracle's restatements of Model.encode (src/chronos2/model.zig:144-20
 C ABI.
 
 A stack of layers composes many f32 reductions: the GPU's and the oracle's summation orders
-differ, and both differ from exact arithmetic by about as much. The bar is therefore twofold:
-the GPU result is within 5e-5 scaled error of the oracle's, and no further from float64 than
-twice the oracle's own distance (plus 1e-6). Covered: scale 1/8 and the model's 1.0, padded and
-all-valid keys (FULL and KEYS_ADDITIVE masks give the same result when every key is valid), no
-layers (final norm only), host and device pointers (same bits), a Chronos-2-base shaped run
-(d 768, 12 heads, d_ff 3072, 577 tokens), and twelve layers, where the bar against float64 is 4x
-the oracle's own drift. The whole forecast (tsfm_chronos2_forecast: instance norm, time-encoded
+differ, and both differ from exact arithmetic by about as much. The bar is _ref.reference_bar:
+against the oracle's 16-lane (AVX-512) build, twice the larger of the reference's own cross-host
+spread (its 8-lane build against its 16-lane build) and the reference's distance from float64
+where a float64 evaluation exists, and never tighter than 1e-5. Covered: scale 1/8 and the
+model's 1.0, padded and all-valid keys (FULL and KEYS_ADDITIVE masks give the same result when
+every key is valid), no layers (final norm only), host and device pointers (same bits), a
+Chronos-2-base shaped run (d 768, 12 heads, d_ff 3072, 577 tokens), and twelve layers.
+The whole forecast (tsfm_chronos2_forecast: instance norm, time-encoded
 patch features, the model, inverse scaling) against the oracle's runChunk on whole, padded and
 sub-patch contexts, cut horizons, asinh space on and off, strided rows, a constant and an
 all-missing series.
@@ -43,19 +44,23 @@ def _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, scal
     return want
 
 
+def _both(orc, orc16, *args):
+    """The oracle's 8-lane and 16-lane results of the same call."""
+    return _oracle(orc, *args), _oracle(orc16, *args)
+
+
 @pytest.mark.parametrize("scale", [0.125, 1.0])
 @pytest.mark.parametrize("pad", [True, False])
-def test_encode_matches_oracle_and_f64(ta, orc, gpu_ready, scale, pad):
+def test_encode_matches_oracle_and_f64(ta, orc, orc16, gpu_ready, scale, pad):
     b, seq, nh, d_ff, n_layers, eps = 3, 45, 2, 256, 3, 1e-6
     x, kv, layers, fn, d = _setup(int(scale * 8) + 10 * pad, b, seq, nh, d_ff, n_layers, pad)
     cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
     got = x.copy()
     rc = ta.chronos2_encode(got, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=scale)
     assert rc == ta.OK, ta.last_error()
-    want = _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, scale)
+    w8, w16 = _both(orc, orc16, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, scale)
     exact = _ref.chronos2_encode_f64(x, kv, b, seq, nh, layers, fn, eps, cos_t, sin_t, scale)
-    assert _ref.scaled_err(got, want) <= 5e-5
-    assert _ref.scaled_err(got, exact) <= 2 * _ref.scaled_err(want, exact) + 1e-6
+    _ref.assert_within_reference_bar(got, w8, w16, exact)
     if not pad:  # every key valid: the KEYS_ADDITIVE mask (keys_all_valid=False) gives the same bits
         again = x.copy()
         rc = ta.chronos2_encode(again, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=scale,
@@ -91,7 +96,7 @@ def test_encode_device_pointers_match_host(ta, orc, gpu_ready):
     assert np.array_equal(xd.cpu().numpy(), host)
 
 
-def test_encode_chronos2_base_shape(ta, orc, gpu_ready):
+def test_encode_chronos2_base_shape(ta, orc, orc16, gpu_ready):
     """d_model 768, 12 heads, d_ff 3072 over 577 tokens (512 context patches, REG, 64 future), two
     layers of the model's scale 1.0."""
     b, seq, nh, d_ff, n_layers, eps = 2, 577, 12, 3072, 2, 1e-6
@@ -100,25 +105,23 @@ def test_encode_chronos2_base_shape(ta, orc, gpu_ready):
     got = x.copy()
     rc = ta.chronos2_encode(got, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=1.0)
     assert rc == ta.OK, ta.last_error()
-    want = _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, 1.0)
-    assert _ref.scaled_err(got, want) <= 5e-5
+    w8, w16 = _both(orc, orc16, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, 1.0)
+    _ref.assert_within_reference_bar(got, w8, w16)
 
 
-def test_encode_twelve_layers_drift_like_the_oracle(ta, orc, gpu_ready):
+def test_encode_twelve_layers_drift_like_the_oracle(ta, orc, orc16, gpu_ready):
     """Twelve Chronos-2-base layers at the model's scale 1.0: every f32 evaluation drifts from the
-    exact result with depth. The GPU stack stays within 4x the oracle's own distance from float64
-    (one accumulator per linear output against the oracle's sixteen lane sums and a tree)."""
+    exact result with depth, the reference's own included; the bar follows it."""
     b, seq, nh, d_ff, n_layers, eps = 1, 145, 12, 3072, 12, 1e-6
     x, kv, layers, fn, d = _setup(12, b, seq, nh, d_ff, n_layers)
     cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
     got = x.copy()
     rc = ta.chronos2_encode(got, kv, cos_t, sin_t, layers, fn, b, seq, d, nh, d_ff, eps, scale=1.0)
     assert rc == ta.OK, ta.last_error()
-    want = _oracle(orc, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, 1.0)
+    w8, w16 = _both(orc, orc16, x, kv, layers, fn, b, seq, d, nh, d_ff, eps, cos_t, sin_t, 1.0)
     exact = _ref.chronos2_encode_f64(x, kv, b, seq, nh, layers, fn, eps, cos_t, sin_t, 1.0)
-    e_orc = _ref.scaled_err(want, exact)
-    assert e_orc < 5e-4  # the f32 reference path itself, for scale
-    assert _ref.scaled_err(got, exact) <= 4 * e_orc + 1e-6
+    assert _ref.scaled_err(w16, exact) < 5e-4  # the f32 reference path itself, for scale
+    _ref.assert_within_reference_bar(got, w8, w16, exact)
 
 
 # ---- the model part of the Chronos-2 forecaster: embedding, encoder, output head ------------------
@@ -138,7 +141,7 @@ def _forward_setup(seed, b, n_ctx, n_out, nh, d_ff, n_layers, ps=16, q=3):
 
 
 @pytest.mark.parametrize("b,n_ctx,n_out", [(3, 20, 4), (2, 64, 8)])
-def test_forward_matches_oracle_and_f64(ta, orc, gpu_ready, b, n_ctx, n_out):
+def test_forward_matches_oracle_and_f64(ta, orc, orc16, gpu_ready, b, n_ctx, n_out):
     nh, d_ff, n_layers, eps, q, ps = 2, 256, 2, 1e-6, 3, 16
     feats, fut, cv, reg, layers, fn, ie, oe, d = _forward_setup(b + n_ctx, b, n_ctx, n_out, nh, d_ff, n_layers)
     seq = n_ctx + 1 + n_out
@@ -147,13 +150,15 @@ def test_forward_matches_oracle_and_f64(ta, orc, gpu_ready, b, n_ctx, n_out):
     rc = ta.chronos2_forward(raw, feats, fut, cv, reg, cos_t, sin_t, layers, fn, ie, oe, b, n_ctx, n_out, d, nh, d_ff,
                              eps)
     assert rc == ta.OK, ta.last_error()
-    want = np.zeros_like(raw)
-    orc.chronos2_model_forward(THREADS, want, feats, fut, cv, reg, b, n_ctx, n_out, d, nh, 64, d_ff, layers, fn, eps,
-                               cos_t, sin_t, 1.0, ie, oe)
+    outs = []
+    for o_ in (orc, orc16):
+        want = np.zeros_like(raw)
+        o_.chronos2_model_forward(THREADS, want, feats, fut, cv, reg, b, n_ctx, n_out, d, nh, 64, d_ff, layers, fn, eps,
+                                  cos_t, sin_t, 1.0, ie, oe)
+        outs.append(want)
     exact = _ref.chronos2_model_forward_f64(feats, fut, cv, reg, b, n_ctx, n_out, nh, layers, fn, eps, cos_t, sin_t,
                                             1.0, ie, oe)
-    assert _ref.scaled_err(raw, want) <= 5e-5
-    assert _ref.scaled_err(raw, exact) <= 2 * _ref.scaled_err(want, exact) + 1e-6
+    _ref.assert_within_reference_bar(raw, *outs, exact)
 
 
 def test_forward_device_pointers_match_host(ta, orc, gpu_ready):
@@ -215,7 +220,7 @@ def _c2_forecast_oracle(orc, c, inputs, n, length, horizon, nh, d_ff, arcsinh, t
 
 
 @pytest.mark.parametrize("length,horizon,arcsinh", [(160, 64, True), (150, 20, True), (9, 16, False)])
-def test_chronos2_forecast_matches_oracle(ta, orc, gpu_ready, length, horizon, arcsinh):
+def test_chronos2_forecast_matches_oracle(ta, orc, orc16, gpu_ready, length, horizon, arcsinh):
     """Whole patches (160), left padding (150) and less than one patch (9); horizons that fill and
     that cut the last future patch; the model's asinh space on and off; ~10 % missing values."""
     nh, d_ff, n, tsc = 2, 256, 4, 8192.0
@@ -224,12 +229,12 @@ def test_chronos2_forecast_matches_oracle(ta, orc, gpu_ready, length, horizon, a
     x = (5.0 + 3.0 * rng.standard_normal((n, length))).astype(np.float32)
     x[rng.random((n, length)) < 0.1] = np.nan
     got = _c2_forecast(ta, c, x, n, length, horizon, nh, d_ff, arcsinh, tsc)
-    want = _c2_forecast_oracle(orc, c, x, n, length, horizon, nh, d_ff, arcsinh, tsc)
+    w8, w16 = (_c2_forecast_oracle(o_, c, x, n, length, horizon, nh, d_ff, arcsinh, tsc) for o_ in (orc, orc16))
     assert np.isfinite(got).all()
-    assert _ref.scaled_err(got, want) <= 5e-5
+    _ref.assert_within_reference_bar(got, w8, w16)
 
 
-def test_chronos2_forecast_strided_rows_and_degenerate_series(ta, orc, gpu_ready):
+def test_chronos2_forecast_strided_rows_and_degenerate_series(ta, orc, orc16, gpu_ready):
     """Rows at a stride and start offset in a wider buffer (as forecast() reads the last
     context_length steps of each (b, t_in) row); a constant series (scale 1e-5) and an all-missing
     one (loc 0, scale 1, no valid context patch: only REG and the future patches are attended)."""
@@ -242,6 +247,7 @@ def test_chronos2_forecast_strided_rows_and_degenerate_series(ta, orc, gpu_ready
     rows()[2][:] = np.nan
     rows()[3][1::4] = np.nan
     got = _c2_forecast(ta, c, buf, n, length, horizon, nh, d_ff, True, tsc, stride=stride, start=start)
-    want = _c2_forecast_oracle(orc, c, buf, n, length, horizon, nh, d_ff, True, tsc, stride=stride, start=start)
+    w8, w16 = (_c2_forecast_oracle(o_, c, buf, n, length, horizon, nh, d_ff, True, tsc, stride=stride, start=start)
+               for o_ in (orc, orc16))
     assert np.isfinite(got).all()
-    assert _ref.scaled_err(got, want) <= 5e-5
+    _ref.assert_within_reference_bar(got, w8, w16)

@@ -179,18 +179,16 @@ def _c2_oracle(orc, w, B):
 
 
 # Scale-1.0 parity. With q, k ~ N(0, 1) and D = 64 unscaled, logits have standard deviation 8 and
-# the softmax amplifies last-bit differences of the 64-term dot products: the oracle (the
-# reference's f32 arithmetic) is itself 1.25e-5 (Chronos-2, 64 series) and 1.16e-5 (Bolt, 256
-# series) from float64 attention on these inputs, so two correct f32 evaluations can differ by up
-# to the sum of their errors. The bar there is accuracy against exact arithmetic: the GPU must be
-# no further from float64 than the reference's own arithmetic (measured on the same series), and
-# within 2.5e-5 of the oracle. At scale 1/8 (the benchmarked shape) the reference is 8e-7 from
-# float64 and the 1e-5 bar applies directly against the oracle.
-TOL_UNSCALED = 2.5e-5
+# the softmax amplifies last-bit differences of the 64-term dot products: the reference's own
+# output moves by ~1.2e-5 between its 8-lane (AVX2) and 16-lane (AVX-512) builds on these inputs.
+# The bar is _ref.reference_bar: twice the larger of that cross-host spread and the reference's
+# distance from float64 (at least 1e-5), against the 16-lane build; the GPU must also be no further
+# from float64 than the reference's worse build. At scale 1/8 (the benchmarked shape) the spread
+# is far below 1e-5 and the bar is the north star's 1e-5.
 
 
 @pytest.mark.parametrize("scale", [0.125, 1.0])
-def test_chronos2_time_attention_full_shape(ta, orc_host, gpu_ready, scale):
+def test_chronos2_time_attention_full_shape(ta, orc, orc16, gpu_ready, scale):
     """Chronos-2 time attention at B=64, H=12, L=577 (RoPE, left-padding mask), scale 1/sqrt(64)
     as benchmarked and 1.0 as the model calls it (src/chronos2/model.zig:306)."""
     from tsfm_attn import workloads
@@ -201,20 +199,23 @@ def test_chronos2_time_attention_full_shape(ta, orc_host, gpu_ready, scale):
     rc = ta.chronos2_time_attention(a["q"], a["k"], a["v"], o, a["rope_cos"], a["rope_sin"], a["key_valid"],
                                     bool(a["key_valid"].all()), w.B, w.n_q, w.H * 64, w.H, 64, scale=scale)
     assert rc == ta.OK, ta.last_error()
-    want, q_rot, k_rot = _c2_oracle(orc_host, w, w.B)
-    err = _ref.scaled_err(o, want)
+    want16, q_rot, k_rot = _c2_oracle(orc16, w, w.B)
+    want8, _, _ = _c2_oracle(orc, w, w.B)
     if scale != 1.0:
-        assert err <= TOL
+        _ref.assert_within_reference_bar(o, want8, want16)
         return
-    assert err <= TOL_UNSCALED
-    gpu_f64, orc_f64 = _ref.f64_errors([o, want], q_rot, k_rot, a["v"], a["key_valid"], 16, w.H, w.n_q, scale)
-    assert gpu_f64 <= orc_f64, (gpu_f64, orc_f64)
+    # float64 attention over the first 16 series
+    gpu_f64, o8_f64, o16_f64 = _ref.f64_errors([o, want8, want16], q_rot, k_rot, a["v"], a["key_valid"], 16, w.H,
+                                               w.n_q, scale)
+    bar = max(_ref.reference_bar(want8, want16)[0], 2.0 * max(o8_f64, o16_f64))
+    assert _ref.scaled_err(o, want16) <= bar
+    assert gpu_f64 <= max(o8_f64, o16_f64), (gpu_f64, o8_f64, o16_f64)
 
 
-def test_bolt_self_attention_full_shape(ta, orc_host, gpu_ready):
+def test_bolt_self_attention_full_shape(ta, orc, orc16, gpu_ready):
     """Chronos-Bolt-base encoder self-attention at B=256, H=12, L=129 with the T5 bias built on the
     device from the (32, 12) table, against the oracle's positionBias + SelfJob (scale 1.0: the
-    accuracy bar above)."""
+    reference-derived bar above)."""
     from tsfm_attn import workloads
 
     w = workloads.bolt()
@@ -226,14 +227,19 @@ def test_bolt_self_attention_full_shape(ta, orc_host, gpu_ready):
     rc = ta.bolt_self_attention(a["q"], a["k"], a["v"], o, a["rel_table"], buckets, a["key_valid"],
                                 bool(a["key_valid"].all()), w.B, L, d, H, 64, 32)
     assert rc == ta.OK, ta.last_error()
-    bias = orc_host.position_bias(a["rel_table"], L, H, 32, 128)
-    want = np.zeros_like(a["q"])
-    orc_host.bolt_self_attention(THREADS, a["q"], a["k"], a["v"], want, bias, a["key_valid"],
-                                 bool(a["key_valid"].all()), w.B, L, d, H, 64)
-    assert _ref.scaled_err(o, want) <= TOL_UNSCALED
-    gpu_f64, orc_f64 = _ref.f64_errors([o, want], a["q"], a["k"], a["v"], a["key_valid"], w.B, H, L, 1.0,
-                                       bias.reshape(H, L, L))
-    assert gpu_f64 <= orc_f64, (gpu_f64, orc_f64)
+    bias = orc16.position_bias(a["rel_table"], L, H, 32, 128)
+    outs = []
+    for o_ in (orc, orc16):
+        want = np.zeros_like(a["q"])
+        o_.bolt_self_attention(THREADS, a["q"], a["k"], a["v"], want, bias, a["key_valid"],
+                               bool(a["key_valid"].all()), w.B, L, d, H, 64)
+        outs.append(want)
+    want8, want16 = outs
+    gpu_f64, o8_f64, o16_f64 = _ref.f64_errors([o, want8, want16], a["q"], a["k"], a["v"], a["key_valid"], w.B, H, L,
+                                               1.0, bias.reshape(H, L, L))
+    bar = max(_ref.reference_bar(want8, want16)[0], 2.0 * max(o8_f64, o16_f64))
+    assert _ref.scaled_err(o, want16) <= bar
+    assert gpu_f64 <= max(o8_f64, o16_f64), (gpu_f64, o8_f64, o16_f64)
     # The dense-bias path (positionBias materialised by the caller) gives the same result.
     o2 = np.zeros_like(a["q"])
     ta.fwd_checked(ta.make_args(q=a["q"], k=a["k"], v=a["v"], o=o2, mask=ta.Mask.KEYS_ADDITIVE, batch=w.B, heads=H,
@@ -269,7 +275,7 @@ def test_timestral_time_attention_f32(ta, orc, gpu_ready, all_valid):
     kv = np.ones((rows, ne), np.uint8) if all_valid else _ref.left_pad_valid(rng, rows, ne, 12)
     bidir = np.array([0, 0, 1, 0, 1, 1], np.uint8)
     first_obs = [0, 5]
-    cos_t, sin_t = orc.timestral_rope_tables(rows // vall, ne, l, h, hd, hd // 2, 10000.0, first_obs)
+    cos_t, sin_t = _ref.timestral_rope_tables(rows // vall, ne, l, h, hd, hd // 2, 10000.0, first_obs)
     o = np.zeros(rows * sl * d, np.float32)
     rc = ta.timestral_time_attention(qkv, o, cos_t, sin_t, kv, all_valid, bidir, rows, vall, ne, l, h, d, nh, hd)
     assert rc == ta.OK, ta.last_error()

@@ -126,7 +126,7 @@ def test_half_timestral_layout_with_rope(ta, orc, gpu_ready, name):
     qkv32 = rng.standard_normal(rows * sl * 3 * d).astype(np.float32)
     kv = _ref.left_pad_valid(rng, rows, ne, 20)
     bidir = np.array([0, 1, 0, 0, 1, 0], np.uint8)
-    cos_t, sin_t = orc.timestral_rope_tables(rows // vall, ne, l, h, hd, hd // 2, 10000.0, [0, 7])
+    cos_t, sin_t = _ref.timestral_rope_tables(rows // vall, ne, l, h, hd, hd // 2, 10000.0, [0, 7])
     qkv_d, qkv_r = _dev(qkv32, name)
     o_d = torch.zeros(rows * sl * d, dtype=_tdtype(name), device="cuda")
     tab = {n: torch.from_numpy(x).cuda() for n, x in (("c", cos_t), ("s", sin_t))}

@@ -80,7 +80,7 @@ def test_timestral_projection_matches_oracle(ta, orc, gpu_ready, gated):
     x = rng.standard_normal((rows * sl, d)).astype(np.float32)
     w_qkv = (rng.standard_normal((3 * d, d)) / np.sqrt(d)).astype(np.float32)
     w_gate = (rng.standard_normal((d, d)) / np.sqrt(d)).astype(np.float32) if gated else None
-    cos_t, sin_t = orc.timestral_rope_tables(groups, ne, l, h, 64, 32, 10000.0, [5, 0])
+    cos_t, sin_t = _ref.timestral_rope_tables(groups, ne, l, h, 64, 32, 10000.0, [5, 0])
     qkv = np.full((rows * sl, 3 * d), -3.0, np.float32)
     gate = np.full((rows * sl, d), -3.0, np.float32) if gated else None
     rc = ta.timestral_qkv_projection(x, w_qkv, qkv, cos_t, sin_t, rows, vall, sl, d, nh, 64, w_gate=w_gate,
@@ -153,7 +153,7 @@ def test_half_outputs_round_the_f32_result(ta, orc, gpu_ready, out, device):
     x = rng.standard_normal((rows * sl, d)).astype(np.float32)
     w_qkv = (rng.standard_normal((3 * d, d)) / np.sqrt(d)).astype(np.float32)
     w_gate = (rng.standard_normal((d, d)) / np.sqrt(d)).astype(np.float32)
-    cos_t, sin_t = orc.timestral_rope_tables(groups, ne, l, h, 64, 32, 10000.0, [3, 0])
+    cos_t, sin_t = _ref.timestral_rope_tables(groups, ne, l, h, 64, 32, 10000.0, [3, 0])
     dt = getattr(torch, out)
     qkv = torch.full((rows * sl, 3 * d), -3.0, dtype=dt)
     gate = torch.full((rows * sl, d), -3.0, dtype=dt)

@@ -744,3 +744,89 @@ def test_chronos2_forecast_preparation_and_inverse_scaling(orc, arcsinh):
     # arcsinh / sinh: libm's single-precision functions against numpy's double ones (an ulp or two).
     tol = 2e-6 if arcsinh else 1e-6
     assert np.allclose(got, want, rtol=tol, atol=tol * np.abs(want).max())
+
+
+# ---- Timestral validity, first observation and partial RoPE (src/timestral/model.zig) -----------
+
+
+@pytest.mark.parametrize("attend_missing", [True, False])
+def test_timestral_key_valid_matches_definition(orc, attend_missing):
+    """model.zig:343-362 against the numpy definition, on random observation masks with leading
+    gaps, inner gaps and an all-missing row and group."""
+    rng = np.random.default_rng(31)
+    rows, vall, ne, ps = 12, 3, 9, 4
+    obs = rng.random((rows, ne * ps)) < 0.15
+    obs[0:3] = False                       # group 0 has no observation at all
+    obs[4, :] = False                      # one all-missing row in an observed group
+    obs[6, : 5 * ps] = False               # leading gap
+    got_kv, got_first, got_all = orc.timestral_key_valid(obs, rows, vall, ne, ps, attend_missing)
+    kv, first, all_valid = _ref.timestral_key_valid(obs, rows, vall, ne, ps, attend_missing)
+    assert np.array_equal(got_kv, kv)
+    assert np.array_equal(got_first, first)
+    assert got_all == all_valid
+
+
+def test_timestral_key_valid_hand_case(orc):
+    """A case written out by hand: ps = 2, two groups of two rows.
+    Row 0: patches (0,0) (1,0) (0,0) -> observed F T F; row 1: (0,0) (0,0) (0,1) -> F F T;
+    group 0's first observed patch is 1. Group 1 (rows 2, 3) has no observation: first_obs 0."""
+    obs = np.array([[0, 0, 1, 0, 0, 0],
+                    [0, 0, 0, 0, 0, 1],
+                    [0, 0, 0, 0, 0, 0],
+                    [0, 0, 0, 0, 0, 0]], np.uint8)
+    kv, first, all_valid = orc.timestral_key_valid(obs, 4, 2, 3, 2, True)
+    assert kv.tolist() == [[0, 1, 1], [0, 0, 1], [0, 0, 0], [0, 0, 0]]
+    assert first.tolist() == [1, 0] and not all_valid
+    kv, first, _ = orc.timestral_key_valid(obs, 4, 2, 3, 2, False)
+    assert kv.tolist() == [[0, 1, 0], [0, 0, 1], [0, 0, 0], [0, 0, 0]]
+    assert first.tolist() == [1, 0]
+    kv, first, all_valid = orc.timestral_key_valid(np.ones((2, 6), np.uint8), 2, 1, 3, 2, False)
+    assert kv.all() and all_valid and first.tolist() == [0, 0]
+
+
+@pytest.mark.parametrize("ne,l,h", [(20, 20, 6), (26, 20, 6)])
+def test_timestral_rope_tables_match_definition(orc, ne, l, h):
+    """model.zig:180-188, 447-463 against float64 tables from the definition. ne > l is the covariate
+    window (decoder token j at time l + j, not ne + j). first_obs differs per group and exceeds some
+    positions (negative times). Past rope_dim / 2 the tables are exactly cos 1, sin 0."""
+    groups, hd, rope_dim, theta = 3, 64, 32, 10000.0
+    first_obs = [0, 7, 25]
+    c, s = orc.timestral_rope_tables(groups, ne, l, h, hd, rope_dim, theta, first_obs)
+    c64, s64, ang = _ref.timestral_rope_tables_f64(groups, ne, l, h, hd, rope_dim, theta, first_obs)
+    c = c.reshape(c64.shape)
+    s = s.reshape(s64.shape)
+    # f32 frequencies and products: relative error of the angle a few 1e-7
+    tol = 1e-6 * (1.0 + np.abs(ang))
+    assert np.all(np.abs(c - c64) <= tol) and np.all(np.abs(s - s64) <= tol)
+    assert np.all(c[:, :, rope_dim // 2:] == 1.0) and np.all(s[:, :, rope_dim // 2:] == 0.0)
+    # the decoder's time base is visible at i = 0 (frequency 1): a table built with ne + j instead
+    # of l + j, or with +first_obs, would miss these by O(1)
+    for g in range(groups):
+        for j in range(h):
+            assert abs(float(c[g, ne + j, 0]) - np.cos(l + j - first_obs[g])) <= 1e-5
+
+
+def test_timestral_rope_application(orc):
+    """TimeJob.rope (model.zig:558-577) against a float64 rotation with each row's group table
+    (g = r // vall): q and k of every head rotated, v untouched, and the dims past rope_dim / 2 (and
+    their partners) bit-identical."""
+    rng = np.random.default_rng(32)
+    rows, vall, ne, l, h, nh, hd, rope_dim = 6, 2, 12, 12, 4, 3, 64, 32
+    d, sl = nh * hd, ne + h
+    first_obs = [0, 5, 9]
+    c, s = orc.timestral_rope_tables(rows // vall, ne, l, h, hd, rope_dim, 10000.0, first_obs)
+    qkv = rng.standard_normal(rows * sl * 3 * d).astype(np.float32)
+    got = qkv.copy()
+    orc.timestral_rope(4, got, c, s, rows, sl, vall, d, nh, hd)
+    want = _ref.timestral_rope_f64(qkv, c, s, rows, sl, vall, d, nh, hd)
+    assert np.max(np.abs(got - want)) <= 2e-6 * max(1.0, np.max(np.abs(want)))
+    g5 = got.reshape(rows, sl, 3, nh, hd)
+    x5 = qkv.reshape(rows, sl, 3, nh, hd)
+    assert np.array_equal(g5[:, :, 2], x5[:, :, 2])
+    keep = np.r_[rope_dim // 2: hd // 2, hd // 2 + rope_dim // 2: hd]
+    assert np.array_equal(g5[..., keep], x5[..., keep])
+    # rotating with another group's table (a wrong g) would differ: rows 0 and 2 share tokens
+    # but not tables
+    assert not np.allclose(g5[0, :, 0], _ref.timestral_rope_f64(qkv, np.roll(c.reshape(3, -1), 1, 0).ravel(),
+                                                                 np.roll(s.reshape(3, -1), 1, 0).ravel(), rows, sl,
+                                                                 vall, d, nh, hd).reshape(rows, sl, 3, nh, hd)[0, :, 0])

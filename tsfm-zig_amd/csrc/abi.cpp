@@ -79,7 +79,18 @@ struct ThreadCtx {
     hipStream_t stream = nullptr;
     void* buf = nullptr;
     size_t cap = 0;
+    // Split-partials buffers of this thread's device-pointer projections, one per (device, caller
+    // stream). Per thread, so that two threads queuing on one stream (the null stream,
+    // hipStreamPerThread) never share a buffer between a product and its reduce.
+    struct SplitBuf {
+        int device;
+        hipStream_t stream;
+        float* buf;
+    };
+    std::vector<SplitBuf> splits;
 };
+
+constexpr size_t kMaxSplitBufs = 8;  // per thread; more streams take a stream-ordered buffer per call
 
 pthread_key_t g_ctx_key;
 pthread_once_t g_ctx_once = PTHREAD_ONCE_INIT;
@@ -89,6 +100,12 @@ void destroy_ctx(void* ptr) {
     if (c == nullptr) return;
     if (c->stream != nullptr) (void)hipStreamDestroy(c->stream);
     if (c->buf != nullptr) (void)hipFree(c->buf);
+    // hipFree waits for the device's queued work, so a product still queued on a caller's stream
+    // has finished with its partials before they are released.
+    for (const ThreadCtx::SplitBuf& b : c->splits) {
+        (void)hipSetDevice(b.device);
+        (void)hipFree(b.buf);
+    }
     delete c;
 }
 
@@ -119,6 +136,31 @@ int ensure_buf(ThreadCtx* c, size_t bytes) {
     c->buf = next;
     c->cap = bytes;
     return TSFM_OK;
+}
+
+// The split-partials buffer for a device-pointer projection queued on `stream` by this thread:
+// the thread's kept buffer for (device, stream), made on first use; past kMaxSplitBufs streams, a
+// stream-ordered allocation that the caller releases with hipFreeAsync after queuing (*owned).
+hipError_t split_buf_for(ThreadCtx* c, hipStream_t stream, float** out, bool* owned) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    *owned = false;
+    for (const ThreadCtx::SplitBuf& b : c->splits)
+        if (b.device == device && b.stream == stream) {
+            *out = b.buf;
+            return hipSuccess;
+        }
+    void* buf = nullptr;
+    if (c->splits.size() >= kMaxSplitBufs) {
+        if ((e = hipMallocAsync(&buf, tsfm::kSplitWorkspaceBytes, stream)) != hipSuccess) return e;
+        *owned = true;
+    } else {
+        if ((e = hipMalloc(&buf, tsfm::kSplitWorkspaceBytes)) != hipSuccess) return e;
+        c->splits.push_back({device, stream, static_cast<float*>(buf)});
+    }
+    *out = static_cast<float*>(buf);
+    return hipSuccess;
 }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -486,8 +528,17 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
                               a->rope_sin};
         for (const void* q : ptrs)
             if (q != nullptr && !aligned(q, 16)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
-        e = tsfm::launch_proj(p, static_cast<hipStream_t>(a->stream));
+        hipStream_t s = static_cast<hipStream_t>(a->stream);
+        float* part = nullptr;
+        bool owned = false;
+        if ((e = split_buf_for(ctx, s, &part, &owned)) != hipSuccess) return hip_fail(e, "split workspace");
+        {
+            tsfm::SplitWorkspace ws(part);
+            e = tsfm::launch_proj(p, s);
+        }
+        const hipError_t f = owned ? hipFreeAsync(part, s) : hipSuccess;
         if (e != hipSuccess) return hip_fail(e, "projection launch");
+        if (f != hipSuccess) return hip_fail(f, "split workspace release");
         return TSFM_OK;
     }
     // Host pointers: stage x, the weights and the tables, run, copy the output rows back.
@@ -507,11 +558,12 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     size_t w_at[4], y_at[4];
     for (int i = 0; i < 4; i++) w_at[i] = plan.take(i < 3 || gated ? w_n : 0);
     for (int i = 0; i < 4; i++) y_at[i] = plan.take(y_n[i]);
-    const size_t c_at = plan.take(t_n), s_at = plan.take(t_n);
+    const size_t c_at = plan.take(t_n), s_at = plan.take(t_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
     rc = ensure_buf(ctx, plan.off);
     if (rc != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
+    tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
     const float* w_src[4] = {a->w_q, a->w_k, a->w_v, a->w_gate};
     struct Up { const void* src; size_t at, n; } ups[] = {
         {a->x, x_at, x_n}, {w_src[0], w_at[0], w_n}, {w_src[1], w_at[1], w_n}, {w_src[2], w_at[2], w_n},
@@ -564,11 +616,23 @@ hipError_t linear_on(const float* x, int64_t x_tok, const float* w, int out, int
     return tsfm::launch_proj(p, s);
 }
 
+// TSFM_UNFUSED_NORM=1 makes linear_norm_on queue the product and the row norm as two launches: the
+// form the fused one must equal bit for bit (a diagnostic switch; same arithmetic either way).
+bool unfused_norm_requested() {
+    const char* e = getenv("TSFM_UNFUSED_NORM");
+    return e != nullptr && e[0] != '\0' && strcmp(e, "0") != 0;
+}
+
 // linear_on followed by nn.rmsNorm of the finished rows into norm_out (may be y): one launch fewer
 // when the product splits its reduction (the reduce normalises the rows), the same bits either way.
 hipError_t linear_norm_on(const float* x, int64_t x_tok, const float* w, int out, int in, float* y, int64_t y_tok,
                           int rows, int epi, const float* resid, const float* norm_scale, float* norm_out,
                           int64_t norm_tok, float eps, hipStream_t s) {
+    if (unfused_norm_requested()) {
+        const hipError_t e = linear_on(x, x_tok, w, out, in, y, y_tok, rows, epi, resid, s);
+        if (e != hipSuccess) return e;
+        return tsfm::launch_rms_norm(y, y_tok, norm_out, norm_tok, norm_scale, rows, out, eps, s);
+    }
     tsfm::ProjParams p{};
     p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi;
     p.resid = resid; p.resid_tok = y_tok;
@@ -662,9 +726,13 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
         if (!ok) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
         hipStream_t s = static_cast<hipStream_t>(a->stream);
         void* scratch = nullptr;
-        if ((e = hipMallocAsync(&scratch, scratch_n, s)) != hipSuccess) return hip_fail(e, "encoder scratch allocation");
-        e = encode_on(a, a->x, a->key_valid, a->rope_cos, a->rope_sin, a->layers, a->final_norm,
-                      static_cast<float*>(scratch), s);
+        if ((e = hipMallocAsync(&scratch, scratch_n + tsfm::kSplitWorkspaceBytes, s)) != hipSuccess)
+            return hip_fail(e, "encoder scratch allocation");
+        {
+            tsfm::SplitWorkspace ws(reinterpret_cast<float*>(static_cast<char*>(scratch) + scratch_n));
+            e = encode_on(a, a->x, a->key_valid, a->rope_cos, a->rope_sin, a->layers, a->final_norm,
+                          static_cast<float*>(scratch), s);
+        }
         const hipError_t f = hipFreeAsync(scratch, s);
         if (e != hipSuccess) return hip_fail(e, "encoder launch");
         if (f != hipSuccess) return hip_fail(f, "encoder scratch release");
@@ -678,7 +746,7 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
     const size_t sizes[11] = {vn, dd, dd, dd, dd, vn, dd, dd, vn, df, df};
     Plan plan;
     const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), c_at = plan.take(t_n), s_at = plan.take(t_n);
-    const size_t fn_at = plan.take(vn), scr_at = plan.take(scratch_n);
+    const size_t fn_at = plan.take(vn), scr_at = plan.take(scratch_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
     std::vector<size_t> w_at((size_t)a->n_layers * 11);
     for (int l = 0; l < a->n_layers; l++)
         for (int i = 0; i < 11; i++) w_at[(size_t)l * 11 + i] = plan.take(sizes[i]);
@@ -686,6 +754,7 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
     if (rc != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
+    tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
     auto up = [&](size_t at, const void* src, size_t n) {
         return hipMemcpyAsync(base + at, src, n, hipMemcpyHostToDevice, s);
     };
@@ -847,10 +916,11 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
         hipStream_t s = static_cast<hipStream_t>(enc.stream);
         Plan plan;
         const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), emb_at = plan.take(emb_n), h_at = plan.take(h_n),
-                     r_at = plan.take(r_n), enc_at = plan.take(enc_n);
+                     r_at = plan.take(r_n), enc_at = plan.take(enc_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
         char* scratch = nullptr;
         if ((e = hipMallocAsync(reinterpret_cast<void**>(&scratch), plan.off, s)) != hipSuccess)
             return hip_fail(e, "forward scratch allocation");
+        tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + part_at));
         e = forward_on(a, enc, a->feats, a->fut_feats, a->ctx_valid, a->reg, a->raw,
                        reinterpret_cast<float*>(scratch + x_at), reinterpret_cast<uint8_t*>(scratch + kv_at),
                        reinterpret_cast<float*>(scratch + emb_at), reinterpret_cast<float*>(scratch + h_at),
@@ -890,11 +960,12 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
     }
     const size_t x_at = st.add(nullptr, x_n), kv_at = st.add(nullptr, kv_n), emb_at = st.add(nullptr, emb_n);
     const size_t h_at = st.add(nullptr, h_n), r_at = st.add(nullptr, r_n), enc_at = st.add(nullptr, enc_n);
-    const size_t raw_at = st.add(nullptr, raw_n);
+    const size_t raw_at = st.add(nullptr, raw_n), part_at = st.add(nullptr, tsfm::kSplitWorkspaceBytes);
     rc = ensure_buf(ctx, st.plan.off);
     if (rc != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
+    tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
     if ((e = st.upload(base, s)) != hipSuccess) return hip_fail(e, "host-to-device copy");
     auto dp = [&](size_t at) { return reinterpret_cast<const float*>(base + at); };
     std::vector<tsfm_chronos2_layer> dev_layers((size_t)enc.n_layers);
@@ -1117,6 +1188,7 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
         Plan plan;
         size_t at[11];
         for (int i = 0; i < 11; i++) at[i] = plan.take(sz[i]);
+        const size_t part_at = plan.take(tsfm::kSplitWorkspaceBytes);
         // The bucket ids live on the device once per (length, buckets, max distance): a per-call
         // upload from pageable memory would make the host wait for the stream to drain before it
         // could queue the forward's launches.
@@ -1128,7 +1200,10 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
             return hip_fail(e, "forward scratch allocation");
         BoltDev dv{a->feats, a->reg, a->dec_start, a->rel_table, a->enc_final_norm, a->dec_final_norm,
                    a->patch_valid, ids, a->enc_layers, a->dec_layers, a->input_embed, a->output_embed, a->raw};
-        e = bolt_forward_on(a, dv, scratch, at, s);
+        {
+            tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + part_at));
+            e = bolt_forward_on(a, dv, scratch, at, s);
+        }
         const hipError_t f = hipFreeAsync(scratch, s);
         if (e != hipSuccess) return hip_fail(e, "forward launch");
         if (f != hipSuccess) return hip_fail(f, "forward scratch release");
@@ -1147,6 +1222,7 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
     const size_t rt_at = st.add(a->rel_table, (size_t)a->rel_buckets * a->heads * 4);
     const size_t ef_at = st.add(a->enc_final_norm, (size_t)d * 4), df_at = st.add(a->dec_final_norm, (size_t)d * 4);
     const size_t raw_at = st.add(nullptr, (size_t)(nb * a->output_embed.out) * 4);
+    const size_t part_at = st.add(nullptr, tsfm::kSplitWorkspaceBytes);
     auto stage_block = [&](const tsfm_resblock& rb, size_t o[6]) {
         o[0] = st.add(rb.hidden_w, (size_t)rb.hid * rb.in * 4);   o[1] = st.add(rb.hidden_b, (size_t)rb.hid * 4);
         o[2] = st.add(rb.output_w, (size_t)rb.out * rb.hid * 4);  o[3] = st.add(rb.output_b, (size_t)rb.out * 4);
@@ -1173,6 +1249,7 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
     if ((rc = ensure_buf(ctx, st.plan.off)) != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
+    tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
     if ((e = st.upload(base, s)) != hipSuccess) return hip_fail(e, "host-to-device copy");
     auto dp = [&](size_t off) { return reinterpret_cast<const float*>(base + off); };
     std::vector<tsfm_bolt_enc_layer> el((size_t)a->n_enc_layers);
@@ -1347,10 +1424,12 @@ int tsfm_sgemm_nt(int m, int n, int k, float alpha, const float* A, int lda, con
     const size_t c_n = ((size_t)(m - 1) * ldc + n) * 4;
     Plan plan;
     const size_t a_at = plan.take(a_n), b_at = plan.take(b_n), c_at = plan.take(c_n);
+    const size_t part_at = plan.take(tsfm::kSplitWorkspaceBytes);
     rc = ensure_buf(ctx, plan.off);
     if (rc != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
+    tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
     hipError_t e;
     if ((e = hipMemcpyAsync(base + a_at, A, a_n, hipMemcpyHostToDevice, s)) != hipSuccess)
         return hip_fail(e, "host-to-device copy");

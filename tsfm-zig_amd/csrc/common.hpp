@@ -168,7 +168,12 @@ __device__ __forceinline__ float sum4(float x) {
 // nn.rmsNorm pieces shared by every kernel that normalises a row (one wave per row, lane l
 // holding the four-column groups 4 l, 4 l + 256, ...): the lane's running sum of squares, the
 // wave-wide total, and the scaled output x * inv * scale, left to right.
-__device__ inline float sumsq4(float ss, f32x4 v) { return ss + (v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]); }
+// Products and sums stay unfused (as the reference's vector `acc += v * v`), so every kernel that
+// shares these helpers rounds the same way.
+__device__ inline float sumsq4(float ss, f32x4 v) {
+#pragma clang fp contract(off)
+    return ss + (v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]);
+}
 
 __device__ inline float rms_inv(float ss, int dim, float eps) {
 #pragma unroll

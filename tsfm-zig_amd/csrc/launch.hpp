@@ -73,6 +73,24 @@ struct ProjParams {
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 
+// Small products split their reduction over workgroups and sum the partial tiles in a fixed order
+// (proj_reduce). The partials go to a device buffer of kSplitWorkspaceBytes that the entry point
+// queuing the products provides, for the duration of its call on the calling thread: a
+// SplitWorkspace on the stack. The buffer must not be in use by work queued on another stream or
+// by another host thread; stream order makes its reuse by consecutive products of one call safe.
+// A split product queued with no workspace set fails with hipErrorInvalidValue.
+constexpr size_t kSplitWorkspaceBytes = (size_t)383 * 128 * 128 * sizeof(float);
+class SplitWorkspace {
+public:
+    explicit SplitWorkspace(float* buf);
+    ~SplitWorkspace();
+    SplitWorkspace(const SplitWorkspace&) = delete;
+    SplitWorkspace& operator=(const SplitWorkspace&) = delete;
+
+private:
+    float* prev_;
+};
+
 // nn.rmsNorm over rows of dim floats (encoder.hip): dim a multiple of 4, rows 16-byte aligned.
 hipError_t launch_rms_norm(const float* x, int64_t x_tok, float* out, int64_t out_tok, const float* scale, int rows,
                            int dim, float eps, hipStream_t stream);

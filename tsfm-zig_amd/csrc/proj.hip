@@ -24,9 +24,6 @@
 // the matrix pipe to two others.
 #include <algorithm>
 
-#include <mutex>
-#include <vector>
-
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -42,6 +39,7 @@ constexpr int GM = 8;            // token tiles that sweep the column tiles toge
 constexpr int LROWS = NT / (BK / 4);  // tile rows one loader pass stages (a float4 per thread)
 constexpr int LPASS = BM / LROWS;     // loader passes per tile
 constexpr size_t kProjLds = (size_t)2 * (BM + BN) * LDS_ROW * sizeof(float);
+static_assert(kSplitWorkspaceBytes == (size_t)383 * BM * BN * sizeof(float), "split workspace size");
 
 // Workgroup tile of a logical id: GM token tiles at a time go through all column tiles, token tile
 // fastest, so the x rows of a group stay in L2 while the weight tiles stream past.
@@ -254,34 +252,13 @@ __global__ __launch_bounds__(256) void proj_reduce_norm(ProjParams p) {
 
 namespace {
 
-// Split partials: one device buffer per (device, stream) for every split product queued on that
-// stream, allocated on first use and kept until the process ends. Stream order makes the reuse
-// safe: a product's reduce has read its partials before the next product on the stream writes
-// them. Calls that overlap on different streams use different buffers. A per-launch stream-ordered
-// allocation costs host time comparable to a small product's whole GPU time.
-constexpr size_t kSplitFloats = (size_t)383 * BM * BN;
-
-float* split_workspace(hipStream_t stream) {
-    struct Entry {
-        int device;
-        hipStream_t stream;
-        float* buf;
-    };
-    static std::mutex mu;
-    static std::vector<Entry> cache;
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    for (const Entry& c : cache)
-        if (c.device == device && c.stream == stream) return c.buf;
-    if (cache.size() >= 64) return nullptr;  // many streams: the product runs unsplit
-    void* buf = nullptr;
-    if (hipMalloc(&buf, kSplitFloats * sizeof(float)) != hipSuccess) return nullptr;
-    cache.push_back({device, stream, static_cast<float*>(buf)});
-    return static_cast<float*>(buf);
-}
+// The split-partials buffer of the calling thread's current library call (SplitWorkspace).
+thread_local float* t_split_ws = nullptr;
 
 }  // namespace
+
+SplitWorkspace::SplitWorkspace(float* buf) : prev_(t_split_ws) { t_split_ws = buf; }
+SplitWorkspace::~SplitWorkspace() { t_split_ws = prev_; }
 
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
@@ -312,13 +289,13 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
             const int per = (steps + s - 1) / s;
             s = (steps + per - 1) / per;
             // s * blocks <= 256 + blocks - 1 < 383 and tokens * width <= blocks * BM * BN, so the
-            // partials always fit the stream's workspace.
-            float* part = split_workspace(stream);
-            if (part != nullptr) {
-                p.splits = s;
-                p.split_steps = per;
-                p.partial = part;
-            }
+            // partials always fit kSplitWorkspaceBytes. The entry point that queues this product
+            // owns the buffer (SplitWorkspace); without one the product is refused rather than
+            // run unsplit, whose single chain would give other bits.
+            if (t_split_ws == nullptr) return hipErrorInvalidValue;
+            p.splits = s;
+            p.split_steps = per;
+            p.partial = t_split_ws;
         }
     }
     if (p.splits > 1) {
