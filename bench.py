@@ -52,9 +52,40 @@ sys.path.insert(0, str(ROOT / "tests"))
 METRIC = "attention TFLOP/s + % MFMA peak; series-forecasts/sec at Chronos-2 shape"
 
 
+GPU_HOST_CPU_SHARE = 16  # host CPUs a one-GPU job is granted on the GPU hosts, whatever nproc shows
+
+
+def _cgroup_cpu_quota():
+    """CPUs allowed by the cgroup v2 (cpu.max) or v1 (cfs quota) limit, or None when unlimited."""
+    try:
+        quota, period = pathlib.Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if quota != "max":
+            return max(1, int(int(quota) // int(period)))
+        return None
+    except (OSError, ValueError):
+        pass
+    try:
+        q = int(pathlib.Path("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read_text())
+        p = int(pathlib.Path("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read_text())
+        return max(1, q // p) if q > 0 else None
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_thread_limits() -> dict:
+    """The host logical cores this process may use, and where each limit comes from."""
+    lim = {"affinity": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)}
+    quota = _cgroup_cpu_quota()
+    if quota is not None:
+        lim["cgroup_quota"] = quota
+    lim["gpu_host_share"] = GPU_HOST_CPU_SHARE
+    return lim
+
+
 def cpu_threads() -> int:
-    # The GPU box grants 16 CPUs per GPU whatever nproc reports.
-    return max(1, min(16, os.cpu_count() or 1))
+    """Threads of the CPU baseline: the logical cores in this process's affinity mask, capped by a
+    cgroup CPU quota and by the one-GPU job's share of the host."""
+    return max(1, min(cpu_thread_limits().values()))
 
 
 def oracle_path() -> pathlib.Path:

@@ -9,7 +9,7 @@
  *   Chronos-2 time attn    RoPE loop + forRange(b*nh, TimeJob)   src/chronos2/model.zig:236-245, 260, 277-309
  *   Timestral time attn    forRange(rows*nh, TimeJob.attend)     src/timestral/model.zig:513-515, 558-635
  * and its arithmetic reaches a device only as two GEMMs per (series, head) through
- *   Backend.sgemm_nt / sgemm_nn                      src/platform/backend.zig:69-72
+ *   Backend.sgemmNT / sgemmNN                        src/platform/backend.zig:51-57
  *   cuda_sgemm_nt / cuda_sgemm_nn                    src/platform/cuda/gemm.c:316-330
  * tsfm_attn_fwd() replaces one whole forRange(B*H, Job.attend) call: the caller keeps its Zig
  * signatures and, at the forRange call site, tries one batched call first and runs its unchanged
@@ -390,10 +390,12 @@ typedef struct tsfm_bolt_forecast_args {
 int tsfm_bolt_forecast(const tsfm_bolt_forecast_args *args);
 
 /* ---------------------------------------------------------------------------------------------
- * The reference backend's GEMM seam, with the signatures of src/platform/cuda/gemm.c so that the
- * reference's own binding (src/platform/cuda/gpu.zig:16-44) can link this library unchanged:
- * nn.linear's weight products (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then
- * run on the gfx950 matrix cores (the projection kernel, one output, no RoPE).
+ * The reference backend's GEMM seam, with the argument lists and return convention of
+ * src/platform/cuda/gemm.c. The reference's binding (src/platform/cuda/gpu.zig:16-44) declares
+ * those functions as cuda_*; a HIP binding is the same file with the extern names changed to
+ * tsfm_* (the Zig side is shown in full in INTEGRATION.md). nn.linear's weight products
+ * (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then run on the gfx950 matrix cores
+ * (the projection kernel, one output, no RoPE).
  *
  * tsfm_weight_register: cuda_weight_register (gemm.c:232-242): a device copy of `len` floats,
  *   NULL on failure. tsfm_weight_release: cuda_weight_release (gemm.c:244-247).

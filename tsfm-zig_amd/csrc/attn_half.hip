@@ -12,7 +12,8 @@
 //                   (k-slot 8g+j = key 4g+j for j<4, key 16+4g+(j-4) for j>=4), A = V^T from LDS
 //                   stored in exactly that key order: [key octet (chunk, g)][dim][8 keys].
 // Softmax in f32 registers; P is rounded to the input type for the second product (round to
-// nearest even); the row sum uses the unrounded f32 probabilities.
+// nearest even); the row sum is taken on the matrix cores over the same rounded P (ones times P),
+// so the weights that are summed are exactly the weights applied to V.
 //
 // The score scale is folded into the exponent: e = exp2(s * scale*log2(e) - m * scale*log2(e)) is
 // one FMA and one v_exp_f32 per score. Tiles below every query's diagonal with all keys valid and

@@ -79,7 +79,7 @@ hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 // SplitWorkspace on the stack. The buffer must not be in use by work queued on another stream or
 // by another host thread; stream order makes its reuse by consecutive products of one call safe.
 // A split product queued with no workspace set fails with hipErrorInvalidValue.
-constexpr size_t kSplitWorkspaceBytes = (size_t)383 * 128 * 128 * sizeof(float);
+constexpr size_t kSplitWorkspaceBytes = (size_t)1536 * 64 * 64 * sizeof(float);
 class SplitWorkspace {
 public:
     explicit SplitWorkspace(float* buf);

@@ -14,14 +14,14 @@
 //
 // One launch computes every output: the output columns are the concatenation [q | k | v | gate]
 // (each heads * 64 wide), so x is streamed through the chip once for all of them. A workgroup
-// computes a 128-token x 128-column tile with K = d_in in 16-wide steps: x and w tiles go
-// HBM/L2 -> registers -> LDS (double-buffered, one barrier per step), and each of the four waves
-// multiplies a 64 x 64 sub-tile with v_mfma_f32_16x16x4_f32, the weight rows as the A operand so
-// that each lane ends with four consecutive output columns of one token (16-byte stores, and the
-// RoPE partner column i + 32 in the same lane); f32 outputs, or bf16/f16 for the half-precision
-// attention path. Three workgroups share a CU (40 KB of LDS and at
-// most 168 registers per lane each), so a wave waiting at its step's barrier or LDS reads leaves
-// the matrix pipe to two others.
+// computes a 64-token x 64-column tile (one head) with K = d_in in 32-wide steps (16-wide when
+// d_in is not a multiple of 32): x and w tiles go HBM/L2 -> registers -> LDS (double-buffered, one
+// barrier per step), and each of the four waves multiplies a 32 x 32 sub-tile with
+// v_mfma_f32_16x16x4_f32 in four accumulation chains, the weight rows as the A operand so that each
+// lane ends with four consecutive output columns of one token (16-byte stores, and the RoPE
+// partner column i + 32 in the same lane); f32 outputs, or bf16/f16 for the half-precision
+// attention path. Four workgroups share a CU (one wave of each per SIMD), so one's step barrier
+// and prologue are covered by the others' products.
 #include <algorithm>
 
 #include "common.hpp"
@@ -30,16 +30,15 @@
 namespace tsfm {
 namespace {
 
-constexpr int BM = 128;          // tokens per workgroup tile
-constexpr int BN = 128;          // output columns per workgroup tile
-constexpr int BK = 16;           // reduction step
-constexpr int LDS_ROW = BK + 4;  // padded LDS row (floats): 8 consecutive rows hit distinct banks
-constexpr int NT = 256;          // four waves: 2 (tokens) x 2 (columns), 64 x 64 each
+constexpr int BM = 64;           // tokens per workgroup tile
+constexpr int BN = 64;           // output columns per workgroup tile: one head
+constexpr int NT = 256;          // four waves: 2 (32 tokens) x 2 (column pairs)
 constexpr int GM = 8;            // token tiles that sweep the column tiles together
-constexpr int LROWS = NT / (BK / 4);  // tile rows one loader pass stages (a float4 per thread)
-constexpr int LPASS = BM / LROWS;     // loader passes per tile
-constexpr size_t kProjLds = (size_t)2 * (BM + BN) * LDS_ROW * sizeof(float);
-static_assert(kSplitWorkspaceBytes == (size_t)383 * BM * BN * sizeof(float), "split workspace size");
+// Reduction step BK (16 or 32; 32 when d_in allows): LDS rows padded to BK + 4 floats, so the 16
+// rows one operand read touches hit distinct banks.
+template <int BK>
+constexpr size_t proj_lds() { return (size_t)2 * (BM + BN) * (BK + 4) * sizeof(float); }
+static_assert(kSplitWorkspaceBytes == (size_t)1536 * BM * BN * sizeof(float), "split workspace size");
 
 // Workgroup tile of a logical id: GM token tiles at a time go through all column tiles, token tile
 // fastest, so the x rows of a group stay in L2 while the weight tiles stream past.
@@ -53,8 +52,20 @@ __device__ __forceinline__ void tile_of(int id, int m_tiles, int n_tiles, int& t
 
 // OUT: element type of the outputs, TSFM_DTYPE_* (0 f32, 1 bf16, 2 f16); the products and RoPE
 // are f32 either way and the result is rounded once, to nearest even, when it is stored.
-template <int OUT>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void qkv_proj(ProjParams p) {
+//
+// Accumulation order. v_mfma_f32_16x16x4_f32 rounds as it accumulates, so one accumulator carried
+// across the whole reduction would be a single chain of d_in rounded additions, several times the
+// error of the reference's nn.lanes vector partial sums (src/core/nn.zig:68-126: 8 or 16 lanes,
+// then a reduction). Each wave therefore keeps four accumulators per output block, one per
+// instruction slot j of a 16-wide chunk (reduction indices 16c + 4g + j), and sums them as a tree
+// at the end: four independent chains of d_in / 4 products, like a 4-lane reference, in a fixed
+// order. Waves of 32 tokens x 32 columns hold the four chains in 64 registers per lane.
+template <int OUT, int BK>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void qkv_proj(ProjParams p) {
+    constexpr int LDS_ROW = BK + 4;
+    constexpr int NX = BM * BK / 4, NW = BN * BK / 4;  // float4s of the x and weight tiles per step
+    constexpr int PER = (NX + NW + NT - 1) / NT;       // float4s a thread stages per step (at most)
+    static_assert(NX % 64 == 0 && (NX + NW) % 64 == 0, "loader slots are whole waves");
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float* const xs = smem;                          // [2][BM][LDS_ROW]
     float* const ws = smem + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
@@ -65,139 +76,168 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     tile_of(p.splits > 1 ? logical / p.splits : logical, p.m_tiles, p.n_tiles, tm, tn);
     const int n_cols = p.width * p.n_out;
 
-    // Loader: thread t stages rows t / (BK / 4) + LROWS i, i < LPASS, columns 4 (t % (BK / 4))
-    // .. + 3 of both tiles. Rows past the end are clamped to the last row: they feed only outputs
-    // that are not stored.
-    const int lr = tid / (BK / 4), lc = (tid % (BK / 4)) * 4;
-    const float* xp[LPASS];
-    const float* wp[LPASS];
+    // Loader: slot f = tid + NT i (i < PER) of a step is float4 f of the x tile (f < NX) or float4
+    // f - NX of the weight tile (f < NX + NW); slots past that are idle (whole waves). A tile's
+    // float4 e is row e / (BK / 4), columns 4 (e % (BK / 4)) .. + 3. Rows past the end are clamped
+    // to the last row: they feed only outputs that are not stored.
+    const float* src[PER];
+    float* dst[PER];
+    int stage[PER];  // floats between the two LDS buffers of this slot's tile; 0 = idle slot
 #pragma unroll
-    for (int i = 0; i < LPASS; i++) {
-        const int m = min(tm * BM + lr + LROWS * i, p.tokens - 1);
-        xp[i] = p.x + (int64_t)m * p.x_tok + lc;
-        const int n = min(tn * BN + lr + LROWS * i, n_cols - 1);
-        const int sel = n / p.width;
-        const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
-        wp[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + lc;
+    for (int i = 0; i < PER; i++) {
+        const int f = tid + NT * i;
+        const bool is_x = f < NX;
+        const int e = is_x ? f : min(f - NX, NW - 1), lr = e / (BK / 4), lc = (e % (BK / 4)) * 4;
+        if (is_x) {
+            src[i] = p.x + (int64_t)min(tm * BM + lr, p.tokens - 1) * p.x_tok + lc;
+        } else {
+            const int n = min(tn * BN + lr, n_cols - 1);
+            const int sel = n / p.width;
+            const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
+            src[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + lc;
+        }
+        dst[i] = (is_x ? xs : ws) + lr * LDS_ROW + lc;
+        stage[i] = f < NX + NW ? (is_x ? BM : BN) * LDS_ROW : 0;
     }
-    f32x4 rx[LPASS], rw[LPASS];
-    auto fetch = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < LPASS; i++) {
-            rx[i] = ld4(xp[i] + k0);
-            rw[i] = ld4(wp[i] + k0);
-        }
-    };
-    auto stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < LPASS; i++) {
-            st4(xs + (buf * BM + lr + LROWS * i) * LDS_ROW + lc, rx[i]);
-            st4(ws + (buf * BN + lr + LROWS * i) * LDS_ROW + lc, rw[i]);
-        }
-    };
 
+    // Wave layout: token block wm (32 tokens), column pair wq: the wave's two 16-column blocks are wq
+    // and wq + 2 of the workgroup's head, so a RoPE pair (i, i + 32) is in one lane.
     // Operand reads: lane l takes row (l & 15) of a 16-row block and the four reduction indices
-    // 4 (l >> 4) .. + 3 of a 16-wide chunk; matrix instruction j of the chunk uses element j, the
-    // same reduction index on both operands.
-    const int wm = wave & 1, wn = wave >> 1;
-    const float* const xr = xs + (wm * 64 + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
-    const float* const wr = ws + (wn * 64 + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
+    // 4 (l >> 4) .. + 3 of a 16-wide chunk; matrix instruction j uses element j, the same reduction
+    // index on both operands.
+    const int wm = wave & 1, wq = wave >> 1;
+    const float* const xr = xs + (wm * 32 + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
+    const float* const wr = ws + (16 * wq + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
 
-    f32x4 acc[4][4];  // [column block][token block]: lane holds columns 4 (l >> 4) + r, token l & 15
+    f32x4 acc[4][2][2];  // [chain j][column block wq, wq + 2][token block]: columns 4 (l >> 4) + r, token l & 15
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 2; b++) acc[j][a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int t0 = split * p.split_steps;
     const int steps = p.splits > 1 ? min(p.d_in / BK, t0 + p.split_steps) : p.d_in / BK;
-    fetch(t0 * BK);
-    stage(0);
+    f32x4 rv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+        if (stage[i]) rv[i] = ld4(src[i] + t0 * BK);
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+        if (stage[i]) st4(dst[i], rv[i]);
     __syncthreads();
     for (int t = t0; t < steps; t++) {
         const int buf = (t - t0) & 1;
-        if (t + 1 < steps) fetch((t + 1) * BK);
+        if (t + 1 < steps) {
 #pragma unroll
-        for (int kc = 0; kc < BK / 16; kc++) {
-            f32x4 wa[4], xb[4];
+            for (int i = 0; i < PER; i++)
+                if (stage[i]) rv[i] = ld4(src[i] + (t + 1) * BK);
+        }
+        // Operands of chunk c + 1 are read from LDS while chunk c's products run.
+        f32x4 wa[2], xb[2];
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                wa[b] = ld4(wr + (buf * BN + 16 * b) * LDS_ROW + 16 * kc);
-                xb[b] = ld4(xr + (buf * BM + 16 * b) * LDS_ROW + 16 * kc);
+        for (int b = 0; b < 2; b++) {
+            wa[b] = ld4(wr + (buf * BN + 32 * b) * LDS_ROW);
+            xb[b] = ld4(xr + (buf * BM + 16 * b) * LDS_ROW);
+        }
+#pragma unroll
+        for (int c = 0; c < BK / 16; c++) {
+            f32x4 wn_[2], xn_[2];
+            if (c + 1 < BK / 16) {
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    wn_[b] = ld4(wr + (buf * BN + 32 * b) * LDS_ROW + 16 * (c + 1));
+                    xn_[b] = ld4(xr + (buf * BM + 16 * b) * LDS_ROW + 16 * (c + 1));
+                }
             }
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++)
+                for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-                    for (int mb = 0; mb < 4; mb++)
-                        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][j], xb[mb][j], acc[nb][mb], 0, 0, 0);
+                    for (int mb = 0; mb < 2; mb++)
+                        acc[j][nb][mb] =
+                            __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][j], xb[mb][j], acc[j][nb][mb], 0, 0, 0);
+            if (c + 1 < BK / 16) {
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    wa[b] = wn_[b];
+                    xb[b] = xn_[b];
+                }
+            }
         }
         // The other buffer was last read in step t - 1, which every wave has left (barrier below).
-        if (t + 1 < steps) stage(buf ^ 1);
+        if (t + 1 < steps) {
+#pragma unroll
+            for (int i = 0; i < PER; i++)
+                if (stage[i]) st4(dst[i] + (buf ^ 1) * stage[i], rv[i]);
+        }
         __syncthreads();
     }
+    f32x4 sum[2][2];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++) sum[nb][mb] = (acc[0][nb][mb] + acc[1][nb][mb]) + (acc[2][nb][mb] + acc[3][nb][mb]);
 
-    // Epilogue: this wave's 64 columns are one head of one output (or, with one output of a width
-    // that is not a multiple of 64, the first columns of a partial block: groups of four columns
-    // past the width are not stored).
-    const int n0 = tn * BN + wn * 64;
+    // Epilogue: this wave's columns are blocks wq and wq + 2 of one head of one output (or, with one
+    // output of a width that is not a multiple of 64, columns of a partial head: groups of four
+    // columns past the width are not stored).
+    const int n0 = tn * BN;
     if (n0 >= n_cols) return;
     const int sel = n0 / p.width, col = n0 - sel * p.width;
+    const int cq = 16 * wq + 4 * (lane >> 4);  // this lane's first column of block wq in the head
     if (p.splits > 1) {  // partial sums only; proj_reduce adds them up in split order and finishes
         // Partial row m of split s holds all n_cols columns (every output side by side).
-        const int cq4 = 4 * (lane >> 4);
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
-            const int m = tm * BM + wm * 64 + mb * 16 + (lane & 15);
+        for (int mb = 0; mb < 2; mb++) {
+            const int m = tm * BM + wm * 32 + mb * 16 + (lane & 15);
             if (m >= p.tokens) continue;
-            float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0 + cq4;
+            float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0 + cq;
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++)
-                if (col + cq4 + 16 * nb < p.width) st4(out + 16 * nb, acc[nb][mb]);
+            for (int nb = 0; nb < 2; nb++)
+                if (col + cq + 32 * nb < p.width) st4(out + 32 * nb, sum[nb][mb]);
         }
         return;
     }
     void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
     const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
     const bool rope = p.rope_cos != nullptr && sel < 2;
-    const int cq = 4 * (lane >> 4);
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) {
-        const int m = tm * BM + wm * 64 + mb * 16 + (lane & 15);
+    for (int mb = 0; mb < 2; mb++) {
+        const int m = tm * BM + wm * 32 + mb * 16 + (lane & 15);
         if (m >= p.tokens) continue;
         if (p.alpha != 1.f) {  // gemmNT's alpha, applied to the finished sum (src/core/nn.zig:100)
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++) acc[nb][mb] *= p.alpha;
+            for (int nb = 0; nb < 2; nb++) sum[nb][mb] *= p.alpha;
         }
         if (rope) {
             // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table.
             const int b = m / p.seq, tok = m - b * p.seq;
             const int table = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
             const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq;
-#pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-                rope4(acc[nb][mb], acc[nb + 2][mb], ld4(p.rope_cos + at + 16 * nb), ld4(p.rope_sin + at + 16 * nb));
+            rope4(sum[0][mb], sum[1][mb], ld4(p.rope_cos + at), ld4(p.rope_sin + at));
         }
         const int64_t at = (int64_t)m * y_tok + col + cq;
         if constexpr (OUT == 0) {
             float* const out = static_cast<float*>(y) + at;
             const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col + cq : nullptr;
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++) {
-                if (col + cq + 16 * nb >= p.width) continue;
-                f32x4 v = acc[nb][mb];
-                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq + 16 * nb);  // nn.linear's bias (linearCols, nn.zig:254)
+            for (int nb = 0; nb < 2; nb++) {
+                if (col + cq + 32 * nb >= p.width) continue;
+                f32x4 v = sum[nb][mb];
+                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq + 32 * nb);  // nn.linear's bias (linearCols, nn.zig:254)
                 if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
-                else if (p.epi == kEpiResidual) v = ld4(res + 16 * nb) + v;  // x + delta, one rounding
-                st4(out + 16 * nb, v);
+                else if (p.epi == kEpiResidual) v = ld4(res + 32 * nb) + v;  // x + delta, one rounding
+                st4(out + 32 * nb, v);
             }
         } else {
             uint16_t* const out = static_cast<uint16_t*>(y) + at;
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++) {
-                const f32x4 v = acc[nb][mb];
-                *reinterpret_cast<u32x2*>(out + 16 * nb) = u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
+            for (int nb = 0; nb < 2; nb++) {
+                const f32x4 v = sum[nb][mb];
+                *reinterpret_cast<u32x2*>(out + 32 * nb) = u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
             }
         }
     }
@@ -260,10 +300,26 @@ thread_local float* t_split_ws = nullptr;
 SplitWorkspace::SplitWorkspace(float* buf) : prev_(t_split_ws) { t_split_ws = buf; }
 SplitWorkspace::~SplitWorkspace() { t_split_ws = prev_; }
 
+namespace {
+
+// The unsplit product: 32-wide steps when d_in allows (half the step barriers), else 16-wide. The
+// chains are the same either way (chain j sums reduction indices 16c + 4g + j in increasing c), so
+// the result does not depend on the step width.
+template <int OUT>
+hipError_t launch_unsplit(const ProjParams& p, int64_t blocks, hipStream_t stream) {
+    if (p.d_in % 32 == 0)
+        hipLaunchKernelGGL((qkv_proj<OUT, 32>), dim3((unsigned)blocks), dim3(NT), proj_lds<32>(), stream, p);
+    else
+        hipLaunchKernelGGL((qkv_proj<OUT, 16>), dim3((unsigned)blocks), dim3(NT), proj_lds<16>(), stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
-    if (p.d_in % BK || p.d_in <= 0 || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 || p.out_dtype > 2 ||
+    if (p.d_in % 16 || p.d_in <= 0 || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 || p.out_dtype > 2 ||
         p.w_ld < p.d_in || p.width % 4 || (p.n_out > 1 && p.width % kHeadDim) ||
         (p.rope_cos != nullptr && p.width % kHeadDim) ||
         (p.out_dtype != 0 && (p.epi != kEpiNone || p.alpha != 1.f || p.bias != nullptr)) ||
@@ -275,23 +331,23 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
-    // and each workgroup walks the whole reduction; split it over workgroups instead, with the
-    // partial tiles summed in a fixed order by proj_reduce. f32 outputs, no RoPE; several outputs
-    // only without an epilogue.
-    const int steps = p.d_in / BK;
+    // and each workgroup walks the whole reduction; split it over workgroups instead (16-wide
+    // steps), with the partial tiles summed in a fixed order by proj_reduce. f32 outputs, no RoPE;
+    // several outputs only without an epilogue.
+    const int steps = p.d_in / 16;
     p.splits = 1;
     p.split_steps = steps;
     p.partial = nullptr;
-    if ((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 128 &&
+    if ((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 512 &&
         steps >= 16) {
-        int s = (int)std::min<int64_t>((256 + blocks - 1) / blocks, std::min(steps / 8, 16));
+        int s = (int)std::min<int64_t>((1024 + blocks - 1) / blocks, std::min(steps / 8, 16));
         if (s >= 2) {
             const int per = (steps + s - 1) / s;
             s = (steps + per - 1) / per;
-            // s * blocks <= 256 + blocks - 1 < 383 and tokens * width <= blocks * BM * BN, so the
+            // s * blocks <= 1024 + blocks - 1 < 1536 and tokens * width <= blocks * BM * BN, so the
             // partials always fit kSplitWorkspaceBytes. The entry point that queues this product
             // owns the buffer (SplitWorkspace); without one the product is refused rather than
-            // run unsplit, whose single chain would give other bits.
+            // run unsplit, which would give other bits.
             if (t_split_ws == nullptr) return hipErrorInvalidValue;
             p.splits = s;
             p.split_steps = per;
@@ -299,7 +355,7 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         }
     }
     if (p.splits > 1) {
-        hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)(blocks * p.splits)), dim3(NT), kProjLds, stream, p);
+        hipLaunchKernelGGL((qkv_proj<0, 16>), dim3((unsigned)(blocks * p.splits)), dim3(NT), proj_lds<16>(), stream, p);
         hipError_t e = hipGetLastError();
         if (e == hipSuccess && p.norm_scale != nullptr) {
             hipLaunchKernelGGL(proj_reduce_norm, dim3((unsigned)((p.tokens + 3) / 4)), dim3(256), 0, stream, p);
@@ -312,19 +368,14 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         return e;
     }
     if (p.norm_scale != nullptr) {
-        hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
-        const hipError_t e = hipGetLastError();
+        const hipError_t e = launch_unsplit<0>(p, blocks, stream);
         if (e != hipSuccess) return e;
         return launch_rms_norm(static_cast<const float*>(p.y0), p.y0_tok, p.norm_out, p.norm_out_tok, p.norm_scale,
                                p.tokens, p.width, p.norm_eps, stream);
     }
-    if (p.out_dtype == 1)
-        hipLaunchKernelGGL(qkv_proj<1>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
-    else if (p.out_dtype == 2)
-        hipLaunchKernelGGL(qkv_proj<2>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
-    else
-        hipLaunchKernelGGL(qkv_proj<0>, dim3((unsigned)blocks), dim3(NT), kProjLds, stream, p);
-    return hipGetLastError();
+    if (p.out_dtype == 1) return launch_unsplit<1>(p, blocks, stream);
+    if (p.out_dtype == 2) return launch_unsplit<2>(p, blocks, stream);
+    return launch_unsplit<0>(p, blocks, stream);
 }
 
 }  // namespace tsfm
