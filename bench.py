@@ -1,13 +1,19 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 attention path.
 
-Default workload (the metric's): Chronos-2 time attention, B=64 series x 12 heads, L=577 tokens,
+Headline workload (the metric's): Chronos-2 time attention, B=64 series x 12 heads, L=577 tokens,
 D=64, f32, RoPE, left-padding key mask, scale 1/8. A step is one batched attention call over the
 whole synthetic batch with every input already resident in HBM. Prints one JSON line with
 whole-job TFLOP/s, the roofline of the dominant kernel (algorithmic work over its HIP-event-timed
-mean launch duration, against the MI355X peak that bounds it), series-forecasts/sec, and the CPU
-baseline: the C restatement of the reference's CPU attention (oracle/, `kind: port`) timed on this
-host's cores over a sample of the same inputs.
+mean launch duration, against the MI355X peak that bounds it) and the CPU baseline: the C
+restatement of the reference's CPU attention (oracle/, `kind: port`) timed on this host's cores
+over a sample of the same inputs, with the parity of the timed output against it.
+
+The default run adds `other_configs`, each measured the same way (timed steps, roofline, CPU
+baseline, parity and the reference-derived parity bar): 1 = bolt_forecast, 2 = bolt, 4 = decode,
+5 = prefill, and 3-e2e = chronos2_forecast, whose whole forecasts per second are the line's
+`series_forecasts_per_s` (the attention call alone gives `attention_series_per_s`).
+`--workload X` measures X alone.
 
 Other workloads (parity-test shapes, measured the same way):
   bolt     Chronos-Bolt-base encoder self-attention, B=256 H=12 L=129, f32, T5 bias, no scale
@@ -29,7 +35,8 @@ Other workloads (parity-test shapes, measured the same way):
            d_ff 3072) over 64 series x 577 tokens, f32, random-init weights; the roofline is over
            the whole stack (every launch but the row norms runs on the f32 matrix cores)
 
-    python bench.py [--steps K] [--warmup W] [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward|bolt_forecast|
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+                    [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward|bolt_forecast|
                      chronos2_forecast]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
@@ -128,10 +135,10 @@ def _check(ta, rc):
         raise RuntimeError(f"tsfm_attn returned {rc}: {ta.last_error()}")
 
 
-def _orc():
+def _orc(lib=None):
     import _oracle
 
-    return _oracle.Oracle(oracle_path())
+    return _oracle.Oracle(lib or oracle_path())
 
 
 def run_chronos2(torch, ta, workloads, peak):
@@ -146,8 +153,8 @@ def run_chronos2(torch, ta, workloads, peak):
         _check(ta, ta.chronos2_time_attention(dev["q"], dev["k"], dev["v"], o, dev["rope_cos"], dev["rope_sin"],
                                               dev["key_valid"], all_valid, w.B, w.n_q, d, w.H, 64, scale=w.scale))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         q = np.ascontiguousarray(a["q"][:B]).ravel().copy()
         k = np.ascontiguousarray(a["k"][:B]).ravel().copy()
         v = np.ascontiguousarray(a["v"][:B]).ravel()
@@ -180,8 +187,8 @@ def run_bolt(torch, ta, workloads, peak):
         _check(ta, ta.bolt_self_attention(dev["q"], dev["k"], dev["v"], o, dev["rel_table"], dev["buckets"],
                                           dev["key_valid"], all_valid, w.B, L, d, w.H, 64, 32))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         q = np.ascontiguousarray(a["q"][:B]).ravel()
         k = np.ascontiguousarray(a["k"][:B]).ravel()
         v = np.ascontiguousarray(a["v"][:B]).ravel()
@@ -214,8 +221,8 @@ def run_prefill(torch, ta, workloads, peak):
     def step():
         _check(ta, ta.fwd(args))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         r = lambda x: np.ascontiguousarray(x[:B]).astype(np.float16).astype(np.float32)
         q, k, v = r(a["q"]), r(a["k"]), r(a["v"])
         kv = np.ascontiguousarray(a["key_valid"][:B])
@@ -259,8 +266,8 @@ def run_decode(torch, ta, workloads, peak):
     def kernel_ms():
         return sum(a0.elapsed_time(a1) for a0, a1 in events) / len(events)
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         r = lambda x: np.ascontiguousarray(x[:B]).astype(np.float32)
         bf = lambda x: torch.from_numpy(r(x)).to(torch.bfloat16).float().numpy()
         q, k, v = bf(a["q"]), bf(a["k"]), bf(a["v"])
@@ -301,8 +308,8 @@ def run_variate(torch, ta, workloads, peak):
         _check(ta, ta.timestral_variate_attention(dev["qkv"], o, dev["key_valid"], roles, True, G, V, L, 0, d, H, 64,
                                                   gate=dev["gate"]))
 
-    def cpu_leg(n):
-        orc = _orc()
+    def cpu_leg(n, lib=None):
+        orc = _orc(lib)
         qkv = np.ascontiguousarray(a["qkv"][: n * V])
         gate = np.ascontiguousarray(a["gate"][: n * V])
         kv = np.ascontiguousarray(a["key_valid"][: n * V])
@@ -332,8 +339,8 @@ def run_proj(torch, ta, workloads, peak):
     def output():
         return torch.stack(outs).reshape(3, w.B, L, d).permute(1, 0, 2, 3).cpu().numpy()
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         x = np.ascontiguousarray(a["x"][: B * L])
         ys = [np.zeros((B * L, d), np.float32) for _ in range(3)]
         t0 = time.perf_counter()
@@ -363,8 +370,8 @@ def run_encoder(torch, ta, workloads, peak):
         _check(ta, ta.chronos2_encode(x, dev["key_valid"], dev["rope_cos"], dev["rope_sin"], layers, dev["final_norm"],
                                       w.B, L, d, w.H, F, m["eps"], keys_all_valid=all_valid, scale=1.0))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         out = np.ascontiguousarray(a["x"][: B * L]).copy()
         kv = np.ascontiguousarray(a["key_valid"][:B]).ravel().copy()
         t0 = time.perf_counter()
@@ -400,8 +407,8 @@ def run_bolt_forward(torch, ta, workloads, peak):
     def step():
         _check(ta, fn(ctypes.byref(args)))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         want = np.zeros((B, m["out"]), np.float32)
         t0 = time.perf_counter()
         orc.bolt_model_forward(cpu_threads(), want, np.ascontiguousarray(a["feats"][: B * npch]),
@@ -437,8 +444,8 @@ def run_bolt_forecast(torch, ta, workloads, peak):
     def step():
         _check(ta, fn(ctypes.byref(args)))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         want = np.zeros((B, m["out"]), np.float32)
         ctx = np.ascontiguousarray(a["ctx"][:B])
         t0 = time.perf_counter()
@@ -474,8 +481,8 @@ def run_chronos2_forecast(torch, ta, workloads, peak):
     def step():
         _check(ta, fn(ctypes.byref(args)))
 
-    def cpu_leg(B):
-        orc = _orc()
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
         want = np.zeros((B, hz, q), np.float32)
         ctx = np.ascontiguousarray(a["ctx"][:B])
         t0 = time.perf_counter()
@@ -495,8 +502,135 @@ def run_chronos2_forecast(torch, ta, workloads, peak):
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
              "variate": run_variate, "proj": run_proj, "encoder": run_encoder, "bolt_forward": run_bolt_forward,
              "bolt_forecast": run_bolt_forecast, "chronos2_forecast": run_chronos2_forecast}
+# The default run: the headline (the Chronos-2 time attention, the metric's shape) and, beside it,
+# every other synthetic shape of the benchmark plus the whole Chronos-2 forecast at the headline's
+# shape (the metric's series-forecasts/sec).
+OTHER_CONFIGS = [("1", "bolt_forecast"), ("2", "bolt"), ("4", "decode"), ("5", "prefill"),
+                 ("3-e2e", "chronos2_forecast")]
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
+
+
+def _other_lane_lib():
+    """The oracle build with the other f32 lane count (the reference on the other kind of host)."""
+    here = oracle_path()
+    other = ROOT / "oracle" / ("liboracle_l8.so" if here.name == "liboracle_l16.so" else "liboracle_l16.so")
+    if other.name == "liboracle_l16.so":
+        info = pathlib.Path("/proc/cpuinfo")
+        if not (info.exists() and " avx512f" in info.read_text()):
+            return None  # this host cannot run the 16-lane build
+    return other if other.exists() else None
+
+
+def measure(torch, bench, steps: int, warmup: int, do_cpu: bool) -> dict:
+    """Time `steps` steps of one workload (after `warmup` steps and SPINUP_S of untimed load, between
+    two full synchronisations), then its CPU baseline and parity. Returns the JSON fields."""
+    import _ref
+    from tsfm_attn import workloads
+
+    w = bench.w
+    stream = torch.cuda.current_stream()
+    warm = getattr(bench, "warm", bench.step)
+    for _ in range(warmup):
+        warm()
+    torch.cuda.synchronize()
+    # The engine clock ramps up over the first milliseconds of load: keep warming (untimed) until
+    # the GPU has been busy for SPINUP_S, so the timed steps do not start on a cold clock.
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < SPINUP_S:
+        for _ in range(8):
+            warm()
+        torch.cuda.synchronize()
+    reset = getattr(bench, "reset_events", None)
+    if reset is not None:
+        reset()
+    # Timed region: the steps between two full synchronisations. A single-launch step gets one
+    # event pair per launch on the stream the kernel runs on (the per-dispatch duration rocprofv3
+    # --kernel-trace reports); a multi-launch step records its dominant kernel itself.
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        bench.step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / steps
+    step_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
+    if bench.kernel_ms is not None:
+        kernel_ms = bench.kernel_ms()
+        work = bench.kernel_work
+    else:
+        kernel_ms = step_ms
+        work = w.flops / 1e12 if bench.bound == "mfma" else w.bytes / 1e9
+    achieved = work / (kernel_ms * 1e-3)
+    flop_peak = workloads.MI355X_PEAK["f32_mfma_tflops" if bench.dtype == "f32" else "f16_mfma_tflops"]
+    value = w.flops / (ms_per_step * 1e-3) / 1e12
+    out = {
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms_per_step, 4),
+        "dtype": bench.dtype,
+        "config": bench.config,
+        "mfma_peak_frac": round(value / flop_peak, 4),
+        "roofline": {
+            "bound": bench.bound,
+            "achieved": round(achieved, 3),
+            "peak": bench.peak,
+            "unit": bench.unit,
+            "frac": round(achieved / bench.peak, 4),
+            "traffic": traffic_for(w.name),
+            # algorithmic work of one dominant-kernel launch, the numerator of `achieved`
+            "work_per_launch": work * (1e12 if bench.bound == "mfma" else 1e9),
+            "work_unit": "FLOP" if bench.bound == "mfma" else "B",
+            "kernel_ms": round(kernel_ms, 4),
+            "step_flops": w.flops,
+            "step_bytes": w.bytes,
+        },
+        "cpu_baseline": None,
+    }
+    if not do_cpu:
+        return out
+    n_series = min(w.B, bench.cpu_default)
+    # The sample is run again until about CPU_SAMPLE_S seconds of CPU work have been timed.
+    dt, want, lanes = bench.cpu_leg(n_series)
+    passes = 1
+    while dt < CPU_SAMPLE_S and passes < 200:
+        dt += bench.cpu_leg(n_series)[0]
+        passes += 1
+    got = bench.output()[:n_series]
+    sample_flops = w.flops * n_series / w.B * passes
+    out["cpu_baseline"] = {
+        "value": round(sample_flops / dt / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": cpu_threads(),
+        "kind": "port",
+        "sample": f"{n_series} of {w.B} series (rows), same inputs, {passes} passes in {dt:.1f} s; C restatement of "
+                  f"the reference CPU path ({lanes} f32 lanes, {cpu_threads()} threads; limits "
+                  f"{cpu_thread_limits()})",
+        "series_forecasts_per_s": round(n_series * passes / dt, 2),
+        "gpu_speedup": round((dt / (n_series * passes)) / (ms_per_step * 1e-3 / w.B), 1),
+    }
+    err = _ref.scaled_err(got, want)
+    out["parity_max_scaled_err"] = float(f"{err:.3e}")
+    if bench.dtype == "f32":
+        # The f32 bar derived from the reference itself: its own 8-lane vs 16-lane spread on this
+        # sample (tests/_ref.py reference_bar), never tighter than 1e-5.
+        other = _other_lane_lib()
+        if other is not None:
+            want_other = bench.cpu_leg(n_series, str(other))[1]
+            pair = (want_other, want) if lanes == 16 else (want, want_other)
+            bar, spread, _ = _ref.reference_bar(*pair)
+            out["parity_bar"] = float(f"{bar:.3e}")
+            out["parity_cross_host_spread"] = float(f"{spread:.3e}")
+            if lanes != 16:  # compare with the 16-lane build, as the tests do
+                out["parity_max_scaled_err"] = float(f"{_ref.scaled_err(got, want_other):.3e}")
+    else:
+        out["parity_bar"] = 1e-2
+    out["parity_ok"] = out["parity_max_scaled_err"] <= out.get("parity_bar", 1e-5)
+    return out
 
 
 def main() -> int:
@@ -504,8 +638,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="chronos2", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-series", type=int, default=None, help="series (rows) in the CPU-baseline sample")
+    ap.add_argument("--workload", default=None, choices=sorted(WORKLOADS),
+                    help="measure only this workload (default: the headline plus every other shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, 3 times (counter calibration)")
@@ -537,106 +671,53 @@ def main() -> int:
         print(f"bench.py: libtsfm_attn unavailable: {ta.last_error()}", file=sys.stderr)
         return 1
 
-    bench = WORKLOADS[args.workload](torch, ta, workloads, workloads.MI355X_PEAK)
+    name = args.workload or "chronos2"
+    bench = WORKLOADS[name](torch, ta, workloads, workloads.MI355X_PEAK)
     w = bench.w
-    stream = torch.cuda.current_stream()
-
-    warm = getattr(bench, "warm", bench.step)
-    for _ in range(args.warmup):
-        warm()
-    torch.cuda.synchronize()
-    # The engine clock ramps up over the first milliseconds of load: keep warming (untimed) until
-    # the GPU has been busy for SPINUP_S, so the timed steps do not start on a cold clock.
-    t_warm = time.perf_counter()
-    while time.perf_counter() - t_warm < SPINUP_S:
-        for _ in range(8):
-            warm()
-        torch.cuda.synchronize()
-    # Timed region: the steps between two full synchronisations. A single-launch step gets one
-    # event pair per launch on the stream the kernel runs on (the per-dispatch duration rocprofv3
-    # --kernel-trace reports); a multi-launch step records its dominant kernel itself.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        bench.step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
-    step_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / args.steps
-    if bench.kernel_ms is not None:
-        kernel_ms = bench.kernel_ms()
-        work = bench.kernel_work
-    else:
-        kernel_ms = step_ms
-        work = w.flops / 1e12 if bench.bound == "mfma" else w.bytes / 1e9
-
-    achieved = work / (kernel_ms * 1e-3)
-    value = w.flops / (ms_per_step * 1e-3) / 1e12
-    flop_peak = workloads.MI355X_PEAK["f32_mfma_tflops" if bench.dtype == "f32" else "f16_mfma_tflops"]
-    n_layers = w.meta.get("num_layers")
+    t_run = time.perf_counter()
+    head = measure(torch, bench, args.steps, args.warmup, not args.no_cpu)
+    print(f"bench.py: {name} measured ({time.perf_counter() - t_run:.0f} s)", file=sys.stderr, flush=True)
+    del bench
     line = {
         "metric": METRIC,
-        "value": round(value, 3),
+        "value": head["value"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": bench.dtype,
+        "dtype": head["dtype"],
         "data": "synthetic",
-        "config": bench.config,
-        "mfma_peak_frac": round(value / flop_peak, 4),
-        "series_forecasts_per_s": round(w.B / (ms_per_step * 1e-3), 1),
-        "roofline": {
-            "bound": bench.bound,
-            "achieved": round(achieved, 3),
-            "peak": bench.peak,
-            "unit": bench.unit,
-            "frac": round(achieved / bench.peak, 4),
-            "traffic": traffic_for(w.name),
-            # algorithmic work of one dominant-kernel launch, the numerator of `achieved`
-            "work_per_launch": work * (1e12 if bench.bound == "mfma" else 1e9),
-            "work_unit": "FLOP" if bench.bound == "mfma" else "B",
-            "kernel_ms": round(kernel_ms, 4),
-            "step_flops": w.flops,
-            "step_bytes": w.bytes,
-        },
-        "cpu_baseline": None,
+        "config": head["config"],
+        "mfma_peak_frac": head["mfma_peak_frac"],
+        # one attention call over the batch: series whose attention one call finishes per second
+        "attention_series_per_s": round(w.B / (head["ms_per_step"] * 1e-3), 1),
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
     }
-    if n_layers:
-        line["series_forecasts_per_s_all_layers"] = round(w.B / (ms_per_step * 1e-3 * n_layers), 1)
-        line["num_layers"] = n_layers
-
-    if not args.no_cpu:
-        n_series = min(w.B, args.cpu_series or bench.cpu_default)
-        # The sample is run again until about CPU_SAMPLE_S seconds of CPU work have been timed.
-        dt, want, lanes = bench.cpu_leg(n_series)
-        passes = 1
-        while dt < CPU_SAMPLE_S and passes < 200:
-            dt += bench.cpu_leg(n_series)[0]
-            passes += 1
-        got = bench.output()[:n_series]
-        import _ref
-
-        sample_flops = w.flops * n_series / w.B * passes
-        line["cpu_baseline"] = {
-            "value": round(sample_flops / dt / 1e12, 5),
-            "unit": "TFLOP/s",
-            "cores": cpu_threads(),
-            "kind": "port",
-            "sample": f"{n_series} of {w.B} series x {w.H} heads, same inputs, {passes} passes in {dt:.1f} s; C "
-                      f"restatement of the reference CPU path ({lanes} f32 lanes, {cpu_threads()} threads)",
-            "series_forecasts_per_s": round(n_series * passes / dt, 2),
-            "gpu_speedup": round((dt / (n_series * passes)) / (ms_per_step * 1e-3 / w.B), 1),
-        }
-        line["parity_max_scaled_err"] = float(f"{_ref.scaled_err(got, want):.3e}")
-
+    for k in ("parity_max_scaled_err", "parity_bar", "parity_cross_host_spread", "parity_ok"):
+        if k in head:
+            line[k] = head[k]
+    if w.meta.get("num_layers"):
+        line["num_layers"] = w.meta["num_layers"]
+    if args.workload is None:
+        others = {}
+        for cfg, wl in OTHER_CONFIGS:
+            b = WORKLOADS[wl](torch, ta, workloads, workloads.MI355X_PEAK)
+            r = measure(torch, b, args.steps, args.warmup, not args.no_cpu)
+            r["workload"] = wl
+            r["series_forecasts_per_s"] = round(b.w.B / (r["ms_per_step"] * 1e-3), 2)
+            others[cfg] = r
+            print(f"bench.py: {wl} measured ({time.perf_counter() - t_run:.0f} s)", file=sys.stderr, flush=True)
+            del b
+            torch.cuda.empty_cache()
+        line["other_configs"] = others
+        # The metric's series-forecasts/sec at the Chronos-2 shape: whole forecasts (64 series x 8192
+        # steps in, 21 quantiles x 1024 steps out, every layer) per second.
+        line["series_forecasts_per_s"] = others["3-e2e"]["series_forecasts_per_s"]
     print(json.dumps(line), flush=True)
     return 0
 
