@@ -226,6 +226,17 @@ typedef struct tsfm_proj_args {
 
 int tsfm_qkv_project(const tsfm_proj_args *args);
 
+/* tsfm_qkv_project that allocates nothing. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory while they run (code under HIP graph capture, serving loops that
+ * forbid hipMalloc). Same arguments and the same result bits as tsfm_qkv_project; device pointers
+ * only (TSFM_ATTN_DEVICE_PTRS; host pointers return TSFM_E_UNSUPPORTED), queued on args->stream.
+ * Small products split their reduction over workgroups; their partial sums go to one 16 MiB array
+ * in the library's device memory per GPU, shared by every call on that GPU and kept between
+ * calls: calls that overlap on one GPU (other streams or threads) race and must be serialised by
+ * the caller. A product whose partials need more than 16 MiB returns TSFM_E_UNSUPPORTED
+ * (tsfm_qkv_project runs it). */
+int tsfm_qkv_project_noalloc(const tsfm_proj_args *args);
+
 /* ---------------------------------------------------------------------------------------------
  * Chronos-2 encoder stack: Model.encode's layer loop and final norm (src/chronos2/model.zig:144-206)
  * in one call, every product on the matrix cores. Per layer, on x (batch * seq tokens of d_model):

@@ -476,7 +476,14 @@ int tsfm_variate_attend(const tsfm_variate_args* a) {
 
 // ---- fused projection ---------------------------------------------------------------------------
 
-int tsfm_qkv_project(const tsfm_proj_args* a) {
+}  // extern "C"
+
+namespace {
+
+// Validates a projection request and fills the kernel parameters with the caller's pointers.
+// Returns TSFM_OK, a non-zero error code, or kNothing when the product is empty.
+constexpr int kNothing = -1;
+int proj_request(const tsfm_proj_args* a, tsfm::ProjParams* pp) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (a->dtype != TSFM_DTYPE_F32) return fail(TSFM_E_UNSUPPORTED, "the projection computes in f32 only");
     if (a->out_dtype < TSFM_DTYPE_F32 || a->out_dtype > TSFM_DTYPE_F16)
@@ -498,36 +505,103 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
                  a->rope_table_stride < 0))
         return fail(TSFM_E_INVALID, "bad RoPE table description");
     const int64_t tokens = (int64_t)a->batch * a->seq;
-    if (tokens == 0 || width == 0) return TSFM_OK;  // nothing to compute
+    if (tokens == 0 || width == 0) return kNothing;
     if (a->d_in == 0 || a->d_in % 16) return fail(TSFM_E_UNSUPPORTED, "d_in %d (supported: multiples of 16)", a->d_in);
     if (tokens > 0x7fffffff || 4 * width > 0x7fffffff) return fail(TSFM_E_UNSUPPORTED, "too many tokens or heads");
     if (a->x_tok % 4 || a->q_tok % 4 || a->k_tok % 4 || a->v_tok % 4 || (gated && a->gate_tok % 4) ||
         (rope && a->rope_table_stride % 4))
         return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
-    int rc = ensure_ready();
-    if (rc != TSFM_OK) return rc;
-    ThreadCtx* ctx = thread_ctx();
-    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
-
     tsfm::ProjParams p{};
     p.x = a->x; p.x_tok = a->x_tok;
     p.w0 = a->w_q; p.w1 = a->w_k; p.w2 = a->w_v; p.w3 = a->w_gate;
     p.w_ld = a->d_in; p.alpha = 1.f; p.epi = tsfm::kEpiNone;
     p.y0 = a->q; p.y1 = a->k; p.y2 = a->v; p.y3 = a->gate;
     p.out_dtype = a->out_dtype;
-    const int64_t oes = (int64_t)elem_size(a->out_dtype);
     p.y0_tok = a->q_tok; p.y1_tok = a->k_tok; p.y2_tok = a->v_tok; p.y3_tok = a->gate_tok;
     p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
     p.rope_table_stride = a->rope_table_stride;
     p.rope_rows_per_table = a->rope_rows_per_table; p.rope_row0 = a->rope_row0;
     p.tokens = (int32_t)tokens; p.seq = a->seq; p.d_in = a->d_in; p.width = (int32_t)width;
     p.n_out = gated ? 4 : 3;
+    *pp = p;
+    return TSFM_OK;
+}
+
+bool device_ptrs_aligned(const tsfm_proj_args* a) {
+    const void* ptrs[] = {a->x, a->w_q, a->w_k, a->w_v, a->w_gate, a->q, a->k, a->v, a->gate, a->rope_cos,
+                          a->rope_sin};
+    for (const void* q : ptrs)
+        if (q != nullptr && !aligned(q, 16)) return false;
+    return true;
+}
+
+// The split partials of tsfm_qkv_project_noalloc: one copy per GPU in the code object's device
+// memory, so the call allocates nothing. Its address on each device is looked up once, with that
+// device current (the array's name is only a host-side stand-in for it).
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_at[kMaxDevices] = {};
+
+hipError_t noalloc_scratch(void** out) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_at[device] == nullptr) {
+        void* ptr = nullptr;
+        if ((e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        if (ptr == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_at[device] = ptr;
+    }
+    *out = g_scratch_at[device];
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsfm_qkv_project_noalloc(const tsfm_proj_args* a) {
+    tsfm::ProjParams p{};
+    int rc = proj_request(a, &p);
+    if (rc == kNothing) return TSFM_OK;
+    if (rc != TSFM_OK) return rc;
+    if (!(a->flags & TSFM_ATTN_DEVICE_PTRS))
+        return fail(TSFM_E_UNSUPPORTED, "tsfm_qkv_project_noalloc takes device pointers only");
+    if (!device_ptrs_aligned(a)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
+    tsfm::ProjParams plan = p;
+    const size_t need = tsfm::proj_split_bytes(plan);
+    if (need > kNoAllocScratchBytes)
+        return fail(TSFM_E_UNSUPPORTED,
+                    "this product's split partials need %zu bytes; tsfm_qkv_project_noalloc holds %zu "
+                    "(use tsfm_qkv_project)", need, kNoAllocScratchBytes);
+    if ((rc = ensure_ready()) != TSFM_OK) return rc;
+    void* part = nullptr;
+    hipError_t e = noalloc_scratch(&part);
+    if (e != hipSuccess) return hip_fail(e, "scratch symbol address");
+    tsfm::SplitWorkspace ws(static_cast<float*>(part));
+    e = tsfm::launch_proj(p, static_cast<hipStream_t>(a->stream));
+    if (e != hipSuccess) return hip_fail(e, "projection launch");
+    return TSFM_OK;
+}
+
+int tsfm_qkv_project(const tsfm_proj_args* a) {
+    tsfm::ProjParams p{};
+    int rc = proj_request(a, &p);
+    if (rc == kNothing) return TSFM_OK;
+    if (rc != TSFM_OK) return rc;
+    const int64_t width = (int64_t)a->heads * a->head_dim, tokens = (int64_t)a->batch * a->seq;
+    const bool gated = a->gate != nullptr, rope = a->rope_cos != nullptr;
+    if ((rc = ensure_ready()) != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    const int64_t oes = (int64_t)elem_size(a->out_dtype);
     hipError_t e;
     if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
-        const void* ptrs[] = {a->x, a->w_q, a->w_k, a->w_v, a->w_gate, a->q, a->k, a->v, a->gate, a->rope_cos,
-                              a->rope_sin};
-        for (const void* q : ptrs)
-            if (q != nullptr && !aligned(q, 16)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
+        if (!device_ptrs_aligned(a)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
         hipStream_t s = static_cast<hipStream_t>(a->stream);
         float* part = nullptr;
         bool owned = false;

@@ -72,6 +72,9 @@ struct ProjParams {
     float norm_eps;
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
+// Bytes of split partials launch_proj will need for this product (0: it runs unsplit); sets the
+// tiling fields of p as launch_proj does.
+size_t proj_split_bytes(ProjParams& p);
 
 // Small products split their reduction over workgroups and sum the partial tiles in a fixed order
 // (proj_reduce). The partials go to a device buffer of kSplitWorkspaceBytes that the entry point

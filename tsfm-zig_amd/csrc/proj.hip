@@ -316,6 +316,30 @@ hipError_t launch_unsplit(const ProjParams& p, int64_t blocks, hipStream_t strea
 
 }  // namespace
 
+size_t proj_split_bytes(ProjParams& p) {
+    p.m_tiles = (p.tokens + BM - 1) / BM;
+    p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
+    const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
+    const int steps = p.d_in / 16;
+    p.splits = 1;
+    p.split_steps = steps;
+    p.partial = nullptr;
+    // f32 outputs, no RoPE; several outputs only without an epilogue; at most half a launch of
+    // tiles (four workgroups per CU), and at least 16 steps to share out.
+    if (!((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 512 &&
+          steps >= 16))
+        return 0;
+    int s = (int)std::min<int64_t>((1024 + blocks - 1) / blocks, std::min(steps / 8, 16));
+    if (s < 2) return 0;
+    const int per = (steps + s - 1) / s;
+    s = (steps + per - 1) / per;
+    p.splits = s;
+    p.split_steps = per;
+    // s * blocks <= 1024 + blocks - 1 < 1536 and tokens * width <= blocks * BM * BN, so the partials
+    // always fit kSplitWorkspaceBytes.
+    return (size_t)s * p.tokens * p.width * p.n_out * sizeof(float);
+}
+
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
@@ -326,34 +350,18 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         (p.bias != nullptr && p.n_out != 1) ||
         (p.norm_scale != nullptr && (p.n_out != 1 || p.out_dtype != 0 || p.norm_out == nullptr)))
         return hipErrorInvalidValue;
-    p.m_tiles = (p.tokens + BM - 1) / BM;
-    p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
-    int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
-    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if ((int64_t)((p.tokens + BM - 1) / BM) * ((p.width * p.n_out + BN - 1) / BN) > 0x7fffffff)
+        return hipErrorInvalidValue;
     // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
     // and each workgroup walks the whole reduction; split it over workgroups instead (16-wide
-    // steps), with the partial tiles summed in a fixed order by proj_reduce. f32 outputs, no RoPE;
-    // several outputs only without an epilogue.
-    const int steps = p.d_in / 16;
-    p.splits = 1;
-    p.split_steps = steps;
-    p.partial = nullptr;
-    if ((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 512 &&
-        steps >= 16) {
-        int s = (int)std::min<int64_t>((1024 + blocks - 1) / blocks, std::min(steps / 8, 16));
-        if (s >= 2) {
-            const int per = (steps + s - 1) / s;
-            s = (steps + per - 1) / per;
-            // s * blocks <= 1024 + blocks - 1 < 1536 and tokens * width <= blocks * BM * BN, so the
-            // partials always fit kSplitWorkspaceBytes. The entry point that queues this product
-            // owns the buffer (SplitWorkspace); without one the product is refused rather than
-            // run unsplit, which would give other bits.
-            if (t_split_ws == nullptr) return hipErrorInvalidValue;
-            p.splits = s;
-            p.split_steps = per;
-            p.partial = t_split_ws;
-        }
+    // steps), with the partial tiles summed in a fixed order by proj_reduce.
+    if (proj_split_bytes(p) > 0) {
+        // The entry point that queues this product owns the partials' buffer (SplitWorkspace);
+        // without one the product is refused rather than run unsplit, which would give other bits.
+        if (t_split_ws == nullptr) return hipErrorInvalidValue;
+        p.partial = t_split_ws;
     }
+    const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
     if (p.splits > 1) {
         hipLaunchKernelGGL((qkv_proj<0, 16>), dim3((unsigned)(blocks * p.splits)), dim3(NT), proj_lds<16>(), stream, p);
         hipError_t e = hipGetLastError();

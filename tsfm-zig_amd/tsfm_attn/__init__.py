@@ -59,6 +59,7 @@ EXPORTS = (
     "tsfm_t5_bucket_table",
     "tsfm_variate_attend",
     "tsfm_qkv_project",
+    "tsfm_qkv_project_noalloc",
     "tsfm_chronos2_encode",
     "tsfm_chronos2_forward",
     "tsfm_bolt_forward",
@@ -420,6 +421,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_variate_attend.restype = ctypes.c_int
     lib.tsfm_qkv_project.argtypes = [ctypes.POINTER(ProjArgs)]
     lib.tsfm_qkv_project.restype = ctypes.c_int
+    lib.tsfm_qkv_project_noalloc.argtypes = [ctypes.POINTER(ProjArgs)]
+    lib.tsfm_qkv_project_noalloc.restype = ctypes.c_int
     lib.tsfm_chronos2_encode.argtypes = [ctypes.POINTER(Chronos2EncodeArgs)]
     lib.tsfm_chronos2_encode.restype = ctypes.c_int
     lib.tsfm_chronos2_forward.argtypes = [ctypes.POINTER(Chronos2ForwardArgs)]
@@ -693,6 +696,11 @@ def timestral_variate_attention(qkv, o, key_valid, roles: Sequence[int], cov: bo
 def qkv_project(args: ProjArgs) -> int:
     """``tsfm_qkv_project``: returns the ABI code."""
     return int(load().tsfm_qkv_project(ctypes.byref(args)))
+
+
+def qkv_project_noalloc(args: ProjArgs) -> int:
+    """``tsfm_qkv_project_noalloc`` (device pointers; allocates nothing): returns the ABI code."""
+    return int(load().tsfm_qkv_project_noalloc(ctypes.byref(args)))
 
 
 def _proj(x, wq, wk, wv, q, k, v, *, batch: int, seq: int, d_in: int, nh: int, hd: int, x_tok: int, y_tok: int,
