@@ -192,6 +192,54 @@ void orc_timestral_variate_attention(size_t threads, const float *qkv, float *o,
 /* nn.mulSigmoid (src/core/nn.zig:423-433). */
 void orc_mul_sigmoid(float *dst, const float *x, const float *g, size_t n);
 
+/* ---- Timestral model and forecaster (tsfm_oracle_timestral.c), rows that are all targets ---- */
+/* nn.siluInPlace, nn.mulSilu, nn.softplus, nn.clampNonfinite (src/core/nn.zig:399-420, 516-563). */
+void orc_silu_in_place(float *x, size_t n);
+void orc_mul_silu(float *dst, const float *gate, const float *up, size_t n);
+float orc_softplus(float x);
+void orc_clamp_nonfinite(float *v, size_t n);
+/* ResBlock(.silu).forward (src/core/resblock.zig:63-79); bias pointers may be NULL. */
+void orc_resblock_silu(size_t threads, float *y, const float *x, size_t rows, const orc_resblock *rb);
+/* Model.patchStats / StatsJob (src/timestral/model.zig:210-216, 712-750): per-patch causal float64
+ * Welford (loc, scale) of (rows, t) rows, each (rows, t / ps). */
+void orc_timestral_patch_stats(size_t threads, float *loc, float *scale, const float *data, const uint8_t *obs,
+                               size_t rows, size_t t, size_t ps, double min_scale);
+/* One attention of a layer (src/timestral/model.zig:19-33): qkv rows permuted to (qkv, head,
+ * head_dim) (permuteQkv, :72-85); gate NULL = no sdpa_sigmoid gate. */
+typedef struct orc_timestral_attn {
+    int is_time;
+    const float *norm, *qkv, *out, *gate;
+} orc_timestral_attn;
+typedef struct orc_timestral_layer {
+    int n_attn;
+    orc_timestral_attn attn[2];
+    const float *mlp_norm, *w12, *w3; /* w12 (2 hid, d) = [gate; up], w3 (d, hid) */
+} orc_timestral_layer;
+/* Model (src/timestral/model.zig:126-200) with its config (src/timestral/config.zig:6-45). */
+typedef struct orc_timestral_model {
+    size_t ps, d, nh, hd, hid, n_layers, q, median, block_size, context_length, rope_dim;
+    float rope_theta, norm_eps, quantile_width_factor;
+    double minimum_scale;
+    int use_asinh, attend_missing;
+    const double *knots;                 /* quantile_knots (q) */
+    orc_resblock patch_proj, head;       /* ResBlock(.silu): (2 ps -> 4d -> d, biases), (d -> 4d -> ps q) */
+    const float *forecast_query, *out_norm;
+    const orc_timestral_layer *layers;
+} orc_timestral_model;
+/* Model.predictBlock (src/timestral/model.zig:220-432) without covariates: ctx/obs (rows, t),
+ * rows = groups * vall; out (rows, h * ps, q) quantiles in data units. */
+void orc_timestral_predict_block(size_t threads, float *out, const orc_timestral_model *m, const float *ctx,
+                                 const uint8_t *obs, size_t t, size_t groups, size_t vall, size_t h);
+/* refineBlock (src/timestral/forecaster.zig:582-662) with every row a target: qs (rows, h ps, q) in place. */
+void orc_timestral_refine_block(float *qs, const orc_timestral_model *m, const float *ctx, const uint8_t *obs,
+                                size_t rows, size_t t, size_t h);
+/* forecaster.forecast (src/timestral/forecaster.zig:57-180, forecastRaw :303-421, blockDecode :423-563)
+ * without covariates: inputs/observed (b, v, t), out (b, v, horizon, q). max_context 0 = the model's
+ * context_length. Returns 0, 1 (a NaN forecast: error.DegenerateInput) or 2 (asymmetric levels). */
+int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
+                           const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon, size_t max_context,
+                           size_t per_shot, float cap_k, float extreme, int symmetric, int clip_nonnegative);
+
 /* Batched selfAttend over (b, h) items with (token, head, dim) layouts: the generic form of
  * the three family jobs above, used by the tests for shapes the families do not fix.
  * q/k/v/o strides: token stride and batch stride in floats; head h at +h*hd. */

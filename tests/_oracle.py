@@ -62,6 +62,46 @@ class BoltDecLayer(ctypes.Structure):
     _fields_ = [(f, _vp) for f in BOLT_DEC_FIELDS]
 
 
+class TimestralAttn(ctypes.Structure):
+    """orc_timestral_attn (oracle/tsfm_oracle.h)."""
+
+    _fields_ = [("is_time", ctypes.c_int), ("norm", _vp), ("qkv", _vp), ("out", _vp), ("gate", _vp)]
+
+
+class TimestralLayer(ctypes.Structure):
+    _fields_ = [("n_attn", ctypes.c_int), ("attn", TimestralAttn * 2), ("mlp_norm", _vp), ("w12", _vp), ("w3", _vp)]
+
+
+class TimestralModel(ctypes.Structure):
+    _fields_ = [(f, _sz) for f in ("ps", "d", "nh", "hd", "hid", "n_layers", "q", "median", "block_size",
+                                   "context_length", "rope_dim")] + \
+               [("rope_theta", _f), ("norm_eps", _f), ("quantile_width_factor", _f), ("minimum_scale", ctypes.c_double),
+                ("use_asinh", ctypes.c_int), ("attend_missing", ctypes.c_int), ("knots", _vp),
+                ("patch_proj", OrcResblock), ("head", OrcResblock), ("forecast_query", _vp), ("out_norm", _vp),
+                ("layers", ctypes.POINTER(TimestralLayer))]
+
+
+def timestral_model_struct(m):
+    """orc_timestral_model from a model dict (tests/_ref.py timestral_model); the returned struct keeps
+    references to everything it points at."""
+    layers = (TimestralLayer * max(1, len(m["layers"])))()
+    for i, ly in enumerate(m["layers"]):
+        layers[i].n_attn = len(ly["attns"])
+        for j, a in enumerate(ly["attns"]):
+            layers[i].attn[j] = TimestralAttn(int(a["is_time"]), ptr(a["norm"]), ptr(a["qkv"]), ptr(a["out"]),
+                                              ptr(a.get("gate")))
+        layers[i].mlp_norm, layers[i].w12, layers[i].w3 = ptr(ly["mlp_norm"]), ptr(ly["w12"]), ptr(ly["w3"])
+    st = TimestralModel(ps=m["ps"], d=m["d"], nh=m["nh"], hd=64, hid=m["hid"], n_layers=len(m["layers"]), q=m["q"],
+                        median=m["median"], block_size=m["block_size"], context_length=m["context_length"],
+                        rope_dim=m["rope_dim"], rope_theta=m["rope_theta"], norm_eps=m["norm_eps"],
+                        quantile_width_factor=m["width_factor"], minimum_scale=m["minimum_scale"],
+                        use_asinh=int(m["use_asinh"]), attend_missing=int(m["attend_missing"]), knots=ptr(m["knots"]),
+                        patch_proj=resblock_struct(m["patch_proj"]), head=resblock_struct(m["head"]),
+                        forecast_query=ptr(m["forecast_query"]), out_norm=ptr(m["out_norm"]), layers=layers)
+    st._keep = (layers, m)
+    return st
+
+
 class Oracle:
     def __init__(self, path):
         self.path = str(path)
@@ -116,6 +156,18 @@ class Oracle:
         L.orc_timestral_variate_attention.argtypes = [_sz, _vp, _vp, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _sz, _sz, _sz,
                                                       _sz]
         L.orc_mul_sigmoid.argtypes = [_vp, _vp, _vp, _sz]
+        L.orc_silu_in_place.argtypes = [_vp, _sz]
+        L.orc_mul_silu.argtypes = [_vp, _vp, _vp, _sz]
+        L.orc_softplus.argtypes = [_f]
+        L.orc_softplus.restype = _f
+        L.orc_clamp_nonfinite.argtypes = [_vp, _sz]
+        L.orc_resblock_silu.argtypes = [_sz, _vp, _vp, _sz, ctypes.POINTER(OrcResblock)]
+        L.orc_timestral_patch_stats.argtypes = [_sz, _vp, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_double]
+        L.orc_timestral_predict_block.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz, _sz]
+        L.orc_timestral_refine_block.argtypes = [_vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz]
+        L.orc_timestral_forecast.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz, _sz, _sz,
+                                             _sz, _f, _f, ctypes.c_int, ctypes.c_int]
+        L.orc_timestral_forecast.restype = ctypes.c_int
         L.orc_batched_self_attend.argtypes = [_sz, ctypes.c_int, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz,
                                               _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
 
@@ -309,3 +361,56 @@ class Oracle:
         self.lib.orc_batched_self_attend(threads, mask, ptr(q), q_tok, q_batch, ptr(k), k_tok, k_batch, ptr(v), v_tok,
                                          v_batch, ptr(o), o_tok, o_batch, ptr(key_valid), kv_batch, ptr(bias), nb, nh,
                                          n, hd, scale)
+
+    # ---- Timestral model and forecaster ----------------------------------------------------------
+
+    def silu_in_place(self, x):
+        self.lib.orc_silu_in_place(ptr(x), x.size)
+
+    def mul_silu(self, dst, gate, up):
+        self.lib.orc_mul_silu(ptr(dst), ptr(gate), ptr(up), dst.size)
+
+    def softplus(self, x):
+        return self.lib.orc_softplus(x)
+
+    def clamp_nonfinite(self, v):
+        self.lib.orc_clamp_nonfinite(ptr(v), v.size)
+
+    def resblock_silu(self, threads, y, x, rows, rb):
+        st = resblock_struct(rb)
+        self.lib.orc_resblock_silu(threads, ptr(y), ptr(x), rows, ctypes.byref(st))
+
+    def timestral_patch_stats(self, threads, data, obs, rows, t, ps, min_scale):
+        data = np.ascontiguousarray(data, np.float32)
+        obs = np.ascontiguousarray(obs, np.uint8)
+        loc = np.zeros(rows * (t // ps), np.float32)
+        scale = np.zeros_like(loc)
+        self.lib.orc_timestral_patch_stats(threads, ptr(loc), ptr(scale), ptr(data), ptr(obs), rows, t, ps, min_scale)
+        return loc.reshape(rows, -1), scale.reshape(rows, -1)
+
+    def timestral_predict_block(self, threads, m, ctx, obs, t, groups, vall, h):
+        ctx = np.ascontiguousarray(ctx, np.float32)
+        obs = np.ascontiguousarray(obs, np.uint8)
+        out = np.zeros((groups * vall, h * m["ps"], m["q"]), np.float32)
+        st = timestral_model_struct(m)
+        self.lib.orc_timestral_predict_block(threads, ptr(out), ctypes.byref(st), ptr(ctx), ptr(obs), t, groups, vall, h)
+        return out
+
+    def timestral_refine_block(self, qs, m, ctx, obs, rows, t, h):
+        st = timestral_model_struct(m)
+        ctx = np.ascontiguousarray(ctx, np.float32)  # held here: the call reads through raw pointers
+        obs = np.ascontiguousarray(obs, np.uint8)
+        self.lib.orc_timestral_refine_block(ptr(qs), ctypes.byref(st), ptr(ctx), ptr(obs), rows, t, h)
+
+    def timestral_forecast(self, threads, m, inputs, observed, b, v, t, horizon, max_context=0, per_shot=32,
+                           cap_k=1e4, extreme=1e30, symmetric=True, clip_nonnegative=True):
+        """(rc, out (b, v, horizon, q))."""
+        inputs = np.ascontiguousarray(inputs, np.float32)
+        observed = np.ascontiguousarray(observed, np.uint8)
+        out = np.zeros((b, v, horizon, m["q"]), np.float32)
+        st = timestral_model_struct(m)
+        rc = self.lib.orc_timestral_forecast(threads, ptr(out), ctypes.byref(st), ptr(inputs), ptr(observed), b, v, t,
+                                             horizon, max_context, per_shot, cap_k, extreme, int(symmetric),
+                                             int(clip_nonnegative))
+        return rc, out
+

@@ -382,3 +382,197 @@ def assert_within_reference_bar(got, lane8, lane16, exact=None):
     err = scaled_err(got, lane16)
     assert err <= bar, f"GPU vs 16-lane oracle {err:.3e} > bar {bar:.3e} (cross-host spread {s:.3e}, f64 {m:.3e})"
     return err, bar
+
+
+# ---- the Timestral model in float64, written from its definitions ---------------------------------
+
+
+def timestral_model(rng, ps=16, d=128, nh=2, hid=256, schedule=("time_variate", "time"), knots=None, block_size=32,
+                    context_length=2048, rope_factor=0.5, use_asinh=True, attend_missing=True, gated=True):
+    """Random-init Timestral weights and config (src/timestral/model.zig:126-200, config.zig:6-45) as a
+    dict: the fused qkv weights already in the permuted (qkv, head, head_dim) row order."""
+    if knots is None:
+        knots = np.array([0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9])
+    knots = np.ascontiguousarray(knots, np.float64)
+    q = len(knots)
+
+    def lin(o, i):
+        return (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+
+    axes = {"time": [True], "variate": [False], "time_variate": [True, False], "variate_time": [False, True]}
+    layers = []
+    for kind in schedule:
+        attns = [dict(is_time=t, norm=norm(), qkv=lin(3 * d, d), out=lin(d, d), gate=lin(d, d) if gated else None)
+                 for t in axes[kind]]
+        layers.append(dict(attns=attns, mlp_norm=norm(), w12=lin(2 * hid, d), w3=lin(d, hid)))
+    pp = resblock(rng, 2 * ps, 4 * d, d)
+    hb = resblock(rng, d, 4 * d, ps * q)
+    for k in ("hidden_b", "output_b", "residual_b"):
+        hb[k] = None  # the head has no biases (model.zig:145)
+    return dict(ps=ps, d=d, nh=nh, hid=hid, q=q, median=int(np.where(knots == 0.5)[0][0]), block_size=block_size,
+                context_length=context_length, rope_dim=int(64 * rope_factor), rope_theta=10000.0, norm_eps=1e-6,
+                minimum_scale=1e-6, use_asinh=use_asinh, attend_missing=attend_missing, width_factor=2.0, knots=knots,
+                patch_proj=pp, head=hb, forecast_query=rng.standard_normal(d).astype(np.float32), out_norm=norm(),
+                layers=layers)
+
+
+def silu_f64(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def resblock_silu_f64(rb, x):
+    """ResBlock(.silu): output(silu(hidden(x))) + residual(x), biases where present."""
+    W = lambda k: np.asarray(rb[k], np.float64)
+    B = lambda k: 0.0 if rb.get(k) is None else np.asarray(rb[k], np.float64)
+    x = np.asarray(x, np.float64)
+    h = silu_f64(x @ W("hidden_w").T + B("hidden_b"))
+    return h @ W("output_w").T + B("output_b") + x @ W("residual_w").T + B("residual_b")
+
+
+def patch_stats_f64(x, obs, ps, min_scale):
+    """Causal per-patch (mean, std) of each row: over the observed values up to the patch's last step,
+    the mean (0 without any) and the sample standard deviation (ddof 1; 0 below two values), at least
+    min_scale. Two-pass numpy statistics, not a running recurrence."""
+    x = np.asarray(x, np.float64)
+    obs = np.asarray(obs, bool)
+    rows, t = x.shape
+    n = t // ps
+    loc = np.zeros((rows, n))
+    scale = np.zeros((rows, n))
+    for r in range(rows):
+        for p in range(n):
+            v = x[r, :(p + 1) * ps][obs[r, :(p + 1) * ps]]
+            loc[r, p] = v.mean() if v.size else 0.0
+            sd = v.std(ddof=1) if v.size >= 2 else 0.0
+            scale[r, p] = max(sd, min_scale)
+    return loc, scale
+
+
+def softplus_f64(x):
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h):
+    """Model.predictBlock without covariates, in float64: (rows, h * ps, q) quantiles in data units."""
+    ps, d, nh, hid, q = m["ps"], m["d"], m["nh"], m["hid"], m["q"]
+    hd, rows = 64, groups * vall
+    n = l = ne = t // ps
+    sl = ne + h
+    ctx = np.asarray(ctx, np.float64).reshape(rows, t)
+    obs = np.asarray(obs, bool).reshape(rows, t)
+    loc, scale = patch_stats_f64(ctx, obs, ps, m["minimum_scale"])
+    sc = np.maximum(np.repeat(scale, ps, axis=1), float(np.finfo(np.float32).eps))
+    v = np.where(obs, (ctx - np.repeat(loc, ps, axis=1)) / sc, 0.0)
+    if m["use_asinh"]:
+        v = np.arcsinh(v)
+    feats = np.concatenate([v.reshape(rows, n, ps), (~obs).reshape(rows, n, ps).astype(np.float64)], axis=2)
+    x = np.zeros((rows, sl, d))
+    x[:, :ne] = resblock_silu_f64(m["patch_proj"], feats.reshape(rows * n, 2 * ps)).reshape(rows, n, d)
+    x[:, ne:] = np.asarray(m["forecast_query"], np.float64)
+    kv, first, _ = timestral_key_valid(obs.astype(np.uint8), rows, vall, ne, ps, m["attend_missing"])
+    c64, s64, _ = timestral_rope_tables_f64(groups, ne, l, h, hd, m["rope_dim"], m["rope_theta"], first)
+    W = lambda a: np.asarray(a, np.float64)
+    half = hd // 2
+
+    def rope(y, g):  # y (sl, nh, hd)
+        cg, sg = c64[g][:, None, :], s64[g][:, None, :]
+        lo, hi = y[..., :half].copy(), y[..., half:].copy()
+        return np.concatenate([lo * cg - hi * sg, hi * cg + lo * sg], axis=-1)
+
+    enc_allowed = [allowed_matrix(3, ne, ne, kv[r]) for r in range(rows)]
+    dec_allowed = [allowed_matrix(5, h, sl, kv[r], q_pos0=ne, ctx_keys=l, chain_start=ne) for r in range(rows)]
+    for ly in m["layers"]:
+        for a in ly["attns"]:
+            xn = rms_norm_f64(x, a["norm"], m["norm_eps"])
+            qkv = (xn @ W(a["qkv"]).T).reshape(rows, sl, 3, nh, hd)
+            if a["is_time"]:
+                o = np.zeros((rows, sl, nh, hd))
+                for r in range(rows):
+                    qr, kr, vr = rope(qkv[r, :, 0], r // vall), rope(qkv[r, :, 1], r // vall), qkv[r, :, 2]
+                    for hh in range(nh):
+                        o[r, :ne, hh] = naive_attend(qr[:ne, hh], kr[:ne, hh], vr[:ne, hh], enc_allowed[r], hd ** -0.5)
+                        o[r, ne:, hh] = naive_attend(qr[ne:, hh], kr[:, hh], vr[:, hh], dec_allowed[r], hd ** -0.5)
+                o = o.reshape(rows, sl, d)
+            else:
+                o = variate_attend_f64(qkv.reshape(rows * sl, 3 * d), kv, [ROLE_TARGET] * vall, False, groups, vall,
+                                       ne, h, d, nh, hd).reshape(rows, sl, d)
+            if a.get("gate") is not None:
+                o = o / (1.0 + np.exp(-(xn @ W(a["gate"]).T)))
+            x = x + o @ W(a["out"]).T
+        xn = rms_norm_f64(x, ly["mlp_norm"], m["norm_eps"])
+        hh_ = xn @ W(ly["w12"]).T
+        x = x + (hh_[..., :hid] * silu_f64(hh_[..., hid:])) @ W(ly["w3"]).T
+    dec = rms_norm_f64(x[:, ne:], m["out_norm"], m["norm_eps"])
+    raw = resblock_silu_f64(m["head"], dec.reshape(rows * h, d)).reshape(rows, h * ps, q)
+    knots, med = np.asarray(m["knots"]), m["median"]
+    widths = np.zeros(q)
+    widths[med + 1:] = knots[med + 1:] - knots[med:-1]
+    widths[:med] = knots[1:med + 1] - knots[:med]
+    inc = m["width_factor"] * widths * softplus_f64(raw)
+    out = np.empty_like(raw)
+    out[..., med] = raw[..., med]
+    out[..., med + 1:] = raw[..., med:med + 1] + np.cumsum(inc[..., med + 1:], axis=-1)
+    out[..., :med] = raw[..., med:med + 1] - np.cumsum(inc[..., :med][..., ::-1], axis=-1)[..., ::-1]
+    if m["use_asinh"]:
+        out = np.sinh(out)
+    return out * scale[:, l - 1, None, None] + loc[:, l - 1, None, None]
+
+
+def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale):
+    """refineBlock (src/timestral/forecaster.zig:582-662) from its definition, with two-pass numpy
+    statistics: horizon patch j is re-framed with the mean and std (ddof 1) of the observed context
+    plus the medians of patches 0..j-1 mapped into their own frames (clipped around the context
+    mean), patch 0 keeping the context's last-patch frame."""
+    qs = np.asarray(qs, np.float32)
+    rows, hps, q = qs.shape
+    h = hps // ps
+    t = ctx.shape[1]
+    l = t // ps
+    loc, scale = patch_stats_f64(ctx, obs, ps, min_scale)
+    clip = np.sqrt(np.float64(np.finfo(np.float32).max)) / 1e3
+    out = np.empty_like(qs)
+    for r in range(rows):
+        loc0, scale0 = np.float32(loc[r, l - 1]), np.float32(scale[r, l - 1])
+        vals = np.asarray(ctx[r], np.float64)[np.asarray(obs[r], bool)]
+        sinh_med = (qs[r, :, med].astype(np.float64) - np.float64(loc0)) / np.float64(scale0)
+        offset = vals.mean() if vals.size else 0.0
+        lj, sj = [], []
+        for j in range(h):
+            mean = vals.mean() if vals.size else 0.0
+            m2 = ((vals - mean) ** 2).sum()
+            sc = max(np.sqrt(max(m2 / max(vals.size - 1.0, 1.0), 0.0)), min_scale)
+            lj.append(np.float32(mean))
+            sj.append(np.float32(sc))
+            folded = np.clip(sinh_med[j * ps:(j + 1) * ps] * sc + mean - offset, -clip, clip) + offset
+            vals = np.concatenate([vals, folded])
+        lj[0], sj[0] = loc0, scale0
+        for s in range(hps):
+            a = (qs[r, s] - loc0) / scale0
+            out[r, s] = a * sj[s // ps] + lj[s // ps]
+    return out
+
+
+def timestral_context(inputs, observed, max_context, ps):
+    """forecastRaw's preparation (src/timestral/forecaster.zig:327-379) for target rows: forward-fill
+    (leading gaps 0), keep the last max_context steps, left-pad to whole patches. (rows, t) values
+    and mask."""
+    x = np.asarray(inputs, np.float32)
+    o = np.asarray(observed, bool)
+    rows, t0 = x.shape
+    keep = min(t0, max_context)
+    t = (keep + ps - 1) // ps * ps
+    vals = np.zeros((rows, t), np.float32)
+    mask = np.zeros((rows, t), bool)
+    for r in range(rows):
+        last, seen = 0.0, False
+        filled = np.zeros(t0, np.float32)
+        for j in range(t0):
+            if o[r, j]:
+                last, seen = x[r, j], True
+            filled[j] = last if seen else 0.0
+        vals[r, t - keep:] = filled[t0 - keep:]
+        mask[r, t - keep:] = o[r, t0 - keep:]
+    return vals, mask

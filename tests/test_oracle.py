@@ -830,3 +830,187 @@ def test_timestral_rope_application(orc):
     assert not np.allclose(g5[0, :, 0], _ref.timestral_rope_f64(qkv, np.roll(c.reshape(3, -1), 1, 0).ravel(),
                                                                  np.roll(s.reshape(3, -1), 1, 0).ravel(), rows, sl,
                                                                  vall, d, nh, hd).reshape(rows, sl, 3, nh, hd)[0, :, 0])
+
+
+# ---- Timestral model and forecaster (oracle/tsfm_oracle_timestral.c) ---------------------------
+
+
+def test_silu_mul_silu_softplus_closed_forms(orc):
+    x = np.linspace(-30, 30, 1001).astype(np.float32)
+    y = x.copy()
+    orc.silu_in_place(y)
+    exact = x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(y - exact) / np.maximum(np.abs(exact), 1)) < 1e-6
+    g = np.random.default_rng(1).standard_normal(1001).astype(np.float32)
+    z = np.zeros_like(x)
+    orc.mul_silu(z, g, x)  # gate * silu(up): a transposed operand order would fail
+    assert np.max(np.abs(z - g * exact) / np.maximum(np.abs(g * exact), 1)) < 1e-6
+    for v in (-30.0, -1.0, 0.0, 3.0, 19.9, 20.0, 20.5, 80.0):
+        want = v if v > 20 else np.log1p(np.exp(v))
+        assert abs(orc.softplus(v) - want) <= 1e-6 * max(1.0, abs(want))
+
+
+def test_clamp_nonfinite_cases(orc):
+    a = np.array([1.0, np.inf, -2.0, -np.inf, np.nan], np.float32)
+    orc.clamp_nonfinite(a)
+    assert a[0] == 1 and a[1] == 1 and a[2] == -2 and a[3] == -2 and np.isnan(a[4])
+    b = np.array([np.inf, -np.inf], np.float32)
+    orc.clamp_nonfinite(b)
+    assert (b == 0).all()
+    c = np.array([3.0, np.nan], np.float32)
+    orc.clamp_nonfinite(c)  # no infinity: untouched
+    assert c[0] == 3 and np.isnan(c[1])
+
+
+def test_resblock_silu_matches_definition(orc):
+    rng = np.random.default_rng(2)
+    rb = _ref.resblock(rng, 32, 64, 48)
+    x = rng.standard_normal((10, 32)).astype(np.float32)
+    y = np.zeros((10, 48), np.float32)
+    orc.resblock_silu(3, y, x, 10, rb)
+    assert _ref.scaled_err(y, _ref.resblock_silu_f64(rb, x)) < 2e-6
+    for k in ("hidden_b", "output_b", "residual_b"):
+        rb[k] = None  # bias = false
+    orc.resblock_silu(3, y, x, 10, rb)
+    assert _ref.scaled_err(y, _ref.resblock_silu_f64(rb, x)) < 2e-6
+
+
+def test_timestral_patch_stats_match_the_definition(orc):
+    """StatsJob (model.zig:712-750) against two-pass numpy statistics of the observed prefix: the
+    running mean, the sample std (ddof 1), min_scale below two values, loc 0 before any."""
+    rng = np.random.default_rng(3)
+    rows, ps, n = 5, 8, 12
+    t = ps * n
+    x = (3 + 2 * rng.standard_normal((rows, t))).astype(np.float32)
+    obs = rng.random((rows, t)) < 0.7
+    obs[1, :30] = False   # leading gap
+    obs[2] = False        # never observed
+    obs[3, :] = False
+    obs[3, 17] = True     # exactly one observation
+    loc, scale = orc.timestral_patch_stats(2, x, obs, rows, t, ps, 1e-6)
+    wl, ws = _ref.patch_stats_f64(x, obs, ps, 1e-6)
+    assert np.allclose(loc, wl, rtol=2e-7, atol=1e-7) and np.allclose(scale, ws, rtol=2e-7, atol=1e-7)
+    assert (loc[2] == 0).all() and (scale[2] == np.float32(1e-6)).all()
+
+
+@pytest.mark.parametrize("attend_missing", [True, False])
+def test_timestral_predict_block_matches_f64(orc, attend_missing):
+    """Model.predictBlock (model.zig:220-432) without covariates against a float64 model written
+    from the definitions (tests/_ref.py): causal per-patch normalisation with asinh, the patch
+    embedding, time attention (causal encoder rows with key validity, block-causal decoder rows,
+    partial RoPE relative to each group's first observation, sigmoid gate), variate attention, the
+    SiLU MLP, the head, and the monotone quantile transform back to data units. Two groups of two
+    variates, leading gaps (one group starts late), scattered missing values."""
+    rng = np.random.default_rng(4 + attend_missing)
+    m = _ref.timestral_model(rng, d=128, nh=2, hid=128, attend_missing=attend_missing)
+    groups, vall, t, h = 2, 2, 16 * 10, 4
+    rows = groups * vall
+    ctx = (5 + 3 * rng.standard_normal((rows, t))).astype(np.float32)
+    obs = rng.random((rows, t)) < 0.9
+    obs[2:4, :40] = False  # group 1's first observed patch is patch 2
+    ctx[~obs] = 0
+    got = orc.timestral_predict_block(3, m, ctx, obs, t, groups, vall, h)
+    want = _ref.timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h)
+    assert got.shape == want.shape
+    assert _ref.scaled_err(got, want) < 5e-5  # measured 5.5e-6
+
+
+def test_timestral_refine_block_matches_definition(orc):
+    rng = np.random.default_rng(6)
+    m = _ref.timestral_model(rng, d=64, nh=1, hid=64)
+    rows, ps, t, h, q = 3, 16, 16 * 8, 4, m["q"]
+    ctx = (10 + 4 * rng.standard_normal((rows, t))).astype(np.float32)
+    obs = rng.random((rows, t)) < 0.85
+    obs[2, :70] = False
+    ctx[~obs] = 0
+    med = (10 + 4 * rng.standard_normal((rows, h * ps))).astype(np.float32)
+    qs = np.sort(med[:, :, None] + rng.standard_normal((rows, h * ps, q)).astype(np.float32), axis=2)
+    qs[:, :, m["median"]] = med
+    got = qs.copy()
+    orc.timestral_refine_block(got, m, ctx, obs, rows, t, h)
+    want = _ref.timestral_refine_f64(qs, ctx, obs, ps, m["median"], m["minimum_scale"])
+    assert _ref.scaled_err(got, want) < 1e-5
+    assert not np.allclose(got[:, ps:], qs[:, ps:])  # later patches do move
+
+
+def _ts_case(seed, b=2, v=2, t0=150, nan_frac=0.1, start_missing=0):
+    rng = np.random.default_rng(seed)
+    m = _ref.timestral_model(rng, d=64, nh=1, hid=64, schedule=("time_variate",))
+    x = (20 + 5 * np.sin(np.arange(t0) / 4.0) + rng.standard_normal((b * v, t0))).astype(np.float32)
+    obs = rng.random((b * v, t0)) >= nan_frac
+    obs[:, :start_missing] = False
+    x[~obs] = 0
+    return m, x, obs
+
+
+def _ts_decode_composed(orc, m, x, obs, b, v, horizon, per_shot, max_context):
+    """blockDecode restated in Python over the oracle's predict_block and refine_block: each block's
+    medians (0 if not finite or huge) become observed context, oldest steps dropped past
+    max_context."""
+    ps, q = m["ps"], m["q"]
+    ctx, mask = _ref.timestral_context(x, obs, max_context, ps)
+    out = np.zeros((b * v, horizon, q), np.float32)
+    remaining, done = -(-horizon // ps), 0
+    while remaining:
+        block = min(per_shot, remaining)
+        blen = block * ps
+        t = ctx.shape[1]
+        qs = orc.timestral_predict_block(3, m, ctx, mask, t, b, v, block)
+        if block > 1:
+            orc.timestral_refine_block(qs, m, ctx, mask, b * v, t, block)
+        take = min(blen, horizon - done)
+        out[:, done:done + take] = qs[:, :take]
+        remaining -= block
+        done += blen
+        if not remaining:
+            break
+        medv = qs[:, :, m["median"]].copy()
+        medv[~np.isfinite(medv) | (np.abs(medv) >= 1e30)] = 0
+        ctx = np.concatenate([ctx, medv], axis=1)
+        mask = np.concatenate([mask, np.ones_like(medv, bool)], axis=1)
+        if ctx.shape[1] > max_context:
+            keep = max(ps, max_context // ps * ps)
+            ctx, mask = ctx[:, -keep:], mask[:, -keep:]
+    return out
+
+
+@pytest.mark.parametrize("horizon,per_shot,max_context", [(40, 4, 2048), (100, 2, 2048), (100, 2, 160)])
+def test_timestral_forecast_block_decode_composition(orc, horizon, per_shot, max_context):
+    """forecast (no averaging, no clip, no cap) = forecastRaw's forward-fill and padding, then
+    blockDecode: one block refined (40 steps), several blocks with median feedback (100 steps in
+    blocks of 2 patches), and a context cap that drops the oldest steps as it grows."""
+    b, v = 2, 2
+    m, x, obs = _ts_case(7, b, v, start_missing=20)
+    rc, got = orc.timestral_forecast(3, m, x, obs, b, v, x.shape[1], horizon, max_context, per_shot, cap_k=0.0,
+                                     symmetric=False, clip_nonnegative=False)
+    assert rc == 0
+    want = _ts_decode_composed(orc, m, x, obs, b, v, horizon, per_shot, max_context)
+    assert np.array_equal(got.reshape(b * v, horizon, -1), want)
+
+
+def test_timestral_forecast_symmetric_clip_and_cap(orc):
+    """Symmetric averaging: 0.5 (f(x) - reverse(f(-x))) over the quantile levels; the clip to zero
+    of series whose observed values are all non-negative; the quantile cap at the context's range
+    widened by cap_k times its last patch scale."""
+    b, v, horizon = 2, 2, 40
+    m, x, obs = _ts_case(8, b, v)
+    t0 = x.shape[1]
+    kw = dict(cap_k=0.0, per_shot=32)
+    _, f = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, symmetric=False, clip_nonnegative=False, **kw)
+    _, g = orc.timestral_forecast(3, m, -x, obs, b, v, t0, horizon, symmetric=False, clip_nonnegative=False, **kw)
+    rc, s = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, symmetric=True, clip_nonnegative=False, **kw)
+    assert rc == 0
+    assert np.allclose(s, 0.5 * (f - g[..., ::-1]), rtol=0, atol=1e-5 * np.abs(f).max())
+    _, c = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, symmetric=True, clip_nonnegative=True, **kw)
+    assert np.array_equal(c, np.maximum(s, 0))  # every series here is positive
+    cap = 0.05
+    _, capped = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, symmetric=False, clip_nonnegative=False,
+                                       cap_k=cap, per_shot=32)
+    ctx, mask = _ref.timestral_context(x, obs, 2048, m["ps"])
+    _, sc = _ref.patch_stats_f64(ctx, mask, m["ps"], m["minimum_scale"])
+    for r in range(b * v):
+        vals = ctx[r][mask[r]]
+        a = np.float32(sc[r, -1]) * np.float32(cap)
+        lo, hi = vals.min() - a, vals.max() + a
+        assert capped.reshape(b * v, -1)[r].min() >= lo - 1e-4 and capped.reshape(b * v, -1)[r].max() <= hi + 1e-4
+    assert not np.array_equal(capped, f)
