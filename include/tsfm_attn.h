@@ -293,7 +293,8 @@ typedef struct tsfm_resblock {
     const float *output_w, *output_b;      /* (out, hid), (out) */
     const float *residual_w, *residual_b;  /* (out, in), (out) */
     int32_t in, hid, out;                  /* in, hid multiples of 16; out of 4 */
-    int32_t act;                           /* 0 = ReLU (ResBlock(.relu), Chronos-2); others unsupported */
+    int32_t act;                           /* 0 = ReLU (ResBlock(.relu), Chronos), 1 = SiLU (ResBlock(.silu),
+                                            * Timestral); biases may be NULL where the model has none */
 } tsfm_resblock;
 
 typedef struct tsfm_chronos2_forward_args {
@@ -399,6 +400,71 @@ typedef struct tsfm_bolt_forecast_args {
 } tsfm_bolt_forecast_args;
 
 int tsfm_bolt_forecast(const tsfm_bolt_forecast_args *args);
+
+/* ---------------------------------------------------------------------------------------------
+ * Timestral forecast: forecaster.forecast (src/timestral/forecaster.zig:57-180) of a batch of
+ * series whose rows are all target variates (no covariates; with covariates the caller keeps its
+ * CPU path), f32, device memory only, asynchronous on `stream` except for one synchronisation
+ * after the first decode block (to learn whether every series has an observation). The whole
+ * forecast runs on the device: forecastRaw's forward-fill and left padding (:303-394), the decode
+ * loop of blockDecode (:423-563) with predictBlock (src/timestral/model.zig:220-432: causal
+ * per-patch statistics, patch embedding, the time / variate transformer, the monotone quantile
+ * head) and refineBlock (:582-662), the median feedback and max_context window, the quantile cap
+ * (:396-418), the mirrored pass of the symmetric average (:107-137, run in the same batch) and the
+ * non-negative clip (:163-178). A forecast whose output contains NaN is returned as is (the
+ * reference reports error.DegenerateInput).
+ * With kv_cache set, decode blocks after the first run only their new patches and decoder tokens,
+ * attending over the time-attention K/V the earlier blocks computed (the reference re-encodes the
+ * whole context every block; the result is the same computation, up to f32 summation order);
+ * blocks after a max_context drop, and every block of a batch that holds a series with no
+ * observation, re-encode in full. */
+typedef struct tsfm_timestral_attn {
+    int32_t is_time;        /* 1: time attention (timeAttention :487-519); 0: variate (:525-544) */
+    const float *norm;      /* (d) attn_norms.<i>.scale */
+    const float *qkv;       /* (3 d, d) wQKV, rows permuted to (qkv, head, head_dim) (permuteQkv :72-85) */
+    const float *out;       /* (d, d) wO */
+    const float *gate;      /* (d, d) _gate (sdpa_sigmoid), or NULL */
+} tsfm_timestral_attn;
+
+typedef struct tsfm_timestral_layer {
+    int32_t n_attn;                 /* 1 or 2, in block_schedule order (config.zig:94-100) */
+    tsfm_timestral_attn attn[2];
+    const float *mlp_norm;          /* (d) */
+    const float *w12;               /* (2 hid, d): gate rows, then up rows (MlpAct :40-46) */
+    const float *w3;                /* (d, hid) */
+} tsfm_timestral_layer;
+
+typedef struct tsfm_timestral_model {
+    int32_t patch, d_model, heads, head_dim, mlp_hidden, n_layers, n_quantiles;
+    int32_t block_size, context_length;
+    int32_t rope_dim;               /* rotated dims: head_dim * rope_partial_factor (config.zig:34-36) */
+    int32_t use_asinh, attend_missing;
+    float rope_theta, norm_eps, minimum_scale, quantile_width_factor;
+    const double *quantile_knots;   /* (n_quantiles) host memory: increasing, containing 0.5 */
+    tsfm_resblock patch_proj;       /* 2 patch -> 4 d -> d, act 1 (SiLU), with biases */
+    tsfm_resblock head;             /* d -> 4 d -> patch * n_quantiles, act 1, no biases */
+    const float *forecast_query;    /* (d) */
+    const float *out_norm;          /* (d) */
+    const tsfm_timestral_layer *layers;  /* n_layers entries, host memory */
+} tsfm_timestral_model;
+
+typedef struct tsfm_timestral_forecast_args {
+    tsfm_timestral_model model;
+    const float *inputs;            /* (batch, variates, len) */
+    const uint8_t *observed;        /* (batch, variates, len): non-zero = observed */
+    int32_t batch, variates, len, horizon;   /* variates 1..16 */
+    int32_t max_context;            /* Options.max_context; 0 = model.context_length */
+    int32_t per_shot_patches;       /* Options.per_shot_horizon_patches; 0 = 32; capped at block_size */
+    float quantile_real_cap_k;      /* Options.quantile_real_cap_k (1e4); 0 disables the cap */
+    float extreme_value_threshold;  /* Options.extreme_value_threshold (1e30) */
+    int32_t symmetric_averaging, clip_nonnegative;  /* Options (both on in the reference) */
+    int32_t kv_cache;               /* non-zero: decode over cached K/V (see above) */
+    uint32_t flags;                 /* TSFM_ATTN_DEVICE_PTRS */
+    float *out;                     /* (batch, variates, horizon, n_quantiles) */
+    void *stream;
+} tsfm_timestral_forecast_args;
+
+int tsfm_timestral_forecast(const tsfm_timestral_forecast_args *args);
 
 /* ---------------------------------------------------------------------------------------------
  * The reference backend's GEMM seam, with the argument lists and return convention of

@@ -39,7 +39,11 @@ def test_library_exports_every_declared_symbol(ta):
                                           ("BoltEncLayer", "tsfm_bolt_enc_layer"), ("BoltDecLayer", "tsfm_bolt_dec_layer"),
                                           ("BoltForwardArgs", "tsfm_bolt_forward_args"),
                                           ("BoltForecastArgs", "tsfm_bolt_forecast_args"),
-                                          ("Chronos2ForecastArgs", "tsfm_chronos2_forecast_args")])
+                                          ("Chronos2ForecastArgs", "tsfm_chronos2_forecast_args"),
+                                          ("TimestralAttn", "tsfm_timestral_attn"),
+                                          ("TimestralLayer", "tsfm_timestral_layer"),
+                                          ("TimestralModel", "tsfm_timestral_model"),
+                                          ("TimestralForecastArgs", "tsfm_timestral_forecast_args")])
 def test_args_struct_layout_matches_header(ta, struct, cname):
     """Compile a tiny C program against the header and compare offsetof() with the ctypes struct."""
     cls = getattr(ta, struct)

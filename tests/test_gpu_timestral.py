@@ -1,0 +1,119 @@
+"""GPU parity of the Timestral forecaster (tsfm_timestral_forecast: forecastRaw, blockDecode with
+predictBlock and refineBlock, the cap, the mirrored average and the clip on the device) against the
+oracle's restatement of forecaster.forecast (src/timestral/forecaster.zig:57-180), which re-encodes
+the whole grown context every decode block as the reference does, through the C ABI.
+
+The device path runs with and without its KV cache (decode blocks after the first run only their
+new patches and decoder tokens over the kept time-attention K/V). Bar: _ref.reference_bar against
+the oracle's 16-lane build: twice the reference's own spread between its 8-lane and 16-lane builds
+on the same forecast (at least 1e-5). Covered: one refined block, several blocks with median
+feedback, a max_context window that drops its oldest steps, a series with no observation (the
+cache is switched off), missing values and leading gaps, several variates per series.
+"""
+import numpy as np
+import pytest
+
+import _ref
+
+pytestmark = pytest.mark.gpu
+
+THREADS = 16
+
+
+def _device_model(m):
+    import torch
+
+    def cu(x):
+        return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+    dm = dict(m)
+    dm["patch_proj"] = {k: cu(v) for k, v in m["patch_proj"].items()}
+    dm["head"] = {k: cu(v) for k, v in m["head"].items()}
+    dm["forecast_query"], dm["out_norm"] = cu(m["forecast_query"]), cu(m["out_norm"])
+    dm["layers"] = [dict(attns=[{k: (cu(v) if isinstance(v, np.ndarray) else v) for k, v in a.items()}
+                                for a in ly["attns"]],
+                         mlp_norm=cu(ly["mlp_norm"]), w12=cu(ly["w12"]), w3=cu(ly["w3"])) for ly in m["layers"]]
+    return dm
+
+
+def _case(seed, b=3, v=2, length=150, nan_frac=0.1, schedule=("time_variate", "time")):
+    rng = np.random.default_rng(seed)
+    m = _ref.timestral_model(rng, d=128, nh=2, hid=256, schedule=schedule)
+    t = np.arange(length)
+    x = (20 + 6 * np.sin(2 * np.pi * t / 24) + 0.02 * t + rng.standard_normal((b * v, length))).astype(np.float32)
+    obs = rng.random((b * v, length)) >= nan_frac
+    obs[:v, :37] = False  # the first series starts late
+    x[~obs] = 0
+    return m, x, obs
+
+
+def _gpu(ta, m, x, obs, b, v, horizon, **kw):
+    import torch
+
+    out = torch.full((b, v, horizon, m["q"]), -7.0, device="cuda")
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    od = torch.from_numpy(np.ascontiguousarray(obs.astype(np.uint8))).cuda()
+    rc = ta.timestral_forecast(out, xd, od, _device_model(m), b, v, x.shape[1], horizon, **kw)
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _oracle(orc, m, x, obs, b, v, horizon, max_context=0, per_shot=32):
+    rc, out = orc.timestral_forecast(THREADS, m, x, obs, b, v, x.shape[1], horizon, max_context, per_shot)
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("kv_cache", [True, False])
+@pytest.mark.parametrize("horizon,per_shot,max_context", [(40, 32, 0), (100, 2, 0), (100, 2, 176)])
+def test_timestral_forecast_matches_reencoding_oracle(ta, orc, orc16, gpu_ready, kv_cache, horizon, per_shot,
+                                                      max_context):
+    b, v = 3, 2
+    m, x, obs = _case(horizon + per_shot)
+    got = _gpu(ta, m, x, obs, b, v, horizon, max_context=max_context, per_shot=per_shot, kv_cache=kv_cache)
+    w8, w16 = (_oracle(o_, m, x, obs, b, v, horizon, max_context, per_shot) for o_ in (orc, orc16))
+    assert np.isfinite(got).all()
+    _ref.assert_within_reference_bar(got, w8, w16)
+
+
+def test_timestral_cached_decode_equals_reencoding(ta, gpu_ready):
+    """Several decode blocks: the cached path (only new patches and decoder tokens per block) and
+    the re-encoding path give the same forecasts up to f32 summation order."""
+    b, v, horizon = 2, 3, 160
+    m, x, obs = _case(21, b, v)
+    cached = _gpu(ta, m, x, obs, b, v, horizon, per_shot=4, kv_cache=True)
+    full = _gpu(ta, m, x, obs, b, v, horizon, per_shot=4, kv_cache=False)
+    assert _ref.scaled_err(cached, full) < 2e-5
+
+
+def test_timestral_series_without_observation(ta, orc, orc16, gpu_ready):
+    """A series with no observation at all: its RoPE origin moves once the medians are fed back, so
+    the device re-encodes every block; it still matches the oracle."""
+    b, v, horizon = 2, 1, 64
+    m, x, obs = _case(5, b, v)
+    obs[1] = False
+    x[1] = 0
+    got = _gpu(ta, m, x, obs, b, v, horizon, per_shot=2, kv_cache=True)
+    w8, w16 = (_oracle(o_, m, x, obs, b, v, horizon, 0, 2) for o_ in (orc, orc16))
+    _ref.assert_within_reference_bar(got, w8, w16)
+
+
+def test_timestral_forecast_argument_errors(ta, gpu_ready):
+    import torch
+
+    b, v, horizon = 1, 1, 16
+    m, x, obs = _case(3, b, v)
+    out = torch.zeros((b, v, horizon, m["q"]), device="cuda")
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    od = torch.from_numpy(np.ascontiguousarray(obs.astype(np.uint8))).cuda()
+    dm = _device_model(m)
+    asym = dict(dm, knots=np.array([0.1, 0.5, 0.8]), q=3)
+    assert ta.timestral_forecast(out, xd, od, asym, b, v, x.shape[1], horizon) == ta.E_INVALID
+    args = ta.timestral_forecast_args(out, xd, od, dm, b, v, x.shape[1], horizon)
+    args.flags = 0  # host pointers are not taken
+    import ctypes
+
+    assert ta.load().tsfm_timestral_forecast(ctypes.byref(args)) == ta.E_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert (out == 0).all()

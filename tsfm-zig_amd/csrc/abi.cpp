@@ -19,9 +19,11 @@
 #include <vector>
 
 #include "../../include/tsfm_attn.h"
+#include "abi_internal.hpp"
 #include "launch.hpp"
 
-namespace {
+namespace tsfm {
+namespace abi {
 
 pthread_once_t g_once = PTHREAD_ONCE_INIT;
 int g_ready = 0;
@@ -72,6 +74,23 @@ int ensure_ready() {
     if (!g_ready) return fail(TSFM_E_UNAVAILABLE, "%s", g_init_err);
     return TSFM_OK;
 }
+
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorNotSupported) return fail(TSFM_E_UNSUPPORTED, "%s: not supported", what);
+    return fail(TSFM_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace abi
+}  // namespace tsfm
+
+using tsfm::abi::ensure_ready;
+using tsfm::abi::fail;
+using tsfm::abi::g_device;
+using tsfm::abi::hip_fail;
+using tsfm::abi::Plan;
+using tsfm::abi::t_err;
+
+namespace {
 
 // ---- per-thread stream and staging buffer -------------------------------------------------------
 
@@ -163,20 +182,6 @@ hipError_t split_buf_for(ThreadCtx* c, hipStream_t stream, float** out, bool* ow
     return hipSuccess;
 }
 
-int hip_fail(hipError_t e, const char* what) {
-    if (e == hipErrorNotSupported) return fail(TSFM_E_UNSUPPORTED, "%s: not supported", what);
-    return fail(TSFM_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
-}
-
-// Sub-allocation plan over the staging buffer (256-byte aligned pieces).
-struct Plan {
-    size_t off = 0;
-    size_t take(size_t bytes) {
-        const size_t at = off;
-        off = (off + bytes + 255) & ~size_t(255);
-        return at;
-    }
-};
 
 size_t elem_size(int dtype) { return dtype == TSFM_DTYPE_F32 ? 4 : 2; }
 

@@ -1,0 +1,34 @@
+// Helpers shared by the translation units that implement the extern "C" ABI (abi.cpp,
+// timestral_abi.cpp): the thread's last-error message, one-time device set-up, and the
+// sub-allocation plan of scratch buffers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace tsfm {
+namespace abi {
+
+// Records this thread's error message (tsfm_attn_last_error) and returns `code`.
+int fail(int code, const char* fmt, ...);
+// Device set-up, once per process; TSFM_OK or TSFM_E_UNAVAILABLE.
+int ensure_ready();
+// fail() for a HIP error: TSFM_E_UNSUPPORTED for hipErrorNotSupported, else TSFM_E_DEVICE.
+int hip_fail(hipError_t e, const char* what);
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Sub-allocation plan over one scratch buffer (256-byte aligned pieces).
+struct Plan {
+    size_t off = 0;
+    size_t take(size_t bytes) {
+        const size_t at = off;
+        off = (off + bytes + 255) & ~size_t(255);
+        return at;
+    }
+};
+
+}  // namespace abi
+}  // namespace tsfm

@@ -42,11 +42,12 @@ struct VariateParams {
 hipError_t launch_variate(const VariateParams& p, hipStream_t stream);
 
 // Fused projection (proj.hip): output sel (0..n_out-1) is y_sel[token, :] = x[token, :] w_sel^T,
+// epilogues: kEpiRelu max(y, 0), kEpiSilu y / (1 + exp(-y)), kEpiResidual resid + y (after the bias),
 // width columns each (a multiple of 64, or of 4 with a single output); outputs 0 and 1 (q, k)
 // get RoPE when rope_cos is set. f32 in (out_dtype:
 // 0 f32, 1 bf16, 2 f16 out); d_in a multiple
 // of 16, width a multiple of 64, x_tok, y*_tok multiples of 4 and 16-byte aligned pointers.
-constexpr int kEpiNone = 0, kEpiRelu = 1, kEpiResidual = 2;
+constexpr int kEpiNone = 0, kEpiRelu = 1, kEpiResidual = 2, kEpiSilu = 3;
 struct ProjParams {
     const float* x; int64_t x_tok;
     const float *w0, *w1, *w2, *w3;  // (width, d_in) row-major each, rows w_ld apart
@@ -57,6 +58,9 @@ struct ProjParams {
     const float* bias;               // per output column, added before the epilogue (one output only)
     void *y0, *y1, *y2, *y3;             // f32, bf16 or f16 elements (out_dtype)
     int64_t y0_tok, y1_tok, y2_tok, y3_tok;
+    // Batch strides of the outputs: token t of series row b goes to b * y_batch + t * y_tok
+    // (0 = rows packed, b * seq * y_tok). Lets a projection write into a longer per-row buffer.
+    int64_t y0_batch, y1_batch, y2_batch, y3_batch;
     const float* rope_cos; const float* rope_sin;
     int64_t rope_table_stride;
     int32_t rope_rows_per_table, rope_row0;
@@ -116,5 +120,51 @@ hipError_t launch_chronos2_finish(const float* raw, const float* loc, const floa
                                   int q, int ps, int horizon, int arcsinh, hipStream_t stream);
 hipError_t launch_bolt_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int per,
                               hipStream_t stream);
+
+// ---- Timestral forecaster pieces (timestral.hip) ----
+struct TsStatsParams {
+    const float* ctx;
+    const uint8_t* mask;
+    int cap_t, cap_p, rows, ps, from, t, attend_missing;
+    double min_scale;
+    float *loc, *scale;
+    uint8_t* key_valid;
+    int* row_first;
+    double *state, *fold;  // (rows, 4) Welford of StatsJob, (rows, 3) refineBlock's patch fold
+};
+struct TsRope {
+    float inv_freq[32];  // model.zig:180-188: zero past rope_dim / 2
+};
+struct TsHead {
+    int ps, q, median, use_asinh;
+    float wf;          // quantile_width_factor
+    float widths[32];  // knot widths (model.zig:392-395), q <= 32
+};
+hipError_t launch_ts_context(const float* inputs, const uint8_t* observed, int R, int rows, int t0, int keep, int t,
+                             float* ctx, uint8_t* mask, int cap_t, uint8_t* nonneg, hipStream_t s);
+hipError_t launch_ts_stats(const TsStatsParams& p, hipStream_t s);
+hipError_t launch_ts_features(const float* ctx, const uint8_t* mask, int cap_t, const float* loc, const float* scale,
+                              int cap_p, int rows, int p0, int l, int ps, int use_asinh, float* feats, hipStream_t s);
+hipError_t launch_ts_rope_tables(const int* row_first, int groups, int vall, int n_tok, const TsRope& rp,
+                                 float* cos_t, float* sin_t, int* first_obs, hipStream_t s);
+hipError_t launch_ts_assemble(const float* emb, const float* query, float* x, int rows, int m, int h, int d,
+                              hipStream_t s);
+hipError_t launch_ts_mul_sigmoid(float* o, const float* g, int64_t n, hipStream_t s);
+hipError_t launch_ts_mul_silu(const float* hbuf, float* a, int64_t tokens, int hid, hipStream_t s);
+hipError_t launch_ts_head_finish(const float* raw, const float* loc, const float* scale, int cap_p, int l, int rows,
+                                 int h, const TsHead& hp, float* qs, hipStream_t s);
+hipError_t launch_ts_refine(float* qs, const float* loc, const float* scale, int cap_p, int l, const double* fold,
+                            int rows, int h, int ps, int q, int median, double min_scale, float* frames,
+                            hipStream_t s);
+hipError_t launch_ts_store_block(const float* qs, int rows, int R, int blen, int done, int horizon, int q, float* out,
+                                 float* mir, hipStream_t s);
+hipError_t launch_ts_feedback(const float* qs, int rows, int blen, int q, int median, float extreme, float* ctx,
+                              uint8_t* mask, int cap_t, int t, hipStream_t s);
+hipError_t launch_ts_slide(const float* src, const uint8_t* src_mask, float* dst, uint8_t* dst_mask, int rows,
+                           int cap_t, int start, int keep, hipStream_t s);
+hipError_t launch_ts_cap_bounds(const float* ctx, const uint8_t* mask, int cap_t, int t, int ps, const float* scale,
+                                int cap_p, int rows, float cap_k, float* bounds, hipStream_t s);
+hipError_t launch_ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R,
+                           int horizon, int q, int cap, int symmetric, int clip, hipStream_t s);
 
 }  // namespace tsfm

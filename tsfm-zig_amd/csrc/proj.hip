@@ -50,6 +50,26 @@ __device__ __forceinline__ void tile_of(int id, int m_tiles, int n_tiles, int& t
     tn = r / gm;
 }
 
+// Element offset of token m (of p.tokens, p.seq per series row) in output sel.
+__device__ __forceinline__ int64_t out_offset(const ProjParams& p, int sel, int m) {
+    const int64_t tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
+    const int64_t bat = sel == 0 ? p.y0_batch : sel == 1 ? p.y1_batch : sel == 2 ? p.y2_batch : p.y3_batch;
+    if (bat == 0) return (int64_t)m * tok;
+    const int b = m / p.seq;
+    return (int64_t)b * bat + (int64_t)(m - b * p.seq) * tok;
+}
+
+// The unary epilogues: nn.relu, and nn.silu (x / (1 + exp(-x))) of ResBlock(.silu).
+__device__ __forceinline__ f32x4 epi_act(int epi, f32x4 v) {
+    if (epi == kEpiRelu) return f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
+    if (epi == kEpiSilu) {
+#pragma clang fp contract(off)
+        return f32x4{v[0] / (1.f + expf(-v[0])), v[1] / (1.f + expf(-v[1])), v[2] / (1.f + expf(-v[2])),
+                     v[3] / (1.f + expf(-v[3]))};
+    }
+    return v;
+}
+
 // OUT: element type of the outputs, TSFM_DTYPE_* (0 f32, 1 bf16, 2 f16); the products and RoPE
 // are f32 either way and the result is rounded once, to nearest even, when it is stored.
 //
@@ -202,7 +222,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
         return;
     }
     void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
-    const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
     const bool rope = p.rope_cos != nullptr && sel < 2;
 #pragma unroll
     for (int mb = 0; mb < 2; mb++) {
@@ -219,7 +238,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
             const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq;
             rope4(sum[0][mb], sum[1][mb], ld4(p.rope_cos + at), ld4(p.rope_sin + at));
         }
-        const int64_t at = (int64_t)m * y_tok + col + cq;
+        const int64_t at = out_offset(p, sel, m) + col + cq;
         if constexpr (OUT == 0) {
             float* const out = static_cast<float*>(y) + at;
             const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col + cq : nullptr;
@@ -228,8 +247,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
                 if (col + cq + 32 * nb >= p.width) continue;
                 f32x4 v = sum[nb][mb];
                 if (p.bias != nullptr) v = v + ld4(p.bias + col + cq + 32 * nb);  // nn.linear's bias (linearCols, nn.zig:254)
-                if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
-                else if (p.epi == kEpiResidual) v = ld4(res + 32 * nb) + v;  // x + delta, one rounding
+                if (p.epi == kEpiResidual) v = ld4(res + 32 * nb) + v;  // x + delta, one rounding
+                else v = epi_act(p.epi, v);
                 st4(out + 32 * nb, v);
             }
         } else {
@@ -256,11 +275,10 @@ __global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
     if (p.alpha != 1.f) v *= p.alpha;
     const int sel = c / p.width, col = c - sel * p.width;
     if (p.bias != nullptr) v = v + ld4(p.bias + col);
-    if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
-    else if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + col) + v;
+    if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + col) + v;
+    else v = epi_act(p.epi, v);
     float* const y = static_cast<float*>(sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3);
-    const int64_t y_tok = sel == 0 ? p.y0_tok : sel == 1 ? p.y1_tok : sel == 2 ? p.y2_tok : p.y3_tok;
-    st4(y + (int64_t)m * y_tok + col, v);
+    st4(y + out_offset(p, sel, m) + col, v);
 }
 
 // proj_reduce for one output followed by the row norm of the finished rows: one wave per token
@@ -271,15 +289,15 @@ __global__ __launch_bounds__(256) void proj_reduce_norm(ProjParams p) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= p.tokens) return;
     const int W = p.width;
-    float* const y = static_cast<float*>(p.y0) + (int64_t)row * p.y0_tok;
+    float* const y = static_cast<float*>(p.y0) + out_offset(p, 0, row);
     float ss = 0.f;
     for (int c = 4 * lane; c < W; c += 256) {
         f32x4 v = ld4(p.partial + (int64_t)row * W + c);
         for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + row) * W + c);
         if (p.alpha != 1.f) v *= p.alpha;
         if (p.bias != nullptr) v = v + ld4(p.bias + c);
-        if (p.epi == kEpiRelu) v = f32x4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
-        else if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)row * p.resid_tok + c) + v;
+        if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)row * p.resid_tok + c) + v;
+        else v = epi_act(p.epi, v);
         st4(y + c, v);
         ss = sumsq4(ss, v);
     }
@@ -348,7 +366,9 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         (p.rope_cos != nullptr && p.width % kHeadDim) ||
         (p.out_dtype != 0 && (p.epi != kEpiNone || p.alpha != 1.f || p.bias != nullptr)) ||
         (p.bias != nullptr && p.n_out != 1) ||
-        (p.norm_scale != nullptr && (p.n_out != 1 || p.out_dtype != 0 || p.norm_out == nullptr)))
+        (p.norm_scale != nullptr && (p.n_out != 1 || p.out_dtype != 0 || p.norm_out == nullptr || p.y0_batch != 0)) ||
+        (p.epi != kEpiNone && (p.y0_batch | p.y1_batch | p.y2_batch | p.y3_batch) != 0) || p.epi < kEpiNone ||
+        p.epi > kEpiSilu)
         return hipErrorInvalidValue;
     if ((int64_t)((p.tokens + BM - 1) / BM) * ((p.width * p.n_out + BN - 1) / BN) > 0x7fffffff)
         return hipErrorInvalidValue;

@@ -60,6 +60,7 @@ EXPORTS = (
     "tsfm_variate_attend",
     "tsfm_qkv_project",
     "tsfm_qkv_project_noalloc",
+    "tsfm_timestral_forecast",
     "tsfm_chronos2_encode",
     "tsfm_chronos2_forward",
     "tsfm_bolt_forward",
@@ -214,6 +215,43 @@ class Resblock(ctypes.Structure):
 
     _fields_ = [(f, ctypes.c_void_p) for f in RESBLOCK_FIELDS] + [
         ("in", ctypes.c_int32), ("hid", ctypes.c_int32), ("out", ctypes.c_int32), ("act", ctypes.c_int32)]
+
+
+class TimestralAttn(ctypes.Structure):
+    """``tsfm_timestral_attn`` (include/tsfm_attn.h)."""
+
+    _fields_ = [("is_time", ctypes.c_int32), ("norm", ctypes.c_void_p), ("qkv", ctypes.c_void_p),
+                ("out", ctypes.c_void_p), ("gate", ctypes.c_void_p)]
+
+
+class TimestralLayer(ctypes.Structure):
+    """``tsfm_timestral_layer``."""
+
+    _fields_ = [("n_attn", ctypes.c_int32), ("attn", TimestralAttn * 2), ("mlp_norm", ctypes.c_void_p),
+                ("w12", ctypes.c_void_p), ("w3", ctypes.c_void_p)]
+
+
+class TimestralModel(ctypes.Structure):
+    """``tsfm_timestral_model``."""
+
+    _fields_ = [(f, ctypes.c_int32) for f in ("patch", "d_model", "heads", "head_dim", "mlp_hidden", "n_layers",
+                                              "n_quantiles", "block_size", "context_length", "rope_dim",
+                                              "use_asinh", "attend_missing")] + \
+               [(f, ctypes.c_float) for f in ("rope_theta", "norm_eps", "minimum_scale", "quantile_width_factor")] + \
+               [("quantile_knots", ctypes.c_void_p), ("patch_proj", Resblock), ("head", Resblock),
+                ("forecast_query", ctypes.c_void_p), ("out_norm", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(TimestralLayer))]
+
+
+class TimestralForecastArgs(ctypes.Structure):
+    """``tsfm_timestral_forecast_args``."""
+
+    _fields_ = [("model", TimestralModel), ("inputs", ctypes.c_void_p), ("observed", ctypes.c_void_p)] + \
+               [(f, ctypes.c_int32) for f in ("batch", "variates", "len", "horizon", "max_context", "per_shot_patches")] + \
+               [("quantile_real_cap_k", ctypes.c_float), ("extreme_value_threshold", ctypes.c_float),
+                ("symmetric_averaging", ctypes.c_int32), ("clip_nonnegative", ctypes.c_int32),
+                ("kv_cache", ctypes.c_int32), ("flags", ctypes.c_uint32), ("out", ctypes.c_void_p),
+                ("stream", ctypes.c_void_p)]
 
 
 class Chronos2EncodeArgs(ctypes.Structure):
@@ -433,6 +471,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_bolt_forecast.restype = ctypes.c_int
     lib.tsfm_chronos2_forecast.argtypes = [ctypes.POINTER(Chronos2ForecastArgs)]
     lib.tsfm_chronos2_forecast.restype = ctypes.c_int
+    lib.tsfm_timestral_forecast.argtypes = [ctypes.POINTER(TimestralForecastArgs)]
+    lib.tsfm_timestral_forecast.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -769,10 +809,10 @@ def chronos2_encode(x, key_valid, cos_t, sin_t, layers: Sequence[dict], final_no
     return int(load().tsfm_chronos2_encode(ctypes.byref(a)))
 
 
-def _resblock(rb: dict) -> Resblock:
-    st = Resblock(act=0)
+def _resblock(rb: dict, act: int = 0) -> Resblock:
+    st = Resblock(act=act)
     for f in RESBLOCK_FIELDS:
-        setattr(st, f, _ptr(rb[f]))
+        setattr(st, f, _ptr(rb.get(f)))
     hid, d_in = (int(x) for x in rb["hidden_w"].shape)
     st.hid = hid
     setattr(st, "in", d_in)
@@ -1014,3 +1054,51 @@ class KvCache:
             self.close()
         except Exception:
             pass
+
+
+# ---- Timestral forecast -------------------------------------------------------------------------
+
+
+def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, variates: int, length: int, horizon: int,
+                            max_context: int = 0, per_shot: int = 32, cap_k: float = 1e4, extreme: float = 1e30,
+                            symmetric: bool = True, clip_nonnegative: bool = True, kv_cache: bool = True,
+                            stream=None) -> "TimestralForecastArgs":
+    """``tsfm_timestral_forecast_args`` over device tensors. `model` holds the config and device
+    weights (keys as in the reference checkpoint's layout: patch_proj/head ResBlocks, layers with
+    attns [is_time, norm, qkv (permuted), out, gate] and mlp_norm/w12/w3, forecast_query, out_norm,
+    knots (host float64 array)). The returned block keeps references to what it points at."""
+    import numpy as np
+
+    layers = (TimestralLayer * max(1, len(model["layers"])))()
+    for i, ly in enumerate(model["layers"]):
+        layers[i].n_attn = len(ly["attns"])
+        for j, at in enumerate(ly["attns"]):
+            layers[i].attn[j] = TimestralAttn(int(at["is_time"]), _ptr(at["norm"]), _ptr(at["qkv"]), _ptr(at["out"]),
+                                              _ptr(at.get("gate")))
+        layers[i].mlp_norm, layers[i].w12, layers[i].w3 = _ptr(ly["mlp_norm"]), _ptr(ly["w12"]), _ptr(ly["w3"])
+    knots = np.ascontiguousarray(model["knots"], np.float64)
+    m = TimestralModel(patch=model["ps"], d_model=model["d"], heads=model["nh"], head_dim=64, mlp_hidden=model["hid"],
+                       n_layers=len(model["layers"]), n_quantiles=model["q"], block_size=model["block_size"],
+                       context_length=model["context_length"], rope_dim=model["rope_dim"],
+                       use_asinh=int(model["use_asinh"]), attend_missing=int(model["attend_missing"]),
+                       rope_theta=model["rope_theta"], norm_eps=model["norm_eps"], minimum_scale=model["minimum_scale"],
+                       quantile_width_factor=model["width_factor"], quantile_knots=knots.ctypes.data,
+                       patch_proj=_resblock(model["patch_proj"], act=1), head=_resblock(model["head"], act=1),
+                       forecast_query=_ptr(model["forecast_query"]), out_norm=_ptr(model["out_norm"]), layers=layers)
+    a = TimestralForecastArgs(model=m, inputs=_ptr(inputs), observed=_ptr(observed), batch=batch, variates=variates,
+                              len=length, horizon=horizon, max_context=max_context, per_shot_patches=per_shot,
+                              quantile_real_cap_k=cap_k, extreme_value_threshold=extreme,
+                              symmetric_averaging=int(symmetric), clip_nonnegative=int(clip_nonnegative),
+                              kv_cache=int(kv_cache), flags=DEVICE_PTRS, out=_ptr(out), stream=_stream_of(out, stream))
+    a._keep = (layers, knots, model, inputs, observed, out)
+    return a
+
+
+def timestral_forecast(out, inputs, observed, model: dict, batch: int, variates: int, length: int, horizon: int,
+                       **kw) -> int:
+    """Timestral forecaster.forecast (src/timestral/forecaster.zig:57-180) without covariates, on
+    device tensors: inputs (batch, variates, length) f32, observed (same) uint8, out (batch,
+    variates, horizon, q). Returns the ABI code."""
+    args = timestral_forecast_args(out, inputs, observed, model, batch, variates, length, horizon, **kw)
+    return int(load().tsfm_timestral_forecast(ctypes.byref(args)))
+
