@@ -424,39 +424,49 @@ def run_bolt_forward(torch, ta, workloads, peak):
 
 
 def run_bolt_forecast(torch, ta, workloads, peak):
+    import shutil
+    import tempfile
+
+    from tsfm_attn import checkpoint
+
     w = workloads.bolt_forward()
     a, m = w.arrays, w.meta
-    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
-    dev = {n: cu(v) for n, v in a.items()}
-    enc = [{k: cu(v) for k, v in ly.items()} for ly in m["enc"]]
-    dec = [{k: cu(v) for k, v in ly.items()} for ly in m["dec"]]
-    ie, oe = ({k: cu(v) for k, v in b.items()} for b in (m["ie"], m["oe"]))
-    out = torch.empty((w.B, m["out"]), dtype=torch.float32, device="cuda")
-    d, F, length = m["d_model"], m["d_ff"], a["ctx"].shape[1]
-
+    d, F, length, P = m["d_model"], m["d_ff"], a["ctx"].shape[1], m["out"] // 9
+    levels = np.linspace(0.1, 0.9, 9).astype(np.float32)
+    host = dict(reg=a["reg"], dec_start=a["dec_start"], rel_table=a["rel_table"], enc_final_norm=a["enc_final_norm"],
+                dec_final_norm=a["dec_final_norm"], enc=m["enc"], dec=m["dec"], ie=m["ie"], oe=m["oe"])
+    # The random-init checkpoint is written as config.json + model.safetensors and read back the way
+    # a caller loads a local model directory; the forecast then runs from the loaded weights.
+    ckpt = tempfile.mkdtemp(prefix="bolt_small_")
+    cfg = checkpoint.bolt_config_dict(d_model=d, d_ff=F, num_heads=w.H, num_layers=len(m["enc"]),
+                                      num_decoder_layers=len(m["dec"]), context_length=2048, patch=16,
+                                      prediction_length=P, quantiles=levels.tolist(), eps=m["eps"],
+                                      buckets=m["buckets"], max_distance=m["max_distance"])
+    checkpoint.write_bolt_checkpoint(ckpt, cfg, host)
+    fc = checkpoint.load_bolt(ckpt)
+    shutil.rmtree(ckpt, ignore_errors=True)  # the weights are on the device now
+    ctx_dev = torch.from_numpy(np.ascontiguousarray(a["ctx"])).cuda()
+    out = torch.empty((w.B, P, 9), dtype=torch.float32, device="cuda")
     # The argument block (about 130 weight pointers) is built once, as a caller holding a loaded
-    # model does; each step is one tsfm_bolt_forecast call.
-    args = ta.bolt_forecast_args(out, dev["ctx"], length, dev["reg"], dev["dec_start"], dev["rel_table"], enc,
-                                 dev["enc_final_norm"], dec, dev["dec_final_norm"], ie, oe, w.B, d, w.H, F, m["eps"],
-                                 num_buckets=m["buckets"], max_distance=m["max_distance"])
-    fn = ta.load().tsfm_bolt_forecast
+    # model does; each step is one forecaster.forecast call (tsfm_bolt_forecast_horizon).
+    args = fc.forecast_args(out, ctx_dev, P)
+    fn = ta.load().tsfm_bolt_forecast_horizon
 
     def step():
         _check(ta, fn(ctypes.byref(args)))
 
+    orc_w = dict(host, d_model=d, heads=w.H, d_ff=F, eps=m["eps"], buckets=m["buckets"], max_distance=m["max_distance"])
+
     def cpu_leg(B, lib=None):
         orc = _orc(lib)
-        want = np.zeros((B, m["out"]), np.float32)
         ctx = np.ascontiguousarray(a["ctx"][:B])
         t0 = time.perf_counter()
-        orc.bolt_forecast(cpu_threads(), want, ctx, length, 0, length, B, 16, 1e-5, a["reg"], a["dec_start"],
-                          a["rel_table"], m["buckets"], m["max_distance"], d, w.H, 64, F, m["enc"],
-                          a["enc_final_norm"], m["dec"], a["dec_final_norm"], m["eps"], m["ie"], m["oe"])
+        want = orc.bolt_forecast_horizon(cpu_threads(), ctx, P, orc_w, P, 2048, levels)
         return time.perf_counter() - t0, want, orc.lanes
 
-    config = {"workload": "bolt_small_forecast", "series": w.B, "context": length, "horizon": 64,
+    config = {"workload": "bolt_small_forecast", "series": w.B, "context": length, "horizon": P,
               "missing": "2 %", "d_model": d, "H": w.H, "d_ff": F, "layers": "6 enc + 6 dec",
-              "head": f"{m['out']} (9 quantiles x 64)", "weights": "random-init f32",
+              "head": f"{m['out']} (9 quantiles x {P})", "weights": "random-init f32, local config.json + model.safetensors",
               "input": "sinusoid (period 24, amplitude 10) + trend + N(0,1), seed 0"}
     return Bench(w, step, lambda: out.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
                  "TFLOP/s", w.B)

@@ -401,6 +401,30 @@ typedef struct tsfm_bolt_forecast_args {
 
 int tsfm_bolt_forecast(const tsfm_bolt_forecast_args *args);
 
+/* Chronos-Bolt forecaster.forecast (src/chronos_bolt/forecaster.zig:22-78) on device memory: any
+ * horizon. The first block forecasts prediction_length steps from the last context_length steps of
+ * each series; while the horizon is not reached, every quantile path becomes its own context row
+ * (the window grows by prediction_length steps, its oldest steps dropped past context_length), the
+ * q x q rows of a series give q * q samples per step, and the next block is their empirical
+ * quantiles at quantile_levels (torch.quantile's linear interpolation, quantileLinear :81-92).
+ * model: the weights and dims (batch = series); model.n_patch, feats, patch_valid, raw and
+ * keys_all_valid are not read. inputs (batch, t_in) f32, NaN = missing; out (batch, horizon, q).
+ * Device pointers only; asynchronous on model.stream. */
+typedef struct tsfm_bolt_horizon_args {
+    tsfm_bolt_forward_args model;
+    const float *inputs;
+    int32_t t_in, horizon;
+    int32_t patch;              /* input_patch_size; input_embed.in = 2 * patch */
+    int32_t prediction_length;  /* P: output_embed.out = n_quantiles * P */
+    int32_t context_length;     /* the window of every block */
+    int32_t n_quantiles;        /* 1..16 */
+    const float *quantile_levels;  /* host, n_quantiles (the config's quantiles as f32) */
+    float norm_eps;
+    float *out;
+} tsfm_bolt_horizon_args;
+
+int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args *args);
+
 /* ---------------------------------------------------------------------------------------------
  * Timestral forecast: forecaster.forecast (src/timestral/forecaster.zig:57-180) of a batch of
  * series whose rows are all target variates (no covariates; with covariates the caller keeps its

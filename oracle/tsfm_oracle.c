@@ -852,6 +852,84 @@ void orc_bolt_forecast(size_t threads, float *out, const float *ctx, size_t stri
     free(loc); free(scale); free(feats); free(pv); free(raw);
 }
 
+float orc_quantile_linear(const float *sorted, size_t n, float level) {
+    const float rank = level * (float)(n - 1);
+    const float lo_f = floorf(rank);
+    const size_t lo = (size_t)lo_f;
+    size_t hi = (size_t)ceilf(rank);
+    if (hi > n - 1) hi = n - 1;
+    const float w = rank - lo_f, a = sorted[lo], bb = sorted[hi];
+    if (w < 0.5f) {
+        const float t = w * (bb - a);
+        return a + t;
+    }
+    const float t = (bb - a) * (1 - w);
+    return bb - t;
+}
+
+static int orc_cmp_f32(const void *x, const void *y) {
+    const float a = *(const float *)x, b = *(const float *)y;
+    return a < b ? -1 : (a > b ? 1 : 0);
+}
+
+static void orc_bolt_block(size_t threads, float *out, const float *ctx, size_t stride, size_t offset, size_t len,
+                           size_t n, size_t ps, float norm_eps, const orc_bolt_model *m) {
+    orc_bolt_forecast(threads, out, ctx, stride, offset, len, n, ps, norm_eps, m->reg, m->dec_start, m->rel_table,
+                      m->num_buckets, m->max_distance, m->d, m->nh, m->hd, m->d_ff, m->enc, m->n_enc, m->enc_final_norm,
+                      m->dec, m->n_dec, m->dec_final_norm, m->eps, m->input_embed, m->output_embed);
+}
+
+/* storeBlock (forecaster.zig:95-103): pred (b, q, P) into out (b, horizon, q) from step start. */
+static void orc_bolt_store(float *out, const float *pred, size_t b, size_t q, size_t P, size_t horizon, size_t start) {
+    for (size_t s = 0; s < b; s++)
+        for (size_t p = 0; p < P && start + p < horizon; p++)
+            for (size_t qi = 0; qi < q; qi++) out[(s * horizon + start + p) * q + qi] = pred[(s * q + qi) * P + p];
+}
+
+void orc_bolt_forecast_horizon(size_t threads, float *out, const float *inputs, size_t b, size_t t_in, size_t horizon,
+                               size_t ps, size_t P, size_t max_ctx, const float *levels, size_t q, float norm_eps,
+                               const orc_bolt_model *m) {
+    const size_t len0 = t_in < max_ctx ? t_in : max_ctx;
+    float *pred = (float *)malloc(b * q * P * sizeof(float));
+    orc_bolt_block(threads, pred, inputs, t_in, t_in - len0, len0, b, ps, norm_eps, m);
+    orc_bolt_store(out, pred, b, q, P, horizon, 0);
+    size_t done = P < horizon ? P : horizon;
+    if (done < horizon) {
+        /* every quantile path its own context row */
+        size_t len = len0;
+        float *cur = (float *)malloc(b * q * len * sizeof(float));
+        for (size_t s = 0; s < b; s++)
+            for (size_t qi = 0; qi < q; qi++)
+                memcpy(cur + (s * q + qi) * len, inputs + s * t_in + t_in - len0, len0 * sizeof(float));
+        float *samples = (float *)malloc(q * q * sizeof(float));
+        float *raw = (float *)malloc(b * q * q * P * sizeof(float));
+        while (done < horizon) {
+            const size_t new_len = len + P < max_ctx ? len + P : max_ctx, skip = len + P - new_len;
+            float *next = (float *)malloc(b * q * new_len * sizeof(float));
+            for (size_t row = 0; row < b * q; row++)
+                for (size_t i = 0; i < new_len; i++) {
+                    const size_t j = skip + i;
+                    next[row * new_len + i] = j < len ? cur[row * len + j] : pred[row * P + (j - len)];
+                }
+            free(cur);
+            cur = next;
+            len = new_len;
+            orc_bolt_block(threads, raw, cur, len, 0, len, b * q, ps, norm_eps, m);
+            for (size_t s = 0; s < b; s++)
+                for (size_t p = 0; p < P; p++) {
+                    for (size_t k = 0; k < q * q; k++) samples[k] = raw[(s * q * q + k) * P + p];
+                    qsort(samples, q * q, sizeof(float), orc_cmp_f32);
+                    for (size_t qi = 0; qi < q; qi++)
+                        pred[(s * q + qi) * P + p] = orc_quantile_linear(samples, q * q, levels[qi]);
+                }
+            orc_bolt_store(out, pred, b, q, P, horizon, done);
+            done += P;
+        }
+        free(cur); free(samples); free(raw);
+    }
+    free(pred);
+}
+
 /* src/chronos2/forecaster.zig:59-204 (runChunk) for the series of one chunk. */
 void orc_chronos2_forecast(size_t threads, float *out, const float *inputs, size_t stride, size_t start, size_t len,
                            size_t n, size_t ps, size_t horizon, float time_scale, int arcsinh, const float *reg,

@@ -160,6 +160,29 @@ void orc_bolt_forecast(size_t threads, float *out, const float *ctx, size_t stri
                        const float *enc_final_norm, const orc_bolt_dec_layer *dec, size_t n_dec,
                        const float *dec_final_norm, float eps, const orc_resblock *input_embed,
                        const orc_resblock *output_embed);
+/* The Chronos-Bolt weights and dims, bundled for the forecaster loop. */
+typedef struct orc_bolt_model {
+    const float *reg, *dec_start, *rel_table;
+    uint32_t num_buckets, max_distance;
+    size_t d, nh, hd, d_ff;
+    const orc_bolt_enc_layer *enc;
+    size_t n_enc;
+    const float *enc_final_norm;
+    const orc_bolt_dec_layer *dec;
+    size_t n_dec;
+    const float *dec_final_norm;
+    float eps;
+    const orc_resblock *input_embed, *output_embed;
+} orc_bolt_model;
+/* quantileLinear (src/chronos_bolt/forecaster.zig:81-92): torch.quantile's linear interpolation
+ * of an ascending slice at `level`, ATen's two-sided lerp. */
+float orc_quantile_linear(const float *sorted, size_t n, float level);
+/* Chronos-Bolt forecaster.forecast (src/chronos_bolt/forecaster.zig:22-78): out (b, horizon, q);
+ * inputs (b, t_in), NaN = missing; levels (q) the config's quantiles as f32; P the model's
+ * prediction_length (output_embed->out = q * P), max_ctx its context_length. */
+void orc_bolt_forecast_horizon(size_t threads, float *out, const float *inputs, size_t b, size_t t_in, size_t horizon,
+                               size_t ps, size_t P, size_t max_ctx, const float *levels, size_t q, float norm_eps,
+                               const orc_bolt_model *m);
 /* Timestral key validity and first observed patch (src/timestral/model.zig:343-362). obs: (rows, w)
  * observation bytes, w = ne * ps; key_valid: (rows, ne) out; first_obs: (rows / vall) out, the first
  * patch with an observation in any row of the group, 0 when the group has none. With

@@ -62,6 +62,39 @@ class BoltDecLayer(ctypes.Structure):
     _fields_ = [(f, _vp) for f in BOLT_DEC_FIELDS]
 
 
+class OrcBoltModel(ctypes.Structure):
+    _fields_ = [("reg", ctypes.c_void_p), ("dec_start", ctypes.c_void_p), ("rel_table", ctypes.c_void_p),
+                ("num_buckets", ctypes.c_uint32), ("max_distance", ctypes.c_uint32), ("d", ctypes.c_size_t),
+                ("nh", ctypes.c_size_t), ("hd", ctypes.c_size_t), ("d_ff", ctypes.c_size_t),
+                ("enc", ctypes.POINTER(BoltEncLayer)), ("n_enc", ctypes.c_size_t), ("enc_final_norm", ctypes.c_void_p),
+                ("dec", ctypes.POINTER(BoltDecLayer)), ("n_dec", ctypes.c_size_t), ("dec_final_norm", ctypes.c_void_p),
+                ("eps", ctypes.c_float), ("input_embed", ctypes.POINTER(OrcResblock)),
+                ("output_embed", ctypes.POINTER(OrcResblock))]
+
+
+def bolt_model_struct(w):
+    """OrcBoltModel over a dict with reg, dec_start, rel_table, enc, dec, enc_final_norm,
+    dec_final_norm, ie, oe (host arrays) and d_model, heads, d_ff, eps, buckets, max_distance. The
+    struct keeps what it points to alive."""
+    enc, dec = w["enc"], w["dec"]
+    ea = (BoltEncLayer * max(1, len(enc)))()
+    for i, ly in enumerate(enc):
+        for f in BOLT_ENC_FIELDS:
+            setattr(ea[i], f, ptr(ly[f]))
+    da = (BoltDecLayer * max(1, len(dec)))()
+    for i, ly in enumerate(dec):
+        for f in BOLT_DEC_FIELDS:
+            setattr(da[i], f, ptr(ly[f]))
+    ie, oe = resblock_struct(w["ie"]), resblock_struct(w["oe"])
+    m = OrcBoltModel(reg=ptr(w["reg"]), dec_start=ptr(w["dec_start"]), rel_table=ptr(w["rel_table"]),
+                     num_buckets=w["buckets"], max_distance=w["max_distance"], d=w["d_model"], nh=w["heads"], hd=64,
+                     d_ff=w["d_ff"], enc=ea, n_enc=len(enc), enc_final_norm=ptr(w["enc_final_norm"]), dec=da,
+                     n_dec=len(dec), dec_final_norm=ptr(w["dec_final_norm"]), eps=w["eps"],
+                     input_embed=ctypes.pointer(ie), output_embed=ctypes.pointer(oe))
+    m._keep = (ea, da, ie, oe, w)
+    return m
+
+
 class TimestralAttn(ctypes.Structure):
     """orc_timestral_attn (oracle/tsfm_oracle.h)."""
 
@@ -168,6 +201,10 @@ class Oracle:
         L.orc_timestral_forecast.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz, _sz, _sz,
                                              _sz, _f, _f, ctypes.c_int, ctypes.c_int]
         L.orc_timestral_forecast.restype = ctypes.c_int
+        L.orc_quantile_linear.argtypes = [_vp, _sz, _f]
+        L.orc_quantile_linear.restype = _f
+        L.orc_bolt_forecast_horizon.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _sz, _f,
+                                                ctypes.POINTER(OrcBoltModel)]
         L.orc_batched_self_attend.argtypes = [_sz, ctypes.c_int, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz, _sz, _vp, _sz,
                                               _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _f]
 
@@ -262,6 +299,21 @@ class Oracle:
                                    ptr(dec_start), ptr(rel_table), buckets, max_distance, d, nh, hd, d_ff, ea, len(enc),
                                    ptr(enc_final_norm), da, len(dec), ptr(dec_final_norm), eps, ctypes.byref(ie),
                                    ctypes.byref(oe))
+
+    def quantile_linear(self, sorted_vals, level):
+        a = np.ascontiguousarray(sorted_vals, np.float32)
+        return np.float32(self.lib.orc_quantile_linear(ptr(a), a.size, level))
+
+    def bolt_forecast_horizon(self, threads, inputs, horizon, w, P, max_ctx, levels, ps=16, norm_eps=1e-5):
+        """(b, horizon, q) of forecaster.forecast for inputs (b, t_in); w as bolt_model_struct takes."""
+        x = np.ascontiguousarray(inputs, np.float32)
+        b, t_in = x.shape
+        lv = np.ascontiguousarray(levels, np.float32)
+        out = np.zeros((b, horizon, lv.size), np.float32)
+        m = bolt_model_struct(w)
+        self.lib.orc_bolt_forecast_horizon(threads, ptr(out), ptr(x), b, t_in, horizon, ps, P, max_ctx, ptr(lv),
+                                           lv.size, norm_eps, ctypes.byref(m))
+        return out
 
     def gemm_nn(self, c, ldc, a, lda, b, ldb, m, n, k):
         self.lib.orc_gemm_nn(ptr(c), ldc, ptr(a), lda, ptr(b), ldb, m, n, k)

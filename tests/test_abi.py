@@ -39,6 +39,7 @@ def test_library_exports_every_declared_symbol(ta):
                                           ("BoltEncLayer", "tsfm_bolt_enc_layer"), ("BoltDecLayer", "tsfm_bolt_dec_layer"),
                                           ("BoltForwardArgs", "tsfm_bolt_forward_args"),
                                           ("BoltForecastArgs", "tsfm_bolt_forecast_args"),
+                                          ("BoltHorizonArgs", "tsfm_bolt_horizon_args"),
                                           ("Chronos2ForecastArgs", "tsfm_chronos2_forecast_args"),
                                           ("TimestralAttn", "tsfm_timestral_attn"),
                                           ("TimestralLayer", "tsfm_timestral_layer"),

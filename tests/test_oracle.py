@@ -1014,3 +1014,83 @@ def test_timestral_forecast_symmetric_clip_and_cap(orc):
         lo, hi = vals.min() - a, vals.max() + a
         assert capped.reshape(b * v, -1)[r].min() >= lo - 1e-4 and capped.reshape(b * v, -1)[r].max() <= hi + 1e-4
     assert not np.array_equal(capped, f)
+
+
+# ---- Chronos-Bolt long horizons (src/chronos_bolt/forecaster.zig:22-92) ----------------------------
+
+
+def test_quantile_linear_reference_cases(orc):
+    """The reference's own test of quantileLinear (forecaster.zig:222-228)."""
+    v = np.array([1, 2, 4, 8, 16], np.float32)
+    assert orc.quantile_linear(v, 0.0) == 1
+    assert orc.quantile_linear(v, 0.5) == 4
+    assert orc.quantile_linear(v, 1.0) == 16
+    assert abs(orc.quantile_linear(v, 0.375) - 3) <= 1e-6
+
+
+@pytest.mark.parametrize("n", [2, 7, 81])
+def test_quantile_linear_is_torch_quantile(orc, n):
+    """torch.quantile (linear interpolation) over sorted random samples, levels on and between the
+    sample ranks, both halves of the lerp: within one f32 rounding of torch's own result."""
+    import torch
+
+    rng = np.random.default_rng(n)
+    for _ in range(20):
+        v = np.sort(rng.standard_normal(n).astype(np.float32) * 10)
+        for lv in (0.0, 0.1, 0.2, 0.25, 0.3, 0.5, 0.6, 0.7, 0.8, 0.9, 0.95, 1.0):
+            want = torch.quantile(torch.from_numpy(v), torch.tensor(lv, dtype=torch.float32)).item()
+            got = float(orc.quantile_linear(v, lv))
+            assert abs(got - want) <= 2.4e-7 * max(1.0, abs(want)), (n, lv, got, want)
+
+
+def _bolt_small(seed=0, P=16, q=9):
+    from tsfm_attn import workloads
+
+    w = workloads.bolt_forward(B=2, n_patch=2, H=2, d_ff=256, n_layers=1, quantiles=q, horizon=P, seed=seed)
+    a, m = w.arrays, w.meta
+    return dict(reg=a["reg"], dec_start=a["dec_start"], rel_table=a["rel_table"], enc=m["enc"], dec=m["dec"],
+                enc_final_norm=a["enc_final_norm"], dec_final_norm=a["dec_final_norm"], ie=m["ie"], oe=m["oe"],
+                d_model=m["d_model"], heads=w.H, d_ff=m["d_ff"], eps=m["eps"], buckets=m["buckets"],
+                max_distance=m["max_distance"])
+
+
+def _bolt_block(orc, w, ctx, P, q):
+    ctx = np.ascontiguousarray(ctx, np.float32)
+    n, length = ctx.shape
+    out = np.zeros((n, q * P), np.float32)
+    orc.bolt_forecast(1, out, ctx, length, 0, length, n, 16, 1e-5, w["reg"], w["dec_start"], w["rel_table"],
+                      w["buckets"], w["max_distance"], w["d_model"], w["heads"], 64, w["d_ff"], w["enc"],
+                      w["enc_final_norm"], w["dec"], w["dec_final_norm"], w["eps"], w["ie"], w["oe"])
+    return out.reshape(n, q, P)
+
+
+@pytest.mark.parametrize("t_in,max_ctx,horizon", [(70, 96, 50), (40, 2048, 16), (40, 2048, 7), (130, 64, 33)])
+def test_bolt_forecast_horizon_composition(orc, t_in, max_ctx, horizon):
+    """forecaster.forecast as a composition of the chunk forecast: block 0 from the last max_ctx
+    steps; then each series' q quantile paths appended to its window (the oldest steps dropped past
+    max_ctx), forecast as q rows each, sorted per step over the q * q outputs and reduced with
+    quantileLinear. Written here with whole-array operations (repeat, concatenate, trailing slice,
+    sort); the oracle's loop must give the same bits."""
+    P, q = 16, 9
+    w = _bolt_small(P=P, q=q)
+    levels = np.linspace(0.1, 0.9, q).astype(np.float32)
+    rng = np.random.default_rng(t_in)
+    b = 2
+    t = np.arange(t_in)
+    x = (10 * np.sin(2 * np.pi * t / 24) + 0.05 * t + rng.standard_normal((b, t_in))).astype(np.float32)
+    x[rng.random(x.shape) < 0.05] = np.nan
+    got = orc.bolt_forecast_horizon(1, x, horizon, w, P, max_ctx, levels)
+
+    ctx = x[:, -max_ctx:]
+    pred = _bolt_block(orc, w, ctx, P, q)
+    steps = [pred.transpose(0, 2, 1)]
+    paths = np.repeat(ctx, q, axis=0)
+    while sum(s.shape[1] for s in steps) < horizon:
+        paths = np.concatenate([paths, pred.reshape(b * q, P)], axis=1)[:, -max_ctx:]
+        srt = np.sort(_bolt_block(orc, w, paths, P, q).reshape(b, q * q, P), axis=1)
+        pred = np.array([[[orc.quantile_linear(srt[s, :, p], lv) for p in range(P)] for lv in levels]
+                         for s in range(b)], np.float32)
+        steps.append(pred.transpose(0, 2, 1))
+    want = np.concatenate(steps, axis=1)[:, :horizon]
+    assert got.shape == (b, horizon, q)
+    assert np.array_equal(got, want)

@@ -121,6 +121,20 @@ hipError_t launch_chronos2_finish(const float* raw, const float* loc, const floa
 hipError_t launch_bolt_finish(const float* raw, const float* loc, const float* scale, float* out, int n, int per,
                               hipStream_t stream);
 
+// ---- Chronos-Bolt long horizons (bolt_horizon.hip) ----
+struct BoltLevels {
+    float v[16];
+};
+// pred (b, q, P) -> steps [start, start + P) of out (b, horizon, q).
+hipError_t launch_bolt_store_block(const float* pred, int b, int q, int P, int horizon, int start, float* out,
+                                   hipStream_t s);
+// dst (rows, new_len): row r = the last new_len steps of (src row r / rep ++ pred row r).
+hipError_t launch_bolt_window(const float* src, int64_t src_stride, int64_t src_off, int len, int rep,
+                              const float* pred, int P, float* dst, int new_len, int rows, hipStream_t s);
+// raw (b * q, q, P) -> pred (b, q, P): the q levels of the q * q samples of each (series, step).
+hipError_t launch_bolt_sample_quantiles(const float* raw, int b, int q, int P, const BoltLevels& lv, float* pred,
+                                        hipStream_t s);
+
 // ---- Timestral forecaster pieces (timestral.hip) ----
 struct TsStatsParams {
     const float* ctx;

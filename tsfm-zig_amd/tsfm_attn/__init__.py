@@ -65,6 +65,7 @@ EXPORTS = (
     "tsfm_chronos2_forward",
     "tsfm_bolt_forward",
     "tsfm_bolt_forecast",
+    "tsfm_bolt_forecast_horizon",
     "tsfm_chronos2_forecast",
     "tsfm_weight_register",
     "tsfm_weight_release",
@@ -362,6 +363,24 @@ class Chronos2ForecastArgs(ctypes.Structure):
     ]
 
 
+class BoltHorizonArgs(ctypes.Structure):
+    """``tsfm_bolt_horizon_args`` (include/tsfm_attn.h)."""
+
+    _fields_ = [
+        ("model", BoltForwardArgs),
+        ("inputs", ctypes.c_void_p),
+        ("t_in", ctypes.c_int32),
+        ("horizon", ctypes.c_int32),
+        ("patch", ctypes.c_int32),
+        ("prediction_length", ctypes.c_int32),
+        ("context_length", ctypes.c_int32),
+        ("n_quantiles", ctypes.c_int32),
+        ("quantile_levels", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
+        ("out", ctypes.c_void_p),
+    ]
+
+
 class BoltForecastArgs(ctypes.Structure):
     """``tsfm_bolt_forecast_args`` (include/tsfm_attn.h)."""
 
@@ -469,6 +488,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_bolt_forward.restype = ctypes.c_int
     lib.tsfm_bolt_forecast.argtypes = [ctypes.POINTER(BoltForecastArgs)]
     lib.tsfm_bolt_forecast.restype = ctypes.c_int
+    lib.tsfm_bolt_forecast_horizon.argtypes = [ctypes.POINTER(BoltHorizonArgs)]
+    lib.tsfm_bolt_forecast_horizon.restype = ctypes.c_int
     lib.tsfm_chronos2_forecast.argtypes = [ctypes.POINTER(Chronos2ForecastArgs)]
     lib.tsfm_chronos2_forecast.restype = ctypes.c_int
     lib.tsfm_timestral_forecast.argtypes = [ctypes.POINTER(TimestralForecastArgs)]
@@ -962,6 +983,42 @@ def bolt_forecast_args(out, ctx, length, reg, dec_start, rel_table, enc_layers, 
     a = BoltForecastArgs(model=m, ctx=_ptr(ctx), stride=length if stride is None else stride, offset=offset,
                          len=length, patch=patch, norm_eps=norm_eps, out=_ptr(out))
     a._keep = m._keep
+    return a
+
+
+def bolt_forecast_horizon(out, inputs, horizon: int, reg, dec_start, rel_table, enc_layers: Sequence[dict],
+                          enc_final_norm, dec_layers: Sequence[dict], dec_final_norm, input_embed: dict,
+                          output_embed: dict, d: int, nh: int, d_ff: int, eps: float, quantile_levels,
+                          prediction_length: int, context_length: int, patch: int = 16, norm_eps: float = 1e-5,
+                          num_buckets: int = 32, max_distance: int = 128, hd: int = 64, stream=None) -> int:
+    """Chronos-Bolt forecaster.forecast (src/chronos_bolt/forecaster.zig:22-78) on device tensors,
+    any horizon: inputs (b, t_in) f32 (NaN = missing), out (b, horizon, q). Returns the ABI code."""
+    a = bolt_forecast_horizon_args(out, inputs, horizon, reg, dec_start, rel_table, enc_layers, enc_final_norm,
+                                   dec_layers, dec_final_norm, input_embed, output_embed, d, nh, d_ff, eps,
+                                   quantile_levels, prediction_length, context_length, patch, norm_eps, num_buckets,
+                                   max_distance, hd, stream)
+    return int(load().tsfm_bolt_forecast_horizon(ctypes.byref(a)))
+
+
+def bolt_forecast_horizon_args(out, inputs, horizon, reg, dec_start, rel_table, enc_layers, enc_final_norm,
+                               dec_layers, dec_final_norm, input_embed, output_embed, d, nh, d_ff, eps,
+                               quantile_levels, prediction_length, context_length, patch=16, norm_eps=1e-5,
+                               num_buckets=32, max_distance=128, hd=64, stream=None) -> BoltHorizonArgs:
+    """The argument block of bolt_forecast_horizon, built once for repeated calls (it keeps what it
+    points to alive)."""
+    import numpy as np
+
+    if not _is_device(inputs):
+        raise ValueError("bolt_forecast_horizon runs on device tensors")
+    b, t_in = int(inputs.shape[0]), int(inputs.shape[1])
+    levels = np.ascontiguousarray(quantile_levels, np.float32)
+    m = bolt_forward_args(enc_layers, dec_layers, None, None, reg, dec_start, rel_table, enc_final_norm, dec_final_norm,
+                          input_embed, output_embed, None, b, 0, d, nh, hd, d_ff, eps, num_buckets, max_distance, False,
+                          True, stream)
+    a = BoltHorizonArgs(model=m, inputs=_ptr(inputs), t_in=t_in, horizon=horizon, patch=patch,
+                        prediction_length=prediction_length, context_length=context_length, n_quantiles=levels.size,
+                        quantile_levels=levels.ctypes.data, norm_eps=norm_eps, out=_ptr(out))
+    a._keep = (m._keep, levels, inputs, out)
     return a
 
 
