@@ -100,6 +100,33 @@ def test_half_long_left_padding(ta, orc, gpu_ready, name, mask):
 
 
 @pytest.mark.parametrize("name", DTYPES)
+@pytest.mark.parametrize("mask", [0, 2, 3])
+@pytest.mark.parametrize("growth", [1 / 64, 1 / 8])
+def test_half_growing_scores(ta, orc, gpu_ready, name, mask, growth):
+    """Keys scaled by 1 + growth * key: each row's maximum score keeps rising along the keys, by
+    several exp2 units per 64-key tile, so mask-free tiles taken against the running max as it
+    stands overflow the weights' range and are redone with the max pass, over and over."""
+    B, H, n = 2, 2, 600
+    q, k, v, kv = _inputs(500 + mask, B, H, n, n)
+    k *= (1.0 + growth * np.arange(n, dtype=np.float32))[None, :, None]
+    got, qr, kr, vr = _run_half(ta, name, mask, q, k, v, kv, B, H, n, n, 0.125)
+    want = _oracle(orc, mask, qr, kr, vr, kv, B, H, n, 0.125)
+    assert _ref.scaled_err(got, want) <= TOL_HALF
+
+
+@pytest.mark.parametrize("name", DTYPES)
+@pytest.mark.parametrize("mask", [0, 2, 3])
+def test_half_scale_one(ta, orc, gpu_ready, name, mask):
+    """Unscaled logits (scale 1.0, standard deviation 8 on these inputs): q is not pre-multiplied
+    by scale * log2(e) (> 1), and the weights are far from uniform."""
+    B, H, n = 2, 2, 400
+    q, k, v, kv = _inputs(600 + mask, B, H, n, n)
+    got, qr, kr, vr = _run_half(ta, name, mask, q, k, v, kv, B, H, n, n, 1.0)
+    want = _oracle(orc, mask, qr, kr, vr, kv, B, H, n, 1.0)
+    assert _ref.scaled_err(got, want) <= TOL_HALF
+
+
+@pytest.mark.parametrize("name", DTYPES)
 def test_half_decoder_mask_matches_float64(ta, gpu_ready, name):
     B, H, ne, h, l = 3, 2, 80, 9, 70
     sl = ne + h
