@@ -504,8 +504,12 @@ int tsfm_timestral_forecast(const tsfm_timestral_forecast_args *args);
  *   with leading dimensions; host pointers, synchronous; b_buf = a registered weight (B unused)
  *   or NULL (B uploaded). 0 = done; non-zero = use the CPU. Runs when k % 16 == 0 and n, lda,
  *   ldb, ldc are multiples of 4 (every linear layer of the three families).
- * tsfm_sgemm_nn: cuda_sgemm_nn (gemm.c:324-330); always returns TSFM_E_UNSUPPORTED (the caller's
- *   CPU path runs): its one user, the attention's P.V product, runs inside tsfm_attn_fwd. */
+ * tsfm_sgemm_nn: cuda_sgemm_nn (gemm.c:324-330): C[m, n] = A[m, k] B[k, n], row-major with leading
+ *   dimensions; host pointers, synchronous; b_buf = a registered weight holding B as [k][ldb]
+ *   (B unused) or NULL (B uploaded). B is transposed on the device and the product runs on the same
+ *   kernel as tsfm_sgemm_nt. Runs when k % 16 == 0 and n, lda, ldc are multiples of 4 (ldb any
+ *   >= n). Its caller in the reference is gemmNN (src/core/nn.zig:165-239), the attention's P.V
+ *   product, which tsfm_attn_fwd runs inside its kernels; this is the seam for any other. */
 void *tsfm_weight_register(const float *data, size_t len);
 void tsfm_weight_release(void *handle);
 int tsfm_sgemm_nt(int m, int n, int k, float alpha, const float *A, int lda, const float *B, int ldb, float *C,

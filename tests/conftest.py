@@ -16,6 +16,13 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a gfx950 (MI355X) GPU")
 
 
+# A sanitizer run (tests/test_sanitizers.py) points the oracle fixtures at the ASan/UBSan builds
+# (liboracle_san_l8.so / liboracle_san_l16.so) and the product fixture at the sanitized library
+# through these variables.
+ORACLE_SANITIZED = os.environ.get("TSFM_TEST_ORACLE_SANITIZED") == "1"
+PRODUCT_OVERRIDE = os.environ.get("TSFM_TEST_PRODUCT_LIB")
+
+
 def _ensure_oracle():
     """The oracle is plain C; build it here if build() has not run yet (gcc only)."""
     lib = ROOT / "oracle" / "liboracle_l8.so"
@@ -23,12 +30,16 @@ def _ensure_oracle():
         subprocess.run(["make", "-C", str(ROOT / "oracle")], check=True, capture_output=True)
 
 
+def _oracle_lib(name):
+    return ROOT / "oracle" / (name.replace("liboracle_", "liboracle_san_") if ORACLE_SANITIZED else name)
+
+
 @pytest.fixture(scope="session")
 def orc():
     _ensure_oracle()
     import _oracle
 
-    return _oracle.Oracle(ROOT / "oracle" / "liboracle_l8.so")
+    return _oracle.Oracle(_oracle_lib("liboracle_l8.so"))
 
 
 @pytest.fixture(scope="session")
@@ -36,7 +47,7 @@ def orc16():
     _ensure_oracle()
     import _oracle
 
-    return _oracle.Oracle(ROOT / "oracle" / "liboracle_l16.so")
+    return _oracle.Oracle(_oracle_lib("liboracle_l16.so"))
 
 
 def host_has_avx512() -> bool:
@@ -51,7 +62,7 @@ def orc_host():
     _ensure_oracle()
     import _oracle
 
-    return _oracle.Oracle(ROOT / "oracle" / ("liboracle_l16.so" if host_has_avx512() else "liboracle_l8.so"))
+    return _oracle.Oracle(_oracle_lib("liboracle_l16.so" if host_has_avx512() else "liboracle_l8.so"))
 
 
 @pytest.fixture(scope="session")
@@ -59,7 +70,10 @@ def ta():
     """The product binding (tsfm-zig_amd/tsfm_attn); fails if the library is not built."""
     import tsfm_attn
 
-    tsfm_attn.load()
+    if PRODUCT_OVERRIDE:
+        tsfm_attn._lib = tsfm_attn.load(PRODUCT_OVERRIDE)
+    else:
+        tsfm_attn.load()
     return tsfm_attn
 
 

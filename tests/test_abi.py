@@ -235,10 +235,22 @@ def test_sgemm_nt_argument_codes(ta, m, n, k, lda, ldb, ldc, code):
     assert ta.last_error()
 
 
-def test_sgemm_nn_declines(ta):
-    a = np.zeros(64, np.float32)
-    lib = ta.load()
-    assert lib.tsfm_sgemm_nn(4, 4, 4, a.ctypes.data, 4, a.ctypes.data, 4, a.ctypes.data, 4, None) == ta.E_UNSUPPORTED
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc,code", [
+    (0, 4, 16, 16, 4, 4, 3),      # empty product
+    (4, 4, 16, 8, 4, 4, 3),       # lda < k
+    (4, 8, 16, 16, 4, 8, 3),      # ldb < n
+    (4, 8, 16, 16, 8, 4, 3),      # ldc < n
+    (4, 4, 12, 12, 4, 4, 2),      # k not a multiple of 16
+    (4, 6, 16, 16, 6, 6, 2),      # n not a multiple of 4
+    (4, 4, 16, 18, 4, 4, 2),      # lda not a multiple of 4
+])
+def test_sgemm_nn_argument_codes(ta, m, n, k, lda, ldb, ldc, code):
+    """cuda_sgemm_nn's arguments (src/platform/cuda/gemm.c:324-330): B is [k][ldb]."""
+    a = np.zeros(max(m, 1) * lda, np.float32)
+    b = np.zeros(k * ldb, np.float32)
+    c = np.zeros(max(m, 1) * ldc, np.float32)
+    assert ta.sgemm_nn(m, n, k, a, lda, b, ldb, c, ldc) == code
+    assert ta.last_error()
 
 
 def _encode_args(ta, **over):
@@ -306,3 +318,103 @@ def test_chronos2_forecast_is_device_only(ta):
     a.model.enc.batch = 1
     assert lib.tsfm_chronos2_forecast(ctypes.byref(a)) == ta.E_UNSUPPORTED
     assert "device" in ta.last_error()
+
+
+_FUZZ = r'''
+import ctypes, math, os, random, sys
+sys.path.insert(0, %r)
+import numpy as np, tsfm_attn as ta
+lib = ta.load(os.environ["TSFM_FUZZ_LIB"]) if os.environ.get("TSFM_FUZZ_LIB") else ta.load()
+assert not lib.tsfm_attn_available()
+rng = random.Random(20261202)
+buf = np.zeros(1 << 16, np.float32)
+kvb = np.ones(4096, np.uint8)
+ints = [-(1 << 31), -5, -1, 0, 1, 2, 17, 64, 129, 577, 2048, (1 << 31) - 1]
+strides = [-(1 << 63), -(1 << 40), -1, 0, 1, 64, 130, 768, 3072, 1 << 26, 1 << 40, (1 << 62)]
+floats = [0.0, 0.125, 1.0, -0.5, math.inf, -math.inf, math.nan]
+ptrs = [None, buf.ctypes.data]
+codes = set()
+def valid():
+    row = 2 * 64
+    return ta.make_args(q=buf, k=buf, v=buf, o=buf, mask=0, batch=2, heads=2, n_q=17, n_k=17, q_tok=row,
+                        q_batch=17 * row, k_tok=row, k_batch=17 * row, v_tok=row, v_batch=17 * row, o_tok=row,
+                        o_batch=17 * row, scale=0.125)
+for it in range(2000):  # a valid block with one to three fields changed
+    a = valid()
+    for _ in range(rng.randint(1, 3)):
+        f = rng.choice([n for n, _ in ta.AttnArgs._fields_ if n != "stream"])
+        t = dict(ta.AttnArgs._fields_)[f]
+        if t is ctypes.c_void_p:
+            setattr(a, f, rng.choice(ptrs + [kvb.ctypes.data]))
+        elif t is ctypes.c_float:
+            setattr(a, f, rng.choice(floats))
+        elif t is ctypes.c_int64:
+            setattr(a, f, rng.choice(strides))
+        elif t is ctypes.c_uint32:
+            setattr(a, f, rng.choice([0, 2, 0xFFFFFFFE]))
+        else:
+            setattr(a, f, rng.choice(ints + [-1, 3, 5, 7, 99]))
+    rc = lib.tsfm_attn_fwd(ctypes.byref(a))
+    assert rc in (0, 1, 2, 3), (it, rc)
+    codes.add(rc)
+for it in range(2000):  # every field random
+    a = ta.AttnArgs()
+    a.dtype = rng.choice([-1, 0, 1, 2, 3, 99])
+    a.mask = rng.choice(range(-1, 8))
+    for f in ("batch", "heads", "n_q", "n_k", "q_pos0", "ctx_keys", "chain_start", "rel_buckets", "rope_half",
+              "rope_rows_per_table", "rope_row0"):
+        setattr(a, f, rng.choice(ints))
+    a.head_dim = rng.choice([0, 16, 32, 64, 128, -64])
+    a.scale = rng.choice(floats)
+    a.flags = rng.choice([0, 2, 0xFFFFFFFE])
+    for f in ("q_tok", "q_batch", "k_tok", "k_batch", "v_tok", "v_batch", "o_tok", "o_batch", "kv_batch",
+              "bias_head", "bias_row", "rope_table_stride"):
+        setattr(a, f, rng.choice(strides))
+    for f in ("q", "k", "v", "o", "bias", "rel_table", "rel_bucket", "rope_cos", "rope_sin"):
+        setattr(a, f, rng.choice(ptrs))
+    a.key_valid = rng.choice([None, kvb.ctypes.data])
+    rc = lib.tsfm_attn_fwd(ctypes.byref(a))
+    assert rc in (0, 1, 2, 3), (it, rc)
+    codes.add(rc)
+def fill(a):
+    for f, t in type(a)._fields_:
+        if f == "stream" or not hasattr(t, "__mro__") or issubclass(t, ctypes.Array):
+            continue
+        if t is ctypes.c_void_p:
+            setattr(a, f, rng.choice(ptrs))
+        elif t is ctypes.c_float:
+            setattr(a, f, rng.choice(floats))
+        elif t is ctypes.c_int64:
+            setattr(a, f, rng.choice(strides + [64, 128, 768, 3 * 768]))
+        elif t is ctypes.c_uint32:
+            setattr(a, f, rng.choice([0, 2, 0xFFFFFFFE]))
+        elif t in (ctypes.c_int32, ctypes.c_int):
+            setattr(a, f, rng.choice(ints + [0, 1, 2, 3, 4, 16, 64, 64, 64]))
+for cls, fn in ((ta.VariateArgs, lib.tsfm_variate_attend), (ta.ProjArgs, lib.tsfm_qkv_project)):
+    fn.argtypes = [ctypes.POINTER(cls)]
+    fn.restype = ctypes.c_int
+    for it in range(3000):
+        a = cls()
+        fill(a)
+        rc = fn(ctypes.byref(a))
+        assert rc in (0, 1, 2, 3), (cls.__name__, it, rc)
+        codes.add(rc)
+print(sorted(codes))
+'''
+
+
+def test_validation_fuzz_returns_codes_and_never_launches():
+    """4000 random argument blocks (extreme dims and strides, null and short buffers, bad dtypes,
+    masks, flags and scales) through tsfm_attn_fwd, and 3000 each through tsfm_variate_attend and
+    tsfm_qkv_project, in a fresh process with TSFM_HIP_DISABLE=1:
+    every call returns one of the ABI's codes, and whatever passes validation stops at the
+    disabled device instead of launching. Under the sanitizer run this is the check that the
+    validation arithmetic has no overflow or out-of-bounds read."""
+    env = dict(os.environ, TSFM_HIP_DISABLE="1")
+    if os.environ.get("TSFM_TEST_PRODUCT_LIB"):
+        env["TSFM_FUZZ_LIB"] = os.environ["TSFM_TEST_PRODUCT_LIB"]
+    r = subprocess.run([sys.executable, "-c", _FUZZ % str(ROOT / "tsfm-zig_amd")], env=env, capture_output=True,
+                       text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    seen = eval(r.stdout.strip().splitlines()[-1])
+    assert {1, 2, 3} <= set(seen), seen  # unavailable (passed validation), unsupported, invalid all reached

@@ -209,6 +209,53 @@ def test_sgemm_nt_matches_oracle_gemm_nt(ta, orc, gpu_ready, m, n, k, pad):
     assert np.abs(got - exact).max() <= 8 * np.abs(ref - exact).max() + 1e-7
 
 
+@pytest.mark.parametrize("m,n,k,pad", [(1, 4, 16, 0), (33, 64, 64, 4), (129, 100, 512, 8), (577, 768, 768, 0),
+                                       (200, 2304, 96, 12)])
+def test_sgemm_nn_matches_oracle_gemm_nn(ta, orc, gpu_ready, m, n, k, pad):
+    """cuda_sgemm_nn's contract (src/platform/cuda/gemm.c:324-330): C = A B with B row-major [k][ldb]
+    (ldb any >= n, here also odd); only the n columns of each C row are written. Against the
+    oracle's gemmNN and float64, the same bars as the transposed product."""
+    rng = np.random.default_rng(7 * m + n + k)
+    lda, ldb, ldc = k + pad, n + pad + 1, n + pad
+    a = rng.standard_normal(m * lda).astype(np.float32)
+    b = rng.standard_normal(k * ldb).astype(np.float32)
+    c = np.full(m * ldc, -9.0, np.float32)
+    assert ta.sgemm_nn(m, n, k, a, lda, b, ldb, c, ldc) == ta.OK, ta.last_error()
+    want = np.zeros(m * ldc, np.float32)
+    orc.gemm_nn(want, ldc, a, lda, b, ldb, m, n, k)
+    got, ref = c.reshape(m, ldc)[:, :n], want.reshape(m, ldc)[:, :n]
+    assert np.all(c.reshape(m, ldc)[:, n:] == -9.0)
+    A = a.reshape(m, lda)[:, :k].astype(np.float64)
+    B = b.reshape(k, ldb)[:, :n].astype(np.float64)
+    exact = A @ B
+    bound = k * 2.0 ** -24 * (np.abs(A) @ np.abs(B)) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.all(np.abs(ref - exact) <= bound)
+    assert np.abs(got - exact).max() <= 8 * np.abs(ref - exact).max() + 1e-7
+
+
+def test_sgemm_nn_registered_weight_gives_the_uploaded_bits(ta, gpu_ready):
+    """B registered once (Weight.handle) gives the same bits as B uploaded with the call, and a
+    permutation matrix as B picks columns of A exactly (a transposed B would apply the inverse)."""
+    rng = np.random.default_rng(11)
+    m, n, k = 70, 48, 48
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    perm = rng.permutation(n)
+    b = np.zeros((k, n), np.float32)
+    b[perm, np.arange(n)] = 1.0  # column j of A B is column perm[j] of A
+    h = ta.weight_register(b)
+    assert h is not None, ta.last_error()
+    try:
+        c1 = np.zeros((m, n), np.float32)
+        c2 = np.zeros((m, n), np.float32)
+        assert ta.sgemm_nn(m, n, k, a, k, b, n, c1, n, b_buf=h) == ta.OK, ta.last_error()
+        assert ta.sgemm_nn(m, n, k, a, k, b, n, c2, n) == ta.OK, ta.last_error()
+    finally:
+        ta.weight_release(h)
+    assert np.array_equal(c1, c2)
+    assert np.array_equal(c1, a[:, perm])
+
+
 def test_registered_weight_linear_matches_oracle(ta, orc, gpu_ready):
     """nn.linear with a registered weight (Weight.handle, src/core/nn.zig:276-283): the same result
     as with the weight uploaded per call, and as the oracle's linear."""

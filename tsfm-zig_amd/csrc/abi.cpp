@@ -207,6 +207,21 @@ hipError_t copy_rows_d2h(void* dst, const void* src, int64_t B, int64_t rows, in
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// Largest element span a strided view may have: 2^46 elements (256 TiB of f32) is past any device or
+// host buffer, and keeps every offset sum below it free of int64 overflow.
+constexpr int64_t kMaxSpan = (int64_t)1 << 46;
+
+// Elements spanned by a (B, n, row) view with non-negative strides, or -1 when that passes
+// kMaxSpan (checked step by step, so no intermediate product overflows).
+int64_t span_checked(int64_t B, int64_t n, int64_t tok, int64_t batch, int64_t row) {
+    if (B <= 0 || n <= 0) return 0;
+    int64_t t1 = 0, t2 = 0, s = 0;
+    if (__builtin_mul_overflow(B - 1, batch, &t1) || __builtin_mul_overflow(n - 1, tok, &t2) ||
+        __builtin_add_overflow(t1, t2, &s) || __builtin_add_overflow(s, row, &s) || s > kMaxSpan)
+        return -1;
+    return s;
+}
+
 int validate(const tsfm_attn_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (a->dtype < TSFM_DTYPE_F32 || a->dtype > TSFM_DTYPE_F16) return fail(TSFM_E_INVALID, "bad dtype %d", a->dtype);
@@ -229,8 +244,13 @@ int validate(const tsfm_attn_args* a) {
     if (a->dtype != TSFM_DTYPE_F32 && !(a->scale >= 0.f))
         return fail(TSFM_E_UNSUPPORTED, "half-precision attention needs a non-negative scale");
     const int64_t esz = a->dtype == TSFM_DTYPE_F32 ? 4 : 2;
-    if (((int64_t)a->n_k + 64) * std::max(a->k_tok, a->v_tok) * esz + 256 > 0xffffffffLL)
+    if (std::max(a->k_tok, a->v_tok) > (0xffffffffLL - 256) / esz / ((int64_t)a->n_k + 64))
         return fail(TSFM_E_UNSUPPORTED, "the K/V rows of one series must span less than 4 GiB");
+    if (span_checked(a->batch, a->n_q, a->q_tok, a->q_batch, row) < 0 ||
+        span_checked(a->batch, a->n_k, a->k_tok, a->k_batch, row) < 0 ||
+        span_checked(a->batch, a->n_k, a->v_tok, a->v_batch, row) < 0 ||
+        span_checked(a->batch, a->n_q, a->o_tok, a->o_batch, row) < 0)
+        return fail(TSFM_E_UNSUPPORTED, "a q/k/v/o view spans more than 2^46 elements");
     const bool reads_valid = a->mask == TSFM_MASK_KEYS_ADDITIVE || a->mask == TSFM_MASK_CAUSAL_KEYS ||
                              a->mask == TSFM_MASK_FULL_KEYS || a->mask == TSFM_MASK_DECODER;
     if (reads_valid && a->key_valid == nullptr) return fail(TSFM_E_INVALID, "mask %d needs key_valid", a->mask);
@@ -240,6 +260,9 @@ int validate(const tsfm_attn_args* a) {
         return fail(TSFM_E_INVALID, "negative decoder bounds");
     if (a->bias != nullptr && a->rel_table != nullptr) return fail(TSFM_E_INVALID, "both dense and T5 bias given");
     if (a->bias != nullptr && (a->bias_head < 0 || a->bias_row < 0)) return fail(TSFM_E_INVALID, "negative bias stride");
+    if (a->bias != nullptr && span_checked(a->heads, a->n_q, a->bias_row, a->bias_head, a->n_k) < 0)
+        return fail(TSFM_E_UNSUPPORTED, "the bias view spans more than 2^46 elements");
+    if (a->kv_batch > kMaxSpan) return fail(TSFM_E_UNSUPPORTED, "kv_batch past 2^46");
     if (a->rel_table != nullptr) {
         if (a->rel_bucket == nullptr || a->rel_buckets <= 0) return fail(TSFM_E_INVALID, "T5 bias needs rel_bucket");
         if (a->q_pos0 != 0) return fail(TSFM_E_UNSUPPORTED, "T5 bias needs q_pos0 == 0");
@@ -423,6 +446,14 @@ int tsfm_variate_attend(const tsfm_variate_args* a) {
         return fail(TSFM_E_INVALID, "kv_row %lld shorter than n_enc %d", (long long)a->kv_row, a->n_enc);
     if (a->qkv_row % 4 || a->qkv_tok % 4 || a->o_row % 4 || a->o_tok % 4 || a->gate_row % 4 || a->gate_tok % 4)
         return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    {
+        const int64_t rows = (int64_t)a->groups * a->vall, D = (int64_t)a->heads * a->head_dim;
+        if (span_checked(rows, a->n_tok, a->qkv_tok, a->qkv_row, 3 * D) < 0 ||
+            span_checked(rows, a->n_tok, a->o_tok, a->o_row, D) < 0 ||
+            (a->gate != nullptr && span_checked(rows, a->n_tok, a->gate_tok, a->gate_row, D) < 0) ||
+            (a->key_valid != nullptr && span_checked(rows, 1, 0, a->kv_row, a->n_enc) < 0))
+            return fail(TSFM_E_UNSUPPORTED, "a view spans more than 2^46 elements");
+    }
     if (a->groups == 0 || a->vall == 0 || a->n_tok == 0 || a->heads == 0) return TSFM_OK;  // nothing to compute
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
@@ -513,6 +544,12 @@ int proj_request(const tsfm_proj_args* a, tsfm::ProjParams* pp) {
     if (tokens == 0 || width == 0) return kNothing;
     if (a->d_in == 0 || a->d_in % 16) return fail(TSFM_E_UNSUPPORTED, "d_in %d (supported: multiples of 16)", a->d_in);
     if (tokens > 0x7fffffff || 4 * width > 0x7fffffff) return fail(TSFM_E_UNSUPPORTED, "too many tokens or heads");
+    if (span_checked(1, tokens, a->x_tok, 0, a->d_in) < 0 || span_checked(1, tokens, a->q_tok, 0, width) < 0 ||
+        span_checked(1, tokens, a->k_tok, 0, width) < 0 || span_checked(1, tokens, a->v_tok, 0, width) < 0 ||
+        (gated && span_checked(1, tokens, a->gate_tok, 0, width) < 0) ||
+        (rope && span_checked(1, (int64_t)a->rope_row0 + a->batch, a->rope_table_stride, 0,
+                              (int64_t)a->seq * a->rope_half) < 0))
+        return fail(TSFM_E_UNSUPPORTED, "a view spans more than 2^46 elements");
     if (a->x_tok % 4 || a->q_tok % 4 || a->k_tok % 4 || a->v_tok % 4 || (gated && a->gate_tok % 4) ||
         (rope && a->rope_table_stride % 4))
         return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
@@ -1532,8 +1569,48 @@ int tsfm_sgemm_nt(int m, int n, int k, float alpha, const float* A, int lda, con
 
 int tsfm_sgemm_nn(int m, int n, int k, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
                   void* b_buf) {
-    (void)m; (void)n; (void)k; (void)A; (void)lda; (void)B; (void)ldb; (void)C; (void)ldc; (void)b_buf;
-    return fail(TSFM_E_UNSUPPORTED, "A x B is not run here: the attention's products run inside tsfm_attn_fwd");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(TSFM_E_INVALID, "empty or negative product %d x %d x %d", m, n, k);
+    if (A == nullptr || C == nullptr || (B == nullptr && b_buf == nullptr)) return fail(TSFM_E_INVALID, "NULL operand");
+    if (lda < k || ldb < n || ldc < n) return fail(TSFM_E_INVALID, "leading dimension shorter than the row");
+    if (k % 16 || n % 4 || lda % 4 || ldc % 4)
+        return fail(TSFM_E_UNSUPPORTED, "k must be a multiple of 16, n, lda and ldc of 4");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    // B [k][ldb] is transposed on the device to B^T [n][k], and the product runs as A (B^T)^T on the
+    // projection kernel, like tsfm_sgemm_nt.
+    const size_t a_n = ((size_t)(m - 1) * lda + k) * 4, b_n = b_buf ? 0 : ((size_t)(k - 1) * ldb + n) * 4;
+    const size_t bt_n = (size_t)n * k * 4, c_n = ((size_t)(m - 1) * ldc + n) * 4;
+    Plan plan;
+    const size_t a_at = plan.take(a_n), b_at = plan.take(b_n), bt_at = plan.take(bt_n), c_at = plan.take(c_n);
+    const size_t part_at = plan.take(tsfm::kSplitWorkspaceBytes);
+    rc = ensure_buf(ctx, plan.off);
+    if (rc != TSFM_OK) return rc;
+    char* base = static_cast<char*>(ctx->buf);
+    hipStream_t s = ctx->stream;
+    tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
+    hipError_t e;
+    if ((e = hipMemcpyAsync(base + a_at, A, a_n, hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "host-to-device copy");
+    if (b_n && (e = hipMemcpyAsync(base + b_at, B, b_n, hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "host-to-device copy");
+    const float* bd = b_buf ? static_cast<const float*>(b_buf) : reinterpret_cast<const float*>(base + b_at);
+    float* bt = reinterpret_cast<float*>(base + bt_at);
+    tsfm::ProjParams p{};
+    p.x = reinterpret_cast<const float*>(base + a_at); p.x_tok = lda;
+    p.w0 = bt; p.w_ld = k; p.alpha = 1.f; p.epi = tsfm::kEpiNone;
+    p.y0 = base + c_at; p.y0_tok = ldc;
+    p.tokens = m; p.seq = m; p.d_in = k; p.width = n; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
+    if ((e = tsfm::launch_transpose_f32(bd, ldb, bt, k, k, n, s)) != hipSuccess ||
+        (e = tsfm::launch_proj(p, s)) != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "GEMM launch");
+    }
+    if ((e = copy_rows_d2h(C, base + c_at, 1, m, 0, (int64_t)ldc * 4, (int64_t)n * 4, s)) != hipSuccess)
+        return hip_fail(e, "device-to-host copy");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream synchronise");
+    return TSFM_OK;
 }
 
 // ---- KV cache ------------------------------------------------------------------------------------
@@ -1604,8 +1681,12 @@ int tsfm_kv_append(tsfm_kv_cache* c, const void* k, int64_t k_tok, int64_t k_bat
     if (c == nullptr || k == nullptr || v == nullptr) return fail(TSFM_E_INVALID, "NULL argument");
     if (n_new < 0 || k_tok < 0 || k_batch < 0 || v_tok < 0 || v_batch < 0) return fail(TSFM_E_INVALID, "negative size");
     if (n_new == 0) return TSFM_OK;
-    if (c->len + n_new > c->cap) return fail(TSFM_E_INVALID, "append of %d exceeds capacity %d (len %d)", n_new, c->cap, c->len);
+    if ((int64_t)c->len + n_new > c->cap)
+        return fail(TSFM_E_INVALID, "append of %d exceeds capacity %d (len %d)", n_new, c->cap, c->len);
     if (k_tok % 8 || k_batch % 8 || v_tok % 8 || v_batch % 8) return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    if (span_checked(c->B, n_new, k_tok, k_batch, (int64_t)c->H * c->D) < 0 ||
+        span_checked(c->B, n_new, v_tok, v_batch, (int64_t)c->H * c->D) < 0)
+        return fail(TSFM_E_UNSUPPORTED, "a k/v view spans more than 2^46 elements");
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
     ThreadCtx* ctx = thread_ctx();
@@ -1644,10 +1725,13 @@ int tsfm_kv_attend(tsfm_kv_cache* c, const void* q, int64_t q_tok, int64_t q_bat
     if (n_q < 0 || q_pos0 < 0 || q_tok < 0 || q_batch < 0 || o_tok < 0 || o_batch < 0)
         return fail(TSFM_E_INVALID, "negative size");
     if (n_q == 0) return TSFM_OK;
-    if (q_pos0 + n_q > c->len) return fail(TSFM_E_INVALID, "queries [%d, %d) beyond cache length %d", q_pos0, q_pos0 + n_q, c->len);
+    if ((int64_t)q_pos0 + n_q > c->len)
+        return fail(TSFM_E_INVALID, "queries [%d, %lld) beyond cache length %d", q_pos0, (long long)q_pos0 + n_q, c->len);
     if (q_tok % 8 || q_batch % 8 || o_tok % 8 || o_batch % 8) return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
     const int64_t row = (int64_t)c->H * c->D;
     if (o_tok < row && n_q > 1) return fail(TSFM_E_INVALID, "o token stride smaller than heads * head_dim");
+    if (span_checked(c->B, n_q, q_tok, q_batch, row) < 0 || span_checked(c->B, n_q, o_tok, o_batch, row) < 0)
+        return fail(TSFM_E_UNSUPPORTED, "a q/o view spans more than 2^46 elements");
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
     ThreadCtx* ctx = thread_ctx();

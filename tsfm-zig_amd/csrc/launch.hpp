@@ -76,6 +76,9 @@ struct ProjParams {
     float norm_eps;
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
+// dst[c][r] = src[r][c] for a rows x cols f32 matrix (row strides in elements).
+hipError_t launch_transpose_f32(const float* src, int64_t ld_src, float* dst, int64_t ld_dst, int rows, int cols,
+                                hipStream_t stream);
 // Bytes of split partials launch_proj will need for this product (0: it runs unsplit); sets the
 // tiling fields of p as launch_proj does.
 size_t proj_split_bytes(ProjParams& p);

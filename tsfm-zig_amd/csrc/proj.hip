@@ -406,4 +406,34 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     return launch_unsplit<0>(p, blocks, stream);
 }
 
+namespace {
+// dst[c][r] = src[r][c] for r < rows, c < cols: 32 x 32 tiles through LDS (one padding column, so
+// the column reads of the tile hit 32 different banks); loads and stores are row-contiguous.
+__global__ __launch_bounds__(256) void transpose_f32(const float* __restrict__ src, int64_t ld_src,
+                                                     float* __restrict__ dst, int64_t ld_dst, int rows, int cols) {
+    __shared__ float t[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 8 rows of 32 per pass
+#pragma unroll
+    for (int i = 0; i < 32; i += 8) {
+        const int r = r0 + ty + i, c = c0 + tx;
+        if (r < rows && c < cols) t[ty + i][tx] = src[(int64_t)r * ld_src + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 32; i += 8) {
+        const int c = c0 + ty + i, r = r0 + tx;
+        if (c < cols && r < rows) dst[(int64_t)c * ld_dst + r] = t[tx][ty + i];
+    }
+}
+}  // namespace
+
+hipError_t launch_transpose_f32(const float* src, int64_t ld_src, float* dst, int64_t ld_dst, int rows, int cols,
+                                hipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
+    hipLaunchKernelGGL(transpose_f32, grid, dim3(256), 0, stream, src, ld_src, dst, ld_dst, rows, cols);
+    return hipGetLastError();
+}
+
 }  // namespace tsfm

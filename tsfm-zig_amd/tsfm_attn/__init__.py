@@ -1040,6 +1040,13 @@ def sgemm_nt(m: int, n: int, k: int, alpha: float, a, lda: int, b, ldb: int, c, 
     return int(load().tsfm_sgemm_nt(m, n, k, alpha, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc, b_buf))
 
 
+def sgemm_nn(m: int, n: int, k: int, a, lda: int, b, ldb: int, c, ldc: int, b_buf=None) -> int:
+    """``tsfm_sgemm_nn`` (Backend.sgemm_nn): c[m, n] = a[m, k] b[k, n] with leading dimensions, host
+    arrays; ``b_buf`` a handle from :func:`weight_register` holding b as [k][ldb] (then ``b`` is
+    unused)."""
+    return int(load().tsfm_sgemm_nn(m, n, k, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc, b_buf))
+
+
 def linear(y, x, rows: int, w, out: int, inp: int, w_buf=None) -> int:
     """nn.linear without bias through the backend seam (src/core/nn.zig:270-293): y (rows, out) =
     x (rows, inp) w (out, inp)^T."""
