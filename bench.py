@@ -248,17 +248,18 @@ def run_decode(torch, ta, workloads, peak):
     cache = ta.KvCache(ta.DTYPE_BF16, w.B, w.H, T)
     cache.append(dev["k"], dev["v"], P, row, T * row, row, T * row)
     stream = torch.cuda.current_stream()
-    events = []  # (start, end) around every attend launch of the timed steps
+    events = []  # (start, end) around every decode-block launch of the timed steps
 
     def step(record=True):
         cache.truncate(P)
         for i in range(nb):
             p0 = P + i * blk
-            cache.append(dev["k"][:, p0:], dev["v"][:, p0:], blk, row, T * row, row, T * row)
             if record:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record(stream)
-            cache.attend(dev["q"][:, p0:], out[:, i * blk:], blk, p0, w.scale, row, T * row, row, nb * blk * row)
+            # One launch per block: the block's K/V into the cache, then its 32 queries over it.
+            cache.append_attend(dev["k"][:, p0:], dev["v"][:, p0:], dev["q"][:, p0:], out[:, i * blk:], blk, w.scale,
+                                row, T * row, row, T * row, row, T * row, row, nb * blk * row)
             if record:
                 e1.record(stream)
                 events.append((e0, e1))
@@ -283,9 +284,11 @@ def run_decode(torch, ta, workloads, peak):
             want[:, i * blk:(i + 1) * blk] = full[:, n - blk:n]
         return time.perf_counter() - t0, want, orc.lanes
 
-    # Work of the dominant kernel (kv_attend), per launch, averaged over the 8 blocks: cache K/V
-    # read + q read + o written, in bytes.
-    bytes_per_attend = w.B * w.H * sum((P + i * blk + blk) * 64 * 2 * 2 + 2 * blk * 64 * 2 for i in range(nb)) / nb
+    # Work of the decode-block kernel (kv_attend<bf16, append>), per launch, averaged over the 8
+    # blocks: the block's K/V read and written into the cache, the cache's K/V read (keys up to the
+    # block's last), q read, o written, in bytes.
+    bytes_per_attend = w.B * w.H * sum((P + i * blk + blk) * 64 * 2 * 2 + 2 * blk * 64 * 2 + 2 * blk * 64 * 2 * 2
+                                       for i in range(nb)) / nb
     config = {"workload": w.name, "B": w.B, "H": w.H, "D": 64, "prefix": P, "blocks": nb, "block": blk,
               "mask": "causal", "scale": w.scale, "layout": "(B, T, H*D) bf16; cache K [B][H][cap][64], V chunked"}
     b = Bench(w, lambda: step(True), lambda: out.float().cpu().numpy(), cpu_leg, config, "bf16", "hbm",

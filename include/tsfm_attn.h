@@ -547,6 +547,15 @@ int tsfm_kv_attend(tsfm_kv_cache *cache, const void *q, int64_t q_tok, int64_t q
                    int64_t o_tok, int64_t o_batch, int32_t n_q, int32_t q_pos0, float scale, uint32_t flags,
                    void *stream);
 
+/* One decode block: tsfm_kv_append of the n_new tokens' k/v, then tsfm_kv_attend of their n_new
+ * queries at positions len.. (len = tsfm_kv_len before the call), with the same results. With
+ * device pointers, n_new == 32 and len a multiple of 32 (Timestral's decode blocks) it is one
+ * launch, in which each (series, head) writes its new K/V into the cache and attends; otherwise the
+ * two calls run in turn. */
+int tsfm_kv_append_attend(tsfm_kv_cache *cache, const void *k, int64_t k_tok, int64_t k_batch, const void *v,
+                          int64_t v_tok, int64_t v_batch, const void *q, int64_t q_tok, int64_t q_batch, void *o,
+                          int64_t o_tok, int64_t o_batch, int32_t n_new, float scale, uint32_t flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

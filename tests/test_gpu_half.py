@@ -233,6 +233,53 @@ def test_kv_decode_full_shape_bf16(ta, orc, gpu_ready):
     assert _ref.scaled_err(got, want[:, 256:]) <= TOL_HALF
 
 
+@pytest.mark.parametrize("name", DTYPES)
+@pytest.mark.parametrize("prefix,blk,nb", [(256, 32, 4), (70, 32, 3), (64, 17, 4), (40, 48, 2)])
+def test_kv_append_attend_equals_the_two_calls(ta, orc, gpu_ready, name, prefix, blk, nb):
+    """One decode block per call (tsfm_kv_append_attend) gives the bits of tsfm_kv_append then
+    tsfm_kv_attend: one launch for blocks of up to 32 tokens (prefixes that leave the new tokens in
+    a partly filled 32-key chunk and 64-key tile), the two calls for 48; and the causal rows of the
+    oracle. Host pointers run through the same entry point too."""
+    from tsfm_attn import workloads
+
+    torch = _torch()
+    w = workloads.timestral_decode(B=3, H=2, prefix=prefix, blocks=nb, block=blk, dtype=name)
+    a = w.arrays
+    row, T = w.H * 64, prefix + nb * blk
+    qd, qr = _dev(a["q"][:, :T], name)
+    kd, kr = _dev(a["k"][:, :T], name)
+    vd, vr = _dev(a["v"][:, :T], name)
+    dt = ta.DTYPE_BF16 if name == "bf16" else ta.DTYPE_F16
+    outs = []
+    for fused in (False, True):
+        out = torch.zeros((w.B, nb * blk, row), dtype=_tdtype(name), device="cuda")
+        with ta.KvCache(dt, w.B, w.H, T) as cache:
+            cache.append(kd, vd, prefix, row, T * row, row, T * row)
+            for i in range(nb):
+                p0 = prefix + i * blk
+                if fused:
+                    cache.append_attend(kd[:, p0:], vd[:, p0:], qd[:, p0:], out[:, i * blk:], blk, w.scale, row,
+                                        T * row, row, T * row, row, T * row, row, nb * blk * row)
+                else:
+                    cache.append(kd[:, p0:], vd[:, p0:], blk, row, T * row, row, T * row)
+                    cache.attend(qd[:, p0:], out[:, i * blk:], blk, p0, w.scale, row, T * row, row, nb * blk * row)
+                assert len(cache) == p0 + blk
+            torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1])
+    want = _oracle(orc, 2, qr, kr, vr, None, w.B, w.H, T, w.scale)
+    assert _ref.scaled_err(outs[1].float().numpy(), want[:, prefix:]) <= TOL_HALF
+    # host pointers: the same entry point stages and synchronises
+    kh, vh, qh = (x.view(torch.int16).cpu().numpy() for x in (kd, vd, qd))  # the raw halves
+    oh = np.zeros((w.B, blk, row), np.int16)
+    with ta.KvCache(dt, w.B, w.H, T) as cache:
+        cache.append(kh, vh, prefix, row, T * row, row, T * row)
+        at = prefix * row * 2  # byte offset of token `prefix` in each (B, T, row) array
+        cache.append_attend(kh.ctypes.data + at, vh.ctypes.data + at, qh.ctypes.data + at, oh, blk, w.scale, row,
+                            T * row, row, T * row, row, T * row, row, blk * row)
+    assert np.array_equal(oh, outs[0][:, :blk].view(torch.int16).numpy())
+
+
 def test_kv_truncate_replays_identically(ta, gpu_ready):
     from tsfm_attn import workloads
 

@@ -1766,4 +1766,45 @@ int tsfm_kv_attend(tsfm_kv_cache* c, const void* q, int64_t q_tok, int64_t q_bat
     return TSFM_OK;
 }
 
+int tsfm_kv_append_attend(tsfm_kv_cache* c, const void* k, int64_t k_tok, int64_t k_batch, const void* v,
+                          int64_t v_tok, int64_t v_batch, const void* q, int64_t q_tok, int64_t q_batch, void* o,
+                          int64_t o_tok, int64_t o_batch, int32_t n_new, float scale, uint32_t flags, void* stream) {
+    if (c == nullptr || k == nullptr || v == nullptr || q == nullptr || o == nullptr)
+        return fail(TSFM_E_INVALID, "NULL argument");
+    if (n_new < 0) return fail(TSFM_E_INVALID, "negative size");
+    if (n_new == 0) return TSFM_OK;
+    const int32_t pos0 = c->len;
+    if (!(flags & TSFM_ATTN_DEVICE_PTRS) || n_new != tsfm::kKvFusedBlock || pos0 % 32 != 0) {
+        // Host pointers (staged by each call), or a block other than 32 tokens on a 32-key boundary:
+        // the two calls.
+        int rc = tsfm_kv_append(c, k, k_tok, k_batch, v, v_tok, v_batch, n_new, flags, stream);
+        if (rc != TSFM_OK) return rc;
+        return tsfm_kv_attend(c, q, q_tok, q_batch, o, o_tok, o_batch, n_new, pos0, scale, flags, stream);
+    }
+    // The checks of both calls, then one launch.
+    if (k_tok < 0 || k_batch < 0 || v_tok < 0 || v_batch < 0 || q_tok < 0 || q_batch < 0 || o_tok < 0 || o_batch < 0)
+        return fail(TSFM_E_INVALID, "negative stride");
+    if ((int64_t)pos0 + n_new > c->cap)
+        return fail(TSFM_E_INVALID, "append of %d exceeds capacity %d (len %d)", n_new, c->cap, c->len);
+    if (k_tok % 8 || k_batch % 8 || v_tok % 8 || v_batch % 8 || q_tok % 8 || q_batch % 8 || o_tok % 8 || o_batch % 8)
+        return fail(TSFM_E_UNSUPPORTED, "strides must be multiples of 16 bytes");
+    const int64_t row = (int64_t)c->H * c->D;
+    if (o_tok < row && n_new > 1) return fail(TSFM_E_INVALID, "o token stride smaller than heads * head_dim");
+    if (span_checked(c->B, n_new, k_tok, k_batch, row) < 0 || span_checked(c->B, n_new, v_tok, v_batch, row) < 0 ||
+        span_checked(c->B, n_new, q_tok, q_batch, row) < 0 || span_checked(c->B, n_new, o_tok, o_batch, row) < 0)
+        return fail(TSFM_E_UNSUPPORTED, "a view spans more than 2^46 elements");
+    if (!aligned(k, 16) || !aligned(v, 16) || !aligned(q, 16) || !aligned(o, 16))
+        return fail(TSFM_E_UNSUPPORTED, "device k/v/q/o must be 16-byte aligned");
+    if (!(scale >= 0.f)) return fail(TSFM_E_UNSUPPORTED, "half-precision attention needs a non-negative scale");
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    tsfm::KvLayout L{c->k, c->v, c->B, c->H, c->cap};
+    const tsfm::KvNew nw{k, k_tok, k_batch, v, v_tok, v_batch};
+    const hipError_t e = tsfm::launch_kv_append_attend(L, c->dtype == TSFM_DTYPE_BF16, nw, q, q_tok, q_batch, o, o_tok,
+                                                       o_batch, n_new, pos0, scale, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "KV append-attend launch");
+    c->len += n_new;
+    return TSFM_OK;
+}
+
 }  // extern "C"

@@ -42,6 +42,24 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 __device__ __forceinline__ u32x4 ldu4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // ---- append ----
+// The 16-byte V slot that starts at key key0 (slot j holds key key0 + j for j < 4, key0 + 16 + (j - 4)
+// for j >= 4) of one dim, after writing the new tokens [pos0, pos0 + n_new) into it; src points at
+// that dim of new token 0. A slot the new tokens cover only in part is read first and its other
+// keys kept.
+__device__ __forceinline__ u32x4 v_slot(const u32x4* slot, const uint16_t* __restrict__ src, int64_t v_tok, int key0,
+                                        int pos0, int n_new) {
+    const bool whole = key0 >= pos0 && key0 + 19 < pos0 + n_new;  // uniform over the 64 dims
+    u32x4 w = whole ? u32x4{0, 0, 0, 0} : *slot;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int t = key0 + (j < 4 ? j : 12 + j) - pos0;
+        if (t < 0 || t >= n_new) continue;
+        const uint32_t x = src[t * v_tok];
+        w[j >> 1] = (j & 1) ? (w[j >> 1] & 0xffffu) | (x << 16) : (w[j >> 1] & 0xffff0000u) | x;
+    }
+    return w;
+}
+
 // K: one thread per (series, head, new token, 8-dim chunk): 16-byte load, 16-byte store.
 // V: one thread per (series, head, touched 32-key chunk, octet, dim) builds the whole 16-byte slot
 //    (8 keys of one dim) in registers and stores it once; consecutive threads take consecutive dims,
@@ -76,27 +94,24 @@ __global__ __launch_bounds__(256) void kv_append(KvLayout c, const uint16_t* __r
     const int64_t bh = (int64_t)b * c.H + h;
     u32x4* slot = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(c.v) +
                                            (((bh * (c.cap / 32) + ch) * 4 + o) * kHeadDim + d) * 8);
-    const int key0 = 32 * ch + 4 * o;  // slot j holds key key0 + j (j < 4) or key0 + 16 + (j - 4)
-    const bool whole = key0 >= pos0 && key0 + 19 < pos0 + n_new;  // uniform over the 64 dims
-    u32x4 w = whole ? u32x4{0, 0, 0, 0} : *slot;
-    const uint16_t* src = v + b * v_batch + h * kHeadDim + d;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int t = key0 + (j < 4 ? j : 12 + j) - pos0;
-        if (t < 0 || t >= n_new) continue;
-        const uint32_t x = src[t * v_tok];
-        w[j >> 1] = (j & 1) ? (w[j >> 1] & 0xffffu) | (x << 16) : (w[j >> 1] & 0xffff0000u) | x;
-    }
-    *slot = w;
+    *slot = v_slot(slot, v + b * v_batch + h * kHeadDim + d, v_tok, 32 * ch + 4 * o, pos0, n_new);
 }
 
 // ---- attend ----
-template <bool BF16>
+// APPEND: the fused block decode of a 32-token block starting on a 32-key boundary (q_pos0 % 32 == 0,
+// n_q == 32). The workgroup -- the only one that reads its (series, head) -- loads the block's K
+// rows and its V chunk (built in the cache's slot order) once, writes them to the cache and to LDS,
+// and the tile holding the new keys takes them from LDS. Only an LDS barrier separates the two:
+// no wave waits for the cache writes, and each wave's first tile, if it holds old keys only, is
+// loading meanwhile.
+template <bool BF16, bool APPEND>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void kv_attend(
     KvLayout c, const uint16_t* __restrict__ q, int64_t q_tok, int64_t q_batch, uint16_t* __restrict__ o, int64_t o_tok,
-    int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k, float scale) {
+    int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k, float scale, KvNew nw) {
     __shared__ float part_m[NWAVE][QB], part_l[NWAVE][QB];
     __shared__ __attribute__((aligned(16))) float part_o[NWAVE][QB][kHeadDim + 4];
+    __shared__ __attribute__((aligned(16))) u32x4 new_k[APPEND ? QB * 8 : 1];        // [token][8 x 16 B]
+    __shared__ __attribute__((aligned(16))) u32x4 new_v[APPEND ? 4 * kHeadDim : 1];  // [octet][dim] slots
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
@@ -111,8 +126,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const int ntiles = (kend + NK - 1) / NK;
     const float c2 = scale * kLog2e;
 
-    const uint16_t* __restrict__ Kc = static_cast<const uint16_t*>(c.k) + (int64_t)bh * c.cap * kHeadDim;
-    const uint16_t* __restrict__ Vc = static_cast<const uint16_t*>(c.v) + (int64_t)bh * c.cap * kHeadDim;
+    // Not __restrict__: with APPEND the kernel writes the new rows through Kw / Vw and reads them
+    // back after the barrier.
+    uint16_t* const Kw = static_cast<uint16_t*>(c.k) + (int64_t)bh * c.cap * kHeadDim;
+    uint16_t* const Vw = static_cast<uint16_t*>(c.v) + (int64_t)bh * c.cap * kHeadDim;
+    const uint16_t* const Kc = Kw;
+    const uint16_t* const Vc = Vw;
 
     u32x4 qf[2][2];
 #pragma unroll
@@ -140,10 +159,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // capacity) are read but always masked: the cache is zero-filled at creation, so they hold
     // finite values and contribute exactly 0.
     u32x4 kf[4][2], vf[2][4];
+    // With APPEND, the 16-key blocks and the 32-key chunk of the new tokens come from LDS (the
+    // choice is uniform: the new block is one whole chunk).
     auto load_k = [&](int kbase) {
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-            const uint16_t* kr = Kc + (int64_t)(kbase + kb * 16 + ql) * kHeadDim + 8 * g;
+            const int key0 = kbase + kb * 16;
+            if (APPEND && key0 >= q_pos0 && key0 < q_pos0 + QB) {
+                const u32x4* kr = new_k + (key0 - q_pos0 + ql) * 8 + g;
+                kf[kb][0] = kr[0];
+                kf[kb][1] = kr[4];
+                continue;
+            }
+            const uint16_t* kr = Kc + (int64_t)(key0 + ql) * kHeadDim + 8 * g;
             kf[kb][0] = ldu4(kr);
             kf[kb][1] = ldu4(kr + 32);
         }
@@ -151,14 +179,50 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     auto load_v = [&](int kbase) {
 #pragma unroll
         for (int ch = 0; ch < 2; ch++) {
-            const uint16_t* vr = Vc + ((((int64_t)(kbase >> 5) + ch) * 4 + g) * kHeadDim + ql) * 8;
+            const int chunk = (kbase >> 5) + ch;
+            if (APPEND && chunk == (q_pos0 >> 5)) {
+#pragma unroll
+                for (int db = 0; db < 4; db++) vf[ch][db] = new_v[g * kHeadDim + ql + 16 * db];
+                continue;
+            }
+            const uint16_t* vr = Vc + (((int64_t)chunk * 4 + g) * kHeadDim + ql) * 8;
 #pragma unroll
             for (int db = 0; db < 4; db++) vf[ch][db] = ldu4(vr + db * 16 * 8);
         }
     };
 
     int t = wave;
-    if (t < ntiles) {
+    if (APPEND) {
+        // New K: one 16-byte piece per thread (32 tokens x 8). New V: one slot per thread (4 octets
+        // x 64 dims of the block's chunk); slot j of octet oc holds token 4 oc + j (j < 4) or
+        // 16 + 4 oc + (j - 4) of the block.
+        const uint16_t* __restrict__ kn = static_cast<const uint16_t*>(nw.k) + b * nw.k_batch + h * kHeadDim;
+        const uint16_t* __restrict__ vn = static_cast<const uint16_t*>(nw.v) + b * nw.v_batch + h * kHeadDim;
+        const int tk = tid >> 3, pc = tid & 7, oc = tid >> 6, d = tid & 63;
+        const u32x4 kin = ldu4(kn + (int64_t)tk * nw.k_tok + 8 * pc);
+        u32x4 vin;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const int t0 = 4 * oc + (w < 2 ? 2 * w : 12 + 2 * w);  // tokens of halves 2w, 2w+1
+            const uint32_t lo = vn[(int64_t)t0 * nw.v_tok + d], hi = vn[(int64_t)(t0 + 1) * nw.v_tok + d];
+            vin[w] = lo | (hi << 16);
+        }
+        const bool early = t < ntiles && t * NK + NK <= q_pos0;  // the wave's first tile holds old keys only
+        if (early) {
+            load_k(t * NK);
+            load_v(t * NK);
+        }
+        new_k[tid] = kin;
+        new_v[tid] = vin;
+        *reinterpret_cast<u32x4*>(Kw + (int64_t)(q_pos0 + tk) * kHeadDim + 8 * pc) = kin;
+        *reinterpret_cast<u32x4*>(Vw + (((int64_t)(q_pos0 >> 5) * 4 + oc) * kHeadDim + d) * 8) = vin;
+        // LDS only: the cache writes need not have landed (this workgroup reads the new rows from LDS).
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (!early && t < ntiles) {
+            load_k(t * NK);
+            load_v(t * NK);
+        }
+    } else if (t < ntiles) {
         load_k(t * NK);
         load_v(t * NK);
     }
@@ -283,14 +347,34 @@ hipError_t launch_kv_attend(const KvLayout& c, bool is_bf16, const void* q, int6
     const int64_t blocks = (int64_t)c.B * c.H * ((n_q + QB - 1) / QB);
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (!(scale >= 0.f)) return hipErrorNotSupported;  // the row max is taken before scaling
+    const KvNew none{};
     if (is_bf16)
-        hipLaunchKernelGGL(kv_attend<true>, dim3((unsigned)blocks), dim3(NT), 0, stream, c,
+        hipLaunchKernelGGL((kv_attend<true, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, c,
                            static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
-                           n_q, q_pos0, n_k, scale);
+                           n_q, q_pos0, n_k, scale, none);
     else
-        hipLaunchKernelGGL(kv_attend<false>, dim3((unsigned)blocks), dim3(NT), 0, stream, c,
+        hipLaunchKernelGGL((kv_attend<false, false>), dim3((unsigned)blocks), dim3(NT), 0, stream, c,
                            static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
-                           n_q, q_pos0, n_k, scale);
+                           n_q, q_pos0, n_k, scale, none);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append_attend(const KvLayout& c, bool is_bf16, const KvNew& nw, const void* q, int64_t q_tok,
+                                   int64_t q_batch, void* o, int64_t o_tok, int64_t o_batch, int32_t n_new,
+                                   int32_t pos0, float scale, hipStream_t stream) {
+    static_assert(kKvFusedBlock == QB, "one workgroup per (series, head)");
+    const int64_t blocks = (int64_t)c.B * c.H;
+    if (n_new != QB || pos0 < 0 || pos0 % 32 != 0 || pos0 + n_new > c.cap || blocks <= 0 || blocks > 0x7fffffff)
+        return hipErrorInvalidValue;
+    if (!(scale >= 0.f)) return hipErrorNotSupported;  // the row max is taken before scaling
+    if (is_bf16)
+        hipLaunchKernelGGL((kv_attend<true, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, c,
+                           static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
+                           n_new, pos0, pos0 + n_new, scale, nw);
+    else
+        hipLaunchKernelGGL((kv_attend<false, true>), dim3((unsigned)blocks), dim3(NT), 0, stream, c,
+                           static_cast<const uint16_t*>(q), q_tok, q_batch, static_cast<uint16_t*>(o), o_tok, o_batch,
+                           n_new, pos0, pos0 + n_new, scale, nw);
     return hipGetLastError();
 }
 

@@ -25,6 +25,19 @@ hipError_t launch_kv_append(const KvLayout& c, bool is_bf16, const void* k, int6
 hipError_t launch_kv_attend(const KvLayout& c, bool is_bf16, const void* q, int64_t q_tok, int64_t q_batch,
                             void* o, int64_t o_tok, int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k,
                             float scale, hipStream_t stream);
+// The K/V of n_new new tokens, (B, n_new, H*64) with token and batch strides in elements.
+struct KvNew {
+    const void* k; int64_t k_tok, k_batch;
+    const void* v; int64_t v_tok, v_batch;
+};
+// Block decode in one launch: the n_new tokens' K/V are written at positions pos0.. of the cache,
+// and their n_new queries (at the same positions) attend causally over keys [0, pos0 + n_new).
+// n_new == kKvFusedBlock and pos0 a multiple of 32 (one workgroup per (series, head), the new
+// tokens one 32-key chunk of the cache).
+constexpr int kKvFusedBlock = 32;
+hipError_t launch_kv_append_attend(const KvLayout& c, bool is_bf16, const KvNew& nw, const void* q, int64_t q_tok,
+                                   int64_t q_batch, void* o, int64_t o_tok, int64_t o_batch, int32_t n_new,
+                                   int32_t pos0, float scale, hipStream_t stream);
 
 // Timestral variate attention (variate.hip). f32; vall <= 16.
 constexpr int kRoleTarget = 0, kRoleKnown = 2;  // model.Role (src/timestral/model.zig:89)

@@ -71,6 +71,7 @@ EXPORTS = (
     "tsfm_weight_release",
     "tsfm_sgemm_nt",
     "tsfm_sgemm_nn",
+    "tsfm_kv_append_attend",
     "tsfm_kv_create",
     "tsfm_kv_free",
     "tsfm_kv_reset",
@@ -466,6 +467,9 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_kv_free.restype = ctypes.c_int
     lib.tsfm_kv_reset.argtypes = [vp]
     lib.tsfm_kv_reset.restype = ctypes.c_int
+    lib.tsfm_kv_append_attend.argtypes = [vp, vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, i32,
+                                          ctypes.c_float, u32, vp]
+    lib.tsfm_kv_append_attend.restype = ctypes.c_int
     lib.tsfm_kv_truncate.argtypes = [vp, i32]
     lib.tsfm_kv_truncate.restype = ctypes.c_int
     lib.tsfm_kv_len.argtypes = [vp]
@@ -1095,6 +1099,17 @@ class KvCache:
         self._check(load().tsfm_kv_attend(self._h, _ptr(q), q_tok, q_batch, _ptr(o), o_tok, o_batch, n_q, q_pos0,
                                           float(scale), DEVICE_PTRS if device else 0,
                                           _stream_of(q, stream) if device else None))
+
+    def append_attend(self, k, v, q, o, n_new: int, scale: float, k_tok: int, k_batch: int, v_tok: int, v_batch: int,
+                      q_tok: int, q_batch: int, o_tok: int, o_batch: int, stream=None) -> None:
+        """One decode block: ``append`` of the new tokens' k/v, then ``attend`` of their queries at
+        positions ``len(self)..`` (one launch for device tensors, n_new == 32 and len(self) a multiple
+        of 32)."""
+        device = _is_device(q)
+        self._check(load().tsfm_kv_append_attend(self._h, _ptr(k), k_tok, k_batch, _ptr(v), v_tok, v_batch, _ptr(q),
+                                                 q_tok, q_batch, _ptr(o), o_tok, o_batch, n_new, float(scale),
+                                                 DEVICE_PTRS if device else 0,
+                                                 _stream_of(q, stream) if device else None))
 
     def truncate(self, length: int) -> None:
         self._check(load().tsfm_kv_truncate(self._h, length))
