@@ -642,149 +642,225 @@ __host__ __device__ inline ResidentLayout resident_layout(int n_q, int n_k, bool
 }
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(6, 6))) void attn_fwd_f32_resident(Params p) {
+__global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd_f32_resident(Params p,
+                                                                                                       int n_items) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     const ResidentLayout lay = resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL);
-    float* const Ks = smem;
-    float* const Vs = smem + lay.v_off;
-    float* const kadd = smem + lay.a_off;
-    float* const lut = smem + lay.l_off + kLutPad;
-    float* const thin_qp = smem + lay.t_off;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
     const int q_tiles = (p.n_q + RQT - 1) / RQT;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = logical / q_tiles, qt = logical % q_tiles;
-    const int b = bh / p.H, h = bh % p.H;
-    const int wq0 = qt * RQT + wave * 16;  // first query of this wave
-    const int qi = wq0 + ql;
+    const int rope_tabs = p.rope_rows_per_table;
 
-    const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.q_batch + h * kHeadDim;
-    const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.k_batch + h * kHeadDim;
-    const float* __restrict__ V = static_cast<const float*>(p.v) + b * p.v_batch + h * kHeadDim;
-    float* __restrict__ O = static_cast<float*>(p.o) + b * p.o_batch + h * kHeadDim;
-    const int rope_tab = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
-    const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
-    const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
-    // Buffer descriptors ending after key n_k - 1: padding rows up to nkp read as zeros.
-    const __amdgpu_buffer_rsrc_t k_buf = make_buf(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 4));
-    const __amdgpu_buffer_rsrc_t v_buf = make_buf(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 4));
-    const __amdgpu_buffer_rsrc_t c_buf = make_buf(RC, ROPE ? (uint32_t)p.n_k * 128u : 0u);
-    const __amdgpu_buffer_rsrc_t s_buf = make_buf(RS, ROPE ? (uint32_t)p.n_k * 128u : 0u);
-    const __amdgpu_buffer_rsrc_t kv_rsrc = make_buf(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid,
-                                                    mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0);
+    // Per item (series, head, query tile): the views of its rows. The K / V descriptors end after key
+    // n_k - 1, so padding rows up to nkp read as zeros.
+    struct Item {
+        int b, h, wq0;
+        const float* Q;
+        const float* RC;
+        const float* RS;
+        __amdgpu_buffer_rsrc_t k_buf, v_buf, c_buf, s_buf, kv_rsrc;
+    };
+    auto item_of = [&](int it) {
+        Item I;
+        const int bh = it / q_tiles, qt = it % q_tiles;
+        I.b = bh / p.H;
+        I.h = bh % p.H;
+        I.wq0 = qt * RQT + wave * 16;
+        I.Q = static_cast<const float*>(p.q) + I.b * p.q_batch + I.h * kHeadDim;
+        const float* K = static_cast<const float*>(p.k) + I.b * p.k_batch + I.h * kHeadDim;
+        const float* V = static_cast<const float*>(p.v) + I.b * p.v_batch + I.h * kHeadDim;
+        const int rope_tab = rope_tabs > 0 ? (p.rope_row0 + I.b) / rope_tabs : 0;
+        I.RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
+        I.RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
+        I.k_buf = make_buf(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 4));
+        I.v_buf = make_buf(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 4));
+        I.c_buf = make_buf(I.RC, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+        I.s_buf = make_buf(I.RS, ROPE ? (uint32_t)p.n_k * 128u : 0u);
+        I.kv_rsrc = make_buf(mask_reads_valid<MASK>() ? p.key_valid + I.b * p.kv_batch : p.key_valid,
+                             mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0);
+        return I;
+    };
 
-    // ---- stage K (rotated), V, key terms, T5 table and q: every load issued before the first wait
-    //      (with RoPE, K and its tables go first and are stored before V is requested: holding all
-    //      of them at once would not fit the register budget) ----
-    f32x4 klo[RKIT], khi[RKIT];
-    auto store_k = [&]() {
+    // ---- staging of one item: loads into registers (K rotated at the store), then stores into one
+    //      of the two LDS buffers ----
+    f32x4 klo[RKIT], khi[RKIT], kcs[RKIT], ksn[RKIT];
+    f32x4 v01[RVIT], v23[RVIT];
+    uint32_t kvb = 1;
+    f32x4 qa[4];  // the next item's raw q (dims 8g..8g+7, 32+8g..32+8g+7 of query wq0 + ql)
+    auto stage_load = [&](const Item& I) {
+#pragma unroll
+        for (int u = 0; u < RKIT; u++) {  // K item = (row, c): dims 4c..4c+3 and 32+4c..32+4c+3
+            const int it = tid + u * RNT, row = it >> 3, c = it & 7;
+            const uint32_t off = (uint32_t)(row * p.k_tok + 4 * c) * 4u;
+            klo[u] = bld4(I.k_buf, off);
+            khi[u] = bld4(I.k_buf, off + 128u);
+            if (ROPE) {
+                const uint32_t coff = (uint32_t)(row * 32 + 4 * c) * 4u;
+                kcs[u] = bld4(I.c_buf, coff);
+                ksn[u] = bld4(I.s_buf, coff);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < RVIT; u++) {  // V item = (quad of 4 rows, dims 2vc, 2vc+1)
+            const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
+            const uint32_t off = (uint32_t)(4 * quad * p.v_tok + 2 * vc) * 4u, step = (uint32_t)p.v_tok * 4u;
+            const f32x2 a = bld2(I.v_buf, off), bb = bld2(I.v_buf, off + step);
+            const f32x2 c = bld2(I.v_buf, off + 2 * step), d = bld2(I.v_buf, off + 3 * step);
+            v01[u] = f32x4{a[0], a[1], bb[0], bb[1]};
+            v23[u] = f32x4{c[0], c[1], d[0], d[1]};
+        }
+        if (mask_reads_valid<MASK>() && tid < lay.nkp) kvb = __builtin_amdgcn_raw_buffer_load_b8(I.kv_rsrc, tid, 0, 0);
+        const int qi = I.wq0 + ql;
+        qa[0] = qa[1] = qa[2] = qa[3] = f32x4{0, 0, 0, 0};
+        if (qi < p.n_q) {
+            const float* src = I.Q + (int64_t)qi * p.q_tok;
+            qa[0] = ld4(src + 8 * g);
+            qa[1] = ld4(src + 8 * g + 4);
+            qa[2] = ld4(src + 32 + 8 * g);
+            qa[3] = ld4(src + 32 + 8 * g + 4);
+        }
+    };
+    // The staged item into buffer `buf`, and the wave's QBlock for it (q rotated and scaled as
+    // load_q does).
+    auto stage_store = [&](const Item& I, float* buf, QBlock& w) {
+        float* const Ks = buf;
+        float* const Vs = buf + lay.v_off;
 #pragma unroll
         for (int u = 0; u < RKIT; u++) {
             const int it = tid + u * RNT, row = it >> 3, c = it & 7;
             if (row >= lay.nkp) continue;
+            if (ROPE) rope4(klo[u], khi[u], kcs[u], ksn[u]);
             st4(Ks + row * KPAD + 4 * c, klo[u]);
             st4(Ks + row * KPAD + 32 + 4 * c, khi[u]);
         }
-    };
 #pragma unroll
-    for (int u = 0; u < RKIT; u++) {  // K item = (row, c): dims 4c..4c+3 and 32+4c..32+4c+3
-        const int it = tid + u * RNT, row = it >> 3, c = it & 7;
-        const uint32_t off = (uint32_t)(row * p.k_tok + 4 * c) * 4u;
-        klo[u] = bld4(k_buf, off);
-        khi[u] = bld4(k_buf, off + 128u);
-    }
-    if (ROPE) {
-        f32x4 kcs[RKIT], ksn[RKIT];
-#pragma unroll
-        for (int u = 0; u < RKIT; u++) {
-            const int it = tid + u * RNT, row = it >> 3, c = it & 7;
-            const uint32_t coff = (uint32_t)(row * 32 + 4 * c) * 4u;
-            kcs[u] = bld4(c_buf, coff);
-            ksn[u] = bld4(s_buf, coff);
+        for (int u = 0; u < RVIT; u++) {
+            const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
+            if (4 * quad >= lay.nkp) continue;
+            float* vd = Vs + quad * (kHeadDim * 4);
+            st4(vd + vslot(2 * vc) * 4, f32x4{v01[u][0], v01[u][2], v23[u][0], v23[u][2]});
+            st4(vd + vslot(2 * vc + 1) * 4, f32x4{v01[u][1], v01[u][3], v23[u][1], v23[u][3]});
+        }
+        if (tid < lay.nkp) buf[lay.a_off + tid] = key_term<MASK>(tid, p.n_k, kvb != 0, p.ctx_keys);
+        if (BIAS == BIAS_REL) fill_rel_lut(buf + lay.l_off, p, I.h, tid, RNT);
+        const int qi = I.wq0 + ql;
+        if (ROPE && qi < p.n_q) {
+            const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
+            rope4(qa[0], qa[2], ld4(I.RC + row + 8 * g), ld4(I.RS + row + 8 * g));
+            rope4(qa[1], qa[3], ld4(I.RC + row + 8 * g + 4), ld4(I.RS + row + 8 * g + 4));
         }
 #pragma unroll
-        for (int u = 0; u < RKIT; u++) rope4(klo[u], khi[u], kcs[u], ksn[u]);
-        store_k();
-    }
-    f32x4 v01[RVIT], v23[RVIT];
+        for (int t = 0; t < 4; t++) {
+            w.q[t] = qa[0][t] * p.scale;
+            w.q[4 + t] = qa[1][t] * p.scale;
+            w.q[8 + t] = qa[2][t] * p.scale;
+            w.q[12 + t] = qa[3][t] * p.scale;
+        }
 #pragma unroll
-    for (int u = 0; u < RVIT; u++) {  // V item = (quad of 4 rows, dims 2vc, 2vc+1)
-        const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
-        const uint32_t off = (uint32_t)(4 * quad * p.v_tok + 2 * vc) * 4u, step = (uint32_t)p.v_tok * 4u;
-        const f32x2 a = bld2(v_buf, off), bb = bld2(v_buf, off + step);
-        const f32x2 c = bld2(v_buf, off + 2 * step), d = bld2(v_buf, off + 3 * step);
-        v01[u] = f32x4{a[0], a[1], bb[0], bb[1]};
-        v23[u] = f32x4{c[0], c[1], d[0], d[1]};
-    }
-    float kterm = 0.f;
-    if (tid < lay.nkp) {
-        const uint32_t kvb = mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, tid, 0, 0) : 1u;
-        kterm = key_term<MASK>(tid, p.n_k, kvb != 0, p.ctx_keys);
-    }
-    QBlock w;
-    load_q<ROPE>(w, Q, RC, RS, p, qi, g);
-    const int wave_nq = max(0, min(16, p.n_q - wq0));
-    if (wave_nq == 1) thin_store_q(w, thin_qp, ql, g);
-    if (BIAS == BIAS_REL) fill_rel_lut(lut - kLutPad, p, h, tid, RNT);
-    if (!ROPE) store_k();
-#pragma unroll
-    for (int u = 0; u < RVIT; u++) {
-        const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
-        if (4 * quad >= lay.nkp) continue;
-        float* vd = Vs + quad * (kHeadDim * 4);
-        st4(vd + vslot(2 * vc) * 4, f32x4{v01[u][0], v01[u][2], v23[u][0], v23[u][2]});
-        st4(vd + vslot(2 * vc + 1) * 4, f32x4{v01[u][1], v01[u][3], v23[u][1], v23[u][3]});
-    }
-    if (tid < lay.nkp) kadd[tid] = kterm;
-    __syncthreads();  // the only barrier: everything below reads LDS that no one writes again
+        for (int db = 0; db < 4; db++) w.o[db] = f32x4{0, 0, 0, 0};
+        w.m = w.ml = kNegInf;
+        w.l = 0.f;
+        if (max(0, min(16, p.n_q - I.wq0)) == 1) thin_store_q(w, buf + lay.t_off, ql, g);
+    };
 
-    if (wave_nq == 0) return;
-    const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
-    if (wave_nq == 1) {  // one query: the VALU path, 64 resident keys at a time
-        for (int kb0 = 0; kb0 < wave_kend; kb0 += 64)
-            attend_thin<MASK, BIAS>(w, p, Ks + kb0 * KPAD, Vs + (kb0 >> 2) * (kHeadDim * 4), kadd + kb0, lut, thin_qp,
-                                    thin_qp + kHeadDim, kb0, min(64, wave_kend - kb0), wq0, h, lane);
-        store_thin(w, O, p, wq0, lane);
-        return;
+    // ---- one item's attention over the keys resident in `buf` ----
+    auto compute = [&](const Item& I, const float* buf, QBlock& w) {
+        const float* const Ks = buf;
+        const float* const Vs = buf + lay.v_off;
+        const float* const kadd = buf + lay.a_off;
+        const float* const lut = buf + lay.l_off + kLutPad;
+        float* const thin_qp = const_cast<float*>(buf) + lay.t_off;
+        float* __restrict__ O = static_cast<float*>(p.o) + I.b * p.o_batch + I.h * kHeadDim;
+        const int wq0 = I.wq0, qi = wq0 + ql, h = I.h;
+        const int wave_nq = max(0, min(16, p.n_q - wq0));
+        if (wave_nq == 0) return;
+        const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
+        if (wave_nq == 1) {  // one query: the VALU path, 64 resident keys at a time
+            for (int kb0 = 0; kb0 < wave_kend; kb0 += 64)
+                attend_thin<MASK, BIAS>(w, p, Ks + kb0 * KPAD, Vs + (kb0 >> 2) * (kHeadDim * 4), kadd + kb0, lut,
+                                        thin_qp, thin_qp + kHeadDim, kb0, min(64, wave_kend - kb0), wq0, h, lane);
+            store_thin(w, O, p, wq0, lane);
+            return;
+        }
+        auto no_hook = [](int, int) {};
+        // 32-key tiles (two key blocks): half the score registers of a 64-key tile. The last few
+        // keys of the row (a tile of at most kValuKeys) go to the VALU after the loop.
+        const int klast = wave_kend > 0 ? (wave_kend - 1) / RNK * RNK : 0;
+        const int kloop = wave_kend - klast <= kValuKeys ? klast : wave_kend;
+        for (int kbase = 0; kbase < kloop; kbase += RNK) {
+            const int nkb = min(2, (wave_kend - kbase + 15) >> 4);
+            // Query slots past n_q (q = 0, never stored) may run mask-free, except with a dense bias.
+            bool plain = kbase + RNK <= wave_kend && (wave_nq == 16 || BIAS != BIAS_DENSE) && MASK != DECODER;
+            if (plain && mask_reads_valid<MASK>())
+                plain = __ballot(lane < RNK && kadd[kbase + (lane & (RNK - 1))] != 0.f) == 0;
+            if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + RNK - 1 <= p.q_pos0 + wq0;
+            const float* kt = Ks + kbase * KPAD;
+            const float* vt = Vs + (kbase >> 2) * (kHeadDim * 4);
+            if (plain)
+                attend_tile<MASK, BIAS, true, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g, no_hook);
+            else
+                attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g, no_hook);
+        }
+        if (kloop < wave_kend)
+            attend_keys_valu<MASK, BIAS, false>(w, p, Ks + kloop * KPAD, Vs + (kloop >> 2) * (kHeadDim * 4),
+                                                kadd + kloop, lut, kloop, wave_kend - kloop, qi, h, g);
+        store_o(w, O, p, qi, g);
+    };
+
+    // ---- persistent loop: item i + gridDim.x loads into registers while item i computes, and is
+    //      stored into the other buffer after it (the one item i - gridDim.x used, whose readers all
+    //      passed the previous barrier) ----
+    int it = blockIdx.x;
+    if (it >= n_items) return;
+    QBlock w;
+    Item cur = item_of(it);
+    stage_load(cur);
+    stage_store(cur, smem, w);
+    __syncthreads();
+    for (int k = 0;; k++) {
+        const int nxt = it + gridDim.x;
+        const bool more = nxt < n_items;
+        Item next;
+        if (more) {
+            next = item_of(nxt);
+            stage_load(next);
+        }
+        float* const cb = smem + (k & 1) * lay.total;
+        compute(cur, cb, w);
+        if (!more) break;
+        stage_store(next, smem + ((k + 1) & 1) * lay.total, w);
+        __syncthreads();
+        cur = next;
+        it = nxt;
     }
-    auto no_hook = [](int, int) {};
-    // 32-key tiles (two key blocks): half the score registers of a 64-key tile, for the 80-VGPR
-    // budget, at the price of one more max/rescale per 64 keys.
-    // The last few keys of the row (a tile of at most kValuKeys) go to the VALU after the loop.
-    const int klast = wave_kend > 0 ? (wave_kend - 1) / RNK * RNK : 0;
-    const int kloop = wave_kend - klast <= kValuKeys ? klast : wave_kend;
-    for (int kbase = 0; kbase < kloop; kbase += RNK) {
-        const int nkb = min(2, (wave_kend - kbase + 15) >> 4);
-        // Query slots past n_q (q = 0, never stored) may run mask-free, except with a dense bias.
-        bool plain = kbase + RNK <= wave_kend && (wave_nq == 16 || BIAS != BIAS_DENSE) && MASK != DECODER;
-        if (plain && mask_reads_valid<MASK>()) plain = __ballot(lane < RNK && kadd[kbase + (lane & (RNK - 1))] != 0.f) == 0;
-        if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + RNK - 1 <= p.q_pos0 + wq0;
-        const float* kt = Ks + kbase * KPAD;
-        const float* vt = Vs + (kbase >> 2) * (kHeadDim * 4);
-        if (plain)
-            attend_tile<MASK, BIAS, true, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g,
-                                             no_hook);
-        else
-            attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g,
-                                              no_hook);
+}
+
+// Compute units of the current device (looked up once per device).
+int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev] = n;
     }
-    if (kloop < wave_kend)
-        attend_keys_valu<MASK, BIAS, false>(w, p, Ks + kloop * KPAD, Vs + (kloop >> 2) * (kHeadDim * 4), kadd + kloop,
-                                            lut, kloop, wave_kend - kloop, qi, h, g);
-    store_o(w, O, p, qi, g);
+    return cached[dev];
 }
 
 template <int MASK, int BIAS, bool ROPE>
 hipError_t launch_one(const Params& p, hipStream_t stream) {
     if (p.n_k <= kResidentKeys) {  // short rows: the whole K/V of a (series, head) in LDS
         const int q_tiles = (p.n_q + RQT - 1) / RQT;
-        const int64_t blocks = (int64_t)p.B * p.H * q_tiles;
-        if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-        const size_t lds = (size_t)resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL).total * sizeof(float);
+        const int64_t items = (int64_t)p.B * p.H * q_tiles;
+        if (items <= 0 || items > 0x7fffffff) return hipErrorInvalidValue;
+        const size_t lds = 2 * (size_t)resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL).total * sizeof(float);
+        const int cus = device_cus();
+        if (cus <= 0) return hipErrorInvalidDevice;
+        const int64_t blocks = items < cus ? items : cus;  // one persistent workgroup per CU
         hipLaunchKernelGGL((attn_fwd_f32_resident<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(RNT), lds, stream,
-                           p);
+                           p, (int)items);
         return hipGetLastError();
     }
     const int q_tiles = (p.n_q + QT - 1) / QT;
