@@ -97,7 +97,7 @@ def test_timestral_projection_matches_oracle(ta, orc, gpu_ready, gated):
                                            (8, 512, 528), (2, 256, 40), (3, 512, 16)])
 def test_bolt_projection_odd_shapes(ta, orc, gpu_ready, nh, d_in, tokens):
     """No RoPE (Chronos-Bolt); d_in != heads * 64; column counts 3 * nh * 64 that end in half a
-    128-column tile; token counts that end in a partial 128-token tile. Three shapes have few
+    128-column tile; token counts that end in a partial 128-token tile. Four shapes have few
     output tiles and a long reduction, so the three outputs are computed as split partials summed
     by the reduce kernel: 1 token x 768 (6 splits), the Chronos-Bolt-small encoder's 528 tokens x
     512 (4 splits), 40 tokens x 256 (2 splits), and 16 tokens x 512 into 576 columns (a last tile
