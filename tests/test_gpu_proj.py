@@ -51,6 +51,32 @@ def test_chronos2_projection_matches_oracle(ta, orc, gpu_ready, b, seq):
         assert _ref.scaled_err(got, ref) <= TOL
 
 
+def test_tile_shapes_give_the_same_bits(ta, orc, gpu_ready):
+    """34 series of 128 tokens, 2304 output columns: 34 x 18 = 612 tiles of 128 x 128, more than two
+    per CU of a 256-CU device with a last round under half full, so the first 28 token tiles take
+    128 x 128 tiles and the rest 64 x 64 ones. One series alone (18 tiles) runs all in 64 x 64 tiles:
+    the blocked accumulation makes its rows the same bits in either launch."""
+    b, seq, d, nh = 34, 128, 768, 12
+    rng = np.random.default_rng(34)
+    x = rng.standard_normal((b * seq, d)).astype(np.float32)
+    wq, wk, wv = _weights(rng, d, d, 3)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    full = [np.full((b * seq, d), -3.0, np.float32) for _ in range(3)]
+    rc = ta.chronos2_qkv_projection(x, wq, wk, wv, *full, cos_t, sin_t, b, seq, d, nh, 64)
+    assert rc == ta.OK, ta.last_error()
+    want = _chronos2_oracle(orc, x, wq, wk, wv, cos_t, sin_t, b, seq, d, nh)
+    for got, ref in zip(full, want):
+        assert _ref.scaled_err(got, ref) <= TOL
+    for s in (0, 20, b - 1):
+        rows = slice(s * seq, (s + 1) * seq)
+        one = [np.full((seq, d), -3.0, np.float32) for _ in range(3)]
+        rc = ta.chronos2_qkv_projection(np.ascontiguousarray(x[rows]), wq, wk, wv, *one, cos_t, sin_t, 1, seq, d,
+                                        nh, 64)
+        assert rc == ta.OK, ta.last_error()
+        for got, ref in zip(one, full):
+            np.testing.assert_array_equal(got, ref[rows])
+
+
 def test_chronos2_projection_device_pointers(ta, orc, gpu_ready):
     import torch
 

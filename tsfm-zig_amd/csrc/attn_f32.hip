@@ -29,6 +29,8 @@
 // LDS per stage: K [64 keys][68] (padded: conflict-free 128-bit reads), V [16 key quads][64 dims,
 // XOR-swizzled][4 keys] (conflict-free transposing writes and operand reads), and one additive mask
 // term per key. Two stages + the T5 table fit two workgroups per CU.
+#include <atomic>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -836,18 +838,21 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
 }
 
-// Compute units of the current device (looked up once per device).
+}  // namespace
+
 int device_cus() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
+
+namespace {
 
 template <int MASK, int BIAS, bool ROPE>
 hipError_t launch_one(const Params& p, hipStream_t stream) {

@@ -79,6 +79,8 @@ struct ProjParams {
     int32_t rope_rows_per_table, rope_row0;
     int32_t tokens, seq, d_in, width, n_out, out_dtype;
     int32_t m_tiles, n_tiles;  // set by launch_proj
+    int32_t m_base;            // set by launch_proj: first token of the launch's token tiles
+    int32_t chunk;             // set by launch_proj: 16-wide reduction units per accumulation chunk
     int32_t splits, split_steps;  // set by launch_proj: reduction split over workgroups (small products)
     float* partial;               // set by launch_proj: [splits][tokens][width] partial sums
     // Optional row norm of the finished product (one f32 output): norm_out = rmsNorm(y0, norm_scale,
@@ -89,6 +91,8 @@ struct ProjParams {
     float norm_eps;
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
+// Compute units of the current device (looked up once per device; 0 if the query fails).
+int device_cus();
 // dst[c][r] = src[r][c] for a rows x cols f32 matrix (row strides in elements).
 hipError_t launch_transpose_f32(const float* src, int64_t ld_src, float* dst, int64_t ld_dst, int rows, int cols,
                                 hipStream_t stream);

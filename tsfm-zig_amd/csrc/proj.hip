@@ -14,14 +14,25 @@
 //
 // One launch computes every output: the output columns are the concatenation [q | k | v | gate]
 // (each heads * 64 wide), so x is streamed through the chip once for all of them. A workgroup
-// computes a 64-token x 64-column tile (one head) with K = d_in in 32-wide steps (16-wide when
-// d_in is not a multiple of 32): x and w tiles go HBM/L2 -> registers -> LDS (double-buffered, one
-// barrier per step), and each of the four waves multiplies a 32 x 32 sub-tile with
-// v_mfma_f32_16x16x4_f32 in four accumulation chains, the weight rows as the A operand so that each
-// lane ends with four consecutive output columns of one token (16-byte stores, and the RoPE
-// partner column i + 32 in the same lane); f32 outputs, or bf16/f16 for the half-precision
-// attention path. Four workgroups share a CU (one wave of each per SIMD), so one's step barrier
-// and prologue are covered by the others' products.
+// computes a token x column tile, K = d_in in 16- or 32-wide steps: x and w tiles go from HBM/L2
+// straight into LDS (global_load_lds_dwordx4, double-buffered, one barrier per step), laid out in
+// the order the operand reads take them (no bank conflicts, no staging registers), and each wave
+// multiplies a 32-token sub-tile with v_mfma_f32_16x16x4_f32, the weight rows as the A operand so
+// that each lane ends with four consecutive output columns of one token (16-byte stores, and the
+// RoPE partner column i + 32 in the same lane); f32 outputs, or bf16/f16 for the half-precision
+// attention path. Large products take 128 x 128 tiles (8 waves of 32 tokens x one 64-column head,
+// two workgroups per CU; the tokens of a last round of tiles that would leave most CUs idle go to
+// a second launch of small tiles); small ones, and those whose reduction is split over
+// workgroups, 64 x 64 tiles (4 waves of 32 x 32, four workgroups per CU).
+//
+// Accumulation order. v_mfma_f32_16x16x4_f32 rounds as it accumulates, so one accumulator carried
+// across the whole reduction would be a chain of d_in / 4 rounded additions, several times the
+// error of the reference's nn.lanes vector partial sums (src/core/nn.zig:68-126: 8 or 16 lanes of
+// d_in / lanes products each, then a reduction). The reduction is therefore blocked: each chunk of
+// c 16-wide units (16 c indices of the workgroup's range) runs as its own chain of 4 c
+// instructions started at zero, and the chunk sums are added in order into the output's total.
+// c ~ sqrt(d_in / 64) (proj_chunk) keeps the longest run of roundings near 4 sqrt(d_in / 16): 12
+// steps at d_in 128, 28 at 768, 56 at 3072, in a fixed order that depends on d_in alone.
 #include <algorithm>
 
 #include "common.hpp"
@@ -30,15 +41,27 @@
 namespace tsfm {
 namespace {
 
-constexpr int BM = 64;           // tokens per workgroup tile
-constexpr int BN = 64;           // output columns per workgroup tile: one head
-constexpr int NT = 256;          // four waves: 2 (32 tokens) x 2 (column pairs)
+// Tile shapes. SMALL: 64 tokens x 64 columns (one head), four waves = 2 (32 tokens) x 2 (column
+// pairs 16 wq + {0, 32}). BIG: 128 tokens x 128 columns (two heads), eight waves = 4 (32 tokens) x
+// 2 (heads), each wave all four 16-column blocks of its head.
+constexpr int BM = 64;           // tokens per SMALL tile (and the unit of the split partials)
+constexpr int BN = 64;           // columns per SMALL tile: one head
 constexpr int GM = 8;            // token tiles that sweep the column tiles together
-// Reduction step BK (16 or 32; 32 when d_in allows): LDS rows padded to BK + 4 floats, so the 16
-// rows one operand read touches hit distinct banks.
-template <int BK>
-constexpr size_t proj_lds() { return (size_t)2 * (BM + BN) * (BK + 4) * sizeof(float); }
+template <bool BIG> constexpr int tile_m() { return BIG ? 128 : 64; }
+template <bool BIG> constexpr int tile_n() { return BIG ? 128 : 64; }
+template <bool BIG> constexpr int threads() { return BIG ? 512 : 256; }
+// Reduction step BK (16 or 32). LDS holds each tile of a step as 1 KB chunks, one per 16 rows x
+// 16 reduction indices, in the order the matrix instructions read them (below): no padding, and
+// every operand read is 64 lanes x 16 contiguous bytes.
+template <int BK, bool BIG>
+constexpr size_t proj_lds() { return (size_t)2 * (tile_m<BIG>() + tile_n<BIG>()) * BK * sizeof(float); }
 static_assert(kSplitWorkspaceBytes == (size_t)1536 * BM * BN * sizeof(float), "split workspace size");
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+// 16 bytes per lane from global memory straight into LDS: lane l's go to lds + 16 l (lds the same
+// for the whole wave).
+__device__ __forceinline__ void load_lds16(const float* g, float* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)lds, 16, 0, 0);
+}
 
 // Workgroup tile of a logical id: GM token tiles at a time go through all column tiles, token tile
 // fastest, so the x rows of a group stay in L2 while the weight tiles stream past.
@@ -72,152 +95,140 @@ __device__ __forceinline__ f32x4 epi_act(int epi, f32x4 v) {
 
 // OUT: element type of the outputs, TSFM_DTYPE_* (0 f32, 1 bf16, 2 f16); the products and RoPE
 // are f32 either way and the result is rounded once, to nearest even, when it is stored.
-//
-// Accumulation order. v_mfma_f32_16x16x4_f32 rounds as it accumulates, so one accumulator carried
-// across the whole reduction would be a single chain of d_in rounded additions, several times the
-// error of the reference's nn.lanes vector partial sums (src/core/nn.zig:68-126: 8 or 16 lanes,
-// then a reduction). Each wave therefore keeps four accumulators per output block, one per
-// instruction slot j of a 16-wide chunk (reduction indices 16c + 4g + j), and sums them as a tree
-// at the end: four independent chains of d_in / 4 products, like a 4-lane reference, in a fixed
-// order. Waves of 32 tokens x 32 columns hold the four chains in 64 registers per lane.
-template <int OUT, int BK>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void qkv_proj(ProjParams p) {
-    constexpr int LDS_ROW = BK + 4;
-    constexpr int NX = BM * BK / 4, NW = BN * BK / 4;  // float4s of the x and weight tiles per step
-    constexpr int PER = (NX + NW + NT - 1) / NT;       // float4s a thread stages per step (at most)
-    static_assert(NX % 64 == 0 && (NX + NW) % 64 == 0, "loader slots are whole waves");
-    extern __shared__ __attribute__((aligned(16))) float smem[];
-    float* const xs = smem;                          // [2][BM][LDS_ROW]
-    float* const ws = smem + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
+template <int OUT, int BK, bool BIG>
+__global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(4, 4))) void qkv_proj(ProjParams p) {
+    constexpr int TM = tile_m<BIG>(), TN = tile_n<BIG>(), NT = threads<BIG>();
+    constexpr int NB = BIG ? 4 : 2;                  // 16-column blocks per wave
+    constexpr int NU = BK / 16;                      // 16-wide reduction units per step
+    constexpr int CX = TM / 16 * NU, CW = TN / 16 * NU;  // 1 KB chunks of the x and weight tiles
+    constexpr int NWAVE = NT / 64, PER = (CX + CW) / NWAVE;  // chunks a wave loads per step
+    constexpr int STAGE = (TM + TN) * BK;            // floats per LDS stage
+    static_assert(PER * NWAVE == CX + CW && CX % NWAVE == 0, "every wave loads PER chunks, all x or all weight");
+    extern __shared__ __attribute__((aligned(16))) float smem[];  // [2][x chunks, weight chunks]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int tm, tn;
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
     const int split = p.splits > 1 ? logical % p.splits : 0;  // this workgroup's share of the reduction
     tile_of(p.splits > 1 ? logical / p.splits : logical, p.m_tiles, p.n_tiles, tm, tn);
     const int n_cols = p.width * p.n_out;
+    const int row0 = p.m_base + tm * TM;  // the tile's first token
 
-    // Loader: slot f = tid + NT i (i < PER) of a step is float4 f of the x tile (f < NX) or float4
-    // f - NX of the weight tile (f < NX + NW); slots past that are idle (whole waves). A tile's
-    // float4 e is row e / (BK / 4), columns 4 (e % (BK / 4)) .. + 3. Rows past the end are clamped
-    // to the last row: they feed only outputs that are not stored.
+    // Loader: wave w loads chunks w + NWAVE i (i < PER) of each step, HBM/L2 straight into LDS
+    // (global_load_lds_dwordx4: lane l's 16 bytes land at the chunk's base + 16 l). Chunk e of the
+    // x tile (of the weight tile: e - CX) is row block e / NU, unit e % NU; lane l loads row
+    // (l & 15) of the block, reduction indices 16 (e % NU) + 4 (l >> 4) .. + 3 of the step. Rows
+    // past the end are clamped to the last row: they feed only outputs that are not stored.
     const float* src[PER];
-    float* dst[PER];
-    int stage[PER];  // floats between the two LDS buffers of this slot's tile; 0 = idle slot
+    int dst[PER];  // float offset of the chunk in a stage (the same for the whole wave)
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const int f = tid + NT * i;
-        const bool is_x = f < NX;
-        const int e = is_x ? f : min(f - NX, NW - 1), lr = e / (BK / 4), lc = (e % (BK / 4)) * 4;
+        const int ch = wave + NWAVE * i;
+        const bool is_x = i < CX / NWAVE;
+        const int e = is_x ? ch : ch - CX, r = (e / NU) * 16 + (lane & 15), kq = 16 * (e % NU) + 4 * (lane >> 4);
         if (is_x) {
-            src[i] = p.x + (int64_t)min(tm * BM + lr, p.tokens - 1) * p.x_tok + lc;
+            src[i] = p.x + (int64_t)min(row0 + r, p.tokens - 1) * p.x_tok + kq;
         } else {
-            const int n = min(tn * BN + lr, n_cols - 1);
+            const int n = min(tn * TN + r, n_cols - 1);
             const int sel = n / p.width;
             const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
-            src[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + lc;
+            src[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + kq;
         }
-        dst[i] = (is_x ? xs : ws) + lr * LDS_ROW + lc;
-        stage[i] = f < NX + NW ? (is_x ? BM : BN) * LDS_ROW : 0;
+        dst[i] = (is_x ? 0 : TM * BK) + e * 256;
     }
+    auto stage_in = [&](int t, int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; i++)
+            load_lds16(src[i] + t * BK, smem + buf * STAGE + dst[i]);
+    };
 
-    // Wave layout: token block wm (32 tokens), column pair wq: the wave's two 16-column blocks are wq
-    // and wq + 2 of the workgroup's head, so a RoPE pair (i, i + 32) is in one lane.
+    // Wave layout: token block wm (32 tokens) and, SMALL, column pair wq (blocks wq and wq + 2 of
+    // the head: a RoPE pair (i, i + 32) in one lane), BIG, head wq of the tile (blocks 0..3; pairs
+    // (0, 2) and (1, 3)). colb(nb): the tile column of the wave's block nb.
     // Operand reads: lane l takes row (l & 15) of a 16-row block and the four reduction indices
-    // 4 (l >> 4) .. + 3 of a 16-wide chunk; matrix instruction j uses element j, the same reduction
-    // index on both operands.
-    const int wm = wave & 1, wq = wave >> 1;
-    const float* const xr = xs + (wm * 32 + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
-    const float* const wr = ws + (16 * wq + (lane & 15)) * LDS_ROW + 4 * (lane >> 4);
+    // 4 (l >> 4) .. + 3 of a 16-wide unit -- 16 bytes at 16 l in the block's chunk of the unit;
+    // matrix instruction j uses element j, the same reduction index on both operands.
+    const int wm = BIG ? (wave & 3) : (wave & 1), wq = BIG ? (wave >> 2) : (wave >> 1);
+    auto colb = [&](int nb) { return BIG ? 64 * wq + 16 * nb : 16 * wq + 32 * nb; };
+    const float* const xr = smem + (2 * wm * NU) * 256 + 4 * lane;
+    const float* const wr = smem + TM * BK + 4 * lane;
 
-    f32x4 acc[4][2][2];  // [chain j][column block wq, wq + 2][token block]: columns 4 (l >> 4) + r, token l & 15
+    // tot: the output's total over the finished chunks; chk: the running chunk.
+    // [column block nb][token block]: columns 4 (l >> 4) + r, token l & 15.
+    f32x4 tot[NB][2], chk[NB][2];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int a = 0; a < NB; a++)
 #pragma unroll
-        for (int a = 0; a < 2; a++)
-#pragma unroll
-            for (int b = 0; b < 2; b++) acc[j][a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < 2; b++) tot[a][b] = chk[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int t0 = split * p.split_steps;
     const int steps = p.splits > 1 ? min(p.d_in / BK, t0 + p.split_steps) : p.d_in / BK;
-    f32x4 rv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++)
-        if (stage[i]) rv[i] = ld4(src[i] + t0 * BK);
-#pragma unroll
-    for (int i = 0; i < PER; i++)
-        if (stage[i]) st4(dst[i], rv[i]);
+    const int units = (steps - t0) * NU;  // 16-wide reduction units of this workgroup
+    int cu = 0;                           // units done in the running chunk
+    stage_in(t0, 0);
     __syncthreads();
     for (int t = t0; t < steps; t++) {
         const int buf = (t - t0) & 1;
-        if (t + 1 < steps) {
+        // The other stage was last read in step t - 1, which every wave has left (barrier below).
+        if (t + 1 < steps) stage_in(t + 1, buf ^ 1);
 #pragma unroll
-            for (int i = 0; i < PER; i++)
-                if (stage[i]) rv[i] = ld4(src[i] + (t + 1) * BK);
-        }
-        // Operands of chunk c + 1 are read from LDS while chunk c's products run.
-        f32x4 wa[2], xb[2];
+        for (int c = 0; c < NU; c++) {
+            const int u = (t - t0) * NU + c;
+            f32x4 wa[NB], xb[2];
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            wa[b] = ld4(wr + (buf * BN + 32 * b) * LDS_ROW);
-            xb[b] = ld4(xr + (buf * BM + 16 * b) * LDS_ROW);
-        }
+            for (int nb = 0; nb < NB; nb++) wa[nb] = ld4(wr + buf * STAGE + ((colb(nb) / 16) * NU + c) * 256);
 #pragma unroll
-        for (int c = 0; c < BK / 16; c++) {
-            f32x4 wn_[2], xn_[2];
-            if (c + 1 < BK / 16) {
+            for (int mb = 0; mb < 2; mb++) xb[mb] = ld4(xr + buf * STAGE + (mb * NU + c) * 256);
+            if (cu == 0) {  // a chunk starts: its chain begins at zero
 #pragma unroll
-                for (int b = 0; b < 2; b++) {
-                    wn_[b] = ld4(wr + (buf * BN + 32 * b) * LDS_ROW + 16 * (c + 1));
-                    xn_[b] = ld4(xr + (buf * BM + 16 * b) * LDS_ROW + 16 * (c + 1));
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++)
+                for (int nb = 0; nb < NB; nb++)
 #pragma unroll
                     for (int mb = 0; mb < 2; mb++)
-                        acc[j][nb][mb] =
-                            __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][j], xb[mb][j], acc[j][nb][mb], 0, 0, 0);
-            if (c + 1 < BK / 16) {
+                        chk[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][0], xb[mb][0],
+                                                                           f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            } else {
 #pragma unroll
-                for (int b = 0; b < 2; b++) {
-                    wa[b] = wn_[b];
-                    xb[b] = xn_[b];
-                }
+                for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                    for (int mb = 0; mb < 2; mb++)
+                        chk[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][0], xb[mb][0], chk[nb][mb], 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 1; j < 4; j++)
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                    for (int mb = 0; mb < 2; mb++)
+                        chk[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[nb][j], xb[mb][j], chk[nb][mb], 0, 0, 0);
+            if (++cu == p.chunk || u == units - 1) {  // the chunk is done: into the total
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                    for (int mb = 0; mb < 2; mb++) tot[nb][mb] += chk[nb][mb];
+                cu = 0;
             }
         }
-        // The other buffer was last read in step t - 1, which every wave has left (barrier below).
-        if (t + 1 < steps) {
-#pragma unroll
-            for (int i = 0; i < PER; i++)
-                if (stage[i]) st4(dst[i] + (buf ^ 1) * stage[i], rv[i]);
-        }
-        __syncthreads();
+        __syncthreads();  // the loads of step t + 1 have landed; nobody reads stage buf any more
     }
-    f32x4 sum[2][2];
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++)
-#pragma unroll
-        for (int mb = 0; mb < 2; mb++) sum[nb][mb] = (acc[0][nb][mb] + acc[1][nb][mb]) + (acc[2][nb][mb] + acc[3][nb][mb]);
+    f32x4 (&sum)[NB][2] = tot;
 
-    // Epilogue: this wave's columns are blocks wq and wq + 2 of one head of one output (or, with one
-    // output of a width that is not a multiple of 64, columns of a partial head: groups of four
-    // columns past the width are not stored).
-    const int n0 = tn * BN;
-    if (n0 >= n_cols) return;
-    const int sel = n0 / p.width, col = n0 - sel * p.width;
-    const int cq = 16 * wq + 4 * (lane >> 4);  // this lane's first column of block wq in the head
+    // Epilogue: the wave's columns of one output (or, with one output of a width that is not a
+    // multiple of 64, columns of a partial head: groups of four columns past the width are not
+    // stored). n0w: the output column (over all outputs) of the wave's head.
+    const int n0w = tn * TN + (BIG ? 64 * wq : 0);
+    if (n0w >= n_cols) return;
+    const int sel = n0w / p.width, col = n0w - sel * p.width;
+    const int c4 = 4 * (lane >> 4);
+    auto cq = [&](int nb) { return (BIG ? 16 * nb : 16 * wq + 32 * nb) + c4; };  // column in the head
     if (p.splits > 1) {  // partial sums only; proj_reduce adds them up in split order and finishes
         // Partial row m of split s holds all n_cols columns (every output side by side).
 #pragma unroll
         for (int mb = 0; mb < 2; mb++) {
-            const int m = tm * BM + wm * 32 + mb * 16 + (lane & 15);
+            const int m = row0 + wm * 32 + mb * 16 + (lane & 15);
             if (m >= p.tokens) continue;
-            float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0 + cq;
+            float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0w;
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-                if (col + cq + 32 * nb < p.width) st4(out + 32 * nb, sum[nb][mb]);
+            for (int nb = 0; nb < NB; nb++)
+                if (col + cq(nb) < p.width) st4(out + cq(nb), sum[nb][mb]);
         }
         return;
     }
@@ -225,38 +236,43 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
     const bool rope = p.rope_cos != nullptr && sel < 2;
 #pragma unroll
     for (int mb = 0; mb < 2; mb++) {
-        const int m = tm * BM + wm * 32 + mb * 16 + (lane & 15);
+        const int m = row0 + wm * 32 + mb * 16 + (lane & 15);
         if (m >= p.tokens) continue;
         if (p.alpha != 1.f) {  // gemmNT's alpha, applied to the finished sum (src/core/nn.zig:100)
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) sum[nb][mb] *= p.alpha;
+            for (int nb = 0; nb < NB; nb++) sum[nb][mb] *= p.alpha;
         }
         if (rope) {
-            // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table.
+            // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table; the
+            // pairs (i, i + 32) are blocks (nb, nb + NB / 2).
             const int b = m / p.seq, tok = m - b * p.seq;
             const int table = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
-            const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq;
-            rope4(sum[0][mb], sum[1][mb], ld4(p.rope_cos + at), ld4(p.rope_sin + at));
+#pragma unroll
+            for (int k = 0; k < NB / 2; k++) {
+                const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq(k);
+                rope4(sum[k][mb], sum[k + NB / 2][mb], ld4(p.rope_cos + at), ld4(p.rope_sin + at));
+            }
         }
-        const int64_t at = out_offset(p, sel, m) + col + cq;
+        const int64_t at = out_offset(p, sel, m) + col;
         if constexpr (OUT == 0) {
             float* const out = static_cast<float*>(y) + at;
-            const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col + cq : nullptr;
+            const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col : nullptr;
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) {
-                if (col + cq + 32 * nb >= p.width) continue;
+            for (int nb = 0; nb < NB; nb++) {
+                if (col + cq(nb) >= p.width) continue;
                 f32x4 v = sum[nb][mb];
-                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq + 32 * nb);  // nn.linear's bias (linearCols, nn.zig:254)
-                if (p.epi == kEpiResidual) v = ld4(res + 32 * nb) + v;  // x + delta, one rounding
+                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq(nb));  // nn.linear's bias (linearCols, nn.zig:254)
+                if (p.epi == kEpiResidual) v = ld4(res + cq(nb)) + v;  // x + delta, one rounding
                 else v = epi_act(p.epi, v);
-                st4(out + 32 * nb, v);
+                st4(out + cq(nb), v);
             }
         } else {
             uint16_t* const out = static_cast<uint16_t*>(y) + at;
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) {
+            for (int nb = 0; nb < NB; nb++) {
                 const f32x4 v = sum[nb][mb];
-                *reinterpret_cast<u32x2*>(out + 32 * nb) = u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
+                *reinterpret_cast<u32x2*>(out + cq(nb)) =
+                    u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
             }
         }
     }
@@ -320,19 +336,58 @@ SplitWorkspace::~SplitWorkspace() { t_split_ws = prev_; }
 
 namespace {
 
-// The unsplit product: 32-wide steps when d_in allows (half the step barriers), else 16-wide. The
-// chains are the same either way (chain j sums reduction indices 16c + 4g + j in increasing c), so
-// the result does not depend on the step width.
+// The unsplit product. BIG tiles when there are enough of them for every CU; SMALL ones take
+// 32-wide steps when d_in allows (half the step barriers), else 16-wide. The accumulation chunks
+// are the same units of 16 p.chunk indices either way, so the result depends on neither the step
+// width nor the tile shape, and one product may mix the two.
+constexpr int64_t kBigTilesMin = 256;
 template <int OUT>
-hipError_t launch_unsplit(const ProjParams& p, int64_t blocks, hipStream_t stream) {
+hipError_t launch_small(ProjParams p, hipStream_t stream) {
+    p.m_tiles = (p.tokens - p.m_base + BM - 1) / BM;
+    p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
+    const unsigned blocks = (unsigned)((int64_t)p.m_tiles * p.n_tiles);
     if (p.d_in % 32 == 0)
-        hipLaunchKernelGGL((qkv_proj<OUT, 32>), dim3((unsigned)blocks), dim3(NT), proj_lds<32>(), stream, p);
+        hipLaunchKernelGGL((qkv_proj<OUT, 32, false>), dim3(blocks), dim3(threads<false>()), (proj_lds<32, false>()),
+                           stream, p);
     else
-        hipLaunchKernelGGL((qkv_proj<OUT, 16>), dim3((unsigned)blocks), dim3(NT), proj_lds<16>(), stream, p);
+        hipLaunchKernelGGL((qkv_proj<OUT, 16, false>), dim3(blocks), dim3(threads<false>()), (proj_lds<16, false>()),
+                           stream, p);
     return hipGetLastError();
 }
 
+template <int OUT>
+hipError_t launch_unsplit(ProjParams p, hipStream_t stream) {
+    const int64_t big_m = (p.tokens + 127) / 128, big_n = (p.width * p.n_out + 127) / 128;
+    if (big_m * big_n < kBigTilesMin) return launch_small<OUT>(p, stream);
+    // BIG tiles run two per CU, in rounds that each take one tile's time. A last round less than
+    // half full would cost a whole one: the token tiles past the full rounds go to SMALL tiles
+    // instead (four per CU, a quarter of the work each), in a second launch.
+    int64_t m_big = big_m;
+    const int64_t slots = 2 * (int64_t)device_cus(), rest = slots > 0 ? (big_m * big_n) % slots : 0;
+    if (slots > 0 && big_m * big_n > slots && rest > 0 && 2 * rest < slots)
+        m_big = std::max<int64_t>(1, (big_m * big_n - rest) / big_n);
+    p.m_tiles = (int32_t)m_big;
+    p.n_tiles = (int32_t)big_n;
+    // 16-wide steps: with 32-wide ones the eight waves' operands, totals and running chunks need
+    // more than the 128 registers that four waves per SIMD leave.
+    hipLaunchKernelGGL((qkv_proj<OUT, 16, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
+                       (proj_lds<16, true>()), stream, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || m_big * 128 >= p.tokens) return e;
+    p.m_base = (int32_t)(m_big * 128);
+    return launch_small<OUT>(p, stream);
+}
+
 }  // namespace
+
+// Accumulation chunk (in 16-wide units) for a workgroup range of `units` units: a chunk's chain is
+// 4 c rounded steps and the chunk totals add units / c more, so c ~ sqrt(units / 4) keeps the
+// longest run of roundings near its minimum, 2 sqrt(4 units) (28 steps at d_in 768, 12 at 128).
+static int proj_chunk(int units) {
+    int c = 1;
+    while (4 * (c + 1) + (units + c) / (c + 1) < 4 * c + (units + c - 1) / c) c++;
+    return c;
+}
 
 size_t proj_split_bytes(ProjParams& p) {
     p.m_tiles = (p.tokens + BM - 1) / BM;
@@ -360,6 +415,7 @@ size_t proj_split_bytes(ProjParams& p) {
 
 hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     ProjParams p = p0;
+    p.m_base = 0;
     if (p.tokens <= 0 || p.width <= 0 || p.n_out <= 0) return hipSuccess;
     if (p.d_in % 16 || p.d_in <= 0 || p.n_out > 4 || p.seq <= 0 || p.out_dtype < 0 || p.out_dtype > 2 ||
         p.w_ld < p.d_in || p.width % 4 || (p.n_out > 1 && p.width % kHeadDim) ||
@@ -382,8 +438,10 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         p.partial = t_split_ws;
     }
     const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
+    p.chunk = proj_chunk(p.splits > 1 ? p.split_steps : p.d_in / 16);
     if (p.splits > 1) {
-        hipLaunchKernelGGL((qkv_proj<0, 16>), dim3((unsigned)(blocks * p.splits)), dim3(NT), proj_lds<16>(), stream, p);
+        hipLaunchKernelGGL((qkv_proj<0, 16, false>), dim3((unsigned)(blocks * p.splits)), dim3(threads<false>()),
+                           (proj_lds<16, false>()), stream, p);
         hipError_t e = hipGetLastError();
         if (e == hipSuccess && p.norm_scale != nullptr) {
             hipLaunchKernelGGL(proj_reduce_norm, dim3((unsigned)((p.tokens + 3) / 4)), dim3(256), 0, stream, p);
@@ -396,14 +454,14 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         return e;
     }
     if (p.norm_scale != nullptr) {
-        const hipError_t e = launch_unsplit<0>(p, blocks, stream);
+        const hipError_t e = launch_unsplit<0>(p, stream);
         if (e != hipSuccess) return e;
         return launch_rms_norm(static_cast<const float*>(p.y0), p.y0_tok, p.norm_out, p.norm_out_tok, p.norm_scale,
                                p.tokens, p.width, p.norm_eps, stream);
     }
-    if (p.out_dtype == 1) return launch_unsplit<1>(p, blocks, stream);
-    if (p.out_dtype == 2) return launch_unsplit<2>(p, blocks, stream);
-    return launch_unsplit<0>(p, blocks, stream);
+    if (p.out_dtype == 1) return launch_unsplit<1>(p, stream);
+    if (p.out_dtype == 2) return launch_unsplit<2>(p, stream);
+    return launch_unsplit<0>(p, stream);
 }
 
 namespace {
