@@ -384,6 +384,17 @@ def assert_within_reference_bar(got, lane8, lane16, exact=None):
     return err, bar
 
 
+def assert_no_further_from_exact(got, lane8, lane16, exact):
+    """The GPU result is at most as far from the float64 evaluation as the reference's worse host
+    build (8 or 16 nn.lanes): its own rounding is no worse than the reference's."""
+    g = scaled_err(got, exact)
+    m = max(scaled_err(lane8, exact), scaled_err(lane16, exact))
+    print(f"distance from f64: GPU {g:.3e}, reference builds {scaled_err(lane8, exact):.3e} / "
+          f"{scaled_err(lane16, exact):.3e}")
+    assert g <= m, f"GPU {g:.3e} from f64 > the reference's {m:.3e}"
+    return g, m
+
+
 # ---- the Timestral model in float64, written from its definitions ---------------------------------
 
 

@@ -78,6 +78,7 @@ def test_bolt_forward_small_shape(ta, orc, orc16, gpu_ready):
     exact = _exact(orc, s, b, n_patch, nh)
     assert _ref.scaled_err(w16, exact) < 5e-4
     _ref.assert_within_reference_bar(raw, w8, w16, exact)
+    _ref.assert_no_further_from_exact(raw, w8, w16, exact)
 
 
 def test_bolt_forward_device_pointers_match_host(ta, orc, gpu_ready):

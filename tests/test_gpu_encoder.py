@@ -122,6 +122,7 @@ def test_encode_twelve_layers_drift_like_the_oracle(ta, orc, orc16, gpu_ready):
     exact = _ref.chronos2_encode_f64(x, kv, b, seq, nh, layers, fn, eps, cos_t, sin_t, 1.0)
     assert _ref.scaled_err(w16, exact) < 5e-4  # the f32 reference path itself, for scale
     _ref.assert_within_reference_bar(got, w8, w16, exact)
+    _ref.assert_no_further_from_exact(got, w8, w16, exact)
 
 
 # ---- the model part of the Chronos-2 forecaster: embedding, encoder, output head ------------------
