@@ -19,8 +19,10 @@
 // Accuracy: the f32 matrix instruction rounds after every product, so one 16-step accumulation
 // chain over the 64 head dims carries ~2.5x the rounding error of the reference's lane-parallel
 // dot product (a few sequential products per SIMD lane, then a tree over lanes). S is therefore
-// accumulated in four independent chains of four instructions, summed as a tree, which brings the
-// scores to the reference's accuracy and gives the matrix pipe four independent dependency chains.
+// accumulated in two independent chains of eight instructions, then added: nine rounded steps
+// instead of sixteen, within the reference's own cross-host spread, and two dependency chains for
+// the matrix pipe. (Four chains of four summed as a tree round six times but cost twelve more VALU
+// instructions per 16-key block, and on gfx950 the f32 matrix instructions and the VALU take turns.)
 //
 // Pipeline: two LDS stages. While the waves compute on stage t&1, tile t+1 is fetched from HBM and
 // written to the other stage in two 32-key halves (one over the S product, one over softmax and
@@ -149,21 +151,21 @@ __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const fl
         hook(0, kb);
         if (!PLAIN && kb >= nkb) continue;
         const float* kr = kt + (kb * 16 + ql) * KPAD;
-        f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+        f32x4 c0 = {0, 0, 0, 0}, c1 = c0;
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {  // dims 8g.. then 32+8g..: eight K values live at a time
             const f32x4 ka = ld4(kr + 32 * hh + 8 * g), kb4 = ld4(kr + 32 * hh + 8 * g + 4);
             const float* qh = w.q + 8 * hh;
             c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[0], qh[0], c0, 0, 0, 0);
             c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[1], qh[1], c1, 0, 0, 0);
-            c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[2], qh[2], c2, 0, 0, 0);
-            c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[3], qh[3], c3, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[2], qh[2], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[3], qh[3], c1, 0, 0, 0);
             c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[0], qh[4], c0, 0, 0, 0);
             c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[1], qh[5], c1, 0, 0, 0);
-            c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[2], qh[6], c2, 0, 0, 0);
-            c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[3], qh[7], c3, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[2], qh[6], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kb4[3], qh[7], c1, 0, 0, 0);
         }
-        sacc[kb] = (c0 + c1) + (c2 + c3);
+        sacc[kb] = c0 + c1;
         // Materialise the sum here: left alone, the optimiser sinks it to the softmax and keeps the
         // chain accumulators of the whole tile live.
         asm volatile("" : "+v"(sacc[kb]));
@@ -210,14 +212,25 @@ __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const fl
         const float ml = big ? 0.f : m_use * kLog2e;
         const float alpha = __builtin_amdgcn_exp2f(big ? (w.m - m_use) * kLog2e : w.ml - ml);
         float lsum = 0.f;
+        if (__ballot(big) == 0) {  // shift is 0 in every lane: x - shift == x
 #pragma unroll
-        for (int kb = 0; kb < NKB; kb++)
+            for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r] - shift, kLog2e, -ml));
-                sacc[kb][r] = e;
-                lsum += e;
-            }
+                for (int r = 0; r < 4; r++) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], kLog2e, -ml));
+                    sacc[kb][r] = e;
+                    lsum += e;
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r] - shift, kLog2e, -ml));
+                    sacc[kb][r] = e;
+                    lsum += e;
+                }
+        }
         w.ml = (big || m_new == kNegInf) ? kNegInf : ml;
         w.l = w.l * alpha + lsum;
         w.m = m_new;
