@@ -431,10 +431,12 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
     // and each workgroup walks the whole reduction; split it over workgroups instead (16-wide
     // steps), with the partial tiles summed in a fixed order by proj_reduce.
-    if (proj_split_bytes(p) > 0) {
+    if (const size_t part_bytes = proj_split_bytes(p); part_bytes > 0) {
         // The entry point that queues this product owns the partials' buffer (SplitWorkspace);
         // without one the product is refused rather than run unsplit, which would give other bits.
-        if (t_split_ws == nullptr) return hipErrorInvalidValue;
+        // The split rule keeps the partials within the buffer; a rule that did not is refused here,
+        // before any kernel could write past it.
+        if (t_split_ws == nullptr || part_bytes > kSplitWorkspaceBytes) return hipErrorInvalidValue;
         p.partial = t_split_ws;
     }
     const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
