@@ -120,14 +120,15 @@ def test_timestral_projection_matches_oracle(ta, orc, gpu_ready, gated):
 
 
 @pytest.mark.parametrize("nh,d_in,tokens", [(3, 96, 200), (1, 32, 5), (5, 160, 129), (12, 768, 1), (2, 48, 77), (1, 16, 3),
-                                           (8, 512, 528), (2, 256, 40), (3, 512, 16)])
+                                           (8, 512, 528), (2, 256, 40), (3, 512, 16), (8, 2048, 16), (1, 2048, 7)])
 def test_bolt_projection_odd_shapes(ta, orc, gpu_ready, nh, d_in, tokens):
     """No RoPE (Chronos-Bolt); d_in != heads * 64; column counts 3 * nh * 64 that end in half a
-    128-column tile; token counts that end in a partial 128-token tile. Four shapes have few
-    output tiles and a long reduction, so the three outputs are computed as split partials summed
-    by the reduce kernel: 1 token x 768 (6 splits), the Chronos-Bolt-small encoder's 528 tokens x
-    512 (4 splits), 40 tokens x 256 (2 splits), and 16 tokens x 512 into 576 columns (a last tile
-    of 64 columns: half its waves store no partials)."""
+    128-column tile; token counts that end in a partial 128-token tile. Two shapes have few output
+    tiles and a long reduction, so the three outputs are computed as split partials summed by the
+    reduce kernel: the Chronos-Bolt-small encoder's 528 tokens x 512 (4 splits) and 40 tokens x
+    256 (2 splits). At most 16 tokens take the 16-token kernel, whose sixteen waves split the
+    reduction inside one workgroup: 1, 3, 5, 7 and 16 tokens, d_in from 16 (one wave with work)
+    to 2048 (eight units per wave, the Chronos-Bolt-small decoder's second feed-forward product)."""
     inner = nh * 64
     rng = np.random.default_rng(nh * 7 + d_in + tokens)
     x = rng.standard_normal((tokens, d_in)).astype(np.float32)

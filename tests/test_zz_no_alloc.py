@@ -1,7 +1,7 @@
 """tsfm_qkv_project_noalloc: the projection entry point that allocates nothing (its split partial
 sums live in a fixed device array of the library), against tsfm_qkv_project on the same inputs,
 through the C ABI. Bit-identical outputs are required: both run the same kernels with the same
-split of the reduction. Two calls in a row (the second smaller) reuse the array; host pointers and
+split of the reduction (16 tokens or fewer: the 16-token kernel, no partials in the array). Two calls in a row (the second smaller) reuse the array; host pointers and
 products whose partials exceed the array are refused before anything is queued.
 """
 import ctypes

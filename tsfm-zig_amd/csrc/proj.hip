@@ -278,6 +278,19 @@ __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
+// The epilogue of four summed columns c .. c + 3 (of all n_out outputs side by side) of token m:
+// alpha, and with one output bias, ReLU or residual; f32 store into the output the columns
+// belong to (width is a multiple of 4, so a group never straddles two outputs).
+__device__ __forceinline__ void finish4(const ProjParams& p, int m, int c, f32x4 v) {
+    if (p.alpha != 1.f) v *= p.alpha;
+    const int sel = c / p.width, col = c - sel * p.width;
+    if (p.bias != nullptr) v = v + ld4(p.bias + col);
+    if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + col) + v;
+    else v = epi_act(p.epi, v);
+    float* const y = static_cast<float*>(sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3);
+    st4(y + out_offset(p, sel, m) + col, v);
+}
+
 // Sum of the split partials in split order (deterministic), then the epilogue: alpha, and with one
 // output bias, ReLU or residual; f32 store into the output the column belongs to. One thread per
 // four columns of a token (width is a multiple of 4, so a group never straddles two outputs).
@@ -288,13 +301,7 @@ __global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
     const int m = (int)(idx / q), c = (int)(idx % q) * 4;
     f32x4 v = ld4(p.partial + (int64_t)m * n_cols + c);
     for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + m) * n_cols + c);
-    if (p.alpha != 1.f) v *= p.alpha;
-    const int sel = c / p.width, col = c - sel * p.width;
-    if (p.bias != nullptr) v = v + ld4(p.bias + col);
-    if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)m * p.resid_tok + col) + v;
-    else v = epi_act(p.epi, v);
-    float* const y = static_cast<float*>(sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3);
-    st4(y + out_offset(p, sel, m) + col, v);
+    finish4(p, m, c, v);
 }
 
 // proj_reduce for one output followed by the row norm of the finished rows: one wave per token
@@ -320,6 +327,70 @@ __global__ __launch_bounds__(256) void proj_reduce_norm(ProjParams p) {
     const float inv = rms_inv(ss, W, p.norm_eps);
     float* const o = p.norm_out + (int64_t)row * p.norm_out_tok;
     for (int c = 4 * lane; c < W; c += 256) st4(o + c, rms_apply(ld4(y + c), inv, ld4(p.norm_scale + c)));
+}
+
+// Products of at most 16 tokens (the Chronos-Bolt decoder: one token per series), f32 outputs, no
+// RoPE. Such a product is a few MB of weights read once: it is bound by how many loads are in
+// flight, not by the matrix cores. A workgroup takes one 16-column tile of every token and its
+// sixteen waves split the reduction: wave w takes the 16-wide units [w U / 16, (w + 1) U / 16) of
+// U = d_in / 16 and issues the loads of up to SKB of them at once, straight from HBM/L2 into
+// registers in the matrix instruction's layout (lane l: row l & 15 of a 16-row block, indices
+// 4 (l >> 4) .. + 3 of the unit), then multiplies them, accumulating blockwise as qkv_proj does.
+// The sixteen 16 x 16 partials meet in LDS and are added in wave order, then the epilogue: one
+// launch where a split over workgroups would need a second one for the sums.
+constexpr int SKW = 16;  // waves of a workgroup
+constexpr int SKB = 8;   // units a wave has in flight
+constexpr int kSkinnyTokens = 16;
+constexpr size_t kSkinnyLds = (size_t)SKW * kSkinnyTokens * 16 * sizeof(float);
+__global__ __launch_bounds__(64 * SKW) void proj_skinny(ProjParams p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];  // [wave][token][16 columns]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n_cols = p.width * p.n_out, tn = blockIdx.x;
+    const int units = p.d_in / 16;
+    const int u0 = wave * units / SKW, u1 = (wave + 1) * units / SKW;
+    const int r = lane & 15, kq = 4 * (lane >> 4);
+    const float* const xr = p.x + (int64_t)min(r, p.tokens - 1) * p.x_tok + kq;
+    const float* wr;
+    {  // weight row of the lane's column (clamped past the last column)
+        const int n = min(tn * 16 + r, n_cols - 1);
+        const int sel = n / p.width;
+        const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
+        wr = w + (int64_t)(n - sel * p.width) * p.w_ld + kq;
+    }
+    f32x4 tot = {0.f, 0.f, 0.f, 0.f}, chk = tot;
+    int cu = 0;  // units done in the running chunk
+    for (int b0 = u0; b0 < u1; b0 += SKB) {
+        const int nb = min(SKB, u1 - b0);
+        f32x4 xs[SKB], ws[SKB];
+#pragma unroll
+        for (int i = 0; i < SKB; i++) {
+            if (i < nb) {
+                xs[i] = ld4(xr + 16 * (b0 + i));
+                ws[i] = ld4(wr + 16 * (b0 + i));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < SKB; i++) {
+            if (i >= nb) break;
+            chk = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[i][0], xs[i][0], cu == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : chk,
+                                                       0, 0, 0);
+#pragma unroll
+            for (int j = 1; j < 4; j++) chk = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[i][j], xs[i][j], chk, 0, 0, 0);
+            if (++cu == p.chunk || b0 + i == u1 - 1) {
+                tot += chk;
+                cu = 0;
+            }
+        }
+    }
+    // Lane l holds columns 4 (l >> 4) .. + 3 of token l & 15.
+    st4(smem + (wave * kSkinnyTokens + r) * 16 + kq, tot);
+    __syncthreads();
+    if (tid >= kSkinnyTokens * 4) return;
+    const int m = tid >> 2, c4 = 4 * (tid & 3), c = tn * 16 + c4;
+    if (m >= p.tokens || c >= n_cols) return;
+    f32x4 v = ld4(smem + m * 16 + c4);
+    for (int w = 1; w < SKW; w++) v = v + ld4(smem + (w * kSkinnyTokens + m) * 16 + c4);
+    finish4(p, m, c, v);
 }
 
 }  // namespace
@@ -389,6 +460,11 @@ static int proj_chunk(int units) {
     return c;
 }
 
+// Products the 16-token kernel takes (proj_skinny).
+static bool skinny(const ProjParams& p) {
+    return p.tokens <= kSkinnyTokens && p.rope_cos == nullptr && p.out_dtype == 0;
+}
+
 size_t proj_split_bytes(ProjParams& p) {
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
@@ -400,7 +476,8 @@ size_t proj_split_bytes(ProjParams& p) {
     // f32 outputs, no RoPE; several outputs only without an epilogue; at most half a launch of
     // tiles (four workgroups per CU), and at least 16 steps to share out.
     if (!((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 512 &&
-          steps >= 16))
+          steps >= 16) ||
+        skinny(p))
         return 0;
     int s = (int)std::min<int64_t>((1024 + blocks - 1) / blocks, std::min(steps / 8, 16));
     if (s < 2) return 0;
@@ -428,6 +505,16 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         return hipErrorInvalidValue;
     if ((int64_t)((p.tokens + BM - 1) / BM) * ((p.width * p.n_out + BN - 1) / BN) > 0x7fffffff)
         return hipErrorInvalidValue;
+    if (skinny(p)) {
+        p.chunk = proj_chunk((p.d_in / 16 + SKW - 1) / SKW);
+        hipLaunchKernelGGL(proj_skinny, dim3((unsigned)((p.width * p.n_out + 15) / 16)), dim3(64 * SKW), kSkinnyLds,
+                           stream, p);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess && p.norm_scale != nullptr)
+            e = launch_rms_norm(static_cast<const float*>(p.y0), p.y0_tok, p.norm_out, p.norm_out_tok, p.norm_scale,
+                                p.tokens, p.width, p.norm_eps, stream);
+        return e;
+    }
     // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
     // and each workgroup walks the whole reduction; split it over workgroups instead (16-wide
     // steps), with the partial tiles summed in a fixed order by proj_reduce.
