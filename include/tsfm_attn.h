@@ -233,8 +233,9 @@ int tsfm_qkv_project(const tsfm_proj_args *args);
  * Small products split their reduction over workgroups; their partial sums go to one 16 MiB array
  * in the library's device memory per GPU, shared by every call on that GPU and kept between
  * calls: calls that overlap on one GPU (other streams or threads) race and must be serialised by
- * the caller. A product whose partials need more than 16 MiB returns TSFM_E_UNSUPPORTED
- * (tsfm_qkv_project runs it). */
+ * the caller. The split rule keeps every product's partials within the array (at most two splits
+ * of 511 tiles of 64 x 64 floats: 16744448 bytes); a product that needed more would return
+ * TSFM_E_UNSUPPORTED. */
 int tsfm_qkv_project_noalloc(const tsfm_proj_args *args);
 
 /* ---------------------------------------------------------------------------------------------

@@ -479,13 +479,17 @@ size_t proj_split_bytes(ProjParams& p) {
           steps >= 16) ||
         skinny(p))
         return 0;
-    int s = (int)std::min<int64_t>((1024 + blocks - 1) / blocks, std::min(steps / 8, 16));
+    // About 512 workgroups (two per CU): more splits of these short reductions cost more in
+    // partial traffic and per-workgroup start-up than they gain in parallelism (measured on the
+    // Chronos-Bolt-small forecast: 1.160 ms for about 1024, 1.106 ms for about 512, 1.185 ms for
+    // at most two splits).
+    int s = (int)std::min<int64_t>((512 + blocks - 1) / blocks, std::min(steps / 8, 16));
     if (s < 2) return 0;
     const int per = (steps + s - 1) / s;
     s = (steps + per - 1) / per;
     p.splits = s;
     p.split_steps = per;
-    // s * blocks <= 1024 + blocks - 1 < 1536 and tokens * width <= blocks * BM * BN, so the partials
+    // s * blocks <= 512 + blocks - 1 < 1536 and tokens * width <= blocks * BM * BN, so the partials
     // always fit kSplitWorkspaceBytes.
     return (size_t)s * p.tokens * p.width * p.n_out * sizeof(float);
 }
