@@ -291,6 +291,22 @@ __device__ __forceinline__ void finish4(const ProjParams& p, int m, int c, f32x4
     st4(y + out_offset(p, sel, m) + col, v);
 }
 
+// The split partials of four columns (split s at at + s stride), summed in split order; the loads
+// of four splits at a time are issued before their adds.
+__device__ __forceinline__ f32x4 split_sum(const float* at, int64_t stride, int splits) {
+    f32x4 v = ld4(at);
+    for (int s = 1; s < splits; s += 4) {
+        f32x4 t[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (s + j < splits) t[j] = ld4(at + (s + j) * stride);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (s + j < splits) v = v + t[j];
+    }
+    return v;
+}
+
 // Sum of the split partials in split order (deterministic), then the epilogue: alpha, and with one
 // output bias, ReLU or residual; f32 store into the output the column belongs to. One thread per
 // four columns of a token (width is a multiple of 4, so a group never straddles two outputs).
@@ -299,33 +315,52 @@ __global__ __launch_bounds__(256) void proj_reduce(ProjParams p) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (int64_t)p.tokens * q) return;
     const int m = (int)(idx / q), c = (int)(idx % q) * 4;
-    f32x4 v = ld4(p.partial + (int64_t)m * n_cols + c);
-    for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + m) * n_cols + c);
-    finish4(p, m, c, v);
+    finish4(p, m, c, split_sum(p.partial + (int64_t)m * n_cols + c, (int64_t)p.tokens * n_cols, p.splits));
 }
 
 // proj_reduce for one output followed by the row norm of the finished rows: one wave per token
 // row sums the partials of its four-column groups in split order, applies the epilogue, stores
 // y0, and keeps the row's sum of squares; then norm_out = y0 * inv * norm_scale. The row norm's
 // grouping and order are rms_norm_rows', so the result has the same bits as the two launches.
+// Rows up to 256 KEEP wide stay in registers between the two passes.
 __global__ __launch_bounds__(256) void proj_reduce_norm(ProjParams p) {
+    constexpr int KEEP = 4;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= p.tokens) return;
     const int W = p.width;
     float* const y = static_cast<float*>(p.y0) + out_offset(p, 0, row);
-    float ss = 0.f;
-    for (int c = 4 * lane; c < W; c += 256) {
-        f32x4 v = ld4(p.partial + (int64_t)row * W + c);
-        for (int s = 1; s < p.splits; s++) v = v + ld4(p.partial + ((int64_t)s * p.tokens + row) * W + c);
+    const int64_t stride = (int64_t)p.tokens * W;
+    auto finish = [&](int c) {
+        f32x4 v = split_sum(p.partial + (int64_t)row * W + c, stride, p.splits);
         if (p.alpha != 1.f) v *= p.alpha;
         if (p.bias != nullptr) v = v + ld4(p.bias + c);
         if (p.epi == kEpiResidual) v = ld4(p.resid + (int64_t)row * p.resid_tok + c) + v;
         else v = epi_act(p.epi, v);
         st4(y + c, v);
-        ss = sumsq4(ss, v);
-    }
-    const float inv = rms_inv(ss, W, p.norm_eps);
+        return v;
+    };
+    float ss = 0.f;
     float* const o = p.norm_out + (int64_t)row * p.norm_out_tok;
+    if (W <= 256 * KEEP) {
+        f32x4 keep[KEEP];
+#pragma unroll
+        for (int i = 0; i < KEEP; i++) {
+            const int c = 4 * lane + 256 * i;
+            if (c < W) {
+                keep[i] = finish(c);
+                ss = sumsq4(ss, keep[i]);
+            }
+        }
+        const float inv = rms_inv(ss, W, p.norm_eps);
+#pragma unroll
+        for (int i = 0; i < KEEP; i++) {
+            const int c = 4 * lane + 256 * i;
+            if (c < W) st4(o + c, rms_apply(keep[i], inv, ld4(p.norm_scale + c)));
+        }
+        return;
+    }
+    for (int c = 4 * lane; c < W; c += 256) ss = sumsq4(ss, finish(c));
+    const float inv = rms_inv(ss, W, p.norm_eps);
     for (int c = 4 * lane; c < W; c += 256) st4(o + c, rms_apply(ld4(y + c), inv, ld4(p.norm_scale + c)));
 }
 
