@@ -125,10 +125,11 @@ def test_bolt_projection_odd_shapes(ta, orc, gpu_ready, nh, d_in, tokens):
     """No RoPE (Chronos-Bolt); d_in != heads * 64; column counts 3 * nh * 64 that end in half a
     128-column tile; token counts that end in a partial 128-token tile. Two shapes have few output
     tiles and a long reduction, so the three outputs are computed as split partials summed by the
-    reduce kernel: the Chronos-Bolt-small encoder's 528 tokens x 512 (4 splits) and 40 tokens x
-    256 (2 splits). At most 16 tokens take the 16-token kernel, whose sixteen waves split the
-    reduction inside one workgroup: 1, 3, 5, 7 and 16 tokens, d_in from 16 (one wave with work)
-    to 2048 (eight units per wave, the Chronos-Bolt-small decoder's second feed-forward product)."""
+    reduce kernel: the Chronos-Bolt-small encoder's 528 tokens x 512, 40 tokens x 256, and 16 or 7
+    tokens over d_in 2048 (the Chronos-Bolt-small decoder's second feed-forward product). Other
+    products of at most 16 tokens take the 16-token kernel, whose sixteen waves split the
+    reduction inside one workgroup: 1, 3, 5 and 16 tokens, d_in from 16 (one wave with work) to
+    768."""
     inner = nh * 64
     rng = np.random.default_rng(nh * 7 + d_in + tokens)
     x = rng.standard_normal((tokens, d_in)).astype(np.float32)

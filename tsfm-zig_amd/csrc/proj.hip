@@ -376,6 +376,10 @@ __global__ __launch_bounds__(256) void proj_reduce_norm(ProjParams p) {
 constexpr int SKW = 16;  // waves of a workgroup
 constexpr int SKB = 8;   // units a wave has in flight
 constexpr int kSkinnyTokens = 16;
+// Longer reductions read more weight bytes per column tile than the few CUs of a 16-token launch
+// (one per 64 columns) pull in time; they split over workgroups instead (measured at d_in 2048:
+// 13 us in one launch, 7 + 4 us split and summed).
+constexpr int kSkinnyMaxIn = 1024;
 constexpr size_t kSkinnyLds = (size_t)SKW * kSkinnyTokens * 16 * sizeof(float);
 __global__ __launch_bounds__(64 * SKW) void proj_skinny(ProjParams p) {
     extern __shared__ __attribute__((aligned(16))) float smem[];  // [wave][token][16 columns]
@@ -497,7 +501,7 @@ static int proj_chunk(int units) {
 
 // Products the 16-token kernel takes (proj_skinny).
 static bool skinny(const ProjParams& p) {
-    return p.tokens <= kSkinnyTokens && p.rope_cos == nullptr && p.out_dtype == 0;
+    return p.tokens <= kSkinnyTokens && p.d_in <= kSkinnyMaxIn && p.rope_cos == nullptr && p.out_dtype == 0;
 }
 
 size_t proj_split_bytes(ProjParams& p) {
