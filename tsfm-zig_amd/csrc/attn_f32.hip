@@ -702,8 +702,31 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     f32x4 klo[RKIT], khi[RKIT], kcs[RKIT], ksn[RKIT];
     f32x4 v01[RVIT], v23[RVIT];
     uint32_t kvb = 1;
+    // T5 table entry tid of an item: the bucket of its relative index does not depend on the item,
+    // so it is read once here; the item's head picks the table value, loaded with the item's other
+    // operands. (Tables longer than the workgroup are filled in stage_store instead.)
+    const int n_lut = p.n_q + p.n_k - 1 + 2 * kLutPad;
+    const bool lut_in_regs = BIAS == BIAS_REL && n_lut <= RNT;
+    int lut_bucket = -1;
+    float lut_val = 0.f;
+    if (lut_in_regs && tid < n_lut) {
+        const int t = min(max(tid - kLutPad, 0), p.n_q + p.n_k - 2);
+        lut_bucket = min(max(p.rel_bucket[t], 0), p.rel_buckets - 1);
+    }
     f32x4 qa[4];  // the next item's raw q (dims 8g..8g+7, 32+8g..32+8g+7 of query wq0 + ql)
     auto stage_load = [&](const Item& I) {
+        // q, the table value and the key_valid byte first, unconditionally (a row past n_q reads
+        // the last row and is zeroed at the store): no register they land in waits on the K/V
+        // loads issued after them.
+        {
+            const float* src = I.Q + (int64_t)min(I.wq0 + ql, p.n_q - 1) * p.q_tok;
+            qa[0] = ld4(src + 8 * g);
+            qa[1] = ld4(src + 8 * g + 4);
+            qa[2] = ld4(src + 32 + 8 * g);
+            qa[3] = ld4(src + 32 + 8 * g + 4);
+        }
+        if (lut_bucket >= 0) lut_val = p.rel_table[lut_bucket * p.H + I.h];
+        if (mask_reads_valid<MASK>() && tid < lay.nkp) kvb = __builtin_amdgcn_raw_buffer_load_b8(I.kv_rsrc, tid, 0, 0);
 #pragma unroll
         for (int u = 0; u < RKIT; u++) {  // K item = (row, c): dims 4c..4c+3 and 32+4c..32+4c+3
             const int it = tid + u * RNT, row = it >> 3, c = it & 7;
@@ -724,16 +747,6 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             const f32x2 c = bld2(I.v_buf, off + 2 * step), d = bld2(I.v_buf, off + 3 * step);
             v01[u] = f32x4{a[0], a[1], bb[0], bb[1]};
             v23[u] = f32x4{c[0], c[1], d[0], d[1]};
-        }
-        if (mask_reads_valid<MASK>() && tid < lay.nkp) kvb = __builtin_amdgcn_raw_buffer_load_b8(I.kv_rsrc, tid, 0, 0);
-        const int qi = I.wq0 + ql;
-        qa[0] = qa[1] = qa[2] = qa[3] = f32x4{0, 0, 0, 0};
-        if (qi < p.n_q) {
-            const float* src = I.Q + (int64_t)qi * p.q_tok;
-            qa[0] = ld4(src + 8 * g);
-            qa[1] = ld4(src + 8 * g + 4);
-            qa[2] = ld4(src + 32 + 8 * g);
-            qa[3] = ld4(src + 32 + 8 * g + 4);
         }
     };
     // The staged item into buffer `buf`, and the wave's QBlock for it (q rotated and scaled as
@@ -758,8 +771,13 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             st4(vd + vslot(2 * vc + 1) * 4, f32x4{v01[u][1], v01[u][3], v23[u][1], v23[u][3]});
         }
         if (tid < lay.nkp) buf[lay.a_off + tid] = key_term<MASK>(tid, p.n_k, kvb != 0, p.ctx_keys);
-        if (BIAS == BIAS_REL) fill_rel_lut(buf + lay.l_off, p, I.h, tid, RNT);
+        if (lut_in_regs) {
+            if (lut_bucket >= 0) buf[lay.l_off + tid] = lut_val;
+        } else if (BIAS == BIAS_REL) {
+            fill_rel_lut(buf + lay.l_off, p, I.h, tid, RNT);
+        }
         const int qi = I.wq0 + ql;
+        if (qi >= p.n_q) qa[0] = qa[1] = qa[2] = qa[3] = f32x4{0, 0, 0, 0};
         if (ROPE && qi < p.n_q) {
             const int64_t row = (int64_t)(p.q_pos0 + qi) * 32;
             rope4(qa[0], qa[2], ld4(I.RC + row + 8 * g), ld4(I.RS + row + 8 * g));
@@ -845,7 +863,10 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         compute(cur, cb, w);
         if (!more) break;
         stage_store(next, smem + ((k + 1) & 1) * lay.total, w);
-        __syncthreads();
+        // LDS-only barrier: the next item's LDS writes are complete and visible, and every wave has
+        // left the buffer the item after it will overwrite. No global access crosses it, so it
+        // does not wait for this item's O stores (a __syncthreads() fence would, once per item).
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         cur = next;
         it = nxt;
     }
