@@ -20,7 +20,9 @@
  *     and promises no partial output. Nothing here aborts the process;
  *   - the caller owns every buffer it passes; the library never frees caller memory;
  *   - the library is thread-safe: device set-up runs once (pthread_once), and each host thread
- *     gets its own HIP stream and device staging buffers, released when the thread exits;
+ *     gets its own HIP stream and device staging buffers, released when the thread exits; the
+ *     device-pointer model calls keep their scratch per (thread, stream, entry point) between
+ *     calls, released the same way;
  *   - results do not depend on how many host threads call in, nor on batch composition: there
  *     are no atomics in any reduction and tile order is fixed.
  *

@@ -107,6 +107,16 @@ struct ThreadCtx {
         float* buf;
     };
     std::vector<SplitBuf> splits;
+    // Scratch buffers of this thread's device-pointer entry points (scratch_acquire), one per
+    // (device, caller stream, entry point).
+    struct ScratchBuf {
+        int device;
+        hipStream_t stream;
+        int slot;
+        char* buf;
+        size_t cap;
+    };
+    std::vector<ScratchBuf> scratch;
 };
 
 constexpr size_t kMaxSplitBufs = 8;  // per thread; more streams take a stream-ordered buffer per call
@@ -122,6 +132,10 @@ void destroy_ctx(void* ptr) {
     // hipFree waits for the device's queued work, so a product still queued on a caller's stream
     // has finished with its partials before they are released.
     for (const ThreadCtx::SplitBuf& b : c->splits) {
+        (void)hipSetDevice(b.device);
+        (void)hipFree(b.buf);
+    }
+    for (const ThreadCtx::ScratchBuf& b : c->scratch) {
         (void)hipSetDevice(b.device);
         (void)hipFree(b.buf);
     }
@@ -181,6 +195,65 @@ hipError_t split_buf_for(ThreadCtx* c, hipStream_t stream, float** out, bool* ow
     *out = static_cast<float*>(buf);
     return hipSuccess;
 }
+
+constexpr size_t kMaxScratchBufs = 16;  // per thread; more take a stream-ordered allocation per call
+
+}  // namespace
+
+namespace tsfm {
+namespace abi {
+
+// Scratch for an entry point's device work queued on `stream` by this thread: a buffer kept per
+// (device, stream, slot) and grown as needed (slot: one per entry point, so that nested calls
+// never share one), so that a caller that repeats a call does not pay a stream-ordered allocation
+// and release each time (about 30 us of host time per pair). Stream order makes reuse by the
+// thread's next call on the same stream safe; another thread has buffers of its own. Growing waits
+// for the stream, then replaces the buffer. Past kMaxScratchBufs buffers (or without a thread
+// context) it returns a stream-ordered allocation that the caller releases with hipFreeAsync after
+// queuing (*owned).
+hipError_t scratch_acquire(hipStream_t stream, int slot, size_t bytes, char** out, bool* owned) {
+    *owned = false;
+    *out = nullptr;
+    bytes = std::max<size_t>(bytes, 256);
+    ThreadCtx* c = thread_ctx();
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    if (c != nullptr) {
+        for (ThreadCtx::ScratchBuf& b : c->scratch)
+            if (b.device == device && b.stream == stream && b.slot == slot) {
+                if (b.cap < bytes) {
+                    if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+                    (void)hipFree(b.buf);
+                    b.buf = nullptr;
+                    b.cap = 0;
+                    void* next = nullptr;
+                    if ((e = hipMalloc(&next, bytes)) != hipSuccess) return e;
+                    b.buf = static_cast<char*>(next);
+                    b.cap = bytes;
+                }
+                *out = b.buf;
+                return hipSuccess;
+            }
+        if (c->scratch.size() < kMaxScratchBufs) {
+            void* buf = nullptr;
+            if ((e = hipMalloc(&buf, bytes)) != hipSuccess) return e;
+            c->scratch.push_back({device, stream, slot, static_cast<char*>(buf), bytes});
+            *out = static_cast<char*>(buf);
+            return hipSuccess;
+        }
+    }
+    void* buf = nullptr;
+    if ((e = hipMallocAsync(&buf, bytes, stream)) != hipSuccess) return e;
+    *out = static_cast<char*>(buf);
+    *owned = true;
+    return hipSuccess;
+}
+
+}  // namespace abi
+}  // namespace tsfm
+
+namespace {
 
 
 size_t elem_size(int dtype) { return dtype == TSFM_DTYPE_F32 ? 4 : 2; }
@@ -841,15 +914,17 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
         }
         if (!ok) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
         hipStream_t s = static_cast<hipStream_t>(a->stream);
-        void* scratch = nullptr;
-        if ((e = hipMallocAsync(&scratch, scratch_n + tsfm::kSplitWorkspaceBytes, s)) != hipSuccess)
+        char* scratch = nullptr;
+        bool owned = false;
+        if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotEncode, scratch_n + tsfm::kSplitWorkspaceBytes, &scratch,
+                                            &owned)) != hipSuccess)
             return hip_fail(e, "encoder scratch allocation");
         {
-            tsfm::SplitWorkspace ws(reinterpret_cast<float*>(static_cast<char*>(scratch) + scratch_n));
+            tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + scratch_n));
             e = encode_on(a, a->x, a->key_valid, a->rope_cos, a->rope_sin, a->layers, a->final_norm,
-                          static_cast<float*>(scratch), s);
+                          reinterpret_cast<float*>(scratch), s);
         }
-        const hipError_t f = hipFreeAsync(scratch, s);
+        const hipError_t f = owned ? hipFreeAsync(scratch, s) : hipSuccess;
         if (e != hipSuccess) return hip_fail(e, "encoder launch");
         if (f != hipSuccess) return hip_fail(f, "encoder scratch release");
         return TSFM_OK;
@@ -1034,14 +1109,15 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
         const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), emb_at = plan.take(emb_n), h_at = plan.take(h_n),
                      r_at = plan.take(r_n), enc_at = plan.take(enc_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
         char* scratch = nullptr;
-        if ((e = hipMallocAsync(reinterpret_cast<void**>(&scratch), plan.off, s)) != hipSuccess)
+        bool owned = false;
+        if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotChronos2Forward, plan.off, &scratch, &owned)) != hipSuccess)
             return hip_fail(e, "forward scratch allocation");
         tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + part_at));
         e = forward_on(a, enc, a->feats, a->fut_feats, a->ctx_valid, a->reg, a->raw,
                        reinterpret_cast<float*>(scratch + x_at), reinterpret_cast<uint8_t*>(scratch + kv_at),
                        reinterpret_cast<float*>(scratch + emb_at), reinterpret_cast<float*>(scratch + h_at),
                        reinterpret_cast<float*>(scratch + r_at), reinterpret_cast<float*>(scratch + enc_at), s);
-        const hipError_t f = hipFreeAsync(scratch, s);
+        const hipError_t f = owned ? hipFreeAsync(scratch, s) : hipSuccess;
         if (e != hipSuccess) return hip_fail(e, "forward launch");
         if (f != hipSuccess) return hip_fail(f, "forward scratch release");
         return TSFM_OK;
@@ -1312,7 +1388,8 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
         if ((e = cached_bucket_ids(buckets, seq, a->rel_buckets, a->rel_max_distance, &ids)) != hipSuccess)
             return hip_fail(e, "bucket id upload");
         char* scratch = nullptr;
-        if ((e = hipMallocAsync(reinterpret_cast<void**>(&scratch), plan.off, s)) != hipSuccess)
+        bool owned = false;
+        if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotBoltForward, plan.off, &scratch, &owned)) != hipSuccess)
             return hip_fail(e, "forward scratch allocation");
         BoltDev dv{a->feats, a->reg, a->dec_start, a->rel_table, a->enc_final_norm, a->dec_final_norm,
                    a->patch_valid, ids, a->enc_layers, a->dec_layers, a->input_embed, a->output_embed, a->raw};
@@ -1320,7 +1397,7 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
             tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + part_at));
             e = bolt_forward_on(a, dv, scratch, at, s);
         }
-        const hipError_t f = hipFreeAsync(scratch, s);
+        const hipError_t f = owned ? hipFreeAsync(scratch, s) : hipSuccess;
         if (e != hipSuccess) return hip_fail(e, "forward launch");
         if (f != hipSuccess) return hip_fail(f, "forward scratch release");
         return TSFM_OK;
@@ -1422,8 +1499,9 @@ int tsfm_bolt_forecast(const tsfm_bolt_forecast_args* a) {
     const size_t f_at = plan.take((size_t)(nb * n_patch * 2 * a->patch) * 4), pv_at = plan.take((size_t)(nb * n_patch));
     const size_t lo_at = plan.take((size_t)nb * 4), sc_at = plan.take((size_t)nb * 4), raw_at = plan.take((size_t)(nb * per) * 4);
     char* buf = nullptr;
+    bool owned = false;
     hipError_t e;
-    if ((e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off, s)) != hipSuccess)
+    if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotBoltForecast, plan.off, &buf, &owned)) != hipSuccess)
         return hip_fail(e, "forecast scratch allocation");
     float* feats = reinterpret_cast<float*>(buf + f_at);
     uint8_t* pv = reinterpret_cast<uint8_t*>(buf + pv_at);
@@ -1438,12 +1516,12 @@ int tsfm_bolt_forecast(const tsfm_bolt_forecast_args* a) {
         m.keys_all_valid = 0;  // validity is only known on the device: the additive mask, exact either way
         rc = tsfm_bolt_forward(&m);
         if (rc != TSFM_OK) {
-            (void)hipFreeAsync(buf, s);
+            if (owned) (void)hipFreeAsync(buf, s);
             return rc;
         }
         e = tsfm::launch_bolt_finish(raw, lo, sc, a->out, (int)nb, (int)per, s);
     }
-    const hipError_t f = hipFreeAsync(buf, s);
+    const hipError_t f = owned ? hipFreeAsync(buf, s) : hipSuccess;
     if (e != hipSuccess) return hip_fail(e, "forecast launch");
     if (f != hipSuccess) return hip_fail(f, "forecast scratch release");
     return TSFM_OK;
@@ -1475,8 +1553,9 @@ int tsfm_chronos2_forecast(const tsfm_chronos2_forecast_args* a) {
     const size_t cv_at = plan.take((size_t)(nb * n_ctx)), lo_at = plan.take((size_t)nb * 4);
     const size_t sc_at = plan.take((size_t)nb * 4), raw_at = plan.take((size_t)(nb * n_out * per) * 4);
     char* buf = nullptr;
+    bool owned = false;
     hipError_t e;
-    if ((e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off, s)) != hipSuccess)
+    if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotChronos2Forecast, plan.off, &buf, &owned)) != hipSuccess)
         return hip_fail(e, "forecast scratch allocation");
     float* feats = reinterpret_cast<float*>(buf + f_at);
     float* fut = reinterpret_cast<float*>(buf + ff_at);
@@ -1492,13 +1571,13 @@ int tsfm_chronos2_forecast(const tsfm_chronos2_forecast_args* a) {
         m.enc.keys_all_valid = 0;  // validity is only known on the device: the additive mask, exact either way
         rc = tsfm_chronos2_forward(&m);
         if (rc != TSFM_OK) {
-            (void)hipFreeAsync(buf, s);
+            if (owned) (void)hipFreeAsync(buf, s);
             return rc;
         }
         e = tsfm::launch_chronos2_finish(raw, lo, sc, a->out, (int)nb, n_out, per / ps, ps, a->horizon,
                                          a->arcsinh ? 1 : 0, s);
     }
-    const hipError_t f = hipFreeAsync(buf, s);
+    const hipError_t f = owned ? hipFreeAsync(buf, s) : hipSuccess;
     if (e != hipSuccess) return hip_fail(e, "forecast launch");
     if (f != hipSuccess) return hip_fail(f, "forecast scratch release");
     return TSFM_OK;

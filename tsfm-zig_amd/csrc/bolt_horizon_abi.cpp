@@ -50,7 +50,8 @@ extern "C" int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args* a) {
     const size_t cur_at1 = plan.take(more ? (size_t)rows * a->context_length * 4 : 0);
     const size_t raw_at = plan.take(more ? (size_t)(rows * q * P) * 4 : 0);
     char* buf = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off, s);
+    bool owned = false;
+    hipError_t e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotBoltHorizon, plan.off, &buf, &owned);
     if (e != hipSuccess) return hip_fail(e, "forecast scratch allocation");
     float* pred = reinterpret_cast<float*>(buf + pred_at);
     float* cur[2] = {reinterpret_cast<float*>(buf + cur_at0), reinterpret_cast<float*>(buf + cur_at1)};
@@ -88,7 +89,7 @@ extern "C" int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args* a) {
             which ^= 1;
         }
     }
-    const hipError_t f = hipFreeAsync(buf, s);
+    const hipError_t f = owned ? hipFreeAsync(buf, s) : hipSuccess;
     if (rc != TSFM_OK) return rc;
     if (e != hipSuccess) return hip_fail(e, "forecast launch");
     if (f != hipSuccess) return hip_fail(f, "forecast scratch release");

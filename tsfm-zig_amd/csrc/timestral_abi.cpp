@@ -165,7 +165,8 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     const size_t at_mir = plan.take((size_t)R * a->horizon * q * 4);
     const size_t at_part = plan.take(tsfm::kSplitWorkspaceBytes);
     char* buf = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off, s);
+    bool owned = false;
+    hipError_t e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotTimestralForecast, plan.off, &buf, &owned);
     if (e != hipSuccess) return hip_fail(e, "forecast scratch allocation");
     auto F = [&](size_t at) { return reinterpret_cast<float*>(buf + at); };
     auto U8 = [&](size_t at) { return reinterpret_cast<uint8_t*>(buf + at); };
@@ -359,7 +360,7 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                                      a->symmetric_averaging ? 1 : 0, a->clip_nonnegative ? 1 : 0, s);
     };
     e = run();
-    const hipError_t f = hipFreeAsync(buf, s);
+    const hipError_t f = owned ? hipFreeAsync(buf, s) : hipSuccess;
     if (e != hipSuccess) return hip_fail(e, "Timestral forecast launch");
     if (f != hipSuccess) return hip_fail(f, "forecast scratch release");
     return TSFM_OK;
