@@ -76,6 +76,7 @@ enum { TSFM_DTYPE_F32 = 0, TSFM_DTYPE_BF16 = 1, TSFM_DTYPE_F16 = 2 };
 
 /* flags */
 #define TSFM_ATTN_DEVICE_PTRS 1u /* every pointer is device memory; the call is asynchronous on `stream` */
+#define TSFM_TIMESTRAL_BF16_ATTN 2u /* tsfm_timestral_forecast: time attention in bf16 (see there) */
 
 /* One batched attention call: o = softmax(mask(scale * q k^T + bias)) v for every (b, h).
  * Replaces: selfAttendRuntime per item (src/core/attn.zig:99-117) inside the forRange calls listed
@@ -444,7 +445,13 @@ int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args *args);
  * attending over the time-attention K/V the earlier blocks computed (the reference re-encodes the
  * whole context every block; the result is the same computation, up to f32 summation order);
  * blocks after a max_context drop, and every block of a batch that holds a series with no
- * observation, re-encode in full. */
+ * observation, re-encode in full.
+ * With TSFM_TIMESTRAL_BF16_ATTN in flags the time attention runs on the bf16 matrix cores: the q/k/v
+ * projections are rounded once to bf16 (after RoPE) into a bf16 K/V cache, the attention keeps f32
+ * scores, softmax and accumulation, and its output is rounded to bf16 and widened back to f32 for
+ * the gate and the out projection. Everything else stays f32. The reference has no such mode (its
+ * time attention is f32); a bf16 forecast agrees with the f32 one to about 1e-2 of the forecast's
+ * scale. */
 typedef struct tsfm_timestral_attn {
     int32_t is_time;        /* 1: time attention (timeAttention :487-519); 0: variate (:525-544) */
     const float *norm;      /* (d) attn_norms.<i>.scale */
@@ -486,7 +493,7 @@ typedef struct tsfm_timestral_forecast_args {
     float extreme_value_threshold;  /* Options.extreme_value_threshold (1e30) */
     int32_t symmetric_averaging, clip_nonnegative;  /* Options (both on in the reference) */
     int32_t kv_cache;               /* non-zero: decode over cached K/V (see above) */
-    uint32_t flags;                 /* TSFM_ATTN_DEVICE_PTRS */
+    uint32_t flags;                 /* TSFM_ATTN_DEVICE_PTRS, optionally | TSFM_TIMESTRAL_BF16_ATTN */
     float *out;                     /* (batch, variates, horizon, n_quantiles) */
     void *stream;
 } tsfm_timestral_forecast_args;

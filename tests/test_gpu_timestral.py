@@ -87,6 +87,31 @@ def test_timestral_cached_decode_equals_reencoding(ta, gpu_ready):
     assert _ref.scaled_err(cached, full) < 2e-5
 
 
+@pytest.mark.parametrize("kv_cache", [True, False])
+def test_timestral_bf16_time_attention(ta, orc16, gpu_ready, kv_cache):
+    """TSFM_TIMESTRAL_BF16_ATTN: the time attention on the bf16 matrix cores over a bf16 K/V cache
+    (q/k/v rounded once after RoPE, f32 softmax and accumulation, the output rounded once),
+    everything else f32. Against the 16-lane oracle's f32 re-encoding forecast, scaled by
+    max(|forecast|, 1): within 1e-2, the half-precision bar (measured about 5e-4). The model has
+    use_asinh off: with it on, the head's outputs are sinh-expanded, so a random-init head's large
+    outputs turn bf16's 2^-9 relative rounding into a few per cent of the forecast (measured
+    2.5e-2 to 5e-2 for these weights) -- the bf16 rounding itself, not the decode. Cached and
+    re-encoded bf16 decoding give the same forecast."""
+    _, x, obs = _case(15, b=2, v=2)
+    m = _ref.timestral_model(np.random.default_rng(5), d=128, nh=2, hid=256, use_asinh=False)
+    b, v, horizon = 2, 2, 40
+    want = _oracle(orc16, m, x, obs, b, v, horizon, per_shot=4)
+    got = _gpu(ta, m, x, obs, b, v, horizon, per_shot=4, kv_cache=kv_cache, attn_bf16=True)
+    assert np.isfinite(got).all()
+    err = _ref.scaled_err(got, want)
+    assert err < 1e-2, err
+    f32 = _gpu(ta, m, x, obs, b, v, horizon, per_shot=4, kv_cache=kv_cache)
+    assert _ref.scaled_err(f32, want) < err  # the bf16 rounding is what moves the forecast
+    if kv_cache:
+        full = _gpu(ta, m, x, obs, b, v, horizon, per_shot=4, kv_cache=False, attn_bf16=True)
+        assert _ref.scaled_err(got, full) < 2e-5
+
+
 def test_timestral_series_without_observation(ta, orc, orc16, gpu_ready):
     """A series with no observation at all: its RoPE origin moves once the medians are fed back, so
     the device re-encodes every block; it still matches the oracle."""
@@ -115,5 +140,7 @@ def test_timestral_forecast_argument_errors(ta, gpu_ready):
     import ctypes
 
     assert ta.load().tsfm_timestral_forecast(ctypes.byref(args)) == ta.E_UNSUPPORTED
+    args.flags = ta.DEVICE_PTRS | 8  # no such flag
+    assert ta.load().tsfm_timestral_forecast(ctypes.byref(args)) == ta.E_INVALID
     torch.cuda.synchronize()
     assert (out == 0).all()

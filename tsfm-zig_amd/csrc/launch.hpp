@@ -184,6 +184,8 @@ hipError_t launch_ts_rope_tables(const int* row_first, int groups, int vall, int
 hipError_t launch_ts_assemble(const float* emb, const float* query, float* x, int rows, int m, int h, int d,
                               hipStream_t s);
 hipError_t launch_ts_mul_sigmoid(float* o, const float* g, int64_t n, hipStream_t s);
+// o = f32(oh) for n bf16 elements (n % 4 == 0), then o / (1 + exp(-g)) when g is given.
+hipError_t launch_ts_from_bf16(const uint16_t* oh, const float* g, float* o, int64_t n, hipStream_t s);
 hipError_t launch_ts_mul_silu(const float* hbuf, float* a, int64_t tokens, int hid, hipStream_t s);
 hipError_t launch_ts_head_finish(const float* raw, const float* loc, const float* scale, int cap_p, int l, int rows,
                                  int h, const TsHead& hp, float* qs, hipStream_t s);

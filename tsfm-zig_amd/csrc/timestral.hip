@@ -215,6 +215,23 @@ __global__ void ts_mul_sigmoid(float* o, const float* g, int64_t n4) {
                            x[3] / (1.f + expf(-gv[3]))});
 }
 
+// The bf16 time-attention output widened to the f32 buffer the out projection reads, with the
+// sigmoid gate of timeAttention (model.zig:517, nn.mulSigmoid) applied as in ts_mul_sigmoid when g is
+// given.
+__global__ void ts_from_bf16(const uint16_t* oh, const float* g, float* o, int64_t n4) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n4) return;
+    const u32x2 w = *reinterpret_cast<const u32x2*>(oh + 4 * idx);
+    f32x4 x = {__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), __uint_as_float(w[1] << 16),
+               __uint_as_float(w[1] & 0xffff0000u)};
+    if (g != nullptr) {
+        const f32x4 gv = ld4(g + 4 * idx);
+        x = f32x4{x[0] / (1.f + expf(-gv[0])), x[1] / (1.f + expf(-gv[1])), x[2] / (1.f + expf(-gv[2])),
+                  x[3] / (1.f + expf(-gv[3]))};
+    }
+    st4(o + 4 * idx, x);
+}
+
 // MlpAct.run (model.zig:40-46) with nn.mulSilu (src/core/nn.zig:410-420): a[t, i] = gate * silu(up)
 // with gate = h[t, i], up = h[t, hid + i].
 __global__ void ts_mul_silu(const float* hbuf, float* a, int64_t tokens, int hid) {
@@ -477,6 +494,11 @@ hipError_t launch_ts_assemble(const float* emb, const float* query, float* x, in
 
 hipError_t launch_ts_mul_sigmoid(float* o, const float* g, int64_t n, hipStream_t s) {
     hipLaunchKernelGGL(ts_mul_sigmoid, dim3(blocks_for(n / 4, 256)), dim3(256), 0, s, o, g, n / 4);
+    return hipGetLastError();
+}
+
+hipError_t launch_ts_from_bf16(const uint16_t* oh, const float* g, float* o, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(ts_from_bf16, dim3(blocks_for(n / 4, 256)), dim3(256), 0, s, oh, g, o, n / 4);
     return hipGetLastError();
 }
 

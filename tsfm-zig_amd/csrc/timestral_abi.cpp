@@ -80,6 +80,7 @@ int check_resblock(const tsfm_resblock& rb, int in, int out, bool biases, const 
 extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     const tsfm_timestral_model& M = a->model;
+    if (a->flags & ~(TSFM_ATTN_DEVICE_PTRS | TSFM_TIMESTRAL_BF16_ATTN)) return fail(TSFM_E_INVALID, "unknown flags");
     if (!(a->flags & TSFM_ATTN_DEVICE_PTRS))
         return fail(TSFM_E_UNSUPPORTED, "the Timestral forecast runs on device memory only (TSFM_ATTN_DEVICE_PTRS)");
     if (a->batch < 0 || a->variates <= 0 || a->len <= 0 || a->horizon <= 0)
@@ -193,6 +194,10 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     for (int i = median + 1; i < q; i++) hp.widths[i] = (float)(M.quantile_knots[i] - M.quantile_knots[i - 1]);
     for (int i = 0; i < median; i++) hp.widths[i] = (float)(M.quantile_knots[i + 1] - M.quantile_knots[i]);
     const float sm_scale = 1.0f / std::sqrt(64.0f);
+    // bf16 time attention: the layer caches hold bf16 q/k/v (the same buffers, half used), and the
+    // attention output goes to VQ as bf16 (VQ serves only the variate layers otherwise).
+    const bool half = (a->flags & TSFM_TIMESTRAL_BF16_ATTN) != 0;
+    uint16_t* OH = reinterpret_cast<uint16_t*>(VQ);
 
     float* const out = a->out;
     const float cap_k = a->quantile_real_cap_k;
@@ -265,30 +270,48 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                         // q/k/v of the block's tokens into the layer's cache at token p0, RoPE'd with
                         // the rows p0.. of each group's table (timeAttention :493-513).
                         float* T = F(at_cache[(size_t)ti++]);
+                        uint16_t* Th = reinterpret_cast<uint16_t*>(T);
+                        auto el = [&](int64_t e) -> void* { return half ? (void*)(Th + e) : (void*)(T + e); };
                         const int64_t tb = (int64_t)cap_tok * 3 * d;
-                        pp.y0 = T + (int64_t)p0 * 3 * d; pp.y1 = T + (int64_t)p0 * 3 * d + d;
-                        pp.y2 = T + (int64_t)p0 * 3 * d + 2 * d;
+                        pp.y0 = el((int64_t)p0 * 3 * d); pp.y1 = el((int64_t)p0 * 3 * d + d);
+                        pp.y2 = el((int64_t)p0 * 3 * d + 2 * d);
+                        if (half) {  // q/k/v rounded to bf16; the gate stays f32 (its own product)
+                            pp.out_dtype = TSFM_DTYPE_BF16; pp.n_out = 3; pp.w3 = nullptr; pp.y3 = nullptr;
+                        }
                         pp.y0_tok = pp.y1_tok = pp.y2_tok = 3 * d;
                         pp.y0_batch = pp.y1_batch = pp.y2_batch = tb;
                         pp.rope_cos = cos_t + (int64_t)p0 * 32; pp.rope_sin = sin_t + (int64_t)p0 * 32;
                         pp.rope_table_stride = (int64_t)cap_tok * 32; pp.rope_rows_per_table = V; pp.rope_row0 = 0;
                         if ((e2 = tsfm::launch_proj(pp, s)) != hipSuccess) return e2;
+                        if (half && at.gate &&
+                            (e2 = linear(XN, d, at.gate, d, d, nullptr, G, d, toks, tsfm::kEpiNone, nullptr, s)) !=
+                                hipSuccess)
+                            return e2;
+                        auto attend = [&](const tsfm::Params& q, int msk) {
+                            return half ? tsfm::launch_attn_half(q, true, msk, tsfm::BIAS_NONE, false, s)
+                                        : tsfm::launch_attn_f32(q, msk, tsfm::BIAS_NONE, false, s);
+                        };
                         // TimeJob.attend (:580-635): encoder queries causal over the valid keys, then
                         // the decoder queries over the valid context keys and their own chain.
                         tsfm::Params ap{};
-                        ap.q = T + (int64_t)p0 * 3 * d; ap.k = T + d; ap.v = T + 2 * d; ap.o = OA;
+                        ap.q = el((int64_t)p0 * 3 * d); ap.k = el(d); ap.v = el(2 * d);
+                        ap.o = half ? (void*)OH : (void*)OA;
                         ap.q_tok = ap.k_tok = ap.v_tok = 3 * d; ap.q_batch = ap.k_batch = ap.v_batch = tb;
                         ap.o_tok = d; ap.o_batch = (int64_t)sl * d;
                         ap.key_valid = kv; ap.kv_batch = cap_p;
                         ap.B = rows; ap.H = nh; ap.n_q = m; ap.n_k = ne; ap.q_pos0 = p0; ap.scale = sm_scale;
-                        if ((e2 = tsfm::launch_attn_f32(ap, TSFM_MASK_CAUSAL_KEYS, tsfm::BIAS_NONE, false, s)) != hipSuccess)
-                            return e2;
-                        ap.q = T + (int64_t)ne * 3 * d; ap.o = OA + (int64_t)m * d;
+                        if ((e2 = attend(ap, TSFM_MASK_CAUSAL_KEYS)) != hipSuccess) return e2;
+                        ap.q = el((int64_t)ne * 3 * d);
+                        ap.o = half ? (void*)(OH + (int64_t)m * d) : (void*)(OA + (int64_t)m * d);
                         ap.n_q = h; ap.n_k = ne + h; ap.q_pos0 = ne; ap.ctx_keys = ne; ap.chain_start = ne;
-                        if ((e2 = tsfm::launch_attn_f32(ap, TSFM_MASK_DECODER, tsfm::BIAS_NONE, false, s)) != hipSuccess)
+                        if ((e2 = attend(ap, TSFM_MASK_DECODER)) != hipSuccess) return e2;
+                        if (half) {
+                            if ((e2 = tsfm::launch_ts_from_bf16(OH, at.gate ? G : nullptr, OA, (int64_t)toks * d, s)) !=
+                                hipSuccess)
+                                return e2;
+                        } else if (at.gate && (e2 = tsfm::launch_ts_mul_sigmoid(OA, G, (int64_t)toks * d, s)) != hipSuccess) {
                             return e2;
-                        if (at.gate && (e2 = tsfm::launch_ts_mul_sigmoid(OA, G, (int64_t)toks * d, s)) != hipSuccess)
-                            return e2;
+                        }
                     } else {
                         // variateAttention (:525-544): the block's token slots only, gate fused.
                         pp.y0 = VQ; pp.y1 = VQ + d; pp.y2 = VQ + 2 * d;

@@ -48,6 +48,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 
 DEVICE_PTRS = 1
+TIMESTRAL_BF16_ATTN = 2  # tsfm_timestral_forecast: time attention in bf16
 
 # Every symbol include/tsfm_attn.h declares.
 EXPORTS = (
@@ -1141,11 +1142,12 @@ class KvCache:
 def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, variates: int, length: int, horizon: int,
                             max_context: int = 0, per_shot: int = 32, cap_k: float = 1e4, extreme: float = 1e30,
                             symmetric: bool = True, clip_nonnegative: bool = True, kv_cache: bool = True,
-                            stream=None) -> "TimestralForecastArgs":
+                            attn_bf16: bool = False, stream=None) -> "TimestralForecastArgs":
     """``tsfm_timestral_forecast_args`` over device tensors. `model` holds the config and device
     weights (keys as in the reference checkpoint's layout: patch_proj/head ResBlocks, layers with
     attns [is_time, norm, qkv (permuted), out, gate] and mlp_norm/w12/w3, forecast_query, out_norm,
-    knots (host float64 array)). The returned block keeps references to what it points at."""
+    knots (host float64 array)). attn_bf16 sets TSFM_TIMESTRAL_BF16_ATTN (time attention on the bf16
+    matrix cores over a bf16 K/V cache). The returned block keeps references to what it points at."""
     import numpy as np
 
     layers = (TimestralLayer * max(1, len(model["layers"])))()
@@ -1168,7 +1170,8 @@ def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, vari
                               len=length, horizon=horizon, max_context=max_context, per_shot_patches=per_shot,
                               quantile_real_cap_k=cap_k, extreme_value_threshold=extreme,
                               symmetric_averaging=int(symmetric), clip_nonnegative=int(clip_nonnegative),
-                              kv_cache=int(kv_cache), flags=DEVICE_PTRS, out=_ptr(out), stream=_stream_of(out, stream))
+                              kv_cache=int(kv_cache), flags=DEVICE_PTRS | (TIMESTRAL_BF16_ATTN if attn_bf16 else 0),
+                              out=_ptr(out), stream=_stream_of(out, stream))
     a._keep = (layers, knots, model, inputs, observed, out)
     return a
 
