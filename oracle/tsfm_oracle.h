@@ -253,12 +253,25 @@ typedef struct orc_timestral_model {
  * rows = groups * vall; out (rows, h * ps, q) quantiles in data units. */
 void orc_timestral_predict_block(size_t threads, float *out, const orc_timestral_model *m, const float *ctx,
                                  const uint8_t *obs, size_t t, size_t groups, size_t vall, size_t h);
+/* Model.predictBlock with covariates: roles (vall) in model.Role order (0 target, 1 past, 2 known;
+ * NULL = all targets), kf/kfm (rows, h * ps) known futures (NULL = blanks); out (groups * targets,
+ * h * ps, q). */
+void orc_timestral_predict_block_cov(size_t threads, float *out, const orc_timestral_model *m, const float *ctx,
+                                     const uint8_t *obs, size_t t, size_t groups, size_t vall, size_t h,
+                                     const uint8_t *roles, const float *kf, const uint8_t *kfm);
 /* refineBlock (src/timestral/forecaster.zig:582-662) with every row a target: qs (rows, h ps, q) in place. */
 void orc_timestral_refine_block(float *qs, const orc_timestral_model *m, const float *ctx, const uint8_t *obs,
                                 size_t rows, size_t t, size_t h);
 /* forecaster.forecast (src/timestral/forecaster.zig:57-180, forecastRaw :303-421, blockDecode :423-563)
  * without covariates: inputs/observed (b, v, t), out (b, v, horizon, q). max_context 0 = the model's
  * context_length. Returns 0, 1 (a NaN forecast: error.DegenerateInput) or 2 (asymmetric levels). */
+/* forecaster.forecast with numeric covariates: past (b, n_past, t), known (b, n_known, t + horizon),
+ * NaN = missing; the mirrored pass negates every covariate row. */
+int orc_timestral_forecast_cov(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
+                               const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon,
+                               const float *past, size_t n_past, const float *known, size_t n_known,
+                               size_t max_context, size_t per_shot, float cap_k, float extreme, int symmetric,
+                               int clip_nonnegative);
 int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
                            const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon, size_t max_context,
                            size_t per_shot, float cap_k, float extreme, int symmetric, int clip_nonnegative);

@@ -136,10 +136,11 @@ void orc_timestral_patch_stats(size_t threads, float *loc, float *scale, const f
 /* inv_freq of Model.load (src/timestral/model.zig:180-188), applied in runTransformer's tables
  * (:447-463) through orc_timestral_rope_tables. */
 
-/* runTransformer (src/timestral/model.zig:434-482) for rows of targets: x (rows, sl, d) in place. */
+/* runTransformer (src/timestral/model.zig:434-482): x (rows, sl, d) in place; roles (vall) in model.Role
+ * order (0 target, 1 past, 2 known), cov = any row not a target (Geo.cov). */
 static void run_transformer(size_t threads, float *x, const orc_timestral_model *m, size_t rows, size_t vall,
                             size_t ne, size_t l, size_t h, const uint8_t *key_valid, int keys_all_valid,
-                            const size_t *first_obs) {
+                            const size_t *first_obs, const uint8_t *roles, int cov) {
     const size_t d = m->d, hid = m->hid, hd = m->hd, nh = m->nh, sl = ne + h, groups = rows / vall;
     const float eps = m->norm_eps;
     float *xn = (float *)malloc(rows * sl * d * sizeof(float));
@@ -152,7 +153,8 @@ static void run_transformer(size_t threads, float *x, const orc_timestral_model 
     float *cos_t = (float *)malloc(groups * sl * (hd / 2) * sizeof(float));
     float *sin_t = (float *)malloc(groups * sl * (hd / 2) * sizeof(float));
     orc_timestral_rope_tables(cos_t, sin_t, groups, ne, l, h, hd, m->rope_dim, m->rope_theta, first_obs);
-    uint8_t *target_roles = (uint8_t *)calloc(vall + 1, 1);
+    uint8_t *bidir = (uint8_t *)calloc(rows + 1, 1); /* TimeJob.attend :600: known rows read every valid key */
+    for (size_t r = 0; r < rows; r++) bidir[r] = cov && roles[r % vall] == 2;
     for (size_t li = 0; li < m->n_layers; li++) {
         const orc_timestral_layer *ly = &m->layers[li];
         for (int ai = 0; ai < ly->n_attn; ai++) {
@@ -163,11 +165,11 @@ static void run_transformer(size_t threads, float *x, const orc_timestral_model 
             if (a->is_time) {
                 /* timeAttention (:487-519): rope, attend per (row, head), gate, out */
                 orc_timestral_rope(threads, qkv, cos_t, sin_t, rows, sl, vall, d, nh, hd);
-                orc_timestral_time_attention(threads, qkv, oa, key_valid, keys_all_valid, NULL, rows, ne, l, h, d,
+                orc_timestral_time_attention(threads, qkv, oa, key_valid, keys_all_valid, bidir, rows, ne, l, h, d,
                                              nh, hd);
             } else {
-                /* variateAttention (:525-544), no covariates */
-                orc_timestral_variate_attention(threads, qkv, oa, key_valid, target_roles, 0, groups, vall, ne, h, d,
+                /* variateAttention (:525-544), with the covariate firewalls when cov */
+                orc_timestral_variate_attention(threads, qkv, oa, key_valid, roles, cov, groups, vall, ne, h, d,
                                                 nh, hd);
             }
             if (a->gate) orc_mul_sigmoid(oa, oa, gate, rows * sl * d);
@@ -182,36 +184,88 @@ static void run_transformer(size_t threads, float *x, const orc_timestral_model 
         orc_add_in_place(x, delta, rows * sl * d);
     }
     free(xn); free(delta); free(mlp_h); free(mlp_a); free(qkv); free(oa); free(gate); free(cos_t); free(sin_t);
-    free(target_roles);
+    free(bidir);
 }
 
-/* Model.predictBlock (src/timestral/model.zig:220-432), every row a target (cov = false): ctx and
- * obs (rows, t), rows = groups * vall; out (rows, h * ps, q) quantiles in data units. loc_out and
- * scale_out, when given, receive the (rows, t / ps) patch statistics. */
-void orc_timestral_predict_block(size_t threads, float *out, const orc_timestral_model *m, const float *ctx,
-                                 const uint8_t *obs, size_t t, size_t groups, size_t vall, size_t h) {
-    const size_t ps = m->ps, d = m->d, q = m->q, rows = groups * vall, l = t / ps, hl = h * ps, n = l, w = t;
+/* Model.predictBlock (src/timestral/model.zig:220-432): ctx/obs (rows, t), rows = groups * vall,
+ * roles (vall) in model.Role order (0 target, 1 past, 2 known; NULL = every row a target); kf/kfm
+ * (rows, h * ps) the known-future values and observations (NULL = blanks). out (groups * n_tgt,
+ * h * ps, q): quantiles in data units of the target rows, series by series. */
+void orc_timestral_predict_block_cov(size_t threads, float *out, const orc_timestral_model *m, const float *ctx,
+                                     const uint8_t *obs, size_t t, size_t groups, size_t vall, size_t h,
+                                     const uint8_t *roles_in, const float *kf, const uint8_t *kfm) {
+    const size_t ps = m->ps, d = m->d, q = m->q, rows = groups * vall, l = t / ps, hl = h * ps;
+    uint8_t *roles = (uint8_t *)calloc(vall + 1, 1);
+    int cov = 0;
+    size_t n_tgt = 0;
+    for (size_t i = 0; i < vall; i++) {
+        roles[i] = roles_in ? roles_in[i] : 0;
+        cov = cov || roles[i] != 0;
+        n_tgt += roles[i] == 0;
+    }
+    /* The window (:253-273): the context, plus (with covariates) the horizon blanks / known futures. */
+    const size_t w = cov ? t + hl : t, n = w / ps;
+    float *full = (float *)malloc(rows * w * sizeof(float) + 1);
+    uint8_t *full_obs = (uint8_t *)malloc(rows * w + 1);
+    for (size_t r = 0; r < rows; r++) {
+        memcpy(full + r * w, ctx + r * t, t * sizeof(float));
+        memcpy(full_obs + r * w, obs + r * t, t);
+        for (size_t j = t; j < w; j++) {
+            full[r * w + j] = kf ? kf[r * hl + j - t] : 0.0f;
+            full_obs[r * w + j] = kf ? (kfm[r * hl + j - t] != 0) : 0;
+        }
+    }
     float *loc = (float *)malloc(rows * n * sizeof(float) + 1);
     float *scale = (float *)malloc(rows * n * sizeof(float) + 1);
-    orc_timestral_patch_stats(threads, loc, scale, ctx, obs, rows, w, ps, m->minimum_scale);
+    orc_timestral_patch_stats(threads, loc, scale, full, full_obs, rows, w, ps, m->minimum_scale);
     const float eps32 = 1.1920929e-07f; /* std.math.floatEps(f32) */
     float *emb_in = (float *)malloc(rows * n * 2 * ps * sizeof(float) + 1);
-    for (size_t r = 0; r < rows; r++)
+    for (size_t r = 0; r < rows; r++) {
+        const int known = cov && roles[r % vall] == 2;
+        /* Known-future rows: whole-window f32 statistics; 0/1 indicator rows skip the asinh (:285-310). */
+        float kloc = 0, kscale = 1;
+        int binary = 0;
+        if (known) {
+            float cnt = 0, sum = 0;
+            int zero_one = 1, any = 0;
+            for (size_t i = 0; i < w; i++)
+                if (full_obs[r * w + i]) {
+                    const float xv = full[r * w + i];
+                    cnt += 1;
+                    sum += xv;
+                    zero_one = zero_one && (xv == 0 || xv == 1);
+                    any = 1;
+                }
+            kloc = sum / fmaxf(cnt, 1.0f);
+            float ss = 0;
+            for (size_t i = 0; i < w; i++)
+                if (full_obs[r * w + i]) {
+                    const float dv = full[r * w + i] - kloc;
+                    ss += dv * dv;
+                }
+            kscale = fmaxf(sqrtf(ss / fmaxf(cnt, 1.0f)), (float)m->minimum_scale);
+            binary = zero_one && any;
+            if (binary) {
+                kloc = 0;
+                kscale = 1;
+            }
+        }
         for (size_t p = 0; p < n; p++) {
-            const float lo = loc[r * n + p];
-            const float sc = fmaxf(scale[r * n + p], eps32);
+            const float lo = known ? kloc : loc[r * n + p];
+            const float sc = fmaxf(known ? kscale : scale[r * n + p], eps32);
             float *dst = emb_in + (r * n + p) * 2 * ps;
             for (size_t i = 0; i < ps; i++) {
-                const int ob = obs[r * w + p * ps + i] != 0;
+                const int ob = full_obs[r * w + p * ps + i] != 0;
                 float v = 0;
                 if (ob) {
-                    v = (ctx[r * w + p * ps + i] - lo) / sc;
-                    if (m->use_asinh) v = asinhf(v);
+                    v = (full[r * w + p * ps + i] - lo) / sc;
+                    if (m->use_asinh && !(known && binary)) v = asinhf(v);
                 }
                 dst[i] = v;
                 dst[ps + i] = ob ? 0.0f : 1.0f;
             }
         }
+    }
     const size_t ne = n, sl = ne + h;
     float *x = (float *)malloc(rows * sl * d * sizeof(float));
     float *enc = (float *)malloc(rows * ne * d * sizeof(float) + 1);
@@ -222,25 +276,33 @@ void orc_timestral_predict_block(size_t threads, float *out, const orc_timestral
     }
     uint8_t *key_valid = (uint8_t *)malloc(rows * ne + 1);
     size_t *first_obs = (size_t *)malloc(groups * sizeof(size_t) + 1);
-    const int all_valid = orc_timestral_key_valid(key_valid, first_obs, obs, rows, vall, ne, ps, m->attend_missing);
-    run_transformer(threads, x, m, rows, vall, ne, l, h, key_valid, all_valid, first_obs);
+    const int all_valid =
+        orc_timestral_key_valid(key_valid, first_obs, full_obs, rows, vall, ne, ps, m->attend_missing);
+    run_transformer(threads, x, m, rows, vall, ne, l, h, key_valid, all_valid, first_obs, roles, cov);
 
-    /* Head on the decoder tokens of every (target) row. */
-    float *dec = (float *)malloc(rows * h * d * sizeof(float));
-    for (size_t r = 0; r < rows; r++)
-        orc_rms_norm(threads, dec + r * h * d, x + (r * sl + ne) * d, h, d, m->out_norm, m->norm_eps);
-    float *raw = (float *)malloc(rows * hl * q * sizeof(float));
-    orc_resblock_silu(threads, raw, dec, rows * h, &m->head);
+    /* Head on the target rows' decoder tokens (:380-391). */
+    const size_t n_out = groups * n_tgt;
+    float *dec = (float *)malloc(n_out * h * d * sizeof(float) + 1);
+    size_t *out_row = (size_t *)malloc(n_out * sizeof(size_t) + 1);
+    for (size_t r = 0, oi = 0; r < rows; r++) {
+        if (roles[r % vall] != 0) continue;
+        orc_rms_norm(threads, dec + oi * h * d, x + (r * sl + ne) * d, h, d, m->out_norm, m->norm_eps);
+        out_row[oi++] = r;
+    }
+    float *raw = (float *)malloc(n_out * hl * q * sizeof(float) + 1);
+    orc_resblock_silu(threads, raw, dec, n_out * h, &m->head);
     const size_t med = m->median;
     float *widths = (float *)calloc(q, sizeof(float));
     for (size_t i = med + 1; i < q; i++) widths[i] = (float)(m->knots[i] - m->knots[i - 1]);
     for (size_t i = 0; i < med; i++) widths[i] = (float)(m->knots[i + 1] - m->knots[i]);
     const float wf = m->quantile_width_factor, big = 3.40282347e38f;
-    for (size_t r = 0; r < rows; r++) {
+    for (size_t oi = 0; oi < n_out; oi++) {
+        const size_t r = out_row[oi];
+        /* Anchor frame: the last context patch (patch l - 1 of the window). */
         const float lo = loc[r * n + l - 1], sc = scale[r * n + l - 1];
         for (size_t s = 0; s < hl; s++) {
-            const float *rv = raw + (r * hl + s) * q;
-            float *ov = out + (r * hl + s) * q;
+            const float *rv = raw + (oi * hl + s) * q;
+            float *ov = out + (oi * hl + s) * q;
             const float mv = rv[med];
             float acc = 0;
             for (size_t i = med + 1; i < q; i++) {
@@ -264,8 +326,14 @@ void orc_timestral_predict_block(size_t threads, float *out, const orc_timestral
             orc_clamp_nonfinite(ov, q);
         }
     }
-    free(loc); free(scale); free(emb_in); free(x); free(enc); free(key_valid); free(first_obs); free(dec); free(raw);
-    free(widths);
+    free(roles); free(full); free(full_obs); free(loc); free(scale); free(emb_in); free(x); free(enc);
+    free(key_valid); free(first_obs); free(dec); free(out_row); free(raw); free(widths);
+}
+
+/* Model.predictBlock with every row a target (cov = false): out (rows, h * ps, q). */
+void orc_timestral_predict_block(size_t threads, float *out, const orc_timestral_model *m, const float *ctx,
+                                 const uint8_t *obs, size_t t, size_t groups, size_t vall, size_t h) {
+    orc_timestral_predict_block_cov(threads, out, m, ctx, obs, t, groups, vall, h, NULL, NULL, NULL);
 }
 
 /* ---- forecaster ------------------------------------------------------------------------------ */
@@ -349,12 +417,15 @@ void orc_timestral_refine_block(float *qs, const orc_timestral_model *m, const f
     free(loc); free(scale); free(sinh_med); free(loc_j); free(scale_j);
 }
 
-/* blockDecode (src/timestral/forecaster.zig:423-563), every row a target: rows/mask (nrows, t_in)
- * padded context, out (nrows, horizon, q). Re-encodes the whole grown context every block. */
+/* blockDecode (src/timestral/forecaster.zig:423-563): rows/mask (groups * vall, t_in) padded context,
+ * roles (vall) with the v target rows first, kf/kfm (groups * vall, hpad) known futures or NULL; out
+ * (groups * v, horizon, q). Re-encodes the whole grown context every block. Feedback: targets carry
+ * their median, known covariates their real future, past-only covariates a blank. */
 static void block_decode(size_t threads, float *out, const orc_timestral_model *m, const float *rows_in,
-                         const uint8_t *mask_in, size_t groups, size_t vall, size_t t_in, size_t horizon,
+                         const uint8_t *mask_in, size_t groups, size_t vall, const uint8_t *roles, size_t v,
+                         const float *kf, const uint8_t *kfm, size_t hpad, size_t t_in, size_t horizon,
                          size_t max_context, size_t per_shot, float extreme) {
-    const size_t ps = m->ps, q = m->q, med = m->median, nrows = groups * vall;
+    const size_t ps = m->ps, q = m->q, med = m->median, nrows = groups * vall, nt = groups * v;
     size_t t = t_in;
     float *ctx = (float *)malloc(nrows * t * sizeof(float) + 1);
     uint8_t *cmask = (uint8_t *)malloc(nrows * t + 1);
@@ -363,10 +434,25 @@ static void block_decode(size_t threads, float *out, const orc_timestral_model *
     size_t remaining = (horizon + ps - 1) / ps, done = 0;
     while (remaining > 0) {
         const size_t block = per_shot < remaining ? per_shot : remaining, blen = block * ps;
-        float *qs = (float *)malloc(nrows * blen * q * sizeof(float));
-        orc_timestral_predict_block(threads, qs, m, ctx, cmask, t, groups, vall, block);
-        if (block > 1) orc_timestral_refine_block(qs, m, ctx, cmask, nrows, t, block);
-        for (size_t r = 0; r < nrows; r++)
+        float *qs = (float *)malloc(nt * blen * q * sizeof(float));
+        float *kfb = NULL;
+        uint8_t *kfmb = NULL;
+        if (kf) {
+            kfb = (float *)malloc(nrows * blen * sizeof(float));
+            kfmb = (uint8_t *)malloc(nrows * blen);
+            for (size_t r = 0; r < nrows; r++) {
+                memcpy(kfb + r * blen, kf + r * hpad + done, blen * sizeof(float));
+                memcpy(kfmb + r * blen, kfm + r * hpad + done, blen);
+            }
+        }
+        orc_timestral_predict_block_cov(threads, qs, m, ctx, cmask, t, groups, vall, block, roles, kfb, kfmb);
+        if (block > 1) /* refineBlock (:582-662) on the target rows g * vall + i, i < v */
+            for (size_t g = 0; g < groups; g++)
+                for (size_t i = 0; i < v; i++) {
+                    const size_t r = g * vall + i;
+                    orc_timestral_refine_block(qs + (g * v + i) * blen * q, m, ctx + r * t, cmask + r * t, 1, t, block);
+                }
+        for (size_t r = 0; r < nt; r++)
             for (size_t s = 0; s < blen; s++) {
                 if (done + s >= horizon) break;
                 memcpy(out + (r * horizon + done + s) * q, qs + (r * blen + s) * q, q * sizeof(float));
@@ -374,7 +460,7 @@ static void block_decode(size_t threads, float *out, const orc_timestral_model *
         remaining -= block;
         done += blen;
         if (remaining == 0) {
-            free(qs);
+            free(qs); free(kfb); free(kfmb);
             break;
         }
         const size_t nt_len = t + blen;
@@ -383,22 +469,33 @@ static void block_decode(size_t threads, float *out, const orc_timestral_model *
         float *nctx = (float *)malloc(nrows * keep_t * sizeof(float));
         uint8_t *nmask = (uint8_t *)malloc(nrows * keep_t);
         const size_t start = nt_len - keep_t, ncopy = start < t ? t - start : 0, s0 = start < t ? 0 : start - t;
-        for (size_t r = 0; r < nrows; r++) {
-            if (ncopy > 0) {
-                memcpy(nctx + r * keep_t, ctx + r * t + start, ncopy * sizeof(float));
-                memcpy(nmask + r * keep_t, cmask + r * t + start, ncopy);
-            }
-            for (size_t s = s0; s < s0 + (keep_t - ncopy); s++) {
-                const size_t j = s - s0 + ncopy;
-                float mv = qs[(r * blen + s) * q + med];
-                if (!isfinite(mv) || fabsf(mv) >= extreme) mv = 0;
-                nctx[r * keep_t + j] = mv;
-                nmask[r * keep_t + j] = 1;
+        for (size_t g = 0; g < groups; g++) {
+            size_t ti = 0;
+            for (size_t i = 0; i < vall; i++) {
+                const size_t r = g * vall + i, trow = g * v + ti;
+                if (ncopy > 0) {
+                    memcpy(nctx + r * keep_t, ctx + r * t + start, ncopy * sizeof(float));
+                    memcpy(nmask + r * keep_t, cmask + r * t + start, ncopy);
+                }
+                for (size_t s = s0; s < s0 + (keep_t - ncopy); s++) {
+                    const size_t j = s - s0 + ncopy;
+                    if (roles[i] == 0) {
+                        float mv = qs[(trow * blen + s) * q + med];
+                        if (!isfinite(mv) || fabsf(mv) >= extreme) mv = 0;
+                        nctx[r * keep_t + j] = mv;
+                        nmask[r * keep_t + j] = 1;
+                    } else if (roles[i] == 2) {
+                        nctx[r * keep_t + j] = kfb[r * blen + s];
+                        nmask[r * keep_t + j] = kfmb[r * blen + s];
+                    } else {
+                        nctx[r * keep_t + j] = 0;
+                        nmask[r * keep_t + j] = 0;
+                    }
+                }
+                if (roles[i] == 0) ti++;
             }
         }
-        free(ctx);
-        free(cmask);
-        free(qs);
+        free(ctx); free(cmask); free(qs); free(kfb); free(kfmb);
         ctx = nctx;
         cmask = nmask;
         t = keep_t;
@@ -407,64 +504,96 @@ static void block_decode(size_t threads, float *out, const orc_timestral_model *
     free(cmask);
 }
 
-/* forecastRaw (src/timestral/forecaster.zig:303-421), no covariates: inputs/observed (b, v, t0);
- * out (b, v, horizon, q). Returns 0, or 1 for a NaN forecast (error.DegenerateInput). */
+/* forecastRaw (src/timestral/forecaster.zig:303-421): inputs/observed (b, v, t0); past (b, n_past,
+ * t0) and known (b, n_known, t0 + horizon) covariates, NaN = missing, either may be NULL with a
+ * count of 0; out (b, v, horizon, q). Returns 0, or 1 for a NaN forecast (error.DegenerateInput). */
 static int forecast_raw(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
-                        const uint8_t *observed, size_t b, size_t v, size_t t0, size_t horizon, size_t max_context,
-                        size_t per_shot, float cap_k, float extreme) {
-    const size_t ps = m->ps, q = m->q, nrows = b * v;
+                        const uint8_t *observed, size_t b, size_t v, size_t t0, size_t horizon, const float *past,
+                        size_t n_past, const float *known, size_t n_known, size_t max_context, size_t per_shot,
+                        float cap_k, float extreme) {
+    const size_t ps = m->ps, q = m->q, vall = v + n_past + n_known, nrows = b * vall;
+    uint8_t *roles = (uint8_t *)malloc(vall + 1);
+    for (size_t i = 0; i < vall; i++) roles[i] = i < v ? 0 : i < v + n_past ? 1 : 2;
     const size_t keep = t0 < max_context ? t0 : max_context, t = (keep + ps - 1) / ps * ps;
+    const size_t hpad = (horizon + ps - 1) / ps * ps;
     float *rows = (float *)calloc(nrows * t + 1, sizeof(float));
     uint8_t *mask = (uint8_t *)calloc(nrows * t + 1, 1);
-    for (size_t r = 0; r < nrows; r++) {
-        float last = 0;
-        int seen = 0;
-        for (size_t j = 0; j < t0; j++) {
-            const size_t idx = r * t0 + j;
-            if (observed[idx]) {
-                last = inputs[idx];
-                seen = 1;
+    float *kf = (float *)calloc(nrows * hpad + 1, sizeof(float));
+    uint8_t *kfm = (uint8_t *)calloc(nrows * hpad + 1, 1);
+    for (size_t s = 0; s < b; s++)
+        for (size_t i = 0; i < vall; i++) {
+            const size_t r = s * vall + i;
+            float last = 0;
+            int seen = 0;
+            for (size_t j = 0; j < t0; j++) {
+                float val;
+                int ob;
+                if (roles[i] == 0) { /* forward-fill the target; leading gaps stay 0 */
+                    const size_t idx = (s * v + i) * t0 + j;
+                    if (observed[idx]) {
+                        last = inputs[idx];
+                        seen = 1;
+                    }
+                    val = seen ? last : 0;
+                    ob = observed[idx] != 0;
+                } else {
+                    const float xv = roles[i] == 1 ? past[(s * n_past + (i - v)) * t0 + j]
+                                                   : known[(s * n_known + (i - v - n_past)) * (t0 + horizon) + j];
+                    ob = !isnan(xv);
+                    val = ob ? xv : 0;
+                }
+                if (j >= t0 - keep) {
+                    const size_t dst = r * t + (t - keep) + (j - (t0 - keep));
+                    rows[dst] = val;
+                    mask[dst] = (uint8_t)ob;
+                }
             }
-            if (j >= t0 - keep) {
-                const size_t dst = r * t + (t - keep) + (j - (t0 - keep));
-                rows[dst] = seen ? last : 0;
-                mask[dst] = observed[idx] ? 1 : 0;
-            }
+            if (roles[i] == 2)
+                for (size_t j = 0; j < horizon; j++) {
+                    const float xv = known[(s * n_known + (i - v - n_past)) * (t0 + horizon) + t0 + j];
+                    kfm[r * hpad + j] = !isnan(xv);
+                    kf[r * hpad + j] = isnan(xv) ? 0 : xv;
+                }
         }
-    }
-    block_decode(threads, out, m, rows, mask, b, v, t, horizon, max_context, per_shot, extreme);
+    block_decode(threads, out, m, rows, mask, b, vall, roles, v, n_known ? kf : NULL, n_known ? kfm : NULL, hpad, t,
+                 horizon, max_context, per_shot, extreme);
     if (cap_k > 0) {
         const size_t n = t / ps;
         float *loc = (float *)malloc(n * sizeof(float) + 1), *scale = (float *)malloc(n * sizeof(float) + 1);
-        for (size_t r = 0; r < nrows; r++) {
-            orc_timestral_patch_stats(1, loc, scale, rows + r * t, mask + r * t, 1, t, ps, m->minimum_scale);
-            float mx = -INFINITY, mn = INFINITY;
-            for (size_t j = 0; j < t; j++)
-                if (mask[r * t + j]) {
-                    mx = rows[r * t + j] > mx ? rows[r * t + j] : mx;
-                    mn = rows[r * t + j] < mn ? rows[r * t + j] : mn;
-                }
-            if (isinf(mx)) mx = 0;
-            if (isinf(mn)) mn = 0;
-            const float a = scale[n - 1] * cap_k, lo = mn - a, hi = mx + a;
-            for (size_t i = 0; i < horizon * q; i++)  /* std.math.clamp: @max(lo, @min(x, hi)) */
-                out[r * horizon * q + i] = fmaxf(lo, fminf(out[r * horizon * q + i], hi));
-        }
+        for (size_t s = 0; s < b; s++)
+            for (size_t i = 0; i < v; i++) {
+                const size_t r = s * vall + i, o = s * v + i;
+                orc_timestral_patch_stats(1, loc, scale, rows + r * t, mask + r * t, 1, t, ps, m->minimum_scale);
+                float mx = -INFINITY, mn = INFINITY;
+                for (size_t j = 0; j < t; j++)
+                    if (mask[r * t + j]) {
+                        mx = rows[r * t + j] > mx ? rows[r * t + j] : mx;
+                        mn = rows[r * t + j] < mn ? rows[r * t + j] : mn;
+                    }
+                if (isinf(mx)) mx = 0;
+                if (isinf(mn)) mn = 0;
+                const float a = scale[n - 1] * cap_k, lo = mn - a, hi = mx + a;
+                for (size_t k = 0; k < horizon * q; k++)  /* std.math.clamp: @max(lo, @min(x, hi)) */
+                    out[o * horizon * q + k] = fmaxf(lo, fminf(out[o * horizon * q + k], hi));
+            }
         free(loc);
         free(scale);
     }
-    free(rows);
-    free(mask);
-    for (size_t i = 0; i < nrows * horizon * q; i++)
+    free(rows); free(mask); free(kf); free(kfm); free(roles);
+    for (size_t i = 0; i < b * v * horizon * q; i++)
         if (isnan(out[i])) return 1;
     return 0;
 }
 
-/* forecaster.forecast + finish (src/timestral/forecaster.zig:57-180), no covariates. Returns 0, 1
- * (a NaN forecast) or 2 (asymmetric quantile levels with symmetric averaging). */
-int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
-                           const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon, size_t max_context,
-                           size_t per_shot, float cap_k, float extreme, int symmetric, int clip_nonnegative) {
+/* forecaster.forecast + finish (src/timestral/forecaster.zig:57-180) with numeric covariates (past
+ * (b, n_past, t), known (b, n_known, t + horizon), NaN = missing). Returns 0, 1 (a NaN forecast) or 2
+ * (asymmetric quantile levels with symmetric averaging). The mirrored pass negates the context and
+ * every covariate row (:112-121). */
+int orc_timestral_forecast_cov(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
+                               const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon,
+                               const float *past, size_t n_past, const float *known, size_t n_known,
+                               size_t max_context, size_t per_shot, float cap_k, float extreme, int symmetric,
+                               int clip_nonnegative) {
     const size_t q = m->q;
     if (max_context == 0) max_context = m->context_length;
     if (per_shot > m->block_size) per_shot = m->block_size;
@@ -474,10 +603,17 @@ int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model
             if (fabs(m->knots[i] + m->knots[q - 1 - i] - 1.0) > 1e-9) return 2;
         float *neg = (float *)malloc(b * v * t * sizeof(float) + 1);
         for (size_t i = 0; i < b * v * t; i++) neg[i] = -inputs[i];
+        float *negp = (float *)malloc(b * n_past * t * sizeof(float) + 1);
+        float *negk = (float *)malloc(b * n_known * (t + horizon) * sizeof(float) + 1);
+        for (size_t i = 0; i < b * n_past * t; i++) negp[i] = -past[i];
+        for (size_t i = 0; i < b * n_known * (t + horizon); i++) negk[i] = -known[i];
         float *mir = (float *)malloc(b * v * horizon * q * sizeof(float));
-        rc = forecast_raw(threads, out, m, inputs, observed, b, v, t, horizon, max_context, per_shot, cap_k, extreme);
-        const int rc2 =
-            forecast_raw(threads, mir, m, neg, observed, b, v, t, horizon, max_context, per_shot, cap_k, extreme);
+        rc = forecast_raw(threads, out, m, inputs, observed, b, v, t, horizon, past, n_past, known, n_known,
+                          max_context, per_shot, cap_k, extreme);
+        const int rc2 = forecast_raw(threads, mir, m, neg, observed, b, v, t, horizon, negp, n_past, negk, n_known,
+                                     max_context, per_shot, cap_k, extreme);
+        free(negp);
+        free(negk);
         if (rc == 0) rc = rc2;
         for (size_t i = 0; i < b * v * horizon; i++)
             for (size_t j = 0; j < q; j++) {
@@ -487,7 +623,8 @@ int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model
         free(neg);
         free(mir);
     } else {
-        rc = forecast_raw(threads, out, m, inputs, observed, b, v, t, horizon, max_context, per_shot, cap_k, extreme);
+        rc = forecast_raw(threads, out, m, inputs, observed, b, v, t, horizon, past, n_past, known, n_known,
+                          max_context, per_shot, cap_k, extreme);
     }
     if (rc != 0) return rc;
     if (clip_nonnegative)
@@ -505,4 +642,12 @@ int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model
                 }
         }
     return 0;
+}
+
+/* forecaster.forecast without covariates. */
+int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
+                           const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon, size_t max_context,
+                           size_t per_shot, float cap_k, float extreme, int symmetric, int clip_nonnegative) {
+    return orc_timestral_forecast_cov(threads, out, m, inputs, observed, b, v, t, horizon, NULL, 0, NULL, 0,
+                                      max_context, per_shot, cap_k, extreme, symmetric, clip_nonnegative);
 }

@@ -201,6 +201,11 @@ class Oracle:
         L.orc_timestral_forecast.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz, _sz, _sz,
                                              _sz, _f, _f, ctypes.c_int, ctypes.c_int]
         L.orc_timestral_forecast.restype = ctypes.c_int
+        L.orc_timestral_predict_block_cov.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz,
+                                                      _sz, _vp, _vp, _vp]
+        L.orc_timestral_forecast_cov.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz, _sz,
+                                                 _vp, _sz, _vp, _sz, _sz, _sz, _f, _f, ctypes.c_int, ctypes.c_int]
+        L.orc_timestral_forecast_cov.restype = ctypes.c_int
         L.orc_quantile_linear.argtypes = [_vp, _sz, _f]
         L.orc_quantile_linear.restype = _f
         L.orc_bolt_forecast_horizon.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _sz, _f,
@@ -447,6 +452,38 @@ class Oracle:
         st = timestral_model_struct(m)
         self.lib.orc_timestral_predict_block(threads, ptr(out), ctypes.byref(st), ptr(ctx), ptr(obs), t, groups, vall, h)
         return out
+
+    def timestral_predict_block_cov(self, threads, m, ctx, obs, t, groups, vall, h, roles, kf=None, kfm=None):
+        """(groups * targets, h * ps, q) quantiles of the target rows."""
+        ctx = np.ascontiguousarray(ctx, np.float32)
+        obs = np.ascontiguousarray(obs, np.uint8)
+        roles = np.ascontiguousarray(roles, np.uint8)
+        kf = None if kf is None else np.ascontiguousarray(kf, np.float32)
+        kfm = None if kfm is None else np.ascontiguousarray(kfm, np.uint8)
+        out = np.zeros((groups * int((roles == 0).sum()), h * m["ps"], m["q"]), np.float32)
+        st = timestral_model_struct(m)
+        self.lib.orc_timestral_predict_block_cov(threads, ptr(out), ctypes.byref(st), ptr(ctx), ptr(obs), t, groups,
+                                                 vall, h, ptr(roles), None if kf is None else ptr(kf),
+                                                 None if kfm is None else ptr(kfm))
+        return out
+
+    def timestral_forecast_cov(self, threads, m, inputs, observed, b, v, t, horizon, past=None, known=None,
+                               max_context=0, per_shot=32, cap_k=1e4, extreme=1e30, symmetric=True,
+                               clip_nonnegative=True):
+        """(rc, out (b, v, horizon, q)); past (b, n_past, t), known (b, n_known, t + horizon), NaN = missing."""
+        inputs = np.ascontiguousarray(inputs, np.float32)
+        observed = np.ascontiguousarray(observed, np.uint8)
+        past = None if past is None else np.ascontiguousarray(past, np.float32)
+        known = None if known is None else np.ascontiguousarray(known, np.float32)
+        n_past = 0 if past is None else past.shape[1]
+        n_known = 0 if known is None else known.shape[1]
+        out = np.zeros((b, v, horizon, m["q"]), np.float32)
+        st = timestral_model_struct(m)
+        rc = self.lib.orc_timestral_forecast_cov(threads, ptr(out), ctypes.byref(st), ptr(inputs), ptr(observed), b,
+                                                 v, t, horizon, None if past is None else ptr(past), n_past,
+                                                 None if known is None else ptr(known), n_known, max_context,
+                                                 per_shot, cap_k, extreme, int(symmetric), int(clip_nonnegative))
+        return rc, out
 
     def timestral_refine_block(self, qs, m, ctx, obs, rows, t, h):
         st = timestral_model_struct(m)

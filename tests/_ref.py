@@ -466,19 +466,42 @@ def softplus_f64(x):
     return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
 
 
-def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h):
-    """Model.predictBlock without covariates, in float64: (rows, h * ps, q) quantiles in data units."""
+def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h, roles=None, kf=None, kfm=None):
+    """Model.predictBlock in float64: (groups * n_targets, h * ps, q) quantiles in data units. roles
+    (vall) in model.Role order (ROLE_TARGET, ROLE_PAST, ROLE_KNOWN; None = all targets); kf/kfm
+    (rows, h * ps) known-future values and observations. With covariates the window spans the
+    context and the horizon, known rows use whole-window mean/std (none for 0/1 rows, which also
+    skip the asinh) and read every valid key, and the variate firewalls apply."""
     ps, d, nh, hid, q = m["ps"], m["d"], m["nh"], m["hid"], m["q"]
     hd, rows = 64, groups * vall
-    n = l = ne = t // ps
+    roles = [ROLE_TARGET] * vall if roles is None else list(roles)
+    cov = any(r != ROLE_TARGET for r in roles)
+    hl = h * ps
+    w = t + hl if cov else t
+    l, n = t // ps, w // ps
+    ne = n
     sl = ne + h
     ctx = np.asarray(ctx, np.float64).reshape(rows, t)
     obs = np.asarray(obs, bool).reshape(rows, t)
+    if cov:
+        fut = np.zeros((rows, hl)) if kf is None else np.asarray(kf, np.float64).reshape(rows, hl)
+        fob = np.zeros((rows, hl), bool) if kf is None else np.asarray(kfm, bool).reshape(rows, hl)
+        ctx, obs = np.concatenate([ctx, fut], 1), np.concatenate([obs, fob], 1)
     loc, scale = patch_stats_f64(ctx, obs, ps, m["minimum_scale"])
-    sc = np.maximum(np.repeat(scale, ps, axis=1), float(np.finfo(np.float32).eps))
-    v = np.where(obs, (ctx - np.repeat(loc, ps, axis=1)) / sc, 0.0)
+    lo_t, sc_t = np.repeat(loc, ps, axis=1), np.repeat(scale, ps, axis=1)
+    asinh_row = np.ones(rows, bool)
+    for r in range(rows):
+        if cov and roles[r % vall] == ROLE_KNOWN:
+            vals = ctx[r][obs[r]]
+            mu = vals.mean() if vals.size else 0.0
+            sd = max(np.sqrt(((vals - mu) ** 2).mean()) if vals.size else 0.0, m["minimum_scale"])
+            if vals.size and np.all((vals == 0) | (vals == 1)):
+                mu, sd, asinh_row[r] = 0.0, 1.0, False
+            lo_t[r], sc_t[r] = mu, sd
+    sc = np.maximum(sc_t, float(np.finfo(np.float32).eps))
+    v = np.where(obs, (ctx - lo_t) / sc, 0.0)
     if m["use_asinh"]:
-        v = np.arcsinh(v)
+        v = np.where(asinh_row[:, None], np.arcsinh(v), v)
     feats = np.concatenate([v.reshape(rows, n, ps), (~obs).reshape(rows, n, ps).astype(np.float64)], axis=2)
     x = np.zeros((rows, sl, d))
     x[:, :ne] = resblock_silu_f64(m["patch_proj"], feats.reshape(rows * n, 2 * ps)).reshape(rows, n, d)
@@ -493,7 +516,8 @@ def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h):
         lo, hi = y[..., :half].copy(), y[..., half:].copy()
         return np.concatenate([lo * cg - hi * sg, hi * cg + lo * sg], axis=-1)
 
-    enc_allowed = [allowed_matrix(3, ne, ne, kv[r]) for r in range(rows)]
+    enc_allowed = [allowed_matrix(4 if cov and roles[r % vall] == ROLE_KNOWN else 3, ne, ne, kv[r])
+                   for r in range(rows)]
     dec_allowed = [allowed_matrix(5, h, sl, kv[r], q_pos0=ne, ctx_keys=l, chain_start=ne) for r in range(rows)]
     for ly in m["layers"]:
         for a in ly["attns"]:
@@ -508,7 +532,7 @@ def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h):
                         o[r, ne:, hh] = naive_attend(qr[ne:, hh], kr[:, hh], vr[:, hh], dec_allowed[r], hd ** -0.5)
                 o = o.reshape(rows, sl, d)
             else:
-                o = variate_attend_f64(qkv.reshape(rows * sl, 3 * d), kv, [ROLE_TARGET] * vall, False, groups, vall,
+                o = variate_attend_f64(qkv.reshape(rows * sl, 3 * d), kv, roles, cov, groups, vall,
                                        ne, h, d, nh, hd).reshape(rows, sl, d)
             if a.get("gate") is not None:
                 o = o / (1.0 + np.exp(-(xn @ W(a["gate"]).T)))
@@ -516,8 +540,9 @@ def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h):
         xn = rms_norm_f64(x, ly["mlp_norm"], m["norm_eps"])
         hh_ = xn @ W(ly["w12"]).T
         x = x + (hh_[..., :hid] * silu_f64(hh_[..., hid:])) @ W(ly["w3"]).T
-    dec = rms_norm_f64(x[:, ne:], m["out_norm"], m["norm_eps"])
-    raw = resblock_silu_f64(m["head"], dec.reshape(rows * h, d)).reshape(rows, h * ps, q)
+    tgt = [r for r in range(rows) if roles[r % vall] == ROLE_TARGET]
+    dec = rms_norm_f64(x[tgt, ne:], m["out_norm"], m["norm_eps"])
+    raw = resblock_silu_f64(m["head"], dec.reshape(len(tgt) * h, d)).reshape(len(tgt), h * ps, q)
     knots, med = np.asarray(m["knots"]), m["median"]
     widths = np.zeros(q)
     widths[med + 1:] = knots[med + 1:] - knots[med:-1]
@@ -529,7 +554,7 @@ def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h):
     out[..., :med] = raw[..., med:med + 1] - np.cumsum(inc[..., :med][..., ::-1], axis=-1)[..., ::-1]
     if m["use_asinh"]:
         out = np.sinh(out)
-    return out * scale[:, l - 1, None, None] + loc[:, l - 1, None, None]
+    return out * scale[tgt, l - 1, None, None] + loc[tgt, l - 1, None, None]
 
 
 def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale):

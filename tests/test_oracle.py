@@ -1094,3 +1094,150 @@ def test_bolt_forecast_horizon_composition(orc, t_in, max_ctx, horizon):
     want = np.concatenate(steps, axis=1)[:, :horizon]
     assert got.shape == (b, horizon, q)
     assert np.array_equal(got, want)
+
+
+# ---- Timestral covariates (past-only and known-future rows) ------------------------------------
+
+def _ts_cov_case(seed, b=2, v=1, n_past=1, n_known=2, t0=150, horizon=40):
+    """Targets plus covariates of both kinds: a past-only row with a gap, a known-future row with
+    missing steps in its future, and (with n_known > 1) a 0/1 indicator row."""
+    rng = np.random.default_rng(seed)
+    m, x, obs = _ts_case(seed, b, v, t0)
+    past = (3 + rng.standard_normal((b, n_past, t0))).astype(np.float32)
+    past[:, :, 40:55] = np.nan
+    steps = np.arange(t0 + horizon)
+    known = np.empty((b, n_known, t0 + horizon), np.float32)
+    for k in range(n_known):
+        known[:, k] = (np.cos(steps / 5.0 + k) * 4 + 10).astype(np.float32)
+        if k == 1:
+            known[:, k] = (steps % 7 < 2).astype(np.float32)
+    known[:, 0, t0 + 3:t0 + 9] = np.nan
+    return m, x, obs, past, known
+
+
+@pytest.mark.parametrize("attend_missing", [True, False])
+def test_timestral_predict_block_covariates_match_f64(orc, attend_missing):
+    """predictBlock (model.zig:220-432) with covariate rows against the float64 model: the window
+    spans context and horizon (blanks for past-only rows, real futures for known rows), known rows
+    normalised by their whole-window mean and population std (0/1 rows neither shifted nor
+    asinh'd), known rows bidirectional in time attention, the variate firewalls, and the head
+    on the target rows only."""
+    rng = np.random.default_rng(11 + attend_missing)
+    m = _ref.timestral_model(rng, d=128, nh=2, hid=128, attend_missing=attend_missing)
+    groups, t, h, ps = 2, 16 * 8, 3, 16
+    roles = np.array([0, 0, 1, 2, 2], np.uint8)
+    vall = len(roles)
+    rows = groups * vall
+    ctx = (5 + 3 * rng.standard_normal((rows, t))).astype(np.float32)
+    obs = rng.random((rows, t)) < 0.9
+    obs[vall:vall + 2, :35] = False  # group 1's targets start late
+    kf = (2 + rng.standard_normal((rows, h * ps))).astype(np.float32)
+    kfm = rng.random((rows, h * ps)) < 0.85
+    for g in range(groups):  # the last row of each series is a 0/1 indicator
+        r = g * vall + 4
+        ctx[r] = (np.arange(t) % 5 == 0)
+        kf[r] = (np.arange(h * ps) % 5 == 0)
+    ctx[~obs] = 0
+    kf[~kfm] = 0
+    got = orc.timestral_predict_block_cov(3, m, ctx, obs, t, groups, vall, h, roles, kf, kfm)
+    want = _ref.timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h, roles, kf, kfm)
+    assert got.shape == want.shape == (groups * 2, h * ps, m["q"])
+    assert _ref.scaled_err(got, want) < 5e-5
+    # The covariates reach the targets: blanking the known futures moves the forecast.
+    blank = orc.timestral_predict_block_cov(3, m, ctx, obs, t, groups, vall, h, roles, None, None)
+    assert _ref.scaled_err(blank, _ref.timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h, roles)) < 5e-5
+    assert not np.allclose(blank, got, rtol=1e-4, atol=1e-4)
+
+
+def _ts_cov_decode_composed(orc, m, x, obs, past, known, b, v, horizon, per_shot, max_context):
+    """forecastRaw + blockDecode with covariates restated over the oracle's predict_block_cov and
+    refine_block: targets forward-filled, covariates NaN-masked; after each block targets carry
+    their medians, known rows their real future, past-only rows a blank."""
+    ps, q = m["ps"], m["q"]
+    n_past, n_known = past.shape[1], known.shape[1]
+    vall, t0 = v + n_past + n_known, x.shape[1]
+    roles = np.array([0] * v + [1] * n_past + [2] * n_known, np.uint8)
+    tctx, tmask = _ref.timestral_context(x, obs, max_context, ps)
+    t = tctx.shape[1]
+    keep = min(t0, max_context)
+    rows = np.zeros((b, vall, t), np.float32)
+    mask = np.zeros((b, vall, t), bool)
+    rows[:, :v], mask[:, :v] = tctx.reshape(b, v, t), tmask.reshape(b, v, t)
+    for k, src in ((v, past), (v + n_past, known[:, :, :t0])):
+        win = src[:, :, t0 - keep:]
+        rows[:, k:k + src.shape[1], t - keep:] = np.nan_to_num(win, nan=0.0)
+        mask[:, k:k + src.shape[1], t - keep:] = ~np.isnan(win)
+    fut = known[:, :, t0:]
+    hpad = -(-horizon // ps) * ps
+    kf = np.zeros((b, vall, hpad), np.float32)
+    kfm = np.zeros((b, vall, hpad), bool)
+    kf[:, v + n_past:, :horizon] = np.nan_to_num(fut, nan=0.0)
+    kfm[:, v + n_past:, :horizon] = ~np.isnan(fut)
+    ctx, cm = rows.reshape(b * vall, t), mask.reshape(b * vall, t)
+    kf, kfm = kf.reshape(b * vall, hpad), kfm.reshape(b * vall, hpad)
+    out = np.zeros((b * v, horizon, q), np.float32)
+    tgt = [g * vall + i for g in range(b) for i in range(v)]
+    remaining, done = -(-horizon // ps), 0
+    while remaining:
+        block = min(per_shot, remaining)
+        blen = block * ps
+        t = ctx.shape[1]
+        qs = orc.timestral_predict_block_cov(3, m, ctx, cm, t, b, vall, block, roles, kf[:, done:done + blen],
+                                             kfm[:, done:done + blen])
+        if block > 1:
+            for oi, r in enumerate(tgt):
+                sub = qs[oi:oi + 1].copy()
+                orc.timestral_refine_block(sub, m, ctx[r:r + 1], cm[r:r + 1], 1, t, block)
+                qs[oi] = sub[0]
+        take = min(blen, horizon - done)
+        out[:, done:done + take] = qs[:, :take]
+        remaining -= block
+        if not remaining:
+            break
+        new = np.zeros((b * vall, blen), np.float32)
+        newm = np.zeros((b * vall, blen), bool)
+        medv = qs[:, :, m["median"]].copy()
+        medv[~np.isfinite(medv) | (np.abs(medv) >= 1e30)] = 0
+        new[tgt], newm[tgt] = medv, True
+        kn = [g * vall + i for g in range(b) for i in range(v + n_past, vall)]
+        new[kn], newm[kn] = kf[kn, done:done + blen], kfm[kn, done:done + blen]
+        done += blen
+        ctx, cm = np.concatenate([ctx, new], 1), np.concatenate([cm, newm], 1)
+        if ctx.shape[1] > max_context:
+            kt = max(ps, max_context // ps * ps)
+            ctx, cm = ctx[:, -kt:], cm[:, -kt:]
+    return out
+
+
+@pytest.mark.parametrize("horizon,per_shot,max_context", [(40, 4, 2048), (100, 2, 2048), (100, 2, 160)])
+def test_timestral_forecast_covariates_block_decode_composition(orc, horizon, per_shot, max_context):
+    b, v = 2, 2
+    m, x, obs, past, known = _ts_cov_case(21, b, v, horizon=horizon)
+    rc, got = orc.timestral_forecast_cov(3, m, x, obs, b, v, x.shape[1], horizon, past, known, max_context, per_shot,
+                                         cap_k=0.0, symmetric=False, clip_nonnegative=False)
+    assert rc == 0
+    want = _ts_cov_decode_composed(orc, m, x, obs, past, known, b, v, horizon, per_shot, max_context)
+    assert np.array_equal(got.reshape(b * v, horizon, -1), want)
+
+
+def test_timestral_forecast_covariates_mirror_and_causality(orc):
+    """Symmetric averaging negates every covariate row in the mirrored pass: the forecast of
+    (-x, -covariates) is exactly the reversed negation of that of (x, covariates) (a mirror that
+    kept the covariates' sign breaks this). Known futures past the first block do not move the
+    first block; the covariates do move the forecast."""
+    b, v, horizon = 2, 1, 64
+    m, x, obs, past, known = _ts_cov_case(22, b, v, horizon=horizon)
+    t0 = x.shape[1]
+    kw = dict(per_shot=2, cap_k=1e4, clip_nonnegative=False)
+    _, f = orc.timestral_forecast_cov(3, m, x, obs, b, v, t0, horizon, past, known, **kw)
+    _, g = orc.timestral_forecast_cov(3, m, -x, obs, b, v, t0, horizon, -past, -known, **kw)
+    assert np.array_equal(g, -f[..., ::-1])
+    _, g2 = orc.timestral_forecast_cov(3, m, -x, obs, b, v, t0, horizon, past, known, **kw)
+    assert not np.array_equal(g2, -f[..., ::-1])
+    k2 = known.copy()
+    k2[:, :, t0 + 32:] += 50
+    _, f2 = orc.timestral_forecast_cov(3, m, x, obs, b, v, t0, horizon, past, k2, **kw)
+    assert np.array_equal(f2[:, :, :32], f[:, :, :32]) and not np.allclose(f2[:, :, 32:], f[:, :, 32:])
+    _, f0 = orc.timestral_forecast_cov(3, m, x, obs, b, v, t0, horizon, **kw)
+    _, f1 = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, **kw)
+    assert np.array_equal(f0, f1) and not np.allclose(f0, f, rtol=1e-3)
