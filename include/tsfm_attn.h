@@ -496,6 +496,12 @@ typedef struct tsfm_timestral_forecast_args {
     uint32_t flags;                 /* TSFM_ATTN_DEVICE_PTRS, optionally | TSFM_TIMESTRAL_BF16_ATTN */
     float *out;                     /* (batch, variates, horizon, n_quantiles) */
     void *stream;
+    /* Numeric covariates (Covariates.past / .known, src/timestral/forecaster.zig:36-46), NaN =
+     * missing; each pointer may be NULL when its count is 0. With covariates every decode block
+     * re-encodes the window (context + horizon) as the reference does: kv_cache is ignored. */
+    const float *past;              /* (batch, n_past, len) past-only covariates */
+    const float *known;             /* (batch, n_known, len + horizon) known-future covariates */
+    int32_t n_past, n_known;        /* variates + n_past + n_known <= 16 */
 } tsfm_timestral_forecast_args;
 
 int tsfm_timestral_forecast(const tsfm_timestral_forecast_args *args);

@@ -144,3 +144,65 @@ def test_timestral_forecast_argument_errors(ta, gpu_ready):
     assert ta.load().tsfm_timestral_forecast(ctypes.byref(args)) == ta.E_INVALID
     torch.cuda.synchronize()
     assert (out == 0).all()
+
+
+def _cov_case(seed, b=2, v=1, n_past=1, n_known=2, length=150, horizon=40):
+    """A past-only row with a gap, a known-future row with missing future steps and a 0/1
+    indicator row (its statistics skipped, no asinh)."""
+    m, x, obs = _case(seed, b, v, length)
+    rng = np.random.default_rng(seed + 100)
+    past = (3 + rng.standard_normal((b, n_past, length))).astype(np.float32)
+    past[:, :, 40:55] = np.nan
+    steps = np.arange(length + horizon)
+    known = np.empty((b, n_known, length + horizon), np.float32)
+    for k in range(n_known):
+        known[:, k] = np.cos(steps / 5.0 + k) * 4 + 10 if k != 1 else (steps % 7 < 2)
+    known[:, 0, length + 3:length + 9] = np.nan
+    return m, x, obs, past, known
+
+
+@pytest.mark.parametrize("horizon,per_shot,max_context,v", [(40, 32, 0, 1), (100, 2, 0, 2), (100, 2, 176, 1)])
+def test_timestral_forecast_with_covariates(ta, orc, orc16, gpu_ready, horizon, per_shot, max_context, v):
+    """Past-only and known-future covariates (forecaster.zig:57-121, 321-394; model.zig:240-330):
+    the window over context and horizon, known rows' whole-window statistics and bidirectional
+    time attention, the variate firewalls, role feedback between blocks, and the mirrored pass over
+    negated covariates, against the oracle's re-encoding forecast at the reference-derived bar."""
+    import torch
+
+    b = 2
+    m, x, obs, past, known = _cov_case(41 + v, b, v, horizon=horizon)
+    t = x.shape[1]
+    out = torch.full((b, v, horizon, m["q"]), -7.0, device="cuda")
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    od = torch.from_numpy(np.ascontiguousarray(obs.astype(np.uint8))).cuda()
+    rc = ta.timestral_forecast(out, xd, od, _device_model(m), b, v, t, horizon, max_context=max_context,
+                               per_shot=per_shot, past=torch.from_numpy(past).cuda(),
+                               known=torch.from_numpy(known).cuda())
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    kw = dict(max_context=max_context, per_shot=per_shot)
+    rc8, w8 = orc.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, known, **kw)
+    rc16, w16 = orc16.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, known, **kw)
+    assert rc8 == 0 and rc16 == 0
+    print(f"covariates horizon={horizon} per_shot={per_shot} max_context={max_context} v={v}", flush=True)
+    err, bar = _ref.assert_within_reference_bar(got, w8, w16)
+    print(f"  err {err:.3g} bar {bar:.3g}", flush=True)
+    _, plain = orc16.timestral_forecast(THREADS, m, x, obs, b, v, t, horizon, max_context, per_shot)
+    assert _ref.scaled_err(got, plain) > 10 * bar  # the covariates do move the forecast
+
+
+def test_timestral_forecast_covariate_errors(ta, gpu_ready):
+    import torch
+
+    m, x, obs, past, known = _cov_case(45)
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    od = torch.from_numpy(np.ascontiguousarray(obs.astype(np.uint8))).cuda()
+    out = torch.zeros((2, 1, 40, m["q"]), device="cuda")
+    a = ta.timestral_forecast_args(out, xd, od, _device_model(m), 2, 1, x.shape[1], 40,
+                                   known=torch.from_numpy(known).cuda())
+    a.known = None  # a count without its array
+    assert ta.load().tsfm_timestral_forecast(ta.ctypes.byref(a)) == ta.E_INVALID
+    big = torch.zeros((2, 16, x.shape[1] + 40), device="cuda")
+    rc = ta.timestral_forecast(out, xd, od, _device_model(m), 2, 1, x.shape[1], 40, known=big)
+    assert rc == ta.E_UNSUPPORTED  # 1 target + 16 covariate rows > 16

@@ -174,13 +174,32 @@ struct TsHead {
     float wf;          // quantile_width_factor
     float widths[32];  // knot widths (model.zig:392-395), q <= 32
 };
-hipError_t launch_ts_context(const float* inputs, const uint8_t* observed, int R, int rows, int t0, int keep, int t,
-                             float* ctx, uint8_t* mask, int cap_t, uint8_t* nonneg, hipStream_t s);
+// forecastRaw's rows: groups of vall rows (V targets, n_past past-only, n_known known-future
+// covariates), groups >= batch the mirrored pass.
+struct TsContextParams {
+    const float* inputs;
+    const uint8_t* observed;
+    const float* past;   // (batch, n_past, t0), NaN = missing
+    const float* known;  // (batch, n_known, t0 + horizon), NaN = missing
+    int batch, V, n_past, n_known, vall, rows, t0, keep, t, horizon, hpad, cap_t;
+    float* ctx;
+    uint8_t* mask;
+    float* kf;     // (rows, hpad) known-future values
+    uint8_t* kfm;  // (rows, hpad) their observation flags
+    uint8_t* nonneg;
+};
+hipError_t launch_ts_context(const TsContextParams& p, hipStream_t s);
+hipError_t launch_ts_window(float* ctx, uint8_t* mask, int cap_t, int t, int blen, const float* kf, const uint8_t* kfm,
+                            int hpad, int done, int vall, int known_from, int rows, hipStream_t s);
+hipError_t launch_ts_known_stats(const float* ctx, const uint8_t* mask, int cap_t, int w, int ps, int rows, int vall,
+                                 int known_from, float min_scale, float* loc, float* scale, int cap_p,
+                                 uint8_t* no_asinh, hipStream_t s);
 hipError_t launch_ts_stats(const TsStatsParams& p, hipStream_t s);
 hipError_t launch_ts_features(const float* ctx, const uint8_t* mask, int cap_t, const float* loc, const float* scale,
-                              int cap_p, int rows, int p0, int l, int ps, int use_asinh, float* feats, hipStream_t s);
-hipError_t launch_ts_rope_tables(const int* row_first, int groups, int vall, int n_tok, const TsRope& rp,
-                                 float* cos_t, float* sin_t, int* first_obs, hipStream_t s);
+                              int cap_p, int rows, int p0, int l, int ps, int use_asinh, const uint8_t* no_asinh,
+                              float* feats, hipStream_t s);
+hipError_t launch_ts_rope_tables(const int* row_first, int groups, int vall, int n_tok, int ne, int shift,
+                                 const TsRope& rp, float* cos_t, float* sin_t, int* first_obs, hipStream_t s);
 hipError_t launch_ts_assemble(const float* emb, const float* query, float* x, int rows, int m, int h, int d,
                               hipStream_t s);
 hipError_t launch_ts_mul_sigmoid(float* o, const float* g, int64_t n, hipStream_t s);
@@ -192,15 +211,15 @@ hipError_t launch_ts_head_finish(const float* raw, const float* loc, const float
 hipError_t launch_ts_refine(float* qs, const float* loc, const float* scale, int cap_p, int l, const double* fold,
                             int rows, int h, int ps, int q, int median, double min_scale, float* frames,
                             hipStream_t s);
-hipError_t launch_ts_store_block(const float* qs, int rows, int R, int blen, int done, int horizon, int q, float* out,
-                                 float* mir, hipStream_t s);
-hipError_t launch_ts_feedback(const float* qs, int rows, int blen, int q, int median, float extreme, float* ctx,
-                              uint8_t* mask, int cap_t, int t, hipStream_t s);
+hipError_t launch_ts_store_block(const float* qs, int rows, int batch, int vall, int V, int blen, int done, int horizon,
+                                 int q, float* out, float* mir, hipStream_t s);
+hipError_t launch_ts_feedback(const float* qs, int rows, int vall, int V, int blen, int q, int median, float extreme,
+                              float* ctx, uint8_t* mask, int cap_t, int t, hipStream_t s);
 hipError_t launch_ts_slide(const float* src, const uint8_t* src_mask, float* dst, uint8_t* dst_mask, int rows,
                            int cap_t, int start, int keep, hipStream_t s);
 hipError_t launch_ts_cap_bounds(const float* ctx, const uint8_t* mask, int cap_t, int t, int ps, const float* scale,
                                 int cap_p, int rows, float cap_k, float* bounds, hipStream_t s);
-hipError_t launch_ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R,
-                           int horizon, int q, int cap, int symmetric, int clip, hipStream_t s);
+hipError_t launch_ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R, int V,
+                           int vall, int horizon, int q, int cap, int symmetric, int clip, hipStream_t s);
 
 }  // namespace tsfm

@@ -22,23 +22,49 @@ namespace {
 
 __device__ __forceinline__ double fmax_d(double a, double b) { return fmax(a, b); }
 
-// forecastRaw's rows (src/timestral/forecaster.zig:344-379), every row a target: forward-fill
-// (leading gaps 0), keep the last `keep` steps, left-pad to t. Rows r >= R are the mirrored pass
-// (the negated series, forecast.zig:114). Also the clip flag of each input row (finish, :163-178).
-__global__ void ts_context(const float* inputs, const uint8_t* observed, int R, int rows, int t0, int keep, int t,
-                           float* ctx, uint8_t* mask, int cap_t, uint8_t* nonneg) {
+// forecastRaw's rows (src/timestral/forecaster.zig:321-379). Row r = g * vall + i of group g (g <
+// batch: forward pass, else the mirrored pass of series g - batch, every value negated,
+// forecast.zig:112-121); i < V targets (forward-filled, leading gaps 0), then n_past past-only
+// and n_known known-future covariates (NaN = missing). Keep the last `keep` steps, left-pad to t;
+// known rows also write their horizon values to kf/kfm (rows, hpad). Also the clip flag of each
+// target input row (finish, :163-178).
+__global__ void ts_context(const TsContextParams p) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= rows) return;
-    const int src = r < R ? r : r - R;
-    const float sign = r < R ? 1.f : -1.f;
-    const float* x = inputs + (int64_t)src * t0;
-    const uint8_t* o = observed + (int64_t)src * t0;
-    float* c = ctx + (int64_t)r * cap_t;
-    uint8_t* mk = mask + (int64_t)r * cap_t;
+    if (r >= p.rows) return;
+    const int g = r / p.vall, i = r % p.vall;
+    const bool mirror = g >= p.batch;
+    const int sidx = mirror ? g - p.batch : g;
+    const float sign = mirror ? -1.f : 1.f;
+    const int t0 = p.t0, keep = p.keep, t = p.t;
+    float* c = p.ctx + (int64_t)r * p.cap_t;
+    uint8_t* mk = p.mask + (int64_t)r * p.cap_t;
     for (int j = 0; j < t - keep; j++) {
         c[j] = 0.f;
         mk[j] = 0;
     }
+    if (i >= p.V) {
+        const bool known = i >= p.V + p.n_past;
+        const float* x = known ? p.known + ((int64_t)sidx * p.n_known + (i - p.V - p.n_past)) * (t0 + p.horizon)
+                               : p.past + ((int64_t)sidx * p.n_past + (i - p.V)) * t0;
+        for (int j = t0 - keep; j < t0; j++) {
+            const float v = sign * x[j];
+            const bool ob = !isnan(v);
+            const int dst = (t - keep) + (j - (t0 - keep));
+            c[dst] = ob ? v : 0.f;
+            mk[dst] = ob ? 1 : 0;
+        }
+        if (known)
+            for (int j = 0; j < p.hpad; j++) {
+                const float v = j < p.horizon ? sign * x[t0 + j] : 0.f;
+                const bool ob = j < p.horizon && !isnan(v);
+                p.kf[(int64_t)r * p.hpad + j] = ob ? v : 0.f;
+                p.kfm[(int64_t)r * p.hpad + j] = ob ? 1 : 0;
+            }
+        return;
+    }
+    const int src = sidx * p.V + i;
+    const float* x = p.inputs + (int64_t)src * t0;
+    const uint8_t* o = p.observed + (int64_t)src * t0;
     float last = 0.f;
     bool seen = false, any = false, all_nonneg = true;
     for (int j = 0; j < t0; j++) {
@@ -58,15 +84,87 @@ __global__ void ts_context(const float* inputs, const uint8_t* observed, int R, 
             mk[dst] = ob ? 1 : 0;
         }
     }
-    if (r < R) nonneg[r] = any && all_nonneg;
+    if (!mirror) p.nonneg[src] = any && all_nonneg;
+}
+
+// predictBlock's window with covariates (model.zig:253-273): steps [t, t + blen) of every row are
+// the block's known futures (known rows, from step `done` of kf) or blanks (targets and past-only
+// rows; the targets' blanks become medians after the block).
+__global__ void ts_window(float* ctx, uint8_t* mask, int cap_t, int t, int blen, const float* kf,
+                          const uint8_t* kfm, int hpad, int done, int vall, int known_from, int rows) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * blen) return;
+    const int r = (int)(idx / blen), j = (int)(idx % blen);
+    const bool known = r % vall >= known_from;
+    ctx[(int64_t)r * cap_t + t + j] = known ? kf[(int64_t)r * hpad + done + j] : 0.f;
+    mask[(int64_t)r * cap_t + t + j] = known ? kfm[(int64_t)r * hpad + done + j] : 0;
+}
+
+// Known-future rows' statistics (model.zig:283-310): float32 mean and population std of the
+// observed steps of the whole window [0, w), at least min_scale; a row of only 0/1 values is
+// neither shifted nor scaled and skips the asinh. Written over every patch of the row's loc and
+// scale; other rows keep their causal statistics. One thread per row, the reference's order.
+__global__ void ts_known_stats(const float* ctx, const uint8_t* mask, int cap_t, int w, int ps, int rows, int vall,
+                               int known_from, float min_scale, float* loc, float* scale, int cap_p,
+                               uint8_t* no_asinh) {
+#pragma clang fp contract(off)
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    if (r % vall < known_from) {
+        no_asinh[r] = 0;
+        return;
+    }
+    const float* x = ctx + (int64_t)r * cap_t;
+    const uint8_t* o = mask + (int64_t)r * cap_t;
+    float cnt = 0.f, sum = 0.f;
+    bool zero_one = true, any = false;
+    for (int i = 0; i < w; i++)
+        if (o[i]) {
+            cnt += 1.f;
+            sum += x[i];
+            zero_one = zero_one && (x[i] == 0.f || x[i] == 1.f);
+            any = true;
+        }
+    float kloc = sum / fmaxf(cnt, 1.f);
+    float ss = 0.f;
+    for (int i = 0; i < w; i++)
+        if (o[i]) {
+            const float dv = x[i] - kloc;
+            ss += dv * dv;
+        }
+    float kscale = fmaxf(sqrtf(ss / fmaxf(cnt, 1.f)), min_scale);
+    const bool binary = zero_one && any;
+    if (binary) {
+        kloc = 0.f;
+        kscale = 1.f;
+    }
+    for (int pt = 0; pt < w / ps; pt++) {
+        loc[(int64_t)r * cap_p + pt] = kloc;
+        scale[(int64_t)r * cap_p + pt] = kscale;
+    }
+    no_asinh[r] = binary ? 1 : 0;
 }
 
 }  // namespace
 
-hipError_t launch_ts_context(const float* inputs, const uint8_t* observed, int R, int rows, int t0, int keep, int t,
-                             float* ctx, uint8_t* mask, int cap_t, uint8_t* nonneg, hipStream_t s) {
-    hipLaunchKernelGGL(ts_context, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, inputs, observed, R, rows, t0,
-                       keep, t, ctx, mask, cap_t, nonneg);
+hipError_t launch_ts_context(const TsContextParams& p, hipStream_t s) {
+    hipLaunchKernelGGL(ts_context, dim3((unsigned)((p.rows + 63) / 64)), dim3(64), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_ts_window(float* ctx, uint8_t* mask, int cap_t, int t, int blen, const float* kf, const uint8_t* kfm,
+                            int hpad, int done, int vall, int known_from, int rows, hipStream_t s) {
+    const int64_t n = (int64_t)rows * blen;
+    hipLaunchKernelGGL(ts_window, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ctx, mask, cap_t, t, blen, kf,
+                       kfm, hpad, done, vall, known_from, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_ts_known_stats(const float* ctx, const uint8_t* mask, int cap_t, int w, int ps, int rows, int vall,
+                                 int known_from, float min_scale, float* loc, float* scale, int cap_p,
+                                 uint8_t* no_asinh, hipStream_t s) {
+    hipLaunchKernelGGL(ts_known_stats, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, ctx, mask, cap_t, w, ps,
+                       rows, vall, known_from, min_scale, loc, scale, cap_p, no_asinh);
     return hipGetLastError();
 }
 
@@ -146,10 +244,11 @@ __global__ void ts_stats(const TsStatsParams p) {
     p.row_first[r] = first;
 }
 
-// predictBlock's patch features (model.zig:281-328, no covariates) of patches [p0, l): values
-// normalised by their patch's causal statistics (asinh'd), then the missing-step mask.
+// predictBlock's patch features (model.zig:281-328) of patches [p0, l): values normalised by their
+// patch's statistics (asinh'd unless the row's no_asinh flag is set), then the missing-step mask.
 __global__ void ts_features(const float* ctx, const uint8_t* mask, int cap_t, const float* loc, const float* scale,
-                            int cap_p, int rows, int p0, int l, int ps, int use_asinh, float* feats) {
+                            int cap_p, int rows, int p0, int l, int ps, int use_asinh, const uint8_t* no_asinh,
+                            float* feats) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int np = l - p0;
     if (idx >= (int64_t)rows * np * ps) return;
@@ -163,7 +262,7 @@ __global__ void ts_features(const float* ctx, const uint8_t* mask, int cap_t, co
     float v = 0.f;
     if (ob) {
         v = (ctx[at] - lo) / sc;
-        if (use_asinh) v = asinhf(v);
+        if (use_asinh && !(no_asinh != nullptr && no_asinh[r])) v = asinhf(v);
     }
     float* f = feats + rp * 2 * ps;
     f[i] = v;
@@ -171,10 +270,11 @@ __global__ void ts_features(const float* ctx, const uint8_t* mask, int cap_t, co
 }
 
 // First observed patch of each group (model.zig:343-360: over the group's rows, 0 when none) and
-// the RoPE tables of runTransformer (:447-463) for token indices [0, n_tok): without covariates the
-// decoder token j sits at index ne + j = its time l + j, so one table serves every block.
-__global__ void ts_rope_tables(const int* row_first, int vall, int n_tok, TsRope rp, float* cos_t, float* sin_t,
-                               int* first_obs) {
+// the RoPE tables of runTransformer (:447-463) for token indices [0, n_tok): encoder token p at time
+// p, decoder token ne + j at time l + j = its index minus shift (ne - l: 0 without covariates, so
+// one table serves every block; the horizon's patches with covariates).
+__global__ void ts_rope_tables(const int* row_first, int vall, int n_tok, int ne, int shift, TsRope rp, float* cos_t,
+                               float* sin_t, int* first_obs) {
     const int g = blockIdx.y;
     int first = 0x7fffffff;
     for (int i = 0; i < vall; i++) {
@@ -186,7 +286,7 @@ __global__ void ts_rope_tables(const int* row_first, int vall, int n_tok, TsRope
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)n_tok * 32) return;
     const int tok = (int)(idx / 32), i = (int)(idx % 32);
-    const float pos = (float)(tok - first);
+    const float pos = (float)((tok < ne ? tok : tok - shift) - first);
     const float ang = rp.inv_freq[i] * pos;
     const int64_t at = ((int64_t)g * n_tok + tok) * 32 + i;
     cos_t[at] = cosf(ang);
@@ -377,25 +477,28 @@ __global__ void ts_refine_apply(float* qs, const float* frames, int rows, int h,
 
 // Store a block's quantiles: steps [done, done + blen) of each row's forecast, those before the
 // horizon (blockDecode :502-507). Rows r < R go to out, the mirrored rows to mir.
-__global__ void ts_store_block(const float* qs, int rows, int R, int blen, int done, int horizon, int q, float* out,
-                               float* mir) {
+__global__ void ts_store_block(const float* qs, int rows, int batch, int vall, int V, int blen, int done, int horizon,
+                               int q, float* out, float* mir) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)rows * blen * q) return;
     const int i = (int)(idx % q);
     const int64_t rs = idx / q;
     const int r = (int)(rs / blen), s = (int)(rs % blen);
-    if (done + s >= horizon) return;
-    float* dst = r < R ? out + ((int64_t)r * horizon + done + s) * q : mir + ((int64_t)(r - R) * horizon + done + s) * q;
+    const int g = r / vall, vi = r % vall;
+    if (done + s >= horizon || vi >= V) return;
+    const int64_t orow = (int64_t)(g < batch ? g : g - batch) * V + vi;
+    float* dst = (g < batch ? out : mir) + (orow * horizon + done + s) * q;
     dst[i] = qs[idx];
 }
 
 // blockDecode's feedback (forecaster.zig:512-555) for target rows: the block's medians (0 when not
 // finite or at least the extreme threshold) become observed steps [t, t + blen) of the context.
-__global__ void ts_feedback(const float* qs, int rows, int blen, int q, int median, float extreme, float* ctx,
-                            uint8_t* mask, int cap_t, int t) {
+__global__ void ts_feedback(const float* qs, int rows, int vall, int V, int blen, int q, int median, float extreme,
+                            float* ctx, uint8_t* mask, int cap_t, int t) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)rows * blen) return;
     const int r = (int)(idx / blen), s = (int)(idx % blen);
+    if (r % vall >= V) return;  // covariate rows: the window already holds their next steps
     float mv = qs[idx * q + median];
     if (!isfinite(mv) || fabsf(mv) >= extreme) mv = 0.f;
     ctx[(int64_t)r * cap_t + t + s] = mv;
@@ -435,23 +538,25 @@ __global__ void ts_cap_bounds(const float* ctx, const uint8_t* mask, int cap_t, 
 // forecast's end (forecaster.zig:107-140, finish :163-178): each pass capped to its own bounds
 // (std.math.clamp: @max(lo, @min(x, hi))), the mirrored pass averaged in level-reversed order, and
 // series whose observed values are all non-negative clipped at 0.
-__global__ void ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R, int horizon,
-                         int q, int cap, int symmetric, int clip) {
+__global__ void ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R, int V,
+                         int vall, int horizon, int q, int cap, int symmetric, int clip) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)R * horizon) return;
     const int r = (int)(idx / horizon);
+    // bounds are per context row: target i of series s is row s * vall + i, its mirror R / V groups on
+    const int fr = (r / V) * vall + r % V, mr = fr + (R / V) * vall;
     float* o = out + idx * q;
     float v[32];
     for (int j = 0; j < q; j++) {
         float f = o[j];
-        if (cap) f = fmaxf(bounds[2 * r], fminf(f, bounds[2 * r + 1]));
+        if (cap) f = fmaxf(bounds[2 * fr], fminf(f, bounds[2 * fr + 1]));
         v[j] = f;
     }
     if (symmetric) {
         const float* m = mir + idx * q;
         for (int j = 0; j < q; j++) {
             float g = m[q - 1 - j];
-            if (cap) g = fmaxf(bounds[2 * (R + r)], fminf(g, bounds[2 * (R + r) + 1]));
+            if (cap) g = fmaxf(bounds[2 * mr], fminf(g, bounds[2 * mr + 1]));
             const float s = v[j] + -g;
             v[j] = 0.5f * s;
         }
@@ -470,18 +575,19 @@ hipError_t launch_ts_stats(const TsStatsParams& p, hipStream_t s) {
 }
 
 hipError_t launch_ts_features(const float* ctx, const uint8_t* mask, int cap_t, const float* loc, const float* scale,
-                              int cap_p, int rows, int p0, int l, int ps, int use_asinh, float* feats, hipStream_t s) {
+                              int cap_p, int rows, int p0, int l, int ps, int use_asinh, const uint8_t* no_asinh,
+                              float* feats, hipStream_t s) {
     const int64_t n = (int64_t)rows * (l - p0) * ps;
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(ts_features, dim3(blocks_for(n, 256)), dim3(256), 0, s, ctx, mask, cap_t, loc, scale, cap_p, rows,
-                       p0, l, ps, use_asinh, feats);
+                       p0, l, ps, use_asinh, no_asinh, feats);
     return hipGetLastError();
 }
 
-hipError_t launch_ts_rope_tables(const int* row_first, int groups, int vall, int n_tok, const TsRope& rp,
-                                 float* cos_t, float* sin_t, int* first_obs, hipStream_t s) {
+hipError_t launch_ts_rope_tables(const int* row_first, int groups, int vall, int n_tok, int ne, int shift,
+                                 const TsRope& rp, float* cos_t, float* sin_t, int* first_obs, hipStream_t s) {
     hipLaunchKernelGGL(ts_rope_tables, dim3(blocks_for((int64_t)n_tok * 32, 256), (unsigned)groups), dim3(256), 0, s,
-                       row_first, vall, n_tok, rp, cos_t, sin_t, first_obs);
+                       row_first, vall, n_tok, ne, shift, rp, cos_t, sin_t, first_obs);
     return hipGetLastError();
 }
 
@@ -526,17 +632,17 @@ hipError_t launch_ts_refine(float* qs, const float* loc, const float* scale, int
     return hipGetLastError();
 }
 
-hipError_t launch_ts_store_block(const float* qs, int rows, int R, int blen, int done, int horizon, int q, float* out,
-                                 float* mir, hipStream_t s) {
-    hipLaunchKernelGGL(ts_store_block, dim3(blocks_for((int64_t)rows * blen * q, 256)), dim3(256), 0, s, qs, rows, R,
-                       blen, done, horizon, q, out, mir);
+hipError_t launch_ts_store_block(const float* qs, int rows, int batch, int vall, int V, int blen, int done, int horizon,
+                                 int q, float* out, float* mir, hipStream_t s) {
+    hipLaunchKernelGGL(ts_store_block, dim3(blocks_for((int64_t)rows * blen * q, 256)), dim3(256), 0, s, qs, rows,
+                       batch, vall, V, blen, done, horizon, q, out, mir);
     return hipGetLastError();
 }
 
-hipError_t launch_ts_feedback(const float* qs, int rows, int blen, int q, int median, float extreme, float* ctx,
-                              uint8_t* mask, int cap_t, int t, hipStream_t s) {
-    hipLaunchKernelGGL(ts_feedback, dim3(blocks_for((int64_t)rows * blen, 256)), dim3(256), 0, s, qs, rows, blen, q,
-                       median, extreme, ctx, mask, cap_t, t);
+hipError_t launch_ts_feedback(const float* qs, int rows, int vall, int V, int blen, int q, int median, float extreme,
+                              float* ctx, uint8_t* mask, int cap_t, int t, hipStream_t s) {
+    hipLaunchKernelGGL(ts_feedback, dim3(blocks_for((int64_t)rows * blen, 256)), dim3(256), 0, s, qs, rows, vall, V,
+                       blen, q, median, extreme, ctx, mask, cap_t, t);
     return hipGetLastError();
 }
 
@@ -554,10 +660,10 @@ hipError_t launch_ts_cap_bounds(const float* ctx, const uint8_t* mask, int cap_t
     return hipGetLastError();
 }
 
-hipError_t launch_ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R,
-                           int horizon, int q, int cap, int symmetric, int clip, hipStream_t s) {
+hipError_t launch_ts_final(float* out, const float* mir, const float* bounds, const uint8_t* nonneg, int R, int V,
+                           int vall, int horizon, int q, int cap, int symmetric, int clip, hipStream_t s) {
     hipLaunchKernelGGL(ts_final, dim3(blocks_for((int64_t)R * horizon, 128)), dim3(128), 0, s, out, mir, bounds, nonneg,
-                       R, horizon, q, cap, symmetric, clip);
+                       R, V, vall, horizon, q, cap, symmetric, clip);
     return hipGetLastError();
 }
 

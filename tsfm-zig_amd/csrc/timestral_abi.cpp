@@ -1,9 +1,11 @@
 // extern "C" tsfm_timestral_forecast (include/tsfm_attn.h): the Timestral forecaster on the device.
 //
 // Reference: src/timestral/forecaster.zig forecast (:57-180), forecastRaw (:303-421), blockDecode
-// (:423-563), refineBlock (:582-662) and src/timestral/model.zig predictBlock (:220-432), for series
-// whose rows are all target variates (no covariates). The forward and the mirrored pass of the
-// symmetric average run as one batch: the mirrored series are rows R..2R-1 of every launch.
+// (:423-563), refineBlock (:582-662) and src/timestral/model.zig predictBlock (:220-432), with
+// numeric past-only and known-future covariate rows after each series' targets. The forward and
+// the mirrored pass of the symmetric average run as one batch: the mirrored series are groups
+// batch..2 batch-1 of every launch. With covariates each block re-encodes its window (the context
+// plus the horizon's known futures or blanks), as the reference does.
 //
 // The reference re-encodes the whole grown context for every decode block (blockDecode calls
 // predictBlock on the full context). Without covariates every encoder layer is causal over
@@ -92,7 +94,11 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
         return fail(TSFM_E_UNSUPPORTED, "patch %d, d_model %d, heads %d, mlp_hidden %d", ps, d, nh, hid);
     if (q < 1 || q > 32 || M.quantile_knots == nullptr) return fail(TSFM_E_UNSUPPORTED, "1 to 32 quantile knots");
     if (M.rope_dim <= 0 || M.rope_dim % 2 || M.rope_dim > 64) return fail(TSFM_E_INVALID, "bad rope_dim %d", M.rope_dim);
-    if (a->variates > 16) return fail(TSFM_E_UNSUPPORTED, "at most 16 variates per series");
+    if (a->n_past < 0 || a->n_known < 0) return fail(TSFM_E_INVALID, "negative covariate count");
+    if ((a->n_past > 0 && !a->past) || (a->n_known > 0 && !a->known))
+        return fail(TSFM_E_INVALID, "a covariate count without its array");
+    if (a->variates + a->n_past + a->n_known > 16)
+        return fail(TSFM_E_UNSUPPORTED, "at most 16 rows (variates and covariates) per series");
     if (M.block_size <= 0 || M.n_layers < 0 || (M.n_layers > 0 && M.layers == nullptr))
         return fail(TSFM_E_INVALID, "bad block_size or layers");
     if (!a->inputs || !a->observed || !a->out || !M.forecast_query || !M.out_norm)
@@ -132,14 +138,20 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     if ((rc = ensure_ready()) != TSFM_OK) return rc;
 
     // ---- sizes ----
-    const int V = a->variates, R = a->batch * V, rows = a->symmetric_averaging ? 2 * R : R, groups = rows / V;
+    const int V = a->variates, R = a->batch * V, n_cov = a->n_past + a->n_known, vall = V + n_cov;
+    const bool cov = n_cov > 0;
+    const int groups = a->symmetric_averaging ? 2 * a->batch : a->batch, rows = groups * vall;
+    uint32_t role_words[4] = {0, 0, 0, 0};  // model.Role per row of a series, byte i = row i
+    for (int i = 0; i < vall; i++)
+        role_words[i / 4] |= (uint32_t)(i < V ? 0 : i < V + a->n_past ? 1 : tsfm::kRoleKnown) << (8 * (i % 4));
     const int max_context = a->max_context > 0 ? a->max_context : M.context_length;
     if (max_context <= 0) return fail(TSFM_E_INVALID, "max_context");
     const int per_shot = std::min(a->per_shot_patches > 0 ? a->per_shot_patches : 32, M.block_size);
     const int keep = std::min(a->len, max_context), t_first = (keep + ps - 1) / ps * ps;
     const int total_patches = (a->horizon + ps - 1) / ps;
-    const int cap_t = t_first + total_patches * ps, cap_p = cap_t / ps, cap_tok = cap_p + per_shot;
-    const int sl_max = cap_p + per_shot;
+    const int cap_t = t_first + total_patches * ps, cap_p = cap_t / ps;
+    const int cap_tok = cap_p + per_shot + (cov ? per_shot : 0), sl_max = cap_tok;  // cov: window + decoder
+    const int hpad = total_patches * ps;
     if ((int64_t)rows * cap_tok * 3 * d > 0x7fffffffLL * 4) return fail(TSFM_E_UNSUPPORTED, "too large");
     hipStream_t s = static_cast<hipStream_t>(a->stream);
 
@@ -150,7 +162,7 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     const size_t at_loc = plan.take(R4 * cap_p), at_scale = plan.take(R4 * cap_p), at_kv = plan.take((size_t)rows * cap_p);
     const size_t at_state = plan.take((size_t)rows * 4 * 8), at_fold = plan.take((size_t)rows * 3 * 8);
     const size_t at_rfirst = plan.take(R4), at_first = plan.take((size_t)groups * 4), at_nonneg = plan.take((size_t)R);
-    const size_t at_bounds = plan.take(R4 * 2);
+    const size_t at_bounds = plan.take(R4 * 2);  // per context row
     const size_t tab = (size_t)groups * cap_tok * 32 * 4;
     const size_t at_cos = plan.take(tab), at_sin = plan.take(tab);
     const size_t at_feats = plan.take(R4 * cap_p * 2 * ps), at_eh = plan.take(R4 * cap_p * M.patch_proj.hid);
@@ -165,6 +177,8 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     const size_t at_qs = plan.take(R4 * per_shot * ps * q), at_fr = plan.take(R4 * per_shot * 2);
     const size_t at_mir = plan.take((size_t)R * a->horizon * q * 4);
     const size_t at_part = plan.take(tsfm::kSplitWorkspaceBytes);
+    const size_t at_kf = plan.take((size_t)rows * hpad * 4 + 4), at_kfm = plan.take((size_t)rows * hpad + 1);
+    const size_t at_noasinh = plan.take((size_t)rows);
     char* buf = nullptr;
     bool owned = false;
     hipError_t e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotTimestralForecast, plan.off, &buf, &owned);
@@ -204,22 +218,37 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     const float eps = M.norm_eps;
 
     auto run = [&]() -> hipError_t {
-        hipError_t e2 = tsfm::launch_ts_context(a->inputs, a->observed, R, rows, a->len, keep, t_first, ctx[0], mask[0],
-                                                cap_t, U8(at_nonneg), s);
+        tsfm::TsContextParams cp{};
+        cp.inputs = a->inputs; cp.observed = a->observed; cp.past = a->past; cp.known = a->known;
+        cp.batch = a->batch; cp.V = V; cp.n_past = a->n_past; cp.n_known = a->n_known; cp.vall = vall; cp.rows = rows;
+        cp.t0 = a->len; cp.keep = keep; cp.t = t_first; cp.horizon = a->horizon; cp.hpad = hpad; cp.cap_t = cap_t;
+        cp.ctx = ctx[0]; cp.mask = mask[0]; cp.kf = F(at_kf); cp.kfm = U8(at_kfm); cp.nonneg = U8(at_nonneg);
+        hipError_t e2 = tsfm::launch_ts_context(cp, s);
         if (e2 != hipSuccess) return e2;
-        bool cache = a->kv_cache != 0;
+        bool cache = a->kv_cache != 0 && !cov;
+        const int known_from = V + a->n_past;  // first known-future row of a series
         int t = t_first, remaining = total_patches, done = 0;
         int stats_from = 0;  // first step of the window whose statistics are not computed yet
         int p0 = 0;          // first token of this block's encoder run: the cache holds tokens [0, p0)
         bool tables_valid = false;
         for (int block_no = 0; remaining > 0; block_no++) {
-            const int h = std::min(per_shot, remaining), blen = h * ps, l = t / ps, ne = l, m = ne - p0, sl = m + h;
+            const int h = std::min(per_shot, remaining), blen = h * ps, l = t / ps;
+            // With covariates the encoder covers the window [0, t + blen): the block's known
+            // futures and blanks are written after the context first (model.zig:253-273).
+            const int ne = cov ? l + h : l, m = ne - p0, sl = m + h, w = ne * ps;
+            if (cov && (e2 = tsfm::launch_ts_window(ctx[cur], mask[cur], cap_t, t, blen, F(at_kf), U8(at_kfm), hpad,
+                                                    done, vall, known_from, rows, s)) != hipSuccess)
+                return e2;
             // 1. causal statistics, key validity and first observation of the new steps
             tsfm::TsStatsParams sp{};
             sp.ctx = ctx[cur]; sp.mask = mask[cur]; sp.cap_t = cap_t; sp.cap_p = cap_p; sp.rows = rows; sp.ps = ps;
-            sp.from = stats_from; sp.t = t; sp.attend_missing = M.attend_missing ? 1 : 0; sp.min_scale = M.minimum_scale;
+            sp.from = stats_from; sp.t = w; sp.attend_missing = M.attend_missing ? 1 : 0; sp.min_scale = M.minimum_scale;
             sp.loc = loc; sp.scale = scale; sp.key_valid = kv; sp.row_first = row_first; sp.state = state; sp.fold = fold;
             if ((e2 = tsfm::launch_ts_stats(sp, s)) != hipSuccess) return e2;
+            if (a->n_known > 0 &&
+                (e2 = tsfm::launch_ts_known_stats(ctx[cur], mask[cur], cap_t, w, ps, rows, vall, known_from,
+                                                  M.minimum_scale, loc, scale, cap_p, U8(at_noasinh), s)) != hipSuccess)
+                return e2;
             if (block_no == 0) {
                 if (cap_k > 0 && (e2 = tsfm::launch_ts_cap_bounds(ctx[cur], mask[cur], cap_t, t, ps, scale, cap_p, rows,
                                                                   cap_k, F(at_bounds), s)) != hipSuccess)
@@ -234,20 +263,21 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                         return e2;
                     for (int g = 0; g < groups && cache; g++) {
                         bool any = false;
-                        for (int i = 0; i < V; i++) any = any || rf[(size_t)(g * V + i)] >= 0;
+                        for (int i = 0; i < vall; i++) any = any || rf[(size_t)(g * vall + i)] >= 0;
                         cache = any;
                     }
                 }
             }
             if (!tables_valid) {
-                if ((e2 = tsfm::launch_ts_rope_tables(row_first, groups, V, cap_tok, rope, cos_t, sin_t, first_obs, s)) !=
-                    hipSuccess)
+                if ((e2 = tsfm::launch_ts_rope_tables(row_first, groups, vall, cap_tok, ne, ne - l, rope, cos_t, sin_t,
+                                                      first_obs, s)) != hipSuccess)
                     return e2;
                 tables_valid = cache;
             }
             // 2. patch embedding of the new patches; [encoder tokens; forecast queries]
-            if ((e2 = tsfm::launch_ts_features(ctx[cur], mask[cur], cap_t, loc, scale, cap_p, rows, p0, l, ps,
-                                               M.use_asinh ? 1 : 0, F(at_feats), s)) != hipSuccess ||
+            if ((e2 = tsfm::launch_ts_features(ctx[cur], mask[cur], cap_t, loc, scale, cap_p, rows, p0, ne, ps,
+                                               M.use_asinh ? 1 : 0, a->n_known > 0 ? U8(at_noasinh) : nullptr,
+                                               F(at_feats), s)) != hipSuccess ||
                 (e2 = resblock_silu(M.patch_proj, F(at_feats), rows * m, F(at_emb), F(at_eh), F(at_er), s)) !=
                     hipSuccess ||
                 (e2 = tsfm::launch_ts_assemble(F(at_emb), M.forecast_query, X, rows, m, h, d, s)) != hipSuccess)
@@ -281,7 +311,7 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                         pp.y0_tok = pp.y1_tok = pp.y2_tok = 3 * d;
                         pp.y0_batch = pp.y1_batch = pp.y2_batch = tb;
                         pp.rope_cos = cos_t + (int64_t)p0 * 32; pp.rope_sin = sin_t + (int64_t)p0 * 32;
-                        pp.rope_table_stride = (int64_t)cap_tok * 32; pp.rope_rows_per_table = V; pp.rope_row0 = 0;
+                        pp.rope_table_stride = (int64_t)cap_tok * 32; pp.rope_rows_per_table = vall; pp.rope_row0 = 0;
                         if ((e2 = tsfm::launch_proj(pp, s)) != hipSuccess) return e2;
                         if (half && at.gate &&
                             (e2 = linear(XN, d, at.gate, d, d, nullptr, G, d, toks, tsfm::kEpiNone, nullptr, s)) !=
@@ -300,10 +330,29 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                         ap.o_tok = d; ap.o_batch = (int64_t)sl * d;
                         ap.key_valid = kv; ap.kv_batch = cap_p;
                         ap.B = rows; ap.H = nh; ap.n_q = m; ap.n_k = ne; ap.q_pos0 = p0; ap.scale = sm_scale;
-                        if ((e2 = attend(ap, TSFM_MASK_CAUSAL_KEYS)) != hipSuccess) return e2;
+                        if (!cov) {
+                            if ((e2 = attend(ap, TSFM_MASK_CAUSAL_KEYS)) != hipSuccess) return e2;
+                        } else {
+                            // Known-future rows read every valid key (TimeJob.attend :600-609): one launch
+                            // per row of a series, its groups batched, with that row's mask.
+                            for (int i = 0; i < vall; i++) {
+                                tsfm::Params ri = ap;
+                                const int64_t esz = half ? 2 : 4;
+                                ri.q = (char*)ap.q + i * tb * esz; ri.k = (char*)ap.k + i * tb * esz;
+                                ri.v = (char*)ap.v + i * tb * esz;
+                                ri.o = (char*)ap.o + i * (int64_t)sl * d * (half ? 2 : 4);
+                                ri.q_batch = ri.k_batch = ri.v_batch = vall * tb; ri.o_batch = vall * (int64_t)sl * d;
+                                ri.key_valid = kv + (int64_t)i * cap_p; ri.kv_batch = (int64_t)vall * cap_p;
+                                ri.B = groups;
+                                if ((e2 = attend(ri, i >= known_from ? TSFM_MASK_FULL_KEYS : TSFM_MASK_CAUSAL_KEYS)) !=
+                                    hipSuccess)
+                                    return e2;
+                            }
+                        }
+                        // Decoder queries read the valid context keys [0, l) and their own chain from ne.
                         ap.q = el((int64_t)ne * 3 * d);
                         ap.o = half ? (void*)(OH + (int64_t)m * d) : (void*)(OA + (int64_t)m * d);
-                        ap.n_q = h; ap.n_k = ne + h; ap.q_pos0 = ne; ap.ctx_keys = ne; ap.chain_start = ne;
+                        ap.n_q = h; ap.n_k = ne + h; ap.q_pos0 = ne; ap.ctx_keys = l; ap.chain_start = ne;
                         if ((e2 = attend(ap, TSFM_MASK_DECODER)) != hipSuccess) return e2;
                         if (half) {
                             if ((e2 = tsfm::launch_ts_from_bf16(OH, at.gate ? G : nullptr, OA, (int64_t)toks * d, s)) !=
@@ -322,7 +371,8 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                         vp.o = OA; vp.o_row = (int64_t)sl * d; vp.o_tok = d;
                         vp.gate = at.gate ? G : nullptr; vp.gate_row = (int64_t)sl * d; vp.gate_tok = d;
                         vp.key_valid = kv + p0; vp.kv_row = cap_p;
-                        vp.groups = groups; vp.vall = V; vp.n_tok = sl; vp.n_enc = m; vp.heads = nh; vp.cov = 0;
+                        vp.groups = groups; vp.vall = vall; vp.n_tok = sl; vp.n_enc = m; vp.heads = nh; vp.cov = cov ? 1 : 0;
+                        for (int i = 0; i < 4; i++) vp.roles[i] = role_words[i];
                         vp.scale = sm_scale;
                         if ((e2 = tsfm::launch_variate(vp, s)) != hipSuccess) return e2;
                     }
@@ -347,15 +397,15 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
             if (h > 1 && (e2 = tsfm::launch_ts_refine(qs, loc, scale, cap_p, l, fold, rows, h, ps, q, median,
                                                       M.minimum_scale, F(at_fr), s)) != hipSuccess)
                 return e2;
-            if ((e2 = tsfm::launch_ts_store_block(qs, rows, R, blen, done, a->horizon, q, out, F(at_mir), s)) !=
-                hipSuccess)
+            if ((e2 = tsfm::launch_ts_store_block(qs, rows, a->batch, vall, V, blen, done, a->horizon, q, out, F(at_mir),
+                                                  s)) != hipSuccess)
                 return e2;
             remaining -= h;
             done += blen;
             if (remaining == 0) break;
             // 5. the medians become context (blockDecode :512-560)
-            if ((e2 = tsfm::launch_ts_feedback(qs, rows, blen, q, median, a->extreme_value_threshold, ctx[cur],
-                                               mask[cur], cap_t, t, s)) != hipSuccess)
+            if ((e2 = tsfm::launch_ts_feedback(qs, rows, vall, V, blen, q, median, a->extreme_value_threshold,
+                                               ctx[cur], mask[cur], cap_t, t, s)) != hipSuccess)
                 return e2;
             const int nt = t + blen;
             if (nt > max_context) {
@@ -379,7 +429,8 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                 tables_valid = false;
             }
         }
-        return tsfm::launch_ts_final(out, F(at_mir), F(at_bounds), U8(at_nonneg), R, a->horizon, q, cap_k > 0 ? 1 : 0,
+        return tsfm::launch_ts_final(out, F(at_mir), F(at_bounds), U8(at_nonneg), R, V, vall, a->horizon, q,
+                                     cap_k > 0 ? 1 : 0,
                                      a->symmetric_averaging ? 1 : 0, a->clip_nonnegative ? 1 : 0, s);
     };
     e = run();

@@ -254,7 +254,8 @@ class TimestralForecastArgs(ctypes.Structure):
                [("quantile_real_cap_k", ctypes.c_float), ("extreme_value_threshold", ctypes.c_float),
                 ("symmetric_averaging", ctypes.c_int32), ("clip_nonnegative", ctypes.c_int32),
                 ("kv_cache", ctypes.c_int32), ("flags", ctypes.c_uint32), ("out", ctypes.c_void_p),
-                ("stream", ctypes.c_void_p)]
+                ("stream", ctypes.c_void_p), ("past", ctypes.c_void_p), ("known", ctypes.c_void_p),
+                ("n_past", ctypes.c_int32), ("n_known", ctypes.c_int32)]
 
 
 class Chronos2EncodeArgs(ctypes.Structure):
@@ -1142,12 +1143,14 @@ class KvCache:
 def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, variates: int, length: int, horizon: int,
                             max_context: int = 0, per_shot: int = 32, cap_k: float = 1e4, extreme: float = 1e30,
                             symmetric: bool = True, clip_nonnegative: bool = True, kv_cache: bool = True,
-                            attn_bf16: bool = False, stream=None) -> "TimestralForecastArgs":
+                            attn_bf16: bool = False, past=None, known=None, stream=None) -> "TimestralForecastArgs":
     """``tsfm_timestral_forecast_args`` over device tensors. `model` holds the config and device
     weights (keys as in the reference checkpoint's layout: patch_proj/head ResBlocks, layers with
     attns [is_time, norm, qkv (permuted), out, gate] and mlp_norm/w12/w3, forecast_query, out_norm,
     knots (host float64 array)). attn_bf16 sets TSFM_TIMESTRAL_BF16_ATTN (time attention on the bf16
-    matrix cores over a bf16 K/V cache). The returned block keeps references to what it points at."""
+    matrix cores over a bf16 K/V cache). past (batch, n_past, length) and known (batch, n_known,
+    length + horizon) are numeric covariates, NaN = missing (forecaster.zig:36-46). The returned block
+    keeps references to what it points at."""
     import numpy as np
 
     layers = (TimestralLayer * max(1, len(model["layers"])))()
@@ -1171,16 +1174,18 @@ def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, vari
                               quantile_real_cap_k=cap_k, extreme_value_threshold=extreme,
                               symmetric_averaging=int(symmetric), clip_nonnegative=int(clip_nonnegative),
                               kv_cache=int(kv_cache), flags=DEVICE_PTRS | (TIMESTRAL_BF16_ATTN if attn_bf16 else 0),
-                              out=_ptr(out), stream=_stream_of(out, stream))
-    a._keep = (layers, knots, model, inputs, observed, out)
+                              out=_ptr(out), stream=_stream_of(out, stream), past=_ptr(past), known=_ptr(known),
+                              n_past=0 if past is None else int(past.shape[1]),
+                              n_known=0 if known is None else int(known.shape[1]))
+    a._keep = (layers, knots, model, inputs, observed, out, past, known)
     return a
 
 
 def timestral_forecast(out, inputs, observed, model: dict, batch: int, variates: int, length: int, horizon: int,
                        **kw) -> int:
-    """Timestral forecaster.forecast (src/timestral/forecaster.zig:57-180) without covariates, on
-    device tensors: inputs (batch, variates, length) f32, observed (same) uint8, out (batch,
-    variates, horizon, q). Returns the ABI code."""
+    """Timestral forecaster.forecast (src/timestral/forecaster.zig:57-180) on device tensors: inputs
+    (batch, variates, length) f32, observed (same) uint8, out (batch, variates, horizon, q);
+    optional numeric covariates past= / known= (see timestral_forecast_args). Returns the ABI code."""
     args = timestral_forecast_args(out, inputs, observed, model, batch, variates, length, horizon, **kw)
     return int(load().tsfm_timestral_forecast(ctypes.byref(args)))
 
