@@ -206,3 +206,11 @@ def test_timestral_forecast_covariate_errors(ta, gpu_ready):
     big = torch.zeros((2, 16, x.shape[1] + 40), device="cuda")
     rc = ta.timestral_forecast(out, xd, od, _device_model(m), 2, 1, x.shape[1], 40, known=big)
     assert rc == ta.E_UNSUPPORTED  # 1 target + 16 covariate rows > 16
+    # config.zig:49-70: a schedule of time ops only cannot route a known future to the targets
+    # (error.KnownCovariatesUnsupported); past-only covariates still run.
+    rng = np.random.default_rng(46)
+    tm = _device_model(_ref.timestral_model(rng, d=128, nh=2, hid=256, schedule=("time", "time")))
+    kd, pd = torch.from_numpy(known).cuda(), torch.from_numpy(past).cuda()
+    assert ta.timestral_forecast(out, xd, od, tm, 2, 1, x.shape[1], 40, known=kd) == ta.E_UNSUPPORTED
+    assert "KnownCovariatesUnsupported" in ta.last_error()
+    assert ta.timestral_forecast(out, xd, od, tm, 2, 1, x.shape[1], 40, past=pd) == ta.OK, ta.last_error()

@@ -135,6 +135,26 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
         for (const float* p : {ly.mlp_norm, ly.w12, ly.w3})
             if (!aligned(p, 16)) return fail(TSFM_E_UNSUPPORTED, "device pointers must be 16-byte aligned");
     }
+    if (a->n_known > 0) {
+        // Config.supportsKnownCovariates (src/timestral/config.zig:49-70): some time op must be
+        // followed by at least one more time op and at least one variate op.
+        std::vector<bool> ops;
+        for (int li = 0; li < M.n_layers; li++)
+            for (int ai = 0; ai < M.layers[li].n_attn; ai++) ops.push_back(M.layers[li].attn[ai].is_time != 0);
+        bool routes = false;
+        for (size_t i = 0; i < ops.size() && !routes; i++) {
+            if (!ops[i]) continue;
+            bool any_time = false, any_variate = false;
+            for (size_t j = i + 1; j < ops.size(); j++) {
+                any_time = any_time || ops[j];
+                any_variate = any_variate || !ops[j];
+            }
+            routes = any_time && any_variate;
+        }
+        if (!routes)
+            return fail(TSFM_E_UNSUPPORTED, "known covariates: the layer schedule cannot route them to the targets "
+                                            "(error.KnownCovariatesUnsupported)");
+    }
     if ((rc = ensure_ready()) != TSFM_OK) return rc;
 
     // ---- sizes ----
