@@ -11,8 +11,9 @@ over a sample of the same inputs, with the parity of the timed output against it
 
 The default run adds `other_configs`, each measured the same way (timed steps, roofline, CPU
 baseline, parity and the reference-derived parity bar): 1 = bolt_forecast, 2 = bolt, 4 = decode,
-5 = prefill, and 3-e2e = chronos2_forecast, whose whole forecasts per second are the line's
-`series_forecasts_per_s` (the attention call alone gives `attention_series_per_s`).
+5 = prefill, 3-e2e = chronos2_forecast, whose whole forecasts per second are the line's
+`series_forecasts_per_s` (the attention call alone gives `attention_series_per_s`), and 4-e2e =
+timestral_forecast, the whole Timestral forecast at the decode shape with and without its cache.
 `--workload X` measures X alone.
 
 Other workloads (parity-test shapes, measured the same way):
@@ -29,6 +30,10 @@ Other workloads (parity-test shapes, measured the same way):
   bolt_forecast  the whole Chronos-Bolt-small forecast at the end-to-end configuration: 16 series
            x 512 raw steps (sinusoid + trend + noise, 2 % NaN) in, 9 quantiles x 64 steps out; the
            instance norm, patching and inverse norm run on the device around bolt_forward
+  timestral_forecast  the whole Timestral forecast at the decode shape (d_model 1024, 16 heads, 4
+           layers): 128 series x 4096 steps in, 8 decode blocks of 32 patches (4096 steps) out, with
+           the K/V cache; the same forecast re-encoding every block (the reference's decode) is
+           timed beside it (`reencode`, `cache_speedup`)
   chronos2_forecast  the whole Chronos-2-base forecast at the attention's shape: 64 series x 8192
            raw steps in (512 patches + REG + 64 future = 577 tokens), 21 quantiles x 1024 steps out
   encoder  the Chronos-2 encoder stack at the Chronos-2-base size (12 layers, d_model 768, 12 heads,
@@ -37,7 +42,7 @@ Other workloads (parity-test shapes, measured the same way):
 
     python bench.py [--steps K] [--warmup W] [--no-cpu]
                     [--workload chronos2|bolt|prefill|decode|variate|proj|encoder|bolt_forward|bolt_forecast|
-                     chronos2_forecast]
+                     chronos2_forecast|timestral_forecast]
     python bench.py --copy-mib N    # plain N MiB device copy: calibrates the HBM byte counters
 """
 import argparse
@@ -512,14 +517,76 @@ def run_chronos2_forecast(torch, ta, workloads, peak):
                  "TFLOP/s", 1)
 
 
+def run_timestral_forecast(torch, ta, workloads, peak):
+    w = workloads.timestral_forecast()
+    a, m = w.arrays, w.meta
+    model = m["model"]
+    cu = lambda x: None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    dm = dict(model)
+    dm["patch_proj"] = {k: cu(v) for k, v in model["patch_proj"].items()}
+    dm["head"] = {k: cu(v) for k, v in model["head"].items()}
+    dm["forecast_query"], dm["out_norm"] = cu(model["forecast_query"]), cu(model["out_norm"])
+    dm["layers"] = [dict(attns=[{k: (cu(v) if isinstance(v, np.ndarray) else v) for k, v in at.items()}
+                                for at in ly["attns"]], mlp_norm=cu(ly["mlp_norm"]), w12=cu(ly["w12"]), w3=cu(ly["w3"]))
+                    for ly in model["layers"]]
+    x, obs = cu(a["inputs"]), cu(a["observed"])
+    T, hz, q = m["context"], m["horizon"], model["q"]
+    outs = {c: torch.empty((w.B, 1, hz, q), dtype=torch.float32, device="cuda") for c in (True, False)}
+    # Argument blocks built once, as a caller holding a loaded model does; a step is one
+    # forecaster.forecast call with the K/V cache (blocks after the first run only their new
+    # patches and decoder tokens). The same call without the cache re-encodes the grown context
+    # every block, as the reference's blockDecode does (src/timestral/forecaster.zig:466-561).
+    args = {c: ta.timestral_forecast_args(outs[c], x, obs, dm, w.B, 1, T, hz, per_shot=m["per_shot"], kv_cache=c)
+            for c in (True, False)}
+    fn = ta.load().tsfm_timestral_forecast
+
+    def step(cached=True):
+        _check(ta, fn(ctypes.byref(args[cached])))
+
+    def cpu_leg(B, lib=None):
+        orc = _orc(lib)
+        t0 = time.perf_counter()
+        rc, want = orc.timestral_forecast(cpu_threads(), model, a["inputs"][:B], a["observed"][:B], B, 1, T, hz, 0,
+                                          m["per_shot"])
+        if rc != 0:
+            raise RuntimeError(f"oracle timestral_forecast returned {rc}")
+        return time.perf_counter() - t0, want, orc.lanes
+
+    def reencode(steps):
+        """The uncached forecast (the reference's re-encoding decode) timed over `steps` calls."""
+        step(False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(False)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        gap = float(((outs[True] - outs[False]).abs() / outs[False].abs().clamp(min=1)).max())
+        return {"ms_per_step": round(ms, 3), "value": round(m["reencode_flops"] / (ms * 1e-3) / 1e12, 3),
+                "unit": "TFLOP/s", "flops": m["reencode_flops"], "steps": steps,
+                "series_forecasts_per_s": round(w.B / (ms * 1e-3), 2), "cached_vs_reencoded_max_scaled_diff": gap}
+
+    config = {"workload": "timestral_forecast", "series": w.B, "variates": 1, "context": T, "horizon": hz,
+              "per_shot_patches": m["per_shot"], "blocks": m["blocks"], "patch": model["ps"], "d_model": m["d_model"],
+              "H": w.H, "mlp_hidden": m["hid"], "layers": m["schedule"], "quantiles": q, "asinh": True,
+              "symmetric_averaging": True, "kv_cache": True, "missing": "oldest 0-25 % + 2 %",
+              "weights": "random-init f32", "input": "sinusoid (period 24, amplitude 10) + trend + N(0,1)"}
+    b = Bench(w, step, lambda: outs[True].cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
+              "TFLOP/s", 1)
+    b.cpu_flops = m["reencode_flops"]  # the CPU leg runs the reference's re-encoding decode
+    b.extra = reencode
+    return b
+
+
 WORKLOADS = {"chronos2": run_chronos2, "bolt": run_bolt, "prefill": run_prefill, "decode": run_decode,
              "variate": run_variate, "proj": run_proj, "encoder": run_encoder, "bolt_forward": run_bolt_forward,
-             "bolt_forecast": run_bolt_forecast, "chronos2_forecast": run_chronos2_forecast}
+             "bolt_forecast": run_bolt_forecast, "chronos2_forecast": run_chronos2_forecast,
+             "timestral_forecast": run_timestral_forecast}
 # The default run: the headline (the Chronos-2 time attention, the metric's shape) and, beside it,
 # every other synthetic shape of the benchmark plus the whole Chronos-2 forecast at the headline's
 # shape (the metric's series-forecasts/sec).
 OTHER_CONFIGS = [("1", "bolt_forecast"), ("2", "bolt"), ("4", "decode"), ("5", "prefill"),
-                 ("3-e2e", "chronos2_forecast")]
+                 ("3-e2e", "chronos2_forecast"), ("4-e2e", "timestral_forecast")]
 SPINUP_S = 0.25  # untimed load before the timed region, after the --warmup steps
 CPU_SAMPLE_S = 10.0  # timed CPU work in the cpu_baseline leg (the sample is repeated up to this)
 
@@ -604,6 +671,10 @@ def measure(torch, bench, steps: int, warmup: int, do_cpu: bool) -> dict:
         },
         "cpu_baseline": None,
     }
+    extra = getattr(bench, "extra", None)
+    if extra is not None:  # a second timing beside the step (the Timestral forecast without its cache)
+        out["reencode"] = extra(min(steps, 3))
+        out["cache_speedup"] = round(out["reencode"]["ms_per_step"] / ms_per_step, 2)
     if not do_cpu:
         return out
     n_series = min(w.B, bench.cpu_default)
@@ -614,7 +685,7 @@ def measure(torch, bench, steps: int, warmup: int, do_cpu: bool) -> dict:
         dt += bench.cpu_leg(n_series)[0]
         passes += 1
     got = bench.output()[:n_series]
-    sample_flops = w.flops * n_series / w.B * passes
+    sample_flops = getattr(bench, "cpu_flops", w.flops) * n_series / w.B * passes
     out["cpu_baseline"] = {
         "value": round(sample_flops / dt / 1e12, 5),
         "unit": "TFLOP/s",

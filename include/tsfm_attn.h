@@ -431,27 +431,34 @@ int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args *args);
 
 /* ---------------------------------------------------------------------------------------------
  * Timestral forecast: forecaster.forecast (src/timestral/forecaster.zig:57-180) of a batch of
- * series whose rows are all target variates (no covariates; with covariates the caller keeps its
- * CPU path), f32, device memory only, asynchronous on `stream` except for one synchronisation
- * after the first decode block (to learn whether every series has an observation). The whole
- * forecast runs on the device: forecastRaw's forward-fill and left padding (:303-394), the decode
- * loop of blockDecode (:423-563) with predictBlock (src/timestral/model.zig:220-432: causal
- * per-patch statistics, patch embedding, the time / variate transformer, the monotone quantile
- * head) and refineBlock (:582-662), the median feedback and max_context window, the quantile cap
- * (:396-418), the mirrored pass of the symmetric average (:107-137, run in the same batch) and the
- * non-negative clip (:163-178). A forecast whose output contains NaN is returned as is (the
- * reference reports error.DegenerateInput).
- * With kv_cache set, decode blocks after the first run only their new patches and decoder tokens,
- * attending over the time-attention K/V the earlier blocks computed (the reference re-encodes the
- * whole context every block; the result is the same computation, up to f32 summation order);
- * blocks after a max_context drop, and every block of a batch that holds a series with no
- * observation, re-encode in full.
+ * series of target variates, optionally with numeric past-only and known-future covariate rows
+ * (Covariates.past / .known, :36-46), f32, device memory only, asynchronous on `stream`.
+ * Categorical covariates (Covariates.cat_past / .cat_known) are target-encoded into numeric rows
+ * by the caller first (tsfm_timestral_encode_categorical below) and passed as past / known rows.
+ * The whole forecast runs on the device: forecastRaw's forward-fill and left padding (:303-394),
+ * the decode loop of blockDecode (:423-563) with predictBlock (src/timestral/model.zig:220-432:
+ * causal per-patch statistics, patch embedding, the time / variate transformer, the monotone
+ * quantile head) and refineBlock (:582-662), the median feedback and max_context window, the
+ * quantile cap (:396-418), the mirrored pass of the symmetric average (:107-137, run in the same
+ * batch) and the non-negative clip (:163-178). A forecast whose output contains NaN is returned as
+ * is (the reference reports error.DegenerateInput).
+ * With kv_cache set and no covariates, decode blocks after the first run only their new patches
+ * and decoder tokens, attending over the time-attention K/V the earlier blocks computed (the
+ * reference re-encodes the whole context every block; the result is the same computation, up to
+ * f32 summation order); blocks after a max_context drop re-encode in full. With covariates the
+ * window depends on each block's horizon, so kv_cache is ignored and every block re-encodes.
  * With TSFM_TIMESTRAL_BF16_ATTN in flags the time attention runs on the bf16 matrix cores: the q/k/v
  * projections are rounded once to bf16 (after RoPE) into a bf16 K/V cache, the attention keeps f32
  * scores, softmax and accumulation, and its output is rounded to bf16 and widened back to f32 for
  * the gate and the out projection. Everything else stays f32. The reference has no such mode (its
  * time attention is f32); a bf16 forecast agrees with the f32 one to about 1e-2 of the forecast's
- * scale. */
+ * scale when the model works in linear space. With use_asinh the head's outputs are sinh-expanded,
+ * which turns bf16's relative rounding into a relative error of the forecast several times larger:
+ * that combination returns TSFM_E_UNSUPPORTED.
+ * Errors as the reference's: covariates with covariate_enabled == 0 (error.CovariatesUnsupported),
+ * known covariates with a schedule that cannot route them (error.KnownCovariatesUnsupported) return
+ * TSFM_E_UNSUPPORTED; a covariate array with a zero count, or a count without its array, returns
+ * TSFM_E_INVALID (error.InvalidInput). */
 typedef struct tsfm_timestral_attn {
     int32_t is_time;        /* 1: time attention (timeAttention :487-519); 0: variate (:525-544) */
     const float *norm;      /* (d) attn_norms.<i>.scale */
@@ -473,6 +480,7 @@ typedef struct tsfm_timestral_model {
     int32_t block_size, context_length;
     int32_t rope_dim;               /* rotated dims: head_dim * rope_partial_factor (config.zig:34-36) */
     int32_t use_asinh, attend_missing;
+    int32_t covariate_enabled;      /* config.covariate_enabled (config.zig:25; true in the reference) */
     float rope_theta, norm_eps, minimum_scale, quantile_width_factor;
     const double *quantile_knots;   /* (n_quantiles) host memory: increasing, containing 0.5 */
     tsfm_resblock patch_proj;       /* 2 patch -> 4 d -> d, act 1 (SiLU), with biases */

@@ -51,6 +51,7 @@ def naive_attend(q, k, v, allowed, scale, bias=None):
     allowed = np.asarray(allowed, bool).copy()
     empty = ~allowed.any(axis=1)
     allowed[empty, :] = True
+    s[empty, :] = 0.0  # equal scores: uniform weights
     s = np.where(allowed, s, -np.inf)
     s = s - s.max(axis=1, keepdims=True)
     p = np.where(allowed, np.exp(s), 0.0)
@@ -557,12 +558,14 @@ def timestral_predict_block_f64(m, ctx, obs, t, groups, vall, h, roles=None, kf=
     return out * scale[tgt, l - 1, None, None] + loc[tgt, l - 1, None, None]
 
 
-def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale):
+def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale, exact=False):
     """refineBlock (src/timestral/forecaster.zig:582-662) from its definition, with two-pass numpy
     statistics: horizon patch j is re-framed with the mean and std (ddof 1) of the observed context
     plus the medians of patches 0..j-1 mapped into their own frames (clipped around the context
-    mean), patch 0 keeping the context's last-patch frame."""
-    qs = np.asarray(qs, np.float32)
+    mean), patch 0 keeping the context's last-patch frame. The frames are kept in f32 as the
+    reference stores them; exact=True keeps every value in float64 instead."""
+    f = np.float64 if exact else np.float32
+    qs = np.asarray(qs, f)
     rows, hps, q = qs.shape
     h = hps // ps
     t = ctx.shape[1]
@@ -571,7 +574,7 @@ def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale):
     clip = np.sqrt(np.float64(np.finfo(np.float32).max)) / 1e3
     out = np.empty_like(qs)
     for r in range(rows):
-        loc0, scale0 = np.float32(loc[r, l - 1]), np.float32(scale[r, l - 1])
+        loc0, scale0 = f(loc[r, l - 1]), f(scale[r, l - 1])
         vals = np.asarray(ctx[r], np.float64)[np.asarray(obs[r], bool)]
         sinh_med = (qs[r, :, med].astype(np.float64) - np.float64(loc0)) / np.float64(scale0)
         offset = vals.mean() if vals.size else 0.0
@@ -580,8 +583,8 @@ def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale):
             mean = vals.mean() if vals.size else 0.0
             m2 = ((vals - mean) ** 2).sum()
             sc = max(np.sqrt(max(m2 / max(vals.size - 1.0, 1.0), 0.0)), min_scale)
-            lj.append(np.float32(mean))
-            sj.append(np.float32(sc))
+            lj.append(f(mean))
+            sj.append(f(sc))
             folded = np.clip(sinh_med[j * ps:(j + 1) * ps] * sc + mean - offset, -clip, clip) + offset
             vals = np.concatenate([vals, folded])
         lj[0], sj[0] = loc0, scale0
@@ -589,6 +592,66 @@ def timestral_refine_f64(qs, ctx, obs, ps, med, min_scale):
             a = (qs[r, s] - loc0) / scale0
             out[r, s] = a * sj[s // ps] + lj[s // ps]
     return out
+
+
+def timestral_forecast_f64(m, x, obs, b, v, horizon, per_shot=32, max_context=0, cap_k=1e4, extreme=1e30,
+                           symmetric=True, clip_nonnegative=True):
+    """forecaster.forecast (src/timestral/forecaster.zig:57-180) for target rows in float64, composed
+    from the definitions above: forecastRaw's context (forward fill, window, left padding), then
+    blockDecode (predict_block, refine_block when a block has more than one patch, medians fed back
+    as observed context, 0 when not finite or at least `extreme`, the oldest steps dropped past
+    max_context), the quantile cap at the context's observed range widened by cap_k times its last
+    patch scale, the symmetric average 0.5 (f(x) - reverse(f(-x))) over the levels, and the clip to
+    zero of series whose observed values are all non-negative. (b, v, horizon, q)."""
+    ps, q, med = m["ps"], m["q"], m["median"]
+    max_context = max_context or m["context_length"]
+    per_shot = min(per_shot, m["block_size"])
+    x = np.asarray(x, np.float32).reshape(b * v, -1)
+    obs = np.asarray(obs, bool).reshape(b * v, -1)
+
+    def raw(xs):
+        ctx, mask = timestral_context(xs, obs, max_context, ps)
+        ctx = ctx.astype(np.float64)
+        ctx0, mask0 = ctx.copy(), mask.copy()
+        out = np.zeros((b * v, horizon, q))
+        remaining, done = -(-horizon // ps), 0
+        while remaining:
+            block = min(per_shot, remaining)
+            blen = block * ps
+            qs = timestral_predict_block_f64(m, ctx, mask, ctx.shape[1], b, v, block)
+            if block > 1:
+                qs = timestral_refine_f64(qs, ctx, mask, ps, med, m["minimum_scale"], exact=True)
+            take = min(blen, horizon - done)
+            out[:, done:done + take] = qs[:, :take]
+            remaining -= block
+            done += blen
+            if not remaining:
+                break
+            fed = qs[:, :, med].copy()
+            fed[~np.isfinite(fed) | (np.abs(fed) >= extreme)] = 0.0
+            ctx = np.concatenate([ctx, fed], axis=1)
+            mask = np.concatenate([mask, np.ones_like(fed, bool)], axis=1)
+            if ctx.shape[1] > max_context:
+                keep = max(ps, max_context // ps * ps)
+                ctx, mask = ctx[:, -keep:], mask[:, -keep:]
+        if cap_k > 0:
+            _, sc = patch_stats_f64(ctx0, mask0, ps, m["minimum_scale"])
+            for r in range(b * v):
+                vals = ctx0[r][mask0[r]]
+                hi, lo = (vals.max(), vals.min()) if vals.size else (0.0, 0.0)
+                a = sc[r, -1] * cap_k
+                out[r] = np.clip(out[r], lo - a, hi + a)
+        return out
+
+    out = raw(x)
+    if symmetric:
+        out = 0.5 * (out - raw(-x)[..., ::-1])
+    if clip_nonnegative:
+        for r in range(b * v):
+            seen = obs[r] & np.isfinite(x[r])
+            if seen.any() and (x[r][seen] >= 0).all():
+                out[r] = np.maximum(out[r], 0.0)
+    return out.reshape(b, v, horizon, q)
 
 
 def timestral_context(inputs, observed, max_context, ps):

@@ -320,6 +320,66 @@ def test_chronos2_forecast_is_device_only(ta):
     assert "device" in ta.last_error()
 
 
+def _timestral_args(ta, **over):
+    """A tsfm_timestral_forecast_args block that passes validation up to the device: host buffers
+    stand in for the device pointers (validation reads only the host-side knots and layers)."""
+    buf = np.zeros(4096, np.float32)
+    knots = np.array([0.1, 0.5, 0.9])
+    layers = (ta.TimestralLayer * 1)()
+    layers[0].n_attn = 1
+    layers[0].attn[0] = ta.TimestralAttn(1, buf.ctypes.data, buf.ctypes.data, buf.ctypes.data, None)
+    layers[0].mlp_norm = layers[0].w12 = layers[0].w3 = buf.ctypes.data
+    def rb(i, h, o, biases):
+        r = ta.Resblock(**{f: buf.ctypes.data for f in ta.RESBLOCK_FIELDS})
+        if not biases:
+            r.hidden_b = r.output_b = r.residual_b = None
+        r.__setattr__("in", i)
+        r.hid, r.out, r.act = h, o, 1
+        return r
+    m = ta.TimestralModel(patch=16, d_model=128, heads=2, head_dim=64, mlp_hidden=256, n_layers=1, n_quantiles=3,
+                          block_size=32, context_length=2048, rope_dim=32, use_asinh=1, attend_missing=1,
+                          covariate_enabled=1, rope_theta=1e4, norm_eps=1e-6, minimum_scale=1e-6,
+                          quantile_width_factor=2.0, quantile_knots=knots.ctypes.data, patch_proj=rb(32, 512, 128, True),
+                          head=rb(128, 512, 48, False), forecast_query=buf.ctypes.data, out_norm=buf.ctypes.data,
+                          layers=layers)
+    a = ta.TimestralForecastArgs(model=m, inputs=buf.ctypes.data, observed=buf.ctypes.data, batch=1, variates=1,
+                                 len=64, horizon=16, quantile_real_cap_k=1e4, extreme_value_threshold=1e30,
+                                 symmetric_averaging=1, clip_nonnegative=1, kv_cache=1, flags=ta.DEVICE_PTRS,
+                                 out=buf.ctypes.data)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a, (buf, knots, layers)
+
+
+def test_timestral_forecast_validation_matches_the_reference_errors(ta):
+    """forecaster.zig:83-104 and the build's own limits, decided before any device work: a
+    covariate array with no rows is error.InvalidInput (TSFM_E_INVALID), covariates on a model with
+    covariate_enabled off are error.CovariatesUnsupported, row counts near INT32_MAX are refused
+    without overflow, and bf16 time attention with use_asinh is refused."""
+    lib = ta.load()
+    f = lambda a: lib.tsfm_timestral_forecast(ctypes.byref(a))
+    buf = np.zeros(64, np.float32)
+    a, keep = _timestral_args(ta, past=buf.ctypes.data, n_past=0)
+    assert f(a) == ta.E_INVALID and "InvalidInput" in ta.last_error()
+    a, keep = _timestral_args(ta, known=buf.ctypes.data, n_known=0)
+    assert f(a) == ta.E_INVALID
+    a, keep = _timestral_args(ta, n_known=2)  # a count without its array
+    assert f(a) == ta.E_INVALID
+    a, keep = _timestral_args(ta, past=buf.ctypes.data, n_past=(1 << 31) - 1)
+    assert f(a) == ta.E_UNSUPPORTED  # 1 + INT32_MAX rows: refused, not wrapped
+    a, keep = _timestral_args(ta, past=buf.ctypes.data, n_past=(1 << 31) - 1, known=buf.ctypes.data,
+                              n_known=(1 << 31) - 1, variates=(1 << 31) - 1)
+    assert f(a) == ta.E_UNSUPPORTED
+    a, keep = _timestral_args(ta, past=buf.ctypes.data, n_past=1)
+    a.model.covariate_enabled = 0
+    assert f(a) == ta.E_UNSUPPORTED and "CovariatesUnsupported" in ta.last_error()
+    a, keep = _timestral_args(ta, flags=ta.DEVICE_PTRS | ta.TIMESTRAL_BF16_ATTN)
+    assert f(a) == ta.E_UNSUPPORTED and "use_asinh" in ta.last_error()
+    if not ta.available():  # host buffers stand in for device memory: never launched
+        a, keep = _timestral_args(ta)
+        assert f(a) == ta.E_UNAVAILABLE  # the unchanged block passes validation, stops at the device
+
+
 _FUZZ = r'''
 import ctypes, math, os, random, sys
 sys.path.insert(0, %r)
@@ -399,14 +459,24 @@ for cls, fn in ((ta.VariateArgs, lib.tsfm_variate_attend), (ta.ProjArgs, lib.tsf
         rc = fn(ctypes.byref(a))
         assert rc in (0, 1, 2, 3), (cls.__name__, it, rc)
         codes.add(rc)
+fn = lib.tsfm_timestral_forecast
+fn.argtypes = [ctypes.POINTER(ta.TimestralForecastArgs)]
+fn.restype = ctypes.c_int
+for it in range(3000):  # model and forecast fields random (counts near INT32_MAX included); no layers array
+    a = ta.TimestralForecastArgs()
+    fill(a)
+    fill(a.model)
+    rc = fn(ctypes.byref(a))
+    assert rc in (0, 1, 2, 3), ("timestral", it, rc)
+    codes.add(rc)
 print(sorted(codes))
 '''
 
 
 def test_validation_fuzz_returns_codes_and_never_launches():
     """4000 random argument blocks (extreme dims and strides, null and short buffers, bad dtypes,
-    masks, flags and scales) through tsfm_attn_fwd, and 3000 each through tsfm_variate_attend and
-    tsfm_qkv_project, in a fresh process with TSFM_HIP_DISABLE=1:
+    masks, flags and scales) through tsfm_attn_fwd, and 3000 each through tsfm_variate_attend,
+    tsfm_qkv_project and tsfm_timestral_forecast, in a fresh process with TSFM_HIP_DISABLE=1:
     every call returns one of the ABI's codes, and whatever passes validation stops at the
     disabled device instead of launching. Under the sanitizer run this is the check that the
     validation arithmetic has no overflow or out-of-bounds read."""

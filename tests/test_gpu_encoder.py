@@ -252,3 +252,39 @@ def test_chronos2_forecast_strided_rows_and_degenerate_series(ta, orc, orc16, gp
                for o_ in (orc, orc16))
     assert np.isfinite(got).all()
     _ref.assert_within_reference_bar(got, w8, w16)
+
+
+def test_chronos2_base_forecast_at_the_metric_shape(ta, orc, orc16, gpu_ready):
+    """The workload behind the benchmark's series-forecasts/s: the Chronos-2-base forecast of 64
+    series x 8192 raw steps (oldest 0-25 % missing, 2 % of the rest) with horizon 1024, 12 layers of
+    d_model 768, 12 heads, d_ff 3072, 21 quantiles, asinh space. All 64 series run on the device in
+    one call, as the benchmark's step does; six of them (the least and most padded and four spread
+    over the batch) are checked against both oracle builds at the reference-derived bar."""
+    import torch
+    from tsfm_attn import workloads
+
+    w = workloads.chronos2_forecast()
+    a, m = w.arrays, w.meta
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    d, F, T, hz, q = m["d_model"], m["d_ff"], m["context"], m["horizon"], m["quantiles"]
+    out = torch.full((w.B, hz, q), -9.0, device="cuda")
+    rc = ta.chronos2_forecast(out, cu(a["ctx"]), T, hz, cu(a["reg"]), cu(a["rope_cos"]), cu(a["rope_sin"]),
+                              [{k: cu(v) for k, v in ly.items()} for ly in m["layers"]], cu(a["final_norm"]),
+                              {k: cu(v) for k, v in m["ie"].items()}, {k: cu(v) for k, v in m["oe"].items()}, w.B, d,
+                              w.H, F, m["eps"], time_scale=m["time_scale"], arcsinh=True)
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    lead = np.isnan(a["ctx"]).argmin(axis=1)  # leading missing steps of each series
+    pick = sorted({int(lead.argmin()), int(lead.argmax()), 9, 27, 40, 63})
+    ctx = np.ascontiguousarray(a["ctx"][pick])
+    outs = []
+    for o_ in (orc, orc16):
+        want = np.zeros((len(pick), hz, q), np.float32)
+        o_.chronos2_forecast(THREADS, want, ctx, T, 0, T, len(pick), m["patch"], hz, m["time_scale"], True, a["reg"], d,
+                             w.H, 64, F, m["layers"], a["final_norm"], m["eps"], a["rope_cos"], a["rope_sin"], 1.0,
+                             m["ie"], m["oe"])
+        outs.append(want)
+    err, bar = _ref.assert_within_reference_bar(got[pick], *outs)
+    print(f"series {pick}: error {err:.3e}, bar {bar:.3e}")

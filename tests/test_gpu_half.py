@@ -184,9 +184,10 @@ def test_half_prefill_full_shape_f16(ta, orc, gpu_ready):
     assert _ref.scaled_err(got, want) <= TOL_HALF
 
 
-def _decode(ta, w, name, blocks=None):
-    """Prefix append, then per block: append 32 K/V, attend its 32 queries. Returns the decoded
-    outputs (B, blocks*32, H*D) as f32 and the rounded inputs."""
+def _decode(ta, w, name, blocks=None, fused=False):
+    """Prefix append, then per block: append 32 K/V, attend its 32 queries (fused: both in one
+    tsfm_kv_append_attend call, the benchmark's decode step). Returns the decoded outputs
+    (B, blocks*32, H*D) as f32 and the rounded inputs."""
     torch = _torch()
     a = w.arrays
     P, nb, blk = w.meta["prefix"], w.meta["blocks"], w.meta["block"]
@@ -202,9 +203,13 @@ def _decode(ta, w, name, blocks=None):
         cache.append(kd, vd, P, row, T * row, row, T * row)
         for i in range(nb):
             p0 = P + i * blk
-            cache.append(kd[:, p0:], vd[:, p0:], blk, row, T * row, row, T * row)
+            if fused:
+                cache.append_attend(kd[:, p0:], vd[:, p0:], qd[:, p0:], out[:, i * blk:], blk, w.scale, row, T * row,
+                                    row, T * row, row, T * row, row, nb * blk * row)
+            else:
+                cache.append(kd[:, p0:], vd[:, p0:], blk, row, T * row, row, T * row)
+                cache.attend(qd[:, p0:], out[:, i * blk:], blk, p0, w.scale, row, T * row, row, nb * blk * row)
             assert len(cache) == p0 + blk
-            cache.attend(qd[:, p0:], out[:, i * blk:], blk, p0, w.scale, row, T * row, row, nb * blk * row)
         torch.cuda.synchronize()
     return out.float().cpu().numpy(), qr, kr, vr
 
@@ -223,14 +228,19 @@ def test_kv_decode_matches_causal_rows(ta, orc, gpu_ready, name):
 
 
 def test_kv_decode_full_shape_bf16(ta, orc, gpu_ready):
-    """Timestral-shaped decode, bf16: B=128, H=16, prefix 256, 8 blocks of 32 queries."""
+    """Timestral-shaped decode, bf16: B=128, H=16, prefix 256, 8 blocks of 32 queries, through the
+    two calls per block and through the one-launch decode block the benchmark times
+    (tsfm_kv_append_attend); both against the causal rows of the oracle, and with the same bits."""
     from tsfm_attn import workloads
 
     w = workloads.timestral_decode()
     got, qr, kr, vr = _decode(ta, w, "bf16")
+    fused = _decode(ta, w, "bf16", fused=True)[0]
     T = 256 + 8 * 32
     want = _oracle(orc, 2, qr, kr, vr, None, w.B, w.H, T, w.scale)
     assert _ref.scaled_err(got, want[:, 256:]) <= TOL_HALF
+    assert _ref.scaled_err(fused, want[:, 256:]) <= TOL_HALF
+    assert np.array_equal(fused, got)
 
 
 @pytest.mark.parametrize("name", DTYPES)

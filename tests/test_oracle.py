@@ -416,6 +416,44 @@ def test_lane_counts_agree(orc, orc16):
         assert _ref.scaled_err(o16, o8) < 1e-6
 
 
+@pytest.mark.parametrize("mask", MASKS)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_batched_self_attend_matches_f64_per_item(orc, mask, with_bias):
+    """orc_batched_self_attend, the oracle of every generic-mask GPU test, on its own: each
+    (series, head) item against float64 attention over that item's own slices. Odd token and batch
+    strides that differ per tensor, a bias that differs per head, key validity that differs per
+    series (one series all invalid), threads over the items; a wrong batch or head offset, a shared
+    bias slice or one series' validity applied to another fails. Padding between views stays
+    untouched."""
+    rng = np.random.default_rng(40 + mask + 10 * with_bias)
+    nb, nh, n, hd, scale = 3, 2, 23, 64, 0.21
+    q_tok, k_tok, v_tok, o_tok = nh * hd + 3, nh * hd + 5, 2 * nh * hd + 1, nh * hd + 7
+    q_b, k_b, v_b, o_b = n * q_tok + 11, n * k_tok + 2, n * v_tok + 9, n * o_tok + 13
+    q = rng.standard_normal(nb * q_b).astype(np.float32)
+    k = rng.standard_normal(nb * k_b).astype(np.float32)
+    v = rng.standard_normal(nb * v_b).astype(np.float32)
+    kv_b = n + 4
+    kv = (rng.random(nb * kv_b) > 0.35).astype(np.uint8)
+    kv[kv_b: kv_b + n] = 0  # series 1: no valid key
+    bias = (rng.standard_normal(nh * n * n) * 0.7).astype(np.float32) if with_bias else None
+    sentinel = np.float32(-777.25)
+    o = np.full(nb * o_b, sentinel, np.float32)
+    orc.batched_self_attend(3, mask, q, q_tok, q_b, k, k_tok, k_b, v, v_tok, v_b, o, o_tok, o_b, kv, kv_b, bias, nb, nh,
+                            n, hd, scale)
+    written = np.zeros(o.size, bool)
+    for b in range(nb):
+        for h in range(nh):
+            rows = lambda x, tok, bat: np.stack([x[b * bat + t * tok + h * hd:][:hd] for t in range(n)])
+            Q, K, V = rows(q, q_tok, q_b), rows(k, k_tok, k_b), rows(v, v_tok, v_b)
+            allowed = _ref.allowed_matrix(mask, n, n, kv[b * kv_b: b * kv_b + n])
+            want = _ref.naive_attend(Q, K, V, allowed, scale, None if bias is None else bias[h * n * n:][:n * n].reshape(n, n))
+            got = rows(o, o_tok, o_b)
+            assert _ref.scaled_err(got, want) < 2e-6, (b, h)
+            for t in range(n):
+                written[b * o_b + t * o_tok + h * hd:][:hd] = True
+    assert (o[~written] == sentinel).all()
+
+
 # ---- Timestral variate attention (VariateJob.run, src/timestral/model.zig:648-709) -------------
 
 
@@ -1014,6 +1052,36 @@ def test_timestral_forecast_symmetric_clip_and_cap(orc):
         lo, hi = vals.min() - a, vals.max() + a
         assert capped.reshape(b * v, -1)[r].min() >= lo - 1e-4 and capped.reshape(b * v, -1)[r].max() <= hi + 1e-4
     assert not np.array_equal(capped, f)
+
+
+@pytest.mark.parametrize("asinh", [False, True])
+@pytest.mark.parametrize("horizon,per_shot,max_context,cap_k,symmetric", [
+    (40, 32, 2048, 0.0, False), (100, 2, 2048, 1e4, True), (100, 2, 176, 1e4, True), (64, 4, 2048, 0.05, True)])
+def test_timestral_forecast_f64_composition_matches_oracle(orc, asinh, horizon, per_shot, max_context, cap_k,
+                                                           symmetric):
+    """_ref.timestral_forecast_f64 (the float64 forecast the GPU tests measure distances from, composed
+    from the float64 predict_block and refine_block definitions with the feedback, window, cap,
+    mirrored average and clip) against the oracle's forecast: one refined block, several blocks with
+    feedback, a context window that drops steps, a cap that binds (cap_k 0.05), a negative series
+    (the clip leaves it alone) and a series without observation. Within f32 distance in linear space
+    (1e-5) and in asinh space (2e-4, where the sinh expansion amplifies the head's f32 error); a
+    wrong mirror, cap or clip moves the forecast by orders of magnitude more."""
+    b, v = 3, 1
+    rng = np.random.default_rng(50 + int(asinh))
+    m = _ref.timestral_model(rng, d=64, nh=1, hid=64, schedule=("time_variate", "time"), use_asinh=asinh)
+    t0 = 150
+    x = (20 + 5 * np.sin(np.arange(t0) / 4.0) + rng.standard_normal((b * v, t0))).astype(np.float32)
+    x[1] = -x[1]
+    obs = rng.random((b * v, t0)) >= 0.1
+    obs[2] = False
+    x[~obs] = 0
+    rc, got = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, max_context, per_shot, cap_k=cap_k,
+                                     symmetric=symmetric, clip_nonnegative=True)
+    assert rc == 0
+    want = _ref.timestral_forecast_f64(m, x, obs, b, v, horizon, per_shot=per_shot, max_context=max_context,
+                                       cap_k=cap_k, symmetric=symmetric, clip_nonnegative=True)
+    assert _ref.scaled_err(got, want) < (2e-4 if asinh else 1e-5)
+    assert (got[1] < 0).any() and (got[0] >= 0).all()  # the clip applies to the positive series only
 
 
 # ---- Chronos-Bolt long horizons (src/chronos_bolt/forecaster.zig:22-92) ----------------------------

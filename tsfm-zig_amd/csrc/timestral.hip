@@ -5,7 +5,8 @@
 //
 // Reference: src/timestral/model.zig (predictBlock :220-432, runTransformer :434-482, StatsJob
 // :712-750) and src/timestral/forecaster.zig (forecast :57-180, forecastRaw :303-421, blockDecode
-// :423-563, refineBlock :582-662), for series whose rows are all target variates.
+// :423-563, refineBlock :582-662), for series of target variates with optional numeric past-only
+// and known-future covariate rows (the window, the known rows' statistics and the role feedback).
 //
 // The sequential recurrences of the reference (the float64 Welford of every row, the fold of
 // refineBlock) run one thread per row in the reference's order, so they give the reference's

@@ -15,8 +15,9 @@
 // encoder token (one (rows, tokens, 3 d) buffer per layer), and a block runs only its new patches
 // and its decoder tokens through the layers, their queries attending over the kept keys. Blocks
 // that change the prefix run in full: after the context window drops its oldest steps
-// (max_context), and for every block when a series had no observation at all (its RoPE origin,
-// the first observed patch, moves once the fed-back medians appear).
+// (max_context). A group with no observation at all moves its RoPE origin (the first observed
+// patch) once the fed-back medians appear; its earlier tokens are invalid keys for every later
+// query, so the RoPE tables are recomputed every block and the cache stays exact.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -97,8 +98,16 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     if (a->n_past < 0 || a->n_known < 0) return fail(TSFM_E_INVALID, "negative covariate count");
     if ((a->n_past > 0 && !a->past) || (a->n_known > 0 && !a->known))
         return fail(TSFM_E_INVALID, "a covariate count without its array");
-    if (a->variates + a->n_past + a->n_known > 16)
+    // forecaster.zig:104: covariates given but no rows (error.InvalidInput)
+    if ((a->past && a->n_past == 0) || (a->known && a->n_known == 0))
+        return fail(TSFM_E_INVALID, "a covariate array with no rows (error.InvalidInput)");
+    if ((a->past || a->known) && !M.covariate_enabled)
+        return fail(TSFM_E_UNSUPPORTED, "covariates with covariate_enabled off (error.CovariatesUnsupported)");
+    if ((int64_t)a->variates + a->n_past + a->n_known > 16)
         return fail(TSFM_E_UNSUPPORTED, "at most 16 rows (variates and covariates) per series");
+    if ((a->flags & TSFM_TIMESTRAL_BF16_ATTN) && M.use_asinh)
+        return fail(TSFM_E_UNSUPPORTED, "bf16 time attention with use_asinh: the sinh expansion of the head "
+                                        "outputs takes the bf16 rounding past the half-precision bar");
     if (M.block_size <= 0 || M.n_layers < 0 || (M.n_layers > 0 && M.layers == nullptr))
         return fail(TSFM_E_INVALID, "bad block_size or layers");
     if (!a->inputs || !a->observed || !a->out || !M.forecast_query || !M.out_norm)
@@ -245,12 +254,11 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
         cp.ctx = ctx[0]; cp.mask = mask[0]; cp.kf = F(at_kf); cp.kfm = U8(at_kfm); cp.nonneg = U8(at_nonneg);
         hipError_t e2 = tsfm::launch_ts_context(cp, s);
         if (e2 != hipSuccess) return e2;
-        bool cache = a->kv_cache != 0 && !cov;
+        const bool cache = a->kv_cache != 0 && !cov;
         const int known_from = V + a->n_past;  // first known-future row of a series
         int t = t_first, remaining = total_patches, done = 0;
         int stats_from = 0;  // first step of the window whose statistics are not computed yet
         int p0 = 0;          // first token of this block's encoder run: the cache holds tokens [0, p0)
-        bool tables_valid = false;
         for (int block_no = 0; remaining > 0; block_no++) {
             const int h = std::min(per_shot, remaining), blen = h * ps, l = t / ps;
             // With covariates the encoder covers the window [0, t + blen): the block's known
@@ -269,31 +277,19 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                 (e2 = tsfm::launch_ts_known_stats(ctx[cur], mask[cur], cap_t, w, ps, rows, vall, known_from,
                                                   M.minimum_scale, loc, scale, cap_p, U8(at_noasinh), s)) != hipSuccess)
                 return e2;
-            if (block_no == 0) {
-                if (cap_k > 0 && (e2 = tsfm::launch_ts_cap_bounds(ctx[cur], mask[cur], cap_t, t, ps, scale, cap_p, rows,
-                                                                  cap_k, F(at_bounds), s)) != hipSuccess)
-                    return e2;
-                if (cache) {
-                    // A series with no observation gets its RoPE origin (first observed patch) from the
-                    // first fed-back medians, which moves every earlier position: no cache then.
-                    std::vector<int> rf((size_t)rows);
-                    if ((e2 = hipMemcpyAsync(rf.data(), row_first, (size_t)rows * 4, hipMemcpyDeviceToHost, s)) !=
-                            hipSuccess ||
-                        (e2 = hipStreamSynchronize(s)) != hipSuccess)
-                        return e2;
-                    for (int g = 0; g < groups && cache; g++) {
-                        bool any = false;
-                        for (int i = 0; i < vall; i++) any = any || rf[(size_t)(g * vall + i)] >= 0;
-                        cache = any;
-                    }
-                }
-            }
-            if (!tables_valid) {
-                if ((e2 = tsfm::launch_ts_rope_tables(row_first, groups, vall, cap_tok, ne, ne - l, rope, cos_t, sin_t,
-                                                      first_obs, s)) != hipSuccess)
-                    return e2;
-                tables_valid = cache;
-            }
+            if (block_no == 0 && cap_k > 0 &&
+                (e2 = tsfm::launch_ts_cap_bounds(ctx[cur], mask[cur], cap_t, t, ps, scale, cap_p, rows, cap_k,
+                                                 F(at_bounds), s)) != hipSuccess)
+                return e2;
+            // The RoPE tables follow each group's first observed patch, recomputed every block: a
+            // group with no observation gets its origin from the first fed-back medians. Its earlier
+            // tokens are then invalid keys for every later query (no observed patch before them), so
+            // their cached K/V, RoPE'd at the old origin, carry zero weight, and the new tokens are
+            // RoPE'd at the new origin exactly as a re-encoding would: the cache stays exact without
+            // the host learning which groups had no observation.
+            if ((e2 = tsfm::launch_ts_rope_tables(row_first, groups, vall, cap_tok, ne, ne - l, rope, cos_t, sin_t,
+                                                  first_obs, s)) != hipSuccess)
+                return e2;
             // 2. patch embedding of the new patches; [encoder tokens; forecast queries]
             if ((e2 = tsfm::launch_ts_features(ctx[cur], mask[cur], cap_t, loc, scale, cap_p, rows, p0, ne, ps,
                                                M.use_asinh ? 1 : 0, a->n_known > 0 ? U8(at_noasinh) : nullptr,
@@ -437,7 +433,6 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                 t = keep_t;
                 stats_from = 0;
                 p0 = 0;
-                tables_valid = false;
             } else if (cache) {
                 stats_from = t;
                 p0 = l;
@@ -446,7 +441,6 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                 stats_from = 0;  // re-encode the grown context, as the reference does
                 p0 = 0;
                 t = nt;
-                tables_valid = false;
             }
         }
         return tsfm::launch_ts_final(out, F(at_mir), F(at_bounds), U8(at_nonneg), R, V, vall, a->horizon, q,

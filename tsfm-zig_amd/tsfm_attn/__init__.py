@@ -239,7 +239,7 @@ class TimestralModel(ctypes.Structure):
 
     _fields_ = [(f, ctypes.c_int32) for f in ("patch", "d_model", "heads", "head_dim", "mlp_hidden", "n_layers",
                                               "n_quantiles", "block_size", "context_length", "rope_dim",
-                                              "use_asinh", "attend_missing")] + \
+                                              "use_asinh", "attend_missing", "covariate_enabled")] + \
                [(f, ctypes.c_float) for f in ("rope_theta", "norm_eps", "minimum_scale", "quantile_width_factor")] + \
                [("quantile_knots", ctypes.c_void_p), ("patch_proj", Resblock), ("head", Resblock),
                 ("forecast_query", ctypes.c_void_p), ("out_norm", ctypes.c_void_p),
@@ -1165,6 +1165,7 @@ def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, vari
                        n_layers=len(model["layers"]), n_quantiles=model["q"], block_size=model["block_size"],
                        context_length=model["context_length"], rope_dim=model["rope_dim"],
                        use_asinh=int(model["use_asinh"]), attend_missing=int(model["attend_missing"]),
+                       covariate_enabled=int(model.get("covariate_enabled", True)),
                        rope_theta=model["rope_theta"], norm_eps=model["norm_eps"], minimum_scale=model["minimum_scale"],
                        quantile_width_factor=model["width_factor"], quantile_knots=knots.ctypes.data,
                        patch_proj=_resblock(model["patch_proj"], act=1), head=_resblock(model["head"], act=1),

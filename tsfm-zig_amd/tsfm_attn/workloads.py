@@ -330,3 +330,82 @@ def bolt_forward(B: int = 16, n_patch: int = 32, H: int = 8, d_ff: int = 2048, n
                     dict(enc=enc, dec=dec, ie=ie, oe=oe, d_model=d, d_ff=d_ff, n_patch=n_patch, out=out, eps=eps,
                          buckets=buckets, max_distance=max_distance, flops=f_enc + f_dec + f_emb,
                          bytes=w_bytes + 4.0 * (feats.size + B * out), seed=seed, num_layers=2 * n_layers))
+
+
+def timestral_forecast(B: int = 128, context_patches: int = 256, blocks: int = 8, per_shot: int = 32, d: int = 1024,
+                       H: int = 16, hid: int = 2816, patch: int = 16, seed: int = 0,
+                       schedule=("time_variate", "time", "time_variate", "time")) -> Workload:
+    """The Timestral forecast at the decode configuration's shape: 128 univariate series of
+    context_patches x 16 steps (4096), a horizon of 8 decode blocks of 32 patches (4096 steps), a
+    Timestral-shaped model of d_model 1024, 16 heads of 64, four layers (time+variate, time,
+    time+variate, time; sigmoid gates), SwiGLU width 2816 (2/3 of 4 d, rounded to 256), 9 quantile
+    knots, asinh space, random-init f32 weights (linear ~ N(0, 1/in), norm scales ~ 1 + N(0, 0.1)).
+    The model dict has the keys of the forecast binding (tsfm_attn.timestral_forecast_args). Each
+    series is a period-24 sinusoid of amplitude 10 plus a trend plus N(0, 1) noise, its oldest
+    0-25 % of steps missing and 2 % of the rest. Symmetric averaging doubles the rows (the mirrored
+    pass). meta carries the FLOP counts of the cached decode (each block runs its new patches and
+    decoder tokens) and of the reference's re-encoding decode (each block re-encodes the grown
+    context)."""
+    rng = np.random.default_rng(seed)
+    knots = np.array([0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9])
+    q = len(knots)
+
+    def lin(o, i):
+        return (rng.standard_normal((o, i)) / np.sqrt(i)).astype(np.float32)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+
+    def resblock(i, h, o, biases=True):
+        rb = dict(hidden_w=lin(h, i), output_w=lin(o, h), residual_w=lin(o, i))
+        for k, n in (("hidden_b", h), ("output_b", o), ("residual_b", o)):
+            rb[k] = (0.1 * rng.standard_normal(n)).astype(np.float32) if biases else None
+        return rb
+
+    axes = {"time": [True], "variate": [False], "time_variate": [True, False], "variate_time": [False, True]}
+    layers = []
+    for kind in schedule:
+        attns = [dict(is_time=t, norm=norm(), qkv=lin(3 * d, d), out=lin(d, d), gate=lin(d, d)) for t in axes[kind]]
+        layers.append(dict(attns=attns, mlp_norm=norm(), w12=lin(2 * hid, d), w3=lin(d, hid)))
+    model = dict(ps=patch, d=d, nh=H, hid=hid, q=q, median=4, block_size=per_shot, context_length=8192, rope_dim=32,
+                 rope_theta=10000.0, norm_eps=1e-6, minimum_scale=1e-6, use_asinh=True, attend_missing=True,
+                 width_factor=2.0, knots=knots, patch_proj=resblock(2 * patch, 4 * d, d),
+                 head=resblock(d, 4 * d, patch * q, biases=False), forecast_query=rng.standard_normal(d).astype(np.float32),
+                 out_norm=norm(), layers=layers)
+    t = context_patches * patch
+    horizon = blocks * per_shot * patch
+    steps = np.arange(t, dtype=np.float64)
+    slope = rng.uniform(-0.01, 0.01, (B, 1))
+    x = 10.0 * np.sin(2 * np.pi * steps / 24.0) + slope * steps + rng.standard_normal((B, t))
+    obs = rng.random((B, t)) >= 0.02
+    lead = rng.integers(0, context_patches // 4 + 1, B) * patch
+    for b in range(B):
+        obs[b, : lead[b]] = False
+    x[~obs] = 0.0
+    rows = 2 * B  # the mirrored pass of the symmetric average runs in the same batch
+    n_time = sum(1 for ly in layers for a in ly["attns"] if a["is_time"])
+    n_var = sum(1 for ly in layers for a in ly["attns"] if not a["is_time"])
+
+    def flops(cached: bool) -> float:
+        f = 0.0
+        for i in range(blocks):
+            l = context_patches + i * per_shot  # encoder tokens (context patches) of block i
+            p0 = l - per_shot if (cached and i > 0) else 0  # first encoder token this block runs
+            m, h = l - p0, per_shot
+            n = m + h
+            f += 2.0 * m * (2 * patch * 4 * d + 4 * d * d + 2 * patch * d)       # patch embedding
+            f += len(layers) * 2.0 * n * 3 * hid * d                                # SwiGLU MLPs
+            f += (n_time + n_var) * 2.0 * n * 5 * d * d                             # q/k/v, gate, out
+            enc_pairs = sum(p0 + j + 1 for j in range(m))                           # causal encoder rows
+            dec_pairs = h * l + h * (h + 1) // 2                                    # context + own chain
+            f += n_time * 4.0 * 64 * H * (enc_pairs + dec_pairs)
+            f += n_var * 4.0 * 64 * H * n                                           # one row per series
+            f += 2.0 * h * (d * 4 * d + 4 * d * patch * q + d * patch * q)         # quantile head
+        return rows * f
+
+    w = Workload("timestral_forecast", "f32", B, H, blocks * per_shot, context_patches + blocks * per_shot, 64,
+                 0.125, dict(inputs=x.astype(np.float32), observed=obs.astype(np.uint8)),
+                 dict(model=model, context=t, horizon=horizon, per_shot=per_shot, blocks=blocks, d_model=d, hid=hid,
+                      n_layers=len(layers), schedule=list(schedule), flops=flops(True),
+                      reencode_flops=flops(False), bytes=0.0, seed=seed, num_layers=len(layers)))
+    return w
