@@ -782,7 +782,8 @@ def main() -> int:
         "roofline": head["roofline"],
         "cpu_baseline": head["cpu_baseline"],
     }
-    for k in ("parity_max_scaled_err", "parity_bar", "parity_cross_host_spread", "parity_ok"):
+    for k in ("parity_max_scaled_err", "parity_bar", "parity_cross_host_spread", "parity_ok", "reencode",
+              "cache_speedup"):
         if k in head:
             line[k] = head[k]
     if w.meta.get("num_layers"):
