@@ -461,6 +461,7 @@ hipError_t launch_mask(const Params& p, int mask, bool rope, hipStream_t s) {
 hipError_t launch_attn_half(const Params& p, bool is_bf16, int mask, int bias, bool rope, hipStream_t s) {
     if (bias != BIAS_NONE) return hipErrorNotSupported;  // the bias-carrying families are f32
     if (!(p.scale >= 0.f)) return hipErrorNotSupported;  // the row max is taken before scaling
+    if (attn_half_pipe_supports(p, mask, bias, rope)) return launch_attn_half_pipe(p, is_bf16, mask, s);
     return is_bf16 ? launch_mask<true>(p, mask, rope, s) : launch_mask<false>(p, mask, rope, s);
 }
 

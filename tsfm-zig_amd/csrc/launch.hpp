@@ -12,6 +12,10 @@ hipError_t launch_attn_f32(const Params& p, int mask, int bias, bool rope, hipSt
 
 // bf16 (is_bf16) or f16 q/k/v/o, f32 accumulation.
 hipError_t launch_attn_half(const Params& p, bool is_bf16, int mask, int bias, bool rope, hipStream_t stream);
+// The pipelined half-precision kernel (attn_prefill.hip): masks FULL, CAUSAL, CAUSAL_KEYS and
+// FULL_KEYS without bias or RoPE, positive scale. launch_attn_half uses it for those calls.
+bool attn_half_pipe_supports(const Params& p, int mask, int bias, bool rope);
+hipError_t launch_attn_half_pipe(const Params& p, bool is_bf16, int mask, hipStream_t stream);
 
 // KV cache: device layout and kernels (kv_cache.hip).
 struct KvLayout {
