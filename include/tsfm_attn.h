@@ -161,13 +161,15 @@ int tsfm_t5_bucket_table(int32_t *out, int32_t n_q, int32_t n_k, uint32_t num_bu
  * and, with cov != 0, neither (role[i] != TARGET and role[j] == TARGET) nor (role[i] == KNOWN and
  * role[j] != KNOWN). Roles are model.Role in declaration order (src/timestral/model.zig:89).
  * With gate != NULL the result is multiplied by sigmoid(gate) (same layout as o) before it is stored.
- * f32 only; vall <= 16 (more rows: TSFM_E_UNSUPPORTED, use the CPU path); head_dim 64. */
+ * f32 only; vall <= TSFM_VARIATE_MAX_ROWS (more rows: TSFM_E_UNSUPPORTED, use the CPU path);
+ * head_dim 64. */
 enum { TSFM_ROLE_TARGET = 0, TSFM_ROLE_PAST = 1, TSFM_ROLE_KNOWN = 2 };
+#define TSFM_VARIATE_MAX_ROWS 256
 
 typedef struct tsfm_variate_args {
     int32_t dtype;     /* TSFM_DTYPE_F32 */
     int32_t groups;    /* series */
-    int32_t vall;      /* rows per series, 1..16 */
+    int32_t vall;      /* rows per series, 1..TSFM_VARIATE_MAX_ROWS */
     int32_t n_tok;     /* token slots per row (sl = ne + h) */
     int32_t n_enc;     /* encoder slots (ne): key_valid applies to slots t < n_enc */
     int32_t heads;     /* H; d_model = heads * head_dim */
@@ -182,7 +184,8 @@ typedef struct tsfm_variate_args {
     void *o;         int64_t o_row, o_tok;     /* (r, t, h, c) */
     const void *gate; int64_t gate_row, gate_tok; /* optional, as o */
     const uint8_t *key_valid; int64_t kv_row;   /* (rows, n_enc) bytes */
-    uint8_t roles[16];                          /* role of row i of every series, i < vall */
+    const uint8_t *roles;                       /* vall bytes of host memory: role of row i of every
+                                                   series (read at the call; may be NULL when cov = 0) */
     void *stream;
 } tsfm_variate_args;
 
@@ -509,7 +512,7 @@ typedef struct tsfm_timestral_forecast_args {
      * re-encodes the window (context + horizon) as the reference does: kv_cache is ignored. */
     const float *past;              /* (batch, n_past, len) past-only covariates */
     const float *known;             /* (batch, n_known, len + horizon) known-future covariates */
-    int32_t n_past, n_known;        /* variates + n_past + n_known <= 16 */
+    int32_t n_past, n_known;        /* variates + n_past + n_known <= TSFM_VARIATE_MAX_ROWS */
 } tsfm_timestral_forecast_args;
 
 int tsfm_timestral_forecast(const tsfm_timestral_forecast_args *args);

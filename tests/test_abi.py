@@ -154,13 +154,16 @@ def _variate_host_args(ta, **over):
     kw.update(over)
     roles = kw.pop("roles", [0, 1, 2])
     a = ta.VariateArgs(**kw)
-    for i, r in enumerate(roles):
-        a.roles[i] = r
-    return a, (qkv, o, kv)
+    role_bytes = None
+    if roles is not None:
+        role_bytes = (ctypes.c_uint8 * max(len(roles), kw["vall"], 1))(*roles)
+        a.roles = role_bytes
+    return a, (qkv, o, kv, role_bytes)
 
 
 @pytest.mark.parametrize("over,code", [
-    (dict(vall=17), 2),            # more rows than one 16-slot score block
+    (dict(vall=257), 2),           # more rows than the kernels' role words hold
+    (dict(roles=None), 3),         # roles are required with cov
     (dict(dtype=2), 2),            # f32 only
     (dict(head_dim=32), 2),
     (dict(n_enc=9), 3),            # more encoder slots than tokens

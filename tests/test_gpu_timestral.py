@@ -237,6 +237,31 @@ def test_timestral_forecast_with_covariates(ta, orc, orc16, gpu_ready, horizon, 
     assert _ref.scaled_err(got, plain) > 10 * bar  # the covariates do move the forecast
 
 
+@pytest.mark.parametrize("v,n_past,n_known", [(1, 8, 8), (2, 12, 10), (1, 16, 16)])
+def test_timestral_forecast_many_rows(ta, orc, orc16, gpu_ready, v, n_past, n_known):
+    """17, 24 and 33 rows per series (targets and covariates): the variate layers take the
+    row-block kernel; against both oracle builds' re-encoding forecasts at the reference-derived
+    bar, over two decode blocks."""
+    import torch
+
+    b, horizon, per_shot = 2, 40, 2
+    m, x, obs, past, known = _cov_case(60 + v + n_past, b, v, n_past=n_past, n_known=n_known, horizon=horizon)
+    t = x.shape[1]
+    out = torch.full((b, v, horizon, m["q"]), -7.0, device="cuda")
+    rc = ta.timestral_forecast(out, torch.from_numpy(x).cuda(), torch.from_numpy(obs.astype(np.uint8)).cuda(),
+                               _device_model(m), b, v, t, horizon, per_shot=per_shot,
+                               past=torch.from_numpy(past).cuda(), known=torch.from_numpy(known).cuda())
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    kw = dict(max_context=0, per_shot=per_shot)
+    rc8, w8 = orc.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, known, **kw)
+    rc16, w16 = orc16.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, known, **kw)
+    assert rc8 == 0 and rc16 == 0
+    err, bar = _ref.assert_within_reference_bar(got, w8, w16)
+    print(f"rows {v + n_past + n_known}: err {err:.3g} bar {bar:.3g}", flush=True)
+
+
 @pytest.mark.parametrize("max_context", [0, 176])
 def test_timestral_forecast_with_covariates_bf16(ta, orc16, gpu_ready, max_context):
     """TSFM_TIMESTRAL_BF16_ATTN with covariates: the per-row time-attention launches over the bf16
@@ -280,9 +305,9 @@ def test_timestral_forecast_covariate_errors(ta, gpu_ready):
                                    known=torch.from_numpy(known).cuda())
     a.known = None  # a count without its array
     assert ta.load().tsfm_timestral_forecast(ta.ctypes.byref(a)) == ta.E_INVALID
-    big = torch.zeros((2, 16, x.shape[1] + 40), device="cuda")
+    big = torch.zeros((2, ta.VARIATE_MAX_ROWS, x.shape[1] + 40), device="cuda")
     rc = ta.timestral_forecast(out, xd, od, _device_model(m), 2, 1, x.shape[1], 40, known=big)
-    assert rc == ta.E_UNSUPPORTED  # 1 target + 16 covariate rows > 16
+    assert rc == ta.E_UNSUPPORTED  # 1 target + 256 covariate rows: more than the kernels' 256
     # config.zig:49-70: a schedule of time ops only cannot route a known future to the targets
     # (error.KnownCovariatesUnsupported); past-only covariates still run.
     rng = np.random.default_rng(46)

@@ -2,10 +2,11 @@
 restatement of VariateJob.run (src/timestral/model.zig:648-709) and nn.mulSigmoid
 (src/core/nn.zig:423-433), through the C ABI.
 
-Bar: scaled error max|gpu - oracle| / max(|oracle|, 1) <= 1e-5 (the f32 tolerance). Covered: every
-row count 1..16 that one 16-slot score block takes (several heads per block below 16 rows, a
-partial last head block), with and without the covariate firewalls, encoder and decoder slots,
-the fused sigmoid gate, host and device pointers, and the singleton case o = v exactly.
+Bar: scaled error max|gpu - oracle| / max(|oracle|, 1) <= 1e-5 (the f32 tolerance). Covered: row
+counts 1..16 that one 16-slot score block takes (several heads per block below 16 rows, a partial
+last head block), and 17, 24, 33 and the largest count, 256, where 16-row query blocks walk 16-row
+key blocks with an online softmax; with and without the covariate firewalls, encoder and decoder
+slots, the fused sigmoid gate, host and device pointers, and the singleton case o = v exactly.
 """
 import numpy as np
 import pytest
@@ -27,7 +28,7 @@ def _inputs(seed, groups, vall, ne, h, d, p_valid=0.7):
 
 
 def _roles(vall):
-    return np.array(([_ref.ROLE_TARGET, _ref.ROLE_PAST, _ref.ROLE_KNOWN, _ref.ROLE_PAST] * 4)[:vall], np.uint8)
+    return np.array(([_ref.ROLE_TARGET, _ref.ROLE_PAST, _ref.ROLE_KNOWN, _ref.ROLE_PAST] * 64)[:vall], np.uint8)
 
 
 def _oracle(orc, qkv, kv, roles, cov, groups, vall, ne, h, d, nh, gate=None):
@@ -39,7 +40,7 @@ def _oracle(orc, qkv, kv, roles, cov, groups, vall, ne, h, d, nh, gate=None):
 
 
 @pytest.mark.parametrize("cov", [False, True])
-@pytest.mark.parametrize("vall", [1, 2, 3, 4, 5, 8, 13, 16])
+@pytest.mark.parametrize("vall", [1, 2, 3, 4, 5, 8, 13, 16, 17, 24, 33])
 def test_variate_matches_oracle(ta, orc, gpu_ready, vall, cov):
     groups, ne, h, nh = 3, 21, 5, 4
     d = nh * 64
@@ -62,6 +63,29 @@ def test_variate_partial_head_block(ta, orc, gpu_ready, vall, nh):
     o = np.zeros((groups * vall, ne + h, d), np.float32)
     assert ta.timestral_variate_attention(qkv, o, kv, roles, True, groups, vall, ne, h, d, nh, 64) == ta.OK
     assert _ref.scaled_err(o, _oracle(orc, qkv, kv, roles, True, groups, vall, ne, h, d, nh)) <= TOL
+
+
+@pytest.mark.parametrize("vall,nh,cov", [(24, 3, True), (256, 2, True), (40, 2, False)])
+def test_variate_many_rows_gate_and_device_pointers(ta, orc, gpu_ready, vall, nh, cov):
+    """More than 16 rows per series: the row-block kernel, with the gate, on device tensors and
+    host arrays (the same bits), against the oracle."""
+    import torch
+
+    groups, ne, h = 2, 11, 3
+    d = nh * 64
+    qkv, kv = _inputs(70 + vall, groups, vall, ne, h, d, p_valid=0.4)
+    gate = (np.random.default_rng(71).standard_normal((groups * vall, ne + h, d)) * 3).astype(np.float32)
+    roles = _roles(vall)
+    want = _oracle(orc, qkv, kv, roles, cov, groups, vall, ne, h, d, nh, gate)
+    o = np.zeros_like(want)
+    assert ta.timestral_variate_attention(qkv, o, kv, roles, cov, groups, vall, ne, h, d, nh, 64, gate=gate) == ta.OK
+    assert _ref.scaled_err(o, want) <= TOL
+    dev = {n: torch.from_numpy(x).cuda() for n, x in dict(qkv=qkv, kv=kv, gate=gate).items()}
+    od = torch.zeros(want.shape, dtype=torch.float32, device="cuda")
+    assert ta.timestral_variate_attention(dev["qkv"], od, dev["kv"], roles, cov, groups, vall, ne, h, d, nh, 64,
+                                          gate=dev["gate"]) == ta.OK
+    torch.cuda.synchronize()
+    assert np.array_equal(od.cpu().numpy(), o)
 
 
 def test_variate_gate_and_device_pointers(ta, orc, gpu_ready):
@@ -95,9 +119,9 @@ def test_variate_singleton_is_exactly_v(ta, gpu_ready):
     assert np.array_equal(o, qkv[:, :, 2 * d:])
 
 
-def test_variate_rows_past_sixteen_are_refused(ta, gpu_ready):
-    groups, vall, ne, h, nh = 1, 17, 4, 0, 1
+def test_variate_rows_past_the_largest_count_are_refused(ta, gpu_ready):
+    groups, vall, ne, h, nh = 1, ta.VARIATE_MAX_ROWS + 1, 4, 0, 1
     d = nh * 64
     qkv, kv = _inputs(51, groups, vall, ne, h, d)
     o = np.zeros((vall, ne + h, d), np.float32)
-    assert ta.timestral_variate_attention(qkv, o, kv, [0] * 16, False, groups, vall, ne, h, d, nh, 64) == ta.E_UNSUPPORTED
+    assert ta.timestral_variate_attention(qkv, o, kv, [0] * vall, False, groups, vall, ne, h, d, nh, 64) == ta.E_UNSUPPORTED

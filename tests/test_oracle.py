@@ -465,12 +465,12 @@ def _variate_inputs(seed, groups, vall, ne, h, d, p_valid=0.7):
     return qkv, kv
 
 
-@pytest.mark.parametrize("vall,cov", [(1, False), (3, False), (5, True), (8, True)])
+@pytest.mark.parametrize("vall,cov", [(1, False), (3, False), (5, True), (8, True), (24, True), (33, False)])
 def test_variate_attention_matches_f64(orc, vall, cov):
     groups, ne, h, nh, hd = 3, 9, 4, 2, 16
     d = nh * hd
     qkv, kv = _variate_inputs(vall, groups, vall, ne, h, d)
-    roles = np.array(([_ref.ROLE_TARGET, _ref.ROLE_PAST, _ref.ROLE_KNOWN] * 4)[:vall], np.uint8)
+    roles = np.array(([_ref.ROLE_TARGET, _ref.ROLE_PAST, _ref.ROLE_KNOWN] * 11)[:vall], np.uint8)
     o = np.zeros((groups * vall, ne + h, d), np.float32)
     orc.timestral_variate_attention(4, qkv, o, kv, roles, cov, groups, vall, ne, h, d, nh, hd)
     want = _ref.variate_attend_f64(qkv, kv, roles, cov, groups, vall, ne, h, d, nh, hd)

@@ -500,17 +500,22 @@ int tsfm_attn_fwd(const tsfm_attn_args* a) {
 
 // ---- Timestral variate attention ----------------------------------------------------------------
 
+static_assert(tsfm::kVariateMaxRows == TSFM_VARIATE_MAX_ROWS, "the kernels' role words cover the ABI's rows");
+
 int tsfm_variate_attend(const tsfm_variate_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (a->dtype != TSFM_DTYPE_F32) return fail(TSFM_E_UNSUPPORTED, "variate attention is f32 only");
     if (a->head_dim != 64) return fail(TSFM_E_UNSUPPORTED, "head_dim %d (supported: 64)", a->head_dim);
     if (a->groups < 0 || a->vall < 0 || a->n_tok < 0 || a->n_enc < 0 || a->heads < 0)
         return fail(TSFM_E_INVALID, "negative size");
-    if (a->vall > 16) return fail(TSFM_E_UNSUPPORTED, "vall %d (supported: up to 16 rows per series)", a->vall);
+    if (a->vall > TSFM_VARIATE_MAX_ROWS)
+        return fail(TSFM_E_UNSUPPORTED, "vall %d (supported: up to %d rows per series)", a->vall, TSFM_VARIATE_MAX_ROWS);
     if (a->n_enc > a->n_tok) return fail(TSFM_E_INVALID, "n_enc %d > n_tok %d", a->n_enc, a->n_tok);
     if (a->qkv == nullptr || a->o == nullptr) return fail(TSFM_E_INVALID, "qkv and o are required");
-    for (int32_t i = 0; i < a->vall; i++)
-        if (a->roles[i] > TSFM_ROLE_KNOWN) return fail(TSFM_E_INVALID, "roles[%d] = %d", i, a->roles[i]);
+    if (a->cov != 0 && a->roles == nullptr && a->vall > 0) return fail(TSFM_E_INVALID, "roles is required with cov");
+    if (a->roles != nullptr)
+        for (int32_t i = 0; i < a->vall; i++)
+            if (a->roles[i] > TSFM_ROLE_KNOWN) return fail(TSFM_E_INVALID, "roles[%d] = %d", i, a->roles[i]);
     if (a->n_enc > 0 && a->vall > 1 && a->key_valid == nullptr) return fail(TSFM_E_INVALID, "key_valid is required");
     if (a->qkv_row < 0 || a->qkv_tok < 0 || a->o_row < 0 || a->o_tok < 0 || a->gate_row < 0 || a->gate_tok < 0 ||
         a->kv_row < 0)
@@ -538,7 +543,8 @@ int tsfm_variate_attend(const tsfm_variate_args* a) {
     p.o = static_cast<float*>(a->o); p.o_row = a->o_row; p.o_tok = a->o_tok;
     p.gate = static_cast<const float*>(a->gate); p.gate_row = a->gate_row; p.gate_tok = a->gate_tok;
     p.key_valid = a->key_valid; p.kv_row = a->kv_row;
-    for (int i = 0; i < 16; i++) p.roles[i >> 2] |= (uint32_t)(i < a->vall ? a->roles[i] : 0) << (8 * (i & 3));
+    if (a->roles != nullptr)
+        for (int i = 0; i < a->vall; i++) p.roles[i >> 2] |= (uint32_t)a->roles[i] << (8 * (i & 3));
     p.groups = a->groups; p.vall = a->vall; p.n_tok = a->n_tok; p.n_enc = a->n_enc; p.heads = a->heads;
     p.cov = a->cov != 0; p.scale = a->scale;
     hipError_t e;

@@ -153,7 +153,6 @@ attn_fwd_half_pipe(Params p) {
     const int wave_nq = max(0, min(QW, p.n_q - wq0));
     const int wave_qlo = p.q_pos0 + wq0;
     const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(wave_qlo + wave_nq - 1, p.n_k, 0) : 0;
-    const int wave_tiles = (wave_kend + NK - 1) / NK;
     const int qpos = wave_qlo + lq;
     const float c2 = p.scale * kLog2e;  // > 0 (checked on the host)
 

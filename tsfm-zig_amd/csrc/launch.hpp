@@ -45,12 +45,13 @@ hipError_t launch_kv_append_attend(const KvLayout& c, bool is_bf16, const KvNew&
 
 // Timestral variate attention (variate.hip). f32; vall <= 16.
 constexpr int kRoleTarget = 0, kRoleKnown = 2;  // model.Role (src/timestral/model.zig:89)
+constexpr int kVariateMaxRows = 256;  // rows per series the variate kernels take (kernel-argument roles)
 struct VariateParams {
     const float* qkv; int64_t qkv_row, qkv_tok;
     float* o; int64_t o_row, o_tok;
     const float* gate; int64_t gate_row, gate_tok;
     const uint8_t* key_valid; int64_t kv_row;
-    uint32_t roles[4];  // 16 role bytes, row i in byte i
+    uint32_t roles[kVariateMaxRows / 4];  // role of row i in byte i % 4 of word i / 4
     int32_t groups, vall, n_tok, n_enc, heads, cov;
     float scale;
     int32_t heads_per_block, nblk;  // set by launch_variate

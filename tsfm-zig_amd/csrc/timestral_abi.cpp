@@ -103,8 +103,8 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
         return fail(TSFM_E_INVALID, "a covariate array with no rows (error.InvalidInput)");
     if ((a->past || a->known) && !M.covariate_enabled)
         return fail(TSFM_E_UNSUPPORTED, "covariates with covariate_enabled off (error.CovariatesUnsupported)");
-    if ((int64_t)a->variates + a->n_past + a->n_known > 16)
-        return fail(TSFM_E_UNSUPPORTED, "at most 16 rows (variates and covariates) per series");
+    if ((int64_t)a->variates + a->n_past + a->n_known > TSFM_VARIATE_MAX_ROWS)
+        return fail(TSFM_E_UNSUPPORTED, "at most %d rows (variates and covariates) per series", TSFM_VARIATE_MAX_ROWS);
     if ((a->flags & TSFM_TIMESTRAL_BF16_ATTN) && M.use_asinh)
         return fail(TSFM_E_UNSUPPORTED, "bf16 time attention with use_asinh: the sinh expansion of the head "
                                         "outputs takes the bf16 rounding past the half-precision bar");
@@ -170,7 +170,7 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     const int V = a->variates, R = a->batch * V, n_cov = a->n_past + a->n_known, vall = V + n_cov;
     const bool cov = n_cov > 0;
     const int groups = a->symmetric_averaging ? 2 * a->batch : a->batch, rows = groups * vall;
-    uint32_t role_words[4] = {0, 0, 0, 0};  // model.Role per row of a series, byte i = row i
+    uint32_t role_words[TSFM_VARIATE_MAX_ROWS / 4] = {};  // model.Role per row of a series, byte i = row i
     for (int i = 0; i < vall; i++)
         role_words[i / 4] |= (uint32_t)(i < V ? 0 : i < V + a->n_past ? 1 : tsfm::kRoleKnown) << (8 * (i % 4));
     const int max_context = a->max_context > 0 ? a->max_context : M.context_length;
@@ -388,7 +388,7 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
                         vp.gate = at.gate ? G : nullptr; vp.gate_row = (int64_t)sl * d; vp.gate_tok = d;
                         vp.key_valid = kv + p0; vp.kv_row = cap_p;
                         vp.groups = groups; vp.vall = vall; vp.n_tok = sl; vp.n_enc = m; vp.heads = nh; vp.cov = cov ? 1 : 0;
-                        for (int i = 0; i < 4; i++) vp.roles[i] = role_words[i];
+                        for (int i = 0; i < TSFM_VARIATE_MAX_ROWS / 4; i++) vp.roles[i] = role_words[i];
                         vp.scale = sm_scale;
                         if ((e2 = tsfm::launch_variate(vp, s)) != hipSuccess) return e2;
                     }

@@ -48,6 +48,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 
 DEVICE_PTRS = 1
+VARIATE_MAX_ROWS = 256  # TSFM_VARIATE_MAX_ROWS: rows per series of the variate and Timestral forecast calls
 TIMESTRAL_BF16_ATTN = 2  # tsfm_timestral_forecast: time attention in bf16
 
 # Every symbol include/tsfm_attn.h declares.
@@ -193,7 +194,7 @@ class VariateArgs(ctypes.Structure):
         ("gate_tok", ctypes.c_int64),
         ("key_valid", ctypes.c_void_p),
         ("kv_row", ctypes.c_int64),
-        ("roles", ctypes.c_uint8 * 16),
+        ("roles", ctypes.POINTER(ctypes.c_uint8)),
         ("stream", ctypes.c_void_p),
     ]
 
@@ -750,7 +751,8 @@ def timestral_variate_attention(qkv, o, key_valid, roles: Sequence[int], cov: bo
     are staged through the library and the call returns when o is written."""
     sl = ne + h
     device = _is_device(qkv)
-    role_bytes = (ctypes.c_uint8 * 16)(*[int(r) for r in list(roles)[:16]])
+    role_list = [int(r) for r in roles]
+    role_bytes = (ctypes.c_uint8 * max(len(role_list), 1))(*role_list)
     a = VariateArgs(dtype=_dtype_code(qkv), groups=groups, vall=vall, n_tok=sl, n_enc=ne, heads=nh, head_dim=hd,
                     cov=int(bool(cov)), scale=1.0 / math.sqrt(hd), flags=DEVICE_PTRS if device else 0,
                     qkv=_ptr(qkv), qkv_row=sl * 3 * d, qkv_tok=3 * d, o=_ptr(o), o_row=sl * d, o_tok=d,
