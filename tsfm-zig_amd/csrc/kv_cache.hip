@@ -13,8 +13,11 @@
 //      {4g..4g+3, 16+4g..16+4g+3} of every dim, so a lane's A operand is one 16-byte load and a
 //      16-lane group reads 256 contiguous bytes.
 // Decode reads both straight from HBM with no LDS staging: one workgroup per
-// (series, head, 32 queries); its four waves take key tiles t = w, w+4, ... and merge their
-// (max, sum, O) partials through LDS at the end (split-key flash decoding).
+// (series, head, 32 queries); its four waves take 32-key tiles t = w, w+4, ... (fine enough that
+// the waves of a 288..544-key decode block finish within a tile of each other) and merge their
+// (max, sum, O) partials through LDS at the end (split-key flash decoding). The Q operands sit in
+// LDS, read again every tile, so a wave holds 126 VGPRs and four workgroups (16 waves, 39 KB of
+// LDS each) fit a CU: 1024 resident workgroups, each with the next tile's loads in flight.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -24,7 +27,8 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int NK = 64;
+constexpr int NK = 32;  // keys per tile: 16-key S blocks x NK / 16, 32-key V chunks x NK / 32
+constexpr int NKB = NK / 16, NCH = NK / 32;
 constexpr int NWAVE = 4;
 constexpr int NT = 64 * NWAVE;
 constexpr int QB = 32;  // queries per workgroup
@@ -105,13 +109,30 @@ __global__ __launch_bounds__(256) void kv_append(KvLayout c, const uint16_t* __r
 // no wave waits for the cache writes, and each wave's first tile, if it holds old keys only, is
 // loading meanwhile.
 template <bool BF16, bool APPEND>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void kv_attend(
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void kv_attend(
     KvLayout c, const uint16_t* __restrict__ q, int64_t q_tok, int64_t q_batch, uint16_t* __restrict__ o, int64_t o_tok,
     int64_t o_batch, int32_t n_q, int32_t q_pos0, int32_t n_k, float scale, KvNew nw) {
-    __shared__ float part_m[NWAVE][QB], part_l[NWAVE][QB];
-    __shared__ __attribute__((aligned(16))) float part_o[NWAVE][QB][kHeadDim + 4];
-    __shared__ __attribute__((aligned(16))) u32x4 new_k[APPEND ? QB * 8 : 1];        // [token][8 x 16 B]
-    __shared__ __attribute__((aligned(16))) u32x4 new_v[APPEND ? 4 * kHeadDim : 1];  // [octet][dim] slots
+    // LDS: the Q operands, and the waves' partial results for the merge at the end or, with
+    // APPEND, the block's new K rows and V chunk during the loop (the last two are separated by a
+    // barrier and share their space).
+    struct Merge {
+        float m[NWAVE][QB], l[NWAVE][QB];
+        float o[NWAVE][QB][kHeadDim + 4];
+    };
+    struct New {
+        u32x4 k[QB * 8];          // [token][8 x 16 B]
+        u32x4 v[4 * kHeadDim];    // [octet][dim] slots
+    };
+    constexpr size_t kLdsBytes = sizeof(Merge) > sizeof(New) ? sizeof(Merge) : sizeof(New);
+    struct Qs {
+        u32x4 f[2][2][64];  // the Q^T operands, [query block][dim half][lane]
+    };
+    __shared__ __attribute__((aligned(16))) char lds[sizeof(Qs) + kLdsBytes];
+    Qs& qs = *reinterpret_cast<Qs*>(lds);
+    Merge& mg = *reinterpret_cast<Merge*>(lds + sizeof(Qs));
+    New& nwl = *reinterpret_cast<New*>(lds + sizeof(Qs));
+    u32x4* const new_k = nwl.k;
+    u32x4* const new_v = nwl.v;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
@@ -133,19 +154,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const uint16_t* const Kc = Kw;
     const uint16_t* const Vc = Vw;
 
-    u32x4 qf[2][2];
+    if (wave == 0) {
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int qi = qi0 + 16 * qb + ql;
-        u32x4 lo = {0, 0, 0, 0}, hi = lo;
-        if (qi < n_q) {
-            const uint16_t* src = q + b * q_batch + (int64_t)qi * q_tok + h * kHeadDim + 8 * g;
-            lo = ldu4(src);
-            hi = ldu4(src + 32);
+        for (int qb = 0; qb < 2; qb++) {
+            const int qi = qi0 + 16 * qb + ql;
+            u32x4 lo = {0, 0, 0, 0}, hi = lo;
+            if (qi < n_q) {
+                const uint16_t* src = q + b * q_batch + (int64_t)qi * q_tok + h * kHeadDim + 8 * g;
+                lo = ldu4(src);
+                hi = ldu4(src + 32);
+            }
+            qs.f[qb][0][lane] = lo;
+            qs.f[qb][1][lane] = hi;
         }
-        qf[qb][0] = lo;
-        qf[qb][1] = hi;
     }
+    if (!APPEND) __syncthreads();
 
     float mc_run[2] = {kNegInf, kNegInf};
     float l_run[2] = {0.f, 0.f};
@@ -158,12 +181,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // Operand fragments of one tile, loaded straight from the cache. Rows past n_k (up to the
     // capacity) are read but always masked: the cache is zero-filled at creation, so they hold
     // finite values and contribute exactly 0.
-    u32x4 kf[4][2], vf[2][4];
+    u32x4 kf[NKB][2], vf[NCH][4];
     // With APPEND, the 16-key blocks and the 32-key chunk of the new tokens come from LDS (the
     // choice is uniform: the new block is one whole chunk).
     auto load_k = [&](int kbase) {
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
+        for (int kb = 0; kb < NKB; kb++) {
             const int key0 = kbase + kb * 16;
             if (APPEND && key0 >= q_pos0 && key0 < q_pos0 + QB) {
                 const u32x4* kr = new_k + (key0 - q_pos0 + ql) * 8 + g;
@@ -178,7 +201,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     };
     auto load_v = [&](int kbase) {
 #pragma unroll
-        for (int ch = 0; ch < 2; ch++) {
+        for (int ch = 0; ch < NCH; ch++) {
             const int chunk = (kbase >> 5) + ch;
             if (APPEND && chunk == (q_pos0 >> 5)) {
 #pragma unroll
@@ -229,9 +252,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     for (; t < ntiles; t += NWAVE) {
         const int kbase = t * NK;
         const int tn = t + NWAVE;
-        f32x4 sacc[4][2];
+        asm volatile("" ::: "memory");  // Q is read from LDS every tile, not kept in registers
+        u32x4 qf[2][2];
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++)
+        for (int qb = 0; qb < 2; qb++) {
+            qf[qb][0] = qs.f[qb][0][lane];
+            qf[qb][1] = qs.f[qb][1][lane];
+        }
+        f32x4 sacc[NKB][2];
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
             for (int qb = 0; qb < 2; qb++)
                 sacc[kb][qb] = mfma<BF16>(kf[kb][1], qf[qb][1], mfma<BF16>(kf[kb][0], qf[qb][0], f32x4{0, 0, 0, 0}));
@@ -243,7 +273,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             const int qpos = qlo + 16 * qb + ql;
             float mloc = kNegInf;
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+            for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     float x = sacc[kb][qb][r];
@@ -258,7 +288,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             mc_run[qb] = mn;
             float lsum = 0.f;
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+            for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][r], c2, -mc_use));
@@ -271,7 +301,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
 
 #pragma unroll
-        for (int ch = 0; ch < 2; ch++) {
+        for (int ch = 0; ch < NCH; ch++) {
             u32x4 pf[2];
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) {
@@ -288,31 +318,32 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
 
     // ---- merge the four waves' partial results ----
+    if (APPEND) __syncthreads();  // every wave is done with the new rows in LDS
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
         const float l = sum4(l_run[qb]);
         const int qq = 16 * qb + ql;
         if (g == 0) {
-            part_m[wave][qq] = mc_run[qb];
-            part_l[wave][qq] = l;
+            mg.m[wave][qq] = mc_run[qb];
+            mg.l[wave][qq] = l;
         }
 #pragma unroll
-        for (int db = 0; db < 4; db++) st4(&part_o[wave][qq][16 * db + 4 * g], oacc[db][qb]);
+        for (int db = 0; db < 4; db++) st4(&mg.o[wave][qq][16 * db + 4 * g], oacc[db][qb]);
     }
     __syncthreads();
     {
         const int qq = tid >> 3, d0 = 8 * (tid & 7);  // 32 queries x 8 dim groups
         float M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < NWAVE; w++) M = fmaxf(M, part_m[w][qq]);
+        for (int w = 0; w < NWAVE; w++) M = fmaxf(M, mg.m[w][qq]);
         float L = 0.f;
         f32x4 a0 = {0, 0, 0, 0}, a1 = a0;
 #pragma unroll
         for (int w = 0; w < NWAVE; w++) {
-            const float f = part_m[w][qq] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(part_m[w][qq] - M);
-            L += f * part_l[w][qq];
-            a0 += f * ld4(&part_o[w][qq][d0]);
-            a1 += f * ld4(&part_o[w][qq][d0 + 4]);
+            const float f = mg.m[w][qq] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mg.m[w][qq] - M);
+            L += f * mg.l[w][qq];
+            a0 += f * ld4(&mg.o[w][qq][d0]);
+            a1 += f * ld4(&mg.o[w][qq][d0 + 4]);
         }
         if (qq < nqv) {
             const float inv = 1.0f / L;
