@@ -133,7 +133,10 @@ __device__ __forceinline__ void load_q(QBlock& w, const float* Q, const float* R
 // and no mask arithmetic; otherwise only the first nkb key blocks are computed and every score goes
 // through the mask rule. hook(phase, kb) runs at fixed points (S block kb, after S, PV block kb)
 // whether or not the block is computed: the streaming kernel stages the next tile there.
-template <int MASK, int BIAS, bool PLAIN, int NKB, class Hook>
+// VROW: vt holds V as rows [key][64] and the O^T accumulator takes the dims in the order
+// 16g + 4r + db (register r of w.o[db]): the V operands of one key for the four dim blocks are then
+// four consecutive floats of its row (the bits of O are the same; only its register order moves).
+template <int MASK, int BIAS, bool PLAIN, int NKB, bool VROW, class Hook>
 __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const float* kt, const float* vt,
                                             const float* kat, const float* lut, int kbase, int nkb, int qi, int h,
                                             int ql, int g, Hook&& hook) {
@@ -246,6 +249,19 @@ __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const fl
     for (int kb = 0; kb < NKB; kb++) {
         hook(2, kb);
         if (!PLAIN && kb >= nkb) continue;
+        if (VROW) {
+            // Lane (ql, g), register r: key 16 kb + 4 g + r, dims 4 ql .. 4 ql + 3 (dim block db ->
+            // dim 4 ql + db).
+            const float* vr = vt + (kb * 16 + 4 * g) * kHeadDim + 4 * ql;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const f32x4 va = ld4(vr + r * kHeadDim);
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+                    w.o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db], sacc[kb][r], w.o[db], 0, 0, 0);
+            }
+            continue;
+        }
         const float* vq4 = vt + (kb * 4 + g) * (kHeadDim * 4);
 #pragma unroll
         for (int dp = 0; dp < 4; dp += 2) {  // two dim blocks at a time: eight V values live
@@ -262,7 +278,8 @@ __device__ __forceinline__ void attend_tile(QBlock& w, const Params& p, const fl
 // The last few keys of a row (at most kValuKeys) on the VALU instead of a whole key block of
 // matrix instructions: per key, the lane's 16-dim partial dot product (four FMA chains and a tree),
 // summed over the query's four lanes, then the same bias, mask and online-softmax update as the
-// tile body with one score, and O += e v. Same tile operands in LDS as attend_tile.
+// tile body with one score, and O += e v. Same tile operands in LDS as attend_tile (VROW: V rows
+// [key][64] and the O register order of attend_tile's VROW).
 constexpr int kValuKeys = 4;
 template <int MASK, int BIAS, bool VROW>
 __device__ __forceinline__ void attend_keys_valu(QBlock& w, const Params& p, const float* kt, const float* vt,
@@ -300,8 +317,8 @@ __device__ __forceinline__ void attend_keys_valu(QBlock& w, const Params& p, con
         for (int db = 0; db < 4; db++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int dim = 16 * db + 4 * g + r;
-                const float vv = VROW ? vt[j * KPAD + dim] : vt[(j >> 2) * (kHeadDim * 4) + vslot(dim) * 4 + (j & 3)];
+                const int dim = VROW ? 16 * g + 4 * r + db : 16 * db + 4 * g + r;
+                const float vv = VROW ? vt[j * kHeadDim + dim] : vt[(j >> 2) * (kHeadDim * 4) + vslot(dim) * 4 + (j & 3)];
                 w.o[db][r] = __builtin_fmaf(e, vv, w.o[db][r] * alpha);
             }
     }
@@ -349,8 +366,9 @@ __device__ __forceinline__ void thin_store_q(const QBlock& w, float* qs, int ql,
 }
 
 // Keys kbase .. kbase + nkeys - 1 (1 <= nkeys <= 64) of query qi. kt / vt / kat: the keys' K rows,
-// V key quads and key terms; qs: the query (thin_store_q); ps: 64 floats of LDS for the weights.
-template <int MASK, int BIAS>
+// V key quads (VROW: V rows [key][64]) and key terms; qs: the query (thin_store_q); ps: 64 floats of
+// LDS for the weights.
+template <int MASK, int BIAS, bool VROW = false>
 __device__ __forceinline__ void attend_thin(QBlock& w, const Params& p, const float* kt, const float* vt,
                                             const float* kat, const float* lut, const float* qs, float* ps, int kbase,
                                             int nkeys, int qi, int h, int lane) {
@@ -385,10 +403,13 @@ __device__ __forceinline__ void attend_thin(QBlock& w, const Params& p, const fl
 
     ps[lane] = e;  // read back below by the same wave: LDS keeps a wave's accesses in order
     float o = w.o[0][0] * alpha;
-    const float* vd = vt + vslot(lane) * 4;
+    const float* vd = vt + (VROW ? lane : vslot(lane) * 4);
     const int nq4 = (nkeys + 3) >> 2;
     for (int kq = 0; kq < nq4; kq++) {
-        const f32x4 p4 = ld4(ps + 4 * kq), v4 = ld4(vd + kq * (kHeadDim * 4));
+        const f32x4 p4 = ld4(ps + 4 * kq);
+        const f32x4 v4 = VROW ? f32x4{vd[(4 * kq) * kHeadDim], vd[(4 * kq + 1) * kHeadDim], vd[(4 * kq + 2) * kHeadDim],
+                                      vd[(4 * kq + 3) * kHeadDim]}
+                              : ld4(vd + kq * (kHeadDim * 4));
         o = __builtin_fmaf(p4[0], v4[0], o);
         o = __builtin_fmaf(p4[1], v4[1], o);
         o = __builtin_fmaf(p4[2], v4[2], o);
@@ -404,14 +425,18 @@ __device__ __forceinline__ void store_thin(const QBlock& w, float* O, const Para
     O[(int64_t)qi * p.o_tok + lane] = w.o[0][0] * inv;
 }
 
-// Normalise and store query qi: lane holds dims 16db + 4g + r.
+// Normalise and store query qi: lane holds dims 16db + 4g + r (VROW: 16g + 4r + db).
+template <bool VROW = false>
 __device__ __forceinline__ void store_o(const QBlock& w, float* O, const Params& p, int qi, int g) {
     const float l = sum4(w.l);
     if (qi >= p.n_q) return;
     const float inv = 1.0f / l;
     float* dst = O + (int64_t)qi * p.o_tok;
 #pragma unroll
-    for (int db = 0; db < 4; db++) st4(dst + 16 * db + 4 * g, w.o[db] * inv);
+    for (int i = 0; i < 4; i++) {
+        if (VROW) st4(dst + 16 * g + 4 * i, f32x4{w.o[0][i], w.o[1][i], w.o[2][i], w.o[3][i]} * inv);
+        else st4(dst + 16 * i + 4 * g, w.o[i] * inv);
+    }
 }
 
 // T5 bias of head h by relative index t = j - i + n_q - 1, stored at lut_raw[kLutPad + t] for t in
@@ -602,10 +627,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void
             // next tile, if the workgroup has one, in one go).
             const bool few = !plain && nkb > 0 && wave_kend - kbase <= kValuKeys;
             if (plain) {
-                attend_tile<MASK, BIAS, true, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g,
+                attend_tile<MASK, BIAS, true, 4, false>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g,
                                                  stage_next);
             } else if (nkb > 0 && !few) {
-                attend_tile<MASK, BIAS, false, 4>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g,
+                attend_tile<MASK, BIAS, false, 4, false>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g,
                                                   stage_next);
             } else if (more) {
                 kvb_next = stage_all(nxt, nbase);
@@ -662,7 +687,7 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     extern __shared__ __attribute__((aligned(16))) float smem[];
     const ResidentLayout lay = resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
     const int q_tiles = (p.n_q + RQT - 1) / RQT;
     const int rope_tabs = p.rope_rows_per_table;
@@ -672,6 +697,8 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     struct Item {
         int b, h, wq0;
         const float* Q;
+        const float* K;
+        const float* V;
         const float* RC;
         const float* RS;
         __amdgpu_buffer_rsrc_t k_buf, v_buf, c_buf, s_buf, kv_rsrc;
@@ -685,6 +712,8 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         I.Q = static_cast<const float*>(p.q) + I.b * p.q_batch + I.h * kHeadDim;
         const float* K = static_cast<const float*>(p.k) + I.b * p.k_batch + I.h * kHeadDim;
         const float* V = static_cast<const float*>(p.v) + I.b * p.v_batch + I.h * kHeadDim;
+        I.K = K;
+        I.V = V;
         const int rope_tab = rope_tabs > 0 ? (p.rope_row0 + I.b) / rope_tabs : 0;
         I.RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
         I.RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
@@ -697,8 +726,13 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         return I;
     };
 
-    // ---- staging of one item: loads into registers (K rotated at the store), then stores into one
-    //      of the two LDS buffers ----
+    // ---- staging of one item. Without RoPE (kDma) K and V go from HBM straight into the other LDS
+    //      buffer (buffer_load ... lds), so no registers hold them through the compute phase: K as
+    //      rows [key][KPAD] (the pad chunk of each row reads zeros out of range), V as rows [key][64]
+    //      (the VROW operand order). With RoPE they load into registers, K is rotated at the store
+    //      and V is stored key-quad-transposed. q, the T5 table value and the key_valid byte load
+    //      into registers either way. ----
+    constexpr bool kDma = !ROPE;
     f32x4 klo[RKIT], khi[RKIT], kcs[RKIT], ksn[RKIT];
     f32x4 v01[RVIT], v23[RVIT];
     uint32_t kvb = 1;
@@ -727,6 +761,7 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         }
         if (lut_bucket >= 0) lut_val = p.rel_table[lut_bucket * p.H + I.h];
         if (mask_reads_valid<MASK>() && tid < lay.nkp) kvb = __builtin_amdgcn_raw_buffer_load_b8(I.kv_rsrc, tid, 0, 0);
+        if (kDma) return;
 #pragma unroll
         for (int u = 0; u < RKIT; u++) {  // K item = (row, c): dims 4c..4c+3 and 32+4c..32+4c+3
             const int it = tid + u * RNT, row = it >> 3, c = it & 7;
@@ -749,26 +784,51 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             v23[u] = f32x4{c[0], c[1], d[0], d[1]};
         }
     };
-    // The staged item into buffer `buf`, and the wave's QBlock for it (q rotated and scaled as
-    // load_q does).
+    // kDma: the item's K and V into buffer `buf`, 1 KB (64 lanes x 16 bytes) per instruction, the
+    // instructions dealt to the waves in turn. K chunk c of the K region is row c / 17, 16-byte piece
+    // c % 17 (piece 16: the row's padding); V chunk c is row c / 16, piece c % 16. Rows from n_k up
+    // to nkp read as zeros (the descriptors end after key n_k - 1). Issued right after the barrier
+    // that released `buf`; read after the wave's `s_waitcnt vmcnt(0)` and the next barrier.
+    auto stage_dma = [&](const Item& I, float* buf) {
+        const uint32_t lbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)buf;
+        const u32x4 kd = buf_desc(I.K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 4));
+        const u32x4 vd = buf_desc(I.V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 4));
+        const int nk_chunks = lay.nkp * (KPAD / 4), nk_ins = (nk_chunks + 63) / 64;
+        const int n_ins = nk_ins + lay.nkp / 4;  // V: nkp rows x 16 pieces = nkp / 4 instructions
+        for (int i = wave; i < n_ins; i += RNW) {
+            if (i < nk_ins) {
+                const int c = 64 * i + lane, row = c / (KPAD / 4), piece = c - row * (KPAD / 4);
+                const uint32_t off = piece < kHeadDim / 4 ? (uint32_t)(row * p.k_tok + 4 * piece) * 4u : 0x80000000u;
+                if (c < nk_chunks) dma16(kd, lbase + 1024u * i, off, 0u);
+            } else {
+                const int c = 64 * (i - nk_ins) + lane, row = c >> 4, piece = c & 15;
+                dma16(vd, lbase + (uint32_t)lay.v_off * 4u + 1024u * (i - nk_ins),
+                      (uint32_t)(row * p.v_tok + 4 * piece) * 4u, 0u);
+            }
+        }
+    };
+    // The staged item's remaining parts into buffer `buf` (with registers: K and V too), and the
+    // wave's QBlock for it (q rotated and scaled as load_q does).
     auto stage_store = [&](const Item& I, float* buf, QBlock& w) {
         float* const Ks = buf;
         float* const Vs = buf + lay.v_off;
+        if (!kDma) {
 #pragma unroll
-        for (int u = 0; u < RKIT; u++) {
-            const int it = tid + u * RNT, row = it >> 3, c = it & 7;
-            if (row >= lay.nkp) continue;
-            if (ROPE) rope4(klo[u], khi[u], kcs[u], ksn[u]);
-            st4(Ks + row * KPAD + 4 * c, klo[u]);
-            st4(Ks + row * KPAD + 32 + 4 * c, khi[u]);
-        }
+            for (int u = 0; u < RKIT; u++) {
+                const int it = tid + u * RNT, row = it >> 3, c = it & 7;
+                if (row >= lay.nkp) continue;
+                if (ROPE) rope4(klo[u], khi[u], kcs[u], ksn[u]);
+                st4(Ks + row * KPAD + 4 * c, klo[u]);
+                st4(Ks + row * KPAD + 32 + 4 * c, khi[u]);
+            }
 #pragma unroll
-        for (int u = 0; u < RVIT; u++) {
-            const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
-            if (4 * quad >= lay.nkp) continue;
-            float* vd = Vs + quad * (kHeadDim * 4);
-            st4(vd + vslot(2 * vc) * 4, f32x4{v01[u][0], v01[u][2], v23[u][0], v23[u][2]});
-            st4(vd + vslot(2 * vc + 1) * 4, f32x4{v01[u][1], v01[u][3], v23[u][1], v23[u][3]});
+            for (int u = 0; u < RVIT; u++) {
+                const int it = tid + u * RNT, quad = it >> 5, vc = it & 31;
+                if (4 * quad >= lay.nkp) continue;
+                float* vd = Vs + quad * (kHeadDim * 4);
+                st4(vd + vslot(2 * vc) * 4, f32x4{v01[u][0], v01[u][2], v23[u][0], v23[u][2]});
+                st4(vd + vslot(2 * vc + 1) * 4, f32x4{v01[u][1], v01[u][3], v23[u][1], v23[u][3]});
+            }
         }
         if (tid < lay.nkp) buf[lay.a_off + tid] = key_term<MASK>(tid, p.n_k, kvb != 0, p.ctx_keys);
         if (lut_in_regs) {
@@ -797,23 +857,23 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         if (max(0, min(16, p.n_q - I.wq0)) == 1) thin_store_q(w, buf + lay.t_off, ql, g);
     };
 
-    // ---- one item's attention over the keys resident in `buf` ----
+    // ---- one item's attention over the keys resident in `buf` (the store follows separately) ----
+    // Offset of key k's V in a buffer's V region: rows (kDma) or key quads.
+    auto v_at = [&](const float* Vs, int k) { return Vs + (kDma ? k * kHeadDim : (k >> 2) * (kHeadDim * 4)); };
     auto compute = [&](const Item& I, const float* buf, QBlock& w) {
         const float* const Ks = buf;
         const float* const Vs = buf + lay.v_off;
         const float* const kadd = buf + lay.a_off;
         const float* const lut = buf + lay.l_off + kLutPad;
         float* const thin_qp = const_cast<float*>(buf) + lay.t_off;
-        float* __restrict__ O = static_cast<float*>(p.o) + I.b * p.o_batch + I.h * kHeadDim;
         const int wq0 = I.wq0, qi = wq0 + ql, h = I.h;
         const int wave_nq = max(0, min(16, p.n_q - wq0));
         if (wave_nq == 0) return;
         const int wave_kend = key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys);
         if (wave_nq == 1) {  // one query: the VALU path, 64 resident keys at a time
             for (int kb0 = 0; kb0 < wave_kend; kb0 += 64)
-                attend_thin<MASK, BIAS>(w, p, Ks + kb0 * KPAD, Vs + (kb0 >> 2) * (kHeadDim * 4), kadd + kb0, lut,
-                                        thin_qp, thin_qp + kHeadDim, kb0, min(64, wave_kend - kb0), wq0, h, lane);
-            store_thin(w, O, p, wq0, lane);
+                attend_thin<MASK, BIAS, kDma>(w, p, Ks + kb0 * KPAD, v_at(Vs, kb0), kadd + kb0, lut, thin_qp,
+                                              thin_qp + kHeadDim, kb0, min(64, wave_kend - kb0), wq0, h, lane);
             return;
         }
         auto no_hook = [](int, int) {};
@@ -829,40 +889,57 @@ __global__ __launch_bounds__(RNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                 plain = __ballot(lane < RNK && kadd[kbase + (lane & (RNK - 1))] != 0.f) == 0;
             if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + RNK - 1 <= p.q_pos0 + wq0;
             const float* kt = Ks + kbase * KPAD;
-            const float* vt = Vs + (kbase >> 2) * (kHeadDim * 4);
+            const float* vt = v_at(Vs, kbase);
             if (plain)
-                attend_tile<MASK, BIAS, true, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g, no_hook);
+                attend_tile<MASK, BIAS, true, 2, kDma>(w, p, kt, vt, kadd + kbase, lut, kbase, 2, qi, h, ql, g,
+                                                       no_hook);
             else
-                attend_tile<MASK, BIAS, false, 2>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g, no_hook);
+                attend_tile<MASK, BIAS, false, 2, kDma>(w, p, kt, vt, kadd + kbase, lut, kbase, nkb, qi, h, ql, g,
+                                                        no_hook);
         }
         if (kloop < wave_kend)
-            attend_keys_valu<MASK, BIAS, false>(w, p, Ks + kloop * KPAD, Vs + (kloop >> 2) * (kHeadDim * 4),
-                                                kadd + kloop, lut, kloop, wave_kend - kloop, qi, h, g);
-        store_o(w, O, p, qi, g);
+            attend_keys_valu<MASK, BIAS, kDma>(w, p, Ks + kloop * KPAD, v_at(Vs, kloop), kadd + kloop, lut, kloop,
+                                               wave_kend - kloop, qi, h, g);
+    };
+    auto store = [&](const Item& I, const QBlock& w) {
+        float* __restrict__ O = static_cast<float*>(p.o) + I.b * p.o_batch + I.h * kHeadDim;
+        const int wave_nq = max(0, min(16, p.n_q - I.wq0));
+        if (wave_nq == 0) return;
+        if (wave_nq == 1) store_thin(w, O, p, I.wq0, lane);
+        else store_o<kDma>(w, O, p, I.wq0 + ql, g);
     };
 
-    // ---- persistent loop: item i + gridDim.x loads into registers while item i computes, and is
-    //      stored into the other buffer after it (the one item i - gridDim.x used, whose readers all
-    //      passed the previous barrier) ----
+    // ---- persistent loop: item i + gridDim.x stages while item i computes, into the other buffer
+    //      (the one item i - gridDim.x used, whose readers all passed the previous barrier); with
+    //      registers, its stores follow item i's compute ----
     int it = blockIdx.x;
     if (it >= n_items) return;
     QBlock w;
     Item cur = item_of(it);
     stage_load(cur);
+    if (kDma) {
+        stage_dma(cur, smem);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     stage_store(cur, smem, w);
     __syncthreads();
     for (int k = 0;; k++) {
         const int nxt = it + gridDim.x;
         const bool more = nxt < n_items;
+        float* const nb = smem + ((k + 1) & 1) * lay.total;
         Item next;
         if (more) {
             next = item_of(nxt);
             stage_load(next);
+            if (kDma) stage_dma(next, nb);
         }
-        float* const cb = smem + (k & 1) * lay.total;
-        compute(cur, cb, w);
+        compute(cur, smem + (k & 1) * lay.total, w);
+        // The next item's LDS copies have landed (waited before this item's O stores are issued, so
+        // the wait does not include them).
+        if (kDma && more) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        store(cur, w);
         if (!more) break;
-        stage_store(next, smem + ((k + 1) & 1) * lay.total, w);
+        stage_store(next, nb, w);
         // LDS-only barrier: the next item's LDS writes are complete and visible, and every wave has
         // left the buffer the item after it will overwrite. No global access crosses it, so it
         // does not wait for this item's O stores (a __syncthreads() fence would, once per item).

@@ -89,24 +89,6 @@ constexpr uint32_t kVBase = 3 * kStageBytes;
 typedef __attribute__((address_space(3))) u32x4* lds_u32x4_ptr;
 __device__ __forceinline__ u32x4 lds_read16(uint32_t addr) { return *(lds_u32x4_ptr)(uintptr_t)addr; }
 
-// 16 bytes per lane from a buffer straight into LDS (lane l's at lds + 16 l), issued as inline
-// assembly: the compiler then does not see an LDS write whose address it cannot separate from the
-// kernel's LDS reads, and does not put a wait for every outstanding global load in front of them.
-// The stage a load fills is read only after the loop's own `s_waitcnt vmcnt(0)` and barrier.
-// (Loads the compiler does not know of only make its own vmcnt waits more conservative.)
-__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-                 : "memory", "m0");
-}
-// Raw buffer descriptor over `bytes` bytes at base (loads past the end return 0), in SGPRs.
-__device__ __forceinline__ u32x4 buf_desc(const void* base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)base;
-    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                 (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
-                 (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), (uint32_t)kBufferConfig};
-}
 __device__ __forceinline__ u32x2 lds_read_tr(uint32_t addr) {
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(uintptr_t)addr));
 }

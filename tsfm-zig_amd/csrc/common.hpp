@@ -138,6 +138,26 @@ constexpr int kBufferConfig = 0x00020000;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferConfig);
 }
+// 16 bytes per lane from a buffer straight into LDS (lane l's at lds + 16 l), issued as inline
+// assembly: the compiler then does not see an LDS write whose address it cannot separate from the
+// kernel's LDS reads, and does not put a wait for every outstanding global load in front of them.
+// A caller reads what a load fills only after its own `s_waitcnt vmcnt(0)` and a barrier.
+// (Loads the compiler does not know of only make its own vmcnt waits more conservative.)
+// lds and soff are wave-uniform (taken from the first lane, so they sit in SGPRs).
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
+                 : "memory", "m0");
+}
+// Raw buffer descriptor over `bytes` bytes at base (loads past the end return 0), in SGPRs.
+__device__ __forceinline__ u32x4 buf_desc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu)),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), (uint32_t)kBufferConfig};
+}
 __device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
