@@ -518,6 +518,43 @@ typedef struct tsfm_timestral_forecast_args {
 int tsfm_timestral_forecast(const tsfm_timestral_forecast_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * Categorical covariates of a Timestral forecast (Covariates.cat_past / .cat_known,
+ * src/timestral/forecaster.zig:34-46), encoded into the numeric rows tsfm_timestral_forecast takes,
+ * as forecast does before its passes (:86-103): with one target variate each code row is
+ * target-encoded against the series' target (encodingTarget :201-217, encodeCategorical
+ * :220-238, targetEncode :243-289, slotOf :292-301), otherwise the codes pass through as f32.
+ *
+ * Encoding target of series s: the forward-filled target from its first observation on, over the
+ * last max_context steps of the context (NaN before the first observation and outside the
+ * window). Per code row: mean = the mean of the finite target values (0 when none); categories =
+ * the distinct finite codes of the context part; a context step whose target is finite adds its
+ * target to its category's sum and count (a non-finite code to the missing category's). A context
+ * code becomes (mean + sum_c) / (1 + count_c) of its category (non-finite codes: the missing
+ * category's), and NaN where both the code and the encoding target are NaN; a future code
+ * (steps t .. len-1) becomes its category's value, the missing category's for NaN, and the mean
+ * for a code not among the categories. Sums in f64 in step order, the result rounded to f32.
+ *
+ * The reference appends the encoded rows after the numeric covariate rows of each series
+ * (catChannels, :186-195): this call writes code row j of series s to out row s * out_rows + row0
+ * + j (len floats each), so a caller builds the combined past / known array in place. Host
+ * memory, synchronous, no device needed. Returns TSFM_OK or TSFM_E_INVALID. */
+typedef struct tsfm_categorical_args {
+    float *out;               /* (batch, out_rows, len) f32 */
+    int32_t out_rows, row0;   /* rows per series in out; the first encoded row's index */
+    const double *codes;      /* (batch, n_cat, len) category codes, NaN = missing */
+    int32_t batch, n_cat;
+    int64_t len;              /* t (past codes) or t + horizon (known codes); >= t */
+    const float *inputs;      /* (batch, variates, t) targets, zeros where unobserved */
+    const uint8_t *observed;  /* (batch, variates, t) */
+    int32_t variates;         /* target variates per series (encoding only when 1) */
+    int64_t t;                /* context steps */
+    int64_t max_context;      /* the forecast's window (its max_context, or the model's
+                                 context_length when that is 0); > 0 */
+} tsfm_categorical_args;
+
+int tsfm_timestral_encode_categorical(const tsfm_categorical_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * The reference backend's GEMM seam, with the argument lists and return convention of
  * src/platform/cuda/gemm.c. The reference's binding (src/platform/cuda/gpu.zig:16-44) declares
  * those functions as cuda_*; a HIP binding is the same file with the extern names changed to

@@ -272,6 +272,10 @@ int orc_timestral_forecast_cov(size_t threads, float *out, const orc_timestral_m
                                const float *past, size_t n_past, const float *known, size_t n_known,
                                size_t max_context, size_t per_shot, float cap_k, float extreme, int symmetric,
                                int clip_nonnegative);
+/* Categorical covariates (src/timestral/forecaster.zig:201-301): codes (b, c, len) f64 -> out (b, c, len) f32. */
+void orc_timestral_encode_categorical(float *out, const double *codes, size_t b, size_t c, size_t len,
+                                      const float *inputs, const uint8_t *observed, size_t v, size_t t,
+                                      size_t max_context);
 int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model *m, const float *inputs,
                            const uint8_t *observed, size_t b, size_t v, size_t t, size_t horizon, size_t max_context,
                            size_t per_shot, float cap_k, float extreme, int symmetric, int clip_nonnegative);

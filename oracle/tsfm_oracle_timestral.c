@@ -13,6 +13,8 @@
  *   nn.siluInPlace / mulSilu / softplus / clampNonfinite   src/core/nn.zig:399-420, 516-563
  *   forecaster forecastRaw / blockDecode / refineBlock / forecast / finish
  *                                      src/timestral/forecaster.zig:57-180, 303-421, 423-563, 565-662
+ *   encodingTarget / encodeCategorical / targetEncode / slotOf
+ *                                      src/timestral/forecaster.zig:201-301
  * with the same arithmetic as the Zig (f32 unfused, f64 where the reference uses f64).
  */
 #include <math.h>
@@ -650,4 +652,109 @@ int orc_timestral_forecast(size_t threads, float *out, const orc_timestral_model
                            size_t per_shot, float cap_k, float extreme, int symmetric, int clip_nonnegative) {
     return orc_timestral_forecast_cov(threads, out, m, inputs, observed, b, v, t, horizon, NULL, 0, NULL, 0,
                                       max_context, per_shot, cap_k, extreme, symmetric, clip_nonnegative);
+}
+
+/* ---- categorical covariates (src/timestral/forecaster.zig:201-301) --------------------------- */
+
+static int orc_cmp_f64(const void *a, const void *b) {
+    const double x = *(const double *)a, y = *(const double *)b;
+    return x < y ? -1 : x > y ? 1 : 0;
+}
+
+/* slotOf (:292-301): index of code in the sorted categories, or -1 for NaN and unknown codes. */
+static long orc_slot_of(const double *cats, size_t nc, double code) {
+    if (isnan(code)) return -1;
+    size_t lo = 0, hi = nc;
+    while (lo < hi) {
+        const size_t mid = lo + (hi - lo) / 2;
+        if (cats[mid] < code) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo < nc && cats[lo] == code ? (long)lo : -1;
+}
+
+/* targetEncode (:243-289), smooth = 1: past codes (t of them) and optional future codes. */
+static void orc_target_encode(const double *target, const double *past, size_t t, const double *future,
+                              size_t nf, float *out_past, float *out_future) {
+    const double smooth = 1.0;
+    double item_count = 0, item_sum = 0;
+    for (size_t i = 0; i < t; i++)
+        if (isfinite(target[i])) {
+            item_count += 1;
+            item_sum += target[i];
+        }
+    const double item_mean = item_count > 0 ? item_sum / item_count : 0.0;
+    double *cats = (double *)malloc((t + 1) * sizeof(double));
+    size_t n = 0;
+    for (size_t i = 0; i < t; i++)
+        if (isfinite(past[i])) cats[n++] = past[i];
+    qsort(cats, n, sizeof(double), orc_cmp_f64);
+    size_t nc = 0;
+    for (size_t i = 0; i < n; i++)
+        if (i == 0 || cats[i] != cats[nc - 1]) cats[nc++] = cats[i];
+    double *sums = (double *)calloc(nc + 1, sizeof(double));
+    double *counts = (double *)calloc(nc + 1, sizeof(double));
+    for (size_t i = 0; i < t; i++) {
+        if (!isfinite(target[i])) continue;
+        const long sl = orc_slot_of(cats, nc, past[i]);
+        const size_t slot = sl < 0 ? nc : (size_t)sl;
+        sums[slot] += target[i];
+        counts[slot] += 1;
+    }
+    for (size_t i = 0; i < t; i++) {
+        const long sl = orc_slot_of(cats, nc, past[i]);
+        const size_t slot = sl < 0 ? nc : (size_t)sl;
+        out_past[i] = (float)((smooth * item_mean + sums[slot]) / (smooth + counts[slot]));
+    }
+    for (size_t i = 0; i < nf; i++) {
+        const double cv = future[i];
+        double v;
+        if (isnan(cv)) {
+            v = (smooth * item_mean + sums[nc]) / (smooth + counts[nc]);
+        } else {
+            const long sl = orc_slot_of(cats, nc, cv);
+            v = sl >= 0 ? (smooth * item_mean + sums[sl]) / (smooth + counts[sl]) : item_mean;
+        }
+        out_future[i] = (float)v;
+    }
+    free(cats);
+    free(sums);
+    free(counts);
+}
+
+/* encodingTarget + encodeCategorical (:201-238): codes (b, c, len) -> out (b, c, len). With v == 1
+ * every code row is target-encoded against the forward-filled target over the last max_context
+ * steps (NaN before the first observation and outside the window), and a missing code where the
+ * target is NaN stays NaN; otherwise the codes pass through as f32. */
+void orc_timestral_encode_categorical(float *out, const double *codes, size_t b, size_t c, size_t len,
+                                      const float *inputs, const uint8_t *observed, size_t v, size_t t,
+                                      size_t max_context) {
+    double *target = (double *)malloc(t * sizeof(double));
+    for (size_t s = 0; s < b; s++) {
+        if (v == 1) {
+            int started = 0;
+            float last = 0;
+            for (size_t i = 0; i < t; i++) {
+                if (observed[s * t + i]) {
+                    started = 1;
+                    last = inputs[s * t + i];
+                }
+                const int in_window = t <= max_context || i >= t - max_context;
+                target[i] = started && in_window ? (double)last : NAN;
+            }
+        }
+        for (size_t j = 0; j < c; j++) {
+            const double *row = codes + (s * c + j) * len;
+            float *dst = out + (s * c + j) * len;
+            if (v != 1) {
+                for (size_t i = 0; i < len; i++) dst[i] = (float)row[i];
+                continue;
+            }
+            orc_target_encode(target, row, t, len > t ? row + t : NULL, len > t ? len - t : 0, dst,
+                              len > t ? dst + t : NULL);
+            for (size_t i = 0; i < t; i++)
+                if (isnan(target[i]) && isnan(row[i])) dst[i] = NAN;
+        }
+    }
+    free(target);
 }

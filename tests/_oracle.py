@@ -206,6 +206,8 @@ class Oracle:
         L.orc_timestral_forecast_cov.argtypes = [_sz, _vp, ctypes.POINTER(TimestralModel), _vp, _vp, _sz, _sz, _sz, _sz,
                                                  _vp, _sz, _vp, _sz, _sz, _sz, _f, _f, ctypes.c_int, ctypes.c_int]
         L.orc_timestral_forecast_cov.restype = ctypes.c_int
+        L.orc_timestral_encode_categorical.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _sz, _sz, _sz]
+        L.orc_timestral_encode_categorical.restype = None
         L.orc_quantile_linear.argtypes = [_vp, _sz, _f]
         L.orc_quantile_linear.restype = _f
         L.orc_bolt_forecast_horizon.argtypes = [_sz, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _sz, _f,
@@ -484,6 +486,17 @@ class Oracle:
                                                  None if known is None else ptr(known), n_known, max_context,
                                                  per_shot, cap_k, extreme, int(symmetric), int(clip_nonnegative))
         return rc, out
+
+    def timestral_encode_categorical(self, codes, inputs, observed, max_context):
+        """codes (b, c, len) f64, inputs / observed (b, v, t) -> (b, c, len) f32."""
+        codes = np.ascontiguousarray(codes, np.float64)
+        inputs = np.ascontiguousarray(inputs, np.float32)
+        observed = np.ascontiguousarray(observed, np.uint8)
+        b, c, n = codes.shape
+        out = np.zeros((b, c, n), np.float32)
+        self.lib.orc_timestral_encode_categorical(ptr(out), ptr(codes), b, c, n, ptr(inputs), ptr(observed),
+                                                  inputs.shape[1], inputs.shape[2], max_context)
+        return out
 
     def timestral_refine_block(self, qs, m, ctx, obs, rows, t, h):
         st = timestral_model_struct(m)

@@ -491,3 +491,47 @@ def test_validation_fuzz_returns_codes_and_never_launches():
     assert r.returncode == 0, r.stderr[-3000:]
     seen = eval(r.stdout.strip().splitlines()[-1])
     assert {1, 2, 3} <= set(seen), seen  # unavailable (passed validation), unsupported, invalid all reached
+
+
+def test_categorical_encoding_matches_the_oracle(ta, orc):
+    """tsfm_timestral_encode_categorical (host) against the oracle's restatement, bit for bit: one
+    and two target variates, past and known code lengths, windows, NaN / infinite / unseen codes,
+    and the rows written at row0 of a wider per-series block (the numeric rows untouched)."""
+    rng = np.random.default_rng(5)
+    for trial in range(30):
+        b, c, t = int(rng.integers(1, 4)), int(rng.integers(1, 4)), int(rng.integers(1, 90))
+        h = int(rng.integers(0, 40)) if trial % 2 else 0
+        v = 1 if trial % 3 else 2
+        x = (rng.standard_normal((b, v, t)) * 5).astype(np.float32)
+        ob = (rng.random((b, v, t)) < 0.7).astype(np.uint8)
+        codes = rng.integers(0, 7, (b, c, t + h)).astype(np.float64) * 1.5
+        codes[rng.random(codes.shape) < 0.2] = np.nan
+        codes[rng.random(codes.shape) < 0.03] = -np.inf
+        window = int(rng.integers(1, 120))
+        want = orc.timestral_encode_categorical(codes, x, ob, window)
+        got = ta.timestral_encode_categorical(codes, x, ob, window)
+        assert np.array_equal(got, want, equal_nan=True), trial
+        wide = np.full((b, c + 3, t + h), 7.0, np.float32)
+        ta.timestral_encode_categorical(codes, x, ob, window, out=wide, row0=2)
+        assert np.array_equal(wide[:, 2:2 + c], want, equal_nan=True)
+        assert (wide[:, :2] == 7).all() and (wide[:, 2 + c:] == 7).all()
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(max_context=0), "max_context"),
+    (dict(row0=2), "outside"),             # rows 2..3 of 2
+    (dict(len=3), "sizes"),                # shorter than t
+    (dict(inputs=None), "inputs and observed"),
+    (dict(codes=None), "out and codes"),
+])
+def test_categorical_encoding_errors(ta, over, msg):
+    x = np.zeros((1, 1, 5), np.float32)
+    ob = np.ones((1, 1, 5), np.uint8)
+    codes = np.zeros((1, 2, 5))
+    out = np.zeros((1, 2, 5), np.float32)
+    kw = dict(out=out.ctypes.data, out_rows=2, row0=0, codes=codes.ctypes.data, batch=1, n_cat=2, len=5,
+              inputs=x.ctypes.data, observed=ob.ctypes.data, variates=1, t=5, max_context=16)
+    kw.update(over)
+    a = ta.CategoricalArgs(**kw)
+    assert ta.load().tsfm_timestral_encode_categorical(ta.ctypes.byref(a)) == ta.E_INVALID
+    assert msg in ta.last_error()

@@ -262,6 +262,45 @@ def test_timestral_forecast_many_rows(ta, orc, orc16, gpu_ready, v, n_past, n_kn
     print(f"rows {v + n_past + n_known}: err {err:.3g} bar {bar:.3g}", flush=True)
 
 
+@pytest.mark.parametrize("v,max_context", [(1, 0), (1, 96), (2, 0)])
+def test_timestral_forecast_with_categorical_covariates(ta, orc, orc16, gpu_ready, v, max_context):
+    """Categorical past and known codes (Covariates.cat_past / .cat_known, forecaster.zig:86-103):
+    encoded on the host by the library (target encoding with one variate, raw codes with two),
+    appended after the numeric rows, forecast on the device; against both oracle builds' forecasts
+    of the oracle-encoded rows at the reference-derived bar."""
+    import torch
+
+    b, horizon, per_shot = 2, 40, 2
+    m, x, obs, past, known = _cov_case(80 + v, b, v, horizon=horizon)
+    t = x.shape[1]
+    rng = np.random.default_rng(81)
+    cat_past = rng.integers(0, 4, (b, 2, t)).astype(np.float64)
+    cat_past[:, 0, 20:30] = np.nan
+    cat_known = (np.arange(t + horizon) // 7 % 3).astype(np.float64)[None, None].repeat(b, 0)
+    cat_known[:, :, t + 5] = 9.0  # a code the context never had
+    out = torch.full((b, v, horizon, m["q"]), -7.0, device="cuda")
+    rc = ta.timestral_forecast(out, torch.from_numpy(x).cuda(), torch.from_numpy(obs.astype(np.uint8)).cuda(),
+                               _device_model(m), b, v, t, horizon, max_context=max_context, per_shot=per_shot,
+                               past=torch.from_numpy(past).cuda(), known=torch.from_numpy(known).cuda(),
+                               cat_past=cat_past, cat_known=cat_known)
+    assert rc == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    window = max_context or m["context_length"]
+    x3, o3 = x.reshape(b, v, t), obs.reshape(b, v, t)
+    enc_p = orc.timestral_encode_categorical(cat_past, x3, o3, window)
+    enc_k = orc.timestral_encode_categorical(cat_known, x3, o3, window)
+    rows_p, rows_k = np.concatenate([past, enc_p], 1), np.concatenate([known, enc_k], 1)
+    kw = dict(max_context=max_context, per_shot=per_shot)
+    rc8, w8 = orc.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, rows_p, rows_k, **kw)
+    rc16, w16 = orc16.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, rows_p, rows_k, **kw)
+    assert rc8 == 0 and rc16 == 0
+    err, bar = _ref.assert_within_reference_bar(got, w8, w16)
+    print(f"categorical v={v} max_context={max_context}: err {err:.3g} bar {bar:.3g}", flush=True)
+    _, numeric_only = orc16.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, known, **kw)
+    assert _ref.scaled_err(got, numeric_only) > 10 * bar  # the categorical rows do move the forecast
+
+
 @pytest.mark.parametrize("max_context", [0, 176])
 def test_timestral_forecast_with_covariates_bf16(ta, orc16, gpu_ready, max_context):
     """TSFM_TIMESTRAL_BF16_ATTN with covariates: the per-row time-attention launches over the bf16

@@ -1309,3 +1309,114 @@ def test_timestral_forecast_covariates_mirror_and_causality(orc):
     _, f0 = orc.timestral_forecast_cov(3, m, x, obs, b, v, t0, horizon, **kw)
     _, f1 = orc.timestral_forecast(3, m, x, obs, b, v, t0, horizon, **kw)
     assert np.array_equal(f0, f1) and not np.allclose(f0, f, rtol=1e-3)
+
+
+# ---- categorical covariates (forecaster.zig:201-301) ---------------------------------------------
+
+
+def _cat_inputs(t, obs=None, values=None):
+    x = np.zeros((1, 1, t), np.float32) if values is None else np.asarray(values, np.float32).reshape(1, 1, t)
+    ob = np.ones((1, 1, t), np.uint8) if obs is None else np.asarray(obs, np.uint8).reshape(1, 1, t)
+    return x, ob
+
+
+def test_categorical_encoding_hand_case(orc):
+    """Smoothed mean-target encoding worked by hand: target 1..6, codes (0, 1, 0, 1, NaN, 0): mean
+    3.5; category 0 holds targets 1, 3, 6 -> (3.5 + 10) / 4; category 1 holds 2, 4 -> (3.5 + 6) / 3;
+    the missing category holds 5 -> (3.5 + 5) / 2. Future codes: 1, NaN, an unseen 7 and +inf (both
+    unseen: the mean)."""
+    x, ob = _cat_inputs(6, values=[1, 2, 3, 4, 5, 6])
+    codes = np.array([[[0, 1, 0, 1, np.nan, 0, 1, np.nan, 7, np.inf]]])
+    got = orc.timestral_encode_categorical(codes, x, ob, 512)[0, 0]
+    c0, c1, cm = np.float32(13.5 / 4), np.float32(9.5 / 3), np.float32(8.5 / 2)
+    want = np.array([c0, c1, c0, c1, cm, c0, c1, cm, 3.5, 3.5], np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_categorical_encoding_window_and_padding(orc):
+    """The encoding target is forward-filled from the first observation and kept only over the
+    last max_context steps: steps before it (or outside the window) carry no target, a missing code
+    there stays NaN (padding), and any other code there still gets its category's value."""
+    t = 8
+    x, ob = _cat_inputs(t, obs=[0, 0, 1, 0, 1, 1, 0, 1], values=[0, 0, 2, 9, 4, 6, 9, 8])
+    codes = np.array([[[np.nan, 5, 5, 5, np.nan, 3, 3, 5]]])
+    # Target over the whole context: (NaN, NaN, 2, 2, 4, 6, 6, 8); mean 28 / 6.
+    got = orc.timestral_encode_categorical(codes, x, ob, 100)[0, 0]
+    mean = 28.0 / 6
+    c5 = np.float32((mean + 2 + 2 + 8) / 4)
+    c3 = np.float32((mean + 6 + 6) / 3)
+    cm = np.float32((mean + 4) / 2)
+    assert np.isnan(got[0]) and np.array_equal(got[1:], [c5, c5, c5, cm, c3, c3, c5])
+    # Window of 4 steps: target (NaN x4, 4, 6, 6, 8); mean 6; step 3's code 5 keeps a value, step 0's
+    # NaN is padding.
+    got = orc.timestral_encode_categorical(codes, x, ob, 4)[0, 0]
+    c5 = np.float32((6 + 8) / 2)
+    c3 = np.float32((6 + 6 + 6) / 3)
+    cm = np.float32((6 + 4) / 2)
+    assert np.isnan(got[0]) and np.array_equal(got[1:], [c5, c5, c5, cm, c3, c3, c5])
+
+
+def test_categorical_encoding_invariants(orc):
+    """A constant target encodes every code to that constant (mean c, (c + n c) / (1 + n) = c); with
+    more than one target variate the codes pass through as float32; a series with no observation
+    encodes to 0 (mean 0, no counts) except its missing codes, which are padding."""
+    rng = np.random.default_rng(3)
+    t, n = 40, 55
+    codes = rng.integers(0, 5, (2, 3, n)).astype(np.float64)
+    codes[rng.random(codes.shape) < 0.2] = np.nan
+    x = np.full((2, 1, t), 2.5, np.float32)
+    ob = (rng.random((2, 1, t)) < 0.7).astype(np.uint8)
+    ob[:, :, 0] = 1
+    assert np.array_equal(orc.timestral_encode_categorical(codes, x, ob, 512), np.full((2, 3, n), 2.5, np.float32))
+    x2 = rng.standard_normal((2, 2, t)).astype(np.float32)
+    got = orc.timestral_encode_categorical(codes, x2, np.ones((2, 2, t), np.uint8), 512)
+    assert np.array_equal(got, codes.astype(np.float32), equal_nan=True)
+    got = orc.timestral_encode_categorical(codes, x, np.zeros((2, 1, t), np.uint8), 512)
+    past = codes[:, :, :t]
+    assert np.array_equal(np.isnan(got[:, :, :t]), np.isnan(past))
+    assert (got[:, :, :t][~np.isnan(past)] == 0).all() and (got[:, :, t:] == 0).all()
+
+
+def test_categorical_encoding_matches_a_dictionary_count(orc):
+    """Random codes (NaN, infinities, unseen future codes), gaps and windows against a count by
+    dictionary in float64, rounded once."""
+    rng = np.random.default_rng(11)
+    for trial in range(20):
+        t, h = int(rng.integers(1, 60)), int(rng.integers(0, 30))
+        b, c = 2, 2
+        x = (rng.standard_normal((b, 1, t)) * 3).astype(np.float32)
+        ob = (rng.random((b, 1, t)) < 0.6).astype(np.uint8)
+        codes = rng.integers(-2, 6, (b, c, t + h)).astype(np.float64)
+        codes[rng.random(codes.shape) < 0.15] = np.nan
+        codes[rng.random(codes.shape) < 0.05] = np.inf
+        window = int(rng.integers(1, 80))
+        got = orc.timestral_encode_categorical(codes, x, ob, window)
+        for s in range(b):
+            tg = np.full(t, np.nan)
+            last, started = 0.0, False
+            for i in range(t):
+                if ob[s, 0, i]:
+                    started, last = True, float(x[s, 0, i])
+                if started and (t <= window or i >= t - window):
+                    tg[i] = last
+            fin = np.isfinite(tg)
+            mean = tg[fin].sum() / fin.sum() if fin.any() else 0.0
+            for j in range(c):
+                row = codes[s, j]
+                seen = {float(v) for v in row[:t] if np.isfinite(v)}
+                key = lambda v: float(v) if (np.isfinite(v) and float(v) in seen) else "missing"
+                sums, counts = {}, {}
+                for i in range(t):
+                    if fin[i]:
+                        k = key(row[i])
+                        sums[k] = sums.get(k, 0.0) + tg[i]
+                        counts[k] = counts.get(k, 0) + 1
+                val = lambda k: (mean + sums.get(k, 0.0)) / (1.0 + counts.get(k, 0))
+                want = np.empty(t + h, np.float32)
+                for i in range(t):
+                    want[i] = np.nan if (np.isnan(tg[i]) and np.isnan(row[i])) else val(key(row[i]))
+                for i in range(t, t + h):
+                    v = row[i]
+                    want[i] = val("missing") if np.isnan(v) else (val(float(v)) if (np.isfinite(v) and float(v) in seen)
+                                                                    else mean)
+                np.testing.assert_allclose(got[s, j], want, rtol=2e-7, atol=0, equal_nan=True, err_msg=str(trial))

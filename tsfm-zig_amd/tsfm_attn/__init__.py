@@ -501,6 +501,8 @@ def load(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.tsfm_chronos2_forecast.restype = ctypes.c_int
     lib.tsfm_timestral_forecast.argtypes = [ctypes.POINTER(TimestralForecastArgs)]
     lib.tsfm_timestral_forecast.restype = ctypes.c_int
+    lib.tsfm_timestral_encode_categorical.argtypes = [ctypes.POINTER(CategoricalArgs)]
+    lib.tsfm_timestral_encode_categorical.restype = ctypes.c_int
     lib.tsfm_weight_register.argtypes = [vp, ctypes.c_size_t]
     lib.tsfm_weight_register.restype = vp
     lib.tsfm_weight_release.argtypes = [vp]
@@ -1184,11 +1186,72 @@ def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, vari
     return a
 
 
+class CategoricalArgs(ctypes.Structure):
+    """``tsfm_categorical_args`` (include/tsfm_attn.h)."""
+    _fields_ = [
+        ("out", ctypes.c_void_p),
+        ("out_rows", ctypes.c_int32),
+        ("row0", ctypes.c_int32),
+        ("codes", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("n_cat", ctypes.c_int32),
+        ("len", ctypes.c_int64),
+        ("inputs", ctypes.c_void_p),
+        ("observed", ctypes.c_void_p),
+        ("variates", ctypes.c_int32),
+        ("t", ctypes.c_int64),
+        ("max_context", ctypes.c_int64),
+    ]
+
+
+def timestral_encode_categorical(codes, inputs, observed, max_context: int, out=None, row0: int = 0) -> np.ndarray:
+    """Categorical covariates as numeric rows (forecaster.zig:86-103, 201-301), on the host:
+    codes (batch, n_cat, len) f64 (NaN = missing, len = t for past codes, t + horizon for known
+    ones), inputs / observed (batch, variates, t). Returns out (batch, out_rows, len) f32 with the
+    encoded rows at row0 .. row0 + n_cat - 1 (a new (batch, n_cat, len) array when out is None).
+    Raises ValueError with the library's message on an invalid request."""
+    codes = np.ascontiguousarray(codes, np.float64)
+    inputs = np.ascontiguousarray(inputs, np.float32)
+    observed = np.ascontiguousarray(observed, np.uint8)
+    b, c, n = codes.shape
+    if out is None:
+        out = np.zeros((b, c, n), np.float32)
+    if out.dtype != np.float32 or not out.flags.c_contiguous or out.ndim != 3 or out.shape[0] != b or out.shape[2] != n:
+        raise ValueError("out must be a C-contiguous (batch, rows, len) float32 array")
+    a = CategoricalArgs(out=out.ctypes.data, out_rows=out.shape[1], row0=row0, codes=codes.ctypes.data, batch=b,
+                        n_cat=c, len=n, inputs=inputs.ctypes.data, observed=observed.ctypes.data,
+                        variates=inputs.shape[1], t=inputs.shape[2], max_context=max_context)
+    rc = int(load().tsfm_timestral_encode_categorical(ctypes.byref(a)))
+    if rc != OK:
+        raise ValueError(last_error())
+    return out
+
+
 def timestral_forecast(out, inputs, observed, model: dict, batch: int, variates: int, length: int, horizon: int,
-                       **kw) -> int:
+                       cat_past=None, cat_known=None, **kw) -> int:
     """Timestral forecaster.forecast (src/timestral/forecaster.zig:57-180) on device tensors: inputs
     (batch, variates, length) f32, observed (same) uint8, out (batch, variates, horizon, q);
-    optional numeric covariates past= / known= (see timestral_forecast_args). Returns the ABI code."""
+    optional numeric covariates past= / known= (see timestral_forecast_args) and categorical codes
+    cat_past= (batch, n, length) / cat_known= (batch, n, length + horizon) as float64 host arrays,
+    encoded on the host (timestral_encode_categorical) and appended after the numeric rows of each
+    series, as the reference does. Returns the ABI code."""
+    if cat_past is not None or cat_known is not None:
+        import torch
+
+        x = inputs.detach().cpu().numpy().reshape(batch, variates, length)
+        ob = observed.detach().cpu().numpy().reshape(batch, variates, length)
+        window = int(kw.get("max_context", 0) or model["context_length"])
+        for key, codes, n in (("past", cat_past, length), ("known", cat_known, length + horizon)):
+            if codes is None:
+                continue
+            codes = np.asarray(codes, np.float64)
+            numeric = kw.get(key)
+            n_num = 0 if numeric is None else int(numeric.shape[1])
+            rows = np.zeros((batch, n_num + codes.shape[1], n), np.float32)
+            if numeric is not None:
+                rows[:, :n_num] = numeric.detach().cpu().numpy()
+            timestral_encode_categorical(codes, x, ob, window, out=rows, row0=n_num)
+            kw[key] = torch.from_numpy(rows).to(out.device)
     args = timestral_forecast_args(out, inputs, observed, model, batch, variates, length, horizon, **kw)
     return int(load().tsfm_timestral_forecast(ctypes.byref(args)))
 
