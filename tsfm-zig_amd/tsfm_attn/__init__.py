@@ -63,6 +63,7 @@ EXPORTS = (
     "tsfm_qkv_project",
     "tsfm_qkv_project_noalloc",
     "tsfm_timestral_forecast",
+    "tsfm_timestral_encode_categorical",
     "tsfm_chronos2_encode",
     "tsfm_chronos2_forward",
     "tsfm_bolt_forward",
