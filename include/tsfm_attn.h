@@ -77,6 +77,13 @@ enum { TSFM_DTYPE_F32 = 0, TSFM_DTYPE_BF16 = 1, TSFM_DTYPE_F16 = 2 };
 /* flags */
 #define TSFM_ATTN_DEVICE_PTRS 1u /* every pointer is device memory; the call is asynchronous on `stream` */
 #define TSFM_TIMESTRAL_BF16_ATTN 2u /* tsfm_timestral_forecast: time attention in bf16 (see there) */
+/* The forecast entry points (tsfm_bolt_forecast, tsfm_bolt_forecast_horizon, tsfm_chronos2_forecast,
+ * tsfm_timestral_forecast), together with TSFM_ATTN_DEVICE_PTRS: the per-call arrays (inputs,
+ * observed, covariates, out) are host memory, the weights and every other model pointer device
+ * memory (a host caller makes them once with tsfm_weight_register). The call copies the arrays in,
+ * runs on the calling thread's own stream (the `stream` fields are not read), copies out back and
+ * returns when it is written. */
+#define TSFM_FORECAST_HOST_IO 4u
 
 /* One batched attention call: o = softmax(mask(scale * q k^T + bias)) v for every (b, h).
  * Replaces: selfAttendRuntime per item (src/core/attn.zig:99-117) inside the forRange calls listed
@@ -328,8 +335,8 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args *args);
  * and start = t_in - len after truncating to context_length, :27-36). patch = input_embed.in / 3;
  * q = output_embed.out / patch; model.n_ctx must be ceil(len / patch) and model.n_out
  * ceil(horizon / patch). model.feats, fut_feats, ctx_valid, raw and enc.keys_all_valid are not read
- * (the additive key mask is used). Device pointers only (TSFM_ATTN_DEVICE_PTRS in model.enc.flags);
- * host callers keep their per-series loops around tsfm_chronos2_forward. */
+ * (the additive key mask is used). Device weights (TSFM_ATTN_DEVICE_PTRS in model.enc.flags); inputs
+ * and out are device memory too, or host memory with TSFM_FORECAST_HOST_IO (synchronous). */
 typedef struct tsfm_chronos2_forecast_args {
     tsfm_chronos2_forward_args model;
     const float *inputs; int64_t stride, start;
@@ -395,8 +402,8 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args *args);
  * ctx[s * stride + offset ..][0..len]; out is (batch, q * P) = (batch, output_embed.out).
  * model.n_patch must be ceil(len / patch); model.feats, model.patch_valid, model.raw and
  * model.keys_all_valid are not read (the additive key mask is used: the same weights as FULL when
- * every patch is observed). Device pointers only (TSFM_ATTN_DEVICE_PTRS in model.flags); host callers keep their
- * per-series loops around tsfm_bolt_forward. */
+ * every patch is observed). Device weights (TSFM_ATTN_DEVICE_PTRS in model.flags); ctx and out are
+ * device memory too, or host memory with TSFM_FORECAST_HOST_IO in model.flags (synchronous). */
 typedef struct tsfm_bolt_forecast_args {
     tsfm_bolt_forward_args model;
     const float *ctx; int64_t stride, offset;
@@ -416,7 +423,8 @@ int tsfm_bolt_forecast(const tsfm_bolt_forecast_args *args);
  * quantiles at quantile_levels (torch.quantile's linear interpolation, quantileLinear :81-92).
  * model: the weights and dims (batch = series); model.n_patch, feats, patch_valid, raw and
  * keys_all_valid are not read. inputs (batch, t_in) f32, NaN = missing; out (batch, horizon, q).
- * Device pointers only; asynchronous on model.stream. */
+ * Device weights; inputs and out device memory (asynchronous on model.stream) or, with
+ * TSFM_FORECAST_HOST_IO in model.flags, host memory (synchronous). */
 typedef struct tsfm_bolt_horizon_args {
     tsfm_bolt_forward_args model;
     const float *inputs;
@@ -435,7 +443,8 @@ int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args *args);
 /* ---------------------------------------------------------------------------------------------
  * Timestral forecast: forecaster.forecast (src/timestral/forecaster.zig:57-180) of a batch of
  * series of target variates, optionally with numeric past-only and known-future covariate rows
- * (Covariates.past / .known, :36-46), f32, device memory only, asynchronous on `stream`.
+ * (Covariates.past / .known, :36-46), f32: device weights, and inputs, observed, covariates and
+ * out in device memory (asynchronous on `stream`) or, with TSFM_FORECAST_HOST_IO, host memory.
  * Categorical covariates (Covariates.cat_past / .cat_known) are target-encoded into numeric rows
  * by the caller first (tsfm_timestral_encode_categorical below) and passed as past / known rows.
  * The whole forecast runs on the device: forecastRaw's forward-fill and left padding (:303-394),
@@ -504,7 +513,8 @@ typedef struct tsfm_timestral_forecast_args {
     float extreme_value_threshold;  /* Options.extreme_value_threshold (1e30) */
     int32_t symmetric_averaging, clip_nonnegative;  /* Options (both on in the reference) */
     int32_t kv_cache;               /* non-zero: decode over cached K/V (see above) */
-    uint32_t flags;                 /* TSFM_ATTN_DEVICE_PTRS, optionally | TSFM_TIMESTRAL_BF16_ATTN */
+    uint32_t flags;                 /* TSFM_ATTN_DEVICE_PTRS, optionally | TSFM_TIMESTRAL_BF16_ATTN
+                                       | TSFM_FORECAST_HOST_IO */
     float *out;                     /* (batch, variates, horizon, n_quantiles) */
     void *stream;
     /* Numeric covariates (Covariates.past / .known, src/timestral/forecaster.zig:36-46), NaN =

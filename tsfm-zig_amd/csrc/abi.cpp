@@ -250,6 +250,45 @@ hipError_t scratch_acquire(hipStream_t stream, int slot, size_t bytes, char** ou
     return hipSuccess;
 }
 
+
+int run_host_io(std::initializer_list<HostArray> ins, std::initializer_list<HostArray> outs,
+                const std::function<int(hipStream_t)>& body) {
+    int rc = ensure_ready();
+    if (rc != TSFM_OK) return rc;
+    ThreadCtx* ctx = thread_ctx();
+    if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
+    const hipStream_t s = ctx->stream;
+    Plan plan;
+    std::vector<size_t> at;
+    for (const HostArray& a : ins) at.push_back(plan.take(a.bytes));
+    for (const HostArray& a : outs) at.push_back(plan.take(a.bytes));
+    char* buf = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&buf), plan.off > 0 ? plan.off : 256, s);
+    if (e != hipSuccess) return hip_fail(e, "host I/O staging allocation");
+    size_t i = 0;
+    for (const HostArray& a : ins) {
+        *a.dev = a.host != nullptr ? buf + at[i] : nullptr;
+        if (e == hipSuccess && a.host != nullptr && a.bytes > 0)
+            e = hipMemcpyAsync(buf + at[i], a.host, a.bytes, hipMemcpyHostToDevice, s);
+        i++;
+    }
+    for (const HostArray& a : outs) *a.dev = buf + at[i++];
+    if (e == hipSuccess) rc = body(s);
+    i = ins.size();
+    for (const HostArray& a : outs) {
+        if (e == hipSuccess && rc == TSFM_OK && a.bytes > 0)
+            e = hipMemcpyAsync(const_cast<void*>(a.host), buf + at[i], a.bytes, hipMemcpyDeviceToHost, s);
+        i++;
+    }
+    const hipError_t f = hipFreeAsync(buf, s);
+    const hipError_t y = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "host I/O copy");
+    if (rc != TSFM_OK) return rc;
+    if (f != hipSuccess) return hip_fail(f, "host I/O staging release");
+    if (y != hipSuccess) return hip_fail(y, "stream synchronise");
+    return TSFM_OK;
+}
+
 }  // namespace abi
 }  // namespace tsfm
 
@@ -1487,9 +1526,24 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
 int tsfm_bolt_forecast(const tsfm_bolt_forecast_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (!(a->model.flags & TSFM_ATTN_DEVICE_PTRS))
-        return fail(TSFM_E_UNSUPPORTED, "the forecast runs on device memory only; host callers use tsfm_bolt_forward");
+        return fail(TSFM_E_UNSUPPORTED, "the forecast takes device weights (TSFM_ATTN_DEVICE_PTRS; TSFM_FORECAST_HOST_IO "
+                                        "for host inputs and outputs); host callers may use tsfm_bolt_forward");
     if (a->len <= 0 || a->patch <= 0 || a->ctx == nullptr || a->out == nullptr || a->stride < 0 || a->offset < 0)
         return fail(TSFM_E_INVALID, "bad context description");
+    if (a->model.flags & TSFM_FORECAST_HOST_IO) {
+        const int64_t nb = a->model.batch, per = a->model.output_embed.out;
+        if (nb < 0 || per < 0) return fail(TSFM_E_INVALID, "negative size");
+        if (nb == 0) return TSFM_OK;
+        tsfm_bolt_forecast_args d = *a;
+        d.model.flags &= ~TSFM_FORECAST_HOST_IO;
+        const size_t ctx_n = (size_t)((nb - 1) * a->stride + a->offset + a->len) * 4;
+        return tsfm::abi::run_host_io({{a->ctx, ctx_n, reinterpret_cast<const void**>(&d.ctx)}},
+                                      {{a->out, (size_t)(nb * per) * 4, const_cast<const void**>(reinterpret_cast<void**>(&d.out))}},
+                                      [&](hipStream_t s) {
+                                          d.model.stream = s;
+                                          return tsfm_bolt_forecast(&d);
+                                      });
+    }
     const int32_t pad = (a->patch - a->len % a->patch) % a->patch, n_patch = (a->len + pad) / a->patch;
     if (a->model.n_patch != n_patch) return fail(TSFM_E_INVALID, "model.n_patch must be ceil(len / patch)");
     if (a->model.input_embed.in != 2 * a->patch) return fail(TSFM_E_INVALID, "input_embed.in must be 2 * patch");
@@ -1536,8 +1590,8 @@ int tsfm_bolt_forecast(const tsfm_bolt_forecast_args* a) {
 int tsfm_chronos2_forecast(const tsfm_chronos2_forecast_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (!(a->model.enc.flags & TSFM_ATTN_DEVICE_PTRS))
-        return fail(TSFM_E_UNSUPPORTED,
-                    "the forecast runs on device memory only; host callers use tsfm_chronos2_forward");
+        return fail(TSFM_E_UNSUPPORTED, "the forecast takes device weights (TSFM_ATTN_DEVICE_PTRS; TSFM_FORECAST_HOST_IO "
+                                        "for host inputs and outputs); host callers may use tsfm_chronos2_forward");
     const int32_t ps = a->model.input_embed.in / 3;
     if (ps <= 0 || a->model.input_embed.in != 3 * ps) return fail(TSFM_E_INVALID, "input_embed.in must be 3 * patch");
     if (a->len <= 0 || a->horizon <= 0 || a->inputs == nullptr || a->out == nullptr || a->stride < 0 || a->start < 0 ||
@@ -1551,6 +1605,18 @@ int tsfm_chronos2_forecast(const tsfm_chronos2_forecast_args* a) {
     const int64_t nb = a->model.enc.batch;
     if (nb < 0) return fail(TSFM_E_INVALID, "negative size");
     if (nb == 0) return TSFM_OK;
+    if (a->model.enc.flags & TSFM_FORECAST_HOST_IO) {
+        tsfm_chronos2_forecast_args d = *a;
+        d.model.enc.flags &= ~TSFM_FORECAST_HOST_IO;
+        const size_t in_n = (size_t)((nb - 1) * a->stride + a->start + a->len) * 4;
+        const size_t out_n = (size_t)(nb * a->horizon * (per / ps)) * 4;
+        return tsfm::abi::run_host_io({{a->inputs, in_n, reinterpret_cast<const void**>(&d.inputs)}},
+                                      {{a->out, out_n, const_cast<const void**>(reinterpret_cast<void**>(&d.out))}},
+                                      [&](hipStream_t s) {
+                                          d.model.enc.stream = s;
+                                          return tsfm_chronos2_forecast(&d);
+                                      });
+    }
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(a->model.enc.stream);

@@ -7,6 +7,8 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
+#include <initializer_list>
 
 namespace tsfm {
 namespace abi {
@@ -36,6 +38,19 @@ enum ScratchSlot { kSlotEncode, kSlotChronos2Forward, kSlotChronos2Forecast, kSl
 // A buffer of at least `bytes` for work queued on `stream` by the calling thread, kept between
 // calls; *owned: a stream-ordered allocation instead, to be released with hipFreeAsync.
 hipError_t scratch_acquire(hipStream_t stream, int slot, size_t bytes, char** out, bool* owned);
+
+// TSFM_FORECAST_HOST_IO: a host array of `bytes` bytes and the device-pointer field that takes its
+// copy (host may be NULL with bytes 0: the field is set to NULL).
+struct HostArray {
+    const void* host;
+    size_t bytes;
+    const void** dev;
+};
+// Uploads every `in` on the calling thread's stream, points its field at the copy, gives every `out`
+// a device buffer, runs body(stream), downloads the outs and synchronises. Returns body's code, or
+// a copy / allocation error.
+int run_host_io(std::initializer_list<HostArray> ins, std::initializer_list<HostArray> outs,
+                const std::function<int(hipStream_t)>& body);
 
 }  // namespace abi
 }  // namespace tsfm

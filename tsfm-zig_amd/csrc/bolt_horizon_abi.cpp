@@ -22,7 +22,8 @@ using tsfm::abi::Plan;
 extern "C" int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     if (!(a->model.flags & TSFM_ATTN_DEVICE_PTRS))
-        return fail(TSFM_E_UNSUPPORTED, "the forecast runs on device memory only (TSFM_ATTN_DEVICE_PTRS)");
+        return fail(TSFM_E_UNSUPPORTED, "the forecast takes device weights (TSFM_ATTN_DEVICE_PTRS; TSFM_FORECAST_HOST_IO "
+                                        "for host inputs and outputs)");
     const int64_t b = a->model.batch;
     const int q = a->n_quantiles, P = a->prediction_length, ps = a->patch;
     if (b < 0 || a->t_in <= 0 || a->horizon <= 0 || ps <= 0 || P <= 0 || a->context_length <= 0)
@@ -33,6 +34,17 @@ extern "C" int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args* a) {
     if (b == 0) return TSFM_OK;
     if (b * q > 0x7fffffff / std::max(a->context_length, q * P))
         return fail(TSFM_E_UNSUPPORTED, "batch * quantiles * context too large");
+    if (a->model.flags & TSFM_FORECAST_HOST_IO) {
+        tsfm_bolt_horizon_args d = *a;
+        d.model.flags &= ~TSFM_FORECAST_HOST_IO;
+        return tsfm::abi::run_host_io(
+            {{a->inputs, (size_t)(b * a->t_in) * 4, reinterpret_cast<const void**>(&d.inputs)}},
+            {{a->out, (size_t)(b * a->horizon * q) * 4, const_cast<const void**>(reinterpret_cast<void**>(&d.out))}},
+            [&](hipStream_t s) {
+                d.model.stream = s;
+                return tsfm_bolt_forecast_horizon(&d);
+            });
+    }
     tsfm::BoltLevels lv{};
     for (int i = 0; i < q; i++) {
         lv.v[i] = a->quantile_levels[i];

@@ -83,9 +83,11 @@ int check_resblock(const tsfm_resblock& rb, int in, int out, bool biases, const 
 extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     if (a == nullptr) return fail(TSFM_E_INVALID, "args is NULL");
     const tsfm_timestral_model& M = a->model;
-    if (a->flags & ~(TSFM_ATTN_DEVICE_PTRS | TSFM_TIMESTRAL_BF16_ATTN)) return fail(TSFM_E_INVALID, "unknown flags");
+    if (a->flags & ~(TSFM_ATTN_DEVICE_PTRS | TSFM_TIMESTRAL_BF16_ATTN | TSFM_FORECAST_HOST_IO))
+        return fail(TSFM_E_INVALID, "unknown flags");
     if (!(a->flags & TSFM_ATTN_DEVICE_PTRS))
-        return fail(TSFM_E_UNSUPPORTED, "the Timestral forecast runs on device memory only (TSFM_ATTN_DEVICE_PTRS)");
+        return fail(TSFM_E_UNSUPPORTED, "the Timestral forecast takes device weights (TSFM_ATTN_DEVICE_PTRS; "
+                                        "TSFM_FORECAST_HOST_IO for host inputs and outputs)");
     if (a->batch < 0 || a->variates <= 0 || a->len <= 0 || a->horizon <= 0)
         return fail(TSFM_E_INVALID, "bad batch, variates, len or horizon");
     if (a->batch == 0) return TSFM_OK;
@@ -163,6 +165,21 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
         if (!routes)
             return fail(TSFM_E_UNSUPPORTED, "known covariates: the layer schedule cannot route them to the targets "
                                             "(error.KnownCovariatesUnsupported)");
+    }
+    if (a->flags & TSFM_FORECAST_HOST_IO) {
+        tsfm_timestral_forecast_args dv = *a;
+        dv.flags &= ~TSFM_FORECAST_HOST_IO;
+        const size_t rows = (size_t)a->batch * a->variates, L = (size_t)a->len, H = (size_t)a->horizon;
+        return tsfm::abi::run_host_io(
+            {{a->inputs, rows * L * 4, reinterpret_cast<const void**>(&dv.inputs)},
+             {a->observed, rows * L, reinterpret_cast<const void**>(&dv.observed)},
+             {a->past, (size_t)a->batch * a->n_past * L * 4, reinterpret_cast<const void**>(&dv.past)},
+             {a->known, (size_t)a->batch * a->n_known * (L + H) * 4, reinterpret_cast<const void**>(&dv.known)}},
+            {{a->out, rows * H * q * 4, const_cast<const void**>(reinterpret_cast<void**>(&dv.out))}},
+            [&](hipStream_t s) {
+                dv.stream = s;
+                return tsfm_timestral_forecast(&dv);
+            });
     }
     if ((rc = ensure_ready()) != TSFM_OK) return rc;
 

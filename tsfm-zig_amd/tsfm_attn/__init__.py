@@ -48,6 +48,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 
 DEVICE_PTRS = 1
+FORECAST_HOST_IO = 4  # TSFM_FORECAST_HOST_IO: the forecasts' per-call arrays in host memory
 VARIATE_MAX_ROWS = 256  # TSFM_VARIATE_MAX_ROWS: rows per series of the variate and Timestral forecast calls
 TIMESTRAL_BF16_ATTN = 2  # tsfm_timestral_forecast: time attention in bf16
 
@@ -908,15 +909,15 @@ def chronos2_forecast_args(out, inputs, length, horizon, reg, cos_t, sin_t, laye
                            arcsinh=False, scale=1.0, hd=64, stream=None) -> Chronos2ForecastArgs:
     """The argument block of chronos2_forecast, built once for repeated tsfm_chronos2_forecast calls
     (the layer array it points to lives as long as the returned object)."""
-    if not _is_device(inputs):
-        raise ValueError("chronos2_forecast runs on device tensors; host callers use chronos2_forward")
     n_ctx, n_out = (length + patch - 1) // patch, (horizon + patch - 1) // patch
     m = _chronos2_args(None, None, None, None, reg, cos_t, sin_t, layers, final_norm, input_embed, output_embed, n,
                        n_ctx, n_out, d, nh, d_ff, eps, False, scale, hd, True, stream)
+    if not _is_device(inputs):  # host inputs and out, device weights: TSFM_FORECAST_HOST_IO
+        m.enc.flags |= FORECAST_HOST_IO
     a = Chronos2ForecastArgs(model=m, inputs=_ptr(inputs), stride=length if stride is None else stride, start=start,
                              len=length, horizon=horizon, time_scale=time_scale, arcsinh=int(bool(arcsinh)),
                              out=_ptr(out))
-    a._keep = m._keep
+    a._keep = (m._keep, inputs, out)
     return a
 
 
@@ -985,15 +986,15 @@ def bolt_forecast_args(out, ctx, length, reg, dec_start, rel_table, enc_layers, 
     """The argument block of bolt_forecast, built once: a caller that forecasts repeatedly with the
     same weights and buffers passes it to tsfm_bolt_forecast each time (the layer arrays it points
     to live as long as the returned object)."""
-    if not _is_device(ctx):
-        raise ValueError("bolt_forecast runs on device tensors; host callers use bolt_forward")
     n_patch = (length + patch - 1) // patch
     m = bolt_forward_args(enc_layers, dec_layers, None, None, reg, dec_start, rel_table, enc_final_norm, dec_final_norm,
                    input_embed, output_embed, None, n, n_patch, d, nh, hd, d_ff, eps, num_buckets, max_distance, False,
                    True, stream)
+    if not _is_device(ctx):  # host context and out, device weights: TSFM_FORECAST_HOST_IO
+        m.flags |= FORECAST_HOST_IO
     a = BoltForecastArgs(model=m, ctx=_ptr(ctx), stride=length if stride is None else stride, offset=offset,
                          len=length, patch=patch, norm_eps=norm_eps, out=_ptr(out))
-    a._keep = m._keep
+    a._keep = (m._keep, ctx, out)
     return a
 
 
@@ -1019,13 +1020,13 @@ def bolt_forecast_horizon_args(out, inputs, horizon, reg, dec_start, rel_table, 
     points to alive)."""
     import numpy as np
 
-    if not _is_device(inputs):
-        raise ValueError("bolt_forecast_horizon runs on device tensors")
     b, t_in = int(inputs.shape[0]), int(inputs.shape[1])
     levels = np.ascontiguousarray(quantile_levels, np.float32)
     m = bolt_forward_args(enc_layers, dec_layers, None, None, reg, dec_start, rel_table, enc_final_norm, dec_final_norm,
                           input_embed, output_embed, None, b, 0, d, nh, hd, d_ff, eps, num_buckets, max_distance, False,
                           True, stream)
+    if not _is_device(inputs):  # host inputs and out, device weights: TSFM_FORECAST_HOST_IO
+        m.flags |= FORECAST_HOST_IO
     a = BoltHorizonArgs(model=m, inputs=_ptr(inputs), t_in=t_in, horizon=horizon, patch=patch,
                         prediction_length=prediction_length, context_length=context_length, n_quantiles=levels.size,
                         quantile_levels=levels.ctypes.data, norm_eps=norm_eps, out=_ptr(out))
@@ -1149,7 +1150,8 @@ def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, vari
                             max_context: int = 0, per_shot: int = 32, cap_k: float = 1e4, extreme: float = 1e30,
                             symmetric: bool = True, clip_nonnegative: bool = True, kv_cache: bool = True,
                             attn_bf16: bool = False, past=None, known=None, stream=None) -> "TimestralForecastArgs":
-    """``tsfm_timestral_forecast_args`` over device tensors. `model` holds the config and device
+    """``tsfm_timestral_forecast_args``: inputs, observed, covariates and out as device tensors, or
+    all as host numpy arrays (TSFM_FORECAST_HOST_IO: synchronous). `model` holds the config and device
     weights (keys as in the reference checkpoint's layout: patch_proj/head ResBlocks, layers with
     attns [is_time, norm, qkv (permuted), out, gate] and mlp_norm/w12/w3, forecast_query, out_norm,
     knots (host float64 array)). attn_bf16 sets TSFM_TIMESTRAL_BF16_ATTN (time attention on the bf16
@@ -1179,7 +1181,9 @@ def timestral_forecast_args(out, inputs, observed, model: dict, batch: int, vari
                               len=length, horizon=horizon, max_context=max_context, per_shot_patches=per_shot,
                               quantile_real_cap_k=cap_k, extreme_value_threshold=extreme,
                               symmetric_averaging=int(symmetric), clip_nonnegative=int(clip_nonnegative),
-                              kv_cache=int(kv_cache), flags=DEVICE_PTRS | (TIMESTRAL_BF16_ATTN if attn_bf16 else 0),
+                              kv_cache=int(kv_cache),
+                              flags=DEVICE_PTRS | (TIMESTRAL_BF16_ATTN if attn_bf16 else 0) |
+                              (0 if _is_device(inputs) else FORECAST_HOST_IO),
                               out=_ptr(out), stream=_stream_of(out, stream), past=_ptr(past), known=_ptr(known),
                               n_past=0 if past is None else int(past.shape[1]),
                               n_known=0 if known is None else int(known.shape[1]))
@@ -1239,8 +1243,10 @@ def timestral_forecast(out, inputs, observed, model: dict, batch: int, variates:
     if cat_past is not None or cat_known is not None:
         import torch
 
-        x = inputs.detach().cpu().numpy().reshape(batch, variates, length)
-        ob = observed.detach().cpu().numpy().reshape(batch, variates, length)
+        host = lambda a: a if isinstance(a, np.ndarray) else a.detach().cpu().numpy()  # noqa: E731
+        device = _is_device(inputs)
+        x = host(inputs).reshape(batch, variates, length)
+        ob = host(observed).reshape(batch, variates, length)
         window = int(kw.get("max_context", 0) or model["context_length"])
         for key, codes, n in (("past", cat_past, length), ("known", cat_known, length + horizon)):
             if codes is None:
@@ -1250,9 +1256,9 @@ def timestral_forecast(out, inputs, observed, model: dict, batch: int, variates:
             n_num = 0 if numeric is None else int(numeric.shape[1])
             rows = np.zeros((batch, n_num + codes.shape[1], n), np.float32)
             if numeric is not None:
-                rows[:, :n_num] = numeric.detach().cpu().numpy()
+                rows[:, :n_num] = host(numeric)
             timestral_encode_categorical(codes, x, ob, window, out=rows, row0=n_num)
-            kw[key] = torch.from_numpy(rows).to(out.device)
+            kw[key] = torch.from_numpy(rows).to(out.device) if device else rows
     args = timestral_forecast_args(out, inputs, observed, model, batch, variates, length, horizon, **kw)
     return int(load().tsfm_timestral_forecast(ctypes.byref(args)))
 
