@@ -454,11 +454,16 @@ int tsfm_bolt_forecast_horizon(const tsfm_bolt_horizon_args *args);
  * quantile cap (:396-418), the mirrored pass of the symmetric average (:107-137, run in the same
  * batch) and the non-negative clip (:163-178). A forecast whose output contains NaN is returned as
  * is (the reference reports error.DegenerateInput).
- * With kv_cache set and no covariates, decode blocks after the first run only their new patches
- * and decoder tokens, attending over the time-attention K/V the earlier blocks computed (the
- * reference re-encodes the whole context every block; the result is the same computation, up to
- * f32 summation order); blocks after a max_context drop re-encode in full. With covariates the
- * window depends on each block's horizon, so kv_cache is ignored and every block re-encodes.
+ * With kv_cache set and no known-future covariates, decode blocks after the first run only their
+ * new patches and decoder tokens, attending over the time-attention K/V the earlier blocks
+ * computed (the reference re-encodes the whole context every block; the result is the same
+ * computation, up to f32 summation order); blocks after a max_context drop re-encode in full.
+ * Past-only covariate rows keep that: every row's encoder tokens are then causal in time (causal
+ * per-patch statistics, causal time attention, variate attention within a token slot), and the
+ * window's blank future patches, which no context token or decoder query reads, are recomputed as
+ * context in the next block. Known-future rows attend over the whole window and take whole-window
+ * statistics, so every token changes when the window grows: with them kv_cache is ignored and
+ * every block re-encodes.
  * With TSFM_TIMESTRAL_BF16_ATTN in flags the time attention runs on the bf16 matrix cores: the q/k/v
  * projections are rounded once to bf16 (after RoPE) into a bf16 K/V cache, the attention keeps f32
  * scores, softmax and accumulation, and its output is rounded to bf16 and widened back to f32 for
@@ -518,8 +523,9 @@ typedef struct tsfm_timestral_forecast_args {
     float *out;                     /* (batch, variates, horizon, n_quantiles) */
     void *stream;
     /* Numeric covariates (Covariates.past / .known, src/timestral/forecaster.zig:36-46), NaN =
-     * missing; each pointer may be NULL when its count is 0. With covariates every decode block
-     * re-encodes the window (context + horizon) as the reference does: kv_cache is ignored. */
+     * missing; each pointer may be NULL when its count is 0. With known-future covariates every
+     * decode block re-encodes the window (context + horizon) as the reference does: kv_cache is
+     * ignored (see above); past-only covariates decode over the cache. */
     const float *past;              /* (batch, n_past, len) past-only covariates */
     const float *known;             /* (batch, n_known, len + horizon) known-future covariates */
     int32_t n_past, n_known;        /* variates + n_past + n_known <= TSFM_VARIATE_MAX_ROWS */

@@ -237,6 +237,41 @@ def test_timestral_forecast_with_covariates(ta, orc, orc16, gpu_ready, horizon, 
     assert _ref.scaled_err(got, plain) > 10 * bar  # the covariates do move the forecast
 
 
+@pytest.mark.parametrize("max_context", [0, 176])
+def test_timestral_cached_decode_with_past_covariates(ta, orc, orc16, gpu_ready, max_context):
+    """Past-only covariates keep every encoder token causal in time, so the K/V cache stays exact:
+    the cached forecast over several decode blocks equals the re-encoding one (up to f32
+    summation order) and both are within the reference-derived bar of the oracle's re-encoding
+    forecast; with a known-future row as well the cache is not used (the two calls agree
+    exactly)."""
+    import torch
+
+    b, v, horizon, per_shot = 2, 2, 100, 2
+    m, x, obs, past, known = _cov_case(70 + max_context, b, v, n_past=3, n_known=1, horizon=horizon)
+    t = x.shape[1]
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+
+    def run(kv_cache, **cov):
+        out = torch.full((b, v, horizon, m["q"]), -7.0, device="cuda")
+        rc = ta.timestral_forecast(out, dev(x), dev(obs.astype(np.uint8)), _device_model(m), b, v, t, horizon,
+                                   max_context=max_context, per_shot=per_shot, kv_cache=kv_cache,
+                                   **{k: dev(a) for k, a in cov.items()})
+        assert rc == ta.OK, ta.last_error()
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    cached, full = run(True, past=past), run(False, past=past)
+    diff = _ref.scaled_err(cached, full)
+    print(f"past covariates, max_context={max_context}: cached vs re-encoded {diff:.3g}", flush=True)
+    assert diff < 2e-5
+    kw = dict(max_context=max_context, per_shot=per_shot)
+    rc8, w8 = orc.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, None, **kw)
+    rc16, w16 = orc16.timestral_forecast_cov(THREADS, m, x, obs, b, v, t, horizon, past, None, **kw)
+    assert rc8 == 0 and rc16 == 0
+    _ref.assert_within_reference_bar(cached, w8, w16)
+    assert np.array_equal(run(True, past=past, known=known), run(False, past=past, known=known))
+
+
 @pytest.mark.parametrize("v,n_past,n_known", [(1, 8, 8), (2, 12, 10), (1, 16, 16)])
 def test_timestral_forecast_many_rows(ta, orc, orc16, gpu_ready, v, n_past, n_known):
     """17, 24 and 33 rows per series (targets and covariates): the variate layers take the

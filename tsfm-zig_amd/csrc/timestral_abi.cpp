@@ -4,8 +4,9 @@
 // (:423-563), refineBlock (:582-662) and src/timestral/model.zig predictBlock (:220-432), with
 // numeric past-only and known-future covariate rows after each series' targets. The forward and
 // the mirrored pass of the symmetric average run as one batch: the mirrored series are groups
-// batch..2 batch-1 of every launch. With covariates each block re-encodes its window (the context
-// plus the horizon's known futures or blanks), as the reference does.
+// batch..2 batch-1 of every launch. With covariates each block's encoder covers its window (the
+// context plus the horizon's known futures or blanks), as the reference's does; with known-future
+// rows every block re-encodes it.
 //
 // The reference re-encodes the whole grown context for every decode block (blockDecode calls
 // predictBlock on the full context). Without covariates every encoder layer is causal over
@@ -271,7 +272,11 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
         cp.ctx = ctx[0]; cp.mask = mask[0]; cp.kf = F(at_kf); cp.kfm = U8(at_kfm); cp.nonneg = U8(at_nonneg);
         hipError_t e2 = tsfm::launch_ts_context(cp, s);
         if (e2 != hipSuccess) return e2;
-        const bool cache = a->kv_cache != 0 && !cov;
+        // Known-future rows attend over the whole window and take whole-window statistics: every
+        // token changes when the window grows. Past-only rows are causal like the targets; their
+        // blank future patches (read by no context token or decoder query) leave the carried
+        // statistics unchanged (zero weight) and are recomputed as context in the next block.
+        const bool cache = a->kv_cache != 0 && a->n_known == 0;
         const int known_from = V + a->n_past;  // first known-future row of a series
         int t = t_first, remaining = total_patches, done = 0;
         int stats_from = 0;  // first step of the window whose statistics are not computed yet
