@@ -95,6 +95,62 @@ __device__ __forceinline__ f32x4 epi_act(int epi, f32x4 v) {
 
 // OUT: element type of the outputs, TSFM_DTYPE_* (0 f32, 1 bf16, 2 f16); the products and RoPE
 // are f32 either way and the result is rounded once, to nearest even, when it is stored.
+// The stores of a wave's finished sums (not split): sum[nb][mb] holds columns cq(nb) .. + 3 of the
+// head at output column n0w (over all outputs) for token row0 + wm * 32 + mb * 16 + (lane & 15):
+// alpha, RoPE of q and k, then bias and ReLU / SiLU / residual (f32) or the rounding (bf16, f16).
+template <int OUT, bool BIG>
+__device__ __forceinline__ void proj_store(const ProjParams& p, f32x4 (&sum)[BIG ? 4 : 2][2], int row0, int n0w, int wm,
+                                           int wq, int lane) {
+    constexpr int NB = BIG ? 4 : 2;
+    const int sel = n0w / p.width, col = n0w - sel * p.width;
+    const int c4 = 4 * (lane >> 4);
+    auto cq = [&](int nb) { return (BIG ? 16 * nb : 16 * wq + 32 * nb) + c4; };  // column in the head
+    void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
+    const bool rope = p.rope_cos != nullptr && sel < 2;
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+        const int m = row0 + wm * 32 + mb * 16 + (lane & 15);
+        if (m >= p.tokens) continue;
+        if (p.alpha != 1.f) {  // gemmNT's alpha, applied to the finished sum (src/core/nn.zig:100)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) sum[nb][mb] *= p.alpha;
+        }
+        if (rope) {
+            // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table; the
+            // pairs (i, i + 32) are blocks (nb, nb + NB / 2).
+            const int b = m / p.seq, tok = m - b * p.seq;
+            const int table = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
+#pragma unroll
+            for (int k = 0; k < NB / 2; k++) {
+                const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq(k);
+                rope4(sum[k][mb], sum[k + NB / 2][mb], ld4(p.rope_cos + at), ld4(p.rope_sin + at));
+            }
+        }
+        const int64_t at = out_offset(p, sel, m) + col;
+        if constexpr (OUT == 0) {
+            float* const out = static_cast<float*>(y) + at;
+            const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col : nullptr;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                if (col + cq(nb) >= p.width) continue;
+                f32x4 v = sum[nb][mb];
+                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq(nb));  // nn.linear's bias (linearCols, nn.zig:254)
+                if (p.epi == kEpiResidual) v = ld4(res + cq(nb)) + v;  // x + delta, one rounding
+                else v = epi_act(p.epi, v);
+                st4(out + cq(nb), v);
+            }
+        } else {
+            uint16_t* const out = static_cast<uint16_t*>(y) + at;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const f32x4 v = sum[nb][mb];
+                *reinterpret_cast<u32x2*>(out + cq(nb)) =
+                    u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
+            }
+        }
+    }
+}
+
 template <int OUT, int BK, bool BIG>
 __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(4, 4))) void qkv_proj(ProjParams p) {
     constexpr int TM = tile_m<BIG>(), TN = tile_n<BIG>(), NT = threads<BIG>();
@@ -232,50 +288,170 @@ __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(
         }
         return;
     }
-    void* const y = sel == 0 ? p.y0 : sel == 1 ? p.y1 : sel == 2 ? p.y2 : p.y3;
-    const bool rope = p.rope_cos != nullptr && sel < 2;
+    proj_store<OUT, BIG>(p, sum, row0, n0w, wm, wq, lane);
+}
+
+// ---- f32 products on the bf16 matrix cores --------------------------------------------------------
+//
+// The large products (128 x 128 tiles) can run their f32 arithmetic as bf16 products: each f32
+// operand is split into three bf16 parts, a = a0 + a1 + a2 (a0 = bf16(a), a1 = bf16(a - a0),
+// a2 = bf16(a - a0 - a1); both differences are exact in f32), so a0..a2 carry a's 24 significant
+// bits. A product a b is the sum of the nine a_i b_j; each is exact in f32 (8 x 8 significant bits),
+// and the three smallest (a1 b2, a2 b1, a2 b2: below 2^-24 of a b) are left out. The other six run
+// on v_mfma_f32_16x16x32_bf16 into the f32 accumulator, smallest first (a2 b0, a0 b2, a1 b1, a1 b0,
+// a0 b1, a0 b0). Each 16x16x32 instruction is 16 cycles against 32 for 16x16x4 f32 with an eighth
+// of the work, so the six take 2.7x fewer matrix cycles than the f32 instructions, and the bf16
+// matrix pipe runs beside the VALU (the f32 one does not). The accumulation stays blocked as in
+// qkv_proj: chunks of 32-wide units, each its own chain started at zero, the chunk sums added in
+// order.
+//
+// Staging: each step (32 reduction indices) the workgroup's 512 threads load the x and weight
+// tiles (128 rows x 32 indices each) as 16-byte loads into registers one step ahead, split them,
+// and write the three bf16 planes into the other LDS stage in the matrix instruction's operand
+// order: per 16 rows x 32 indices, lane l's 16 bytes (row l & 15, indices 8 (l >> 4) .. + 7) at 16 l.
+// 48 KB per stage, two stages: one workgroup (8 waves) per CU.
+constexpr int X3_BK = 32;  // reduction indices per step
+// Per tile shape: the bytes of one bf16 plane of one tile (rows x 32 indices x 2 bytes), the three
+// planes of a tile, a stage (weight tile, then x tile), and both stages.
+template <bool BIG> constexpr int x3_plane() { return tile_m<BIG>() * X3_BK * 2; }
+template <bool BIG> constexpr int x3_stage() { return 2 * 3 * x3_plane<BIG>(); }
+template <bool BIG> constexpr size_t x3_lds() { return 2 * (size_t)x3_stage<BIG>(); }
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) u32x4* lds_u32x4_p;
+typedef __attribute__((address_space(3))) u32x2* lds_u32x2_p;
+
+// a = hi + mid + lo as bf16 pairs (two values per word, the first in the low half).
+__device__ __forceinline__ void split3(f32x4 v, u32x2& hi, u32x2& mid, u32x2& lo) {
+#pragma clang fp contract(off)
+    auto widen = [](uint32_t w, int half) { return __uint_as_float(half ? (w & 0xffff0000u) : (w << 16)); };
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++) {
-        const int m = row0 + wm * 32 + mb * 16 + (lane & 15);
-        if (m >= p.tokens) continue;
-        if (p.alpha != 1.f) {  // gemmNT's alpha, applied to the finished sum (src/core/nn.zig:100)
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) sum[nb][mb] *= p.alpha;
-        }
-        if (rope) {
-            // Token t of series row b: row t of table (rope_row0 + b) / rope_rows_per_table; the
-            // pairs (i, i + 32) are blocks (nb, nb + NB / 2).
-            const int b = m / p.seq, tok = m - b * p.seq;
-            const int table = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
-#pragma unroll
-            for (int k = 0; k < NB / 2; k++) {
-                const int64_t at = (int64_t)table * p.rope_table_stride + (int64_t)tok * (kHeadDim / 2) + cq(k);
-                rope4(sum[k][mb], sum[k + NB / 2][mb], ld4(p.rope_cos + at), ld4(p.rope_sin + at));
-            }
-        }
-        const int64_t at = out_offset(p, sel, m) + col;
-        if constexpr (OUT == 0) {
-            float* const out = static_cast<float*>(y) + at;
-            const float* const res = p.epi == kEpiResidual ? p.resid + (int64_t)m * p.resid_tok + col : nullptr;
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) {
-                if (col + cq(nb) >= p.width) continue;
-                f32x4 v = sum[nb][mb];
-                if (p.bias != nullptr) v = v + ld4(p.bias + col + cq(nb));  // nn.linear's bias (linearCols, nn.zig:254)
-                if (p.epi == kEpiResidual) v = ld4(res + cq(nb)) + v;  // x + delta, one rounding
-                else v = epi_act(p.epi, v);
-                st4(out + cq(nb), v);
-            }
-        } else {
-            uint16_t* const out = static_cast<uint16_t*>(y) + at;
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) {
-                const f32x4 v = sum[nb][mb];
-                *reinterpret_cast<u32x2*>(out + cq(nb)) =
-                    u32x2{pack2<OUT == 1>(v[0], v[1]), pack2<OUT == 1>(v[2], v[3])};
-            }
-        }
+    for (int i = 0; i < 2; i++) {
+        const float a = v[2 * i], b = v[2 * i + 1];
+        const uint32_t h = pack2<true>(a, b);
+        const float ra = a - widen(h, 0), rb = b - widen(h, 1);
+        const uint32_t m = pack2<true>(ra, rb);
+        const float sa = ra - widen(m, 0), sb = rb - widen(m, 1);
+        hi[i] = h;
+        mid[i] = m;
+        lo[i] = pack2<true>(sa, sb);
     }
+}
+
+__device__ __forceinline__ f32x4 mfma_x3(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c, 0,
+                                                   0, 0);
+}
+
+// Tiles and waves as qkv_proj's: BIG 128 x 128 (8 waves of 32 tokens x one head, each its four
+// column blocks), SMALL 64 x 64 (4 waves of 32 tokens x column blocks wq and wq + 2). Per output
+// element the products and their order depend on d_in and the chunk alone, so both shapes give the
+// same bits for the same row.
+template <int OUT, bool BIG>
+__global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(BIG ? 2 : 3, BIG ? 2 : 3))) void
+qkv_proj_x3(ProjParams p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int T = tile_m<BIG>(), NT = threads<BIG>(), NB = BIG ? 4 : 2;
+    constexpr int PLANE = x3_plane<BIG>(), TILE = 3 * PLANE, STAGE = x3_stage<BIG>();
+    static_assert(T * 8 == 2 * NT, "each thread loads two 16-byte slots of each tile per step");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, tm, tn);
+    const int n_cols = p.width * p.n_out;
+    const int row0 = p.m_base + tm * T;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)smem;
+
+    // Loader: 16-byte slot e = tid + NT i (i < 2) of each tile: row e / 8, indices 4 (e % 8) .. + 3
+    // of the step. Rows past the end are clamped to the last row (they feed only outputs that are
+    // not stored). dst: the slot's byte offset in a plane (16-row block, then lane (row, index / 8)).
+    const float* wsrc[2];
+    const float* xsrc[2];
+    uint32_t dst[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int e = tid + NT * i, r = e >> 3, kq = 4 * (e & 7);
+        const int n = min(tn * T + r, n_cols - 1), sel = n / p.width;
+        const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
+        wsrc[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + kq;
+        xsrc[i] = p.x + (int64_t)min(row0 + r, p.tokens - 1) * p.x_tok + kq;
+        dst[i] = (uint32_t)((r >> 4) * 1024 + ((kq >> 3) * 16 + (r & 15)) * 16 + (kq & 7) * 2);
+    }
+    f32x4 pw[2], px[2];
+    auto load = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            pw[i] = ld4(wsrc[i] + t * X3_BK);
+            px[i] = ld4(xsrc[i] + t * X3_BK);
+        }
+    };
+    auto store = [&](int buf) {
+        const uint32_t st = lds0 + (uint32_t)buf * STAGE;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            u32x2 h, m, l;
+            split3(pw[i], h, m, l);
+            *(lds_u32x2_p)(uintptr_t)(st + dst[i]) = h;
+            *(lds_u32x2_p)(uintptr_t)(st + PLANE + dst[i]) = m;
+            *(lds_u32x2_p)(uintptr_t)(st + 2 * PLANE + dst[i]) = l;
+            split3(px[i], h, m, l);
+            *(lds_u32x2_p)(uintptr_t)(st + TILE + dst[i]) = h;
+            *(lds_u32x2_p)(uintptr_t)(st + TILE + PLANE + dst[i]) = m;
+            *(lds_u32x2_p)(uintptr_t)(st + TILE + 2 * PLANE + dst[i]) = l;
+        }
+    };
+
+    // Wave (wm, wq): tokens 32 wm .. + 31 (blocks 2 wm, 2 wm + 1); column block cb(nb).
+    const int wm = BIG ? (wave & 3) : (wave & 1), wq = BIG ? (wave >> 2) : (wave >> 1);
+    auto cb = [&](int nb) { return BIG ? 4 * wq + nb : wq + 2 * nb; };
+    f32x4 tot[NB][2], chk[NB][2];
+#pragma unroll
+    for (int a = 0; a < NB; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) tot[a][b] = chk[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int steps = p.d_in / X3_BK;
+    int cu = 0;  // units done in the running chunk
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < steps; t++) {
+        const uint32_t st = lds0 + (uint32_t)(t & 1) * STAGE;
+        if (t + 1 < steps) load(t + 1);
+        u32x4 a[3][NB], b[3][2];
+#pragma unroll
+        for (int pl = 0; pl < 3; pl++) {
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                a[pl][nb] = *(lds_u32x4_p)(uintptr_t)(st + pl * PLANE + cb(nb) * 1024 + lane * 16);
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+                b[pl][mb] = *(lds_u32x4_p)(uintptr_t)(st + TILE + pl * PLANE + (2 * wm + mb) * 1024 + lane * 16);
+        }
+        // The six products, smallest first: (weight part, x part).
+        constexpr int kA[6] = {2, 0, 1, 1, 0, 0}, kB[6] = {0, 2, 1, 0, 1, 0};
+        const bool fresh = cu == 0;  // a chunk starts: its chain begins at zero
+#pragma unroll
+        for (int j = 0; j < 6; j++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+                    chk[nb][mb] = mfma_x3(a[kA[j]][nb], b[kB[j]][mb],
+                                          (j == 0 && fresh) ? f32x4{0.f, 0.f, 0.f, 0.f} : chk[nb][mb]);
+        if (++cu == p.chunk || t == steps - 1) {
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++) tot[nb][mb] += chk[nb][mb];
+            cu = 0;
+        }
+        // Stage t + 1 goes to the other buffer, last read in step t - 1 (every wave has passed the
+        // barrier after it).
+        if (t + 1 < steps) store((t + 1) & 1);
+        __syncthreads();
+    }
+    const int n0w = tn * T + (BIG ? 64 * wq : 0);
+    if (n0w >= n_cols) return;
+    proj_store<OUT, BIG>(p, tot, row0, n0w, wm, wq, lane);
 }
 
 // The epilogue of four summed columns c .. c + 3 (of all n_out outputs side by side) of token m:
@@ -456,7 +632,11 @@ hipError_t launch_small(ProjParams p, hipStream_t stream) {
     p.m_tiles = (p.tokens - p.m_base + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
     const unsigned blocks = (unsigned)((int64_t)p.m_tiles * p.n_tiles);
-    if (p.d_in % 32 == 0)
+    if (p.d_in % X3_BK == 0) {
+        p.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
+        hipLaunchKernelGGL((qkv_proj_x3<OUT, false>), dim3(blocks), dim3(threads<false>()), (x3_lds<false>()), stream,
+                           p);
+    } else if (p.d_in % 32 == 0)
         hipLaunchKernelGGL((qkv_proj<OUT, 32, false>), dim3(blocks), dim3(threads<false>()), (proj_lds<32, false>()),
                            stream, p);
     else
@@ -469,6 +649,24 @@ template <int OUT>
 hipError_t launch_unsplit(ProjParams p, hipStream_t stream) {
     const int64_t big_m = (p.tokens + 127) / 128, big_n = (p.width * p.n_out + 127) / 128;
     if (big_m * big_n < kBigTilesMin) return launch_small<OUT>(p, stream);
+    if (p.d_in % X3_BK == 0) {
+        // The bf16 three-way split, one workgroup per CU: the token tiles past the full rounds go
+        // to SMALL tiles when the last round would be less than half full, as below.
+        int64_t m_big = big_m;
+        const int64_t slots = (int64_t)device_cus(), rest = slots > 0 ? (big_m * big_n) % slots : 0;
+        if (slots > 0 && big_m * big_n > slots && rest > 0 && 2 * rest < slots)
+            m_big = std::max<int64_t>(1, (big_m * big_n - rest) / big_n);
+        ProjParams q = p;
+        q.m_tiles = (int32_t)m_big;
+        q.n_tiles = (int32_t)big_n;
+        q.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
+        hipLaunchKernelGGL((qkv_proj_x3<OUT, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
+                           (x3_lds<true>()), stream, q);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess || m_big * 128 >= p.tokens) return e;
+        p.m_base = (int32_t)(m_big * 128);
+        return launch_small<OUT>(p, stream);
+    }
     // BIG tiles run two per CU, in rounds that each take one tile's time. A last round less than
     // half full would cost a whole one: the token tiles past the full rounds go to SMALL tiles
     // instead (four per CU, a quarter of the work each), in a second launch.
