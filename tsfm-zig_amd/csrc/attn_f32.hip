@@ -1,11 +1,12 @@
-// Fused f32 attention for gfx950: one workgroup = one (series, head) x 128 queries.
+// f32 attention for short rows (n_k <= 144: Chronos-Bolt's 129-token rows), on the f32 matrix
+// cores (v_mfma_f32_16x16x4_f32). Longer rows take the bf16x3 streaming kernel (attn_x3.hip).
 //
 // The reference computes one (series, head) at a time with a materialised n x n score matrix:
 // gemmNT -> bias -> masked softmax -> gemmNN (src/core/attn.zig:72-96). Here the whole batch is one
-// launch and no score matrix exists: K/V tiles of 64 keys are staged in LDS and both products run
-// on the f32 matrix cores (v_mfma_f32_16x16x4_f32) with an online softmax in registers.
+// launch and no score matrix exists: each (series, head)'s K/V sit in LDS and both products run on
+// the matrix cores with an online softmax in registers.
 //
-// Wave layout (8 waves x 16 queries; four waves per SIMD hide each other's latencies):
+// Wave layout (one wave per 16 queries):
 //   S^T = K . Q^T   A = K rows (16 keys) from LDS, B = Q^T (16 queries) held in VGPRs.
 //                   Accumulator lane l holds query l%16 and keys 4*(l/16)+r, r=0..3.
 //   O^T += V^T . P^T  A = V^T (16 dims x 4 keys) from LDS, B = P^T straight from the S^T
@@ -23,14 +24,9 @@
 // instead of sixteen, within the reference's own cross-host spread, and two dependency chains for
 // the matrix pipe. (Four chains of four summed as a tree round six times but cost twelve more VALU
 // instructions per 16-key block, and on gfx950 the f32 matrix instructions and the VALU take turns.)
-//
-// Pipeline: two LDS stages. While the waves compute on stage t&1, tile t+1 is fetched from HBM and
-// written to the other stage in two 32-key halves (one over the S product, one over softmax and
-// the PV product), 13 registers per thread; one barrier per tile. The whole wave state (q, O,
-// scores, operands, staging) fits 128 registers, which gives four waves per SIMD.
-// LDS per stage: K [64 keys][68] (padded: conflict-free 128-bit reads), V [16 key quads][64 dims,
-// XOR-swizzled][4 keys] (conflict-free transposing writes and operand reads), and one additive mask
-// term per key. Two stages + the T5 table fit two workgroups per CU.
+// LDS: K [keys][68] (padded: conflict-free 128-bit reads), V as rows [key][64] (DMA-staged) or
+// [key quad][64 dims, XOR-swizzled][4 keys] (register-staged with RoPE), one additive mask term per
+// key.
 #include <atomic>
 
 #include "common.hpp"
@@ -39,46 +35,13 @@
 namespace tsfm {
 namespace {
 
-constexpr int NK = 64;          // keys per LDS tile
-constexpr int QW = 16;          // queries per wave (one 16-query block)
-constexpr int NWAVE = 8;
-constexpr int NT = 64 * NWAVE;  // threads per workgroup
-constexpr int QT = QW * NWAVE;  // queries per workgroup
 constexpr int KPAD = 68;        // K row pitch in LDS (floats)
-constexpr int kLutPad = 16;     // T5 table margin on each side (entries)
-
-struct Stage {
-    float k[NK * KPAD];      // [key][KPAD], RoPE applied
-    float v[NK * kHeadDim];  // [key quad][swizzled dim][4 keys]
-    float kadd[NK];          // additive mask term of each key (0, -FLT_MAX or -inf)
-};
 
 // Swizzled V slot of a head dim: XOR of bits 3..4 into bits 0..1 spreads both the transposing
 // writes (stride 4 dims) and the operand reads (16 consecutive dims) over all LDS banks.
 __device__ __forceinline__ int vslot(int dim) { return dim ^ ((dim >> 3) & 3); }
 
-// Additive mask term of one key: the part of the reference's mask rule (src/core/attn.zig:35-67,
-// src/timestral/model.zig:612-632) that depends on the key alone. Keys past n_k are tile padding.
-template <int MASK>
-__device__ __forceinline__ float key_term(int key, int n_k, bool valid, int ctx_keys) {
-    if (key >= n_k) return kNegInf;
-    if (MASK == KEYS_ADDITIVE) return valid ? 0.f : -kFltMax;
-    if (MASK == CAUSAL_KEYS || MASK == FULL_KEYS) return valid ? 0.f : kNegInf;
-    if (MASK == DECODER) return (key < ctx_keys && valid) ? 0.f : kNegInf;
-    return 0.f;  // FULL, CAUSAL
-}
-
-// The whole mask rule for one scaled, biased score x, given its key term ka.
-template <int MASK>
-__device__ __forceinline__ float masked(float x, float ka, int key, int qpos, int n_k, int chain_start) {
-    if (MASK == CAUSAL) return key <= qpos ? x + ka : kNegInf;
-    if (MASK == CAUSAL_KEYS) return (key == qpos && key < n_k) ? x : (key <= qpos ? x + ka : kNegInf);
-    if (MASK == FULL_KEYS) return (key == qpos && key < n_k) ? x : x + ka;
-    if (MASK == DECODER) return (key >= chain_start && key <= qpos && key < n_k) ? x : x + ka;
-    return x + ka;  // FULL, KEYS_ADDITIVE: x + 0, x + (-FLT_MAX), or -inf for padding
-}
-
-// ---- one wave's 16-query block: state and the per-tile arithmetic shared by both kernels ----
+// ---- one wave's 16-query block: state and the per-tile arithmetic ----
 
 // Q^T operand q[s] (step s < 8 -> dim 8g+s, s >= 8 -> dim 32+8g+(s-8) of query ql), the O^T
 // accumulator (lane: query ql, dims 16db + 4g + r) and the online-softmax state of the lane's query.
@@ -439,212 +402,6 @@ __device__ __forceinline__ void store_o(const QBlock& w, float* O, const Params&
     }
 }
 
-// T5 bias of head h by relative index t = j - i + n_q - 1, stored at lut_raw[kLutPad + t] for t in
-// [-kLutPad, n_q + n_k - 1 + kLutPad): the margins repeat the end values (the bucket of the nearest
-// real index), so padded keys and query slots index it without a clamp.
-__device__ __forceinline__ void fill_rel_lut(float* lut_raw, const Params& p, int h, int tid, int nthreads) {
-    const int n_rel = p.n_q + p.n_k - 1;
-    for (int u = tid; u < n_rel + 2 * kLutPad; u += nthreads) {
-        const int t = min(max(u - kLutPad, 0), n_rel - 1);
-        lut_raw[u] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
-    }
-}
-
-// ---- streaming kernel: K/V tiles through two LDS stages ----------------------------------------
-
-template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_fwd_f32(Params p) {
-    __shared__ __attribute__((aligned(16))) Stage stage[2];
-    __shared__ float lut_raw[BIAS == BIAS_REL ? kRelMax + 2 * kLutPad : 1];
-    __shared__ __attribute__((aligned(16))) float thin_qp[2 * kHeadDim];  // a thin wave's q and weights
-    float* const lut = lut_raw + (BIAS == BIAS_REL ? kLutPad : 0);
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ql = lane & 15, g = lane >> 4;
-    const int q_tiles = (p.n_q + QT - 1) / QT;
-    const int logical = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = logical / q_tiles;
-    int qt = logical % q_tiles;
-    if (MASK == CAUSAL || MASK == CAUSAL_KEYS) qt = q_tiles - 1 - qt;  // longest rows first
-    const int b = bh / p.H, h = bh % p.H;
-    const int q0 = qt * QT;
-    const int wq0 = q0 + wave * QW;
-    const int qi = wq0 + ql;
-
-    const float* __restrict__ Q = static_cast<const float*>(p.q) + b * p.q_batch + h * kHeadDim;
-    const float* __restrict__ K = static_cast<const float*>(p.k) + b * p.k_batch + h * kHeadDim;
-    const float* __restrict__ V = static_cast<const float*>(p.v) + b * p.v_batch + h * kHeadDim;
-    float* __restrict__ O = static_cast<float*>(p.o) + b * p.o_batch + h * kHeadDim;
-    const int rope_tab = p.rope_rows_per_table > 0 ? (p.rope_row0 + b) / p.rope_rows_per_table : 0;
-    const float* __restrict__ RC = ROPE ? p.rope_cos + rope_tab * p.rope_table_stride : nullptr;
-    const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
-
-    // Key range of the workgroup and of this wave (tiles past it are skipped).
-    const int wg_qhi = p.q_pos0 + min(p.n_q, q0 + QT) - 1;
-    const int kend = key_end_for<MASK>(wg_qhi, p.n_k, p.ctx_keys);
-    const int wave_nq = max(0, min(QW, p.n_q - wq0));
-    const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys) : 0;
-    const int ntiles = (kend + NK - 1) / NK;
-    const bool thin = wave_nq == 1;  // one query: the VALU path (attend_thin)
-
-    // key_valid of this row through a buffer descriptor sized to the bytes the mask reads: a read
-    // past them returns 0 (= invalid), so the load needs neither a bounds test nor a branch.
-    const __amdgpu_buffer_rsrc_t kv_rsrc = make_buf(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid,
-                                                    mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0);
-
-    // ---- tile staging: HBM -> registers -> LDS, one 16-key quarter at a time (6 registers) ----
-    // K: thread -> key row tid/32 of the quarter, dims c and c+32 with c = tid%32 (a RoPE pair).
-    // V: wave w -> half w%2 of key quad w/2 of the quarter, lane -> dim: two keys of one dim, half
-    //    of a 16-byte slot of the transposed layout. Key valid bytes: lane = key of the tile, in every
-    //    wave, with the tile's first quarter.
-    // All through buffer descriptors that end after key n_k - 1: rows past it (tile padding) read
-    // as zeros, so a partial tile needs no clamping and no branch.
-    const int krow = tid >> 5, kc = tid & 31;
-    struct Quarter {  // one thread's share of a 16-key quarter tile, in flight from HBM to LDS
-        float klo, khi, kcs, ksn;
-        f32x2 v;  // V rows 4*(wave/2) + 2*(wave%2) + 0..1 of the quarter, dim `lane`
-    };
-    const __amdgpu_buffer_rsrc_t k_buf = make_buf(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 4));
-    const __amdgpu_buffer_rsrc_t v_buf = make_buf(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 4));
-    const __amdgpu_buffer_rsrc_t c_buf = make_buf(RC, ROPE ? (uint32_t)p.n_k * 128u : 0u);
-    const __amdgpu_buffer_rsrc_t s_buf = make_buf(RS, ROPE ? (uint32_t)p.n_k * 128u : 0u);
-    const uint32_t koff = (uint32_t)(krow * p.k_tok + kc) * 4u;
-    const uint32_t voff = (uint32_t)((4 * (wave >> 1) + 2 * (wave & 1)) * p.v_tok + lane) * 4u;
-    const uint32_t coff = (uint32_t)(krow * 32 + kc) * 4u;
-
-    auto fetch = [&](int qbase, Quarter& hs) {  // keys [qbase, qbase + 16)
-        const uint32_t kq = koff + (uint32_t)(qbase * p.k_tok) * 4u;
-        hs.klo = bld1(k_buf, kq);
-        hs.khi = bld1(k_buf, kq + 128u);
-        const uint32_t vq = voff + (uint32_t)(qbase * p.v_tok) * 4u;
-        hs.v = f32x2{bld1(v_buf, vq), bld1(v_buf, vq + (uint32_t)p.v_tok * 4u)};
-        if (ROPE) {
-            hs.kcs = bld1(c_buf, coff + (uint32_t)qbase * 128u);
-            hs.ksn = bld1(s_buf, coff + (uint32_t)qbase * 128u);
-        }
-    };
-    auto store = [&](Stage& st, int quarter, Quarter& hs) {
-        if (ROPE) {
-#pragma clang fp contract(off)
-            const float x1 = hs.klo, x2 = hs.khi;  // nn.ropeHalf, src/core/nn.zig:453-460
-            hs.klo = x1 * hs.kcs - x2 * hs.ksn;
-            hs.khi = x2 * hs.kcs + x1 * hs.ksn;
-        }
-        float* kd = st.k + (quarter * 16 + krow) * KPAD + kc;
-        kd[0] = hs.klo;
-        kd[32] = hs.khi;
-        st2(st.v + (quarter * 4 + (wave >> 1)) * (kHeadDim * 4) + vslot(lane) * 4 + 2 * (wave & 1), hs.v);
-    };
-    // key_valid byte of key tbase + lane (returned as loaded; 1 for masks that do not read it).
-    auto fetch_valid = [&](int tbase) -> uint32_t {
-        return mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, tbase + lane, 0, 0) : 1u;
-    };
-    // Additive mask term of key tbase + lane, and the tile's mask-free test (every term 0).
-    auto kterm = [&](int tbase, uint32_t kvb) { return key_term<MASK>(tbase + lane, p.n_k, kvb != 0, p.ctx_keys); };
-    auto all_valid = [&](int tbase, uint32_t kvb) { return __ballot(kterm(tbase, kvb) != 0.f) == 0; };
-    // A whole tile in one go, quarter by quarter (for waves with no products to hide it behind);
-    // returns the tile's key_valid bytes.
-    auto stage_all = [&](Stage& st, int tbase) {
-        Quarter hs;
-        const uint32_t kvb = fetch_valid(tbase);
-#pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            fetch(tbase + 16 * qq, hs);
-            store(st, qq, hs);
-        }
-        st.kadd[lane] = kterm(tbase, kvb);
-        return kvb;
-    };
-
-    // Prologue: tile 0's four quarters, q and the T5 table are all requested before anything waits.
-    uint32_t kvb_next = fetch_valid(0);  // key_valid bytes of the tile being staged
-    {
-        Quarter s0, s1, s2, s3;
-        fetch(0, s0);
-        fetch(16, s1);
-        fetch(32, s2);
-        fetch(48, s3);
-        QBlock w;
-        load_q<ROPE>(w, Q, RC, RS, p, qi, g);
-        if (thin) thin_store_q(w, thin_qp, ql, g);
-        if (BIAS == BIAS_REL) fill_rel_lut(lut_raw, p, h, tid, NT);
-        store(stage[0], 0, s0);
-        store(stage[0], 1, s1);
-        store(stage[0], 2, s2);
-        store(stage[0], 3, s3);
-        stage[0].kadd[lane] = kterm(0, kvb_next);  // every wave writes the same 64 terms
-        bool next_all_valid = all_valid(0, kvb_next);  // of the tile about to be computed
-        __syncthreads();
-
-        if (thin) {
-            // Same staging and barriers as the loop below, one whole tile at a time.
-            for (int t = 0; t < ntiles; t++) {
-                const int kbase = t * NK;
-                const Stage& st = stage[t & 1];
-                if (kbase < wave_kend)
-                    attend_thin<MASK, BIAS>(w, p, st.k, st.v, st.kadd, lut, thin_qp, thin_qp + kHeadDim, kbase,
-                                            min(NK, wave_kend - kbase), wq0, h, lane);
-                if (t + 1 < ntiles) stage_all(stage[(t + 1) & 1], kbase + NK);
-                __syncthreads();
-            }
-            store_thin(w, O, p, wq0, lane);
-            return;
-        }
-        for (int t = 0; t < ntiles; t++) {
-            const int kbase = t * NK;
-            const Stage& st = stage[t & 1];
-            Stage& nxt = stage[(t + 1) & 1];
-            const int nbase = kbase + NK;
-            const bool more = t + 1 < ntiles;
-            // The next tile passes through one quarter register set, a quarter per quarter of this
-            // tile's work: fetched at S blocks 0, 1, 3 and PV block 2, stored one step later.
-            Quarter sq;
-            auto stage_next = [&](int phase, int kb) {
-                if (!more) return;
-                if (phase == 0 && kb == 0) {
-                    fetch(nbase, sq);
-                    kvb_next = fetch_valid(nbase);
-                }
-                if (phase == 0 && (kb == 1 || kb == 3)) {
-                    store(nxt, kb >> 1, sq);
-                    fetch(nbase + 16 * (kb / 2 + 1), sq);
-                }
-                if (phase == 1) nxt.kadd[lane] = kterm(nbase, kvb_next);
-                if (phase == 2 && kb == 2) {
-                    store(nxt, 2, sq);
-                    fetch(nbase + 48, sq);
-                }
-            };
-            const int nkb = min(4, max(0, (wave_kend - kbase + 15) >> 4));
-            // Mask-free tile: all 64 keys below wave_kend (<= n_k) and valid and, for the causal
-            // masks, every query at or past the tile's last key. Query slots past n_q hold q = 0 and
-            // are never stored, so they may run mask-free too, except with a dense bias (no bias
-            // row to read).
-            bool plain = kbase + NK <= wave_kend && (wave_nq == QW || BIAS != BIAS_DENSE) && MASK != DECODER &&
-                         next_all_valid;
-            if (MASK == CAUSAL || MASK == CAUSAL_KEYS) plain = plain && kbase + NK - 1 <= p.q_pos0 + wq0;
-            // A wave with only a few keys left in this tile takes them on the VALU (and stages the
-            // next tile, if the workgroup has one, in one go).
-            const bool few = !plain && nkb > 0 && wave_kend - kbase <= kValuKeys;
-            if (plain) {
-                attend_tile<MASK, BIAS, true, 4, false>(w, p, st.k, st.v, st.kadd, lut, kbase, 4, qi, h, ql, g,
-                                                 stage_next);
-            } else if (nkb > 0 && !few) {
-                attend_tile<MASK, BIAS, false, 4, false>(w, p, st.k, st.v, st.kadd, lut, kbase, nkb, qi, h, ql, g,
-                                                  stage_next);
-            } else if (more) {
-                kvb_next = stage_all(nxt, nbase);
-            }
-            if (few) attend_keys_valu<MASK, BIAS, false>(w, p, st.k, st.v, st.kadd, lut, kbase, wave_kend - kbase, qi, h, g);
-            if (more && (plain || (nkb > 0 && !few))) store(nxt, 3, sq);
-            // The next tile's flag, from its key_valid bytes fetched at the start of this one.
-            if (more) next_all_valid = all_valid(nbase, kvb_next);
-            __syncthreads();
-        }
-        store_o(w, O, p, qi, g);
-    }
-}
-
 // ---- short rows: every key resident in LDS ------------------------------------------------------
 //
 // Chronos-Bolt rows are short (at most 128 patches + REG = 129 tokens). Streamed through the
@@ -967,22 +724,15 @@ namespace {
 
 template <int MASK, int BIAS, bool ROPE>
 hipError_t launch_one(const Params& p, hipStream_t stream) {
-    if (p.n_k <= kResidentKeys) {  // short rows: the whole K/V of a (series, head) in LDS
-        const int q_tiles = (p.n_q + RQT - 1) / RQT;
-        const int64_t items = (int64_t)p.B * p.H * q_tiles;
-        if (items <= 0 || items > 0x7fffffff) return hipErrorInvalidValue;
-        const size_t lds = 2 * (size_t)resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL).total * sizeof(float);
-        const int cus = device_cus();
-        if (cus <= 0) return hipErrorInvalidDevice;
-        const int64_t blocks = items < cus ? items : cus;  // one persistent workgroup per CU
-        hipLaunchKernelGGL((attn_fwd_f32_resident<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(RNT), lds, stream,
-                           p, (int)items);
-        return hipGetLastError();
-    }
-    const int q_tiles = (p.n_q + QT - 1) / QT;
-    const int64_t blocks = (int64_t)p.B * p.H * q_tiles;
-    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_f32<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(NT), 0, stream, p);
+    const int q_tiles = (p.n_q + RQT - 1) / RQT;
+    const int64_t items = (int64_t)p.B * p.H * q_tiles;
+    if (items <= 0 || items > 0x7fffffff) return hipErrorInvalidValue;
+    const size_t lds = 2 * (size_t)resident_layout(p.n_q, p.n_k, BIAS == BIAS_REL).total * sizeof(float);
+    const int cus = device_cus();
+    if (cus <= 0) return hipErrorInvalidDevice;
+    const int64_t blocks = items < cus ? items : cus;  // one persistent workgroup per CU
+    hipLaunchKernelGGL((attn_fwd_f32_resident<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(RNT), lds, stream, p,
+                       (int)items);
     return hipGetLastError();
 }
 
@@ -1003,6 +753,8 @@ hipError_t launch_bias(const Params& p, int bias, bool rope, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_attn_f32(const Params& p, int mask, int bias, bool rope, hipStream_t s) {
+    // Rows longer than the resident kernel takes: the bf16x3 streaming kernel (attn_x3.hip).
+    if (p.n_k > kResidentKeys) return launch_attn_x3(p, mask, bias, rope, s);
     switch (mask) {
     case FULL: return launch_bias<FULL>(p, bias, rope, s);
     case KEYS_ADDITIVE: return launch_bias<KEYS_ADDITIVE>(p, bias, rope, s);

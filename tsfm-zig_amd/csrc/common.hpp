@@ -96,6 +96,27 @@ __device__ __forceinline__ float apply_mask(float x, int key, int qpos, int n_k,
     return x;
 }
 
+// Additive mask term of one key: the part of the reference's mask rule (src/core/attn.zig:35-67,
+// src/timestral/model.zig:612-632) that depends on the key alone. Keys past n_k are tile padding.
+template <int MASK>
+__device__ __forceinline__ float key_term(int key, int n_k, bool valid, int ctx_keys) {
+    if (key >= n_k) return kNegInf;
+    if (MASK == KEYS_ADDITIVE) return valid ? 0.f : -kFltMax;
+    if (MASK == CAUSAL_KEYS || MASK == FULL_KEYS) return valid ? 0.f : kNegInf;
+    if (MASK == DECODER) return (key < ctx_keys && valid) ? 0.f : kNegInf;
+    return 0.f;  // FULL, CAUSAL
+}
+
+// The whole mask rule for one scaled, biased score x, given its key term ka.
+template <int MASK>
+__device__ __forceinline__ float masked(float x, float ka, int key, int qpos, int n_k, int chain_start) {
+    if (MASK == CAUSAL) return key <= qpos ? x + ka : kNegInf;
+    if (MASK == CAUSAL_KEYS) return (key == qpos && key < n_k) ? x : (key <= qpos ? x + ka : kNegInf);
+    if (MASK == FULL_KEYS) return (key == qpos && key < n_k) ? x : x + ka;
+    if (MASK == DECODER) return (key >= chain_start && key <= qpos && key < n_k) ? x : x + ka;
+    return x + ka;  // FULL, KEYS_ADDITIVE: x + 0, x + (-FLT_MAX), or -inf for padding
+}
+
 // Bytes of key_valid per row the mask reads: DECODER only tests keys below ctx_keys.
 template <int MASK>
 __device__ __forceinline__ int valid_len(int n_k, int ctx_keys) {
@@ -114,6 +135,19 @@ __device__ __forceinline__ void rope4(f32x4& lo, f32x4& hi, f32x4 c, f32x4 s) {
     const f32x4 x1 = lo, x2 = hi;
     lo = x1 * c - x2 * s;
     hi = x2 * c + x1 * s;
+}
+
+constexpr int kLutPad = 32;  // T5 table margin on each side (entries): one 32-key chunk
+
+// T5 bias of head h by relative index t = j - i + n_q - 1, stored at lut_raw[kLutPad + t] for t in
+// [-kLutPad, n_q + n_k - 1 + kLutPad): the margins repeat the end values (the bucket of the nearest
+// real index), so padded keys and query slots index it without a clamp.
+__device__ __forceinline__ void fill_rel_lut(float* lut_raw, const Params& p, int h, int tid, int nthreads) {
+    const int n_rel = p.n_q + p.n_k - 1;
+    for (int u = tid; u < n_rel + 2 * kLutPad; u += nthreads) {
+        const int t = min(max(u - kLutPad, 0), n_rel - 1);
+        lut_raw[u] = p.rel_table[min(max(p.rel_bucket[t], 0), p.rel_buckets - 1) * p.H + h];
+    }
 }
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }

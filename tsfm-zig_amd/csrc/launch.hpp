@@ -9,6 +9,7 @@ namespace tsfm {
 
 // f32 q/k/v/o; mask = TSFM_MASK_*, bias = BiasKind.
 hipError_t launch_attn_f32(const Params& p, int mask, int bias, bool rope, hipStream_t stream);
+hipError_t launch_attn_x3(const Params& p, int mask, int bias, bool rope, hipStream_t stream);
 
 // bf16 (is_bf16) or f16 q/k/v/o, f32 accumulation.
 hipError_t launch_attn_half(const Params& p, bool is_bf16, int mask, int bias, bool rope, hipStream_t stream);
