@@ -38,6 +38,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int XQ = 32;                        // queries per wave
 constexpr int XK = 32;                        // keys per chunk
 constexpr int XMAXW = 8;                      // waves per workgroup, at most
+constexpr float kSlack = 5.5f;                // 8 ln 2 - a margin: weights stay below 2^8
 constexpr int XMINW = 4;                      // and at least (256 threads: one K and one V item each)
 constexpr int XNT = 64 * XMAXW;
 constexpr int kPlane = XK * kHeadDim / 2;     // dwords per bf16 plane of a chunk's K or V (4 KB)
@@ -299,30 +300,49 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         mloc = fmaxf(mloc, v);
                     }
                 }
-                const float m_new = fmaxf(m, pair_max(mloc));
-                const float m_use = m_new == kNegInf ? 0.f : m_new;
-                // As the f32 path: e = exp2(x log2e - m log2e) with ml = m log2e rounded once; a row
-                // whose max is still an additively masked score (about -FLT_MAX) takes
-                // exp2((x - m) log2e), which gives it the reference's uniform weights
-                // (src/core/nn.zig:470-505 on scores + (-floatMax)).
-                const bool big = m_use < -1e30f;
-                const float shift = big ? m_use : 0.f;
-                const float ml_new = big ? 0.f : m_use * kLog2e;
-                const float alpha = __builtin_amdgcn_exp2f(big ? (m - m_use) * kLog2e : ml - ml_new);
+                // The weights' reference max m trails the running max by at most kSlack: a chunk whose
+                // max stays within it leaves m, ml, l and O as they are (weights up to 2^8), which
+                // saves the rescale of O in most chunks; the normalised result is the same.
+                const float mc = pair_max(mloc);
+                float shift = 0.f, mlw = ml;
+                bool shifted = false;
+                if (__ballot(!(m > -1e30f && mc <= m + kSlack)) != 0) {
+                    const float m_new = fmaxf(m, mc);
+                    const float m_use = m_new == kNegInf ? 0.f : m_new;
+                    // As the f32 path: e = exp2(x log2e - m log2e) with ml = m log2e rounded once; a
+                    // row whose max is still an additively masked score (about -FLT_MAX) takes
+                    // exp2((x - m) log2e), which gives it the reference's uniform weights
+                    // (src/core/nn.zig:470-505 on scores + (-floatMax)).
+                    const bool big = m_use < -1e30f;
+                    shift = big ? m_use : 0.f;
+                    mlw = big ? 0.f : m_use * kLog2e;
+                    const float alpha = __builtin_amdgcn_exp2f(big ? (m - m_use) * kLog2e : ml - mlw);
+                    ml = (big || m_new == kNegInf) ? kNegInf : mlw;
+                    l = l * alpha;
+                    m = m_new;
+                    shifted = __ballot(big) != 0;
+                    if (__ballot(alpha != 1.f) != 0) {
+                        o[0] *= alpha;
+                        o[1] *= alpha;
+                    }
+                }
                 float lsum = 0.f;
+                if (!shifted) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r] - shift, kLog2e, -ml_new));
-                    x[r] = e;
-                    lsum += e;
+                    for (int r = 0; r < 16; r++) {
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r], kLog2e, -mlw));
+                        x[r] = e;
+                        lsum += e;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r] - shift, kLog2e, -mlw));
+                        x[r] = e;
+                        lsum += e;
+                    }
                 }
-                ml = (big || m_new == kNegInf) ? kNegInf : ml_new;
-                l = l * alpha + lsum;
-                m = m_new;
-                if (__ballot(alpha != 1.f) != 0) {
-                    o[0] *= alpha;
-                    o[1] *= alpha;
-                }
+                l = l + lsum;
 #pragma unroll
                 for (int j = 0; j < 2; j++)
 #pragma unroll
