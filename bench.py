@@ -133,6 +133,9 @@ class Bench:
     # timed steps, from events the step recorded around it; None = the step is one launch.
     kernel_ms: Optional[Callable[[], float]] = None
     kernel_work: Optional[float] = None  # algorithmic work per dominant launch (bound's unit)
+    # The dominant matrix work is f32 arithmetic run on the bf16 matrix cores as a three-way split
+    # (six bf16 products per f32 product): the line then also reports that pipe's own ceiling.
+    x3: bool = False
 
 
 def _check(ta, rc):
@@ -174,7 +177,7 @@ def run_chronos2(torch, ta, workloads, peak):
     config = {"workload": w.name, "B": w.B, "H": w.H, "L": w.n_q, "D": 64, "mask": "keys_additive", "rope": True,
               "scale": w.scale, "layout": "(B, L, H*D) f32"}
     return Bench(w, step, lambda: o.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
-                 "TFLOP/s", w.B)
+                 "TFLOP/s", w.B, x3=True)
 
 
 def run_bolt(torch, ta, workloads, peak):
@@ -374,7 +377,7 @@ def run_proj(torch, ta, workloads, peak):
 
     config = {"workload": w.name, "B": w.B, "L": L, "d_model": d, "H": w.H, "outputs": "q,k,v", "rope": True,
               "layout": "x (B*L, d), W (d, d) x3, q/k/v (B*L, d) f32"}
-    return Bench(w, step, output, cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"], "TFLOP/s", 16)
+    return Bench(w, step, output, cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"], "TFLOP/s", 16, x3=True)
 
 
 def run_encoder(torch, ta, workloads, peak):
@@ -404,7 +407,7 @@ def run_encoder(torch, ta, workloads, peak):
     config = {"workload": w.name, "B": w.B, "L": L, "d_model": d, "H": w.H, "d_ff": F, "layers": m["n_layers"],
               "mask": "keys_additive", "rope": True, "scale": 1.0, "weights": "random-init f32"}
     b = Bench(w, step, lambda: x.cpu().numpy().reshape(w.B, L, d), cpu_leg, config, "f32", "mfma",
-              peak["f32_mfma_tflops"], "TFLOP/s", 1)
+              peak["f32_mfma_tflops"], "TFLOP/s", 1, x3=True)
     return b
 
 
@@ -528,7 +531,7 @@ def run_chronos2_forecast(torch, ta, workloads, peak):
               "missing": "oldest 0-25 % + 2 %", "weights": "random-init f32",
               "input": "sinusoid (period 24, amplitude 10) + trend + N(0,1)"}
     return Bench(w, step, lambda: out.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
-                 "TFLOP/s", 1)
+                 "TFLOP/s", 1, x3=True)
 
 
 def run_timestral_forecast(torch, ta, workloads, peak):
@@ -586,7 +589,7 @@ def run_timestral_forecast(torch, ta, workloads, peak):
               "symmetric_averaging": True, "kv_cache": True, "missing": "oldest 0-25 % + 2 %",
               "weights": "random-init f32", "input": "sinusoid (period 24, amplitude 10) + trend + N(0,1)"}
     b = Bench(w, step, lambda: outs[True].cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
-              "TFLOP/s", 1)
+              "TFLOP/s", 1, x3=True)
     b.cpu_flops = m["reencode_flops"]  # the CPU leg runs the reference's re-encoding decode
     b.extra = reencode
     return b
@@ -688,6 +691,15 @@ def measure(torch, bench, steps: int, warmup: int, do_cpu: bool) -> dict:
         },
         "cpu_baseline": None,
     }
+    if bench.x3:
+        # f32 products as six bf16 products each on v_mfma_f32_{32x32x16,16x16x32}_bf16: the pipe's
+        # f32-equivalent ceiling is the bf16 dense peak / 6 (above the f32 matrix peak of `peak`).
+        pipe_peak = workloads.MI355X_PEAK["bf16_mfma_tflops"] / 6
+        out["roofline"]["bf16x3_pipe"] = {
+            "bf16_products_per_f32_product": 6,
+            "peak_f32_equiv": round(pipe_peak, 1),
+            "frac": round(achieved / pipe_peak, 4),
+        }
     extra = getattr(bench, "extra", None)
     if extra is not None:  # a second timing beside the step (the Timestral forecast without its cache)
         out["reencode"] = extra(min(steps, 3))

@@ -151,6 +151,28 @@ __device__ __forceinline__ void proj_store(const ProjParams& p, f32x4 (&sum)[BIG
     }
 }
 
+// The partial sums of a split reduction: partial row m of split s holds all n_cols columns (every
+// output side by side); proj_reduce adds the splits up in split order and finishes. Same wave
+// layout as proj_store.
+template <bool BIG>
+__device__ __forceinline__ void proj_partial(const ProjParams& p, f32x4 (&sum)[BIG ? 4 : 2][2], int row0, int n0w,
+                                             int wm, int wq, int lane, int split) {
+    constexpr int NB = BIG ? 4 : 2;
+    const int n_cols = p.width * p.n_out;
+    const int col = n0w - (n0w / p.width) * p.width;
+    const int c4 = 4 * (lane >> 4);
+    auto cq = [&](int nb) { return (BIG ? 16 * nb : 16 * wq + 32 * nb) + c4; };  // column in the head
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+        const int m = row0 + wm * 32 + mb * 16 + (lane & 15);
+        if (m >= p.tokens) continue;
+        float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0w;
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            if (col + cq(nb) < p.width) st4(out + cq(nb), sum[nb][mb]);
+    }
+}
+
 template <int OUT, int BK, bool BIG>
 __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(4, 4))) void qkv_proj(ProjParams p) {
     constexpr int TM = tile_m<BIG>(), TN = tile_n<BIG>(), NT = threads<BIG>();
@@ -272,20 +294,8 @@ __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(
     // stored). n0w: the output column (over all outputs) of the wave's head.
     const int n0w = tn * TN + (BIG ? 64 * wq : 0);
     if (n0w >= n_cols) return;
-    const int sel = n0w / p.width, col = n0w - sel * p.width;
-    const int c4 = 4 * (lane >> 4);
-    auto cq = [&](int nb) { return (BIG ? 16 * nb : 16 * wq + 32 * nb) + c4; };  // column in the head
     if (p.splits > 1) {  // partial sums only; proj_reduce adds them up in split order and finishes
-        // Partial row m of split s holds all n_cols columns (every output side by side).
-#pragma unroll
-        for (int mb = 0; mb < 2; mb++) {
-            const int m = row0 + wm * 32 + mb * 16 + (lane & 15);
-            if (m >= p.tokens) continue;
-            float* const out = p.partial + ((int64_t)split * p.tokens + m) * n_cols + n0w;
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++)
-                if (col + cq(nb) < p.width) st4(out + cq(nb), sum[nb][mb]);
-        }
+        proj_partial<BIG>(p, sum, row0, n0w, wm, wq, lane, split);
         return;
     }
     proj_store<OUT, BIG>(p, sum, row0, n0w, wm, wq, lane);
@@ -355,7 +365,9 @@ qkv_proj_x3(ProjParams p) {
     static_assert(T * 8 == 2 * NT, "each thread loads two 16-byte slots of each tile per step");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int tm, tn;
-    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, tm, tn);
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int split = p.splits > 1 ? logical % p.splits : 0;  // this workgroup's share of the reduction
+    tile_of(p.splits > 1 ? logical / p.splits : logical, p.m_tiles, p.n_tiles, tm, tn);
     const int n_cols = p.width * p.n_out;
     const int row0 = p.m_base + tm * T;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)smem;
@@ -408,13 +420,16 @@ qkv_proj_x3(ProjParams p) {
 #pragma unroll
         for (int b = 0; b < 2; b++) tot[a][b] = chk[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int steps = p.d_in / X3_BK;
+    // Steps [t0, steps) of 32 indices: the whole reduction, or this split's share (split_steps
+    // counts 16-wide units and is even when the reduction is split for this kernel).
+    const int t0 = p.splits > 1 ? split * (p.split_steps / 2) : 0;
+    const int steps = p.splits > 1 ? min(p.d_in / X3_BK, t0 + p.split_steps / 2) : p.d_in / X3_BK;
     int cu = 0;  // units done in the running chunk
-    load(0);
+    load(t0);
     store(0);
     __syncthreads();
-    for (int t = 0; t < steps; t++) {
-        const uint32_t st = lds0 + (uint32_t)(t & 1) * STAGE;
+    for (int t = t0; t < steps; t++) {
+        const uint32_t st = lds0 + (uint32_t)((t - t0) & 1) * STAGE;
         if (t + 1 < steps) load(t + 1);
         u32x4 a[3][NB], b[3][2];
 #pragma unroll
@@ -446,11 +461,15 @@ qkv_proj_x3(ProjParams p) {
         }
         // Stage t + 1 goes to the other buffer, last read in step t - 1 (every wave has passed the
         // barrier after it).
-        if (t + 1 < steps) store((t + 1) & 1);
+        if (t + 1 < steps) store((t + 1 - t0) & 1);
         __syncthreads();
     }
     const int n0w = tn * T + (BIG ? 64 * wq : 0);
     if (n0w >= n_cols) return;
+    if (p.splits > 1) {
+        proj_partial<BIG>(p, tot, row0, n0w, wm, wq, lane, split);
+        return;
+    }
     proj_store<OUT, BIG>(p, tot, row0, n0w, wm, wq, lane);
 }
 
@@ -722,8 +741,10 @@ size_t proj_split_bytes(ProjParams& p) {
     // at most two splits).
     int s = (int)std::min<int64_t>((512 + blocks - 1) / blocks, std::min(steps / 8, 16));
     if (s < 2) return 0;
-    const int per = (steps + s - 1) / s;
+    int per = (steps + s - 1) / s;
+    if (p.d_in % X3_BK == 0) per += per & 1;  // whole 32-index steps for the bf16x3 kernel
     s = (steps + per - 1) / per;
+    if (s < 2) return 0;
     p.splits = s;
     p.split_steps = per;
     // s * blocks <= 512 + blocks - 1 < 1536 and tokens * width <= blocks * BM * BN, so the partials
@@ -770,8 +791,15 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.m_tiles * p.n_tiles;
     p.chunk = proj_chunk(p.splits > 1 ? p.split_steps : p.d_in / 16);
     if (p.splits > 1) {
-        hipLaunchKernelGGL((qkv_proj<0, 16, false>), dim3((unsigned)(blocks * p.splits)), dim3(threads<false>()),
-                           (proj_lds<16, false>()), stream, p);
+        if (p.d_in % X3_BK == 0) {
+            ProjParams q = p;
+            q.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
+            hipLaunchKernelGGL((qkv_proj_x3<0, false>), dim3((unsigned)(blocks * p.splits)), dim3(threads<false>()),
+                               (x3_lds<false>()), stream, q);
+        } else {
+            hipLaunchKernelGGL((qkv_proj<0, 16, false>), dim3((unsigned)(blocks * p.splits)), dim3(threads<false>()),
+                               (proj_lds<16, false>()), stream, p);
+        }
         hipError_t e = hipGetLastError();
         if (e == hipSuccess && p.norm_scale != nullptr) {
             hipLaunchKernelGGL(proj_reduce_norm, dim3((unsigned)((p.tokens + 3) / 4)), dim3(256), 0, stream, p);
