@@ -302,3 +302,39 @@ def test_registered_weight_linear_matches_oracle(ta, orc, gpu_ready):
         ta.weight_release(h)
     assert np.array_equal(y1, y2)
     assert _ref.scaled_err(y1, _linear(orc, x, w)) <= TOL
+
+
+def test_presplit_operands_give_the_same_bits(ta, orc, gpu_ready):
+    """A product of at least 2^30 multiply-adds through tsfm_qkv_project splits x and the weights
+    into bf16 parts once (its operand workspace) and reads them with DMA; tsfm_qkv_project_noalloc
+    has no such workspace and splits its tiles as it loads them. Same split, same products in the
+    same order: bit-identical q/k/v, both within the bar of the oracle."""
+    import torch
+
+    b, seq, d, nh = 8, 577, 768, 12
+    tokens, inner = b * seq, nh * 64
+    assert tokens * 3 * inner * d >= 1 << 30
+    rng = np.random.default_rng(577)
+    x = rng.standard_normal((tokens, d)).astype(np.float32)
+    ws = _weights(rng, inner, d, 3)
+    cos_t, sin_t = orc.chronos2_rope_tables(seq, 64, 10000.0)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    dx, dw, dc, ds = cu(x), [cu(w) for w in ws], cu(cos_t), cu(sin_t)
+
+    def run(fn):
+        outs = [torch.full((tokens, inner), -3.0, device="cuda") for _ in range(3)]
+        a = ta.ProjArgs(dtype=ta.DTYPE_F32, out_dtype=ta.DTYPE_F32, batch=b, seq=seq, d_in=d, heads=nh, head_dim=64,
+                        flags=ta.DEVICE_PTRS, rope_half=32, rope_rows_per_table=0, rope_row0=0, rope_table_stride=0,
+                        x=dx.data_ptr(), x_tok=d, w_q=dw[0].data_ptr(), w_k=dw[1].data_ptr(), w_v=dw[2].data_ptr(),
+                        w_gate=None, q=outs[0].data_ptr(), q_tok=inner, k=outs[1].data_ptr(), k_tok=inner,
+                        v=outs[2].data_ptr(), v_tok=inner, gate=None, gate_tok=0, rope_cos=dc.data_ptr(),
+                        rope_sin=ds.data_ptr(), stream=0)
+        assert fn(a) == ta.OK, ta.last_error()
+        torch.cuda.synchronize()
+        return [o.cpu().numpy() for o in outs]
+
+    pre, own = run(ta.qkv_project), run(ta.qkv_project_noalloc)
+    want = _chronos2_oracle(orc, x, *ws, cos_t, sin_t, b, seq, d, nh)
+    for got, alt, ref in zip(pre, own, want):
+        np.testing.assert_array_equal(got, alt)
+        assert _ref.scaled_err(got, ref) <= TOL

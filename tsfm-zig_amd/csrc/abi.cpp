@@ -766,13 +766,23 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
         float* part = nullptr;
         bool owned = false;
         if ((e = split_buf_for(ctx, s, &part, &owned)) != hipSuccess) return hip_fail(e, "split workspace");
+        const size_t planes_n = tsfm::proj_plane_bytes(tokens, a->d_in, width * (gated ? 4 : 3));
+        char* planes = nullptr;
+        bool planes_owned = false;
+        if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotProject, planes_n, &planes, &planes_owned)) != hipSuccess) {
+            if (owned) (void)hipFreeAsync(part, s);
+            return hip_fail(e, "operand split workspace");
+        }
         {
             tsfm::SplitWorkspace ws(part);
+            tsfm::PlaneWorkspace pws(planes, planes_n);
             e = tsfm::launch_proj(p, s);
         }
         const hipError_t f = owned ? hipFreeAsync(part, s) : hipSuccess;
+        const hipError_t g = planes_owned ? hipFreeAsync(planes, s) : hipSuccess;
         if (e != hipSuccess) return hip_fail(e, "projection launch");
         if (f != hipSuccess) return hip_fail(f, "split workspace release");
+        if (g != hipSuccess) return hip_fail(g, "operand split workspace release");
         return TSFM_OK;
     }
     // Host pointers: stage x, the weights and the tables, run, copy the output rows back.
@@ -793,11 +803,14 @@ int tsfm_qkv_project(const tsfm_proj_args* a) {
     for (int i = 0; i < 4; i++) w_at[i] = plan.take(i < 3 || gated ? w_n : 0);
     for (int i = 0; i < 4; i++) y_at[i] = plan.take(y_n[i]);
     const size_t c_at = plan.take(t_n), s_at = plan.take(t_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
+    const size_t planes_n = tsfm::proj_plane_bytes(tokens, a->d_in, width * (gated ? 4 : 3));
+    const size_t planes_at = plan.take(planes_n);
     rc = ensure_buf(ctx, plan.off);
     if (rc != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
     tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
+    tsfm::PlaneWorkspace pws(base + planes_at, planes_n);
     const float* w_src[4] = {a->w_q, a->w_k, a->w_v, a->w_gate};
     struct Up { const void* src; size_t at, n; } ups[] = {
         {a->x, x_at, x_n}, {w_src[0], w_at[0], w_n}, {w_src[1], w_at[1], w_n}, {w_src[2], w_at[2], w_n},
@@ -948,6 +961,7 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
     const size_t scratch_n = (size_t)(rows * (5 * d + F)) * 4;
+    const size_t planes_n = tsfm::proj_plane_bytes(rows, std::max(d, F), std::max(3 * d, F));
     hipError_t e;
     if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
         bool ok = aligned(a->x, 16) && aligned(a->rope_cos, 16) && aligned(a->rope_sin, 16) && aligned(a->final_norm, 16);
@@ -961,11 +975,12 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
         hipStream_t s = static_cast<hipStream_t>(a->stream);
         char* scratch = nullptr;
         bool owned = false;
-        if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotEncode, scratch_n + tsfm::kSplitWorkspaceBytes, &scratch,
-                                            &owned)) != hipSuccess)
+        if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotEncode, scratch_n + tsfm::kSplitWorkspaceBytes + planes_n,
+                                            &scratch, &owned)) != hipSuccess)
             return hip_fail(e, "encoder scratch allocation");
         {
             tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + scratch_n));
+            tsfm::PlaneWorkspace pws(scratch + scratch_n + tsfm::kSplitWorkspaceBytes, planes_n);
             e = encode_on(a, a->x, a->key_valid, a->rope_cos, a->rope_sin, a->layers, a->final_norm,
                           reinterpret_cast<float*>(scratch), s);
         }
@@ -983,6 +998,7 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
     Plan plan;
     const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), c_at = plan.take(t_n), s_at = plan.take(t_n);
     const size_t fn_at = plan.take(vn), scr_at = plan.take(scratch_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
+    const size_t planes_at = plan.take(planes_n);
     std::vector<size_t> w_at((size_t)a->n_layers * 11);
     for (int l = 0; l < a->n_layers; l++)
         for (int i = 0; i < 11; i++) w_at[(size_t)l * 11 + i] = plan.take(sizes[i]);
@@ -991,6 +1007,7 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
     tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
+    tsfm::PlaneWorkspace pws(base + planes_at, planes_n);
     auto up = [&](size_t at, const void* src, size_t n) {
         return hipMemcpyAsync(base + at, src, n, hipMemcpyHostToDevice, s);
     };
@@ -1135,6 +1152,7 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
     const size_t h_n = (size_t)(rows * hid) * 4, r_n = (size_t)(rows * outw) * 4;
     const size_t enc_n = (size_t)(rows * (5 * d + F)) * 4;
     const size_t raw_n = (size_t)(rows_fut * a->output_embed.out) * 4;
+    const size_t planes_n = tsfm::proj_plane_bytes(rows, std::max({d, F, hid}), std::max({3 * d, F, hid, outw}));
     hipError_t e;
     if (enc.flags & TSFM_ATTN_DEVICE_PTRS) {
         bool ok = aligned(a->feats, 16) && aligned(a->fut_feats, 16) && aligned(a->reg, 16) && aligned(a->raw, 16) &&
@@ -1153,11 +1171,13 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
         Plan plan;
         const size_t x_at = plan.take(x_n), kv_at = plan.take(kv_n), emb_at = plan.take(emb_n), h_at = plan.take(h_n),
                      r_at = plan.take(r_n), enc_at = plan.take(enc_n), part_at = plan.take(tsfm::kSplitWorkspaceBytes);
+        const size_t planes_at = plan.take(planes_n);
         char* scratch = nullptr;
         bool owned = false;
         if ((e = tsfm::abi::scratch_acquire(s, tsfm::abi::kSlotChronos2Forward, plan.off, &scratch, &owned)) != hipSuccess)
             return hip_fail(e, "forward scratch allocation");
         tsfm::SplitWorkspace ws(reinterpret_cast<float*>(scratch + part_at));
+        tsfm::PlaneWorkspace pws(scratch + planes_at, planes_n);
         e = forward_on(a, enc, a->feats, a->fut_feats, a->ctx_valid, a->reg, a->raw,
                        reinterpret_cast<float*>(scratch + x_at), reinterpret_cast<uint8_t*>(scratch + kv_at),
                        reinterpret_cast<float*>(scratch + emb_at), reinterpret_cast<float*>(scratch + h_at),
@@ -1198,11 +1218,13 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
     const size_t x_at = st.add(nullptr, x_n), kv_at = st.add(nullptr, kv_n), emb_at = st.add(nullptr, emb_n);
     const size_t h_at = st.add(nullptr, h_n), r_at = st.add(nullptr, r_n), enc_at = st.add(nullptr, enc_n);
     const size_t raw_at = st.add(nullptr, raw_n), part_at = st.add(nullptr, tsfm::kSplitWorkspaceBytes);
+    const size_t planes_at = st.add(nullptr, planes_n);
     rc = ensure_buf(ctx, st.plan.off);
     if (rc != TSFM_OK) return rc;
     char* base = static_cast<char*>(ctx->buf);
     hipStream_t s = ctx->stream;
     tsfm::SplitWorkspace ws(reinterpret_cast<float*>(base + part_at));
+    tsfm::PlaneWorkspace pws(base + planes_at, planes_n);
     if ((e = st.upload(base, s)) != hipSuccess) return hip_fail(e, "host-to-device copy");
     auto dp = [&](size_t at) { return reinterpret_cast<const float*>(base + at); };
     std::vector<tsfm_chronos2_layer> dev_layers((size_t)enc.n_layers);

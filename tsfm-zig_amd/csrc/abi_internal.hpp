@@ -34,7 +34,7 @@ struct Plan {
 
 // Scratch of the device-pointer entry points (abi.cpp): one slot per entry point.
 enum ScratchSlot { kSlotEncode, kSlotChronos2Forward, kSlotChronos2Forecast, kSlotBoltForward, kSlotBoltForecast,
-                   kSlotBoltHorizon, kSlotTimestralForecast };
+                   kSlotBoltHorizon, kSlotTimestralForecast, kSlotProject };
 // A buffer of at least `bytes` for work queued on `stream` by the calling thread, kept between
 // calls; *owned: a stream-ordered allocation instead, to be released with hipFreeAsync.
 hipError_t scratch_acquire(hipStream_t stream, int slot, size_t bytes, char** out, bool* owned);

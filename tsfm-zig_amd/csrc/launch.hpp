@@ -89,6 +89,8 @@ struct ProjParams {
     int32_t chunk;             // set by launch_proj: 16-wide reduction units per accumulation chunk
     int32_t splits, split_steps;  // set by launch_proj: reduction split over workgroups (small products)
     float* partial;               // set by launch_proj: [splits][tokens][width] partial sums
+    const void* xp;               // set by launch_proj: x and the weights pre-split into bf16 parts
+    const void* wp;               // (PlaneWorkspace), or null: the product splits its own tiles
     // Optional row norm of the finished product (one f32 output): norm_out = rmsNorm(y0, norm_scale,
     // norm_eps), the same arithmetic as launch_rms_norm; may be y0 itself.
     const float* norm_scale;
@@ -122,6 +124,24 @@ public:
 
 private:
     float* prev_;
+};
+
+// f32 products with d_in a multiple of 32 run on the bf16 matrix cores as three bf16 parts per
+// operand. With a PlaneWorkspace set, launch_proj splits x and the weights once per product into
+// that buffer (proj_plane_bytes of it) and the product reads the parts from there; without one (or
+// with one too small) the product splits its own tiles as it loads them. Both give the same bits.
+// Same rules of ownership and lifetime as SplitWorkspace.
+size_t proj_plane_bytes(int64_t tokens, int64_t d_in, int64_t n_cols);
+class PlaneWorkspace {
+public:
+    PlaneWorkspace(void* buf, size_t bytes);
+    ~PlaneWorkspace();
+    PlaneWorkspace(const PlaneWorkspace&) = delete;
+    PlaneWorkspace& operator=(const PlaneWorkspace&) = delete;
+
+private:
+    void* prev_;
+    size_t prev_bytes_;
 };
 
 // nn.rmsNorm over rows of dim floats (encoder.hip): dim a multiple of 4, rows 16-byte aligned.

@@ -473,6 +473,142 @@ qkv_proj_x3(ProjParams p) {
     proj_store<OUT, BIG>(p, tot, row0, n0w, wm, wq, lane);
 }
 
+// ---- pre-split operands -----------------------------------------------------------------------
+//
+// When the calling entry point provides a workspace (PlaneWorkspace), x and the weights are split
+// once per product by split_planes into the layout the matrix instruction reads, and qkv_proj_x3p
+// takes its tiles from there straight into LDS (buffer_load ... lds): no staging registers and no
+// VALU split inside the product, three LDS stages (DMA two steps ahead), one barrier per step.
+// Same split, same products in the same order as qkv_proj_x3, so the two give the same bits.
+//
+// Layout of a pre-split (rows x d_in) matrix, KC = d_in / 32: 1 KB chunks, one per (16-row block rb,
+// 32-index step kc, part pl), at ((rb KC + kc) 3 + pl) KB; in a chunk, lane l's 16 bytes (row
+// 16 rb + (l & 15), indices 32 kc + 8 (l >> 4) .. + 7, as bf16) at 16 l. Rows past the matrix are
+// zeros.
+constexpr int kPlaneChunk = 1024;
+struct SplitSrc {
+    const float* src[4];  // row r comes from src[r / per], row r % per
+    int64_t ld;
+    int32_t per, rows, kc;
+};
+__global__ __launch_bounds__(256) void split_planes(SplitSrc s, uint8_t* __restrict__ dst) {
+    const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // chunk (rb, kc)
+    const int lane = threadIdx.x & 63;
+    if (c >= (int64_t)((s.rows + 15) / 16) * s.kc) return;
+    const int rb = (int)(c / s.kc), kc = (int)(c - (int64_t)rb * s.kc);
+    const int row = rb * 16 + (lane & 15), k0 = kc * 32 + 8 * (lane >> 4);
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+    if (row < s.rows) {
+        const int sel = row / s.per;
+        const float* r = s.src[sel] + (int64_t)(row - sel * s.per) * s.ld + k0;
+        a = ld4(r);
+        b = ld4(r + 4);
+    }
+    u32x2 h0, m0, l0, h1, m1, l1;
+    split3(a, h0, m0, l0);
+    split3(b, h1, m1, l1);
+    uint8_t* const out = dst + c * 3 * kPlaneChunk + 16 * lane;
+    *reinterpret_cast<u32x4*>(out) = u32x4{h0[0], h0[1], h1[0], h1[1]};
+    *reinterpret_cast<u32x4*>(out + kPlaneChunk) = u32x4{m0[0], m0[1], m1[0], m1[1]};
+    *reinterpret_cast<u32x4*>(out + 2 * kPlaneChunk) = u32x4{l0[0], l0[1], l1[0], l1[1]};
+}
+
+template <int OUT, bool BIG>
+__global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_proj_x3p(ProjParams p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int T = tile_m<BIG>(), NT = threads<BIG>(), NB = BIG ? 4 : 2;
+    constexpr int PLANE = x3_plane<BIG>(), TILE = 3 * PLANE, STAGE = x3_stage<BIG>();
+    constexpr int RB = T / 16, NWAVE = NT / 64, PER = 6 * RB / NWAVE;  // chunks a wave loads per step
+    static_assert(PER * NWAVE == 6 * RB && PER == 6, "six 1 KB chunks per wave and step");
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tm, tn;
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int split = p.splits > 1 ? logical % p.splits : 0;  // this workgroup's share of the reduction
+    tile_of(p.splits > 1 ? logical / p.splits : logical, p.m_tiles, p.n_tiles, tm, tn);
+    const int n_cols = p.width * p.n_out;
+    const int row0 = p.m_base + tm * T;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)smem;
+
+    // The tile's row blocks of the pre-split weights (columns) and x (tokens), through descriptors
+    // that end with the matrix: blocks past it read as zeros (they feed only outputs not stored).
+    const int kc = p.d_in / X3_BK;
+    const int rbw = tn * RB, rbx = row0 / 16;
+    const int nw = max(0, min(RB, (n_cols + 15) / 16 - rbw)), nx = max(0, min(RB, (p.tokens + 15) / 16 - rbx));
+    const u32x4 wd = buf_desc(static_cast<const uint8_t*>(p.wp) + (int64_t)rbw * kc * 3 * kPlaneChunk,
+                              (uint32_t)((int64_t)nw * kc * 3 * kPlaneChunk));
+    const u32x4 xd = buf_desc(static_cast<const uint8_t*>(p.xp) + (int64_t)rbx * kc * 3 * kPlaneChunk,
+                              (uint32_t)((int64_t)nx * kc * 3 * kPlaneChunk));
+    // Step t into stage buf: chunk c = wave + NWAVE i of the step is (weights, then x) part pl of row
+    // block rb, landing where qkv_proj_x3 writes it.
+    auto issue = [&](int t, int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = wave + NWAVE * i, side = c / (3 * RB), rem = c - side * 3 * RB;
+            const int pl = rem / RB, rb = rem - pl * RB;
+            const uint32_t src = (uint32_t)(((rb * kc + t) * 3 + pl) * kPlaneChunk) + 16u * lane;
+            dma16(side ? xd : wd, lds0 + (uint32_t)(buf * STAGE + side * TILE + pl * PLANE + rb * kPlaneChunk), src,
+                  0u);
+        }
+    };
+
+    const int wm = BIG ? (wave & 3) : (wave & 1), wq = BIG ? (wave >> 2) : (wave >> 1);
+    auto cb = [&](int nb) { return BIG ? 4 * wq + nb : wq + 2 * nb; };
+    f32x4 tot[NB][2], chk[NB][2];
+#pragma unroll
+    for (int a = 0; a < NB; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) tot[a][b] = chk[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int t0 = p.splits > 1 ? split * (p.split_steps / 2) : 0;
+    const int steps = p.splits > 1 ? min(kc, t0 + p.split_steps / 2) : kc;
+    int cu = 0;  // units done in the running chunk
+    issue(t0, 0);
+    if (t0 + 1 < steps) issue(t0 + 1, 1);
+    for (int t = t0; t < steps; t++) {
+        // This wave's chunks of step t have landed (those of step t + 1 may still be in flight),
+        // then every wave's; every wave has also left step t - 1, whose stage step t + 2 reuses.
+        if (t + 1 < steps) asm volatile("s_waitcnt vmcnt(6)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + 2 < steps) issue(t + 2, (t + 2 - t0) % 3);
+        const uint32_t st = lds0 + (uint32_t)((t - t0) % 3) * STAGE;
+        u32x4 a[3][NB], b[3][2];
+#pragma unroll
+        for (int pl = 0; pl < 3; pl++) {
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+                a[pl][nb] = *(lds_u32x4_p)(uintptr_t)(st + pl * PLANE + cb(nb) * 1024 + lane * 16);
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+                b[pl][mb] = *(lds_u32x4_p)(uintptr_t)(st + TILE + pl * PLANE + (2 * wm + mb) * 1024 + lane * 16);
+        }
+        constexpr int kA[6] = {2, 0, 1, 1, 0, 0}, kB[6] = {0, 2, 1, 0, 1, 0};
+#pragma unroll
+        for (int j = 0; j < 6; j++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++) chk[nb][mb] = mfma_x3(a[kA[j]][nb], b[kB[j]][mb], chk[nb][mb]);
+        if (++cu == p.chunk || t == steps - 1) {  // the chunk is done: into the total, the next starts at zero
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++) {
+                    tot[nb][mb] += chk[nb][mb];
+                    chk[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            cu = 0;
+        }
+    }
+    const int n0w = tn * T + (BIG ? 64 * wq : 0);
+    if (n0w >= n_cols) return;
+    if (p.splits > 1) {
+        proj_partial<BIG>(p, tot, row0, n0w, wm, wq, lane, split);
+        return;
+    }
+    proj_store<OUT, BIG>(p, tot, row0, n0w, wm, wq, lane);
+}
+template <bool BIG> constexpr size_t x3p_lds() { return 3 * (size_t)x3_stage<BIG>(); }  // three stages
+
 // The epilogue of four summed columns c .. c + 3 (of all n_out outputs side by side) of token m:
 // alpha, and with one output bias, ReLU or residual; f32 store into the output the columns
 // belong to (width is a multiple of 4, so a group never straddles two outputs).
@@ -633,11 +769,26 @@ namespace {
 
 // The split-partials buffer of the calling thread's current library call (SplitWorkspace).
 thread_local float* t_split_ws = nullptr;
+// The pre-split operand buffer of the calling thread's current library call (PlaneWorkspace).
+thread_local void* t_plane_ws = nullptr;
+thread_local size_t t_plane_bytes = 0;
 
 }  // namespace
 
 SplitWorkspace::SplitWorkspace(float* buf) : prev_(t_split_ws) { t_split_ws = buf; }
 SplitWorkspace::~SplitWorkspace() { t_split_ws = prev_; }
+PlaneWorkspace::PlaneWorkspace(void* buf, size_t bytes) : prev_(t_plane_ws), prev_bytes_(t_plane_bytes) {
+    t_plane_ws = buf;
+    t_plane_bytes = buf != nullptr ? bytes : 0;
+}
+PlaneWorkspace::~PlaneWorkspace() {
+    t_plane_ws = prev_;
+    t_plane_bytes = prev_bytes_;
+}
+size_t proj_plane_bytes(int64_t tokens, int64_t d_in, int64_t n_cols) {
+    if (tokens <= 0 || d_in <= 0 || n_cols <= 0 || d_in % X3_BK) return 0;
+    return (size_t)((tokens + 15) / 16 + (n_cols + 15) / 16) * (size_t)(d_in / X3_BK) * 3 * kPlaneChunk;
+}
 
 namespace {
 
@@ -653,8 +804,12 @@ hipError_t launch_small(ProjParams p, hipStream_t stream) {
     const unsigned blocks = (unsigned)((int64_t)p.m_tiles * p.n_tiles);
     if (p.d_in % X3_BK == 0) {
         p.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
-        hipLaunchKernelGGL((qkv_proj_x3<OUT, false>), dim3(blocks), dim3(threads<false>()), (x3_lds<false>()), stream,
-                           p);
+        if (p.xp != nullptr)
+            hipLaunchKernelGGL((qkv_proj_x3p<OUT, false>), dim3(blocks), dim3(threads<false>()), (x3p_lds<false>()),
+                               stream, p);
+        else
+            hipLaunchKernelGGL((qkv_proj_x3<OUT, false>), dim3(blocks), dim3(threads<false>()), (x3_lds<false>()),
+                               stream, p);
     } else if (p.d_in % 32 == 0)
         hipLaunchKernelGGL((qkv_proj<OUT, 32, false>), dim3(blocks), dim3(threads<false>()), (proj_lds<32, false>()),
                            stream, p);
@@ -679,8 +834,12 @@ hipError_t launch_unsplit(ProjParams p, hipStream_t stream) {
         q.m_tiles = (int32_t)m_big;
         q.n_tiles = (int32_t)big_n;
         q.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
-        hipLaunchKernelGGL((qkv_proj_x3<OUT, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
-                           (x3_lds<true>()), stream, q);
+        if (q.xp != nullptr)
+            hipLaunchKernelGGL((qkv_proj_x3p<OUT, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
+                               (x3p_lds<true>()), stream, q);
+        else
+            hipLaunchKernelGGL((qkv_proj_x3<OUT, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
+                               (x3_lds<true>()), stream, q);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess || m_big * 128 >= p.tokens) return e;
         p.m_base = (int32_t)(m_big * 128);
@@ -777,6 +936,27 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
                                 p.tokens, p.width, p.norm_eps, stream);
         return e;
     }
+    // Pre-split operands when the entry point lent a large enough PlaneWorkspace.
+    p.xp = p.wp = nullptr;
+    const int64_t n_cols = (int64_t)p.width * p.n_out;
+    // Only products of at least 2^30 multiply-adds: the two split launches cost more than they save
+    // on smaller ones.
+    if (t_plane_ws != nullptr && p.d_in % X3_BK == 0 && (int64_t)p.tokens * n_cols * p.d_in >= ((int64_t)1 << 30)) {
+        if (proj_plane_bytes(p.tokens, p.d_in, n_cols) <= t_plane_bytes) {
+            const int kc = p.d_in / X3_BK;
+            uint8_t* const xp = static_cast<uint8_t*>(t_plane_ws);
+            uint8_t* const wp = xp + (size_t)((p.tokens + 15) / 16) * kc * 3 * kPlaneChunk;
+            SplitSrc sx = {{p.x, p.x, p.x, p.x}, p.x_tok, p.tokens, p.tokens, kc};
+            SplitSrc sw = {{p.w0, p.w1 ? p.w1 : p.w0, p.w2 ? p.w2 : p.w0, p.w3 ? p.w3 : p.w0}, p.w_ld, p.width,
+                           (int32_t)n_cols, kc};
+            const int64_t cx = (int64_t)((p.tokens + 15) / 16) * kc, cw = (n_cols + 15) / 16 * kc;
+            hipLaunchKernelGGL(split_planes, dim3((unsigned)((cx + 3) / 4)), dim3(256), 0, stream, sx, xp);
+            hipLaunchKernelGGL(split_planes, dim3((unsigned)((cw + 3) / 4)), dim3(256), 0, stream, sw, wp);
+            if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+            p.xp = xp;
+            p.wp = wp;
+        }
+    }
     // Small products (a few token tiles: the decoder's 16 rows, short encoders) leave most CUs idle
     // and each workgroup walks the whole reduction; split it over workgroups instead (16-wide
     // steps), with the partial tiles summed in a fixed order by proj_reduce.
@@ -794,8 +974,12 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         if (p.d_in % X3_BK == 0) {
             ProjParams q = p;
             q.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
-            hipLaunchKernelGGL((qkv_proj_x3<0, false>), dim3((unsigned)(blocks * p.splits)), dim3(threads<false>()),
-                               (x3_lds<false>()), stream, q);
+            if (q.xp != nullptr)
+                hipLaunchKernelGGL((qkv_proj_x3p<0, false>), dim3((unsigned)(blocks * p.splits)),
+                                   dim3(threads<false>()), (x3p_lds<false>()), stream, q);
+            else
+                hipLaunchKernelGGL((qkv_proj_x3<0, false>), dim3((unsigned)(blocks * p.splits)),
+                                   dim3(threads<false>()), (x3_lds<false>()), stream, q);
         } else {
             hipLaunchKernelGGL((qkv_proj<0, 16, false>), dim3((unsigned)(blocks * p.splits)), dim3(threads<false>()),
                                (proj_lds<16, false>()), stream, p);

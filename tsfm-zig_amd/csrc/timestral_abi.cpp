@@ -224,6 +224,8 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     const size_t at_qs = plan.take(R4 * per_shot * ps * q), at_fr = plan.take(R4 * per_shot * 2);
     const size_t at_mir = plan.take((size_t)R * a->horizon * q * 4);
     const size_t at_part = plan.take(tsfm::kSplitWorkspaceBytes);
+    const size_t planes_n = tsfm::proj_plane_bytes((int64_t)rows * sl_max, std::max(d, hid), std::max(3 * d, 2 * hid));
+    const size_t at_planes = plan.take(planes_n);
     const size_t at_kf = plan.take((size_t)rows * hpad * 4 + 4), at_kfm = plan.take((size_t)rows * hpad + 1);
     const size_t at_noasinh = plan.take((size_t)rows);
     char* buf = nullptr;
@@ -233,6 +235,7 @@ extern "C" int tsfm_timestral_forecast(const tsfm_timestral_forecast_args* a) {
     auto F = [&](size_t at) { return reinterpret_cast<float*>(buf + at); };
     auto U8 = [&](size_t at) { return reinterpret_cast<uint8_t*>(buf + at); };
     tsfm::SplitWorkspace ws(F(at_part));
+    tsfm::PlaneWorkspace pws(buf + at_planes, planes_n);
 
     float* ctx[2] = {F(at_ctx0), F(at_ctx1)};
     uint8_t* mask[2] = {U8(at_mk0), U8(at_mk1)};
