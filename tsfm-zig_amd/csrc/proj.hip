@@ -609,6 +609,101 @@ __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(
 }
 template <bool BIG> constexpr size_t x3p_lds() { return 3 * (size_t)x3_stage<BIG>(); }  // three stages
 
+// The widest tiles, for the largest pre-split products: 256 tokens x 128 columns per workgroup,
+// eight waves of 64 tokens x one 64-column head each (4 x 4 blocks of 16 x 16): per 32-index step
+// a wave reads 24 KB of operands for 96 matrix instructions, against 18 KB for 48 with 32-token
+// waves. Two LDS stages of 72 KB (DMA one step ahead). Same products, same order, same bits.
+constexpr int kWideM = 256;
+constexpr int kWideStage = 3 * (kWideM + 128) * X3_BK * 2;  // bytes: weights then x, three parts each
+template <int OUT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_proj_x3w(ProjParams p) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int RBW = 128 / 16, RBX = kWideM / 16, NCH = 3 * (RBW + RBX), PER = NCH / 8;
+    constexpr int PW = RBW * 1024, PX = RBX * 1024, XOFF = 3 * PW;  // part sizes, x offset (bytes)
+    static_assert(PER * 8 == NCH, "every wave loads PER chunks");
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tm, tn;
+    tile_of(xcd_remap(blockIdx.x, gridDim.x), p.m_tiles, p.n_tiles, tm, tn);
+    const int n_cols = p.width * p.n_out;
+    const int row0 = p.m_base + tm * kWideM;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)smem;
+    const int kc = p.d_in / X3_BK;
+    const int rbw = tn * RBW, rbx = row0 / 16;
+    const int nw = max(0, min(RBW, (n_cols + 15) / 16 - rbw)), nx = max(0, min(RBX, (p.tokens + 15) / 16 - rbx));
+    const u32x4 wd = buf_desc(static_cast<const uint8_t*>(p.wp) + (int64_t)rbw * kc * 3 * kPlaneChunk,
+                              (uint32_t)((int64_t)nw * kc * 3 * kPlaneChunk));
+    const u32x4 xd = buf_desc(static_cast<const uint8_t*>(p.xp) + (int64_t)rbx * kc * 3 * kPlaneChunk,
+                              (uint32_t)((int64_t)nx * kc * 3 * kPlaneChunk));
+    // Step t into stage buf: chunk c = wave + 8 i is weight part c / RBW, block c % RBW (c < 3 RBW),
+    // else x part, block of c - 3 RBW.
+    auto issue = [&](int t, int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = wave + 8 * i;
+            const bool is_x = c >= 3 * RBW;
+            const int e = is_x ? c - 3 * RBW : c, per = is_x ? RBX : RBW;
+            const int pl = e / per, rb = e - pl * per;
+            const uint32_t src = (uint32_t)(((rb * kc + t) * 3 + pl) * kPlaneChunk) + 16u * lane;
+            const uint32_t dst = (uint32_t)(buf * kWideStage + (is_x ? XOFF + pl * PX : pl * PW) + rb * kPlaneChunk);
+            dma16(is_x ? xd : wd, lds0 + dst, src, 0u);
+        }
+    };
+
+    const int wm = wave & 3, wq = wave >> 2;  // tokens 64 wm .. + 63, head wq of the tile
+    f32x4 tot[4][4], chk[4][4];  // [column block nb][token block mb]
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) tot[a][b] = chk[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int cu = 0;  // units done in the running chunk
+    issue(0, 0);
+    for (int t = 0; t < kc; t++) {
+        // This step's chunks have landed, for this wave and then every wave; every wave has left
+        // step t - 1, whose stage step t + 1 reuses.
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + 1 < kc) issue(t + 1, (t + 1) & 1);
+        const uint32_t st = lds0 + (uint32_t)(t & 1) * kWideStage;
+        u32x4 a[3][4], b[3][4];
+#pragma unroll
+        for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                a[pl][k] = *(lds_u32x4_p)(uintptr_t)(st + pl * PW + (4 * wq + k) * 1024 + lane * 16);
+                b[pl][k] = *(lds_u32x4_p)(uintptr_t)(st + XOFF + pl * PX + (4 * wm + k) * 1024 + lane * 16);
+            }
+        constexpr int kA[6] = {2, 0, 1, 1, 0, 0}, kB[6] = {0, 2, 1, 0, 1, 0};
+#pragma unroll
+        for (int j = 0; j < 6; j++)
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++) chk[nb][mb] = mfma_x3(a[kA[j]][nb], b[kB[j]][mb], chk[nb][mb]);
+        if (++cu == p.chunk || t == kc - 1) {  // the chunk is done: into the total, the next starts at zero
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++) {
+                    tot[nb][mb] += chk[nb][mb];
+                    chk[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            cu = 0;
+        }
+    }
+    const int n0w = tn * 128 + 64 * wq;
+    if (n0w >= n_cols) return;
+    // Token blocks (0, 1) and (2, 3) are the 32-token rows 2 wm and 2 wm + 1 of proj_store's layout.
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+        f32x4 s2[4][2];
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            s2[nb][0] = tot[nb][2 * h2];
+            s2[nb][1] = tot[nb][2 * h2 + 1];
+        }
+        proj_store<OUT, true>(p, s2, row0, n0w, 2 * wm + h2, wq, lane);
+    }
+}
+
 // The epilogue of four summed columns c .. c + 3 (of all n_out outputs side by side) of token m:
 // alpha, and with one output bias, ReLU or residual; f32 store into the output the columns
 // belong to (width is a multiple of 4, so a group never straddles two outputs).
@@ -821,8 +916,27 @@ hipError_t launch_small(ProjParams p, hipStream_t stream) {
 
 template <int OUT>
 hipError_t launch_unsplit(ProjParams p, hipStream_t stream) {
-    const int64_t big_m = (p.tokens + 127) / 128, big_n = (p.width * p.n_out + 127) / 128;
+    // The token rows from p.m_base on (0 at the first call).
+    const int64_t rows = (int64_t)p.tokens - p.m_base;
+    const int64_t big_m = (rows + 127) / 128, big_n = (p.width * p.n_out + 127) / 128;
     if (big_m * big_n < kBigTilesMin) return launch_small<OUT>(p, stream);
+    if (p.d_in % X3_BK == 0 && p.xp != nullptr && p.splits <= 1 && p.m_base == 0) {
+        // Pre-split operands: 256 x 128 tiles, one workgroup per CU, in whole rounds; the token rows
+        // past them go to 128 x 128 / 64 x 64 tiles below.
+        const int64_t wide_m = rows / kWideM, slots = (int64_t)device_cus();
+        const int64_t m_wide = slots > 0 ? (wide_m * big_n - (wide_m * big_n) % slots) / big_n : 0;
+        if (m_wide > 0) {
+            ProjParams q = p;
+            q.m_tiles = (int32_t)m_wide;
+            q.n_tiles = (int32_t)big_n;
+            q.chunk = std::max(1, (p.chunk + 1) / 2);  // units of 32 indices
+            hipLaunchKernelGGL((qkv_proj_x3w<OUT>), dim3((unsigned)(m_wide * big_n)), dim3(512),
+                               (size_t)(2 * kWideStage), stream, q);
+            if (const hipError_t e = hipGetLastError(); e != hipSuccess || m_wide * kWideM >= rows) return e;
+            p.m_base = (int32_t)(m_wide * kWideM);
+            return launch_unsplit<OUT>(p, stream);
+        }
+    }
     if (p.d_in % X3_BK == 0) {
         // The bf16 three-way split, one workgroup per CU: the token tiles past the full rounds go
         // to SMALL tiles when the last round would be less than half full, as below.
@@ -841,8 +955,8 @@ hipError_t launch_unsplit(ProjParams p, hipStream_t stream) {
             hipLaunchKernelGGL((qkv_proj_x3<OUT, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
                                (x3_lds<true>()), stream, q);
         const hipError_t e = hipGetLastError();
-        if (e != hipSuccess || m_big * 128 >= p.tokens) return e;
-        p.m_base = (int32_t)(m_big * 128);
+        if (e != hipSuccess || m_big * 128 >= rows) return e;
+        p.m_base += (int32_t)(m_big * 128);
         return launch_small<OUT>(p, stream);
     }
     // BIG tiles run two per CU, in rounds that each take one tile's time. A last round less than
@@ -859,8 +973,8 @@ hipError_t launch_unsplit(ProjParams p, hipStream_t stream) {
     hipLaunchKernelGGL((qkv_proj<OUT, 16, true>), dim3((unsigned)(m_big * big_n)), dim3(threads<true>()),
                        (proj_lds<16, true>()), stream, p);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || m_big * 128 >= p.tokens) return e;
-    p.m_base = (int32_t)(m_big * 128);
+    if (e != hipSuccess || m_big * 128 >= rows) return e;
+    p.m_base += (int32_t)(m_big * 128);
     return launch_small<OUT>(p, stream);
 }
 
