@@ -854,12 +854,14 @@ namespace {
 // One nn.linear on the matrix cores: y = x w^T over rows tokens, with an optional ReLU or residual
 // (y = resid + x w^T) epilogue.
 hipError_t linear_on(const float* x, int64_t x_tok, const float* w, int out, int in, float* y, int64_t y_tok,
-                     int rows, int epi, const float* resid, hipStream_t s, const float* bias = nullptr) {
+                     int rows, int epi, const float* resid, hipStream_t s, const float* bias = nullptr,
+                     const void* x_pre = nullptr, void* y_planes = nullptr) {
     tsfm::ProjParams p{};
     p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi; p.bias = bias;
     p.resid = resid; p.resid_tok = y_tok;
     p.y0 = y; p.y0_tok = y_tok;
     p.tokens = rows; p.seq = rows; p.d_in = in; p.width = out; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
+    p.x_pre = x_pre; p.y_planes = y_planes;
     return tsfm::launch_proj(p, s);
 }
 
@@ -890,6 +892,13 @@ hipError_t linear_norm_on(const float* x, int64_t x_tok, const float* w, int out
 }
 
 // The layer loop on device buffers. scratch: xn, q, k, v, ab (rows x d each), then h (rows x d_ff).
+// encode_on's scratch: x_norm, q, k, v, the attention output and the MLP hidden rows in f32, then
+// the pre-split x_norm, group values and MLP hidden rows of the fused path.
+size_t encode_scratch_bytes(int64_t rows, int64_t d, int64_t F) {
+    return (size_t)(rows * (5 * d + F)) * 4 + 2 * tsfm::plane_operand_bytes(rows, d) +
+           tsfm::plane_operand_bytes(rows, F);
+}
+
 hipError_t encode_on(const tsfm_chronos2_encode_args* a, float* x, const uint8_t* kv, const float* cs,
                      const float* sn, const tsfm_chronos2_layer* layers, const float* final_norm, float* scratch,
                      hipStream_t s) {
@@ -901,17 +910,32 @@ hipError_t encode_on(const tsfm_chronos2_encode_args* a, float* x, const uint8_t
     float* ab = v + rows * d;
     float* h = ab + rows * d;
     const int R = (int)rows, D = (int)d, F = a->d_ff;
+    // With a PlaneWorkspace for these products, the row norms and the group-value and MLP-input
+    // products write their results split into bf16 parts (after the f32 scratch,
+    // encode_scratch_bytes), and the products after them read those parts directly: no f32 round
+    // trip and no separate split for x.
+    const bool fused = d % 32 == 0 && F % 32 == 0 && tsfm::proj_planes_ready(rows, d, d) &&
+                       tsfm::proj_planes_ready(rows, d, F) && tsfm::proj_planes_ready(rows, F, d);
+    char* const pl = reinterpret_cast<char*>(h + rows * F);
+    void* const xn_pl = pl;
+    void* const v_pl = pl + tsfm::plane_operand_bytes(rows, d);
+    void* const h_pl = pl + 2 * tsfm::plane_operand_bytes(rows, d);
+    auto norm = [&](const float* scale) {
+        return fused ? tsfm::launch_rms_norm_planes(x, d, xn_pl, scale, R, D, a->eps, s)
+                     : tsfm::launch_rms_norm(x, d, xn, d, scale, R, D, a->eps, s);
+    };
     hipError_t e = hipSuccess;
     for (int l = 0; l < a->n_layers && e == hipSuccess; l++) {
         const tsfm_chronos2_layer& ly = layers[l];
         // time attention
-        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.time_norm, R, D, a->eps, s)) != hipSuccess) break;
+        if ((e = norm(ly.time_norm)) != hipSuccess) break;
         tsfm::ProjParams p{};
         p.x = xn; p.x_tok = d; p.w0 = ly.time_q; p.w1 = ly.time_k; p.w2 = ly.time_v; p.w_ld = d;
         p.alpha = 1.f; p.epi = tsfm::kEpiNone;
         p.y0 = q; p.y1 = k; p.y2 = v; p.y0_tok = p.y1_tok = p.y2_tok = d;
         p.rope_cos = cs; p.rope_sin = sn;
         p.tokens = R; p.seq = a->seq; p.d_in = D; p.width = D; p.n_out = 3; p.out_dtype = TSFM_DTYPE_F32;
+        p.x_pre = fused ? xn_pl : nullptr;
         if ((e = tsfm::launch_proj(p, s)) != hipSuccess) break;
         tsfm::Params ap{};
         ap.q = q; ap.k = k; ap.v = v; ap.o = ab;
@@ -923,13 +947,21 @@ hipError_t encode_on(const tsfm_chronos2_encode_args* a, float* x, const uint8_t
         if ((e = tsfm::launch_attn_f32(ap, mask, tsfm::BIAS_NONE, false, s)) != hipSuccess) break;
         if ((e = linear_on(ab, d, ly.time_o, D, D, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
         // group attention with singleton groups
-        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.group_norm, R, D, a->eps, s)) != hipSuccess) break;
-        if ((e = linear_on(xn, d, ly.group_v, D, D, v, d, R, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_on(v, d, ly.group_o, D, D, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+        if ((e = norm(ly.group_norm)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.group_v, D, D, v, d, R, tsfm::kEpiNone, nullptr, s, nullptr,
+                           fused ? xn_pl : nullptr, fused ? v_pl : nullptr)) != hipSuccess)
+            break;
+        if ((e = linear_on(v, d, ly.group_o, D, D, x, d, R, tsfm::kEpiResidual, x, s, nullptr,
+                           fused ? v_pl : nullptr)) != hipSuccess)
+            break;
         // MLP
-        if ((e = tsfm::launch_rms_norm(x, d, xn, d, ly.mlp_norm, R, D, a->eps, s)) != hipSuccess) break;
-        if ((e = linear_on(xn, d, ly.mlp_wi, F, D, h, F, R, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_on(h, F, ly.mlp_wo, D, F, x, d, R, tsfm::kEpiResidual, x, s)) != hipSuccess) break;
+        if ((e = norm(ly.mlp_norm)) != hipSuccess) break;
+        if ((e = linear_on(xn, d, ly.mlp_wi, F, D, h, F, R, tsfm::kEpiRelu, nullptr, s, nullptr,
+                           fused ? xn_pl : nullptr, fused ? h_pl : nullptr)) != hipSuccess)
+            break;
+        if ((e = linear_on(h, F, ly.mlp_wo, D, F, x, d, R, tsfm::kEpiResidual, x, s, nullptr,
+                           fused ? h_pl : nullptr)) != hipSuccess)
+            break;
     }
     if (e == hipSuccess) e = tsfm::launch_rms_norm(x, d, x, d, final_norm, R, D, a->eps, s);
     return e;
@@ -960,7 +992,7 @@ int tsfm_chronos2_encode(const tsfm_chronos2_encode_args* a) {
     if (rows > 0x7fffffff / 4) return fail(TSFM_E_UNSUPPORTED, "too many tokens");
     int rc = ensure_ready();
     if (rc != TSFM_OK) return rc;
-    const size_t scratch_n = (size_t)(rows * (5 * d + F)) * 4;
+    const size_t scratch_n = encode_scratch_bytes(rows, d, F);
     const size_t planes_n = tsfm::proj_plane_bytes(rows, std::max(d, F), std::max(3 * d, F));
     hipError_t e;
     if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
@@ -1150,7 +1182,7 @@ int tsfm_chronos2_forward(const tsfm_chronos2_forward_args* a) {
     const int64_t outw = std::max<int64_t>(d, a->output_embed.out);
     const size_t x_n = (size_t)(rows * d) * 4, kv_n = (size_t)rows, emb_n = (size_t)(rows * d) * 4;
     const size_t h_n = (size_t)(rows * hid) * 4, r_n = (size_t)(rows * outw) * 4;
-    const size_t enc_n = (size_t)(rows * (5 * d + F)) * 4;
+    const size_t enc_n = encode_scratch_bytes(rows, d, F);
     const size_t raw_n = (size_t)(rows_fut * a->output_embed.out) * 4;
     const size_t planes_n = tsfm::proj_plane_bytes(rows, std::max({d, F, hid}), std::max({3 * d, F, hid, outw}));
     hipError_t e;

@@ -91,6 +91,11 @@ struct ProjParams {
     float* partial;               // set by launch_proj: [splits][tokens][width] partial sums
     const void* xp;               // set by launch_proj: x and the weights pre-split into bf16 parts
     const void* wp;               // (PlaneWorkspace), or null: the product splits its own tiles
+    // Optional, for products that pass proj_planes_ready: x already split by its producer
+    // (launch_rms_norm_planes or another product's y_planes; x is then not read), and / or the
+    // result written split (one f32 output, width a multiple of 32, no RoPE) instead of into y0.
+    const void* x_pre;
+    void* y_planes;
     // Optional row norm of the finished product (one f32 output): norm_out = rmsNorm(y0, norm_scale,
     // norm_eps), the same arithmetic as launch_rms_norm; may be y0 itself.
     const float* norm_scale;
@@ -132,6 +137,16 @@ private:
 // with one too small) the product splits its own tiles as it loads them. Both give the same bits.
 // Same rules of ownership and lifetime as SplitWorkspace.
 size_t proj_plane_bytes(int64_t tokens, int64_t d_in, int64_t n_cols);
+// Bytes of one pre-split (rows x cols) operand (cols a multiple of 32), as launch_rms_norm_planes
+// and a product's y_planes write it.
+size_t plane_operand_bytes(int64_t rows, int64_t cols);
+// A product of this shape may take x_pre / y_planes: a PlaneWorkspace holds its weights' parts,
+// d_in is a multiple of 32 and the product is large enough to run on pre-split operands.
+bool proj_planes_ready(int64_t tokens, int64_t d_in, int64_t n_cols);
+// rmsNorm of rows (as launch_rms_norm, the same bits), written split into bf16 parts for a product
+// (dim a multiple of 32).
+hipError_t launch_rms_norm_planes(const float* x, int64_t x_tok, void* planes, const float* scale, int rows, int dim,
+                                  float eps, hipStream_t stream);
 class PlaneWorkspace {
 public:
     PlaneWorkspace(void* buf, size_t bytes);

@@ -95,6 +95,28 @@ __device__ __forceinline__ f32x4 epi_act(int epi, f32x4 v) {
 
 // OUT: element type of the outputs, TSFM_DTYPE_* (0 f32, 1 bf16, 2 f16); the products and RoPE
 // are f32 either way and the result is rounded once, to nearest even, when it is stored.
+// The bf16x3 products: reduction indices per step of their kernels, and the bytes of one chunk of
+// the pre-split operand layout (16 rows x 32 indices of one part, see split_planes).
+constexpr int X3_BK = 32;
+constexpr int kPlaneChunk = 1024;
+
+// a = hi + mid + lo as bf16 pairs (two values per word, the first in the low half).
+__device__ __forceinline__ void split3(f32x4 v, u32x2& hi, u32x2& mid, u32x2& lo) {
+#pragma clang fp contract(off)
+    auto widen = [](uint32_t w, int half) { return __uint_as_float(half ? (w & 0xffff0000u) : (w << 16)); };
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float a = v[2 * i], b = v[2 * i + 1];
+        const uint32_t h = pack2<true>(a, b);
+        const float ra = a - widen(h, 0), rb = b - widen(h, 1);
+        const uint32_t m = pack2<true>(ra, rb);
+        const float sa = ra - widen(m, 0), sb = rb - widen(m, 1);
+        hi[i] = h;
+        mid[i] = m;
+        lo[i] = pack2<true>(sa, sb);
+    }
+}
+
 // The stores of a wave's finished sums (not split): sum[nb][mb] holds columns cq(nb) .. + 3 of the
 // head at output column n0w (over all outputs) for token row0 + wm * 32 + mb * 16 + (lane & 15):
 // alpha, RoPE of q and k, then bias and ReLU / SiLU / residual (f32) or the rounding (bf16, f16).
@@ -137,6 +159,20 @@ __device__ __forceinline__ void proj_store(const ProjParams& p, f32x4 (&sum)[BIG
                 if (p.bias != nullptr) v = v + ld4(p.bias + col + cq(nb));  // nn.linear's bias (linearCols, nn.zig:254)
                 if (p.epi == kEpiResidual) v = ld4(res + cq(nb)) + v;  // x + delta, one rounding
                 else v = epi_act(p.epi, v);
+                if (p.y_planes != nullptr) {
+                    // Columns c .. c + 3 of row m in the pre-split layout of a (tokens x width)
+                    // operand: chunk (m / 16, c / 32), lane 16 ((c % 32) / 8) + m % 16, bytes 2 (c % 8).
+                    const int c = col + cq(nb), kcw = p.width / X3_BK;
+                    u32x2 hp, mp, lp;
+                    split3(v, hp, mp, lp);
+                    uint8_t* const q = static_cast<uint8_t*>(p.y_planes) +
+                                       ((int64_t)(m >> 4) * kcw + c / X3_BK) * 3 * kPlaneChunk +
+                                       (16 * ((c % X3_BK) >> 3) + (m & 15)) * 16 + 2 * (c & 7);
+                    *reinterpret_cast<u32x2*>(q) = hp;
+                    *reinterpret_cast<u32x2*>(q + kPlaneChunk) = mp;
+                    *reinterpret_cast<u32x2*>(q + 2 * kPlaneChunk) = lp;
+                    continue;
+                }
                 st4(out + cq(nb), v);
             }
         } else {
@@ -320,7 +356,6 @@ __global__ __launch_bounds__(threads<BIG>()) __attribute__((amdgpu_waves_per_eu(
 // and write the three bf16 planes into the other LDS stage in the matrix instruction's operand
 // order: per 16 rows x 32 indices, lane l's 16 bytes (row l & 15, indices 8 (l >> 4) .. + 7) at 16 l.
 // 48 KB per stage, two stages: one workgroup (8 waves) per CU.
-constexpr int X3_BK = 32;  // reduction indices per step
 // Per tile shape: the bytes of one bf16 plane of one tile (rows x 32 indices x 2 bytes), the three
 // planes of a tile, a stage (weight tile, then x tile), and both stages.
 template <bool BIG> constexpr int x3_plane() { return tile_m<BIG>() * X3_BK * 2; }
@@ -329,23 +364,6 @@ template <bool BIG> constexpr size_t x3_lds() { return 2 * (size_t)x3_stage<BIG>
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) u32x4* lds_u32x4_p;
 typedef __attribute__((address_space(3))) u32x2* lds_u32x2_p;
-
-// a = hi + mid + lo as bf16 pairs (two values per word, the first in the low half).
-__device__ __forceinline__ void split3(f32x4 v, u32x2& hi, u32x2& mid, u32x2& lo) {
-#pragma clang fp contract(off)
-    auto widen = [](uint32_t w, int half) { return __uint_as_float(half ? (w & 0xffff0000u) : (w << 16)); };
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const float a = v[2 * i], b = v[2 * i + 1];
-        const uint32_t h = pack2<true>(a, b);
-        const float ra = a - widen(h, 0), rb = b - widen(h, 1);
-        const uint32_t m = pack2<true>(ra, rb);
-        const float sa = ra - widen(m, 0), sb = rb - widen(m, 1);
-        hi[i] = h;
-        mid[i] = m;
-        lo[i] = pack2<true>(sa, sb);
-    }
-}
 
 __device__ __forceinline__ f32x4 mfma_x3(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c, 0,
@@ -485,7 +503,6 @@ qkv_proj_x3(ProjParams p) {
 // 32-index step kc, part pl), at ((rb KC + kc) 3 + pl) KB; in a chunk, lane l's 16 bytes (row
 // 16 rb + (l & 15), indices 32 kc + 8 (l >> 4) .. + 7, as bf16) at 16 l. Rows past the matrix are
 // zeros.
-constexpr int kPlaneChunk = 1024;
 struct SplitSrc {
     const float* src[4];  // row r comes from src[r / per], row r % per
     int64_t ld;
@@ -511,6 +528,44 @@ __global__ __launch_bounds__(256) void split_planes(SplitSrc s, uint8_t* __restr
     *reinterpret_cast<u32x4*>(out) = u32x4{h0[0], h0[1], h1[0], h1[1]};
     *reinterpret_cast<u32x4*>(out + kPlaneChunk) = u32x4{m0[0], m0[1], m1[0], m1[1]};
     *reinterpret_cast<u32x4*>(out + 2 * kPlaneChunk) = u32x4{l0[0], l0[1], l1[0], l1[1]};
+}
+
+// rmsNorm of 16 rows per workgroup into the pre-split layout: each wave reduces four rows with the
+// lane mapping of rms_norm_rows (so the norms are the same bits), then the workgroup writes the
+// rows' chunks, 1 KB per wave at a time.
+__global__ __launch_bounds__(256) void rms_norm_planes(const float* __restrict__ x, int64_t x_tok,
+                                                       uint8_t* __restrict__ dst, const float* __restrict__ scale,
+                                                       int rows, int dim, float eps) {
+    __shared__ float inv_s[16];
+    const int rb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * wave + i, row = rb * 16 + r;
+        if (row >= rows) continue;  // wave-uniform
+        const float* xr = x + (int64_t)row * x_tok;
+        float ss = 0.f;
+        for (int c = 4 * lane; c < dim; c += 256) ss = sumsq4(ss, ld4(xr + c));
+        const float inv = rms_inv(ss, dim, eps);
+        if (lane == 0) inv_s[r] = inv;
+    }
+    __syncthreads();
+    const int kc = dim / X3_BK, r = lane & 15, row = rb * 16 + r;
+    for (int k = wave; k < kc; k += 4) {
+        const int c0 = k * X3_BK + 8 * (lane >> 4);
+        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+        if (row < rows) {
+            const float* xr = x + (int64_t)row * x_tok + c0;
+            a = rms_apply(ld4(xr), inv_s[r], ld4(scale + c0));
+            b = rms_apply(ld4(xr + 4), inv_s[r], ld4(scale + c0 + 4));
+        }
+        u32x2 h0, m0, l0, h1, m1, l1;
+        split3(a, h0, m0, l0);
+        split3(b, h1, m1, l1);
+        uint8_t* const out = dst + ((int64_t)rb * kc + k) * 3 * kPlaneChunk + 16 * lane;
+        *reinterpret_cast<u32x4*>(out) = u32x4{h0[0], h0[1], h1[0], h1[1]};
+        *reinterpret_cast<u32x4*>(out + kPlaneChunk) = u32x4{m0[0], m0[1], m1[0], m1[1]};
+        *reinterpret_cast<u32x4*>(out + 2 * kPlaneChunk) = u32x4{l0[0], l0[1], l1[0], l1[1]};
+    }
 }
 
 template <int OUT, bool BIG>
@@ -884,6 +939,27 @@ size_t proj_plane_bytes(int64_t tokens, int64_t d_in, int64_t n_cols) {
     if (tokens <= 0 || d_in <= 0 || n_cols <= 0 || d_in % X3_BK) return 0;
     return (size_t)((tokens + 15) / 16 + (n_cols + 15) / 16) * (size_t)(d_in / X3_BK) * 3 * kPlaneChunk;
 }
+size_t plane_operand_bytes(int64_t rows, int64_t cols) {
+    if (rows <= 0 || cols <= 0 || cols % X3_BK) return 0;
+    return (size_t)((rows + 15) / 16) * (size_t)(cols / X3_BK) * 3 * kPlaneChunk;
+}
+// Products of at least 2^30 multiply-adds run on pre-split operands when a workspace is lent: the
+// split launches cost more than they save on smaller ones.
+static bool planes_pay(int64_t tokens, int64_t d_in, int64_t n_cols) {
+    return d_in % X3_BK == 0 && tokens * n_cols * d_in >= ((int64_t)1 << 30);
+}
+bool proj_planes_ready(int64_t tokens, int64_t d_in, int64_t n_cols) {
+    return t_plane_ws != nullptr && planes_pay(tokens, d_in, n_cols) &&
+           plane_operand_bytes(n_cols, d_in) <= t_plane_bytes;
+}
+hipError_t launch_rms_norm_planes(const float* x, int64_t x_tok, void* planes, const float* scale, int rows, int dim,
+                                  float eps, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (dim <= 0 || dim % X3_BK) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rms_norm_planes, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, x, x_tok,
+                       static_cast<uint8_t*>(planes), scale, rows, dim, eps);
+    return hipGetLastError();
+}
 
 namespace {
 
@@ -991,7 +1067,8 @@ static int proj_chunk(int units) {
 
 // Products the 16-token kernel takes (proj_skinny).
 static bool skinny(const ProjParams& p) {
-    return p.tokens <= kSkinnyTokens && p.d_in <= kSkinnyMaxIn && p.rope_cos == nullptr && p.out_dtype == 0;
+    return p.tokens <= kSkinnyTokens && p.d_in <= kSkinnyMaxIn && p.rope_cos == nullptr && p.out_dtype == 0 &&
+           p.x_pre == nullptr && p.y_planes == nullptr;
 }
 
 size_t proj_split_bytes(ProjParams& p) {
@@ -1002,6 +1079,7 @@ size_t proj_split_bytes(ProjParams& p) {
     p.splits = 1;
     p.split_steps = steps;
     p.partial = nullptr;
+    if (p.x_pre != nullptr || p.y_planes != nullptr) return 0;  // pre-split operands: never split
     // f32 outputs, no RoPE; several outputs only without an epilogue; at most half a launch of
     // tiles (four workgroups per CU), and at least 16 steps to share out.
     if (!((p.n_out == 1 || p.epi == kEpiNone) && p.rope_cos == nullptr && p.out_dtype == 0 && blocks < 512 &&
@@ -1050,24 +1128,31 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
                                 p.tokens, p.width, p.norm_eps, stream);
         return e;
     }
-    // Pre-split operands when the entry point lent a large enough PlaneWorkspace.
+    // Pre-split operands when the entry point lent a large enough PlaneWorkspace: the weights split
+    // into it, and x too unless its producer split it (x_pre). x_pre / y_planes need that path.
     p.xp = p.wp = nullptr;
     const int64_t n_cols = (int64_t)p.width * p.n_out;
-    // Only products of at least 2^30 multiply-adds: the two split launches cost more than they save
-    // on smaller ones.
-    if (t_plane_ws != nullptr && p.d_in % X3_BK == 0 && (int64_t)p.tokens * n_cols * p.d_in >= ((int64_t)1 << 30)) {
-        if (proj_plane_bytes(p.tokens, p.d_in, n_cols) <= t_plane_bytes) {
+    const bool fused = p.x_pre != nullptr || p.y_planes != nullptr;
+    if (fused && (!proj_planes_ready(p.tokens, p.d_in, n_cols) ||
+                  (p.y_planes != nullptr && (p.n_out != 1 || p.width % X3_BK || p.out_dtype != 0 || p.rope_cos != nullptr))))
+        return hipErrorInvalidValue;
+    if (t_plane_ws != nullptr && planes_pay(p.tokens, p.d_in, n_cols)) {
+        const size_t xb = p.x_pre != nullptr ? 0 : plane_operand_bytes(p.tokens, p.d_in);
+        if (xb + plane_operand_bytes(n_cols, p.d_in) <= t_plane_bytes) {
             const int kc = p.d_in / X3_BK;
             uint8_t* const xp = static_cast<uint8_t*>(t_plane_ws);
-            uint8_t* const wp = xp + (size_t)((p.tokens + 15) / 16) * kc * 3 * kPlaneChunk;
-            SplitSrc sx = {{p.x, p.x, p.x, p.x}, p.x_tok, p.tokens, p.tokens, kc};
+            uint8_t* const wp = xp + xb;
             SplitSrc sw = {{p.w0, p.w1 ? p.w1 : p.w0, p.w2 ? p.w2 : p.w0, p.w3 ? p.w3 : p.w0}, p.w_ld, p.width,
                            (int32_t)n_cols, kc};
-            const int64_t cx = (int64_t)((p.tokens + 15) / 16) * kc, cw = (n_cols + 15) / 16 * kc;
-            hipLaunchKernelGGL(split_planes, dim3((unsigned)((cx + 3) / 4)), dim3(256), 0, stream, sx, xp);
+            if (p.x_pre == nullptr) {
+                SplitSrc sx = {{p.x, p.x, p.x, p.x}, p.x_tok, p.tokens, p.tokens, kc};
+                const int64_t cx = (int64_t)((p.tokens + 15) / 16) * kc;
+                hipLaunchKernelGGL(split_planes, dim3((unsigned)((cx + 3) / 4)), dim3(256), 0, stream, sx, xp);
+            }
+            const int64_t cw = (n_cols + 15) / 16 * kc;
             hipLaunchKernelGGL(split_planes, dim3((unsigned)((cw + 3) / 4)), dim3(256), 0, stream, sw, wp);
             if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-            p.xp = xp;
+            p.xp = p.x_pre != nullptr ? p.x_pre : xp;
             p.wp = wp;
         }
     }
