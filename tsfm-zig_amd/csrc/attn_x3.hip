@@ -131,7 +131,10 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int kend = key_end_for<MASK>(wg_qhi, p.n_k, p.ctx_keys);
     const int wave_nq = max(0, min(XQ, p.n_q - wq0));
     const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys) : 0;
-    const int nchunks = (kend + XK - 1) / XK;
+    // Rows of 32k + 1 keys under the masks whose key range is the whole row: the last key on the VALU
+    // after the chunks (one dot product per query instead of a 32-key chunk of matrix work).
+    const bool tail_key = (MASK == FULL || MASK == KEYS_ADDITIVE || MASK == FULL_KEYS) && p.n_k % XK == 1 && p.n_k > 1;
+    const int nchunks = tail_key ? p.n_k / XK : (kend + XK - 1) / XK;
 
     const __amdgpu_buffer_rsrc_t kv_rsrc = make_buf(mask_reads_valid<MASK>() ? p.key_valid + b * p.kv_batch : p.key_valid,
                                                     mask_reads_valid<MASK>() ? valid_len<MASK>(p.n_k, p.ctx_keys) : 0);
@@ -237,6 +240,29 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
     if (BIAS == BIAS_REL) fill_rel_lut(lut_raw, p, h, tid, nt);
+    // The tail key's K row (rotated, as the staged rows are) and V row, and its key term.
+    __shared__ __attribute__((aligned(16))) float ktail[kHeadDim], vtail[kHeadDim];
+    __shared__ float tail_add;
+    if (tail_key && tid < kHeadDim) {
+        const int kt = p.n_k - 1;
+        if (tid < 32) {
+#pragma clang fp contract(off)
+            float x1 = K[(int64_t)kt * p.k_tok + tid], x2 = K[(int64_t)kt * p.k_tok + tid + 32];
+            if (ROPE) {  // nn.ropeHalf, src/core/nn.zig:453-460
+                const float c = RC[(int64_t)kt * 32 + tid], sn = RS[(int64_t)kt * 32 + tid];
+                const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
+                x1 = y1;
+                x2 = y2;
+            }
+            ktail[tid] = x1;
+            ktail[tid + 32] = x2;
+        }
+        vtail[tid] = V[(int64_t)kt * p.v_tok + tid];
+        if (tid == 0) {
+            const bool valid = mask_reads_valid<MASK>() ? p.key_valid[b * p.kv_batch + kt] != 0 : true;
+            tail_add = key_term<MASK>(kt, p.n_k, valid, p.ctx_keys);
+        }
+    }
     store_chunk(stage[0], 0);
     __syncthreads();
 
@@ -245,6 +271,38 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int qpos = p.q_pos0 + qi;
     const int qc = min(qi, p.n_q - 1);  // the T5 row of a query slot past n_q (its scores are dropped)
     const int kx = ql & 7, vx = (ql >> 2) & 3;
+
+    // Online update for a new score max mc of the lane's query: the weights' reference max m trails
+    // the running max by at most kSlack, so a max that stays within it leaves m, ml, l and O as they
+    // are (weights up to 2^8; the normalised result is the same) and O is rescaled in few chunks.
+    // Returns the shift and the exp2-unit max the weights are formed against; shifted: some lane
+    // of the wave needs the shift.
+    auto update = [&](float mc, float& shift, float& mlw, bool& shifted) {
+#pragma clang fp contract(off)
+        shift = 0.f;
+        mlw = ml;
+        shifted = false;
+        if (__ballot(!(m > -1e30f && mc <= m + kSlack)) != 0) {
+            const float m_new = fmaxf(m, mc);
+            const float m_use = m_new == kNegInf ? 0.f : m_new;
+            // As the f32 path: e = exp2(x log2e - m log2e) with ml = m log2e rounded once; a row whose
+            // max is still an additively masked score (about -FLT_MAX) takes exp2((x - m) log2e),
+            // which gives it the reference's uniform weights (src/core/nn.zig:470-505 on scores +
+            // (-floatMax)).
+            const bool big = m_use < -1e30f;
+            shift = big ? m_use : 0.f;
+            mlw = big ? 0.f : m_use * kLog2e;
+            const float alpha = __builtin_amdgcn_exp2f(big ? (m - m_use) * kLog2e : ml - mlw);
+            ml = (big || m_new == kNegInf) ? kNegInf : mlw;
+            l = l * alpha;
+            m = m_new;
+            shifted = __ballot(big) != 0;
+            if (__ballot(alpha != 1.f) != 0) {
+                o[0] *= alpha;
+                o[1] *= alpha;
+            }
+        }
+    };
 
     for (int t = 0; t < nchunks; t++) {
         const int kbase = t * XK;
@@ -300,32 +358,9 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         mloc = fmaxf(mloc, v);
                     }
                 }
-                // The weights' reference max m trails the running max by at most kSlack: a chunk whose
-                // max stays within it leaves m, ml, l and O as they are (weights up to 2^8), which
-                // saves the rescale of O in most chunks; the normalised result is the same.
-                const float mc = pair_max(mloc);
-                float shift = 0.f, mlw = ml;
-                bool shifted = false;
-                if (__ballot(!(m > -1e30f && mc <= m + kSlack)) != 0) {
-                    const float m_new = fmaxf(m, mc);
-                    const float m_use = m_new == kNegInf ? 0.f : m_new;
-                    // As the f32 path: e = exp2(x log2e - m log2e) with ml = m log2e rounded once; a
-                    // row whose max is still an additively masked score (about -FLT_MAX) takes
-                    // exp2((x - m) log2e), which gives it the reference's uniform weights
-                    // (src/core/nn.zig:470-505 on scores + (-floatMax)).
-                    const bool big = m_use < -1e30f;
-                    shift = big ? m_use : 0.f;
-                    mlw = big ? 0.f : m_use * kLog2e;
-                    const float alpha = __builtin_amdgcn_exp2f(big ? (m - m_use) * kLog2e : ml - mlw);
-                    ml = (big || m_new == kNegInf) ? kNegInf : mlw;
-                    l = l * alpha;
-                    m = m_new;
-                    shifted = __ballot(big) != 0;
-                    if (__ballot(alpha != 1.f) != 0) {
-                        o[0] *= alpha;
-                        o[1] *= alpha;
-                    }
-                }
+                float shift, mlw;
+                bool shifted;
+                update(pair_max(mloc), shift, mlw, shifted);
                 float lsum = 0.f;
                 if (!shifted) {
 #pragma unroll
@@ -378,6 +413,41 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     // ---- normalise and store: lane (ql, hh) holds dims 32db + 8g + 4hh .. +3 of query qi ----
+    if (tail_key && wave_nq > 0) {
+#pragma clang fp contract(off)
+        // The lane's 32 dims of its query, exactly, from the three parts (hi + mid, then lo), and
+        // their share of the dot product with the tail key; the pair of lanes adds the halves.
+        auto part = [](uint32_t w, int half) { return __uint_as_float(half ? (w & 0xffff0000u) : (w << 16)); };
+        float acc = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const f32x4 k0 = ld4(ktail + 16 * s + 8 * hh), k1 = ld4(ktail + 16 * s + 8 * hh + 4);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int w = j >> 1, hf = j & 1;
+                const float qv = (part(qf[0][s][w], hf) + part(qf[1][s][w], hf)) + part(qf[2][s][w], hf);
+                acc = __builtin_fmaf(qv, j < 4 ? k0[j] : k1[j - 4], acc);
+            }
+        }
+        const int key = p.n_k - 1;
+        float x = pair_sum(acc);
+        if (BIAS == BIAS_REL) x = x + lut[key - qc + p.n_q - 1];
+        if (BIAS == BIAS_DENSE && qi < p.n_q) x = x + p.bias[h * p.bias_head + (int64_t)qi * p.bias_row + key];
+        x = masked<MASK>(x, tail_add, key, qpos, p.n_k, p.chain_start);
+        float shift, mlw;
+        bool shifted;
+        update(x, shift, mlw, shifted);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x - shift, kLog2e, -mlw));
+        l = l + (hh == 0 ? e : 0.f);  // the pair shares one key
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const f32x4 v4 = ld4(vtail + 32 * db + 8 * g4 + 4 * hh);
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[db][4 * g4 + i] = __builtin_fmaf(e, v4[i], o[db][4 * g4 + i]);
+            }
+    }
     const float lt = pair_sum(l);
     if (qi >= p.n_q || wave_nq == 0) return;
     const float inv = 1.0f / lt;
