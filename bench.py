@@ -210,7 +210,7 @@ def run_bolt(torch, ta, workloads, peak):
     config = {"workload": w.name, "B": w.B, "H": w.H, "L": L, "D": 64, "mask": "keys_additive", "bias": "t5 32/128",
               "scale": 1.0, "layout": "(B, L, H*D) f32"}
     return Bench(w, step, lambda: o.cpu().numpy(), cpu_leg, config, "f32", "mfma", peak["f32_mfma_tflops"],
-                 "TFLOP/s", w.B)
+                 "TFLOP/s", w.B, x3=True)
 
 
 def run_prefill(torch, ta, workloads, peak):

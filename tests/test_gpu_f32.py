@@ -73,6 +73,59 @@ def test_masks_match_oracle(ta, orc, gpu_ready, mask, n):
     assert _ref.scaled_err(got, want) <= TOL
 
 
+@pytest.mark.parametrize("mask", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("n", [161, 257])
+def test_single_trailing_query_and_key_match_oracle(ta, orc, gpu_ready, mask, n):
+    """n = 32k + 1 with one workgroup per (series, head) in the bf16x3 kernel: the last query runs on
+    the VALU at the end of the workgroup (each wave a slice of its keys, merged through LDS), and for
+    the non-causal masks the last key runs on the VALU after the 32-key chunks."""
+    B, H = 2, 3
+    q, k, v, kv = _inputs(300 + n + 7 * mask, B, H, n, n)
+    got = run_generic(ta, mask, q, k, v, kv, B, H, n, n, 0.125)
+    want = oracle_generic(orc, mask, q, k, v, kv, B, H, n, 0.125)
+    assert _ref.scaled_err(got, want) <= TOL
+
+
+@pytest.mark.parametrize("mask", [1, 3])
+def test_single_trailing_query_with_dense_bias(ta, orc, gpu_ready, mask):
+    B, H, n = 2, 2, 161
+    q, k, v, kv = _inputs(60 + mask, B, H, n, n)
+    bias = np.random.default_rng(61).standard_normal((H, n, n)).astype(np.float32)
+    got = run_generic(ta, mask, q, k, v, kv, B, H, n, n, 0.125, bias=bias, bias_head=n * n, bias_row=n)
+    row = H * 64
+    want = np.zeros((B, n, row), np.float32)
+    orc.batched_self_attend(THREADS, mask, q, row, n * row, k, row, n * row, v, row, n * row, want, row, n * row, kv,
+                            n, bias, B, H, n, 64, 0.125)
+    assert _ref.scaled_err(got, want) <= TOL
+
+
+def test_single_trailing_query_all_invalid_row_is_uniform(ta, orc, gpu_ready):
+    """A row whose keys are all invalid (additive -FLT_MAX) keeps the reference's uniform weights in
+    the single-query VALU pass and the last-key pass as in the chunks."""
+    B, H, n = 2, 2, 161
+    q, k, v, kv = _inputs(13, B, H, n, n)
+    kv[0, :] = 0
+    got = run_generic(ta, 1, q, k, v, kv, B, H, n, n, 1.0)
+    want = oracle_generic(orc, 1, q, k, v, kv, B, H, n, 1.0)
+    assert _ref.scaled_err(got, want) <= TOL
+
+
+def test_decoder_single_trailing_query_matches_float64(ta, gpu_ready):
+    """DECODER rows of 33 queries over 183 keys: the bf16x3 kernel with the last query on the VALU."""
+    B, H, ne, h, l = 2, 2, 150, 33, 140
+    sl = ne + h
+    q, k, v, _ = _inputs(19, B, H, h, sl)
+    rng = np.random.default_rng(20)
+    kv = (rng.random((B, ne)) > 0.25).astype(np.uint8)
+    got = run_generic(ta, 5, q, k, v, kv, B, H, h, sl, 0.125, q_pos0=ne, ctx_keys=l, chain_start=ne)
+    for b in range(B):
+        allowed = _ref.allowed_matrix(5, h, sl, kv[b], q_pos0=ne, ctx_keys=l, chain_start=ne)
+        for hh in range(H):
+            sel = slice(hh * 64, hh * 64 + 64)
+            want = _ref.naive_attend(q[b, :, sel], k[b, :, sel], v[b, :, sel], allowed, 0.125)
+            assert _ref.scaled_err(got[b, :, sel], want) <= TOL
+
+
 @pytest.mark.parametrize("mask", [1, 3])
 @pytest.mark.parametrize("n", [17, 145, 577])
 def test_dense_bias_matches_oracle(ta, orc, gpu_ready, mask, n):

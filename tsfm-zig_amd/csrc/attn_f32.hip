@@ -753,8 +753,11 @@ hipError_t launch_bias(const Params& p, int bias, bool rope, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_attn_f32(const Params& p, int mask, int bias, bool rope, hipStream_t s) {
-    // Rows longer than the resident kernel takes: the bf16x3 streaming kernel (attn_x3.hip).
-    if (p.n_k > kResidentKeys) return launch_attn_x3(p, mask, bias, rope, s);
+    // Rows longer than the resident kernel takes, and short rows of at least three 32-query blocks
+    // in launches of at least two (series, head) pairs per CU: the bf16x3 streaming kernel
+    // (attn_x3.hip). Fewer pairs leave its workgroups too few; the resident kernel keeps one per CU.
+    if (p.n_k > kResidentKeys || (p.n_q >= 96 && (int64_t)p.B * p.H >= 2 * (int64_t)device_cus()))
+        return launch_attn_x3(p, mask, bias, rope, s);
     switch (mask) {
     case FULL: return launch_bias<FULL>(p, bias, rope, s);
     case KEYS_ADDITIVE: return launch_bias<KEYS_ADDITIVE>(p, bias, rope, s);

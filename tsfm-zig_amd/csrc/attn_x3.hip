@@ -89,6 +89,11 @@ __device__ __forceinline__ void split4(f32x4 v, u32x2& hi, u32x2& mid, u32x2& lo
     mid = u32x2{a.m, b.m};
     lo = u32x2{a.l, b.l};
 }
+// 1 for a row of 32k + 1 queries that one workgroup takes (1 <= k <= 8): its last query runs
+// outside the 32-query blocks, at the end of the workgroup, instead of as a 32-query block of its own
+// (longer rows keep that block: there the pass would lengthen one workgroup in three).
+__host__ __device__ inline int thin_query(int n_q) { return (n_q > XQ && n_q <= XMAXW * XQ + 1 && n_q % XQ == 1) ? 1 : 0; }
+
 __device__ __forceinline__ float pair_max(float x) {  // lanes l and l ^ 32
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -108,7 +113,11 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int qt_n = nw * XQ;
-    const int q_tiles = (p.n_q + qt_n - 1) / qt_n;
+    // A row of 32k + 1 queries: the 32-query blocks take the first 32k, and the last query runs on
+    // the VALU at the end of the workgroup of the last blocks (see below).
+    const int thin = thin_query(p.n_q);
+    const int n_main = p.n_q - thin;
+    const int q_tiles = (n_main + qt_n - 1) / qt_n;
     const int logical = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = logical / q_tiles;
     int qt = logical % q_tiles;
@@ -127,9 +136,9 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float* __restrict__ RS = ROPE ? p.rope_sin + rope_tab * p.rope_table_stride : nullptr;
 
     // Key range of the workgroup (chunks past it are not staged) and of this wave.
-    const int wg_qhi = p.q_pos0 + min(p.n_q, q0 + qt_n) - 1;
+    const int wg_qhi = p.q_pos0 + min(n_main, q0 + qt_n) - 1;
     const int kend = key_end_for<MASK>(wg_qhi, p.n_k, p.ctx_keys);
-    const int wave_nq = max(0, min(XQ, p.n_q - wq0));
+    const int wave_nq = max(0, min(XQ, n_main - wq0));
     const int wave_kend = wave_nq > 0 ? key_end_for<MASK>(p.q_pos0 + wq0 + wave_nq - 1, p.n_k, p.ctx_keys) : 0;
     // Rows of 32k + 1 keys under the masks whose key range is the whole row: the last key on the VALU
     // after the chunks (one dot product per query instead of a 32-key chunk of matrix work).
@@ -213,14 +222,14 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     u32x4 qf[3][4];  // [plane][k-step]: dims 16s + 8 hh .. +7 of query qi
     {
         f32x4 qa[4][2];
-        const float* src = Q + (int64_t)min(qi, p.n_q - 1) * p.q_tok;
+        const float* src = Q + (int64_t)min(qi, n_main - 1) * p.q_tok;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             qa[s][0] = ld4(src + 16 * s + 8 * hh);
             qa[s][1] = ld4(src + 16 * s + 8 * hh + 4);
         }
         if (ROPE) {
-            const int64_t row = (int64_t)(p.q_pos0 + min(qi, p.n_q - 1)) * 32;
+            const int64_t row = (int64_t)(p.q_pos0 + min(qi, n_main - 1)) * 32;
 #pragma unroll
             for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     rope4(qa[s][i], qa[s + 2][i], ld4(RC + row + 16 * s + 8 * hh + 4 * i),
                           ld4(RS + row + 16 * s + 8 * hh + 4 * i));
         }
-        const float sc = qi < p.n_q ? p.scale : 0.f;  // query slots past n_q: q = 0, never stored
+        const float sc = qi < n_main ? p.scale : 0.f;  // query slots past the blocks: q = 0, never stored
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             u32x2 a0, a1, a2, b0, b1, b2;
@@ -449,23 +458,115 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
     }
     const float lt = pair_sum(l);
-    if (qi >= p.n_q || wave_nq == 0) return;
-    const float inv = 1.0f / lt;
-    float* dst = O + (int64_t)qi * p.o_tok + 4 * hh;
+    if (qi < n_main && wave_nq > 0) {
+        const float inv = 1.0f / lt;
+        float* dst = O + (int64_t)qi * p.o_tok + 4 * hh;
 #pragma unroll
-    for (int db = 0; db < 2; db++)
+        for (int db = 0; db < 2; db++)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++)
-            st4(dst + 32 * db + 8 * g4,
-                f32x4{o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]} * inv);
+            for (int g4 = 0; g4 < 4; g4++)
+                st4(dst + 32 * db + 8 * g4,
+                    f32x4{o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]} * inv);
+    }
+
+    // ---- the single query past the blocks (n_q = 32k + 1), in the workgroup of the last blocks:
+    //      each wave takes a slice of its keys from K / V in global memory (just staged: mostly in
+    //      L2) on the VALU, lane = key for the scores and lane = dim for O; the slices' maxima, sums
+    //      and partial rows are merged through LDS. Weights exp2((x - m) log2e), exact for rows that
+    //      only have additively masked scores so far (the reference's uniform weights). ----
+    if (!thin || qt != q_tiles - 1) return;
+    __shared__ __attribute__((aligned(16))) float tq[kHeadDim];
+    __shared__ float tw[XMAXW][kHeadDim];  // a wave's weights of a 64-key batch, then its partial row
+    __shared__ float tml[XMAXW][2];        // a wave's max and weight sum
+    const int qn = p.n_q - 1, qposn = p.q_pos0 + qn;
+    const int kend_n = key_end_for<MASK>(qposn, p.n_k, p.ctx_keys);
+    if (wave == 0 && lane < 32) {
+#pragma clang fp contract(off)
+        float x1 = Q[(int64_t)qn * p.q_tok + lane], x2 = Q[(int64_t)qn * p.q_tok + lane + 32];
+        if (ROPE) {  // nn.ropeHalf, src/core/nn.zig:453-460
+            const float c = RC[(int64_t)qposn * 32 + lane], sn = RS[(int64_t)qposn * 32 + lane];
+            const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
+            x1 = y1;
+            x2 = y2;
+        }
+        tq[lane] = x1 * p.scale;
+        tq[lane + 32] = x2 * p.scale;
+    }
+    __syncthreads();
+    const int per = (kend_n + nw - 1) / nw, k0 = wave * per, k1 = min(kend_n, k0 + per);
+    float mw = kNegInf, lw = 0.f, ow = 0.f;
+    for (int kb = k0; kb < k1; kb += 64) {
+#pragma clang fp contract(off)
+        const int key = kb + lane;
+        float x = kNegInf;
+        if (key < k1) {
+            const float* kr = K + (int64_t)key * p.k_tok;
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                f32x4 lo = ld4(kr + 4 * c), hi = ld4(kr + 32 + 4 * c);
+                if (ROPE) rope4(lo, hi, ld4(RC + (int64_t)key * 32 + 4 * c), ld4(RS + (int64_t)key * 32 + 4 * c));
+                const f32x4 qa = ld4(tq + 4 * c), qb = ld4(tq + 32 + 4 * c);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_fmaf(qb[i], hi[i], __builtin_fmaf(qa[i], lo[i], acc));
+            }
+            x = acc;
+            if (BIAS == BIAS_REL) x = x + lut[key];  // relative index key - qn + n_q - 1 = key
+            if (BIAS == BIAS_DENSE) x = x + p.bias[h * p.bias_head + (int64_t)qn * p.bias_row + key];
+            const uint32_t kvb = mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, key, 0, 0) : 1u;
+            x = masked<MASK>(x, key_term<MASK>(key, p.n_k, kvb != 0, p.ctx_keys), key, qposn, p.n_k, p.chain_start);
+        }
+        float cm = x;
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o2));
+        const float mn = fmaxf(mw, cm);
+        if (mn == kNegInf) continue;  // wave-uniform: nothing to weigh yet
+        const float alpha = mw == kNegInf ? 0.f : __builtin_amdgcn_exp2f((mw - mn) * kLog2e);
+        const float e = key < k1 ? __builtin_amdgcn_exp2f((x - mn) * kLog2e) : 0.f;
+        lw = lw * alpha + e;  // the lane's share of the slice's sum
+        ow = ow * alpha;
+        tw[wave][lane] = e;  // read back by the same wave: LDS keeps a wave's accesses in order
+        // O += sum_j e_j v_j, sixteen rows' loads in flight at a time (rows past the slice carry
+        // weight 0 and read the slice's last row).
+        const int nk = min(64, k1 - kb);
+        const float* vr = V + (int64_t)kb * p.v_tok + lane;
+        for (int j0 = 0; j0 < nk; j0 += 16) {
+            float vv[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) vv[i] = vr[(int64_t)min(j0 + i, nk - 1) * p.v_tok];
+#pragma unroll
+            for (int i = 0; i < 16; i++) ow = __builtin_fmaf(j0 + i < nk ? tw[wave][j0 + i] : 0.f, vv[i], ow);
+        }
+        mw = mn;
+    }
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) lw += __shfl_xor(lw, o2);
+    if (lane == 0) {
+        tml[wave][0] = mw;
+        tml[wave][1] = lw;
+    }
+    tw[wave][lane] = ow;
+    __syncthreads();
+    if (wave != 0) return;
+    float M = kNegInf;
+    for (int w = 0; w < nw; w++) M = fmaxf(M, tml[w][0]);
+    float L = 0.f, acc = 0.f;
+    for (int w = 0; w < nw; w++) {
+        if (tml[w][0] == kNegInf) continue;
+        const float sw = __builtin_amdgcn_exp2f((tml[w][0] - M) * kLog2e);
+        L = L + tml[w][1] * sw;
+        acc = acc + tw[w][lane] * sw;
+    }
+    O[(int64_t)qn * p.o_tok + lane] = acc / L;
 }
 
 template <int MASK, int BIAS, bool ROPE>
 hipError_t launch_one(const Params& p, hipStream_t stream) {
-    const int qb = (p.n_q + XQ - 1) / XQ;
+    const int n_main = p.n_q - thin_query(p.n_q);
+    const int qb = (n_main + XQ - 1) / XQ;
     const int q_tiles = (qb + XMAXW - 1) / XMAXW;
     const int nw = max(XMINW, (qb + q_tiles - 1) / q_tiles);
-    const int64_t blocks = (int64_t)p.B * p.H * ((p.n_q + nw * XQ - 1) / (nw * XQ));
+    const int64_t blocks = (int64_t)p.B * p.H * ((n_main + nw * XQ - 1) / (nw * XQ));
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL((attn_fwd_x3<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(64 * nw), 0, stream, p);
     return hipGetLastError();
