@@ -104,9 +104,9 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_x3(Params p) {
+__global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(ROPE ? 2 : 3, ROPE ? 2 : 3))) void attn_fwd_x3(Params p) {
     __shared__ __attribute__((aligned(16))) XStage stage[2];
-    __shared__ float lut_raw[BIAS == BIAS_REL ? kRelMax + 2 * kLutPad : 1];
+    extern __shared__ float lut_raw[];  // the T5 table (n_q + n_k - 1 + margins), sized at launch
     float* const lut = lut_raw + (BIAS == BIAS_REL ? kLutPad : 0);
 
     const int nt = blockDim.x, nw = nt >> 6;
@@ -475,9 +475,12 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     //      and partial rows are merged through LDS. Weights exp2((x - m) log2e), exact for rows that
     //      only have additively masked scores so far (the reference's uniform weights). ----
     if (!thin || qt != q_tiles - 1) return;
-    __shared__ __attribute__((aligned(16))) float tq[kHeadDim];
-    __shared__ float tw[XMAXW][kHeadDim];  // a wave's weights of a 64-key batch, then its partial row
-    __shared__ float tml[XMAXW][2];        // a wave's max and weight sum
+    // In the first stage's K parts, free now (every wave has passed the last chunk's barrier):
+    // the query, a wave's weights of a 64-key batch and then its partial row, a wave's max and sum.
+    float* const tq = reinterpret_cast<float*>(stage[0].k[0]);
+    float (*const tw)[kHeadDim] = reinterpret_cast<float (*)[kHeadDim]>(tq + kHeadDim);
+    float (*const tml)[2] = reinterpret_cast<float (*)[2]>(tq + kHeadDim + XMAXW * kHeadDim);
+    static_assert((1 + XMAXW) * kHeadDim + 2 * XMAXW <= kPlane, "the single-query pass fits one K part");
     const int qn = p.n_q - 1, qposn = p.q_pos0 + qn;
     const int kend_n = key_end_for<MASK>(qposn, p.n_k, p.ctx_keys);
     if (wave == 0 && lane < 32) {
@@ -568,7 +571,8 @@ hipError_t launch_one(const Params& p, hipStream_t stream) {
     const int nw = max(XMINW, (qb + q_tiles - 1) / q_tiles);
     const int64_t blocks = (int64_t)p.B * p.H * ((n_main + nw * XQ - 1) / (nw * XQ));
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_fwd_x3<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(64 * nw), 0, stream, p);
+    const size_t lut_bytes = BIAS == BIAS_REL ? (size_t)(p.n_q + p.n_k - 1 + 2 * kLutPad) * sizeof(float) : 0;
+    hipLaunchKernelGGL((attn_fwd_x3<MASK, BIAS, ROPE>), dim3((unsigned)blocks), dim3(64 * nw), lut_bytes, stream, p);
     return hipGetLastError();
 }
 
