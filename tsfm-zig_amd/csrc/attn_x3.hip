@@ -37,7 +37,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int XQ = 32;                        // queries per wave
 constexpr int XK = 32;                        // keys per chunk
-constexpr int XMAXW = 8;                      // waves per workgroup, at most
+constexpr int XMAXW = 4;                      // waves per workgroup, at most: three per CU
 constexpr float kSlack = 5.5f;                // 8 ln 2 - a margin: weights stay below 2^8
 constexpr int XMINW = 4;                      // and at least (256 threads: one K and one V item each)
 constexpr int XNT = 64 * XMAXW;
@@ -104,7 +104,7 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 template <int MASK, int BIAS, bool ROPE>
-__global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(ROPE ? 2 : 3, ROPE ? 2 : 3))) void attn_fwd_x3(Params p) {
+__global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd_x3(Params p) {
     __shared__ __attribute__((aligned(16))) XStage stage[2];
     extern __shared__ float lut_raw[];  // the T5 table (n_q + n_k - 1 + margins), sized at launch
     float* const lut = lut_raw + (BIAS == BIAS_REL ? kLutPad : 0);
