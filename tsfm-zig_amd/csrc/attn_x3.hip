@@ -114,7 +114,7 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int ql = lane & 31, hh = lane >> 5;
     const int qt_n = nw * XQ;
     // A row of 32k + 1 queries: the 32-query blocks take the first 32k, and the last query runs on
-    // the VALU at the end of the workgroup of the last blocks (see below).
+    // the VALU at the start of the workgroup of the last blocks (see below).
     const int thin = thin_query(p.n_q);
     const int n_main = p.n_q - thin;
     const int q_tiles = (n_main + qt_n - 1) / qt_n;
@@ -218,6 +218,104 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
     // ---- the wave's queries: rotated, scaled (the scale is a power of two in every family, so
     //      (scale q) . k is the reference's alpha (q . k) bit for bit) and split ----
+    if (BIAS == BIAS_REL) fill_rel_lut(lut_raw, p, h, tid, nt);
+    if (thin && qt == q_tiles - 1) {
+        // ---- the single query past the blocks (n_q = 32k + 1), in the workgroup of the last blocks,
+        //      before the blocks' own work: each wave takes a slice of the keys from K / V in global
+        //      memory on the VALU (bringing them into L2 for the staging that follows), lane = key for
+        //      the scores and lane = dim for O; the slices' maxima, sums and partial rows are merged
+        //      through LDS. Weights exp2((x - m) log2e), exact for rows that only have additively
+        //      masked scores so far (the reference's uniform weights). ----
+        // In the second stage's K parts, first written at the end of chunk 0 (after the barrier that
+        // follows the staging of chunk 0, which wave 0 reaches once its merge is done): the query, a
+        // wave's weights of a 64-key batch and then its partial row, a wave's max and sum.
+        float* const tq = reinterpret_cast<float*>(stage[1].k[0]);
+        float (*const tw)[kHeadDim] = reinterpret_cast<float (*)[kHeadDim]>(tq + kHeadDim);
+        float (*const tml)[2] = reinterpret_cast<float (*)[2]>(tq + kHeadDim + XMAXW * kHeadDim);
+        static_assert((1 + XMAXW) * kHeadDim + 2 * XMAXW <= kPlane, "the single-query pass fits one K part");
+        const int qn = p.n_q - 1, qposn = p.q_pos0 + qn;
+        const int kend_n = key_end_for<MASK>(qposn, p.n_k, p.ctx_keys);
+        if (wave == 0 && lane < 32) {
+    #pragma clang fp contract(off)
+            float x1 = Q[(int64_t)qn * p.q_tok + lane], x2 = Q[(int64_t)qn * p.q_tok + lane + 32];
+            if (ROPE) {  // nn.ropeHalf, src/core/nn.zig:453-460
+                const float c = RC[(int64_t)qposn * 32 + lane], sn = RS[(int64_t)qposn * 32 + lane];
+                const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
+                x1 = y1;
+                x2 = y2;
+            }
+            tq[lane] = x1 * p.scale;
+            tq[lane + 32] = x2 * p.scale;
+        }
+        __syncthreads();
+        const int per = (kend_n + nw - 1) / nw, k0 = wave * per, k1 = min(kend_n, k0 + per);
+        float mw = kNegInf, lw = 0.f, ow = 0.f;
+        for (int kb = k0; kb < k1; kb += 64) {
+    #pragma clang fp contract(off)
+            const int key = kb + lane;
+            float x = kNegInf;
+            if (key < k1) {
+                const float* kr = K + (int64_t)key * p.k_tok;
+                float acc = 0.f;
+    #pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    f32x4 lo = ld4(kr + 4 * c), hi = ld4(kr + 32 + 4 * c);
+                    if (ROPE) rope4(lo, hi, ld4(RC + (int64_t)key * 32 + 4 * c), ld4(RS + (int64_t)key * 32 + 4 * c));
+                    const f32x4 qa = ld4(tq + 4 * c), qb = ld4(tq + 32 + 4 * c);
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) acc = __builtin_fmaf(qb[i], hi[i], __builtin_fmaf(qa[i], lo[i], acc));
+                }
+                x = acc;
+                if (BIAS == BIAS_REL) x = x + lut[key];  // relative index key - qn + n_q - 1 = key
+                if (BIAS == BIAS_DENSE) x = x + p.bias[h * p.bias_head + (int64_t)qn * p.bias_row + key];
+                const uint32_t kvb = mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, key, 0, 0) : 1u;
+                x = masked<MASK>(x, key_term<MASK>(key, p.n_k, kvb != 0, p.ctx_keys), key, qposn, p.n_k, p.chain_start);
+            }
+            float cm = x;
+    #pragma unroll
+            for (int o2 = 32; o2 > 0; o2 >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o2));
+            const float mn = fmaxf(mw, cm);
+            if (mn == kNegInf) continue;  // wave-uniform: nothing to weigh yet
+            const float alpha = mw == kNegInf ? 0.f : __builtin_amdgcn_exp2f((mw - mn) * kLog2e);
+            const float e = key < k1 ? __builtin_amdgcn_exp2f((x - mn) * kLog2e) : 0.f;
+            lw = lw * alpha + e;  // the lane's share of the slice's sum
+            ow = ow * alpha;
+            tw[wave][lane] = e;  // read back by the same wave: LDS keeps a wave's accesses in order
+            // O += sum_j e_j v_j, sixteen rows' loads in flight at a time (rows past the slice carry
+            // weight 0 and read the slice's last row).
+            const int nk = min(64, k1 - kb);
+            const float* vr = V + (int64_t)kb * p.v_tok + lane;
+            for (int j0 = 0; j0 < nk; j0 += 16) {
+                float vv[16];
+    #pragma unroll
+                for (int i = 0; i < 16; i++) vv[i] = vr[(int64_t)min(j0 + i, nk - 1) * p.v_tok];
+    #pragma unroll
+                for (int i = 0; i < 16; i++) ow = __builtin_fmaf(j0 + i < nk ? tw[wave][j0 + i] : 0.f, vv[i], ow);
+            }
+            mw = mn;
+        }
+    #pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) lw += __shfl_xor(lw, o2);
+        if (lane == 0) {
+            tml[wave][0] = mw;
+            tml[wave][1] = lw;
+        }
+        tw[wave][lane] = ow;
+        __syncthreads();
+        if (wave == 0) {
+        float M = kNegInf;
+        for (int w = 0; w < nw; w++) M = fmaxf(M, tml[w][0]);
+        float L = 0.f, acc = 0.f;
+        for (int w = 0; w < nw; w++) {
+            if (tml[w][0] == kNegInf) continue;
+            const float sw = __builtin_amdgcn_exp2f((tml[w][0] - M) * kLog2e);
+            L = L + tml[w][1] * sw;
+            acc = acc + tw[w][lane] * sw;
+        }
+        O[(int64_t)qn * p.o_tok + lane] = acc / L;
+        }
+
+    }
     load_chunk(0);
     u32x4 qf[3][4];  // [plane][k-step]: dims 16s + 8 hh .. +7 of query qi
     {
@@ -248,7 +346,6 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             qf[2][s] = u32x4{a2[0], a2[1], b2[0], b2[1]};
         }
     }
-    if (BIAS == BIAS_REL) fill_rel_lut(lut_raw, p, h, tid, nt);
     // The tail key's K row (rotated, as the staged rows are) and V row, and its key term.
     __shared__ __attribute__((aligned(16))) float ktail[kHeadDim], vtail[kHeadDim];
     __shared__ float tail_add;
@@ -469,98 +566,6 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                     f32x4{o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]} * inv);
     }
 
-    // ---- the single query past the blocks (n_q = 32k + 1), in the workgroup of the last blocks:
-    //      each wave takes a slice of its keys from K / V in global memory (just staged: mostly in
-    //      L2) on the VALU, lane = key for the scores and lane = dim for O; the slices' maxima, sums
-    //      and partial rows are merged through LDS. Weights exp2((x - m) log2e), exact for rows that
-    //      only have additively masked scores so far (the reference's uniform weights). ----
-    if (!thin || qt != q_tiles - 1) return;
-    // In the first stage's K parts, free now (every wave has passed the last chunk's barrier):
-    // the query, a wave's weights of a 64-key batch and then its partial row, a wave's max and sum.
-    float* const tq = reinterpret_cast<float*>(stage[0].k[0]);
-    float (*const tw)[kHeadDim] = reinterpret_cast<float (*)[kHeadDim]>(tq + kHeadDim);
-    float (*const tml)[2] = reinterpret_cast<float (*)[2]>(tq + kHeadDim + XMAXW * kHeadDim);
-    static_assert((1 + XMAXW) * kHeadDim + 2 * XMAXW <= kPlane, "the single-query pass fits one K part");
-    const int qn = p.n_q - 1, qposn = p.q_pos0 + qn;
-    const int kend_n = key_end_for<MASK>(qposn, p.n_k, p.ctx_keys);
-    if (wave == 0 && lane < 32) {
-#pragma clang fp contract(off)
-        float x1 = Q[(int64_t)qn * p.q_tok + lane], x2 = Q[(int64_t)qn * p.q_tok + lane + 32];
-        if (ROPE) {  // nn.ropeHalf, src/core/nn.zig:453-460
-            const float c = RC[(int64_t)qposn * 32 + lane], sn = RS[(int64_t)qposn * 32 + lane];
-            const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
-            x1 = y1;
-            x2 = y2;
-        }
-        tq[lane] = x1 * p.scale;
-        tq[lane + 32] = x2 * p.scale;
-    }
-    __syncthreads();
-    const int per = (kend_n + nw - 1) / nw, k0 = wave * per, k1 = min(kend_n, k0 + per);
-    float mw = kNegInf, lw = 0.f, ow = 0.f;
-    for (int kb = k0; kb < k1; kb += 64) {
-#pragma clang fp contract(off)
-        const int key = kb + lane;
-        float x = kNegInf;
-        if (key < k1) {
-            const float* kr = K + (int64_t)key * p.k_tok;
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                f32x4 lo = ld4(kr + 4 * c), hi = ld4(kr + 32 + 4 * c);
-                if (ROPE) rope4(lo, hi, ld4(RC + (int64_t)key * 32 + 4 * c), ld4(RS + (int64_t)key * 32 + 4 * c));
-                const f32x4 qa = ld4(tq + 4 * c), qb = ld4(tq + 32 + 4 * c);
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc = __builtin_fmaf(qb[i], hi[i], __builtin_fmaf(qa[i], lo[i], acc));
-            }
-            x = acc;
-            if (BIAS == BIAS_REL) x = x + lut[key];  // relative index key - qn + n_q - 1 = key
-            if (BIAS == BIAS_DENSE) x = x + p.bias[h * p.bias_head + (int64_t)qn * p.bias_row + key];
-            const uint32_t kvb = mask_reads_valid<MASK>() ? __builtin_amdgcn_raw_buffer_load_b8(kv_rsrc, key, 0, 0) : 1u;
-            x = masked<MASK>(x, key_term<MASK>(key, p.n_k, kvb != 0, p.ctx_keys), key, qposn, p.n_k, p.chain_start);
-        }
-        float cm = x;
-#pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o2));
-        const float mn = fmaxf(mw, cm);
-        if (mn == kNegInf) continue;  // wave-uniform: nothing to weigh yet
-        const float alpha = mw == kNegInf ? 0.f : __builtin_amdgcn_exp2f((mw - mn) * kLog2e);
-        const float e = key < k1 ? __builtin_amdgcn_exp2f((x - mn) * kLog2e) : 0.f;
-        lw = lw * alpha + e;  // the lane's share of the slice's sum
-        ow = ow * alpha;
-        tw[wave][lane] = e;  // read back by the same wave: LDS keeps a wave's accesses in order
-        // O += sum_j e_j v_j, sixteen rows' loads in flight at a time (rows past the slice carry
-        // weight 0 and read the slice's last row).
-        const int nk = min(64, k1 - kb);
-        const float* vr = V + (int64_t)kb * p.v_tok + lane;
-        for (int j0 = 0; j0 < nk; j0 += 16) {
-            float vv[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) vv[i] = vr[(int64_t)min(j0 + i, nk - 1) * p.v_tok];
-#pragma unroll
-            for (int i = 0; i < 16; i++) ow = __builtin_fmaf(j0 + i < nk ? tw[wave][j0 + i] : 0.f, vv[i], ow);
-        }
-        mw = mn;
-    }
-#pragma unroll
-    for (int o2 = 32; o2 > 0; o2 >>= 1) lw += __shfl_xor(lw, o2);
-    if (lane == 0) {
-        tml[wave][0] = mw;
-        tml[wave][1] = lw;
-    }
-    tw[wave][lane] = ow;
-    __syncthreads();
-    if (wave != 0) return;
-    float M = kNegInf;
-    for (int w = 0; w < nw; w++) M = fmaxf(M, tml[w][0]);
-    float L = 0.f, acc = 0.f;
-    for (int w = 0; w < nw; w++) {
-        if (tml[w][0] == kNegInf) continue;
-        const float sw = __builtin_amdgcn_exp2f((tml[w][0] - M) * kLog2e);
-        L = L + tml[w][1] * sw;
-        acc = acc + tw[w][lane] * sw;
-    }
-    O[(int64_t)qn * p.o_tok + lane] = acc / L;
 }
 
 template <int MASK, int BIAS, bool ROPE>
