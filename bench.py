@@ -256,15 +256,15 @@ def run_decode(torch, ta, workloads, peak):
     cache = ta.KvCache(ta.DTYPE_BF16, w.B, w.H, T)
     cache.append(dev["k"], dev["v"], P, row, T * row, row, T * row)
     stream = torch.cuda.current_stream()
-    events = []  # (start, end) around every decode-block launch of the timed steps
+    events = []  # (start, end) around the 8 decode-block launches of each timed step
     pool = []    # event pairs made (and recorded once) before the timed steps
     # The block views, made once: the host issues a launch in a few microseconds, ahead of the
-    # GPU, so the event pair around a launch brackets the kernel and not the host's Python.
+    # GPU, so the event pair around a step's launches brackets the kernels and not the host's Python.
     views = [(dev["k"][:, P + i * blk:], dev["v"][:, P + i * blk:], dev["q"][:, P + i * blk:], out[:, i * blk:])
              for i in range(nb)]
 
     def prepare(steps):
-        while len(pool) < steps * nb:
+        while len(pool) < steps:
             pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             pair[0].record(stream)
             pair[1].record(stream)
@@ -272,21 +272,23 @@ def run_decode(torch, ta, workloads, peak):
         torch.cuda.synchronize()
 
     def step(record=True):
-        cache.truncate(P)
+        cache.truncate(P)  # host-side length only
+        if record:
+            e0, e1 = pool[len(events)]
+            e0.record(stream)
         for i in range(nb):
             kb, vb, qb, ob = views[i]
-            if record:
-                e0, e1 = pool[len(events)]
-                e0.record(stream)
             # One launch per block: the block's K/V into the cache, then its 32 queries over it.
             cache.append_attend(kb, vb, qb, ob, blk, w.scale, row, T * row, row, T * row, row, T * row, row,
                                 nb * blk * row, stream)
-            if record:
-                e1.record(stream)
-                events.append((e0, e1))
+        if record:
+            e1.record(stream)
+            events.append((e0, e1))
 
     def kernel_ms():
-        return sum(a0.elapsed_time(a1) for a0, a1 in events) / len(events)
+        # Per launch: the 8 back-to-back launches of a step between one event pair (the gaps between
+        # them included), so no event sits between two launches.
+        return sum(a0.elapsed_time(a1) for a0, a1 in events) / (len(events) * nb)
 
     def cpu_leg(B, lib=None):
         orc = _orc(lib)
