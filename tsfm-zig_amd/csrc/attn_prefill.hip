@@ -20,8 +20,7 @@
 // buffer descriptors whose range ends after the last key, so a ragged tail reads zeros), K two
 // tiles ahead in the operand order of the S^T instruction (each operand read is 1 KB of contiguous
 // LDS), V one tile ahead as rows with their 16-byte chunks XOR-swizzled by key (conflict-free
-// transposing reads). No staging registers, one barrier per tile; the barrier waits for every copy
-// but the newest tile's K (issued last, needed two tiles on), which stays in flight across it.
+// transposing reads). No staging registers, one barrier per tile.
 //
 // Softmax in f32 registers, in exp2 units: e = exp2(s * scale*log2(e) - m). A block's weights are
 // formed against the current m first; m moves only when they show it must (a lane's rounded
@@ -157,7 +156,6 @@ attn_fwd_half_pipe(Params p) {
     // offset (the host keeps a (series, head) span of K or V below 4 GiB).
     const u32x4 k_buf = buf_desc(K, (uint32_t)(((int64_t)(p.n_k - 1) * p.k_tok + kHeadDim) * 2));
     const u32x4 v_buf = buf_desc(V, (uint32_t)(((int64_t)(p.n_k - 1) * p.v_tok + kHeadDim) * 2));
-    const u32x4 kv_buf = buf_desc(kValid ? (const void*)KV : (const void*)K, kValid ? (uint32_t)p.n_k : 0u);
     uint32_t k_off[2], v_off[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
@@ -398,25 +396,14 @@ attn_fwd_half_pipe(Params p) {
     // staging of tiles t+1 (V) and t+2 (K) is issued first and published by the barrier at the end.
     for (int t = 0; t < ntiles; t++) {
         const bool more1 = t + 1 < ntiles, more2 = t + 2 < ntiles;
-        // Issue order: tile t+1's V, tile t+2's key-valid byte, tile t+2's K. The end of the tile
-        // waits for all but the last two (K of t+2, needed only two tiles on), so the K copies stay
-        // in flight across the barrier.
+        const uint32_t kb2 = more2 ? kv_byte(t + 2) : 0u;
+        if (more2) stage_k(t + 2);
         if (more1) stage_v(t + 1);
-        uint32_t kb2 = 0u;
-        if (more2) {
-            if (kValid)
-                asm volatile("buffer_load_ubyte %0, %1, %2, 0 offen" : "=v"(kb2) : "v"((uint32_t)((t + 2) * NK + lane)), "s"(kv_buf) : "memory");
-            else
-                kb2 = 1u;
-            stage_k(t + 2);
-        }
         __builtin_amdgcn_sched_barrier(0);
         block(2 * t, sa, sb, vm0, vm0);
         block(2 * t + 1, sb, sa, vm0, vm1);
-        if (more2)
-            asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" : "+v"(kb2) : : "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" : "+v"(kb2) : : "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
         vm0 = vm1;
         vm1 = __ballot(kb2 != 0);
     }
