@@ -646,21 +646,22 @@ def measure(torch, bench, steps: int, warmup: int, do_cpu: bool) -> dict:
     prepare = getattr(bench, "prepare", None)  # untimed set-up the timed steps use (event pools)
     if prepare is not None:
         prepare(steps)
-    # Timed region: the steps between two full synchronisations. A single-launch step gets one
-    # event pair per launch on the stream the kernel runs on (the per-dispatch duration rocprofv3
-    # --kernel-trace reports); a multi-launch step records its dominant kernel itself.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    # Timed region: the steps between two full synchronisations. One event pair on the stream the
+    # kernels run on brackets all the steps (no event between two steps' launches), so a
+    # single-launch step's figure is the per-dispatch duration rocprofv3 --kernel-trace reports
+    # plus the GPU's gap between two launches; a multi-launch step records its dominant kernel
+    # itself.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(steps):
-        starts[i].record(stream)
         bench.step()
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / steps
-    step_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
+    step_ms = start.elapsed_time(end) / steps
     if bench.kernel_ms is not None:
         kernel_ms = bench.kernel_ms()
         work = bench.kernel_work
