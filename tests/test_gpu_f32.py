@@ -265,6 +265,27 @@ def test_chronos2_time_attention_full_shape(ta, orc, orc16, gpu_ready, scale):
     assert gpu_f64 <= max(o8_f64, o16_f64), (gpu_f64, o8_f64, o16_f64)
 
 
+def test_chronos2_time_attention_back_to_back_launches_agree(ta, gpu_ready):
+    """The benchmarked Chronos-2 launch (B=64, H=12, L=577, RoPE, left padding) six times back to
+    back on one stream, no synchronisation in between: the same bits every time (the kernel is
+    deterministic, so a staged chunk read before every wave's copy landed shows up)."""
+    import torch
+    from tsfm_attn import workloads
+
+    w = workloads.chronos2(scale=0.125)
+    a = w.arrays
+    dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).cuda() for n in ("q", "k", "v", "rope_cos", "rope_sin",
+                                                                            "key_valid")}
+    outs = [torch.full_like(dev["q"], -7.0) for _ in range(6)]
+    for o in outs:
+        assert ta.chronos2_time_attention(dev["q"], dev["k"], dev["v"], o, dev["rope_cos"], dev["rope_sin"],
+                                          dev["key_valid"], bool(a["key_valid"].all()), w.B, w.n_q, w.H * 64, w.H,
+                                          64, scale=0.125) == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32))
+
+
 def test_bolt_self_attention_full_shape(ta, orc, orc16, gpu_ready):
     """Chronos-Bolt-base encoder self-attention at B=256, H=12, L=129 with the T5 bias built on the
     device from the (32, 12) table, against the oracle's positionBias + SelfJob (scale 1.0: the

@@ -184,6 +184,32 @@ def test_half_prefill_full_shape_f16(ta, orc, gpu_ready):
     assert _ref.scaled_err(got, want) <= TOL_HALF
 
 
+def test_half_prefill_back_to_back_launches_agree(ta, gpu_ready):
+    """The config-5 prefill launched six times back to back on one stream (no synchronisation in
+    between, as a timed loop runs it) gives the same bits every time: the kernel is deterministic,
+    so a copy into LDS that a wave read before it landed shows up as a difference."""
+    torch = _torch()
+    from tsfm_attn import workloads
+
+    w = workloads.timestral_prefill()
+    a = w.arrays
+    row = w.H * 64
+    qd, _ = _dev(a["q"], "f16")
+    kd, _ = _dev(a["k"], "f16")
+    vd, _ = _dev(a["v"], "f16")
+    kvd = torch.from_numpy(np.ascontiguousarray(a["key_valid"])).cuda()
+    outs = [torch.full((w.B, w.n_q, row), -7.0, dtype=torch.float16, device="cuda") for _ in range(6)]
+    for od in outs:
+        ta.fwd_checked(ta.make_args(q=qd, k=kd, v=vd, o=od, mask=3, batch=w.B, heads=w.H, n_q=w.n_q, n_k=w.n_k,
+                                    q_tok=row, q_batch=w.n_q * row, k_tok=row, k_batch=w.n_k * row, v_tok=row,
+                                    v_batch=w.n_k * row, o_tok=row, o_batch=w.n_q * row, scale=w.scale,
+                                    key_valid=kvd, kv_batch=a["key_valid"].shape[1]))
+    torch.cuda.synchronize()
+    first = outs[0].view(torch.int16)
+    for od in outs[1:]:
+        assert torch.equal(od.view(torch.int16), first)
+
+
 def _decode(ta, w, name, blocks=None, fused=False):
     """Prefix append, then per block: append 32 K/V, attend its 32 queries (fused: both in one
     tsfm_kv_append_attend call, the benchmark's decode step). Returns the decoded outputs
