@@ -323,6 +323,29 @@ def test_bolt_self_attention_full_shape(ta, orc, orc16, gpu_ready):
     assert np.array_equal(o, o2)
 
 
+def test_bolt_self_attention_back_to_back_launches_agree(ta, gpu_ready):
+    """The benchmarked Chronos-Bolt-base launch (B=256, H=12, L=129: the single query 128 on the
+    VALU before the blocks, with the second LDS stage as its scratch) six times back to back on one
+    stream, no synchronisation in between: the same bits every time."""
+    import torch
+    from tsfm_attn import workloads
+
+    w = workloads.bolt()
+    a = w.arrays
+    L, H, d = w.n_q, w.H, w.H * 64
+    buckets = np.zeros(2 * L - 1, np.int32)
+    assert ta.load().tsfm_t5_bucket_table(buckets.ctypes.data, L, L, 32, 128) == ta.OK
+    dev = {n: torch.from_numpy(np.ascontiguousarray(a[n])).cuda() for n in ("q", "k", "v", "rel_table", "key_valid")}
+    db = torch.from_numpy(buckets).cuda()
+    outs = [torch.full_like(dev["q"], -7.0) for _ in range(6)]
+    for o in outs:
+        assert ta.bolt_self_attention(dev["q"], dev["k"], dev["v"], o, dev["rel_table"], db, dev["key_valid"],
+                                      bool(a["key_valid"].all()), w.B, L, d, H, 64, 32) == ta.OK, ta.last_error()
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32))
+
+
 def test_bolt_cross_attention(ta, orc, gpu_ready):
     rng = np.random.default_rng(13)
     nb, seq, nh = 16, 33, 8

@@ -338,3 +338,36 @@ def test_presplit_operands_give_the_same_bits(ta, orc, gpu_ready):
     for got, alt, ref in zip(pre, own, want):
         np.testing.assert_array_equal(got, alt)
         assert _ref.scaled_err(got, ref) <= TOL
+
+
+def test_presplit_product_back_to_back_launches_agree(ta, gpu_ready):
+    """The benchmarked q/k/v projection (64 x 577 tokens, d 768, RoPE: 256 x 128 tiles staged by
+    DMA in two LDS stages, then the rows past them) four times back to back on one stream, no
+    synchronisation in between: the same bits every time (a stage read before its copies landed
+    would show up)."""
+    import torch
+
+    b, seq, d, nh = 64, 577, 768, 12
+    tokens, inner = b * seq, nh * 64
+    rng = np.random.default_rng(64577)
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    dx = cu(rng.standard_normal((tokens, d)).astype(np.float32))
+    dw = [cu(w) for w in _weights(rng, inner, d, 3)]
+    cos_t = np.cos(np.outer(np.arange(seq), 10000.0 ** (-np.arange(32) / 32))).astype(np.float32)
+    sin_t = np.sin(np.outer(np.arange(seq), 10000.0 ** (-np.arange(32) / 32))).astype(np.float32)
+    dc, ds = cu(cos_t), cu(sin_t)
+    runs = []
+    for _ in range(4):
+        outs = [torch.full((tokens, inner), -3.0, device="cuda") for _ in range(3)]
+        a = ta.ProjArgs(dtype=ta.DTYPE_F32, out_dtype=ta.DTYPE_F32, batch=b, seq=seq, d_in=d, heads=nh, head_dim=64,
+                        flags=ta.DEVICE_PTRS, rope_half=32, rope_rows_per_table=0, rope_row0=0, rope_table_stride=0,
+                        x=dx.data_ptr(), x_tok=d, w_q=dw[0].data_ptr(), w_k=dw[1].data_ptr(), w_v=dw[2].data_ptr(),
+                        w_gate=None, q=outs[0].data_ptr(), q_tok=inner, k=outs[1].data_ptr(), k_tok=inner,
+                        v=outs[2].data_ptr(), v_tok=inner, gate=None, gate_tok=0, rope_cos=dc.data_ptr(),
+                        rope_sin=ds.data_ptr(), stream=0)
+        assert ta.qkv_project(a) == ta.OK, ta.last_error()
+        runs.append(outs)
+    torch.cuda.synchronize()
+    for outs in runs[1:]:
+        for got, first in zip(outs, runs[0]):
+            assert torch.equal(got.view(torch.int32), first.view(torch.int32))
