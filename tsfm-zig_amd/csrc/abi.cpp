@@ -1305,7 +1305,8 @@ struct BoltDev {  // device-side pointers of one call
 };
 
 // Scratch: x (rows x d), kv (rows bytes), emb (rows x d), xn (rows x d), q/k/v/ab (rows x inner
-// each), hbuf (rows x max(d_ff, hid)), rbuf (rows x max(d, head out)); the decoder reuses q/k/v/ab.
+// each), hbuf (rows x max(d_ff, hid)), rbuf (rows x max(d, head out)), the bucket ids, and the
+// cross-attention K/V of every decoder layer (2 x layers x rows x inner); the decoder reuses q/v/ab.
 hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, char* scratch, const size_t* at,
                            hipStream_t s) {
     const int nb = a->batch, np = a->n_patch, seq = np + 1, d = a->d_model, inner = a->heads * a->head_dim;
@@ -1354,6 +1355,24 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
             hipSuccess)
             break;
     }
+    // ---- the cross-attention K/V of every decoder layer from the encoder output: layers two at a
+    //      time, one product of four outputs (fewer, fuller launches than one per layer) ----
+    float* const ckv = reinterpret_cast<float*>(scratch + at[11]);
+    const int64_t kv_n = (int64_t)R * inner;
+    for (int l = 0; l < a->n_dec_layers && e == hipSuccess; l += 2) {
+        const bool pair = l + 1 < a->n_dec_layers;
+        tsfm::ProjParams p{};
+        p.x = x; p.x_tok = d; p.w_ld = d; p.alpha = 1.f;
+        p.w0 = dv.dec[l].cross_k; p.w1 = dv.dec[l].cross_v;
+        p.y0 = ckv + (2 * l) * kv_n; p.y1 = ckv + (2 * l + 1) * kv_n;
+        if (pair) {
+            p.w2 = dv.dec[l + 1].cross_k; p.w3 = dv.dec[l + 1].cross_v;
+            p.y2 = ckv + (2 * l + 2) * kv_n; p.y3 = ckv + (2 * l + 3) * kv_n;
+        }
+        p.y0_tok = p.y1_tok = p.y2_tok = p.y3_tok = inner;
+        p.tokens = R; p.seq = seq; p.d_in = d; p.width = inner; p.n_out = pair ? 4 : 2; p.out_dtype = TSFM_DTYPE_F32;
+        e = tsfm::launch_proj(p, s);
+    }
     // ---- decoder (Model.decode): one token per series; y (nb x d) in emb ----
     float* y = emb;
     if (e == hipSuccess) e = tsfm::launch_broadcast_rows(dv.dec_start, y, nb, d, s);
@@ -1371,13 +1390,8 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
             break;
         // cross-attention to the encoder output
         if ((e = linear_on(xn, d, ly.cross_q, inner, d, q, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
-        tsfm::ProjParams p{};
-        p.x = x; p.x_tok = d; p.w0 = ly.cross_k; p.w1 = ly.cross_v; p.w_ld = d; p.alpha = 1.f;
-        p.y0 = k; p.y1 = v; p.y0_tok = p.y1_tok = inner;
-        p.tokens = R; p.seq = seq; p.d_in = d; p.width = inner; p.n_out = 2; p.out_dtype = TSFM_DTYPE_F32;
-        if ((e = tsfm::launch_proj(p, s)) != hipSuccess) break;
         tsfm::Params ap{};  // CrossJob.attend (:349-381): one query per (series, head), key mask, no scale
-        ap.q = q; ap.k = k; ap.v = v; ap.o = ab;
+        ap.q = q; ap.k = ckv + (2 * l) * kv_n; ap.v = ckv + (2 * l + 1) * kv_n; ap.o = ab;
         ap.q_tok = inner; ap.q_batch = inner; ap.o_tok = inner; ap.o_batch = inner;
         ap.k_tok = ap.v_tok = inner; ap.k_batch = ap.v_batch = (int64_t)seq * inner;
         ap.key_valid = kv; ap.kv_batch = seq;
@@ -1469,16 +1483,16 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
         return rc;
     const int64_t hid = std::max(std::max<int64_t>(a->input_embed.hid, a->output_embed.hid), F);
     const int64_t rw = std::max<int64_t>(d, a->output_embed.out);
-    const size_t sz[11] = {(size_t)(R * d) * 4, (size_t)R, (size_t)(R * d) * 4, (size_t)(R * d) * 4,
+    const size_t sz[12] = {(size_t)(R * d) * 4, (size_t)R, (size_t)(R * d) * 4, (size_t)(R * d) * 4,
                            (size_t)(R * inner) * 4, (size_t)(R * inner) * 4, (size_t)(R * inner) * 4,
                            (size_t)(R * inner) * 4, (size_t)(R * hid) * 4, (size_t)(R * rw) * 4,
-                           buckets.size() * 4};
+                           buckets.size() * 4, (size_t)(2 * a->n_dec_layers * R * inner) * 4};
     hipError_t e;
     if (a->flags & TSFM_ATTN_DEVICE_PTRS) {
         hipStream_t s = static_cast<hipStream_t>(a->stream);
         Plan plan;
-        size_t at[11];
-        for (int i = 0; i < 11; i++) at[i] = plan.take(sz[i]);
+        size_t at[12];
+        for (int i = 0; i < 12; i++) at[i] = plan.take(sz[i]);
         const size_t part_at = plan.take(tsfm::kSplitWorkspaceBytes);
         // The bucket ids live on the device once per (length, buckets, max distance): a per-call
         // upload from pageable memory would make the host wait for the stream to drain before it
@@ -1504,9 +1518,10 @@ int tsfm_bolt_forward(const tsfm_bolt_forward_args* a) {
     ThreadCtx* ctx = thread_ctx();
     if (ctx == nullptr) return fail(TSFM_E_DEVICE, "cannot create the thread's HIP stream");
     Staging st;
-    size_t at[11];
+    size_t at[12];
     for (int i = 0; i < 10; i++) at[i] = st.add(nullptr, sz[i]);
     at[10] = st.add(buckets.data(), sz[10]);
+    at[11] = st.add(nullptr, sz[11]);
     const int64_t pin = a->input_embed.in;
     const size_t feats_at = st.add(a->feats, (size_t)(nb * a->n_patch * pin) * 4);
     const size_t pv_at = st.add(a->patch_valid, (size_t)(nb * a->n_patch));
