@@ -865,6 +865,18 @@ hipError_t linear_on(const float* x, int64_t x_tok, const float* w, int out, int
     return tsfm::launch_proj(p, s);
 }
 
+// linear_on with the input rows normalised as they are loaded (x read as rmsNorm(x, in_scale, eps)):
+// products of at most 16 rows (tsfm::proj_fuses_input_norm), one launch fewer than the norm first.
+hipError_t linear_in_norm_on(const float* x, int64_t x_tok, const float* in_scale, float eps, const float* w, int out,
+                             int in, float* y, int64_t y_tok, int rows, int epi, hipStream_t s) {
+    tsfm::ProjParams p{};
+    p.x = x; p.x_tok = x_tok; p.w0 = w; p.w_ld = in; p.alpha = 1.f; p.epi = epi;
+    p.y0 = y; p.y0_tok = y_tok;
+    p.tokens = rows; p.seq = rows; p.d_in = in; p.width = out; p.n_out = 1; p.out_dtype = TSFM_DTYPE_F32;
+    p.in_norm_scale = in_scale; p.in_norm_eps = eps;
+    return tsfm::launch_proj(p, s);
+}
+
 // TSFM_UNFUSED_NORM=1 makes linear_norm_on queue the product and the row norm as two launches: the
 // form the fused one must equal bit for bit (a diagnostic switch; same arithmetic either way).
 bool unfused_norm_requested() {
@@ -1376,20 +1388,36 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
     // ---- decoder (Model.decode): one token per series; y (nb x d) in emb ----
     float* y = emb;
     if (e == hipSuccess) e = tsfm::launch_broadcast_rows(dv.dec_start, y, nb, d, s);
-    if (e == hipSuccess)
+    // With at most 16 series the decoder's products normalise their input rows as they load them
+    // (the same bits as a norm launch first); otherwise each row norm is its own launch or is fused
+    // into the producing product.
+    const bool in_norm = tsfm::proj_fuses_input_norm(nb, d) && !unfused_norm_requested();
+    if (e == hipSuccess && (!in_norm || a->n_dec_layers == 0))
         e = tsfm::launch_rms_norm(y, d, xn, d, a->n_dec_layers > 0 ? dv.dec[0].self_norm : dv.dec_final_norm, nb, d,
                                   a->eps, s);
     for (int l = 0; l < a->n_dec_layers && e == hipSuccess; l++) {
         const tsfm_bolt_dec_layer& ly = dv.dec[l];
         const bool last = l + 1 == a->n_dec_layers;
-        // self-attention over the single decoder token: o(v(norm(y))); the o projection also
-        // normalises y for the cross-attention
-        if ((e = linear_on(xn, d, ly.self_v, inner, d, v, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_norm_on(v, inner, ly.self_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, ly.cross_norm, xn, d,
-                                a->eps, s)) != hipSuccess)
-            break;
-        // cross-attention to the encoder output
-        if ((e = linear_on(xn, d, ly.cross_q, inner, d, q, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess) break;
+        // self-attention over the single decoder token: o(v(norm(y)))
+        if (in_norm) {
+            if ((e = linear_in_norm_on(y, d, ly.self_norm, a->eps, ly.self_v, inner, d, v, inner, nb, tsfm::kEpiNone,
+                                       s)) != hipSuccess)
+                break;
+            if ((e = linear_on(v, inner, ly.self_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess) break;
+            if ((e = linear_in_norm_on(y, d, ly.cross_norm, a->eps, ly.cross_q, inner, d, q, inner, nb,
+                                       tsfm::kEpiNone, s)) != hipSuccess)
+                break;
+        } else {
+            // the o projection also normalises y for the cross-attention
+            if ((e = linear_on(xn, d, ly.self_v, inner, d, v, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess)
+                break;
+            if ((e = linear_norm_on(v, inner, ly.self_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, ly.cross_norm, xn,
+                                    d, a->eps, s)) != hipSuccess)
+                break;
+            if ((e = linear_on(xn, d, ly.cross_q, inner, d, q, inner, nb, tsfm::kEpiNone, nullptr, s)) != hipSuccess)
+                break;
+        }
+        // cross-attention to the encoder output (its K/V computed above)
         tsfm::Params ap{};  // CrossJob.attend (:349-381): one query per (series, head), key mask, no scale
         ap.q = q; ap.k = ckv + (2 * l) * kv_n; ap.v = ckv + (2 * l + 1) * kv_n; ap.o = ab;
         ap.q_tok = inner; ap.q_batch = inner; ap.o_tok = inner; ap.o_batch = inner;
@@ -1397,14 +1425,27 @@ hipError_t bolt_forward_on(const tsfm_bolt_forward_args* a, const BoltDev& dv, c
         ap.key_valid = kv; ap.kv_batch = seq;
         ap.B = nb; ap.H = a->heads; ap.n_q = 1; ap.n_k = seq; ap.scale = 1.f;
         if ((e = tsfm::launch_attn_f32(ap, TSFM_MASK_KEYS_ADDITIVE, tsfm::BIAS_NONE, false, s)) != hipSuccess) break;
-        if ((e = linear_norm_on(ab, inner, ly.cross_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, ly.ffn_norm, xn, d,
-                                a->eps, s)) != hipSuccess)
-            break;
         // FFN; wo also normalises y for the next layer (or the final norm)
-        if ((e = linear_on(xn, d, ly.wi, F, d, hb, F, nb, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
-        if ((e = linear_norm_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y,
-                                last ? dv.dec_final_norm : dv.dec[l + 1].self_norm, xn, d, a->eps, s)) != hipSuccess)
-            break;
+        if (in_norm) {
+            if ((e = linear_on(ab, inner, ly.cross_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, s)) != hipSuccess)
+                break;
+            if ((e = linear_in_norm_on(y, d, ly.ffn_norm, a->eps, ly.wi, F, d, hb, F, nb, tsfm::kEpiRelu, s)) !=
+                hipSuccess)
+                break;
+            e = last ? linear_norm_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y, dv.dec_final_norm, xn, d,
+                                      a->eps, s)
+                     : linear_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y, s);
+            if (e != hipSuccess) break;
+        } else {
+            if ((e = linear_norm_on(ab, inner, ly.cross_o, d, inner, y, d, nb, tsfm::kEpiResidual, y, ly.ffn_norm, xn,
+                                    d, a->eps, s)) != hipSuccess)
+                break;
+            if ((e = linear_on(xn, d, ly.wi, F, d, hb, F, nb, tsfm::kEpiRelu, nullptr, s)) != hipSuccess) break;
+            if ((e = linear_norm_on(hb, F, ly.wo, d, F, y, d, nb, tsfm::kEpiResidual, y,
+                                    last ? dv.dec_final_norm : dv.dec[l + 1].self_norm, xn, d, a->eps, s)) !=
+                hipSuccess)
+                break;
+        }
     }
     if (e == hipSuccess) e = resblock_on(dv.oe, xn, nb, dv.raw, hb, rb, s);
     return e;

@@ -102,8 +102,14 @@ struct ProjParams {
     float* norm_out;
     int64_t norm_out_tok;
     float norm_eps;
+    // Optional row norm of the input, for products of at most 16 tokens (the 16-token kernel): x is
+    // read as rmsNorm(x, in_norm_scale, in_norm_eps), the same arithmetic as launch_rms_norm.
+    const float* in_norm_scale;
+    float in_norm_eps;
 };
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
+// Whether a product of `tokens` rows (f32 output, no RoPE, no pre-split operands) takes in_norm_scale.
+bool proj_fuses_input_norm(int64_t tokens, int64_t d_in);
 // Compute units of the current device (looked up once per device; 0 if the query fails).
 int device_cus();
 // dst[c][r] = src[r][c] for a rows x cols f32 matrix (row strides in elements).

@@ -864,12 +864,27 @@ constexpr int kSkinnyMaxIn = 1024;
 constexpr size_t kSkinnyLds = (size_t)SKW * kSkinnyTokens * 16 * sizeof(float);
 __global__ __launch_bounds__(64 * SKW) void proj_skinny(ProjParams p) {
     extern __shared__ __attribute__((aligned(16))) float smem[];  // [wave][token][16 columns]
+    __shared__ float inv_s[kSkinnyTokens];
+    static_assert(SKW == kSkinnyTokens, "one wave per token row for the input norm");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_cols = p.width * p.n_out, tn = blockIdx.x;
     const int units = p.d_in / 16;
     const int u0 = wave * units / SKW, u1 = (wave + 1) * units / SKW;
     const int r = lane & 15, kq = 4 * (lane >> 4);
     const float* const xr = p.x + (int64_t)min(r, p.tokens - 1) * p.x_tok + kq;
+    const bool in_norm = p.in_norm_scale != nullptr;  // uniform
+    if (in_norm) {
+        // Wave w: the norm of token row w (clamped as the loads are), with rms_norm_rows' lane
+        // mapping and order, so the normalised inputs have its bits.
+        const float* const xw = p.x + (int64_t)min(wave, p.tokens - 1) * p.x_tok;
+        float ss = 0.f;
+        for (int i = 4 * lane; i < p.d_in; i += 256) ss = sumsq4(ss, ld4(xw + i));
+        const float inv = rms_inv(ss, p.d_in, p.in_norm_eps);
+        if (lane == 0) inv_s[wave] = inv;
+        __syncthreads();
+    }
+    const float inv_r = in_norm ? inv_s[r] : 1.f;
+    const float* const sr = in_norm ? p.in_norm_scale + kq : nullptr;
     const float* wr;
     {  // weight row of the lane's column (clamped past the last column)
         const int n = min(tn * 16 + r, n_cols - 1);
@@ -888,6 +903,11 @@ __global__ __launch_bounds__(64 * SKW) void proj_skinny(ProjParams p) {
                 xs[i] = ld4(xr + 16 * (b0 + i));
                 ws[i] = ld4(wr + 16 * (b0 + i));
             }
+        }
+        if (in_norm) {
+#pragma unroll
+            for (int i = 0; i < SKB; i++)
+                if (i < nb) xs[i] = rms_apply(xs[i], inv_r, ld4(sr + 16 * (b0 + i)));
         }
 #pragma unroll
         for (int i = 0; i < SKB; i++) {
@@ -1071,6 +1091,10 @@ static bool skinny(const ProjParams& p) {
            p.x_pre == nullptr && p.y_planes == nullptr;
 }
 
+bool proj_fuses_input_norm(int64_t tokens, int64_t d_in) {
+    return tokens > 0 && tokens <= kSkinnyTokens && d_in > 0 && d_in <= kSkinnyMaxIn && d_in % 16 == 0;
+}
+
 size_t proj_split_bytes(ProjParams& p) {
     p.m_tiles = (p.tokens + BM - 1) / BM;
     p.n_tiles = (p.width * p.n_out + BN - 1) / BN;
@@ -1118,6 +1142,7 @@ hipError_t launch_proj(const ProjParams& p0, hipStream_t stream) {
         return hipErrorInvalidValue;
     if ((int64_t)((p.tokens + BM - 1) / BM) * ((p.width * p.n_out + BN - 1) / BN) > 0x7fffffff)
         return hipErrorInvalidValue;
+    if (p.in_norm_scale != nullptr && !skinny(p)) return hipErrorInvalidValue;  // the 16-token kernel only
     if (skinny(p)) {
         p.chunk = proj_chunk((p.d_in / 16 + SKW - 1) / SKW);
         hipLaunchKernelGGL(proj_skinny, dim3((unsigned)((p.width * p.n_out + 15) / 16)), dim3(64 * SKW), kSkinnyLds,
