@@ -150,8 +150,9 @@ def test_thread_exit_releases_and_library_keeps_working(ta, gpu_ready):
 
 def test_fused_row_norm_equals_the_separate_launch(ta, gpu_ready):
     """The Chronos-Bolt forward normalises the rows of each split residual product inside the
-    product's reduce; TSFM_UNFUSED_NORM=1 queues the product and nn.rmsNorm as two launches
-    instead. The forward's output has the same bits either way."""
+    product's reduce, and (at most 16 series) its decoder's 16-row products normalise their input
+    rows as they load them; TSFM_UNFUSED_NORM=1 queues every product and nn.rmsNorm as separate
+    launches instead. The forward's output has the same bits either way."""
     import os
 
     import torch
