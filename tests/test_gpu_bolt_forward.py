@@ -67,6 +67,19 @@ def test_bolt_forward_matches_oracle_and_f64(ta, orc, orc16, gpu_ready, all_vali
     _ref.assert_within_reference_bar(raw, w8, w16, _exact(orc, s, b, n_patch, nh))
 
 
+@pytest.mark.parametrize("b,n_dec", [(20, 3), (5, 3)])
+def test_bolt_forward_decoder_paths(ta, orc, orc16, gpu_ready, b, n_dec):
+    """The decoder's two forms against the oracle: more than 16 series (row norms as launches or in
+    the producing product) and at most 16 (the 16-row products normalise their inputs on load);
+    an odd number of decoder layers, so the last cross-attention K/V product runs one layer alone
+    (the others two layers per four-output product)."""
+    n_patch, nh, d_ff, out = 12, 2, 256, 32
+    s = _setup(90 + b, b, n_patch, nh, d_ff, 2, n_dec, out)
+    raw = _run(ta, s, b, n_patch, nh, d_ff, out)
+    w8, w16 = (_oracle(o_, s, b, n_patch, nh, d_ff, out) for o_ in (orc, orc16))
+    _ref.assert_within_reference_bar(raw, w8, w16, _exact(orc, s, b, n_patch, nh))
+
+
 def test_bolt_forward_small_shape(ta, orc, orc16, gpu_ready):
     """Chronos-Bolt-small: d_model 512, 8 heads of 64, d_ff 2048, 6 + 6 layers, 32 patches + REG,
     9 quantiles x 64 steps; 16 series. Twelve f32 layers: every evaluation drifts from the exact
