@@ -390,15 +390,19 @@ qkv_proj_x3(ProjParams p) {
     const int row0 = p.m_base + tm * T;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)smem;
 
-    // Loader: 16-byte slot e = tid + NT i (i < 2) of each tile: row e / 8, indices 4 (e % 8) .. + 3
-    // of the step. Rows past the end are clamped to the last row (they feed only outputs that are
-    // not stored). dst: the slot's byte offset in a plane (16-row block, then lane (row, index / 8)).
+    // Loader: 16-byte slot e = tid + NT i (i < 2) of each tile, taken in plane order so a wave's
+    // LDS writes cover 512 contiguous bytes (no bank conflicts): 16-row block e / 128; within it,
+    // lane-slot s = (e % 128) / 2 holds row s % 16, indices 8 (s / 16) .. + 7, of which the slot
+    // takes the half e % 2: indices 8 (s / 16) + 4 (e % 2) .. + 3 of the step. Rows past the end
+    // are clamped to the last row (they feed only outputs that are not stored). dst: the slot's
+    // byte offset in a plane (16-row block, then lane (row, index / 8)).
     const float* wsrc[2];
     const float* xsrc[2];
     uint32_t dst[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int e = tid + NT * i, r = e >> 3, kq = 4 * (e & 7);
+        const int e = tid + NT * i, sl = (e & 127) >> 1;
+        const int r = 16 * (e >> 7) + (sl & 15), kq = 8 * (sl >> 4) + 4 * (e & 1);
         const int n = min(tn * T + r, n_cols - 1), sel = n / p.width;
         const float* w = sel == 0 ? p.w0 : sel == 1 ? p.w1 : sel == 2 ? p.w2 : p.w3;
         wsrc[i] = w + (int64_t)(n - sel * p.width) * p.w_ld + kq;
