@@ -161,7 +161,10 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int vx_item = tid - (nt - 256);
     const bool v_role = vx_item >= 0;
     const int kr_item = tid >> 3, kc_item = tid & 7;
-    const int vq_item = vx_item >> 5, vd_item = vx_item & 31;
+    // V quads with bits 0 and 1 of vx_item >> 5 swapped: the two half-waves of a wave then write
+    // different 8-byte halves of their 16-byte columns, which halves the LDS bank conflicts of the
+    // V stores (a store's lanes spread over twice the banks).
+    const int vq_item = ((vx_item >> 5) & 4) | (((vx_item >> 5) & 1) << 1) | ((vx_item >> 6) & 1), vd_item = vx_item & 31;
     f32x4 k_lo, k_hi, k_cs, k_sn;  // K item: dims lo / hi and, with RoPE, its rotation
     f32x4 v_01, v_23;              // V item: keys 0, 1 / keys 2, 3 of the quad, (dim, dim + 1) pairs
     uint32_t kvb = 1;              // key_valid byte of key tid of the chunk being staged (threads < 32)
