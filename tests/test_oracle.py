@@ -478,7 +478,7 @@ def test_variate_attention_matches_f64(orc, vall, cov):
 
 
 def test_variate_singleton_is_v(orc):
-    """vall = 1: every row reads only itself, so o = v exactly (the survey's singleton pin)."""
+    """vall = 1: every row reads only itself, so o = v exactly (a singleton series pins the gather without any softmax arithmetic)."""
     groups, ne, h, nh, hd = 4, 7, 3, 2, 16
     d = nh * hd
     qkv, kv = _variate_inputs(1, groups, 1, ne, h, d, p_valid=0.0)
