@@ -574,7 +574,7 @@ int tsfm_timestral_encode_categorical(const tsfm_categorical_args *args);
  * The reference backend's GEMM seam, with the argument lists and return convention of
  * src/platform/cuda/gemm.c. The reference's binding (src/platform/cuda/gpu.zig:16-44) declares
  * those functions as cuda_*; a HIP binding is the same file with the extern names changed to
- * tsfm_* (the Zig side is shown in full in INTEGRATION.md). nn.linear's weight products
+ * tsfm_*. nn.linear's weight products
  * (src/core/nn.zig:270-293) and gemmNT (src/core/nn.zig:49-60) then run on the gfx950 matrix cores
  * (the projection kernel, one output, no RoPE).
  *

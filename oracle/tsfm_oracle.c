@@ -1,7 +1,7 @@
 /*
  * tsfm_oracle.c -- CPU oracle for the tsfm-zig attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the CPU
+ * TEST INFRASTRUCTURE ONLY: what the HIP kernels are checked against, and the CPU
  * baseline that bench.py times beside them. Product code never calls it.
  *
  * A C restatement of the reference's builtin CPU path (`-Dblas=builtin`, the

@@ -1,7 +1,7 @@
 /*
  * tsfm_oracle.h -- CPU oracle for the tsfm-zig attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: the parity tests, the
+ * TEST INFRASTRUCTURE ONLY. Results are checked against this library: the parity tests, the
  * smoke check and the CPU-baseline leg of bench.py call it. Product code never
  * links, loads or calls it, and nothing falls back to it.
  *

@@ -1,7 +1,7 @@
 /*
  * tsfm_oracle_timestral.c -- CPU oracle: the Timestral model forward and forecaster.
  *
- * TEST INFRASTRUCTURE ONLY (see tsfm_oracle.h): the checker for the device Timestral path, never
+ * TEST INFRASTRUCTURE ONLY (see tsfm_oracle.h): what the device Timestral path is checked against, never
  * linked or called by the product.
  *
  * Restates, for series whose rows are all target variates (no covariates):

@@ -1,6 +1,6 @@
 """ctypes wrapper of the CPU oracle (oracle/liboracle_l*.so) for the tests and the CPU baseline.
 
-Test infrastructure: the checker, never the thing measured or shipped.
+Test infrastructure: results are checked against it; it is never the thing measured or shipped.
 """
 import ctypes
 

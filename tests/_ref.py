@@ -372,7 +372,7 @@ def reference_bar(lane8, lane16, exact=None):
     evaluation as accurate as the reference on its worse host is within m of exact, hence within
     2m of the 16-lane build (triangle inequality). Without `exact`, s stands in for m (s <= 2m;
     for independent rounding s ~ 1.4 m). Bar = max(1e-5, 2 max(s, m)): never tighter than the
-    north star's 1e-5, never looser than the reference's own cross-host floor needs."""
+    1e-5 parity target, never looser than the reference's own cross-host floor needs."""
     s = scaled_err(lane8, lane16)
     m = 0.0 if exact is None else max(scaled_err(lane8, exact), scaled_err(lane16, exact))
     return max(1e-5, 2.0 * max(s, m)), s, m

@@ -237,7 +237,7 @@ def _c2_oracle(orc, w, B):
 # The bar is _ref.reference_bar: twice the larger of that cross-host spread and the reference's
 # distance from float64 (at least 1e-5), against the 16-lane build; the GPU must also be no further
 # from float64 than the reference's worse build. At scale 1/8 (the benchmarked shape) the spread
-# is far below 1e-5 and the bar is the north star's 1e-5.
+# is far below 1e-5 and the bar is the 1e-5 parity target.
 
 
 @pytest.mark.parametrize("scale", [0.125, 1.0])

@@ -138,7 +138,7 @@ def test_timestral_forecast_accuracy_class(ta, orc, orc16, gpu_ready):
     forecast composed from float64 definitions), against the reference's own two builds, over eight
     inputs (seeds 5-8, one and two variates, a series without observation, several decode blocks),
     cached and re-encoded.
-    - In linear space (use_asinh off) every case is within the north star's 1e-5 of the 16-lane
+    - In linear space (use_asinh off) every case is within the 1e-5 parity target of the 16-lane
       oracle (measured at most 1.4e-6).
     - In asinh space the head's outputs are sinh-expanded, so the forecast's scaled error is the
       absolute f32 error of the head's output: every f32 evaluation, the reference's included, is
