@@ -558,15 +558,28 @@ __global__ __launch_bounds__(XNT) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             }
     }
     const float lt = pair_sum(l);
-    if (qi < n_main && wave_nq > 0) {
+    if (wave_nq > 0) {
+        // Through the wave's own 8 KB of the stages (idle since the loop's last barrier), so that a
+        // store instruction writes four whole 256-byte rows: row r's 16-byte column c sits at
+        // c ^ (r & 15), which keeps both the writes and the reads free of bank conflicts.
+        float* const ob = reinterpret_cast<float*>(&stage[0]) + wave * (XQ * kHeadDim);
         const float inv = 1.0f / lt;
-        float* dst = O + (int64_t)qi * p.o_tok + 4 * hh;
 #pragma unroll
         for (int db = 0; db < 2; db++)
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++)
-                st4(dst + 32 * db + 8 * g4,
-                    f32x4{o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]} * inv);
+            for (int g4 = 0; g4 < 4; g4++) {
+                const int c = 8 * db + 2 * g4 + hh;
+                *reinterpret_cast<f32x4*>(ob + ql * kHeadDim + 4 * (c ^ (ql & 15))) =
+                    f32x4{o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]} * inv;
+            }
+        const int c = lane & 15;
+#pragma unroll
+        for (int k = 0; k < XQ / 4; k++) {
+            const int r = (lane >> 4) + 4 * k;
+            if (r < wave_nq)
+                st4(O + (int64_t)(wq0 + r) * p.o_tok + 4 * c,
+                    *reinterpret_cast<const f32x4*>(ob + r * kHeadDim + 4 * (c ^ (r & 15))));
+        }
     }
 
 }
